@@ -1,0 +1,147 @@
+/*
+ * rsllm_hip.h — C ABI of the MI355X (gfx950) quantized mat-vec / mat-mul
+ * backend for rsLLM.
+ *
+ * Each entry point replaces one function of the reference's CPU path
+ * (citations: paths relative to the rsLLM tree, crates/<crate>/src/...).
+ * Arguments keep the reference's meaning and order; slices become
+ * (pointer, length) pairs so the same length checks can run here, in the
+ * same order, with the same error classes.
+ *
+ * Two flavours:
+ *   - host-pointer entry points: synchronous drop-ins for the Rust functions
+ *     (buffers are caller-owned host memory; `out` is valid on return);
+ *   - `_dev` entry points: device pointers, enqueued on the caller's
+ *     hipStream_t, no host synchronisation.
+ *
+ * Weights in device memory are in the "device layout" written by
+ * rsllm_hip_prepare_weights_dev: for Q4_K it is the GGUF byte stream
+ * itself; Q6_K / Q8_0 / Q4_0 matrices are split into field planes of the
+ * same total size (see rsllm_hip_prepare_weights_dev).
+ *
+ * Thread safety: every entry point may be called from any thread. Process
+ * state (device ordinal, registered weights) is guarded by a mutex; each
+ * calling thread gets its own stream and staging buffers for the host-pointer
+ * entry points.
+ */
+#ifndef RSLLM_HIP_H
+#define RSLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Opaque stream handle: a hipStream_t (NULL = the default stream). */
+typedef void *rsllm_hip_stream_t;
+
+/* Status codes. 1..4 mirror rsllm_backend_cpu::Error
+ * (backend-cpu/src/error.rs:7-43), 5..6 mirror rsllm_gguf::Error's
+ * dequant variants (rsllm-gguf/src/error.rs:69-80). */
+typedef enum rsllm_hip_status {
+    RSLLM_HIP_OK = 0,
+    RSLLM_HIP_ERR_SHAPE_MISMATCH = 1,        /* Error::ShapeMismatch(&str) */
+    RSLLM_HIP_ERR_NOT_BLOCK_ALIGNED = 2,     /* Error::NotBlockAligned{what,actual,block} */
+    RSLLM_HIP_ERR_NON_FINITE_INPUT = 3,      /* Error::NonFiniteInput(&str) */
+    RSLLM_HIP_ERR_UNSUPPORTED_TIER = 4,      /* Error::UnsupportedTier(&str) */
+    RSLLM_HIP_ERR_DEQUANT_SIZE_MISMATCH = 5, /* Error::DequantSizeMismatch{src_bytes,expected_bytes} */
+    RSLLM_HIP_ERR_UNSUPPORTED_DEQUANT = 6,   /* Error::UnsupportedDequant(name) */
+    RSLLM_HIP_ERR_DEVICE = 7,                /* a HIP runtime call failed (no reference counterpart) */
+    RSLLM_HIP_ERR_INVALID_ARGUMENT = 8,      /* NULL pointer with nonzero length, or a shape the
+                                                reference would panic on (row_len == 0 in
+                                                parallel.rs:44) */
+    RSLLM_HIP_ERR_UNIMPLEMENTED = 10         /* dtype the reference accepts but this backend does
+                                                not implement yet (Q2_K, IQ2_XXS, Q4_1, Q5_K, Q8_K) */
+} rsllm_hip_status;
+
+/* GgmlType ids (rsllm-gguf/src/tensor.rs:26-85) used by this ABI. */
+enum {
+    RSLLM_GGML_F32 = 0, RSLLM_GGML_F16 = 1, RSLLM_GGML_Q4_0 = 2, RSLLM_GGML_Q4_1 = 3,
+    RSLLM_GGML_Q8_0 = 8, RSLLM_GGML_Q2_K = 10, RSLLM_GGML_Q4_K = 12, RSLLM_GGML_Q5_K = 13,
+    RSLLM_GGML_Q6_K = 14, RSLLM_GGML_Q8_K = 15, RSLLM_GGML_IQ2_XXS = 16, RSLLM_GGML_BF16 = 30
+};
+
+/* Details of the last error on the calling thread.
+ * what/actual/block: NotBlockAligned (error.rs:18-25);
+ * src_bytes/expected_bytes: DequantSizeMismatch (gguf error.rs:71-76). */
+typedef struct rsllm_hip_error_detail {
+    int32_t status;
+    const char *message; /* the reference's message text where it has one */
+    const char *what;
+    size_t actual, block;
+    size_t src_bytes, expected_bytes;
+} rsllm_hip_error_detail;
+
+void rsllm_hip_last_error(rsllm_hip_error_detail *out);
+
+/* Backend handle analogue: CpuBackend::new (backend-cpu/src/lib.rs:50-53)
+ * plus device choice. Optional; the first call of any entry point performs
+ * it with device 0. */
+int rsllm_hip_init(int device_ordinal);
+
+/* BackendCapability analogue (rsllm-cal/src/lib.rs:62-75,
+ * backend-cpu/src/capability.rs:119-131). */
+typedef struct rsllm_hip_capability {
+    const char *backend; /* "rocm" */
+    const char *arch;    /* "gfx950" */
+    int q4k_matmul, q6k_matmul, q8_0_matmul, q2k_matmul, iq2xxs_matmul, fp8_kv_cache;
+} rsllm_hip_capability;
+void rsllm_hip_capability_get(rsllm_hip_capability *out);
+
+/* ---- quantized matmul --------------------------------------------------- */
+
+/* matmul_quant_f32 (backend-cpu/src/ops/quant_matmul.rs:45-119).
+ * out[t*out_dim + o] = sum_i deq(W)[o, i] * x[t*in_dim + i]; `out` is
+ * overwritten. Validation order as :57-92: dtype, in_dim % block,
+ * weights_len, x_len, out_len. Accepted dtypes: Q4_K, Q8_0, Q4_0, and Q6_K
+ * (a deliberate superset: the reference's guard rejects Q6_K). `tier` is
+ * accepted and ignored, as the reference ignores it (:55).
+ * Weights are uploaded for this call unless the same (pointer, length,
+ * dtype, in_dim) was registered with rsllm_hip_register_weights. */
+int rsllm_hip_matmul_quant_f32(float *out, size_t out_len, const uint8_t *weights,
+                               size_t weights_len, const float *x, size_t x_len, size_t n_tok,
+                               size_t in_dim, size_t out_dim, uint32_t dtype, uint32_t tier);
+
+/* Device-pointer matmul_quant_f32: same validation; `weights` in device
+ * layout; enqueued on `stream`. */
+int rsllm_hip_matmul_quant_f32_dev(float *out, size_t out_len, const uint8_t *weights,
+                                   size_t weights_len, const float *x, size_t x_len,
+                                   size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype,
+                                   rsllm_hip_stream_t stream);
+
+/* ---- weights residency ----------------------------------------------------
+ * The reference borrows weights from the GGUF mmap for the life of the
+ * GgufFile (rsllm-gguf/src/file.rs:81-97, models/src/dsv4/loader.rs:199-216).
+ * Registering uploads a tensor once (converted to the device layout);
+ * later host-pointer calls with the same (pointer, length, dtype, in_dim)
+ * use the device copy. Release frees every registered tensor. */
+int rsllm_hip_register_weights(const uint8_t *weights, size_t weights_len, uint32_t dtype,
+                               size_t in_dim);
+int rsllm_hip_release_weights(void);
+
+/* GGUF rows -> device layout: `len` bytes holding whole rows of `in_dim`
+ * elements (rows = len / row_bytes, nb = in_dim / block_elems). Q4_K:
+ * unchanged (`dst` may equal `src`). Q6_K, Q8_0, Q4_0: the matrix is split
+ * into field planes of the same total size, each row-major over
+ * (row, block): Q6_K [ql rows*nb*128 | qh rows*nb*64 | scales rows*nb*16 |
+ * d rows*nb*2], Q8_0 [qs rows*nb*32 | d rows*nb*2], Q4_0 [qs rows*nb*16 |
+ * d rows*nb*2]; `dst` must not overlap `src`. Enqueued on `stream`. */
+int rsllm_hip_prepare_weights_dev(uint8_t *dst, const uint8_t *src, size_t len, uint32_t dtype,
+                                  size_t in_dim, rsllm_hip_stream_t stream);
+
+/* ---- dequantisation ------------------------------------------------------ */
+
+/* dequant_to_f32 (rsllm-gguf/src/dequant/mod.rs:69-85): decode `src` (GGUF
+ * bytes) into dst[dst_len]. Bit-exact with the reference for F32, F16, BF16,
+ * Q4_0, Q4_K, Q6_K, Q8_0. Size rule of q4_k.rs:36-49 (and siblings). */
+int rsllm_hip_dequant_to_f32(uint32_t dtype, const uint8_t *src, size_t src_len, float *dst,
+                             size_t dst_len);
+int rsllm_hip_dequant_to_f32_dev(uint32_t dtype, const uint8_t *src, size_t src_len, float *dst,
+                                 size_t dst_len, rsllm_hip_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RSLLM_HIP_H */

@@ -1,0 +1,284 @@
+"""Host-side mirror of rsllm-backend-cpu's quantized-matmul interface, backed
+by librsllm_hip.so through its C ABI (include/rsllm_hip.h).
+
+Names, argument order and error classes follow the reference:
+
+* ``matmul_quant_f32(out, weights, x, n_tok, in_dim, out_dim, dtype, tier)``
+  — backend-cpu/src/ops/quant_matmul.rs:45-54
+* ``dequant_to_f32(dtype, src, dst)`` — rsllm-gguf/src/dequant/mod.rs:69
+* ``Error`` subclasses — backend-cpu/src/error.rs:7-43 and
+  rsllm-gguf/src/error.rs:69-80
+* ``HipBackend`` — the ``CpuBackend`` handle (backend-cpu/src/lib.rs:43-107)
+  with ``kind()`` / ``capability()`` (rsllm-cal/src/lib.rs:84-90)
+
+There is no CPU fallback: if the shared library is missing, importing this
+module raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+from .ggml import GgmlType
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "librsllm_hip.so")
+
+# ---------------------------------------------------------------------------
+# Status codes (include/rsllm_hip.h)
+# ---------------------------------------------------------------------------
+OK = 0
+ERR_SHAPE_MISMATCH = 1
+ERR_NOT_BLOCK_ALIGNED = 2
+ERR_NON_FINITE_INPUT = 3
+ERR_UNSUPPORTED_TIER = 4
+ERR_DEQUANT_SIZE_MISMATCH = 5
+ERR_UNSUPPORTED_DEQUANT = 6
+ERR_DEVICE = 7
+ERR_INVALID_ARGUMENT = 8
+ERR_UNIMPLEMENTED = 10
+
+
+class SimdTier(enum.IntEnum):
+    """backend-cpu/src/capability.rs:20-35. Accepted and ignored by the
+    matmul, as the reference ignores it (quant_matmul.rs:55)."""
+
+    Neon = 0
+    Avx512 = 1
+    Avx2 = 2
+    Scalar = 3
+
+
+class Error(Exception):
+    status = -1
+
+    def __init__(self, message: str = "", **fields):
+        super().__init__(message)
+        self.message = message
+        for k, v in fields.items():
+            setattr(self, k, v)
+
+
+class ShapeMismatch(Error):
+    status = ERR_SHAPE_MISMATCH
+
+
+class NotBlockAligned(Error):
+    status = ERR_NOT_BLOCK_ALIGNED
+
+
+class NonFiniteInput(Error):
+    status = ERR_NON_FINITE_INPUT
+
+
+class UnsupportedTier(Error):
+    status = ERR_UNSUPPORTED_TIER
+
+
+class DequantSizeMismatch(Error):
+    status = ERR_DEQUANT_SIZE_MISMATCH
+
+
+class UnsupportedDequant(Error):
+    status = ERR_UNSUPPORTED_DEQUANT
+
+
+class DeviceError(Error):
+    status = ERR_DEVICE
+
+
+class InvalidArgument(Error):
+    status = ERR_INVALID_ARGUMENT
+
+
+class Unimplemented(Error):
+    status = ERR_UNIMPLEMENTED
+
+
+_ERRORS = {c.status: c for c in (ShapeMismatch, NotBlockAligned, NonFiniteInput, UnsupportedTier,
+                                 DequantSizeMismatch, UnsupportedDequant, DeviceError,
+                                 InvalidArgument, Unimplemented)}
+
+
+class _ErrorDetail(ctypes.Structure):
+    _fields_ = [("status", ctypes.c_int32), ("message", ctypes.c_char_p), ("what", ctypes.c_char_p),
+                ("actual", ctypes.c_size_t), ("block", ctypes.c_size_t),
+                ("src_bytes", ctypes.c_size_t), ("expected_bytes", ctypes.c_size_t)]
+
+
+class _Capability(ctypes.Structure):
+    _fields_ = [("backend", ctypes.c_char_p), ("arch", ctypes.c_char_p),
+                ("q4k_matmul", ctypes.c_int), ("q6k_matmul", ctypes.c_int),
+                ("q8_0_matmul", ctypes.c_int), ("q2k_matmul", ctypes.c_int),
+                ("iq2xxs_matmul", ctypes.c_int), ("fp8_kv_cache", ctypes.c_int)]
+
+
+# Every symbol include/rsllm_hip.h declares, with its ctypes signature.
+_P, _S, _U32, _I = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_int
+SIGNATURES = {
+    "rsllm_hip_last_error": ([ctypes.POINTER(_ErrorDetail)], None),
+    "rsllm_hip_init": ([_I], _I),
+    "rsllm_hip_capability_get": ([ctypes.POINTER(_Capability)], None),
+    "rsllm_hip_matmul_quant_f32": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _U32], _I),
+    "rsllm_hip_matmul_quant_f32_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _P], _I),
+    "rsllm_hip_register_weights": ([_P, _S, _U32, _S], _I),
+    "rsllm_hip_release_weights": ([], _I),
+    "rsllm_hip_prepare_weights_dev": ([_P, _P, _S, _U32, _S, _P], _I),
+    "rsllm_hip_dequant_to_f32": ([_U32, _P, _S, _P, _S], _I),
+    "rsllm_hip_dequant_to_f32_dev": ([_U32, _P, _S, _P, _S, _P], _I),
+}
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -m rsllm_amd.build` "
+            "(there is no CPU fallback)")
+    # PyTorch-ROCm ships its own libamdhip64.so.7 (same SONAME as
+    # /opt/rocm's). Loading torch first makes the dynamic linker bind this
+    # library to torch's copy, so the process has ONE HIP runtime and torch
+    # tensors, streams and events interoperate with these entry points. Two
+    # runtimes in one process do not share devices.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    return lib
+
+
+LIB = _load()
+
+
+def _check(rc: int) -> None:
+    if rc == OK:
+        return
+    d = _ErrorDetail()
+    LIB.rsllm_hip_last_error(ctypes.byref(d))
+    cls = _ERRORS.get(rc, Error)
+    msg = (d.message or b"").decode(errors="replace")
+    raise cls(msg, what=(d.what or b"").decode() or None, actual=d.actual, block=d.block,
+              src_bytes=d.src_bytes, expected_bytes=d.expected_bytes)
+
+
+def _host_ptr(a):
+    if a is None:
+        return None, 0
+    if isinstance(a, (bytes, bytearray, memoryview)):
+        a = np.frombuffer(a, dtype=np.uint8)
+    if not isinstance(a, np.ndarray):
+        raise TypeError("expected a numpy array or bytes")
+    if not a.flags.c_contiguous:
+        raise ValueError("array must be C-contiguous")
+    return (a.ctypes.data_as(ctypes.c_void_p) if a.size else None), a.size
+
+
+def _host_f32(a, name):
+    if not (isinstance(a, np.ndarray) and a.dtype == np.float32):
+        raise TypeError(f"{name} must be a float32 numpy array")
+    return _host_ptr(a)
+
+
+# ---------------------------------------------------------------------------
+# Host-pointer entry points (synchronous drop-ins)
+# ---------------------------------------------------------------------------
+
+def matmul_quant_f32(out: np.ndarray, weights, x: np.ndarray, n_tok: int, in_dim: int,
+                     out_dim: int, dtype, tier: SimdTier = SimdTier.Scalar) -> None:
+    """out[t*out_dim + o] = sum_i deq(W)[o, i] * x[t*in_dim + i] (overwrites ``out``)."""
+    po, no = _host_f32(out, "out")
+    pw, nw = _host_ptr(weights)
+    px, nx = _host_f32(x, "x")
+    _check(LIB.rsllm_hip_matmul_quant_f32(po, no, pw, nw, px, nx, n_tok, in_dim, out_dim,
+                                          int(dtype), int(tier)))
+
+
+def dequant_to_f32(dtype, src, dst: np.ndarray) -> None:
+    ps, ns = _host_ptr(src)
+    pd, nd = _host_f32(dst, "dst")
+    _check(LIB.rsllm_hip_dequant_to_f32(int(dtype), ps, ns, pd, nd))
+
+
+def register_weights(weights: np.ndarray, dtype, in_dim: int) -> None:
+    pw, nw = _host_ptr(weights)
+    _check(LIB.rsllm_hip_register_weights(pw, nw, int(dtype), in_dim))
+
+
+def release_weights() -> None:
+    _check(LIB.rsllm_hip_release_weights())
+
+
+def init(device: int = 0) -> None:
+    _check(LIB.rsllm_hip_init(device))
+
+
+# ---------------------------------------------------------------------------
+# Device-pointer entry points: arguments are raw device addresses (ints, e.g.
+# torch.Tensor.data_ptr()) with element counts, and a hipStream_t (int).
+# ---------------------------------------------------------------------------
+
+def matmul_quant_f32_dev(out_ptr: int, out_len: int, w_ptr: int, w_len: int, x_ptr: int,
+                         x_len: int, n_tok: int, in_dim: int, out_dim: int, dtype,
+                         stream: int = 0) -> None:
+    _check(LIB.rsllm_hip_matmul_quant_f32_dev(out_ptr or None, out_len, w_ptr or None, w_len,
+                                              x_ptr or None, x_len, n_tok, in_dim, out_dim,
+                                              int(dtype), stream or None))
+
+
+def prepare_weights_dev(dst_ptr: int, src_ptr: int, nbytes: int, dtype, in_dim: int,
+                        stream: int = 0) -> None:
+    _check(LIB.rsllm_hip_prepare_weights_dev(dst_ptr or None, src_ptr or None, nbytes, int(dtype),
+                                             in_dim, stream or None))
+
+
+def dequant_to_f32_dev(dtype, src_ptr: int, src_len: int, dst_ptr: int, dst_len: int,
+                       stream: int = 0) -> None:
+    _check(LIB.rsllm_hip_dequant_to_f32_dev(int(dtype), src_ptr or None, src_len, dst_ptr or None,
+                                            dst_len, stream or None))
+
+
+# ---------------------------------------------------------------------------
+# Backend handle
+# ---------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class BackendCapability:
+    backend: str
+    arch: str
+    q4k_matmul: bool
+    q6k_matmul: bool
+    q8_0_matmul: bool
+    q2k_matmul: bool
+    iq2xxs_matmul: bool
+    fp8_kv_cache: bool
+
+
+class HipBackend:
+    """Analogue of ``CpuBackend``: cheap, stateless, shareable."""
+
+    def kind(self) -> str:
+        return "Rocm"
+
+    def capability(self) -> BackendCapability:
+        c = _Capability()
+        LIB.rsllm_hip_capability_get(ctypes.byref(c))
+        return BackendCapability(c.backend.decode(), c.arch.decode(), bool(c.q4k_matmul),
+                                 bool(c.q6k_matmul), bool(c.q8_0_matmul), bool(c.q2k_matmul),
+                                 bool(c.iq2xxs_matmul), bool(c.fp8_kv_cache))
+
+
+__all__ = [
+    "GgmlType", "SimdTier", "Error", "ShapeMismatch", "NotBlockAligned", "NonFiniteInput",
+    "UnsupportedTier", "DequantSizeMismatch", "UnsupportedDequant", "DeviceError",
+    "InvalidArgument", "Unimplemented", "matmul_quant_f32", "dequant_to_f32", "register_weights",
+    "release_weights", "init", "matmul_quant_f32_dev", "prepare_weights_dev",
+    "dequant_to_f32_dev", "HipBackend", "BackendCapability", "LIB", "LIB_PATH", "SIGNATURES",
+]

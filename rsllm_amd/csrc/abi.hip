@@ -1,0 +1,395 @@
+// C-ABI entry points: argument validation in the reference's order, process
+// state (device, registered weights), per-thread streams and staging, and
+// dispatch to the kernel launchers.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/rsllm_hip.h"
+#include "kernels.h"
+
+using namespace rsllm_hip;
+
+namespace {
+
+// ---- error state (per thread) -------------------------------------------
+struct ErrState {
+    rsllm_hip_error_detail d{};
+    std::string msg;
+};
+thread_local ErrState g_err;
+
+int set_err(int status, const char *msg, const char *what = nullptr, size_t a = 0, size_t b = 0,
+            size_t src = 0, size_t exp = 0) {
+    g_err.msg = msg ? msg : "";
+    g_err.d.status = status;
+    g_err.d.message = g_err.msg.c_str();
+    g_err.d.what = what;
+    g_err.d.actual = a;
+    g_err.d.block = b;
+    g_err.d.src_bytes = src;
+    g_err.d.expected_bytes = exp;
+    return status;
+}
+
+int ok() { return set_err(RSLLM_HIP_OK, ""); }
+
+int dev_err(hipError_t e, const char *where) {
+    std::string m = std::string(where) + ": " + hipGetErrorString(e);
+    return set_err(RSLLM_HIP_ERR_DEVICE, m.c_str());
+}
+
+#define HIP_TRY(expr, where)                         \
+    do {                                             \
+        hipError_t e_ = (expr);                      \
+        if (e_ != hipSuccess) return dev_err(e_, where); \
+    } while (0)
+
+// ---- process state --------------------------------------------------------
+std::mutex g_mu;
+int g_device = 0;
+bool g_inited = false;
+
+struct Registered {
+    const uint8_t *host;
+    size_t len;
+    uint32_t dtype;
+    size_t in_dim;
+    uint8_t *dev;
+};
+std::vector<Registered> g_registry;
+
+// ---- per-thread state -----------------------------------------------------
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    hipError_t ensure(size_t n) {
+        if (n <= cap) return hipSuccess;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+        size_t want = n < 4096 ? 4096 : n;
+        hipError_t e = hipMalloc(&p, want);
+        if (e == hipSuccess) cap = want;
+        return e;
+    }
+};
+
+struct ThreadCtx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    DevBuf w_raw, w_dev, x, y;
+};
+thread_local ThreadCtx t_ctx;
+
+int ensure_device() {
+    int dev;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_inited = true;
+        dev = g_device;
+    }
+    HIP_TRY(hipSetDevice(dev), "hipSetDevice");
+    if (t_ctx.device != dev || !t_ctx.stream) {
+        HIP_TRY(hipStreamCreateWithFlags(&t_ctx.stream, hipStreamNonBlocking), "hipStreamCreate");
+        t_ctx.device = dev;
+    }
+    return RSLLM_HIP_OK;
+}
+
+bool fits_int(size_t v) { return v <= (size_t)INT_MAX; }
+
+bool mul_ok(size_t a, size_t b, size_t *r) { return !__builtin_mul_overflow(a, b, r); }
+
+// dtypes matmul_quant_f32 accepts (quant_matmul.rs:57-64), and which of
+// them this backend implements.
+bool matmul_dtype_known(uint32_t t) {
+    return t == T_Q4_K || t == T_Q2_K || t == T_IQ2_XXS || t == T_Q4_0 || t == T_Q8_0 ||
+           t == T_Q6_K;
+}
+bool matmul_dtype_impl(uint32_t t) { return t == T_Q4_K || t == T_Q8_0 || t == T_Q4_0 || t == T_Q6_K; }
+
+// Shared validation of matmul_quant_f32 (quant_matmul.rs:57-92), then the
+// parallel.rs:44 row_len > 0 assertion.
+int validate_matmul(size_t out_len, const void *w, size_t w_len, const void *x, size_t x_len,
+                    const void *out, size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype) {
+    if (!matmul_dtype_known(dtype))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_quant_f32: unsupported dtype for MoE expert matmul");
+    const size_t be = block_elems_of(dtype);
+    if (in_dim % be != 0)
+        return set_err(RSLLM_HIP_ERR_NOT_BLOCK_ALIGNED, "`in_dim` is not a multiple of the block",
+                       "in_dim", in_dim, be);
+    size_t need;
+    if (!mul_ok(out_dim, row_bytes_of(dtype, in_dim), &need) || w_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_quant_f32: weights must be out_dim * (in_dim / block_elem * "
+                       "block_bytes)");
+    if (!mul_ok(n_tok, in_dim, &need) || x_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "matmul_quant_f32: x must be n_tok * in_dim");
+    if (!mul_ok(n_tok, out_dim, &need) || out_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_quant_f32: out must be n_tok * out_dim");
+    if (out_dim == 0)
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                       "for_each_row_mut: row_len must be non-zero (out_dim == 0)");
+    if ((w_len && !w) || (x_len && !x) || (out_len && !out))
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "NULL pointer with a nonzero length");
+    if (!matmul_dtype_impl(dtype))
+        return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED,
+                       "matmul_quant_f32: dtype accepted by the reference is not implemented by "
+                       "the HIP backend");
+    if (!fits_int(n_tok) || !fits_int(in_dim) || !fits_int(out_dim))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "matmul_quant_f32: dimension exceeds 2^31-1");
+    return RSLLM_HIP_OK;
+}
+
+const char *ggml_name(uint32_t t) {
+    switch (t) {
+    case 0: return "f32"; case 1: return "f16"; case 2: return "q4_0"; case 3: return "q4_1";
+    case 6: return "q5_0"; case 7: return "q5_1"; case 8: return "q8_0"; case 9: return "q8_1";
+    case 10: return "q2_k"; case 11: return "q3_k"; case 12: return "q4_k"; case 13: return "q5_k";
+    case 14: return "q6_k"; case 15: return "q8_k"; case 16: return "iq2_xxs";
+    case 30: return "bf16";
+    default: return "unknown";
+    }
+}
+
+// dequant_to_f32's dispatch and size rule (dequant/mod.rs:69-85,
+// q4_k.rs:36-49, float.rs check_size).
+int validate_dequant(uint32_t dtype, const void *src, size_t src_len, const void *dst,
+                     size_t dst_len) {
+    const bool impl = dtype == T_F32 || dtype == T_F16 || dtype == T_BF16 || dtype == T_Q4_0 ||
+                      dtype == T_Q4_K || dtype == T_Q6_K || dtype == T_Q8_0;
+    const bool ref_decodable = impl || dtype == 3 /*Q4_1*/ || dtype == 13 /*Q5_K*/ ||
+                               dtype == T_Q2_K || dtype == 15 /*Q8_K*/ || dtype == T_IQ2_XXS;
+    if (!ref_decodable) {
+        std::string m = std::string("dtype `") + ggml_name(dtype) +
+                        "` is not yet supported for dequantization in this build";
+        return set_err(RSLLM_HIP_ERR_UNSUPPORTED_DEQUANT, m.c_str(), ggml_name(dtype));
+    }
+    if (!impl)
+        return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED,
+                       "dequant_to_f32: dtype decodable by the reference is not implemented by "
+                       "the HIP backend");
+    const size_t be = block_elems_of(dtype), bb = block_bytes_of(dtype);
+    size_t expected;
+    if (be > 1 && dst_len % be != 0) {
+        expected = (dst_len + be - 1) / be * bb;
+        return set_err(RSLLM_HIP_ERR_DEQUANT_SIZE_MISMATCH, "dequant size mismatch", nullptr, 0, 0,
+                       src_len, expected);
+    }
+    if (!mul_ok(dst_len / be, bb, &expected) || src_len != expected)
+        return set_err(RSLLM_HIP_ERR_DEQUANT_SIZE_MISMATCH, "dequant size mismatch", nullptr, 0, 0,
+                       src_len, expected);
+    if ((src_len && !src) || (dst_len && !dst))
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "NULL pointer with a nonzero length");
+    return RSLLM_HIP_OK;
+}
+
+const uint8_t *find_registered(const uint8_t *host, size_t len, uint32_t dtype, size_t in_dim) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (const auto &r : g_registry)
+        if (r.host == host && r.len == len && r.dtype == dtype && r.in_dim == in_dim) return r.dev;
+    return nullptr;
+}
+
+bool needs_prepare(uint32_t dtype) { return dtype != T_Q4_K; }
+
+}  // namespace
+
+extern "C" {
+
+void rsllm_hip_last_error(rsllm_hip_error_detail *out) {
+    if (!out) return;
+    *out = g_err.d;
+    out->message = g_err.msg.c_str();
+}
+
+int rsllm_hip_init(int device_ordinal) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) return dev_err(e, "hipGetDeviceCount");
+    if (device_ordinal < 0 || device_ordinal >= n)
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "device ordinal out of range");
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_device = device_ordinal;
+        g_inited = true;
+    }
+    int rc = ensure_device();
+    return rc ? rc : ok();
+}
+
+void rsllm_hip_capability_get(rsllm_hip_capability *out) {
+    if (!out) return;
+    out->backend = "rocm";
+    out->arch = "gfx950";
+    out->q4k_matmul = 1;
+    out->q6k_matmul = 1;
+    out->q8_0_matmul = 1;
+    out->q2k_matmul = 0;
+    out->iq2xxs_matmul = 0;
+    out->fp8_kv_cache = 0;
+}
+
+int rsllm_hip_matmul_quant_f32_dev(float *out, size_t out_len, const uint8_t *weights,
+                                   size_t weights_len, const float *x, size_t x_len,
+                                   size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype,
+                                   rsllm_hip_stream_t stream) {
+    int rc = validate_matmul(out_len, weights, weights_len, x, x_len, out, n_tok, in_dim, out_dim,
+                             dtype);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    if (n_tok == 0) return ok();
+    if (in_dim == 0) {
+        HIP_TRY(launch_fill_zero(out, out_len, s), "fill_zero");
+        return ok();
+    }
+    HIP_TRY(launch_gemv(dtype, weights, x, out, (int)n_tok, (int)in_dim, (int)out_dim, s), "gemv");
+    return ok();
+}
+
+int rsllm_hip_matmul_quant_f32(float *out, size_t out_len, const uint8_t *weights,
+                               size_t weights_len, const float *x, size_t x_len, size_t n_tok,
+                               size_t in_dim, size_t out_dim, uint32_t dtype, uint32_t tier) {
+    (void)tier;  // quant_matmul.rs:55
+    int rc = validate_matmul(out_len, weights, weights_len, x, x_len, out, n_tok, in_dim, out_dim,
+                             dtype);
+    if (rc) return rc;
+    if (n_tok == 0) return ok();
+    if (in_dim == 0) {  // every dot is empty: 0.0 (quant_matmul.rs:110-114)
+        std::memset(out, 0, out_len * sizeof(float));
+        return ok();
+    }
+    if ((rc = ensure_device())) return rc;
+    ThreadCtx &c = t_ctx;
+    const uint8_t *dw = find_registered(weights, weights_len, dtype, in_dim);
+    if (!dw) {
+        HIP_TRY(c.w_raw.ensure(weights_len), "hipMalloc");
+        HIP_TRY(hipMemcpyAsync(c.w_raw.p, weights, weights_len, hipMemcpyHostToDevice, c.stream),
+                "upload weights");
+        dw = (const uint8_t *)c.w_raw.p;
+        if (needs_prepare(dtype)) {
+            HIP_TRY(c.w_dev.ensure(weights_len), "hipMalloc");
+            HIP_TRY(launch_prepare(dtype, dw, (uint8_t *)c.w_dev.p, out_dim, in_dim, c.stream),
+                    "prepare weights");
+            dw = (const uint8_t *)c.w_dev.p;
+        }
+    }
+    HIP_TRY(c.x.ensure(x_len * sizeof(float)), "hipMalloc");
+    HIP_TRY(c.y.ensure(out_len * sizeof(float)), "hipMalloc");
+    HIP_TRY(hipMemcpyAsync(c.x.p, x, x_len * sizeof(float), hipMemcpyHostToDevice, c.stream),
+            "upload x");
+    HIP_TRY(launch_gemv(dtype, dw, (const float *)c.x.p, (float *)c.y.p, (int)n_tok, (int)in_dim,
+                        (int)out_dim, c.stream),
+            "gemv");
+    HIP_TRY(hipMemcpyAsync(out, c.y.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
+            "download out");
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    return ok();
+}
+
+int rsllm_hip_register_weights(const uint8_t *weights, size_t weights_len, uint32_t dtype,
+                               size_t in_dim) {
+    if (!matmul_dtype_impl(dtype))
+        return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED, "register_weights: dtype not implemented");
+    const size_t be = block_elems_of(dtype);
+    if (in_dim == 0 || in_dim % be != 0)
+        return set_err(RSLLM_HIP_ERR_NOT_BLOCK_ALIGNED, "`in_dim` is not a multiple of the block",
+                       "in_dim", in_dim, be);
+    const size_t rb = row_bytes_of(dtype, in_dim);
+    if (weights_len % rb != 0 || (weights_len && !weights))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "register_weights: length is not a whole number of rows");
+    if (find_registered(weights, weights_len, dtype, in_dim)) return ok();
+    int rc = ensure_device();
+    if (rc) return rc;
+    uint8_t *raw = nullptr, *dev = nullptr;
+    HIP_TRY(hipMalloc(&dev, weights_len ? weights_len : 1), "hipMalloc");
+    hipError_t e;
+    if (!needs_prepare(dtype)) {
+        e = hipMemcpy(dev, weights, weights_len, hipMemcpyHostToDevice);
+    } else {
+        e = hipMalloc(&raw, weights_len ? weights_len : 1);
+        if (e == hipSuccess) e = hipMemcpy(raw, weights, weights_len, hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = launch_prepare(dtype, raw, dev, weights_len / rb, in_dim, t_ctx.stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(t_ctx.stream);
+        if (raw) (void)hipFree(raw);
+    }
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return dev_err(e, "register_weights");
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_registry.push_back({weights, weights_len, dtype, in_dim, dev});
+    return ok();
+}
+
+int rsllm_hip_release_weights(void) {
+    std::vector<Registered> regs;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        regs.swap(g_registry);
+    }
+    if (!regs.empty()) {
+        int rc = ensure_device();
+        if (rc) return rc;
+        HIP_TRY(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        for (auto &r : regs) (void)hipFree(r.dev);
+    }
+    return ok();
+}
+
+int rsllm_hip_prepare_weights_dev(uint8_t *dst, const uint8_t *src, size_t len, uint32_t dtype,
+                                  size_t in_dim, rsllm_hip_stream_t stream) {
+    if (!matmul_dtype_impl(dtype))
+        return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED, "prepare_weights: dtype not implemented");
+    const size_t be = block_elems_of(dtype);
+    if (in_dim == 0 || in_dim % be != 0)
+        return set_err(RSLLM_HIP_ERR_NOT_BLOCK_ALIGNED, "`in_dim` is not a multiple of the block",
+                       "in_dim", in_dim, be);
+    const size_t rb = row_bytes_of(dtype, in_dim);
+    if (len % rb != 0)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "prepare_weights: length is not a whole number of rows");
+    if (len && (!dst || !src))
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "NULL pointer with a nonzero length");
+    if (dtype != T_Q4_K && len && dst < src + len && src < dst + len)
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "prepare_weights: dst overlaps src");
+    HIP_TRY(launch_prepare(dtype, src, dst, len / rb, in_dim, (hipStream_t)stream), "prepare");
+    return ok();
+}
+
+int rsllm_hip_dequant_to_f32_dev(uint32_t dtype, const uint8_t *src, size_t src_len, float *dst,
+                                 size_t dst_len, rsllm_hip_stream_t stream) {
+    int rc = validate_dequant(dtype, src, src_len, dst, dst_len);
+    if (rc) return rc;
+    HIP_TRY(launch_dequant(dtype, src, dst, dst_len, (hipStream_t)stream), "dequant");
+    return ok();
+}
+
+int rsllm_hip_dequant_to_f32(uint32_t dtype, const uint8_t *src, size_t src_len, float *dst,
+                             size_t dst_len) {
+    int rc = validate_dequant(dtype, src, src_len, dst, dst_len);
+    if (rc) return rc;
+    if (dst_len == 0) return ok();
+    if ((rc = ensure_device())) return rc;
+    ThreadCtx &c = t_ctx;
+    HIP_TRY(c.w_raw.ensure(src_len), "hipMalloc");
+    HIP_TRY(c.y.ensure(dst_len * sizeof(float)), "hipMalloc");
+    HIP_TRY(hipMemcpyAsync(c.w_raw.p, src, src_len, hipMemcpyHostToDevice, c.stream), "upload");
+    HIP_TRY(launch_dequant(dtype, (const uint8_t *)c.w_raw.p, (float *)c.y.p, dst_len, c.stream),
+            "dequant");
+    HIP_TRY(hipMemcpyAsync(dst, c.y.p, dst_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
+            "download");
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    return ok();
+}
+
+}  // extern "C"

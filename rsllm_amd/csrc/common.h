@@ -1,0 +1,52 @@
+// Device helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace rsllm_hip {
+
+// GgmlType ids (rsllm-gguf/src/tensor.rs:26-85).
+enum : uint32_t {
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q2_K = 10,
+    T_Q4_K = 12, T_Q6_K = 14, T_IQ2_XXS = 16, T_BF16 = 30
+};
+
+constexpr int kQ4kBytes = 144;
+constexpr int kQ6kBytes = 210;
+constexpr int kQ8Bytes = 34;
+
+// Exact f16 -> f32 widening of a 16-bit pattern (v_cvt_f32_f16 keeps f16
+// subnormals: the f16 denormal mode is "preserve" on gfx9).
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// Sum over the 64 lanes of a wavefront; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Byte b (0..3) of a dword as float: one v_cvt_f32_ubyte{b}.
+__device__ __forceinline__ float ubyte_f(uint32_t v, int b) {
+    return (float)((v >> (8 * b)) & 0xFFu);
+}
+
+// (sc, m) of Q4_K sub-block j from the three scale dwords s0 = bytes 0-3,
+// s1 = bytes 4-7, s2 = bytes 8-11 (q4_k_scale_min, dequant/mod.rs:48-58).
+__device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                              uint32_t &sc, uint32_t &m) {
+    if (j < 4) {
+        sc = (s0 >> (8 * j)) & 63u;
+        m = (s1 >> (8 * j)) & 63u;
+    } else {
+        const int q = 8 * (j - 4);
+        sc = ((s2 >> q) & 15u) | (((s0 >> (q + 6)) & 3u) << 4);
+        m = ((s2 >> (q + 4)) & 15u) | (((s1 >> (q + 6)) & 3u) << 4);
+    }
+}
+
+}  // namespace rsllm_hip

@@ -1,0 +1,219 @@
+// GGUF block decode to f32 (bit-exact with the reference dequantizers) and
+// the one-time re-layout of weights into the device layout the GEMV kernels
+// read.
+//
+// Bit-exactness: every product in the reference formulas is exact in f32
+// (Q4_K: d*sc <= 17 significant bits, times q <= 4 bits; Q6_K:
+// d*sc*(q-32) <= 23 bits; Q8_0/Q4_0: <= 18 bits), so the only rounding is
+// Q4_K's final subtraction. Contraction is switched off anyway so each line
+// is evaluated exactly as written.
+#include "kernels.h"
+
+namespace rsllm_hip {
+
+#pragma clang fp contract(off)
+
+// One thread per (block, 32-element sub-block j): q4_k.rs:51-89.
+__global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t *__restrict__ src,
+                                                     float *__restrict__ dst, size_t n_blocks) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= n_blocks * 8) return;
+    const size_t b = gid >> 3;
+    const int j = (int)(gid & 7);
+    const uint8_t *blk = src + b * kQ4kBytes;
+    const float d = f16_to_f32(blk[0] | (blk[1] << 8));
+    const float dmin = f16_to_f32(blk[2] | (blk[3] << 8));
+    uint32_t s[3];
+    for (int i = 0; i < 3; i++)
+        s[i] = blk[4 + 4 * i] | (blk[5 + 4 * i] << 8) | (blk[6 + 4 * i] << 16) |
+               ((uint32_t)blk[7 + 4 * i] << 24);
+    uint32_t sc, m;
+    q4k_scale_min(j, s[0], s[1], s[2], sc, m);
+    const float d1 = d * (float)sc;
+    const float m1f = dmin * (float)m;
+    const uint8_t *q = blk + 16 + 32 * (j >> 1);
+    const int shift = (j & 1) ? 4 : 0;
+    float *o = dst + b * 256 + 32 * j;
+    for (int l = 0; l < 32; l += 4) {
+        float4 v;
+        v.x = d1 * (float)((q[l + 0] >> shift) & 15) - m1f;
+        v.y = d1 * (float)((q[l + 1] >> shift) & 15) - m1f;
+        v.z = d1 * (float)((q[l + 2] >> shift) & 15) - m1f;
+        v.w = d1 * (float)((q[l + 3] >> shift) & 15) - m1f;
+        *reinterpret_cast<float4 *>(o + l) = v;
+    }
+}
+
+// One thread per (block, 32-element group g): q6_k.rs:50-99. Group g covers
+// elements 32g..32g+31 = half h = g/4, stride k = g%4.
+__global__ __launch_bounds__(256) void k_dequant_q6k(const uint8_t *__restrict__ src,
+                                                     float *__restrict__ dst, size_t n_blocks) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= n_blocks * 8) return;
+    const size_t b = gid >> 3;
+    const int g = (int)(gid & 7);
+    const int h = g >> 2, k = g & 3;
+    const uint8_t *blk = src + b * kQ6kBytes;
+    const float d = f16_to_f32(blk[208] | (blk[209] << 8));
+    const uint8_t *ql = blk + 64 * h + 32 * (k & 1);
+    const uint8_t *qh = blk + 128 + 32 * h;
+    const int8_t *scl = reinterpret_cast<const int8_t *>(blk + 192 + 8 * h + 2 * k);
+    const int nshift = (k >= 2) ? 4 : 0;
+    float *o = dst + b * 256 + 32 * g;
+    for (int l = 0; l < 32; l += 4) {
+        float r[4];
+        for (int u = 0; u < 4; u++) {
+            const int ll = l + u;
+            const int q = (((ql[ll] >> nshift) & 15) | (((qh[ll] >> (2 * k)) & 3) << 4)) - 32;
+            r[u] = d * (float)scl[ll >> 4] * (float)q;
+        }
+        *reinterpret_cast<float4 *>(o + l) = make_float4(r[0], r[1], r[2], r[3]);
+    }
+}
+
+// One thread per Q8_0 block: q8_0.rs:44-60.
+__global__ __launch_bounds__(256) void k_dequant_q8_0(const uint8_t *__restrict__ src,
+                                                      float *__restrict__ dst, size_t n_blocks) {
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_blocks) return;
+    const uint8_t *blk = src + b * kQ8Bytes;
+    const float d = f16_to_f32(blk[0] | (blk[1] << 8));
+    float *o = dst + b * 32;
+    for (int j = 0; j < 32; j += 4) {
+        float4 v;
+        v.x = (float)(int8_t)blk[2 + j] * d;
+        v.y = (float)(int8_t)blk[3 + j] * d;
+        v.z = (float)(int8_t)blk[4 + j] * d;
+        v.w = (float)(int8_t)blk[5 + j] * d;
+        *reinterpret_cast<float4 *>(o + j) = v;
+    }
+}
+
+// One thread per Q4_0 block: q4_0.rs:47-61.
+__global__ __launch_bounds__(256) void k_dequant_q4_0(const uint8_t *__restrict__ src,
+                                                      float *__restrict__ dst, size_t n_blocks) {
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_blocks) return;
+    const uint8_t *blk = src + b * 18;
+    const float d = f16_to_f32(blk[0] | (blk[1] << 8));
+    float *o = dst + b * 32;
+    for (int j = 0; j < 16; j++) {
+        const int x0 = (blk[2 + j] & 15) - 8;
+        const int x1 = (blk[2 + j] >> 4) - 8;
+        o[j] = (float)x0 * d;
+        o[j + 16] = (float)x1 * d;
+    }
+}
+
+// F32 / F16 / BF16 arms (float.rs): element-wise widening.
+__global__ __launch_bounds__(256) void k_dequant_float(const uint8_t *__restrict__ src,
+                                                       float *__restrict__ dst, size_t n,
+                                                       uint32_t dtype) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    if (dtype == T_F32) {
+        const uint8_t *p = src + 4 * i;
+        const uint32_t u = p[0] | (p[1] << 8) | (p[2] << 16) | ((uint32_t)p[3] << 24);
+        dst[i] = __builtin_bit_cast(float, u);
+    } else if (dtype == T_F16) {
+        dst[i] = f16_to_f32(src[2 * i] | (src[2 * i + 1] << 8));
+    } else {
+        const uint32_t u = ((uint32_t)(src[2 * i] | (src[2 * i + 1] << 8))) << 16;
+        dst[i] = __builtin_bit_cast(float, u);
+    }
+}
+
+#pragma clang fp contract(on)
+
+// ---- device layout ---------------------------------------------------------
+// Q4_K: GGUF bytes unchanged (144-byte blocks and rows are 16-byte aligned).
+// Q6_K, Q8_0, Q4_0: the matrix (rows x nb blocks) is split into field planes
+// of the same total size, each plane row-major over (row, block):
+//   Q6_K: [ql rows*nb*128 | qh rows*nb*64 | scales rows*nb*16 | d rows*nb*2]
+//   Q8_0: [qs rows*nb*32 | d rows*nb*2]
+//   Q4_0: [qs rows*nb*16 | d rows*nb*2]
+// so every 16-byte lane load is naturally aligned whatever nb is.
+// One thread per block; GGUF blocks are 2-byte aligned, read as u16.
+__global__ __launch_bounds__(256) void k_prepare_q6k(const uint8_t *__restrict__ src,
+                                                     uint8_t *__restrict__ dst, size_t n_blocks) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_blocks) return;
+    const uint16_t *s = reinterpret_cast<const uint16_t *>(src + i * kQ6kBytes);
+    uint16_t *ql = reinterpret_cast<uint16_t *>(dst + i * 128);
+    uint16_t *qh = reinterpret_cast<uint16_t *>(dst + n_blocks * 128 + i * 64);
+    uint16_t *sc = reinterpret_cast<uint16_t *>(dst + n_blocks * 192 + i * 16);
+    uint16_t *dd = reinterpret_cast<uint16_t *>(dst + n_blocks * 208 + i * 2);
+    for (int k = 0; k < 64; k++) ql[k] = s[k];
+    for (int k = 0; k < 32; k++) qh[k] = s[64 + k];
+    for (int k = 0; k < 8; k++) sc[k] = s[96 + k];
+    dd[0] = s[104];
+}
+
+// Q8_0 (block_bytes 34) and Q4_0 (18): [d | qs] -> qs plane + d plane.
+__global__ __launch_bounds__(256) void k_prepare_q8_0(const uint8_t *__restrict__ src,
+                                                      uint8_t *__restrict__ dst, size_t n_blocks,
+                                                      int block_bytes) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_blocks) return;
+    const int qbytes = block_bytes - 2;
+    const uint16_t *s = reinterpret_cast<const uint16_t *>(src + i * block_bytes);
+    uint16_t *qs = reinterpret_cast<uint16_t *>(dst + i * qbytes);
+    uint16_t *dd = reinterpret_cast<uint16_t *>(dst + n_blocks * qbytes + i * 2);
+    for (int k = 0; k < qbytes / 2; k++) qs[k] = s[1 + k];
+    dd[0] = s[0];
+}
+
+static inline unsigned grid_for(size_t n, unsigned bs) { return (unsigned)((n + bs - 1) / bs); }
+
+hipError_t launch_dequant(uint32_t dtype, const uint8_t *src, float *dst, size_t n_elems,
+                          hipStream_t s) {
+    if (n_elems == 0) return hipSuccess;
+    switch (dtype) {
+    case T_Q4_K:
+        k_dequant_q4k<<<grid_for(n_elems / 256 * 8, 256), 256, 0, s>>>(src, dst, n_elems / 256);
+        break;
+    case T_Q6_K:
+        k_dequant_q6k<<<grid_for(n_elems / 256 * 8, 256), 256, 0, s>>>(src, dst, n_elems / 256);
+        break;
+    case T_Q8_0:
+        k_dequant_q8_0<<<grid_for(n_elems / 32, 256), 256, 0, s>>>(src, dst, n_elems / 32);
+        break;
+    case T_Q4_0:
+        k_dequant_q4_0<<<grid_for(n_elems / 32, 256), 256, 0, s>>>(src, dst, n_elems / 32);
+        break;
+    case T_F32:
+    case T_F16:
+    case T_BF16:
+        k_dequant_float<<<grid_for(n_elems, 256), 256, 0, s>>>(src, dst, n_elems, dtype);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_prepare(uint32_t dtype, const uint8_t *src, uint8_t *dst, size_t rows,
+                          size_t in_dim, hipStream_t s) {
+    const size_t bytes = rows * row_bytes_of(dtype, in_dim);
+    if (bytes == 0) return hipSuccess;
+    const size_t n_blocks = rows * (in_dim / block_elems_of(dtype));
+    switch (dtype) {
+    case T_Q4_K:
+        if (src != dst) return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
+        return hipSuccess;
+    case T_Q6_K:
+        k_prepare_q6k<<<grid_for(n_blocks, 256), 256, 0, s>>>(src, dst, n_blocks);
+        break;
+    case T_Q8_0:
+        k_prepare_q8_0<<<grid_for(n_blocks, 256), 256, 0, s>>>(src, dst, n_blocks, 34);
+        break;
+    case T_Q4_0:
+        k_prepare_q8_0<<<grid_for(n_blocks, 256), 256, 0, s>>>(src, dst, n_blocks, 18);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace rsllm_hip

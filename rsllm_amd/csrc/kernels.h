@@ -1,0 +1,53 @@
+// Host-side launchers of the gfx950 kernels. Every launcher enqueues on the
+// given stream and returns the launch status; shapes are validated by the
+// C-ABI layer (abi.hip) before any launcher is called.
+#pragma once
+
+#include "common.h"
+
+namespace rsllm_hip {
+
+inline size_t block_elems_of(uint32_t t) {
+    switch (t) {
+    case T_F32: case T_F16: case T_BF16: return 1;
+    case T_Q4_0: case T_Q8_0: return 32;
+    case T_Q2_K: case T_Q4_K: case T_Q6_K: case T_IQ2_XXS: return 256;
+    default: return 0;
+    }
+}
+
+inline size_t block_bytes_of(uint32_t t) {
+    switch (t) {
+    case T_F32: return 4;
+    case T_F16: case T_BF16: return 2;
+    case T_Q4_0: return 18;
+    case T_Q8_0: return 34;
+    case T_Q2_K: return 84;
+    case T_Q4_K: return 144;
+    case T_Q6_K: return 210;
+    case T_IQ2_XXS: return 66;
+    default: return 0;
+    }
+}
+
+inline size_t row_bytes_of(uint32_t t, size_t in_dim) {
+    const size_t be = block_elems_of(t);
+    return be ? in_dim / be * block_bytes_of(t) : 0;
+}
+
+// dequant.hip
+hipError_t launch_dequant(uint32_t dtype, const uint8_t *src, float *dst, size_t n_elems,
+                          hipStream_t s);
+// GGUF rows -> device layout (dst must not alias src, except for Q4_K).
+hipError_t launch_prepare(uint32_t dtype, const uint8_t *src, uint8_t *dst, size_t rows,
+                          size_t in_dim, hipStream_t s);
+
+// gemv.hip: y[t, o] = sum_i W[o, i] x[t, i] for t < n_tok, W in device layout.
+hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, const float *x, float *y, int n_tok,
+                       int in_dim, int out_dim, hipStream_t s);
+
+// Fill n floats with zero (used for in_dim == 0; no hipMemset so the call
+// stays capturable into a graph).
+hipError_t launch_fill_zero(float *y, size_t n, hipStream_t s);
+
+}  // namespace rsllm_hip

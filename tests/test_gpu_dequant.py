@@ -1,0 +1,107 @@
+"""Dequantisation on the GPU is bit-exact with the oracle (the reference's
+dequant_to_f32, rsllm-gguf/src/dequant/mod.rs:69-85) — on every block of the
+benchmark configs and on blocks with special f16 scales."""
+import numpy as np
+import pytest
+
+from rsllm_amd import synth
+from rsllm_amd.ggml import GgmlType as G
+
+pytestmark = pytest.mark.gpu
+
+# Special f16 scale patterns: zero, -0, smallest subnormal, largest
+# subnormal, smallest normal, 1.0, max finite, -max, +inf, -inf, qNaN.
+SPECIAL_F16 = [0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x3C00, 0x7BFF, 0xFBFF, 0x7C00, 0xFC00,
+               0x7E00]
+
+
+def assert_bits_equal(got: np.ndarray, want: np.ndarray):
+    assert got.shape == want.shape
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn), "NaN positions differ"
+    g, w = got[~gn].view(np.uint32), want[~wn].view(np.uint32)
+    bad = np.nonzero(g != w)[0]
+    assert bad.size == 0, f"{bad.size} elements differ, first at {bad[:5]}: {got[~gn][bad[:5]]} vs {want[~wn][bad[:5]]}"
+
+
+def special_blocks(dtype, n_per=4, seed=7):
+    be, bb = {G.Q4_K: (256, 144), G.Q6_K: (256, 210), G.Q8_0: (32, 34)}[dtype]
+    blocks = synth.weight(dtype, len(SPECIAL_F16) * n_per, be, seed).reshape(-1, bb).copy()
+    for i, pat in enumerate(SPECIAL_F16):
+        for r in range(n_per):
+            row = blocks[i * n_per + r]
+            lo, hi = pat & 0xFF, pat >> 8
+            if dtype == G.Q4_K:
+                row[0], row[1] = lo, hi                          # d
+                p2 = SPECIAL_F16[(i + r + 1) % len(SPECIAL_F16)]
+                row[2], row[3] = p2 & 0xFF, p2 >> 8              # dmin
+            elif dtype == G.Q6_K:
+                row[208], row[209] = lo, hi
+            else:
+                row[0], row[1] = lo, hi
+    return blocks.reshape(-1)
+
+
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0])
+def test_dequant_special_scales_bit_exact(oracle, hip, dtype):
+    src = special_blocks(dtype)
+    n = src.size // dtype.block_bytes() * dtype.block_elements()
+    rc, want = oracle.dequant(int(dtype), src, n)
+    assert rc == 0
+    got = np.empty(n, np.float32)
+    hip.dequant_to_f32(dtype, src, got)
+    assert_bits_equal(got, want)
+
+
+# (dtype, out_dim, in_dim) of every benchmark weight matrix.
+CONFIG_MATRICES = [
+    (G.Q4_K, 4096, 4096),     # C0
+    (G.Q6_K, 14336, 4096),    # C1
+    (G.Q6_K, 4096, 14336),    # C1
+    (G.Q8_0, 4096, 4096),     # C2 Q/O
+    (G.Q8_0, 1024, 4096),     # C2 K/V
+    (G.Q4_K, 2048, 7168),     # C3 gate/up (one expert)
+    (G.Q4_K, 7168, 2048),     # C3 down (one expert)
+    (G.Q4_K, 14336, 4096),    # C4
+]
+
+
+@pytest.mark.parametrize("dtype,out_dim,in_dim", CONFIG_MATRICES)
+def test_dequant_config_matrix_bit_exact(oracle, hip, dtype, out_dim, in_dim):
+    src = synth.weight(dtype, out_dim, in_dim, seed=1000 + out_dim + in_dim)
+    n = out_dim * in_dim
+    rc, want = oracle.dequant(int(dtype), src, n)
+    assert rc == 0
+    got = np.empty(n, np.float32)
+    hip.dequant_to_f32(dtype, src, got)
+    assert_bits_equal(got, want)
+    # f16-subnormal scales are present in this data (about 5% of blocks).
+    if dtype in (G.Q4_K, G.Q6_K):
+        off = 0 if dtype == G.Q4_K else 208
+        d = src.reshape(-1, dtype.block_bytes())[:, off:off + 2].copy().view(np.uint16).reshape(-1)
+        assert ((d & 0x7C00) == 0).mean() > 0.01
+
+
+@pytest.mark.parametrize("dtype", [G.F32, G.F16, G.BF16, G.Q4_0])
+def test_dequant_other_arms_bit_exact(oracle, hip, dtype):
+    g = synth.rng(5)
+    n = 4096
+    src = g.integers(0, 256, size=dtype.byte_size(n), dtype=np.uint8)
+    rc, want = oracle.dequant(int(dtype), src, n)
+    assert rc == 0
+    got = np.empty(n, np.float32)
+    hip.dequant_to_f32(dtype, src, got)
+    assert_bits_equal(got, want)
+
+
+def test_dequant_dev_entry_point(oracle, hip):
+    import torch
+    src = synth.weight(G.Q6_K, 64, 512, seed=3)
+    n = 64 * 512
+    rc, want = oracle.dequant(int(G.Q6_K), src, n)
+    d_src = torch.from_numpy(src).cuda()
+    d_dst = torch.empty(n, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    hip.dequant_to_f32_dev(G.Q6_K, d_src.data_ptr(), src.size, d_dst.data_ptr(), n, stream)
+    torch.cuda.synchronize()
+    assert_bits_equal(d_dst.cpu().numpy(), want)

@@ -1,0 +1,91 @@
+"""GEMV / matmul_quant_f32 on the GPU against the oracle (the reference's
+matmul_quant_f32, backend-cpu/src/ops/quant_matmul.rs:45-119): max|Δ|/max|y|
+<= 1e-3 (REL_TOL) on seeded inputs, ragged shapes, every benchmark shape."""
+import numpy as np
+import pytest
+
+from conftest import REL_TOL, rel_err
+from rsllm_amd import synth
+from rsllm_amd.ggml import GgmlType as G
+
+pytestmark = pytest.mark.gpu
+
+
+def run_both(oracle, hip, dtype, out_dim, in_dim, n_tok, seed):
+    w = synth.weight(dtype, out_dim, in_dim, seed)
+    x = synth.activations(n_tok, in_dim, seed + 1).reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, x, n_tok, in_dim, out_dim, int(dtype), allow_q6k=True)
+    assert rc == 0
+    got = np.full(n_tok * out_dim, np.nan, np.float32)
+    hip.matmul_quant_f32(got, w, x, n_tok, in_dim, out_dim, dtype)
+    return got, want
+
+
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q4_0])
+@pytest.mark.parametrize("out_dim,in_dim", [(1, 256), (7, 512), (33, 768), (100, 2048), (257, 1280)])
+@pytest.mark.parametrize("n_tok", [1, 2, 3, 5, 8, 13])
+def test_gemv_ragged_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
+    got, want = run_both(oracle, hip, dtype, out_dim, in_dim, n_tok, seed=out_dim * 31 + n_tok)
+    assert not np.isnan(got).any()
+    assert rel_err(got, want) <= REL_TOL
+
+
+# Benchmark shapes at full size (BASELINE configs C0-C2).
+@pytest.mark.parametrize("dtype,out_dim,in_dim,n_tok", [
+    (G.Q4_K, 4096, 4096, 1),
+    (G.Q6_K, 14336, 4096, 1), (G.Q6_K, 14336, 4096, 4), (G.Q6_K, 14336, 4096, 8),
+    (G.Q6_K, 4096, 14336, 1), (G.Q6_K, 4096, 14336, 4), (G.Q6_K, 4096, 14336, 8),
+    (G.Q8_0, 4096, 4096, 1), (G.Q8_0, 4096, 4096, 2), (G.Q8_0, 4096, 4096, 4),
+    (G.Q8_0, 4096, 4096, 8), (G.Q8_0, 4096, 4096, 16), (G.Q8_0, 4096, 4096, 32),
+    (G.Q8_0, 1024, 4096, 1), (G.Q8_0, 1024, 4096, 32),
+])
+def test_gemv_config_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
+    got, want = run_both(oracle, hip, dtype, out_dim, in_dim, n_tok, seed=11)
+    err = rel_err(got, want)
+    print(f"{dtype.name} {out_dim}x{in_dim} B={n_tok}: rel err {err:.3e}")
+    assert err <= REL_TOL
+
+
+def test_registered_weights_path(oracle, hip):
+    dtype, out_dim, in_dim = G.Q6_K, 300, 1024
+    w = synth.weight(dtype, out_dim, in_dim, 3)
+    x = synth.activations(2, in_dim, 4).reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, x, 2, in_dim, out_dim, int(dtype))
+    hip.register_weights(w, dtype, in_dim)
+    try:
+        got = np.empty(2 * out_dim, np.float32)
+        hip.matmul_quant_f32(got, w, x, 2, in_dim, out_dim, dtype)
+        assert rel_err(got, want) <= REL_TOL
+    finally:
+        hip.release_weights()
+
+
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0])
+def test_dev_entry_point_matches_host(oracle, hip, dtype):
+    import torch
+    out_dim, in_dim, n_tok = 129, 2048, 3
+    w = synth.weight(dtype, out_dim, in_dim, 9)
+    x = synth.activations(n_tok, in_dim, 10).reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, x, n_tok, in_dim, out_dim, int(dtype))
+    d_raw = torch.from_numpy(w).cuda()
+    d_w = torch.empty_like(d_raw)
+    d_x = torch.from_numpy(x).cuda()
+    d_y = torch.full((n_tok * out_dim,), float("nan"), device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    hip.prepare_weights_dev(d_w.data_ptr(), d_raw.data_ptr(), w.size, dtype, in_dim, s)
+    hip.matmul_quant_f32_dev(d_y.data_ptr(), d_y.numel(), d_w.data_ptr(), w.size, d_x.data_ptr(),
+                             x.size, n_tok, in_dim, out_dim, dtype, s)
+    torch.cuda.synchronize()
+    assert rel_err(d_y.cpu().numpy(), want) <= REL_TOL
+
+
+def test_in_dim_zero_gives_zeros(hip):
+    out = np.full(6, np.nan, np.float32)
+    hip.matmul_quant_f32(out, np.zeros(0, np.uint8), np.zeros(0, np.float32), 2, 0, 3, G.Q4_K)
+    assert np.array_equal(out, np.zeros(6, np.float32))
+
+
+def test_n_tok_zero_is_noop(hip):
+    w = synth.weight(G.Q8_0, 4, 64, 1)
+    out = np.zeros(0, np.float32)
+    hip.matmul_quant_f32(out, w, np.zeros(0, np.float32), 0, 64, 4, G.Q8_0)
