@@ -82,7 +82,7 @@ struct DevBuf {
 struct ThreadCtx {
     int device = -1;
     hipStream_t stream = nullptr;
-    DevBuf w_raw, w_dev, x, y;
+    DevBuf w_raw, w_dev, x, y, xq;
 };
 thread_local ThreadCtx t_ctx;
 
@@ -145,6 +145,9 @@ int validate_matmul(size_t out_len, const void *w, size_t w_len, const void *x, 
                        "the HIP backend");
     if (!fits_int(n_tok) || !fits_int(in_dim) || !fits_int(out_dim))
         return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "matmul_quant_f32: dimension exceeds 2^31-1");
+    if (w_len > kMaxWeightBytes)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_quant_f32: weight tensors above 4 GiB are not supported");
     return RSLLM_HIP_OK;
 }
 
@@ -250,7 +253,11 @@ int rsllm_hip_matmul_quant_f32_dev(float *out, size_t out_len, const uint8_t *we
         HIP_TRY(launch_fill_zero(out, out_len, s), "fill_zero");
         return ok();
     }
-    HIP_TRY(launch_gemv(dtype, weights, x, out, (int)n_tok, (int)in_dim, (int)out_dim, s), "gemv");
+    if ((rc = ensure_device())) return rc;
+    HIP_TRY(t_ctx.xq.ensure(gemv_scratch_bytes(dtype, (int)n_tok, (int)in_dim)), "hipMalloc");
+    HIP_TRY(launch_gemv(dtype, weights, weights_len, x, (uint8_t *)t_ctx.xq.p, out, (int)n_tok,
+                        (int)in_dim, (int)out_dim, s),
+            "gemv");
     return ok();
 }
 
@@ -285,12 +292,62 @@ int rsllm_hip_matmul_quant_f32(float *out, size_t out_len, const uint8_t *weight
     HIP_TRY(c.y.ensure(out_len * sizeof(float)), "hipMalloc");
     HIP_TRY(hipMemcpyAsync(c.x.p, x, x_len * sizeof(float), hipMemcpyHostToDevice, c.stream),
             "upload x");
-    HIP_TRY(launch_gemv(dtype, dw, (const float *)c.x.p, (float *)c.y.p, (int)n_tok, (int)in_dim,
-                        (int)out_dim, c.stream),
+    HIP_TRY(c.xq.ensure(gemv_scratch_bytes(dtype, (int)n_tok, (int)in_dim)), "hipMalloc");
+    HIP_TRY(launch_gemv(dtype, dw, weights_len, (const float *)c.x.p, (uint8_t *)c.xq.p,
+                        (float *)c.y.p, (int)n_tok, (int)in_dim, (int)out_dim, c.stream),
             "gemv");
     HIP_TRY(hipMemcpyAsync(out, c.y.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
             "download out");
     HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    return ok();
+}
+
+size_t rsllm_hip_xq_bytes(uint32_t dtype, size_t n_tok, size_t in_dim) {
+    if (!matmul_dtype_impl(dtype) || !fits_int(n_tok) || !fits_int(in_dim)) return 0;
+    return gemv_scratch_bytes(dtype, (int)n_tok, (int)in_dim);
+}
+
+int rsllm_hip_quantize_x_dev(uint32_t dtype, const float *x, size_t x_len, size_t n_tok,
+                             size_t in_dim, uint8_t *xq, size_t xq_len, rsllm_hip_stream_t stream) {
+    if (!matmul_dtype_impl(dtype))
+        return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED, "quantize_x: dtype not implemented");
+    const size_t be = block_elems_of(dtype);
+    if (in_dim % be != 0)
+        return set_err(RSLLM_HIP_ERR_NOT_BLOCK_ALIGNED, "`in_dim` is not a multiple of the block",
+                       "in_dim", in_dim, be);
+    size_t need;
+    if (!mul_ok(n_tok, in_dim, &need) || x_len != need || !fits_int(n_tok) || !fits_int(in_dim))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "quantize_x: x must be n_tok * in_dim");
+    if (xq_len != rsllm_hip_xq_bytes(dtype, n_tok, in_dim))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "quantize_x: xq must be rsllm_hip_xq_bytes");
+    if ((x_len && !x) || (xq_len && !xq))
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "NULL pointer with a nonzero length");
+    HIP_TRY(launch_quantize_x(dtype, x, xq, (int)n_tok, (int)in_dim, (hipStream_t)stream),
+            "quantize_x");
+    return ok();
+}
+
+int rsllm_hip_matmul_prequant_dev(float *out, size_t out_len, const uint8_t *weights,
+                                  size_t weights_len, const uint8_t *xq, size_t xq_len,
+                                  size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype,
+                                  rsllm_hip_stream_t stream) {
+    // Same validation as matmul_quant_f32 with the x length check replaced.
+    size_t x_len_equiv;
+    if (!mul_ok(n_tok, in_dim, &x_len_equiv)) x_len_equiv = 0;
+    int rc = validate_matmul(out_len, weights, weights_len, xq, x_len_equiv, out, n_tok, in_dim,
+                             out_dim, dtype);
+    if (rc) return rc;
+    if (xq_len != rsllm_hip_xq_bytes(dtype, n_tok, in_dim) || (xq_len && !xq))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "matmul_prequant: xq must be rsllm_hip_xq_bytes");
+    hipStream_t s = (hipStream_t)stream;
+    if (n_tok == 0) return ok();
+    if (in_dim == 0) {
+        HIP_TRY(launch_fill_zero(out, out_len, s), "fill_zero");
+        return ok();
+    }
+    HIP_TRY(launch_gemv_prequant(dtype, weights, weights_len, xq, out, (int)n_tok, (int)in_dim,
+                                 (int)out_dim, s),
+            "gemv");
     return ok();
 }
 

@@ -35,6 +35,19 @@ __device__ __forceinline__ float ubyte_f(uint32_t v, int b) {
     return (float)((v >> (8 * b)) & 0xFFu);
 }
 
+// Dword i (0..3) of a uint4 without indexing a local array (a runtime index
+// into an array would be placed in scratch memory).
+__device__ __forceinline__ uint32_t sel4(const uint4 &v, int i) {
+    const uint32_t a = (i & 1) ? v.y : v.x;
+    const uint32_t b = (i & 1) ? v.w : v.z;
+    return (i & 2) ? b : a;
+}
+
+// Signed byte i (0..15) of a uint4.
+__device__ __forceinline__ int sbyte16(const uint4 &v, int i) {
+    return (int)(int8_t)(sel4(v, i >> 2) >> (8 * (i & 3)));
+}
+
 // (sc, m) of Q4_K sub-block j from the three scale dwords s0 = bytes 0-3,
 // s1 = bytes 4-7, s2 = bytes 8-11 (q4_k_scale_min, dequant/mod.rs:48-58).
 __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2,

@@ -127,38 +127,47 @@ __global__ __launch_bounds__(256) void k_dequant_float(const uint8_t *__restrict
 
 // ---- device layout ---------------------------------------------------------
 // Q4_K: GGUF bytes unchanged (144-byte blocks and rows are 16-byte aligned).
-// Q6_K, Q8_0, Q4_0: the matrix (rows x nb blocks) is split into field planes
-// of the same total size, each plane row-major over (row, block):
-//   Q6_K: [ql rows*nb*128 | qh rows*nb*64 | scales rows*nb*16 | d rows*nb*2]
-//   Q8_0: [qs rows*nb*32 | d rows*nb*2]
-//   Q4_0: [qs rows*nb*16 | d rows*nb*2]
-// so every 16-byte lane load is naturally aligned whatever nb is.
+// Q6_K, Q8_0, Q4_0: blocks are taken 8 at a time in matrix order (row-major
+// over (row, block)) and each group of r <= 8 blocks becomes one contiguous
+// super-tile with the fields split out:
+//   Q6_K [ql r*128 | qh r*64 | scales r*16 | d r*2]   (8 blocks = 1680 B)
+//   Q8_0 [qs r*32 | d r*2]                             (8 blocks =  272 B)
+//   Q4_0 [qs r*16 | d r*2]                             (8 blocks =  144 B)
+// r = 8 except in the last super-tile of the matrix. The total size equals
+// the GGUF size, every field offset is a multiple of 16 (2 for d), and a
+// wavefront reading 8 consecutive blocks reads one contiguous region.
 // One thread per block; GGUF blocks are 2-byte aligned, read as u16.
 __global__ __launch_bounds__(256) void k_prepare_q6k(const uint8_t *__restrict__ src,
                                                      uint8_t *__restrict__ dst, size_t n_blocks) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_blocks) return;
+    const size_t S = i >> 3, j = i & 7;
+    const size_t r = (S < (n_blocks >> 3)) ? 8 : (n_blocks & 7);
+    uint8_t *st = dst + S * 1680;
     const uint16_t *s = reinterpret_cast<const uint16_t *>(src + i * kQ6kBytes);
-    uint16_t *ql = reinterpret_cast<uint16_t *>(dst + i * 128);
-    uint16_t *qh = reinterpret_cast<uint16_t *>(dst + n_blocks * 128 + i * 64);
-    uint16_t *sc = reinterpret_cast<uint16_t *>(dst + n_blocks * 192 + i * 16);
-    uint16_t *dd = reinterpret_cast<uint16_t *>(dst + n_blocks * 208 + i * 2);
+    uint16_t *ql = reinterpret_cast<uint16_t *>(st + j * 128);
+    uint16_t *qh = reinterpret_cast<uint16_t *>(st + r * 128 + j * 64);
+    uint16_t *sc = reinterpret_cast<uint16_t *>(st + r * 192 + j * 16);
+    uint16_t *dd = reinterpret_cast<uint16_t *>(st + r * 208 + j * 2);
     for (int k = 0; k < 64; k++) ql[k] = s[k];
     for (int k = 0; k < 32; k++) qh[k] = s[64 + k];
     for (int k = 0; k < 8; k++) sc[k] = s[96 + k];
     dd[0] = s[104];
 }
 
-// Q8_0 (block_bytes 34) and Q4_0 (18): [d | qs] -> qs plane + d plane.
+// Q8_0 (block_bytes 34) and Q4_0 (18): [d | qs] -> super-tile [qs... | d...].
 __global__ __launch_bounds__(256) void k_prepare_q8_0(const uint8_t *__restrict__ src,
                                                       uint8_t *__restrict__ dst, size_t n_blocks,
                                                       int block_bytes) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_blocks) return;
     const int qbytes = block_bytes - 2;
+    const size_t S = i >> 3, j = i & 7;
+    const size_t r = (S < (n_blocks >> 3)) ? 8 : (n_blocks & 7);
+    uint8_t *st = dst + S * 8 * block_bytes;
     const uint16_t *s = reinterpret_cast<const uint16_t *>(src + i * block_bytes);
-    uint16_t *qs = reinterpret_cast<uint16_t *>(dst + i * qbytes);
-    uint16_t *dd = reinterpret_cast<uint16_t *>(dst + n_blocks * qbytes + i * 2);
+    uint16_t *qs = reinterpret_cast<uint16_t *>(st + j * qbytes);
+    uint16_t *dd = reinterpret_cast<uint16_t *>(st + r * qbytes + j * 2);
     for (int k = 0; k < qbytes / 2; k++) qs[k] = s[1 + k];
     dd[0] = s[0];
 }

@@ -1,299 +1,365 @@
 // Quantized GEMV, batch 1..n: y[t, o] = sum_i deq(W)[o, i] * x[t, i].
 //
 // Restates matmul_quant_f32 (rsllm-backend-cpu/src/ops/quant_matmul.rs:45-119)
-// without materialising dequantised rows: each lane decodes its 16-byte
-// slice of a block in registers and folds the block scales out of the inner
-// sum, e.g. for Q4_K sub-block j
-//     sum_l (d*sc_j*q_l - dmin*m_j) x_l = (d*sc_j) sum_l q_l x_l - (dmin*m_j) sum_l x_l.
-// Products and sums are fp32; only the summation order differs from the
-// reference's sequential dot.
+// without materialising dequantised rows.
 //
-// Work split: a workgroup is 4 wavefronts; a wavefront owns R consecutive
-// rows and BT consecutive tokens. Within a wavefront, 8 lanes share one
-// block (one 16-byte load each, fully coalesced: 64 lanes read 8 whole
-// blocks = 1152 contiguous bytes for Q4_K) and the 8 lane groups stride over
-// the row's blocks. The per-lane partials are combined with a wavefront
-// butterfly at the end.
+// Arithmetic. x is first re-expressed per 16-element group g as
+//     x~_i = s_g * (128 * h_i + l_i),  h in [-127, 127], l in [-64, 64] (int8),
+//     s_g = amax_g / 16256,  |x_i - x~_i| <= s_g / 2 = amax_g / 32512,
+// i.e. about 15 bits relative to the group's largest element. A lane decodes
+// a 16-byte slice of quantised weights to small integers (Q4_K 0..15,
+// Q6_K 0..63, Q4_0 0..15, Q8_0 -128..127) and dots them with both limbs using
+// v_dot4_i32_i8 (4 exact int8 MACs per instruction, exact int32 sums). Each
+// 16-element partial is then scaled once in fp32:
+//     Q4_K  (d*sc_j) * s_g * (128 H + L) - (dmin*m_j) * sum_g x
+//     Q6_K  (d*sc_e) * (s_g * (128 H + L) - 32 * sum_g x)
+//     Q8_0  d * s_g * (128 H + L)
+//     Q4_0  d * (s_g * (128 H + L) - 8 * sum_g x)
+// (sum_g x is the fp32 sum of the original x over the group). Only the
+// limb representation of x and the summation order differ from the
+// reference; the output error is far inside the 1e-3 budget.
+//
+// Shape. The kernel streams: a wavefront owns RT rows x one K column of 8
+// units (a unit is 128 bytes of quantised payload read by 8 lanes with one
+// 16-byte load each: one super-block for Q4_K/Q6_K, 4 blocks for Q8_0, 8
+// blocks for Q4_0), issues every load of the column at once, computes, and
+// the wavefronts of a workgroup (one per column, up to 16) combine their
+// per-row partials through LDS. Weight loads are raw buffer loads, and the
+// activation limbs are stored lane-major by the pre-pass so a wavefront's
+// activation loads are contiguous 1 KB reads as well.
 #include "kernels.h"
 
 namespace rsllm_hip {
 
-__device__ __forceinline__ void load16f(const float *__restrict__ p, float (&v)[16]) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float4 f = *reinterpret_cast<const float4 *>(p + 4 * i);
-        v[4 * i + 0] = f.x;
-        v[4 * i + 1] = f.y;
-        v[4 * i + 2] = f.z;
-        v[4 * i + 3] = f.w;
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+__device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    // word 3 = 0x00020000: the raw-buffer configuration of the gfx9 family
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
+}
+
+// 128 * sum(q . h) + sum(q . l) over one 16-element group, exact in int32
+// (|q| <= 128, |h| <= 127, |l| <= 64).
+__device__ __forceinline__ int dot16_limbs(const uint32_t (&q)[4], const uint4 &h, const uint4 &l) {
+    int ah = 0, al = 0;
+    ah = __builtin_amdgcn_sdot4((int)q[0], (int)h.x, ah, false);
+    al = __builtin_amdgcn_sdot4((int)q[0], (int)l.x, al, false);
+    ah = __builtin_amdgcn_sdot4((int)q[1], (int)h.y, ah, false);
+    al = __builtin_amdgcn_sdot4((int)q[1], (int)l.y, al, false);
+    ah = __builtin_amdgcn_sdot4((int)q[2], (int)h.z, ah, false);
+    al = __builtin_amdgcn_sdot4((int)q[2], (int)l.z, al, false);
+    ah = __builtin_amdgcn_sdot4((int)q[3], (int)h.w, ah, false);
+    al = __builtin_amdgcn_sdot4((int)q[3], (int)l.w, al, false);
+    return ah * 128 + al;
+}
+
+// Activation limbs of one lane: groups "lo" and "hi" (see each format for
+// which elements they are). meta = (s_lo, sum_lo, s_hi, sum_hi).
+struct XSlice {
+    uint4 hlo, hhi, llo, lhi, meta;
+};
+
+// ---- formats ------------------------------------------------------------------
+// Each format gives: kEPU (elements per unit), kXF (activation fields per
+// lane: 5 = two groups, 3 = one group), units(in_dim), the element ranges of
+// a lane's groups, valid(), load() of a weight slice, dot().
+
+// Q4_K, GGUF layout. Lane (ks, k) of column c reads block u = 8c + ks: the
+// header (d, dmin, 12 scale bytes) and qs bytes 16k..16k+15 = elements
+// l = 16*(k&1) + 0..15 of sub-blocks 2p (low nibbles, group "lo") and 2p+1
+// (high nibbles, group "hi"), p = k/2.
+struct FQ4K {
+    static constexpr int kEPU = 256, kXF = 5;
+    struct Slice {
+        uint4 hdr, qs;
+    };
+    __device__ static int units(int in_dim) { return in_dim >> 8; }
+    __device__ static int elem_lo(int unit, int k) { return unit * 256 + 64 * (k >> 1) + 16 * (k & 1); }
+    __device__ static int elem_hi(int unit, int k) { return elem_lo(unit, k) + 32; }
+    __device__ static bool valid(int unit, int, int in_dim) { return unit < (in_dim >> 8); }
+    __device__ static void load(Slice &s, __amdgpu_buffer_rsrc_t r, int row, int unit, int k,
+                                int in_dim, int) {
+        const uint32_t off = ((uint32_t)row * (uint32_t)(in_dim >> 8) + (uint32_t)unit) * 144u;
+        s.hdr = bload16(r, off, 0);
+        s.qs = bload16(r, off + 16u + 16u * k, 0);
     }
+    __device__ static float dot(const Slice &s, int k, const XSlice &x) {
+        const int p = k >> 1;
+        const float d = f16_to_f32(s.hdr.x & 0xFFFFu);
+        const float dmin = f16_to_f32(s.hdr.x >> 16);
+        uint32_t sc, m;
+        q4k_scale_min(2 * p, s.hdr.y, s.hdr.z, s.hdr.w, sc, m);
+        const float dl = d * (float)sc, ml = dmin * (float)m;
+        q4k_scale_min(2 * p + 1, s.hdr.y, s.hdr.z, s.hdr.w, sc, m);
+        const float dh = d * (float)sc, mh = dmin * (float)m;
+        const uint32_t lo[4] = {s.qs.x & 0x0F0F0F0Fu, s.qs.y & 0x0F0F0F0Fu, s.qs.z & 0x0F0F0F0Fu,
+                                s.qs.w & 0x0F0F0F0Fu};
+        const uint32_t hi[4] = {(s.qs.x >> 4) & 0x0F0F0F0Fu, (s.qs.y >> 4) & 0x0F0F0F0Fu,
+                                (s.qs.z >> 4) & 0x0F0F0F0Fu, (s.qs.w >> 4) & 0x0F0F0F0Fu};
+        const float slo = __uint_as_float(x.meta.x), sumlo = __uint_as_float(x.meta.y);
+        const float shi = __uint_as_float(x.meta.z), sumhi = __uint_as_float(x.meta.w);
+        const float plo = (float)dot16_limbs(lo, x.hlo, x.llo) * slo;
+        const float phi = (float)dot16_limbs(hi, x.hhi, x.lhi) * shi;
+        return dl * plo - ml * sumlo + dh * phi - mh * sumhi;
+    }
+};
+
+// Q6_K, super-tile layout. Lane (ks, k) of column c reads block u = 8c + ks:
+// ql bytes 16k..16k+15 (half h = k/4; stride kq = (k&3)/2 in the low nibbles =
+// group "lo", kq+2 in the high nibbles = group "hi"; elements l = 16*(k&1) +
+// 0..15), the 16 qh bytes holding their high bit pairs (bits 2kq and 2kq+4),
+// the block's 16 scales and d. Element e = 128h + 32kq + l uses scale e/16.
+struct FQ6K {
+    static constexpr int kEPU = 256, kXF = 5;
+    struct Slice {
+        uint4 ql, qh, sc;
+        uint32_t d;
+    };
+    __device__ static int units(int in_dim) { return in_dim >> 8; }
+    __device__ static int elem_lo(int unit, int k) {
+        return unit * 256 + 128 * (k >> 2) + 32 * ((k & 3) >> 1) + 16 * (k & 1);
+    }
+    __device__ static int elem_hi(int unit, int k) { return elem_lo(unit, k) + 64; }
+    __device__ static bool valid(int unit, int, int in_dim) { return unit < (in_dim >> 8); }
+    __device__ static void load(Slice &s, __amdgpu_buffer_rsrc_t r, int row, int unit, int k,
+                                int in_dim, int out_dim) {
+        const uint32_t nb = (uint32_t)(in_dim >> 8);
+        const uint32_t nblk = (uint32_t)out_dim * nb;
+        const uint32_t bi = (uint32_t)row * nb + (uint32_t)unit;
+        const uint32_t S = bi >> 3, j = bi & 7;
+        const uint32_t rS = (S < (nblk >> 3)) ? 8u : (nblk & 7u);
+        const uint32_t base = S * 1680u;
+        s.ql = bload16(r, base + j * 128u + 16u * k, 0);
+        s.qh = bload16(r, base + rS * 128u + j * 64u + 32u * (k >> 2) + 16u * (k & 1), 0);
+        s.sc = bload16(r, base + rS * 192u + j * 16u, 0);
+        s.d = bload2(r, base + rS * 208u + j * 2u, 0);
+    }
+    __device__ static float dot(const Slice &s, int k, const XSlice &x) {
+        const int kq = (k & 3) >> 1;
+        const int sci = 8 * (k >> 2) + 2 * kq + (k & 1);  // scale of group "lo"; "hi" uses +4
+        const float d = f16_to_f32(s.d);
+        const float dlo = d * (float)sbyte16(s.sc, sci);
+        const float dhi = d * (float)sbyte16(s.sc, sci + 4);
+        const uint32_t sl = 4 - 2 * kq, sh = 2 * kq;
+        const uint32_t lo[4] = {
+            (s.ql.x & 0x0F0F0F0Fu) | ((s.qh.x << sl) & 0x30303030u),
+            (s.ql.y & 0x0F0F0F0Fu) | ((s.qh.y << sl) & 0x30303030u),
+            (s.ql.z & 0x0F0F0F0Fu) | ((s.qh.z << sl) & 0x30303030u),
+            (s.ql.w & 0x0F0F0F0Fu) | ((s.qh.w << sl) & 0x30303030u)};
+        const uint32_t hi[4] = {
+            ((s.ql.x >> 4) & 0x0F0F0F0Fu) | ((s.qh.x >> sh) & 0x30303030u),
+            ((s.ql.y >> 4) & 0x0F0F0F0Fu) | ((s.qh.y >> sh) & 0x30303030u),
+            ((s.ql.z >> 4) & 0x0F0F0F0Fu) | ((s.qh.z >> sh) & 0x30303030u),
+            ((s.ql.w >> 4) & 0x0F0F0F0Fu) | ((s.qh.w >> sh) & 0x30303030u)};
+        const float plo = (float)dot16_limbs(lo, x.hlo, x.llo) * __uint_as_float(x.meta.x) -
+                          32.f * __uint_as_float(x.meta.y);
+        const float phi = (float)dot16_limbs(hi, x.hhi, x.lhi) * __uint_as_float(x.meta.z) -
+                          32.f * __uint_as_float(x.meta.w);
+        return dlo * plo + dhi * phi;
+    }
+};
+
+// Q8_0 (Q4 = false) and Q4_0 (Q4 = true), super-tile layout.
+// Q8_0: unit = 4 blocks (128 elements); lane (ks, k) reads half k&1 of block
+//       32c + 4ks + k/2: 16 signed weights = one group.
+// Q4_0: unit = 8 blocks (256 elements); lane (ks, k) reads block 64c + 8ks + k:
+//       low nibbles = elements 0..15 (group "lo"), high = 16..31 ("hi"), minus 8.
+template <bool Q4>
+struct FQ8 {
+    static constexpr int kEPU = Q4 ? 256 : 128, kXF = Q4 ? 5 : 3;
+    static constexpr int kQB = Q4 ? 16 : 32, kSTB = Q4 ? 144 : 272;
+    struct Slice {
+        uint4 q;
+        uint32_t d;
+    };
+    __device__ static int units(int in_dim) { return (in_dim + kEPU - 1) / kEPU; }
+    __device__ static int block_of(int unit, int k) { return Q4 ? unit * 8 + k : unit * 4 + (k >> 1); }
+    __device__ static int elem_lo(int unit, int k) { return Q4 ? 32 * block_of(unit, k) : unit * 128 + 16 * k; }
+    __device__ static int elem_hi(int unit, int k) { return elem_lo(unit, k) + 16; }
+    __device__ static bool valid(int unit, int k, int in_dim) { return block_of(unit, k) < (in_dim >> 5); }
+    __device__ static void load(Slice &s, __amdgpu_buffer_rsrc_t r, int row, int unit, int k,
+                                int in_dim, int out_dim) {
+        const uint32_t nb = (uint32_t)(in_dim >> 5);
+        const uint32_t nblk = (uint32_t)out_dim * nb;
+        const uint32_t b = (uint32_t)block_of(unit, k);
+        const uint32_t bi = (uint32_t)row * nb + (b < nb ? b : nb - 1);
+        const uint32_t S = bi >> 3, j = bi & 7;
+        const uint32_t rS = (S < (nblk >> 3)) ? 8u : (nblk & 7u);
+        const uint32_t base = S * (uint32_t)kSTB;
+        s.q = bload16(r, base + j * (uint32_t)kQB + (Q4 ? 0u : 16u * (k & 1)), 0);
+        s.d = bload2(r, base + rS * (uint32_t)kQB + j * 2u, 0);
+    }
+    __device__ static float dot(const Slice &s, int, const XSlice &x) {
+        const float d = f16_to_f32(s.d);
+        if (Q4) {
+            const uint32_t lo[4] = {s.q.x & 0x0F0F0F0Fu, s.q.y & 0x0F0F0F0Fu, s.q.z & 0x0F0F0F0Fu,
+                                    s.q.w & 0x0F0F0F0Fu};
+            const uint32_t hi[4] = {(s.q.x >> 4) & 0x0F0F0F0Fu, (s.q.y >> 4) & 0x0F0F0F0Fu,
+                                    (s.q.z >> 4) & 0x0F0F0F0Fu, (s.q.w >> 4) & 0x0F0F0F0Fu};
+            const float plo = (float)dot16_limbs(lo, x.hlo, x.llo) * __uint_as_float(x.meta.x) -
+                              8.f * __uint_as_float(x.meta.y);
+            const float phi = (float)dot16_limbs(hi, x.hhi, x.lhi) * __uint_as_float(x.meta.z) -
+                              8.f * __uint_as_float(x.meta.w);
+            return d * (plo + phi);
+        }
+        const uint32_t q[4] = {s.q.x, s.q.y, s.q.z, s.q.w};
+        return d * ((float)dot16_limbs(q, x.hlo, x.llo) * __uint_as_float(x.meta.x));
+    }
+};
+
+// ---- activation pre-pass -------------------------------------------------------
+// Per token: ncols columns x kXF fields x 64 lanes x 16 bytes. Fields:
+// 0 h_lo, 1 l_lo, 2 meta (s_lo, sum_lo, s_hi, sum_hi), 3 h_hi, 4 l_hi
+// (kXF = 3 keeps fields 0..2). Groups past in_dim are written as zeros.
+__device__ __forceinline__ void quant_group(const float *__restrict__ x, int e, int in_dim,
+                                            uint4 &h, uint4 &l, float &s, float &sum) {
+    float v[16];
+    if (e >= 0 && e + 16 <= in_dim) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 f = *reinterpret_cast<const float4 *>(x + e + 4 * i);
+            v[4 * i] = f.x;
+            v[4 * i + 1] = f.y;
+            v[4 * i + 2] = f.z;
+            v[4 * i + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = 0.f;
+    }
+    float amax = 0.f;
+    sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
+    }
+    s = amax * (1.0f / 16256.0f);
+    const float inv = amax > 0.f ? 16256.0f / amax : 0.f;
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        uint32_t hh = 0, ll = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float t = v[4 * u + b] * inv;
+            const float hq = fminf(fmaxf(rintf(t * (1.0f / 128.0f)), -127.f), 127.f);
+            const float lq = fminf(fmaxf(rintf(t - 128.f * hq), -64.f), 64.f);
+            hh |= ((uint32_t)(int32_t)hq & 0xFFu) << (8 * b);
+            ll |= ((uint32_t)(int32_t)lq & 0xFFu) << (8 * b);
+        }
+        hw[u] = hh;
+        lw[u] = ll;
+    }
+    h = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    l = make_uint4(lw[0], lw[1], lw[2], lw[3]);
 }
 
-__device__ __forceinline__ float sum16(const float (&v)[16]) {
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) s += v[i];
-    return s;
+// One thread per 16-element group: thread (lane, half) of column `col` writes
+// its limbs to field 0/1 (half 0, "lo") or 3/4 (half 1, "hi") and its
+// (s, sum) pair to the lower or upper 8 bytes of the meta field.
+template <class F>
+__global__ __launch_bounds__(256) void k_quant_x(const float *__restrict__ x, uint8_t *__restrict__ xq,
+                                                 int in_dim, int ncols, int n_tok) {
+    constexpr int kHalves = F::kXF == 5 ? 2 : 1;
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    const int per_tok = ncols * 64 * kHalves;
+    if (gid >= per_tok * n_tok) return;
+    const int t = gid / per_tok, rem = gid % per_tok;
+    const int col = rem / (64 * kHalves), r2 = rem % (64 * kHalves);
+    const int half = r2 / 64, lane = r2 % 64;
+    const int k = lane & 7, unit = col * 8 + (lane >> 3);
+    const bool ok = unit < F::units(in_dim) && F::valid(unit, k, in_dim);
+    const int e = ok ? (half ? F::elem_hi(unit, k) : F::elem_lo(unit, k)) : -1;
+    uint4 h, l;
+    float s, sum;
+    quant_group(x + (size_t)t * in_dim, e, in_dim, h, l, s, sum);
+    uint8_t *base = xq + ((size_t)t * ncols + col) * F::kXF * 1024 + lane * 16;
+    *reinterpret_cast<uint4 *>(base + (half ? 3 : 0) * 1024) = h;
+    *reinterpret_cast<uint4 *>(base + (half ? 4 : 1) * 1024) = l;
+    *reinterpret_cast<float2 *>(base + 2 * 1024 + 8 * half) = make_float2(s, sum);
 }
 
-// Dot of 16 bytes (4 dwords, each byte an unsigned value) with 16 floats.
-__device__ __forceinline__ float dot16_u8(const uint32_t (&q)[4], const float (&xv)[16]) {
-    float s = 0.f;
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-#pragma unroll
-        for (int b = 0; b < 4; b++) s += ubyte_f(q[u], b) * xv[4 * u + b];
-    return s;
-}
+// ---- GEMV --------------------------------------------------------------------
+// blockDim = 64 * NW (NW = min(columns, kMaxWaves)); grid = (ceil(out_dim /
+// RT), ceil(n_tok / BT)). Wavefront w handles columns w, w + NW, ...
+constexpr int kMaxWaves = 8;
 
-// ---- Q4_K (GGUF layout) --------------------------------------------------
-// Lane (grp, k): block b = grp + 8*i of the row, qs bytes 16k..16k+15, i.e.
-// sub-block pair p = k/2, elements l = 16*(k&1) + 0..15 of sub-blocks 2p (low
-// nibbles) and 2p+1 (high nibbles).
-template <int R, int BT>
-__global__ __launch_bounds__(256) void k_gemv_q4k(const uint8_t *__restrict__ w,
-                                                  const float *__restrict__ x,
-                                                  float *__restrict__ y, int n_tok, int in_dim,
-                                                  int out_dim) {
-    const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-    if (row0 >= out_dim) return;
+template <class F, int RT, int BT>
+__global__ __launch_bounds__(64 * kMaxWaves) void k_gemv(const uint8_t *__restrict__ w, uint32_t w_bytes,
+                                               const uint8_t *__restrict__ xq, uint32_t xq_bytes,
+                                               float *__restrict__ y, int n_tok, int in_dim,
+                                               int out_dim) {
+    __shared__ float red[kMaxWaves * RT * BT];
+    const int nw = blockDim.x >> 6;
+    // wavefront index, made explicitly uniform so per-column offsets stay scalar
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, k = lane & 7, ks = lane >> 3;
+    const int row0 = blockIdx.x * RT;
     const int t0 = blockIdx.y * BT;
-    const int nb = in_dim >> 8;
-    const size_t row_bytes = (size_t)nb * kQ4kBytes;
-    const int grp = lane >> 3, k = lane & 7;
-    const int p = k >> 1;
-    const int jlo = 2 * p, jhi = 2 * p + 1;
-    const uint8_t *wrow[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) wrow[r] = w + (size_t)min(row0 + r, out_dim - 1) * row_bytes;
-    const float *xt[BT];
-#pragma unroll
-    for (int t = 0; t < BT; t++) xt[t] = x + (size_t)min(t0 + t, n_tok - 1) * in_dim;
+    const int nunits = F::units(in_dim);
+    const int ncols = (nunits + 7) >> 3;
+    const uint32_t col_bytes = (uint32_t)F::kXF * 1024u;
+    const uint32_t tok_bytes = (uint32_t)ncols * col_bytes;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, xq_bytes);
 
-    float acc[R][BT];
+    float acc[RT][BT];
 #pragma unroll
-    for (int r = 0; r < R; r++)
+    for (int r = 0; r < RT; r++)
 #pragma unroll
         for (int t = 0; t < BT; t++) acc[r][t] = 0.f;
 
-    for (int b = grp; b < nb; b += 8) {
-        uint4 hdr[R], qv[R];
+    for (int col = wv; col < ncols; col += nw) {
+        const int unit = col * 8 + ks;
+        typename F::Slice sl[RT];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint8_t *blk = wrow[r] + (size_t)b * kQ4kBytes;
-            hdr[r] = *reinterpret_cast<const uint4 *>(blk);
-            qv[r] = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * k);
-        }
-        float dlo[R], mlo[R], dhi[R], mhi[R];
-        uint32_t qlo[R][4], qhi[R][4];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const float d = f16_to_f32(hdr[r].x & 0xFFFFu);
-            const float dmin = f16_to_f32(hdr[r].x >> 16);
-            uint32_t sc, m;
-            q4k_scale_min(jlo, hdr[r].y, hdr[r].z, hdr[r].w, sc, m);
-            dlo[r] = d * (float)sc;
-            mlo[r] = dmin * (float)m;
-            q4k_scale_min(jhi, hdr[r].y, hdr[r].z, hdr[r].w, sc, m);
-            dhi[r] = d * (float)sc;
-            mhi[r] = dmin * (float)m;
-            const uint32_t q4[4] = {qv[r].x, qv[r].y, qv[r].z, qv[r].w};
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                qlo[r][u] = q4[u] & 0x0F0F0F0Fu;
-                qhi[r][u] = (q4[u] >> 4) & 0x0F0F0F0Fu;
-            }
-        }
-        const int xo = b * 256 + 64 * p + 16 * (k & 1);
+        for (int r = 0; r < RT; r++)
+            F::load(sl[r], rw, min(row0 + r, out_dim - 1), min(unit, nunits - 1), k, in_dim, out_dim);
+        XSlice xs[BT];
 #pragma unroll
         for (int t = 0; t < BT; t++) {
-            float xl[16], xh[16];
-            load16f(xt[t] + xo, xl);
-            load16f(xt[t] + xo + 32, xh);
-            const float sl = sum16(xl), sh = sum16(xh);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const float pl = dot16_u8(qlo[r], xl);
-                const float ph = dot16_u8(qhi[r], xh);
-                acc[r][t] += dlo[r] * pl - mlo[r] * sl + dhi[r] * ph - mhi[r] * sh;
+            const uint32_t so = (uint32_t)min(t0 + t, n_tok - 1) * tok_bytes + (uint32_t)col * col_bytes;
+            const uint32_t vo = (uint32_t)lane * 16u;
+            xs[t].hlo = bload16(rx, vo, so);
+            xs[t].llo = bload16(rx, vo + 1024u, so);
+            xs[t].meta = bload16(rx, vo + 2048u, so);
+            if (F::kXF == 5) {
+                xs[t].hhi = bload16(rx, vo + 3072u, so);
+                xs[t].lhi = bload16(rx, vo + 4096u, so);
             }
+        }
+        if (unit < nunits && F::valid(unit, k, in_dim)) {
+#pragma unroll
+            for (int t = 0; t < BT; t++)
+#pragma unroll
+                for (int r = 0; r < RT; r++) acc[r][t] += F::dot(sl[r], k, xs[t]);
         }
     }
 #pragma unroll
-    for (int r = 0; r < R; r++)
+    for (int r = 0; r < RT; r++)
 #pragma unroll
-        for (int t = 0; t < BT; t++) {
-            const float v = wave_sum(acc[r][t]);
-            if (lane == 0 && row0 + r < out_dim && t0 + t < n_tok)
-                y[(size_t)(t0 + t) * out_dim + row0 + r] = v;
-        }
-}
-
-// ---- Q6_K (device layout: matrix planes [ql | qh | scales | d]) ------------
-// Lane (grp, k): ql bytes 16k..16k+15 of block b: half h = k/4; those bytes
-// hold stride kq = (k&3)/2 (low nibbles) and kq+2 (high nibbles), elements
-// l = 16*(k&1) + 0..15, with their high bits in qh[32h + l] >> 2*kq (and
-// >> 2*kq+4). Element index e = 128h + 32*kq + l; scale index e/16.
-template <int R, int BT>
-__global__ __launch_bounds__(256) void k_gemv_q6k(const uint8_t *__restrict__ w,
-                                                  const float *__restrict__ x,
-                                                  float *__restrict__ y, int n_tok, int in_dim,
-                                                  int out_dim) {
-    const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-    if (row0 >= out_dim) return;
-    const int t0 = blockIdx.y * BT;
-    const int nb = in_dim >> 8;
-    const size_t nblk = (size_t)out_dim * nb;  // blocks in the matrix = plane length
-    const uint8_t *qh_plane = w + nblk * 128;
-    const uint8_t *sc_plane = w + nblk * 192;
-    const uint8_t *d_plane = w + nblk * 208;
-    const int grp = lane >> 3, k = lane & 7;
-    const int h = k >> 2, kq = (k & 3) >> 1, l0 = 16 * (k & 1);
-    const int sc_lo = 8 * h + 2 * kq + (k & 1);  // scale index for e_lo; e_hi uses +4
-    const int e_lo = 128 * h + 32 * kq + l0;
-    size_t rblk[R];  // index of the row's first block
+        for (int t = 0; t < BT; t++) acc[r][t] = wave_sum(acc[r][t]);
+    if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < R; r++) rblk[r] = (size_t)min(row0 + r, out_dim - 1) * nb;
-    const float *xt[BT];
+        for (int r = 0; r < RT; r++)
 #pragma unroll
-    for (int t = 0; t < BT; t++) xt[t] = x + (size_t)min(t0 + t, n_tok - 1) * in_dim;
-
-    float acc[R][BT];
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int t = 0; t < BT; t++) acc[r][t] = 0.f;
-
-    for (int b = grp; b < nb; b += 8) {
-        float slo[R], shi[R];
-        uint32_t qlo[R][4], qhi[R][4];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const size_t bi = rblk[r] + b;
-            const uint4 qlv = *reinterpret_cast<const uint4 *>(w + bi * 128 + 16 * k);
-            const uint4 qhv = *reinterpret_cast<const uint4 *>(qh_plane + bi * 64 + 32 * h + l0);
-            const uint4 scv = *reinterpret_cast<const uint4 *>(sc_plane + bi * 16);
-            const uint32_t dbits = *reinterpret_cast<const uint16_t *>(d_plane + bi * 2);
-            const float d = f16_to_f32(dbits);
-            const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
-            const int8_t s_lo = (int8_t)(scw[sc_lo >> 2] >> (8 * (sc_lo & 3)));
-            const int8_t s_hi = (int8_t)(scw[(sc_lo + 4) >> 2] >> (8 * ((sc_lo + 4) & 3)));
-            slo[r] = d * (float)s_lo;
-            shi[r] = d * (float)s_hi;
-            const uint32_t ql4[4] = {qlv.x, qlv.y, qlv.z, qlv.w};
-            const uint32_t qh4[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                qlo[r][u] = (ql4[u] & 0x0F0F0F0Fu) | (((qh4[u] >> (2 * kq)) & 0x03030303u) << 4);
-                qhi[r][u] = ((ql4[u] >> 4) & 0x0F0F0F0Fu) |
-                            (((qh4[u] >> (2 * kq + 4)) & 0x03030303u) << 4);
-            }
-        }
-        const int xo = b * 256 + e_lo;
-#pragma unroll
-        for (int t = 0; t < BT; t++) {
-            float xl[16], xh[16];
-            load16f(xt[t] + xo, xl);
-            load16f(xt[t] + xo + 64, xh);
-            const float sl = sum16(xl), sh = sum16(xh);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const float pl = dot16_u8(qlo[r], xl) - 32.f * sl;
-                const float ph = dot16_u8(qhi[r], xh) - 32.f * sh;
-                acc[r][t] += slo[r] * pl + shi[r] * ph;
-            }
-        }
+            for (int t = 0; t < BT; t++) red[(r * BT + t) * kMaxWaves + wv] = acc[r][t];
     }
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int t = 0; t < BT; t++) {
-            const float v = wave_sum(acc[r][t]);
-            if (lane == 0 && row0 + r < out_dim && t0 + t < n_tok)
-                y[(size_t)(t0 + t) * out_dim + row0 + r] = v;
-        }
-}
-
-// ---- Q8_0 / Q4_0 (device layout: matrix planes [qs | d]) -------------------
-// Lane owns 16-byte qs chunks c = lane + 64*i. Q8_0: chunk c is half c&1 of
-// block c/2 (16 signed weights). Q4_0: chunk c is block c (16 bytes, low
-// nibbles = elements 0..15, high nibbles = 16..31, each minus 8).
-template <int R, int BT, bool Q4>
-__global__ __launch_bounds__(256) void k_gemv_q8(const uint8_t *__restrict__ w,
-                                                 const float *__restrict__ x,
-                                                 float *__restrict__ y, int n_tok, int in_dim,
-                                                 int out_dim) {
-    const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-    if (row0 >= out_dim) return;
-    const int t0 = blockIdx.y * BT;
-    const int nb = in_dim >> 5;
-    const int qbytes = Q4 ? 16 : 32;
-    const uint8_t *d_plane = w + (size_t)out_dim * nb * qbytes;
-    const int nchunks = Q4 ? nb : 2 * nb;
-    size_t rblk[R];  // index of the row's first block
-#pragma unroll
-    for (int r = 0; r < R; r++) rblk[r] = (size_t)min(row0 + r, out_dim - 1) * nb;
-    const float *xt[BT];
-#pragma unroll
-    for (int t = 0; t < BT; t++) xt[t] = x + (size_t)min(t0 + t, n_tok - 1) * in_dim;
-
-    float acc[R][BT];
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int t = 0; t < BT; t++) acc[r][t] = 0.f;
-
-    for (int c = lane; c < nchunks; c += 64) {
-        const int b = Q4 ? c : (c >> 1);
-        float dd[R];
-        uint32_t q[R][4], q2[R][4];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint4 v =
-                *reinterpret_cast<const uint4 *>(w + rblk[r] * qbytes + (size_t)c * 16);
-            dd[r] = f16_to_f32(*reinterpret_cast<const uint16_t *>(d_plane + (rblk[r] + b) * 2));
-            const uint32_t v4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                if (Q4) {
-                    q[r][u] = v4[u] & 0x0F0F0F0Fu;
-                    q2[r][u] = (v4[u] >> 4) & 0x0F0F0F0Fu;
-                } else {
-                    q[r][u] = v4[u] ^ 0x80808080u;  // signed byte s -> s + 128 as unsigned
-                }
-            }
-        }
-        const int xo = Q4 ? 32 * b : 16 * c;
-#pragma unroll
-        for (int t = 0; t < BT; t++) {
-            float xa[16];
-            load16f(xt[t] + xo, xa);
-            const float sa = sum16(xa);
-            if (Q4) {
-                float xb[16];
-                load16f(xt[t] + xo + 16, xb);
-                const float sb = sum16(xb);
-#pragma unroll
-                for (int r = 0; r < R; r++)
-                    acc[r][t] += dd[r] * ((dot16_u8(q[r], xa) - 8.f * sa) +
-                                          (dot16_u8(q2[r], xb) - 8.f * sb));
-            } else {
-#pragma unroll
-                for (int r = 0; r < R; r++) acc[r][t] += dd[r] * (dot16_u8(q[r], xa) - 128.f * sa);
-            }
-        }
+    __syncthreads();
+    if ((int)threadIdx.x < RT * BT) {
+        const int r = threadIdx.x / BT, t = threadIdx.x % BT;
+        float v = 0.f;
+        for (int q = 0; q < nw; q++) v += red[threadIdx.x * kMaxWaves + q];
+        if (row0 + r < out_dim && t0 + t < n_tok) y[(size_t)(t0 + t) * out_dim + row0 + r] = v;
     }
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int t = 0; t < BT; t++) {
-            const float v = wave_sum(acc[r][t]);
-            if (lane == 0 && row0 + r < out_dim && t0 + t < n_tok)
-                y[(size_t)(t0 + t) * out_dim + row0 + r] = v;
-        }
 }
 
 __global__ void k_fill_zero(float *y, size_t n) {
@@ -307,27 +373,84 @@ hipError_t launch_fill_zero(float *y, size_t n, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int R, int BT>
-static hipError_t gemv_rb(uint32_t dtype, const uint8_t *w, const float *x, float *y, int n_tok,
-                          int in_dim, int out_dim, hipStream_t s) {
-    const dim3 grid((unsigned)((out_dim + 4 * R - 1) / (4 * R)), (unsigned)((n_tok + BT - 1) / BT));
+template <class F>
+static size_t xq_bytes_for(int n_tok, int in_dim) {
+    const int nunits = (in_dim + F::kEPU - 1) / F::kEPU;
+    const int ncols = (nunits + 7) / 8;
+    return (size_t)n_tok * ncols * F::kXF * 1024;
+}
+
+size_t gemv_scratch_bytes(uint32_t dtype, int n_tok, int in_dim) {
     switch (dtype) {
-    case T_Q4_K: k_gemv_q4k<R, BT><<<grid, 256, 0, s>>>(w, x, y, n_tok, in_dim, out_dim); break;
-    case T_Q6_K: k_gemv_q6k<R, BT><<<grid, 256, 0, s>>>(w, x, y, n_tok, in_dim, out_dim); break;
-    case T_Q8_0: k_gemv_q8<R, BT, false><<<grid, 256, 0, s>>>(w, x, y, n_tok, in_dim, out_dim); break;
-    case T_Q4_0: k_gemv_q8<R, BT, true><<<grid, 256, 0, s>>>(w, x, y, n_tok, in_dim, out_dim); break;
-    default: return hipErrorInvalidValue;
+    case T_Q4_K: return xq_bytes_for<FQ4K>(n_tok, in_dim);
+    case T_Q6_K: return xq_bytes_for<FQ6K>(n_tok, in_dim);
+    case T_Q8_0: return xq_bytes_for<FQ8<false>>(n_tok, in_dim);
+    case T_Q4_0: return xq_bytes_for<FQ8<true>>(n_tok, in_dim);
+    default: return 0;
     }
+}
+
+template <class F, int RT, int BT>
+static hipError_t go(const uint8_t *w, size_t w_bytes, const uint8_t *xq, size_t xqb, float *y,
+                     int n_tok, int in_dim, int out_dim, hipStream_t s) {
+    const int ncols = ((in_dim + F::kEPU - 1) / F::kEPU + 7) / 8;
+    const int nw = ncols < kMaxWaves ? ncols : kMaxWaves;
+    const dim3 grid((unsigned)((out_dim + RT - 1) / RT), (unsigned)((n_tok + BT - 1) / BT));
+    k_gemv<F, RT, BT><<<grid, 64 * nw, 0, s>>>(w, (uint32_t)w_bytes, xq, (uint32_t)xqb, y, n_tok,
+                                               in_dim, out_dim);
     return hipGetLastError();
 }
 
-hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, const float *x, float *y, int n_tok,
-                       int in_dim, int out_dim, hipStream_t s) {
+template <class F>
+static hipError_t quantize(const float *x, uint8_t *xq, int n_tok, int in_dim, hipStream_t s) {
+    const int ncols = ((in_dim + F::kEPU - 1) / F::kEPU + 7) / 8;
+    const int threads = n_tok * ncols * 64 * (F::kXF == 5 ? 2 : 1);
+    k_quant_x<F><<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(x, xq, in_dim, ncols, n_tok);
+    return hipGetLastError();
+}
+
+template <class F>
+static hipError_t gemv_pre(const uint8_t *w, size_t w_bytes, const uint8_t *xq, float *y, int n_tok,
+                           int in_dim, int out_dim, hipStream_t s) {
+    const size_t xqb = xq_bytes_for<F>(n_tok, in_dim);
+    if (n_tok == 1) return go<F, 4, 1>(w, w_bytes, xq, xqb, y, n_tok, in_dim, out_dim, s);
+    if (n_tok == 2) return go<F, 2, 2>(w, w_bytes, xq, xqb, y, n_tok, in_dim, out_dim, s);
+    if (n_tok <= 4) return go<F, 2, 4>(w, w_bytes, xq, xqb, y, n_tok, in_dim, out_dim, s);
+    return go<F, 1, 8>(w, w_bytes, xq, xqb, y, n_tok, in_dim, out_dim, s);
+}
+
+hipError_t launch_quantize_x(uint32_t dtype, const float *x, uint8_t *xq, int n_tok, int in_dim,
+                             hipStream_t s) {
+    if (n_tok <= 0 || in_dim <= 0) return hipSuccess;
+    switch (dtype) {
+    case T_Q4_K: return quantize<FQ4K>(x, xq, n_tok, in_dim, s);
+    case T_Q6_K: return quantize<FQ6K>(x, xq, n_tok, in_dim, s);
+    case T_Q8_0: return quantize<FQ8<false>>(x, xq, n_tok, in_dim, s);
+    case T_Q4_0: return quantize<FQ8<true>>(x, xq, n_tok, in_dim, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gemv_prequant(uint32_t dtype, const uint8_t *w, size_t w_bytes,
+                                const uint8_t *xq, float *y, int n_tok, int in_dim, int out_dim,
+                                hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
-    if (n_tok == 1) return gemv_rb<2, 1>(dtype, w, x, y, n_tok, in_dim, out_dim, s);
-    if (n_tok == 2) return gemv_rb<2, 2>(dtype, w, x, y, n_tok, in_dim, out_dim, s);
-    if (n_tok <= 4) return gemv_rb<1, 4>(dtype, w, x, y, n_tok, in_dim, out_dim, s);
-    return gemv_rb<1, 8>(dtype, w, x, y, n_tok, in_dim, out_dim, s);
+    switch (dtype) {
+    case T_Q4_K: return gemv_pre<FQ4K>(w, w_bytes, xq, y, n_tok, in_dim, out_dim, s);
+    case T_Q6_K: return gemv_pre<FQ6K>(w, w_bytes, xq, y, n_tok, in_dim, out_dim, s);
+    case T_Q8_0: return gemv_pre<FQ8<false>>(w, w_bytes, xq, y, n_tok, in_dim, out_dim, s);
+    case T_Q4_0: return gemv_pre<FQ8<true>>(w, w_bytes, xq, y, n_tok, in_dim, out_dim, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
+                       uint8_t *xq_scratch, float *y, int n_tok, int in_dim, int out_dim,
+                       hipStream_t s) {
+    if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
+    hipError_t e = launch_quantize_x(dtype, x, xq_scratch, n_tok, in_dim, s);
+    if (e != hipSuccess) return e;
+    return launch_gemv_prequant(dtype, w, w_bytes, xq_scratch, y, n_tok, in_dim, out_dim, s);
 }
 
 }  // namespace rsllm_hip

@@ -42,9 +42,24 @@ hipError_t launch_dequant(uint32_t dtype, const uint8_t *src, float *dst, size_t
 hipError_t launch_prepare(uint32_t dtype, const uint8_t *src, uint8_t *dst, size_t rows,
                           size_t in_dim, hipStream_t s);
 
-// gemv.hip: y[t, o] = sum_i W[o, i] x[t, i] for t < n_tok, W in device layout.
-hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, const float *x, float *y, int n_tok,
-                       int in_dim, int out_dim, hipStream_t s);
+// gemv.hip: y[t, o] = sum_i W[o, i] x[t, i] for t < n_tok, W (w_bytes bytes)
+// in device layout. Runs the activation pre-pass into `xq_scratch`, which
+// must hold gemv_scratch_bytes(dtype, n_tok, in_dim) bytes.
+hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
+                       uint8_t *xq_scratch, float *y, int n_tok, int in_dim, int out_dim,
+                       hipStream_t s);
+size_t gemv_scratch_bytes(uint32_t dtype, int n_tok, int in_dim);
+// The two halves of launch_gemv: the activation pre-pass (format-specific
+// int8 two-limb layout) and the GEMV on pre-quantised activations.
+hipError_t launch_quantize_x(uint32_t dtype, const float *x, uint8_t *xq, int n_tok, int in_dim,
+                             hipStream_t s);
+hipError_t launch_gemv_prequant(uint32_t dtype, const uint8_t *w, size_t w_bytes,
+                                const uint8_t *xq, float *y, int n_tok, int in_dim, int out_dim,
+                                hipStream_t s);
+
+// Largest weight tensor the buffer-addressed kernels accept (offsets are
+// 32-bit).
+constexpr size_t kMaxWeightBytes = 0xFFFFFF00u;
 
 // Fill n floats with zero (used for in_dim == 0; no hipMemset so the call
 // stays capturable into a graph).

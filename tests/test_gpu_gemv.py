@@ -89,3 +89,31 @@ def test_n_tok_zero_is_noop(hip):
     w = synth.weight(G.Q8_0, 4, 64, 1)
     out = np.zeros(0, np.float32)
     hip.matmul_quant_f32(out, w, np.zeros(0, np.float32), 0, 64, 4, G.Q8_0)
+
+
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q4_0])
+def test_prequant_entry_points_match_one_shot(oracle, hip, dtype):
+    """quantize_x_dev + matmul_prequant_dev is the same computation as
+    matmul_quant_f32_dev: identical outputs, and within tolerance of the oracle."""
+    import torch
+    out_dim, in_dim, n_tok = 77, 1280, 2
+    w = synth.weight(dtype, out_dim, in_dim, 21)
+    x = synth.activations(n_tok, in_dim, 22).reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, x, n_tok, in_dim, out_dim, int(dtype))
+    s = torch.cuda.current_stream().cuda_stream
+    d_raw = torch.from_numpy(w).cuda()
+    d_w = torch.empty_like(d_raw)
+    hip.prepare_weights_dev(d_w.data_ptr(), d_raw.data_ptr(), w.size, dtype, in_dim, s)
+    d_x = torch.from_numpy(x).cuda()
+    y1 = torch.empty(n_tok * out_dim, device="cuda")
+    y2 = torch.empty(n_tok * out_dim, device="cuda")
+    hip.matmul_quant_f32_dev(y1.data_ptr(), y1.numel(), d_w.data_ptr(), w.size, d_x.data_ptr(),
+                             x.size, n_tok, in_dim, out_dim, dtype, s)
+    nb = hip.xq_bytes(dtype, n_tok, in_dim)
+    xq = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    hip.quantize_x_dev(dtype, d_x.data_ptr(), x.size, n_tok, in_dim, xq.data_ptr(), nb, s)
+    hip.matmul_prequant_dev(y2.data_ptr(), y2.numel(), d_w.data_ptr(), w.size, xq.data_ptr(), nb,
+                            n_tok, in_dim, out_dim, dtype, s)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert rel_err(y2.cpu().numpy(), want) <= REL_TOL
