@@ -16,8 +16,8 @@
  *
  * Weights in device memory are in the "device layout" written by
  * rsllm_hip_prepare_weights_dev: for Q4_K it is the GGUF byte stream
- * itself; Q6_K / Q8_0 / Q4_0 matrices are split into field planes of the
- * same total size (see rsllm_hip_prepare_weights_dev).
+ * itself; Q6_K / Q8_0 / Q4_0 matrices are regrouped into 8-block super-tiles
+ * of the same total size (see rsllm_hip_prepare_weights_dev).
  *
  * Thread safety: every entry point may be called from any thread. Process
  * state (device ordinal, registered weights) is guarded by a mutex; each
@@ -139,14 +139,34 @@ int rsllm_hip_register_weights(const uint8_t *weights, size_t weights_len, uint3
 int rsllm_hip_release_weights(void);
 
 /* GGUF rows -> device layout: `len` bytes holding whole rows of `in_dim`
- * elements (rows = len / row_bytes, nb = in_dim / block_elems). Q4_K:
- * unchanged (`dst` may equal `src`). Q6_K, Q8_0, Q4_0: the matrix is split
- * into field planes of the same total size, each row-major over
- * (row, block): Q6_K [ql rows*nb*128 | qh rows*nb*64 | scales rows*nb*16 |
- * d rows*nb*2], Q8_0 [qs rows*nb*32 | d rows*nb*2], Q4_0 [qs rows*nb*16 |
- * d rows*nb*2]; `dst` must not overlap `src`. Enqueued on `stream`. */
+ * elements (n = len / block_bytes blocks in matrix order, row-major over
+ * (row, block)). Q4_K: unchanged (`dst` may equal `src`). Q6_K, Q8_0, Q4_0:
+ * the blocks are regrouped into super-tiles of 8 consecutive blocks (the
+ * last tile holds the n % 8 remaining blocks, r of them), each tile split
+ * into field runs so that every field of every block is 16-byte aligned:
+ *   Q6_K  [ql r*128 | qh r*64 | scales r*16 | d r*2]   (8 blocks: 1680 B)
+ *   Q8_0  [qs r*32 | d r*2]                           (8 blocks: 272 B)
+ *   Q4_0  [qs r*16 | d r*2]                           (8 blocks: 144 B)
+ * with r = 8 except in the last tile; tile S starts at byte
+ * S * 8 * block_bytes. `dst` must not overlap `src`. Enqueued on `stream`. */
 int rsllm_hip_prepare_weights_dev(uint8_t *dst, const uint8_t *src, size_t len, uint32_t dtype,
                                   size_t in_dim, rsllm_hip_stream_t stream);
+
+/* ---- prefill GEMM (bf16 activations) ---------------------------------------
+ * The prefill form of matmul_quant_f32 (backend-cpu/src/ops/quant_matmul.rs:
+ * 45-119, called from models/src/engine_impl.rs:277 prefill with n_tok = T):
+ * out[t * out_dim + o] = sum_i deq(W)[o, i] * f32(x[t * in_dim + i]) for a
+ * GGUF Q4_K weight (device copy of the GGUF bytes) and bf16 activations
+ * (x_len = n_tok * in_dim 16-bit patterns). Runs on the matrix cores
+ * (f16 MFMA, fp32 accumulation); within 1e-3 (max|d|/max|y|) of the
+ * reference on f32(x). Validation as matmul_quant_f32 (dtype -> in_dim %
+ * 256 -> weights -> x -> out); dtypes other than Q4_K return
+ * RSLLM_HIP_ERR_UNIMPLEMENTED. Uses a per-thread device workspace of about
+ * 2 * n_tok * in_dim bytes; enqueued on `stream`. */
+int rsllm_hip_matmul_q4k_bf16_dev(float *out, size_t out_len, const uint8_t *weights,
+                                  size_t weights_len, const uint16_t *x_bf16, size_t x_len,
+                                  size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype,
+                                  rsllm_hip_stream_t stream);
 
 /* ---- dequantisation ------------------------------------------------------ */
 

@@ -133,6 +133,7 @@ SIGNATURES = {
     "rsllm_hip_xq_bytes": ([_U32, _S, _S], _S),
     "rsllm_hip_quantize_x_dev": ([_U32, _P, _S, _S, _S, _P, _S, _P], _I),
     "rsllm_hip_matmul_prequant_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _P], _I),
+    "rsllm_hip_matmul_q4k_bf16_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _P], _I),
 }
 
 
@@ -254,6 +255,16 @@ def matmul_prequant_dev(out_ptr: int, out_len: int, w_ptr: int, w_len: int, xq_p
                                              int(dtype), stream or None))
 
 
+def matmul_q4k_bf16_dev(out_ptr: int, out_len: int, w_ptr: int, w_len: int, x_ptr: int,
+                        x_len: int, n_tok: int, in_dim: int, out_dim: int, dtype,
+                        stream: int = 0) -> None:
+    """Prefill GEMM: Q4_K weights (GGUF bytes on the device) times bf16
+    activations (``x_len`` 16-bit values), fp32 output on the MFMA path."""
+    _check(LIB.rsllm_hip_matmul_q4k_bf16_dev(out_ptr or None, out_len, w_ptr or None, w_len,
+                                             x_ptr or None, x_len, n_tok, in_dim, out_dim,
+                                             int(dtype), stream or None))
+
+
 def prepare_weights_dev(dst_ptr: int, src_ptr: int, nbytes: int, dtype, in_dim: int,
                         stream: int = 0) -> None:
     _check(LIB.rsllm_hip_prepare_weights_dev(dst_ptr or None, src_ptr or None, nbytes, int(dtype),
@@ -301,5 +312,6 @@ __all__ = [
     "UnsupportedTier", "DequantSizeMismatch", "UnsupportedDequant", "DeviceError",
     "InvalidArgument", "Unimplemented", "matmul_quant_f32", "dequant_to_f32", "register_weights",
     "release_weights", "init", "matmul_quant_f32_dev", "prepare_weights_dev",
-    "dequant_to_f32_dev", "xq_bytes", "quantize_x_dev", "matmul_prequant_dev", "HipBackend", "BackendCapability", "LIB", "LIB_PATH", "SIGNATURES",
+    "dequant_to_f32_dev", "xq_bytes", "quantize_x_dev", "matmul_prequant_dev",
+    "matmul_q4k_bf16_dev", "HipBackend", "BackendCapability", "LIB", "LIB_PATH", "SIGNATURES",
 ]

@@ -6,6 +6,9 @@ into rsllm_amd/librsllm_hip.so. Flags:
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                  no v_pk_*_f32 generation
   -O3 -fPIC -std=c++17
+prefill.hip additionally gets -mllvm -amdgpu-mfma-vgpr-form: MFMA
+accumulators are allocated in VGPRs (the kernel fits in 256), which keeps
+the accumulate-in-place form and avoids accumulator copies between MFMAs.
 Run: python -m rsllm_amd.build  (or __graft_entry__.build()).
 """
 from __future__ import annotations
@@ -21,7 +24,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librsllm_hip.so")
 
-SOURCES = ["abi.hip", "dequant.hip", "gemv.hip"]
+SOURCES = ["abi.hip", "dequant.hip", "gemv.hip", "prefill.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -41,9 +44,15 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
+EXTRA_FLAGS = {
+    "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o",
+           obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")

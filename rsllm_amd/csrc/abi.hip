@@ -82,7 +82,7 @@ struct DevBuf {
 struct ThreadCtx {
     int device = -1;
     hipStream_t stream = nullptr;
-    DevBuf w_raw, w_dev, x, y, xq;
+    DevBuf w_raw, w_dev, x, y, xq, xh;
 };
 thread_local ThreadCtx t_ctx;
 
@@ -348,6 +348,36 @@ int rsllm_hip_matmul_prequant_dev(float *out, size_t out_len, const uint8_t *wei
     HIP_TRY(launch_gemv_prequant(dtype, weights, weights_len, xq, out, (int)n_tok, (int)in_dim,
                                  (int)out_dim, s),
             "gemv");
+    return ok();
+}
+
+int rsllm_hip_matmul_q4k_bf16_dev(float *out, size_t out_len, const uint8_t *weights,
+                                  size_t weights_len, const uint16_t *x_bf16, size_t x_len,
+                                  size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype,
+                                  rsllm_hip_stream_t stream) {
+    int rc = validate_matmul(out_len, weights, weights_len, x_bf16, x_len, out, n_tok, in_dim,
+                             out_dim, dtype);
+    if (rc) return rc;
+    if (dtype != T_Q4_K)
+        return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED,
+                       "matmul_q4k_bf16: only Q4_K weights have a prefill GEMM");
+    if (x_len > (size_t)INT_MAX)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_q4k_bf16: n_tok * in_dim exceeds 2^31-1");
+    if (((uintptr_t)weights | (uintptr_t)x_bf16) & 15)
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                       "matmul_q4k_bf16: weights and x must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    if (n_tok == 0) return ok();
+    if (in_dim == 0) {
+        HIP_TRY(launch_fill_zero(out, out_len, s), "fill_zero");
+        return ok();
+    }
+    if ((rc = ensure_device())) return rc;
+    HIP_TRY(t_ctx.xh.ensure(prefill_scratch_bytes((int)n_tok, (int)in_dim)), "hipMalloc");
+    HIP_TRY(launch_prefill_q4k(weights, weights_len, x_bf16, (uint8_t *)t_ctx.xh.p, out,
+                               (int)n_tok, (int)in_dim, (int)out_dim, s),
+            "prefill_q4k");
     return ok();
 }
 

@@ -1,0 +1,392 @@
+// Prefill GEMM: out[t, o] = sum_i deq(W)[o, i] * x[t, i] for a Q4_K weight W
+// [out_dim x in_dim] and bf16 activations x [n_tok x in_dim], fp32 output.
+//
+// The reference computes this as matmul_quant_f32 on f32(bf16 x)
+// (backend-cpu/src/ops/quant_matmul.rs:45-119): every weight row is
+// dequantised once per token and dotted in f32. Here it is one dense
+// contraction on the CDNA4 matrix cores:
+//
+// 1. k_prefill_x: per token t, x is scaled by 2^e_t so that max|x_t| lands in
+//    [2^14, 2^15) and converted to f16. bf16 has an 8-bit significand, so the
+//    conversion is exact for every element within 2^-29 of the token's
+//    maximum; 2^-e_t is kept to undo the scaling in the epilogue.
+// 2. k_prefill_q4k: W is dequantised in registers to f16,
+//    w = f16(d*sc_j) * q - f16(dmin*m_j) (packed f16 FMA, q exact), straight
+//    into the operands of v_mfma_f32_16x16x32_f16 against the f16
+//    activations; products accumulate in fp32. The f16 weight rounding
+//    (about 2^-11 relative per weight) keeps the output within about 3e-4
+//    of the reference, inside the 1e-3 budget.
+//
+// Tiling: a workgroup is 4 wavefronts and covers 256 weight rows x 128
+// tokens; a wavefront owns 64 rows (4 MFMA tiles) x 128 tokens (8 tiles), 32
+// accumulator tiles held in VGPRs. The weights are the MFMA A operand and the
+// activations the B operand, so every lane ends with 4 consecutive outputs of
+// one token. The K loop runs in steps of
+// half a super-block (128 elements). Each step's activations (128 tokens x
+// 128 f16, 32 KB) and raw weight bytes (256 rows x 80 B: the 16-byte block
+// header and the 64 qs bytes of that half, 20 KB) are copied global->LDS by
+// DMA into one of three stage buffers, two steps ahead of their use.
+//
+// K order: inside a super-block, MFMA chunk c (0..7) gives lane group q
+// (lanes 16q..16q+15) sub-block 2q + (c & 1), positions 8 * (c >> 1) .. + 7,
+// so a lane's weights for one half are 16 contiguous qs bytes (low nibbles
+// for even c, high for odd c); the activation stage is laid out in the same
+// order. Half h holds positions 16h .. 16h + 15 of every sub-block.
+#include "kernels.h"
+
+namespace rsllm_hip {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kPfTok = 128;                      // tokens per workgroup
+constexpr int kPfRowsWave = 64;                  // weight rows per wavefront
+constexpr int kPfRowsWg = 4 * kPfRowsWave;       // weight rows per workgroup
+constexpr int kPfXBytes = kPfTok * 256;          // activation stage: 128 rows x 128 f16
+constexpr int kPfWRow = 80;                      // weight stage row: header + 64 qs bytes
+constexpr int kPfWBytes = kPfRowsWg * kPfWRow;   // weight stage: 20 KB
+constexpr int kPfStage = kPfXBytes + kPfWBytes;  // 53248
+constexpr int kPfNStage = 3;                     // stage buffers (two steps of prefetch)
+constexpr int kPfLds = kPfNStage * kPfStage;     // 159744 bytes
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// ---- activation pre-pass: bf16 -> scaled f16 ----------------------------------
+// One workgroup per token; 16-byte loads and stores (8 elements per access).
+// in_dim is a multiple of 256.
+__global__ __launch_bounds__(256) void k_prefill_x(const uint16_t *__restrict__ x,
+                                                   _Float16 *__restrict__ xh,
+                                                   float *__restrict__ unscale, int in_dim) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const uint4 *xt = reinterpret_cast<const uint4 *>(x + (size_t)t * in_dim);
+    const int n8 = in_dim >> 3;
+    // |bf16| bits: the largest finite magnitude has the largest bit pattern
+    uint32_t mbits = 0;
+    for (int i = tid; i < n8; i += 256) {
+        const uint4 v = xt[i];
+        const uint32_t a = max(v.x & 0x7FFF7FFFu, v.y & 0x7FFF7FFFu);
+        const uint32_t b = max(v.z & 0x7FFF7FFFu, v.w & 0x7FFF7FFFu);
+        const uint32_t c = max(a, b);
+        mbits = max(mbits, max(c & 0xFFFFu, c >> 16));
+    }
+    // NaN patterns (above 0x7F80) do not pick the scale; infinity does
+    if (mbits > 0x7F80u) mbits = 0;
+    float amax = __uint_as_float(mbits << 16);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // e: amax * 2^e in [2^14, 2^15) for finite nonzero amax (exponent from the bits)
+    int e = 0;
+    if (amax > 0.f && amax <= 3.4e38f) {
+        const int ex = (int)((__float_as_uint(amax) >> 23) & 0xFF) - 127;
+        e = 14 - (ex < -126 ? -126 : ex);
+        if (e > 120) e = 120;
+    }
+    const float up = __uint_as_float((uint32_t)(127 + e) << 23);
+    if (tid == 0) unscale[t] = __uint_as_float((uint32_t)(127 - e) << 23);
+    uint4 *ht = reinterpret_cast<uint4 *>(xh + (size_t)t * in_dim);
+    for (int i = tid; i < n8; i += 256) {
+        const uint4 v = xt[i];
+        const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const _Float16 lo = (_Float16)(__uint_as_float(in[k] << 16) * up);
+            const _Float16 hi = (_Float16)(__uint_as_float(in[k] & 0xFFFF0000u) * up);
+            o[k] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+        }
+        ht[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// ---- GEMM -------------------------------------------------------------------------
+// (sc, m) of Q4_K sub-block j for a lane-dependent j, without branches
+// (q4_k_scale_min, dequant/mod.rs:48-58): both encodings are decoded and
+// selected.
+__device__ __forceinline__ void pf_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                             uint32_t &sc, uint32_t &m) {
+    const int sh = 8 * (j & 3);
+    const uint32_t a = s0 >> sh, b = s1 >> sh, c = s2 >> sh;
+    const uint32_t sc_hi = (c & 15u) | ((a >> 2) & 48u);
+    const uint32_t m_hi = ((c >> 4) & 15u) | ((b >> 2) & 48u);
+    sc = j < 4 ? (a & 63u) : sc_hi;
+    m = j < 4 ? (b & 63u) : m_hi;
+}
+
+// Eight f16 weights of one chunk: qs bytes b0..b7 are dwords d0 (b0..b3) and
+// d1 (b4..b7); `hi` selects the high nibbles. w = q * dsc - dm.
+// A byte 0..15 read as fp8 e4m3 is q * 2^-9 exactly (subnormal for q < 8,
+// exponent 1 above), and v_cvt_scalef32_pk_f16_fp8 applies its scale as a
+// power of two, so a scale of 2^9 yields the integer q in f16 exactly — two
+// weights per instruction.
+__device__ __forceinline__ h8 pf_dequant8(uint32_t d0, uint32_t d1, bool hi, h2 dsc, h2 dm) {
+    if (hi) { d0 >>= 4; d1 >>= 4; }
+    d0 &= 0x0F0F0F0Fu;
+    d1 &= 0x0F0F0F0Fu;
+    const h2 q0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 512.0f, false);  // bytes 0, 1
+    const h2 q1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 512.0f, true);   // bytes 2, 3
+    const h2 q2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 512.0f, false);
+    const h2 q3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 512.0f, true);
+    const h2 w0 = q0 * dsc - dm, w1 = q1 * dsc - dm, w2 = q2 * dsc - dm, w3 = q3 * dsc - dm;
+    h8 r;
+    r[0] = w0[0]; r[1] = w0[1]; r[2] = w1[0]; r[3] = w1[1];
+    r[4] = w2[0]; r[5] = w2[1]; r[6] = w3[0]; r[7] = w3[1];
+    return r;
+}
+
+struct pf_true { static constexpr bool value = true; };
+struct pf_false { static constexpr bool value = false; };
+
+// dword i (0..3) of a uint4 for a compile-time i
+__device__ __forceinline__ uint32_t pf_u4(const uint4 &v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+__global__ __launch_bounds__(256) void k_prefill_q4k(const uint8_t *__restrict__ w,
+                                                     const _Float16 *__restrict__ xh,
+                                                     const float *__restrict__ unscale,
+                                                     float *__restrict__ out, int n_tok, int in_dim,
+                                                     int out_dim) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * kPfRowsWg;  // first weight row of the workgroup
+    const int t0 = blockIdx.y * kPfTok;
+    const int nb = in_dim >> 8;
+    const int nsteps = 2 * nb;
+
+    // DMA sources. Activations: instruction p of this wave moves token rows
+    // 4g .. 4g + 3 (g = 8 wv + p), lane i to row 4g + i / 16, slot i % 16;
+    // slot s of token row tl holds chunk k = s ^ (tl & 15), i.e. elements
+    // 32 (k >> 1) + 16h + 8 (k & 1) .. + 7 of the super-block. Rows past
+    // n_tok repeat the last token (their outputs are not stored).
+    uint32_t xoff[8];
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+        const int tl = 4 * (8 * wv + p) + (lane >> 4);
+        const int k = (lane & 15) ^ (tl & 15);
+        const int t = min(t0 + tl, n_tok - 1);
+        xoff[p] = (uint32_t)t * (uint32_t)in_dim + 32u * (k >> 1) + 8u * (k & 1);
+    }
+    // Weights: instruction p of this wave moves 16-byte pieces j = 64 g + i
+    // (g = 5 wv + p) of the stage, row j / 5, piece j % 5: piece 0 is the
+    // block header, piece 1 + q the qs bytes 32q + 16h .. + 15. The five
+    // instructions of wave wv cover exactly its own 64 rows. Bit 0 of woff
+    // marks a qs piece (offset + 16h).
+    uint32_t woff[5];
+#pragma unroll
+    for (int p = 0; p < 5; p++) {
+        const int j = 64 * (5 * wv + p) + lane;
+        const int row = j / 5, part = j - 5 * row;
+        const uint32_t rowg = (uint32_t)min(n0 + row, out_dim - 1);
+        woff[p] = rowg * (uint32_t)nb * 144u + (part ? 16u + 32u * (part - 1) + 1u : 0u);
+    }
+    auto stage = [&](int st, uint8_t *buf) {
+        const int s = st >> 1, h = st & 1;
+#pragma unroll
+        for (int p = 0; p < 8; p++)
+            __builtin_amdgcn_global_load_lds((const void *)(xh + xoff[p] + s * 256 + 16 * h),
+                                             (lds_void *)(buf + 1024 * (8 * wv + p)), 16, 0, 0);
+#pragma unroll
+        for (int p = 0; p < 5; p++) {
+            const uint32_t o = (woff[p] & ~1u) + (uint32_t)s * 144u + (woff[p] & 1u) * 16u * h;
+            __builtin_amdgcn_global_load_lds((const void *)(w + o),
+                                             (lds_void *)(buf + kPfXBytes + 1024 * (5 * wv + p)),
+                                             16, 0, 0);
+        }
+    };
+    // A operand of group g (chunk g / 8 of the step, row tile g % 8):
+    // elements of sub-block 2q + (c & 1) at positions 16h + 8 (c >> 1) .. + 7.
+    auto read_a = [&](const uint8_t *buf, int g) -> h8 {
+        const int c = g >> 3, mt = g & 7;
+        const int k = 2 * (2 * q + (c & 1)) + (c >> 1);
+        return *reinterpret_cast<const h8 *>(buf + (mt * 16 + r16) * 256 + ((k ^ r16) << 4));
+    };
+    // this lane's weight rows in the stage: wave rows 16 nt + r16
+    const int wrow = (wv * kPfRowsWave + r16) * kPfWRow;
+
+    f4 acc[8][4];
+#pragma unroll
+    for (int mt = 0; mt < 8; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // f16 (d*sc, dmin*m) of sub-blocks 2q + hb, broadcast to both halves
+    h2 dsc[4][2], dmn[4][2];
+    uint4 qs[4];
+    h8 bq[4];
+    // Weight bytes of one step for this lane (qs piece of its q) and the
+    // block scales (every stage carries the block header).
+    auto load_step_weights = [&](const uint8_t *buf) {
+        const uint8_t *wb = buf + kPfXBytes + wrow;
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) {
+            qs[nt] = *reinterpret_cast<const uint4 *>(wb + nt * 16 * kPfWRow + 16 + 16 * q);
+            const uint4 hd = *reinterpret_cast<const uint4 *>(wb + nt * 16 * kPfWRow);
+            const float d = f16_to_f32(hd.x & 0xFFFFu);
+            const float dmin = f16_to_f32(hd.x >> 16);
+#pragma unroll
+            for (int hb = 0; hb < 2; hb++) {
+                uint32_t sc, m;
+                pf_scale_min(2 * q + hb, hd.y, hd.z, hd.w, sc, m);
+                const _Float16 a = (_Float16)(d * (float)sc), b = (_Float16)(dmin * (float)m);
+                dsc[nt][hb] = h2{a, a};
+                dmn[nt][hb] = h2{b, b};
+            }
+        }
+    };
+    // B operands of chunk c (0..3) of the current step
+    auto dequant = [&](int c, int nt) -> h8 {
+        const int run = c >> 1;  // bytes 8 run .. 8 run + 7 of the lane's 16
+        return pf_dequant8(pf_u4(qs[nt], 2 * run), pf_u4(qs[nt], 2 * run + 1), (c & 1) != 0,
+                           dsc[nt][c & 1], dmn[nt][c & 1]);
+    };
+
+    // Stages st + 1 and st + 2 are in flight while step st is computed: the
+    // DMA of stage st + 3 is issued right after the barrier in step st, into
+    // the buffer step st used. Stage indices past the last step repeat the
+    // last stage into a buffer nothing reads again, so every step has the
+    // same number of DMA instructions in flight.
+    auto sbuf = [&](int st) { return smem + (st % kPfNStage) * kPfStage; };
+    stage(0, sbuf(0));
+    stage(1, sbuf(1));
+    stage(min(2, nsteps - 1), sbuf(2));
+    __builtin_amdgcn_s_waitcnt(0x4F7A);  // vmcnt(26): stage 0 of this wave landed
+    __syncthreads();
+    load_step_weights(sbuf(0));
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) bq[nt] = dequant(0, nt);
+    h8 a0 = read_a(sbuf(0), 0), a1 = read_a(sbuf(0), 1);
+
+    // One K step: 32 groups (4 chunks x 8 row tiles) of 4 MFMAs. Operand
+    // reads run two groups ahead (across the step boundary), B operands are
+    // dequantised one chunk ahead (chunk 3 prepares the next step's chunk 0
+    // from the next stage's weight rows). MORE: a next step exists.
+    auto step = [&](int st, auto more_tag) {
+        constexpr bool more = decltype(more_tag)::value;
+        uint8_t *buf = sbuf(st);
+        const uint8_t *nbuf = sbuf(st + 1);
+        h8 bn[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (more && c == 3) {
+                // stage st + 1: this wave's own weight rows are in once its
+                // own DMA has completed (stage st + 2 may still be in flight)
+                __builtin_amdgcn_s_waitcnt(0x0F7D);  // vmcnt(13)
+                load_step_weights(nbuf);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 8; mt++) {
+                const int g = 8 * c + mt;
+                if (more && g == 30) {
+                    // every wave has its operands up to group 31 in registers
+                    // and its stage-(st+1) DMA complete: the next stage's
+                    // activation rows become readable and `buf` is free for
+                    // stage st + 3. (The barrier's own wait also covers
+                    // stage st + 2, whose DMA was issued a step earlier.)
+                    __syncthreads();
+                    stage(min(st + 3, nsteps - 1), buf);
+                }
+                h8 a2 = a1;
+                if (g + 2 < 32) a2 = read_a(buf, g + 2);
+                else if (more) a2 = read_a(nbuf, g - 30);
+                const h8 acur = a0;
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bq[nt], acur, acc[mt][nt], 0, 0, 0);
+                if (mt & 1) {
+                    if (c < 3) bn[mt >> 1] = dequant(c + 1, mt >> 1);
+                    else if (more) bn[mt >> 1] = dequant(0, mt >> 1);
+                }
+                a0 = a1;
+                a1 = a2;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (c < 3 || more) {
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++) bq[nt] = bn[nt];
+            }
+        }
+    };
+    for (int st = 0; st + 1 < nsteps; st++) step(st, pf_true{});
+    step(nsteps - 1, pf_false{});
+
+    // The weights are the MFMA A operand, so tile (mt, nt) has weight rows
+    // as its rows: lane (r16, q) holds outputs o = 16 nt + 4q + i (i = 0..3)
+    // of token t = 16 mt + r16 — four consecutive outputs of one token, one
+    // 16-byte store. The unscale vector is padded to whole 128-token tiles.
+    float us[8];
+#pragma unroll
+    for (int mt = 0; mt < 8; mt++) us[mt] = unscale[t0 + mt * 16 + r16];
+    const int ow = n0 + wv * kPfRowsWave + 4 * q;
+    const bool vec = (out_dim & 3) == 0;
+#pragma unroll
+    for (int mt = 0; mt < 8; mt++) {
+        const int t = t0 + mt * 16 + r16;
+        if (t >= n_tok) continue;
+        float *orow = out + (size_t)t * out_dim;
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) {
+            const int o = ow + 16 * nt;
+            const f4 v = acc[mt][nt] * us[mt];
+            if (vec && o + 3 < out_dim) {
+                *reinterpret_cast<f4 *>(orow + o) = v;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (o + i < out_dim) orow[o + i] = v[i];
+            }
+        }
+    }
+}
+
+size_t prefill_scratch_bytes(int n_tok, int in_dim) {
+    // f16 activations, then one f32 unscale per token padded to whole
+    // 128-token tiles (16-byte aligned)
+    const size_t tiles = ((size_t)n_tok + kPfTok - 1) / kPfTok;
+    return ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16 + tiles * kPfTok * 4;
+}
+
+hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *x_bf16,
+                              uint8_t *scratch, float *out, int n_tok, int in_dim, int out_dim,
+                              hipStream_t s) {
+    if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_prefill_q4k,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kPfLds);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
+    float *unscale = reinterpret_cast<float *>(scratch + ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16);
+    k_prefill_x<<<(unsigned)n_tok, 256, 0, s>>>(x_bf16, xh, unscale, in_dim);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 grid((unsigned)((out_dim + kPfRowsWg - 1) / kPfRowsWg),
+                    (unsigned)((n_tok + kPfTok - 1) / kPfTok));
+    (void)w_bytes;
+    k_prefill_q4k<<<grid, 256, kPfLds, s>>>(w, xh, unscale, out, n_tok, in_dim, out_dim);
+    return hipGetLastError();
+}
+
+}  // namespace rsllm_hip

@@ -1,0 +1,129 @@
+"""Prefill GEMM (Q4_K weights x bf16 activations, MFMA) against the oracle:
+the reference's matmul_quant_f32 (backend-cpu/src/ops/quant_matmul.rs:45-119)
+on f32(bf16 x). Bar: max|Δ|/max|y| <= 1e-3 (REL_TOL), checked over the whole
+output and also per token where a token has at least 1000 outputs (each
+token's activations are scaled separately on the device, so a token of small
+magnitude must not lose accuracy; with few outputs per token the per-token
+max|y| is dominated by chance cancellation, which the metric does not
+measure). Weights enter the matrix cores as f16 (d*sc, dmin*m rounded to f16,
+one f16 fma per weight), which puts the measured error at about 3e-4."""
+import numpy as np
+import pytest
+
+from conftest import REL_TOL, rel_err
+from rsllm_amd import synth
+from rsllm_amd.ggml import GgmlType as G
+
+pytestmark = pytest.mark.gpu
+
+
+def run_prefill(hip, w, xb, n_tok, in_dim, out_dim):
+    import torch
+    s = torch.cuda.current_stream().cuda_stream
+    d_w = torch.from_numpy(w).cuda()
+    d_x = torch.from_numpy(xb.view(np.int16)).cuda()
+    d_y = torch.full((n_tok * out_dim,), float("nan"), device="cuda")
+    hip.matmul_q4k_bf16_dev(d_y.data_ptr(), d_y.numel(), d_w.data_ptr(), w.size, d_x.data_ptr(),
+                            xb.size, n_tok, in_dim, out_dim, G.Q4_K, s)
+    torch.cuda.synchronize()
+    return d_y.cpu().numpy()
+
+
+def check(oracle, got, w, xb, tokens, n_tok, in_dim, out_dim, per_token=True):
+    """Compare rows `tokens` of the GPU output with the oracle on those tokens."""
+    xf = synth.bf16_bits_to_f32(xb.reshape(n_tok, in_dim)[tokens]).reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, xf, len(tokens), in_dim, out_dim, int(G.Q4_K))
+    assert rc == 0
+    g = got.reshape(n_tok, out_dim)[tokens]
+    want = want.reshape(len(tokens), out_dim)
+    assert not np.isnan(g).any()
+    err = rel_err(g, want)
+    print(f"prefill {out_dim}x{in_dim} T={n_tok}: rel err {err:.3e}")
+    assert err <= REL_TOL, f"rel err {err:.3e}"
+    if per_token and out_dim >= 1000:
+        worst = max(rel_err(g[i], want[i]) for i in range(len(tokens)))
+        assert worst <= REL_TOL, f"worst per-token rel err {worst:.3e}"
+    return err
+
+
+@pytest.mark.parametrize("out_dim,in_dim", [(1, 256), (17, 512), (256, 256), (300, 768),
+                                            (1000, 2048)])
+@pytest.mark.parametrize("n_tok", [1, 5, 128, 129, 300])
+def test_prefill_ragged_shapes(oracle, hip, out_dim, in_dim, n_tok):
+    w = synth.weight(G.Q4_K, out_dim, in_dim, seed=out_dim + 7 * n_tok)
+    xb = synth.bf16_activations(n_tok, in_dim, seed=in_dim + n_tok).reshape(-1)
+    got = run_prefill(hip, w, xb, n_tok, in_dim, out_dim)
+    check(oracle, got, w, xb, np.arange(n_tok), n_tok, in_dim, out_dim)
+
+
+def test_prefill_token_scales(oracle, hip):
+    """Tokens spanning 60 binades (1e-18 .. 1e18), a zero token, and one
+    token with a single nonzero element: each token is exact to 1e-3 of its
+    own outputs."""
+    out_dim, in_dim, n_tok = 1024, 1024, 9
+    w = synth.weight(G.Q4_K, out_dim, in_dim, seed=5)
+    x = synth.activations(n_tok, in_dim, seed=6)
+    for t, sc in enumerate([1e-18, 1e-9, 1e-3, 1.0, 1e3, 1e9, 1e18]):
+        x[t] *= sc
+    x[7] = 0.0
+    x[8] = 0.0
+    x[8, 300] = -2.5
+    xb = synth.f32_to_bf16_bits(x).reshape(-1)
+    got = run_prefill(hip, w, xb, n_tok, in_dim, out_dim)
+    yz = got.reshape(n_tok, out_dim)[7]
+    assert np.array_equal(yz, np.zeros(out_dim, np.float32))
+    check(oracle, got, w, xb, np.array([0, 1, 2, 3, 4, 5, 6, 8]), n_tok, in_dim, out_dim)
+
+
+def test_prefill_special_blocks(oracle, hip):
+    """Weight blocks with subnormal / zero d and dmin, and extreme scales."""
+    out_dim, in_dim, n_tok = 64, 512, 33
+    w = synth.weight(G.Q4_K, out_dim, in_dim, seed=8).reshape(-1, 144).copy()
+    g = np.random.default_rng(9)
+    idx = g.choice(w.shape[0], size=w.shape[0] // 3, replace=False)
+    choices = np.array([0x0000, 0x0001, 0x03FF, 0x0400, 0x1400, 0x2000], np.uint16)
+    d = g.choice(choices, size=(len(idx), 2))
+    w[idx, 0:4] = d.view(np.uint8).reshape(len(idx), 4)
+    w = w.reshape(-1)
+    xb = synth.bf16_activations(n_tok, in_dim, seed=10).reshape(-1)
+    got = run_prefill(hip, w, xb, n_tok, in_dim, out_dim)
+    check(oracle, got, w, xb, np.arange(n_tok), n_tok, in_dim, out_dim, per_token=False)
+
+
+@pytest.mark.parametrize("n_tok", [512, 2048])
+def test_prefill_config_shape(oracle, hip, n_tok):
+    """Config C4: Q4_K (out, in) = (14336, 4096), T in {512, 2048}. The oracle
+    runs on a spread subset of tokens (every token's output is independent)."""
+    out_dim, in_dim = 14336, 4096
+    w = synth.weight(G.Q4_K, out_dim, in_dim, seed=404)
+    xb = synth.bf16_activations(n_tok, in_dim, seed=405).reshape(-1)
+    got = run_prefill(hip, w, xb, n_tok, in_dim, out_dim)
+    tokens = np.unique(np.concatenate([np.arange(0, 8), np.arange(125, 131),
+                                       np.linspace(0, n_tok - 1, 24).astype(int)]))
+    err = check(oracle, got, w, xb, tokens, n_tok, in_dim, out_dim)
+    print(f"C4 T={n_tok}: rel err {err:.3e} over {len(tokens)} tokens")
+
+
+def test_prefill_validation(hip):
+    import torch
+    w = synth.weight(G.Q4_K, 4, 256, seed=1)
+    d_w = torch.from_numpy(w).cuda()
+    d_x = torch.zeros(2 * 256, dtype=torch.int16, device="cuda")
+    d_y = torch.zeros(2 * 4, device="cuda")
+    w8 = synth.weight(G.Q8_0, 4, 256, seed=1)
+    d_w8 = torch.from_numpy(w8).cuda()
+    with pytest.raises(hip.Unimplemented):
+        hip.matmul_q4k_bf16_dev(d_y.data_ptr(), 8, d_w8.data_ptr(), w8.size, d_x.data_ptr(), 512,
+                                2, 256, 4, G.Q8_0)
+    with pytest.raises(hip.NotBlockAligned):
+        hip.matmul_q4k_bf16_dev(d_y.data_ptr(), 8, d_w.data_ptr(), w.size, d_x.data_ptr(), 512, 2,
+                                100, 4, G.Q4_K)
+    with pytest.raises(hip.ShapeMismatch):
+        hip.matmul_q4k_bf16_dev(d_y.data_ptr(), 8, d_w.data_ptr(), w.size, d_x.data_ptr(), 511, 2,
+                                256, 4, G.Q4_K)
+    # n_tok = 0 is a no-op; in_dim = 0 gives zeros
+    hip.matmul_q4k_bf16_dev(None, 0, d_w.data_ptr(), w.size, None, 0, 0, 256, 4, G.Q4_K)
+    d_y.fill_(float("nan"))
+    hip.matmul_q4k_bf16_dev(d_y.data_ptr(), 8, None, 0, None, 0, 2, 0, 4, G.Q4_K)
+    torch.cuda.synchronize()
+    assert torch.equal(d_y.cpu(), torch.zeros(8))
