@@ -23,9 +23,11 @@
 // activations the B operand, so every lane ends with 4 consecutive outputs of
 // one token. The K loop runs in steps of
 // half a super-block (128 elements). Each step's activations (128 tokens x
-// 128 f16, 32 KB) and raw weight bytes (256 rows x 80 B: the 16-byte block
-// header and the 64 qs bytes of that half, 20 KB) are copied global->LDS by
-// DMA into one of three stage buffers, two steps ahead of their use.
+// 128 f16, 32 KB), weight bytes (256 rows x the 64 qs bytes of that half,
+// 16 KB) and block headers (256 rows x 16 bytes) are copied global->LDS by
+// DMA into one of two stage buffers while the other is computed. Each
+// thread turns its own row's header into f16 (d*sc_j, dmin*m_j) once per
+// step and leaves them in LDS for the lanes that dequantise that row.
 //
 // K order: inside a super-block, MFMA chunk c (0..7) gives lane group q
 // (lanes 16q..16q+15) sub-block 2q + (c & 1), positions 8 * (c >> 1) .. + 7,
@@ -45,11 +47,12 @@ constexpr int kPfTok = 128;                      // tokens per workgroup
 constexpr int kPfRowsWave = 64;                  // weight rows per wavefront
 constexpr int kPfRowsWg = 4 * kPfRowsWave;       // weight rows per workgroup
 constexpr int kPfXBytes = kPfTok * 256;          // activation stage: 128 rows x 128 f16
-constexpr int kPfWRow = 80;                      // weight stage row: header + 64 qs bytes
-constexpr int kPfWBytes = kPfRowsWg * kPfWRow;   // weight stage: 20 KB
-constexpr int kPfStage = kPfXBytes + kPfWBytes;  // 53248
-constexpr int kPfNStage = 3;                     // stage buffers (two steps of prefetch)
-constexpr int kPfLds = kPfNStage * kPfStage;     // 159744 bytes
+constexpr int kPfQsBytes = kPfRowsWg * 64;      // weight qs stage: 256 rows x 64 bytes
+constexpr int kPfHdBytes = kPfRowsWg * 16;      // weight header stage: 256 rows x 16 bytes
+constexpr int kPfStage = kPfXBytes + kPfQsBytes + kPfHdBytes;  // 53248
+constexpr int kPfNStage = 2;                    // stage buffers
+constexpr int kPfScOff = kPfNStage * kPfStage;  // f16 block scales: 256 rows x 32 bytes
+constexpr int kPfLds = kPfScOff + kPfRowsWg * 32;  // 114688 bytes
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -105,19 +108,6 @@ __global__ __launch_bounds__(256) void k_prefill_x(const uint16_t *__restrict__ 
 }
 
 // ---- GEMM -------------------------------------------------------------------------
-// (sc, m) of Q4_K sub-block j for a lane-dependent j, without branches
-// (q4_k_scale_min, dequant/mod.rs:48-58): both encodings are decoded and
-// selected.
-__device__ __forceinline__ void pf_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2,
-                                             uint32_t &sc, uint32_t &m) {
-    const int sh = 8 * (j & 3);
-    const uint32_t a = s0 >> sh, b = s1 >> sh, c = s2 >> sh;
-    const uint32_t sc_hi = (c & 15u) | ((a >> 2) & 48u);
-    const uint32_t m_hi = ((c >> 4) & 15u) | ((b >> 2) & 48u);
-    sc = j < 4 ? (a & 63u) : sc_hi;
-    m = j < 4 ? (b & 63u) : m_hi;
-}
-
 // Eight f16 weights of one chunk: qs bytes b0..b7 are dwords d0 (b0..b3) and
 // d1 (b4..b7); `hi` selects the high nibbles. w = q * dsc - dm.
 // A byte 0..15 read as fp8 e4m3 is q * 2^-9 exactly (subnormal for q < 8,
@@ -174,32 +164,35 @@ __global__ __launch_bounds__(256) void k_prefill_q4k(const uint8_t *__restrict__
         const int t = min(t0 + tl, n_tok - 1);
         xoff[p] = (uint32_t)t * (uint32_t)in_dim + 32u * (k >> 1) + 8u * (k & 1);
     }
-    // Weights: instruction p of this wave moves 16-byte pieces j = 64 g + i
-    // (g = 5 wv + p) of the stage, row j / 5, piece j % 5: piece 0 is the
-    // block header, piece 1 + q the qs bytes 32q + 16h .. + 15. The five
-    // instructions of wave wv cover exactly its own 64 rows. Bit 0 of woff
-    // marks a qs piece (offset + 16h).
-    uint32_t woff[5];
+    // Weight qs: instruction p (g = 4 wv + p) moves pieces j = 64 g + i, row
+    // j / 4, slot j % 4 holding qs piece k = slot ^ ((row >> 2) & 3) (bytes
+    // 32k + 16h .. + 15 of the block), so the operand reads below hit 16
+    // distinct bank groups. Headers: one instruction per wave, lane i moves
+    // the header of row 64 wv + i. Both cover exactly this wave's own rows.
+    uint32_t qoff[4];
 #pragma unroll
-    for (int p = 0; p < 5; p++) {
-        const int j = 64 * (5 * wv + p) + lane;
-        const int row = j / 5, part = j - 5 * row;
+    for (int p = 0; p < 4; p++) {
+        const int j = 64 * (4 * wv + p) + lane;
+        const int row = j >> 2, k = (j & 3) ^ ((row >> 2) & 3);
         const uint32_t rowg = (uint32_t)min(n0 + row, out_dim - 1);
-        woff[p] = rowg * (uint32_t)nb * 144u + (part ? 16u + 32u * (part - 1) + 1u : 0u);
+        qoff[p] = rowg * (uint32_t)nb * 144u + 16u + 32u * k;
     }
-    auto stage = [&](int st, uint8_t *buf) {
+    const uint32_t hoff = (uint32_t)min(n0 + 64 * wv + lane, out_dim - 1) * (uint32_t)nb * 144u;
+    // DMA instruction p (0..12) of stage st into buf: 0..7 activations,
+    // 8..11 qs, 12 headers.
+    auto dma_piece = [&](int st, uint8_t *buf, int p) {
         const int s = st >> 1, h = st & 1;
-#pragma unroll
-        for (int p = 0; p < 8; p++)
+        if (p < 8)
             __builtin_amdgcn_global_load_lds((const void *)(xh + xoff[p] + s * 256 + 16 * h),
                                              (lds_void *)(buf + 1024 * (8 * wv + p)), 16, 0, 0);
-#pragma unroll
-        for (int p = 0; p < 5; p++) {
-            const uint32_t o = (woff[p] & ~1u) + (uint32_t)s * 144u + (woff[p] & 1u) * 16u * h;
-            __builtin_amdgcn_global_load_lds((const void *)(w + o),
-                                             (lds_void *)(buf + kPfXBytes + 1024 * (5 * wv + p)),
-                                             16, 0, 0);
-        }
+        else if (p < 12)
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(w + qoff[p - 8] + s * 144 + 16 * h),
+                (lds_void *)(buf + kPfXBytes + 1024 * (4 * wv + p - 8)), 16, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(w + hoff + s * 144),
+                (lds_void *)(buf + kPfXBytes + kPfQsBytes + 1024 * wv), 16, 0, 0);
     };
     // A operand of group g (chunk g / 8 of the step, row tile g % 8):
     // elements of sub-block 2q + (c & 1) at positions 16h + 8 (c >> 1) .. + 7.
@@ -208,8 +201,10 @@ __global__ __launch_bounds__(256) void k_prefill_q4k(const uint8_t *__restrict__
         const int k = 2 * (2 * q + (c & 1)) + (c >> 1);
         return *reinterpret_cast<const h8 *>(buf + (mt * 16 + r16) * 256 + ((k ^ r16) << 4));
     };
-    // this lane's weight rows in the stage: wave rows 16 nt + r16
-    const int wrow = (wv * kPfRowsWave + r16) * kPfWRow;
+    // this lane's weight rows in the stage: wave rows 16 nt + r16; qs piece
+    // q sits in slot q ^ ((row >> 2) & 3) = q ^ (r16 >> 2) (rows 16 nt + r16)
+    const int wrow = wv * kPfRowsWave + r16;
+    const int qslot = q ^ (r16 >> 2);
 
     f4 acc[8][4];
 #pragma unroll
@@ -217,48 +212,66 @@ __global__ __launch_bounds__(256) void k_prefill_q4k(const uint8_t *__restrict__
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
 
-    // f16 (d*sc, dmin*m) of sub-blocks 2q + hb, broadcast to both halves
-    h2 dsc[4][2], dmn[4][2];
+    // f16 scales of this lane's sub-blocks 2q, 2q + 1: .x = (d*sc_2q,
+    // d*sc_2q+1), .y = (dmin*m_2q, dmin*m_2q+1)
+    uint2 sc[4];
     uint4 qs[4];
     h8 bq[4];
-    // Weight bytes of one step for this lane (qs piece of its q) and the
-    // block scales (every stage carries the block header).
+    uint8_t *const scl = smem + kPfScOff;
     auto load_step_weights = [&](const uint8_t *buf) {
-        const uint8_t *wb = buf + kPfXBytes + wrow;
+        // this thread's row 64 wv + lane: header -> 16 f16 scales into LDS,
+        // record layout per q: {d*sc_2q, d*sc_2q+1, dmin*m_2q, dmin*m_2q+1}
+        // (q4_k_scale_min, dequant/mod.rs:48-58, on four bytes at a time)
+        {
+            const uint4 hd = *reinterpret_cast<const uint4 *>(buf + kPfXBytes + kPfQsBytes + 16 * (64 * wv + lane));
+            const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+            const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu, m_lo = hd.z & 0x3F3F3F3Fu;
+            const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+            const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+            uint32_t rec[8];
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+                // sub-blocks 2qq, 2qq + 1: bytes of the low (j < 4) or high word
+                const uint32_t sw = qq < 2 ? sc_lo : sc_hi, mw = qq < 2 ? m_lo : m_hi;
+                const int b = 2 * (qq & 1);
+                const _Float16 a0 = (_Float16)(d * (float)((sw >> (8 * b)) & 0xFFu));
+                const _Float16 a1 = (_Float16)(d * (float)((sw >> (8 * b + 8)) & 0xFFu));
+                const _Float16 m0 = (_Float16)(dmin * (float)((mw >> (8 * b)) & 0xFFu));
+                const _Float16 m1 = (_Float16)(dmin * (float)((mw >> (8 * b + 8)) & 0xFFu));
+                rec[2 * qq] = __builtin_bit_cast(uint32_t, h2{a0, a1});
+                rec[2 * qq + 1] = __builtin_bit_cast(uint32_t, h2{m0, m1});
+            }
+            uint4 *dst = reinterpret_cast<uint4 *>(scl + 32 * (64 * wv + lane));
+            dst[0] = make_uint4(rec[0], rec[1], rec[2], rec[3]);
+            dst[1] = make_uint4(rec[4], rec[5], rec[6], rec[7]);
+        }
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) {
-            qs[nt] = *reinterpret_cast<const uint4 *>(wb + nt * 16 * kPfWRow + 16 + 16 * q);
-            const uint4 hd = *reinterpret_cast<const uint4 *>(wb + nt * 16 * kPfWRow);
-            const float d = f16_to_f32(hd.x & 0xFFFFu);
-            const float dmin = f16_to_f32(hd.x >> 16);
-#pragma unroll
-            for (int hb = 0; hb < 2; hb++) {
-                uint32_t sc, m;
-                pf_scale_min(2 * q + hb, hd.y, hd.z, hd.w, sc, m);
-                const _Float16 a = (_Float16)(d * (float)sc), b = (_Float16)(dmin * (float)m);
-                dsc[nt][hb] = h2{a, a};
-                dmn[nt][hb] = h2{b, b};
-            }
+            const int row = wrow + 16 * nt;
+            qs[nt] = *reinterpret_cast<const uint4 *>(buf + kPfXBytes + row * 64 + qslot * 16);
+            sc[nt] = *reinterpret_cast<const uint2 *>(scl + row * 32 + q * 8);
         }
     };
     // B operands of chunk c (0..3) of the current step
     auto dequant = [&](int c, int nt) -> h8 {
         const int run = c >> 1;  // bytes 8 run .. 8 run + 7 of the lane's 16
-        return pf_dequant8(pf_u4(qs[nt], 2 * run), pf_u4(qs[nt], 2 * run + 1), (c & 1) != 0,
-                           dsc[nt][c & 1], dmn[nt][c & 1]);
+        const h2 d2 = __builtin_bit_cast(h2, sc[nt].x), m2 = __builtin_bit_cast(h2, sc[nt].y);
+        const h2 ds = (c & 1) ? d2.yy : d2.xx;
+        const h2 dm = (c & 1) ? m2.yy : m2.xx;
+        return pf_dequant8(pf_u4(qs[nt], 2 * run), pf_u4(qs[nt], 2 * run + 1), (c & 1) != 0, ds,
+                           dm);
     };
 
-    // Stages st + 1 and st + 2 are in flight while step st is computed: the
-    // DMA of stage st + 3 is issued right after the barrier in step st, into
-    // the buffer step st used. Stage indices past the last step repeat the
-    // last stage into a buffer nothing reads again, so every step has the
-    // same number of DMA instructions in flight.
-    auto sbuf = [&](int st) { return smem + (st % kPfNStage) * kPfStage; };
-    stage(0, sbuf(0));
-    stage(1, sbuf(1));
-    stage(min(2, nsteps - 1), sbuf(2));
-    __builtin_amdgcn_s_waitcnt(0x4F7A);  // vmcnt(26): stage 0 of this wave landed
+    // Stage st + 1 is in flight while step st is computed: its DMA is issued
+    // right after the barrier in step st - 1, into the buffer step st - 1
+    // used. The last step's DMA repeats the last stage into a buffer nothing
+    // reads again.
+    auto sbuf = [&](int st) { return smem + (st & 1) * kPfStage; };
+#pragma unroll
+    for (int p = 0; p < 13; p++) dma_piece(0, sbuf(0), p);
     __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 4; p++) dma_piece(1, sbuf(1), p);  // nsteps >= 2 (in_dim >= 256)
     load_step_weights(sbuf(0));
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) bq[nt] = dequant(0, nt);
@@ -267,7 +280,10 @@ __global__ __launch_bounds__(256) void k_prefill_q4k(const uint8_t *__restrict__
     // One K step: 32 groups (4 chunks x 8 row tiles) of 4 MFMAs. Operand
     // reads run two groups ahead (across the step boundary), B operands are
     // dequantised one chunk ahead (chunk 3 prepares the next step's chunk 0
-    // from the next stage's weight rows). MORE: a next step exists.
+    // from the next stage's weight rows). The DMA of stage st + 2 is spread
+    // so the CU's return path is never flooded: instructions 0..3 after the
+    // barrier in groups 30, 31 of step st, 4..12 one per group in groups
+    // 0..8 of step st + 1. MORE: a next step exists.
     auto step = [&](int st, auto more_tag) {
         constexpr bool more = decltype(more_tag)::value;
         uint8_t *buf = sbuf(st);
@@ -278,21 +294,26 @@ __global__ __launch_bounds__(256) void k_prefill_q4k(const uint8_t *__restrict__
             __builtin_amdgcn_sched_barrier(0);
             if (more && c == 3) {
                 // stage st + 1: this wave's own weight rows are in once its
-                // own DMA has completed (stage st + 2 may still be in flight)
-                __builtin_amdgcn_s_waitcnt(0x0F7D);  // vmcnt(13)
+                // own DMA has completed
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
                 load_step_weights(nbuf);
             }
 #pragma unroll
             for (int mt = 0; mt < 8; mt++) {
                 const int g = 8 * c + mt;
+                if (more && g <= 8)  // rest of stage st + 1
+                    dma_piece(min(st + 1, nsteps - 1), buf + (nbuf - buf), 4 + g);
                 if (more && g == 30) {
                     // every wave has its operands up to group 31 in registers
                     // and its stage-(st+1) DMA complete: the next stage's
                     // activation rows become readable and `buf` is free for
-                    // stage st + 3. (The barrier's own wait also covers
-                    // stage st + 2, whose DMA was issued a step earlier.)
+                    // stage st + 2 (the last stage again when there is none;
+                    // nothing reads it then)
                     __syncthreads();
-                    stage(min(st + 3, nsteps - 1), buf);
+                }
+                if (more && g >= 30) {
+                    dma_piece(min(st + 2, nsteps - 1), buf, 2 * (g - 30));
+                    dma_piece(min(st + 2, nsteps - 1), buf, 2 * (g - 30) + 1);
                 }
                 h8 a2 = a1;
                 if (g + 2 < 32) a2 = read_a(buf, g + 2);
@@ -377,14 +398,15 @@ hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *
         if (e != hipSuccess) return e;
         attr_set = true;
     }
+    (void)w_bytes;
+    const size_t tiles = ((size_t)n_tok + kPfTok - 1) / kPfTok;
+    const size_t xb = ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16;
     _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
-    float *unscale = reinterpret_cast<float *>(scratch + ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16);
+    float *unscale = reinterpret_cast<float *>(scratch + xb);
     k_prefill_x<<<(unsigned)n_tok, 256, 0, s>>>(x_bf16, xh, unscale, in_dim);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 grid((unsigned)((out_dim + kPfRowsWg - 1) / kPfRowsWg),
-                    (unsigned)((n_tok + kPfTok - 1) / kPfTok));
-    (void)w_bytes;
+    const dim3 grid((unsigned)((out_dim + kPfRowsWg - 1) / kPfRowsWg), (unsigned)tiles);
     k_prefill_q4k<<<grid, 256, kPfLds, s>>>(w, xh, unscale, out, n_tok, in_dim, out_dim);
     return hipGetLastError();
 }
