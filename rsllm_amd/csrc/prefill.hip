@@ -57,32 +57,64 @@ constexpr int kPfLds = kPfScOff + kPfRowsWg * 32;  // 114688 bytes
 typedef __attribute__((address_space(3))) void lds_void;
 
 // ---- activation pre-pass: bf16 -> scaled f16 ----------------------------------
-// One workgroup per token; 16-byte loads and stores (8 elements per access).
-// in_dim is a multiple of 256.
+// One workgroup (256 threads) per token; each thread moves 16-byte pieces (8
+// elements). Up to kPxCache pieces per thread (in_dim <= 16384) stay in
+// registers between the max pass and the conversion, so the token is read
+// once; longer rows are read twice. in_dim is a multiple of 256.
+constexpr int kPxCache = 8;
+
+__device__ __forceinline__ uint32_t px_absmax_bits(const uint4 v) {
+    // |bf16| bit patterns order like the magnitudes (finite values)
+    const uint32_t a = max(v.x & 0x7FFF7FFFu, v.y & 0x7FFF7FFFu);
+    const uint32_t b = max(v.z & 0x7FFF7FFFu, v.w & 0x7FFF7FFFu);
+    const uint32_t c = max(a, b);
+    return max(c & 0xFFFFu, c >> 16);
+}
+
+__device__ __forceinline__ uint4 px_convert(const uint4 v, float up) {
+    const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const _Float16 lo = (_Float16)(__uint_as_float(in[k] << 16) * up);
+        const _Float16 hi = (_Float16)(__uint_as_float(in[k] & 0xFFFF0000u) * up);
+        o[k] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 __global__ __launch_bounds__(256) void k_prefill_x(const uint16_t *__restrict__ x,
                                                    _Float16 *__restrict__ xh,
                                                    float *__restrict__ unscale, int in_dim) {
-    __shared__ float red[4];
+    __shared__ uint32_t red[4];
     const int t = blockIdx.x, tid = threadIdx.x;
     const uint4 *xt = reinterpret_cast<const uint4 *>(x + (size_t)t * in_dim);
-    const int n8 = in_dim >> 3;
-    // |bf16| bits: the largest finite magnitude has the largest bit pattern
+    uint4 *ht = reinterpret_cast<uint4 *>(xh + (size_t)t * in_dim);
+    const int n8 = in_dim >> 3;  // 16-byte pieces in the row (a multiple of 32)
+    const bool cached = n8 <= 256 * kPxCache;
+    uint4 c[kPxCache];
     uint32_t mbits = 0;
-    for (int i = tid; i < n8; i += 256) {
-        const uint4 v = xt[i];
-        const uint32_t a = max(v.x & 0x7FFF7FFFu, v.y & 0x7FFF7FFFu);
-        const uint32_t b = max(v.z & 0x7FFF7FFFu, v.w & 0x7FFF7FFFu);
-        const uint32_t c = max(a, b);
-        mbits = max(mbits, max(c & 0xFFFFu, c >> 16));
+    if (cached) {
+#pragma unroll
+        for (int i = 0; i < kPxCache; i++) {
+            const int idx = i * 256 + tid;
+            if (idx < n8) {
+                c[i] = xt[idx];
+                mbits = max(mbits, px_absmax_bits(c[i]));
+            }
+        }
+    } else {
+        for (int idx = tid; idx < n8; idx += 256) mbits = max(mbits, px_absmax_bits(xt[idx]));
     }
     // NaN patterns (above 0x7F80) do not pick the scale; infinity does
     if (mbits > 0x7F80u) mbits = 0;
-    float amax = __uint_as_float(mbits << 16);
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    for (int off = 32; off >= 1; off >>= 1) mbits = max(mbits, (uint32_t)__shfl_xor((int)mbits, off, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = mbits;
     __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mbits = max(max(red[0], red[1]), max(red[2], red[3]));
+    const float amax = __uint_as_float(mbits << 16);
     // e: amax * 2^e in [2^14, 2^15) for finite nonzero amax (exponent from the bits)
     int e = 0;
     if (amax > 0.f && amax <= 3.4e38f) {
@@ -92,18 +124,14 @@ __global__ __launch_bounds__(256) void k_prefill_x(const uint16_t *__restrict__ 
     }
     const float up = __uint_as_float((uint32_t)(127 + e) << 23);
     if (tid == 0) unscale[t] = __uint_as_float((uint32_t)(127 - e) << 23);
-    uint4 *ht = reinterpret_cast<uint4 *>(xh + (size_t)t * in_dim);
-    for (int i = tid; i < n8; i += 256) {
-        const uint4 v = xt[i];
-        const uint32_t in[4] = {v.x, v.y, v.z, v.w};
-        uint32_t o[4];
+    if (cached) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const _Float16 lo = (_Float16)(__uint_as_float(in[k] << 16) * up);
-            const _Float16 hi = (_Float16)(__uint_as_float(in[k] & 0xFFFF0000u) * up);
-            o[k] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+        for (int i = 0; i < kPxCache; i++) {
+            const int idx = i * 256 + tid;
+            if (idx < n8) ht[idx] = px_convert(c[i], up);
         }
-        ht[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    } else {
+        for (int idx = tid; idx < n8; idx += 256) ht[idx] = px_convert(xt[idx], up);
     }
 }
 

@@ -56,6 +56,17 @@ def test_prefill_ragged_shapes(oracle, hip, out_dim, in_dim, n_tok):
     check(oracle, got, w, xb, np.arange(n_tok), n_tok, in_dim, out_dim)
 
 
+@pytest.mark.parametrize("in_dim", [16384, 16640])
+def test_prefill_long_rows(oracle, hip, in_dim):
+    """Rows at and past the activation pre-pass's register cache (16384
+    elements per token): the longer row is read twice instead of once."""
+    out_dim, n_tok = 64, 3
+    w = synth.weight(G.Q4_K, out_dim, in_dim, seed=in_dim)
+    xb = synth.bf16_activations(n_tok, in_dim, seed=in_dim + 1).reshape(-1)
+    got = run_prefill(hip, w, xb, n_tok, in_dim, out_dim)
+    check(oracle, got, w, xb, np.arange(n_tok), n_tok, in_dim, out_dim)
+
+
 def test_prefill_token_scales(oracle, hip):
     """Tokens spanning 60 binades (1e-18 .. 1e18), a zero token, and one
     token with a single nonzero element: each token is exact to 1e-3 of its
