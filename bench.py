@@ -19,6 +19,12 @@ roofline     = the same bytes per launch / mean duration of the dominant kernel
 cpu_baseline = the CPU oracle (a C restatement of the reference CPU path,
                one thread per token as the reference's rayon split gives at
                batch 1) timed on a bounded sample of the same GEMVs.
+prefill      = BASELINE.json configs[4] (C4): Q4_K weight (out, in) =
+               (14336, 4096) times bf16 activations [T x 4096], T = 512 and
+               2048, fp32 output, on the MFMA path; TFLOP/s = 2 T in out / the
+               event-timed mean of a run of back-to-back calls (activation
+               pre-pass + GEMM), against the 2.5 PFLOP/s dense f16/bf16 MFMA
+               peak, with its own bounded CPU-oracle sample.
 
 `--gpus N` with N > 1 exits: this build targets one GPU.
 """
@@ -33,6 +39,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
 def parse():
@@ -44,7 +51,80 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--extra", action="store_true", help="also time the other configs")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the C4 prefill leg")
+    ap.add_argument("--prefill-iters", type=int, default=20)
     return ap.parse_args()
+
+
+def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
+    """C4: Q4_K (14336, 4096) x bf16 [T x 4096] on the MFMA path, T = 512, 2048."""
+    import torch
+    out_dim, in_dim = 14336, 4096
+    w_host = synth.weight(G.Q4_K, out_dim, in_dim, seed=404)
+    d_w = torch.from_numpy(w_host).to(dev)
+    sptr = stream.cuda_stream
+    res = {"workload": "C4 Q4_K prefill GEMM (out, in) = (14336, 4096), bf16 x [T x 4096]",
+           "peak_tflops": MFMA_F16_PEAK_TFLOPS, "by_tokens": []}
+    xs_host = {}
+    for T in (512, 2048):
+        xb = synth.bf16_activations(T, in_dim, seed=405).reshape(-1)
+        xs_host[T] = xb
+        d_x = torch.from_numpy(xb.view(np.int16)).to(dev)
+        d_y = torch.empty(T * out_dim, dtype=torch.float32, device=dev)
+
+        def call():
+            B.matmul_q4k_bf16_dev(d_y.data_ptr(), d_y.numel(), d_w.data_ptr(), d_w.numel(),
+                                  d_x.data_ptr(), d_x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(iters):
+            call()
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / iters
+        tflops = 2.0 * T * in_dim * out_dim / (us * 1e-6) / 1e12
+        entry = {"tokens": T, "us_per_op": round(us, 2), "tflops": round(tflops, 1),
+                 "frac_of_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+        if with_cpu and T == 512:
+            # parity spot check on a spread of tokens
+            sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+            from oracle import oracle as O
+            toks = np.linspace(0, T - 1, 8).astype(int)
+            xf = synth.bf16_bits_to_f32(xb.reshape(T, in_dim)[toks]).reshape(-1)
+            rc, want = O.matmul_quant_f32(w_host, xf, len(toks), in_dim, out_dim, int(G.Q4_K))
+            got = d_y.cpu().numpy().reshape(T, out_dim)[toks].reshape(-1)
+            entry["check"] = {"max_rel_err_vs_oracle": float(np.abs(got - want).max() /
+                                                             np.abs(want).max()),
+                              "tokens_checked": len(toks), "tolerance": 1e-3}
+        res["by_tokens"].append(entry)
+        del d_x, d_y
+    best = max(res["by_tokens"], key=lambda e: e["tflops"])
+    res["roofline"] = {"bound": "mfma", "achieved": best["tflops"], "peak": MFMA_F16_PEAK_TFLOPS,
+                       "unit": "TFLOP/s", "frac": best["frac_of_peak"],
+                       "tokens": best["tokens"]}
+    if with_cpu:
+        # reference CPU path (oracle, all host threads = min(n_tok, cores) as
+        # the rayon split gives) on a bounded token sample, scaled to TFLOP/s
+        from oracle import oracle as O
+        n_thr = O.lib().orc_num_cores()
+        xb = xs_host[512]
+        n_done, t_cpu = 0, 0.0
+        while t_cpu < cpu_seconds / 2:
+            toks = n_thr
+            xf = synth.bf16_bits_to_f32(xb.reshape(512, in_dim)[:toks]).reshape(-1)
+            t0 = time.perf_counter()
+            O.matmul_quant_f32(w_host, xf, toks, in_dim, out_dim, int(G.Q4_K), n_threads=n_thr)
+            t_cpu += time.perf_counter() - t0
+            n_done += toks
+        res["cpu_baseline"] = {
+            "value": 2.0 * n_done * in_dim * out_dim / t_cpu / 1e12, "unit": "TFLOP/s",
+            "cores": n_thr, "kind": "port",
+            "sample": f"{n_done} tokens of C4 (Q4_K 14336x4096) in {t_cpu:.1f} s, oracle "
+                      f"matmul_quant_f32 with one thread per token ({n_thr} threads)"}
+    return res
 
 
 def main():
@@ -199,6 +279,10 @@ def main():
             "us_per_op": t_cpu / n_ops * 1e6,
         }
 
+    prefill = None if args.no_prefill else bench_prefill(B, synth, G, dev, stream,
+                                                          args.prefill_iters, not args.no_cpu,
+                                                          args.cpu_seconds)
+
     line = {
         "metric": "Q4_K/Q6_K GEMV GB/s (% of HBM peak); Q4_K prefill GEMM TFLOP/s",
         "value": round(value, 2),
@@ -235,6 +319,7 @@ def main():
         "per_kernel": per_kernel,
         "cpu_baseline": cpu_baseline,
         "check": check,
+        "prefill": prefill,
     }
     print(json.dumps(line))
 
