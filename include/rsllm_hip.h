@@ -168,6 +168,43 @@ int rsllm_hip_matmul_q4k_bf16_dev(float *out, size_t out_len, const uint8_t *wei
                                   size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype,
                                   rsllm_hip_stream_t stream);
 
+/* ---- routed experts (MoE) ---------------------------------------------------
+ * accumulate_moe_outputs (models/src/dsv4/moe.rs:648-707) with
+ * apply_expert_swiglu (:479-502) and apply_swiglu_clamp (:515-531): for
+ * every token t and slot i with weights[t*k+i] != 0 and e = ids[t*k+i]:
+ *   out[t] += weights[t*k+i] * down[e] (silu(min(gate[e] x_t, c)) *
+ *                                       clamp(up[e] x_t, -c, c))
+ * with the clamp applied only when c > 1e-6 (NaN passes through), slots
+ * accumulated in i order. `out` [n_tok x n_embd] is ACCUMULATED into (the
+ * caller pre-clears or pre-fills it, as the reference's caller does).
+ * gate, up: n_expert stacked [n_ff x n_embd] matrices of dtype_gate_up
+ * (gate_up_len bytes each blob); down: n_expert stacked [n_embd x n_ff]
+ * matrices of dtype_down (StackedExperts::expert, moe.rs:69-108). Q4_K
+ * blobs are the GGUF bytes; other dtypes are in the device layout
+ * (rsllm_hip_prepare_weights_dev over the whole blob), which needs each
+ * expert's block count to be a multiple of 8. ids, weights: n_tok * k.
+ * Validation: dtypes, then n_embd % block(gate/up) and n_ff % block(down)
+ * (NotBlockAligned), blob lengths, x, out, ids lengths (ShapeMismatch);
+ * n_tok * k <= 4096. The reference panics on an expert id out of range:
+ * the host entry point returns RSLLM_HIP_ERR_INVALID_ARGUMENT, the device
+ * entry point (which cannot inspect ids) skips such slots. Uses a
+ * per-thread device workspace. */
+int rsllm_hip_moe_routed_dev(float *out, size_t out_len, const float *x, size_t x_len,
+                             const uint8_t *gate, const uint8_t *up, size_t gate_up_len,
+                             const uint8_t *down, size_t down_len, const int32_t *ids,
+                             const float *weights, size_t ids_len, size_t n_tok, size_t n_embd,
+                             size_t n_ff, size_t n_expert, size_t k, uint32_t dtype_gate_up,
+                             uint32_t dtype_down, float clamp, rsllm_hip_stream_t stream);
+/* Host-pointer form (synchronous). Expert blobs registered with
+ * rsllm_hip_register_weights (in_dim n_embd for gate/up, n_ff for down) are
+ * used from the device; otherwise they are uploaded for the call. */
+int rsllm_hip_moe_routed(float *out, size_t out_len, const float *x, size_t x_len,
+                         const uint8_t *gate, const uint8_t *up, size_t gate_up_len,
+                         const uint8_t *down, size_t down_len, const int32_t *ids,
+                         const float *weights, size_t ids_len, size_t n_tok, size_t n_embd,
+                         size_t n_ff, size_t n_expert, size_t k, uint32_t dtype_gate_up,
+                         uint32_t dtype_down, float clamp);
+
 /* ---- dequantisation ------------------------------------------------------ */
 
 /* dequant_to_f32 (rsllm-gguf/src/dequant/mod.rs:69-85): decode `src` (GGUF

@@ -59,6 +59,10 @@ def lib() -> ctypes.CDLL:
         L.orc_matmul_q8_0_batch.argtypes = [P, S, P, S, P, S, P, S, S, S, S, I]
         L.orc_silu.argtypes = [ctypes.c_float]
         L.orc_silu.restype = ctypes.c_float
+        L.orc_sigmoid.argtypes = [ctypes.c_float]
+        L.orc_sigmoid.restype = ctypes.c_float
+        L.orc_swiglu_clamp.argtypes = [P, P, S, ctypes.c_float]
+        L.orc_swiglu_clamp.restype = None
         L.orc_moe_routed.argtypes = [P, P, S, S, S, P, P, P, U32, U32, S, P, P, S, ctypes.c_float]
         L.orc_last_detail.argtypes = [P, P]
         L.orc_num_cores.restype = I
@@ -152,6 +156,19 @@ def matmul_q8_0_batch(w, xq, xscale, n_tok, in_dim, out_dim, n_threads=0):
 
 def silu(x: float) -> float:
     return lib().orc_silu(x)
+
+
+def sigmoid(x: float) -> float:
+    return lib().orc_sigmoid(x)
+
+
+def swiglu_clamp(gate: np.ndarray, up: np.ndarray, c: float):
+    """apply_swiglu_clamp on copies; returns (gate, up)."""
+    g = np.ascontiguousarray(gate, dtype=np.float32).copy()
+    u = np.ascontiguousarray(up, dtype=np.float32).copy()
+    assert g.size == u.size
+    lib().orc_swiglu_clamp(_p(g), _p(u), g.size, ctypes.c_float(c))
+    return g, u
 
 
 def moe_routed(out, x, n_tok, n_embd, n_ff, gate, up, down, dtype_gu, dtype_down, n_expert, ids,

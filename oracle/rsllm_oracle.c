@@ -474,6 +474,19 @@ static float sigmoid_stable(float x) {
 }
 
 float orc_silu(float x) { return x * sigmoid_stable(x); }
+float orc_sigmoid(float x) { return sigmoid_stable(x); }
+
+/* apply_swiglu_clamp, moe.rs:515-531: only when c > 1e-6; gate from above,
+ * up both sides; NaN passes (every comparison with NaN is false). */
+void orc_swiglu_clamp(float *h_gate, float *h_up, size_t n, float c) {
+    if (c <= 1e-6f) return;
+    for (size_t j = 0; j < n; j++)
+        if (h_gate[j] > c) h_gate[j] = c;
+    for (size_t j = 0; j < n; j++) {
+        if (h_up[j] > c) h_up[j] = c;
+        else if (h_up[j] < -c) h_up[j] = -c;
+    }
+}
 
 /* ---- routed experts: moe.rs:479-531 and :648-707 -------------------------- */
 int orc_moe_routed(float *out, const float *x, size_t n_tok, size_t n_embd, size_t n_ff,
@@ -505,14 +518,7 @@ int orc_moe_routed(float *out, const float *x, size_t n_tok, size_t n_embd, size
                 rc = orc_matmul_quant_f32(h_up, n_ff, up + (size_t)e * gu_stride, gu_stride, x_t,
                                           n_embd, 1, n_embd, n_ff, dtype_gate_up, 1, 1);
             if (rc) break;
-            if (clamp > 1e-6f) { /* apply_swiglu_clamp :515-531 */
-                for (size_t j = 0; j < n_ff; j++)
-                    if (h_gate[j] > clamp) h_gate[j] = clamp;
-                for (size_t j = 0; j < n_ff; j++) {
-                    if (h_up[j] > clamp) h_up[j] = clamp;
-                    else if (h_up[j] < -clamp) h_up[j] = -clamp;
-                }
-            }
+            orc_swiglu_clamp(h_gate, h_up, n_ff, clamp);
             for (size_t j = 0; j < n_ff; j++) h_act[j] = orc_silu(h_gate[j]) * h_up[j];
             rc = orc_matmul_quant_f32(eo, n_embd, down + (size_t)e * d_stride, d_stride, h_act,
                                       n_ff, 1, n_ff, n_embd, dtype_down, 1, 1);

@@ -96,7 +96,10 @@ int orc_matmul_q8_0_batch(float *out, size_t out_len, const uint8_t *w, size_t w
                           int n_threads);
 
 /* sigmoid / silu / swiglu, rsllm-backend-cpu/src/ops/scalar.rs:57-86 */
+float orc_sigmoid(float x);
 float orc_silu(float x);
+/* apply_swiglu_clamp, rsllm-models/src/dsv4/moe.rs:515-531 (in place) */
+void orc_swiglu_clamp(float *h_gate, float *h_up, size_t n, float c);
 
 /* Routed-expert composition: accumulate_moe_outputs moe.rs:648-707 with
  * apply_expert_swiglu moe.rs:479-502 and apply_swiglu_clamp moe.rs:515-531,

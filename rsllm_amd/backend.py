@@ -134,6 +134,10 @@ SIGNATURES = {
     "rsllm_hip_quantize_x_dev": ([_U32, _P, _S, _S, _S, _P, _S, _P], _I),
     "rsllm_hip_matmul_prequant_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _P], _I),
     "rsllm_hip_matmul_q4k_bf16_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _P], _I),
+    "rsllm_hip_moe_routed_dev": ([_P, _S, _P, _S, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _S,
+                                  _S, _U32, _U32, ctypes.c_float, _P], _I),
+    "rsllm_hip_moe_routed": ([_P, _S, _P, _S, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _S, _S,
+                              _U32, _U32, ctypes.c_float], _I),
 }
 
 
@@ -265,6 +269,42 @@ def matmul_q4k_bf16_dev(out_ptr: int, out_len: int, w_ptr: int, w_len: int, x_pt
                                              int(dtype), stream or None))
 
 
+def moe_routed(out: np.ndarray, x: np.ndarray, gate, up, down, ids: np.ndarray,
+               weights: np.ndarray, n_tok: int, n_embd: int, n_ff: int, n_expert: int, k: int,
+               dtype_gate_up, dtype_down, clamp: float = 10.0) -> None:
+    """Routed experts (accumulate_moe_outputs): ``out`` [n_tok x n_embd] is
+    accumulated into. gate/up/down are the stacked expert blobs (bytes)."""
+    po, no = _host_f32(out, "out")
+    px, nx = _host_f32(x, "x")
+    pg, ng = _host_ptr(gate)
+    pu, nu = _host_ptr(up)
+    pd, nd = _host_ptr(down)
+    if nu != ng:
+        raise ShapeMismatch("moe_routed: gate and up blobs differ in size")
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    if ids.size != weights.size:
+        raise ShapeMismatch("moe_routed: ids and weights differ in length")
+    pi, ni = _host_ptr(ids)
+    pw, _ = _host_ptr(weights)
+    _check(LIB.rsllm_hip_moe_routed(po, no, px, nx, pg, pu, ng, pd, nd, pi, pw, ni, n_tok, n_embd,
+                                    n_ff, n_expert, k, int(dtype_gate_up), int(dtype_down),
+                                    clamp))
+
+
+def moe_routed_dev(out_ptr: int, out_len: int, x_ptr: int, x_len: int, gate_ptr: int,
+                   up_ptr: int, gate_up_len: int, down_ptr: int, down_len: int, ids_ptr: int,
+                   weights_ptr: int, ids_len: int, n_tok: int, n_embd: int, n_ff: int,
+                   n_expert: int, k: int, dtype_gate_up, dtype_down, clamp: float = 10.0,
+                   stream: int = 0) -> None:
+    _check(LIB.rsllm_hip_moe_routed_dev(out_ptr or None, out_len, x_ptr or None, x_len,
+                                        gate_ptr or None, up_ptr or None, gate_up_len,
+                                        down_ptr or None, down_len, ids_ptr or None,
+                                        weights_ptr or None, ids_len, n_tok, n_embd, n_ff,
+                                        n_expert, k, int(dtype_gate_up), int(dtype_down), clamp,
+                                        stream or None))
+
+
 def prepare_weights_dev(dst_ptr: int, src_ptr: int, nbytes: int, dtype, in_dim: int,
                         stream: int = 0) -> None:
     _check(LIB.rsllm_hip_prepare_weights_dev(dst_ptr or None, src_ptr or None, nbytes, int(dtype),
@@ -313,5 +353,5 @@ __all__ = [
     "InvalidArgument", "Unimplemented", "matmul_quant_f32", "dequant_to_f32", "register_weights",
     "release_weights", "init", "matmul_quant_f32_dev", "prepare_weights_dev",
     "dequant_to_f32_dev", "xq_bytes", "quantize_x_dev", "matmul_prequant_dev",
-    "matmul_q4k_bf16_dev", "HipBackend", "BackendCapability", "LIB", "LIB_PATH", "SIGNATURES",
+    "matmul_q4k_bf16_dev", "moe_routed", "moe_routed_dev", "HipBackend", "BackendCapability", "LIB", "LIB_PATH", "SIGNATURES",
 ]

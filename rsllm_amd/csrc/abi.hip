@@ -82,7 +82,7 @@ struct DevBuf {
 struct ThreadCtx {
     int device = -1;
     hipStream_t stream = nullptr;
-    DevBuf w_raw, w_dev, x, y, xq, xh;
+    DevBuf w_raw, w_dev, x, y, xq, xh, moe, moe_in, moe_w[3];
 };
 thread_local ThreadCtx t_ctx;
 
@@ -378,6 +378,155 @@ int rsllm_hip_matmul_q4k_bf16_dev(float *out, size_t out_len, const uint8_t *wei
     HIP_TRY(launch_prefill_q4k(weights, weights_len, x_bf16, (uint8_t *)t_ctx.xh.p, out,
                                (int)n_tok, (int)in_dim, (int)out_dim, s),
             "prefill_q4k");
+    return ok();
+}
+
+// Shared validation of the routed-expert entry points, in the order of the
+// reference's own checks for the matmuls involved.
+static int validate_moe(size_t out_len, size_t x_len, size_t gate_up_len, size_t down_len,
+                        size_t ids_len, size_t n_tok, size_t n_embd, size_t n_ff,
+                        size_t n_expert, size_t k, uint32_t dt_gu, uint32_t dt_d,
+                        const void *out, const void *x, const void *gate, const void *up,
+                        const void *down, const void *ids, const void *weights) {
+    if (!matmul_dtype_known(dt_gu) || !matmul_dtype_known(dt_d))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "moe_routed: unsupported dtype for MoE expert matmul");
+    const size_t be_gu = block_elems_of(dt_gu), be_d = block_elems_of(dt_d);
+    if (n_embd % be_gu != 0)
+        return set_err(RSLLM_HIP_ERR_NOT_BLOCK_ALIGNED, "`in_dim` is not a multiple of the block",
+                       "in_dim", n_embd, be_gu);
+    if (n_ff % be_d != 0)
+        return set_err(RSLLM_HIP_ERR_NOT_BLOCK_ALIGNED, "`in_dim` is not a multiple of the block",
+                       "in_dim", n_ff, be_d);
+    size_t need, per;
+    if (!mul_ok(n_ff, row_bytes_of(dt_gu, n_embd), &per) || !mul_ok(per, n_expert, &need) ||
+        gate_up_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "moe_routed: gate/up blobs must be n_expert * n_ff rows of n_embd");
+    if (!mul_ok(n_embd, row_bytes_of(dt_d, n_ff), &per) || !mul_ok(per, n_expert, &need) ||
+        down_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "moe_routed: down blob must be n_expert * n_embd rows of n_ff");
+    if (!mul_ok(n_tok, n_embd, &need) || x_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "moe_routed: x must be n_tok * n_embd");
+    if (out_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "moe_routed: out must be n_tok * n_embd");
+    if (!mul_ok(n_tok, k, &need) || ids_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "moe_routed: ids/weights must be n_tok * k");
+    if (n_embd == 0 || n_ff == 0 || n_expert == 0)
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                       "for_each_row_mut: row_len must be non-zero (n_embd, n_ff, n_expert)");
+    if ((out_len && (!out || !x)) || (gate_up_len && (!gate || !up)) || (down_len && !down) ||
+        (ids_len && (!ids || !weights)))
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "NULL pointer with a nonzero length");
+    if (!matmul_dtype_impl(dt_gu) || !matmul_dtype_impl(dt_d))
+        return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED,
+                       "moe_routed: dtype accepted by the reference is not implemented by the "
+                       "HIP backend");
+    if (ids_len > 4096)
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "moe_routed: n_tok * k must be <= 4096");
+    if (!fits_int(n_tok) || !fits_int(n_embd) || !fits_int(n_ff) || !fits_int(n_expert) ||
+        !fits_int(k) || gate_up_len / n_expert > kMaxWeightBytes ||
+        down_len / n_expert > kMaxWeightBytes)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "moe_routed: dimension out of range");
+    // the device layout of non-Q4_K formats groups 8 blocks: every expert
+    // must start on a group boundary
+    if ((dt_gu != T_Q4_K && ((n_ff * (n_embd / be_gu)) % 8 != 0)) ||
+        (dt_d != T_Q4_K && ((n_embd * (n_ff / be_d)) % 8 != 0)))
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                       "moe_routed: blocks per expert must be a multiple of 8 for this dtype");
+    return RSLLM_HIP_OK;
+}
+
+int rsllm_hip_moe_routed_dev(float *out, size_t out_len, const float *x, size_t x_len,
+                             const uint8_t *gate, const uint8_t *up, size_t gate_up_len,
+                             const uint8_t *down, size_t down_len, const int32_t *ids,
+                             const float *weights, size_t ids_len, size_t n_tok, size_t n_embd,
+                             size_t n_ff, size_t n_expert, size_t k, uint32_t dtype_gate_up,
+                             uint32_t dtype_down, float clamp, rsllm_hip_stream_t stream) {
+    int rc = validate_moe(out_len, x_len, gate_up_len, down_len, ids_len, n_tok, n_embd, n_ff,
+                          n_expert, k, dtype_gate_up, dtype_down, out, x, gate, up, down, ids,
+                          weights);
+    if (rc) return rc;
+    if (n_tok == 0 || k == 0) return ok();
+    if ((rc = ensure_device())) return rc;
+    HIP_TRY(t_ctx.moe.ensure(moe_scratch_bytes(dtype_gate_up, dtype_down, (int)n_tok, (int)k,
+                                               (int)n_expert, (int)n_embd, (int)n_ff)),
+            "hipMalloc");
+    HIP_TRY(launch_moe(dtype_gate_up, dtype_down, gate, up, down, gate_up_len / n_expert,
+                       down_len / n_expert, x, ids, weights, out, (uint8_t *)t_ctx.moe.p,
+                       (int)n_tok, (int)k, (int)n_expert, (int)n_embd, (int)n_ff, clamp,
+                       (hipStream_t)stream),
+            "moe");
+    return ok();
+}
+
+int rsllm_hip_moe_routed(float *out, size_t out_len, const float *x, size_t x_len,
+                         const uint8_t *gate, const uint8_t *up, size_t gate_up_len,
+                         const uint8_t *down, size_t down_len, const int32_t *ids,
+                         const float *weights, size_t ids_len, size_t n_tok, size_t n_embd,
+                         size_t n_ff, size_t n_expert, size_t k, uint32_t dtype_gate_up,
+                         uint32_t dtype_down, float clamp) {
+    int rc = validate_moe(out_len, x_len, gate_up_len, down_len, ids_len, n_tok, n_embd, n_ff,
+                          n_expert, k, dtype_gate_up, dtype_down, out, x, gate, up, down, ids,
+                          weights);
+    if (rc) return rc;
+    for (size_t p = 0; p < ids_len; p++)
+        if (weights[p] != 0.0f && (ids[p] < 0 || (size_t)ids[p] >= n_expert))
+            return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                           "StackedExperts::expert: expert index out of range");
+    if (n_tok == 0 || k == 0) return ok();
+    if ((rc = ensure_device())) return rc;
+    ThreadCtx &c = t_ctx;
+    // expert blobs: registered device copies, else uploaded (and converted to
+    // the device layout) for this call
+    const uint8_t *blob[3] = {gate, up, down};
+    const size_t blen[3] = {gate_up_len, gate_up_len, down_len};
+    const uint32_t bdt[3] = {dtype_gate_up, dtype_gate_up, dtype_down};
+    const size_t bin[3] = {n_embd, n_embd, n_ff};
+    const uint8_t *dev[3];
+    for (int i = 0; i < 3; i++) {
+        dev[i] = find_registered(blob[i], blen[i], bdt[i], bin[i]);
+        if (dev[i]) continue;
+        DevBuf &dst = c.moe_w[i];
+        if (!needs_prepare(bdt[i])) {
+            HIP_TRY(dst.ensure(blen[i]), "hipMalloc");
+            HIP_TRY(hipMemcpyAsync(dst.p, blob[i], blen[i], hipMemcpyHostToDevice, c.stream),
+                    "upload experts");
+        } else {
+            HIP_TRY(c.w_raw.ensure(blen[i]), "hipMalloc");
+            HIP_TRY(dst.ensure(blen[i]), "hipMalloc");
+            HIP_TRY(hipMemcpyAsync(c.w_raw.p, blob[i], blen[i], hipMemcpyHostToDevice, c.stream),
+                    "upload experts");
+            HIP_TRY(launch_prepare(bdt[i], (const uint8_t *)c.w_raw.p, (uint8_t *)dst.p,
+                                   blen[i] / row_bytes_of(bdt[i], bin[i]), bin[i], c.stream),
+                    "prepare experts");
+        }
+        dev[i] = (const uint8_t *)dst.p;
+    }
+    // inputs: x | out | ids | weights, 256-byte aligned pieces
+    const size_t a_x = (x_len * 4 + 255) / 256 * 256, a_o = (out_len * 4 + 255) / 256 * 256;
+    const size_t a_i = (ids_len * 4 + 255) / 256 * 256;
+    HIP_TRY(c.moe_in.ensure(a_x + a_o + 2 * a_i), "hipMalloc");
+    uint8_t *base = (uint8_t *)c.moe_in.p;
+    float *d_x = (float *)base, *d_out = (float *)(base + a_x);
+    int32_t *d_ids = (int32_t *)(base + a_x + a_o);
+    float *d_w = (float *)(base + a_x + a_o + a_i);
+    HIP_TRY(hipMemcpyAsync(d_x, x, x_len * 4, hipMemcpyHostToDevice, c.stream), "upload x");
+    HIP_TRY(hipMemcpyAsync(d_out, out, out_len * 4, hipMemcpyHostToDevice, c.stream), "upload out");
+    HIP_TRY(hipMemcpyAsync(d_ids, ids, ids_len * 4, hipMemcpyHostToDevice, c.stream), "upload ids");
+    HIP_TRY(hipMemcpyAsync(d_w, weights, ids_len * 4, hipMemcpyHostToDevice, c.stream),
+            "upload weights");
+    HIP_TRY(c.moe.ensure(moe_scratch_bytes(dtype_gate_up, dtype_down, (int)n_tok, (int)k,
+                                           (int)n_expert, (int)n_embd, (int)n_ff)),
+            "hipMalloc");
+    HIP_TRY(launch_moe(dtype_gate_up, dtype_down, dev[0], dev[1], dev[2], gate_up_len / n_expert,
+                       down_len / n_expert, d_x, d_ids, d_w, d_out, (uint8_t *)c.moe.p,
+                       (int)n_tok, (int)k, (int)n_expert, (int)n_embd, (int)n_ff, clamp, c.stream),
+            "moe");
+    HIP_TRY(hipMemcpyAsync(out, d_out, out_len * 4, hipMemcpyDeviceToHost, c.stream),
+            "download out");
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
     return ok();
 }
 

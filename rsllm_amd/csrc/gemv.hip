@@ -362,6 +362,150 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv(const uint8_t *__restri
     }
 }
 
+// ---- grouped GEMV (routed experts) ------------------------------------------
+// Slot lists sorted by expert: expert e owns slots [off[e], off[e + 1]).
+// Workgroup (row tile, e, m) computes y_m[s, rows] = W_m[e] x~[row(s)] for
+// every slot s of expert e, in token batches of 4, 2 or 1 (one weight pass
+// per batch); row(s) = tok[s] (gate/up: the slot's token) or s (down: the
+// slot's own activation). W_m[e] starts at w[m] + e * w_stride.
+struct GroupedArgs {
+    const uint8_t *w[2];
+    uint32_t w_stride;
+    const uint8_t *xq;
+    uint32_t xq_bytes;
+    const int *off;
+    const int *tok;  // nullptr: row(s) = s
+    float *y[2];
+    int in_dim, out_dim;
+};
+
+template <class F, int RT, int BT>
+__device__ __forceinline__ void grouped_batch(const GroupedArgs &a, __amdgpu_buffer_rsrc_t rw,
+                                              __amdgpu_buffer_rsrc_t rx, float *y, int s_base,
+                                              int row0, float *red) {
+    const int nw = blockDim.x >> 6;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, k = lane & 7, ks = lane >> 3;
+    const int nunits = F::units(a.in_dim);
+    const int ncols = (nunits + 7) >> 3;
+    const uint32_t col_bytes = (uint32_t)F::kXF * 1024u;
+    const uint32_t tok_bytes = (uint32_t)ncols * col_bytes;
+    uint32_t trow[BT];
+#pragma unroll
+    for (int t = 0; t < BT; t++)
+        trow[t] = (uint32_t)(a.tok ? a.tok[s_base + t] : s_base + t);
+
+    float acc[RT][BT];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int t = 0; t < BT; t++) acc[r][t] = 0.f;
+
+    for (int col = wv; col < ncols; col += nw) {
+        const int unit = col * 8 + ks;
+        typename F::Slice sl[RT];
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+            F::load(sl[r], rw, min(row0 + r, a.out_dim - 1), min(unit, nunits - 1), k, a.in_dim,
+                    a.out_dim);
+        XSlice xs[BT];
+#pragma unroll
+        for (int t = 0; t < BT; t++) {
+            const uint32_t so = trow[t] * tok_bytes + (uint32_t)col * col_bytes;
+            const uint32_t vo = (uint32_t)lane * 16u;
+            xs[t].hlo = bload16(rx, vo, so);
+            xs[t].llo = bload16(rx, vo + 1024u, so);
+            xs[t].meta = bload16(rx, vo + 2048u, so);
+            if (F::kXF == 5) {
+                xs[t].hhi = bload16(rx, vo + 3072u, so);
+                xs[t].lhi = bload16(rx, vo + 4096u, so);
+            }
+        }
+        if (unit < nunits && F::valid(unit, k, a.in_dim)) {
+#pragma unroll
+            for (int t = 0; t < BT; t++)
+#pragma unroll
+                for (int r = 0; r < RT; r++) acc[r][t] += F::dot(sl[r], k, xs[t]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int t = 0; t < BT; t++) acc[r][t] = wave_sum(acc[r][t]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int t = 0; t < BT; t++) red[(r * BT + t) * kMaxWaves + wv] = acc[r][t];
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < RT * BT) {
+        const int r = threadIdx.x / BT, t = threadIdx.x % BT;
+        float v = 0.f;
+        for (int q = 0; q < nw; q++) v += red[threadIdx.x * kMaxWaves + q];
+        if (row0 + r < a.out_dim) y[(size_t)(s_base + t) * a.out_dim + row0 + r] = v;
+    }
+    __syncthreads();  // red is reused by the next batch
+}
+
+template <class F, int RT>
+__global__ __launch_bounds__(64 * kMaxWaves) void k_gemv_grouped(GroupedArgs a) {
+    __shared__ float red[kMaxWaves * RT * 4];
+    const int e = blockIdx.y, m = blockIdx.z;
+    const int s0 = a.off[e], cnt = a.off[e + 1] - s0;
+    if (cnt <= 0) return;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w[m] + (size_t)e * a.w_stride, a.w_stride);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.xq, a.xq_bytes);
+    const int row0 = blockIdx.x * RT;
+    int done = 0;
+    while (cnt - done >= 4) {
+        grouped_batch<F, RT, 4>(a, rw, rx, a.y[m], s0 + done, row0, red);
+        done += 4;
+    }
+    if (cnt - done >= 2) {
+        grouped_batch<F, RT, 2>(a, rw, rx, a.y[m], s0 + done, row0, red);
+        done += 2;
+    }
+    if (cnt - done >= 1) grouped_batch<F, RT, 1>(a, rw, rx, a.y[m], s0 + done, row0, red);
+}
+
+template <class F>
+static hipError_t grouped(const GroupedArgs &a, int n_expert, int n_mat, hipStream_t s) {
+    constexpr int RT = 2;
+    const int ncols = ((a.in_dim + F::kEPU - 1) / F::kEPU + 7) / 8;
+    const int nw = ncols < kMaxWaves ? ncols : kMaxWaves;
+    const dim3 grid((unsigned)((a.out_dim + RT - 1) / RT), (unsigned)n_expert, (unsigned)n_mat);
+    k_gemv_grouped<F, RT><<<grid, 64 * nw, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_grouped(uint32_t dtype, const uint8_t *w0, const uint8_t *w1,
+                               size_t w_stride, const uint8_t *xq, size_t xq_bytes,
+                               const int *off, const int *tok, float *y0, float *y1, int n_expert,
+                               int in_dim, int out_dim, hipStream_t s) {
+    if (n_expert <= 0 || out_dim <= 0 || in_dim <= 0) return hipSuccess;
+    GroupedArgs a;
+    a.w[0] = w0;
+    a.w[1] = w1 ? w1 : w0;
+    a.w_stride = (uint32_t)w_stride;
+    a.xq = xq;
+    a.xq_bytes = (uint32_t)xq_bytes;
+    a.off = off;
+    a.tok = tok;
+    a.y[0] = y0;
+    a.y[1] = y1 ? y1 : y0;
+    a.in_dim = in_dim;
+    a.out_dim = out_dim;
+    const int n_mat = w1 ? 2 : 1;
+    switch (dtype) {
+    case T_Q4_K: return grouped<FQ4K>(a, n_expert, n_mat, s);
+    case T_Q6_K: return grouped<FQ6K>(a, n_expert, n_mat, s);
+    case T_Q8_0: return grouped<FQ8<false>>(a, n_expert, n_mat, s);
+    case T_Q4_0: return grouped<FQ8<true>>(a, n_expert, n_mat, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 __global__ void k_fill_zero(float *y, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) y[i] = 0.f;

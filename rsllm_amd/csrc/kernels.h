@@ -57,6 +57,18 @@ hipError_t launch_gemv_prequant(uint32_t dtype, const uint8_t *w, size_t w_bytes
                                 const uint8_t *xq, float *y, int n_tok, int in_dim, int out_dim,
                                 hipStream_t s);
 
+// Grouped GEMV for routed experts (gemv.hip): slots sorted by expert,
+// expert e owns slots [off[e], off[e+1]) (off on the device, n_expert + 1
+// entries). For each slot s: y_m[s * out_dim + o] = sum_i W_m[e][o, i] *
+// x~[row(s), i], m = 0 (w0 -> y0) and, when w1 is given, m = 1 (w1 -> y1);
+// W_m[e] starts at w_m + e * w_stride (device layout); row(s) = tok[s], or s
+// when tok is null; xq holds the activation limbs of those rows
+// (launch_quantize_x layout, xq_bytes bytes).
+hipError_t launch_gemv_grouped(uint32_t dtype, const uint8_t *w0, const uint8_t *w1,
+                               size_t w_stride, const uint8_t *xq, size_t xq_bytes,
+                               const int *off, const int *tok, float *y0, float *y1, int n_expert,
+                               int in_dim, int out_dim, hipStream_t s);
+
 // prefill.hip: out[t, o] = sum_i deq(W)[o, i] * x[t, i] for a raw GGUF Q4_K
 // weight W [out_dim x in_dim] and bf16 activations x [n_tok x in_dim]
 // (n_tok x out_dim fp32 output, overwritten). `scratch` holds
@@ -66,6 +78,17 @@ size_t prefill_scratch_bytes(int n_tok, int in_dim);
 hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *x_bf16,
                               uint8_t *scratch, float *out, int n_tok, int in_dim, int out_dim,
                               hipStream_t s);
+
+// moe.hip: routed experts (accumulate_moe_outputs). Expert e of gate/up is
+// at gate/up + e * gu_stride, of down at down + e * d_stride (device
+// layout); ids, wts: [n_tok x k] on the device; out [n_tok x n_embd] is
+// accumulated into. `scratch` holds moe_scratch_bytes(...) bytes.
+size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_expert,
+                         int n_embd, int n_ff);
+hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
+                      const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
+                      const int *ids, const float *wts, float *out, uint8_t *scratch, int n_tok,
+                      int k, int n_expert, int n_embd, int n_ff, float clamp, hipStream_t s);
 
 // Largest weight tensor the buffer-addressed kernels accept (offsets are
 // 32-bit).

@@ -1,0 +1,123 @@
+"""Routed-expert MoE on the GPU against the oracle (accumulate_moe_outputs,
+rsllm-models/src/dsv4/moe.rs:648-707 with apply_expert_swiglu :479-502 and
+apply_swiglu_clamp :515-531, every matmul as matmul_quant_f32):
+max|Δ|/max|y| <= 1e-3 over the accumulated output, on small shapes with
+every format pairing, duplicated experts, skipped (w = 0) slots, engaged
+clamps, and on C3 shapes (64 experts of gate/up 2048x7168, down 7168x2048,
+Q4_K, top-8) with the oracle on a subset of tokens."""
+import numpy as np
+import pytest
+
+from conftest import REL_TOL, rel_err
+from rsllm_amd import synth
+from rsllm_amd.ggml import GgmlType as G
+
+pytestmark = pytest.mark.gpu
+
+
+def make_case(n_tok, n_embd, n_ff, n_expert, k, dt_gu, dt_d, seed):
+    gate = synth.weight(dt_gu, n_expert * n_ff, n_embd, seed)
+    up = synth.weight(dt_gu, n_expert * n_ff, n_embd, seed + 1)
+    down = synth.weight(dt_d, n_expert * n_embd, n_ff, seed + 2)
+    x = synth.activations(n_tok, n_embd, seed + 3)
+    ids, w = synth.moe_routing(n_tok, n_expert, k, seed + 4)
+    return gate, up, down, x, ids, w
+
+
+def run_oracle(oracle, base, x, gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k, dt_gu,
+               dt_d, clamp=10.0):
+    out = base.copy()
+    rc = oracle.moe_routed(out, x, n_tok, n_embd, n_ff, gate, up, down, int(dt_gu), int(dt_d),
+                           n_expert, ids, w, k, clamp)
+    assert rc == 0
+    return out
+
+
+@pytest.mark.parametrize("dt_gu,dt_d", [(G.Q4_K, G.Q4_K), (G.Q4_K, G.Q6_K), (G.Q8_0, G.Q8_0),
+                                        (G.Q6_K, G.Q4_0)])
+@pytest.mark.parametrize("n_tok,k", [(1, 2), (3, 3), (8, 4)])
+def test_moe_small(oracle, hip, dt_gu, dt_d, n_tok, k):
+    n_embd, n_ff, n_expert = 512, 256, 6
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, dt_gu, dt_d,
+                                          17 * n_tok + k)
+    if n_tok > 1:
+        w[1, k - 1] = 0.0  # skipped slot
+    base = synth.activations(n_tok, n_embd, 5).reshape(-1)
+    want = run_oracle(oracle, base, x, gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                      dt_gu, dt_d)
+    got = base.copy()
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   dt_gu, dt_d, 10.0)
+    err = rel_err(got - base, want - base)
+    print(f"moe {dt_gu.name}/{dt_d.name} T={n_tok} k={k}: rel err {err:.3e}")
+    assert err <= REL_TOL
+
+
+def test_moe_clamp_engaged_and_all_tokens_on_one_expert(oracle, hip):
+    n_tok, n_embd, n_ff, n_expert, k = 9, 256, 512, 4, 2
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.Q4_K, G.Q4_K, 31)
+    x = (x * 300.0).astype(np.float32)     # gate/up far past the clamp
+    ids[:, 0] = 2                          # 9 tokens on expert 2: batches of 4, 4, 1
+    ids[:, 1] = np.where(ids[:, 1] == 2, 3, ids[:, 1])
+    base = np.zeros(n_tok * n_embd, np.float32)
+    want = run_oracle(oracle, base, x, gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                      G.Q4_K, G.Q4_K)
+    got = base.copy()
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   G.Q4_K, G.Q4_K, 10.0)
+    assert rel_err(got, want) <= REL_TOL
+
+
+def test_moe_zero_weights_and_clamp_off(oracle, hip):
+    n_tok, n_embd, n_ff, n_expert, k = 4, 256, 256, 5, 3
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.Q4_K, G.Q4_K, 41)
+    w[0, :] = 0.0
+    base = synth.activations(n_tok, n_embd, 42).reshape(-1)
+    want = run_oracle(oracle, base, x, gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                      G.Q4_K, G.Q4_K, clamp=0.0)
+    got = base.copy()
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   G.Q4_K, G.Q4_K, 0.0)
+    assert np.array_equal(got[:n_embd], base[:n_embd])  # token 0: every slot skipped
+    assert rel_err(got - base, want - base) <= REL_TOL
+
+
+def test_moe_validation(hip):
+    n_tok, n_embd, n_ff, n_expert, k = 2, 256, 256, 3, 2
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.Q4_K, G.Q4_K, 61)
+    out = np.zeros(n_tok * n_embd, np.float32)
+    bad = ids.copy()
+    bad[1, 0] = n_expert
+    with pytest.raises(hip.InvalidArgument):
+        hip.moe_routed(out, x.reshape(-1), gate, up, down, bad, w, n_tok, n_embd, n_ff, n_expert,
+                       k, G.Q4_K, G.Q4_K, 10.0)
+    with pytest.raises(hip.NotBlockAligned):
+        hip.moe_routed(out, x.reshape(-1), gate, up, down, ids, w, n_tok, 200, n_ff, n_expert, k,
+                       G.Q4_K, G.Q4_K, 10.0)
+    with pytest.raises(hip.ShapeMismatch):
+        hip.moe_routed(out, x.reshape(-1), gate, up, down[:-144], ids, w, n_tok, n_embd, n_ff,
+                       n_expert, k, G.Q4_K, G.Q4_K, 10.0)
+
+
+@pytest.mark.parametrize("n_tok", [1, 8, 32])
+def test_moe_c3_shapes(oracle, hip, n_tok):
+    """C3 shapes with 16 experts (every expert's kernel path is the same as
+    with 64); the oracle runs on up to 6 tokens (tokens are independent)."""
+    n_embd, n_ff, n_expert, k = 7168, 2048, 16, 8
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.Q4_K, G.Q4_K, 300)
+    base = np.zeros(n_tok * n_embd, np.float32)
+    got = base.copy()
+    hip.register_weights(gate, G.Q4_K, n_embd)
+    hip.register_weights(up, G.Q4_K, n_embd)
+    hip.register_weights(down, G.Q4_K, n_ff)
+    try:
+        hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                       G.Q4_K, G.Q4_K, 10.0)
+    finally:
+        hip.release_weights()
+    toks = np.unique(np.linspace(0, n_tok - 1, min(n_tok, 6)).astype(int))
+    want = run_oracle(oracle, np.zeros(len(toks) * n_embd, np.float32), x[toks], gate, up, down,
+                      ids[toks], w[toks], len(toks), n_embd, n_ff, n_expert, k, G.Q4_K, G.Q4_K)
+    err = rel_err(got.reshape(n_tok, n_embd)[toks], want.reshape(len(toks), n_embd))
+    print(f"moe C3 T={n_tok}: rel err {err:.3e}")
+    assert err <= REL_TOL
