@@ -218,22 +218,10 @@ struct FQ8 {
 // Per token: ncols columns x kXF fields x 64 lanes x 16 bytes. Fields:
 // 0 h_lo, 1 l_lo, 2 meta (s_lo, sum_lo, s_hi, sum_hi), 3 h_hi, 4 l_hi
 // (kXF = 3 keeps fields 0..2). Groups past in_dim are written as zeros.
-__device__ __forceinline__ void quant_group(const float *__restrict__ x, int e, int in_dim,
-                                            uint4 &h, uint4 &l, float &s, float &sum) {
-    float v[16];
-    if (e >= 0 && e + 16 <= in_dim) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 f = *reinterpret_cast<const float4 *>(x + e + 4 * i);
-            v[4 * i] = f.x;
-            v[4 * i + 1] = f.y;
-            v[4 * i + 2] = f.z;
-            v[4 * i + 3] = f.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; i++) v[i] = 0.f;
-    }
+// Two int8 limbs of 16 values: v ~= s * (128 h + l), s = amax / 16256;
+// `sum` is the fp32 sum of the values.
+__device__ __forceinline__ void quant_values(const float (&v)[16], uint4 &h, uint4 &l, float &s,
+                                             float &sum) {
     float amax = 0.f;
     sum = 0.f;
 #pragma unroll
@@ -262,6 +250,46 @@ __device__ __forceinline__ void quant_group(const float *__restrict__ x, int e, 
     l = make_uint4(lw[0], lw[1], lw[2], lw[3]);
 }
 
+// Group of x starting at element e (e < 0 or past in_dim: zeros).
+__device__ __forceinline__ void quant_group(const float *__restrict__ x, int e, int in_dim,
+                                            uint4 &h, uint4 &l, float &s, float &sum) {
+    float v[16];
+    if (e >= 0 && e + 16 <= in_dim) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 f = *reinterpret_cast<const float4 *>(x + e + 4 * i);
+            v[4 * i] = f.x;
+            v[4 * i + 1] = f.y;
+            v[4 * i + 2] = f.z;
+            v[4 * i + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = 0.f;
+    }
+    quant_values(v, h, l, s, sum);
+}
+
+// Routed-expert SwiGLU with the pre-activation clamp (apply_swiglu_clamp,
+// rsllm-models/src/dsv4/moe.rs:515-531: only when c > 1e-6, gate from above,
+// up both sides, NaN passes) and silu(g) * u with the stable logistic of
+// scalar::sigmoid (rsllm-backend-cpu/src/ops/scalar.rs:57-71).
+__device__ __forceinline__ float swiglu_clamped(float g, float u, float c) {
+    if (c > 1e-6f) {
+        if (g > c) g = c;
+        if (u > c) u = c;
+        else if (u < -c) u = -c;
+    }
+    float sg;
+    if (g >= 0.0f) {
+        sg = 1.0f / (1.0f + expf(-g));
+    } else {
+        const float e = expf(g);
+        sg = e / (1.0f + e);
+    }
+    return g * sg * u;
+}
+
 // One thread per 16-element group: thread (lane, half) of column `col` writes
 // its limbs to field 0/1 (half 0, "lo") or 3/4 (half 1, "hi") and its
 // (s, sum) pair to the lower or upper 8 bytes of the meta field.
@@ -281,6 +309,43 @@ __global__ __launch_bounds__(256) void k_quant_x(const float *__restrict__ x, ui
     uint4 h, l;
     float s, sum;
     quant_group(x + (size_t)t * in_dim, e, in_dim, h, l, s, sum);
+    uint8_t *base = xq + ((size_t)t * ncols + col) * F::kXF * 1024 + lane * 16;
+    *reinterpret_cast<uint4 *>(base + (half ? 3 : 0) * 1024) = h;
+    *reinterpret_cast<uint4 *>(base + (half ? 4 : 1) * 1024) = l;
+    *reinterpret_cast<float2 *>(base + 2 * 1024 + 8 * half) = make_float2(s, sum);
+}
+
+// k_quant_x on the SwiGLU of two row-major [rows x n] inputs (gate, up
+// pre-activations), for rows < off[n_expert] (the routed slots in use).
+template <class F>
+__global__ __launch_bounds__(256) void k_quant_swiglu(const float *__restrict__ hg,
+                                                      const float *__restrict__ hu, float c,
+                                                      uint8_t *__restrict__ xq, int n, int ncols,
+                                                      int n_rows, const int *__restrict__ off,
+                                                      int n_expert) {
+    constexpr int kHalves = F::kXF == 5 ? 2 : 1;
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    const int per_row = ncols * 64 * kHalves;
+    const int rows = min(n_rows, off[n_expert]);
+    if (gid >= per_row * rows) return;
+    const int t = gid / per_row, rem = gid % per_row;
+    const int col = rem / (64 * kHalves), r2 = rem % (64 * kHalves);
+    const int half = r2 / 64, lane = r2 % 64;
+    const int k = lane & 7, unit = col * 8 + (lane >> 3);
+    const bool ok = unit < F::units(n) && F::valid(unit, k, n);
+    const int e = ok ? (half ? F::elem_hi(unit, k) : F::elem_lo(unit, k)) : -1;
+    float v[16];
+    if (e >= 0 && e + 16 <= n) {
+        const float *g = hg + (size_t)t * n + e, *u = hu + (size_t)t * n + e;
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = swiglu_clamped(g[i], u[i], c);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = 0.f;
+    }
+    uint4 h, l;
+    float s, sum;
+    quant_values(v, h, l, s, sum);
     uint8_t *base = xq + ((size_t)t * ncols + col) * F::kXF * 1024 + lane * 16;
     *reinterpret_cast<uint4 *>(base + (half ? 3 : 0) * 1024) = h;
     *reinterpret_cast<uint4 *>(base + (half ? 4 : 1) * 1024) = l;
@@ -375,6 +440,8 @@ struct GroupedArgs {
     uint32_t xq_bytes;
     const int *off;
     const int *tok;  // nullptr: row(s) = s
+    const int *act;  // active experts (blockIdx.y indexes it), count in *n_act
+    const int *n_act;
     float *y[2];
     int in_dim, out_dim;
 };
@@ -451,7 +518,8 @@ __device__ __forceinline__ void grouped_batch(const GroupedArgs &a, __amdgpu_buf
 template <class F, int RT>
 __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv_grouped(GroupedArgs a) {
     __shared__ float red[kMaxWaves * RT * 4];
-    const int e = blockIdx.y, m = blockIdx.z;
+    if ((int)blockIdx.y >= *a.n_act) return;
+    const int e = a.act[blockIdx.y], m = blockIdx.z;
     const int s0 = a.off[e], cnt = a.off[e + 1] - s0;
     if (cnt <= 0) return;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w[m] + (size_t)e * a.w_stride, a.w_stride);
@@ -470,20 +538,21 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv_grouped(GroupedArgs a) 
 }
 
 template <class F>
-static hipError_t grouped(const GroupedArgs &a, int n_expert, int n_mat, hipStream_t s) {
+static hipError_t grouped(const GroupedArgs &a, int grid_experts, int n_mat, hipStream_t s) {
     constexpr int RT = 2;
     const int ncols = ((a.in_dim + F::kEPU - 1) / F::kEPU + 7) / 8;
     const int nw = ncols < kMaxWaves ? ncols : kMaxWaves;
-    const dim3 grid((unsigned)((a.out_dim + RT - 1) / RT), (unsigned)n_expert, (unsigned)n_mat);
+    const dim3 grid((unsigned)((a.out_dim + RT - 1) / RT), (unsigned)grid_experts, (unsigned)n_mat);
     k_gemv_grouped<F, RT><<<grid, 64 * nw, 0, s>>>(a);
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_grouped(uint32_t dtype, const uint8_t *w0, const uint8_t *w1,
                                size_t w_stride, const uint8_t *xq, size_t xq_bytes,
-                               const int *off, const int *tok, float *y0, float *y1, int n_expert,
-                               int in_dim, int out_dim, hipStream_t s) {
-    if (n_expert <= 0 || out_dim <= 0 || in_dim <= 0) return hipSuccess;
+                               const int *off, const int *tok, const int *act, const int *n_act,
+                               int grid_experts, float *y0, float *y1, int in_dim, int out_dim,
+                               hipStream_t s) {
+    if (grid_experts <= 0 || out_dim <= 0 || in_dim <= 0) return hipSuccess;
     GroupedArgs a;
     a.w[0] = w0;
     a.w[1] = w1 ? w1 : w0;
@@ -492,16 +561,18 @@ hipError_t launch_gemv_grouped(uint32_t dtype, const uint8_t *w0, const uint8_t 
     a.xq_bytes = (uint32_t)xq_bytes;
     a.off = off;
     a.tok = tok;
+    a.act = act;
+    a.n_act = n_act;
     a.y[0] = y0;
     a.y[1] = y1 ? y1 : y0;
     a.in_dim = in_dim;
     a.out_dim = out_dim;
     const int n_mat = w1 ? 2 : 1;
     switch (dtype) {
-    case T_Q4_K: return grouped<FQ4K>(a, n_expert, n_mat, s);
-    case T_Q6_K: return grouped<FQ6K>(a, n_expert, n_mat, s);
-    case T_Q8_0: return grouped<FQ8<false>>(a, n_expert, n_mat, s);
-    case T_Q4_0: return grouped<FQ8<true>>(a, n_expert, n_mat, s);
+    case T_Q4_K: return grouped<FQ4K>(a, grid_experts, n_mat, s);
+    case T_Q6_K: return grouped<FQ6K>(a, grid_experts, n_mat, s);
+    case T_Q8_0: return grouped<FQ8<false>>(a, grid_experts, n_mat, s);
+    case T_Q4_0: return grouped<FQ8<true>>(a, grid_experts, n_mat, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -571,6 +642,29 @@ hipError_t launch_quantize_x(uint32_t dtype, const float *x, uint8_t *xq, int n_
     case T_Q6_K: return quantize<FQ6K>(x, xq, n_tok, in_dim, s);
     case T_Q8_0: return quantize<FQ8<false>>(x, xq, n_tok, in_dim, s);
     case T_Q4_0: return quantize<FQ8<true>>(x, xq, n_tok, in_dim, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <class F>
+static hipError_t quantize_swiglu(const float *hg, const float *hu, float c, uint8_t *xq, int n_rows,
+                                  int n, const int *off, int n_expert, hipStream_t s) {
+    const int ncols = ((n + F::kEPU - 1) / F::kEPU + 7) / 8;
+    const int threads = n_rows * ncols * 64 * (F::kXF == 5 ? 2 : 1);
+    k_quant_swiglu<F><<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(hg, hu, c, xq, n, ncols,
+                                                                       n_rows, off, n_expert);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_swiglu(uint32_t dtype, const float *hg, const float *hu, float clamp,
+                                  uint8_t *xq, int n_rows, int n, const int *off, int n_expert,
+                                  hipStream_t s) {
+    if (n_rows <= 0 || n <= 0) return hipSuccess;
+    switch (dtype) {
+    case T_Q4_K: return quantize_swiglu<FQ4K>(hg, hu, clamp, xq, n_rows, n, off, n_expert, s);
+    case T_Q6_K: return quantize_swiglu<FQ6K>(hg, hu, clamp, xq, n_rows, n, off, n_expert, s);
+    case T_Q8_0: return quantize_swiglu<FQ8<false>>(hg, hu, clamp, xq, n_rows, n, off, n_expert, s);
+    case T_Q4_0: return quantize_swiglu<FQ8<true>>(hg, hu, clamp, xq, n_rows, n, off, n_expert, s);
     default: return hipErrorInvalidValue;
     }
 }

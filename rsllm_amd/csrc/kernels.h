@@ -63,11 +63,18 @@ hipError_t launch_gemv_prequant(uint32_t dtype, const uint8_t *w, size_t w_bytes
 // x~[row(s), i], m = 0 (w0 -> y0) and, when w1 is given, m = 1 (w1 -> y1);
 // W_m[e] starts at w_m + e * w_stride (device layout); row(s) = tok[s], or s
 // when tok is null; xq holds the activation limbs of those rows
-// (launch_quantize_x layout, xq_bytes bytes).
+// (launch_quantize_x layout, xq_bytes bytes). Workgroup row y of the grid
+// (grid_experts rows) serves expert act[y] when y < *n_act.
 hipError_t launch_gemv_grouped(uint32_t dtype, const uint8_t *w0, const uint8_t *w1,
                                size_t w_stride, const uint8_t *xq, size_t xq_bytes,
-                               const int *off, const int *tok, float *y0, float *y1, int n_expert,
-                               int in_dim, int out_dim, hipStream_t s);
+                               const int *off, const int *tok, const int *act, const int *n_act,
+                               int grid_experts, float *y0, float *y1, int in_dim, int out_dim,
+                               hipStream_t s);
+// launch_quantize_x applied to silu(min(g, c)) * clamp(u, -c, c) of the
+// first min(n_rows, off[n_expert]) rows of hg, hu ([n_rows x n]).
+hipError_t launch_quantize_swiglu(uint32_t dtype, const float *hg, const float *hu, float clamp,
+                                  uint8_t *xq, int n_rows, int n, const int *off, int n_expert,
+                                  hipStream_t s);
 
 // prefill.hip: out[t, o] = sum_i deq(W)[o, i] * x[t, i] for a raw GGUF Q4_K
 // weight W [out_dim x in_dim] and bf16 activations x [n_tok x in_dim]

@@ -10,12 +10,12 @@
 // gate/up and down matrices are streamed once per batch of up to 4 of its
 // tokens (grouped GEMV, gemv.hip):
 //   1. k_moe_route: slots sorted by expert (ties in (t, i) order), per-expert
-//      offsets, slot -> token, (t, i) -> slot; slots with w == 0 are skipped
-//      (moe.rs:681-683).
+//      offsets, slot -> token, (t, i) -> slot, the list of active experts;
+//      slots with w == 0 are skipped (moe.rs:681-683).
 //   2. activation limbs of x for the gate/up format;
 //   3. grouped GEMV, gate and up in one launch -> hg, hu [slot x n_ff];
-//   4. k_moe_swiglu: clamp (only when c > 1e-6; NaN passes) and silu(g) * u;
-//   5. activation limbs of the per-slot SwiGLU output for the down format;
+//   4+5. clamp (only when c > 1e-6; NaN passes), silu(g) * u and the
+//      activation limbs for the down format in one pass;
 //   6. grouped GEMV, down -> yd [slot x n_embd];
 //   7. k_moe_accumulate: out[t, j] += w[t, i] * yd[slot(t, i), j] in i order,
 //      as the reference's `out_t[j] += we * expert_out[j]` (no contraction).
@@ -23,72 +23,53 @@
 
 namespace rsllm_hip {
 
-// One workgroup. Deterministic: a slot's rank inside its expert is the
-// number of earlier valid slots with the same expert.
+// One workgroup. ids and weights are cached in LDS; a slot's rank inside its
+// expert is the number of earlier valid slots with the same expert
+// (deterministic order). Also lists the experts with at least one slot, in
+// ascending order (act, count in *n_act), for the grouped GEMV grids.
 __global__ __launch_bounds__(256) void k_moe_route(const int *__restrict__ ids,
                                                    const float *__restrict__ wts, int n_pairs,
                                                    int k, int n_expert, int *__restrict__ off,
                                                    int *__restrict__ slot_tok,
-                                                   int *__restrict__ slot_of) {
-    extern __shared__ int cnt[];  // n_expert + 1
+                                                   int *__restrict__ slot_of,
+                                                   int *__restrict__ act, int *__restrict__ n_act) {
+    extern __shared__ int lds[];
+    int *cnt = lds;                     // n_expert + 1
+    int *eid = lds + n_expert + 1;      // n_pairs: expert id, or -1 for a skipped slot
     const int tid = threadIdx.x;
     for (int e = tid; e <= n_expert; e += 256) cnt[e] = 0;
     __syncthreads();
     for (int p = tid; p < n_pairs; p += 256) {
         const int e = ids[p];
-        if (wts[p] != 0.0f && e >= 0 && e < n_expert) atomicAdd(&cnt[e], 1);
+        const bool valid = wts[p] != 0.0f && e >= 0 && e < n_expert;
+        eid[p] = valid ? e : -1;
+        if (valid) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
     if (tid == 0) {
-        int run = 0;
+        int run = 0, na = 0;
         for (int e = 0; e < n_expert; e++) {
             const int c = cnt[e];
             cnt[e] = run;
             off[e] = run;
+            if (c) act[na++] = e;
             run += c;
         }
-        cnt[n_expert] = run;
         off[n_expert] = run;
+        *n_act = na;
     }
     __syncthreads();
     for (int p = tid; p < n_pairs; p += 256) {
-        const int e = ids[p];
-        const bool valid = wts[p] != 0.0f && e >= 0 && e < n_expert;
+        const int e = eid[p];
         int slot = -1;
-        if (valid) {
+        if (e >= 0) {
             int rank = 0;
-            for (int q = 0; q < p; q++)
-                rank += (ids[q] == e && wts[q] != 0.0f) ? 1 : 0;
+            for (int q = 0; q < p; q++) rank += eid[q] == e ? 1 : 0;
             slot = cnt[e] + rank;
             slot_tok[slot] = p / k;
         }
         slot_of[p] = slot;
     }
-}
-
-// Numerically stable logistic, as scalar::sigmoid (rsllm-backend-cpu/src/ops/scalar.rs:57-66).
-__device__ __forceinline__ float moe_sigmoid(float x) {
-    if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
-    const float e = expf(x);
-    return e / (1.0f + e);
-}
-
-// act[s, j] for s < n_slots (= off[n_expert]); rows past it are left alone.
-__global__ __launch_bounds__(256) void k_moe_swiglu(const float *__restrict__ hg,
-                                                    const float *__restrict__ hu,
-                                                    float *__restrict__ act,
-                                                    const int *__restrict__ off, int n_expert,
-                                                    int n_ff, float c) {
-    const int n_slots = off[n_expert];
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (size_t)n_slots * n_ff) return;
-    float g = hg[i], u = hu[i];
-    if (c > 1e-6f) {
-        if (g > c) g = c;
-        if (u > c) u = c;
-        else if (u < -c) u = -c;
-    }
-    act[i] = g * moe_sigmoid(g) * u;
 }
 
 __global__ __launch_bounds__(256) void k_moe_accumulate(float *__restrict__ out,
@@ -117,13 +98,13 @@ size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_
     size_t b = 0;
     auto add = [&](size_t n) { b += (n + 255) / 256 * 256; };
     add((size_t)(n_expert + 1) * 4);                      // off
+    add((size_t)(n_expert + 1) * 4);                      // act, n_act
     add(P * 4);                                           // slot_tok
     add(P * 4);                                           // slot_of
     add(gemv_scratch_bytes(dt_gu, n_tok, n_embd));        // x limbs
     add(P * n_ff * 4);                                    // hg
     add(P * n_ff * 4);                                    // hu
-    add(P * n_ff * 4);                                    // act
-    add(gemv_scratch_bytes(dt_d, (int)P, n_ff));          // act limbs
+    add(gemv_scratch_bytes(dt_d, (int)P, n_ff));          // SwiGLU limbs
     add(P * n_embd * 4);                                  // yd
     return b;
 }
@@ -141,31 +122,33 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
         return r;
     };
     int *off = reinterpret_cast<int *>(take((size_t)(n_expert + 1) * 4));
+    int *act = reinterpret_cast<int *>(take((size_t)(n_expert + 1) * 4));
+    int *n_act = act + n_expert;
     int *slot_tok = reinterpret_cast<int *>(take(P * 4));
     int *slot_of = reinterpret_cast<int *>(take(P * 4));
     const size_t xq1_bytes = gemv_scratch_bytes(dt_gu, n_tok, n_embd);
     uint8_t *xq1 = take(xq1_bytes);
     float *hg = reinterpret_cast<float *>(take(P * n_ff * 4));
     float *hu = reinterpret_cast<float *>(take(P * n_ff * 4));
-    float *act = reinterpret_cast<float *>(take(P * n_ff * 4));
     const size_t xq2_bytes = gemv_scratch_bytes(dt_d, (int)P, n_ff);
     uint8_t *xq2 = take(xq2_bytes);
     float *yd = reinterpret_cast<float *>(take(P * n_embd * 4));
+    // at most min(n_expert, n_tok * k) experts are active
+    const int grid_experts = (int)(P < (size_t)n_expert ? P : (size_t)n_expert);
 
-    k_moe_route<<<1, 256, (size_t)(n_expert + 1) * 4, s>>>(ids, wts, (int)P, k, n_expert, off,
-                                                           slot_tok, slot_of);
+    k_moe_route<<<1, 256, (size_t)(n_expert + 1 + P) * 4, s>>>(ids, wts, (int)P, k, n_expert, off,
+                                                               slot_tok, slot_of, act, n_act);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if ((e = launch_quantize_x(dt_gu, x, xq1, n_tok, n_embd, s)) != hipSuccess) return e;
-    if ((e = launch_gemv_grouped(dt_gu, gate, up, gu_stride, xq1, xq1_bytes, off, slot_tok, hg, hu,
-                                 n_expert, n_embd, n_ff, s)) != hipSuccess)
+    if ((e = launch_gemv_grouped(dt_gu, gate, up, gu_stride, xq1, xq1_bytes, off, slot_tok, act,
+                                 n_act, grid_experts, hg, hu, n_embd, n_ff, s)) != hipSuccess)
         return e;
-    k_moe_swiglu<<<(unsigned)((P * n_ff + 255) / 256), 256, 0, s>>>(hg, hu, act, off, n_expert,
-                                                                    n_ff, clamp);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    if ((e = launch_quantize_x(dt_d, act, xq2, (int)P, n_ff, s)) != hipSuccess) return e;
-    if ((e = launch_gemv_grouped(dt_d, down, nullptr, d_stride, xq2, xq2_bytes, off, nullptr, yd,
-                                 nullptr, n_expert, n_ff, n_embd, s)) != hipSuccess)
+    if ((e = launch_quantize_swiglu(dt_d, hg, hu, clamp, xq2, (int)P, n_ff, off, n_expert, s)) !=
+        hipSuccess)
+        return e;
+    if ((e = launch_gemv_grouped(dt_d, down, nullptr, d_stride, xq2, xq2_bytes, off, nullptr, act,
+                                 n_act, grid_experts, yd, nullptr, n_ff, n_embd, s)) != hipSuccess)
         return e;
     k_moe_accumulate<<<(unsigned)(((size_t)n_tok * n_embd + 255) / 256), 256, 0, s>>>(
         out, yd, wts, slot_of, n_tok, k, n_embd);
