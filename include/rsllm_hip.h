@@ -205,6 +205,51 @@ int rsllm_hip_moe_routed(float *out, size_t out_len, const float *x, size_t x_le
                          size_t n_ff, size_t n_expert, size_t k, uint32_t dtype_gate_up,
                          uint32_t dtype_down, float clamp);
 
+/* ---- Q8_0 int8-activation path ---------------------------------------------
+ * quantize_q8_0_batch (backend-cpu/src/ops/q8_0.rs:95-129, per token
+ * quantize_q8_0_activation :42-88): x [n_tok x in_dim] -> xq [n_tok x blocks
+ * x 32] int8 and scale [n_tok x blocks], blocks = ceil(in_dim / 32); per
+ * block d = amax / 127, q = clamp(round_half_even(x / d), -128, 127) (x * (1
+ * / d) exactly as the reference), a partial last block zero-padded.
+ * Bit-exact with the reference. Validation order :101-118: x_len, xq_len,
+ * scale_len (ShapeMismatch); in_dim == 0 is INVALID_ARGUMENT (the
+ * reference's par_chunks_mut(0) panics). A non-finite input returns
+ * RSLLM_HIP_ERR_NON_FINITE_INPUT (:67-69); xq and scale are then
+ * unspecified. */
+int rsllm_hip_quantize_q8_0_batch(const float *x, size_t x_len, int8_t *xq, size_t xq_len,
+                                  float *scale, size_t scale_len, size_t n_tok, size_t in_dim);
+/* Device-pointer form, enqueued on `stream`. Non-finite inputs cannot be
+ * reported synchronously: when `status` (a device int32) is non-NULL it is
+ * set to 0, or to 1 if any input was non-finite, once the work completes. */
+int rsllm_hip_quantize_q8_0_batch_dev(const float *x, size_t x_len, int8_t *xq, size_t xq_len,
+                                      float *scale, size_t scale_len, size_t n_tok,
+                                      size_t in_dim, int32_t *status, rsllm_hip_stream_t stream);
+
+/* matmul_q8_0_batch (backend-cpu/src/ops/q8_0.rs:217-263): out[t*out_dim + o]
+ * = sum over blocks b, in order, of (wscale[o,b] * xscale[t,b]) * dot_i32(
+ * wq[o,b], xq[t,b]) (dot_q8_0_row_scalar :163-193; a non-finite weight scale
+ * counts as 0, :143-146; only the first in_dim - 32 b lanes of a partial
+ * last block take part). `weights` are raw GGUF Q8_0 rows (out_dim * blocks
+ * * 34 bytes, in_dim need not be a multiple of 32). Bit-exact with the
+ * reference's scalar tier. Validation order :229-252: weights_len, xq_len,
+ * xscale_len, out_len (ShapeMismatch); out_dim == 0 is INVALID_ARGUMENT
+ * (parallel.rs:44). `tier` is accepted and ignored (the scalar result is
+ * what every call returns). Weights are uploaded (and regrouped into the
+ * device layout) for the call unless the same (pointer, length) was
+ * registered as Q8_0 with this in_dim. */
+int rsllm_hip_matmul_q8_0_batch(float *out, size_t out_len, const uint8_t *weights,
+                                size_t weights_len, const int8_t *xq, size_t xq_len,
+                                const float *xscale, size_t xscale_len, size_t n_tok,
+                                size_t in_dim, size_t out_dim, uint32_t tier);
+/* Device-pointer form, enqueued on `stream`: `weights` in the device layout
+ * (rsllm_hip_prepare_weights_dev of the GGUF rows with in_dim rounded up to
+ * a multiple of 32 — the same bytes matmul_quant_f32_dev takes for Q8_0),
+ * weights and xq 16-byte aligned. */
+int rsllm_hip_matmul_q8_0_batch_dev(float *out, size_t out_len, const uint8_t *weights,
+                                    size_t weights_len, const int8_t *xq, size_t xq_len,
+                                    const float *xscale, size_t xscale_len, size_t n_tok,
+                                    size_t in_dim, size_t out_dim, rsllm_hip_stream_t stream);
+
 /* ---- dequantisation ------------------------------------------------------ */
 
 /* dequant_to_f32 (rsllm-gguf/src/dequant/mod.rs:69-85): decode `src` (GGUF

@@ -138,6 +138,10 @@ SIGNATURES = {
                                   _S, _U32, _U32, ctypes.c_float, _P], _I),
     "rsllm_hip_moe_routed": ([_P, _S, _P, _S, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _S, _S,
                               _U32, _U32, ctypes.c_float], _I),
+    "rsllm_hip_quantize_q8_0_batch": ([_P, _S, _P, _S, _P, _S, _S, _S], _I),
+    "rsllm_hip_quantize_q8_0_batch_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _P, _P], _I),
+    "rsllm_hip_matmul_q8_0_batch": ([_P, _S, _P, _S, _P, _S, _P, _S, _S, _S, _S, _U32], _I),
+    "rsllm_hip_matmul_q8_0_batch_dev": ([_P, _S, _P, _S, _P, _S, _P, _S, _S, _S, _S, _P], _I),
 }
 
 
@@ -305,6 +309,49 @@ def moe_routed_dev(out_ptr: int, out_len: int, x_ptr: int, x_len: int, gate_ptr:
                                         stream or None))
 
 
+def quantize_q8_0_batch(x: np.ndarray, xq: np.ndarray, scale: np.ndarray, n_tok: int,
+                        in_dim: int) -> None:
+    """quantize_q8_0_batch (backend-cpu/src/ops/q8_0.rs:95-129): fills ``xq``
+    (int8, n_tok * ceil(in_dim/32) * 32) and ``scale`` (float32)."""
+    px, nx = _host_f32(x, "x")
+    if not (isinstance(xq, np.ndarray) and xq.dtype == np.int8):
+        raise TypeError("xq must be an int8 numpy array")
+    pq, nq = _host_ptr(xq)
+    ps, ns = _host_f32(scale, "scale")
+    _check(LIB.rsllm_hip_quantize_q8_0_batch(px, nx, pq, nq, ps, ns, n_tok, in_dim))
+
+
+def matmul_q8_0_batch(out: np.ndarray, weights, xq: np.ndarray, xscale: np.ndarray, n_tok: int,
+                      in_dim: int, out_dim: int, tier: SimdTier = SimdTier.Scalar) -> None:
+    """matmul_q8_0_batch (backend-cpu/src/ops/q8_0.rs:217-263): raw GGUF Q8_0
+    weight rows times pre-quantised activations; ``out`` is overwritten."""
+    po, no = _host_f32(out, "out")
+    pw, nw = _host_ptr(weights)
+    if not (isinstance(xq, np.ndarray) and xq.dtype == np.int8):
+        raise TypeError("xq must be an int8 numpy array")
+    pq, nq = _host_ptr(xq)
+    ps, ns = _host_f32(xscale, "xscale")
+    _check(LIB.rsllm_hip_matmul_q8_0_batch(po, no, pw, nw, pq, nq, ps, ns, n_tok, in_dim, out_dim,
+                                           int(tier)))
+
+
+def quantize_q8_0_batch_dev(x_ptr: int, x_len: int, xq_ptr: int, xq_len: int, scale_ptr: int,
+                            scale_len: int, n_tok: int, in_dim: int, status_ptr: int = 0,
+                            stream: int = 0) -> None:
+    _check(LIB.rsllm_hip_quantize_q8_0_batch_dev(x_ptr or None, x_len, xq_ptr or None, xq_len,
+                                                 scale_ptr or None, scale_len, n_tok, in_dim,
+                                                 status_ptr or None, stream or None))
+
+
+def matmul_q8_0_batch_dev(out_ptr: int, out_len: int, w_ptr: int, w_len: int, xq_ptr: int,
+                          xq_len: int, xscale_ptr: int, xscale_len: int, n_tok: int, in_dim: int,
+                          out_dim: int, stream: int = 0) -> None:
+    _check(LIB.rsllm_hip_matmul_q8_0_batch_dev(out_ptr or None, out_len, w_ptr or None, w_len,
+                                               xq_ptr or None, xq_len, xscale_ptr or None,
+                                               xscale_len, n_tok, in_dim, out_dim,
+                                               stream or None))
+
+
 def prepare_weights_dev(dst_ptr: int, src_ptr: int, nbytes: int, dtype, in_dim: int,
                         stream: int = 0) -> None:
     _check(LIB.rsllm_hip_prepare_weights_dev(dst_ptr or None, src_ptr or None, nbytes, int(dtype),
@@ -353,5 +400,7 @@ __all__ = [
     "InvalidArgument", "Unimplemented", "matmul_quant_f32", "dequant_to_f32", "register_weights",
     "release_weights", "init", "matmul_quant_f32_dev", "prepare_weights_dev",
     "dequant_to_f32_dev", "xq_bytes", "quantize_x_dev", "matmul_prequant_dev",
-    "matmul_q4k_bf16_dev", "moe_routed", "moe_routed_dev", "HipBackend", "BackendCapability", "LIB", "LIB_PATH", "SIGNATURES",
+    "matmul_q4k_bf16_dev", "moe_routed", "moe_routed_dev", "quantize_q8_0_batch",
+    "matmul_q8_0_batch", "quantize_q8_0_batch_dev", "matmul_q8_0_batch_dev", "HipBackend",
+    "BackendCapability", "LIB", "LIB_PATH", "SIGNATURES",
 ]

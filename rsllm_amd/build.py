@@ -24,7 +24,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librsllm_hip.so")
 
-SOURCES = ["abi.hip", "dequant.hip", "gemv.hip", "prefill.hip", "moe.hip"]
+SOURCES = ["abi.hip", "dequant.hip", "gemv.hip", "prefill.hip", "moe.hip", "q8_int8.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -530,6 +530,171 @@ int rsllm_hip_moe_routed(float *out, size_t out_len, const float *x, size_t x_le
     return ok();
 }
 
+// quantize_q8_0_batch's checks (q8_0.rs:101-118), then the panic of
+// par_chunks_mut(0) for in_dim == 0.
+static int validate_q8_quantize(const void *x, size_t x_len, const void *xq, size_t xq_len,
+                                const void *scale, size_t scale_len, size_t n_tok,
+                                size_t in_dim) {
+    const size_t blocks = (in_dim + 31) / 32;
+    size_t need, nb;
+    if (!mul_ok(n_tok, in_dim, &need) || x_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "quantize_q8_0_batch: x must be n_tok*in_dim");
+    if (!mul_ok(n_tok, blocks, &nb) || !mul_ok(nb, 32, &need) || xq_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "quantize_q8_0_batch: xq must be n_tok*blocks*32");
+    if (scale_len != nb)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "quantize_q8_0_batch: scale must be n_tok*blocks");
+    if (in_dim == 0)
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "par_chunks_mut: chunk size must be non-zero");
+    if ((x_len && !x) || (xq_len && (!xq || !scale)))
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "NULL pointer with a nonzero length");
+    if (!fits_int(xq_len))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "quantize_q8_0_batch: xq exceeds 2^31-1");
+    return RSLLM_HIP_OK;
+}
+
+// matmul_q8_0_batch's checks (q8_0.rs:229-252), then for_each_row_mut's
+// row_len assertion (parallel.rs:44).
+static int validate_q8_matmul(const void *out, size_t out_len, const void *w, size_t w_len,
+                              const void *xq, size_t xq_len, const void *xscale,
+                              size_t xscale_len, size_t n_tok, size_t in_dim, size_t out_dim) {
+    const size_t blocks = (in_dim + 31) / 32;
+    size_t need, nb;
+    if (!mul_ok(out_dim, blocks, &nb) || !mul_ok(nb, 34, &need) || w_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_q8_0_batch: weights must be out_dim*blocks*34");
+    if (!mul_ok(n_tok, blocks, &nb) || !mul_ok(nb, 32, &need) || xq_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "matmul_q8_0_batch: xq must be n_tok*blocks*32");
+    if (xscale_len != nb)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_q8_0_batch: xscale must be n_tok*blocks");
+    if (!mul_ok(n_tok, out_dim, &need) || out_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "matmul_q8_0_batch: out must be n_tok*out_dim");
+    if (out_dim == 0)
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                       "for_each_row_mut: row_len must be non-zero (out_dim == 0)");
+    if ((w_len && !w) || (xq_len && (!xq || !xscale)) || (out_len && !out))
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "NULL pointer with a nonzero length");
+    if (!fits_int(n_tok) || !fits_int(in_dim) || !fits_int(out_dim) || w_len > kMaxWeightBytes)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "matmul_q8_0_batch: dimension out of range");
+    return RSLLM_HIP_OK;
+}
+
+int rsllm_hip_quantize_q8_0_batch_dev(const float *x, size_t x_len, int8_t *xq, size_t xq_len,
+                                      float *scale, size_t scale_len, size_t n_tok,
+                                      size_t in_dim, int32_t *status, rsllm_hip_stream_t stream) {
+    int rc = validate_q8_quantize(x, x_len, xq, xq_len, scale, scale_len, n_tok, in_dim);
+    if (rc) return rc;
+    if ((((uintptr_t)x | (uintptr_t)scale | (uintptr_t)status) & 3) || ((uintptr_t)xq & 15))
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                       "quantize_q8_0_batch: xq must be 16-byte aligned, x/scale/status 4-byte");
+    hipStream_t s = (hipStream_t)stream;
+    if (status) HIP_TRY(launch_fill_zero(reinterpret_cast<float *>(status), 1, s), "fill_zero");
+    if (n_tok == 0) return ok();
+    HIP_TRY(launch_q8_quantize(x, xq, scale, (int)n_tok, (int)in_dim, status, s), "q8_quantize");
+    return ok();
+}
+
+int rsllm_hip_quantize_q8_0_batch(const float *x, size_t x_len, int8_t *xq, size_t xq_len,
+                                  float *scale, size_t scale_len, size_t n_tok, size_t in_dim) {
+    int rc = validate_q8_quantize(x, x_len, xq, xq_len, scale, scale_len, n_tok, in_dim);
+    if (rc) return rc;
+    if (n_tok == 0) return ok();
+    if ((rc = ensure_device())) return rc;
+    ThreadCtx &c = t_ctx;
+    const size_t a_x = (x_len * 4 + 255) / 256 * 256, a_q = (xq_len + 255) / 256 * 256;
+    const size_t a_s = (scale_len * 4 + 255) / 256 * 256;
+    HIP_TRY(c.x.ensure(a_x + a_q + a_s + 256), "hipMalloc");
+    uint8_t *base = (uint8_t *)c.x.p;
+    float *d_x = (float *)base;
+    int8_t *d_q = (int8_t *)(base + a_x);
+    float *d_s = (float *)(base + a_x + a_q);
+    int32_t *d_st = (int32_t *)(base + a_x + a_q + a_s);
+    HIP_TRY(hipMemcpyAsync(d_x, x, x_len * 4, hipMemcpyHostToDevice, c.stream), "upload x");
+    HIP_TRY(launch_fill_zero(reinterpret_cast<float *>(d_st), 1, c.stream), "fill_zero");
+    HIP_TRY(launch_q8_quantize(d_x, d_q, d_s, (int)n_tok, (int)in_dim, d_st, c.stream),
+            "q8_quantize");
+    int32_t st = 0;
+    HIP_TRY(hipMemcpyAsync(xq, d_q, xq_len, hipMemcpyDeviceToHost, c.stream), "download xq");
+    HIP_TRY(hipMemcpyAsync(scale, d_s, scale_len * 4, hipMemcpyDeviceToHost, c.stream),
+            "download scale");
+    HIP_TRY(hipMemcpyAsync(&st, d_st, 4, hipMemcpyDeviceToHost, c.stream), "download status");
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    if (st)
+        return set_err(RSLLM_HIP_ERR_NON_FINITE_INPUT, "quantize_q8_0: activation");
+    return ok();
+}
+
+int rsllm_hip_matmul_q8_0_batch_dev(float *out, size_t out_len, const uint8_t *weights,
+                                    size_t weights_len, const int8_t *xq, size_t xq_len,
+                                    const float *xscale, size_t xscale_len, size_t n_tok,
+                                    size_t in_dim, size_t out_dim, rsllm_hip_stream_t stream) {
+    int rc = validate_q8_matmul(out, out_len, weights, weights_len, xq, xq_len, xscale,
+                                xscale_len, n_tok, in_dim, out_dim);
+    if (rc) return rc;
+    if ((((uintptr_t)weights | (uintptr_t)xq) & 15) || (((uintptr_t)xscale | (uintptr_t)out) & 3))
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                       "matmul_q8_0_batch: weights and xq must be 16-byte aligned, xscale and out "
+                       "4-byte");
+    hipStream_t s = (hipStream_t)stream;
+    if (n_tok == 0) return ok();
+    if (in_dim == 0) {
+        HIP_TRY(launch_fill_zero(out, out_len, s), "fill_zero");
+        return ok();
+    }
+    HIP_TRY(launch_q8_int8_matmul(weights, weights_len, xq, xscale, out, (int)n_tok, (int)in_dim,
+                                  (int)out_dim, s),
+            "q8_matmul");
+    return ok();
+}
+
+int rsllm_hip_matmul_q8_0_batch(float *out, size_t out_len, const uint8_t *weights,
+                                size_t weights_len, const int8_t *xq, size_t xq_len,
+                                const float *xscale, size_t xscale_len, size_t n_tok,
+                                size_t in_dim, size_t out_dim, uint32_t tier) {
+    (void)tier;  // every tier returns the scalar tier's result (q8_0.rs:271-296)
+    int rc = validate_q8_matmul(out, out_len, weights, weights_len, xq, xq_len, xscale,
+                                xscale_len, n_tok, in_dim, out_dim);
+    if (rc) return rc;
+    if (n_tok == 0) return ok();
+    if (in_dim == 0) {  // zero blocks: every dot is 0.0
+        std::memset(out, 0, out_len * sizeof(float));
+        return ok();
+    }
+    if ((rc = ensure_device())) return rc;
+    ThreadCtx &c = t_ctx;
+    // device layout: a registered copy (Q8_0 with this in_dim), else the rows
+    // uploaded and regrouped for this call
+    const uint8_t *dw = find_registered(weights, weights_len, T_Q8_0, in_dim);
+    if (!dw) {
+        HIP_TRY(c.w_raw.ensure(weights_len), "hipMalloc");
+        HIP_TRY(c.w_dev.ensure(weights_len), "hipMalloc");
+        HIP_TRY(hipMemcpyAsync(c.w_raw.p, weights, weights_len, hipMemcpyHostToDevice, c.stream),
+                "upload weights");
+        HIP_TRY(launch_prepare(T_Q8_0, (const uint8_t *)c.w_raw.p, (uint8_t *)c.w_dev.p, out_dim,
+                               (in_dim + 31) / 32 * 32, c.stream),
+                "prepare weights");
+        dw = (const uint8_t *)c.w_dev.p;
+    }
+    const size_t a_q = (xq_len + 255) / 256 * 256;
+    HIP_TRY(c.x.ensure(a_q + xscale_len * 4), "hipMalloc");
+    int8_t *d_q = (int8_t *)c.x.p;
+    float *d_s = (float *)((uint8_t *)c.x.p + a_q);
+    HIP_TRY(hipMemcpyAsync(d_q, xq, xq_len, hipMemcpyHostToDevice, c.stream), "upload xq");
+    HIP_TRY(hipMemcpyAsync(d_s, xscale, xscale_len * 4, hipMemcpyHostToDevice, c.stream),
+            "upload xscale");
+    HIP_TRY(c.y.ensure(out_len * sizeof(float)), "hipMalloc");
+    HIP_TRY(launch_q8_int8_matmul(dw, weights_len, d_q, d_s,
+                                  (float *)c.y.p, (int)n_tok, (int)in_dim, (int)out_dim,
+                                  c.stream),
+            "q8_matmul");
+    HIP_TRY(hipMemcpyAsync(out, c.y.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
+            "download out");
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    return ok();
+}
+
 int rsllm_hip_register_weights(const uint8_t *weights, size_t weights_len, uint32_t dtype,
                                size_t in_dim) {
     if (!matmul_dtype_impl(dtype))

@@ -31,19 +31,6 @@
 
 namespace rsllm_hip {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
-    return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
-}
-__device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
-}
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
-    // word 3 = 0x00020000: the raw-buffer configuration of the gfx9 family
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
-}
 
 // 128 * sum(q . h) + sum(q . l) over one 16-element group, exact in int32
 // (|q| <= 128, |h| <= 127, |l| <= 64).

@@ -97,6 +97,17 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
                       const int *ids, const float *wts, float *out, uint8_t *scratch, int n_tok,
                       int k, int n_expert, int n_embd, int n_ff, float clamp, hipStream_t s);
 
+// q8_int8.hip: the Q8_0 int8-activation path. launch_q8_quantize writes
+// xq [n_tok x blocks x 32] int8 and scale [n_tok x blocks] (blocks =
+// ceil(in_dim / 32)) and ORs 1 into *status (if non-null) when a token has
+// a non-finite input. launch_q8_int8_matmul: out [n_tok x out_dim] from raw
+// GGUF Q8_0 rows (w_bytes bytes) and those activations.
+hipError_t launch_q8_quantize(const float *x, int8_t *xq, float *scale, int n_tok, int in_dim,
+                              int *status, hipStream_t s);
+hipError_t launch_q8_int8_matmul(const uint8_t *w, size_t w_bytes, const int8_t *xq,
+                                 const float *xscale, float *out, int n_tok, int in_dim,
+                                 int out_dim, hipStream_t s);
+
 // Largest weight tensor the buffer-addressed kernels accept (offsets are
 // 32-bit).
 constexpr size_t kMaxWeightBytes = 0xFFFFFF00u;

@@ -41,7 +41,6 @@ namespace rsllm_hip {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
-typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kPfTok = 128;                      // tokens per workgroup
 constexpr int kPfRowsWave = 64;                  // weight rows per wavefront

@@ -195,3 +195,240 @@ def q4_0_matmul_case():
     x = np.cos(np.arange(n_tok * in_dim, dtype=np.float32) * np.float32(0.07)).astype(np.float32)
     wq = np.concatenate([pack_q4_0_row(w[o * in_dim:(o + 1) * in_dim]) for o in range(out_dim)])
     return wq, x, n_tok, in_dim, out_dim
+
+
+# --- Q8_0 int8-activation path (backend-cpu/src/ops/q8_0.rs) -----------------
+# An implementation is a pair of callables:
+#   quantize(x_flat, n_tok, in_dim) -> (status, int8[n_tok*blocks*32], f32[n_tok*blocks])
+#   matmul(w, xq, xscale, n_tok, in_dim, out_dim) -> (status, f32[n_tok*out_dim])
+# KATs are (name, run(quantize, matmul)) and raise AssertionError on mismatch.
+NON_FINITE_INPUT, SHAPE_MISMATCH = 3, 1
+
+
+def pack_q8_0_row_with(quantize, w) -> np.ndarray:
+    """The reference test helper pack_q8_0_row (q8_0.rs:302-320): quantize the
+    row as an activation, then store f16(scale) and the 32 quants per block."""
+    w = np.asarray(w, np.float32)
+    rc, q, s = quantize(w, 1, w.size)
+    assert rc == 0
+    out = []
+    for b in range(s.size):
+        out.append(np.frombuffer(f16_bytes(float(s[b])), np.uint8))
+        out.append(q[b * 32:(b + 1) * 32].view(np.uint8))
+    return np.concatenate(out)
+
+
+def _ref_round_trip(quantize, matmul):
+    # quantize_round_trip_within_tolerance (q8_0.rs:323-343)
+    x = ((np.arange(64, dtype=np.float32) - np.float32(32.0)) * np.float32(0.1)).astype(np.float32)
+    rc, q, s = quantize(x, 1, 64)
+    assert rc == 0
+    rec = q.astype(np.float32).reshape(2, 32) * s[:, None]
+    assert np.all(np.abs(rec - x.reshape(2, 32)) < 0.05)
+
+
+def _ref_zero(quantize, matmul):
+    # quantize_zero_input_is_zero (:345-353)
+    rc, q, s = quantize(np.zeros(32, np.float32), 1, 32)
+    assert rc == 0 and s[0] == 0.0 and np.all(q == 0)
+
+
+def _ref_pad(quantize, matmul):
+    # quantize_pads_partial_block_to_zero (:355-365): 20 ones; the tail is 0
+    # and (closed form) the ones quantize to 127 with scale 1/127
+    rc, q, s = quantize(np.ones(20, np.float32), 1, 20)
+    assert rc == 0 and np.all(q[20:] == 0) and np.all(q[:20] == 127)
+    assert s[0] == np.float32(1.0) / np.float32(127.0)
+
+
+def _ref_dot_full_precision(quantize, matmul):
+    # dot_q8_0_row_matches_full_precision (:367-389)
+    i = np.arange(96, dtype=np.float32)
+    w = np.sin(i * np.float32(0.07) - np.float32(3.0)).astype(np.float32)
+    x = np.cos(i * np.float32(0.11) + np.float32(1.0)).astype(np.float32)
+    row = pack_q8_0_row_with(quantize, w)
+    rc, xq, xs = quantize(x, 1, 96)
+    assert rc == 0
+    rc, got = matmul(row, xq, xs, 1, 96, 1)
+    assert rc == 0
+    want = float(np.dot(w.astype(np.float64), x.astype(np.float64)))
+    assert abs(got[0] - want) < 0.01 * max(abs(want), 1.0)
+
+
+def _ref_matmul_naive(quantize, matmul):
+    # matmul_q8_0_batch_matches_naive (:391-452): in 64, out 4, 2 tokens
+    in_dim, out_dim, n_tok = 64, 4, 2
+    wf = np.sin(np.arange(out_dim * in_dim, dtype=np.float32) * np.float32(0.013)
+                + np.float32(0.1)).astype(np.float32)
+    x = np.cos(np.arange(n_tok * in_dim, dtype=np.float32) * np.float32(0.027)
+               - np.float32(0.2)).astype(np.float32)
+    w = np.concatenate([pack_q8_0_row_with(quantize, wf[o * in_dim:(o + 1) * in_dim])
+                        for o in range(out_dim)])
+    rc, xq, xs = quantize(x, n_tok, in_dim)
+    assert rc == 0
+    rc, out = matmul(w, xq, xs, n_tok, in_dim, out_dim)
+    assert rc == 0
+    want = x.reshape(n_tok, in_dim).astype(np.float64) @ wf.reshape(out_dim, in_dim).T.astype(np.float64)
+    assert np.all(np.abs(out.reshape(n_tok, out_dim) - want) < 0.01 * np.maximum(np.abs(want), 1.0))
+
+
+def _ref_matmul_shape(quantize, matmul):
+    # matmul_rejects_shape_mismatch (:454-459): empty weights, in 32, out 4
+    rc, _ = matmul(np.zeros(0, np.uint8), np.zeros(0, np.int8), np.zeros(0, np.float32), 1, 32, 4)
+    assert rc == SHAPE_MISMATCH
+
+
+def _ref_nan_inf(quantize, matmul):
+    # quantize_rejects_nan_input / _inf_input (:461-477)
+    for x in ([1.0, 2.0, np.nan, 3.0], [1.0, np.inf, 2.0]):
+        x = np.array(x, np.float32)
+        rc, _, _ = quantize(x, 1, x.size)
+        assert rc == NON_FINITE_INPUT
+
+
+def _ref_nonfinite_scale(quantize, matmul):
+    # dot_q8_0_row_ignores_nonfinite_scale (:529-545): scale bits 0x7E00, quants
+    # 127, xq 1, xscale 1 -> exactly 0.0; also for +-inf scales (:143-146)
+    for bits in (0x7E00, 0x7C00, 0xFC00):
+        row = np.concatenate([np.array([bits & 0xFF, bits >> 8], np.uint8),
+                              np.full(32, 127, np.uint8)])
+        rc, out = matmul(row, np.ones(32, np.int8), np.ones(1, np.float32), 1, 32, 1)
+        assert rc == 0 and out[0] == 0.0 and not np.signbit(out[0])
+
+
+def _closed_ties_even(quantize, matmul):
+    """Closed form: amax 127 gives d = 1 and id = 1 exactly, so q = x rounded
+    half to even (round_ties_even, :79): 2.5 -> 2, 3.5 -> 4, -2.5 -> -2,
+    0.5 -> 0, -1.5 -> -2; a half-away-from-zero rounding fails it."""
+    x = np.zeros(32, np.float32)
+    x[:8] = [127.0, 2.5, 3.5, -2.5, 0.5, -0.5, 1.5, -1.5]
+    rc, q, s = quantize(x, 1, 32)
+    assert rc == 0 and s[0] == 1.0
+    assert q[:8].tolist() == [127, 2, 4, -2, 0, 0, 2, -2]
+
+
+def _closed_overflowing_inverse(quantize, matmul):
+    """amax = 1e-40 gives a subnormal d whose inverse overflows to inf: then
+    x * id is +-inf (saturating `as i32`, clamped: 127 / -128) and 0 * inf is
+    NaN (`as i32` -> 0). Pins the saturating cast, the clamp bounds and
+    subnormal arithmetic (no flush to zero)."""
+    x = np.zeros(32, np.float32)
+    x[0], x[1], x[2] = np.float32(-1e-40), np.float32(1e-41), np.float32(-1e-45)
+    rc, q, s = quantize(x, 1, 32)
+    assert rc == 0
+    assert s[0] == np.float32(1e-40) / np.float32(127.0) and s[0] != 0.0
+    assert q[:4].tolist() == [-128, 127, -128, 0]
+
+
+def _closed_exact_sum(quantize, matmul):
+    """Power-of-two scales and small dots make every product and partial sum
+    exact, so the result is the integer dot computed in Python: pins block
+    order, the f16 scale byte order, signed quants, per-token scales and the
+    partial last block (weight tail bytes are garbage, xq tail nonzero; only
+    the first in_dim - 32 b lanes count, :183-187)."""
+    for wide_w in (True, False):
+        _exact_sum_case(matmul, wide_w)
+
+
+def _exact_sum_case(matmul, wide_w):
+    # one operand spans the full int8 range, the other |q| <= 4, and scale
+    # exponents span 6 octaves: every partial sum needs at most 22 bits
+    rng = np.random.default_rng(7 + wide_w)
+    n_tok, in_dim, out_dim = 3, 100, 5
+    blocks = 4
+    wide, narrow = (-128, 128), (-4, 5)
+    wq = rng.integers(*(wide if wide_w else narrow), size=(out_dim, blocks, 32)).astype(np.int8)
+    xq = rng.integers(*(narrow if wide_w else wide), size=(n_tok, blocks, 32)).astype(np.int8)
+    wexp = rng.integers(-2, 2, size=(out_dim, blocks))
+    xexp = rng.integers(-2, 2, size=(n_tok, blocks))
+    w = np.concatenate([pack_q8_0(2.0 ** int(wexp[o, b]), wq[o, b])
+                        for o in range(out_dim) for b in range(blocks)])
+    xs = (2.0 ** xexp).astype(np.float32).reshape(-1)
+    rc, out = matmul(w, xq.reshape(-1), xs, n_tok, in_dim, out_dim)
+    assert rc == 0
+    want = np.zeros((n_tok, out_dim))
+    for t in range(n_tok):
+        for o in range(out_dim):
+            acc = 0
+            for b in range(blocks):
+                bn = min(32, in_dim - 32 * b)
+                dot = int(np.dot(wq[o, b, :bn].astype(np.int64), xq[t, b, :bn].astype(np.int64)))
+                acc += dot * 2.0 ** (int(wexp[o, b]) + int(xexp[t, b]))
+            want[t, o] = acc
+    assert np.array_equal(out.reshape(n_tok, out_dim).astype(np.float64), want)
+
+
+def _closed_sequential_order(quantize, matmul):
+    """Block products 2^24, 1, 1, -2^24 summed left to right in f32 give
+    (2^24 + 1 -> 2^24, ties to even) ... -> 0.0; exact summation gives 2 and
+    right-to-left 2. Pins `acc += ...` in block order from 0.0 (:175-190)."""
+    qs = np.zeros((4, 32), np.int8)
+    qs[0, :4] = 64
+    qs[1, 0] = 1
+    qs[2, 0] = 1
+    qs[3, :4] = -64
+    w = np.concatenate([pack_q8_0(1.0, qs[b]) for b in range(4)])
+    xq = np.zeros((4, 32), np.int8)
+    xq[0, :4] = 64
+    xq[1, 0] = 1
+    xq[2, 0] = 1
+    xq[3, :4] = 64
+    xs = np.array([1024.0, 1.0, 1.0, 1024.0], np.float32)
+    rc, out = matmul(w, xq.reshape(-1), xs, 1, 128, 1)
+    assert rc == 0 and out[0] == 0.0
+
+
+def _closed_scale_association(quantize, matmul):
+    """The product is (wscale * xscale) * dot, each step rounded to f32
+    (Rust's left-associative `wscale * xscale[b] * dot as f32`). With
+    wscale = 1 + 2^-10 (f16-exact), xscale = 1 + 2^-14 + 2^-23 and
+    dot = 32385 the two associations round differently."""
+    ws = np.float32(np.float16(1.0 + 2.0 ** -10))
+    xs = np.float32(1.0 + 2.0 ** -14 + 2.0 ** -23)
+    qs = np.zeros(32, np.int8)
+    xq = np.zeros(32, np.int8)
+    # dot = 127 * 127 * 2 + 127 = 32385
+    qs[:3] = [127, 127, 1]
+    xq[:3] = [127, 127, 127]
+    dot = np.float32(32385.0)
+    left = np.float32(np.float32(ws * xs) * dot)
+    right = np.float32(ws * np.float32(xs * dot))
+    assert left != right, "choose constants whose associations differ"
+    w = pack_q8_0(float(ws), qs)
+    rc, out = matmul(w, xq, np.array([xs], np.float32), 1, 32, 1)
+    assert rc == 0 and out[0] == left
+
+
+def _closed_no_contraction(quantize, matmul):
+    """`acc += p` rounds p first (Rust never contracts to an FMA): block 0
+    contributes -p exactly (scale 1, xscale -p, dot 1) and block 1 the
+    inexact p = (ws * xs) * dot, so the sum is exactly 0.0; a fused
+    multiply-add would leave p's rounding error."""
+    ws = np.float32(np.float16(1.0 + 2.0 ** -10))
+    xs = np.float32(1.0 + 2.0 ** -14 + 2.0 ** -23)
+    p = np.float32(np.float32(ws * xs) * np.float32(32385.0))
+    from fractions import Fraction
+    assert Fraction(float(np.float32(ws * xs))) * 32385 != Fraction(float(p))
+    q0 = np.zeros(32, np.int8)
+    q0[0] = 1
+    q1 = np.zeros(32, np.int8)
+    q1[:3] = [127, 127, 1]
+    w = np.concatenate([pack_q8_0(1.0, q0), pack_q8_0(float(ws), q1)])
+    xq = np.zeros(64, np.int8)
+    xq[0] = 1
+    xq[32:35] = [127, 127, 127]
+    rc, out = matmul(w, xq, np.array([-p, xs], np.float32), 1, 64, 1)
+    assert rc == 0 and out[0] == 0.0
+
+
+def q8_kats():
+    return [("ref_round_trip", _ref_round_trip), ("ref_zero", _ref_zero), ("ref_pad", _ref_pad),
+            ("ref_dot_full_precision", _ref_dot_full_precision),
+            ("ref_matmul_naive", _ref_matmul_naive), ("ref_matmul_shape", _ref_matmul_shape),
+            ("ref_nan_inf", _ref_nan_inf), ("ref_nonfinite_scale", _ref_nonfinite_scale),
+            ("closed_ties_even", _closed_ties_even),
+            ("closed_overflowing_inverse", _closed_overflowing_inverse),
+            ("closed_exact_sum", _closed_exact_sum),
+            ("closed_sequential_order", _closed_sequential_order),
+            ("closed_scale_association", _closed_scale_association),
+            ("closed_no_contraction", _closed_no_contraction)]
