@@ -12,10 +12,10 @@ the 256 MB Infinity Cache; steps rotate through the copies.
 value        = whole-job algorithmic bytes / wall time of the K timed steps
                (bytes = packed weight bytes + x + y, per launch)
 roofline     = the same bytes per launch / mean duration of the dominant kernel
-               (the GEMV on pre-quantised x), measured with one HIP-event pair
-               around a run of K back-to-back launches on the launch stream,
-               vs 8 TB/s; the timed steps run the full drop-in path (x pre-pass
-               + GEMV) and give `value`
+               (at batch 1 the whole drop-in call is one kernel, k_gemv1, which
+               quantises x in LDS), measured with one HIP-event pair around a
+               run of K back-to-back launches of one shape on the launch
+               stream, vs 8 TB/s
 cpu_baseline = the CPU oracle (a C restatement of the reference CPU path,
                one thread per token as the reference's rayon split gives at
                batch 1) timed on a bounded sample of the same GEMVs.
@@ -204,25 +204,15 @@ def main():
     ms_per_step = gpu_ms / args.steps
     value = bytes_per_step * args.steps / (gpu_ms * 1e-3) / 1e9
 
-    # ---- dominant kernel duration: the GEMV alone on pre-quantised x, timed
-    # as the event-bracketed mean over a run of back-to-back launches (one
-    # event pair per run, so event overhead is amortised over the run).
-    xqs = []
-    for si, (out_dim, in_dim, _, _) in enumerate(mats):
-        nb = B.xq_bytes(dtype, n_tok, in_dim)
-        xq = torch.empty(nb, dtype=torch.uint8, device=dev)
-        B.quantize_x_dev(dtype, xs[si].data_ptr(), xs[si].numel(), n_tok, in_dim, xq.data_ptr(), nb,
-                         sptr)
-        xqs.append(xq)
-    torch.cuda.synchronize()
+    # ---- dominant kernel duration: at batch 1 each drop-in call is ONE
+    # kernel (the fused GEMV, x quantised in LDS), timed as the
+    # event-bracketed mean over a run of back-to-back launches of one shape
+    # (one event pair per run, so event overhead is amortised over the run).
     per_kernel = []
     kern_us = []
     for si, (out_dim, in_dim, _, _) in enumerate(mats):
         def gemv_only(c):
-            w = reps[c][si]
-            B.matmul_prequant_dev(ys[si].data_ptr(), ys[si].numel(), w.data_ptr(), w.numel(),
-                                  xqs[si].data_ptr(), xqs[si].numel(), n_tok, in_dim, out_dim,
-                                  dtype, sptr)
+            launch(si, c)
         for i in range(copies):
             gemv_only(i)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -312,7 +302,7 @@ def main():
             "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "rsllm_hip::k_gemv<FQ6K, 4, 1>",
+            "kernel": "rsllm_hip::k_gemv1<FQ6K, RT, NWV> (x quantised in LDS, one launch)",
             "kernel_shape": per_kernel[dom]["shape"],
             "kernel_us_mean": round(kern_us[dom], 3),
         },

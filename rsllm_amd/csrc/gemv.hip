@@ -218,6 +218,10 @@ __device__ __forceinline__ void quant_values(const float (&v)[16], uint4 &h, uin
     }
     s = amax * (1.0f / 16256.0f);
     const float inv = amax > 0.f ? 16256.0f / amax : 0.f;
+    // t = v / s in [-16256, 16256]; h = rint(t / 128) in [-127, 127] and
+    // l = rint(t - 128 h) in [-64, 64] need no clamping. Both are formed
+    // biased by 128 (exact integers in [1, 255]) so v_cvt_pk_u8_f32 packs
+    // them, and the bias is removed per dword with one xor.
     uint32_t hw[4], lw[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -225,22 +229,22 @@ __device__ __forceinline__ void quant_values(const float (&v)[16], uint4 &h, uin
 #pragma unroll
         for (int b = 0; b < 4; b++) {
             const float t = v[4 * u + b] * inv;
-            const float hq = fminf(fmaxf(rintf(t * (1.0f / 128.0f)), -127.f), 127.f);
-            const float lq = fminf(fmaxf(rintf(t - 128.f * hq), -64.f), 64.f);
-            hh |= ((uint32_t)(int32_t)hq & 0xFFu) << (8 * b);
-            ll |= ((uint32_t)(int32_t)lq & 0xFFu) << (8 * b);
+            const float hb = rintf(fmaf(t, 1.0f / 128.0f, 128.0f));    // h + 128
+            const float lb = rintf(fmaf(-128.0f, hb, t + 16512.0f));    // l + 128
+            hh = __builtin_amdgcn_cvt_pk_u8_f32(hb, b, hh);
+            ll = __builtin_amdgcn_cvt_pk_u8_f32(lb, b, ll);
         }
-        hw[u] = hh;
-        lw[u] = ll;
+        hw[u] = hh ^ 0x80808080u;
+        lw[u] = ll ^ 0x80808080u;
     }
     h = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     l = make_uint4(lw[0], lw[1], lw[2], lw[3]);
 }
 
-// Group of x starting at element e (e < 0 or past in_dim: zeros).
-__device__ __forceinline__ void quant_group(const float *__restrict__ x, int e, int in_dim,
-                                            uint4 &h, uint4 &l, float &s, float &sum) {
-    float v[16];
+// The 16 values of the group starting at element e (e < 0 or past in_dim:
+// zeros).
+__device__ __forceinline__ void load_group(const float *__restrict__ x, int e, int in_dim,
+                                           float (&v)[16]) {
     if (e >= 0 && e + 16 <= in_dim) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -254,6 +258,13 @@ __device__ __forceinline__ void quant_group(const float *__restrict__ x, int e, 
 #pragma unroll
         for (int i = 0; i < 16; i++) v[i] = 0.f;
     }
+}
+
+// Group of x starting at element e (e < 0 or past in_dim: zeros).
+__device__ __forceinline__ void quant_group(const float *__restrict__ x, int e, int in_dim,
+                                            uint4 &h, uint4 &l, float &s, float &sum) {
+    float v[16];
+    load_group(x, e, in_dim, v);
     quant_values(v, h, l, s, sum);
 }
 
@@ -343,6 +354,9 @@ __global__ __launch_bounds__(256) void k_quant_swiglu(const float *__restrict__ 
 // blockDim = 64 * NW (NW = min(columns, kMaxWaves)); grid = (ceil(out_dim /
 // RT), ceil(n_tok / BT)). Wavefront w handles columns w, w + NW, ...
 constexpr int kMaxWaves = 8;
+// LDS of the fused batch-1 GEMV (the quantised x of one token): up to 160 KB,
+// in_dim <= 32768 for the 256-element formats.
+constexpr size_t kGemv1MaxLds = 160 * 1024;
 
 template <class F, int RT, int BT>
 __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv(const uint8_t *__restrict__ w, uint32_t w_bytes,
@@ -412,6 +426,124 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv(const uint8_t *__restri
         for (int q = 0; q < nw; q++) v += red[threadIdx.x * kMaxWaves + q];
         if (row0 + r < out_dim && t0 + t < n_tok) y[(size_t)(t0 + t) * out_dim + row0 + r] = v;
     }
+}
+
+// ---- batch-1 GEMV with the activation pre-pass fused -------------------------
+// Workgroup = NWV wavefronts of RT rows each. Prologue: the workgroup
+// quantises x into LDS in the pre-pass layout (thread i takes groups i,
+// i + 64 NWV, ...); its first x loads are issued before the first column's
+// weight loads, so both latencies overlap. Then every wavefront streams all
+// columns of its RT rows, the next column's weights in flight while the
+// current one is computed, and lane 0 writes each row's total. No other
+// launch is needed, and x is read once per workgroup instead of once per
+// wavefront and column.
+template <class F, int RT, int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_gemv1(const uint8_t *__restrict__ w,
+                                                   uint32_t w_bytes,
+                                                   const float *__restrict__ x,
+                                                   float *__restrict__ y, int in_dim,
+                                                   int out_dim) {
+    extern __shared__ uint4 xl[];
+    constexpr int kHalves = F::kXF == 5 ? 2 : 1;
+    constexpr int kThreads = 64 * NWV;
+    const int lane = threadIdx.x & 63, k = lane & 7, ks = lane >> 3;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nunits = F::units(in_dim), ncols = (nunits + 7) >> 3;
+    const int n_groups = ncols * 64 * kHalves;
+    const int row0 = (blockIdx.x * NWV + wv) * RT;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
+
+    auto group_elem = [&](int g) {
+        const int col = g / (64 * kHalves), r2 = g % (64 * kHalves);
+        const int half = r2 >> 6, ln = r2 & 63;
+        const int kk = ln & 7, unit = col * 8 + (ln >> 3);
+        const bool ok = unit < nunits && F::valid(unit, kk, in_dim);
+        return ok ? (half ? F::elem_hi(unit, kk) : F::elem_lo(unit, kk)) : -1;
+    };
+    auto quant_store = [&](int g, const float (&v)[16]) {
+        uint4 h, l;
+        float sc, sum;
+        quant_values(v, h, l, sc, sum);
+        const int col = g / (64 * kHalves), r2 = g % (64 * kHalves);
+        const int half = r2 >> 6, ln = r2 & 63;
+        uint4 *b = xl + col * F::kXF * 64 + ln;
+        b[(half ? 3 : 0) * 64] = h;
+        b[(half ? 4 : 1) * 64] = l;
+        reinterpret_cast<float2 *>(b + 2 * 64)[half] = make_float2(sc, sum);
+    };
+    typename F::Slice a[RT], b[RT];
+    auto load_col = [&](typename F::Slice (&sl)[RT], int col) {
+        const int unit = min(col * 8 + ks, nunits - 1);
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+            F::load(sl[r], rw, min(row0 + r, out_dim - 1), unit, k, in_dim, out_dim);
+    };
+
+    const int g0 = threadIdx.x;
+    float v0[16];
+    load_group(x, g0 < n_groups ? group_elem(g0) : -1, in_dim, v0);
+    load_col(a, 0);
+    if (g0 < n_groups) quant_store(g0, v0);
+    for (int g = g0 + kThreads; g < n_groups; g += kThreads) {
+        float v[16];
+        load_group(x, group_elem(g), in_dim, v);
+        quant_store(g, v);
+    }
+    __syncthreads();
+
+    float acc[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) acc[r] = 0.f;
+    auto body = [&](typename F::Slice (&cur)[RT], typename F::Slice (&nxt)[RT], int col) {
+        if (col + 1 < ncols) load_col(nxt, col + 1);
+        XSlice xs;
+        const uint4 *bx = xl + col * F::kXF * 64 + lane;
+        xs.hlo = bx[0];
+        xs.llo = bx[64];
+        xs.meta = bx[128];
+        if (F::kXF == 5) {
+            xs.hhi = bx[192];
+            xs.lhi = bx[256];
+        }
+        const int unit = col * 8 + ks;
+        if (unit < nunits && F::valid(unit, k, in_dim)) {
+#pragma unroll
+            for (int r = 0; r < RT; r++) acc[r] += F::dot(cur[r], k, xs);
+        }
+    };
+    for (int col = 0; col < ncols; col += 2) {
+        body(a, b, col);
+        if (col + 1 < ncols) body(b, a, col + 1);
+    }
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const float v = wave_sum(acc[r]);
+        if (lane == 0 && row0 + r < out_dim) y[row0 + r] = v;
+    }
+}
+
+template <class F>
+static size_t gemv1_lds_bytes(int in_dim) {
+    const int ncols = ((in_dim + F::kEPU - 1) / F::kEPU + 7) >> 3;
+    return (size_t)ncols * F::kXF * 1024;
+}
+
+template <class F, int RT, int NWV>
+static hipError_t gemv1_go(const uint8_t *w, size_t w_bytes, const float *x, float *y, int in_dim,
+                           int out_dim, hipStream_t s) {
+    const size_t lds = gemv1_lds_bytes<F>(in_dim);
+    static bool attr_set = false;  // per instantiation; idempotent if raced
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemv1<F, RT, NWV>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)kGemv1MaxLds);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const int rows_wg = RT * NWV;
+    k_gemv1<F, RT, NWV><<<(unsigned)((out_dim + rows_wg - 1) / rows_wg), 64 * NWV, lds, s>>>(
+        w, (uint32_t)w_bytes, x, y, in_dim, out_dim);
+    return hipGetLastError();
 }
 
 // ---- grouped GEMV (routed experts) ------------------------------------------
@@ -669,10 +801,48 @@ hipError_t launch_gemv_prequant(uint32_t dtype, const uint8_t *w, size_t w_bytes
     }
 }
 
+// Batch 1: the fused kernel. RT = 2 rows per wavefront for tall matrices
+// (out_dim >= 3 in_dim), else 1; 16 wavefronts per workgroup unless that
+// leaves fewer than 256 workgroups (then 8, then 4). Chosen from sweeps of
+// the C1-C3 shapes on MI355X.
+template <class F>
+static hipError_t gemv1(const uint8_t *w, size_t w_bytes, const float *x, float *y, int in_dim,
+                        int out_dim, hipStream_t s) {
+    const int rt = out_dim >= 3 * in_dim ? 2 : 1;
+    const int nwv = out_dim / (rt * 16) >= 256 ? 16 : (out_dim / (rt * 8) >= 256 ? 8 : 4);
+    if (rt == 2) {
+        if (nwv == 16) return gemv1_go<F, 2, 16>(w, w_bytes, x, y, in_dim, out_dim, s);
+        if (nwv == 8) return gemv1_go<F, 2, 8>(w, w_bytes, x, y, in_dim, out_dim, s);
+        return gemv1_go<F, 2, 4>(w, w_bytes, x, y, in_dim, out_dim, s);
+    }
+    if (nwv == 16) return gemv1_go<F, 1, 16>(w, w_bytes, x, y, in_dim, out_dim, s);
+    if (nwv == 8) return gemv1_go<F, 1, 8>(w, w_bytes, x, y, in_dim, out_dim, s);
+    return gemv1_go<F, 1, 4>(w, w_bytes, x, y, in_dim, out_dim, s);
+}
+
+static bool gemv1_fits(uint32_t dtype, int in_dim) {
+    switch (dtype) {
+    case T_Q4_K: return gemv1_lds_bytes<FQ4K>(in_dim) <= kGemv1MaxLds;
+    case T_Q6_K: return gemv1_lds_bytes<FQ6K>(in_dim) <= kGemv1MaxLds;
+    case T_Q8_0: return gemv1_lds_bytes<FQ8<false>>(in_dim) <= kGemv1MaxLds;
+    case T_Q4_0: return gemv1_lds_bytes<FQ8<true>>(in_dim) <= kGemv1MaxLds;
+    default: return false;
+    }
+}
+
 hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
                        uint8_t *xq_scratch, float *y, int n_tok, int in_dim, int out_dim,
                        hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
+    if (n_tok == 1 && gemv1_fits(dtype, in_dim)) {
+        switch (dtype) {
+        case T_Q4_K: return gemv1<FQ4K>(w, w_bytes, x, y, in_dim, out_dim, s);
+        case T_Q6_K: return gemv1<FQ6K>(w, w_bytes, x, y, in_dim, out_dim, s);
+        case T_Q8_0: return gemv1<FQ8<false>>(w, w_bytes, x, y, in_dim, out_dim, s);
+        case T_Q4_0: return gemv1<FQ8<true>>(w, w_bytes, x, y, in_dim, out_dim, s);
+        default: return hipErrorInvalidValue;
+        }
+    }
     hipError_t e = launch_quantize_x(dtype, x, xq_scratch, n_tok, in_dim, s);
     if (e != hipSuccess) return e;
     return launch_gemv_prequant(dtype, w, w_bytes, xq_scratch, y, n_tok, in_dim, out_dim, s);

@@ -43,8 +43,9 @@ hipError_t launch_prepare(uint32_t dtype, const uint8_t *src, uint8_t *dst, size
                           size_t in_dim, hipStream_t s);
 
 // gemv.hip: y[t, o] = sum_i W[o, i] x[t, i] for t < n_tok, W (w_bytes bytes)
-// in device layout. Runs the activation pre-pass into `xq_scratch`, which
-// must hold gemv_scratch_bytes(dtype, n_tok, in_dim) bytes.
+// in device layout. Batch 1 is one launch that quantises x in LDS; larger
+// batches run the activation pre-pass into `xq_scratch`, which must hold
+// gemv_scratch_bytes(dtype, n_tok, in_dim) bytes, then the GEMV.
 hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
                        uint8_t *xq_scratch, float *y, int n_tok, int in_dim, int out_dim,
                        hipStream_t s);
@@ -100,8 +101,8 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
 // q8_int8.hip: the Q8_0 int8-activation path. launch_q8_quantize writes
 // xq [n_tok x blocks x 32] int8 and scale [n_tok x blocks] (blocks =
 // ceil(in_dim / 32)) and ORs 1 into *status (if non-null) when a token has
-// a non-finite input. launch_q8_int8_matmul: out [n_tok x out_dim] from raw
-// GGUF Q8_0 rows (w_bytes bytes) and those activations.
+// a non-finite input. launch_q8_int8_matmul: out [n_tok x out_dim] from Q8_0
+// weights in the device layout (w_bytes bytes) and those activations.
 hipError_t launch_q8_quantize(const float *x, int8_t *xq, float *scale, int n_tok, int in_dim,
                               int *status, hipStream_t s);
 hipError_t launch_q8_int8_matmul(const uint8_t *w, size_t w_bytes, const int8_t *xq,
