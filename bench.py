@@ -50,7 +50,9 @@ def parse():
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0 = auto)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--extra", action="store_true", help="also time the other configs")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the C0/C1-batched/C2/C3 legs and the copy-bandwidth probe")
+    ap.add_argument("--extra-iters", type=int, default=100)
     ap.add_argument("--no-prefill", action="store_true", help="skip the C4 prefill leg")
     ap.add_argument("--prefill-iters", type=int, default=20)
     return ap.parse_args()
@@ -125,6 +127,186 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
             "sample": f"{n_done} tokens of C4 (Q4_K 14336x4096) in {t_cpu:.1f} s, oracle "
                       f"matmul_quant_f32 with one thread per token ({n_thr} threads)"}
     return res
+
+
+def _time(fn, iters, stream):
+    """Mean microseconds per call over `iters` back-to-back calls, one HIP
+    event pair on the launch stream around the whole run."""
+    import torch
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for i in range(iters):
+        fn(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / iters
+
+
+def _rotating(t, min_bytes=640e6):
+    """Distinct device copies of `t` totalling >= min_bytes (> the 256 MB
+    Infinity Cache), so every timed launch streams its weights from HBM."""
+    n = max(2, int(np.ceil(min_bytes / t.numel())))
+    return [t] + [t.clone() for _ in range(n - 1)]
+
+
+def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
+    """The other configs: device copy bandwidth, C0, C1 at B = 4 / 8, C2 (f32-x
+    path and the bit-exact int8-activation path), C3 routed experts."""
+    import torch
+    sptr = stream.cuda_stream
+    out = {}
+    # ---- measured device copy bandwidth (read + write) ----
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    us = _time(lambda i: dst.copy_(src), 20, stream)
+    out["device_copy"] = {"bytes_moved": 2 * src.numel(), "us": round(us, 1),
+                          "GBps": round(2 * src.numel() / (us * 1e-6) / 1e9, 1),
+                          "what": "torch copy_ of 1 GiB device -> device (read + write)"}
+    del src, dst
+
+    # ---- GEMV configs through matmul_quant_f32_dev ----
+    def gemv_case(tag, dtype, out_dim, in_dim, n_tok, seed):
+        w_host = synth.weight(dtype, out_dim, in_dim, seed)
+        raw = torch.from_numpy(w_host).to(dev)
+        prep = torch.empty_like(raw)
+        B.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), dtype, in_dim, sptr)
+        del raw
+        reps = _rotating(prep)
+        x_host = synth.activations(n_tok, in_dim, seed + 1).reshape(-1)
+        x = torch.from_numpy(x_host).to(dev)
+        y = torch.empty(n_tok * out_dim, dtype=torch.float32, device=dev)
+
+        def call(i):
+            w = reps[i % len(reps)]
+            B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
+                                   x.numel(), n_tok, in_dim, out_dim, dtype, sptr)
+        for i in range(len(reps)):
+            call(i)
+        us = _time(call, iters, stream)
+        nbytes = prep.numel() + n_tok * (in_dim + out_dim) * 4
+        e = {"config": tag, "dtype": dtype.name, "shape": f"{out_dim}x{in_dim}", "batch": n_tok,
+             "bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+             "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if with_cpu:
+            sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+            from oracle import oracle as O
+            rc, want = O.matmul_quant_f32(w_host, x_host, n_tok, in_dim, out_dim, int(dtype),
+                                          allow_q6k=True)
+            got = y.cpu().numpy()
+            e["max_rel_err_vs_oracle"] = float(np.abs(got - want).max() / np.abs(want).max())
+        del reps, prep
+        return e
+
+    rows = [gemv_case("C0", G.Q4_K, 4096, 4096, 1, 500)]
+    for n_tok in (4, 8):
+        rows.append(gemv_case("C1", G.Q6_K, 14336, 4096, n_tok, 510))
+        rows.append(gemv_case("C1", G.Q6_K, 4096, 14336, n_tok, 520))
+    for (o, i_) in ((4096, 4096), (1024, 4096)):
+        for n_tok in (1, 8, 32):
+            rows.append(gemv_case("C2", G.Q8_0, o, i_, n_tok, 530 + o // 1024))
+    out["gemv"] = rows
+
+    # ---- C2 through the int8-activation path (quantize + matmul, bit-exact) ----
+    q8 = []
+    for (o, i_) in ((4096, 4096), (1024, 4096)):
+        w_host = synth.weight(G.Q8_0, o, i_, 540 + o // 1024)
+        raw = torch.from_numpy(w_host).to(dev)
+        prep = torch.empty_like(raw)
+        B.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), G.Q8_0, i_, sptr)
+        del raw
+        reps = _rotating(prep)
+        blocks = i_ // 32
+        for n_tok in (1, 2, 4, 8, 16, 32):
+            x_host = synth.activations(n_tok, i_, 550 + n_tok).reshape(-1)
+            x = torch.from_numpy(x_host).to(dev)
+            xq = torch.empty(n_tok * blocks * 32, dtype=torch.int8, device=dev)
+            xs = torch.empty(n_tok * blocks, dtype=torch.float32, device=dev)
+            y = torch.empty(n_tok * o, dtype=torch.float32, device=dev)
+
+            def quant(i):
+                B.quantize_q8_0_batch_dev(x.data_ptr(), x.numel(), xq.data_ptr(), xq.numel(),
+                                          xs.data_ptr(), xs.numel(), n_tok, i_, 0, sptr)
+
+            def mm(i):
+                w = reps[i % len(reps)]
+                B.matmul_q8_0_batch_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(),
+                                        xq.data_ptr(), xq.numel(), xs.data_ptr(), xs.numel(),
+                                        n_tok, i_, o, sptr)
+            quant(0)
+            for i in range(len(reps)):
+                mm(i)
+            us_q = _time(quant, iters, stream)
+            us_m = _time(mm, iters, stream)
+            nbytes = prep.numel() + n_tok * blocks * 36 + n_tok * o * 4
+            e = {"shape": f"{o}x{i_}", "batch": n_tok, "quantize_us": round(us_q, 3),
+                 "matmul_us": round(us_m, 3), "matmul_bytes": nbytes,
+                 "matmul_GBps": round(nbytes / (us_m * 1e-6) / 1e9, 1),
+                 "frac_hbm": round(nbytes / (us_m * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+            if with_cpu and n_tok in (1, 32):
+                from oracle import oracle as O
+                rc, oq, os_ = O.quantize_q8_0_batch(x_host, n_tok, i_)
+                rc, want = O.matmul_q8_0_batch(w_host, oq, os_, n_tok, i_, o)
+                e["bit_exact_vs_oracle"] = bool(
+                    np.array_equal(xq.cpu().numpy(), oq) and
+                    np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32)))
+            q8.append(e)
+        del reps, prep
+    out["q8_int8"] = q8
+
+    # ---- C3 routed experts (64 experts, Q4_K gate/up 2048x7168, down 7168x2048, top-8) ----
+    n_expert, n_embd, n_ff, k = 64, 7168, 2048, 8
+    gate = synth.weight(G.Q4_K, n_expert * n_ff, n_embd, 600)
+    up = synth.weight(G.Q4_K, n_expert * n_ff, n_embd, 601)
+    down = synth.weight(G.Q4_K, n_expert * n_embd, n_ff, 602)
+    d_g, d_u, d_d = (torch.from_numpy(a).to(dev) for a in (gate, up, down))
+    per_expert = (gate.nbytes + up.nbytes + down.nbytes) // n_expert
+    moe = []
+    for T in (1, 8, 32):
+        x_host = synth.activations(T, n_embd, 610 + T).reshape(-1)
+        ids, wts = synth.moe_routing(T, n_expert, k, 620 + T)
+        x = torch.from_numpy(x_host).to(dev)
+        d_ids = torch.from_numpy(ids.reshape(-1)).to(dev)
+        d_w = torch.from_numpy(wts.reshape(-1)).to(dev)
+        y = torch.zeros(T * n_embd, dtype=torch.float32, device=dev)
+
+        def call(i):
+            B.moe_routed_dev(y.data_ptr(), y.numel(), x.data_ptr(), x.numel(), d_g.data_ptr(),
+                             d_u.data_ptr(), gate.nbytes, d_d.data_ptr(), down.nbytes,
+                             d_ids.data_ptr(), d_w.data_ptr(), ids.size, T, n_embd, n_ff, n_expert,
+                             k, G.Q4_K, G.Q4_K, 10.0, sptr)
+        for i in range(3):
+            call(i)
+        us = _time(call, max(10, iters // 4), stream)
+        n_act = len(np.unique(ids))
+        nbytes = n_act * per_expert + 2 * T * n_embd * 4
+        e = {"tokens": T, "active_experts": n_act, "bytes": nbytes, "us": round(us, 2),
+             "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+             "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if with_cpu and T == 1:
+            from oracle import oracle as O
+            y.zero_()
+            call(0)
+            torch.cuda.synchronize()
+            want = np.zeros(T * n_embd, np.float32)
+            t0 = time.perf_counter()
+            rc = O.moe_routed(want, x_host, T, n_embd, n_ff, gate, up, down, int(G.Q4_K),
+                              int(G.Q4_K), n_expert, ids, wts, k, 10.0)
+            t_cpu = time.perf_counter() - t0
+            got = y.cpu().numpy()
+            e["max_rel_err_vs_oracle"] = float(np.abs(got - want).max() / np.abs(want).max())
+            e["cpu_baseline"] = {"value": nbytes / t_cpu / 1e9, "unit": "GB/s", "cores": 1,
+                                 "kind": "port",
+                                 "sample": f"1 token, {k} experts x 3 GEMVs in {t_cpu:.2f} s, "
+                                           "oracle moe_routed (accumulate_moe_outputs "
+                                           "composition of matmul_quant_f32)"}
+        moe.append(e)
+    out["moe"] = {"workload": "C3 64 experts, Q4_K gate/up (2048, 7168), down (7168, 2048), "
+                              "top-8, softmax weights", "by_tokens": moe}
+    del d_g, d_u, d_d
+    return out
 
 
 def main():
@@ -273,6 +455,9 @@ def main():
                                                           args.prefill_iters, not args.no_cpu,
                                                           args.cpu_seconds)
 
+    extra = None if args.no_extra else bench_extra(B, synth, G, dev, stream, args.extra_iters,
+                                                    not args.no_cpu)
+
     line = {
         "metric": "Q4_K/Q6_K GEMV GB/s (% of HBM peak); Q4_K prefill GEMM TFLOP/s",
         "value": round(value, 2),
@@ -310,6 +495,7 @@ def main():
         "cpu_baseline": cpu_baseline,
         "check": check,
         "prefill": prefill,
+        "extra": extra,
     }
     print(json.dumps(line))
 
