@@ -24,7 +24,8 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librsllm_hip.so")
 
-SOURCES = ["abi.hip", "dequant.hip", "gemv.hip", "prefill.hip", "moe.hip", "q8_int8.hip"]
+SOURCES = ["abi.hip", "dequant.hip", "gemv.hip", "gemv_mfma.hip", "prefill.hip", "moe.hip",
+           "q8_int8.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -46,6 +47,7 @@ def hipcc() -> str:
 
 EXTRA_FLAGS = {
     "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "gemv_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

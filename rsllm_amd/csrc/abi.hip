@@ -254,7 +254,7 @@ int rsllm_hip_matmul_quant_f32_dev(float *out, size_t out_len, const uint8_t *we
         return ok();
     }
     if ((rc = ensure_device())) return rc;
-    HIP_TRY(t_ctx.xq.ensure(gemv_scratch_bytes(dtype, (int)n_tok, (int)in_dim)), "hipMalloc");
+    HIP_TRY(t_ctx.xq.ensure(gemv_work_bytes(dtype, (int)n_tok, (int)in_dim, (int)out_dim)), "hipMalloc");
     HIP_TRY(launch_gemv(dtype, weights, weights_len, x, (uint8_t *)t_ctx.xq.p, out, (int)n_tok,
                         (int)in_dim, (int)out_dim, s),
             "gemv");
@@ -292,7 +292,7 @@ int rsllm_hip_matmul_quant_f32(float *out, size_t out_len, const uint8_t *weight
     HIP_TRY(c.y.ensure(out_len * sizeof(float)), "hipMalloc");
     HIP_TRY(hipMemcpyAsync(c.x.p, x, x_len * sizeof(float), hipMemcpyHostToDevice, c.stream),
             "upload x");
-    HIP_TRY(c.xq.ensure(gemv_scratch_bytes(dtype, (int)n_tok, (int)in_dim)), "hipMalloc");
+    HIP_TRY(c.xq.ensure(gemv_work_bytes(dtype, (int)n_tok, (int)in_dim, (int)out_dim)), "hipMalloc");
     HIP_TRY(launch_gemv(dtype, dw, weights_len, (const float *)c.x.p, (uint8_t *)c.xq.p,
                         (float *)c.y.p, (int)n_tok, (int)in_dim, (int)out_dim, c.stream),
             "gemv");

@@ -39,6 +39,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint3
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
 }
 
+// Packed f16 vectors of the MFMA paths.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Eight 4-bit codes (the low nibbles of two dwords, or the high nibbles when
+// `hi`) -> 8 f16 values q * dsc - dm. v_cvt_scalef32_pk_f16_fp8 reads each
+// byte 0..15 as an e4m3 value q * 2^-9 (exact) and applies a power-of-two
+// scale, so a scale of 2^9 yields the integer q in f16 exactly, two per
+// instruction; one packed FMA then applies the block scales (one rounding).
+__device__ __forceinline__ f16x8 dequant_q4x8_f16(uint32_t d0, uint32_t d1, bool hi, f16x2 dsc,
+                                                  f16x2 dm) {
+    if (hi) {
+        d0 >>= 4;
+        d1 >>= 4;
+    }
+    d0 &= 0x0F0F0F0Fu;
+    d1 &= 0x0F0F0F0Fu;
+    const f16x2 q0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 512.0f, false);  // bytes 0, 1
+    const f16x2 q1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 512.0f, true);   // bytes 2, 3
+    const f16x2 q2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 512.0f, false);
+    const f16x2 q3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 512.0f, true);
+    const f16x2 w0 = q0 * dsc - dm, w1 = q1 * dsc - dm, w2 = q2 * dsc - dm, w3 = q3 * dsc - dm;
+    f16x8 r;
+    r[0] = w0[0]; r[1] = w0[1]; r[2] = w1[0]; r[3] = w1[1];
+    r[4] = w2[0]; r[5] = w2[1]; r[6] = w3[0]; r[7] = w3[1];
+    return r;
+}
+
 // Sum over the 64 lanes of a wavefront; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

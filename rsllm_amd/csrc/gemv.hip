@@ -724,6 +724,15 @@ size_t gemv_scratch_bytes(uint32_t dtype, int n_tok, int in_dim) {
     }
 }
 
+size_t gemv_work_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
+    size_t b = gemv_scratch_bytes(dtype, n_tok, in_dim);
+    if (gemv_mfma_supported(dtype, n_tok, in_dim, out_dim)) {
+        const size_t m = gemv_mfma_scratch_bytes(n_tok, in_dim);
+        if (m > b) b = m;
+    }
+    return b;
+}
+
 template <class F, int RT, int BT>
 static hipError_t go(const uint8_t *w, size_t w_bytes, const uint8_t *xq, size_t xqb, float *y,
                      int n_tok, int in_dim, int out_dim, hipStream_t s) {
@@ -834,6 +843,8 @@ hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const f
                        uint8_t *xq_scratch, float *y, int n_tok, int in_dim, int out_dim,
                        hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
+    if (gemv_mfma_supported(dtype, n_tok, in_dim, out_dim))
+        return launch_gemv_mfma(dtype, w, w_bytes, x, xq_scratch, y, n_tok, in_dim, out_dim, s);
     if (n_tok == 1 && gemv1_fits(dtype, in_dim)) {
         switch (dtype) {
         case T_Q4_K: return gemv1<FQ4K>(w, w_bytes, x, y, in_dim, out_dim, s);

@@ -1,0 +1,328 @@
+// Batched GEMV (5..32 tokens) on the matrix cores: y[t, o] = sum_i W[o, i] x[t, i].
+//
+// Restates matmul_quant_f32 (rsllm-backend-cpu/src/ops/quant_matmul.rs:45-119)
+// for the decode batches of C1/C2-style shapes, where the int8-limb GEMV
+// (gemv.hip) spends VALU work per (weight, token) pair and stops being
+// memory-bound above a few tokens. Here each weight is dequantised once to
+// f16 in registers — f16(d*sc)*q - f16(dmin*m) for Q4_K (one rounding, as the
+// prefill GEMM), (q - 32)*f16(d*sc) for Q6_K (q - 32 exact, one rounding) —
+// and the tokens are the N dimension of v_mfma_f32_16x16x32_f16 (16 or 32
+// tokens per pass, fp32 accumulation), so the dequant cost is independent of
+// the batch.
+//
+// Activations: a pre-pass scales each token by 2^e (max |x| into
+// [2^14, 2^15)) and stores it as f16 in MFMA operand order,
+//   xh[((s * 4 + j) * 4 + q) * ntp + t][0..7] = f16(2^e_t x[t, F::elem(s, j, q) + 0..7]),
+// s = K step of 128 elements, j = MFMA of the step, q = lane group, ntp =
+// padded token count (16 or 32, padding tokens zero); unscale[t] = 2^-e_t.
+//
+// Kernel: workgroup = NK wavefronts over the same 16*RT weight rows; wavefront
+// w takes K steps [w * nsteps / NK, (w + 1) * nsteps / NK) with the next
+// step's weights and activations in flight while the current one is
+// computed. Lane (r, q) = (lane % 16, lane / 16) dequantises 32 weights of
+// row r per step (8 for each of the 4 MFMAs). The NK partial tiles are added
+// through LDS in wavefront order (deterministic), scaled by 2^-e_t, stored.
+#include "kernels.h"
+
+namespace rsllm_hip {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMfStep = 128;  // K elements per step
+
+__device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0);
+}
+
+// Q4_K (GGUF layout). Step s = half (s & 1) of super-block s >> 1. Lane group
+// q reads qs bytes 32q + 16 (s & 1) .. + 15 (sub-block pair q): low nibbles are
+// sub-block 2q, positions 16 (s & 1) + 0..15; high nibbles sub-block 2q + 1.
+// MFMA j: low (j even) / high (j odd) nibbles of bytes 0..7 (j < 2) or 8..15.
+struct MQ4K {
+    struct W {
+        uint4 hdr, qs;
+    };
+    __device__ static int elem(int s, int j, int q) {
+        return 256 * (s >> 1) + 64 * q + 32 * (j & 1) + 16 * (s & 1) + 8 * (j >> 1);
+    }
+    __device__ static void load(W &w, __amdgpu_buffer_rsrc_t r, int row, int s, int q, int in_dim,
+                                int) {
+        const uint32_t off = ((uint32_t)row * (uint32_t)(in_dim >> 8) + (uint32_t)(s >> 1)) * 144u;
+        w.hdr = bload16(r, off, 0);
+        w.qs = bload16(r, off + 16u + 32u * (uint32_t)q + 16u * (uint32_t)(s & 1), 0);
+    }
+    __device__ static void dequant(const W &w, int q, int, f16x8 (&a)[4]) {
+        const float d = f16_to_f32(w.hdr.x & 0xFFFFu), dmin = f16_to_f32(w.hdr.x >> 16);
+        // (sc, m) of sub-blocks 2q and 2q + 1 (q4_k_scale_min, dequant/mod.rs:48-58),
+        // both forms computed and selected per lane
+        const uint32_t s0 = w.hdr.y, s1 = w.hdr.z, s2 = w.hdr.w;
+        uint32_t sc[2], m[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int jj = 2 * q + u;
+            const uint32_t sh = 8u * (uint32_t)(jj & 3);
+            const uint32_t lo_sc = (s0 >> sh) & 63u, lo_m = (s1 >> sh) & 63u;
+            const uint32_t b2 = (s2 >> sh) & 0xFFu;
+            const uint32_t hi_sc = (b2 & 15u) | (((s0 >> sh) >> 6) & 3u) << 4;
+            const uint32_t hi_m = (b2 >> 4) | (((s1 >> sh) >> 6) & 3u) << 4;
+            sc[u] = jj < 4 ? lo_sc : hi_sc;
+            m[u] = jj < 4 ? lo_m : hi_m;
+        }
+        const _Float16 dl = (_Float16)(d * (float)sc[0]), ml = (_Float16)(dmin * (float)m[0]);
+        const _Float16 dh = (_Float16)(d * (float)sc[1]), mh = (_Float16)(dmin * (float)m[1]);
+        const f16x2 dsl = {dl, dl}, dml = {ml, ml}, dsh = {dh, dh}, dmh = {mh, mh};
+        a[0] = dequant_q4x8_f16(w.qs.x, w.qs.y, false, dsl, dml);
+        a[1] = dequant_q4x8_f16(w.qs.x, w.qs.y, true, dsh, dmh);
+        a[2] = dequant_q4x8_f16(w.qs.z, w.qs.w, false, dsl, dml);
+        a[3] = dequant_q4x8_f16(w.qs.z, w.qs.w, true, dsh, dmh);
+    }
+};
+
+// Four 6-bit codes (bytes 0..63 of q6) -> f16 (q - 32) * dsc. v_perm_b32 pairs
+// each byte with 0x64, the f16 pattern of 1024 + q (exact); subtracting 1056
+// gives q - 32 exactly, and the multiply rounds once.
+__device__ __forceinline__ void q6x4_f16(uint32_t q6, f16x2 dsc, f16x2 &w01, f16x2 &w23) {
+    const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, q6, 0x04010400u);
+    const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, q6, 0x04030402u);
+    const f16x2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};
+    w01 = (__builtin_bit_cast(f16x2, p01) - bias) * dsc;
+    w23 = (__builtin_bit_cast(f16x2, p23) - bias) * dsc;
+}
+
+// Q6_K (super-tile device layout). Step s = half h = s & 1 of block s >> 1.
+// Lane group q reads ql bytes 64h + 16q .. + 15 and qh bytes 32h + 16 (q & 1)
+// .. + 15: low nibbles are elements 128h + 16q + b (high bits at 2 (q >> 1)),
+// high nibbles elements 128h + 64 + 16q + b (high bits at 4 + 2 (q >> 1));
+// their scales are sc[8h + q] and sc[8h + q + 4].
+struct MQ6K {
+    struct W {
+        uint4 ql, qh;
+        uint32_t sl, sh, d;
+    };
+    __device__ static int elem(int s, int j, int q) {
+        return 256 * (s >> 1) + 128 * (s & 1) + 16 * q + 64 * (j & 1) + 8 * (j >> 1);
+    }
+    __device__ static void load(W &w, __amdgpu_buffer_rsrc_t r, int row, int s, int q, int in_dim,
+                                int out_dim) {
+        const uint32_t nb = (uint32_t)(in_dim >> 8);
+        const uint32_t nblk = (uint32_t)out_dim * nb;
+        const uint32_t bi = (uint32_t)row * nb + (uint32_t)(s >> 1);
+        const uint32_t S = bi >> 3, jb = bi & 7u;
+        const uint32_t rS = (S < (nblk >> 3)) ? 8u : (nblk & 7u);
+        const uint32_t base = S * 1680u, h = (uint32_t)(s & 1);
+        w.ql = bload16(r, base + jb * 128u + 64u * h + 16u * (uint32_t)q, 0);
+        w.qh = bload16(r, base + rS * 128u + jb * 64u + 32u * h + 16u * (uint32_t)(q & 1), 0);
+        w.sl = bload4(r, base + rS * 192u + jb * 16u + 8u * h);
+        w.sh = bload4(r, base + rS * 192u + jb * 16u + 8u * h + 4u);
+        w.d = bload2(r, base + rS * 208u + jb * 2u, 0);
+    }
+    __device__ static void dequant(const W &w, int q, int, f16x8 (&a)[4]) {
+        const float d = f16_to_f32(w.d);
+        const float scl = (float)(int)(int8_t)(w.sl >> (8 * q));
+        const float sch = (float)(int)(int8_t)(w.sh >> (8 * q));
+        const _Float16 dl = (_Float16)(d * scl), dh = (_Float16)(d * sch);
+        const f16x2 dsl = {dl, dl}, dsh = {dh, dh};
+        const uint32_t shl = 2u * (uint32_t)(q >> 1), shh = 4u + shl;
+        const uint32_t l[4] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w};
+        const uint32_t hb[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const bool hi = j & 1;
+            const int p = 2 * (j >> 1);
+            f16x2 v[4];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t nib = hi ? (l[p + u] >> 4) & 0x0F0F0F0Fu : l[p + u] & 0x0F0F0F0Fu;
+                const uint32_t top = ((hb[p + u] >> (hi ? shh : shl)) & 0x03030303u) << 4;
+                q6x4_f16(nib | top, hi ? dsh : dsl, v[2 * u], v[2 * u + 1]);
+            }
+            f16x8 r;
+            r[0] = v[0][0]; r[1] = v[0][1]; r[2] = v[1][0]; r[3] = v[1][1];
+            r[4] = v[2][0]; r[5] = v[2][1]; r[6] = v[3][0]; r[7] = v[3][1];
+            a[j] = r;
+        }
+    }
+};
+
+// ---- activation pre-pass ---------------------------------------------------------
+// One workgroup per padded token: max |x| over the row, e with max * 2^e in
+// [2^14, 2^15) (e in [-126, 126]; a zero row gets e = 0), then each thread
+// writes 8-element pieces in operand order. Padding tokens write zeros.
+template <class F>
+__global__ __launch_bounds__(256) void k_mf_x(const float *__restrict__ x, _Float16 *__restrict__ xh,
+                                              float *__restrict__ unscale, int n_tok, int in_dim,
+                                              int ntp) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int nsteps = in_dim / kMfStep;
+    const bool real = t < n_tok;
+    const float *xt = x + (size_t)(real ? t : 0) * in_dim;
+    float amax = 0.f;
+    if (real)
+        for (int i = tid * 4; i < in_dim; i += 1024) {
+            const float4 v = *reinterpret_cast<const float4 *>(xt + i);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (amax > 0.f && amax <= 3.4e38f) {
+        int ex;
+        frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
+        e = min(max(15 - ex, -126), 126);
+    }
+    const float up = ldexpf(1.0f, e);
+    if (tid == 0) unscale[t] = real ? ldexpf(1.0f, -e) : 0.f;
+    for (int g = tid; g < nsteps * 16; g += 256) {
+        const int s = g >> 4, j = (g >> 2) & 3, q = g & 3;
+        uint4 o = make_uint4(0, 0, 0, 0);
+        if (real) {
+            const float *p = xt + F::elem(s, j, q);
+            const float4 v0 = *reinterpret_cast<const float4 *>(p);
+            const float4 v1 = *reinterpret_cast<const float4 *>(p + 4);
+            f16x8 h;
+            h[0] = (_Float16)(v0.x * up); h[1] = (_Float16)(v0.y * up);
+            h[2] = (_Float16)(v0.z * up); h[3] = (_Float16)(v0.w * up);
+            h[4] = (_Float16)(v1.x * up); h[5] = (_Float16)(v1.y * up);
+            h[6] = (_Float16)(v1.z * up); h[7] = (_Float16)(v1.w * up);
+            o = __builtin_bit_cast(uint4, h);
+        }
+        *reinterpret_cast<uint4 *>(xh + ((size_t)g * ntp + t) * 8) = o;
+    }
+}
+
+// ---- GEMV ----------------------------------------------------------------------------
+template <class F, int NT, int NK, int RT>
+__global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__ w, uint32_t w_bytes,
+                                                     const _Float16 *__restrict__ xh,
+                                                     uint32_t xh_bytes,
+                                                     const float *__restrict__ unscale,
+                                                     float *__restrict__ y, int n_tok, int in_dim,
+                                                     int out_dim) {
+    __shared__ f32x4 red[NK * RT * NT * 64];
+    constexpr int ntp = NT * 16;
+    const int lane = threadIdx.x & 63, r16 = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row0 = blockIdx.x * 16 * RT;
+    const int nsteps = in_dim / kMfStep;
+    const int s0 = nsteps * wv / NK, s1 = nsteps * (wv + 1) / NK;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xh, xh_bytes);
+
+    f32x4 acc[RT][NT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[rt][nt] = {0.f, 0.f, 0.f, 0.f};
+
+    typename F::W wa[RT], wb[RT];
+    uint4 xa[4][NT], xb[4][NT];
+    auto load = [&](typename F::W (&wr)[RT], uint4 (&xr)[4][NT], int s) {
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+            F::load(wr[rt], rw, min(row0 + 16 * rt + r16, out_dim - 1), s, q, in_dim, out_dim);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+                xr[j][nt] = bload16(rx, (uint32_t)((((s * 4 + j) * 4 + q) * ntp + nt * 16 + r16) * 16), 0);
+    };
+    auto compute = [&](const typename F::W (&wr)[RT], const uint4 (&xr)[4][NT], int s) {
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            f16x8 a[4];
+            F::dequant(wr[rt], q, s, a);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        a[j], __builtin_bit_cast(f16x8, xr[j][nt]), acc[rt][nt], 0, 0, 0);
+        }
+    };
+    if (s0 < s1) {
+        load(wa, xa, s0);
+        for (int s = s0; s < s1; s += 2) {
+            if (s + 1 < s1) load(wb, xb, s + 1);
+            compute(wa, xa, s);
+            if (s + 1 < s1) {
+                if (s + 2 < s1) load(wa, xa, s + 2);
+                compute(wb, xb, s + 1);
+            }
+        }
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) red[((wv * RT + rt) * NT + nt) * 64 + lane] = acc[rt][nt];
+    __syncthreads();
+    for (int c = threadIdx.x; c < RT * NT * 64; c += 64 * NK) {
+        const int rt = c / (NT * 64), nt = (c / 64) % NT, ln = c % 64;
+        f32x4 v = red[(rt * NT + nt) * 64 + ln];
+        for (int k = 1; k < NK; k++) v += red[((k * RT + rt) * NT + nt) * 64 + ln];
+        const int t = nt * 16 + (ln & 15);
+        const int o = row0 + 16 * rt + 4 * (ln >> 4);  // D rows 4 (lane / 16) + 0..3
+        if (t < n_tok) {
+            const float us = unscale[t];
+            float *yt = y + (size_t)t * out_dim;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (o + i < out_dim) yt[o + i] = v[i] * us;
+        }
+    }
+}
+
+// ---- launchers -----------------------------------------------------------------------
+// Taken from 5 tokens up: below that the int8-limb GEMV, whose VALU work
+// grows with the batch, is still faster (C1: 26 vs 29 us at 4 tokens, 55 vs
+// 29 us at 8). f16 weights and activations put the expected max|d|/max|y|
+// near 4e-4 for outputs of many rows (the maxima of both then track their
+// standard deviations); a matrix of a few dozen rows can exceed 1e-3 by
+// chance, so short matrices stay on the int8-limb GEMV.
+bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
+    return (dtype == T_Q4_K || dtype == T_Q6_K) && n_tok >= 5 && n_tok <= 32 &&
+           in_dim % 256 == 0 && in_dim > 0 && out_dim >= 1024;
+}
+
+size_t gemv_mfma_scratch_bytes(int n_tok, int in_dim) {
+    const size_t ntp = n_tok <= 16 ? 16 : 32;
+    return (ntp * (size_t)in_dim * 2 + 255) / 256 * 256 + ntp * 4;
+}
+
+template <class F, int NT, int NK, int RT>
+static hipError_t mf_go(const uint8_t *w, size_t w_bytes, const float *x, uint8_t *scratch, float *y,
+                        int n_tok, int in_dim, int out_dim, hipStream_t s) {
+    constexpr int ntp = NT * 16;
+    const size_t xh_bytes = ((size_t)ntp * in_dim * 2 + 255) / 256 * 256;
+    _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
+    float *unscale = reinterpret_cast<float *>(scratch + xh_bytes);
+    k_mf_x<F><<<ntp, 256, 0, s>>>(x, xh, unscale, n_tok, in_dim, ntp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int rows_wg = 16 * RT;
+    k_gemv_mf<F, NT, NK, RT><<<(unsigned)((out_dim + rows_wg - 1) / rows_wg), 64 * NK, 0, s>>>(
+        w, (uint32_t)w_bytes, xh, (uint32_t)xh_bytes, unscale, y, n_tok, in_dim, out_dim);
+    return hipGetLastError();
+}
+
+template <class F>
+static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, uint8_t *scratch,
+                              float *y, int n_tok, int in_dim, int out_dim, hipStream_t s) {
+    if (n_tok <= 16) return mf_go<F, 1, 8, 1>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
+    return mf_go<F, 2, 8, 1>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
+}
+
+hipError_t launch_gemv_mfma(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
+                            uint8_t *scratch, float *y, int n_tok, int in_dim, int out_dim,
+                            hipStream_t s) {
+    switch (dtype) {
+    case T_Q4_K: return mf_dispatch<MQ4K>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
+    case T_Q6_K: return mf_dispatch<MQ6K>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace rsllm_hip

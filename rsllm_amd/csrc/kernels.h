@@ -43,13 +43,25 @@ hipError_t launch_prepare(uint32_t dtype, const uint8_t *src, uint8_t *dst, size
                           size_t in_dim, hipStream_t s);
 
 // gemv.hip: y[t, o] = sum_i W[o, i] x[t, i] for t < n_tok, W (w_bytes bytes)
-// in device layout. Batch 1 is one launch that quantises x in LDS; larger
-// batches run the activation pre-pass into `xq_scratch`, which must hold
-// gemv_scratch_bytes(dtype, n_tok, in_dim) bytes, then the GEMV.
+// in device layout. Batch 1 is one launch that quantises x in LDS; 5..32
+// tokens of Q4_K / Q6_K run on the matrix cores (gemv_mfma.hip); other
+// batches run the activation pre-pass, then the GEMV. `xq_scratch` must hold
+// gemv_work_bytes(dtype, n_tok, in_dim, out_dim) bytes.
 hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
                        uint8_t *xq_scratch, float *y, int n_tok, int in_dim, int out_dim,
                        hipStream_t s);
 size_t gemv_scratch_bytes(uint32_t dtype, int n_tok, int in_dim);
+// Scratch launch_gemv needs for this call (>= gemv_scratch_bytes; the MFMA
+// path for 2..32 tokens keeps f16 activations there).
+size_t gemv_work_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim);
+
+// gemv_mfma.hip: the same product for 5..32 tokens of Q4_K / Q6_K on the
+// matrix cores (weights dequantised to f16 once, tokens as the MFMA's N).
+bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim);
+size_t gemv_mfma_scratch_bytes(int n_tok, int in_dim);
+hipError_t launch_gemv_mfma(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
+                            uint8_t *scratch, float *y, int n_tok, int in_dim, int out_dim,
+                            hipStream_t s);
 // The two halves of launch_gemv: the activation pre-pass (format-specific
 // int8 two-limb layout) and the GEMV on pre-quantised activations.
 hipError_t launch_quantize_x(uint32_t dtype, const float *x, uint8_t *xq, int n_tok, int in_dim,

@@ -142,18 +142,7 @@ __global__ __launch_bounds__(256) void k_prefill_x(const uint16_t *__restrict__ 
 // power of two, so a scale of 2^9 yields the integer q in f16 exactly — two
 // weights per instruction.
 __device__ __forceinline__ h8 pf_dequant8(uint32_t d0, uint32_t d1, bool hi, h2 dsc, h2 dm) {
-    if (hi) { d0 >>= 4; d1 >>= 4; }
-    d0 &= 0x0F0F0F0Fu;
-    d1 &= 0x0F0F0F0Fu;
-    const h2 q0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 512.0f, false);  // bytes 0, 1
-    const h2 q1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 512.0f, true);   // bytes 2, 3
-    const h2 q2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 512.0f, false);
-    const h2 q3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 512.0f, true);
-    const h2 w0 = q0 * dsc - dm, w1 = q1 * dsc - dm, w2 = q2 * dsc - dm, w3 = q3 * dsc - dm;
-    h8 r;
-    r[0] = w0[0]; r[1] = w0[1]; r[2] = w1[0]; r[3] = w1[1];
-    r[4] = w2[0]; r[5] = w2[1]; r[6] = w3[0]; r[7] = w3[1];
-    return r;
+    return dequant_q4x8_f16(d0, d1, hi, dsc, dm);
 }
 
 struct pf_true { static constexpr bool value = true; };

@@ -30,11 +30,34 @@ def test_gemv_ragged_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
     assert rel_err(got, want) <= REL_TOL
 
 
+# The matrix-core path (5..32 tokens of Q4_K / Q6_K, out_dim >= 1024): one
+# and two 16-token tiles, partial tiles, row counts off the 16-row tile, few K
+# steps per wavefront (in 256) and many (in 7168), token scales far apart.
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K])
+@pytest.mark.parametrize("out_dim,in_dim", [(1024, 256), (1030, 1024), (2000, 7168), (4097, 512)])
+@pytest.mark.parametrize("n_tok", [5, 15, 16, 17, 31, 32])
+def test_gemv_mfma_batches(oracle, hip, dtype, out_dim, in_dim, n_tok):
+    w = synth.weight(dtype, out_dim, in_dim, 7 + n_tok)
+    x = synth.activations(n_tok, in_dim, 8 + n_tok)
+    x *= (np.float32(10.0) ** ((np.arange(n_tok) % 7) - 3)).astype(np.float32)[:, None]
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, x, n_tok, in_dim, out_dim, int(dtype))
+    got = np.empty(n_tok * out_dim, np.float32)
+    hip.matmul_quant_f32(got, w, x, n_tok, in_dim, out_dim, dtype)
+    # per token: each token's outputs against that token's own maximum
+    g = got.reshape(n_tok, out_dim)
+    wv = want.reshape(n_tok, out_dim)
+    for t in range(n_tok):
+        if np.abs(wv[t]).max() > 0:
+            assert rel_err(g[t], wv[t]) <= REL_TOL, f"token {t}"
+
+
 # Benchmark shapes at full size (BASELINE configs C0-C2).
 @pytest.mark.parametrize("dtype,out_dim,in_dim,n_tok", [
     (G.Q4_K, 4096, 4096, 1),
     (G.Q6_K, 14336, 4096, 1), (G.Q6_K, 14336, 4096, 4), (G.Q6_K, 14336, 4096, 8),
     (G.Q6_K, 4096, 14336, 1), (G.Q6_K, 4096, 14336, 4), (G.Q6_K, 4096, 14336, 8),
+    (G.Q6_K, 14336, 4096, 32), (G.Q4_K, 4096, 4096, 16),
     (G.Q8_0, 4096, 4096, 1), (G.Q8_0, 4096, 4096, 2), (G.Q8_0, 4096, 4096, 4),
     (G.Q8_0, 4096, 4096, 8), (G.Q8_0, 4096, 4096, 16), (G.Q8_0, 4096, 4096, 32),
     (G.Q8_0, 1024, 4096, 1), (G.Q8_0, 1024, 4096, 32),
