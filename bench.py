@@ -19,6 +19,10 @@ roofline     = the same bytes per launch / mean duration of the dominant kernel
 cpu_baseline = the CPU oracle (a C restatement of the reference CPU path,
                one thread per token as the reference's rayon split gives at
                batch 1) timed on a bounded sample of the same GEMVs.
+traffic      = HBM bytes per launch of the dominant kernel from two rocprofv3
+               --pmc passes (FETCH_SIZE, WRITE_SIZE) over a child run of this
+               script (--pmc-probe), each counter scaled by bytes / counter of a
+               device copy of known size in the same pass
 prefill      = BASELINE.json configs[4] (C4): Q4_K weight (out, in) =
                (14336, 4096) times bf16 activations [T x 4096], T = 512 and
                2048, fp32 output, on the MFMA path; TFLOP/s = 2 T in out / the
@@ -53,6 +57,10 @@ def parse():
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the C0/C1-batched/C2/C3 legs and the copy-bandwidth probe")
     ap.add_argument("--extra-iters", type=int, default=100)
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc passes that measure roofline.traffic")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="internal: the workload run under rocprofv3 --pmc (prints no JSON)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C4 prefill leg")
     ap.add_argument("--prefill-iters", type=int, default=20)
     return ap.parse_args()
@@ -148,6 +156,91 @@ def _rotating(t, min_bytes=640e6):
     Infinity Cache), so every timed launch streams its weights from HBM."""
     n = max(2, int(np.ceil(min_bytes / t.numel())))
     return [t] + [t.clone() for _ in range(n - 1)]
+
+
+PMC_COPY_BYTES = 256 << 20
+
+
+def pmc_probe():
+    """Run under rocprofv3 --pmc by pmc_traffic(): three device copies of
+    PMC_COPY_BYTES (the calibration kernel, bytes known) and then the dominant
+    kernel of the bench line (C1 14336x4096 Q6_K batch-1 GEMV, one launch per
+    call) streaming its weights from HBM through rotating copies."""
+    import torch
+    from rsllm_amd import backend as B
+    from rsllm_amd import synth
+    from rsllm_amd.ggml import GgmlType as G
+    dev = torch.device("cuda:0")
+    sptr = torch.cuda.current_stream().cuda_stream
+    a = torch.empty(PMC_COPY_BYTES, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    del a, b
+    out_dim, in_dim = 14336, 4096
+    w_host = synth.weight(G.Q6_K, out_dim, in_dim, seed=100)
+    raw = torch.from_numpy(w_host).to(dev)
+    prep = torch.empty_like(raw)
+    B.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), G.Q6_K, in_dim, sptr)
+    del raw
+    reps = _rotating(prep)
+    x = torch.from_numpy(synth.activations(1, in_dim, seed=200)).to(dev).reshape(-1)
+    y = torch.empty(out_dim, dtype=torch.float32, device=dev)
+    for i in range(len(reps) + 8):
+        w = reps[i % len(reps)]
+        B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
+                               x.numel(), 1, in_dim, out_dim, G.Q6_K, sptr)
+    torch.cuda.synchronize()
+
+
+def pmc_traffic():
+    """roofline.traffic: HBM bytes per launch of the dominant kernel from two
+    rocprofv3 --pmc passes over a child run of pmc_probe() (FETCH_SIZE, then
+    WRITE_SIZE, KiB per dispatch). Each counter is scaled by bytes / counter of
+    the calibration copy in the same pass, whose read and write sizes are
+    known. Returns (bytes or None, details)."""
+    import shutil
+    import sqlite3
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(exe):
+        return None, {"error": "rocprofv3 not found"}
+    here = os.path.abspath(__file__)
+    env = dict(os.environ, TMPDIR="/tmp")
+    det = {"calibration": f"device copy of {PMC_COPY_BYTES} bytes (read {PMC_COPY_BYTES}, "
+                          f"write {PMC_COPY_BYTES})"}
+    total = 0.0
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="rsllm_pmc_", dir="/tmp")
+        cmd = ["timeout", "-s", "KILL", "120", exe, "--pmc", ctr, "-d", d, "-o", "p", "--",
+               sys.executable, here, "--pmc-probe"]
+        try:
+            r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True, timeout=150)
+        except subprocess.TimeoutExpired:
+            return None, {"error": f"{ctr} pass timed out"}
+        dbs = [os.path.join(root, f) for root, _, fs in os.walk(d) for f in fs if f.endswith(".db")]
+        if r.returncode != 0 or not dbs:
+            return None, {"error": f"{ctr} pass failed (rc {r.returncode})",
+                          "stderr_tail": r.stderr[-400:]}
+        rows = sqlite3.connect(dbs[0]).execute(
+            "select name, counter_value from pmc_events where counter_name = ? "
+            "order by dispatch_id", (ctr,)).fetchall()
+        shutil.rmtree(d, ignore_errors=True)
+        # the calibration copies are the probe's first three copy dispatches
+        # (later ones are weight uploads and clones of other sizes)
+        copy = [v for n, v in rows if "copyBuffer" in n][:3]
+        gemv = [v for n, v in rows if "k_gemv1" in n][-8:]
+        if not copy or not gemv:
+            return None, {"error": f"{ctr}: kernels not found in the pass"}
+        factor = PMC_COPY_BYTES / (float(np.median(copy)) * 1024.0)
+        kib = float(np.median(gemv))
+        det[ctr] = {"gemv_kib_per_dispatch": round(kib, 1),
+                    "copy_kib_per_dispatch": round(float(np.median(copy)), 1),
+                    "factor_bytes_per_counted_byte": round(factor, 4),
+                    "bytes_per_launch": round(kib * 1024.0 * factor)}
+        total += kib * 1024.0 * factor
+    return round(total), det
 
 
 def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
@@ -316,6 +409,12 @@ def main():
         print("bench.py measures one MI355X: this build has no multi-GPU path "
               "(sharding is described in DESIGN.md); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_probe:
+        pmc_probe()
+        return
+    # the counter passes run first, in child processes, before this process
+    # touches the GPU
+    traffic, traffic_detail = (None, {"skipped": True}) if args.no_traffic else pmc_traffic()
 
     import torch
 
@@ -486,7 +585,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_detail": traffic_detail,
             "kernel": "rsllm_hip::k_gemv1<FQ6K, RT, NWV> (x quantised in LDS, one launch)",
             "kernel_shape": per_kernel[dom]["shape"],
             "kernel_us_mean": round(kern_us[dom], 3),
