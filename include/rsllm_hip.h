@@ -16,8 +16,9 @@
  *
  * Weights in device memory are in the "device layout" written by
  * rsllm_hip_prepare_weights_dev: for Q4_K it is the GGUF byte stream
- * itself; Q6_K / Q8_0 / Q4_0 matrices are regrouped into 8-block super-tiles
- * of the same total size (see rsllm_hip_prepare_weights_dev).
+ * itself; Q6_K / Q8_0 / Q4_0 / Q2_K / IQ2_XXS matrices are regrouped into
+ * 8-block super-tiles of the same total size (see
+ * rsllm_hip_prepare_weights_dev).
  *
  * Thread safety: every entry point may be called from any thread. Process
  * state (device ordinal, registered weights) is guarded by a mutex; each
@@ -53,7 +54,7 @@ typedef enum rsllm_hip_status {
                                                 reference would panic on (row_len == 0 in
                                                 parallel.rs:44) */
     RSLLM_HIP_ERR_UNIMPLEMENTED = 10         /* dtype the reference accepts but this backend does
-                                                not implement yet (Q2_K, IQ2_XXS, Q4_1, Q5_K, Q8_K) */
+                                                not implement (dequant of Q4_1, Q5_K, Q8_K) */
 } rsllm_hip_status;
 
 /* GgmlType ids (rsllm-gguf/src/tensor.rs:26-85) used by this ABI. */
@@ -95,8 +96,9 @@ void rsllm_hip_capability_get(rsllm_hip_capability *out);
 /* matmul_quant_f32 (backend-cpu/src/ops/quant_matmul.rs:45-119).
  * out[t*out_dim + o] = sum_i deq(W)[o, i] * x[t*in_dim + i]; `out` is
  * overwritten. Validation order as :57-92: dtype, in_dim % block,
- * weights_len, x_len, out_len. Accepted dtypes: Q4_K, Q8_0, Q4_0, and Q6_K
- * (a deliberate superset: the reference's guard rejects Q6_K). `tier` is
+ * weights_len, x_len, out_len. Accepted dtypes: Q4_K, Q2_K, IQ2_XXS, Q4_0,
+ * Q8_0 (the reference's guard), and Q6_K (a deliberate superset: the
+ * reference's guard rejects Q6_K). `tier` is
  * accepted and ignored, as the reference ignores it (:55).
  * Weights are uploaded for this call unless the same (pointer, length,
  * dtype, in_dim) was registered with rsllm_hip_register_weights. */
@@ -140,13 +142,15 @@ int rsllm_hip_release_weights(void);
 
 /* GGUF rows -> device layout: `len` bytes holding whole rows of `in_dim`
  * elements (n = len / block_bytes blocks in matrix order, row-major over
- * (row, block)). Q4_K: unchanged (`dst` may equal `src`). Q6_K, Q8_0, Q4_0:
- * the blocks are regrouped into super-tiles of 8 consecutive blocks (the
- * last tile holds the n % 8 remaining blocks, r of them), each tile split
- * into field runs so that every field of every block is 16-byte aligned:
- *   Q6_K  [ql r*128 | qh r*64 | scales r*16 | d r*2]   (8 blocks: 1680 B)
- *   Q8_0  [qs r*32 | d r*2]                           (8 blocks: 272 B)
- *   Q4_0  [qs r*16 | d r*2]                           (8 blocks: 144 B)
+ * (row, block)). Q4_K: unchanged (`dst` may equal `src`). Q6_K, Q8_0, Q4_0,
+ * Q2_K, IQ2_XXS: the blocks are regrouped into super-tiles of 8 consecutive
+ * blocks (the last tile holds the n % 8 remaining blocks, r of them), each
+ * tile split into field runs so that every field of every block is aligned:
+ *   Q6_K    [ql r*128 | qh r*64 | scales r*16 | d r*2]   (8 blocks: 1680 B)
+ *   Q8_0    [qs r*32 | d r*2]                           (8 blocks: 272 B)
+ *   Q4_0    [qs r*16 | d r*2]                           (8 blocks: 144 B)
+ *   Q2_K    [qs r*64 | scales r*16 | (d, dmin) r*4]     (8 blocks: 672 B)
+ *   IQ2_XXS [qs r*64 | d r*2]                           (8 blocks: 528 B)
  * with r = 8 except in the last tile; tile S starts at byte
  * S * 8 * block_bytes. `dst` must not overlap `src`. Enqueued on `stream`. */
 int rsllm_hip_prepare_weights_dev(uint8_t *dst, const uint8_t *src, size_t len, uint32_t dtype,
@@ -254,7 +258,8 @@ int rsllm_hip_matmul_q8_0_batch_dev(float *out, size_t out_len, const uint8_t *w
 
 /* dequant_to_f32 (rsllm-gguf/src/dequant/mod.rs:69-85): decode `src` (GGUF
  * bytes) into dst[dst_len]. Bit-exact with the reference for F32, F16, BF16,
- * Q4_0, Q4_K, Q6_K, Q8_0. Size rule of q4_k.rs:36-49 (and siblings). */
+ * Q4_0, Q4_K, Q6_K, Q8_0, Q2_K, IQ2_XXS. Size rule of q4_k.rs:36-49 (and
+ * siblings). */
 int rsllm_hip_dequant_to_f32(uint32_t dtype, const uint8_t *src, size_t src_len, float *dst,
                              size_t dst_len);
 int rsllm_hip_dequant_to_f32_dev(uint32_t dtype, const uint8_t *src, size_t src_len, float *dst,

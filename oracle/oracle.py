@@ -65,6 +65,8 @@ def lib() -> ctypes.CDLL:
         L.orc_swiglu_clamp.restype = None
         L.orc_moe_routed.argtypes = [P, P, S, S, S, P, P, P, U32, U32, S, P, P, S, ctypes.c_float]
         L.orc_last_detail.argtypes = [P, P]
+        L.orc_iq2xxs_grid.argtypes = [I]
+        L.orc_iq2xxs_grid.restype = ctypes.c_uint64
         L.orc_num_cores.restype = I
         _lib = L
     return _lib
@@ -252,4 +254,50 @@ def np_dequant_q8_0(src: np.ndarray) -> np.ndarray:
     return (q * d).astype(np.float32).reshape(-1)
 
 
-NP_DEQUANT = {Q4_K: np_dequant_q4k, Q6_K: np_dequant_q6k, Q8_0: np_dequant_q8_0}
+def np_dequant_q2k(src: np.ndarray) -> np.ndarray:
+    """Q2_K from the block layout (q2_k.rs:9-31), vectorised: element e of a
+    block: sub-block e // 16, code at shift 2 ((e % 128) // 32) of qs byte
+    32 (e // 128) + e % 32; (d * sc) * q - dmin * m in float32."""
+    b = np.asarray(src, np.uint8).reshape(-1, 84)
+    d = b[:, 80:82].copy().view(np.float16).astype(np.float32)
+    dmin = b[:, 82:84].copy().view(np.float16).astype(np.float32)
+    e = np.arange(256)
+    sc = b[:, e // 16]
+    byte = b[:, 16 + 32 * (e // 128) + e % 32]
+    q = ((byte >> (2 * ((e % 128) // 32))) & 3).astype(np.float32)
+    dl = (d * (sc & 15).astype(np.float32)).astype(np.float32)
+    ml = (dmin * (sc >> 4).astype(np.float32)).astype(np.float32)
+    return ((dl * q).astype(np.float32) - ml).astype(np.float32).reshape(-1)
+
+
+def iq2xxs_grid() -> np.ndarray:
+    """The IQ2_XXS codebook as [256, 8] int8 (from the C restatement)."""
+    g = np.array([lib().orc_iq2xxs_grid(i) for i in range(256)], np.uint64)
+    return g.view(np.uint8).reshape(256, 8).view(np.int8)
+
+
+def np_dequant_iq2xxs(src: np.ndarray) -> np.ndarray:
+    """IQ2_XXS from the block layout (iq2_xxs.rs:12-33), vectorised; the sign
+    byte of index i is i with bit 7 = parity(i)."""
+    b = np.asarray(src, np.uint8).reshape(-1, 66)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    aux = b[:, 2:66].copy().view(np.uint32).reshape(-1, 8, 2)
+    grid = iq2xxs_grid().astype(np.float32)
+    out = np.empty((b.shape[0], 8, 4, 8), np.float32)
+    db = (d[:, None] * (np.float32(0.5) + (aux[:, :, 1] >> 28).astype(np.float32)) *
+          np.float32(0.25)).astype(np.float32)
+    for l in range(4):
+        gi = (aux[:, :, 0] >> (8 * l)) & 0xFF
+        si = (aux[:, :, 1] >> (7 * l)) & 0x7F
+        par = np.zeros_like(si)
+        for bit in range(7):
+            par ^= (si >> bit) & 1
+        signs = si | (par << 7)
+        neg = ((signs[:, :, None] >> np.arange(8)) & 1).astype(bool)
+        v = (db[:, :, None] * grid[gi]).astype(np.float32)
+        out[:, :, l, :] = np.where(neg, -v, v)
+    return out.reshape(-1)
+
+
+NP_DEQUANT = {Q4_K: np_dequant_q4k, Q6_K: np_dequant_q6k, Q8_0: np_dequant_q8_0,
+              Q2_K: np_dequant_q2k, IQ2_XXS: np_dequant_iq2xxs}

@@ -243,6 +243,98 @@ static int dequant_float(uint32_t t, const uint8_t *src, size_t src_len, float *
 }
 
 /* ---- dequant_to_f32: rsllm-gguf/src/dequant/mod.rs:69-85 ----------------- */
+/* Q2_K, rsllm-gguf/src/dequant/q2_k.rs:39-98: 84-byte blocks [scales 16 |
+ * qs 64 | d | dmin]; element e of a block uses sub-block e / 16 (scale nibble
+ * low, min nibble high) and 2-bit code (qs[32 (e / 128) + (e % 32)] >>
+ * 2 ((e % 128) / 32)) & 3; value (d * sc) * q - dmin * m, evaluated as the
+ * reference does: dl = d * sc, ml = dmin * m (both exact), dl * q (exact),
+ * then one rounding in the subtraction. */
+int orc_dequant_q2_k(const uint8_t *src, size_t src_len, float *dst, size_t n) {
+    int rc = check_blocks(src_len, n, 256, 84);
+    if (rc) return rc;
+    for (size_t b = 0; b < n / 256; b++) {
+        const uint8_t *blk = src + b * 84;
+        const float d = rd_f16(blk + 80), dmin = rd_f16(blk + 82);
+        for (int e = 0; e < 256; e++) {
+            const uint8_t sc = blk[e / 16];
+            const float dl = d * (float)(sc & 0x0F);
+            const float ml = dmin * (float)(sc >> 4);
+            const int q = (blk[16 + 32 * (e / 128) + (e % 32)] >> (2 * ((e % 128) / 32))) & 3;
+            dst[b * 256 + e] = dl * (float)q - ml;
+        }
+    }
+    return ORC_OK;
+}
+
+/* IQ2_XXS codebook (ggml's iq2xxs_grid, the GGUF format constant): entry i
+ * holds 8 bytes from {8, 25, 43}; stored here as base-3 numbers (byte j =
+ * digit j, 8 -> 0, 25 -> 1, 43 -> 2). */
+static const uint16_t kIq2Codes[256] = {
+       0,    2,    4,    6,    8,   10,   12,   18,   20,   24,   26,   28,   30,   36,   42,   46,
+      48,   54,   56,   62,   74,   82,   84,   90,   94,  108,  138,  150,  162,  164,  182,  218,
+     244,  246,  252,  262,  264,  270,  272,  276,  288,  298,  300,  306,  318,  324,  326,  330,
+     342,  356,  376,  378,  388,  412,  414,  432,  462,  480,  486,  490,  492,  498,  510,  514,
+     516,  522,  524,  546,  570,  594,  650,  660,  730,  732,  738,  748,  756,  774,  786,  792,
+     796,  810,  816,  828,  846,  854,  864,  912,  922,  972,  978,  990,  994, 1006, 1026, 1068,
+    1100, 1134, 1148, 1216, 1218, 1224, 1242, 1270, 1296, 1300, 1368, 1414, 1458, 1460, 1466, 1488,
+    1504, 1512, 1514, 1564, 1572, 1620, 1622, 1702, 1704, 1710, 1728, 1742, 1782, 1810, 1830, 1926,
+    1950, 1962, 2010, 2136, 2188, 2190, 2196, 2202, 2206, 2208, 2214, 2220, 2228, 2232, 2242, 2244,
+    2250, 2268, 2286, 2314, 2322, 2326, 2350, 2358, 2382, 2390, 2400, 2430, 2436, 2448, 2484, 2500,
+    2522, 2532, 2592, 2674, 2676, 2682, 2700, 2704, 2754, 2796, 2800, 2810, 2866, 2898, 2916, 2922,
+    2926, 2932, 2934, 2970, 2976, 3000, 3026, 3072, 3142, 3222, 3224, 3248, 3322, 3360, 3402, 3412,
+    3418, 3450, 3510, 3570, 3648, 3654, 3672, 3696, 3726, 3766, 3822, 3852, 3888, 3892, 3978, 3980,
+    4026, 4160, 4374, 4376, 4382, 4402, 4430, 4458, 4470, 4482, 4546, 4618, 4620, 4626, 4630, 4644,
+    4662, 4698, 4730, 4764, 4786, 4806, 4824, 4862, 4944, 5032, 5106, 5112, 5124, 5130, 5176, 5198,
+    5238, 5296, 5346, 5366, 5376, 5464, 5644, 5688, 5834, 5868, 5890, 5920, 5994, 6090, 6354, 6402,
+};
+
+static uint64_t iq2_grid_entry(int i) {
+    static const uint8_t val[3] = {8, 25, 43};
+    uint32_t c = kIq2Codes[i];
+    uint64_t v = 0;
+    for (int j = 0; j < 8; j++) {
+        v |= (uint64_t)val[c % 3] << (8 * j);
+        c /= 3;
+    }
+    return v;
+}
+
+uint64_t orc_iq2xxs_grid(int i) { return (i >= 0 && i < 256) ? iq2_grid_entry(i) : 0; }
+
+/* IQ2_XXS, rsllm-gguf/src/dequant/iq2_xxs.rs:47-113: 66-byte blocks [d |
+ * 8 sub-groups x (u32 grid indices, u32 signs/extra)]. Sub-group g: db = d *
+ * (0.5 + (aux1 >> 28)) * 0.25; element 8l + j = db * grid[aux0 byte l][j] *
+ * sign, negative when bit j of ksigns(aux1 >> 7l & 127) is set, where
+ * ksigns(i) = i with bit 7 = parity of i (the format's sign table). Every
+ * product is exact. */
+int orc_dequant_iq2_xxs(const uint8_t *src, size_t src_len, float *dst, size_t n) {
+    int rc = check_blocks(src_len, n, 256, 66);
+    if (rc) return rc;
+    for (size_t b = 0; b < n / 256; b++) {
+        const uint8_t *blk = src + b * 66;
+        const float d = rd_f16(blk);
+        for (int g = 0; g < 8; g++) {
+            const uint8_t *q = blk + 2 + 8 * g;
+            const uint32_t aux0 = (uint32_t)q[0] | (uint32_t)q[1] << 8 | (uint32_t)q[2] << 16 |
+                                  (uint32_t)q[3] << 24;
+            const uint32_t aux1 = (uint32_t)q[4] | (uint32_t)q[5] << 8 | (uint32_t)q[6] << 16 |
+                                  (uint32_t)q[7] << 24;
+            const float db = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
+            for (int l = 0; l < 4; l++) {
+                const uint64_t grid = iq2_grid_entry((aux0 >> (8 * l)) & 0xFF);
+                const uint32_t si = (aux1 >> (7 * l)) & 0x7F;
+                const uint32_t signs = si | ((uint32_t)__builtin_parity(si) << 7);
+                for (int j = 0; j < 8; j++) {
+                    const float gv = (float)(int8_t)(grid >> (8 * j));
+                    const float sg = (signs >> j) & 1 ? -1.0f : 1.0f;
+                    dst[b * 256 + 32 * g + 8 * l + j] = db * gv * sg;
+                }
+            }
+        }
+    }
+    return ORC_OK;
+}
+
 int orc_dequant_to_f32(uint32_t t, const uint8_t *src, size_t src_len, float *dst, size_t n) {
     switch (t) {
     case ORC_F32: case ORC_F16: case ORC_BF16: return dequant_float(t, src, src_len, dst, n);
@@ -250,6 +342,8 @@ int orc_dequant_to_f32(uint32_t t, const uint8_t *src, size_t src_len, float *ds
     case ORC_Q4_K: return orc_dequant_q4_k(src, src_len, dst, n);
     case ORC_Q6_K: return orc_dequant_q6_k(src, src_len, dst, n);
     case ORC_Q8_0: return orc_dequant_q8_0(src, src_len, dst, n);
+    case ORC_Q2_K: return orc_dequant_q2_k(src, src_len, dst, n);
+    case ORC_IQ2_XXS: return orc_dequant_iq2_xxs(src, src_len, dst, n);
     default: return fail2(ORC_UNSUPPORTED_DEQUANT, t, 0);
     }
 }

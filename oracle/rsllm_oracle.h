@@ -60,10 +60,16 @@ int orc_dequant_q4_k(const uint8_t *src, size_t src_len, float *dst, size_t n);
 int orc_dequant_q6_k(const uint8_t *src, size_t src_len, float *dst, size_t n);
 int orc_dequant_q8_0(const uint8_t *src, size_t src_len, float *dst, size_t n);
 int orc_dequant_q4_0(const uint8_t *src, size_t src_len, float *dst, size_t n);
+/* dequant_q2_k     rsllm-gguf/src/dequant/q2_k.rs:39-98
+ * dequant_iq2_xxs  rsllm-gguf/src/dequant/iq2_xxs.rs:47-113 (codebook
+ * iq2_xxs/tables.rs; orc_iq2xxs_grid(i) returns entry i as a u64) */
+int orc_dequant_q2_k(const uint8_t *src, size_t src_len, float *dst, size_t n);
+int orc_dequant_iq2_xxs(const uint8_t *src, size_t src_len, float *dst, size_t n);
+uint64_t orc_iq2xxs_grid(int i);
 
 /* dequant_to_f32, rsllm-gguf/src/dequant/mod.rs:69-85 (the arms restated
- * here: F32, F16, BF16, Q4_0, Q4_K, Q6_K, Q8_0; the rest report
- * ORC_UNSUPPORTED_DEQUANT). */
+ * here: F32, F16, BF16, Q4_0, Q4_K, Q6_K, Q8_0, Q2_K, IQ2_XXS; the rest
+ * report ORC_UNSUPPORTED_DEQUANT). */
 int orc_dequant_to_f32(uint32_t dtype, const uint8_t *src, size_t src_len, float *dst, size_t n);
 
 /* matmul_quant_f32, rsllm-backend-cpu/src/ops/quant_matmul.rs:45-119.

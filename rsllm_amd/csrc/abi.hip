@@ -111,7 +111,10 @@ bool matmul_dtype_known(uint32_t t) {
     return t == T_Q4_K || t == T_Q2_K || t == T_IQ2_XXS || t == T_Q4_0 || t == T_Q8_0 ||
            t == T_Q6_K;
 }
-bool matmul_dtype_impl(uint32_t t) { return t == T_Q4_K || t == T_Q8_0 || t == T_Q4_0 || t == T_Q6_K; }
+bool matmul_dtype_impl(uint32_t t) {
+    return t == T_Q4_K || t == T_Q8_0 || t == T_Q4_0 || t == T_Q6_K || t == T_Q2_K ||
+           t == T_IQ2_XXS;
+}
 
 // Shared validation of matmul_quant_f32 (quant_matmul.rs:57-92), then the
 // parallel.rs:44 row_len > 0 assertion.
@@ -167,9 +170,10 @@ const char *ggml_name(uint32_t t) {
 int validate_dequant(uint32_t dtype, const void *src, size_t src_len, const void *dst,
                      size_t dst_len) {
     const bool impl = dtype == T_F32 || dtype == T_F16 || dtype == T_BF16 || dtype == T_Q4_0 ||
-                      dtype == T_Q4_K || dtype == T_Q6_K || dtype == T_Q8_0;
+                      dtype == T_Q4_K || dtype == T_Q6_K || dtype == T_Q8_0 || dtype == T_Q2_K ||
+                      dtype == T_IQ2_XXS;
     const bool ref_decodable = impl || dtype == 3 /*Q4_1*/ || dtype == 13 /*Q5_K*/ ||
-                               dtype == T_Q2_K || dtype == 15 /*Q8_K*/ || dtype == T_IQ2_XXS;
+                               dtype == 15 /*Q8_K*/;
     if (!ref_decodable) {
         std::string m = std::string("dtype `") + ggml_name(dtype) +
                         "` is not yet supported for dequantization in this build";
@@ -235,8 +239,8 @@ void rsllm_hip_capability_get(rsllm_hip_capability *out) {
     out->q4k_matmul = 1;
     out->q6k_matmul = 1;
     out->q8_0_matmul = 1;
-    out->q2k_matmul = 0;
-    out->iq2xxs_matmul = 0;
+    out->q2k_matmul = 1;
+    out->iq2xxs_matmul = 1;
     out->fp8_kv_cache = 0;
 }
 

@@ -4,9 +4,11 @@
 //
 // Bit-exactness: every product in the reference formulas is exact in f32
 // (Q4_K: d*sc <= 17 significant bits, times q <= 4 bits; Q6_K:
-// d*sc*(q-32) <= 23 bits; Q8_0/Q4_0: <= 18 bits), so the only rounding is
-// Q4_K's final subtraction. Contraction is switched off anyway so each line
+// d*sc*(q-32) <= 23 bits; Q8_0/Q4_0: <= 18 bits; Q2_K: d*sc <= 15 bits,
+// times q <= 2; IQ2_XXS: d*(0.5+e)*0.25 <= 16 bits, times the grid byte
+// <= 6), so the only roundings are the final subtractions of Q4_K and Q2_K. Contraction is switched off anyway so each line
 // is evaluated exactly as written.
+#include "iq2xxs_grid.h"
 #include "kernels.h"
 
 namespace rsllm_hip {
@@ -127,12 +129,14 @@ __global__ __launch_bounds__(256) void k_dequant_float(const uint8_t *__restrict
 
 // ---- device layout ---------------------------------------------------------
 // Q4_K: GGUF bytes unchanged (144-byte blocks and rows are 16-byte aligned).
-// Q6_K, Q8_0, Q4_0: blocks are taken 8 at a time in matrix order (row-major
+// Q6_K, Q8_0, Q4_0, Q2_K, IQ2_XXS: blocks are taken 8 at a time in matrix order (row-major
 // over (row, block)) and each group of r <= 8 blocks becomes one contiguous
 // super-tile with the fields split out:
 //   Q6_K [ql r*128 | qh r*64 | scales r*16 | d r*2]   (8 blocks = 1680 B)
 //   Q8_0 [qs r*32 | d r*2]                             (8 blocks =  272 B)
 //   Q4_0 [qs r*16 | d r*2]                             (8 blocks =  144 B)
+//   Q2_K [qs r*64 | scales r*16 | (d, dmin) r*4]       (8 blocks =  672 B)
+//   IQ2_XXS [qs r*64 | d r*2]                          (8 blocks =  528 B)
 // r = 8 except in the last super-tile of the matrix. The total size equals
 // the GGUF size, every field offset is a multiple of 16 (2 for d), and a
 // wavefront reading 8 consecutive blocks reads one contiguous region.
@@ -172,6 +176,95 @@ __global__ __launch_bounds__(256) void k_prepare_q8_0(const uint8_t *__restrict_
     dd[0] = s[0];
 }
 
+// One thread per (block, 16-element sub-block s): q2_k.rs:62-94. Element
+// 16s + l (l < 16) of the block: code at shift 2 ((16s % 128) / 32) of qs
+// byte 32 (s / 8) + 16 (s & 1) + l; dl = d * sc, ml = dmin * m.
+__global__ __launch_bounds__(256) void k_dequant_q2k(const uint8_t *__restrict__ src,
+                                                     float *__restrict__ dst, size_t n_blocks) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= n_blocks * 16) return;
+    const size_t b = gid >> 4;
+    const int sb = (int)(gid & 15);
+    const uint8_t *blk = src + b * 84;
+    const float d = f16_to_f32(blk[80] | (blk[81] << 8));
+    const float dmin = f16_to_f32(blk[82] | (blk[83] << 8));
+    const uint32_t sc = blk[sb];
+    const float dl = d * (float)(sc & 15u);
+    const float ml = dmin * (float)(sc >> 4);
+    const uint8_t *q = blk + 16 + 32 * (sb >> 3) + 16 * (sb & 1);
+    const int shift = 2 * ((sb & 7) >> 1);
+    float *o = dst + b * 256 + 16 * sb;
+    for (int l = 0; l < 16; l += 4) {
+        float4 v;
+        v.x = dl * (float)((q[l + 0] >> shift) & 3) - ml;
+        v.y = dl * (float)((q[l + 1] >> shift) & 3) - ml;
+        v.z = dl * (float)((q[l + 2] >> shift) & 3) - ml;
+        v.w = dl * (float)((q[l + 3] >> shift) & 3) - ml;
+        *reinterpret_cast<float4 *>(o + l) = v;
+    }
+}
+
+// One thread per (block, sub-group g, slot l): iq2_xxs.rs:66-111. Eight
+// elements db * grid_byte * sign, db = d * (0.5 + extra) * 0.25.
+__global__ __launch_bounds__(256) void k_dequant_iq2xxs(const uint8_t *__restrict__ src,
+                                                        float *__restrict__ dst,
+                                                        size_t n_blocks) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= n_blocks * 32) return;
+    const size_t b = gid >> 5;
+    const int g = (int)((gid >> 2) & 7), l = (int)(gid & 3);
+    const uint8_t *blk = src + b * 66;
+    const float d = f16_to_f32(blk[0] | (blk[1] << 8));
+    const uint8_t *q = blk + 2 + 8 * g;
+    const uint32_t aux1 = q[4] | (q[5] << 8) | (q[6] << 16) | ((uint32_t)q[7] << 24);
+    const float db = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
+    const uint64_t grid = kIq2Grid.v[q[l]];
+    const uint32_t signs = iq2_signs((aux1 >> (7 * l)) & 0x7Fu);
+    float r[8];
+    for (int j = 0; j < 8; j++) {
+        const float gv = (float)(int)(int8_t)(grid >> (8 * j));
+        const float sg = ((signs >> j) & 1u) ? -1.0f : 1.0f;
+        r[j] = db * gv * sg;
+    }
+    float *o = dst + b * 256 + 32 * g + 8 * l;
+    *reinterpret_cast<float4 *>(o) = make_float4(r[0], r[1], r[2], r[3]);
+    *reinterpret_cast<float4 *>(o + 4) = make_float4(r[4], r[5], r[6], r[7]);
+}
+
+// Q2_K (84-byte blocks, 4-byte aligned) -> super-tile [qs r*64 | scales r*16 |
+// (d, dmin) r*4].
+__global__ __launch_bounds__(256) void k_prepare_q2k(const uint8_t *__restrict__ src,
+                                                     uint8_t *__restrict__ dst, size_t n_blocks) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_blocks) return;
+    const size_t S = i >> 3, j = i & 7;
+    const size_t r = (S < (n_blocks >> 3)) ? 8 : (n_blocks & 7);
+    uint8_t *st = dst + S * 8 * 84;
+    const uint32_t *s = reinterpret_cast<const uint32_t *>(src + i * 84);
+    uint32_t *qs = reinterpret_cast<uint32_t *>(st + j * 64);
+    uint32_t *sc = reinterpret_cast<uint32_t *>(st + r * 64 + j * 16);
+    uint32_t *dd = reinterpret_cast<uint32_t *>(st + r * 80 + j * 4);
+    for (int k = 0; k < 16; k++) qs[k] = s[4 + k];
+    for (int k = 0; k < 4; k++) sc[k] = s[k];
+    dd[0] = s[20];
+}
+
+// IQ2_XXS (66-byte blocks, 2-byte aligned) -> super-tile [qs r*64 | d r*2].
+__global__ __launch_bounds__(256) void k_prepare_iq2xxs(const uint8_t *__restrict__ src,
+                                                        uint8_t *__restrict__ dst,
+                                                        size_t n_blocks) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_blocks) return;
+    const size_t S = i >> 3, j = i & 7;
+    const size_t r = (S < (n_blocks >> 3)) ? 8 : (n_blocks & 7);
+    uint8_t *st = dst + S * 8 * 66;
+    const uint16_t *s = reinterpret_cast<const uint16_t *>(src + i * 66);
+    uint16_t *qs = reinterpret_cast<uint16_t *>(st + j * 64);
+    uint16_t *dd = reinterpret_cast<uint16_t *>(st + r * 64 + j * 2);
+    for (int k = 0; k < 32; k++) qs[k] = s[1 + k];
+    dd[0] = s[0];
+}
+
 static inline unsigned grid_for(size_t n, unsigned bs) { return (unsigned)((n + bs - 1) / bs); }
 
 hipError_t launch_dequant(uint32_t dtype, const uint8_t *src, float *dst, size_t n_elems,
@@ -189,6 +282,13 @@ hipError_t launch_dequant(uint32_t dtype, const uint8_t *src, float *dst, size_t
         break;
     case T_Q4_0:
         k_dequant_q4_0<<<grid_for(n_elems / 32, 256), 256, 0, s>>>(src, dst, n_elems / 32);
+        break;
+    case T_Q2_K:
+        k_dequant_q2k<<<grid_for(n_elems / 256 * 16, 256), 256, 0, s>>>(src, dst, n_elems / 256);
+        break;
+    case T_IQ2_XXS:
+        k_dequant_iq2xxs<<<grid_for(n_elems / 256 * 32, 256), 256, 0, s>>>(src, dst,
+                                                                         n_elems / 256);
         break;
     case T_F32:
     case T_F16:
@@ -218,6 +318,12 @@ hipError_t launch_prepare(uint32_t dtype, const uint8_t *src, uint8_t *dst, size
         break;
     case T_Q4_0:
         k_prepare_q8_0<<<grid_for(n_blocks, 256), 256, 0, s>>>(src, dst, n_blocks, 18);
+        break;
+    case T_Q2_K:
+        k_prepare_q2k<<<grid_for(n_blocks, 256), 256, 0, s>>>(src, dst, n_blocks);
+        break;
+    case T_IQ2_XXS:
+        k_prepare_iq2xxs<<<grid_for(n_blocks, 256), 256, 0, s>>>(src, dst, n_blocks);
         break;
     default:
         return hipErrorInvalidValue;

@@ -27,6 +27,7 @@
 // per-row partials through LDS. Weight loads are raw buffer loads, and the
 // activation limbs are stored lane-major by the pre-pass so a wavefront's
 // activation loads are contiguous 1 KB reads as well.
+#include "iq2xxs_grid.h"
 #include "kernels.h"
 
 namespace rsllm_hip {
@@ -198,6 +199,108 @@ struct FQ8 {
         }
         const uint32_t q[4] = {s.q.x, s.q.y, s.q.z, s.q.w};
         return d * ((float)dot16_limbs(q, x.hlo, x.llo) * __uint_as_float(x.meta.x));
+    }
+};
+
+// Q2_K, super-tile layout [qs 8x64 | scales 8x16 | (d, dmin) 8x4]. Lane (ks, k)
+// of column c reads block u = 8c + ks: qs bytes 16 (k / 2) .. + 15 (half h = k / 4,
+// run r = (k / 2) & 1) and takes the 2-bit codes at shifts 4p and 4p + 2
+// (p = k & 1): elements 128h + 64p + 16r + 0..15 (group "lo", sub-block
+// 8h + 4p + r) and the same + 32 (group "hi", sub-block + 2), as
+// dequant_q2_k's element order (q2_k.rs:62-94) gives.
+struct FQ2K {
+    static constexpr int kEPU = 256, kXF = 5;
+    struct Slice {
+        uint4 qs, sc;
+        uint32_t dd;
+    };
+    __device__ static int units(int in_dim) { return in_dim >> 8; }
+    __device__ static int elem_lo(int unit, int k) {
+        return unit * 256 + 128 * (k >> 2) + 64 * (k & 1) + 16 * ((k >> 1) & 1);
+    }
+    __device__ static int elem_hi(int unit, int k) { return elem_lo(unit, k) + 32; }
+    __device__ static bool valid(int unit, int, int in_dim) { return unit < (in_dim >> 8); }
+    __device__ static void load(Slice &s, __amdgpu_buffer_rsrc_t r, int row, int unit, int k,
+                                int in_dim, int out_dim) {
+        const uint32_t nb = (uint32_t)(in_dim >> 8);
+        const uint32_t nblk = (uint32_t)out_dim * nb;
+        const uint32_t bi = (uint32_t)row * nb + (uint32_t)unit;
+        const uint32_t S = bi >> 3, j = bi & 7;
+        const uint32_t rS = (S < (nblk >> 3)) ? 8u : (nblk & 7u);
+        const uint32_t base = S * 672u;
+        s.qs = bload16(r, base + j * 64u + 16u * (uint32_t)(k >> 1), 0);
+        s.sc = bload16(r, base + rS * 64u + j * 16u, 0);
+        s.dd = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)(base + rS * 80u + j * 4u), 0, 0);
+    }
+    __device__ static float dot(const Slice &s, int k, const XSlice &x) {
+        const float d = f16_to_f32(s.dd & 0xFFFFu), dmin = f16_to_f32(s.dd >> 16);
+        const int sub = 8 * (k >> 2) + 4 * (k & 1) + ((k >> 1) & 1);
+        const uint32_t sl = (uint32_t)sbyte16(s.sc, sub) & 0xFFu;
+        const uint32_t sh = (uint32_t)sbyte16(s.sc, sub + 2) & 0xFFu;
+        const float dl = d * (float)(sl & 15u), ml = dmin * (float)(sl >> 4);
+        const float dh = d * (float)(sh & 15u), mh = dmin * (float)(sh >> 4);
+        const uint32_t shl = 4u * (uint32_t)(k & 1), shh = shl + 2u;
+        const uint32_t lo[4] = {(s.qs.x >> shl) & 0x03030303u, (s.qs.y >> shl) & 0x03030303u,
+                                (s.qs.z >> shl) & 0x03030303u, (s.qs.w >> shl) & 0x03030303u};
+        const uint32_t hi[4] = {(s.qs.x >> shh) & 0x03030303u, (s.qs.y >> shh) & 0x03030303u,
+                                (s.qs.z >> shh) & 0x03030303u, (s.qs.w >> shh) & 0x03030303u};
+        const float plo = (float)dot16_limbs(lo, x.hlo, x.llo) * __uint_as_float(x.meta.x);
+        const float phi = (float)dot16_limbs(hi, x.hhi, x.lhi) * __uint_as_float(x.meta.z);
+        return dl * plo - ml * __uint_as_float(x.meta.y) + dh * phi - mh * __uint_as_float(x.meta.w);
+    }
+};
+
+// Four sign bits (bytes 0..3) applied to four positive int8 magnitudes: each
+// flagged byte becomes its two's complement; no byte is 0, so the +1 never
+// carries into the next byte.
+__device__ __forceinline__ uint32_t iq2_apply_signs(uint32_t mag, uint32_t bits4) {
+    const uint32_t one = (bits4 * 0x00204081u) & 0x01010101u;  // bit i -> byte i
+    const uint32_t m = (one << 8) - one;                       // 0xFF per flagged byte
+    return (mag ^ m) + one;
+}
+
+// IQ2_XXS, super-tile layout [qs 8x64 | d 8x2]. Lane (ks, k) of column c reads
+// sub-group k (8 bytes) of block u = 8c + ks: elements 32k + 0..15 (grid slots
+// 0, 1: group "lo") and 32k + 16..31 (slots 2, 3: "hi"), each an exact int8
+// +-{8, 25, 43} (iq2_xxs.rs:66-111); the sub-group scale
+// db = d * (0.5 + extra) * 0.25 multiplies the whole slice.
+struct FIQ2XXS {
+    static constexpr int kEPU = 256, kXF = 5;
+    struct Slice {
+        uint32_t a0, a1, d;
+    };
+    __device__ static int units(int in_dim) { return in_dim >> 8; }
+    __device__ static int elem_lo(int unit, int k) { return unit * 256 + 32 * k; }
+    __device__ static int elem_hi(int unit, int k) { return elem_lo(unit, k) + 16; }
+    __device__ static bool valid(int unit, int, int in_dim) { return unit < (in_dim >> 8); }
+    __device__ static void load(Slice &s, __amdgpu_buffer_rsrc_t r, int row, int unit, int k,
+                                int in_dim, int out_dim) {
+        const uint32_t nb = (uint32_t)(in_dim >> 8);
+        const uint32_t nblk = (uint32_t)out_dim * nb;
+        const uint32_t bi = (uint32_t)row * nb + (uint32_t)unit;
+        const uint32_t S = bi >> 3, j = bi & 7;
+        const uint32_t rS = (S < (nblk >> 3)) ? 8u : (nblk & 7u);
+        const uint32_t base = S * 528u;
+        const uint32_t off = base + j * 64u + 8u * (uint32_t)k;
+        s.a0 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+        s.a1 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)(off + 4u), 0, 0);
+        s.d = bload2(r, base + rS * 64u + j * 2u, 0);
+    }
+    __device__ static float dot(const Slice &s, int, const XSlice &x) {
+        const float db = f16_to_f32(s.d) * (0.5f + (float)(s.a1 >> 28)) * 0.25f;
+        uint32_t w[8];
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            const uint64_t g = kIq2Grid.v[(s.a0 >> (8 * l)) & 0xFFu];
+            const uint32_t sg = iq2_signs((s.a1 >> (7 * l)) & 0x7Fu);
+            w[2 * l] = iq2_apply_signs((uint32_t)g, sg & 15u);
+            w[2 * l + 1] = iq2_apply_signs((uint32_t)(g >> 32), sg >> 4);
+        }
+        const uint32_t lo[4] = {w[0], w[1], w[2], w[3]};
+        const uint32_t hi[4] = {w[4], w[5], w[6], w[7]};
+        const float plo = (float)dot16_limbs(lo, x.hlo, x.llo) * __uint_as_float(x.meta.x);
+        const float phi = (float)dot16_limbs(hi, x.hhi, x.lhi) * __uint_as_float(x.meta.z);
+        return db * (plo + phi);
     }
 };
 
@@ -692,6 +795,8 @@ hipError_t launch_gemv_grouped(uint32_t dtype, const uint8_t *w0, const uint8_t 
     case T_Q6_K: return grouped<FQ6K>(a, grid_experts, n_mat, s);
     case T_Q8_0: return grouped<FQ8<false>>(a, grid_experts, n_mat, s);
     case T_Q4_0: return grouped<FQ8<true>>(a, grid_experts, n_mat, s);
+    case T_Q2_K: return grouped<FQ2K>(a, grid_experts, n_mat, s);
+    case T_IQ2_XXS: return grouped<FIQ2XXS>(a, grid_experts, n_mat, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -720,6 +825,8 @@ size_t gemv_scratch_bytes(uint32_t dtype, int n_tok, int in_dim) {
     case T_Q6_K: return xq_bytes_for<FQ6K>(n_tok, in_dim);
     case T_Q8_0: return xq_bytes_for<FQ8<false>>(n_tok, in_dim);
     case T_Q4_0: return xq_bytes_for<FQ8<true>>(n_tok, in_dim);
+    case T_Q2_K: return xq_bytes_for<FQ2K>(n_tok, in_dim);
+    case T_IQ2_XXS: return xq_bytes_for<FIQ2XXS>(n_tok, in_dim);
     default: return 0;
     }
 }
@@ -770,6 +877,8 @@ hipError_t launch_quantize_x(uint32_t dtype, const float *x, uint8_t *xq, int n_
     case T_Q6_K: return quantize<FQ6K>(x, xq, n_tok, in_dim, s);
     case T_Q8_0: return quantize<FQ8<false>>(x, xq, n_tok, in_dim, s);
     case T_Q4_0: return quantize<FQ8<true>>(x, xq, n_tok, in_dim, s);
+    case T_Q2_K: return quantize<FQ2K>(x, xq, n_tok, in_dim, s);
+    case T_IQ2_XXS: return quantize<FIQ2XXS>(x, xq, n_tok, in_dim, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -793,6 +902,8 @@ hipError_t launch_quantize_swiglu(uint32_t dtype, const float *hg, const float *
     case T_Q6_K: return quantize_swiglu<FQ6K>(hg, hu, clamp, xq, n_rows, n, off, n_expert, s);
     case T_Q8_0: return quantize_swiglu<FQ8<false>>(hg, hu, clamp, xq, n_rows, n, off, n_expert, s);
     case T_Q4_0: return quantize_swiglu<FQ8<true>>(hg, hu, clamp, xq, n_rows, n, off, n_expert, s);
+    case T_Q2_K: return quantize_swiglu<FQ2K>(hg, hu, clamp, xq, n_rows, n, off, n_expert, s);
+    case T_IQ2_XXS: return quantize_swiglu<FIQ2XXS>(hg, hu, clamp, xq, n_rows, n, off, n_expert, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -806,6 +917,8 @@ hipError_t launch_gemv_prequant(uint32_t dtype, const uint8_t *w, size_t w_bytes
     case T_Q6_K: return gemv_pre<FQ6K>(w, w_bytes, xq, y, n_tok, in_dim, out_dim, s);
     case T_Q8_0: return gemv_pre<FQ8<false>>(w, w_bytes, xq, y, n_tok, in_dim, out_dim, s);
     case T_Q4_0: return gemv_pre<FQ8<true>>(w, w_bytes, xq, y, n_tok, in_dim, out_dim, s);
+    case T_Q2_K: return gemv_pre<FQ2K>(w, w_bytes, xq, y, n_tok, in_dim, out_dim, s);
+    case T_IQ2_XXS: return gemv_pre<FIQ2XXS>(w, w_bytes, xq, y, n_tok, in_dim, out_dim, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -835,6 +948,8 @@ static bool gemv1_fits(uint32_t dtype, int in_dim) {
     case T_Q6_K: return gemv1_lds_bytes<FQ6K>(in_dim) <= kGemv1MaxLds;
     case T_Q8_0: return gemv1_lds_bytes<FQ8<false>>(in_dim) <= kGemv1MaxLds;
     case T_Q4_0: return gemv1_lds_bytes<FQ8<true>>(in_dim) <= kGemv1MaxLds;
+    case T_Q2_K: return gemv1_lds_bytes<FQ2K>(in_dim) <= kGemv1MaxLds;
+    case T_IQ2_XXS: return gemv1_lds_bytes<FIQ2XXS>(in_dim) <= kGemv1MaxLds;
     default: return false;
     }
 }
@@ -851,6 +966,8 @@ hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const f
         case T_Q6_K: return gemv1<FQ6K>(w, w_bytes, x, y, in_dim, out_dim, s);
         case T_Q8_0: return gemv1<FQ8<false>>(w, w_bytes, x, y, in_dim, out_dim, s);
         case T_Q4_0: return gemv1<FQ8<true>>(w, w_bytes, x, y, in_dim, out_dim, s);
+        case T_Q2_K: return gemv1<FQ2K>(w, w_bytes, x, y, in_dim, out_dim, s);
+        case T_IQ2_XXS: return gemv1<FIQ2XXS>(w, w_bytes, x, y, in_dim, out_dim, s);
         default: return hipErrorInvalidValue;
         }
     }

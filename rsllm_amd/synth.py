@@ -84,8 +84,25 @@ def q4_0_blocks(g: np.random.Generator, n_blocks: int) -> np.ndarray:
     return out
 
 
+def q2k_blocks(g: np.random.Generator, n_blocks: int) -> np.ndarray:
+    """[n_blocks, 84] uint8 Q2_K blocks: 16 scale bytes (4-bit scale, 4-bit
+    min) and 64 qs bytes uniform; d, dmin = f16(|N(0, 1e-3)|)."""
+    out = g.integers(0, 256, size=(n_blocks, 84), dtype=np.uint8)
+    out[:, 80:82] = _f16_abs_normal(g, n_blocks, 1e-3).view(np.uint8).reshape(n_blocks, 2)
+    out[:, 82:84] = _f16_abs_normal(g, n_blocks, 1e-3).view(np.uint8).reshape(n_blocks, 2)
+    return out
+
+
+def iq2xxs_blocks(g: np.random.Generator, n_blocks: int) -> np.ndarray:
+    """[n_blocks, 66] uint8 IQ2_XXS blocks: d = f16(|N(0, 1e-3)|), grid
+    indices, 7-bit sign indices and 4-bit extras uniform."""
+    out = g.integers(0, 256, size=(n_blocks, 66), dtype=np.uint8)
+    out[:, 0:2] = _f16_abs_normal(g, n_blocks, 1e-3).view(np.uint8).reshape(n_blocks, 2)
+    return out
+
+
 _BLOCKS = {GgmlType.Q4_K: q4k_blocks, GgmlType.Q6_K: q6k_blocks, GgmlType.Q8_0: q8_0_blocks,
-           GgmlType.Q4_0: q4_0_blocks}
+           GgmlType.Q4_0: q4_0_blocks, GgmlType.Q2_K: q2k_blocks, GgmlType.IQ2_XXS: iq2xxs_blocks}
 
 
 def weight(dtype: GgmlType, out_dim: int, in_dim: int, seed: int) -> np.ndarray:

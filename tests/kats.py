@@ -14,6 +14,7 @@ from __future__ import annotations
 import numpy as np
 
 Q4_0, Q8_0, Q4_K, Q6_K, F32, F16, BF16, Q3_K = 2, 8, 12, 14, 0, 1, 30, 11
+Q2_K, IQ2_XXS = 10, 16
 DEQUANT_SIZE_MISMATCH, UNSUPPORTED_DEQUANT = 5, 6
 
 
@@ -85,6 +86,33 @@ def pack_q4_0_row(x: np.ndarray) -> np.ndarray:
         q = np.clip(np.floor(blk * idv + np.float32(8.5)).astype(np.int32), 0, 15).astype(np.uint8)
         out.append(np.concatenate([np.frombuffer(f16_bytes(d), np.uint8),
                                    (q[0:16] | (q[16:32] << 4)).astype(np.uint8)]))
+    return np.concatenate(out)
+
+
+def pack_q2k(d, dmin, sc, m, q2) -> np.ndarray:
+    """Inverse of the Q2_K decoder (the reference's pack_block, q2_k.rs:111-162):
+    scales[j] = m_j << 4 | sc_j; element e = 128h + 32k + l (l < 32) is the
+    2-bit field at shift 2k of qs[32h + l]; d, dmin at bytes 80, 82."""
+    out = np.zeros(84, np.uint8)
+    for j in range(16):
+        out[j] = ((m[j] & 15) << 4) | (sc[j] & 15)
+    for e in range(256):
+        h, k, l = e // 128, (e % 128) // 32, e % 32
+        out[16 + 32 * h + l] |= (int(q2[e]) & 3) << (2 * k)
+    out[80:82] = np.frombuffer(f16_bytes(d), np.uint8)
+    out[82:84] = np.frombuffer(f16_bytes(dmin), np.uint8)
+    return out
+
+
+def pack_iq2xxs(d, grids, signs, extras) -> np.ndarray:
+    """Inverse of the IQ2_XXS decoder (the reference's pack_block,
+    iq2_xxs.rs:131-157): per sub-group, u32 of 4 grid indices, then u32 of
+    4 7-bit sign indices (bits 7l..7l+6) and the 4-bit extra in bits 28-31."""
+    out = [np.frombuffer(f16_bytes(d), np.uint8)]
+    for g in range(8):
+        a0 = sum(int(grids[g][l]) << (8 * l) for l in range(4))
+        a1 = sum(int(signs[g][l]) << (7 * l) for l in range(4)) | (int(extras[g]) << 28)
+        out.append(np.frombuffer(np.array([a0, a1], np.uint32).tobytes(), np.uint8))
     return np.concatenate(out)
 
 
@@ -183,6 +211,68 @@ def dequant_kats():
               _close([2.0 if i % 2 == 0 else -2.0 for i in range(32)], 1e-3)))
     k.append(("fake_llama_q4_0", Q4_0, pack_q4_0(1.0, [i % 16 for i in range(32)]), 32,
               _close([(i % 16) - 8.0 for i in range(32)], 1e-3)))
+    # q2_k.rs:171-189 zero_quants_yields_minus_min_per_sub_block
+    m16 = list(range(16))
+    k.append(("q2k_zero_quants_minus_min", Q2_K, pack_q2k(1.0, 1.0, [0] * 16, m16, [0] * 256), 256,
+              _close(np.repeat(-np.array(m16, np.float32), 16), 1e-3)))
+    # q2_k.rs:192-211 distinct_per_sub_block_scales
+    k.append(("q2k_distinct_sub_block_scales", Q2_K, pack_q2k(1.0, 0.0, m16, [0] * 16, [1] * 256),
+              256, _close(np.repeat(np.array(m16, np.float32), 16), 1e-2)))
+    # q2_k.rs:214-232 full_2bit_range_with_offset
+    q2 = [i % 4 for i in range(256)]
+    k.append(("q2k_full_2bit_range_with_offset", Q2_K, pack_q2k(0.5, 0.25, [4] * 16, [2] * 16, q2),
+              256, _close(2.0 * np.array(q2, np.float32) - 0.5, 1e-2)))
+    # q2_k.rs:235-262 distinct_sc_and_m_combined
+    sc = [(j % 4) + 1 for j in range(16)]
+    mm = [((15 - j) % 4) + 1 for j in range(16)]
+    k.append(("q2k_distinct_sc_and_m_combined", Q2_K, pack_q2k(1.0, 1.0, sc, mm, [2] * 256), 256,
+              _close(np.repeat(2.0 * np.array(sc, np.float32) - np.array(mm, np.float32), 16),
+                     1e-3)))
+    # q2_k.rs:265-272 wrong_src_size_errors; dequant/mod.rs:273-289 dispatch arm
+    k.append(("q2k_wrong_src_size", Q2_K, np.zeros(83, np.uint8), 256,
+              _status(DEQUANT_SIZE_MISMATCH)))
+    blk = np.concatenate([np.full(16, 3, np.uint8), np.full(64, 0x55, np.uint8),
+                          np.frombuffer(f16_bytes(1.0) + f16_bytes(0.0), np.uint8)])
+    k.append(("q2k_dispatch_arm", Q2_K, blk, 256, _close(np.full(256, 3.0), 1e-2)))
+    # iq2_xxs.rs:188-198 zero_grid_yields_zero
+    z4 = [[0] * 4 for _ in range(8)]
+    k.append(("iq2xxs_zero_d", IQ2_XXS, pack_iq2xxs(0.0, z4, z4, [0] * 8), 256,
+              _close(np.zeros(256), 1e-3)))
+    # iq2_xxs.rs:200-212 uniform_pattern_uniform_output
+    k.append(("iq2xxs_uniform", IQ2_XXS, pack_iq2xxs(1.0, z4, z4, [0] * 8), 256,
+              _close(np.ones(256), 1e-3)))
+    # iq2_xxs.rs:214-233 extras_scale_subgroups_independently
+    k.append(("iq2xxs_extras", IQ2_XXS, pack_iq2xxs(1.0, z4, z4, list(range(8))), 256,
+              _close(np.repeat(1.0 + 2.0 * np.arange(8), 32), 1e-3)))
+    # iq2_xxs.rs:235-246 signs_flip_negate_elements
+    k.append(("iq2xxs_all_signs", IQ2_XXS, pack_iq2xxs(1.0, z4, [[127] * 4] * 8, [0] * 8), 256,
+              _close(-np.ones(256), 1e-3)))
+    # iq2_xxs.rs:248-329 distinct_l_slots_within_one_subgroup
+    g = [[0, 1, 2, 3]] + [[0] * 4] * 7
+    want = np.ones(256, np.float32)
+    want[0:8] = 1.0
+    want[8:16] = [-5.375, 1, 1, 1, 1, 1, 1, -1.0]
+    want[16:24] = [3.125, -3.125, 1, 1, 1, 1, 1, -1.0]
+    want[24:32] = [-1.0, -5.375, 1, 1, 1, 1, 1, 1]
+    k.append(("iq2xxs_distinct_l_slots", IQ2_XXS, pack_iq2xxs(1.0, g, g, [0] * 8), 256,
+              _close(want, 1e-3)))
+    # iq2_xxs.rs:331-389 distinct_subgroups_with_distinct_grids_and_extras
+    want = np.ones(256, np.float32)
+    for l in range(4):
+        want[32 + 8 * l:32 + 8 * l + 8] = [16.125] + [3.0] * 7
+        want[128 + 8 * l:128 + 8 * l + 8] = [48.375, 48.375] + [9.0] * 6
+    grid_idx = [[i] * 4 for i in range(8)]
+    dst_check = want.copy()
+
+    def check_subgroups(rc, got, w=dst_check):
+        assert rc == 0, f"status {rc}"
+        for sl in (slice(0, 32), slice(32, 64), slice(128, 160)):
+            assert np.all(np.abs(got[sl] - w[sl]) < 1e-3)
+    k.append(("iq2xxs_distinct_subgroups", IQ2_XXS, pack_iq2xxs(1.0, grid_idx, z4, list(range(8))),
+              256, check_subgroups))
+    # iq2_xxs.rs:391-399 wrong_src_size_errors; dequant/mod.rs iq2_xxs dispatch arm
+    k.append(("iq2xxs_wrong_src_size", IQ2_XXS, np.zeros(65, np.uint8), 256,
+              _status(DEQUANT_SIZE_MISMATCH)))
     return k
 
 

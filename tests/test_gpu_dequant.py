@@ -4,6 +4,7 @@ benchmark configs and on blocks with special f16 scales."""
 import numpy as np
 import pytest
 
+import kats
 from rsllm_amd import synth
 from rsllm_amd.ggml import GgmlType as G
 
@@ -25,7 +26,8 @@ def assert_bits_equal(got: np.ndarray, want: np.ndarray):
 
 
 def special_blocks(dtype, n_per=4, seed=7):
-    be, bb = {G.Q4_K: (256, 144), G.Q6_K: (256, 210), G.Q8_0: (32, 34)}[dtype]
+    be, bb = {G.Q4_K: (256, 144), G.Q6_K: (256, 210), G.Q8_0: (32, 34), G.Q2_K: (256, 84),
+              G.IQ2_XXS: (256, 66)}[dtype]
     blocks = synth.weight(dtype, len(SPECIAL_F16) * n_per, be, seed).reshape(-1, bb).copy()
     for i, pat in enumerate(SPECIAL_F16):
         for r in range(n_per):
@@ -37,12 +39,16 @@ def special_blocks(dtype, n_per=4, seed=7):
                 row[2], row[3] = p2 & 0xFF, p2 >> 8              # dmin
             elif dtype == G.Q6_K:
                 row[208], row[209] = lo, hi
+            elif dtype == G.Q2_K:
+                row[80], row[81] = lo, hi                        # d
+                p2 = SPECIAL_F16[(i + r + 1) % len(SPECIAL_F16)]
+                row[82], row[83] = p2 & 0xFF, p2 >> 8            # dmin
             else:
                 row[0], row[1] = lo, hi
     return blocks.reshape(-1)
 
 
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0])
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K, G.IQ2_XXS])
 def test_dequant_special_scales_bit_exact(oracle, hip, dtype):
     src = special_blocks(dtype)
     n = src.size // dtype.block_bytes() * dtype.block_elements()
@@ -63,6 +69,8 @@ CONFIG_MATRICES = [
     (G.Q4_K, 2048, 7168),     # C3 gate/up (one expert)
     (G.Q4_K, 7168, 2048),     # C3 down (one expert)
     (G.Q4_K, 14336, 4096),    # C4
+    (G.Q2_K, 7168, 2048),     # a DS-V4-Flash-style routed down expert
+    (G.IQ2_XXS, 2048, 7168),  # a DS-V4-Flash-style routed gate/up expert
 ]
 
 
@@ -105,3 +113,18 @@ def test_dequant_dev_entry_point(oracle, hip):
     hip.dequant_to_f32_dev(G.Q6_K, d_src.data_ptr(), src.size, d_dst.data_ptr(), n, stream)
     torch.cuda.synchronize()
     assert_bits_equal(d_dst.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("kat", [k for k in kats.dequant_kats() if k[1] in (kats.Q2_K, kats.IQ2_XXS)],
+                         ids=lambda k: k[0])
+def test_reference_q2k_iq2xxs_kats_on_gpu(hip, kat):
+    """The reference's Q2_K / IQ2_XXS dequant tests (q2_k.rs:171-272,
+    iq2_xxs.rs:188-399, dequant/mod.rs:273-289) through librsllm_hip.so."""
+    name, dtype, src, n, check = kat
+    got = np.empty(n, np.float32)
+    try:
+        hip.dequant_to_f32(dtype, src, got)
+        rc = 0
+    except hip.Error as e:
+        rc = e.status
+    check(rc, got)

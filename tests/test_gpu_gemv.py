@@ -21,7 +21,7 @@ def run_both(oracle, hip, dtype, out_dim, in_dim, n_tok, seed):
     return got, want
 
 
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q4_0])
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q4_0, G.Q2_K, G.IQ2_XXS])
 @pytest.mark.parametrize("out_dim,in_dim", [(1, 256), (7, 512), (33, 768), (100, 2048), (257, 1280)])
 @pytest.mark.parametrize("n_tok", [1, 2, 3, 5, 8, 13])
 def test_gemv_ragged_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
@@ -61,6 +61,8 @@ def test_gemv_mfma_batches(oracle, hip, dtype, out_dim, in_dim, n_tok):
     (G.Q8_0, 4096, 4096, 1), (G.Q8_0, 4096, 4096, 2), (G.Q8_0, 4096, 4096, 4),
     (G.Q8_0, 4096, 4096, 8), (G.Q8_0, 4096, 4096, 16), (G.Q8_0, 4096, 4096, 32),
     (G.Q8_0, 1024, 4096, 1), (G.Q8_0, 1024, 4096, 32),
+    (G.Q2_K, 7168, 2048, 1), (G.Q2_K, 7168, 2048, 8),
+    (G.IQ2_XXS, 2048, 7168, 1), (G.IQ2_XXS, 2048, 7168, 8),
 ])
 def test_gemv_config_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
     got, want = run_both(oracle, hip, dtype, out_dim, in_dim, n_tok, seed=11)

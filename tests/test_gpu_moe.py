@@ -33,7 +33,8 @@ def run_oracle(oracle, base, x, gate, up, down, ids, w, n_tok, n_embd, n_ff, n_e
     return out
 
 
-@pytest.mark.parametrize("dt_gu,dt_d", [(G.Q4_K, G.Q4_K), (G.Q4_K, G.Q6_K), (G.Q8_0, G.Q8_0),
+@pytest.mark.parametrize("dt_gu,dt_d", [(G.IQ2_XXS, G.Q2_K), (G.Q4_K, G.Q2_K),
+                                        (G.Q4_K, G.Q4_K), (G.Q4_K, G.Q6_K), (G.Q8_0, G.Q8_0),
                                         (G.Q6_K, G.Q4_0)])
 @pytest.mark.parametrize("n_tok,k", [(1, 2), (3, 3), (8, 4)])
 def test_moe_small(oracle, hip, dt_gu, dt_d, n_tok, k):

@@ -71,7 +71,7 @@ def test_np_scale_min_matches_oracle_all_12bit_pairs(oracle):
             assert oracle.q4k_scale_min(j, q[i]) == (sc[i, j], m[i, j])
 
 
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0])
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K, G.IQ2_XXS])
 def test_oracle_matches_independent_numpy_restatement(oracle, dtype):
     w = synth.weight(dtype, 512, 4096, seed=int(dtype))
     n = 512 * 4096
@@ -102,7 +102,7 @@ def test_q4k_closed_form_invariants(oracle):
                           np.broadcast_to(-(dmin * m[:, :, None]), (64, 8, 32)))
 
 
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q4_0])
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q4_0, G.Q2_K, G.IQ2_XXS])
 def test_matmul_equals_dequant_then_float64_dot(oracle, dtype):
     out_dim, in_dim, n_tok = 37, 1024, 3
     if dtype == G.Q4_0:
@@ -180,3 +180,42 @@ def test_reference_q4_0_matmul_kat(oracle):
                 want = np.float32(want + np.float32(wd[o, i] * x[t * in_dim + i]))
             got = out[t * out_dim + o]
             assert abs(got - want) < 1e-4 * max(abs(want), 1.0)
+
+
+def test_iq2xxs_codebook(oracle):
+    """The IQ2_XXS grid (iq2_xxs/tables.rs) against the reference's own
+    assertions (iq2_xxs.rs:165-186 and the decoded entries 0-4 quoted in its
+    tests, :248-389), plus invariants a transcription slip would break: 256
+    distinct entries, every byte in {8, 25, 43}, ascending as u64."""
+    g = [oracle.lib().orc_iq2xxs_grid(i) for i in range(256)]
+    assert g[0] == 0x0808080808080808
+    assert g[1] == 0x080808080808082B
+    assert g[2] == 0x0808080808081919
+    assert g[3] == 0x0808080808082B08
+    assert g[4] == 0x0808080808082B2B
+    assert g[255] == 0x2B2B2B1908081908
+    assert len(set(g)) == 256
+    assert all(g[i] < g[i + 1] for i in range(255))
+    b = np.array(g, np.uint64).view(np.uint8)
+    assert set(b.tolist()) <= {8, 25, 43}
+
+
+def test_q2k_closed_form_invariants(oracle):
+    """dmin = 0 => (d * sc) * q exactly; all codes 0 => -(dmin * m)."""
+    g = synth.rng(21)
+    blocks = synth.q2k_blocks(g, 32)
+    b0 = blocks.copy()
+    b0[:, 82:84] = 0
+    rc, v = oracle.dequant(kats.Q2_K, b0.reshape(-1), 32 * 256)
+    assert rc == 0
+    d = b0[:, 80:82].copy().view(np.float16).astype(np.float64)
+    e = np.arange(256)
+    sc = (b0[:, e // 16] & 15).astype(np.float64)
+    q = ((b0[:, 16 + 32 * (e // 128) + e % 32] >> (2 * ((e % 128) // 32))) & 3).astype(np.float64)
+    assert np.array_equal(v.reshape(32, 256).astype(np.float64), d * sc * q)
+    b1 = blocks.copy()
+    b1[:, 16:80] = 0
+    rc, v = oracle.dequant(kats.Q2_K, b1.reshape(-1), 32 * 256)
+    dmin = b1[:, 82:84].copy().view(np.float16).astype(np.float64)
+    m = (b1[:, e // 16] >> 4).astype(np.float64)
+    assert np.array_equal(v.reshape(32, 256).astype(np.float64), -(dmin * m) + 0.0)
