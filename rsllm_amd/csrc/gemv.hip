@@ -4,17 +4,17 @@
 // without materialising dequantised rows.
 //
 // Arithmetic. x is first re-expressed per 16-element group g as
-//     x~_i = s_g * (128 * h_i + l_i),  h in [-127, 127], l in [-64, 64] (int8),
-//     s_g = amax_g / 16256,  |x_i - x~_i| <= s_g / 2 = amax_g / 32512,
-// i.e. about 15 bits relative to the group's largest element. A lane decodes
+//     x~_i = s_g * (256 * h_i + l_i),  h in [-127, 127], l in [-128, 127] (int8),
+//     s_g = amax_g / 32512,  |x_i - x~_i| <= s_g / 2 = amax_g / 65024,
+// i.e. about 16 bits relative to the group's largest element. A lane decodes
 // a 16-byte slice of quantised weights to small integers (Q4_K 0..15,
 // Q6_K 0..63, Q4_0 0..15, Q8_0 -128..127) and dots them with both limbs using
 // v_dot4_i32_i8 (4 exact int8 MACs per instruction, exact int32 sums). Each
 // 16-element partial is then scaled once in fp32:
-//     Q4_K  (d*sc_j) * s_g * (128 H + L) - (dmin*m_j) * sum_g x
-//     Q6_K  (d*sc_e) * (s_g * (128 H + L) - 32 * sum_g x)
-//     Q8_0  d * s_g * (128 H + L)
-//     Q4_0  d * (s_g * (128 H + L) - 8 * sum_g x)
+//     Q4_K  (d*sc_j) * s_g * (256 H + L) - (dmin*m_j) * sum_g x
+//     Q6_K  (d*sc_e) * (s_g * (256 H + L) - 32 * sum_g x)
+//     Q8_0  d * s_g * (256 H + L)
+//     Q4_0  d * (s_g * (256 H + L) - 8 * sum_g x)
 // (sum_g x is the fp32 sum of the original x over the group). Only the
 // limb representation of x and the summation order differ from the
 // reference; the output error is far inside the 1e-3 budget.
@@ -33,8 +33,8 @@
 namespace rsllm_hip {
 
 
-// 128 * sum(q . h) + sum(q . l) over one 16-element group, exact in int32
-// (|q| <= 128, |h| <= 127, |l| <= 64).
+// 256 * sum(q . h) + sum(q . l) over one 16-element group, exact in int32
+// (|q| <= 128, |h| <= 127, |l| <= 128: at most 16 * 128 * 32640 < 2^31).
 __device__ __forceinline__ int dot16_limbs(const uint32_t (&q)[4], const uint4 &h, const uint4 &l) {
     int ah = 0, al = 0;
     ah = __builtin_amdgcn_sdot4((int)q[0], (int)h.x, ah, false);
@@ -45,7 +45,7 @@ __device__ __forceinline__ int dot16_limbs(const uint32_t (&q)[4], const uint4 &
     al = __builtin_amdgcn_sdot4((int)q[2], (int)l.z, al, false);
     ah = __builtin_amdgcn_sdot4((int)q[3], (int)h.w, ah, false);
     al = __builtin_amdgcn_sdot4((int)q[3], (int)l.w, al, false);
-    return ah * 128 + al;
+    return ah * 256 + al;
 }
 
 // Activation limbs of one lane: groups "lo" and "hi" (see each format for
@@ -211,8 +211,8 @@ struct FQ8 {
 struct FQ2K {
     static constexpr int kEPU = 256, kXF = 5;
     struct Slice {
-        uint4 qs, sc;
-        uint32_t dd;
+        uint4 qs;
+        uint32_t sc, dd;  // sc: the scale dword holding both of the lane's scale bytes
     };
     __device__ static int units(int in_dim) { return in_dim >> 8; }
     __device__ static int elem_lo(int unit, int k) {
@@ -229,14 +229,17 @@ struct FQ2K {
         const uint32_t rS = (S < (nblk >> 3)) ? 8u : (nblk & 7u);
         const uint32_t base = S * 672u;
         s.qs = bload16(r, base + j * 64u + 16u * (uint32_t)(k >> 1), 0);
-        s.sc = bload16(r, base + rS * 64u + j * 16u, 0);
+        // scale bytes sub and sub + 2 (see dot) share dword sub / 4 = 2 (k / 4) + (k & 1)
+        s.sc = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+            r, (int)(base + rS * 64u + j * 16u + 8u * (uint32_t)(k >> 2) + 4u * (uint32_t)(k & 1)), 0, 0);
         s.dd = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)(base + rS * 80u + j * 4u), 0, 0);
     }
     __device__ static float dot(const Slice &s, int k, const XSlice &x) {
         const float d = f16_to_f32(s.dd & 0xFFFFu), dmin = f16_to_f32(s.dd >> 16);
-        const int sub = 8 * (k >> 2) + 4 * (k & 1) + ((k >> 1) & 1);
-        const uint32_t sl = (uint32_t)sbyte16(s.sc, sub) & 0xFFu;
-        const uint32_t sh = (uint32_t)sbyte16(s.sc, sub + 2) & 0xFFu;
+        // scale bytes sub = 8 (k / 4) + 4 (k & 1) + ((k / 2) & 1) and sub + 2
+        const uint32_t c = 8u * (uint32_t)((k >> 1) & 1);
+        const uint32_t sl = (s.sc >> c) & 0xFFu;
+        const uint32_t sh = (s.sc >> (c + 16u)) & 0xFFu;
         const float dl = d * (float)(sl & 15u), ml = dmin * (float)(sl >> 4);
         const float dh = d * (float)(sh & 15u), mh = dmin * (float)(sh >> 4);
         const uint32_t shl = 4u * (uint32_t)(k & 1), shh = shl + 2u;
@@ -308,8 +311,10 @@ struct FIQ2XXS {
 // Per token: ncols columns x kXF fields x 64 lanes x 16 bytes. Fields:
 // 0 h_lo, 1 l_lo, 2 meta (s_lo, sum_lo, s_hi, sum_hi), 3 h_hi, 4 l_hi
 // (kXF = 3 keeps fields 0..2). Groups past in_dim are written as zeros.
-// Two int8 limbs of 16 values: v ~= s * (128 h + l), s = amax / 16256;
-// `sum` is the fp32 sum of the values.
+// Two int8 limbs of 16 values: v ~= s * (256 h + l), s = amax / 32512;
+// `sum` is the fp32 sum of the values. A group holding NaN gets s = NaN, so
+// every output it feeds is NaN (as in the fp32 reference); +-Inf gives
+// s = Inf and limbs 0, hence NaN as well.
 __device__ __forceinline__ void quant_values(const float (&v)[16], uint4 &h, uint4 &l, float &s,
                                              float &sum) {
     float amax = 0.f;
@@ -319,26 +324,29 @@ __device__ __forceinline__ void quant_values(const float (&v)[16], uint4 &h, uin
         amax = fmaxf(amax, fabsf(v[i]));
         sum += v[i];
     }
-    s = amax * (1.0f / 16256.0f);
-    const float inv = amax > 0.f ? 16256.0f / amax : 0.f;
-    // t = v / s in [-16256, 16256]; h = rint(t / 128) in [-127, 127] and
-    // l = rint(t - 128 h) in [-64, 64] need no clamping. Both are formed
-    // biased by 128 (exact integers in [1, 255]) so v_cvt_pk_u8_f32 packs
-    // them, and the bias is removed per dword with one xor.
+    s = sum == sum ? amax * (1.0f / 32512.0f) : sum;
+    // t = v / s in [-32512, 32512] (beyond by a few ulp of the approximate
+    // reciprocal at most; round(t) stays within +-32512). f = t + 128 +
+    // 1.5 * 2^23 rounds t to the nearest integer (ties to even) in the one
+    // rounding of the fma, and leaves u = round(t) + 128 in the low 16 bits
+    // of f's encoding, as a 16-bit two's complement integer. Then
+    //     h = u >> 8 in [-127, 127]                 (byte 1 of f),
+    //     l = round(t) - 256 h = (u & 255) - 128    (byte 0 of f, xor 0x80),
+    // so round(t) = 256 h + l exactly; v_perm_b32 gathers the bytes. Groups
+    // with amax below 2^-100 quantise to zero limbs.
+    const float inv = amax > 0x1p-100f ? 32512.0f * __builtin_amdgcn_rcpf(amax) : 0.f;
     uint32_t hw[4], lw[4];
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        uint32_t hh = 0, ll = 0;
+    for (int q = 0; q < 4; q++) {
+        uint32_t u[4];
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const float t = v[4 * u + b] * inv;
-            const float hb = rintf(fmaf(t, 1.0f / 128.0f, 128.0f));    // h + 128
-            const float lb = rintf(fmaf(-128.0f, hb, t + 16512.0f));    // l + 128
-            hh = __builtin_amdgcn_cvt_pk_u8_f32(hb, b, hh);
-            ll = __builtin_amdgcn_cvt_pk_u8_f32(lb, b, ll);
-        }
-        hw[u] = hh ^ 0x80808080u;
-        lw[u] = ll ^ 0x80808080u;
+        for (int b = 0; b < 4; b++) u[b] = __float_as_uint(fmaf(v[4 * q + b], inv, 12583040.0f));
+        const uint32_t l01 = __builtin_amdgcn_perm(u[1], u[0], 0x0C0C0400u);
+        const uint32_t l23 = __builtin_amdgcn_perm(u[3], u[2], 0x04000C0Cu);
+        const uint32_t h01 = __builtin_amdgcn_perm(u[1], u[0], 0x0C0C0501u);
+        const uint32_t h23 = __builtin_amdgcn_perm(u[3], u[2], 0x05010C0Cu);
+        lw[q] = (l01 | l23) ^ 0x80808080u;
+        hw[q] = h01 | h23;
     }
     h = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     l = make_uint4(lw[0], lw[1], lw[2], lw[3]);
@@ -532,121 +540,209 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv(const uint8_t *__restri
 }
 
 // ---- batch-1 GEMV with the activation pre-pass fused -------------------------
-// Workgroup = NWV wavefronts of RT rows each. Prologue: the workgroup
-// quantises x into LDS in the pre-pass layout (thread i takes groups i,
-// i + 64 NWV, ...); its first x loads are issued before the first column's
-// weight loads, so both latencies overlap. Then every wavefront streams all
-// columns of its RT rows, the next column's weights in flight while the
-// current one is computed, and lane 0 writes each row's total. No other
-// launch is needed, and x is read once per workgroup instead of once per
-// wavefront and column.
-template <class F, int RT, int NWV>
-__global__ __launch_bounds__(64 * NWV) void k_gemv1(const uint8_t *__restrict__ w,
-                                                   uint32_t w_bytes,
-                                                   const float *__restrict__ x,
-                                                   float *__restrict__ y, int in_dim,
-                                                   int out_dim) {
+// One launch of n_wg workgroups (one or two per CU) of NW wavefronts.
+//
+// Rows. Workgroup b owns rows b + n_wg * l (l = 0, 1, ...); wavefront w of
+// it takes that list's entries w, w + NW, ... and streams each row's K
+// columns (a column = 8 units, one weight "tile") in order, PD tiles in
+// flight, keeping the row's per-lane partials in registers: one wavefront
+// reduction per row, lane 0 writes the total. Concurrent wavefronts
+// therefore read neighbouring rows, and every CU gets the same number of
+// rows to within one per wavefront.
+//
+// Prologue. The workgroup quantises x into LDS in the pre-pass layout
+// (thread i takes groups i, i + 64 NW, ...; whole wavefronts without a group
+// skip it). Its x loads are issued first and the first PD - 1 tiles right
+// after, so the weight stream runs while x is quantised.
+//
+// Loads are branch-free: a tile past the wavefront's last one is read through
+// a zero-length buffer resource (the hardware returns zeros without memory
+// traffic), and compiler scheduling barriers keep each step's loads ahead of
+// its arithmetic, so the waits before each tile's arithmetic leave the later
+// tiles in flight.
+//
+// DPP row reductions (quad_perm, row_half_mirror, row_mirror) plus four lane
+// reads sum a wavefront; the order is fixed, so results are deterministic.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 47));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    return (a + b) + (c + d);
+}
+
+template <class F, int NW, int PD, int GPT>
+__global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w, uint32_t w_bytes,
+                                                  const float *__restrict__ x,
+                                                  float *__restrict__ y, int in_dim, int out_dim,
+                                                  int n_wg) {
     extern __shared__ uint4 xl[];
     constexpr int kHalves = F::kXF == 5 ? 2 : 1;
-    constexpr int kThreads = 64 * NWV;
+    constexpr int kThreads = 64 * NW;
     const int lane = threadIdx.x & 63, k = lane & 7, ks = lane >> 3;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nunits = F::units(in_dim), ncols = (nunits + 7) >> 3;
     const int n_groups = ncols * 64 * kHalves;
-    const int row0 = (blockIdx.x * NWV + wv) * RT;
+    const int r0 = blockIdx.x;
+    const int nrows = (out_dim - r0 + n_wg - 1) / n_wg;                 // this workgroup's rows
+    const int my_rows = nrows > wv ? (nrows - wv + NW - 1) / NW : 0;   // this wavefront's rows
+    const int T = my_rows * ncols;                                       // its tiles
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
+    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(w, 0);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)in_dim * 4u);
 
     auto group_elem = [&](int g) {
         const int col = g / (64 * kHalves), r2 = g % (64 * kHalves);
         const int half = r2 >> 6, ln = r2 & 63;
         const int kk = ln & 7, unit = col * 8 + (ln >> 3);
-        const bool ok = unit < nunits && F::valid(unit, kk, in_dim);
+        const bool ok = g < n_groups && unit < nunits && F::valid(unit, kk, in_dim);
         return ok ? (half ? F::elem_hi(unit, kk) : F::elem_lo(unit, kk)) : -1;
     };
-    auto quant_store = [&](int g, const float (&v)[16]) {
+    auto row_of = [&](int j) { return r0 + n_wg * (wv + NW * j); };
+    typename F::Slice buf[PD];
+    auto load_tile = [&](typename F::Slice &sl, int t) {
+        const int j = t / ncols, col = t - j * ncols;
+        const int unit = min(col * 8 + ks, nunits - 1);
+        const __amdgpu_buffer_rsrc_t r = t < T ? rw : rnull;
+        F::load(sl, r, min(row_of(j), out_dim - 1), unit, k, in_dim, out_dim);
+    };
+
+    // Prologue: x loads, the first tiles, then quantisation into LDS. Group
+    // indices past n_groups store into one spare column.
+    uint4 xv[GPT][4];
+#pragma unroll
+    for (int i = 0; i < GPT; i++) {
+        if (wv * 64 + i * kThreads >= n_groups) continue;
+        const int e = group_elem(threadIdx.x + i * kThreads);
+        const uint32_t off = e >= 0 ? (uint32_t)e * 4u : 0x80000000u;  // past the end: zeros
+#pragma unroll
+        for (int q = 0; q < 4; q++) xv[i][q] = bload16(rx, off + 16u * q, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < PD - 1; j++) load_tile(buf[j], j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < GPT; i++) {
+        if (wv * 64 + i * kThreads >= n_groups) continue;
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            v[4 * q] = __uint_as_float(xv[i][q].x);
+            v[4 * q + 1] = __uint_as_float(xv[i][q].y);
+            v[4 * q + 2] = __uint_as_float(xv[i][q].z);
+            v[4 * q + 3] = __uint_as_float(xv[i][q].w);
+        }
         uint4 h, l;
         float sc, sum;
         quant_values(v, h, l, sc, sum);
-        const int col = g / (64 * kHalves), r2 = g % (64 * kHalves);
+        const int g = threadIdx.x + i * kThreads;
+        const int gg = g < n_groups ? g : n_groups;
+        const int col = gg / (64 * kHalves), r2 = gg % (64 * kHalves);
         const int half = r2 >> 6, ln = r2 & 63;
         uint4 *b = xl + col * F::kXF * 64 + ln;
         b[(half ? 3 : 0) * 64] = h;
         b[(half ? 4 : 1) * 64] = l;
         reinterpret_cast<float2 *>(b + 2 * 64)[half] = make_float2(sc, sum);
-    };
-    typename F::Slice a[RT], b[RT];
-    auto load_col = [&](typename F::Slice (&sl)[RT], int col) {
-        const int unit = min(col * 8 + ks, nunits - 1);
-#pragma unroll
-        for (int r = 0; r < RT; r++)
-            F::load(sl[r], rw, min(row0 + r, out_dim - 1), unit, k, in_dim, out_dim);
-    };
-
-    const int g0 = threadIdx.x;
-    float v0[16];
-    load_group(x, g0 < n_groups ? group_elem(g0) : -1, in_dim, v0);
-    load_col(a, 0);
-    if (g0 < n_groups) quant_store(g0, v0);
-    for (int g = g0 + kThreads; g < n_groups; g += kThreads) {
-        float v[16];
-        load_group(x, group_elem(g), in_dim, v);
-        quant_store(g, v);
     }
     __syncthreads();
 
-    float acc[RT];
+    float acc = 0.f;
+    int col = 0, j = 0;
+    for (int t0 = 0; t0 < T; t0 += PD) {
 #pragma unroll
-    for (int r = 0; r < RT; r++) acc[r] = 0.f;
-    auto body = [&](typename F::Slice (&cur)[RT], typename F::Slice (&nxt)[RT], int col) {
-        if (col + 1 < ncols) load_col(nxt, col + 1);
-        XSlice xs;
-        const uint4 *bx = xl + col * F::kXF * 64 + lane;
-        xs.hlo = bx[0];
-        xs.llo = bx[64];
-        xs.meta = bx[128];
-        if (F::kXF == 5) {
-            xs.hhi = bx[192];
-            xs.lhi = bx[256];
+        for (int jj = 0; jj < PD; jj++) {
+            const int t = t0 + jj;
+            load_tile(buf[(jj + PD - 1) % PD], t + PD - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            XSlice xs;
+            const uint4 *bx = xl + col * F::kXF * 64 + lane;
+            xs.hlo = bx[0];
+            xs.llo = bx[64];
+            xs.meta = bx[128];
+            if (F::kXF == 5) {
+                xs.hhi = bx[192];
+                xs.lhi = bx[256];
+            }
+            const int unit = col * 8 + ks;
+            const bool ok = t < T && unit < nunits && F::valid(unit, k, in_dim);
+            const float d = F::dot(buf[jj], k, xs);
+            acc += ok ? d : 0.f;
+            if (col == ncols - 1) {
+                const float tot = wave_sum_dpp(acc);
+                if (lane == 0 && t < T) y[row_of(j)] = tot;
+                acc = 0.f;
+                col = 0;
+                j++;
+            } else {
+                col++;
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        const int unit = col * 8 + ks;
-        if (unit < nunits && F::valid(unit, k, in_dim)) {
-#pragma unroll
-            for (int r = 0; r < RT; r++) acc[r] += F::dot(cur[r], k, xs);
-        }
-    };
-    for (int col = 0; col < ncols; col += 2) {
-        body(a, b, col);
-        if (col + 1 < ncols) body(b, a, col + 1);
-    }
-#pragma unroll
-    for (int r = 0; r < RT; r++) {
-        const float v = wave_sum(acc[r]);
-        if (lane == 0 && row0 + r < out_dim) y[row0 + r] = v;
     }
 }
 
+// LDS of k_gemv1: the quantised x (ncols columns) plus one spare column.
 template <class F>
 static size_t gemv1_lds_bytes(int in_dim) {
     const int ncols = ((in_dim + F::kEPU - 1) / F::kEPU + 7) >> 3;
-    return (size_t)ncols * F::kXF * 1024;
+    return (size_t)(ncols + 1) * F::kXF * 1024;
 }
 
-template <class F, int RT, int NWV>
+// Groups of x per thread the prologue needs (1, 2 or 4; 0 = too long).
+template <class F>
+static int gemv1_gpt(int in_dim, int nw) {
+    const int ncols = ((in_dim + F::kEPU - 1) / F::kEPU + 7) >> 3;
+    const int groups = ncols * 64 * (F::kXF == 5 ? 2 : 1);
+    const int gpt = (groups + 64 * nw - 1) / (64 * nw);
+    return gpt <= 1 ? 1 : gpt <= 2 ? 2 : gpt <= 4 ? 4 : 0;
+}
+
+// Compute units of the current device (cached per device ordinal).
+static int device_cus() {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+template <class F, int NW, int PD, int GPT>
 static hipError_t gemv1_go(const uint8_t *w, size_t w_bytes, const float *x, float *y, int in_dim,
-                           int out_dim, hipStream_t s) {
-    const size_t lds = gemv1_lds_bytes<F>(in_dim);
+                           int out_dim, int n_wg, hipStream_t s) {
     static bool attr_set = false;  // per instantiation; idempotent if raced
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemv1<F, RT, NWV>,
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemv1<F, NW, PD, GPT>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)kGemv1MaxLds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    const int rows_wg = RT * NWV;
-    k_gemv1<F, RT, NWV><<<(unsigned)((out_dim + rows_wg - 1) / rows_wg), 64 * NWV, lds, s>>>(
-        w, (uint32_t)w_bytes, x, y, in_dim, out_dim);
+    n_wg = min(n_wg, out_dim);
+    k_gemv1<F, NW, PD, GPT><<<(unsigned)n_wg, 64 * NW, gemv1_lds_bytes<F>(in_dim), s>>>(
+        w, (uint32_t)w_bytes, x, y, in_dim, out_dim, n_wg);
     return hipGetLastError();
+}
+
+template <class F, int NW, int PD>
+static hipError_t gemv1_gpt_go(const uint8_t *w, size_t w_bytes, const float *x, float *y,
+                               int in_dim, int out_dim, int n_wg, hipStream_t s) {
+    switch (gemv1_gpt<F>(in_dim, NW)) {
+    case 1: return gemv1_go<F, NW, PD, 1>(w, w_bytes, x, y, in_dim, out_dim, n_wg, s);
+    case 2: return gemv1_go<F, NW, PD, 2>(w, w_bytes, x, y, in_dim, out_dim, n_wg, s);
+    case 4: return gemv1_go<F, NW, PD, 4>(w, w_bytes, x, y, in_dim, out_dim, n_wg, s);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 // ---- grouped GEMV (routed experts) ------------------------------------------
@@ -923,33 +1019,35 @@ hipError_t launch_gemv_prequant(uint32_t dtype, const uint8_t *w, size_t w_bytes
     }
 }
 
-// Batch 1: the fused kernel. RT = 2 rows per wavefront for tall matrices
-// (out_dim >= 3 in_dim), else 1; 16 wavefronts per workgroup unless that
-// leaves fewer than 256 workgroups (then 8, then 4). Chosen from sweeps of
-// the C1-C3 shapes on MI355X.
+// Batch 1: the fused kernel. Matrices of 32 MB or more (the weight stream
+// dominates) use 8-wavefront workgroups: two per CU with two tiles in flight
+// for tall matrices (out_dim >= 2 in_dim), one per CU with three for the
+// rest; smaller ones use one 16-wavefront workgroup per CU with two tiles in
+// flight. Chosen from sweeps of the C0-C3 shapes on MI355X.
 template <class F>
 static hipError_t gemv1(const uint8_t *w, size_t w_bytes, const float *x, float *y, int in_dim,
                         int out_dim, hipStream_t s) {
-    const int rt = out_dim >= 3 * in_dim ? 2 : 1;
-    const int nwv = out_dim / (rt * 16) >= 256 ? 16 : (out_dim / (rt * 8) >= 256 ? 8 : 4);
-    if (rt == 2) {
-        if (nwv == 16) return gemv1_go<F, 2, 16>(w, w_bytes, x, y, in_dim, out_dim, s);
-        if (nwv == 8) return gemv1_go<F, 2, 8>(w, w_bytes, x, y, in_dim, out_dim, s);
-        return gemv1_go<F, 2, 4>(w, w_bytes, x, y, in_dim, out_dim, s);
+    const int cus = device_cus();
+    if (w_bytes >= ((size_t)32 << 20)) {
+        if (out_dim >= 2 * in_dim) return gemv1_gpt_go<F, 8, 2>(w, w_bytes, x, y, in_dim, out_dim, 2 * cus, s);
+        return gemv1_gpt_go<F, 8, 3>(w, w_bytes, x, y, in_dim, out_dim, cus, s);
     }
-    if (nwv == 16) return gemv1_go<F, 1, 16>(w, w_bytes, x, y, in_dim, out_dim, s);
-    if (nwv == 8) return gemv1_go<F, 1, 8>(w, w_bytes, x, y, in_dim, out_dim, s);
-    return gemv1_go<F, 1, 4>(w, w_bytes, x, y, in_dim, out_dim, s);
+    return gemv1_gpt_go<F, 16, 2>(w, w_bytes, x, y, in_dim, out_dim, cus, s);
+}
+
+template <class F>
+static bool gemv1_fits_f(int in_dim) {
+    return gemv1_lds_bytes<F>(in_dim) <= kGemv1MaxLds && gemv1_gpt<F>(in_dim, 8) != 0;
 }
 
 static bool gemv1_fits(uint32_t dtype, int in_dim) {
     switch (dtype) {
-    case T_Q4_K: return gemv1_lds_bytes<FQ4K>(in_dim) <= kGemv1MaxLds;
-    case T_Q6_K: return gemv1_lds_bytes<FQ6K>(in_dim) <= kGemv1MaxLds;
-    case T_Q8_0: return gemv1_lds_bytes<FQ8<false>>(in_dim) <= kGemv1MaxLds;
-    case T_Q4_0: return gemv1_lds_bytes<FQ8<true>>(in_dim) <= kGemv1MaxLds;
-    case T_Q2_K: return gemv1_lds_bytes<FQ2K>(in_dim) <= kGemv1MaxLds;
-    case T_IQ2_XXS: return gemv1_lds_bytes<FIQ2XXS>(in_dim) <= kGemv1MaxLds;
+    case T_Q4_K: return gemv1_fits_f<FQ4K>(in_dim);
+    case T_Q6_K: return gemv1_fits_f<FQ6K>(in_dim);
+    case T_Q8_0: return gemv1_fits_f<FQ8<false>>(in_dim);
+    case T_Q4_0: return gemv1_fits_f<FQ8<true>>(in_dim);
+    case T_Q2_K: return gemv1_fits_f<FQ2K>(in_dim);
+    case T_IQ2_XXS: return gemv1_fits_f<FIQ2XXS>(in_dim);
     default: return false;
     }
 }
