@@ -587,7 +587,7 @@ def main():
             "frac": round(ach / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_detail": traffic_detail,
-            "kernel": "rsllm_hip::k_gemv1<FQ6K, RT, NWV> (x quantised in LDS, one launch)",
+            "kernel": "rsllm_hip::k_gemv1<FQ6K, NW, PD, GPT> (x quantised in LDS, one launch)",
             "kernel_shape": per_kernel[dom]["shape"],
             "kernel_us_mean": round(kern_us[dom], 3),
         },
