@@ -19,7 +19,7 @@
 //   6. grouped GEMV, down -> yd [slot x n_embd];
 //   7. k_moe_accumulate: out[t, j] += w[t, i] * yd[slot(t, i), j] in i order,
 //      as the reference's `out_t[j] += we * expert_out[j]` (no contraction).
-#include "kernels.h"
+#include "gemv_formats.h"
 
 namespace rsllm_hip {
 
@@ -92,6 +92,512 @@ __global__ __launch_bounds__(256) void k_moe_accumulate(float *__restrict__ out,
     out[i] = v;
 }
 
+
+// ---- fused path for a few tokens (decode) -----------------------------------
+// For n_tok * k <= kFusedPairs the layer is two launches:
+//   k_moe_gu:   every workgroup routes the (t, i) pairs in LDS, quantises x of
+//               all tokens into LDS, then streams gate and up rows; the
+//               epilogue of a (row, expert) applies the clamp and SwiGLU and
+//               writes h[slot, row];
+//   k_moe_down: routes again (same result), quantises h of all slots into
+//               LDS, streams down rows; the epilogue of a row adds
+//               w[t, i] * y[slot(t, i), row] into out[t, row] in i order.
+// Rows are dealt as in k_gemv1 (workgroup b owns rows b + n_wg * l, a
+// wavefront streams whole rows); a row's tiles walk the active experts
+// ("chunks" of at most kChunk slots of one expert), PD tiles in flight, each
+// expert's weights read once per row for all its slots.
+constexpr int kFusedPairs = 32;
+constexpr int kChunk = 4;
+
+struct MoeRoute {
+    int n_chunks;
+    int chunk_e[kFusedPairs], chunk_s0[kFusedPairs], chunk_n[kFusedPairs];
+    int slot_tok[kFusedPairs];  // token of each slot
+    int slot_of[kFusedPairs];   // pair (t * k + i) -> slot, -1 if skipped
+    float wt[kFusedPairs];      // pair weights
+    int eid[kFusedPairs];       // pair -> expert, -1 if skipped
+    int nch[kFusedPairs];       // at an expert's first pair: its chunk count, else 0
+};
+
+// Threads p < P route pair p (P = n_tok * k <= kFusedPairs). Slots sorted by
+// expert, ties in pair order, as k_moe_route; skipped pairs (w == 0 or an
+// expert id out of range) get no slot. Ends with a workgroup barrier.
+__device__ __forceinline__ void moe_route_lds(MoeRoute &r, int e_p, float w_p, int P, int k,
+                                              int n_expert) {
+    const int p = threadIdx.x;
+    const bool valid = p < P && w_p != 0.0f && e_p >= 0 && e_p < n_expert;
+    if (p < P) {
+        r.eid[p] = valid ? e_p : -1;
+        r.wt[p] = w_p;
+    }
+    __syncthreads();
+    int below = 0, rank = 0, cnt = 0;
+    if (p < P) {
+        for (int q = 0; q < P; q++) {
+            const int eq = r.eid[q];
+            if (!valid || eq < 0) continue;
+            if (eq < e_p) below++;
+            if (eq == e_p) {
+                cnt++;
+                if (q < p) rank++;
+            }
+        }
+        r.nch[p] = valid && rank == 0 ? (cnt + kChunk - 1) / kChunk : 0;
+    }
+    __syncthreads();
+    if (p < P) {
+        int chunks_below = 0, chunks_all = 0;
+        for (int q = 0; q < P; q++) {
+            const int c = r.nch[q];
+            chunks_all += c;
+            if (valid && r.eid[q] < e_p) chunks_below += c;
+        }
+        const int slot = valid ? below + rank : -1;
+        r.slot_of[p] = slot;
+        if (valid) r.slot_tok[slot] = p / k;
+        if (valid && rank == 0) {
+            for (int c = 0; c * kChunk < cnt; c++) {
+                r.chunk_e[chunks_below + c] = e_p;
+                r.chunk_s0[chunks_below + c] = below + c * kChunk;
+                r.chunk_n[chunks_below + c] = min(kChunk, cnt - c * kChunk);
+            }
+        }
+        if (p == 0) r.n_chunks = chunks_all;
+    }
+    __syncthreads();
+}
+
+// Quantise GPT groups per thread of `rows` rows of length in_dim (row stride
+// in_dim floats) into LDS in the pre-pass layout (row-major: row, column,
+// field, lane). `vals` holds the values, loaded by moe_load_groups.
+template <class F, int GPT>
+struct MoeGroups {
+    uint4 v[GPT][4];
+};
+
+template <class F, int NW, int GPT>
+__device__ __forceinline__ void moe_load_groups(MoeGroups<F, GPT> &g, const float *src,
+                                                int rows, int in_dim) {
+    constexpr int kHalves = F::kXF == 5 ? 2 : 1;
+    const int nunits = F::units(in_dim), ncols = (nunits + 7) >> 3;
+    const int per_row = ncols * 64 * kHalves, n_groups = rows * per_row;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, (uint32_t)rows * (uint32_t)in_dim * 4u);
+#pragma unroll
+    for (int i = 0; i < GPT; i++) {
+        if (wv * 64 + i * 64 * NW >= n_groups) continue;
+        const int gidx = threadIdx.x + i * 64 * NW;
+        const int row = gidx / per_row, rem = gidx % per_row;
+        const int col = rem / (64 * kHalves), r2 = rem % (64 * kHalves);
+        const int half = r2 >> 6, ln = r2 & 63;
+        const int kk = ln & 7, unit = col * 8 + (ln >> 3);
+        const bool ok = gidx < n_groups && unit < nunits && F::valid(unit, kk, in_dim);
+        const int e = ok ? (half ? F::elem_hi(unit, kk) : F::elem_lo(unit, kk)) : -1;
+        const uint32_t off = e >= 0 ? ((uint32_t)row * (uint32_t)in_dim + (uint32_t)e) * 4u
+                                    : 0x80000000u;
+#pragma unroll
+        for (int q = 0; q < 4; q++) g.v[i][q] = bload16(rs, off + 16u * q, 0);
+    }
+}
+
+template <class F, int NW, int GPT>
+__device__ __forceinline__ void moe_store_groups(const MoeGroups<F, GPT> &g, uint4 *xl, int rows,
+                                                 int in_dim) {
+    constexpr int kHalves = F::kXF == 5 ? 2 : 1;
+    const int nunits = F::units(in_dim), ncols = (nunits + 7) >> 3;
+    const int per_row = ncols * 64 * kHalves, n_groups = rows * per_row;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int i = 0; i < GPT; i++) {
+        if (wv * 64 + i * 64 * NW >= n_groups) continue;
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            v[4 * q] = __uint_as_float(g.v[i][q].x);
+            v[4 * q + 1] = __uint_as_float(g.v[i][q].y);
+            v[4 * q + 2] = __uint_as_float(g.v[i][q].z);
+            v[4 * q + 3] = __uint_as_float(g.v[i][q].w);
+        }
+        uint4 h, l;
+        float sc, sum;
+        quant_values(v, h, l, sc, sum);
+        const int gidx = threadIdx.x + i * 64 * NW;
+        const int gg = gidx < n_groups ? gidx : n_groups;  // spare column past the end
+        const int row = gg / per_row, rem = gg % per_row;
+        const int col = rem / (64 * kHalves), r2 = rem % (64 * kHalves);
+        const int half = r2 >> 6, ln = r2 & 63;
+        uint4 *b = xl + ((size_t)row * ncols + col) * F::kXF * 64 + ln;
+        b[(half ? 3 : 0) * 64] = h;
+        b[(half ? 4 : 1) * 64] = l;
+        reinterpret_cast<float2 *>(b + 2 * 64)[half] = make_float2(sc, sum);
+    }
+}
+
+// Gate/up. Tile = (row r, chunk ch, column c): one gate and one up slice.
+template <class F, int NW, int PD, int GPT>
+__global__ __launch_bounds__(64 * NW) void k_moe_gu(const uint8_t *__restrict__ gate,
+                                                   const uint8_t *__restrict__ up,
+                                                   uint32_t stride, const float *__restrict__ x,
+                                                   const int *__restrict__ ids,
+                                                   const float *__restrict__ wts,
+                                                   float *__restrict__ h, int n_tok, int k,
+                                                   int n_expert, int in_dim, int out_dim,
+                                                   float clamp, int n_wg) {
+    extern __shared__ uint4 xlds[];
+    __shared__ MoeRoute rt;
+    const int lane = threadIdx.x & 63, kk = lane & 7, ks = lane >> 3;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int P = n_tok * k;
+    const int nunits = F::units(in_dim), ncols = (nunits + 7) >> 3;
+    const uint32_t tok_fields = (uint32_t)ncols * F::kXF * 64;  // uint4 per token in LDS
+
+    int e_p = -1;
+    float w_p = 0.f;
+    if ((int)threadIdx.x < P) {
+        e_p = ids[threadIdx.x];
+        w_p = wts[threadIdx.x];
+    }
+    MoeGroups<F, GPT> xg;
+    moe_load_groups<F, NW, GPT>(xg, x, n_tok, in_dim);
+    moe_route_lds(rt, e_p, w_p, P, k, n_expert);
+
+    const int r0 = blockIdx.x;
+    const int nrows = (out_dim - r0 + n_wg - 1) / n_wg;
+    const int my_rows = nrows > wv ? (nrows - wv + NW - 1) / NW : 0;
+    const int n_chunks = __builtin_amdgcn_readfirstlane(rt.n_chunks);
+    const int T = my_rows * n_chunks * ncols;
+    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(gate, 0);
+
+    typename F::Slice bg[PD], bu[PD];
+    // load cursor: tile index lt -> (lj, lch, lc)
+    int lj = 0, lch = 0, lc = 0;
+    int le = n_chunks > 0 ? __builtin_amdgcn_readfirstlane(rt.chunk_e[0]) : 0;
+    auto load_next = [&](typename F::Slice &sg, typename F::Slice &su, int lt) {
+        const bool ok = lt < T;
+        const int row = min(r0 + n_wg * (wv + NW * lj), out_dim - 1);
+        const size_t base = (size_t)le * stride;
+        const __amdgpu_buffer_rsrc_t rg = ok ? make_rsrc(gate + base, stride) : rnull;
+        const __amdgpu_buffer_rsrc_t ru = ok ? make_rsrc(up + base, stride) : rnull;
+        const int unit = min(lc * 8 + ks, nunits - 1);
+        F::load(sg, rg, row, unit, kk, in_dim, out_dim);
+        F::load(su, ru, row, unit, kk, in_dim, out_dim);
+        if (++lc == ncols) {
+            lc = 0;
+            if (++lch == n_chunks) {
+                lch = 0;
+                lj++;
+            }
+            le = __builtin_amdgcn_readfirstlane(rt.chunk_e[lch]);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < PD - 1; j++) load_next(bg[j], bu[j], j);
+    __builtin_amdgcn_sched_barrier(0);
+    moe_store_groups<F, NW, GPT>(xg, xlds, n_tok, in_dim);
+    __syncthreads();
+
+    // compute cursor
+    int cj = 0, cch = 0, cc = 0;
+    float ag[kChunk], au[kChunk];
+#pragma unroll
+    for (int q = 0; q < kChunk; q++) ag[q] = au[q] = 0.f;
+    for (int t0 = 0; t0 < T; t0 += PD) {
+#pragma unroll
+        for (int jj = 0; jj < PD; jj++) {
+            const int t = t0 + jj;
+            load_next(bg[(jj + PD - 1) % PD], bu[(jj + PD - 1) % PD], t + PD - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (t < T) {
+                const int n = __builtin_amdgcn_readfirstlane(rt.chunk_n[cch]);
+                const int s0 = __builtin_amdgcn_readfirstlane(rt.chunk_s0[cch]);
+                const int unit = cc * 8 + ks;
+                const bool okl = unit < nunits && F::valid(unit, kk, in_dim);
+#pragma unroll
+                for (int q = 0; q < kChunk; q++) {
+                    if (q < n) {
+                        const int tok = __builtin_amdgcn_readfirstlane(rt.slot_tok[s0 + q]);
+                        const uint4 *bx = xlds + tok * tok_fields + cc * F::kXF * 64 + lane;
+                        XSlice xs;
+                        xs.hlo = bx[0];
+                        xs.llo = bx[64];
+                        xs.meta = bx[128];
+                        if (F::kXF == 5) {
+                            xs.hhi = bx[192];
+                            xs.lhi = bx[256];
+                        }
+                        const float dg = F::dot(bg[jj], kk, xs), du = F::dot(bu[jj], kk, xs);
+                        ag[q] += okl ? dg : 0.f;
+                        au[q] += okl ? du : 0.f;
+                    }
+                }
+                if (++cc == ncols) {
+                    const int row = r0 + n_wg * (wv + NW * cj);
+#pragma unroll
+                    for (int q = 0; q < kChunk; q++) {
+                        if (q < n) {
+                            const float g = wave_sum_dpp(ag[q]), u = wave_sum_dpp(au[q]);
+                            if (lane == 0) h[(size_t)(s0 + q) * out_dim + row] = swiglu_clamped(g, u, clamp);
+                        }
+                        ag[q] = au[q] = 0.f;
+                    }
+                    cc = 0;
+                    if (++cch == n_chunks) {
+                        cch = 0;
+                        cj++;
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// Down. Tile = (row r, chunk ch, column c). After a row's last tile, lanes
+// t < n_tok add w[t, i] * y[slot(t, i)] into out[t, r] in i order.
+template <class F, int NW, int PD, int GPT>
+__global__ __launch_bounds__(64 * NW) void k_moe_down(const uint8_t *__restrict__ down,
+                                                     uint32_t stride, const float *__restrict__ h,
+                                                     const int *__restrict__ ids,
+                                                     const float *__restrict__ wts,
+                                                     float *__restrict__ out, int n_tok, int k,
+                                                     int n_expert, int in_dim, int out_dim,
+                                                     int n_wg) {
+#pragma clang fp contract(off)
+    extern __shared__ uint4 xlds[];
+    __shared__ MoeRoute rt;
+    __shared__ float ys[NW][kFusedPairs];
+    const int lane = threadIdx.x & 63, kk = lane & 7, ks = lane >> 3;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int P = n_tok * k;
+    const int nunits = F::units(in_dim), ncols = (nunits + 7) >> 3;
+    const uint32_t slot_fields = (uint32_t)ncols * F::kXF * 64;
+
+    int e_p = -1;
+    float w_p = 0.f;
+    if ((int)threadIdx.x < P) {
+        e_p = ids[threadIdx.x];
+        w_p = wts[threadIdx.x];
+    }
+    // h rows of all P slots (rows past the valid slots are unused)
+    MoeGroups<F, GPT> xg;
+    moe_load_groups<F, NW, GPT>(xg, h, P, in_dim);
+    moe_route_lds(rt, e_p, w_p, P, k, n_expert);
+
+    const int r0 = blockIdx.x;
+    const int nrows = (out_dim - r0 + n_wg - 1) / n_wg;
+    const int my_rows = nrows > wv ? (nrows - wv + NW - 1) / NW : 0;
+    const int n_chunks = __builtin_amdgcn_readfirstlane(rt.n_chunks);
+    const int T = my_rows * n_chunks * ncols;
+    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(down, 0);
+
+    typename F::Slice bw[PD];
+    int lj = 0, lch = 0, lc = 0;
+    int le = n_chunks > 0 ? __builtin_amdgcn_readfirstlane(rt.chunk_e[0]) : 0;
+    auto load_next = [&](typename F::Slice &sw, int lt) {
+        const bool ok = lt < T;
+        const int row = min(r0 + n_wg * (wv + NW * lj), out_dim - 1);
+        const __amdgpu_buffer_rsrc_t rw = ok ? make_rsrc(down + (size_t)le * stride, stride) : rnull;
+        F::load(sw, rw, row, min(lc * 8 + ks, nunits - 1), kk, in_dim, out_dim);
+        if (++lc == ncols) {
+            lc = 0;
+            if (++lch == n_chunks) {
+                lch = 0;
+                lj++;
+            }
+            le = __builtin_amdgcn_readfirstlane(rt.chunk_e[lch]);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < PD - 1; j++) load_next(bw[j], j);
+    __builtin_amdgcn_sched_barrier(0);
+    moe_store_groups<F, NW, GPT>(xg, xlds, P, in_dim);
+    __syncthreads();
+
+    int cj = 0, cch = 0, cc = 0;
+    float acc[kChunk];
+#pragma unroll
+    for (int q = 0; q < kChunk; q++) acc[q] = 0.f;
+    for (int t0 = 0; t0 < T; t0 += PD) {
+#pragma unroll
+        for (int jj = 0; jj < PD; jj++) {
+            const int t = t0 + jj;
+            load_next(bw[(jj + PD - 1) % PD], t + PD - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (t < T) {
+                const int n = __builtin_amdgcn_readfirstlane(rt.chunk_n[cch]);
+                const int s0 = __builtin_amdgcn_readfirstlane(rt.chunk_s0[cch]);
+                const int unit = cc * 8 + ks;
+                const bool okl = unit < nunits && F::valid(unit, kk, in_dim);
+#pragma unroll
+                for (int q = 0; q < kChunk; q++) {
+                    if (q < n) {
+                        const uint4 *bx = xlds + (s0 + q) * slot_fields + cc * F::kXF * 64 + lane;
+                        XSlice xs;
+                        xs.hlo = bx[0];
+                        xs.llo = bx[64];
+                        xs.meta = bx[128];
+                        if (F::kXF == 5) {
+                            xs.hhi = bx[192];
+                            xs.lhi = bx[256];
+                        }
+                        const float d = F::dot(bw[jj], kk, xs);
+                        acc[q] += okl ? d : 0.f;
+                    }
+                }
+                if (++cc == ncols) {
+#pragma unroll
+                    for (int q = 0; q < kChunk; q++) {
+                        if (q < n) {
+                            const float y = wave_sum_dpp(acc[q]);
+                            if (lane == 0) ys[wv][s0 + q] = y;
+                        }
+                        acc[q] = 0.f;
+                    }
+                    cc = 0;
+                    if (++cch == n_chunks) {
+                        // row done: weighted sum into out in i order
+                        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                        const int row = r0 + n_wg * (wv + NW * cj);
+                        if (lane < n_tok) {
+                            float* o = out + (size_t)lane * out_dim + row;
+                            float v = *o;
+                            for (int i = 0; i < k; i++) {
+                                const int sl = rt.slot_of[lane * k + i];
+                                if (sl >= 0) {
+                                    const float prod = rt.wt[lane * k + i] * ys[wv][sl];
+                                    v = v + prod;
+                                }
+                            }
+                            *o = v;
+                        }
+                        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                        cch = 0;
+                        cj++;
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// LDS (dynamic part) of the two fused kernels.
+template <class F>
+static size_t moe_x_lds(int rows, int in_dim) {
+    const int ncols = ((in_dim + F::kEPU - 1) / F::kEPU + 7) >> 3;
+    return ((size_t)rows * ncols + 1) * F::kXF * 1024;
+}
+template <class F>
+static int moe_gpt(int rows, int in_dim, int nw) {
+    const int ncols = ((in_dim + F::kEPU - 1) / F::kEPU + 7) >> 3;
+    const int groups = rows * ncols * 64 * (F::kXF == 5 ? 2 : 1);
+    const int g = (groups + 64 * nw - 1) / (64 * nw);
+    return g <= 1 ? 1 : g <= 2 ? 2 : g <= 4 ? 4 : 0;
+}
+constexpr size_t kMoeMaxLds = 152 * 1024;
+
+template <class F, int NW, int PD, int GPT>
+static hipError_t gu_go(const uint8_t *gate, const uint8_t *up, size_t stride, const float *x,
+                        const int *ids, const float *wts, float *h, int n_tok, int k, int n_expert,
+                        int n_embd, int n_ff, float clamp, int n_wg, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_moe_gu<F, NW, PD, GPT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMoeMaxLds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    n_wg = min(n_wg, n_ff);
+    k_moe_gu<F, NW, PD, GPT><<<(unsigned)n_wg, 64 * NW, moe_x_lds<F>(n_tok, n_embd), s>>>(
+        gate, up, (uint32_t)stride, x, ids, wts, h, n_tok, k, n_expert, n_embd, n_ff, clamp, n_wg);
+    return hipGetLastError();
+}
+
+template <class F, int NW, int PD, int GPT>
+static hipError_t down_go(const uint8_t *down, size_t stride, const float *h, const int *ids,
+                          const float *wts, float *out, int n_tok, int k, int n_expert, int n_embd,
+                          int n_ff, int n_wg, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_moe_down<F, NW, PD, GPT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMoeMaxLds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    n_wg = min(n_wg, n_embd);
+    k_moe_down<F, NW, PD, GPT><<<(unsigned)n_wg, 64 * NW, moe_x_lds<F>(n_tok * k, n_ff), s>>>(
+        down, (uint32_t)stride, h, ids, wts, out, n_tok, k, n_expert, n_ff, n_embd, n_wg);
+    return hipGetLastError();
+}
+
+constexpr int kMoeNW = 16, kMoePD = 2;
+
+template <class F>
+static bool gu_fits(int n_tok, int n_embd) {
+    return moe_x_lds<F>(n_tok, n_embd) <= kMoeMaxLds && moe_gpt<F>(n_tok, n_embd, kMoeNW) != 0;
+}
+template <class F>
+static bool down_fits(int P, int n_ff) {
+    return moe_x_lds<F>(P, n_ff) <= kMoeMaxLds && moe_gpt<F>(P, n_ff, kMoeNW) != 0;
+}
+
+template <class F>
+static hipError_t gu_launch(const uint8_t *gate, const uint8_t *up, size_t stride, const float *x,
+                            const int *ids, const float *wts, float *h, int n_tok, int k,
+                            int n_expert, int n_embd, int n_ff, float clamp, hipStream_t s) {
+    const int n_wg = device_cus();
+    switch (moe_gpt<F>(n_tok, n_embd, kMoeNW)) {
+    case 1: return gu_go<F, kMoeNW, kMoePD, 1>(gate, up, stride, x, ids, wts, h, n_tok, k, n_expert, n_embd, n_ff, clamp, n_wg, s);
+    case 2: return gu_go<F, kMoeNW, kMoePD, 2>(gate, up, stride, x, ids, wts, h, n_tok, k, n_expert, n_embd, n_ff, clamp, n_wg, s);
+    case 4: return gu_go<F, kMoeNW, kMoePD, 4>(gate, up, stride, x, ids, wts, h, n_tok, k, n_expert, n_embd, n_ff, clamp, n_wg, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <class F>
+static hipError_t down_launch(const uint8_t *down, size_t stride, const float *h, const int *ids,
+                              const float *wts, float *out, int n_tok, int k, int n_expert,
+                              int n_embd, int n_ff, hipStream_t s) {
+    const int n_wg = device_cus();
+    switch (moe_gpt<F>(n_tok * k, n_ff, kMoeNW)) {
+    case 1: return down_go<F, kMoeNW, kMoePD, 1>(down, stride, h, ids, wts, out, n_tok, k, n_expert, n_embd, n_ff, n_wg, s);
+    case 2: return down_go<F, kMoeNW, kMoePD, 2>(down, stride, h, ids, wts, out, n_tok, k, n_expert, n_embd, n_ff, n_wg, s);
+    case 4: return down_go<F, kMoeNW, kMoePD, 4>(down, stride, h, ids, wts, out, n_tok, k, n_expert, n_embd, n_ff, n_wg, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+#define MOE_FORMATS(X)                                                                             \
+    X(T_Q4_K, FQ4K) X(T_Q6_K, FQ6K) X(T_Q8_0, FQ8<false>) X(T_Q4_0, FQ8<true>) X(T_Q2_K, FQ2K)     \
+    X(T_IQ2_XXS, FIQ2XXS)
+
+static bool moe_fused_fits(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_embd, int n_ff,
+                           size_t gu_stride, size_t d_stride) {
+    if (n_tok * k > kFusedPairs || n_tok > 64) return false;
+    if (gu_stride >= ((size_t)1 << 31) || d_stride >= ((size_t)1 << 31)) return false;
+    bool a = false, b = false;
+#define X(T, F) if (dt_gu == T) a = gu_fits<F>(n_tok, n_embd); if (dt_d == T) b = down_fits<F>(n_tok * k, n_ff);
+    MOE_FORMATS(X)
+#undef X
+    return a && b;
+}
+
+static hipError_t moe_fused(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
+                            const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
+                            const int *ids, const float *wts, float *out, float *h, int n_tok,
+                            int k, int n_expert, int n_embd, int n_ff, float clamp, hipStream_t s) {
+    hipError_t e = hipErrorInvalidValue;
+#define X(T, F) if (dt_gu == T) e = gu_launch<F>(gate, up, gu_stride, x, ids, wts, h, n_tok, k, n_expert, n_embd, n_ff, clamp, s);
+    MOE_FORMATS(X)
+#undef X
+    if (e != hipSuccess) return e;
+    e = hipErrorInvalidValue;
+#define X(T, F) if (dt_d == T) e = down_launch<F>(down, d_stride, h, ids, wts, out, n_tok, k, n_expert, n_embd, n_ff, s);
+    MOE_FORMATS(X)
+#undef X
+    return e;
+}
+
 size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_expert,
                          int n_embd, int n_ff) {
     const size_t P = (size_t)n_tok * k;
@@ -133,6 +639,9 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
     const size_t xq2_bytes = gemv_scratch_bytes(dt_d, (int)P, n_ff);
     uint8_t *xq2 = take(xq2_bytes);
     float *yd = reinterpret_cast<float *>(take(P * n_embd * 4));
+    if (moe_fused_fits(dt_gu, dt_d, n_tok, k, n_embd, n_ff, gu_stride, d_stride))
+        return moe_fused(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x, ids, wts, out, hg,
+                         n_tok, k, n_expert, n_embd, n_ff, clamp, s);
     // at most min(n_expert, n_tok * k) experts are active
     const int grid_experts = (int)(P < (size_t)n_expert ? P : (size_t)n_expert);
 

@@ -100,7 +100,7 @@ def test_moe_validation(hip):
                        n_expert, k, G.Q4_K, G.Q4_K, 10.0)
 
 
-@pytest.mark.parametrize("n_tok", [1, 8, 32])
+@pytest.mark.parametrize("n_tok", [1, 2, 3, 8, 32])
 def test_moe_c3_shapes(oracle, hip, n_tok):
     """C3 shapes with 16 experts (every expert's kernel path is the same as
     with 64); the oracle runs on up to 6 tokens (tokens are independent)."""
@@ -121,4 +121,31 @@ def test_moe_c3_shapes(oracle, hip, n_tok):
                       ids[toks], w[toks], len(toks), n_embd, n_ff, n_expert, k, G.Q4_K, G.Q4_K)
     err = rel_err(got.reshape(n_tok, n_embd)[toks], want.reshape(len(toks), n_embd))
     print(f"moe C3 T={n_tok}: rel err {err:.3e}")
+    assert err <= REL_TOL
+
+
+@pytest.mark.parametrize("n_tok,k,dup", [(4, 7, False), (4, 7, True), (4, 8, True), (2, 5, True),
+                                         (6, 4, True)])
+def test_moe_fused_boundary_and_duplicates(oracle, hip, n_tok, k, dup):
+    """n_tok * k pairs up to 32 with all slots in LDS take the two-launch
+    fused path (routing in every workgroup, SwiGLU and the weighted sum in
+    the GEMV epilogues); (4, 8) at n_ff 256 needs more LDS than allowed and
+    takes the multi-launch path. `dup` makes a token pick one expert twice
+    and puts six pairs on expert 0 (more slots than one pass of 4)."""
+    n_embd, n_ff, n_expert = 512, 256, 9
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.Q4_K, G.Q6_K,
+                                          91 + n_tok + k)
+    if dup:
+        ids[0, 1] = ids[0, 0]
+        flat = ids.reshape(-1)
+        flat[: min(6, flat.size)] = 0
+    w[n_tok - 1, 0] = 0.0
+    base = synth.activations(n_tok, n_embd, 8).reshape(-1)
+    want = run_oracle(oracle, base, x, gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                      G.Q4_K, G.Q6_K)
+    got = base.copy()
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   G.Q4_K, G.Q6_K, 10.0)
+    err = rel_err(got - base, want - base)
+    print(f"moe fused boundary T={n_tok} k={k} dup={dup}: rel err {err:.3e}")
     assert err <= REL_TOL
