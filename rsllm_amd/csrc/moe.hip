@@ -94,18 +94,17 @@ __global__ __launch_bounds__(256) void k_moe_accumulate(float *__restrict__ out,
 
 
 // ---- fused path for a few tokens (decode) -----------------------------------
-// For n_tok * k <= kFusedPairs the layer is two launches:
-//   k_moe_gu:   every workgroup routes the (t, i) pairs in LDS, quantises x of
-//               all tokens into LDS, then streams gate and up rows; the
-//               epilogue of a (row, expert) applies the clamp and SwiGLU and
-//               writes h[slot, row];
-//   k_moe_down: routes again (same result), quantises h of all slots into
-//               LDS, streams down rows; the epilogue of a row adds
-//               w[t, i] * y[slot(t, i), row] into out[t, row] in i order.
-// Rows are dealt as in k_gemv1 (workgroup b owns rows b + n_wg * l, a
-// wavefront streams whole rows); a row's tiles walk the active experts
-// ("chunks" of at most kChunk slots of one expert), PD tiles in flight, each
-// expert's weights read once per row for all its slots.
+// For n_tok * k <= kFusedPairs (and x, h fitting in LDS) the layer is two
+// launches of k_moe_fused:
+//   gate/up: every workgroup routes the (t, i) pairs in LDS, quantises x of
+//            all tokens into LDS, streams gate and up rows, and writes
+//            h[slot, row] = SwiGLU with the pre-activation clamp;
+//   down:    routes again (same result), quantises h of all slots into LDS,
+//            streams down rows, and adds w[t, i] * y[slot(t, i), row] into
+//            out[t, row] in i order.
+// The active experts are walked as "chunks" of at most kChunk slots of one
+// expert, so each expert row is read once for all of its slots. Pairs that
+// pick the same expert twice are separate slots, as in the reference.
 constexpr int kFusedPairs = 32;
 constexpr int kChunk = 4;
 
@@ -233,144 +232,35 @@ __device__ __forceinline__ void moe_store_groups(const MoeGroups<F, GPT> &g, uin
     }
 }
 
-// Gate/up. Tile = (row r, chunk ch, column c): one gate and one up slice.
-template <class F, int NW, int PD, int GPT>
-__global__ __launch_bounds__(64 * NW) void k_moe_gu(const uint8_t *__restrict__ gate,
-                                                   const uint8_t *__restrict__ up,
-                                                   uint32_t stride, const float *__restrict__ x,
-                                                   const int *__restrict__ ids,
-                                                   const float *__restrict__ wts,
-                                                   float *__restrict__ h, int n_tok, int k,
-                                                   int n_expert, int in_dim, int out_dim,
-                                                   float clamp, int n_wg) {
-    extern __shared__ uint4 xlds[];
-    __shared__ MoeRoute rt;
-    const int lane = threadIdx.x & 63, kk = lane & 7, ks = lane >> 3;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int P = n_tok * k;
-    const int nunits = F::units(in_dim), ncols = (nunits + 7) >> 3;
-    const uint32_t tok_fields = (uint32_t)ncols * F::kXF * 64;  // uint4 per token in LDS
-
-    int e_p = -1;
-    float w_p = 0.f;
-    if ((int)threadIdx.x < P) {
-        e_p = ids[threadIdx.x];
-        w_p = wts[threadIdx.x];
-    }
-    MoeGroups<F, GPT> xg;
-    moe_load_groups<F, NW, GPT>(xg, x, n_tok, in_dim);
-    moe_route_lds(rt, e_p, w_p, P, k, n_expert);
-
-    const int r0 = blockIdx.x;
-    const int nrows = (out_dim - r0 + n_wg - 1) / n_wg;
-    const int my_rows = nrows > wv ? (nrows - wv + NW - 1) / NW : 0;
-    const int n_chunks = __builtin_amdgcn_readfirstlane(rt.n_chunks);
-    const int T = my_rows * n_chunks * ncols;
-    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(gate, 0);
-
-    typename F::Slice bg[PD], bu[PD];
-    // load cursor: tile index lt -> (lj, lch, lc)
-    int lj = 0, lch = 0, lc = 0;
-    int le = n_chunks > 0 ? __builtin_amdgcn_readfirstlane(rt.chunk_e[0]) : 0;
-    auto load_next = [&](typename F::Slice &sg, typename F::Slice &su, int lt) {
-        const bool ok = lt < T;
-        const int row = min(r0 + n_wg * (wv + NW * lj), out_dim - 1);
-        const size_t base = (size_t)le * stride;
-        const __amdgpu_buffer_rsrc_t rg = ok ? make_rsrc(gate + base, stride) : rnull;
-        const __amdgpu_buffer_rsrc_t ru = ok ? make_rsrc(up + base, stride) : rnull;
-        const int unit = min(lc * 8 + ks, nunits - 1);
-        F::load(sg, rg, row, unit, kk, in_dim, out_dim);
-        F::load(su, ru, row, unit, kk, in_dim, out_dim);
-        if (++lc == ncols) {
-            lc = 0;
-            if (++lch == n_chunks) {
-                lch = 0;
-                lj++;
-            }
-            le = __builtin_amdgcn_readfirstlane(rt.chunk_e[lch]);
-        }
-    };
-#pragma unroll
-    for (int j = 0; j < PD - 1; j++) load_next(bg[j], bu[j], j);
-    __builtin_amdgcn_sched_barrier(0);
-    moe_store_groups<F, NW, GPT>(xg, xlds, n_tok, in_dim);
-    __syncthreads();
-
-    // compute cursor
-    int cj = 0, cch = 0, cc = 0;
-    float ag[kChunk], au[kChunk];
-#pragma unroll
-    for (int q = 0; q < kChunk; q++) ag[q] = au[q] = 0.f;
-    for (int t0 = 0; t0 < T; t0 += PD) {
-#pragma unroll
-        for (int jj = 0; jj < PD; jj++) {
-            const int t = t0 + jj;
-            load_next(bg[(jj + PD - 1) % PD], bu[(jj + PD - 1) % PD], t + PD - 1);
-            __builtin_amdgcn_sched_barrier(0);
-            if (t < T) {
-                const int n = __builtin_amdgcn_readfirstlane(rt.chunk_n[cch]);
-                const int s0 = __builtin_amdgcn_readfirstlane(rt.chunk_s0[cch]);
-                const int unit = cc * 8 + ks;
-                const bool okl = unit < nunits && F::valid(unit, kk, in_dim);
-#pragma unroll
-                for (int q = 0; q < kChunk; q++) {
-                    if (q < n) {
-                        const int tok = __builtin_amdgcn_readfirstlane(rt.slot_tok[s0 + q]);
-                        const uint4 *bx = xlds + tok * tok_fields + cc * F::kXF * 64 + lane;
-                        XSlice xs;
-                        xs.hlo = bx[0];
-                        xs.llo = bx[64];
-                        xs.meta = bx[128];
-                        if (F::kXF == 5) {
-                            xs.hhi = bx[192];
-                            xs.lhi = bx[256];
-                        }
-                        const float dg = F::dot(bg[jj], kk, xs), du = F::dot(bu[jj], kk, xs);
-                        ag[q] += okl ? dg : 0.f;
-                        au[q] += okl ? du : 0.f;
-                    }
-                }
-                if (++cc == ncols) {
-                    const int row = r0 + n_wg * (wv + NW * cj);
-#pragma unroll
-                    for (int q = 0; q < kChunk; q++) {
-                        if (q < n) {
-                            const float g = wave_sum_dpp(ag[q]), u = wave_sum_dpp(au[q]);
-                            if (lane == 0) h[(size_t)(s0 + q) * out_dim + row] = swiglu_clamped(g, u, clamp);
-                        }
-                        ag[q] = au[q] = 0.f;
-                    }
-                    cc = 0;
-                    if (++cch == n_chunks) {
-                        cch = 0;
-                        cj++;
-                    }
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-}
-
-// Down. Tile = (row r, chunk ch, column c). After a row's last tile, lanes
-// t < n_tok add w[t, i] * y[slot(t, i)] into out[t, r] in i order.
-template <class F, int NW, int PD, int GPT>
-__global__ __launch_bounds__(64 * NW) void k_moe_down(const uint8_t *__restrict__ down,
-                                                     uint32_t stride, const float *__restrict__ h,
-                                                     const int *__restrict__ ids,
-                                                     const float *__restrict__ wts,
-                                                     float *__restrict__ out, int n_tok, int k,
-                                                     int n_expert, int in_dim, int out_dim,
-                                                     int n_wg) {
+// One kernel body for both halves (GU = true: gate and up; false: down).
+// Workgroup b owns rows b + n_wg * l (l < nrows). Its tiles (chunk ch, row l,
+// column c), chunk-major, are split into NW contiguous runs, one per
+// wavefront: within a run the expert changes only at chunk boundaries and
+// consecutive tiles are consecutive bytes of one expert's matrix. PD tiles
+// are in flight. When a (chunk, row) completes, the values of the chunk's
+// slots go to LDS (stage[l][slot]); after the stream and a barrier the
+// workgroup writes them out:
+//   GU:    h[slot, row] = silu(min(g, c)) * clamp(u, -c, c)  (per slot),
+//   down:  out[t, row] += w[t, i] * y[slot(t, i), row]  in i order  (per token).
+template <class F, int NW, int PD, int GPT, bool GU>
+__global__ __launch_bounds__(64 * NW) void k_moe_fused(
+    const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, uint32_t stride,
+    const float *__restrict__ src, int src_rows, const int *__restrict__ ids,
+    const float *__restrict__ wts, float *__restrict__ dst, int n_tok, int k, int n_expert,
+    int in_dim, int out_dim, float clamp, int n_wg) {
 #pragma clang fp contract(off)
     extern __shared__ uint4 xlds[];
     __shared__ MoeRoute rt;
-    __shared__ float ys[NW][kFusedPairs];
     const int lane = threadIdx.x & 63, kk = lane & 7, ks = lane >> 3;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int P = n_tok * k;
     const int nunits = F::units(in_dim), ncols = (nunits + 7) >> 3;
-    const uint32_t slot_fields = (uint32_t)ncols * F::kXF * 64;
+    const uint32_t row_fields = (uint32_t)ncols * F::kXF * 64;  // uint4 per LDS x row
+    const int r0 = blockIdx.x;
+    const int nrows = (out_dim - r0 + n_wg - 1) / n_wg;
+    // stage[l][slot] (GU: [l][slot] holds g, [l][P + slot] u)
+    float *stage = reinterpret_cast<float *>(xlds + ((size_t)src_rows * ncols + 1) * F::kXF * 64);
+    constexpr int kVals = GU ? 2 : 1;
 
     int e_p = -1;
     float w_p = 0.f;
@@ -378,60 +268,72 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const uint8_t *__restrict_
         e_p = ids[threadIdx.x];
         w_p = wts[threadIdx.x];
     }
-    // h rows of all P slots (rows past the valid slots are unused)
     MoeGroups<F, GPT> xg;
-    moe_load_groups<F, NW, GPT>(xg, h, P, in_dim);
+    moe_load_groups<F, NW, GPT>(xg, src, src_rows, in_dim);
     moe_route_lds(rt, e_p, w_p, P, k, n_expert);
 
-    const int r0 = blockIdx.x;
-    const int nrows = (out_dim - r0 + n_wg - 1) / n_wg;
-    const int my_rows = nrows > wv ? (nrows - wv + NW - 1) / NW : 0;
     const int n_chunks = __builtin_amdgcn_readfirstlane(rt.n_chunks);
-    const int T = my_rows * n_chunks * ncols;
-    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(down, 0);
+    const int per_chunk = nrows * ncols;
+    const int W = n_chunks * per_chunk;
+    const int t_beg = (int)(((long long)W * wv) / NW), t_end = (int)(((long long)W * (wv + 1)) / NW);
+    const int T = t_end - t_beg;
+    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(w0, 0);
 
-    typename F::Slice bw[PD];
-    int lj = 0, lch = 0, lc = 0;
-    int le = n_chunks > 0 ? __builtin_amdgcn_readfirstlane(rt.chunk_e[0]) : 0;
-    auto load_next = [&](typename F::Slice &sw, int lt) {
+    typename F::Slice b0[PD], b1[PD];
+    // load cursor at tile t_beg
+    int lch = T > 0 ? t_beg / per_chunk : 0;
+    int ll = T > 0 ? (t_beg - lch * per_chunk) / ncols : 0;
+    int lc = T > 0 ? t_beg - lch * per_chunk - ll * ncols : 0;
+    int le = T > 0 ? __builtin_amdgcn_readfirstlane(rt.chunk_e[lch]) : 0;
+    auto load_next = [&](typename F::Slice &s0_, typename F::Slice &s1_, int lt) {
         const bool ok = lt < T;
-        const int row = min(r0 + n_wg * (wv + NW * lj), out_dim - 1);
-        const __amdgpu_buffer_rsrc_t rw = ok ? make_rsrc(down + (size_t)le * stride, stride) : rnull;
-        F::load(sw, rw, row, min(lc * 8 + ks, nunits - 1), kk, in_dim, out_dim);
+        const size_t base = (size_t)le * stride;
+        const int unit = min(lc * 8 + ks, nunits - 1);
+        const int row = min(r0 + n_wg * ll, out_dim - 1);
+        F::load(s0_, ok ? make_rsrc(w0 + base, stride) : rnull, row, unit, kk, in_dim, out_dim);
+        if (GU) F::load(s1_, ok ? make_rsrc(w1 + base, stride) : rnull, row, unit, kk, in_dim, out_dim);
         if (++lc == ncols) {
             lc = 0;
-            if (++lch == n_chunks) {
-                lch = 0;
-                lj++;
+            if (++ll == nrows) {
+                ll = 0;
+                if (++lch < n_chunks) le = __builtin_amdgcn_readfirstlane(rt.chunk_e[lch]);
             }
-            le = __builtin_amdgcn_readfirstlane(rt.chunk_e[lch]);
         }
     };
 #pragma unroll
-    for (int j = 0; j < PD - 1; j++) load_next(bw[j], j);
+    for (int j = 0; j < PD - 1; j++) load_next(b0[j], b1[j], j);
     __builtin_amdgcn_sched_barrier(0);
-    moe_store_groups<F, NW, GPT>(xg, xlds, P, in_dim);
+    moe_store_groups<F, NW, GPT>(xg, xlds, src_rows, in_dim);
     __syncthreads();
 
-    int cj = 0, cch = 0, cc = 0;
-    float acc[kChunk];
+    // compute cursor
+    int cch = lch, cl = 0, cc = 0;
+    {
+        const int c0 = T > 0 ? t_beg / per_chunk : 0;
+        cch = c0;
+        cl = T > 0 ? (t_beg - c0 * per_chunk) / ncols : 0;
+        cc = T > 0 ? t_beg - c0 * per_chunk - cl * ncols : 0;
+    }
+    int cn = T > 0 ? __builtin_amdgcn_readfirstlane(rt.chunk_n[cch]) : 0;
+    int cs0 = T > 0 ? __builtin_amdgcn_readfirstlane(rt.chunk_s0[cch]) : 0;
+    float a0[kChunk], a1[kChunk];
 #pragma unroll
-    for (int q = 0; q < kChunk; q++) acc[q] = 0.f;
+    for (int q = 0; q < kChunk; q++) a0[q] = a1[q] = 0.f;
     for (int t0 = 0; t0 < T; t0 += PD) {
 #pragma unroll
         for (int jj = 0; jj < PD; jj++) {
             const int t = t0 + jj;
-            load_next(bw[(jj + PD - 1) % PD], t + PD - 1);
+            load_next(b0[(jj + PD - 1) % PD], b1[(jj + PD - 1) % PD], t + PD - 1);
             __builtin_amdgcn_sched_barrier(0);
             if (t < T) {
-                const int n = __builtin_amdgcn_readfirstlane(rt.chunk_n[cch]);
-                const int s0 = __builtin_amdgcn_readfirstlane(rt.chunk_s0[cch]);
                 const int unit = cc * 8 + ks;
                 const bool okl = unit < nunits && F::valid(unit, kk, in_dim);
 #pragma unroll
                 for (int q = 0; q < kChunk; q++) {
-                    if (q < n) {
-                        const uint4 *bx = xlds + (s0 + q) * slot_fields + cc * F::kXF * 64 + lane;
+                    if (q < cn) {
+                        // GU: x row = the slot's token; down: x row = the slot
+                        const int xr = GU ? __builtin_amdgcn_readfirstlane(rt.slot_tok[cs0 + q]) : cs0 + q;
+                        const uint4 *bx = xlds + xr * row_fields + cc * F::kXF * 64 + lane;
                         XSlice xs;
                         xs.hlo = bx[0];
                         xs.llo = bx[64];
@@ -440,43 +342,63 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const uint8_t *__restrict_
                             xs.hhi = bx[192];
                             xs.lhi = bx[256];
                         }
-                        const float d = F::dot(bw[jj], kk, xs);
-                        acc[q] += okl ? d : 0.f;
+                        const float d0 = F::dot(b0[jj], kk, xs);
+                        a0[q] += okl ? d0 : 0.f;
+                        if (GU) {
+                            const float d1 = F::dot(b1[jj], kk, xs);
+                            a1[q] += okl ? d1 : 0.f;
+                        }
                     }
                 }
                 if (++cc == ncols) {
 #pragma unroll
                     for (int q = 0; q < kChunk; q++) {
-                        if (q < n) {
-                            const float y = wave_sum_dpp(acc[q]);
-                            if (lane == 0) ys[wv][s0 + q] = y;
+                        if (q < cn) {
+                            const float v0 = wave_sum_dpp(a0[q]);
+                            const float v1 = GU ? wave_sum_dpp(a1[q]) : 0.f;
+                            if (lane == 0) {
+                                stage[(size_t)cl * kVals * P + cs0 + q] = v0;
+                                if (GU) stage[(size_t)cl * kVals * P + P + cs0 + q] = v1;
+                            }
                         }
-                        acc[q] = 0.f;
+                        a0[q] = a1[q] = 0.f;
                     }
                     cc = 0;
-                    if (++cch == n_chunks) {
-                        // row done: weighted sum into out in i order
-                        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                        const int row = r0 + n_wg * (wv + NW * cj);
-                        if (lane < n_tok) {
-                            float* o = out + (size_t)lane * out_dim + row;
-                            float v = *o;
-                            for (int i = 0; i < k; i++) {
-                                const int sl = rt.slot_of[lane * k + i];
-                                if (sl >= 0) {
-                                    const float prod = rt.wt[lane * k + i] * ys[wv][sl];
-                                    v = v + prod;
-                                }
-                            }
-                            *o = v;
+                    if (++cl == nrows) {
+                        cl = 0;
+                        if (++cch < n_chunks) {
+                            cn = __builtin_amdgcn_readfirstlane(rt.chunk_n[cch]);
+                            cs0 = __builtin_amdgcn_readfirstlane(rt.chunk_s0[cch]);
                         }
-                        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                        cch = 0;
-                        cj++;
                     }
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    __syncthreads();
+    if (n_chunks == 0) return;
+    if (GU) {
+        // h[slot, row] for the valid slots (a slot belongs to exactly one chunk)
+        const int n_slots = rt.chunk_s0[n_chunks - 1] + rt.chunk_n[n_chunks - 1];
+        for (int i = threadIdx.x; i < nrows * n_slots; i += 64 * NW) {
+            const int l = i / n_slots, sl = i % n_slots;
+            const float g = stage[(size_t)l * 2 * P + sl], u = stage[(size_t)l * 2 * P + P + sl];
+            dst[(size_t)sl * out_dim + r0 + n_wg * l] = swiglu_clamped(g, u, clamp);
+        }
+    } else {
+        for (int i = threadIdx.x; i < nrows * n_tok; i += 64 * NW) {
+            const int l = i / n_tok, t = i % n_tok;
+            float *o = dst + (size_t)t * out_dim + r0 + n_wg * l;
+            float v = *o;
+            for (int q = 0; q < k; q++) {
+                const int sl = rt.slot_of[t * k + q];
+                if (sl >= 0) {
+                    const float prod = rt.wt[t * k + q] * stage[(size_t)l * P + sl];
+                    v = v + prod;
+                }
+            }
+            *o = v;
         }
     }
 }
@@ -494,51 +416,63 @@ static int moe_gpt(int rows, int in_dim, int nw) {
     const int g = (groups + 64 * nw - 1) / (64 * nw);
     return g <= 1 ? 1 : g <= 2 ? 2 : g <= 4 ? 4 : 0;
 }
+// LDS of k_moe_fused: the quantised x rows plus one spare column, then the
+// stage of (rows per workgroup) x P values (x 2 for gate/up).
+template <class F>
+static size_t moe_fused_lds(int src_rows, int in_dim, int out_dim, int n_wg, int P, bool gu) {
+    const int rows_wg = (out_dim + n_wg - 1) / n_wg;
+    return moe_x_lds<F>(src_rows, in_dim) + (size_t)rows_wg * P * (gu ? 2 : 1) * 4;
+}
 constexpr size_t kMoeMaxLds = 152 * 1024;
+
+template <class F, int NW, int PD, int GPT, bool GU>
+static hipError_t fused_go(const uint8_t *w0, const uint8_t *w1, size_t stride, const float *src,
+                           int src_rows, const int *ids, const float *wts, float *dst, int n_tok,
+                           int k, int n_expert, int in_dim, int out_dim, float clamp, int n_wg,
+                           hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_moe_fused<F, NW, PD, GPT, GU>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMoeMaxLds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    n_wg = min(n_wg, out_dim);
+    const size_t lds = moe_fused_lds<F>(src_rows, in_dim, out_dim, n_wg, n_tok * k, GU);
+    k_moe_fused<F, NW, PD, GPT, GU><<<(unsigned)n_wg, 64 * NW, lds, s>>>(
+        w0, w1, (uint32_t)stride, src, src_rows, ids, wts, dst, n_tok, k, n_expert, in_dim,
+        out_dim, clamp, n_wg);
+    return hipGetLastError();
+}
 
 template <class F, int NW, int PD, int GPT>
 static hipError_t gu_go(const uint8_t *gate, const uint8_t *up, size_t stride, const float *x,
                         const int *ids, const float *wts, float *h, int n_tok, int k, int n_expert,
                         int n_embd, int n_ff, float clamp, int n_wg, hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_moe_gu<F, NW, PD, GPT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMoeMaxLds);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
-    n_wg = min(n_wg, n_ff);
-    k_moe_gu<F, NW, PD, GPT><<<(unsigned)n_wg, 64 * NW, moe_x_lds<F>(n_tok, n_embd), s>>>(
-        gate, up, (uint32_t)stride, x, ids, wts, h, n_tok, k, n_expert, n_embd, n_ff, clamp, n_wg);
-    return hipGetLastError();
+    return fused_go<F, NW, PD, GPT, true>(gate, up, stride, x, n_tok, ids, wts, h, n_tok, k,
+                                          n_expert, n_embd, n_ff, clamp, n_wg, s);
 }
 
 template <class F, int NW, int PD, int GPT>
 static hipError_t down_go(const uint8_t *down, size_t stride, const float *h, const int *ids,
                           const float *wts, float *out, int n_tok, int k, int n_expert, int n_embd,
                           int n_ff, int n_wg, hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_moe_down<F, NW, PD, GPT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMoeMaxLds);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
-    n_wg = min(n_wg, n_embd);
-    k_moe_down<F, NW, PD, GPT><<<(unsigned)n_wg, 64 * NW, moe_x_lds<F>(n_tok * k, n_ff), s>>>(
-        down, (uint32_t)stride, h, ids, wts, out, n_tok, k, n_expert, n_ff, n_embd, n_wg);
-    return hipGetLastError();
+    return fused_go<F, NW, PD, GPT, false>(down, down, stride, h, n_tok * k, ids, wts, out, n_tok,
+                                           k, n_expert, n_ff, n_embd, 0.f, n_wg, s);
 }
 
 constexpr int kMoeNW = 16, kMoePD = 2;
 
 template <class F>
-static bool gu_fits(int n_tok, int n_embd) {
-    return moe_x_lds<F>(n_tok, n_embd) <= kMoeMaxLds && moe_gpt<F>(n_tok, n_embd, kMoeNW) != 0;
+static bool gu_fits(int n_tok, int k, int n_embd, int n_ff) {
+    return moe_fused_lds<F>(n_tok, n_embd, n_ff, min(device_cus(), n_ff), n_tok * k, true) <=
+               kMoeMaxLds &&
+           moe_gpt<F>(n_tok, n_embd, kMoeNW) != 0;
 }
 template <class F>
-static bool down_fits(int P, int n_ff) {
-    return moe_x_lds<F>(P, n_ff) <= kMoeMaxLds && moe_gpt<F>(P, n_ff, kMoeNW) != 0;
+static bool down_fits(int P, int n_ff, int n_embd) {
+    return moe_fused_lds<F>(P, n_ff, n_embd, min(device_cus(), n_embd), P, false) <= kMoeMaxLds &&
+           moe_gpt<F>(P, n_ff, kMoeNW) != 0;
 }
 
 template <class F>
@@ -576,7 +510,7 @@ static bool moe_fused_fits(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int 
     if (n_tok * k > kFusedPairs || n_tok > 64) return false;
     if (gu_stride >= ((size_t)1 << 31) || d_stride >= ((size_t)1 << 31)) return false;
     bool a = false, b = false;
-#define X(T, F) if (dt_gu == T) a = gu_fits<F>(n_tok, n_embd); if (dt_d == T) b = down_fits<F>(n_tok * k, n_ff);
+#define X(T, F) if (dt_gu == T) a = gu_fits<F>(n_tok, k, n_embd, n_ff); if (dt_d == T) b = down_fits<F>(n_tok * k, n_ff, n_embd);
     MOE_FORMATS(X)
 #undef X
     return a && b;
