@@ -117,11 +117,13 @@ int rsllm_hip_matmul_quant_f32_dev(float *out, size_t out_len, const uint8_t *we
  * x across several weight matrices of the same dtype and in_dim (e.g. an
  * FFN's gate and up projections) or time the GEMV alone. No reference
  * counterpart: matmul_quant_f32 takes f32 x directly. x is re-expressed per
- * 16-element group as s * (128 h + l) with int8 limbs (about 15 bits
+ * 16-element group as s * (256 h + l) with int8 limbs (about 16 bits
  * relative to the group's largest element) in a dtype-specific lane-major
  * layout of rsllm_hip_xq_bytes(dtype, n_tok, in_dim) bytes.
  * rsllm_hip_matmul_prequant_dev is rsllm_hip_matmul_quant_f32_dev with xq in
- * place of x (same validation, x_len replaced by xq_len). */
+ * place of x (same validation, x_len replaced by xq_len). The products are
+ * the same; the summation order can differ from the one-shot call's kernel,
+ * so the two agree to a few ulp, not bit for bit. */
 size_t rsllm_hip_xq_bytes(uint32_t dtype, size_t n_tok, size_t in_dim);
 int rsllm_hip_quantize_x_dev(uint32_t dtype, const float *x, size_t x_len, size_t n_tok,
                              size_t in_dim, uint8_t *xq, size_t xq_len, rsllm_hip_stream_t stream);

@@ -178,32 +178,36 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv(const uint8_t *__restri
 // its arithmetic, so the waits before each tile's arithmetic leave the later
 // tiles in flight.
 //
-template <class F, int NW, int PD, int GPT>
+template <class F, int NW, int PD, int GPT, int BT = 1>
 __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w, uint32_t w_bytes,
                                                   const float *__restrict__ x,
                                                   float *__restrict__ y, int in_dim, int out_dim,
-                                                  int n_wg) {
+                                                  int n_wg, int n_tok) {
     extern __shared__ uint4 xl[];
     constexpr int kHalves = F::kXF == 5 ? 2 : 1;
     constexpr int kThreads = 64 * NW;
     const int lane = threadIdx.x & 63, k = lane & 7, ks = lane >> 3;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nunits = F::units(in_dim), ncols = (nunits + 7) >> 3;
-    const int n_groups = ncols * 64 * kHalves;
+    const int per_tok = ncols * 64 * kHalves;                           // groups per token
+    const int n_groups = per_tok * BT;
+    const uint32_t tok_fields = (uint32_t)ncols * F::kXF * 64;          // uint4 per token in LDS
     const int r0 = blockIdx.x;
     const int nrows = (out_dim - r0 + n_wg - 1) / n_wg;                 // this workgroup's rows
     const int my_rows = nrows > wv ? (nrows - wv + NW - 1) / NW : 0;   // this wavefront's rows
     const int T = my_rows * ncols;                                       // its tiles
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
     const __amdgpu_buffer_rsrc_t rnull = make_rsrc(w, 0);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)in_dim * 4u);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)n_tok * (uint32_t)in_dim * 4u);
 
-    auto group_elem = [&](int g) {
-        const int col = g / (64 * kHalves), r2 = g % (64 * kHalves);
+    // group g (token g / per_tok) -> first element offset in x, or -1
+    auto group_off = [&](int g) {
+        const int t = g / per_tok, rem = g - t * per_tok;
+        const int col = rem / (64 * kHalves), r2 = rem % (64 * kHalves);
         const int half = r2 >> 6, ln = r2 & 63;
         const int kk = ln & 7, unit = col * 8 + (ln >> 3);
-        const bool ok = g < n_groups && unit < nunits && F::valid(unit, kk, in_dim);
-        return ok ? (half ? F::elem_hi(unit, kk) : F::elem_lo(unit, kk)) : -1;
+        const bool ok = g < n_groups && t < n_tok && unit < nunits && F::valid(unit, kk, in_dim);
+        return ok ? t * in_dim + (half ? F::elem_hi(unit, kk) : F::elem_lo(unit, kk)) : -1;
     };
     auto row_of = [&](int j) { return r0 + n_wg * (wv + NW * j); };
     typename F::Slice buf[PD];
@@ -214,13 +218,14 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
         F::load(sl, r, min(row_of(j), out_dim - 1), unit, k, in_dim, out_dim);
     };
 
-    // Prologue: x loads, the first tiles, then quantisation into LDS. Group
+    // Prologue: x loads, the first tiles, then quantisation into LDS (token
+    // t's columns at t * tok_fields; tokens past n_tok quantise zeros). Group
     // indices past n_groups store into one spare column.
     uint4 xv[GPT][4];
 #pragma unroll
     for (int i = 0; i < GPT; i++) {
         if (wv * 64 + i * kThreads >= n_groups) continue;
-        const int e = group_elem(threadIdx.x + i * kThreads);
+        const int e = group_off(threadIdx.x + i * kThreads);
         const uint32_t off = e >= 0 ? (uint32_t)e * 4u : 0x80000000u;  // past the end: zeros
 #pragma unroll
         for (int q = 0; q < 4; q++) xv[i][q] = bload16(rx, off + 16u * q, 0);
@@ -245,16 +250,19 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
         quant_values(v, h, l, sc, sum);
         const int g = threadIdx.x + i * kThreads;
         const int gg = g < n_groups ? g : n_groups;
-        const int col = gg / (64 * kHalves), r2 = gg % (64 * kHalves);
+        const int t = gg / per_tok, rem = gg - t * per_tok;
+        const int col = rem / (64 * kHalves), r2 = rem % (64 * kHalves);
         const int half = r2 >> 6, ln = r2 & 63;
-        uint4 *b = xl + col * F::kXF * 64 + ln;
+        uint4 *b = xl + t * tok_fields + col * F::kXF * 64 + ln;
         b[(half ? 3 : 0) * 64] = h;
         b[(half ? 4 : 1) * 64] = l;
         reinterpret_cast<float2 *>(b + 2 * 64)[half] = make_float2(sc, sum);
     }
     __syncthreads();
 
-    float acc = 0.f;
+    float acc[BT];
+#pragma unroll
+    for (int tk = 0; tk < BT; tk++) acc[tk] = 0.f;
     int col = 0, j = 0;
     for (int t0 = 0; t0 < T; t0 += PD) {
 #pragma unroll
@@ -262,23 +270,29 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
             const int t = t0 + jj;
             load_tile(buf[(jj + PD - 1) % PD], t + PD - 1);
             __builtin_amdgcn_sched_barrier(0);
-            XSlice xs;
-            const uint4 *bx = xl + col * F::kXF * 64 + lane;
-            xs.hlo = bx[0];
-            xs.llo = bx[64];
-            xs.meta = bx[128];
-            if (F::kXF == 5) {
-                xs.hhi = bx[192];
-                xs.lhi = bx[256];
-            }
             const int unit = col * 8 + ks;
             const bool ok = t < T && unit < nunits && F::valid(unit, k, in_dim);
-            const float d = F::dot(buf[jj], k, xs);
-            acc += ok ? d : 0.f;
+#pragma unroll
+            for (int tk = 0; tk < BT; tk++) {
+                XSlice xs;
+                const uint4 *bx = xl + tk * tok_fields + col * F::kXF * 64 + lane;
+                xs.hlo = bx[0];
+                xs.llo = bx[64];
+                xs.meta = bx[128];
+                if (F::kXF == 5) {
+                    xs.hhi = bx[192];
+                    xs.lhi = bx[256];
+                }
+                const float d = F::dot(buf[jj], k, xs);
+                acc[tk] += ok ? d : 0.f;
+            }
             if (col == ncols - 1) {
-                const float tot = wave_sum_dpp(acc);
-                if (lane == 0 && t < T) y[row_of(j)] = tot;
-                acc = 0.f;
+#pragma unroll
+                for (int tk = 0; tk < BT; tk++) {
+                    const float tot = wave_sum_dpp(acc[tk]);
+                    if (lane == 0 && t < T && tk < n_tok) y[(size_t)tk * out_dim + row_of(j)] = tot;
+                    acc[tk] = 0.f;
+                }
                 col = 0;
                 j++;
             } else {
@@ -289,46 +303,47 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
     }
 }
 
-// LDS of k_gemv1: the quantised x (ncols columns) plus one spare column.
+// LDS of k_gemv1: the quantised x (bt tokens x ncols columns) plus one
+// spare column.
 template <class F>
-static size_t gemv1_lds_bytes(int in_dim) {
+static size_t gemv1_lds_bytes(int in_dim, int bt = 1) {
     const int ncols = ((in_dim + F::kEPU - 1) / F::kEPU + 7) >> 3;
-    return (size_t)(ncols + 1) * F::kXF * 1024;
+    return (size_t)(bt * ncols + 1) * F::kXF * 1024;
 }
 
 // Groups of x per thread the prologue needs (1, 2 or 4; 0 = too long).
 template <class F>
-static int gemv1_gpt(int in_dim, int nw) {
+static int gemv1_gpt(int in_dim, int nw, int bt = 1) {
     const int ncols = ((in_dim + F::kEPU - 1) / F::kEPU + 7) >> 3;
-    const int groups = ncols * 64 * (F::kXF == 5 ? 2 : 1);
+    const int groups = bt * ncols * 64 * (F::kXF == 5 ? 2 : 1);
     const int gpt = (groups + 64 * nw - 1) / (64 * nw);
     return gpt <= 1 ? 1 : gpt <= 2 ? 2 : gpt <= 4 ? 4 : 0;
 }
 
-template <class F, int NW, int PD, int GPT>
+template <class F, int NW, int PD, int GPT, int BT>
 static hipError_t gemv1_go(const uint8_t *w, size_t w_bytes, const float *x, float *y, int in_dim,
-                           int out_dim, int n_wg, hipStream_t s) {
+                           int out_dim, int n_tok, int n_wg, hipStream_t s) {
     static bool attr_set = false;  // per instantiation; idempotent if raced
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemv1<F, NW, PD, GPT>,
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemv1<F, NW, PD, GPT, BT>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)kGemv1MaxLds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
     n_wg = min(n_wg, out_dim);
-    k_gemv1<F, NW, PD, GPT><<<(unsigned)n_wg, 64 * NW, gemv1_lds_bytes<F>(in_dim), s>>>(
-        w, (uint32_t)w_bytes, x, y, in_dim, out_dim, n_wg);
+    k_gemv1<F, NW, PD, GPT, BT><<<(unsigned)n_wg, 64 * NW, gemv1_lds_bytes<F>(in_dim, BT), s>>>(
+        w, (uint32_t)w_bytes, x, y, in_dim, out_dim, n_wg, n_tok);
     return hipGetLastError();
 }
 
-template <class F, int NW, int PD>
+template <class F, int NW, int PD, int BT = 1>
 static hipError_t gemv1_gpt_go(const uint8_t *w, size_t w_bytes, const float *x, float *y,
-                               int in_dim, int out_dim, int n_wg, hipStream_t s) {
-    switch (gemv1_gpt<F>(in_dim, NW)) {
-    case 1: return gemv1_go<F, NW, PD, 1>(w, w_bytes, x, y, in_dim, out_dim, n_wg, s);
-    case 2: return gemv1_go<F, NW, PD, 2>(w, w_bytes, x, y, in_dim, out_dim, n_wg, s);
-    case 4: return gemv1_go<F, NW, PD, 4>(w, w_bytes, x, y, in_dim, out_dim, n_wg, s);
+                               int in_dim, int out_dim, int n_tok, int n_wg, hipStream_t s) {
+    switch (gemv1_gpt<F>(in_dim, NW, BT)) {
+    case 1: return gemv1_go<F, NW, PD, 1, BT>(w, w_bytes, x, y, in_dim, out_dim, n_tok, n_wg, s);
+    case 2: return gemv1_go<F, NW, PD, 2, BT>(w, w_bytes, x, y, in_dim, out_dim, n_tok, n_wg, s);
+    case 4: return gemv1_go<F, NW, PD, 4, BT>(w, w_bytes, x, y, in_dim, out_dim, n_tok, n_wg, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -617,27 +632,49 @@ static hipError_t gemv1(const uint8_t *w, size_t w_bytes, const float *x, float 
                         int out_dim, hipStream_t s) {
     const int cus = device_cus();
     if (w_bytes >= ((size_t)32 << 20)) {
-        if (out_dim >= 2 * in_dim) return gemv1_gpt_go<F, 8, 2>(w, w_bytes, x, y, in_dim, out_dim, 2 * cus, s);
-        return gemv1_gpt_go<F, 8, 3>(w, w_bytes, x, y, in_dim, out_dim, cus, s);
+        if (out_dim >= 2 * in_dim) return gemv1_gpt_go<F, 8, 2>(w, w_bytes, x, y, in_dim, out_dim, 1, 2 * cus, s);
+        return gemv1_gpt_go<F, 8, 3>(w, w_bytes, x, y, in_dim, out_dim, 1, cus, s);
     }
-    return gemv1_gpt_go<F, 16, 2>(w, w_bytes, x, y, in_dim, out_dim, cus, s);
+    return gemv1_gpt_go<F, 16, 2>(w, w_bytes, x, y, in_dim, out_dim, 1, cus, s);
 }
 
 template <class F>
-static bool gemv1_fits_f(int in_dim) {
-    return gemv1_lds_bytes<F>(in_dim) <= kGemv1MaxLds && gemv1_gpt<F>(in_dim, 8) != 0;
+static bool gemv1_fits_f(int in_dim, int bt) {
+    return gemv1_lds_bytes<F>(in_dim, bt) <= kGemv1MaxLds &&
+           gemv1_gpt<F>(in_dim, bt == 1 ? 8 : 16, bt) != 0;
 }
 
-static bool gemv1_fits(uint32_t dtype, int in_dim) {
-    switch (dtype) {
-    case T_Q4_K: return gemv1_fits_f<FQ4K>(in_dim);
-    case T_Q6_K: return gemv1_fits_f<FQ6K>(in_dim);
-    case T_Q8_0: return gemv1_fits_f<FQ8<false>>(in_dim);
-    case T_Q4_0: return gemv1_fits_f<FQ8<true>>(in_dim);
-    case T_Q2_K: return gemv1_fits_f<FQ2K>(in_dim);
-    case T_IQ2_XXS: return gemv1_fits_f<FIQ2XXS>(in_dim);
-    default: return false;
+// Tokens the fused kernel takes as one batch (x of all of them in LDS):
+// 1, 2, 4 or 8; 0 if n_tok does not fit.
+template <class F>
+static int gemv1_bt(int n_tok, int in_dim) {
+    const int bt = n_tok <= 1 ? 1 : n_tok <= 2 ? 2 : n_tok <= 4 ? 4 : n_tok <= 8 ? 8 : 0;
+    return bt && gemv1_fits_f<F>(in_dim, bt) ? bt : 0;
+}
+
+// 2..8 tokens: one 16-wavefront workgroup per CU, two tiles in flight
+// (sweeps of the C0-C2 shapes at 2, 4 and 8 tokens).
+template <class F>
+static hipError_t gemv1_batch(const uint8_t *w, size_t w_bytes, const float *x, float *y,
+                              int n_tok, int in_dim, int out_dim, hipStream_t s) {
+    const int cus = device_cus();
+    switch (gemv1_bt<F>(n_tok, in_dim)) {
+    case 2: return gemv1_gpt_go<F, 16, 2, 2>(w, w_bytes, x, y, in_dim, out_dim, n_tok, cus, s);
+    case 4: return gemv1_gpt_go<F, 16, 2, 4>(w, w_bytes, x, y, in_dim, out_dim, n_tok, cus, s);
+    case 8: return gemv1_gpt_go<F, 16, 2, 8>(w, w_bytes, x, y, in_dim, out_dim, n_tok, cus, s);
+    default: return hipErrorInvalidValue;
     }
+}
+
+#define GEMV_FORMATS(X)                                                                            \
+    X(T_Q4_K, FQ4K) X(T_Q6_K, FQ6K) X(T_Q8_0, FQ8<false>) X(T_Q4_0, FQ8<true>) X(T_Q2_K, FQ2K)     \
+    X(T_IQ2_XXS, FIQ2XXS)
+
+static int gemv1_tokens(uint32_t dtype, int n_tok, int in_dim) {
+#define X(T, F) if (dtype == T) return gemv1_bt<F>(n_tok, in_dim);
+    GEMV_FORMATS(X)
+#undef X
+    return 0;
 }
 
 hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
@@ -646,16 +683,18 @@ hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const f
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
     if (gemv_mfma_supported(dtype, n_tok, in_dim, out_dim))
         return launch_gemv_mfma(dtype, w, w_bytes, x, xq_scratch, y, n_tok, in_dim, out_dim, s);
-    if (n_tok == 1 && gemv1_fits(dtype, in_dim)) {
-        switch (dtype) {
-        case T_Q4_K: return gemv1<FQ4K>(w, w_bytes, x, y, in_dim, out_dim, s);
-        case T_Q6_K: return gemv1<FQ6K>(w, w_bytes, x, y, in_dim, out_dim, s);
-        case T_Q8_0: return gemv1<FQ8<false>>(w, w_bytes, x, y, in_dim, out_dim, s);
-        case T_Q4_0: return gemv1<FQ8<true>>(w, w_bytes, x, y, in_dim, out_dim, s);
-        case T_Q2_K: return gemv1<FQ2K>(w, w_bytes, x, y, in_dim, out_dim, s);
-        case T_IQ2_XXS: return gemv1<FIQ2XXS>(w, w_bytes, x, y, in_dim, out_dim, s);
-        default: return hipErrorInvalidValue;
-        }
+    const int bt = gemv1_tokens(dtype, n_tok, in_dim);
+    if (bt == 1) {
+#define X(T, F) if (dtype == T) return gemv1<F>(w, w_bytes, x, y, in_dim, out_dim, s);
+        GEMV_FORMATS(X)
+#undef X
+        return hipErrorInvalidValue;
+    }
+    if (bt > 1) {
+#define X(T, F) if (dtype == T) return gemv1_batch<F>(w, w_bytes, x, y, n_tok, in_dim, out_dim, s);
+        GEMV_FORMATS(X)
+#undef X
+        return hipErrorInvalidValue;
     }
     hipError_t e = launch_quantize_x(dtype, x, xq_scratch, n_tok, in_dim, s);
     if (e != hipSuccess) return e;

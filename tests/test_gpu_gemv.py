@@ -118,8 +118,10 @@ def test_n_tok_zero_is_noop(hip):
 
 @pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q4_0])
 def test_prequant_entry_points_match_one_shot(oracle, hip, dtype):
-    """quantize_x_dev + matmul_prequant_dev is the same computation as
-    matmul_quant_f32_dev: identical outputs, and within tolerance of the oracle."""
+    """quantize_x_dev + matmul_prequant_dev is the same product as
+    matmul_quant_f32_dev (same activation limbs; the one-shot call may sum in
+    another order): agreement to 1e-6 of max|y|, both within tolerance of
+    the oracle."""
     import torch
     out_dim, in_dim, n_tok = 77, 1280, 2
     w = synth.weight(dtype, out_dim, in_dim, 21)
@@ -140,5 +142,7 @@ def test_prequant_entry_points_match_one_shot(oracle, hip, dtype):
     hip.matmul_prequant_dev(y2.data_ptr(), y2.numel(), d_w.data_ptr(), w.size, xq.data_ptr(), nb,
                             n_tok, in_dim, out_dim, dtype, s)
     torch.cuda.synchronize()
-    assert torch.equal(y1, y2)
-    assert rel_err(y2.cpu().numpy(), want) <= REL_TOL
+    a, b = y1.cpu().numpy(), y2.cpu().numpy()
+    assert np.abs(a - b).max() <= 1e-6 * np.abs(b).max()
+    assert rel_err(a, want) <= REL_TOL
+    assert rel_err(b, want) <= REL_TOL
