@@ -22,13 +22,26 @@
 // computed. Lane (r, q) = (lane % 16, lane / 16) dequantises 32 weights of
 // row r per step (8 for each of the 4 MFMAs). The NK partial tiles are added
 // through LDS in wavefront order (deterministic), scaled by 2^-e_t, stored.
-#include "kernels.h"
+#include "gemv_formats.h"
 
 namespace rsllm_hip {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMfStep = 128;  // K elements per step
+
+// Max over a wavefront (every lane gets it): DPP row reductions plus lane reads.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 47));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
 
 __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0);
@@ -44,6 +57,13 @@ struct MQ4K {
     };
     __device__ static int elem(int s, int j, int q) {
         return 256 * (s >> 1) + 64 * q + 32 * (j & 1) + 16 * (s & 1) + 8 * (j >> 1);
+    }
+    // inverse of elem for an 8-aligned element offset: (s, j, q)
+    __device__ static void piece(int e, int &s, int &j, int &q) {
+        const int r = e & 255;
+        q = r >> 6;
+        s = 2 * (e >> 8) + ((r >> 4) & 1);
+        j = ((r >> 5) & 1) + 2 * ((r >> 3) & 1);
     }
     __device__ static void load(W &w, __amdgpu_buffer_rsrc_t r, int row, int s, int q, int in_dim,
                                 int) {
@@ -101,6 +121,12 @@ struct MQ6K {
     };
     __device__ static int elem(int s, int j, int q) {
         return 256 * (s >> 1) + 128 * (s & 1) + 16 * q + 64 * (j & 1) + 8 * (j >> 1);
+    }
+    __device__ static void piece(int e, int &s, int &j, int &q) {
+        const int r = e & 255;
+        s = 2 * (e >> 8) + (r >> 7);
+        j = ((r >> 6) & 1) + 2 * ((r >> 3) & 1);
+        q = (r >> 4) & 3;
     }
     __device__ static void load(W &w, __amdgpu_buffer_rsrc_t r, int row, int s, int q, int in_dim,
                                 int out_dim) {
@@ -275,6 +301,217 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__
     }
 }
 
+// ---- fused batched GEMV: activations converted into LDS ------------------------------
+// One launch of n_wg workgroups (one per CU) of NW wavefronts, for n_tok <=
+// 16 tokens whose f16 activations fit in LDS (n_tok * in_dim * 2 bytes).
+//
+// Prologue: per-token max |x| (LDS atomic max on the float bits, all values
+// being non-negative), then every 8-element piece of x scaled by 2^e_t into
+// f16 at LDS slot ((s * 4 + j) * 4 + q) * n_tok + t (MFMA operand order);
+// unscale[t] = 2^-e_t. Lanes of tokens >= n_tok read a zero slot.
+// Rows: blocks of 16 (the MFMA M); workgroup b owns blocks b + n_wg * l.
+// Every wavefront streams its share of K steps [w ns / NW, (w + 1) ns / NW)
+// of each of those blocks, PD steps in flight; after a block its partial D
+// goes to LDS, and after the stream the workgroup adds the NW partials in
+// wavefront order (deterministic), scales by 2^-e_t and stores.
+template <class F, int NW, int PD, int XP>
+__global__ __launch_bounds__(64 * NW) void k_gemv_mfb(const uint8_t *__restrict__ w,
+                                                      uint32_t w_bytes,
+                                                      const float *__restrict__ x,
+                                                      float *__restrict__ y, int n_tok,
+                                                      int in_dim, int out_dim, int n_wg) {
+    extern __shared__ uint4 lds[];
+    __shared__ uint32_t amax_bits[16];
+    __shared__ float unscale[16];
+    constexpr int kThreads = 64 * NW;
+    const int lane = threadIdx.x & 63, r16 = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ns = in_dim / kMfStep;
+    const int n_rb = (out_dim + 15) >> 4;
+    const int rb0 = blockIdx.x;
+    const int nrb = (n_rb - rb0 + n_wg - 1) / n_wg;  // this workgroup's row blocks
+    const int s_beg = ns * wv / NW, s_end = ns * (wv + 1) / NW, my_ns = s_end - s_beg;
+    const int T = nrb * my_ns;  // this wavefront's tiles (block-major)
+    uint4 *xs = lds;                                              // n_tok * in_dim / 8 slots
+    uint4 *zero = lds + (size_t)n_tok * in_dim / 8;               // one zero slot
+    f32x4 *part = reinterpret_cast<f32x4 *>(zero + 1);            // [nrb][NW][64]
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
+    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(w, 0);
+
+    typename F::W buf[PD];
+    auto load_tile = [&](typename F::W &wt, int t) {
+        const int l = my_ns > 0 ? t / my_ns : 0;
+        const int s = s_beg + (t - l * my_ns);
+        const int row = min(16 * (rb0 + n_wg * l) + r16, out_dim - 1);
+        F::load(wt, t < T ? rw : rnull, row, min(s, ns - 1), q, in_dim, out_dim);
+    };
+
+    // Prologue. x is read once: XP 8-element pieces per thread (piece i =
+    // thread + k * 64 NW, token 8 i / in_dim), issued before the first
+    // tiles' weight loads; per-token max |x| by LDS atomic max on the float
+    // bits (non-negative values order like their bits); then the pieces are
+    // scaled, converted and stored.
+    const int n8 = n_tok * in_dim / 8;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)n8 * 32u);
+    uint4 xv[XP][2];
+#pragma unroll
+    for (int r = 0; r < XP; r++) {
+        const uint32_t i = threadIdx.x + r * kThreads;
+        xv[r][0] = bload16(rx, i * 32u, 0);
+        xv[r][1] = bload16(rx, i * 32u + 16u, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < PD - 1; j++) load_tile(buf[j], j);
+    __builtin_amdgcn_sched_barrier(0);
+    if (threadIdx.x < 16) amax_bits[threadIdx.x] = 0u;
+    if (threadIdx.x == 0) *zero = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < XP; r++) {
+        const int i = threadIdx.x + r * kThreads;
+        float m = 0.f;  // pieces past the end read zeros
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(__uint_as_float(xv[r][h].x)), fabsf(__uint_as_float(xv[r][h].y))),
+                               fmaxf(fabsf(__uint_as_float(xv[r][h].z)), fabsf(__uint_as_float(xv[r][h].w)))));
+        }
+        // a wavefront's 64 pieces span at most two tokens (in_dim >= 512):
+        // reduce per token over the wavefront, then one atomic per token
+        const int tl = min((8 * (i - lane)) / in_dim, n_tok - 1);
+        const int tt = min((8 * i) / in_dim, n_tok - 1);
+        const float m_lo = wave_max(tt == tl ? m : 0.f), m_hi = wave_max(tt != tl ? m : 0.f);
+        if (lane == 0 && i - lane < n8) {
+            atomicMax(&amax_bits[tl], __float_as_uint(m_lo));
+            if (tl + 1 < n_tok) atomicMax(&amax_bits[tl + 1], __float_as_uint(m_hi));
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const float amax = __uint_as_float(amax_bits[threadIdx.x]);
+        int e = 0;
+        if (amax > 0.f && amax <= 3.4e38f) {
+            int ex;
+            frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
+            e = min(max(15 - ex, -126), 126);
+        }
+        amax_bits[threadIdx.x] = (uint32_t)e;
+        unscale[threadIdx.x] = ldexpf(1.0f, -e);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < XP; r++) {
+        const int i = threadIdx.x + r * kThreads;
+        if (i < n8) {
+            const int t = (8 * i) / in_dim, e0 = 8 * i - t * in_dim;
+            const float up = ldexpf(1.0f, (int)amax_bits[t]);
+            f16x8 h;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                h[4 * u] = (_Float16)(__uint_as_float(xv[r][u].x) * up);
+                h[4 * u + 1] = (_Float16)(__uint_as_float(xv[r][u].y) * up);
+                h[4 * u + 2] = (_Float16)(__uint_as_float(xv[r][u].z) * up);
+                h[4 * u + 3] = (_Float16)(__uint_as_float(xv[r][u].w) * up);
+            }
+            int s, j, qq;
+            F::piece(e0, s, j, qq);
+            xs[((s * 4 + j) * 4 + qq) * n_tok + t] = __builtin_bit_cast(uint4, h);
+        }
+    }
+    __syncthreads();
+
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    int l = 0, sc = 0;  // compute cursor: block l, step s_beg + sc
+    const bool tok_ok = r16 < n_tok;
+    for (int t0 = 0; t0 < T; t0 += PD) {
+#pragma unroll
+        for (int jj = 0; jj < PD; jj++) {
+            const int t = t0 + jj;
+            load_tile(buf[(jj + PD - 1) % PD], t + PD - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (t < T) {
+                const int s = s_beg + sc;
+                f16x8 a[4];
+                F::dequant(buf[jj], q, s, a);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint4 *px = tok_ok ? xs + ((s * 4 + j) * 4 + q) * n_tok + r16 : zero;
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        a[j], __builtin_bit_cast(f16x8, *px), acc, 0, 0, 0);
+                }
+                if (++sc == my_ns) {
+                    part[((size_t)l * NW + wv) * 64 + lane] = acc;
+                    acc = {0.f, 0.f, 0.f, 0.f};
+                    sc = 0;
+                    l++;
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if (my_ns == 0)  // more wavefronts than K steps: this one contributes zeros
+        for (int b = 0; b < nrb; b++) part[((size_t)b * NW + wv) * 64 + lane] = acc;
+    __syncthreads();
+    // D lane layout: rows 4 (lane / 16) + 0..3, column (token) lane % 16
+    for (int c = threadIdx.x; c < nrb * 64; c += kThreads) {
+        const int b = c >> 6, ln = c & 63;
+        f32x4 v = part[((size_t)b * NW) * 64 + ln];
+        for (int k = 1; k < NW; k++) v += part[((size_t)b * NW + k) * 64 + ln];
+        const int tk = ln & 15;
+        const int o = 16 * (rb0 + n_wg * b) + 4 * (ln >> 4);
+        if (tk < n_tok) {
+            const float us = unscale[tk];
+            float *yt = y + (size_t)tk * out_dim;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (o + i < out_dim) yt[o + i] = v[i] * us;
+        }
+    }
+}
+
+template <class F>
+static size_t mfb_lds_bytes(int n_tok, int in_dim, int out_dim, int n_wg, int nw) {
+    const int n_rb = (out_dim + 15) >> 4;
+    const int nrb = (n_rb + n_wg - 1) / n_wg;
+    return ((size_t)n_tok * in_dim / 8 + 1) * 16 + (size_t)nrb * nw * 64 * 16;
+}
+constexpr size_t kMfbMaxLds = 152 * 1024;
+
+template <class F, int NW, int PD, int XP>
+static hipError_t mfb_go(const uint8_t *w, size_t w_bytes, const float *x, float *y, int n_tok,
+                         int in_dim, int out_dim, int n_wg, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemv_mfb<F, NW, PD, XP>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMfbMaxLds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    n_wg = min(n_wg, (out_dim + 15) >> 4);
+    k_gemv_mfb<F, NW, PD, XP><<<(unsigned)n_wg, 64 * NW, mfb_lds_bytes<F>(n_tok, in_dim, out_dim, n_wg, NW), s>>>(
+        w, (uint32_t)w_bytes, x, y, n_tok, in_dim, out_dim, n_wg);
+    return hipGetLastError();
+}
+
+// Pieces of x per thread (1, 2, 4 or 8; 0 = too many).
+static int mfb_xp(int n_tok, int in_dim, int nw) {
+    const int n8 = n_tok * in_dim / 8, thr = 64 * nw;
+    const int xp = (n8 + thr - 1) / thr;
+    return xp <= 1 ? 1 : xp <= 2 ? 2 : xp <= 4 ? 4 : xp <= 8 ? 8 : 0;
+}
+
+template <class F, int NW, int PD>
+static hipError_t mfb_xp_go(const uint8_t *w, size_t w_bytes, const float *x, float *y, int n_tok,
+                            int in_dim, int out_dim, int n_wg, hipStream_t s) {
+    switch (mfb_xp(n_tok, in_dim, NW)) {
+    case 1: return mfb_go<F, NW, PD, 1>(w, w_bytes, x, y, n_tok, in_dim, out_dim, n_wg, s);
+    case 2: return mfb_go<F, NW, PD, 2>(w, w_bytes, x, y, n_tok, in_dim, out_dim, n_wg, s);
+    case 4: return mfb_go<F, NW, PD, 4>(w, w_bytes, x, y, n_tok, in_dim, out_dim, n_wg, s);
+    case 8: return mfb_go<F, NW, PD, 8>(w, w_bytes, x, y, n_tok, in_dim, out_dim, n_wg, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 // ---- launchers -----------------------------------------------------------------------
 // Taken from 5 tokens up: below that the int8-limb GEMV, whose VALU work
 // grows with the batch, is still faster (C1: 26 vs 29 us at 4 tokens, 55 vs
@@ -308,9 +545,17 @@ static hipError_t mf_go(const uint8_t *w, size_t w_bytes, const float *x, uint8_
     return hipGetLastError();
 }
 
+// 5..8 tokens of tall matrices (out_dim >= 8192) whose f16 activations fit
+// in LDS take the fused kernel (C1 14336x4096 at 8 tokens: 24 vs 29 us); the
+// rest the two-launch kernel, which is faster on short matrices and does not
+// need x in LDS.
 template <class F>
 static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, uint8_t *scratch,
                               float *y, int n_tok, int in_dim, int out_dim, hipStream_t s) {
+    const int cus = device_cus();
+    if (n_tok <= 8 && out_dim >= 8192 && mfb_xp(n_tok, in_dim, 16) != 0 &&
+        mfb_lds_bytes<F>(n_tok, in_dim, out_dim, cus, 16) <= kMfbMaxLds)
+        return mfb_xp_go<F, 16, 2>(w, w_bytes, x, y, n_tok, in_dim, out_dim, cus, s);
     if (n_tok <= 16) return mf_go<F, 1, 8, 1>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
     return mf_go<F, 2, 8, 1>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
 }

@@ -52,6 +52,31 @@ def test_gemv_mfma_batches(oracle, hip, dtype, out_dim, in_dim, n_tok):
             assert rel_err(g[t], wv[t]) <= REL_TOL, f"token {t}"
 
 
+# The fused matrix-core kernel (5..8 tokens, out_dim >= 8192, f16 x in LDS):
+# row counts off the 16-row block, K steps fewer than wavefronts (256 -> 2
+# steps over 16 wavefronts) and many, token scales far apart, one token
+# zero.
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K])
+@pytest.mark.parametrize("out_dim,in_dim", [(8192, 256), (8200, 1024), (9001, 3072)])
+@pytest.mark.parametrize("n_tok", [5, 6, 8])
+def test_gemv_mfma_fused_lds(oracle, hip, dtype, out_dim, in_dim, n_tok):
+    w = synth.weight(dtype, out_dim, in_dim, 70 + n_tok)
+    x = synth.activations(n_tok, in_dim, 80 + n_tok)
+    x *= (np.float32(10.0) ** ((np.arange(n_tok) % 7) - 3)).astype(np.float32)[:, None]
+    x[1] = 0.0
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, x, n_tok, in_dim, out_dim, int(dtype))
+    got = np.full(n_tok * out_dim, np.nan, np.float32)
+    hip.matmul_quant_f32(got, w, x, n_tok, in_dim, out_dim, dtype)
+    g = got.reshape(n_tok, out_dim)
+    wv = want.reshape(n_tok, out_dim)
+    assert not np.isnan(g).any()
+    assert np.all(g[1] == 0.0)
+    for t in range(n_tok):
+        if np.abs(wv[t]).max() > 0:
+            assert rel_err(g[t], wv[t]) <= REL_TOL, f"token {t}"
+
+
 # Benchmark shapes at full size (BASELINE configs C0-C2).
 @pytest.mark.parametrize("dtype,out_dim,in_dim,n_tok", [
     (G.Q4_K, 4096, 4096, 1),
