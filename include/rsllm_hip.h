@@ -211,6 +211,64 @@ int rsllm_hip_moe_routed(float *out, size_t out_len, const float *x, size_t x_le
                          size_t n_ff, size_t n_expert, size_t k, uint32_t dtype_gate_up,
                          uint32_t dtype_down, float clamp);
 
+/* ---- caller chain: matmul_weight_f32, matmul_grouped_lora_down ------------
+ * rsllm_hip_matmul_weight_f32 replaces matmul_weight_f32
+ * (rsllm-models/src/dsv4/weight.rs:113-169): out[t, o] = sum_i W[o, i] x[t, i]
+ * for a WeightBlob. dtype 0 (GGML F32) is the F32 arm: `weights` holds
+ * out_dim * in_dim f32 values, weights_len counts bytes (out_dim * in_dim *
+ * 4). Any other dtype is the Quant arm, matmul_quant_f32 on the blob.
+ * Validation in the reference's order:
+ *   out_len != n_tok * out_dim            SHAPE_MISMATCH (matmul_weight_f32.out)
+ *   x_len != n_tok * in_dim               SHAPE_MISMATCH (matmul_weight_f32.x)
+ *   F32: weights_len != out_dim*in_dim*4  SHAPE_MISMATCH (.weight_f32)
+ *   Quant: every error of matmul_quant_f32 (dtype, block alignment,
+ *          lengths) becomes SHAPE_MISMATCH (.quant), as the reference maps
+ *          it; out_dim == 0 (a panic there) is INVALID_ARGUMENT.
+ *
+ * rsllm_hip_matmul_grouped_lora_down replaces matmul_grouped_lora_down
+ * (weight.rs:209-266): x is [n_tok x n_groups * group_dim], out
+ * [n_tok x n_groups * rank], weights n_groups stacked [rank x group_dim]
+ * row-major matrices (the [n_groups * rank x group_dim] matrix), F32 or a
+ * quant dtype as above; out[t, g * rank + o] = sum_i W_g[o, i]
+ * x[t, g * group_dim + i]. Validation: x length (.x), out length (.out),
+ * then for the groups grouped_weight_slice (weight.rs:271-323: group_dim *
+ * rank a multiple of the block (.alignment), each group's slice inside the
+ * blob (.f32 / .quant)) and the group's matmul_weight_f32 checks, all
+ * SHAPE_MISMATCH; n_groups == 0 is OK. The reference computes group by group
+ * and can fail on a later group's slice after writing earlier groups; here
+ * every check runs before anything is written.
+ *
+ * Device forms: weights in this backend's device layout (Quant arm:
+ * rsllm_hip_prepare_weights_dev of the [n_groups * rank x group_dim]
+ * matrix; F32: as is), x and out on the device, enqueued on `stream`. When
+ * the x of all groups for every token fits in LDS (up to 8 tokens) and
+ * group_dim is a multiple of the kernel's 8-block column, all groups are one
+ * launch; otherwise each group is its own launch. A group's launch needs the
+ * group to be a whole number of 8-block super-tiles of the device layout
+ * (non-Q4_K dtypes: rank * group_dim / block elements a multiple of 8). The
+ * host form converts each such unaligned group to the device layout on its
+ * own and always computes; the device form, given the whole matrix's
+ * layout, returns RSLLM_HIP_ERR_UNIMPLEMENTED (writing nothing) for
+ * unaligned groups when the one-launch form does not apply. The host form
+ * uses a registered copy of the blob only when the groups use all of it and
+ * are whole super-tiles. */
+int rsllm_hip_matmul_weight_f32(float *out, size_t out_len, const uint8_t *weights,
+                                size_t weights_len, const float *x, size_t x_len, size_t n_tok,
+                                size_t in_dim, size_t out_dim, uint32_t dtype);
+int rsllm_hip_matmul_weight_f32_dev(float *out, size_t out_len, const uint8_t *weights,
+                                    size_t weights_len, const float *x, size_t x_len,
+                                    size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype,
+                                    rsllm_hip_stream_t stream);
+int rsllm_hip_matmul_grouped_lora_down(float *out, size_t out_len, const uint8_t *weights,
+                                       size_t weights_len, const float *x, size_t x_len,
+                                       size_t n_tok, size_t n_groups, size_t group_dim,
+                                       size_t rank, uint32_t dtype);
+int rsllm_hip_matmul_grouped_lora_down_dev(float *out, size_t out_len, const uint8_t *weights,
+                                           size_t weights_len, const float *x, size_t x_len,
+                                           size_t n_tok, size_t n_groups, size_t group_dim,
+                                           size_t rank, uint32_t dtype,
+                                           rsllm_hip_stream_t stream);
+
 /* ---- Q8_0 int8-activation path ---------------------------------------------
  * quantize_q8_0_batch (backend-cpu/src/ops/q8_0.rs:95-129, per token
  * quantize_q8_0_activation :42-88): x [n_tok x in_dim] -> xq [n_tok x blocks

@@ -64,6 +64,8 @@ def lib() -> ctypes.CDLL:
         L.orc_swiglu_clamp.argtypes = [P, P, S, ctypes.c_float]
         L.orc_swiglu_clamp.restype = None
         L.orc_moe_routed.argtypes = [P, P, S, S, S, P, P, P, U32, U32, S, P, P, S, ctypes.c_float]
+        L.orc_matmul_weight_f32.argtypes = [P, S, P, S, P, S, S, S, S, U32, I]
+        L.orc_matmul_grouped_lora_down.argtypes = [P, S, P, S, P, S, S, S, S, S, U32, I]
         L.orc_last_detail.argtypes = [P, P]
         L.orc_iq2xxs_grid.argtypes = [I]
         L.orc_iq2xxs_grid.restype = ctypes.c_uint64
@@ -108,6 +110,36 @@ def matmul_quant_f32(w, x, n_tok, in_dim, out_dim, dtype, allow_q6k=True, n_thre
     out = np.full(max(n_out, 0), np.nan, dtype=np.float32)
     rc = lib().orc_matmul_quant_f32(_p(out), out.size, _p(w), w.size, _p(x), x.size, n_tok, in_dim,
                                     out_dim, dtype, int(allow_q6k), n_threads)
+    return rc, out
+
+
+def _weight_bytes(w):
+    """Byte view of a weight blob: f32 arrays keep their bytes."""
+    w = np.ascontiguousarray(w)
+    return w.reshape(-1).view(np.uint8)
+
+
+def matmul_weight_f32(w, x, n_tok, in_dim, out_dim, dtype, allow_q6k=True, out_len=None):
+    """Returns (status, out); ``w`` is float32 for dtype F32, else bytes."""
+    wb = _weight_bytes(w)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    n_out = n_tok * out_dim if out_len is None else out_len
+    out = np.full(max(n_out, 0), np.nan, dtype=np.float32)
+    rc = lib().orc_matmul_weight_f32(_p(out), out.size, _p(wb), wb.size, _p(x), x.size, n_tok,
+                                     in_dim, out_dim, dtype, int(allow_q6k))
+    return rc, out
+
+
+def matmul_grouped_lora_down(w, x, n_tok, n_groups, group_dim, rank, dtype, allow_q6k=True,
+                             out_len=None):
+    """Returns (status, out); out starts as NaN so unwritten groups show."""
+    wb = _weight_bytes(w)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    n_out = n_tok * n_groups * rank if out_len is None else out_len
+    out = np.full(max(n_out, 0), np.nan, dtype=np.float32)
+    rc = lib().orc_matmul_grouped_lora_down(_p(out), out.size, _p(wb), wb.size, _p(x), x.size,
+                                            n_tok, n_groups, group_dim, rank, dtype,
+                                            int(allow_q6k))
     return rc, out
 
 

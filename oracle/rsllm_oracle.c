@@ -31,6 +31,12 @@
  *                         integer dots vs numpy int64, rint ties-to-even
  *   orc_moe_routed        w == 0 skip, clamp KATs (moe.rs:791-833 semantics),
  *                         linearity in the routing weights, float64 recompute
+ *   orc_matmul_weight_f32 / orc_matmul_grouped_lora_down
+ *                         the reference's tests (weight.rs:329-463: hand
+ *                         dot, group isolation, slice alignment and offsets,
+ *                         out-shape rejection), float64 recompute of the F32
+ *                         arm, the grouped form equal to per-group
+ *                         orc_matmul_quant_f32 on the slices
  */
 #define _GNU_SOURCE
 #include "rsllm_oracle.h"
@@ -444,6 +450,84 @@ int orc_matmul_quant_f32_rows(float *out, const uint8_t *w, const float *x, size
     mm_ctx c = {out, w, x, in_dim, out_dim, in_dim / be * bb, row0, row1, dtype};
     run_tasks(n_tok, n_threads, mm_token, &c);
     return ORC_OK;
+}
+
+/* ---- matmul_weight_f32: rsllm-models/src/dsv4/weight.rs:113-169 ------------ */
+int orc_matmul_weight_f32(float *out, size_t out_len, const uint8_t *w, size_t w_len,
+                          const float *x, size_t x_len, size_t n_tok, size_t in_dim,
+                          size_t out_dim, uint32_t dtype, int allow_q6k) {
+    size_t need;
+    if (__builtin_mul_overflow(n_tok, out_dim, &need) || out_len != need) /* :121-127 */
+        return fail2(ORC_SHAPE_MISMATCH, 10, 0);
+    if (__builtin_mul_overflow(n_tok, in_dim, &need) || x_len != need) /* :128-134 */
+        return fail2(ORC_SHAPE_MISMATCH, 11, 0);
+    if (dtype == ORC_F32) {
+        if (__builtin_mul_overflow(out_dim, in_dim, &need) || w_len != need * 4) /* :141-146 */
+            return fail2(ORC_SHAPE_MISMATCH, 12, 0);
+        for (size_t t = 0; t < n_tok; t++) { /* :148-157 */
+            const float *xr = x + t * in_dim;
+            float *orow = out + t * out_dim;
+            for (size_t o = 0; o < out_dim; o++) {
+                float dot = 0.0f, wv;
+                for (size_t i = 0; i < in_dim; i++) {
+                    memcpy(&wv, w + (o * in_dim + i) * 4, 4);
+                    dot += wv * xr[i];
+                }
+                orow[o] = dot;
+            }
+        }
+        return ORC_OK;
+    }
+    int rc = orc_matmul_quant_f32(out, out_len, w, w_len, x, x_len, n_tok, in_dim, out_dim, dtype,
+                                  allow_q6k, 1);
+    if (rc == ORC_OK || rc == ORC_PANIC) return rc;
+    return fail2(ORC_SHAPE_MISMATCH, 13, 0); /* :160-167 map_err */
+}
+
+/* ---- matmul_grouped_lora_down: weight.rs:209-266, slices :271-323 ------- */
+int orc_matmul_grouped_lora_down(float *out, size_t out_len, const uint8_t *w, size_t w_len,
+                                 const float *x, size_t x_len, size_t n_tok, size_t n_groups,
+                                 size_t group_dim, size_t rank, uint32_t dtype, int allow_q6k) {
+    size_t total_in, total_out, need;
+    if (__builtin_mul_overflow(n_groups, group_dim, &total_in) ||
+        __builtin_mul_overflow(n_tok, total_in, &need) || x_len != need) /* :219-225 */
+        return fail2(ORC_SHAPE_MISMATCH, 20, 0);
+    if (__builtin_mul_overflow(n_groups, rank, &total_out) ||
+        __builtin_mul_overflow(n_tok, total_out, &need) || out_len != need) /* :226-232 */
+        return fail2(ORC_SHAPE_MISMATCH, 21, 0);
+    float *xg = malloc((n_tok * group_dim + 1) * sizeof(float)); /* :239-240 */
+    float *og = malloc((n_tok * rank + 1) * sizeof(float));
+    int rc = ORC_OK;
+    const size_t epg = group_dim * rank;
+    for (size_t g = 0; g < n_groups && rc == ORC_OK; g++) { /* :241 */
+        for (size_t t = 0; t < n_tok; t++) /* :243-246 gather */
+            memcpy(xg + t * group_dim, x + t * total_in + g * group_dim, group_dim * sizeof(float));
+        /* grouped_weight_slice (:271-323) */
+        const uint8_t *wg;
+        size_t wg_len;
+        if (dtype == ORC_F32) {
+            size_t start = g * epg, end = start + epg;
+            if (end > w_len / 4) { rc = fail2(ORC_SHAPE_MISMATCH, 22, g); break; }
+            wg = w + start * 4;
+            wg_len = epg * 4;
+        } else {
+            size_t be = orc_block_elements(dtype), bb = orc_block_bytes(dtype);
+            if (be == 0) { rc = fail2(ORC_SHAPE_MISMATCH, 13, g); break; } /* not a known type */
+            if (epg % be != 0) { rc = fail2(ORC_SHAPE_MISMATCH, 23, g); break; }
+            size_t stride = epg / be * bb, start = g * stride, end = start + stride;
+            if (end > w_len) { rc = fail2(ORC_SHAPE_MISMATCH, 24, g); break; }
+            wg = w + start;
+            wg_len = stride;
+        }
+        rc = orc_matmul_weight_f32(og, n_tok * rank, wg, wg_len, xg, n_tok * group_dim, n_tok,
+                                   group_dim, rank, dtype, allow_q6k); /* :248-256 */
+        if (rc != ORC_OK) break;
+        for (size_t t = 0; t < n_tok; t++) /* :258-261 scatter */
+            memcpy(out + t * total_out + g * rank, og + t * rank, rank * sizeof(float));
+    }
+    free(xg);
+    free(og);
+    return rc;
 }
 
 /* ---- quantize_q8_0_activation: rsllm-backend-cpu/src/ops/q8_0.rs:42-88 --- */

@@ -119,6 +119,26 @@ int orc_moe_routed(float *out, const float *x, size_t n_tok, size_t n_embd, size
                    uint32_t dtype_gate_up, uint32_t dtype_down, size_t n_expert,
                    const int32_t *ids, const float *weights, size_t k, float clamp);
 
+/* matmul_weight_f32, rsllm-models/src/dsv4/weight.rs:113-169. dtype ORC_F32:
+ * w holds out_dim * in_dim f32 values (w_len in bytes), naive sequential dot
+ * (:148-158); otherwise orc_matmul_quant_f32 (allow_q6k as there) with every
+ * non-panic error reported as ORC_SHAPE_MISMATCH (:160-167). Errors of
+ * this function itself: detail a = 10 (out), 11 (x), 12 (weight_f32),
+ * 13 (quant). */
+int orc_matmul_weight_f32(float *out, size_t out_len, const uint8_t *w, size_t w_len,
+                          const float *x, size_t x_len, size_t n_tok, size_t in_dim,
+                          size_t out_dim, uint32_t dtype, int allow_q6k);
+
+/* matmul_grouped_lora_down, weight.rs:209-266, with grouped_weight_slice
+ * :271-323: per group g, gather x columns, matmul_weight_f32 on the g-th
+ * [rank x group_dim] slice, scatter into out. Errors (all ORC_SHAPE_MISMATCH,
+ * detail a): 20 (x), 21 (out), 22 (slice f32), 23 (slice alignment),
+ * 24 (slice quant), or matmul_weight_f32's; detail b = the failing group.
+ * As in the reference, groups before a failing one are already written. */
+int orc_matmul_grouped_lora_down(float *out, size_t out_len, const uint8_t *w, size_t w_len,
+                                 const float *x, size_t x_len, size_t n_tok, size_t n_groups,
+                                 size_t group_dim, size_t rank, uint32_t dtype, int allow_q6k);
+
 /* Online core count (what rayon's global pool would size itself to). */
 int orc_num_cores(void);
 

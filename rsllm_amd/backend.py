@@ -142,6 +142,11 @@ SIGNATURES = {
     "rsllm_hip_quantize_q8_0_batch_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _P, _P], _I),
     "rsllm_hip_matmul_q8_0_batch": ([_P, _S, _P, _S, _P, _S, _P, _S, _S, _S, _S, _U32], _I),
     "rsllm_hip_matmul_q8_0_batch_dev": ([_P, _S, _P, _S, _P, _S, _P, _S, _S, _S, _S, _P], _I),
+    "rsllm_hip_matmul_weight_f32": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32], _I),
+    "rsllm_hip_matmul_weight_f32_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _P], _I),
+    "rsllm_hip_matmul_grouped_lora_down": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _S, _U32], _I),
+    "rsllm_hip_matmul_grouped_lora_down_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _S, _U32, _P],
+                                               _I),
 }
 
 
@@ -193,6 +198,15 @@ def _host_ptr(a):
     return (a.ctypes.data_as(ctypes.c_void_p) if a.size else None), a.size
 
 
+def _host_bytes(a):
+    """Pointer and byte length of any C-contiguous array (or bytes)."""
+    if isinstance(a, np.ndarray) and a.dtype != np.uint8:
+        if not a.flags.c_contiguous:
+            raise ValueError("array must be C-contiguous")
+        a = a.reshape(-1).view(np.uint8)
+    return _host_ptr(a)
+
+
 def _host_f32(a, name):
     if not (isinstance(a, np.ndarray) and a.dtype == np.float32):
         raise TypeError(f"{name} must be a float32 numpy array")
@@ -211,6 +225,47 @@ def matmul_quant_f32(out: np.ndarray, weights, x: np.ndarray, n_tok: int, in_dim
     px, nx = _host_f32(x, "x")
     _check(LIB.rsllm_hip_matmul_quant_f32(po, no, pw, nw, px, nx, n_tok, in_dim, out_dim,
                                           int(dtype), int(tier)))
+
+
+def matmul_weight_f32(out: np.ndarray, weights, x: np.ndarray, n_tok: int, in_dim: int,
+                      out_dim: int, dtype) -> None:
+    """matmul_weight_f32 (rsllm-models/src/dsv4/weight.rs:113-169): dtype
+    GgmlType.F32 takes ``weights`` as out_dim * in_dim f32 values (an f32
+    array, or its bytes); any other dtype is matmul_quant_f32 on the blob, its
+    errors reported as ShapeMismatch."""
+    po, no = _host_f32(out, "out")
+    pw, nw = _host_bytes(weights)
+    px, nx = _host_f32(x, "x")
+    _check(LIB.rsllm_hip_matmul_weight_f32(po, no, pw, nw, px, nx, n_tok, in_dim, out_dim,
+                                           int(dtype)))
+
+
+def matmul_weight_f32_dev(out_ptr: int, out_len: int, w_ptr: int, w_len: int, x_ptr: int,
+                          x_len: int, n_tok: int, in_dim: int, out_dim: int, dtype,
+                          stream: int = 0) -> None:
+    _check(LIB.rsllm_hip_matmul_weight_f32_dev(out_ptr or None, out_len, w_ptr or None, w_len,
+                                               x_ptr or None, x_len, n_tok, in_dim, out_dim,
+                                               int(dtype), stream or None))
+
+
+def matmul_grouped_lora_down(out: np.ndarray, weights, x: np.ndarray, n_tok: int, n_groups: int,
+                             group_dim: int, rank: int, dtype) -> None:
+    """matmul_grouped_lora_down (weight.rs:209-266): x [n_tok x n_groups *
+    group_dim] through n_groups stacked [rank x group_dim] weights into out
+    [n_tok x n_groups * rank]."""
+    po, no = _host_f32(out, "out")
+    pw, nw = _host_bytes(weights)
+    px, nx = _host_f32(x, "x")
+    _check(LIB.rsllm_hip_matmul_grouped_lora_down(po, no, pw, nw, px, nx, n_tok, n_groups,
+                                                  group_dim, rank, int(dtype)))
+
+
+def matmul_grouped_lora_down_dev(out_ptr: int, out_len: int, w_ptr: int, w_len: int, x_ptr: int,
+                                 x_len: int, n_tok: int, n_groups: int, group_dim: int, rank: int,
+                                 dtype, stream: int = 0) -> None:
+    _check(LIB.rsllm_hip_matmul_grouped_lora_down_dev(out_ptr or None, out_len, w_ptr or None,
+                                                      w_len, x_ptr or None, x_len, n_tok, n_groups,
+                                                      group_dim, rank, int(dtype), stream or None))
 
 
 def dequant_to_f32(dtype, src, dst: np.ndarray) -> None:

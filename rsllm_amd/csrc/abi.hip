@@ -207,6 +207,182 @@ const uint8_t *find_registered(const uint8_t *host, size_t len, uint32_t dtype, 
 
 bool needs_prepare(uint32_t dtype) { return dtype != T_Q4_K; }
 
+
+// ---- caller chain (weight.rs:113-266) --------------------------------------
+// matmul_weight_f32: out, x lengths (:121-135), then the F32 arm's weight
+// length (:141-146) or matmul_quant_f32 with any error of it reported as
+// ShapeMismatch "matmul_weight_f32.quant" (:160-167). matmul_quant_f32's
+// out_dim == 0 is a panic in the reference (not an Err) and stays
+// INVALID_ARGUMENT, as do NULL pointers; UNIMPLEMENTED passes through.
+int validate_weight_f32(size_t out_len, const void *w, size_t w_len, const void *x, size_t x_len,
+                        const void *out, size_t n_tok, size_t in_dim, size_t out_dim,
+                        uint32_t dtype) {
+    size_t need;
+    if (!mul_ok(n_tok, out_dim, &need) || out_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_weight_f32.out: out must be n_tok * out_dim");
+    if (!mul_ok(n_tok, in_dim, &need) || x_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_weight_f32.x: x must be n_tok * in_dim");
+    if (dtype == T_F32) {
+        size_t e;
+        if (!mul_ok(out_dim, in_dim, &e) || !mul_ok(e, 4, &need) || w_len != need)
+            return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                           "matmul_weight_f32.weight_f32: weights must be out_dim * in_dim f32");
+        if ((w_len && !w) || (x_len && !x) || (out_len && !out))
+            return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "NULL pointer with a nonzero length");
+        if (!fits_int(n_tok) || !fits_int(in_dim) || !fits_int(out_dim) || w_len > kMaxWeightBytes)
+            return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "matmul_weight_f32: size exceeds 2^31-1");
+        return RSLLM_HIP_OK;
+    }
+    const int rc = validate_matmul(out_len, w, w_len, x, x_len, out, n_tok, in_dim, out_dim, dtype);
+    if (rc == RSLLM_HIP_ERR_SHAPE_MISMATCH || rc == RSLLM_HIP_ERR_NOT_BLOCK_ALIGNED) {
+        const std::string m = std::string("matmul_weight_f32.quant: ") + g_err.msg;
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, m.c_str());
+    }
+    return rc;
+}
+
+// matmul_grouped_lora_down (:209-266): x, out lengths, then per group g in
+// order grouped_weight_slice (:271-323: alignment of the group's element
+// count to the block, the slice's end within the blob) and
+// matmul_weight_f32 on the group. The group checks are the same for every g
+// except the slice end, so they reduce to: alignment, group 0's end, the
+// group matmul's checks, then the last group's end. All of them are
+// ShapeMismatch in the reference; n_groups == 0 is Ok.
+int validate_lora_down(size_t out_len, const void *w, size_t w_len, const void *x, size_t x_len,
+                       const void *out, size_t n_tok, size_t n_groups, size_t group_dim,
+                       size_t rank, uint32_t dtype, size_t *stride_out) {
+    size_t total_in, total_out, need;
+    if (!mul_ok(n_groups, group_dim, &total_in) || !mul_ok(n_tok, total_in, &need) || x_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_grouped_lora_down.x: x must be n_tok * n_groups * group_dim");
+    if (!mul_ok(n_groups, rank, &total_out) || !mul_ok(n_tok, total_out, &need) || out_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_grouped_lora_down.out: out must be n_tok * n_groups * rank");
+    *stride_out = 0;
+    if (n_groups == 0) return RSLLM_HIP_OK;
+    size_t epg;
+    if (!mul_ok(group_dim, rank, &epg))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "grouped_weight_slice: size overflow");
+    size_t stride;
+    const char *end_key;
+    if (dtype == T_F32) {
+        if (!mul_ok(epg, 4, &stride))
+            return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "grouped_weight_slice: size overflow");
+        end_key = "grouped_weight_slice.f32: the group's slice ends past the blob";
+    } else {
+        const size_t be = block_elems_of(dtype), bb = block_bytes_of(dtype);
+        if (be == 0 || !matmul_dtype_known(dtype))
+            return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                           "matmul_weight_f32.quant: unsupported dtype for MoE expert matmul");
+        if (epg % be != 0)
+            return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                           "grouped_weight_slice.alignment: group_dim * rank is not a multiple "
+                           "of the block");
+        stride = epg / be * bb;
+        end_key = "grouped_weight_slice.quant: the group's slice ends past the blob";
+    }
+    if (stride > w_len) return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, end_key);
+    // group 0's matmul_weight_f32 (its out and x lengths match by construction)
+    size_t o0, x0;
+    if (!mul_ok(n_tok, rank, &o0) || !mul_ok(n_tok, group_dim, &x0))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "matmul_grouped_lora_down: size overflow");
+    int rc = validate_weight_f32(o0, w, stride, x, x0, out, n_tok, group_dim, rank, dtype);
+    if (rc) return rc;
+    if (!mul_ok(n_groups, stride, &need) || need > w_len)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, end_key);
+    if (need > kMaxWeightBytes)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH,
+                       "matmul_grouped_lora_down: stacked weights above 4 GiB are not supported");
+    if (!fits_int(total_in) || !fits_int(total_out) || !mul_ok(n_tok, total_in, &need) ||
+        !fits_int(need) || !mul_ok(n_tok, total_out, &need) || !fits_int(need))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "matmul_grouped_lora_down: size exceeds 2^31-1");
+    *stride_out = stride;
+    return RSLLM_HIP_OK;
+}
+
+// matmul_weight_f32 on device pointers (validated).
+int weight_f32_compute(float *out, size_t out_len, const uint8_t *w, size_t w_len, const float *x,
+                       size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype, hipStream_t s) {
+    if (n_tok == 0 || out_dim == 0) return ok();
+    if (in_dim == 0) {  // every dot is empty
+        HIP_TRY(launch_fill_zero(out, out_len, s), "fill_zero");
+        return ok();
+    }
+    if (dtype == T_F32) {
+        HIP_TRY(launch_gemv_f32((const float *)w, x, out, (int)n_tok, (int)in_dim, (int)out_dim,
+                                (int)in_dim, (int)in_dim, (int)out_dim, (int)out_dim, s),
+                "gemv_f32");
+        return ok();
+    }
+    HIP_TRY(t_ctx.xq.ensure(gemv_work_bytes(dtype, (int)n_tok, (int)in_dim, (int)out_dim)), "hipMalloc");
+    HIP_TRY(launch_gemv(dtype, w, w_len, x, (uint8_t *)t_ctx.xq.p, out, (int)n_tok, (int)in_dim,
+                        (int)out_dim, s),
+            "gemv");
+    return ok();
+}
+
+// matmul_grouped_lora_down on device pointers (validated; stride = bytes of
+// one group's [rank x group_dim] weights). The stacked blob is the
+// [n_groups * rank x group_dim] row-major matrix, so when the x of every
+// group and token fits in LDS (up to 8 tokens) one launch covers all groups,
+// row r reading x group r / rank; otherwise one launch per group (strided x
+// and y, or x gathered and y scattered for more tokens).
+// group_layout: each group's slice was converted to the device layout on its
+// own (only the per-group launches read it that way).
+int lora_down_compute(float *out, size_t out_len, const uint8_t *w, size_t stride, const float *x,
+                      size_t n_tok, size_t n_groups, size_t group_dim, size_t rank,
+                      uint32_t dtype, hipStream_t s, bool group_layout = false) {
+    if (n_tok == 0 || n_groups == 0 || rank == 0) return ok();
+    if (group_dim == 0) {
+        HIP_TRY(launch_fill_zero(out, out_len, s), "fill_zero");
+        return ok();
+    }
+    const int T = (int)n_tok, G = (int)n_groups, D = (int)group_dim, R = (int)rank;
+    const int tin = G * D, tout = G * R;
+    if (dtype == T_F32) {
+        HIP_TRY(launch_gemv_f32((const float *)w, x, out, T, D, tout, tin, tin, tout, R, s),
+                "gemv_f32");
+        return ok();
+    }
+    hipError_t e = hipErrorNotSupported;
+    if (!group_layout) {
+        e = launch_gemv_rows(dtype, w, stride * n_groups, x, out, T, D, tout, tin, tin, tout, R, s);
+        if (e == hipSuccess) return ok();
+        if (e != hipErrorNotSupported) return dev_err(e, "gemv_rows");
+        (void)hipGetLastError();
+    }
+    // one launch per group: group g's weights are rows [g R, (g + 1) R) of the
+    // stacked matrix; in the super-tile layouts that is whole super-tiles only
+    // when R * (blocks per row) is a multiple of 8
+    if (!group_layout && needs_prepare(dtype) && (rank * (group_dim / block_elems_of(dtype))) % 8 != 0)
+        return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED,
+                       "matmul_grouped_lora_down: groups that do not end on a super-tile of the "
+                       "device layout need the one-launch form (x of every group and token in "
+                       "LDS, group_dim a multiple of the 8-block column)");
+    for (int g = 0; g < G; g++) {
+        const uint8_t *wg = w + (size_t)g * stride;
+        e = launch_gemv_rows(dtype, wg, stride, x + (size_t)g * D, out + (size_t)g * R, T, D, R, D,
+                             tin, tout, R, s);
+        if (e == hipSuccess) continue;
+        if (e != hipErrorNotSupported) return dev_err(e, "gemv_rows");
+        (void)hipGetLastError();
+        ThreadCtx &c = t_ctx;
+        HIP_TRY(c.xh.ensure((size_t)T * D * 4 + (size_t)T * R * 4), "hipMalloc");
+        float *xg = (float *)c.xh.p, *yg = xg + (size_t)T * D;
+        HIP_TRY(hipMemcpy2DAsync(xg, (size_t)D * 4, x + (size_t)g * D, (size_t)tin * 4,
+                                 (size_t)D * 4, (size_t)T, hipMemcpyDeviceToDevice, s),
+                "gather x");
+        HIP_TRY(c.xq.ensure(gemv_work_bytes(dtype, T, D, R)), "hipMalloc");
+        HIP_TRY(launch_gemv(dtype, wg, stride, xg, (uint8_t *)c.xq.p, yg, T, D, R, s), "gemv");
+        HIP_TRY(hipMemcpy2DAsync(out + (size_t)g * R, (size_t)tout * 4, yg, (size_t)R * 4,
+                                 (size_t)R * 4, (size_t)T, hipMemcpyDeviceToDevice, s),
+                "scatter y");
+    }
+    return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -793,6 +969,129 @@ int rsllm_hip_dequant_to_f32(uint32_t dtype, const uint8_t *src, size_t src_len,
             "dequant");
     HIP_TRY(hipMemcpyAsync(dst, c.y.p, dst_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
             "download");
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    return ok();
+}
+
+
+// ---- caller chain -------------------------------------------------------------
+int rsllm_hip_matmul_weight_f32_dev(float *out, size_t out_len, const uint8_t *weights,
+                                    size_t weights_len, const float *x, size_t x_len,
+                                    size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype,
+                                    rsllm_hip_stream_t stream) {
+    int rc = validate_weight_f32(out_len, weights, weights_len, x, x_len, out, n_tok, in_dim,
+                                 out_dim, dtype);
+    if (rc) return rc;
+    if ((rc = ensure_device())) return rc;
+    return weight_f32_compute(out, out_len, weights, weights_len, x, n_tok, in_dim, out_dim, dtype,
+                              (hipStream_t)stream);
+}
+
+int rsllm_hip_matmul_weight_f32(float *out, size_t out_len, const uint8_t *weights,
+                                size_t weights_len, const float *x, size_t x_len, size_t n_tok,
+                                size_t in_dim, size_t out_dim, uint32_t dtype) {
+    int rc = validate_weight_f32(out_len, weights, weights_len, x, x_len, out, n_tok, in_dim,
+                                 out_dim, dtype);
+    if (rc) return rc;
+    if (n_tok == 0 || out_dim == 0) return ok();
+    if ((rc = ensure_device())) return rc;
+    ThreadCtx &c = t_ctx;
+    const uint8_t *dw =
+        dtype == T_F32 ? nullptr : find_registered(weights, weights_len, dtype, in_dim);
+    if (!dw && weights_len) {
+        HIP_TRY(c.w_raw.ensure(weights_len), "hipMalloc");
+        HIP_TRY(hipMemcpyAsync(c.w_raw.p, weights, weights_len, hipMemcpyHostToDevice, c.stream),
+                "upload weights");
+        dw = (const uint8_t *)c.w_raw.p;
+        if (dtype != T_F32 && needs_prepare(dtype) && in_dim) {
+            HIP_TRY(c.w_dev.ensure(weights_len), "hipMalloc");
+            HIP_TRY(launch_prepare(dtype, dw, (uint8_t *)c.w_dev.p, out_dim, in_dim, c.stream),
+                    "prepare weights");
+            dw = (const uint8_t *)c.w_dev.p;
+        }
+    }
+    HIP_TRY(c.x.ensure(x_len * sizeof(float) + 16), "hipMalloc");
+    HIP_TRY(c.y.ensure(out_len * sizeof(float)), "hipMalloc");
+    if (x_len)
+        HIP_TRY(hipMemcpyAsync(c.x.p, x, x_len * sizeof(float), hipMemcpyHostToDevice, c.stream),
+                "upload x");
+    rc = weight_f32_compute((float *)c.y.p, out_len, dw, weights_len, (const float *)c.x.p, n_tok,
+                            in_dim, out_dim, dtype, c.stream);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(out, c.y.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
+            "download out");
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    return ok();
+}
+
+int rsllm_hip_matmul_grouped_lora_down_dev(float *out, size_t out_len, const uint8_t *weights,
+                                           size_t weights_len, const float *x, size_t x_len,
+                                           size_t n_tok, size_t n_groups, size_t group_dim,
+                                           size_t rank, uint32_t dtype,
+                                           rsllm_hip_stream_t stream) {
+    size_t stride;
+    int rc = validate_lora_down(out_len, weights, weights_len, x, x_len, out, n_tok, n_groups,
+                                group_dim, rank, dtype, &stride);
+    if (rc) return rc;
+    if ((rc = ensure_device())) return rc;
+    return lora_down_compute(out, out_len, weights, stride, x, n_tok, n_groups, group_dim, rank,
+                             dtype, (hipStream_t)stream);
+}
+
+int rsllm_hip_matmul_grouped_lora_down(float *out, size_t out_len, const uint8_t *weights,
+                                       size_t weights_len, const float *x, size_t x_len,
+                                       size_t n_tok, size_t n_groups, size_t group_dim,
+                                       size_t rank, uint32_t dtype) {
+    size_t stride;
+    int rc = validate_lora_down(out_len, weights, weights_len, x, x_len, out, n_tok, n_groups,
+                                group_dim, rank, dtype, &stride);
+    if (rc) return rc;
+    if (n_tok == 0 || n_groups == 0 || rank == 0) return ok();
+    if ((rc = ensure_device())) return rc;
+    ThreadCtx &c = t_ctx;
+    // The blob may be longer; the groups use this much. The device layout
+    // packs 8 blocks per super-tile with a shorter last one, so a group's
+    // slice of the whole matrix's layout is the group's own layout only when
+    // the group is whole super-tiles; otherwise each group is converted on
+    // its own and run by the per-group launches. A registered copy (the whole
+    // blob's layout) is used only when it is exactly the groups' rows and
+    // they are whole super-tiles.
+    const size_t used = stride * n_groups;
+    const bool prep = dtype != T_F32 && needs_prepare(dtype) && group_dim;
+    const bool per_group = prep && (rank * (group_dim / block_elems_of(dtype))) % 8 != 0;
+    const uint8_t *dw = dtype == T_F32 || used != weights_len || per_group
+                            ? nullptr
+                            : find_registered(weights, weights_len, dtype, group_dim);
+    if (!dw) {
+        HIP_TRY(c.w_raw.ensure(used), "hipMalloc");
+        HIP_TRY(hipMemcpyAsync(c.w_raw.p, weights, used, hipMemcpyHostToDevice, c.stream),
+                "upload weights");
+        dw = (const uint8_t *)c.w_raw.p;
+        if (prep) {
+            HIP_TRY(c.w_dev.ensure(used), "hipMalloc");
+            uint8_t *wd = (uint8_t *)c.w_dev.p;
+            if (!per_group) {
+                HIP_TRY(launch_prepare(dtype, dw, wd, n_groups * rank, group_dim, c.stream),
+                        "prepare weights");
+            } else {
+                for (size_t g = 0; g < n_groups; g++)
+                    HIP_TRY(launch_prepare(dtype, dw + g * stride, wd + g * stride, rank,
+                                           group_dim, c.stream),
+                            "prepare weights");
+            }
+            dw = wd;
+        }
+    }
+    HIP_TRY(c.x.ensure(x_len * sizeof(float) + 16), "hipMalloc");
+    HIP_TRY(c.y.ensure(out_len * sizeof(float)), "hipMalloc");
+    if (x_len)
+        HIP_TRY(hipMemcpyAsync(c.x.p, x, x_len * sizeof(float), hipMemcpyHostToDevice, c.stream),
+                "upload x");
+    rc = lora_down_compute((float *)c.y.p, out_len, dw, stride, (const float *)c.x.p, n_tok,
+                           n_groups, group_dim, rank, dtype, c.stream, per_group);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(out, c.y.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
+            "download out");
     HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
     return ok();
 }

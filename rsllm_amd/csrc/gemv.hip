@@ -178,36 +178,48 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv(const uint8_t *__restri
 // its arithmetic, so the waits before each tile's arithmetic leave the later
 // tiles in flight.
 //
+// Rows and x. Weight row r dots x columns [g * in_dim, (g + 1) * in_dim) of
+// each token, g = r / rows_per_group (one group: rows_per_group = out_dim);
+// the LDS image holds x_dim = n_groups * in_dim values per token, token t of
+// x at x + t * x_stride; y[t, r] at y + t * y_stride + r.
+struct Gemv1Shape {
+    int in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group;
+};
+
 template <class F, int NW, int PD, int GPT, int BT = 1>
 __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w, uint32_t w_bytes,
                                                   const float *__restrict__ x,
-                                                  float *__restrict__ y, int in_dim, int out_dim,
+                                                  float *__restrict__ y, Gemv1Shape sh,
                                                   int n_wg, int n_tok) {
+    const int in_dim = sh.in_dim, out_dim = sh.out_dim;
     extern __shared__ uint4 xl[];
     constexpr int kHalves = F::kXF == 5 ? 2 : 1;
     constexpr int kThreads = 64 * NW;
     const int lane = threadIdx.x & 63, k = lane & 7, ks = lane >> 3;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nunits = F::units(in_dim), ncols = (nunits + 7) >> 3;
-    const int per_tok = ncols * 64 * kHalves;                           // groups per token
+    // x image: columns of the whole x_dim (group boundaries fall on columns)
+    const int xunits = F::units(sh.x_dim), xcols = (xunits + 7) >> 3;
+    const int per_tok = xcols * 64 * kHalves;                           // limb groups per token
     const int n_groups = per_tok * BT;
-    const uint32_t tok_fields = (uint32_t)ncols * F::kXF * 64;          // uint4 per token in LDS
+    const uint32_t tok_fields = (uint32_t)xcols * F::kXF * 64;          // uint4 per token in LDS
     const int r0 = blockIdx.x;
     const int nrows = (out_dim - r0 + n_wg - 1) / n_wg;                 // this workgroup's rows
     const int my_rows = nrows > wv ? (nrows - wv + NW - 1) / NW : 0;   // this wavefront's rows
     const int T = my_rows * ncols;                                       // its tiles
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
     const __amdgpu_buffer_rsrc_t rnull = make_rsrc(w, 0);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)n_tok * (uint32_t)in_dim * 4u);
+    const __amdgpu_buffer_rsrc_t rx =
+        make_rsrc(x, ((uint32_t)(n_tok - 1) * (uint32_t)sh.x_stride + (uint32_t)sh.x_dim) * 4u);
 
-    // group g (token g / per_tok) -> first element offset in x, or -1
+    // limb group g (token g / per_tok) -> first element offset in x, or -1
     auto group_off = [&](int g) {
         const int t = g / per_tok, rem = g - t * per_tok;
         const int col = rem / (64 * kHalves), r2 = rem % (64 * kHalves);
         const int half = r2 >> 6, ln = r2 & 63;
         const int kk = ln & 7, unit = col * 8 + (ln >> 3);
-        const bool ok = g < n_groups && t < n_tok && unit < nunits && F::valid(unit, kk, in_dim);
-        return ok ? t * in_dim + (half ? F::elem_hi(unit, kk) : F::elem_lo(unit, kk)) : -1;
+        const bool ok = g < n_groups && t < n_tok && unit < xunits && F::valid(unit, kk, sh.x_dim);
+        return ok ? t * sh.x_stride + (half ? F::elem_hi(unit, kk) : F::elem_lo(unit, kk)) : -1;
     };
     auto row_of = [&](int j) { return r0 + n_wg * (wv + NW * j); };
     typename F::Slice buf[PD];
@@ -264,6 +276,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
 #pragma unroll
     for (int tk = 0; tk < BT; tk++) acc[tk] = 0.f;
     int col = 0, j = 0;
+    int xc0 = (row_of(0) / sh.rows_per_group) * ncols;  // x column of the row's group
     for (int t0 = 0; t0 < T; t0 += PD) {
 #pragma unroll
         for (int jj = 0; jj < PD; jj++) {
@@ -275,7 +288,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
 #pragma unroll
             for (int tk = 0; tk < BT; tk++) {
                 XSlice xs;
-                const uint4 *bx = xl + tk * tok_fields + col * F::kXF * 64 + lane;
+                const uint4 *bx = xl + tk * tok_fields + (xc0 + col) * F::kXF * 64 + lane;
                 xs.hlo = bx[0];
                 xs.llo = bx[64];
                 xs.meta = bx[128];
@@ -290,11 +303,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
 #pragma unroll
                 for (int tk = 0; tk < BT; tk++) {
                     const float tot = wave_sum_dpp(acc[tk]);
-                    if (lane == 0 && t < T && tk < n_tok) y[(size_t)tk * out_dim + row_of(j)] = tot;
+                    if (lane == 0 && t < T && tk < n_tok)
+                        y[(size_t)tk * sh.y_stride + row_of(j)] = tot;
                     acc[tk] = 0.f;
                 }
                 col = 0;
                 j++;
+                xc0 = (min(row_of(j), out_dim - 1) / sh.rows_per_group) * ncols;
             } else {
                 col++;
             }
@@ -303,11 +318,11 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
     }
 }
 
-// LDS of k_gemv1: the quantised x (bt tokens x ncols columns) plus one
-// spare column.
+// LDS of k_gemv1: the quantised x (bt tokens x the columns of x_dim) plus
+// one spare column.
 template <class F>
-static size_t gemv1_lds_bytes(int in_dim, int bt = 1) {
-    const int ncols = ((in_dim + F::kEPU - 1) / F::kEPU + 7) >> 3;
+static size_t gemv1_lds_bytes(int x_dim, int bt = 1) {
+    const int ncols = ((x_dim + F::kEPU - 1) / F::kEPU + 7) >> 3;
     return (size_t)(bt * ncols + 1) * F::kXF * 1024;
 }
 
@@ -321,8 +336,8 @@ static int gemv1_gpt(int in_dim, int nw, int bt = 1) {
 }
 
 template <class F, int NW, int PD, int GPT, int BT>
-static hipError_t gemv1_go(const uint8_t *w, size_t w_bytes, const float *x, float *y, int in_dim,
-                           int out_dim, int n_tok, int n_wg, hipStream_t s) {
+static hipError_t gemv1_go(const uint8_t *w, size_t w_bytes, const float *x, float *y,
+                           const Gemv1Shape &sh, int n_tok, int n_wg, hipStream_t s) {
     static bool attr_set = false;  // per instantiation; idempotent if raced
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void *)k_gemv1<F, NW, PD, GPT, BT>,
@@ -331,21 +346,26 @@ static hipError_t gemv1_go(const uint8_t *w, size_t w_bytes, const float *x, flo
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    n_wg = min(n_wg, out_dim);
-    k_gemv1<F, NW, PD, GPT, BT><<<(unsigned)n_wg, 64 * NW, gemv1_lds_bytes<F>(in_dim, BT), s>>>(
-        w, (uint32_t)w_bytes, x, y, in_dim, out_dim, n_wg, n_tok);
+    n_wg = min(n_wg, sh.out_dim);
+    k_gemv1<F, NW, PD, GPT, BT><<<(unsigned)n_wg, 64 * NW, gemv1_lds_bytes<F>(sh.x_dim, BT), s>>>(
+        w, (uint32_t)w_bytes, x, y, sh, n_wg, n_tok);
     return hipGetLastError();
 }
 
 template <class F, int NW, int PD, int BT = 1>
 static hipError_t gemv1_gpt_go(const uint8_t *w, size_t w_bytes, const float *x, float *y,
-                               int in_dim, int out_dim, int n_tok, int n_wg, hipStream_t s) {
-    switch (gemv1_gpt<F>(in_dim, NW, BT)) {
-    case 1: return gemv1_go<F, NW, PD, 1, BT>(w, w_bytes, x, y, in_dim, out_dim, n_tok, n_wg, s);
-    case 2: return gemv1_go<F, NW, PD, 2, BT>(w, w_bytes, x, y, in_dim, out_dim, n_tok, n_wg, s);
-    case 4: return gemv1_go<F, NW, PD, 4, BT>(w, w_bytes, x, y, in_dim, out_dim, n_tok, n_wg, s);
+                               const Gemv1Shape &sh, int n_tok, int n_wg, hipStream_t s) {
+    switch (gemv1_gpt<F>(sh.x_dim, NW, BT)) {
+    case 1: return gemv1_go<F, NW, PD, 1, BT>(w, w_bytes, x, y, sh, n_tok, n_wg, s);
+    case 2: return gemv1_go<F, NW, PD, 2, BT>(w, w_bytes, x, y, sh, n_tok, n_wg, s);
+    case 4: return gemv1_go<F, NW, PD, 4, BT>(w, w_bytes, x, y, sh, n_tok, n_wg, s);
     default: return hipErrorInvalidValue;
     }
+}
+
+static Gemv1Shape plain_shape(int n_tok, int in_dim, int out_dim) {
+    (void)n_tok;
+    return Gemv1Shape{in_dim, out_dim, in_dim, in_dim, out_dim, out_dim};
 }
 
 // ---- grouped GEMV (routed experts) ------------------------------------------
@@ -628,14 +648,14 @@ hipError_t launch_gemv_prequant(uint32_t dtype, const uint8_t *w, size_t w_bytes
 // rest; smaller ones use one 16-wavefront workgroup per CU with two tiles in
 // flight. Chosen from sweeps of the C0-C3 shapes on MI355X.
 template <class F>
-static hipError_t gemv1(const uint8_t *w, size_t w_bytes, const float *x, float *y, int in_dim,
-                        int out_dim, hipStream_t s) {
+static hipError_t gemv1(const uint8_t *w, size_t w_bytes, const float *x, float *y,
+                        const Gemv1Shape &sh, hipStream_t s) {
     const int cus = device_cus();
     if (w_bytes >= ((size_t)32 << 20)) {
-        if (out_dim >= 2 * in_dim) return gemv1_gpt_go<F, 8, 2>(w, w_bytes, x, y, in_dim, out_dim, 1, 2 * cus, s);
-        return gemv1_gpt_go<F, 8, 3>(w, w_bytes, x, y, in_dim, out_dim, 1, cus, s);
+        if (sh.out_dim >= 2 * sh.in_dim) return gemv1_gpt_go<F, 8, 2>(w, w_bytes, x, y, sh, 1, 2 * cus, s);
+        return gemv1_gpt_go<F, 8, 3>(w, w_bytes, x, y, sh, 1, cus, s);
     }
-    return gemv1_gpt_go<F, 16, 2>(w, w_bytes, x, y, in_dim, out_dim, 1, cus, s);
+    return gemv1_gpt_go<F, 16, 2>(w, w_bytes, x, y, sh, 1, cus, s);
 }
 
 template <class F>
@@ -656,12 +676,12 @@ static int gemv1_bt(int n_tok, int in_dim) {
 // (sweeps of the C0-C2 shapes at 2, 4 and 8 tokens).
 template <class F>
 static hipError_t gemv1_batch(const uint8_t *w, size_t w_bytes, const float *x, float *y,
-                              int n_tok, int in_dim, int out_dim, hipStream_t s) {
+                              const Gemv1Shape &sh, int n_tok, hipStream_t s) {
     const int cus = device_cus();
-    switch (gemv1_bt<F>(n_tok, in_dim)) {
-    case 2: return gemv1_gpt_go<F, 16, 2, 2>(w, w_bytes, x, y, in_dim, out_dim, n_tok, cus, s);
-    case 4: return gemv1_gpt_go<F, 16, 2, 4>(w, w_bytes, x, y, in_dim, out_dim, n_tok, cus, s);
-    case 8: return gemv1_gpt_go<F, 16, 2, 8>(w, w_bytes, x, y, in_dim, out_dim, n_tok, cus, s);
+    switch (gemv1_bt<F>(n_tok, sh.x_dim)) {
+    case 2: return gemv1_gpt_go<F, 16, 2, 2>(w, w_bytes, x, y, sh, n_tok, cus, s);
+    case 4: return gemv1_gpt_go<F, 16, 2, 4>(w, w_bytes, x, y, sh, n_tok, cus, s);
+    case 8: return gemv1_gpt_go<F, 16, 2, 8>(w, w_bytes, x, y, sh, n_tok, cus, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -677,6 +697,140 @@ static int gemv1_tokens(uint32_t dtype, int n_tok, int in_dim) {
     return 0;
 }
 
+// ---- f32 weights (WeightBlob::F32) ----------------------------------------------
+// y[t * y_stride + r] = sum_i w[r * in_dim + i] * x[t * x_stride + g(r) * in_dim + i],
+// g(r) = r / rows_per_group: matmul_weight_f32's F32 arm (weight.rs:139-158)
+// and, with groups, matmul_grouped_lora_down over F32 blobs. Rows are dealt
+// as in k_gemv1 and streamed whole: a tile is 256 consecutive elements (lane
+// l takes l, l + 64, l + 128, l + 192: four coalesced dword loads), PD tiles
+// in flight, fp32 FMA; tokens in chunks of BT (one weight pass per chunk).
+template <int NW, int PD, int BT>
+__global__ __launch_bounds__(64 * NW) void k_gemv_f32(const float *__restrict__ w,
+                                                     const float *__restrict__ x,
+                                                     float *__restrict__ y, Gemv1Shape sh,
+                                                     int n_wg, int n_tok) {
+    const int in_dim = sh.in_dim, out_dim = sh.out_dim;
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r0 = blockIdx.x;
+    const int nrows = (out_dim - r0 + n_wg - 1) / n_wg;
+    const int my_rows = nrows > wv ? (nrows - wv + NW - 1) / NW : 0;
+    const int ncols = (in_dim + 255) >> 8;
+    const int T = my_rows * ncols;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)((size_t)out_dim * in_dim * 4u));
+    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(w, 0);
+    const __amdgpu_buffer_rsrc_t rx =
+        make_rsrc(x, ((uint32_t)(n_tok - 1) * (uint32_t)sh.x_stride + (uint32_t)sh.x_dim) * 4u);
+    auto row_of = [&](int j) { return r0 + n_wg * (wv + NW * j); };
+    struct Tile {
+        float v[4];
+    };
+    for (int t_base = 0; t_base < n_tok; t_base += BT) {
+        Tile buf[PD];
+        auto load_tile = [&](Tile &tl, int t) {
+            const int j = t / ncols, col = t - j * ncols;
+            const uint32_t rowoff = (uint32_t)min(row_of(j), out_dim - 1) * (uint32_t)in_dim;
+            const __amdgpu_buffer_rsrc_t r = t < T ? rw : rnull;
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const int e = col * 256 + m * 64 + lane;
+                const uint32_t off = e < in_dim ? (rowoff + (uint32_t)e) * 4u : 0x80000000u;
+                tl.v[m] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+            }
+        };
+#pragma unroll
+        for (int jj = 0; jj < PD - 1; jj++) load_tile(buf[jj], jj);
+        float acc[BT];
+#pragma unroll
+        for (int tk = 0; tk < BT; tk++) acc[tk] = 0.f;
+        int col = 0, j = 0;
+        for (int t0 = 0; t0 < T; t0 += PD) {
+#pragma unroll
+            for (int jj = 0; jj < PD; jj++) {
+                const int t = t0 + jj;
+                load_tile(buf[(jj + PD - 1) % PD], t + PD - 1);
+                __builtin_amdgcn_sched_barrier(0);
+                const int row = min(row_of(j), out_dim - 1);
+                const uint32_t xg = (uint32_t)(row / sh.rows_per_group) * (uint32_t)in_dim;
+#pragma unroll
+                for (int tk = 0; tk < BT; tk++) {
+                    const uint32_t xt = (uint32_t)(t_base + tk) * (uint32_t)sh.x_stride + xg;
+#pragma unroll
+                    for (int m = 0; m < 4; m++) {
+                        const int e = col * 256 + m * 64 + lane;
+                        const bool ok = e < in_dim && t < T && t_base + tk < n_tok;
+                        const uint32_t off = ok ? (xt + (uint32_t)e) * 4u : 0x80000000u;
+                        const float xv = __uint_as_float(
+                            (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rx, (int)off, 0, 0));
+                        acc[tk] = fmaf(buf[jj].v[m], xv, acc[tk]);
+                    }
+                }
+                if (col == ncols - 1) {
+#pragma unroll
+                    for (int tk = 0; tk < BT; tk++) {
+                        const float tot = wave_sum_dpp(acc[tk]);
+                        if (lane == 0 && t < T && t_base + tk < n_tok)
+                            y[(size_t)(t_base + tk) * sh.y_stride + row_of(j)] = tot;
+                        acc[tk] = 0.f;
+                    }
+                    col = 0;
+                    j++;
+                } else {
+                    col++;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+}
+
+hipError_t launch_gemv_f32(const float *w, const float *x, float *y, int n_tok, int in_dim,
+                           int out_dim, int x_dim, int x_stride, int y_stride, int rows_per_group,
+                           hipStream_t s) {
+    if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
+    const Gemv1Shape sh{in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group};
+    const int n_wg = min(device_cus(), out_dim);
+    // x offsets are 32-bit byte offsets: launch in token chunks of < 2 GiB of x
+    const size_t per = ((size_t)1 << 29) / (size_t)(x_stride > 0 ? x_stride : 1);
+    const int chunk = per == 0 ? 1 : per > (size_t)n_tok ? n_tok : (int)per;
+    for (int t0 = 0; t0 < n_tok; t0 += chunk) {
+        k_gemv_f32<16, 2, 4><<<(unsigned)n_wg, 64 * 16, 0, s>>>(
+            w, x + (size_t)t0 * x_stride, y + (size_t)t0 * y_stride, sh, n_wg,
+            min(chunk, n_tok - t0));
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// Quantized rows with strided / grouped x and y through k_gemv1 (up to 8
+// tokens with their x in LDS). hipErrorNotSupported: shape not covered.
+hipError_t launch_gemv_rows(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
+                            float *y, int n_tok, int in_dim, int out_dim, int x_dim, int x_stride,
+                            int y_stride, int rows_per_group, hipStream_t s) {
+    if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
+    const Gemv1Shape sh{in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group};
+    const int bt = gemv1_tokens(dtype, n_tok, x_dim);
+    if (bt == 0) return hipErrorNotSupported;
+    if (x_dim != in_dim) {  // several groups: each must start on an x column
+        size_t be = 0;
+#define X(T, F) if (dtype == T) be = (size_t)F::kEPU * 8;
+        GEMV_FORMATS(X)
+#undef X
+        if (be == 0 || in_dim % be != 0) return hipErrorNotSupported;
+    }
+    if (bt == 1) {
+#define X(T, F) if (dtype == T) return gemv1<F>(w, w_bytes, x, y, sh, s);
+        GEMV_FORMATS(X)
+#undef X
+    } else {
+#define X(T, F) if (dtype == T) return gemv1_batch<F>(w, w_bytes, x, y, sh, n_tok, s);
+        GEMV_FORMATS(X)
+#undef X
+    }
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
                        uint8_t *xq_scratch, float *y, int n_tok, int in_dim, int out_dim,
                        hipStream_t s) {
@@ -684,14 +838,15 @@ hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const f
     if (gemv_mfma_supported(dtype, n_tok, in_dim, out_dim))
         return launch_gemv_mfma(dtype, w, w_bytes, x, xq_scratch, y, n_tok, in_dim, out_dim, s);
     const int bt = gemv1_tokens(dtype, n_tok, in_dim);
+    const Gemv1Shape sh = plain_shape(n_tok, in_dim, out_dim);
     if (bt == 1) {
-#define X(T, F) if (dtype == T) return gemv1<F>(w, w_bytes, x, y, in_dim, out_dim, s);
+#define X(T, F) if (dtype == T) return gemv1<F>(w, w_bytes, x, y, sh, s);
         GEMV_FORMATS(X)
 #undef X
         return hipErrorInvalidValue;
     }
     if (bt > 1) {
-#define X(T, F) if (dtype == T) return gemv1_batch<F>(w, w_bytes, x, y, n_tok, in_dim, out_dim, s);
+#define X(T, F) if (dtype == T) return gemv1_batch<F>(w, w_bytes, x, y, sh, n_tok, s);
         GEMV_FORMATS(X)
 #undef X
         return hipErrorInvalidValue;

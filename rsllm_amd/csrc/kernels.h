@@ -55,6 +55,19 @@ size_t gemv_scratch_bytes(uint32_t dtype, int n_tok, int in_dim);
 // path for 2..32 tokens keeps f16 activations there).
 size_t gemv_work_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim);
 
+// gemv.hip, caller chain (weight.rs:113-266): f32 weights
+// (WeightBlob::F32) and quantized rows with strided / grouped x and y:
+// y[t * y_stride + r] = sum_i W[r, i] x[t * x_stride + (r / rows_per_group)
+// * in_dim + i], x_dim = n_groups * in_dim values of x per token.
+// launch_gemv_rows returns hipErrorNotSupported for shapes it does not cover
+// (more than 8 tokens, x too long for LDS, groups not on x columns).
+hipError_t launch_gemv_f32(const float *w, const float *x, float *y, int n_tok, int in_dim,
+                           int out_dim, int x_dim, int x_stride, int y_stride, int rows_per_group,
+                           hipStream_t s);
+hipError_t launch_gemv_rows(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
+                            float *y, int n_tok, int in_dim, int out_dim, int x_dim, int x_stride,
+                            int y_stride, int rows_per_group, hipStream_t s);
+
 // gemv_mfma.hip: the same product for 5..32 tokens of Q4_K / Q6_K on the
 // matrix cores (weights dequantised to f16 once, tokens as the MFMA's N).
 bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim);
