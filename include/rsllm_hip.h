@@ -269,6 +269,39 @@ int rsllm_hip_matmul_grouped_lora_down_dev(float *out, size_t out_len, const uin
                                            size_t rank, uint32_t dtype,
                                            rsllm_hip_stream_t stream);
 
+/* ---- shared expert: apply_shared_expert / apply_expert_swiglu ---------------
+ * rsllm_hip_apply_shared_expert replaces apply_shared_expert
+ * (rsllm-models/src/dsv4/moe.rs:422-455): every token t of x [n_tok x
+ * n_embd] through apply_expert_swiglu (:479-502),
+ *   out[t] = down @ (silu(min(gate @ x[t], c)) * clamp(up @ x[t], -c, c)),
+ * out [n_tok x n_embd] overwritten. apply_expert_swiglu on one token is the
+ * n_tok = 1 call. gate and up are [n_ff x n_embd] and down [n_embd x n_ff]
+ * WeightBlobs, each F32 (dtype 0, length in bytes) or a quant dtype of its
+ * own; the clamp is skipped when clamp <= 1e-6 (apply_swiglu_clamp
+ * :515-531, so 0 stands for the reference's None). Validation:
+ * check_moe_shapes (:557-573) x_len then out_len (SHAPE_MISMATCH "moe.x" /
+ * "moe.out"), then, if n_tok > 0, matmul_weight_f32's checks of the gate,
+ * up and down calls in that order (as for rsllm_hip_matmul_weight_f32).
+ * Gate and up of one quant format with a quant down run as one routed
+ * expert of weight 1 through the routed-expert kernels (SwiGLU in the
+ * gate/up epilogue); other combinations as separate GEMVs and an
+ * elementwise SwiGLU. Host blobs registered with
+ * rsllm_hip_register_weights are used from the device.
+ *
+ * Device form: blobs in the device layout (rsllm_hip_prepare_weights_dev
+ * for quant formats; F32 as is), enqueued on `stream`. */
+int rsllm_hip_apply_shared_expert(float *out, size_t out_len, const float *x, size_t x_len,
+                                  const uint8_t *gate, size_t gate_len, uint32_t dtype_gate,
+                                  const uint8_t *up, size_t up_len, uint32_t dtype_up,
+                                  const uint8_t *down, size_t down_len, uint32_t dtype_down,
+                                  size_t n_tok, size_t n_embd, size_t n_ff, float clamp);
+int rsllm_hip_apply_shared_expert_dev(float *out, size_t out_len, const float *x, size_t x_len,
+                                      const uint8_t *gate, size_t gate_len, uint32_t dtype_gate,
+                                      const uint8_t *up, size_t up_len, uint32_t dtype_up,
+                                      const uint8_t *down, size_t down_len, uint32_t dtype_down,
+                                      size_t n_tok, size_t n_embd, size_t n_ff, float clamp,
+                                      rsllm_hip_stream_t stream);
+
 /* ---- Q8_0 int8-activation path ---------------------------------------------
  * quantize_q8_0_batch (backend-cpu/src/ops/q8_0.rs:95-129, per token
  * quantize_q8_0_activation :42-88): x [n_tok x in_dim] -> xq [n_tok x blocks

@@ -66,6 +66,8 @@ def lib() -> ctypes.CDLL:
         L.orc_moe_routed.argtypes = [P, P, S, S, S, P, P, P, U32, U32, S, P, P, S, ctypes.c_float]
         L.orc_matmul_weight_f32.argtypes = [P, S, P, S, P, S, S, S, S, U32, I]
         L.orc_matmul_grouped_lora_down.argtypes = [P, S, P, S, P, S, S, S, S, S, U32, I]
+        L.orc_apply_shared_expert.argtypes = [P, S, P, S, P, S, U32, P, S, U32, P, S, U32, S, S, S,
+                                              ctypes.c_float]
         L.orc_last_detail.argtypes = [P, P]
         L.orc_iq2xxs_grid.argtypes = [I]
         L.orc_iq2xxs_grid.restype = ctypes.c_uint64
@@ -215,6 +217,19 @@ def moe_routed(out, x, n_tok, n_embd, n_ff, gate, up, down, dtype_gu, dtype_down
     return lib().orc_moe_routed(_p(out), _p(x), n_tok, n_embd, n_ff, _p(gate), _p(up), _p(down),
                                 dtype_gu, dtype_down, n_expert, _p(ids), _p(weights), k,
                                 ctypes.c_float(clamp))
+
+
+def apply_shared_expert(x, gate, dt_gate, up, dt_up, down, dt_down, n_tok, n_embd, n_ff, clamp,
+                        out_len=None):
+    """Returns (status, out); weights are float32 arrays for F32, else bytes."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    g, u, d = _weight_bytes(gate), _weight_bytes(up), _weight_bytes(down)
+    n_out = n_tok * n_embd if out_len is None else out_len
+    out = np.full(max(n_out, 0), np.nan, dtype=np.float32)
+    rc = lib().orc_apply_shared_expert(_p(out), out.size, _p(x), x.size, _p(g), g.size, dt_gate,
+                                       _p(u), u.size, dt_up, _p(d), d.size, dt_down, n_tok, n_embd,
+                                       n_ff, ctypes.c_float(clamp))
+    return rc, out
 
 
 def num_cores() -> int:

@@ -37,6 +37,11 @@
  *                         out-shape rejection), float64 recompute of the F32
  *                         arm, the grouped form equal to per-group
  *                         orc_matmul_quant_f32 on the slices
+ *   orc_apply_shared_expert
+ *                         the reference's clamp test (moe.rs:743-789:
+ *                         identity F32 weights, x[0] = 1e3 gives silu(10) *
+ *                         10), equality with orc_moe_routed on one expert
+ *                         of weight 1, float64 recompute of the F32 form
  */
 #define _GNU_SOURCE
 #include "rsllm_oracle.h"
@@ -664,6 +669,46 @@ void orc_swiglu_clamp(float *h_gate, float *h_up, size_t n, float c) {
         if (h_up[j] > c) h_up[j] = c;
         else if (h_up[j] < -c) h_up[j] = -c;
     }
+}
+
+/* ---- shared expert: apply_shared_expert moe.rs:422-455 ----------------------
+ * check_moe_shapes (:557-573: x then out), then per token apply_expert_swiglu
+ * (:479-502): gate and up through matmul_weight_f32, the clamp, silu(g) * u
+ * (scalar.rs:80-86), down through matmul_weight_f32 into out_t (overwritten).
+ * Errors: ORC_SHAPE_MISMATCH detail a = 30 (x), 31 (out), else those of
+ * orc_matmul_weight_f32 with detail b = 0 (gate), 1 (up), 2 (down). */
+int orc_apply_shared_expert(float *out, size_t out_len, const float *x, size_t x_len,
+                            const uint8_t *gate, size_t gate_len, uint32_t dt_gate,
+                            const uint8_t *up, size_t up_len, uint32_t dt_up,
+                            const uint8_t *down, size_t down_len, uint32_t dt_down, size_t n_tok,
+                            size_t n_embd, size_t n_ff, float clamp) {
+    size_t need;
+    if (__builtin_mul_overflow(n_tok, n_embd, &need) || x_len != need)
+        return fail2(ORC_SHAPE_MISMATCH, 30, 0);
+    if (out_len != need) return fail2(ORC_SHAPE_MISMATCH, 31, 0);
+    float *h_gate = (float *)malloc(sizeof(float) * (n_ff + 1));
+    float *h_up = (float *)malloc(sizeof(float) * (n_ff + 1));
+    float *h_act = (float *)malloc(sizeof(float) * (n_ff + 1));
+    int rc = ORC_OK;
+    size_t a, b;
+    for (size_t t = 0; t < n_tok && rc == ORC_OK; t++) {
+        const float *x_t = x + t * n_embd;
+        rc = orc_matmul_weight_f32(h_gate, n_ff, gate, gate_len, x_t, n_embd, 1, n_embd, n_ff,
+                                   dt_gate, 1);
+        if (rc) { orc_last_detail(&a, &b); fail2(rc, a, 0); break; }
+        rc = orc_matmul_weight_f32(h_up, n_ff, up, up_len, x_t, n_embd, 1, n_embd, n_ff, dt_up,
+                                   1);
+        if (rc) { orc_last_detail(&a, &b); fail2(rc, a, 1); break; }
+        orc_swiglu_clamp(h_gate, h_up, n_ff, clamp);
+        for (size_t j = 0; j < n_ff; j++) h_act[j] = orc_silu(h_gate[j]) * h_up[j];
+        rc = orc_matmul_weight_f32(out + t * n_embd, n_embd, down, down_len, h_act, n_ff, 1, n_ff,
+                                   n_embd, dt_down, 1);
+        if (rc) { orc_last_detail(&a, &b); fail2(rc, a, 2); break; }
+    }
+    free(h_gate);
+    free(h_up);
+    free(h_act);
+    return rc;
 }
 
 /* ---- routed experts: moe.rs:479-531 and :648-707 -------------------------- */

@@ -139,6 +139,17 @@ int orc_matmul_grouped_lora_down(float *out, size_t out_len, const uint8_t *w, s
                                  const float *x, size_t x_len, size_t n_tok, size_t n_groups,
                                  size_t group_dim, size_t rank, uint32_t dtype, int allow_q6k);
 
+/* apply_shared_expert, rsllm-models/src/dsv4/moe.rs:422-455 with
+ * apply_expert_swiglu :479-502 (one expert through every token; out is
+ * overwritten). Each matrix is a WeightBlob of its own dtype (ORC_F32 or a
+ * quant type). Errors: ORC_SHAPE_MISMATCH detail a = 30 (x), 31 (out), or
+ * orc_matmul_weight_f32's with detail b = 0 / 1 / 2 for gate / up / down. */
+int orc_apply_shared_expert(float *out, size_t out_len, const float *x, size_t x_len,
+                            const uint8_t *gate, size_t gate_len, uint32_t dt_gate,
+                            const uint8_t *up, size_t up_len, uint32_t dt_up,
+                            const uint8_t *down, size_t down_len, uint32_t dt_down, size_t n_tok,
+                            size_t n_embd, size_t n_ff, float clamp);
+
 /* Online core count (what rayon's global pool would size itself to). */
 int orc_num_cores(void);
 

@@ -147,6 +147,10 @@ SIGNATURES = {
     "rsllm_hip_matmul_grouped_lora_down": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _S, _U32], _I),
     "rsllm_hip_matmul_grouped_lora_down_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _S, _U32, _P],
                                                _I),
+    "rsllm_hip_apply_shared_expert": ([_P, _S, _P, _S, _P, _S, _U32, _P, _S, _U32, _P, _S, _U32,
+                                       _S, _S, _S, ctypes.c_float], _I),
+    "rsllm_hip_apply_shared_expert_dev": ([_P, _S, _P, _S, _P, _S, _U32, _P, _S, _U32, _P, _S,
+                                           _U32, _S, _S, _S, ctypes.c_float, _P], _I),
 }
 
 
@@ -362,6 +366,34 @@ def moe_routed_dev(out_ptr: int, out_len: int, x_ptr: int, x_len: int, gate_ptr:
                                         weights_ptr or None, ids_len, n_tok, n_embd, n_ff,
                                         n_expert, k, int(dtype_gate_up), int(dtype_down), clamp,
                                         stream or None))
+
+
+def apply_shared_expert(out: np.ndarray, x: np.ndarray, gate, dtype_gate, up, dtype_up, down,
+                        dtype_down, n_tok: int, n_embd: int, n_ff: int,
+                        clamp: float = 10.0) -> None:
+    """apply_shared_expert (rsllm-models/src/dsv4/moe.rs:422-455): every
+    token of x [n_tok x n_embd] through one SwiGLU expert (apply_expert_swiglu
+    :479-502) into ``out`` (overwritten). Each blob is F32 values (dtype
+    GgmlType.F32) or quantized bytes of its own dtype."""
+    po, no = _host_f32(out, "out")
+    px, nx = _host_f32(x, "x")
+    pg, ng = _host_bytes(gate)
+    pu, nu = _host_bytes(up)
+    pd, nd = _host_bytes(down)
+    _check(LIB.rsllm_hip_apply_shared_expert(po, no, px, nx, pg, ng, int(dtype_gate), pu, nu,
+                                             int(dtype_up), pd, nd, int(dtype_down), n_tok,
+                                             n_embd, n_ff, clamp))
+
+
+def apply_shared_expert_dev(out_ptr: int, out_len: int, x_ptr: int, x_len: int, gate_ptr: int,
+                            gate_len: int, dtype_gate, up_ptr: int, up_len: int, dtype_up,
+                            down_ptr: int, down_len: int, dtype_down, n_tok: int, n_embd: int,
+                            n_ff: int, clamp: float = 10.0, stream: int = 0) -> None:
+    _check(LIB.rsllm_hip_apply_shared_expert_dev(out_ptr or None, out_len, x_ptr or None, x_len,
+                                                 gate_ptr or None, gate_len, int(dtype_gate),
+                                                 up_ptr or None, up_len, int(dtype_up),
+                                                 down_ptr or None, down_len, int(dtype_down),
+                                                 n_tok, n_embd, n_ff, clamp, stream or None))
 
 
 def quantize_q8_0_batch(x: np.ndarray, xq: np.ndarray, scale: np.ndarray, n_tok: int,

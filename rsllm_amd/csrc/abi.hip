@@ -207,6 +207,30 @@ const uint8_t *find_registered(const uint8_t *host, size_t len, uint32_t dtype, 
 
 bool needs_prepare(uint32_t dtype) { return dtype != T_Q4_K; }
 
+// A host weight blob on the device for one call: its registered copy, else
+// uploaded into `dst` (quant formats other than Q4_K converted to the device
+// layout through the w_raw staging buffer). F32 blobs are uploaded as is.
+int blob_on_device(const uint8_t *blob, size_t len, uint32_t dtype, size_t in_dim, DevBuf &dst,
+                   const uint8_t **dev) {
+    ThreadCtx &c = t_ctx;
+    if (dtype != T_F32 && (*dev = find_registered(blob, len, dtype, in_dim))) return RSLLM_HIP_OK;
+    HIP_TRY(dst.ensure(len), "hipMalloc");
+    if (dtype == T_F32 || !needs_prepare(dtype) || in_dim == 0) {
+        if (len)
+            HIP_TRY(hipMemcpyAsync(dst.p, blob, len, hipMemcpyHostToDevice, c.stream),
+                    "upload weights");
+    } else {
+        HIP_TRY(c.w_raw.ensure(len), "hipMalloc");
+        HIP_TRY(hipMemcpyAsync(c.w_raw.p, blob, len, hipMemcpyHostToDevice, c.stream),
+                "upload weights");
+        HIP_TRY(launch_prepare(dtype, (const uint8_t *)c.w_raw.p, (uint8_t *)dst.p,
+                               len / row_bytes_of(dtype, in_dim), in_dim, c.stream),
+                "prepare weights");
+    }
+    *dev = (const uint8_t *)dst.p;
+    return RSLLM_HIP_OK;
+}
+
 
 // ---- caller chain (weight.rs:113-266) --------------------------------------
 // matmul_weight_f32: out, x lengths (:121-135), then the F32 arm's weight
@@ -381,6 +405,71 @@ int lora_down_compute(float *out, size_t out_len, const uint8_t *w, size_t strid
                 "scatter y");
     }
     return ok();
+}
+
+// ---- shared expert (moe.rs:422-502) ------------------------------------------
+// check_moe_shapes (:557-573: x, then out), then the matmul_weight_f32
+// checks of the first token's gate (n_embd -> n_ff), up and down (n_ff ->
+// n_embd) calls, which are the same for every token; n_tok == 0 runs no
+// matmul and is Ok.
+int validate_shared(size_t out_len, const void *out, size_t x_len, const void *x,
+                    const uint8_t *gate, size_t gate_len, uint32_t dt_gate, const uint8_t *up,
+                    size_t up_len, uint32_t dt_up, const uint8_t *down, size_t down_len,
+                    uint32_t dt_down, size_t n_tok, size_t n_embd, size_t n_ff) {
+    static const float kInternal = 0.f;  // stands for the h_gate / h_up / h_act scratch
+    size_t need;
+    if (!mul_ok(n_tok, n_embd, &need) || x_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "moe.x: x must be n_tok * n_embd");
+    if (out_len != need)
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "moe.out: out must be n_tok * n_embd");
+    if (n_tok == 0) return RSLLM_HIP_OK;
+    int rc = validate_weight_f32(n_ff, gate, gate_len, x, n_embd, &kInternal, 1, n_embd, n_ff,
+                                 dt_gate);
+    if (!rc) rc = validate_weight_f32(n_ff, up, up_len, x, n_embd, &kInternal, 1, n_embd, n_ff,
+                                      dt_up);
+    if (!rc) rc = validate_weight_f32(n_embd, down, down_len, &kInternal, n_ff, out, 1, n_ff,
+                                      n_embd, dt_down);
+    if (rc) return rc;
+    if (!mul_ok(n_tok, n_ff, &need) || !fits_int(need) || !fits_int(n_tok * n_embd))
+        return set_err(RSLLM_HIP_ERR_SHAPE_MISMATCH, "apply_shared_expert: size exceeds 2^31-1");
+    return RSLLM_HIP_OK;
+}
+
+// apply_shared_expert on device pointers (validated). Gate and up of one
+// quant format with a quant down run as one routed expert of weight 1
+// through launch_moe (SwiGLU in the gate/up epilogue, out = 0 + 1 * y);
+// anything else as gate, up (matmul_weight_f32), k_swiglu, down.
+int shared_compute(float *out, const float *x, const uint8_t *gate, size_t gate_len,
+                   uint32_t dt_gate, const uint8_t *up, size_t up_len, uint32_t dt_up,
+                   const uint8_t *down, size_t down_len, uint32_t dt_down, size_t n_tok,
+                   size_t n_embd, size_t n_ff, float clamp, hipStream_t s) {
+    if (n_tok == 0 || n_embd == 0) return ok();
+    ThreadCtx &c = t_ctx;
+    const int T = (int)n_tok, E = (int)n_embd, FF = (int)n_ff;
+    if (dt_gate == dt_up && dt_gate != T_F32 && dt_down != T_F32 && n_ff) {
+        const size_t mb = (moe_scratch_bytes(dt_gate, dt_down, T, 1, 1, E, FF) + 255) / 256 * 256;
+        const size_t rb = (n_tok * 4 + 255) / 256 * 256;
+        HIP_TRY(c.moe.ensure(mb + 2 * rb), "hipMalloc");
+        uint8_t *scr = (uint8_t *)c.moe.p;
+        int *ids = (int *)(scr + mb);
+        float *w = (float *)(scr + mb + rb);
+        HIP_TRY(launch_fill_route(ids, w, T, s), "fill_route");
+        HIP_TRY(launch_fill_zero(out, n_tok * n_embd, s), "fill_zero");
+        HIP_TRY(launch_moe(dt_gate, dt_down, gate, up, down, gate_len, down_len, x, ids, w, out,
+                           scr, T, 1, 1, E, FF, clamp, s),
+                "moe");
+        return ok();
+    }
+    const size_t hb = (n_tok * n_ff * 4 + 255) / 256 * 256;
+    HIP_TRY(c.xh.ensure(3 * hb + 256), "hipMalloc");
+    float *hg = (float *)c.xh.p, *hu = (float *)((uint8_t *)c.xh.p + hb),
+          *ha = (float *)((uint8_t *)c.xh.p + 2 * hb);
+    int rc = weight_f32_compute(hg, n_tok * n_ff, gate, gate_len, x, n_tok, n_embd, n_ff, dt_gate, s);
+    if (!rc) rc = weight_f32_compute(hu, n_tok * n_ff, up, up_len, x, n_tok, n_embd, n_ff, dt_up, s);
+    if (rc) return rc;
+    HIP_TRY(launch_swiglu(hg, hu, ha, n_tok * n_ff, clamp, s), "swiglu");
+    return weight_f32_compute(out, n_tok * n_embd, down, down_len, ha, n_tok, n_ff, n_embd,
+                              dt_down, s);
 }
 
 }  // namespace
@@ -665,25 +754,9 @@ int rsllm_hip_moe_routed(float *out, size_t out_len, const float *x, size_t x_le
     const uint32_t bdt[3] = {dtype_gate_up, dtype_gate_up, dtype_down};
     const size_t bin[3] = {n_embd, n_embd, n_ff};
     const uint8_t *dev[3];
-    for (int i = 0; i < 3; i++) {
-        dev[i] = find_registered(blob[i], blen[i], bdt[i], bin[i]);
-        if (dev[i]) continue;
-        DevBuf &dst = c.moe_w[i];
-        if (!needs_prepare(bdt[i])) {
-            HIP_TRY(dst.ensure(blen[i]), "hipMalloc");
-            HIP_TRY(hipMemcpyAsync(dst.p, blob[i], blen[i], hipMemcpyHostToDevice, c.stream),
-                    "upload experts");
-        } else {
-            HIP_TRY(c.w_raw.ensure(blen[i]), "hipMalloc");
-            HIP_TRY(dst.ensure(blen[i]), "hipMalloc");
-            HIP_TRY(hipMemcpyAsync(c.w_raw.p, blob[i], blen[i], hipMemcpyHostToDevice, c.stream),
-                    "upload experts");
-            HIP_TRY(launch_prepare(bdt[i], (const uint8_t *)c.w_raw.p, (uint8_t *)dst.p,
-                                   blen[i] / row_bytes_of(bdt[i], bin[i]), bin[i], c.stream),
-                    "prepare experts");
-        }
-        dev[i] = (const uint8_t *)dst.p;
-    }
+    for (int i = 0; i < 3; i++)
+        if ((rc = blob_on_device(blob[i], blen[i], bdt[i], bin[i], c.moe_w[i], &dev[i])))
+            return rc;
     // inputs: x | out | ids | weights, 256-byte aligned pieces
     const size_t a_x = (x_len * 4 + 255) / 256 * 256, a_o = (out_len * 4 + 255) / 256 * 256;
     const size_t a_i = (ids_len * 4 + 255) / 256 * 256;
@@ -1089,6 +1162,54 @@ int rsllm_hip_matmul_grouped_lora_down(float *out, size_t out_len, const uint8_t
                 "upload x");
     rc = lora_down_compute((float *)c.y.p, out_len, dw, stride, (const float *)c.x.p, n_tok,
                            n_groups, group_dim, rank, dtype, c.stream, per_group);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(out, c.y.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
+            "download out");
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    return ok();
+}
+
+// ---- shared expert --------------------------------------------------------------
+int rsllm_hip_apply_shared_expert_dev(float *out, size_t out_len, const float *x, size_t x_len,
+                                      const uint8_t *gate, size_t gate_len, uint32_t dtype_gate,
+                                      const uint8_t *up, size_t up_len, uint32_t dtype_up,
+                                      const uint8_t *down, size_t down_len, uint32_t dtype_down,
+                                      size_t n_tok, size_t n_embd, size_t n_ff, float clamp,
+                                      rsllm_hip_stream_t stream) {
+    int rc = validate_shared(out_len, out, x_len, x, gate, gate_len, dtype_gate, up, up_len,
+                             dtype_up, down, down_len, dtype_down, n_tok, n_embd, n_ff);
+    if (rc) return rc;
+    if ((rc = ensure_device())) return rc;
+    return shared_compute(out, x, gate, gate_len, dtype_gate, up, up_len, dtype_up, down,
+                          down_len, dtype_down, n_tok, n_embd, n_ff, clamp, (hipStream_t)stream);
+}
+
+int rsllm_hip_apply_shared_expert(float *out, size_t out_len, const float *x, size_t x_len,
+                                  const uint8_t *gate, size_t gate_len, uint32_t dtype_gate,
+                                  const uint8_t *up, size_t up_len, uint32_t dtype_up,
+                                  const uint8_t *down, size_t down_len, uint32_t dtype_down,
+                                  size_t n_tok, size_t n_embd, size_t n_ff, float clamp) {
+    int rc = validate_shared(out_len, out, x_len, x, gate, gate_len, dtype_gate, up, up_len,
+                             dtype_up, down, down_len, dtype_down, n_tok, n_embd, n_ff);
+    if (rc) return rc;
+    if (n_tok == 0 || n_embd == 0) return ok();
+    if ((rc = ensure_device())) return rc;
+    ThreadCtx &c = t_ctx;
+    const uint8_t *blob[3] = {gate, up, down};
+    const size_t blen[3] = {gate_len, up_len, down_len};
+    const uint32_t bdt[3] = {dtype_gate, dtype_up, dtype_down};
+    const size_t bin[3] = {n_embd, n_embd, n_ff};
+    const uint8_t *dev[3];
+    for (int i = 0; i < 3; i++)
+        if ((rc = blob_on_device(blob[i], blen[i], bdt[i], bin[i], c.moe_w[i], &dev[i])))
+            return rc;
+    HIP_TRY(c.x.ensure(x_len * sizeof(float) + 16), "hipMalloc");
+    HIP_TRY(c.y.ensure(out_len * sizeof(float)), "hipMalloc");
+    HIP_TRY(hipMemcpyAsync(c.x.p, x, x_len * sizeof(float), hipMemcpyHostToDevice, c.stream),
+            "upload x");
+    rc = shared_compute((float *)c.y.p, (const float *)c.x.p, dev[0], gate_len, dtype_gate, dev[1],
+                        up_len, dtype_up, dev[2], down_len, dtype_down, n_tok, n_embd, n_ff, clamp,
+                        c.stream);
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(out, c.y.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
             "download out");

@@ -123,6 +123,13 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
                       const int *ids, const float *wts, float *out, uint8_t *scratch, int n_tok,
                       int k, int n_expert, int n_embd, int n_ff, float clamp, hipStream_t s);
 
+// moe.hip, shared expert: elementwise clamped SwiGLU a = silu(min(g, c)) *
+// clamp(u, -c, c) (no clamp when c <= 1e-6), and the one-expert routing
+// table (ids 0, weights 1) for running one expert over n tokens.
+hipError_t launch_swiglu(const float *g, const float *u, float *a, size_t n, float c,
+                         hipStream_t s);
+hipError_t launch_fill_route(int *ids, float *w, int n, hipStream_t s);
+
 // q8_int8.hip: the Q8_0 int8-activation path. launch_q8_quantize writes
 // xq [n_tok x blocks x 32] int8 and scale [n_tok x blocks] (blocks =
 // ceil(in_dim / 32)) and ORs 1 into *status (if non-null) when a token has

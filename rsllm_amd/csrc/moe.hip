@@ -234,8 +234,8 @@ __device__ __forceinline__ void moe_store_groups(const MoeGroups<F, GPT> &g, uin
 
 // One kernel body for both halves (GU = true: gate and up; false: down).
 // Workgroup b owns rows b + n_wg * l (l < nrows). Its tiles (chunk ch, row l,
-// column c), chunk-major, are split into NW contiguous runs, one per
-// wavefront: within a run the expert changes only at chunk boundaries and
+// column c), chunk-major, are split into NW contiguous runs of whole (chunk,
+// row) pairs, one per wavefront: within a run the expert changes only at chunk boundaries and
 // consecutive tiles are consecutive bytes of one expert's matrix. PD tiles
 // are in flight. When a (chunk, row) completes, the values of the chunk's
 // slots go to LDS (stage[l][slot]); after the stream and a barrier the
@@ -274,8 +274,11 @@ __global__ __launch_bounds__(64 * NW) void k_moe_fused(
 
     const int n_chunks = __builtin_amdgcn_readfirstlane(rt.n_chunks);
     const int per_chunk = nrows * ncols;
-    const int W = n_chunks * per_chunk;
-    const int t_beg = (int)(((long long)W * wv) / NW), t_end = (int)(((long long)W * (wv + 1)) / NW);
+    // runs are whole (chunk, row) pairs: a row's columns are summed by one
+    // wavefront, which writes the row's values when its last column is done
+    const int R = n_chunks * nrows;
+    const int t_beg = (int)(((long long)R * wv) / NW) * ncols,
+              t_end = (int)(((long long)R * (wv + 1)) / NW) * ncols;
     const int T = t_end - t_beg;
     const __amdgpu_buffer_rsrc_t rnull = make_rsrc(w0, 0);
 
@@ -595,6 +598,41 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
         return e;
     k_moe_accumulate<<<(unsigned)(((size_t)n_tok * n_embd + 255) / 256), 256, 0, s>>>(
         out, yd, wts, slot_of, n_tok, k, n_embd);
+    return hipGetLastError();
+}
+
+// ---- shared expert (apply_shared_expert, moe.rs:422-455) ---------------------
+// a[i] = silu(min(g[i], c)) * clamp(u[i], -c, c): apply_swiglu_clamp
+// (:515-531) then scalar::swiglu, for weights the routed-expert kernels do
+// not take (F32 blobs, gate and up of different formats).
+__global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ g,
+                                                const float *__restrict__ u,
+                                                float *__restrict__ a, size_t n, float c) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) a[i] = swiglu_clamped(g[i], u[i], c);
+}
+
+hipError_t launch_swiglu(const float *g, const float *u, float *a, size_t n, float c,
+                         hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    k_swiglu<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(g, u, a, n, c);
+    return hipGetLastError();
+}
+
+// The routing table of one expert with weight 1 for every token, which runs
+// the shared expert through launch_moe.
+__global__ __launch_bounds__(256) void k_fill_route(int *__restrict__ ids, float *__restrict__ w,
+                                                    int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        ids[i] = 0;
+        w[i] = 1.0f;
+    }
+}
+
+hipError_t launch_fill_route(int *ids, float *w, int n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    k_fill_route<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(ids, w, n);
     return hipGetLastError();
 }
 

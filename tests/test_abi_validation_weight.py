@@ -80,3 +80,42 @@ def test_lora_down_longer_blob_is_accepted_by_validation(hip):
     # the slices only need to end inside the blob (weight.rs:313-319); this
     # does not reach the device because n_tok is 0
     lora(hip, 0, np.zeros(6 * 34 + 100, np.uint8), 0, 0, 3, 32, 2, G.Q8_0)
+
+
+# ---- apply_shared_expert (moe.rs:422-455: check_moe_shapes :557-573, then the
+# gate, up and down matmul_weight_f32 checks) ----
+
+def shared(hip, out_len, x_len, gate, dg, up, du, down, dd, n_tok, n_embd, n_ff):
+    hip.apply_shared_expert(np.zeros(out_len, np.float32), np.zeros(x_len, np.float32), gate, dg,
+                            up, du, down, dd, n_tok, n_embd, n_ff, 10.0)
+
+
+_E, _F = 64, 32
+_G = np.zeros(_F * _E, np.float32)
+_D = np.zeros(_E * _F, np.float32)
+_Q = np.zeros(_F * 2 * 34, np.uint8)   # Q8_0 [32 x 64]
+
+
+@pytest.mark.parametrize("args,msg", [
+    ((2 * _E, 2 * _E - 1, _G, G.F32, _G, G.F32, _D, G.F32, 2, _E, _F), "moe.x"),
+    ((2 * _E - 1, 2 * _E - 1, _G, G.F32, _G, G.F32, _D, G.F32, 2, _E, _F), "moe.x"),  # x first
+    ((3, 2 * _E, _G, G.F32, _G, G.F32, _D, G.F32, 2, _E, _F), "moe.out"),
+    ((2 * _E, 2 * _E, _G[:-1], G.F32, _G, G.F32, _D, G.F32, 2, _E, _F), "weight_f32"),
+    ((2 * _E, 2 * _E, _G, G.F32, _Q[:-1], G.Q8_0, _D, G.F32, 2, _E, _F), "matmul_weight_f32.quant"),
+    ((2 * _E, 2 * _E, _G, G.F32, _Q, G.Q8_0, _D[:-1], G.F32, 2, _E, _F), "weight_f32"),
+    ((2 * 96, 2 * 96, np.zeros(_F * 96, np.float32), G.F32, np.zeros(_F * 96, np.float32), G.F32,
+      np.zeros(96 * 34, np.uint8), G.Q4_K, 2, 96, _F), "matmul_weight_f32.quant"),  # n_ff 32 % 256
+])
+def test_shared_expert_errors_in_order(hip, args, msg):
+    with pytest.raises(hip.ShapeMismatch, match=msg):
+        shared(hip, *args)
+
+
+def test_shared_expert_no_tokens_skips_the_matmul_checks(hip):
+    shared(hip, 0, 0, _G[:-1], G.F32, _G, G.F32, _D, G.F32, 0, _E, _F)
+
+
+def test_shared_expert_quant_zero_n_ff_panics_in_reference(hip):
+    with pytest.raises(hip.InvalidArgument):
+        shared(hip, _E, _E, np.zeros(0, np.uint8), G.Q8_0, np.zeros(0, np.uint8), G.Q8_0,
+               np.zeros(0, np.uint8), G.Q8_0, 1, _E, 0)

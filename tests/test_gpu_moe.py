@@ -149,3 +149,22 @@ def test_moe_fused_boundary_and_duplicates(oracle, hip, n_tok, k, dup):
     err = rel_err(got - base, want - base)
     print(f"moe fused boundary T={n_tok} k={k} dup={dup}: rel err {err:.3e}")
     assert err <= REL_TOL
+
+
+@pytest.mark.parametrize("dt_gu,dt_d", [(G.Q8_0, G.Q8_0), (G.Q6_K, G.Q4_0), (G.Q4_K, G.Q8_0)])
+@pytest.mark.parametrize("n_embd,n_ff", [(4096, 512), (2048, 512), (1024, 2048), (4096, 2048)])
+@pytest.mark.parametrize("n_tok,k", [(1, 1), (2, 1), (2, 3)])
+def test_moe_fused_rows_spanning_columns(oracle, hip, dt_gu, dt_d, n_embd, n_ff, n_tok, k):
+    """Fused path with in_dim over several 8-unit x columns and few rows per
+    workgroup, so wavefront runs would end inside a row if they were not
+    whole (chunk, row) pairs."""
+    n_expert = 3
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, dt_gu, dt_d,
+                                          7 * n_tok + k)
+    base = np.zeros(n_tok * n_embd, np.float32)
+    want = run_oracle(oracle, base, x, gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                      dt_gu, dt_d)
+    got = base.copy()
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   dt_gu, dt_d, 10.0)
+    assert rel_err(got, want) <= REL_TOL

@@ -1,0 +1,115 @@
+"""apply_shared_expert / apply_expert_swiglu (rsllm-models/src/dsv4/moe.rs:
+422-502) on the GPU against the oracle: max|Δ|/max|y| <= 1e-3 (REL_TOL) for
+the routed-expert route (gate and up of one quant format, quant down; fused
+up to 32 tokens, multi-launch above) and the general route (F32 blobs,
+mixed formats), with the clamp engaged and off, the reference's clamp test
+at DS-V4's shapes, and the device-pointer form."""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import REL_TOL, rel_err
+from rsllm_amd import synth
+from rsllm_amd.ggml import GgmlType as G
+
+pytestmark = pytest.mark.gpu
+
+
+def blob(dt, rows, cols, seed):
+    if dt == G.F32:
+        return (np.random.default_rng(seed).standard_normal(rows * cols) * 0.05).astype(np.float32)
+    return synth.weight(dt, rows, cols, seed)
+
+
+def run_case(oracle, hip, dg, du, dd, n_tok, n_embd, n_ff, clamp, seed, x_scale=1.0):
+    gate, up = blob(dg, n_ff, n_embd, seed), blob(du, n_ff, n_embd, seed + 1)
+    down = blob(dd, n_embd, n_ff, seed + 2)
+    x = (synth.activations(n_tok, n_embd, seed + 3) * x_scale).astype(np.float32)
+    toks = np.unique(np.linspace(0, n_tok - 1, min(n_tok, 5)).astype(int))
+    rc, want = oracle.apply_shared_expert(x[toks], gate, int(dg), up, int(du), down, int(dd),
+                                          len(toks), n_embd, n_ff, clamp)
+    assert rc == 0
+    got = np.full(n_tok * n_embd, np.nan, np.float32)
+    hip.apply_shared_expert(got, x.reshape(-1), gate, dg, up, du, down, dd, n_tok, n_embd, n_ff,
+                            clamp)
+    assert not np.isnan(got).any()
+    return rel_err(got.reshape(n_tok, n_embd)[toks], want.reshape(len(toks), n_embd))
+
+
+@pytest.mark.parametrize("dg,dd", [(G.Q4_K, G.Q6_K), (G.Q8_0, G.Q8_0), (G.IQ2_XXS, G.Q2_K),
+                                   (G.Q6_K, G.Q4_0)])
+@pytest.mark.parametrize("n_tok", [1, 3, 8, 40])
+def test_shared_expert_routed_route(oracle, hip, dg, dd, n_tok):
+    err = run_case(oracle, hip, dg, dg, dd, n_tok, 1024, 512, 10.0, 11 + n_tok)
+    print(f"shared {dg.name}/{dd.name} T={n_tok}: rel err {err:.3e}")
+    assert err <= REL_TOL
+
+
+@pytest.mark.parametrize("dg,du,dd", [(G.F32, G.F32, G.F32), (G.Q4_K, G.Q6_K, G.Q8_0),
+                                      (G.F32, G.F32, G.Q4_K), (G.Q8_0, G.Q8_0, G.F32)])
+@pytest.mark.parametrize("n_tok", [1, 5, 33])
+def test_shared_expert_general_route(oracle, hip, dg, du, dd, n_tok):
+    err = run_case(oracle, hip, dg, du, dd, n_tok, 512, 256, 10.0, 5 + n_tok)
+    assert err <= REL_TOL
+
+
+@pytest.mark.parametrize("dg,du,dd", [(G.Q4_K, G.Q4_K, G.Q4_K), (G.F32, G.F32, G.F32)])
+@pytest.mark.parametrize("clamp", [0.0, 10.0])
+def test_shared_expert_clamp_engaged_and_off(oracle, hip, dg, du, dd, clamp):
+    # x scaled so gate / up outputs pass 10 on many lanes
+    err = run_case(oracle, hip, dg, du, dd, 4, 512, 256, clamp, 77, x_scale=300.0)
+    assert err <= REL_TOL
+
+
+def test_reference_clamp_test_dsv4_shapes(hip):
+    # moe.rs:743-789 at n_embd 4096, n_ff 2048 with identity-truncation F32 weights
+    n_embd, n_ff = 4096, 2048
+    eye = np.zeros((n_ff, n_embd), np.float32)
+    eye[np.arange(n_ff), np.arange(n_ff)] = 1.0
+    gate = eye.reshape(-1)
+    down = np.ascontiguousarray(eye.T).reshape(-1)
+    x = np.zeros(n_embd, np.float32)
+    x[0] = 1e3
+    out = np.full(n_embd, np.nan, np.float32)
+    hip.apply_shared_expert(out, x, gate, G.F32, gate, G.F32, down, G.F32, 1, n_embd, n_ff, 10.0)
+    assert 90.0 < out[0] < 110.0
+    assert abs(out[0] - 10.0 / (1.0 + math.exp(-10.0)) * 10.0) < 1e-3
+    assert not out[1:].any()
+
+
+def test_shared_expert_dsv4_q8_0(oracle, hip):
+    """DS-V4 shared expert shapes (n_embd 4096, n_ff 2048) in Q8_0."""
+    err = run_case(oracle, hip, G.Q8_0, G.Q8_0, G.Q8_0, 2, 4096, 2048, 10.0, 123)
+    assert err <= REL_TOL
+
+
+@pytest.mark.parametrize("dg,du,dd", [(G.Q8_0, G.Q8_0, G.Q6_K), (G.F32, G.Q4_K, G.Q8_0)])
+def test_shared_expert_device_form(oracle, hip, dg, du, dd):
+    import torch
+    n_tok, n_embd, n_ff = 6, 1024, 512
+    gate, up = blob(dg, n_ff, n_embd, 1), blob(du, n_ff, n_embd, 2)
+    down = blob(dd, n_embd, n_ff, 3)
+    x = synth.activations(n_tok, n_embd, 4)
+    s = torch.cuda.current_stream().cuda_stream
+    dev = []
+    for w, dt, in_dim in ((gate, dg, n_embd), (up, du, n_embd), (down, dd, n_ff)):
+        wb = w.view(np.uint8)
+        raw = torch.from_numpy(wb.copy()).cuda()
+        if dt == G.F32:
+            dev.append((raw, wb.size))
+            continue
+        d = torch.empty_like(raw)
+        hip.prepare_weights_dev(d.data_ptr(), raw.data_ptr(), wb.size, dt, in_dim, s)
+        dev.append((d, wb.size))
+    d_x = torch.from_numpy(x.reshape(-1).copy()).cuda()
+    d_y = torch.full((n_tok * n_embd,), float("nan"), device="cuda")
+    hip.apply_shared_expert_dev(d_y.data_ptr(), d_y.numel(), d_x.data_ptr(), d_x.numel(),
+                                dev[0][0].data_ptr(), dev[0][1], dg, dev[1][0].data_ptr(),
+                                dev[1][1], du, dev[2][0].data_ptr(), dev[2][1], dd, n_tok, n_embd,
+                                n_ff, 10.0, s)
+    torch.cuda.synchronize()
+    rc, want = oracle.apply_shared_expert(x, gate, int(dg), up, int(du), down, int(dd), n_tok,
+                                          n_embd, n_ff, 10.0)
+    assert rc == 0
+    assert rel_err(d_y.cpu().numpy(), want) <= REL_TOL
