@@ -154,7 +154,7 @@ def _time(fn, iters, stream):
 def _rotating(t, min_bytes=640e6):
     """Distinct device copies of `t` totalling >= min_bytes (> the 256 MB
     Infinity Cache), so every timed launch streams its weights from HBM."""
-    n = max(2, int(np.ceil(min_bytes / t.numel())))
+    n = max(2, int(np.ceil(min_bytes / (t.numel() * t.element_size()))))
     return [t] + [t.clone() for _ in range(n - 1)]
 
 
@@ -348,6 +348,88 @@ def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
             q8.append(e)
         del reps, prep
     out["q8_int8"] = q8
+
+    # ---- caller chain at DS-V4 Flash shapes (weight.rs:113-266, moe.rs:422-502) ----
+    chain = []
+    # matmul_grouped_lora_down: attn_output_a, 8 groups of [1024 x 4096] Q8_0
+    n_g, g_dim, rank = 8, 4096, 1024
+    w_host = synth.weight(G.Q8_0, n_g * rank, g_dim, 700)
+    raw = torch.from_numpy(w_host).to(dev)
+    prep = torch.empty_like(raw)
+    B.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), G.Q8_0, g_dim, sptr)
+    del raw
+    reps = _rotating(prep)
+    for n_tok in (1, 2, 4, 8, 16):
+        x = torch.from_numpy(synth.activations(n_tok, n_g * g_dim, 701).reshape(-1)).to(dev)
+        y = torch.empty(n_tok * n_g * rank, dtype=torch.float32, device=dev)
+
+        def lora(i):
+            w = reps[i % len(reps)]
+            B.matmul_grouped_lora_down_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(),
+                                           x.data_ptr(), x.numel(), n_tok, n_g, g_dim, rank,
+                                           G.Q8_0, sptr)
+        for i in range(len(reps)):
+            lora(i)
+        us = _time(lora, iters, stream)
+        nbytes = prep.numel() + n_tok * n_g * (g_dim + rank) * 4
+        chain.append({"op": "matmul_grouped_lora_down", "dtype": "Q8_0",
+                      "shape": f"{n_g} x [{rank}x{g_dim}]", "batch": n_tok, "bytes": nbytes,
+                      "us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                      "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+    del reps, prep
+    # apply_shared_expert: gate/up [2048 x 4096], down [4096 x 2048], Q8_0
+    e_dim, f_dim = 4096, 2048
+    blobs = []
+    for j, (r_, c_) in enumerate(((f_dim, e_dim), (f_dim, e_dim), (e_dim, f_dim))):
+        raw = torch.from_numpy(synth.weight(G.Q8_0, r_, c_, 710 + j)).to(dev)
+        p_ = torch.empty_like(raw)
+        B.prepare_weights_dev(p_.data_ptr(), raw.data_ptr(), raw.numel(), G.Q8_0, c_, sptr)
+        blobs.append(p_)
+        del raw
+    shared_bytes = sum(b_.numel() for b_ in blobs)
+    n_copies = max(2, int(640e6 // shared_bytes) + 1)
+    copies = [blobs] + [[b_.clone() for b_ in blobs] for _ in range(n_copies - 1)]
+    for n_tok in (1, 4, 8):
+        x = torch.from_numpy(synth.activations(n_tok, e_dim, 720).reshape(-1)).to(dev)
+        y = torch.empty(n_tok * e_dim, dtype=torch.float32, device=dev)
+
+        def shared(i):
+            g_, u_, d_ = copies[i % len(copies)]
+            B.apply_shared_expert_dev(y.data_ptr(), y.numel(), x.data_ptr(), x.numel(),
+                                      g_.data_ptr(), g_.numel(), G.Q8_0, u_.data_ptr(),
+                                      u_.numel(), G.Q8_0, d_.data_ptr(), d_.numel(), G.Q8_0,
+                                      n_tok, e_dim, f_dim, 10.0, sptr)
+        for i in range(len(copies)):
+            shared(i)
+        us = _time(shared, iters, stream)
+        nbytes = shared_bytes + 2 * n_tok * e_dim * 4
+        chain.append({"op": "apply_shared_expert", "dtype": "Q8_0",
+                      "shape": f"gate/up {f_dim}x{e_dim}, down {e_dim}x{f_dim}", "batch": n_tok,
+                      "bytes": nbytes, "us": round(us, 3),
+                      "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                      "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+    del copies, blobs
+    # matmul_weight_f32, F32 arm: 4096 x 4096 f32 weights
+    wf = torch.randn(4096 * 4096, dtype=torch.float32, device=dev)
+    reps = _rotating(wf)
+    for n_tok in (1, 4):
+        x = torch.randn(n_tok * 4096, dtype=torch.float32, device=dev)
+        y = torch.empty(n_tok * 4096, dtype=torch.float32, device=dev)
+
+        def wf32(i):
+            w = reps[i % len(reps)]
+            B.matmul_weight_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel() * 4,
+                                    x.data_ptr(), x.numel(), n_tok, 4096, 4096, G.F32, sptr)
+        for i in range(len(reps)):
+            wf32(i)
+        us = _time(wf32, iters, stream)
+        nbytes = wf.numel() * 4 + n_tok * 8192 * 4
+        chain.append({"op": "matmul_weight_f32", "dtype": "F32", "shape": "4096x4096",
+                      "batch": n_tok, "bytes": nbytes, "us": round(us, 3),
+                      "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                      "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+    del reps, wf
+    out["caller_chain"] = chain
 
     # ---- C3 routed experts (64 experts, Q4_K gate/up 2048x7168, down 7168x2048, top-8) ----
     # Two device copies of the expert stacks and 8 routings per T: call i

@@ -240,18 +240,17 @@ int rsllm_hip_moe_routed(float *out, size_t out_len, const float *x, size_t x_le
  *
  * Device forms: weights in this backend's device layout (Quant arm:
  * rsllm_hip_prepare_weights_dev of the [n_groups * rank x group_dim]
- * matrix; F32: as is), x and out on the device, enqueued on `stream`. When
- * the x of all groups for every token fits in LDS (up to 8 tokens) and
- * group_dim is a multiple of the kernel's 8-block column, all groups are one
- * launch; otherwise each group is its own launch. A group's launch needs the
- * group to be a whole number of 8-block super-tiles of the device layout
- * (non-Q4_K dtypes: rank * group_dim / block elements a multiple of 8). The
- * host form converts each such unaligned group to the device layout on its
- * own and always computes; the device form, given the whole matrix's
- * layout, returns RSLLM_HIP_ERR_UNIMPLEMENTED (writing nothing) for
- * unaligned groups when the one-launch form does not apply. The host form
+ * matrix; F32: as is), x and out on the device, enqueued on `stream`. Each
+ * chunk of up to 8 tokens is one launch for all groups (each workgroup holds
+ * one group's x in LDS). A group_dim too long for that (over about 60k
+ * elements for the 256-element formats) runs each group as its own launch
+ * on gathered x, which needs the group to be a whole number of 8-block
+ * super-tiles of the device layout (non-Q4_K dtypes: rank * group_dim /
+ * block elements a multiple of 8). For such groups that are not, the host
+ * form converts each group to the device layout on its own, and the device
+ * form returns RSLLM_HIP_ERR_UNIMPLEMENTED (writing nothing). The host form
  * uses a registered copy of the blob only when the groups use all of it and
- * are whole super-tiles. */
+ * it is not converted group by group. */
 int rsllm_hip_matmul_weight_f32(float *out, size_t out_len, const uint8_t *weights,
                                 size_t weights_len, const float *x, size_t x_len, size_t n_tok,
                                 size_t in_dim, size_t out_dim, uint32_t dtype);

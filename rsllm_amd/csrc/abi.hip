@@ -349,10 +349,11 @@ int weight_f32_compute(float *out, size_t out_len, const uint8_t *w, size_t w_le
 
 // matmul_grouped_lora_down on device pointers (validated; stride = bytes of
 // one group's [rank x group_dim] weights). The stacked blob is the
-// [n_groups * rank x group_dim] row-major matrix, so when the x of every
-// group and token fits in LDS (up to 8 tokens) one launch covers all groups,
-// row r reading x group r / rank; otherwise one launch per group (strided x
-// and y, or x gathered and y scattered for more tokens).
+// [n_groups * rank x group_dim] row-major matrix, so each chunk of up to 8
+// tokens is one launch for all groups (workgroups dealt per group, each with
+// its group's x in LDS, row r reading x group r / rank). Only when one
+// group's x is too long for LDS does each group run its own launch on
+// gathered x, scattered into out.
 // group_layout: each group's slice was converted to the device layout on its
 // own (only the per-group launches read it that way).
 int lora_down_compute(float *out, size_t out_len, const uint8_t *w, size_t stride, const float *x,
@@ -377,28 +378,22 @@ int lora_down_compute(float *out, size_t out_len, const uint8_t *w, size_t strid
         if (e != hipErrorNotSupported) return dev_err(e, "gemv_rows");
         (void)hipGetLastError();
     }
-    // one launch per group: group g's weights are rows [g R, (g + 1) R) of the
-    // stacked matrix; in the super-tile layouts that is whole super-tiles only
-    // when R * (blocks per row) is a multiple of 8
+    // one launch per group on gathered x: group g's weights are rows
+    // [g R, (g + 1) R) of the stacked matrix; in the super-tile layouts that
+    // is whole super-tiles only when R * (blocks per row) is a multiple of 8
     if (!group_layout && needs_prepare(dtype) && (rank * (group_dim / block_elems_of(dtype))) % 8 != 0)
         return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED,
                        "matmul_grouped_lora_down: groups that do not end on a super-tile of the "
-                       "device layout need the one-launch form (x of every group and token in "
-                       "LDS, group_dim a multiple of the 8-block column)");
+                       "device layout, with one group's x too long for LDS");
+    ThreadCtx &c = t_ctx;
+    HIP_TRY(c.xh.ensure((size_t)T * D * 4 + (size_t)T * R * 4), "hipMalloc");
+    HIP_TRY(c.xq.ensure(gemv_work_bytes(dtype, T, D, R)), "hipMalloc");
+    float *xg = (float *)c.xh.p, *yg = xg + (size_t)T * D;
     for (int g = 0; g < G; g++) {
         const uint8_t *wg = w + (size_t)g * stride;
-        e = launch_gemv_rows(dtype, wg, stride, x + (size_t)g * D, out + (size_t)g * R, T, D, R, D,
-                             tin, tout, R, s);
-        if (e == hipSuccess) continue;
-        if (e != hipErrorNotSupported) return dev_err(e, "gemv_rows");
-        (void)hipGetLastError();
-        ThreadCtx &c = t_ctx;
-        HIP_TRY(c.xh.ensure((size_t)T * D * 4 + (size_t)T * R * 4), "hipMalloc");
-        float *xg = (float *)c.xh.p, *yg = xg + (size_t)T * D;
         HIP_TRY(hipMemcpy2DAsync(xg, (size_t)D * 4, x + (size_t)g * D, (size_t)tin * 4,
                                  (size_t)D * 4, (size_t)T, hipMemcpyDeviceToDevice, s),
                 "gather x");
-        HIP_TRY(c.xq.ensure(gemv_work_bytes(dtype, T, D, R)), "hipMalloc");
         HIP_TRY(launch_gemv(dtype, wg, stride, xg, (uint8_t *)c.xq.p, yg, T, D, R, s), "gemv");
         HIP_TRY(hipMemcpy2DAsync(out + (size_t)g * R, (size_t)tout * 4, yg, (size_t)R * 4,
                                  (size_t)R * 4, (size_t)T, hipMemcpyDeviceToDevice, s),
@@ -1125,13 +1120,15 @@ int rsllm_hip_matmul_grouped_lora_down(float *out, size_t out_len, const uint8_t
     // The blob may be longer; the groups use this much. The device layout
     // packs 8 blocks per super-tile with a shorter last one, so a group's
     // slice of the whole matrix's layout is the group's own layout only when
-    // the group is whole super-tiles; otherwise each group is converted on
-    // its own and run by the per-group launches. A registered copy (the whole
-    // blob's layout) is used only when it is exactly the groups' rows and
-    // they are whole super-tiles.
+    // the group is whole super-tiles. Groups that are not, and that need the
+    // per-group launches (one group's x too long for LDS), are converted one
+    // by one. A
+    // registered copy (the whole blob's layout) is used only when it is
+    // exactly the groups' rows and is not converted per group.
     const size_t used = stride * n_groups;
     const bool prep = dtype != T_F32 && needs_prepare(dtype) && group_dim;
-    const bool per_group = prep && (rank * (group_dim / block_elems_of(dtype))) % 8 != 0;
+    const bool per_group = prep && (rank * (group_dim / block_elems_of(dtype))) % 8 != 0 &&
+                           !gemv_rows_fits(dtype, (int)group_dim);
     const uint8_t *dw = dtype == T_F32 || used != weights_len || per_group
                             ? nullptr
                             : find_registered(weights, weights_len, dtype, group_dim);

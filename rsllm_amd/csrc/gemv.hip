@@ -178,19 +178,22 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv(const uint8_t *__restri
 // its arithmetic, so the waits before each tile's arithmetic leave the later
 // tiles in flight.
 //
-// Rows and x. Weight row r dots x columns [g * in_dim, (g + 1) * in_dim) of
-// each token, g = r / rows_per_group (one group: rows_per_group = out_dim);
-// the LDS image holds x_dim = n_groups * in_dim values per token, token t of
-// x at x + t * x_stride; y[t, r] at y + t * y_stride + r.
+// Groups. The rows form groups of rows_per_group consecutive rows (one
+// group: rows_per_group = out_dim); row r of group g = r / rows_per_group
+// dots x columns [g * in_dim, (g + 1) * in_dim) of each token. Workgroups
+// are dealt group-major, wpg per group: workgroup b serves group b / wpg and
+// takes that group's rows b % wpg + wpg * l, and its LDS image holds only
+// that group's x. Token t of x starts at x + t * x_stride (x_dim readable
+// values from there); y[t, r] is at y + t * y_stride + r.
 struct Gemv1Shape {
-    int in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group;
+    int in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group, wpg;
 };
 
 template <class F, int NW, int PD, int GPT, int BT = 1>
 __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w, uint32_t w_bytes,
                                                   const float *__restrict__ x,
                                                   float *__restrict__ y, Gemv1Shape sh,
-                                                  int n_wg, int n_tok) {
+                                                  int n_tok) {
     const int in_dim = sh.in_dim, out_dim = sh.out_dim;
     extern __shared__ uint4 xl[];
     constexpr int kHalves = F::kXF == 5 ? 2 : 1;
@@ -198,13 +201,14 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
     const int lane = threadIdx.x & 63, k = lane & 7, ks = lane >> 3;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nunits = F::units(in_dim), ncols = (nunits + 7) >> 3;
-    // x image: columns of the whole x_dim (group boundaries fall on columns)
-    const int xunits = F::units(sh.x_dim), xcols = (xunits + 7) >> 3;
-    const int per_tok = xcols * 64 * kHalves;                           // limb groups per token
+    const int per_tok = ncols * 64 * kHalves;                           // limb groups per token
     const int n_groups = per_tok * BT;
-    const uint32_t tok_fields = (uint32_t)xcols * F::kXF * 64;          // uint4 per token in LDS
-    const int r0 = blockIdx.x;
-    const int nrows = (out_dim - r0 + n_wg - 1) / n_wg;                 // this workgroup's rows
+    const uint32_t tok_fields = (uint32_t)ncols * F::kXF * 64;          // uint4 per token in LDS
+    const int wpg = sh.wpg, R = sh.rows_per_group;
+    const int gsel = blockIdx.x / wpg;                                   // this workgroup's group
+    const int r0 = blockIdx.x - gsel * wpg;
+    const int row_base = gsel * R;
+    const int nrows = r0 < R ? (R - r0 + wpg - 1) / wpg : 0;            // this workgroup's rows
     const int my_rows = nrows > wv ? (nrows - wv + NW - 1) / NW : 0;   // this wavefront's rows
     const int T = my_rows * ncols;                                       // its tiles
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
@@ -218,10 +222,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
         const int col = rem / (64 * kHalves), r2 = rem % (64 * kHalves);
         const int half = r2 >> 6, ln = r2 & 63;
         const int kk = ln & 7, unit = col * 8 + (ln >> 3);
-        const bool ok = g < n_groups && t < n_tok && unit < xunits && F::valid(unit, kk, sh.x_dim);
-        return ok ? t * sh.x_stride + (half ? F::elem_hi(unit, kk) : F::elem_lo(unit, kk)) : -1;
+        const bool ok = g < n_groups && t < n_tok && unit < nunits && F::valid(unit, kk, in_dim);
+        return ok ? t * sh.x_stride + gsel * in_dim +
+                        (half ? F::elem_hi(unit, kk) : F::elem_lo(unit, kk))
+                  : -1;
     };
-    auto row_of = [&](int j) { return r0 + n_wg * (wv + NW * j); };
+    auto row_of = [&](int j) { return row_base + r0 + wpg * (wv + NW * j); };
     typename F::Slice buf[PD];
     auto load_tile = [&](typename F::Slice &sl, int t) {
         const int j = t / ncols, col = t - j * ncols;
@@ -276,7 +282,6 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
 #pragma unroll
     for (int tk = 0; tk < BT; tk++) acc[tk] = 0.f;
     int col = 0, j = 0;
-    int xc0 = (row_of(0) / sh.rows_per_group) * ncols;  // x column of the row's group
     for (int t0 = 0; t0 < T; t0 += PD) {
 #pragma unroll
         for (int jj = 0; jj < PD; jj++) {
@@ -288,7 +293,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
 #pragma unroll
             for (int tk = 0; tk < BT; tk++) {
                 XSlice xs;
-                const uint4 *bx = xl + tk * tok_fields + (xc0 + col) * F::kXF * 64 + lane;
+                const uint4 *bx = xl + tk * tok_fields + col * F::kXF * 64 + lane;
                 xs.hlo = bx[0];
                 xs.llo = bx[64];
                 xs.meta = bx[128];
@@ -309,7 +314,6 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
                 }
                 col = 0;
                 j++;
-                xc0 = (min(row_of(j), out_dim - 1) / sh.rows_per_group) * ncols;
             } else {
                 col++;
             }
@@ -318,11 +322,11 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
     }
 }
 
-// LDS of k_gemv1: the quantised x (bt tokens x the columns of x_dim) plus
-// one spare column.
+// LDS of k_gemv1: the quantised x (bt tokens x the columns of one group's
+// in_dim) plus one spare column.
 template <class F>
-static size_t gemv1_lds_bytes(int x_dim, int bt = 1) {
-    const int ncols = ((x_dim + F::kEPU - 1) / F::kEPU + 7) >> 3;
+static size_t gemv1_lds_bytes(int in_dim, int bt = 1) {
+    const int ncols = ((in_dim + F::kEPU - 1) / F::kEPU + 7) >> 3;
     return (size_t)(bt * ncols + 1) * F::kXF * 1024;
 }
 
@@ -346,16 +350,21 @@ static hipError_t gemv1_go(const uint8_t *w, size_t w_bytes, const float *x, flo
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    n_wg = min(n_wg, sh.out_dim);
-    k_gemv1<F, NW, PD, GPT, BT><<<(unsigned)n_wg, 64 * NW, gemv1_lds_bytes<F>(sh.x_dim, BT), s>>>(
-        w, (uint32_t)w_bytes, x, y, sh, n_wg, n_tok);
+    // n_wg workgroups dealt over the groups (at least one per group, at most
+    // one per row)
+    Gemv1Shape g = sh;
+    const int n_grp = sh.out_dim / sh.rows_per_group;
+    g.wpg = max(1, min(n_wg / n_grp, sh.rows_per_group));
+    k_gemv1<F, NW, PD, GPT, BT>
+        <<<(unsigned)(n_grp * g.wpg), 64 * NW, gemv1_lds_bytes<F>(sh.in_dim, BT), s>>>(
+            w, (uint32_t)w_bytes, x, y, g, n_tok);
     return hipGetLastError();
 }
 
 template <class F, int NW, int PD, int BT = 1>
 static hipError_t gemv1_gpt_go(const uint8_t *w, size_t w_bytes, const float *x, float *y,
                                const Gemv1Shape &sh, int n_tok, int n_wg, hipStream_t s) {
-    switch (gemv1_gpt<F>(sh.x_dim, NW, BT)) {
+    switch (gemv1_gpt<F>(sh.in_dim, NW, BT)) {
     case 1: return gemv1_go<F, NW, PD, 1, BT>(w, w_bytes, x, y, sh, n_tok, n_wg, s);
     case 2: return gemv1_go<F, NW, PD, 2, BT>(w, w_bytes, x, y, sh, n_tok, n_wg, s);
     case 4: return gemv1_go<F, NW, PD, 4, BT>(w, w_bytes, x, y, sh, n_tok, n_wg, s);
@@ -365,7 +374,7 @@ static hipError_t gemv1_gpt_go(const uint8_t *w, size_t w_bytes, const float *x,
 
 static Gemv1Shape plain_shape(int n_tok, int in_dim, int out_dim) {
     (void)n_tok;
-    return Gemv1Shape{in_dim, out_dim, in_dim, in_dim, out_dim, out_dim};
+    return Gemv1Shape{in_dim, out_dim, in_dim, in_dim, out_dim, out_dim, 1};
 }
 
 // ---- grouped GEMV (routed experts) ------------------------------------------
@@ -678,7 +687,7 @@ template <class F>
 static hipError_t gemv1_batch(const uint8_t *w, size_t w_bytes, const float *x, float *y,
                               const Gemv1Shape &sh, int n_tok, hipStream_t s) {
     const int cus = device_cus();
-    switch (gemv1_bt<F>(n_tok, sh.x_dim)) {
+    switch (gemv1_bt<F>(n_tok, sh.in_dim)) {
     case 2: return gemv1_gpt_go<F, 16, 2, 2>(w, w_bytes, x, y, sh, n_tok, cus, s);
     case 4: return gemv1_gpt_go<F, 16, 2, 4>(w, w_bytes, x, y, sh, n_tok, cus, s);
     case 8: return gemv1_gpt_go<F, 16, 2, 8>(w, w_bytes, x, y, sh, n_tok, cus, s);
@@ -788,7 +797,7 @@ hipError_t launch_gemv_f32(const float *w, const float *x, float *y, int n_tok, 
                            int out_dim, int x_dim, int x_stride, int y_stride, int rows_per_group,
                            hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
-    const Gemv1Shape sh{in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group};
+    const Gemv1Shape sh{in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group, 0};
     const int n_wg = min(device_cus(), out_dim);
     // x offsets are 32-bit byte offsets: launch in token chunks of < 2 GiB of x
     const size_t per = ((size_t)1 << 29) / (size_t)(x_stride > 0 ? x_stride : 1);
@@ -803,32 +812,39 @@ hipError_t launch_gemv_f32(const float *w, const float *x, float *y, int n_tok, 
     return hipSuccess;
 }
 
-// Quantized rows with strided / grouped x and y through k_gemv1 (up to 8
-// tokens with their x in LDS). hipErrorNotSupported: shape not covered.
+// Quantized rows with strided / grouped x and y through k_gemv1, tokens in
+// chunks of up to 8 (one group's x for a chunk in LDS; each chunk is one
+// pass over the weights). hipErrorNotSupported: one group's x is too long for
+// LDS even for one token.
+bool gemv_rows_fits(uint32_t dtype, int in_dim) { return gemv1_tokens(dtype, 1, in_dim) != 0; }
+
 hipError_t launch_gemv_rows(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
                             float *y, int n_tok, int in_dim, int out_dim, int x_dim, int x_stride,
                             int y_stride, int rows_per_group, hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
-    const Gemv1Shape sh{in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group};
-    const int bt = gemv1_tokens(dtype, n_tok, x_dim);
-    if (bt == 0) return hipErrorNotSupported;
-    if (x_dim != in_dim) {  // several groups: each must start on an x column
-        size_t be = 0;
-#define X(T, F) if (dtype == T) be = (size_t)F::kEPU * 8;
-        GEMV_FORMATS(X)
+    if (rows_per_group <= 0 || out_dim % rows_per_group != 0) return hipErrorInvalidValue;
+    if (!gemv_rows_fits(dtype, in_dim)) return hipErrorNotSupported;
+    for (int t0 = 0; t0 < n_tok;) {
+        // the largest chunk of at most 8 tokens whose x fits in LDS
+        int c = n_tok - t0 < 8 ? n_tok - t0 : 8;
+        while (c > 1 && gemv1_tokens(dtype, c, in_dim) == 0) c = (c + 1) / 2;
+        const Gemv1Shape sh{in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group, 1};
+        const float *xc = x + (size_t)t0 * x_stride;
+        float *yc = y + (size_t)t0 * y_stride;
+        hipError_t e = hipErrorInvalidValue;
+        if (c == 1) {
+#define X(T, F) if (dtype == T) e = gemv1<F>(w, w_bytes, xc, yc, sh, s);
+            GEMV_FORMATS(X)
 #undef X
-        if (be == 0 || in_dim % be != 0) return hipErrorNotSupported;
+        } else {
+#define X(T, F) if (dtype == T) e = gemv1_batch<F>(w, w_bytes, xc, yc, sh, c, s);
+            GEMV_FORMATS(X)
+#undef X
+        }
+        if (e != hipSuccess) return e;
+        t0 += c;
     }
-    if (bt == 1) {
-#define X(T, F) if (dtype == T) return gemv1<F>(w, w_bytes, x, y, sh, s);
-        GEMV_FORMATS(X)
-#undef X
-    } else {
-#define X(T, F) if (dtype == T) return gemv1_batch<F>(w, w_bytes, x, y, sh, n_tok, s);
-        GEMV_FORMATS(X)
-#undef X
-    }
-    return hipErrorInvalidValue;
+    return hipSuccess;
 }
 
 hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,

@@ -59,14 +59,17 @@ size_t gemv_work_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim);
 // (WeightBlob::F32) and quantized rows with strided / grouped x and y:
 // y[t * y_stride + r] = sum_i W[r, i] x[t * x_stride + (r / rows_per_group)
 // * in_dim + i], x_dim = n_groups * in_dim values of x per token.
-// launch_gemv_rows returns hipErrorNotSupported for shapes it does not cover
-// (more than 8 tokens, x too long for LDS, groups not on x columns).
+// launch_gemv_rows (weights in the whole matrix's device layout; tokens in
+// chunks of up to 8, one pass over the weights each) returns
+// hipErrorNotSupported when one group's x is too long for LDS
+// (gemv_rows_fits is false).
 hipError_t launch_gemv_f32(const float *w, const float *x, float *y, int n_tok, int in_dim,
                            int out_dim, int x_dim, int x_stride, int y_stride, int rows_per_group,
                            hipStream_t s);
 hipError_t launch_gemv_rows(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
                             float *y, int n_tok, int in_dim, int out_dim, int x_dim, int x_stride,
                             int y_stride, int rows_per_group, hipStream_t s);
+bool gemv_rows_fits(uint32_t dtype, int in_dim);
 
 // gemv_mfma.hip: the same product for 5..32 tokens of Q4_K / Q6_K on the
 // matrix cores (weights dequantised to f16 once, tokens as the MFMA's N).

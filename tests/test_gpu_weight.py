@@ -104,7 +104,7 @@ def test_grouped_lora_down_small(oracle, hip, dtype, n_groups, group_dim, rank, 
 ])
 @pytest.mark.parametrize("n_tok", [9, 20])
 def test_grouped_lora_down_many_tokens(oracle, hip, dtype, n_groups, group_dim, rank, n_tok):
-    """More than 8 tokens: one launch per group (gathered x, scattered y)."""
+    """More than 8 tokens: one launch per chunk of up to 8 tokens."""
     w, x = grouped_case(dtype, n_tok, n_groups, group_dim, rank, 70 + n_tok)
     toks = np.array([0, 3, n_tok - 1])
     want = oracle_grouped(oracle, w, x, toks, n_groups, group_dim, rank, dtype)
@@ -114,37 +114,66 @@ def test_grouped_lora_down_many_tokens(oracle, hip, dtype, n_groups, group_dim, 
     assert rel_err(got.reshape(n_tok, -1)[toks], want) <= REL_TOL
 
 
-@pytest.mark.parametrize("dtype,group_dim,rank", [(G.Q8_0, 96, 5), (G.Q6_K, 256, 3)])
-def test_grouped_lora_down_unaligned_groups(oracle, hip, dtype, group_dim, rank):
-    """Groups that are not whole super-tiles of the device layout: the host
-    form converts each group on its own and runs them one launch each; the
-    device form (whole-matrix layout) has no such path for 9 tokens and
-    reports Unimplemented without writing."""
+def lora_dev(hip, w, x, n_tok, n_groups, group_dim, rank, dtype):
+    """The device form on a whole-matrix device layout; returns the output
+    (NaN where nothing was written) or raises."""
     import torch
-    n_tok, n_groups = 9, 3
-    w, x = grouped_case(dtype, n_tok, n_groups, group_dim, rank, 3)
-    want = oracle_grouped(oracle, w, x, np.arange(n_tok), n_groups, group_dim, rank, dtype)
-    got = np.full(n_tok * n_groups * rank, np.nan, np.float32)
-    hip.matmul_grouped_lora_down(got, w, x.reshape(-1), n_tok, n_groups, group_dim, rank, dtype)
-    assert rel_err(got.reshape(n_tok, -1), want) <= REL_TOL
     s = torch.cuda.current_stream().cuda_stream
     d_raw = torch.from_numpy(w).cuda()
     d_w = torch.empty_like(d_raw)
     hip.prepare_weights_dev(d_w.data_ptr(), d_raw.data_ptr(), w.size, dtype, group_dim, s)
     d_x = torch.from_numpy(x.reshape(-1).copy()).cuda()
     d_y = torch.full((n_tok * n_groups * rank,), float("nan"), device="cuda")
-    with pytest.raises(hip.Unimplemented):
+    try:
         hip.matmul_grouped_lora_down_dev(d_y.data_ptr(), d_y.numel(), d_w.data_ptr(), w.size,
                                          d_x.data_ptr(), d_x.numel(), n_tok, n_groups, group_dim,
                                          rank, dtype, s)
-    torch.cuda.synchronize()
-    assert torch.isnan(d_y).all()
+    finally:
+        torch.cuda.synchronize()
+    return d_y.cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype,group_dim,rank", [(G.Q8_0, 96, 5), (G.Q6_K, 256, 3)])
+@pytest.mark.parametrize("n_tok", [3, 9, 17])
+def test_grouped_lora_down_unaligned_groups(oracle, hip, dtype, group_dim, rank, n_tok):
+    """Groups that are not whole 8-block super-tiles of the device layout run
+    as one launch per chunk of up to 8 tokens on the whole matrix's layout,
+    host and device forms alike."""
+    n_groups = 3
+    w, x = grouped_case(dtype, n_tok, n_groups, group_dim, rank, 3)
+    want = oracle_grouped(oracle, w, x, np.arange(n_tok), n_groups, group_dim, rank, dtype)
+    got = np.full(n_tok * n_groups * rank, np.nan, np.float32)
+    hip.matmul_grouped_lora_down(got, w, x.reshape(-1), n_tok, n_groups, group_dim, rank, dtype)
+    assert rel_err(got.reshape(n_tok, -1), want) <= REL_TOL
+    got = lora_dev(hip, w, x, n_tok, n_groups, group_dim, rank, dtype)
+    assert rel_err(got.reshape(n_tok, -1), want) <= REL_TOL
+
+
+@pytest.mark.parametrize("rank", [8, 3])
+def test_grouped_lora_down_groups_too_long_for_lds(oracle, hip, rank):
+    """A Q8_0 group of 32800 elements (more than one token's x fits in LDS)
+    runs per group on gathered x. With rank 8 the groups are whole
+    super-tiles (8 x 1025 blocks) and both forms compute; with rank 3 they
+    are not: the host form converts each group on its own, the device form
+    reports Unimplemented and writes nothing."""
+    n_tok, n_groups, group_dim = 2, 2, 32800
+    w, x = grouped_case(G.Q8_0, n_tok, n_groups, group_dim, rank, 8)
+    want = oracle_grouped(oracle, w, x, np.arange(n_tok), n_groups, group_dim, rank, G.Q8_0)
+    got = np.full(n_tok * n_groups * rank, np.nan, np.float32)
+    hip.matmul_grouped_lora_down(got, w, x.reshape(-1), n_tok, n_groups, group_dim, rank, G.Q8_0)
+    assert rel_err(got.reshape(n_tok, -1), want) <= REL_TOL
+    if rank == 8:
+        got = lora_dev(hip, w, x, n_tok, n_groups, group_dim, rank, G.Q8_0)
+        assert rel_err(got.reshape(n_tok, -1), want) <= REL_TOL
+    else:
+        with pytest.raises(hip.Unimplemented):
+            lora_dev(hip, w, x, n_tok, n_groups, group_dim, rank, G.Q8_0)
 
 
 @pytest.mark.parametrize("n_tok", [1, 2, 5, 16])
 def test_grouped_lora_down_dsv4_attn_output_a(oracle, hip, n_tok):
     """DS-V4 Flash attn_output_a: 8 groups of [1024 x 4096] Q8_0 (weight.rs:
-    171-182); 1 token is one launch, 2..8 one launch per group, 16 gathered."""
+    171-182); each chunk of up to 8 tokens is one launch."""
     n_groups, group_dim, rank = 8, 4096, 1024
     w, x = grouped_case(G.Q8_0, n_tok, n_groups, group_dim, rank, 900)
     toks = np.unique(np.array([0, n_tok // 2, n_tok - 1]))
