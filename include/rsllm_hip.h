@@ -142,6 +142,61 @@ int rsllm_hip_register_weights(const uint8_t *weights, size_t weights_len, uint3
                                size_t in_dim);
 int rsllm_hip_release_weights(void);
 
+/* ---- whole-model residency ---------------------------------------------------
+ * No single reference function: this replaces keeping weights only in the
+ * GGUF mmap (GgufFile::open, rsllm-gguf/src/file.rs:81-97; tensor_bytes
+ * :181-187; resolve_blob, models/src/dsv4/loader.rs:199-216) when the
+ * matmuls run on the GPU. The caller lists every tensor once, after opening
+ * the file:
+ *   name    TensorInfo::name;
+ *   data    GgufFile::tensor_bytes (host memory, e.g. inside the mmap);
+ *   len     its byte length;
+ *   dtype   TensorInfo::raw_type (GgmlType id);
+ *   in_dim  row length (shape[0]) for tensors used as matmul weights (F32 or
+ *           a matmul format), else 0.
+ * rsllm_hip_model_upload copies all of them into one device allocation, in
+ * list order (each 256-byte aligned, so stacked expert tensors stay
+ * contiguous), through pinned staging, converting matmul tensors (in_dim !=
+ * 0) to the device layout; the rest are copied as is. Matmul tensors are
+ * registered under their
+ * host range, like rsllm_hip_register_weights, so the host-pointer entry
+ * points use the resident copy. An upload whose fingerprint
+ * (GgufFile::fingerprint, file.rs:175-177: names, types and shapes only),
+ * tensor table and sampled payload digest (16 windows of 256 bytes per
+ * tensor) match a live model on the same device returns that model, adds a
+ * reference and registers the new host ranges, without copying: two files
+ * of one layout that differ only outside the sampled windows would be taken
+ * for the same. Errors, all before any device work: INVALID_ARGUMENT for
+ * NULL arguments or duplicate names, SHAPE_MISMATCH for a matmul tensor
+ * whose length is not whole rows of a block-aligned in_dim. Uploads are
+ * serialised with each other and with the lookups below.
+ * rsllm_hip_model_tensor returns a tensor's device address and length (the
+ * device-layout bytes the _dev entry points take). rsllm_hip_model_release
+ * drops one reference; the last one removes the registrations and frees
+ * the allocation after the device is idle. rsllm_hip_release_weights does
+ * not touch models. */
+typedef struct rsllm_hip_tensor_desc {
+    const char *name;
+    const uint8_t *data;
+    size_t len;
+    uint32_t dtype;
+    size_t in_dim;
+} rsllm_hip_tensor_desc;
+
+typedef struct rsllm_hip_model_info {
+    uint64_t device_bytes;   /* size of the model's device allocation */
+    uint64_t uploaded_bytes; /* payload bytes copied when it was uploaded */
+    double upload_seconds;   /* wall time of that upload */
+    uint32_t refs, n_tensors;
+} rsllm_hip_model_info;
+
+int rsllm_hip_model_upload(const uint8_t *fingerprint /* 32 bytes */,
+                           const rsllm_hip_tensor_desc *tensors, size_t n_tensors,
+                           uint64_t *model);
+int rsllm_hip_model_tensor(uint64_t model, const char *name, const uint8_t **dev, size_t *len);
+int rsllm_hip_model_info_get(uint64_t model, rsllm_hip_model_info *out);
+int rsllm_hip_model_release(uint64_t model);
+
 /* GGUF rows -> device layout: `len` bytes holding whole rows of `in_dim`
  * elements (n = len / block_bytes blocks in matrix order, row-major over
  * (row, block)). Q4_K: unchanged (`dst` may equal `src`). Q6_K, Q8_0, Q4_0,

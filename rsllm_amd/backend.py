@@ -117,6 +117,18 @@ class _Capability(ctypes.Structure):
                 ("iq2xxs_matmul", ctypes.c_int), ("fp8_kv_cache", ctypes.c_int)]
 
 
+class TensorDesc(ctypes.Structure):
+    """rsllm_hip_tensor_desc: one GGUF tensor for rsllm_hip_model_upload."""
+    _fields_ = [("name", ctypes.c_char_p), ("data", ctypes.c_void_p), ("len", ctypes.c_size_t),
+                ("dtype", ctypes.c_uint32), ("in_dim", ctypes.c_size_t)]
+
+
+class ModelInfo(ctypes.Structure):
+    _fields_ = [("device_bytes", ctypes.c_uint64), ("uploaded_bytes", ctypes.c_uint64),
+                ("upload_seconds", ctypes.c_double), ("refs", ctypes.c_uint32),
+                ("n_tensors", ctypes.c_uint32)]
+
+
 # Every symbol include/rsllm_hip.h declares, with its ctypes signature.
 _P, _S, _U32, _I = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_int
 SIGNATURES = {
@@ -127,6 +139,12 @@ SIGNATURES = {
     "rsllm_hip_matmul_quant_f32_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _P], _I),
     "rsllm_hip_register_weights": ([_P, _S, _U32, _S], _I),
     "rsllm_hip_release_weights": ([], _I),
+    "rsllm_hip_model_upload": ([_P, ctypes.POINTER(TensorDesc), _S,
+                                ctypes.POINTER(ctypes.c_uint64)], _I),
+    "rsllm_hip_model_tensor": ([ctypes.c_uint64, ctypes.c_char_p, ctypes.POINTER(_P),
+                                ctypes.POINTER(_S)], _I),
+    "rsllm_hip_model_info_get": ([ctypes.c_uint64, ctypes.POINTER(ModelInfo)], _I),
+    "rsllm_hip_model_release": ([ctypes.c_uint64], _I),
     "rsllm_hip_prepare_weights_dev": ([_P, _P, _S, _U32, _S, _P], _I),
     "rsllm_hip_dequant_to_f32": ([_U32, _P, _S, _P, _S], _I),
     "rsllm_hip_dequant_to_f32_dev": ([_U32, _P, _S, _P, _S, _P], _I),
@@ -285,6 +303,44 @@ def register_weights(weights: np.ndarray, dtype, in_dim: int) -> None:
 
 def release_weights() -> None:
     _check(LIB.rsllm_hip_release_weights())
+
+
+def model_upload(fingerprint: bytes, tensors) -> int:
+    """Upload a whole checkpoint once (rsllm_hip_model_upload). ``tensors`` is
+    a sequence of (name, array, dtype, in_dim); each array is the tensor's
+    payload (C-contiguous, any dtype: its bytes are taken, e.g. a slice of an
+    np.memmap of the GGUF file) and must outlive its use by host-pointer
+    calls. Returns the model id."""
+    if len(fingerprint) != 32:
+        raise ValueError("fingerprint must be 32 bytes")
+    descs = (TensorDesc * max(len(tensors), 1))()
+    keep = []
+    for i, (name, arr, dtype, in_dim) in enumerate(tensors):
+        ptr, n = _host_bytes(arr)
+        nm = name.encode()
+        keep.append(nm)
+        descs[i] = TensorDesc(nm, ptr.value if ptr is not None else None, n, int(dtype), in_dim)
+    fp = ctypes.create_string_buffer(bytes(fingerprint), 32)
+    mid = ctypes.c_uint64()
+    _check(LIB.rsllm_hip_model_upload(fp, descs, len(tensors), ctypes.byref(mid)))
+    return mid.value
+
+
+def model_tensor(model: int, name: str):
+    """(device address, byte length) of one tensor of an uploaded model."""
+    dev, n = _P(), _S()
+    _check(LIB.rsllm_hip_model_tensor(model, name.encode(), ctypes.byref(dev), ctypes.byref(n)))
+    return dev.value or 0, n.value
+
+
+def model_info(model: int) -> dict:
+    info = ModelInfo()
+    _check(LIB.rsllm_hip_model_info_get(model, ctypes.byref(info)))
+    return {f: getattr(info, f) for f, _ in ModelInfo._fields_}
+
+
+def model_release(model: int) -> None:
+    _check(LIB.rsllm_hip_model_release(model))
 
 
 def init(device: int = 0) -> None:

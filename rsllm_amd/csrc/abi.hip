@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "../../include/rsllm_hip.h"
+#include "abi_internal.h"
 #include "kernels.h"
 
 using namespace rsllm_hip;
@@ -54,12 +55,16 @@ std::mutex g_mu;
 int g_device = 0;
 bool g_inited = false;
 
+// Host tensors with a device copy. owner 0: rsllm_hip_register_weights (dev
+// owned by the entry); otherwise the id of the uploaded model whose arena
+// holds dev.
 struct Registered {
     const uint8_t *host;
     size_t len;
     uint32_t dtype;
     size_t in_dim;
     uint8_t *dev;
+    uint64_t owner;
 };
 std::vector<Registered> g_registry;
 
@@ -213,7 +218,7 @@ bool needs_prepare(uint32_t dtype) { return dtype != T_Q4_K; }
 int blob_on_device(const uint8_t *blob, size_t len, uint32_t dtype, size_t in_dim, DevBuf &dst,
                    const uint8_t **dev) {
     ThreadCtx &c = t_ctx;
-    if (dtype != T_F32 && (*dev = find_registered(blob, len, dtype, in_dim))) return RSLLM_HIP_OK;
+    if ((*dev = find_registered(blob, len, dtype, in_dim))) return RSLLM_HIP_OK;
     HIP_TRY(dst.ensure(len), "hipMalloc");
     if (dtype == T_F32 || !needs_prepare(dtype) || in_dim == 0) {
         if (len)
@@ -468,6 +473,30 @@ int shared_compute(float *out, const float *x, const uint8_t *gate, size_t gate_
 }
 
 }  // namespace
+
+// ---- interface for the other host-side files (abi_internal.h) --------------
+namespace rsllm_hip::abi {
+int set_error(int status, const char *msg) { return set_err(status, msg); }
+int ok_status() { return ok(); }
+int device_error(hipError_t e, const char *where) { return dev_err(e, where); }
+int ensure_current_device() { return ensure_device(); }
+void registry_add(const uint8_t *host, size_t len, uint32_t dtype, size_t in_dim, uint8_t *dev,
+                  uint64_t owner) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (const auto &r : g_registry)
+        if (r.host == host && r.len == len && r.dtype == dtype && r.in_dim == in_dim &&
+            r.dev == dev && r.owner == owner)
+            return;
+    g_registry.push_back({host, len, dtype, in_dim, dev, owner});
+}
+void registry_drop_owner(uint64_t owner) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    std::vector<Registered> keep;
+    for (auto &r : g_registry)
+        if (r.owner != owner) keep.push_back(r);
+    g_registry.swap(keep);
+}
+}  // namespace rsllm_hip::abi
 
 extern "C" {
 
@@ -976,7 +1005,7 @@ int rsllm_hip_register_weights(const uint8_t *weights, size_t weights_len, uint3
         return dev_err(e, "register_weights");
     }
     std::lock_guard<std::mutex> lk(g_mu);
-    g_registry.push_back({weights, weights_len, dtype, in_dim, dev});
+    g_registry.push_back({weights, weights_len, dtype, in_dim, dev, 0});
     return ok();
 }
 
@@ -984,7 +1013,9 @@ int rsllm_hip_release_weights(void) {
     std::vector<Registered> regs;
     {
         std::lock_guard<std::mutex> lk(g_mu);
-        regs.swap(g_registry);
+        std::vector<Registered> keep;
+        for (auto &r : g_registry) (r.owner ? keep : regs).push_back(r);
+        g_registry.swap(keep);
     }
     if (!regs.empty()) {
         int rc = ensure_device();
@@ -1064,8 +1095,7 @@ int rsllm_hip_matmul_weight_f32(float *out, size_t out_len, const uint8_t *weigh
     if (n_tok == 0 || out_dim == 0) return ok();
     if ((rc = ensure_device())) return rc;
     ThreadCtx &c = t_ctx;
-    const uint8_t *dw =
-        dtype == T_F32 ? nullptr : find_registered(weights, weights_len, dtype, in_dim);
+    const uint8_t *dw = find_registered(weights, weights_len, dtype, in_dim);
     if (!dw && weights_len) {
         HIP_TRY(c.w_raw.ensure(weights_len), "hipMalloc");
         HIP_TRY(hipMemcpyAsync(c.w_raw.p, weights, weights_len, hipMemcpyHostToDevice, c.stream),
@@ -1129,7 +1159,7 @@ int rsllm_hip_matmul_grouped_lora_down(float *out, size_t out_len, const uint8_t
     const bool prep = dtype != T_F32 && needs_prepare(dtype) && group_dim;
     const bool per_group = prep && (rank * (group_dim / block_elems_of(dtype))) % 8 != 0 &&
                            !gemv_rows_fits(dtype, (int)group_dim);
-    const uint8_t *dw = dtype == T_F32 || used != weights_len || per_group
+    const uint8_t *dw = used != weights_len || per_group
                             ? nullptr
                             : find_registered(weights, weights_len, dtype, group_dim);
     if (!dw) {

@@ -1,0 +1,29 @@
+// Interface between the C-ABI files: the per-thread error state, the device
+// choice and the registry of host tensors with device copies live in
+// abi.hip; residency.hip (whole-model upload) uses them through these calls.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace rsllm_hip::abi {
+
+// Record the calling thread's error (rsllm_hip_last_error) and return status.
+int set_error(int status, const char *msg);
+// Record success and return RSLLM_HIP_OK.
+int ok_status();
+// Record a HIP runtime failure at `where` and return RSLLM_HIP_ERR_DEVICE.
+int device_error(hipError_t e, const char *where);
+// Make the process's device current on this thread (and create the thread's
+// stream); returns a status.
+int ensure_current_device();
+// Host tensor (host, len, dtype, in_dim) -> device copy at dev, owned by the
+// uploaded model `owner` (never 0). Host-pointer entry points find it.
+void registry_add(const uint8_t *host, size_t len, uint32_t dtype, size_t in_dim, uint8_t *dev,
+                  uint64_t owner);
+// Remove every entry of one owner.
+void registry_drop_owner(uint64_t owner);
+
+}  // namespace rsllm_hip::abi

@@ -301,11 +301,10 @@ hipError_t launch_dequant(uint32_t dtype, const uint8_t *src, float *dst, size_t
     return hipGetLastError();
 }
 
-hipError_t launch_prepare(uint32_t dtype, const uint8_t *src, uint8_t *dst, size_t rows,
-                          size_t in_dim, hipStream_t s) {
-    const size_t bytes = rows * row_bytes_of(dtype, in_dim);
+hipError_t launch_prepare_blocks(uint32_t dtype, const uint8_t *src, uint8_t *dst,
+                                 size_t n_blocks, hipStream_t s) {
+    const size_t bytes = n_blocks * block_bytes_of(dtype);
     if (bytes == 0) return hipSuccess;
-    const size_t n_blocks = rows * (in_dim / block_elems_of(dtype));
     switch (dtype) {
     case T_Q4_K:
         if (src != dst) return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
@@ -329,6 +328,13 @@ hipError_t launch_prepare(uint32_t dtype, const uint8_t *src, uint8_t *dst, size
         return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_prepare(uint32_t dtype, const uint8_t *src, uint8_t *dst, size_t rows,
+                          size_t in_dim, hipStream_t s) {
+    const size_t be = block_elems_of(dtype);
+    if (be == 0) return hipErrorInvalidValue;
+    return launch_prepare_blocks(dtype, src, dst, rows * (in_dim / be), s);
 }
 
 }  // namespace rsllm_hip

@@ -41,6 +41,16 @@ hipError_t launch_dequant(uint32_t dtype, const uint8_t *src, float *dst, size_t
 // GGUF rows -> device layout (dst must not alias src, except for Q4_K).
 hipError_t launch_prepare(uint32_t dtype, const uint8_t *src, uint8_t *dst, size_t rows,
                           size_t in_dim, hipStream_t s);
+// The same over n_blocks consecutive blocks. The layout packs 8 blocks per
+// super-tile from the first block on (the last one may be shorter), so a
+// matrix converted in pieces that start on multiples of 8 blocks, at the
+// same byte offsets, is byte-identical to the matrix converted whole.
+hipError_t launch_prepare_blocks(uint32_t dtype, const uint8_t *src, uint8_t *dst,
+                                 size_t n_blocks, hipStream_t s);
+// Formats whose device layout differs from the GGUF bytes.
+inline bool layout_converted(uint32_t t) {
+    return t == T_Q6_K || t == T_Q8_0 || t == T_Q4_0 || t == T_Q2_K || t == T_IQ2_XXS;
+}
 
 // gemv.hip: y[t, o] = sum_i W[o, i] x[t, i] for t < n_tok, W (w_bytes bytes)
 // in device layout. Batch 1 is one launch that quantises x in LDS; 5..32
