@@ -431,6 +431,35 @@ def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
     del reps, wf
     out["caller_chain"] = chain
 
+    # ---- whole-model upload (GGUF mapping -> device arena, device layout) ----
+    n_each, rows_q6, rows_q4 = 8, 40000, 58000
+    base = np.random.default_rng(800).integers(0, 256, 16 << 20, dtype=np.uint8)
+    tensors = []
+    for j in range(n_each):
+        for dt, rows, rb in ((G.Q6_K, rows_q6, 3360), (G.Q4_K, rows_q4, 2304)):
+            n = rows * rb
+            a = np.resize(base, n) ^ np.uint8(j * 2 + (dt == G.Q6_K))
+            tensors.append((f"blk.{j}.{dt.name.lower()}.weight", a, dt, 4096))
+    total = sum(t[1].size for t in tensors)
+    runs = []
+    for r in range(3):
+        fp = bytes([r]) * 32
+        t0 = time.perf_counter()
+        mid = B.model_upload(fp, tensors)
+        wall = time.perf_counter() - t0
+        info = B.model_info(mid)
+        B.model_release(mid)
+        runs.append((wall, info["upload_seconds"]))
+    best = min(runs)
+    out["model_upload"] = {
+        "bytes": total, "tensors": len(tensors),
+        "what": "16 tensors of 134 MB (8 Q6_K converted to the device layout, 8 Q4_K copied) "
+                "from host memory into one device arena; best of 3 uploads",
+        "seconds": round(best[0], 4), "GBps": round(total / best[0] / 1e9, 2),
+        "library_seconds": round(best[1], 4),
+        "all_runs_s": [round(w, 4) for w, _ in runs]}
+    del tensors, base
+
     # ---- C3 routed experts (64 experts, Q4_K gate/up 2048x7168, down 7168x2048, top-8) ----
     # Two device copies of the expert stacks and 8 routings per T: call i
     # uses copy i % 2 and routing (i // 2) % 8, so consecutive calls never
