@@ -61,6 +61,9 @@ def parse():
                     help="skip the two rocprofv3 --pmc passes that measure roofline.traffic")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="internal: the workload run under rocprofv3 --pmc (prints no JSON)")
+    ap.add_argument("--prefill-probe", type=int, default=0, metavar="T",
+                    help="internal: only run the C4 prefill call at T tokens 5 times (the "
+                         "workload for rocprofv3 counter passes; prints no JSON)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C4 prefill leg")
     ap.add_argument("--prefill-iters", type=int, default=20)
     return ap.parse_args()
@@ -190,6 +193,24 @@ def pmc_probe():
         w = reps[i % len(reps)]
         B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
                                x.numel(), 1, in_dim, out_dim, G.Q6_K, sptr)
+    torch.cuda.synchronize()
+
+
+def prefill_probe(T):
+    """The C4 prefill call (Q4_K 14336x4096 weights, bf16 x [T x 4096]) five
+    times, for rocprofv3 runs that count MFMA and VALU work per dispatch."""
+    import torch
+    from rsllm_amd import backend as B
+    from rsllm_amd import synth
+    from rsllm_amd.ggml import GgmlType as G
+    out_dim, in_dim = 14336, 4096
+    sptr = torch.cuda.current_stream().cuda_stream
+    w = torch.from_numpy(synth.weight(G.Q4_K, out_dim, in_dim, seed=300)).cuda()
+    x = torch.from_numpy(synth.bf16_activations(T, in_dim, seed=301).reshape(-1)).cuda()
+    y = torch.empty(T * out_dim, dtype=torch.float32, device="cuda")
+    for _ in range(5):
+        B.matmul_q4k_bf16_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
+                              x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
     torch.cuda.synchronize()
 
 
@@ -536,6 +557,9 @@ def main():
         sys.exit(2)
     if args.pmc_probe:
         pmc_probe()
+        return
+    if args.prefill_probe:
+        prefill_probe(args.prefill_probe)
         return
     # the counter passes run first, in child processes, before this process
     # touches the GPU
