@@ -465,6 +465,9 @@ static hipError_t down_go(const uint8_t *down, size_t stride, const float *h, co
 }
 
 constexpr int kMoeNW = 16, kMoePD = 2;
+// Most token chunks the fused pair is run over before the multi-launch path
+// takes over.
+constexpr int kMaxFusedChunks = 16;
 
 template <class F>
 static bool gu_fits(int n_tok, int k, int n_embd, int n_ff) {
@@ -579,6 +582,23 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
     if (moe_fused_fits(dt_gu, dt_d, n_tok, k, n_embd, n_ff, gu_stride, d_stride))
         return moe_fused(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x, ids, wts, out, hg,
                          n_tok, k, n_expert, n_embd, n_ff, clamp, s);
+    // More tokens than the fused pair takes: the fused pair over token
+    // chunks when few chunks cover them (tokens are independent; each chunk
+    // re-reads the experts it shares with the others).
+    int tc = n_tok;
+    while (tc > 1 && !moe_fused_fits(dt_gu, dt_d, tc, k, n_embd, n_ff, gu_stride, d_stride)) tc--;
+    if (moe_fused_fits(dt_gu, dt_d, tc, k, n_embd, n_ff, gu_stride, d_stride) &&
+        (n_tok + tc - 1) / tc <= kMaxFusedChunks) {
+        for (int t0 = 0; t0 < n_tok; t0 += tc) {
+            const int nt = n_tok - t0 < tc ? n_tok - t0 : tc;
+            const hipError_t e =
+                moe_fused(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x + (size_t)t0 * n_embd,
+                          ids + (size_t)t0 * k, wts + (size_t)t0 * k, out + (size_t)t0 * n_embd,
+                          hg, nt, k, n_expert, n_embd, n_ff, clamp, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     // at most min(n_expert, n_tok * k) experts are active
     const int grid_experts = (int)(P < (size_t)n_expert ? P : (size_t)n_expert);
 
