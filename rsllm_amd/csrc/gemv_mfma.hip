@@ -1,11 +1,13 @@
-// Batched GEMV (5..32 tokens) on the matrix cores: y[t, o] = sum_i W[o, i] x[t, i].
+// Batched GEMV (5..32 tokens; Q8_0 from 9) on the matrix cores:
+// y[t, o] = sum_i W[o, i] x[t, i].
 //
 // Restates matmul_quant_f32 (rsllm-backend-cpu/src/ops/quant_matmul.rs:45-119)
 // for the decode batches of C1/C2-style shapes, where the int8-limb GEMV
 // (gemv.hip) spends VALU work per (weight, token) pair and stops being
 // memory-bound above a few tokens. Here each weight is dequantised once to
 // f16 in registers — f16(d*sc)*q - f16(dmin*m) for Q4_K (one rounding, as the
-// prefill GEMM), (q - 32)*f16(d*sc) for Q6_K (q - 32 exact, one rounding) —
+// prefill GEMM), (q - 32)*f16(d*sc) for Q6_K (q - 32 exact, one rounding),
+// q*d for Q8_0 (q exact, one rounding) —
 // and the tokens are the N dimension of v_mfma_f32_16x16x32_f16 (16 or 32
 // tokens per pass, fp32 accumulation), so the dequant cost is independent of
 // the batch.
@@ -165,6 +167,57 @@ struct MQ6K {
             f16x8 r;
             r[0] = v[0][0]; r[1] = v[0][1]; r[2] = v[1][0]; r[3] = v[1][1];
             r[4] = v[2][0]; r[5] = v[2][1]; r[6] = v[3][0]; r[7] = v[3][1];
+            a[j] = r;
+        }
+    }
+};
+
+// Q8_0 (super-tile device layout [qs 8x32 | d 8x2]). Step s = blocks 4s ..
+// 4s + 3 of the row; lane group q takes block 4s + q, MFMA j its elements
+// 8j .. 8j + 7. A code q (int8) becomes f16 exactly as the pattern 0x64 with
+// byte q ^ 0x80 (1024 + q + 128) minus 1152; the multiply by the f16 block
+// scale rounds once.
+struct MQ8 {
+    struct W {
+        uint4 q0, q1;
+        uint32_t d;
+    };
+    __device__ static int elem(int s, int j, int q) { return 128 * s + 32 * q + 8 * j; }
+    __device__ static void piece(int e, int &s, int &j, int &q) {
+        s = e >> 7;
+        q = (e >> 5) & 3;
+        j = (e >> 3) & 3;
+    }
+    __device__ static void load(W &w, __amdgpu_buffer_rsrc_t r, int row, int s, int q, int in_dim,
+                                int out_dim) {
+        const uint32_t nb = (uint32_t)(in_dim >> 5);
+        const uint32_t nblk = (uint32_t)out_dim * nb;
+        const uint32_t bi = (uint32_t)row * nb + 4u * (uint32_t)s + (uint32_t)q;
+        const uint32_t S = bi >> 3, jb = bi & 7u;
+        const uint32_t rS = (S < (nblk >> 3)) ? 8u : (nblk & 7u);
+        const uint32_t base = S * 272u;
+        w.q0 = bload16(r, base + jb * 32u, 0);
+        w.q1 = bload16(r, base + jb * 32u + 16u, 0);
+        w.d = bload2(r, base + rS * 32u + jb * 2u, 0);
+    }
+    __device__ static void dequant(const W &w, int, int, f16x8 (&a)[4]) {
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(w.d & 0xFFFFu));
+        const f16x2 dd = {d, d};
+        const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+        const uint32_t v[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            f16x8 r;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t b = v[2 * j + u] ^ 0x80808080u;
+                const f16x2 w01 = (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u)) - bias) * dd;
+                const f16x2 w23 = (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)) - bias) * dd;
+                r[4 * u] = w01[0];
+                r[4 * u + 1] = w01[1];
+                r[4 * u + 2] = w23[0];
+                r[4 * u + 3] = w23[1];
+            }
             a[j] = r;
         }
     }
@@ -520,8 +573,11 @@ static hipError_t mfb_xp_go(const uint8_t *w, size_t w_bytes, const float *x, fl
 // standard deviations); a matrix of a few dozen rows can exceed 1e-3 by
 // chance, so short matrices stay on the int8-limb GEMV.
 bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
-    return (dtype == T_Q4_K || dtype == T_Q6_K) && n_tok >= 5 && n_tok <= 32 &&
-           in_dim % 256 == 0 && in_dim > 0 && out_dim >= 1024;
+    // Q8_0 from 9 tokens: up to 8 the int8-limb kernel with x in LDS is as
+    // fast on 4096 x 4096 and faster on 1024-row matrices
+    const int min_tok = dtype == T_Q8_0 ? 9 : 5;
+    return (dtype == T_Q4_K || dtype == T_Q6_K || dtype == T_Q8_0) && n_tok >= min_tok &&
+           n_tok <= 32 && in_dim % 256 == 0 && in_dim > 0 && out_dim >= 1024;
 }
 
 size_t gemv_mfma_scratch_bytes(int n_tok, int in_dim) {
@@ -566,6 +622,7 @@ hipError_t launch_gemv_mfma(uint32_t dtype, const uint8_t *w, size_t w_bytes, co
     switch (dtype) {
     case T_Q4_K: return mf_dispatch<MQ4K>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
     case T_Q6_K: return mf_dispatch<MQ6K>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
+    case T_Q8_0: return mf_dispatch<MQ8>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
     default: return hipErrorInvalidValue;
     }
 }

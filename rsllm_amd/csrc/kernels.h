@@ -54,7 +54,8 @@ inline bool layout_converted(uint32_t t) {
 
 // gemv.hip: y[t, o] = sum_i W[o, i] x[t, i] for t < n_tok, W (w_bytes bytes)
 // in device layout. Batch 1 is one launch that quantises x in LDS; 5..32
-// tokens of Q4_K / Q6_K run on the matrix cores (gemv_mfma.hip); other
+// tokens of Q4_K / Q6_K and 9..32 of Q8_0 run on the matrix cores
+// (gemv_mfma.hip); other
 // batches run the activation pre-pass, then the GEMV. `xq_scratch` must hold
 // gemv_work_bytes(dtype, n_tok, in_dim, out_dim) bytes.
 hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
@@ -81,8 +82,9 @@ hipError_t launch_gemv_rows(uint32_t dtype, const uint8_t *w, size_t w_bytes, co
                             int y_stride, int rows_per_group, hipStream_t s);
 bool gemv_rows_fits(uint32_t dtype, int in_dim);
 
-// gemv_mfma.hip: the same product for 5..32 tokens of Q4_K / Q6_K on the
-// matrix cores (weights dequantised to f16 once, tokens as the MFMA's N).
+// gemv_mfma.hip: the same product for 5..32 tokens of Q4_K / Q6_K (9..32 of
+// Q8_0) on the matrix cores (weights dequantised to f16 once, tokens as the
+// MFMA's N).
 bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim);
 size_t gemv_mfma_scratch_bytes(int n_tok, int in_dim);
 hipError_t launch_gemv_mfma(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,

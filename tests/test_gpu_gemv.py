@@ -30,12 +30,13 @@ def test_gemv_ragged_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
     assert rel_err(got, want) <= REL_TOL
 
 
-# The matrix-core path (5..32 tokens of Q4_K / Q6_K, out_dim >= 1024): one
-# and two 16-token tiles, partial tiles, row counts off the 16-row tile, few K
-# steps per wavefront (in 256) and many (in 7168), token scales far apart.
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K])
+# The matrix-core path (5..32 tokens of Q4_K / Q6_K / Q8_0, out_dim >= 1024):
+# one and two 16-token tiles, partial tiles, row counts off the 16-row tile,
+# few K steps per wavefront (in 256) and many (in 7168), token scales far
+# apart.
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0])
 @pytest.mark.parametrize("out_dim,in_dim", [(1024, 256), (1030, 1024), (2000, 7168), (4097, 512)])
-@pytest.mark.parametrize("n_tok", [5, 15, 16, 17, 31, 32])
+@pytest.mark.parametrize("n_tok", [5, 9, 15, 16, 17, 31, 32])
 def test_gemv_mfma_batches(oracle, hip, dtype, out_dim, in_dim, n_tok):
     w = synth.weight(dtype, out_dim, in_dim, 7 + n_tok)
     x = synth.activations(n_tok, in_dim, 8 + n_tok)
@@ -55,7 +56,7 @@ def test_gemv_mfma_batches(oracle, hip, dtype, out_dim, in_dim, n_tok):
 # The fused matrix-core kernel (5..8 tokens, out_dim >= 8192, f16 x in LDS):
 # row counts off the 16-row block, K steps fewer than wavefronts (256 -> 2
 # steps over 16 wavefronts) and many, token scales far apart, one token
-# zero.
+# zero. (Q8_0 takes the matrix cores from 9 tokens only.)
 @pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K])
 @pytest.mark.parametrize("out_dim,in_dim", [(8192, 256), (8200, 1024), (9001, 3072)])
 @pytest.mark.parametrize("n_tok", [5, 6, 8])
