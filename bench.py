@@ -64,6 +64,9 @@ def parse():
     ap.add_argument("--prefill-probe", type=int, default=0, metavar="T",
                     help="internal: only run the C4 prefill call at T tokens 5 times (the "
                          "workload for rocprofv3 counter passes; prints no JSON)")
+    ap.add_argument("--moe-probe", type=int, default=0, metavar="T",
+                    help="internal: only run the C3 routed-expert call at T tokens 8 times "
+                         "(for rocprofv3 kernel traces; prints no JSON)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C4 prefill leg")
     ap.add_argument("--prefill-iters", type=int, default=20)
     return ap.parse_args()
@@ -211,6 +214,32 @@ def prefill_probe(T):
     for _ in range(5):
         B.matmul_q4k_bf16_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
                               x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
+    torch.cuda.synchronize()
+
+
+def moe_probe(T):
+    """The C3 routed-expert call (64 experts, Q4_K gate/up 2048x7168, down
+    7168x2048, top-8) at T tokens, 8 calls over 8 routings."""
+    import torch
+    from rsllm_amd import backend as B
+    from rsllm_amd import synth
+    from rsllm_amd.ggml import GgmlType as G
+    n_expert, n_embd, n_ff, k = 64, 7168, 2048, 8
+    sptr = torch.cuda.current_stream().cuda_stream
+    gate = synth.weight(G.Q4_K, n_expert * n_ff, n_embd, 600)
+    up = synth.weight(G.Q4_K, n_expert * n_ff, n_embd, 601)
+    down = synth.weight(G.Q4_K, n_expert * n_embd, n_ff, 602)
+    d_g, d_u, d_d = (torch.from_numpy(a).cuda() for a in (gate, up, down))
+    x = torch.from_numpy(synth.activations(T, n_embd, 610 + T).reshape(-1)).cuda()
+    y = torch.zeros(T * n_embd, dtype=torch.float32, device="cuda")
+    for r in range(8):
+        ids, wts = synth.moe_routing(T, n_expert, k, 620 + T + 1000 * r)
+        d_i = torch.from_numpy(ids.reshape(-1)).cuda()
+        d_w = torch.from_numpy(wts.reshape(-1)).cuda()
+        B.moe_routed_dev(y.data_ptr(), y.numel(), x.data_ptr(), x.numel(), d_g.data_ptr(),
+                         d_u.data_ptr(), gate.nbytes, d_d.data_ptr(), down.nbytes, d_i.data_ptr(),
+                         d_w.data_ptr(), ids.size, T, n_embd, n_ff, n_expert, k, G.Q4_K, G.Q4_K,
+                         10.0, sptr)
     torch.cuda.synchronize()
 
 
@@ -560,6 +589,9 @@ def main():
         return
     if args.prefill_probe:
         prefill_probe(args.prefill_probe)
+        return
+    if args.moe_probe:
+        moe_probe(args.moe_probe)
         return
     # the counter passes run first, in child processes, before this process
     # touches the GPU
