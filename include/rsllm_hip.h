@@ -173,8 +173,10 @@ int rsllm_hip_release_weights(void);
  * rsllm_hip_model_tensor returns a tensor's device address and length (the
  * device-layout bytes the _dev entry points take). rsllm_hip_model_release
  * drops one reference; the last one removes the registrations and frees
- * the allocation after the device is idle. rsllm_hip_release_weights does
- * not touch models. */
+ * the allocation after the device is idle. Calls that use the model must
+ * not be in flight on other threads while its last reference is released
+ * (the same holds for rsllm_hip_release_weights and registered tensors).
+ * rsllm_hip_release_weights does not touch models. */
 typedef struct rsllm_hip_tensor_desc {
     const char *name;
     const uint8_t *data;

@@ -131,6 +131,7 @@ int validate_tensor(const rsllm_hip_tensor_desc &d) {
 }
 
 // Parallel host copy (the source is usually a file mapping being paged in).
+// Pieces no thread could be started for are copied by the caller.
 void copy_parallel(uint8_t *dst, const uint8_t *src, size_t n) {
     if (n < (8u << 20)) {
         memcpy(dst, src, n);
@@ -140,7 +141,11 @@ void copy_parallel(uint8_t *dst, const uint8_t *src, size_t n) {
     std::vector<std::thread> th;
     for (size_t o = 0; o < n; o += per) {
         const size_t m = std::min(per, n - o);
-        th.emplace_back([=] { memcpy(dst + o, src + o, m); });
+        try {
+            th.emplace_back([=] { memcpy(dst + o, src + o, m); });
+        } catch (...) {
+            memcpy(dst + o, src + o, m);
+        }
     }
     for (auto &t : th) t.join();
 }
@@ -151,6 +156,8 @@ struct Staging {
     hipEvent_t done[2] = {nullptr, nullptr};
     hipStream_t s = nullptr;
     ~Staging() {
+        // work still queued (an upload that failed part way) ends first
+        if (s) (void)hipStreamSynchronize(s);
         for (int b = 0; b < 2; b++) {
             if (done[b]) (void)hipEventDestroy(done[b]);
             if (host[b]) (void)hipHostFree(host[b]);
