@@ -338,10 +338,10 @@ int rsllm_hip_matmul_grouped_lora_down_dev(float *out, size_t out_len, const uin
  * check_moe_shapes (:557-573) x_len then out_len (SHAPE_MISMATCH "moe.x" /
  * "moe.out"), then, if n_tok > 0, matmul_weight_f32's checks of the gate,
  * up and down calls in that order (as for rsllm_hip_matmul_weight_f32).
- * Gate and up of one quant format with a quant down run as one routed
- * expert of weight 1 through the routed-expert kernels (SwiGLU in the
- * gate/up epilogue); other combinations as separate GEMVs and an
- * elementwise SwiGLU. Host blobs registered with
+ * Gate and up of one quant format run as one GEMV launch per chunk of up to
+ * 8 tokens (the two matrices as two row groups on the same x), then an
+ * elementwise SwiGLU and the down GEMV; other combinations (F32 blobs,
+ * mixed formats) run gate and up as separate GEMVs. Host blobs registered with
  * rsllm_hip_register_weights are used from the device.
  *
  * Device form: blobs in the device layout (rsllm_hip_prepare_weights_dev

@@ -436,9 +436,11 @@ int validate_shared(size_t out_len, const void *out, size_t x_len, const void *x
 }
 
 // apply_shared_expert on device pointers (validated). Gate and up of one
-// quant format with a quant down run as one routed expert of weight 1
-// through launch_moe (SwiGLU in the gate/up epilogue, out = 0 + 1 * y);
-// anything else as gate, up (matmul_weight_f32), k_swiglu, down.
+// quant format run as one launch per chunk of up to 8 tokens (the two
+// matrices as two row groups of one GEMV on the same x, h = [gate | up] per
+// token), then the clamped SwiGLU and the down projection; other
+// combinations (F32 blobs, mixed formats) run gate and up through
+// matmul_weight_f32 separately.
 int shared_compute(float *out, const float *x, const uint8_t *gate, size_t gate_len,
                    uint32_t dt_gate, const uint8_t *up, size_t up_len, uint32_t dt_up,
                    const uint8_t *down, size_t down_len, uint32_t dt_down, size_t n_tok,
@@ -446,19 +448,16 @@ int shared_compute(float *out, const float *x, const uint8_t *gate, size_t gate_
     if (n_tok == 0 || n_embd == 0) return ok();
     ThreadCtx &c = t_ctx;
     const int T = (int)n_tok, E = (int)n_embd, FF = (int)n_ff;
-    if (dt_gate == dt_up && dt_gate != T_F32 && dt_down != T_F32 && n_ff) {
-        const size_t mb = (moe_scratch_bytes(dt_gate, dt_down, T, 1, 1, E, FF) + 255) / 256 * 256;
-        const size_t rb = (n_tok * 4 + 255) / 256 * 256;
-        HIP_TRY(c.moe.ensure(mb + 2 * rb), "hipMalloc");
-        uint8_t *scr = (uint8_t *)c.moe.p;
-        int *ids = (int *)(scr + mb);
-        float *w = (float *)(scr + mb + rb);
-        HIP_TRY(launch_fill_route(ids, w, T, s), "fill_route");
-        HIP_TRY(launch_fill_zero(out, n_tok * n_embd, s), "fill_zero");
-        HIP_TRY(launch_moe(dt_gate, dt_down, gate, up, down, gate_len, down_len, x, ids, w, out,
-                           scr, T, 1, 1, E, FF, clamp, s),
-                "moe");
-        return ok();
+    if (dt_gate == dt_up && dt_gate != T_F32 && gate_len == up_len && n_ff &&
+        gemv_rows_fits(dt_gate, E)) {
+        const size_t hb = (n_tok * n_ff * 8 + 255) / 256 * 256;
+        HIP_TRY(c.xh.ensure(hb + n_tok * n_ff * 4 + 256), "hipMalloc");
+        float *h = (float *)c.xh.p, *act = (float *)((uint8_t *)c.xh.p + hb);
+        HIP_TRY(launch_gemv_pair(dt_gate, gate, up, gate_len, x, h, T, E, FF, 2 * FF, s),
+                "gemv_pair");
+        HIP_TRY(launch_swiglu_pair(h, act, T, FF, clamp, s), "swiglu");
+        return weight_f32_compute(out, n_tok * n_embd, down, down_len, act, n_tok, n_ff, n_embd,
+                                  dt_down, s);
     }
     const size_t hb = (n_tok * n_ff * 4 + 255) / 256 * 256;
     HIP_TRY(c.xh.ensure(3 * hb + 256), "hipMalloc");

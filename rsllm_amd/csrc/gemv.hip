@@ -180,13 +180,19 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv(const uint8_t *__restri
 //
 // Groups. The rows form groups of rows_per_group consecutive rows (one
 // group: rows_per_group = out_dim); row r of group g = r / rows_per_group
-// dots x columns [g * in_dim, (g + 1) * in_dim) of each token. Workgroups
-// are dealt group-major, wpg per group: workgroup b serves group b / wpg and
-// takes that group's rows b % wpg + wpg * l, and its LDS image holds only
-// that group's x. Token t of x starts at x + t * x_stride (x_dim readable
-// values from there); y[t, r] is at y + t * y_stride + r.
+// dots x columns [g * x_gstride, g * x_gstride + in_dim) of each token.
+// Workgroups are dealt group-major, wpg per group: workgroup b serves group
+// b / wpg and takes that group's rows b % wpg + wpg * l, and its LDS image
+// holds only that group's x. Token t of x starts at x + t * x_stride (x_dim
+// readable values from there); y[t, r] is at y + t * y_stride + r.
+// Weights: one matrix of out_dim rows at w; or, with w1 set, two matrices of
+// rows_per_group rows each (group 0 at w, group 1 at w1, w1_bytes long), as
+// an FFN's gate and up projections of one x (x_gstride 0).
 struct Gemv1Shape {
     int in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group, wpg;
+    int x_gstride;
+    const uint8_t *w1;
+    uint32_t w1_bytes;
 };
 
 template <class F, int NW, int PD, int GPT, int BT = 1>
@@ -211,7 +217,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
     const int nrows = r0 < R ? (R - r0 + wpg - 1) / wpg : 0;            // this workgroup's rows
     const int my_rows = nrows > wv ? (nrows - wv + NW - 1) / NW : 0;   // this wavefront's rows
     const int T = my_rows * ncols;                                       // its tiles
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
+    // the matrix this workgroup's rows belong to: its rows, and the first
+    // global row in it
+    const bool pair = sh.w1 != nullptr;
+    const __amdgpu_buffer_rsrc_t rw =
+        pair && gsel ? make_rsrc(sh.w1, sh.w1_bytes) : make_rsrc(w, w_bytes);
+    const int mrows = pair ? R : out_dim, mbase = pair ? row_base : 0;
     const __amdgpu_buffer_rsrc_t rnull = make_rsrc(w, 0);
     const __amdgpu_buffer_rsrc_t rx =
         make_rsrc(x, ((uint32_t)(n_tok - 1) * (uint32_t)sh.x_stride + (uint32_t)sh.x_dim) * 4u);
@@ -223,7 +234,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
         const int half = r2 >> 6, ln = r2 & 63;
         const int kk = ln & 7, unit = col * 8 + (ln >> 3);
         const bool ok = g < n_groups && t < n_tok && unit < nunits && F::valid(unit, kk, in_dim);
-        return ok ? t * sh.x_stride + gsel * in_dim +
+        return ok ? t * sh.x_stride + gsel * sh.x_gstride +
                         (half ? F::elem_hi(unit, kk) : F::elem_lo(unit, kk))
                   : -1;
     };
@@ -232,8 +243,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
     auto load_tile = [&](typename F::Slice &sl, int t) {
         const int j = t / ncols, col = t - j * ncols;
         const int unit = min(col * 8 + ks, nunits - 1);
-        const __amdgpu_buffer_rsrc_t r = t < T ? rw : rnull;
-        F::load(sl, r, min(row_of(j), out_dim - 1), unit, k, in_dim, out_dim);
+        const __amdgpu_buffer_rsrc_t r = t < T ? rw : rnull;  // rows past T: no traffic
+        F::load(sl, r, min(row_of(j), out_dim - 1) - mbase, unit, k, in_dim, mrows);
     };
 
     // Prologue: x loads, the first tiles, then quantisation into LDS (token
@@ -374,7 +385,7 @@ static hipError_t gemv1_gpt_go(const uint8_t *w, size_t w_bytes, const float *x,
 
 static Gemv1Shape plain_shape(int n_tok, int in_dim, int out_dim) {
     (void)n_tok;
-    return Gemv1Shape{in_dim, out_dim, in_dim, in_dim, out_dim, out_dim, 1};
+    return Gemv1Shape{in_dim, out_dim, in_dim, in_dim, out_dim, out_dim, 1, in_dim, nullptr, 0};
 }
 
 // ---- grouped GEMV (routed experts) ------------------------------------------
@@ -797,7 +808,8 @@ hipError_t launch_gemv_f32(const float *w, const float *x, float *y, int n_tok, 
                            int out_dim, int x_dim, int x_stride, int y_stride, int rows_per_group,
                            hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
-    const Gemv1Shape sh{in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group, 0};
+    const Gemv1Shape sh{in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group,
+                        0,      in_dim,  nullptr, 0};
     const int n_wg = min(device_cus(), out_dim);
     // x offsets are 32-bit byte offsets: launch in token chunks of < 2 GiB of x
     const size_t per = ((size_t)1 << 29) / (size_t)(x_stride > 0 ? x_stride : 1);
@@ -818,19 +830,14 @@ hipError_t launch_gemv_f32(const float *w, const float *x, float *y, int n_tok, 
 // LDS even for one token.
 bool gemv_rows_fits(uint32_t dtype, int in_dim) { return gemv1_tokens(dtype, 1, in_dim) != 0; }
 
-hipError_t launch_gemv_rows(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
-                            float *y, int n_tok, int in_dim, int out_dim, int x_dim, int x_stride,
-                            int y_stride, int rows_per_group, hipStream_t s) {
-    if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
-    if (rows_per_group <= 0 || out_dim % rows_per_group != 0) return hipErrorInvalidValue;
-    if (!gemv_rows_fits(dtype, in_dim)) return hipErrorNotSupported;
+// k_gemv1 over token chunks of up to 8 (the largest whose x fits in LDS).
+static hipError_t gemv1_chunks(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
+                               float *y, int n_tok, const Gemv1Shape &sh, hipStream_t s) {
     for (int t0 = 0; t0 < n_tok;) {
-        // the largest chunk of at most 8 tokens whose x fits in LDS
         int c = n_tok - t0 < 8 ? n_tok - t0 : 8;
-        while (c > 1 && gemv1_tokens(dtype, c, in_dim) == 0) c = (c + 1) / 2;
-        const Gemv1Shape sh{in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group, 1};
-        const float *xc = x + (size_t)t0 * x_stride;
-        float *yc = y + (size_t)t0 * y_stride;
+        while (c > 1 && gemv1_tokens(dtype, c, sh.in_dim) == 0) c = (c + 1) / 2;
+        const float *xc = x + (size_t)t0 * sh.x_stride;
+        float *yc = y + (size_t)t0 * sh.y_stride;
         hipError_t e = hipErrorInvalidValue;
         if (c == 1) {
 #define X(T, F) if (dtype == T) e = gemv1<F>(w, w_bytes, xc, yc, sh, s);
@@ -845,6 +852,27 @@ hipError_t launch_gemv_rows(uint32_t dtype, const uint8_t *w, size_t w_bytes, co
         t0 += c;
     }
     return hipSuccess;
+}
+
+hipError_t launch_gemv_rows(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
+                            float *y, int n_tok, int in_dim, int out_dim, int x_dim, int x_stride,
+                            int y_stride, int rows_per_group, hipStream_t s) {
+    if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
+    if (rows_per_group <= 0 || out_dim % rows_per_group != 0) return hipErrorInvalidValue;
+    if (!gemv_rows_fits(dtype, in_dim)) return hipErrorNotSupported;
+    const Gemv1Shape sh{in_dim, out_dim, x_dim, x_stride, y_stride, rows_per_group,
+                        1,      in_dim,  nullptr, 0};
+    return gemv1_chunks(dtype, w, w_bytes, x, y, n_tok, sh, s);
+}
+
+hipError_t launch_gemv_pair(uint32_t dtype, const uint8_t *w0, const uint8_t *w1, size_t w_bytes,
+                            const float *x, float *y, int n_tok, int in_dim, int rows,
+                            int y_stride, hipStream_t s) {
+    if (n_tok <= 0 || rows <= 0) return hipSuccess;
+    if (!gemv_rows_fits(dtype, in_dim)) return hipErrorNotSupported;
+    const Gemv1Shape sh{in_dim, 2 * rows, in_dim, in_dim, y_stride, rows,
+                        1,      0,        w1,     (uint32_t)w_bytes};
+    return gemv1_chunks(dtype, w0, w_bytes, x, y, n_tok, sh, s);
 }
 
 hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,

@@ -81,6 +81,13 @@ hipError_t launch_gemv_rows(uint32_t dtype, const uint8_t *w, size_t w_bytes, co
                             float *y, int n_tok, int in_dim, int out_dim, int x_dim, int x_stride,
                             int y_stride, int rows_per_group, hipStream_t s);
 bool gemv_rows_fits(uint32_t dtype, int in_dim);
+// Two matrices of `rows` rows and in_dim columns (device layouts of their
+// own, w_bytes each) on one x [n_tok x in_dim]: y[t * y_stride + r] for
+// r < rows from w0, y[t * y_stride + rows + r] from w1. Same token chunks
+// and hipErrorNotSupported as launch_gemv_rows.
+hipError_t launch_gemv_pair(uint32_t dtype, const uint8_t *w0, const uint8_t *w1, size_t w_bytes,
+                            const float *x, float *y, int n_tok, int in_dim, int rows,
+                            int y_stride, hipStream_t s);
 
 // gemv_mfma.hip: the same product for 5..32 tokens of Q4_K / Q6_K (9..32 of
 // Q8_0) on the matrix cores (weights dequantised to f16 once, tokens as the
@@ -139,11 +146,12 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
                       int k, int n_expert, int n_embd, int n_ff, float clamp, hipStream_t s);
 
 // moe.hip, shared expert: elementwise clamped SwiGLU a = silu(min(g, c)) *
-// clamp(u, -c, c) (no clamp when c <= 1e-6), and the one-expert routing
-// table (ids 0, weights 1) for running one expert over n tokens.
+// clamp(u, -c, c) (no clamp when c <= 1e-6).
 hipError_t launch_swiglu(const float *g, const float *u, float *a, size_t n, float c,
                          hipStream_t s);
-hipError_t launch_fill_route(int *ids, float *w, int n, hipStream_t s);
+// a[t * n + i] = SwiGLU(h[t * 2n + i], h[t * 2n + n + i]) (gate and up side
+// by side per token, as launch_gemv_pair writes them).
+hipError_t launch_swiglu_pair(const float *h, float *a, int n_tok, int n, float c, hipStream_t s);
 
 // q8_int8.hip: the Q8_0 int8-activation path. launch_q8_quantize writes
 // xq [n_tok x blocks x 32] int8 and scale [n_tok x blocks] (blocks =

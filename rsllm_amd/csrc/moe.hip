@@ -623,8 +623,8 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
 
 // ---- shared expert (apply_shared_expert, moe.rs:422-455) ---------------------
 // a[i] = silu(min(g[i], c)) * clamp(u[i], -c, c): apply_swiglu_clamp
-// (:515-531) then scalar::swiglu, for weights the routed-expert kernels do
-// not take (F32 blobs, gate and up of different formats).
+// (:515-531) then scalar::swiglu, on gate and up outputs kept apart
+// (k_swiglu) or side by side per token (k_swiglu_pair).
 __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ g,
                                                 const float *__restrict__ u,
                                                 float *__restrict__ a, size_t n, float c) {
@@ -639,20 +639,20 @@ hipError_t launch_swiglu(const float *g, const float *u, float *a, size_t n, flo
     return hipGetLastError();
 }
 
-// The routing table of one expert with weight 1 for every token, which runs
-// the shared expert through launch_moe.
-__global__ __launch_bounds__(256) void k_fill_route(int *__restrict__ ids, float *__restrict__ w,
-                                                    int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) {
-        ids[i] = 0;
-        w[i] = 1.0f;
-    }
+__global__ __launch_bounds__(256) void k_swiglu_pair(const float *__restrict__ h,
+                                                     float *__restrict__ a, size_t total, int n,
+                                                     float c) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const size_t t = i / (size_t)n, j = i - t * (size_t)n;
+    const float *ht = h + t * 2 * (size_t)n;
+    a[i] = swiglu_clamped(ht[j], ht[n + j], c);
 }
 
-hipError_t launch_fill_route(int *ids, float *w, int n, hipStream_t s) {
-    if (n <= 0) return hipSuccess;
-    k_fill_route<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(ids, w, n);
+hipError_t launch_swiglu_pair(const float *h, float *a, int n_tok, int n, float c, hipStream_t s) {
+    const size_t total = (size_t)n_tok * (size_t)n;
+    if (total == 0) return hipSuccess;
+    k_swiglu_pair<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(h, a, total, n, c);
     return hipGetLastError();
 }
 
