@@ -678,10 +678,19 @@ static hipError_t gemv1(const uint8_t *w, size_t w_bytes, const float *x, float 
     return gemv1_gpt_go<F, 16, 2>(w, w_bytes, x, y, sh, 1, cus, s);
 }
 
+// Wavefronts per workgroup of the batched kernel for BT tokens. Eight
+// tokens of a five-field x image (every format but Q8_0) take 8 wavefronts:
+// a 1024-thread workgroup caps a thread at 128 VGPRs, and eight tokens'
+// accumulators and x slices then spill to scratch (3-5x slower on MI355X).
+template <class F>
+constexpr int gemv1_batch_nw(int bt) {
+    return bt == 8 && F::kXF == 5 ? 8 : 16;
+}
+
 template <class F>
 static bool gemv1_fits_f(int in_dim, int bt) {
     return gemv1_lds_bytes<F>(in_dim, bt) <= kGemv1MaxLds &&
-           gemv1_gpt<F>(in_dim, bt == 1 ? 8 : 16, bt) != 0;
+           gemv1_gpt<F>(in_dim, bt == 1 ? 8 : gemv1_batch_nw<F>(bt), bt) != 0;
 }
 
 // Tokens the fused kernel takes as one batch (x of all of them in LDS):
@@ -692,8 +701,9 @@ static int gemv1_bt(int n_tok, int in_dim) {
     return bt && gemv1_fits_f<F>(in_dim, bt) ? bt : 0;
 }
 
-// 2..8 tokens: one 16-wavefront workgroup per CU, two tiles in flight
-// (sweeps of the C0-C2 shapes at 2, 4 and 8 tokens).
+// 2..8 tokens: one workgroup per CU, two tiles in flight, 16 wavefronts
+// (8 for gemv1_batch_nw's case); sweeps of the C0-C2 shapes at 2, 4 and 8
+// tokens.
 template <class F>
 static hipError_t gemv1_batch(const uint8_t *w, size_t w_bytes, const float *x, float *y,
                               const Gemv1Shape &sh, int n_tok, hipStream_t s) {
@@ -701,7 +711,8 @@ static hipError_t gemv1_batch(const uint8_t *w, size_t w_bytes, const float *x, 
     switch (gemv1_bt<F>(n_tok, sh.in_dim)) {
     case 2: return gemv1_gpt_go<F, 16, 2, 2>(w, w_bytes, x, y, sh, n_tok, cus, s);
     case 4: return gemv1_gpt_go<F, 16, 2, 4>(w, w_bytes, x, y, sh, n_tok, cus, s);
-    case 8: return gemv1_gpt_go<F, 16, 2, 8>(w, w_bytes, x, y, sh, n_tok, cus, s);
+    case 8:
+        return gemv1_gpt_go<F, gemv1_batch_nw<F>(8), 2, 8>(w, w_bytes, x, y, sh, n_tok, cus, s);
     default: return hipErrorInvalidValue;
     }
 }
