@@ -274,18 +274,16 @@ __global__ __launch_bounds__(256) void k_mf_x(const float *__restrict__ x, _Floa
 }
 
 // ---- GEMV ----------------------------------------------------------------------------
+// One workgroup's 16 * RT rows from row0 against the n_tok (<= 16 * NT)
+// token columns of xh, y[t * out_dim + o]; red: NK * RT * NT * 64 f32x4 of LDS.
 template <class F, int NT, int NK, int RT>
-__global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__ w, uint32_t w_bytes,
-                                                     const _Float16 *__restrict__ xh,
-                                                     uint32_t xh_bytes,
-                                                     const float *__restrict__ unscale,
-                                                     float *__restrict__ y, int n_tok, int in_dim,
-                                                     int out_dim) {
-    __shared__ f32x4 red[NK * RT * NT * 64];
+__device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t w_bytes,
+                                        const _Float16 *__restrict__ xh, uint32_t xh_bytes,
+                                        const float *__restrict__ unscale, float *__restrict__ y,
+                                        int n_tok, int in_dim, int out_dim, int row0, f32x4 *red) {
     constexpr int ntp = NT * 16;
     const int lane = threadIdx.x & 63, r16 = lane & 15, q = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int row0 = blockIdx.x * 16 * RT;
     const int nsteps = in_dim / kMfStep;
     const int s0 = nsteps * wv / NK, s1 = nsteps * (wv + 1) / NK;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
@@ -352,6 +350,144 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__
                 if (o + i < out_dim) yt[o + i] = v[i] * us;
         }
     }
+}
+
+template <class F, int NT, int NK, int RT>
+__global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__ w, uint32_t w_bytes,
+                                                     const _Float16 *__restrict__ xh,
+                                                     uint32_t xh_bytes,
+                                                     const float *__restrict__ unscale,
+                                                     float *__restrict__ y, int n_tok, int in_dim,
+                                                     int out_dim) {
+    __shared__ f32x4 red[NK * RT * NT * 64];
+    mf_rows<F, NT, NK, RT>(w, w_bytes, xh, xh_bytes, unscale, y, n_tok, in_dim, out_dim,
+                           blockIdx.x * 16 * RT, red);
+}
+
+// ---- routed experts grouped by expert (many tokens) --------------------------------
+// Slots sorted by expert (k_moe_route): expert e owns sorted slots [off[e],
+// off[e + 1]). k_mfg_batches cuts each expert's slots into batches of up to
+// kMfgBatch; a batch is the token set (the N dimension) of one pass of
+// mf_rows over that expert's rows, so each expert's weights are streamed once
+// per kMfgBatch of its slots. Batch b's activation image sits at
+// xh + b * in_dim * kMfgBatch (the k_mf_x layout with ntp = kMfgBatch) and
+// its scales at unscale + b * kMfgBatch; its rows go to y + first * out_dim.
+constexpr int kMfgBatch = 16;
+
+struct MfgBatch {
+    int first, count, expert, pad;
+};
+
+// Most batches P sorted slots over n_expert experts can form.
+static int mfg_max_batches(int n_pairs, int n_expert) {
+    return (n_pairs + kMfgBatch - 1) / kMfgBatch + (n_pairs < n_expert ? n_pairs : n_expert);
+}
+
+// One thread: experts in ascending order, batches in slot order.
+__global__ void k_mfg_batches(const int *__restrict__ off, int n_expert, MfgBatch *__restrict__ bat,
+                              int *__restrict__ n_bat) {
+    if (threadIdx.x != 0) return;
+    int nb = 0;
+    for (int e = 0; e < n_expert; e++) {
+        const int f0 = off[e], c = off[e + 1] - f0;
+        for (int f = 0; f < c; f += kMfgBatch)
+            bat[nb++] = MfgBatch{f0 + f, c - f < kMfgBatch ? c - f : kMfgBatch, e, 0};
+    }
+    *n_bat = nb;
+}
+
+// Activation image of batch blockIdx.y, token column blockIdx.x (the k_mf_x
+// conversion): row = x[tok[first + t]] (SWIGLU false) or the clamped SwiGLU
+// of rows first + t of hg, hu (SWIGLU true); columns past the batch's count
+// are zeros with unscale 0.
+template <class F, bool SWIGLU>
+__global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
+                                               const float *__restrict__ hu,
+                                               const int *__restrict__ tok,
+                                               const MfgBatch *__restrict__ bat,
+                                               const int *__restrict__ n_bat, float clamp,
+                                               _Float16 *__restrict__ xh,
+                                               float *__restrict__ unscale, int in_dim) {
+    __shared__ float red[4];
+    const int b = blockIdx.y, t = blockIdx.x, tid = threadIdx.x;
+    if (b >= *n_bat) return;
+    const MfgBatch bt = bat[b];
+    const bool real = t < bt.count;
+    const size_t row = real ? (SWIGLU ? (size_t)(bt.first + t) : (size_t)tok[bt.first + t]) : 0;
+    const float *xt = x + row * in_dim;
+    const float *ut = hu + (SWIGLU ? row * in_dim : 0);
+    auto val4 = [&](int i) {
+        float4 v = *reinterpret_cast<const float4 *>(xt + i);
+        if (SWIGLU) {
+            const float4 u = *reinterpret_cast<const float4 *>(ut + i);
+            v = make_float4(swiglu_clamped(v.x, u.x, clamp), swiglu_clamped(v.y, u.y, clamp),
+                            swiglu_clamped(v.z, u.z, clamp), swiglu_clamped(v.w, u.w, clamp));
+        }
+        return v;
+    };
+    const int nsteps = in_dim / kMfStep;
+    float amax = 0.f;
+    if (real)
+        for (int i = tid * 4; i < in_dim; i += 1024) {
+            const float4 v = val4(i);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (amax > 0.f && amax <= 3.4e38f) {
+        int ex;
+        frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
+        e = min(max(15 - ex, -126), 126);
+    }
+    const float up = ldexpf(1.0f, e);
+    float *us = unscale + (size_t)b * kMfgBatch;
+    _Float16 *xb = xh + (size_t)b * in_dim * kMfgBatch;
+    if (tid == 0) us[t] = real ? ldexpf(1.0f, -e) : 0.f;
+    for (int g = tid; g < nsteps * 16; g += 256) {
+        const int s = g >> 4, j = (g >> 2) & 3, q = g & 3;
+        uint4 o = make_uint4(0, 0, 0, 0);
+        if (real) {
+            const int i = F::elem(s, j, q);
+            const float4 v0 = val4(i), v1 = val4(i + 4);
+            f16x8 h;
+            h[0] = (_Float16)(v0.x * up); h[1] = (_Float16)(v0.y * up);
+            h[2] = (_Float16)(v0.z * up); h[3] = (_Float16)(v0.w * up);
+            h[4] = (_Float16)(v1.x * up); h[5] = (_Float16)(v1.y * up);
+            h[6] = (_Float16)(v1.z * up); h[7] = (_Float16)(v1.w * up);
+            o = __builtin_bit_cast(uint4, h);
+        }
+        *reinterpret_cast<uint4 *>(xb + ((size_t)g * kMfgBatch + t) * 8) = o;
+    }
+}
+
+// Grid (row blocks, batch slots, matrices): workgroup (x, b, m) computes
+// rows 16 RT x of W_m[expert(b)] = w_m + expert * w_stride for batch b's
+// slots into y_m. Batch slots past *n_bat exit at once.
+template <class F, int NK, int RT>
+__global__ __launch_bounds__(64 * NK) void k_gemv_mfg(const uint8_t *__restrict__ w0,
+                                                      const uint8_t *__restrict__ w1,
+                                                      size_t w_stride,
+                                                      const _Float16 *__restrict__ xh,
+                                                      const float *__restrict__ unscale,
+                                                      const MfgBatch *__restrict__ bat,
+                                                      const int *__restrict__ n_bat,
+                                                      float *__restrict__ y0, float *__restrict__ y1,
+                                                      int in_dim, int out_dim) {
+    __shared__ f32x4 red[NK * RT * (kMfgBatch / 16) * 64];
+    const int b = blockIdx.y;
+    if (b >= *n_bat) return;
+    const MfgBatch bt = bat[b];
+    const bool m1 = blockIdx.z != 0;
+    const uint8_t *w = (m1 ? w1 : w0) + (size_t)bt.expert * w_stride;
+    float *y = (m1 ? y1 : y0) + (size_t)bt.first * out_dim;
+    const size_t img = (size_t)in_dim * kMfgBatch;
+    mf_rows<F, kMfgBatch / 16, NK, RT>(w, (uint32_t)w_stride, xh + b * img, (uint32_t)(img * 2),
+                                       unscale + (size_t)b * kMfgBatch, y, bt.count, in_dim,
+                                       out_dim, blockIdx.x * 16 * RT, red);
 }
 
 // ---- fused batched GEMV: activations converted into LDS ------------------------------
@@ -614,6 +750,85 @@ static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, 
         return mfb_xp_go<F, 16, 2>(w, w_bytes, x, y, n_tok, in_dim, out_dim, cus, s);
     if (n_tok <= 16) return mf_go<F, 1, 8, 1>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
     return mf_go<F, 2, 8, 1>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
+}
+
+// Both GEMVs' outputs at least 1024 rows, as gemv_mfma_supported asks (the
+// f16 roundings of the gate/up and down passes add up: C3 measures 6e-4 at
+// 8 tokens).
+bool moe_mfma_supported(uint32_t dt_gu, uint32_t dt_d, int n_embd, int n_ff) {
+    auto ok = [](uint32_t d) { return d == T_Q4_K || d == T_Q6_K || d == T_Q8_0; };
+    return ok(dt_gu) && ok(dt_d) && n_embd >= 1024 && n_ff >= 1024 && n_embd % 256 == 0 &&
+           n_ff % 256 == 0;
+}
+
+size_t moe_mfma_scratch_bytes(int n_pairs, int n_expert, int n_embd, int n_ff) {
+    const size_t nb = (size_t)mfg_max_batches(n_pairs, n_expert);
+    auto al = [](size_t n) { return (n + 255) / 256 * 256; };
+    return al(nb * sizeof(MfgBatch)) + al(4) + al(nb * kMfgBatch * (size_t)n_embd * 2) +
+           al(nb * kMfgBatch * 4) + al(nb * kMfgBatch * (size_t)n_ff * 2) + al(nb * kMfgBatch * 4);
+}
+
+template <class F>
+static hipError_t mfg_pass(const uint8_t *w0, const uint8_t *w1, size_t w_stride, const float *x,
+                           const float *hu, const int *tok, const MfgBatch *bat, const int *n_bat,
+                           int max_b, float clamp, _Float16 *xh, float *us, float *y0, float *y1,
+                           int in_dim, int out_dim, hipStream_t s) {
+    const dim3 gx(kMfgBatch, (unsigned)max_b);
+    if (hu)
+        k_mfg_x<F, true><<<gx, 256, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim);
+    else
+        k_mfg_x<F, false><<<gx, 256, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    constexpr int NK = 4, RT = 4;
+    const dim3 g((unsigned)((out_dim + 16 * RT - 1) / (16 * RT)), (unsigned)max_b, w1 ? 2u : 1u);
+    k_gemv_mfg<F, NK, RT><<<g, 64 * NK, 0, s>>>(w0, w1, w_stride, xh, us, bat, n_bat, y0, y1,
+                                                in_dim, out_dim);
+    return hipGetLastError();
+}
+
+static hipError_t mfg_pass_dt(uint32_t dt, const uint8_t *w0, const uint8_t *w1, size_t w_stride,
+                              const float *x, const float *hu, const int *tok, const MfgBatch *bat,
+                              const int *n_bat, int max_b, float clamp, _Float16 *xh, float *us,
+                              float *y0, float *y1, int in_dim, int out_dim, hipStream_t s) {
+#define MFG(F) mfg_pass<F>(w0, w1, w_stride, x, hu, tok, bat, n_bat, max_b, clamp, xh, us, y0, y1, in_dim, out_dim, s)
+    switch (dt) {
+    case T_Q4_K: return MFG(MQ4K);
+    case T_Q6_K: return MFG(MQ6K);
+    case T_Q8_0: return MFG(MQ8);
+    default: return hipErrorInvalidValue;
+    }
+#undef MFG
+}
+
+hipError_t launch_moe_mfma(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
+                           const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
+                           const int *off, const int *slot_tok, int n_pairs, int n_expert,
+                           float *hg, float *hu, float *yd, uint8_t *scratch, int n_embd, int n_ff,
+                           float clamp, hipStream_t s) {
+    if (!moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff)) return hipErrorInvalidValue;
+    if (gu_stride > 0xFFFFFFFFu || d_stride > 0xFFFFFFFFu) return hipErrorInvalidValue;
+    const int max_b = mfg_max_batches(n_pairs, n_expert);
+    uint8_t *p = scratch;
+    auto take = [&](size_t n) {
+        uint8_t *r = p;
+        p += (n + 255) / 256 * 256;
+        return r;
+    };
+    MfgBatch *bat = reinterpret_cast<MfgBatch *>(take((size_t)max_b * sizeof(MfgBatch)));
+    int *n_bat = reinterpret_cast<int *>(take(4));
+    _Float16 *xh1 = reinterpret_cast<_Float16 *>(take((size_t)max_b * kMfgBatch * n_embd * 2));
+    float *us1 = reinterpret_cast<float *>(take((size_t)max_b * kMfgBatch * 4));
+    _Float16 *xh2 = reinterpret_cast<_Float16 *>(take((size_t)max_b * kMfgBatch * n_ff * 2));
+    float *us2 = reinterpret_cast<float *>(take((size_t)max_b * kMfgBatch * 4));
+    k_mfg_batches<<<1, 64, 0, s>>>(off, n_expert, bat, n_bat);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if ((e = mfg_pass_dt(dt_gu, gate, up, gu_stride, x, nullptr, slot_tok, bat, n_bat, max_b, 0.f,
+                         xh1, us1, hg, hu, n_embd, n_ff, s)) != hipSuccess)
+        return e;
+    return mfg_pass_dt(dt_d, down, nullptr, d_stride, hg, hu, nullptr, bat, n_bat, max_b, clamp,
+                       xh2, us2, yd, nullptr, n_ff, n_embd, s);
 }
 
 hipError_t launch_gemv_mfma(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,

@@ -124,6 +124,21 @@ hipError_t launch_quantize_swiglu(uint32_t dtype, const float *hg, const float *
                                   uint8_t *xq, int n_rows, int n, const int *off, int n_expert,
                                   hipStream_t s);
 
+// gemv_mfma.hip, routed experts on the matrix cores (Q4_K, Q6_K and Q8_0;
+// n_embd and n_ff multiples of 256). Slots sorted by expert as
+// launch_gemv_grouped's (off: n_expert + 1 entries on the device, slot_tok:
+// the token of each sorted slot, n_pairs = n_tok * k bounding the slot
+// count). Writes hg, hu [slot x n_ff] (gate and up of x[slot_tok[slot]])
+// and yd [slot x n_embd] (down of the clamped SwiGLU of hg, hu). `scratch`
+// holds moe_mfma_scratch_bytes(n_pairs, n_expert, n_embd, n_ff) bytes.
+bool moe_mfma_supported(uint32_t dt_gu, uint32_t dt_d, int n_embd, int n_ff);
+size_t moe_mfma_scratch_bytes(int n_pairs, int n_expert, int n_embd, int n_ff);
+hipError_t launch_moe_mfma(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
+                           const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
+                           const int *off, const int *slot_tok, int n_pairs, int n_expert,
+                           float *hg, float *hu, float *yd, uint8_t *scratch, int n_embd, int n_ff,
+                           float clamp, hipStream_t s);
+
 // prefill.hip: out[t, o] = sum_i deq(W)[o, i] * x[t, i] for a raw GGUF Q4_K
 // weight W [out_dim x in_dim] and bf16 activations x [n_tok x in_dim]
 // (n_tok x out_dim fp32 output, overwritten). `scratch` holds

@@ -8,7 +8,9 @@
 // re-reading each selected expert's weights once per token. Here the
 // (token, slot) pairs are grouped by expert on the device, and each expert's
 // gate/up and down matrices are streamed once per batch of up to 4 of its
-// tokens (grouped GEMV, gemv.hip):
+// tokens (grouped GEMV, gemv.hip; for Q4_K, Q6_K and Q8_0 from
+// kMoeMfmaMinTok tokens, batches of up to 16 on the matrix cores instead,
+// launch_moe_mfma in gemv_mfma.hip, steps 2-6 there):
 //   1. k_moe_route: slots sorted by expert (ties in (t, i) order), per-expert
 //      offsets, slot -> token, (t, i) -> slot, the list of active experts;
 //      slots with w == 0 are skipped (moe.rs:681-683).
@@ -552,8 +554,19 @@ size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_
     add(P * n_ff * 4);                                    // hu
     add(gemv_scratch_bytes(dt_d, (int)P, n_ff));          // SwiGLU limbs
     add(P * n_embd * 4);                                  // yd
+    if (moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff))
+        add(moe_mfma_scratch_bytes((int)P, n_expert, n_embd, n_ff));
     return b;
 }
+
+// Calls the fused pair does not take in one go run, from this many tokens,
+// grouped by expert on the matrix cores (formats moe_mfma_supported takes):
+// each expert's weights are streamed once per batch of up to 16 of its
+// slots, where the fused pair over token chunks streams them once per chunk
+// that routes to the expert. C3 (64 experts, top-8) on MI355X: 411 vs 401 us
+// at 8 tokens, 537 vs 741 us at 16, 596 vs 1492 us at 32; below 8 tokens the
+// chunks are faster (276 vs 226 us at 4).
+constexpr int kMoeMfmaMinTok = 8;
 
 hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
                       const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
@@ -579,7 +592,25 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
     const size_t xq2_bytes = gemv_scratch_bytes(dt_d, (int)P, n_ff);
     uint8_t *xq2 = take(xq2_bytes);
     float *yd = reinterpret_cast<float *>(take(P * n_embd * 4));
-    if (moe_fused_fits(dt_gu, dt_d, n_tok, k, n_embd, n_ff, gu_stride, d_stride))
+    const bool fused1 = moe_fused_fits(dt_gu, dt_d, n_tok, k, n_embd, n_ff, gu_stride, d_stride);
+    const bool mfma = !fused1 && moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff) &&
+                      n_tok >= kMoeMfmaMinTok && gu_stride <= 0xFFFFFFFFu &&
+                      d_stride <= 0xFFFFFFFFu && P <= (size_t)1 << 20;
+    if (mfma) {
+        uint8_t *mscratch = take(moe_mfma_scratch_bytes((int)P, n_expert, n_embd, n_ff));
+        k_moe_route<<<1, 256, (size_t)(n_expert + 1 + P) * 4, s>>>(
+            ids, wts, (int)P, k, n_expert, off, slot_tok, slot_of, act, n_act);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        if ((e = launch_moe_mfma(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x, off,
+                                 slot_tok, (int)P, n_expert, hg, hu, yd, mscratch, n_embd, n_ff,
+                                 clamp, s)) != hipSuccess)
+            return e;
+        k_moe_accumulate<<<(unsigned)(((size_t)n_tok * n_embd + 255) / 256), 256, 0, s>>>(
+            out, yd, wts, slot_of, n_tok, k, n_embd);
+        return hipGetLastError();
+    }
+    if (fused1)
         return moe_fused(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x, ids, wts, out, hg,
                          n_tok, k, n_expert, n_embd, n_ff, clamp, s);
     // More tokens than the fused pair takes: the fused pair over token

@@ -168,3 +168,30 @@ def test_moe_fused_rows_spanning_columns(oracle, hip, dt_gu, dt_d, n_embd, n_ff,
     hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
                    dt_gu, dt_d, 10.0)
     assert rel_err(got, want) <= REL_TOL
+
+
+@pytest.mark.parametrize("dt_gu,dt_d", [(G.Q4_K, G.Q6_K), (G.Q8_0, G.Q4_K), (G.Q6_K, G.Q8_0),
+                                        (G.Q2_K, G.Q4_0)])
+@pytest.mark.parametrize("n_tok,k", [(40, 2), (5, 8), (9, 8)])
+def test_moe_grouped_many_tokens(oracle, hip, dt_gu, dt_d, n_tok, k):
+    """Calls the fused pair does not take in one go run grouped by expert:
+    on the matrix cores for Q4_K / Q6_K / Q8_0 from 8 tokens (each expert's
+    slots in batches of up to 16), through the int8-limb grouped GEMV for
+    the other formats and fewer tokens. Every token's first pick is expert
+    0 (40 slots: three batches, the last partial), token 1 picks one expert
+    twice and one slot has weight 0."""
+    n_embd, n_ff, n_expert = 1024, 1024, 9
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, dt_gu, dt_d,
+                                          500 + n_tok + k)
+    ids[:, 0] = 0
+    ids[1, 1] = ids[1, 0]
+    w[3, 1] = 0.0
+    base = synth.activations(n_tok, n_embd, 9).reshape(-1)
+    want = run_oracle(oracle, base, x, gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                      dt_gu, dt_d)
+    got = base.copy()
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   dt_gu, dt_d, 10.0)
+    err = rel_err(got - base, want - base)
+    print(f"moe grouped {dt_gu.name}/{dt_d.name} T={n_tok} k={k}: rel err {err:.3e}")
+    assert err <= REL_TOL
