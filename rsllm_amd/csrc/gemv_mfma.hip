@@ -748,6 +748,15 @@ static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, 
     if (n_tok <= 8 && out_dim >= 8192 && mfb_xp(n_tok, in_dim, 16) != 0 &&
         mfb_lds_bytes<F>(n_tok, in_dim, out_dim, cus, 16) <= kMfbMaxLds)
         return mfb_xp_go<F, 16, 2>(w, w_bytes, x, y, n_tok, in_dim, out_dim, cus, s);
+    // Every workgroup reads the whole activation image, so more rows per
+    // workgroup read it fewer times; 4 row tiles (4 wavefronts over K) where
+    // that still leaves 224 or more workgroups (C1 14336 x 4096 Q4_K: 20.6 vs
+    // 23.7 us at 16 tokens, 23.4 vs 28.3 us at 32), one row tile over 8
+    // wavefronts otherwise (4096-row matrices take 1.4-2x longer with 4).
+    if (out_dim >= 224 * 64) {
+        if (n_tok <= 16) return mf_go<F, 1, 4, 4>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
+        return mf_go<F, 2, 4, 4>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
+    }
     if (n_tok <= 16) return mf_go<F, 1, 8, 1>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
     return mf_go<F, 2, 8, 1>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
 }
