@@ -366,40 +366,18 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__
 
 // ---- routed experts grouped by expert (many tokens) --------------------------------
 // Slots sorted by expert (k_moe_route): expert e owns sorted slots [off[e],
-// off[e + 1]). k_mfg_batches cuts each expert's slots into batches of up to
-// kMfgBatch; a batch is the token set (the N dimension) of one pass of
-// mf_rows over that expert's rows, so each expert's weights are streamed once
-// per kMfgBatch of its slots. Batch b's activation image sits at
+// off[e + 1]), cut into batches of up to kMfgBatch (k_moe_route lists them);
+// a batch is the token set (the N dimension) of one pass of mf_rows over
+// that expert's rows, so each expert's weights are streamed once per
+// kMfgBatch of its slots. Batch b's activation image sits at
 // xh + b * in_dim * kMfgBatch (the k_mf_x layout with ntp = kMfgBatch) and
 // its scales at unscale + b * kMfgBatch; its rows go to y + first * out_dim.
-constexpr int kMfgBatch = 16;
-
-struct MfgBatch {
-    int first, count, expert, pad;
-};
-
-// Most batches P sorted slots over n_expert experts can form.
-static int mfg_max_batches(int n_pairs, int n_expert) {
-    return (n_pairs + kMfgBatch - 1) / kMfgBatch + (n_pairs < n_expert ? n_pairs : n_expert);
-}
-
-// One thread: experts in ascending order, batches in slot order.
-__global__ void k_mfg_batches(const int *__restrict__ off, int n_expert, MfgBatch *__restrict__ bat,
-                              int *__restrict__ n_bat) {
-    if (threadIdx.x != 0) return;
-    int nb = 0;
-    for (int e = 0; e < n_expert; e++) {
-        const int f0 = off[e], c = off[e + 1] - f0;
-        for (int f = 0; f < c; f += kMfgBatch)
-            bat[nb++] = MfgBatch{f0 + f, c - f < kMfgBatch ? c - f : kMfgBatch, e, 0};
-    }
-    *n_bat = nb;
-}
 
 // Activation image of batch blockIdx.y, token column blockIdx.x (the k_mf_x
 // conversion): row = x[tok[first + t]] (SWIGLU false) or the clamped SwiGLU
-// of rows first + t of hg, hu (SWIGLU true); columns past the batch's count
-// are zeros with unscale 0.
+// of rows first + t of hg, hu (SWIGLU true). Columns past the batch's count
+// are left as they are: column t of an MFMA's B operand reaches only column
+// t of its result, and those outputs are not stored.
 template <class F, bool SWIGLU>
 __global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
                                                const float *__restrict__ hu,
@@ -412,8 +390,8 @@ __global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
     const int b = blockIdx.y, t = blockIdx.x, tid = threadIdx.x;
     if (b >= *n_bat) return;
     const MfgBatch bt = bat[b];
-    const bool real = t < bt.count;
-    const size_t row = real ? (SWIGLU ? (size_t)(bt.first + t) : (size_t)tok[bt.first + t]) : 0;
+    if (t >= bt.count) return;
+    const size_t row = SWIGLU ? (size_t)(bt.first + t) : (size_t)tok[bt.first + t];
     const float *xt = x + row * in_dim;
     const float *ut = hu + (SWIGLU ? row * in_dim : 0);
     auto val4 = [&](int i) {
@@ -427,11 +405,10 @@ __global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
     };
     const int nsteps = in_dim / kMfStep;
     float amax = 0.f;
-    if (real)
-        for (int i = tid * 4; i < in_dim; i += 1024) {
-            const float4 v = val4(i);
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        }
+    for (int i = tid * 4; i < in_dim; i += 1024) {
+        const float4 v = val4(i);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
     if ((tid & 63) == 0) red[tid >> 6] = amax;
@@ -446,21 +423,17 @@ __global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
     const float up = ldexpf(1.0f, e);
     float *us = unscale + (size_t)b * kMfgBatch;
     _Float16 *xb = xh + (size_t)b * in_dim * kMfgBatch;
-    if (tid == 0) us[t] = real ? ldexpf(1.0f, -e) : 0.f;
+    if (tid == 0) us[t] = ldexpf(1.0f, -e);
     for (int g = tid; g < nsteps * 16; g += 256) {
         const int s = g >> 4, j = (g >> 2) & 3, q = g & 3;
-        uint4 o = make_uint4(0, 0, 0, 0);
-        if (real) {
-            const int i = F::elem(s, j, q);
-            const float4 v0 = val4(i), v1 = val4(i + 4);
-            f16x8 h;
-            h[0] = (_Float16)(v0.x * up); h[1] = (_Float16)(v0.y * up);
-            h[2] = (_Float16)(v0.z * up); h[3] = (_Float16)(v0.w * up);
-            h[4] = (_Float16)(v1.x * up); h[5] = (_Float16)(v1.y * up);
-            h[6] = (_Float16)(v1.z * up); h[7] = (_Float16)(v1.w * up);
-            o = __builtin_bit_cast(uint4, h);
-        }
-        *reinterpret_cast<uint4 *>(xb + ((size_t)g * kMfgBatch + t) * 8) = o;
+        const int i = F::elem(s, j, q);
+        const float4 v0 = val4(i), v1 = val4(i + 4);
+        f16x8 h;
+        h[0] = (_Float16)(v0.x * up); h[1] = (_Float16)(v0.y * up);
+        h[2] = (_Float16)(v0.z * up); h[3] = (_Float16)(v0.w * up);
+        h[4] = (_Float16)(v1.x * up); h[5] = (_Float16)(v1.y * up);
+        h[6] = (_Float16)(v1.z * up); h[7] = (_Float16)(v1.w * up);
+        *reinterpret_cast<uint4 *>(xb + ((size_t)g * kMfgBatch + t) * 8) = __builtin_bit_cast(uint4, h);
     }
 }
 
@@ -773,7 +746,7 @@ bool moe_mfma_supported(uint32_t dt_gu, uint32_t dt_d, int n_embd, int n_ff) {
 size_t moe_mfma_scratch_bytes(int n_pairs, int n_expert, int n_embd, int n_ff) {
     const size_t nb = (size_t)mfg_max_batches(n_pairs, n_expert);
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
-    return al(nb * sizeof(MfgBatch)) + al(4) + al(nb * kMfgBatch * (size_t)n_embd * 2) +
+    return mfg_batch_bytes(n_pairs, n_expert) + al(nb * kMfgBatch * (size_t)n_embd * 2) +
            al(nb * kMfgBatch * 4) + al(nb * kMfgBatch * (size_t)n_ff * 2) + al(nb * kMfgBatch * 4);
 }
 
@@ -812,27 +785,23 @@ static hipError_t mfg_pass_dt(uint32_t dt, const uint8_t *w0, const uint8_t *w1,
 
 hipError_t launch_moe_mfma(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
                            const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
-                           const int *off, const int *slot_tok, int n_pairs, int n_expert,
-                           float *hg, float *hu, float *yd, uint8_t *scratch, int n_embd, int n_ff,
-                           float clamp, hipStream_t s) {
+                           const int *slot_tok, const MfgBatch *bat, const int *n_bat,
+                           int n_pairs, int n_expert, float *hg, float *hu, float *yd,
+                           uint8_t *scratch, int n_embd, int n_ff, float clamp, hipStream_t s) {
     if (!moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff)) return hipErrorInvalidValue;
     if (gu_stride > 0xFFFFFFFFu || d_stride > 0xFFFFFFFFu) return hipErrorInvalidValue;
     const int max_b = mfg_max_batches(n_pairs, n_expert);
-    uint8_t *p = scratch;
+    uint8_t *p = scratch + mfg_batch_bytes(n_pairs, n_expert);
     auto take = [&](size_t n) {
         uint8_t *r = p;
         p += (n + 255) / 256 * 256;
         return r;
     };
-    MfgBatch *bat = reinterpret_cast<MfgBatch *>(take((size_t)max_b * sizeof(MfgBatch)));
-    int *n_bat = reinterpret_cast<int *>(take(4));
     _Float16 *xh1 = reinterpret_cast<_Float16 *>(take((size_t)max_b * kMfgBatch * n_embd * 2));
     float *us1 = reinterpret_cast<float *>(take((size_t)max_b * kMfgBatch * 4));
     _Float16 *xh2 = reinterpret_cast<_Float16 *>(take((size_t)max_b * kMfgBatch * n_ff * 2));
     float *us2 = reinterpret_cast<float *>(take((size_t)max_b * kMfgBatch * 4));
-    k_mfg_batches<<<1, 64, 0, s>>>(off, n_expert, bat, n_bat);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    hipError_t e;
     if ((e = mfg_pass_dt(dt_gu, gate, up, gu_stride, x, nullptr, slot_tok, bat, n_bat, max_b, 0.f,
                          xh1, us1, hg, hu, n_embd, n_ff, s)) != hipSuccess)
         return e;

@@ -131,13 +131,28 @@ hipError_t launch_quantize_swiglu(uint32_t dtype, const float *hg, const float *
 // count). Writes hg, hu [slot x n_ff] (gate and up of x[slot_tok[slot]])
 // and yd [slot x n_embd] (down of the clamped SwiGLU of hg, hu). `scratch`
 // holds moe_mfma_scratch_bytes(n_pairs, n_expert, n_embd, n_ff) bytes.
+// The batches: each active expert's sorted slots cut into runs of up to
+// kMfgBatch (experts ascending, runs in slot order), *n_bat of them, as
+// k_moe_route lists them; at most mfg_max_batches(n_pairs, n_expert).
+// `scratch` holds moe_mfma_scratch_bytes(...) bytes: the batch list and its
+// count first (mfg_batch_bytes), then the activation images.
+constexpr int kMfgBatch = 16;
+struct MfgBatch {
+    int first, count, expert, pad;
+};
+inline int mfg_max_batches(int n_pairs, int n_expert) {
+    return (n_pairs + kMfgBatch - 1) / kMfgBatch + (n_pairs < n_expert ? n_pairs : n_expert);
+}
+inline size_t mfg_batch_bytes(int n_pairs, int n_expert) {
+    return ((size_t)mfg_max_batches(n_pairs, n_expert) * sizeof(MfgBatch) + 255) / 256 * 256 + 256;
+}
 bool moe_mfma_supported(uint32_t dt_gu, uint32_t dt_d, int n_embd, int n_ff);
 size_t moe_mfma_scratch_bytes(int n_pairs, int n_expert, int n_embd, int n_ff);
 hipError_t launch_moe_mfma(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
                            const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
-                           const int *off, const int *slot_tok, int n_pairs, int n_expert,
-                           float *hg, float *hu, float *yd, uint8_t *scratch, int n_embd, int n_ff,
-                           float clamp, hipStream_t s);
+                           const int *slot_tok, const MfgBatch *bat, const int *n_bat,
+                           int n_pairs, int n_expert, float *hg, float *hu, float *yd,
+                           uint8_t *scratch, int n_embd, int n_ff, float clamp, hipStream_t s);
 
 // prefill.hip: out[t, o] = sum_i deq(W)[o, i] * x[t, i] for a raw GGUF Q4_K
 // weight W [out_dim x in_dim] and bf16 activations x [n_tok x in_dim]

@@ -28,13 +28,16 @@ namespace rsllm_hip {
 // One workgroup. ids and weights are cached in LDS; a slot's rank inside its
 // expert is the number of earlier valid slots with the same expert
 // (deterministic order). Also lists the experts with at least one slot, in
-// ascending order (act, count in *n_act), for the grouped GEMV grids.
+// ascending order (act, count in *n_act), for the grouped GEMV grids, and,
+// when bat is given, the matrix-core batches (MfgBatch, count in *n_bat).
 __global__ __launch_bounds__(256) void k_moe_route(const int *__restrict__ ids,
                                                    const float *__restrict__ wts, int n_pairs,
                                                    int k, int n_expert, int *__restrict__ off,
                                                    int *__restrict__ slot_tok,
                                                    int *__restrict__ slot_of,
-                                                   int *__restrict__ act, int *__restrict__ n_act) {
+                                                   int *__restrict__ act, int *__restrict__ n_act,
+                                                   MfgBatch *__restrict__ bat,
+                                                   int *__restrict__ n_bat) {
     extern __shared__ int lds[];
     int *cnt = lds;                     // n_expert + 1
     int *eid = lds + n_expert + 1;      // n_pairs: expert id, or -1 for a skipped slot
@@ -49,16 +52,20 @@ __global__ __launch_bounds__(256) void k_moe_route(const int *__restrict__ ids,
     }
     __syncthreads();
     if (tid == 0) {
-        int run = 0, na = 0;
+        int run = 0, na = 0, nb = 0;
         for (int e = 0; e < n_expert; e++) {
             const int c = cnt[e];
             cnt[e] = run;
             off[e] = run;
             if (c) act[na++] = e;
+            if (bat)
+                for (int f = 0; f < c; f += kMfgBatch)
+                    bat[nb++] = MfgBatch{run + f, c - f < kMfgBatch ? c - f : kMfgBatch, e, 0};
             run += c;
         }
         off[n_expert] = run;
         *n_act = na;
+        if (bat) *n_bat = nb;
     }
     __syncthreads();
     for (int p = tid; p < n_pairs; p += 256) {
@@ -598,12 +605,14 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
                       d_stride <= 0xFFFFFFFFu && P <= (size_t)1 << 20;
     if (mfma) {
         uint8_t *mscratch = take(moe_mfma_scratch_bytes((int)P, n_expert, n_embd, n_ff));
+        MfgBatch *bat = reinterpret_cast<MfgBatch *>(mscratch);
+        int *n_bat = reinterpret_cast<int *>(mscratch + mfg_batch_bytes((int)P, n_expert) - 256);
         k_moe_route<<<1, 256, (size_t)(n_expert + 1 + P) * 4, s>>>(
-            ids, wts, (int)P, k, n_expert, off, slot_tok, slot_of, act, n_act);
+            ids, wts, (int)P, k, n_expert, off, slot_tok, slot_of, act, n_act, bat, n_bat);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        if ((e = launch_moe_mfma(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x, off,
-                                 slot_tok, (int)P, n_expert, hg, hu, yd, mscratch, n_embd, n_ff,
+        if ((e = launch_moe_mfma(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x, slot_tok,
+                                 bat, n_bat, (int)P, n_expert, hg, hu, yd, mscratch, n_embd, n_ff,
                                  clamp, s)) != hipSuccess)
             return e;
         k_moe_accumulate<<<(unsigned)(((size_t)n_tok * n_embd + 255) / 256), 256, 0, s>>>(
@@ -633,8 +642,8 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
     // at most min(n_expert, n_tok * k) experts are active
     const int grid_experts = (int)(P < (size_t)n_expert ? P : (size_t)n_expert);
 
-    k_moe_route<<<1, 256, (size_t)(n_expert + 1 + P) * 4, s>>>(ids, wts, (int)P, k, n_expert, off,
-                                                               slot_tok, slot_of, act, n_act);
+    k_moe_route<<<1, 256, (size_t)(n_expert + 1 + P) * 4, s>>>(
+        ids, wts, (int)P, k, n_expert, off, slot_tok, slot_of, act, n_act, nullptr, nullptr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if ((e = launch_quantize_x(dt_gu, x, xq1, n_tok, n_embd, s)) != hipSuccess) return e;
