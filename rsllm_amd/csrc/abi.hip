@@ -377,6 +377,17 @@ int lora_down_compute(float *out, size_t out_len, const uint8_t *w, size_t strid
         return ok();
     }
     hipError_t e = hipErrorNotSupported;
+    // 9 or more tokens of the matrix-core formats: one pass over the stacked
+    // matrix per 16 tokens, on the matrix cores
+    if (!group_layout && lora_mfma_supported(dtype, T, D, G, R)) {
+        ThreadCtx &c = t_ctx;
+        HIP_TRY(c.xq.ensure(lora_mfma_scratch_bytes(T, D, G)), "hipMalloc");
+        e = launch_lora_mfma(dtype, w, stride * n_groups, x, tin, out, tout, (uint8_t *)c.xq.p, T,
+                             D, G, R, s);
+        if (e == hipSuccess) return ok();
+        if (e != hipErrorNotSupported) return dev_err(e, "lora_mfma");
+        (void)hipGetLastError();
+    }
     if (!group_layout) {
         e = launch_gemv_rows(dtype, w, stride * n_groups, x, out, T, D, tout, tin, tin, tout, R, s);
         if (e == hipSuccess) return ok();

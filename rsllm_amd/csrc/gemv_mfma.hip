@@ -275,12 +275,13 @@ __global__ __launch_bounds__(256) void k_mf_x(const float *__restrict__ x, _Floa
 
 // ---- GEMV ----------------------------------------------------------------------------
 // One workgroup's 16 * RT rows from row0 against the n_tok (<= 16 * NT)
-// token columns of xh, y[t * out_dim + o]; red: NK * RT * NT * 64 f32x4 of LDS.
+// token columns of xh, y[t * y_stride + o]; red: NK * RT * NT * 64 f32x4 of LDS.
 template <class F, int NT, int NK, int RT>
 __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t w_bytes,
                                         const _Float16 *__restrict__ xh, uint32_t xh_bytes,
                                         const float *__restrict__ unscale, float *__restrict__ y,
-                                        int n_tok, int in_dim, int out_dim, int row0, f32x4 *red) {
+                                        int n_tok, int in_dim, int out_dim, int y_stride, int row0,
+                                        f32x4 *red) {
     constexpr int ntp = NT * 16;
     const int lane = threadIdx.x & 63, r16 = lane & 15, q = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -344,7 +345,7 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
         const int o = row0 + 16 * rt + 4 * (ln >> 4);  // D rows 4 (lane / 16) + 0..3
         if (t < n_tok) {
             const float us = unscale[t];
-            float *yt = y + (size_t)t * out_dim;
+            float *yt = y + (size_t)t * y_stride;
 #pragma unroll
             for (int i = 0; i < 4; i++)
                 if (o + i < out_dim) yt[o + i] = v[i] * us;
@@ -360,7 +361,7 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__
                                                      float *__restrict__ y, int n_tok, int in_dim,
                                                      int out_dim) {
     __shared__ f32x4 red[NK * RT * NT * 64];
-    mf_rows<F, NT, NK, RT>(w, w_bytes, xh, xh_bytes, unscale, y, n_tok, in_dim, out_dim,
+    mf_rows<F, NT, NK, RT>(w, w_bytes, xh, xh_bytes, unscale, y, n_tok, in_dim, out_dim, out_dim,
                            blockIdx.x * 16 * RT, red);
 }
 
@@ -373,36 +374,14 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__
 // xh + b * in_dim * kMfgBatch (the k_mf_x layout with ntp = kMfgBatch) and
 // its scales at unscale + b * kMfgBatch; its rows go to y + first * out_dim.
 
-// Activation image of batch blockIdx.y, token column blockIdx.x (the k_mf_x
-// conversion): row = x[tok[first + t]] (SWIGLU false) or the clamped SwiGLU
-// of rows first + t of hg, hu (SWIGLU true). Columns past the batch's count
-// are left as they are: column t of an MFMA's B operand reaches only column
-// t of its result, and those outputs are not stored.
-template <class F, bool SWIGLU>
-__global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
-                                               const float *__restrict__ hu,
-                                               const int *__restrict__ tok,
-                                               const MfgBatch *__restrict__ bat,
-                                               const int *__restrict__ n_bat, float clamp,
-                                               _Float16 *__restrict__ xh,
-                                               float *__restrict__ unscale, int in_dim) {
+// One token column of a kMfgBatch-wide activation image (the k_mf_x
+// conversion, one workgroup of 256 threads): val4(i) gives elements
+// i .. i + 3 of the column's row; the column's pieces go to xb, 2^-e to *us.
+template <class F, class V>
+__device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 *__restrict__ xb,
+                                            float *__restrict__ us) {
     __shared__ float red[4];
-    const int b = blockIdx.y, t = blockIdx.x, tid = threadIdx.x;
-    if (b >= *n_bat) return;
-    const MfgBatch bt = bat[b];
-    if (t >= bt.count) return;
-    const size_t row = SWIGLU ? (size_t)(bt.first + t) : (size_t)tok[bt.first + t];
-    const float *xt = x + row * in_dim;
-    const float *ut = hu + (SWIGLU ? row * in_dim : 0);
-    auto val4 = [&](int i) {
-        float4 v = *reinterpret_cast<const float4 *>(xt + i);
-        if (SWIGLU) {
-            const float4 u = *reinterpret_cast<const float4 *>(ut + i);
-            v = make_float4(swiglu_clamped(v.x, u.x, clamp), swiglu_clamped(v.y, u.y, clamp),
-                            swiglu_clamped(v.z, u.z, clamp), swiglu_clamped(v.w, u.w, clamp));
-        }
-        return v;
-    };
+    const int tid = threadIdx.x;
     const int nsteps = in_dim / kMfStep;
     float amax = 0.f;
     for (int i = tid * 4; i < in_dim; i += 1024) {
@@ -421,9 +400,7 @@ __global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
         e = min(max(15 - ex, -126), 126);
     }
     const float up = ldexpf(1.0f, e);
-    float *us = unscale + (size_t)b * kMfgBatch;
-    _Float16 *xb = xh + (size_t)b * in_dim * kMfgBatch;
-    if (tid == 0) us[t] = ldexpf(1.0f, -e);
+    if (tid == 0) *us = ldexpf(1.0f, -e);
     for (int g = tid; g < nsteps * 16; g += 256) {
         const int s = g >> 4, j = (g >> 2) & 3, q = g & 3;
         const int i = F::elem(s, j, q);
@@ -435,6 +412,75 @@ __global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
         h[6] = (_Float16)(v1.z * up); h[7] = (_Float16)(v1.w * up);
         *reinterpret_cast<uint4 *>(xb + ((size_t)g * kMfgBatch + t) * 8) = __builtin_bit_cast(uint4, h);
     }
+}
+
+// Activation image of batch blockIdx.y, token column blockIdx.x: row =
+// x[tok[first + t]] (SWIGLU false) or the clamped SwiGLU of rows first + t
+// of hg, hu (SWIGLU true). Columns past the batch's count are left as they
+// are: column t of an MFMA's B operand reaches only column t of its result,
+// and those outputs are not stored.
+template <class F, bool SWIGLU>
+__global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
+                                               const float *__restrict__ hu,
+                                               const int *__restrict__ tok,
+                                               const MfgBatch *__restrict__ bat,
+                                               const int *__restrict__ n_bat, float clamp,
+                                               _Float16 *__restrict__ xh,
+                                               float *__restrict__ unscale, int in_dim) {
+    const int b = blockIdx.y, t = blockIdx.x;
+    if (b >= *n_bat) return;
+    const MfgBatch bt = bat[b];
+    if (t >= bt.count) return;
+    const size_t row = SWIGLU ? (size_t)(bt.first + t) : (size_t)tok[bt.first + t];
+    const float *xt = x + row * in_dim;
+    const float *ut = hu + (SWIGLU ? row * in_dim : 0);
+    auto val4 = [&](int i) {
+        float4 v = *reinterpret_cast<const float4 *>(xt + i);
+        if (SWIGLU) {
+            const float4 u = *reinterpret_cast<const float4 *>(ut + i);
+            v = make_float4(swiglu_clamped(v.x, u.x, clamp), swiglu_clamped(v.y, u.y, clamp),
+                            swiglu_clamped(v.z, u.z, clamp), swiglu_clamped(v.w, u.w, clamp));
+        }
+        return v;
+    };
+    mf_x_column<F>(val4, in_dim, t, xh + (size_t)b * in_dim * kMfgBatch,
+                   unscale + (size_t)b * kMfgBatch + t);
+}
+
+// ---- grouped LoRA-down on the matrix cores ----------------------------------------
+// One stacked matrix of G * R rows (device layout as one matrix); row r dots
+// group g = r / R's slice x[t * x_stride + g * D .. + D). Image (g, c) holds
+// tokens 16 c .. 16 c + 15 of group g's slice (kMfgBatch = 16 columns).
+template <class F>
+__global__ __launch_bounds__(256) void k_mfl_x(const float *__restrict__ x, int x_stride, int n_tok,
+                                               int D, int nchunks, _Float16 *__restrict__ xh,
+                                               float *__restrict__ unscale) {
+    const int b = blockIdx.y, g = b / nchunks, tc = (b - g * nchunks) * kMfgBatch + blockIdx.x;
+    if (tc >= n_tok) return;
+    const float *xt = x + (size_t)tc * x_stride + (size_t)g * D;
+    auto val4 = [&](int i) { return *reinterpret_cast<const float4 *>(xt + i); };
+    mf_x_column<F>(val4, D, blockIdx.x, xh + (size_t)b * D * kMfgBatch,
+                   unscale + (size_t)b * kMfgBatch + blockIdx.x);
+}
+
+// Grid (G R / 64, chunks): workgroup (x, c) computes rows 64 x .. 64 x + 63
+// (one group: R is a multiple of 64) for tokens 16 c .. into y[t * y_stride + row].
+template <class F>
+__global__ __launch_bounds__(256) void k_gemv_mfl(const uint8_t *__restrict__ w, uint32_t w_bytes,
+                                                  const _Float16 *__restrict__ xh,
+                                                  const float *__restrict__ unscale,
+                                                  float *__restrict__ y, int y_stride, int n_tok,
+                                                  int D, int R, int out_dim, int nchunks) {
+    constexpr int NK = 4, RT = 4;
+    __shared__ f32x4 red[NK * RT * (kMfgBatch / 16) * 64];
+    const int row0 = blockIdx.x * 16 * RT, c = blockIdx.y;
+    const int b = (row0 / R) * nchunks + c;
+    const int t0 = c * kMfgBatch;
+    const size_t img = (size_t)D * kMfgBatch;
+    mf_rows<F, kMfgBatch / 16, NK, RT>(w, w_bytes, xh + b * img, (uint32_t)(img * 2),
+                                       unscale + (size_t)b * kMfgBatch, y + (size_t)t0 * y_stride,
+                                       min(kMfgBatch, n_tok - t0), D, out_dim, y_stride, row0,
+                                       red);
 }
 
 // Grid (row blocks, batch slots, matrices): workgroup (x, b, m) computes
@@ -460,7 +506,7 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mfg(const uint8_t *__restrict_
     const size_t img = (size_t)in_dim * kMfgBatch;
     mf_rows<F, kMfgBatch / 16, NK, RT>(w, (uint32_t)w_stride, xh + b * img, (uint32_t)(img * 2),
                                        unscale + (size_t)b * kMfgBatch, y, bt.count, in_dim,
-                                       out_dim, blockIdx.x * 16 * RT, red);
+                                       out_dim, out_dim, blockIdx.x * 16 * RT, red);
 }
 
 // ---- fused batched GEMV: activations converted into LDS ------------------------------
@@ -807,6 +853,47 @@ hipError_t launch_moe_mfma(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
         return e;
     return mfg_pass_dt(dt_d, down, nullptr, d_stride, hg, hu, nullptr, bat, n_bat, max_b, clamp,
                        xh2, us2, yd, nullptr, n_ff, n_embd, s);
+}
+
+bool lora_mfma_supported(uint32_t dtype, int n_tok, int D, int G, int R) {
+    return (dtype == T_Q4_K || dtype == T_Q6_K || dtype == T_Q8_0) && n_tok >= 9 && D > 0 &&
+           D % 256 == 0 && R > 0 && R % 64 == 0 && (long long)G * R >= 1024;
+}
+
+size_t lora_mfma_scratch_bytes(int n_tok, int D, int G) {
+    const size_t nb = (size_t)G * ((n_tok + kMfgBatch - 1) / kMfgBatch);
+    return (nb * kMfgBatch * (size_t)D * 2 + 255) / 256 * 256 + nb * kMfgBatch * 4;
+}
+
+template <class F>
+static hipError_t mfl_go(const uint8_t *w, size_t w_bytes, const float *x, int x_stride, float *y,
+                         int y_stride, uint8_t *scratch, int n_tok, int D, int G, int R,
+                         hipStream_t s) {
+    const int nchunks = (n_tok + kMfgBatch - 1) / kMfgBatch;
+    const size_t nb = (size_t)G * nchunks;
+    _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
+    float *us = reinterpret_cast<float *>(scratch + (nb * kMfgBatch * (size_t)D * 2 + 255) / 256 * 256);
+    k_mfl_x<F><<<dim3(kMfgBatch, (unsigned)nb), 256, 0, s>>>(x, x_stride, n_tok, D, nchunks, xh, us);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int out_dim = G * R;
+    k_gemv_mfl<F><<<dim3((unsigned)(out_dim / 64), (unsigned)nchunks), 256, 0, s>>>(
+        w, (uint32_t)w_bytes, xh, us, y, y_stride, n_tok, D, R, out_dim, nchunks);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_mfma(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
+                            int x_stride, float *y, int y_stride, uint8_t *scratch, int n_tok,
+                            int D, int G, int R, hipStream_t s) {
+    if (!lora_mfma_supported(dtype, n_tok, D, G, R) || w_bytes > 0xFFFFFFFFu ||
+        (size_t)G * ((n_tok + kMfgBatch - 1) / kMfgBatch) > 65535)
+        return hipErrorNotSupported;
+    switch (dtype) {
+    case T_Q4_K: return mfl_go<MQ4K>(w, w_bytes, x, x_stride, y, y_stride, scratch, n_tok, D, G, R, s);
+    case T_Q6_K: return mfl_go<MQ6K>(w, w_bytes, x, x_stride, y, y_stride, scratch, n_tok, D, G, R, s);
+    case T_Q8_0: return mfl_go<MQ8>(w, w_bytes, x, x_stride, y, y_stride, scratch, n_tok, D, G, R, s);
+    default: return hipErrorNotSupported;
+    }
 }
 
 hipError_t launch_gemv_mfma(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,

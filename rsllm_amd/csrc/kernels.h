@@ -154,6 +154,19 @@ hipError_t launch_moe_mfma(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
                            int n_pairs, int n_expert, float *hg, float *hu, float *yd,
                            uint8_t *scratch, int n_embd, int n_ff, float clamp, hipStream_t s);
 
+// gemv_mfma.hip, matmul_grouped_lora_down on the matrix cores: y[t *
+// y_stride + g * R + r] = sum_i W[g R + r, i] x[t * x_stride + g * D + i]
+// for a stacked Q4_K / Q6_K / Q8_0 matrix of G * R rows (device layout as
+// one matrix, w_bytes < 4 GiB), 9 or more tokens, D a multiple of 256, R of
+// 64, G * R >= 1024 (lora_mfma_supported). `scratch` holds
+// lora_mfma_scratch_bytes(n_tok, D, G) bytes. hipErrorNotSupported outside
+// those shapes.
+bool lora_mfma_supported(uint32_t dtype, int n_tok, int D, int G, int R);
+size_t lora_mfma_scratch_bytes(int n_tok, int D, int G);
+hipError_t launch_lora_mfma(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
+                            int x_stride, float *y, int y_stride, uint8_t *scratch, int n_tok,
+                            int D, int G, int R, hipStream_t s);
+
 // prefill.hip: out[t, o] = sum_i deq(W)[o, i] * x[t, i] for a raw GGUF Q4_K
 // weight W [out_dim x in_dim] and bf16 activations x [n_tok x in_dim]
 // (n_tok x out_dim fp32 output, overwritten). `scratch` holds

@@ -170,10 +170,11 @@ def test_grouped_lora_down_groups_too_long_for_lds(oracle, hip, rank):
             lora_dev(hip, w, x, n_tok, n_groups, group_dim, rank, G.Q8_0)
 
 
-@pytest.mark.parametrize("n_tok", [1, 2, 5, 16])
+@pytest.mark.parametrize("n_tok", [1, 2, 5, 9, 16, 33])
 def test_grouped_lora_down_dsv4_attn_output_a(oracle, hip, n_tok):
     """DS-V4 Flash attn_output_a: 8 groups of [1024 x 4096] Q8_0 (weight.rs:
-    171-182); each chunk of up to 8 tokens is one launch."""
+    171-182); up to 8 tokens one launch of the int8-limb kernel, from 9 the
+    matrix cores in chunks of 16 tokens (33: the last chunk has one)."""
     n_groups, group_dim, rank = 8, 4096, 1024
     w, x = grouped_case(G.Q8_0, n_tok, n_groups, group_dim, rank, 900)
     toks = np.unique(np.array([0, n_tok // 2, n_tok - 1]))
@@ -237,3 +238,22 @@ def test_device_forms(oracle, hip, dtype, n_tok):
     rc, want_z = oracle.matmul_weight_f32(w, x0, n_tok, group_dim, n_groups * rank, int(dtype))
     assert rc == 0
     assert rel_err(d_z.cpu().numpy(), want_z) <= REL_TOL
+
+
+@pytest.mark.parametrize("dtype,n_groups,group_dim,rank", [
+    (G.Q4_K, 2, 1024, 512), (G.Q6_K, 4, 2048, 256), (G.Q8_0, 3, 512, 384),
+])
+@pytest.mark.parametrize("n_tok", [9, 20, 40])
+def test_grouped_lora_down_matrix_cores(oracle, hip, dtype, n_groups, group_dim, rank, n_tok):
+    """9 or more tokens with ranks that are multiples of 64 and at least 1024
+    outputs per token: the matrix-core path (one pass over the stacked matrix
+    per 16 tokens; a workgroup's 64 rows belong to one group)."""
+    w, x = grouped_case(dtype, n_tok, n_groups, group_dim, rank, 300 + n_tok)
+    toks = np.unique(np.minimum(np.array([0, 15, 16, n_tok - 1]), n_tok - 1))
+    want = oracle_grouped(oracle, w, x, toks, n_groups, group_dim, rank, dtype)
+    got = np.full(n_tok * n_groups * rank, np.nan, np.float32)
+    hip.matmul_grouped_lora_down(got, w, x.reshape(-1), n_tok, n_groups, group_dim, rank, dtype)
+    assert not np.isnan(got).any()
+    err = rel_err(got.reshape(n_tok, -1)[toks], want)
+    print(f"lora_down mfma {G(dtype).name} T={n_tok} {n_groups}x[{rank}x{group_dim}]: rel err {err:.3e}")
+    assert err <= REL_TOL
