@@ -439,7 +439,7 @@ def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
     shared_bytes = sum(b_.numel() for b_ in blobs)
     n_copies = max(2, int(640e6 // shared_bytes) + 1)
     copies = [blobs] + [[b_.clone() for b_ in blobs] for _ in range(n_copies - 1)]
-    for n_tok in (1, 4, 8):
+    for n_tok in (1, 4, 8, 16):
         x = torch.from_numpy(synth.activations(n_tok, e_dim, 720).reshape(-1)).to(dev)
         y = torch.empty(n_tok * e_dim, dtype=torch.float32, device=dev)
 

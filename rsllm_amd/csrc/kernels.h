@@ -124,8 +124,8 @@ hipError_t launch_quantize_swiglu(uint32_t dtype, const float *hg, const float *
                                   uint8_t *xq, int n_rows, int n, const int *off, int n_expert,
                                   hipStream_t s);
 
-// gemv_mfma.hip, routed experts on the matrix cores (Q4_K, Q6_K and Q8_0;
-// n_embd and n_ff multiples of 256). Slots sorted by expert as
+// gemv_mfma.hip, routed experts on the matrix cores (Q4_K gate/up and down;
+// n_embd and n_ff multiples of 256, at least 1024). Slots sorted by expert as
 // launch_gemv_grouped's (off: n_expert + 1 entries on the device, slot_tok:
 // the token of each sorted slot, n_pairs = n_tok * k bounding the slot
 // count). Writes hg, hu [slot x n_ff] (gate and up of x[slot_tok[slot]])

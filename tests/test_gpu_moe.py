@@ -170,14 +170,14 @@ def test_moe_fused_rows_spanning_columns(oracle, hip, dt_gu, dt_d, n_embd, n_ff,
     assert rel_err(got, want) <= REL_TOL
 
 
-@pytest.mark.parametrize("dt_gu,dt_d", [(G.Q4_K, G.Q6_K), (G.Q8_0, G.Q4_K), (G.Q6_K, G.Q8_0),
-                                        (G.Q2_K, G.Q4_0)])
+@pytest.mark.parametrize("dt_gu,dt_d", [(G.Q4_K, G.Q4_K), (G.Q4_K, G.Q6_K), (G.Q8_0, G.Q4_K),
+                                        (G.Q6_K, G.Q8_0), (G.Q2_K, G.Q4_0)])
 @pytest.mark.parametrize("n_tok,k", [(40, 2), (5, 8), (9, 8)])
 def test_moe_grouped_many_tokens(oracle, hip, dt_gu, dt_d, n_tok, k):
     """Calls the fused pair does not take in one go run grouped by expert:
-    on the matrix cores for Q4_K / Q6_K / Q8_0 from 8 tokens (each expert's
-    slots in batches of up to 16), through the int8-limb grouped GEMV for
-    the other formats and fewer tokens. Every token's first pick is expert
+    on the matrix cores for Q4_K experts from 8 tokens (each expert's slots
+    in batches of up to 16), through the fused pair over token chunks or the
+    int8-limb grouped GEMV otherwise. Every token's first pick is expert
     0 (40 slots: three batches, the last partial), token 1 picks one expert
     twice and one slot has weight 0."""
     n_embd, n_ff, n_expert = 1024, 1024, 9
@@ -194,4 +194,26 @@ def test_moe_grouped_many_tokens(oracle, hip, dt_gu, dt_d, n_tok, k):
                    dt_gu, dt_d, 10.0)
     err = rel_err(got - base, want - base)
     print(f"moe grouped {dt_gu.name}/{dt_d.name} T={n_tok} k={k}: rel err {err:.3e}")
+    assert err <= REL_TOL
+
+
+@pytest.mark.parametrize("dt", [G.Q8_0, G.Q6_K, G.Q4_K])
+@pytest.mark.parametrize("n_tok", [9, 16, 32])
+def test_moe_grouped_dsv4_like_shapes(oracle, hip, dt, n_tok):
+    """DS-V4-like expert shapes (n_embd 4096, n_ff 2048), all three matrices
+    in one format, checked on up to 6 tokens against the 1e-3 bound. Q4_K
+    takes the matrix-core route (two f16-rounded GEMVs in sequence); Q6_K
+    and Q8_0 exceeded or neared the bound there (1.2e-3, 9.3e-4) and take
+    the int8-limb routes."""
+    n_embd, n_ff, n_expert, k = 4096, 2048, 16, 6
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, dt, dt,
+                                          700 + n_tok + int(dt))
+    got = np.zeros(n_tok * n_embd, np.float32)
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   dt, dt, 10.0)
+    toks = np.unique(np.linspace(0, n_tok - 1, min(n_tok, 6)).astype(int))
+    want = run_oracle(oracle, np.zeros(len(toks) * n_embd, np.float32), x[toks], gate, up, down,
+                      ids[toks], w[toks], len(toks), n_embd, n_ff, n_expert, k, dt, dt)
+    err = rel_err(got.reshape(n_tok, n_embd)[toks], want.reshape(len(toks), n_embd))
+    print(f"moe dsv4-like {dt.name} T={n_tok}: rel err {err:.3e}")
     assert err <= REL_TOL

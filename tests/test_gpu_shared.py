@@ -78,9 +78,11 @@ def test_reference_clamp_test_dsv4_shapes(hip):
     assert not out[1:].any()
 
 
-def test_shared_expert_dsv4_q8_0(oracle, hip):
-    """DS-V4 shared expert shapes (n_embd 4096, n_ff 2048) in Q8_0."""
-    err = run_case(oracle, hip, G.Q8_0, G.Q8_0, G.Q8_0, 2, 4096, 2048, 10.0, 123)
+@pytest.mark.parametrize("n_tok", [2, 16])
+def test_shared_expert_dsv4_q8_0(oracle, hip, n_tok):
+    """DS-V4 shared expert shapes (n_embd 4096, n_ff 2048) in Q8_0: the
+    paired gate/up launch at 2 tokens, the matrix-core GEMVs at 16."""
+    err = run_case(oracle, hip, G.Q8_0, G.Q8_0, G.Q8_0, n_tok, 4096, 2048, 10.0, 123)
     assert err <= REL_TOL
 
 
