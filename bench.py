@@ -59,6 +59,10 @@ def parse():
     ap.add_argument("--extra-iters", type=int, default=100)
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc passes that measure roofline.traffic")
+    ap.add_argument("--gemv-probe", action="store_true",
+                    help="internal: the batch-1 GEMVs run under rocprofv3 --kernel-trace")
+    ap.add_argument("--no-trace", action="store_true",
+                    help="skip the kernel-trace pass (roofline from HIP events only)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="internal: the workload run under rocprofv3 --pmc (prints no JSON)")
     ap.add_argument("--prefill-probe", type=int, default=0, metavar="T",
@@ -143,6 +147,12 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
     return res
 
 
+def _progress(msg):
+    """One line per finished stage on stderr (the JSON line stays alone on
+    stdout)."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
 def _time(fn, iters, stream):
     """Mean microseconds per call over `iters` back-to-back calls, one HIP
     event pair on the launch stream around the whole run."""
@@ -165,13 +175,15 @@ def _rotating(t, min_bytes=640e6):
 
 
 PMC_COPY_BYTES = 256 << 20
+PMC_LAUNCHES = 24  # per C1 shape; the last 8 of each are counted
 
 
 def pmc_probe():
     """Run under rocprofv3 --pmc by pmc_traffic(): three device copies of
     PMC_COPY_BYTES (the calibration kernel, bytes known) and then the dominant
-    kernel of the bench line (C1 14336x4096 Q6_K batch-1 GEMV, one launch per
-    call) streaming its weights from HBM through rotating copies."""
+    kernels of the bench line (C1 Q6_K batch-1 GEMV, 14336x4096 then
+    4096x14336, one launch per call, PMC_LAUNCHES each) streaming their
+    weights from HBM through rotating copies."""
     import torch
     from rsllm_amd import backend as B
     from rsllm_amd import synth
@@ -183,20 +195,21 @@ def pmc_probe():
     for _ in range(3):
         b.copy_(a)
     del a, b
-    out_dim, in_dim = 14336, 4096
-    w_host = synth.weight(G.Q6_K, out_dim, in_dim, seed=100)
-    raw = torch.from_numpy(w_host).to(dev)
-    prep = torch.empty_like(raw)
-    B.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), G.Q6_K, in_dim, sptr)
-    del raw
-    reps = _rotating(prep)
-    x = torch.from_numpy(synth.activations(1, in_dim, seed=200)).to(dev).reshape(-1)
-    y = torch.empty(out_dim, dtype=torch.float32, device=dev)
-    for i in range(len(reps) + 8):
-        w = reps[i % len(reps)]
-        B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
-                               x.numel(), 1, in_dim, out_dim, G.Q6_K, sptr)
-    torch.cuda.synchronize()
+    for si, (out_dim, in_dim) in enumerate(((14336, 4096), (4096, 14336))):
+        w_host = synth.weight(G.Q6_K, out_dim, in_dim, seed=100 + si)
+        raw = torch.from_numpy(w_host).to(dev)
+        prep = torch.empty_like(raw)
+        B.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), G.Q6_K, in_dim, sptr)
+        del raw
+        reps = _rotating(prep)
+        x = torch.from_numpy(synth.activations(1, in_dim, seed=200 + si)).to(dev).reshape(-1)
+        y = torch.empty(out_dim, dtype=torch.float32, device=dev)
+        for i in range(PMC_LAUNCHES):
+            w = reps[i % len(reps)]
+            B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
+                                   x.numel(), 1, in_dim, out_dim, G.Q6_K, sptr)
+        torch.cuda.synchronize()
+        del reps, prep
 
 
 def prefill_probe(T):
@@ -243,12 +256,132 @@ def moe_probe(T):
     torch.cuda.synchronize()
 
 
+TRACE_LAUNCHES = 64
+# (tag, dtype name, out_dim, in_dim) of the batch-1 GEMVs --gemv-probe runs,
+# in launch order: C1 both orientations (the bench line), then C0
+PROBE_GEMVS = [("C1", "Q6_K", 14336, 4096), ("C1", "Q6_K", 4096, 14336), ("C0", "Q4_K", 4096, 4096)]
+
+
+def gemv_probe():
+    """Run under rocprofv3 --kernel-trace by kernel_trace(): the batch-1
+    GEMVs of PROBE_GEMVS, TRACE_LAUNCHES launches each through
+    matmul_quant_f32_dev (one kernel per call at batch 1), every launch
+    reading a different weight copy (> 640 MB of copies per shape) so the
+    weights stream from HBM."""
+    import torch
+    from rsllm_amd import backend as B
+    from rsllm_amd import synth
+    from rsllm_amd.ggml import GgmlType as G
+    dev = torch.device("cuda:0")
+    sptr = torch.cuda.current_stream().cuda_stream
+    for si, (_, dname, out_dim, in_dim) in enumerate(PROBE_GEMVS):
+        dtype = G[dname]
+        w_host = synth.weight(dtype, out_dim, in_dim, seed=100 + si)
+        raw = torch.from_numpy(w_host).to(dev)
+        prep = torch.empty_like(raw)
+        B.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), dtype, in_dim, sptr)
+        del raw
+        reps = _rotating(prep)
+        x = torch.from_numpy(synth.activations(1, in_dim, seed=200 + si)).to(dev).reshape(-1)
+        y = torch.empty(out_dim, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        for i in range(TRACE_LAUNCHES):
+            w = reps[i % len(reps)]
+            B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
+                                   x.numel(), 1, in_dim, out_dim, dtype, sptr)
+        torch.cuda.synchronize()
+        del reps, prep
+
+
+def kernel_trace():
+    """Kernel-trace durations of the batch-1 GEMVs: one rocprofv3
+    --kernel-trace pass over a child run of gemv_probe(). The k_gemv1
+    dispatches come in PROBE_GEMVS order, TRACE_LAUNCHES per shape; the first
+    8 of each shape are dropped (warm-up). Returns a list of per-shape
+    summaries (mean / median / p10 / p90 in microseconds) or an error dict."""
+    import shutil
+    import sqlite3
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(exe):
+        return {"error": "rocprofv3 not found"}
+    here = os.path.abspath(__file__)
+    env = dict(os.environ, TMPDIR="/tmp")
+    d = tempfile.mkdtemp(prefix="rsllm_kt_", dir="/tmp")
+    cmd = ["timeout", "-s", "KILL", "150", exe, "--kernel-trace", "-d", d, "-o", "p", "--",
+           sys.executable, here, "--gemv-probe"]
+    try:
+        r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True, timeout=180)
+    except subprocess.TimeoutExpired:
+        return {"error": "kernel-trace pass timed out"}
+    dbs = [os.path.join(root, f) for root, _, fs in os.walk(d) for f in fs if f.endswith(".db")]
+    if not dbs:
+        return {"error": f"kernel-trace pass failed (rc {r.returncode})",
+                "stderr_tail": r.stderr[-400:]}
+    rows = sqlite3.connect(dbs[0]).execute(
+        "select name, duration from kernels order by dispatch_id").fetchall()
+    shutil.rmtree(d, ignore_errors=True)
+    durs = [(n, v) for n, v in rows if "k_gemv1" in n]
+    if len(durs) != TRACE_LAUNCHES * len(PROBE_GEMVS):
+        return {"error": f"expected {TRACE_LAUNCHES * len(PROBE_GEMVS)} k_gemv1 dispatches, "
+                         f"found {len(durs)}"}
+    out = []
+    for si, (tag, dname, out_dim, in_dim) in enumerate(PROBE_GEMVS):
+        part = durs[si * TRACE_LAUNCHES:(si + 1) * TRACE_LAUNCHES][8:]
+        us = np.array([v for _, v in part], dtype=np.float64) / 1e3
+        out.append({"config": tag, "dtype": dname, "shape": f"{out_dim}x{in_dim}",
+                    "kernel": part[0][0].split("(")[0], "n": int(us.size),
+                    "us_mean": round(float(us.mean()), 3),
+                    "us_median": round(float(np.median(us)), 3),
+                    "us_p10": round(float(np.percentile(us, 10)), 3),
+                    "us_p90": round(float(np.percentile(us, 90)), 3)})
+    return out
+
+
+def bench_stream_read(B, dev, stream, iters):
+    """extra.stream_read: the streaming-read ceiling for the byte counts of the
+    batch-1 GEMVs (C1 48.2 MB, C0 9.47 MB): rsllm_hip_stream_read_dev over
+    rotating buffers (> 640 MB), swept over grid size, workgroup size, loads
+    in flight and access order; the best configuration per size and its
+    GB/s."""
+    import torch
+    sptr = stream.cuda_stream
+    res = []
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    for tag, nbytes in (("C1", 48242688), ("C0", 9469952)):
+        nbytes = nbytes // 16 * 16
+        reps = _rotating(torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1))
+        sink = torch.empty(4 * cus * 1024, dtype=torch.int32, device=dev)
+        best = None
+        for n_wg in (cus, 2 * cus, 4 * cus):
+            for threads in (256, 512, 1024):
+                for unroll in (2, 4, 8):
+                    for contiguous in (1, 0):
+                        def call(i):
+                            B.stream_read_dev(reps[i % len(reps)].data_ptr(), nbytes,
+                                              sink.data_ptr(), sink.numel(), n_wg, threads,
+                                              unroll, contiguous, sptr)
+                        for i in range(len(reps)):
+                            call(i)
+                        us = _time(call, iters, stream)
+                        if best is None or us < best["us"]:
+                            best = {"config": tag, "bytes": nbytes, "us": round(us, 3),
+                                    "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                    "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                    "n_wg": n_wg, "threads": threads, "unroll": unroll,
+                                    "contiguous": bool(contiguous)}
+        res.append(best)
+        del reps, sink
+    return res
+
+
 def pmc_traffic():
     """roofline.traffic: HBM bytes per launch of the dominant kernel from two
     rocprofv3 --pmc passes over a child run of pmc_probe() (FETCH_SIZE, then
     WRITE_SIZE, KiB per dispatch). Each counter is scaled by bytes / counter of
     the calibration copy in the same pass, whose read and write sizes are
-    known. Returns (bytes or None, details)."""
+    known. Returns ({shape: bytes} or None, details)."""
     import shutil
     import sqlite3
     import subprocess
@@ -260,7 +393,7 @@ def pmc_traffic():
     env = dict(os.environ, TMPDIR="/tmp")
     det = {"calibration": f"device copy of {PMC_COPY_BYTES} bytes (read {PMC_COPY_BYTES}, "
                           f"write {PMC_COPY_BYTES})"}
-    total = 0.0
+    totals = {}
     for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
         d = tempfile.mkdtemp(prefix="rsllm_pmc_", dir="/tmp")
         cmd = ["timeout", "-s", "KILL", "120", exe, "--pmc", ctr, "-d", d, "-o", "p", "--",
@@ -280,17 +413,19 @@ def pmc_traffic():
         # the calibration copies are the probe's first three copy dispatches
         # (later ones are weight uploads and clones of other sizes)
         copy = [v for n, v in rows if "copyBuffer" in n][:3]
-        gemv = [v for n, v in rows if "k_gemv1" in n][-8:]
-        if not copy or not gemv:
+        gemv = [v for n, v in rows if "k_gemv1" in n]
+        if not copy or len(gemv) != 2 * PMC_LAUNCHES:
             return None, {"error": f"{ctr}: kernels not found in the pass"}
         factor = PMC_COPY_BYTES / (float(np.median(copy)) * 1024.0)
-        kib = float(np.median(gemv))
-        det[ctr] = {"gemv_kib_per_dispatch": round(kib, 1),
-                    "copy_kib_per_dispatch": round(float(np.median(copy)), 1),
-                    "factor_bytes_per_counted_byte": round(factor, 4),
-                    "bytes_per_launch": round(kib * 1024.0 * factor)}
-        total += kib * 1024.0 * factor
-    return round(total), det
+        per_shape = []
+        for si, shape in enumerate(("14336x4096", "4096x14336")):
+            kib = float(np.median(gemv[(si + 1) * PMC_LAUNCHES - 8:(si + 1) * PMC_LAUNCHES]))
+            per_shape.append({"shape": shape, "gemv_kib_per_dispatch": round(kib, 1),
+                              "bytes_per_launch": round(kib * 1024.0 * factor)})
+            totals[shape] = totals.get(shape, 0.0) + kib * 1024.0 * factor
+        det[ctr] = {"copy_kib_per_dispatch": round(float(np.median(copy)), 1),
+                    "factor_bytes_per_counted_byte": round(factor, 4), "per_shape": per_shape}
+    return {k: round(v) for k, v in totals.items()}, det
 
 
 def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
@@ -351,6 +486,9 @@ def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
         for n_tok in (1, 8, 32):
             rows.append(gemv_case("C2", G.Q8_0, o, i_, n_tok, 530 + o // 1024))
     out["gemv"] = rows
+    _progress("extra: gemv done")
+    out["stream_read"] = bench_stream_read(B, dev, stream, iters)
+    _progress("extra: stream_read done")
 
     # ---- C2 through the int8-activation path (quantize + matmul, bit-exact) ----
     q8 = []
@@ -398,6 +536,7 @@ def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
             q8.append(e)
         del reps, prep
     out["q8_int8"] = q8
+    _progress("extra: q8_int8 done")
 
     # ---- caller chain at DS-V4 Flash shapes (weight.rs:113-266, moe.rs:422-502) ----
     chain = []
@@ -587,6 +726,9 @@ def main():
     if args.pmc_probe:
         pmc_probe()
         return
+    if args.gemv_probe:
+        gemv_probe()
+        return
     if args.prefill_probe:
         prefill_probe(args.prefill_probe)
         return
@@ -596,6 +738,9 @@ def main():
     # the counter passes run first, in child processes, before this process
     # touches the GPU
     traffic, traffic_detail = (None, {"skipped": True}) if args.no_traffic else pmc_traffic()
+    _progress("counter passes done")
+    trace = {"skipped": True} if args.no_trace else kernel_trace()
+    _progress("kernel-trace pass done")
 
     import torch
 
@@ -690,8 +835,20 @@ def main():
                            "us_mean": round(us, 3),
                            "GBps": round(bytes_per_launch[si] / (us * 1e-6) / 1e9, 1)})
     dom = max(range(len(mats)), key=lambda s: kern_us[s])
-    ach = bytes_per_launch[dom] / (kern_us[dom] * 1e-6) / 1e9
+    ach_events = bytes_per_launch[dom] / (kern_us[dom] * 1e-6) / 1e9
+    # roofline from the kernel trace of the same launches when the trace pass
+    # ran (its per-dispatch durations exclude launch gaps); the event mean
+    # stays beside it
+    trace_ok = isinstance(trace, list)
+    if trace_ok:
+        tr_us = [trace[si]["us_mean"] for si in range(len(mats))]
+        dom = max(range(len(mats)), key=lambda s: tr_us[s])
+        dom_us = tr_us[dom]
+    else:
+        dom_us = kern_us[dom]
+    ach = bytes_per_launch[dom] / (dom_us * 1e-6) / 1e9
 
+    _progress("bench line timed")
     # ---- correctness spot check of this run's outputs vs the oracle ----
     # (ys hold the last GEMV-only launch: same weights bytes, same x)
     check = None
@@ -731,10 +888,12 @@ def main():
             "us_per_op": t_cpu / n_ops * 1e6,
         }
 
+    _progress("check and CPU baseline done")
     prefill = None if args.no_prefill else bench_prefill(B, synth, G, dev, stream,
                                                           args.prefill_iters, not args.no_cpu,
                                                           args.cpu_seconds)
 
+    _progress("prefill leg done")
     extra = None if args.no_extra else bench_extra(B, synth, G, dev, stream, args.extra_iters,
                                                     not args.no_cpu)
 
@@ -749,7 +908,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q6_k weights, f32 activations/accumulation",
+        "dtype": "q6_k weights; x re-expressed per 16-element group as two int8 limbs "
+                 "(about 16 significant bits); exact int32 dots, fp32 scaling and sums",
         "data": "synthetic (seeded PCG64 GGUF Q6_K blocks with BASELINE.json C1 statistics; "
                 "x ~ N(0,1) fp32)",
         "config": {
@@ -766,11 +926,16 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
+            "traffic": traffic.get(per_kernel[dom]["shape"]) if traffic else None,
+            "traffic_by_shape": traffic,
             "traffic_detail": traffic_detail,
             "kernel": "rsllm_hip::k_gemv1<FQ6K, NW, PD, GPT> (x quantised in LDS, one launch)",
             "kernel_shape": per_kernel[dom]["shape"],
-            "kernel_us_mean": round(kern_us[dom], 3),
+            "kernel_us_mean": round(dom_us, 3),
+            "kernel_us_from": "rocprofv3 kernel trace" if trace_ok else "HIP events",
+            "kernel_us_events": round(kern_us[dom], 3),
+            "achieved_events": round(ach_events, 2),
+            "trace": trace,
         },
         "per_kernel": per_kernel,
         "cpu_baseline": cpu_baseline,

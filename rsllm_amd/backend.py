@@ -169,6 +169,7 @@ SIGNATURES = {
                                        _S, _S, _S, ctypes.c_float], _I),
     "rsllm_hip_apply_shared_expert_dev": ([_P, _S, _P, _S, _P, _S, _U32, _P, _S, _U32, _P, _S,
                                            _U32, _S, _S, _S, ctypes.c_float, _P], _I),
+    "rsllm_hip_stream_read_dev": ([_P, _S, _P, _S, _I, _I, _I, _I, _P], _I),
 }
 
 
@@ -505,6 +506,14 @@ def dequant_to_f32_dev(dtype, src_ptr: int, src_len: int, dst_ptr: int, dst_len:
                        stream: int = 0) -> None:
     _check(LIB.rsllm_hip_dequant_to_f32_dev(int(dtype), src_ptr or None, src_len, dst_ptr or None,
                                             dst_len, stream or None))
+
+
+def stream_read_dev(p: int, nbytes: int, sink_ptr: int, sink_len: int, n_wg: int, threads: int,
+                    unroll: int, contiguous: bool, stream: int = 0) -> None:
+    """Measurement aid (no reference counterpart): a pure streaming read of
+    nbytes at device pointer p."""
+    _check(LIB.rsllm_hip_stream_read_dev(p or None, nbytes, sink_ptr or None, sink_len, n_wg,
+                                         threads, unroll, int(bool(contiguous)), stream or None))
 
 
 # ---------------------------------------------------------------------------

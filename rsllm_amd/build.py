@@ -25,7 +25,7 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librsllm_hip.so")
 
 SOURCES = ["abi.hip", "dequant.hip", "gemv.hip", "gemv_mfma.hip", "prefill.hip", "moe.hip",
-           "q8_int8.hip", "residency.hip"]
+           "q8_int8.hip", "residency.hip", "probe.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
