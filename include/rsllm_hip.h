@@ -113,6 +113,23 @@ int rsllm_hip_matmul_quant_f32_dev(float *out, size_t out_len, const uint8_t *we
                                    size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype,
                                    rsllm_hip_stream_t stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (work under HIP graph capture, serving loops or harnesses that
+ * forbid hipMalloc): rsllm_hip_matmul_quant_f32_dev with the same arguments,
+ * validation and results, whose activation workspace is a static array of
+ * RSLLM_HIP_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends)
+ * instead of memory the library allocates; the call itself allocates and
+ * frees nothing. A call whose workspace would exceed that size (many tokens
+ * of a long row) returns RSLLM_HIP_ERR_INVALID_ARGUMENT. Every call on one
+ * GPU shares its array and leaves its contents behind: calls that overlap in
+ * time on one GPU (two streams, or two threads) race on it, so enqueue them
+ * on one stream. */
+#define RSLLM_HIP_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int rsllm_hip_matmul_quant_f32_dev_noalloc(float *out, size_t out_len, const uint8_t *weights,
+                                           size_t weights_len, const float *x, size_t x_len,
+                                           size_t n_tok, size_t in_dim, size_t out_dim,
+                                           uint32_t dtype, rsllm_hip_stream_t stream);
+
 /* Activations pre-quantised for the GEMV kernels, for callers that reuse one
  * x across several weight matrices of the same dtype and in_dim (e.g. an
  * FFN's gate and up projections) or time the GEMV alone. No reference

@@ -137,6 +137,7 @@ SIGNATURES = {
     "rsllm_hip_capability_get": ([ctypes.POINTER(_Capability)], None),
     "rsllm_hip_matmul_quant_f32": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _U32], _I),
     "rsllm_hip_matmul_quant_f32_dev": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _P], _I),
+    "rsllm_hip_matmul_quant_f32_dev_noalloc": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _P], _I),
     "rsllm_hip_register_weights": ([_P, _S, _U32, _S], _I),
     "rsllm_hip_release_weights": ([], _I),
     "rsllm_hip_model_upload": ([_P, ctypes.POINTER(TensorDesc), _S,
@@ -359,6 +360,20 @@ def matmul_quant_f32_dev(out_ptr: int, out_len: int, w_ptr: int, w_len: int, x_p
     _check(LIB.rsllm_hip_matmul_quant_f32_dev(out_ptr or None, out_len, w_ptr or None, w_len,
                                               x_ptr or None, x_len, n_tok, in_dim, out_dim,
                                               int(dtype), stream or None))
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20
+
+
+def matmul_quant_f32_dev_noalloc(out_ptr: int, out_len: int, w_ptr: int, w_len: int, x_ptr: int,
+                                 x_len: int, n_tok: int, in_dim: int, out_dim: int, dtype,
+                                 stream: int = 0) -> None:
+    """matmul_quant_f32_dev whose workspace is the library's static per-GPU
+    array (NOALLOC_SCRATCH_BYTES): no allocation in the call. Calls that
+    overlap on one GPU race on that array."""
+    _check(LIB.rsllm_hip_matmul_quant_f32_dev_noalloc(out_ptr or None, out_len, w_ptr or None,
+                                                      w_len, x_ptr or None, x_len, n_tok, in_dim,
+                                                      out_dim, int(dtype), stream or None))
 
 
 def xq_bytes(dtype, n_tok: int, in_dim: int) -> int:

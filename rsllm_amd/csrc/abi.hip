@@ -108,6 +108,49 @@ int ensure_device() {
 
 bool fits_int(size_t v) { return v <= (size_t)INT_MAX; }
 
+// ---- static workspace of the no-allocation entry point ---------------------
+// One copy of `scratch` per GPU, held until the process ends. In host code the
+// array's name is not a device address: the address hipGetSymbolAddress gives
+// for a device (looked up once per device, with that device current) is the
+// only one passed to kernels.
+constexpr size_t kNoAllocScratchBytes = RSLLM_HIP_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[kMaxDevices] = {};
+
+// Address of `scratch` on device `dev`, which must be current.
+int noalloc_scratch(int dev, uint8_t **p) {
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "device ordinal out of range");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return dev_err(e, "hipGetSymbolAddress(scratch)");
+        if (!ptr) return set_err(RSLLM_HIP_ERR_DEVICE, "hipGetSymbolAddress(scratch): null");
+        g_scratch_ptr[dev] = static_cast<uint8_t *>(ptr);
+    }
+    *p = g_scratch_ptr[dev];
+    return RSLLM_HIP_OK;
+}
+
+// The process's device made current, without creating a stream or touching
+// any allocator.
+int current_device_noalloc(int *dev_out) {
+    int dev;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_inited = true;
+        dev = g_device;
+    }
+    int cur = -1;
+    HIP_TRY(hipGetDevice(&cur), "hipGetDevice");
+    if (cur != dev) HIP_TRY(hipSetDevice(dev), "hipSetDevice");
+    *dev_out = dev;
+    return RSLLM_HIP_OK;
+}
+
 bool mul_ok(size_t a, size_t b, size_t *r) { return !__builtin_mul_overflow(a, b, r); }
 
 // dtypes matmul_quant_f32 accepts (quant_matmul.rs:57-64), and which of
@@ -528,6 +571,9 @@ int rsllm_hip_init(int device_ordinal) {
         g_inited = true;
     }
     int rc = ensure_device();
+    if (rc) return rc;
+    uint8_t *ws;  // the no-allocation workspace's address on this device
+    rc = noalloc_scratch(device_ordinal, &ws);
     return rc ? rc : ok();
 }
 
@@ -560,6 +606,37 @@ int rsllm_hip_matmul_quant_f32_dev(float *out, size_t out_len, const uint8_t *we
     HIP_TRY(t_ctx.xq.ensure(gemv_work_bytes(dtype, (int)n_tok, (int)in_dim, (int)out_dim)), "hipMalloc");
     HIP_TRY(launch_gemv(dtype, weights, weights_len, x, (uint8_t *)t_ctx.xq.p, out, (int)n_tok,
                         (int)in_dim, (int)out_dim, s),
+            "gemv");
+    return ok();
+}
+
+int rsllm_hip_matmul_quant_f32_dev_noalloc(float *out, size_t out_len, const uint8_t *weights,
+                                           size_t weights_len, const float *x, size_t x_len,
+                                           size_t n_tok, size_t in_dim, size_t out_dim,
+                                           uint32_t dtype, rsllm_hip_stream_t stream) {
+    int rc = validate_matmul(out_len, weights, weights_len, x, x_len, out, n_tok, in_dim, out_dim,
+                             dtype);
+    if (rc) return rc;
+    const size_t need =
+        n_tok && in_dim ? gemv_work_bytes(dtype, (int)n_tok, (int)in_dim, (int)out_dim) : 0;
+    if (need > kNoAllocScratchBytes) {
+        const std::string m = "matmul_quant_f32_dev_noalloc: the call needs " +
+                              std::to_string(need) + " bytes of workspace, above the static " +
+                              std::to_string(kNoAllocScratchBytes) + "-byte maximum";
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, m.c_str());
+    }
+    hipStream_t s = (hipStream_t)stream;
+    if (n_tok == 0) return ok();
+    int dev;
+    if ((rc = current_device_noalloc(&dev))) return rc;
+    if (in_dim == 0) {
+        HIP_TRY(launch_fill_zero(out, out_len, s), "fill_zero");
+        return ok();
+    }
+    uint8_t *ws;
+    if ((rc = noalloc_scratch(dev, &ws))) return rc;
+    HIP_TRY(launch_gemv(dtype, weights, weights_len, x, ws, out, (int)n_tok, (int)in_dim,
+                        (int)out_dim, s),
             "gemv");
     return ok();
 }

@@ -1,0 +1,65 @@
+"""rsllm_hip_matmul_quant_f32_dev_noalloc: the same results as
+rsllm_hip_matmul_quant_f32_dev (it runs the same kernels, with the static
+per-GPU workspace in place of the library-allocated one), on calls that use
+that workspace, twice in a row with the second call smaller; and the
+rejection of a call whose workspace would exceed the static maximum."""
+import numpy as np
+import pytest
+
+from conftest import REL_TOL, rel_err
+from rsllm_amd import synth
+from rsllm_amd.ggml import GgmlType as G
+
+# (dtype, out_dim, in_dim, n_tok): each takes a kernel path that uses the
+# workspace: the matrix-core batched GEMV (f16 activation image) for 5..32
+# tokens of >= 1024 rows, the activation pre-pass + GEMV otherwise
+CALLS = [
+    [(G.Q4_K, 4096, 4096, 24), (G.Q6_K, 1024, 2048, 12)],   # matrix cores, then smaller
+    [(G.Q8_0, 512, 4096, 20), (G.Q4_K, 256, 1024, 11)],     # pre-pass path, then smaller
+    [(G.Q6_K, 2048, 4096, 32), (G.Q2_K, 300, 512, 13)],     # mixed paths, then smaller
+]
+
+
+def _run(hip, torch, fn, w_dev, x_dev, n_tok, in_dim, out_dim, dtype):
+    y = torch.full((n_tok * out_dim,), float("nan"), dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    fn(y.data_ptr(), y.numel(), w_dev.data_ptr(), w_dev.numel(), x_dev.data_ptr(), x_dev.numel(),
+       n_tok, in_dim, out_dim, dtype, s)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("calls", CALLS)
+def test_noalloc_matches_dev_entry(hip, oracle, calls):
+    import torch
+    hip.init(0)
+    s = torch.cuda.current_stream().cuda_stream
+    for i, (dtype, out_dim, in_dim, n_tok) in enumerate(calls):
+        print(f"noalloc call {i}: {dtype.name} {out_dim}x{in_dim} T={n_tok}", flush=True)
+        w = synth.weight(dtype, out_dim, in_dim, seed=900 + i)
+        raw = torch.from_numpy(w).cuda()
+        prep = torch.empty_like(raw)
+        hip.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), dtype, in_dim, s)
+        x = synth.activations(n_tok, in_dim, seed=910 + i).reshape(-1)
+        xd = torch.from_numpy(x).cuda()
+        got = _run(hip, torch, hip.matmul_quant_f32_dev_noalloc, prep, xd, n_tok, in_dim, out_dim,
+                   dtype)
+        ref = _run(hip, torch, hip.matmul_quant_f32_dev, prep, xd, n_tok, in_dim, out_dim, dtype)
+        # the same kernels on the same inputs: bit for bit
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        rc, want = oracle.matmul_quant_f32(w, x, n_tok, in_dim, out_dim, int(dtype))
+        assert rc == 0
+        assert rel_err(got, want) <= REL_TOL
+
+
+def test_noalloc_rejects_workspace_above_the_maximum(hip):
+    # 32 tokens of a 600k-element Q8_0 row need a 38 MB f16 activation image;
+    # validation and the size check run before any device work (placeholder
+    # addresses, never dereferenced)
+    in_dim, out_dim, n_tok = 600_064, 1024, 32
+    w_len = out_dim * (in_dim // 32) * 34
+    fake = 1 << 40
+    with pytest.raises(hip.InvalidArgument, match="workspace"):
+        hip.matmul_quant_f32_dev_noalloc(fake, n_tok * out_dim, fake, w_len, fake, n_tok * in_dim,
+                                         n_tok, in_dim, out_dim, G.Q8_0, 0)
