@@ -20,10 +20,19 @@
  * 8-block super-tiles of the same total size (see
  * rsllm_hip_prepare_weights_dev).
  *
- * Thread safety: every entry point may be called from any thread. Process
- * state (device ordinal, registered weights) is guarded by a mutex; each
- * calling thread gets its own stream and staging buffers for the host-pointer
- * entry points.
+ * Thread safety: every entry point may be called from any thread, as
+ * CpuBackend (backend-cpu/src/lib.rs:42-45) may. Process state (device
+ * ordinal, the registry of device copies) is guarded by a mutex, and the
+ * registry is a hash map keyed by host address. Each calling thread gets its
+ * own stream and host<->device staging for the host-pointer entry points.
+ * The kernels' device workspace belongs to a stream: one set per (device,
+ * stream), used by every call enqueued on that stream and locked while a
+ * call enqueues, so calls on different streams never share workspace and
+ * threads sharing a stream take turns. A call that uses a registered or
+ * model-resident tensor holds a reference to its device memory until it has
+ * synchronised, so a release on another thread never frees memory under it.
+ * Device pointers a caller obtained itself (rsllm_hip_model_tensor) are the
+ * caller's to keep alive: release a model only after work using them ends.
  */
 #ifndef RSLLM_HIP_H
 #define RSLLM_HIP_H
@@ -154,10 +163,19 @@ int rsllm_hip_matmul_prequant_dev(float *out, size_t out_len, const uint8_t *wei
  * GgufFile (rsllm-gguf/src/file.rs:81-97, models/src/dsv4/loader.rs:199-216).
  * Registering uploads a tensor once (converted to the device layout);
  * later host-pointer calls with the same (pointer, length, dtype, in_dim)
- * use the device copy. Release frees every registered tensor. */
+ * use the device copy. Release removes every registered tensor; the device
+ * copy of one that a call on another thread is using is freed when that call
+ * ends. */
 int rsllm_hip_register_weights(const uint8_t *weights, size_t weights_len, uint32_t dtype,
                                size_t in_dim);
 int rsllm_hip_release_weights(void);
+
+/* No reference counterpart (the reference has no streams): frees the device
+ * workspace the library keeps for `stream` on the current device, for a
+ * caller about to destroy that stream. Work still enqueued there finishes
+ * first (hipFree waits for the device); a later call on the stream makes a
+ * new set. */
+int rsllm_hip_stream_release(rsllm_hip_stream_t stream);
 
 /* ---- whole-model residency ---------------------------------------------------
  * No single reference function: this replaces keeping weights only in the
@@ -189,11 +207,11 @@ int rsllm_hip_release_weights(void);
  * serialised with each other and with the lookups below.
  * rsllm_hip_model_tensor returns a tensor's device address and length (the
  * device-layout bytes the _dev entry points take). rsllm_hip_model_release
- * drops one reference; the last one removes the registrations and frees
- * the allocation after the device is idle. Calls that use the model must
- * not be in flight on other threads while its last reference is released
- * (the same holds for rsllm_hip_release_weights and registered tensors).
- * rsllm_hip_release_weights does not touch models. */
+ * drops one reference; the last one removes the registrations, and the
+ * allocation is freed once no host-pointer call in flight still uses one of
+ * its tensors. `_dev` work on addresses from rsllm_hip_model_tensor must end
+ * before the last release. rsllm_hip_release_weights does not touch
+ * models. */
 typedef struct rsllm_hip_tensor_desc {
     const char *name;
     const uint8_t *data;

@@ -5,8 +5,12 @@
 
 #include <climits>
 #include <cstring>
+#include <map>
+#include <memory>
 #include <mutex>
 #include <string>
+#include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "../../include/rsllm_hip.h"
@@ -55,18 +59,27 @@ std::mutex g_mu;
 int g_device = 0;
 bool g_inited = false;
 
-// Host tensors with a device copy. owner 0: rsllm_hip_register_weights (dev
-// owned by the entry); otherwise the id of the uploaded model whose arena
-// holds dev.
+// Host tensors with a device copy, keyed by host address. owner 0:
+// rsllm_hip_register_weights (the entry's own allocation); otherwise the id
+// of the uploaded model whose arena holds dev. `keep` shares ownership of the
+// device memory: a call that found the entry holds its own reference until it
+// has synchronised, so a release running meanwhile frees nothing it reads.
 struct Registered {
-    const uint8_t *host;
     size_t len;
     uint32_t dtype;
     size_t in_dim;
-    uint8_t *dev;
+    const uint8_t *dev;
     uint64_t owner;
+    std::shared_ptr<void> keep;
 };
-std::vector<Registered> g_registry;
+std::unordered_multimap<const uint8_t *, Registered> g_registry;
+
+// A registered device copy held for the length of one call.
+struct Lease {
+    const uint8_t *dev = nullptr;
+    std::shared_ptr<void> keep;
+    explicit operator bool() const { return dev != nullptr; }
+};
 
 // ---- per-thread state -----------------------------------------------------
 struct DevBuf {
@@ -84,12 +97,54 @@ struct DevBuf {
     }
 };
 
+// Per calling thread: the stream and host<->device staging of the
+// host-pointer entry points (each such call synchronises before it returns).
 struct ThreadCtx {
     int device = -1;
     hipStream_t stream = nullptr;
-    DevBuf w_raw, w_dev, x, y, xq, xh, moe, moe_in, moe_w[3];
+    DevBuf w_raw, w_dev, x, y, moe_in, moe_w[3];
 };
 thread_local ThreadCtx t_ctx;
+
+// Device workspace of the kernels (activation images, MoE tables and
+// intermediates), one set per (device, stream). Work on one stream runs in
+// order, so every call enqueued on that stream can use the same set; `mu` is
+// held while a call sizes the set and enqueues, so threads that share a
+// stream take turns, and calls on different streams never share a set. A
+// buffer that grows is freed with hipFree, which waits for the device first.
+struct Scratch {
+    std::mutex mu;
+    DevBuf xq, xh, moe;
+    ~Scratch() {
+        for (DevBuf *b : {&xq, &xh, &moe})
+            if (b->p) (void)hipFree(b->p);
+    }
+};
+std::mutex g_scratch_map_mu;
+// never destroyed: its buffers are freed only by rsllm_hip_stream_release,
+// not at process exit (when the HIP runtime may already be gone)
+auto *g_scratch_map = new std::map<std::pair<int, hipStream_t>, std::shared_ptr<Scratch>>();
+
+// The current device's set for stream `st`, locked for the caller.
+struct ScratchLease {
+    std::shared_ptr<Scratch> keep;
+    std::unique_lock<std::mutex> lk;
+    Scratch *operator->() const { return keep.get(); }
+    Scratch &operator*() const { return *keep; }
+};
+ScratchLease stream_scratch(hipStream_t st) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::shared_ptr<Scratch> sc;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_map_mu);
+        auto &p = (*g_scratch_map)[{dev, st}];
+        if (!p) p = std::make_shared<Scratch>();
+        sc = p;
+    }
+    ScratchLease l{sc, std::unique_lock<std::mutex>(sc->mu)};
+    return l;
+}
 
 int ensure_device() {
     int dev;
@@ -246,11 +301,14 @@ int validate_dequant(uint32_t dtype, const void *src, size_t src_len, const void
     return RSLLM_HIP_OK;
 }
 
-const uint8_t *find_registered(const uint8_t *host, size_t len, uint32_t dtype, size_t in_dim) {
+Lease find_registered(const uint8_t *host, size_t len, uint32_t dtype, size_t in_dim) {
     std::lock_guard<std::mutex> lk(g_mu);
-    for (const auto &r : g_registry)
-        if (r.host == host && r.len == len && r.dtype == dtype && r.in_dim == in_dim) return r.dev;
-    return nullptr;
+    const auto range = g_registry.equal_range(host);
+    for (auto it = range.first; it != range.second; ++it) {
+        const Registered &r = it->second;
+        if (r.len == len && r.dtype == dtype && r.in_dim == in_dim) return Lease{r.dev, r.keep};
+    }
+    return Lease{};
 }
 
 bool needs_prepare(uint32_t dtype) { return dtype != T_Q4_K; }
@@ -259,9 +317,12 @@ bool needs_prepare(uint32_t dtype) { return dtype != T_Q4_K; }
 // uploaded into `dst` (quant formats other than Q4_K converted to the device
 // layout through the w_raw staging buffer). F32 blobs are uploaded as is.
 int blob_on_device(const uint8_t *blob, size_t len, uint32_t dtype, size_t in_dim, DevBuf &dst,
-                   const uint8_t **dev) {
+                   Lease &lease, const uint8_t **dev) {
     ThreadCtx &c = t_ctx;
-    if ((*dev = find_registered(blob, len, dtype, in_dim))) return RSLLM_HIP_OK;
+    if ((lease = find_registered(blob, len, dtype, in_dim))) {
+        *dev = lease.dev;
+        return RSLLM_HIP_OK;
+    }
     HIP_TRY(dst.ensure(len), "hipMalloc");
     if (dtype == T_F32 || !needs_prepare(dtype) || in_dim == 0) {
         if (len)
@@ -376,7 +437,8 @@ int validate_lora_down(size_t out_len, const void *w, size_t w_len, const void *
 
 // matmul_weight_f32 on device pointers (validated).
 int weight_f32_compute(float *out, size_t out_len, const uint8_t *w, size_t w_len, const float *x,
-                       size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype, hipStream_t s) {
+                       size_t n_tok, size_t in_dim, size_t out_dim, uint32_t dtype, hipStream_t s,
+                       Scratch &sc) {
     if (n_tok == 0 || out_dim == 0) return ok();
     if (in_dim == 0) {  // every dot is empty
         HIP_TRY(launch_fill_zero(out, out_len, s), "fill_zero");
@@ -388,8 +450,8 @@ int weight_f32_compute(float *out, size_t out_len, const uint8_t *w, size_t w_le
                 "gemv_f32");
         return ok();
     }
-    HIP_TRY(t_ctx.xq.ensure(gemv_work_bytes(dtype, (int)n_tok, (int)in_dim, (int)out_dim)), "hipMalloc");
-    HIP_TRY(launch_gemv(dtype, w, w_len, x, (uint8_t *)t_ctx.xq.p, out, (int)n_tok, (int)in_dim,
+    HIP_TRY(sc.xq.ensure(gemv_work_bytes(dtype, (int)n_tok, (int)in_dim, (int)out_dim)), "hipMalloc");
+    HIP_TRY(launch_gemv(dtype, w, w_len, x, (uint8_t *)sc.xq.p, out, (int)n_tok, (int)in_dim,
                         (int)out_dim, s),
             "gemv");
     return ok();
@@ -406,7 +468,7 @@ int weight_f32_compute(float *out, size_t out_len, const uint8_t *w, size_t w_le
 // own (only the per-group launches read it that way).
 int lora_down_compute(float *out, size_t out_len, const uint8_t *w, size_t stride, const float *x,
                       size_t n_tok, size_t n_groups, size_t group_dim, size_t rank,
-                      uint32_t dtype, hipStream_t s, bool group_layout = false) {
+                      uint32_t dtype, hipStream_t s, Scratch &sc, bool group_layout = false) {
     if (n_tok == 0 || n_groups == 0 || rank == 0) return ok();
     if (group_dim == 0) {
         HIP_TRY(launch_fill_zero(out, out_len, s), "fill_zero");
@@ -423,9 +485,8 @@ int lora_down_compute(float *out, size_t out_len, const uint8_t *w, size_t strid
     // 9 or more tokens of the matrix-core formats: one pass over the stacked
     // matrix per 16 tokens, on the matrix cores
     if (!group_layout && lora_mfma_supported(dtype, T, D, G, R)) {
-        ThreadCtx &c = t_ctx;
-        HIP_TRY(c.xq.ensure(lora_mfma_scratch_bytes(T, D, G)), "hipMalloc");
-        e = launch_lora_mfma(dtype, w, stride * n_groups, x, tin, out, tout, (uint8_t *)c.xq.p, T,
+        HIP_TRY(sc.xq.ensure(lora_mfma_scratch_bytes(T, D, G)), "hipMalloc");
+        e = launch_lora_mfma(dtype, w, stride * n_groups, x, tin, out, tout, (uint8_t *)sc.xq.p, T,
                              D, G, R, s);
         if (e == hipSuccess) return ok();
         if (e != hipErrorNotSupported) return dev_err(e, "lora_mfma");
@@ -444,16 +505,15 @@ int lora_down_compute(float *out, size_t out_len, const uint8_t *w, size_t strid
         return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED,
                        "matmul_grouped_lora_down: groups that do not end on a super-tile of the "
                        "device layout, with one group's x too long for LDS");
-    ThreadCtx &c = t_ctx;
-    HIP_TRY(c.xh.ensure((size_t)T * D * 4 + (size_t)T * R * 4), "hipMalloc");
-    HIP_TRY(c.xq.ensure(gemv_work_bytes(dtype, T, D, R)), "hipMalloc");
-    float *xg = (float *)c.xh.p, *yg = xg + (size_t)T * D;
+    HIP_TRY(sc.xh.ensure((size_t)T * D * 4 + (size_t)T * R * 4), "hipMalloc");
+    HIP_TRY(sc.xq.ensure(gemv_work_bytes(dtype, T, D, R)), "hipMalloc");
+    float *xg = (float *)sc.xh.p, *yg = xg + (size_t)T * D;
     for (int g = 0; g < G; g++) {
         const uint8_t *wg = w + (size_t)g * stride;
         HIP_TRY(hipMemcpy2DAsync(xg, (size_t)D * 4, x + (size_t)g * D, (size_t)tin * 4,
                                  (size_t)D * 4, (size_t)T, hipMemcpyDeviceToDevice, s),
                 "gather x");
-        HIP_TRY(launch_gemv(dtype, wg, stride, xg, (uint8_t *)c.xq.p, yg, T, D, R, s), "gemv");
+        HIP_TRY(launch_gemv(dtype, wg, stride, xg, (uint8_t *)sc.xq.p, yg, T, D, R, s), "gemv");
         HIP_TRY(hipMemcpy2DAsync(out + (size_t)g * R, (size_t)tout * 4, yg, (size_t)R * 4,
                                  (size_t)R * 4, (size_t)T, hipMemcpyDeviceToDevice, s),
                 "scatter y");
@@ -498,31 +558,32 @@ int validate_shared(size_t out_len, const void *out, size_t x_len, const void *x
 int shared_compute(float *out, const float *x, const uint8_t *gate, size_t gate_len,
                    uint32_t dt_gate, const uint8_t *up, size_t up_len, uint32_t dt_up,
                    const uint8_t *down, size_t down_len, uint32_t dt_down, size_t n_tok,
-                   size_t n_embd, size_t n_ff, float clamp, hipStream_t s) {
+                   size_t n_embd, size_t n_ff, float clamp, hipStream_t s, Scratch &sc) {
     if (n_tok == 0 || n_embd == 0) return ok();
-    ThreadCtx &c = t_ctx;
     const int T = (int)n_tok, E = (int)n_embd, FF = (int)n_ff;
     if (dt_gate == dt_up && dt_gate != T_F32 && gate_len == up_len && n_ff &&
         gemv_rows_fits(dt_gate, E)) {
         const size_t hb = (n_tok * n_ff * 8 + 255) / 256 * 256;
-        HIP_TRY(c.xh.ensure(hb + n_tok * n_ff * 4 + 256), "hipMalloc");
-        float *h = (float *)c.xh.p, *act = (float *)((uint8_t *)c.xh.p + hb);
+        HIP_TRY(sc.xh.ensure(hb + n_tok * n_ff * 4 + 256), "hipMalloc");
+        float *h = (float *)sc.xh.p, *act = (float *)((uint8_t *)sc.xh.p + hb);
         HIP_TRY(launch_gemv_pair(dt_gate, gate, up, gate_len, x, h, T, E, FF, 2 * FF, s),
                 "gemv_pair");
         HIP_TRY(launch_swiglu_pair(h, act, T, FF, clamp, s), "swiglu");
         return weight_f32_compute(out, n_tok * n_embd, down, down_len, act, n_tok, n_ff, n_embd,
-                                  dt_down, s);
+                                  dt_down, s, sc);
     }
     const size_t hb = (n_tok * n_ff * 4 + 255) / 256 * 256;
-    HIP_TRY(c.xh.ensure(3 * hb + 256), "hipMalloc");
-    float *hg = (float *)c.xh.p, *hu = (float *)((uint8_t *)c.xh.p + hb),
-          *ha = (float *)((uint8_t *)c.xh.p + 2 * hb);
-    int rc = weight_f32_compute(hg, n_tok * n_ff, gate, gate_len, x, n_tok, n_embd, n_ff, dt_gate, s);
-    if (!rc) rc = weight_f32_compute(hu, n_tok * n_ff, up, up_len, x, n_tok, n_embd, n_ff, dt_up, s);
+    HIP_TRY(sc.xh.ensure(3 * hb + 256), "hipMalloc");
+    float *hg = (float *)sc.xh.p, *hu = (float *)((uint8_t *)sc.xh.p + hb),
+          *ha = (float *)((uint8_t *)sc.xh.p + 2 * hb);
+    int rc = weight_f32_compute(hg, n_tok * n_ff, gate, gate_len, x, n_tok, n_embd, n_ff, dt_gate, s,
+                                sc);
+    if (!rc)
+        rc = weight_f32_compute(hu, n_tok * n_ff, up, up_len, x, n_tok, n_embd, n_ff, dt_up, s, sc);
     if (rc) return rc;
     HIP_TRY(launch_swiglu(hg, hu, ha, n_tok * n_ff, clamp, s), "swiglu");
     return weight_f32_compute(out, n_tok * n_embd, down, down_len, ha, n_tok, n_ff, n_embd,
-                              dt_down, s);
+                              dt_down, s, sc);
 }
 
 }  // namespace
@@ -534,20 +595,38 @@ int ok_status() { return ok(); }
 int device_error(hipError_t e, const char *where) { return dev_err(e, where); }
 int ensure_current_device() { return ensure_device(); }
 void registry_add(const uint8_t *host, size_t len, uint32_t dtype, size_t in_dim, uint8_t *dev,
-                  uint64_t owner) {
+                  uint64_t owner, std::shared_ptr<void> keep) {
     std::lock_guard<std::mutex> lk(g_mu);
-    for (const auto &r : g_registry)
-        if (r.host == host && r.len == len && r.dtype == dtype && r.in_dim == in_dim &&
-            r.dev == dev && r.owner == owner)
+    const auto range = g_registry.equal_range(host);
+    for (auto it = range.first; it != range.second; ++it) {
+        const Registered &r = it->second;
+        if (r.len == len && r.dtype == dtype && r.in_dim == in_dim && r.dev == dev &&
+            r.owner == owner)
             return;
-    g_registry.push_back({host, len, dtype, in_dim, dev, owner});
+    }
+    g_registry.emplace(host, Registered{len, dtype, in_dim, dev, owner, std::move(keep)});
 }
 void registry_drop_owner(uint64_t owner) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    std::vector<Registered> keep;
-    for (auto &r : g_registry)
-        if (r.owner != owner) keep.push_back(r);
-    g_registry.swap(keep);
+    std::vector<std::shared_ptr<void>> drop;  // released after the lock
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        for (auto it = g_registry.begin(); it != g_registry.end();) {
+            if (it->second.owner == owner) {
+                drop.push_back(std::move(it->second.keep));
+                it = g_registry.erase(it);
+            } else {
+                ++it;
+            }
+        }
+    }
+}
+DevMem::~DevMem() {
+    if (!p) return;
+    int cur = -1;
+    const bool other = hipGetDevice(&cur) == hipSuccess && cur != device;
+    if (other) (void)hipSetDevice(device);
+    (void)hipFree(p);
+    if (other) (void)hipSetDevice(cur);
 }
 }  // namespace rsllm_hip::abi
 
@@ -603,8 +682,9 @@ int rsllm_hip_matmul_quant_f32_dev(float *out, size_t out_len, const uint8_t *we
         return ok();
     }
     if ((rc = ensure_device())) return rc;
-    HIP_TRY(t_ctx.xq.ensure(gemv_work_bytes(dtype, (int)n_tok, (int)in_dim, (int)out_dim)), "hipMalloc");
-    HIP_TRY(launch_gemv(dtype, weights, weights_len, x, (uint8_t *)t_ctx.xq.p, out, (int)n_tok,
+    ScratchLease sc = stream_scratch(s);
+    HIP_TRY(sc->xq.ensure(gemv_work_bytes(dtype, (int)n_tok, (int)in_dim, (int)out_dim)), "hipMalloc");
+    HIP_TRY(launch_gemv(dtype, weights, weights_len, x, (uint8_t *)sc->xq.p, out, (int)n_tok,
                         (int)in_dim, (int)out_dim, s),
             "gemv");
     return ok();
@@ -655,7 +735,8 @@ int rsllm_hip_matmul_quant_f32(float *out, size_t out_len, const uint8_t *weight
     }
     if ((rc = ensure_device())) return rc;
     ThreadCtx &c = t_ctx;
-    const uint8_t *dw = find_registered(weights, weights_len, dtype, in_dim);
+    const Lease reg = find_registered(weights, weights_len, dtype, in_dim);
+    const uint8_t *dw = reg.dev;
     if (!dw) {
         HIP_TRY(c.w_raw.ensure(weights_len), "hipMalloc");
         HIP_TRY(hipMemcpyAsync(c.w_raw.p, weights, weights_len, hipMemcpyHostToDevice, c.stream),
@@ -672,8 +753,9 @@ int rsllm_hip_matmul_quant_f32(float *out, size_t out_len, const uint8_t *weight
     HIP_TRY(c.y.ensure(out_len * sizeof(float)), "hipMalloc");
     HIP_TRY(hipMemcpyAsync(c.x.p, x, x_len * sizeof(float), hipMemcpyHostToDevice, c.stream),
             "upload x");
-    HIP_TRY(c.xq.ensure(gemv_work_bytes(dtype, (int)n_tok, (int)in_dim, (int)out_dim)), "hipMalloc");
-    HIP_TRY(launch_gemv(dtype, dw, weights_len, (const float *)c.x.p, (uint8_t *)c.xq.p,
+    ScratchLease sc = stream_scratch(c.stream);
+    HIP_TRY(sc->xq.ensure(gemv_work_bytes(dtype, (int)n_tok, (int)in_dim, (int)out_dim)), "hipMalloc");
+    HIP_TRY(launch_gemv(dtype, dw, weights_len, (const float *)c.x.p, (uint8_t *)sc->xq.p,
                         (float *)c.y.p, (int)n_tok, (int)in_dim, (int)out_dim, c.stream),
             "gemv");
     HIP_TRY(hipMemcpyAsync(out, c.y.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
@@ -754,8 +836,9 @@ int rsllm_hip_matmul_q4k_bf16_dev(float *out, size_t out_len, const uint8_t *wei
         return ok();
     }
     if ((rc = ensure_device())) return rc;
-    HIP_TRY(t_ctx.xh.ensure(prefill_scratch_bytes((int)n_tok, (int)in_dim)), "hipMalloc");
-    HIP_TRY(launch_prefill_q4k(weights, weights_len, x_bf16, (uint8_t *)t_ctx.xh.p, out,
+    ScratchLease sc = stream_scratch(s);
+    HIP_TRY(sc->xh.ensure(prefill_scratch_bytes((int)n_tok, (int)in_dim)), "hipMalloc");
+    HIP_TRY(launch_prefill_q4k(weights, weights_len, x_bf16, (uint8_t *)sc->xh.p, out,
                                (int)n_tok, (int)in_dim, (int)out_dim, s),
             "prefill_q4k");
     return ok();
@@ -830,11 +913,12 @@ int rsllm_hip_moe_routed_dev(float *out, size_t out_len, const float *x, size_t 
     if (rc) return rc;
     if (n_tok == 0 || k == 0) return ok();
     if ((rc = ensure_device())) return rc;
-    HIP_TRY(t_ctx.moe.ensure(moe_scratch_bytes(dtype_gate_up, dtype_down, (int)n_tok, (int)k,
-                                               (int)n_expert, (int)n_embd, (int)n_ff)),
+    ScratchLease sc = stream_scratch((hipStream_t)stream);
+    HIP_TRY(sc->moe.ensure(moe_scratch_bytes(dtype_gate_up, dtype_down, (int)n_tok, (int)k,
+                                             (int)n_expert, (int)n_embd, (int)n_ff)),
             "hipMalloc");
     HIP_TRY(launch_moe(dtype_gate_up, dtype_down, gate, up, down, gate_up_len / n_expert,
-                       down_len / n_expert, x, ids, weights, out, (uint8_t *)t_ctx.moe.p,
+                       down_len / n_expert, x, ids, weights, out, (uint8_t *)sc->moe.p,
                        (int)n_tok, (int)k, (int)n_expert, (int)n_embd, (int)n_ff, clamp,
                        (hipStream_t)stream),
             "moe");
@@ -865,8 +949,9 @@ int rsllm_hip_moe_routed(float *out, size_t out_len, const float *x, size_t x_le
     const uint32_t bdt[3] = {dtype_gate_up, dtype_gate_up, dtype_down};
     const size_t bin[3] = {n_embd, n_embd, n_ff};
     const uint8_t *dev[3];
+    Lease reg[3];
     for (int i = 0; i < 3; i++)
-        if ((rc = blob_on_device(blob[i], blen[i], bdt[i], bin[i], c.moe_w[i], &dev[i])))
+        if ((rc = blob_on_device(blob[i], blen[i], bdt[i], bin[i], c.moe_w[i], reg[i], &dev[i])))
             return rc;
     // inputs: x | out | ids | weights, 256-byte aligned pieces
     const size_t a_x = (x_len * 4 + 255) / 256 * 256, a_o = (out_len * 4 + 255) / 256 * 256;
@@ -881,11 +966,12 @@ int rsllm_hip_moe_routed(float *out, size_t out_len, const float *x, size_t x_le
     HIP_TRY(hipMemcpyAsync(d_ids, ids, ids_len * 4, hipMemcpyHostToDevice, c.stream), "upload ids");
     HIP_TRY(hipMemcpyAsync(d_w, weights, ids_len * 4, hipMemcpyHostToDevice, c.stream),
             "upload weights");
-    HIP_TRY(c.moe.ensure(moe_scratch_bytes(dtype_gate_up, dtype_down, (int)n_tok, (int)k,
-                                           (int)n_expert, (int)n_embd, (int)n_ff)),
+    ScratchLease sc = stream_scratch(c.stream);
+    HIP_TRY(sc->moe.ensure(moe_scratch_bytes(dtype_gate_up, dtype_down, (int)n_tok, (int)k,
+                                             (int)n_expert, (int)n_embd, (int)n_ff)),
             "hipMalloc");
     HIP_TRY(launch_moe(dtype_gate_up, dtype_down, dev[0], dev[1], dev[2], gate_up_len / n_expert,
-                       down_len / n_expert, d_x, d_ids, d_w, d_out, (uint8_t *)c.moe.p,
+                       down_len / n_expert, d_x, d_ids, d_w, d_out, (uint8_t *)sc->moe.p,
                        (int)n_tok, (int)k, (int)n_expert, (int)n_embd, (int)n_ff, clamp, c.stream),
             "moe");
     HIP_TRY(hipMemcpyAsync(out, d_out, out_len * 4, hipMemcpyDeviceToHost, c.stream),
@@ -1030,7 +1116,8 @@ int rsllm_hip_matmul_q8_0_batch(float *out, size_t out_len, const uint8_t *weigh
     ThreadCtx &c = t_ctx;
     // device layout: a registered copy (Q8_0 with this in_dim), else the rows
     // uploaded and regrouped for this call
-    const uint8_t *dw = find_registered(weights, weights_len, T_Q8_0, in_dim);
+    const Lease reg = find_registered(weights, weights_len, T_Q8_0, in_dim);
+    const uint8_t *dw = reg.dev;
     if (!dw) {
         HIP_TRY(c.w_raw.ensure(weights_len), "hipMalloc");
         HIP_TRY(c.w_dev.ensure(weights_len), "hipMalloc");
@@ -1074,42 +1161,54 @@ int rsllm_hip_register_weights(const uint8_t *weights, size_t weights_len, uint3
     if (find_registered(weights, weights_len, dtype, in_dim)) return ok();
     int rc = ensure_device();
     if (rc) return rc;
-    uint8_t *raw = nullptr, *dev = nullptr;
-    HIP_TRY(hipMalloc(&dev, weights_len ? weights_len : 1), "hipMalloc");
+    auto mem = std::make_shared<abi::DevMem>();
+    HIP_TRY(hipGetDevice(&mem->device), "hipGetDevice");
+    HIP_TRY(hipMalloc(&mem->p, weights_len ? weights_len : 1), "hipMalloc");
     hipError_t e;
     if (!needs_prepare(dtype)) {
-        e = hipMemcpy(dev, weights, weights_len, hipMemcpyHostToDevice);
+        e = hipMemcpy(mem->p, weights, weights_len, hipMemcpyHostToDevice);
     } else {
+        uint8_t *raw = nullptr;
         e = hipMalloc(&raw, weights_len ? weights_len : 1);
         if (e == hipSuccess) e = hipMemcpy(raw, weights, weights_len, hipMemcpyHostToDevice);
         if (e == hipSuccess)
-            e = launch_prepare(dtype, raw, dev, weights_len / rb, in_dim, t_ctx.stream);
+            e = launch_prepare(dtype, raw, mem->p, weights_len / rb, in_dim, t_ctx.stream);
         if (e == hipSuccess) e = hipStreamSynchronize(t_ctx.stream);
         if (raw) (void)hipFree(raw);
     }
-    if (e != hipSuccess) {
-        (void)hipFree(dev);
-        return dev_err(e, "register_weights");
-    }
-    std::lock_guard<std::mutex> lk(g_mu);
-    g_registry.push_back({weights, weights_len, dtype, in_dim, dev, 0});
+    if (e != hipSuccess) return dev_err(e, "register_weights");
+    // a thread that registered the same tensor meanwhile wins; this copy is
+    // then dropped (freed) when `mem` goes out of scope
+    if (find_registered(weights, weights_len, dtype, in_dim)) return ok();
+    uint8_t *dev = mem->p;
+    abi::registry_add(weights, weights_len, dtype, in_dim, dev, 0, std::move(mem));
     return ok();
 }
 
 int rsllm_hip_release_weights(void) {
-    std::vector<Registered> regs;
+    // the entries' references are dropped after the lock: an allocation no
+    // call holds is freed here (hipFree waits for the device first); one a
+    // call in flight still holds is freed when that call drops it
+    int rc = ensure_device();
+    if (rc) return rc;
+    abi::registry_drop_owner(0);
+    return ok();
+}
+
+int rsllm_hip_stream_release(rsllm_hip_stream_t stream) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+    std::shared_ptr<Scratch> gone;
     {
-        std::lock_guard<std::mutex> lk(g_mu);
-        std::vector<Registered> keep;
-        for (auto &r : g_registry) (r.owner ? keep : regs).push_back(r);
-        g_registry.swap(keep);
+        std::lock_guard<std::mutex> lk(g_scratch_map_mu);
+        auto it = g_scratch_map->find({dev, (hipStream_t)stream});
+        if (it != g_scratch_map->end()) {
+            gone = std::move(it->second);
+            g_scratch_map->erase(it);
+        }
     }
-    if (!regs.empty()) {
-        int rc = ensure_device();
-        if (rc) return rc;
-        HIP_TRY(hipDeviceSynchronize(), "hipDeviceSynchronize");
-        for (auto &r : regs) (void)hipFree(r.dev);
-    }
+    // freed here, or by the last call still holding the set
+    gone.reset();
     return ok();
 }
 
@@ -1169,8 +1268,9 @@ int rsllm_hip_matmul_weight_f32_dev(float *out, size_t out_len, const uint8_t *w
                                  out_dim, dtype);
     if (rc) return rc;
     if ((rc = ensure_device())) return rc;
+    ScratchLease sc = stream_scratch((hipStream_t)stream);
     return weight_f32_compute(out, out_len, weights, weights_len, x, n_tok, in_dim, out_dim, dtype,
-                              (hipStream_t)stream);
+                              (hipStream_t)stream, *sc);
 }
 
 int rsllm_hip_matmul_weight_f32(float *out, size_t out_len, const uint8_t *weights,
@@ -1182,7 +1282,8 @@ int rsllm_hip_matmul_weight_f32(float *out, size_t out_len, const uint8_t *weigh
     if (n_tok == 0 || out_dim == 0) return ok();
     if ((rc = ensure_device())) return rc;
     ThreadCtx &c = t_ctx;
-    const uint8_t *dw = find_registered(weights, weights_len, dtype, in_dim);
+    const Lease reg = find_registered(weights, weights_len, dtype, in_dim);
+    const uint8_t *dw = reg.dev;
     if (!dw && weights_len) {
         HIP_TRY(c.w_raw.ensure(weights_len), "hipMalloc");
         HIP_TRY(hipMemcpyAsync(c.w_raw.p, weights, weights_len, hipMemcpyHostToDevice, c.stream),
@@ -1200,8 +1301,9 @@ int rsllm_hip_matmul_weight_f32(float *out, size_t out_len, const uint8_t *weigh
     if (x_len)
         HIP_TRY(hipMemcpyAsync(c.x.p, x, x_len * sizeof(float), hipMemcpyHostToDevice, c.stream),
                 "upload x");
+    ScratchLease sc = stream_scratch(c.stream);
     rc = weight_f32_compute((float *)c.y.p, out_len, dw, weights_len, (const float *)c.x.p, n_tok,
-                            in_dim, out_dim, dtype, c.stream);
+                            in_dim, out_dim, dtype, c.stream, *sc);
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(out, c.y.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
             "download out");
@@ -1219,8 +1321,9 @@ int rsllm_hip_matmul_grouped_lora_down_dev(float *out, size_t out_len, const uin
                                 group_dim, rank, dtype, &stride);
     if (rc) return rc;
     if ((rc = ensure_device())) return rc;
+    ScratchLease sc = stream_scratch((hipStream_t)stream);
     return lora_down_compute(out, out_len, weights, stride, x, n_tok, n_groups, group_dim, rank,
-                             dtype, (hipStream_t)stream);
+                             dtype, (hipStream_t)stream, *sc);
 }
 
 int rsllm_hip_matmul_grouped_lora_down(float *out, size_t out_len, const uint8_t *weights,
@@ -1246,9 +1349,10 @@ int rsllm_hip_matmul_grouped_lora_down(float *out, size_t out_len, const uint8_t
     const bool prep = dtype != T_F32 && needs_prepare(dtype) && group_dim;
     const bool per_group = prep && (rank * (group_dim / block_elems_of(dtype))) % 8 != 0 &&
                            !gemv_rows_fits(dtype, (int)group_dim);
-    const uint8_t *dw = used != weights_len || per_group
-                            ? nullptr
-                            : find_registered(weights, weights_len, dtype, group_dim);
+    const Lease reg = used != weights_len || per_group
+                          ? Lease{}
+                          : find_registered(weights, weights_len, dtype, group_dim);
+    const uint8_t *dw = reg.dev;
     if (!dw) {
         HIP_TRY(c.w_raw.ensure(used), "hipMalloc");
         HIP_TRY(hipMemcpyAsync(c.w_raw.p, weights, used, hipMemcpyHostToDevice, c.stream),
@@ -1274,8 +1378,9 @@ int rsllm_hip_matmul_grouped_lora_down(float *out, size_t out_len, const uint8_t
     if (x_len)
         HIP_TRY(hipMemcpyAsync(c.x.p, x, x_len * sizeof(float), hipMemcpyHostToDevice, c.stream),
                 "upload x");
+    ScratchLease sc = stream_scratch(c.stream);
     rc = lora_down_compute((float *)c.y.p, out_len, dw, stride, (const float *)c.x.p, n_tok,
-                           n_groups, group_dim, rank, dtype, c.stream, per_group);
+                           n_groups, group_dim, rank, dtype, c.stream, *sc, per_group);
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(out, c.y.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
             "download out");
@@ -1294,8 +1399,10 @@ int rsllm_hip_apply_shared_expert_dev(float *out, size_t out_len, const float *x
                              dtype_up, down, down_len, dtype_down, n_tok, n_embd, n_ff);
     if (rc) return rc;
     if ((rc = ensure_device())) return rc;
+    ScratchLease sc = stream_scratch((hipStream_t)stream);
     return shared_compute(out, x, gate, gate_len, dtype_gate, up, up_len, dtype_up, down,
-                          down_len, dtype_down, n_tok, n_embd, n_ff, clamp, (hipStream_t)stream);
+                          down_len, dtype_down, n_tok, n_embd, n_ff, clamp, (hipStream_t)stream,
+                          *sc);
 }
 
 int rsllm_hip_apply_shared_expert(float *out, size_t out_len, const float *x, size_t x_len,
@@ -1314,16 +1421,18 @@ int rsllm_hip_apply_shared_expert(float *out, size_t out_len, const float *x, si
     const uint32_t bdt[3] = {dtype_gate, dtype_up, dtype_down};
     const size_t bin[3] = {n_embd, n_embd, n_ff};
     const uint8_t *dev[3];
+    Lease reg[3];
     for (int i = 0; i < 3; i++)
-        if ((rc = blob_on_device(blob[i], blen[i], bdt[i], bin[i], c.moe_w[i], &dev[i])))
+        if ((rc = blob_on_device(blob[i], blen[i], bdt[i], bin[i], c.moe_w[i], reg[i], &dev[i])))
             return rc;
     HIP_TRY(c.x.ensure(x_len * sizeof(float) + 16), "hipMalloc");
     HIP_TRY(c.y.ensure(out_len * sizeof(float)), "hipMalloc");
     HIP_TRY(hipMemcpyAsync(c.x.p, x, x_len * sizeof(float), hipMemcpyHostToDevice, c.stream),
             "upload x");
+    ScratchLease sc = stream_scratch(c.stream);
     rc = shared_compute((float *)c.y.p, (const float *)c.x.p, dev[0], gate_len, dtype_gate, dev[1],
                         up_len, dtype_up, dev[2], down_len, dtype_down, n_tok, n_embd, n_ff, clamp,
-                        c.stream);
+                        c.stream, *sc);
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(out, c.y.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c.stream),
             "download out");

@@ -7,8 +7,22 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <memory>
 
 namespace rsllm_hip::abi {
+
+// A device allocation, freed when the last reference to it goes (hipFree,
+// which synchronises the device first, on the device it was made on).
+// Registry entries and the calls that use them share ownership, so memory a
+// call is reading is never freed under it.
+struct DevMem {
+    uint8_t *p = nullptr;
+    int device = 0;
+    DevMem() = default;
+    DevMem(const DevMem &) = delete;
+    DevMem &operator=(const DevMem &) = delete;
+    ~DevMem();
+};
 
 // Record the calling thread's error (rsllm_hip_last_error) and return status.
 int set_error(int status, const char *msg);
@@ -20,10 +34,12 @@ int device_error(hipError_t e, const char *where);
 // stream); returns a status.
 int ensure_current_device();
 // Host tensor (host, len, dtype, in_dim) -> device copy at dev, owned by the
-// uploaded model `owner` (never 0). Host-pointer entry points find it.
+// uploaded model `owner` (never 0), inside the allocation `keep` holds alive.
+// Host-pointer entry points find it.
 void registry_add(const uint8_t *host, size_t len, uint32_t dtype, size_t in_dim, uint8_t *dev,
-                  uint64_t owner);
-// Remove every entry of one owner.
+                  uint64_t owner, std::shared_ptr<void> keep);
+// Remove every entry of one owner (memory still used by a call in flight is
+// freed when that call drops its reference).
 void registry_drop_owner(uint64_t owner);
 
 }  // namespace rsllm_hip::abi

@@ -56,6 +56,9 @@ struct Model {
     uint64_t digest;
     int device;
     std::vector<Tensor> t;
+    // the arena; registry entries of the model share it, so it is freed when
+    // the model is released and no call in flight still reads it
+    std::shared_ptr<abi::DevMem> mem;
     uint8_t *arena = nullptr;
     size_t arena_bytes = 0;
     uint32_t refs = 0;
@@ -213,7 +216,7 @@ void register_host_ranges(const Model &m, const rsllm_hip_tensor_desc *d) {
     for (size_t i = 0; i < m.t.size(); i++)
         if (m.t[i].matmul)
             abi::registry_add(d[i].data, d[i].len, d[i].dtype, d[i].in_dim, m.arena + m.t[i].off,
-                              m.id);
+                              m.id, m.mem);
 }
 
 Model *find_model(uint64_t id) {
@@ -269,12 +272,12 @@ int rsllm_hip_model_upload(const uint8_t *fingerprint, const rsllm_hip_tensor_de
     }
     m->arena_bytes = off;
     const auto t0 = std::chrono::steady_clock::now();
-    if (off) HIP_TRY(hipMalloc((void **)&m->arena, off), "hipMalloc arena");
+    m->mem = std::make_shared<abi::DevMem>();
+    m->mem->device = dev;
+    if (off) HIP_TRY(hipMalloc((void **)&m->mem->p, off), "hipMalloc arena");
+    m->arena = m->mem->p;
     rc = upload(*m, tensors, n_tensors);
-    if (rc) {
-        (void)hipFree(m->arena);
-        return rc;
-    }
+    if (rc) return rc;  // m (and its arena) is dropped
     m->seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     m->refs = 1;
     register_host_ranges(*m, tensors);
@@ -328,11 +331,11 @@ int rsllm_hip_model_release(uint64_t model) {
             return abi::set_error(RSLLM_HIP_ERR_INVALID_ARGUMENT, "model_release: unknown model");
     }
     if (gone) {
+        // the registry's references go first; the arena is freed when the
+        // model's own reference below and every call in flight that found
+        // one of its tensors have let go (hipFree waits for the device)
         abi::registry_drop_owner(gone->id);
-        int rc = abi::ensure_current_device();
-        if (rc) return rc;
-        HIP_TRY(hipDeviceSynchronize(), "hipDeviceSynchronize");
-        (void)hipFree(gone->arena);
+        gone.reset();
     }
     return abi::ok_status();
 }
