@@ -283,10 +283,13 @@ int rsllm_hip_matmul_q4k_bf16_dev(float *out, size_t out_len, const uint8_t *wei
  * expert's block count to be a multiple of 8. ids, weights: n_tok * k.
  * Validation: dtypes, then n_embd % block(gate/up) and n_ff % block(down)
  * (NotBlockAligned), blob lengths, x, out, ids lengths (ShapeMismatch);
- * n_tok * k <= 4096. The reference panics on an expert id out of range:
- * the host entry point returns RSLLM_HIP_ERR_INVALID_ARGUMENT, the device
- * entry point (which cannot inspect ids) skips such slots. Uses a
- * per-thread device workspace. */
+ * n_expert <= 16384. Any number of tokens (the reference's prefill passes
+ * every token of the forward pass, moe.rs:281,346): calls of more than 8192
+ * (token, slot) pairs run in token chunks, each routed and computed on its
+ * own, which gives the same result. The reference panics on an expert id
+ * out of range: the host entry point returns RSLLM_HIP_ERR_INVALID_ARGUMENT,
+ * the device entry point (which cannot inspect ids) skips such slots. Uses
+ * the stream's device workspace. */
 int rsllm_hip_moe_routed_dev(float *out, size_t out_len, const float *x, size_t x_len,
                              const uint8_t *gate, const uint8_t *up, size_t gate_up_len,
                              const uint8_t *down, size_t down_len, const int32_t *ids,

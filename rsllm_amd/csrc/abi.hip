@@ -561,7 +561,13 @@ int shared_compute(float *out, const float *x, const uint8_t *gate, size_t gate_
                    size_t n_embd, size_t n_ff, float clamp, hipStream_t s, Scratch &sc) {
     if (n_tok == 0 || n_embd == 0) return ok();
     const int T = (int)n_tok, E = (int)n_embd, FF = (int)n_ff;
-    if (dt_gate == dt_up && dt_gate != T_F32 && gate_len == up_len && n_ff &&
+    // gate and up of one quant format as one paired launch per chunk of up
+    // to 8 tokens; from 9 tokens the matrix-core formats run gate and up as
+    // two matrix-core GEMVs instead (one pass over each matrix per 16 or 32
+    // tokens, exact weights)
+    const bool mfma_gu = T >= 9 && gemv_mfma_supported(dt_gate, T, E, FF) &&
+                         gemv_mfma_supported(dt_up, T, E, FF);
+    if (!mfma_gu && dt_gate == dt_up && dt_gate != T_F32 && gate_len == up_len && n_ff &&
         gemv_rows_fits(dt_gate, E)) {
         const size_t hb = (n_tok * n_ff * 8 + 255) / 256 * 256;
         HIP_TRY(sc.xh.ensure(hb + n_tok * n_ff * 4 + 256), "hipMalloc");
@@ -886,8 +892,9 @@ static int validate_moe(size_t out_len, size_t x_len, size_t gate_up_len, size_t
         return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED,
                        "moe_routed: dtype accepted by the reference is not implemented by the "
                        "HIP backend");
-    if (ids_len > 4096)
-        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT, "moe_routed: n_tok * k must be <= 4096");
+    if (n_expert > 16384)
+        return set_err(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                       "moe_routed: n_expert above 16384 is not supported");
     if (!fits_int(n_tok) || !fits_int(n_embd) || !fits_int(n_ff) || !fits_int(n_expert) ||
         !fits_int(k) || gate_up_len / n_expert > kMaxWeightBytes ||
         down_len / n_expert > kMaxWeightBytes)

@@ -4,26 +4,28 @@
 // Restates matmul_quant_f32 (rsllm-backend-cpu/src/ops/quant_matmul.rs:45-119)
 // for the decode batches of C1/C2-style shapes, where the int8-limb GEMV
 // (gemv.hip) spends VALU work per (weight, token) pair and stops being
-// memory-bound above a few tokens. Here each weight is dequantised once to
-// f16 in registers — f16(d*sc)*q - f16(dmin*m) for Q4_K (one rounding, as the
-// prefill GEMM), (q - 32)*f16(d*sc) for Q6_K (q - 32 exact, one rounding),
-// q*d for Q8_0 (q exact, one rounding) —
-// and the tokens are the N dimension of v_mfma_f32_16x16x32_f16 (16 or 32
-// tokens per pass, fp32 accumulation), so the dequant cost is independent of
-// the batch.
+// memory-bound above a few tokens. Here each weight is decoded once per pass
+// into an exact f16 integer — Q4_K sc*q, Q6_K sc*(q - 32), Q8_0 q — the B
+// operand of v_mfma_f32_16x16x32_f16, against 16 tokens of activations as
+// the A operand (fp32 accumulation), so the decode cost is independent of
+// the batch. The per-row scales the reference applies in f32 (d, and
+// dmin*m for Q4_K through a second MFMA with B = m) multiply each step's
+// MFMA result in fp32: the weights reach the products exactly.
 //
 // Activations: a pre-pass scales each token by 2^e (max |x| into
 // [2^14, 2^15)) and stores it as f16 in MFMA operand order,
 //   xh[((s * 4 + j) * 4 + q) * ntp + t][0..7] = f16(2^e_t x[t, F::elem(s, j, q) + 0..7]),
 // s = K step of 128 elements, j = MFMA of the step, q = lane group, ntp =
 // padded token count (16 or 32, padding tokens zero); unscale[t] = 2^-e_t.
+// That f16 rounding (at most 2^-11 relative per element) is the only one.
 //
 // Kernel: workgroup = NK wavefronts over the same 16*RT weight rows; wavefront
 // w takes K steps [w * nsteps / NK, (w + 1) * nsteps / NK) with the next
 // step's weights and activations in flight while the current one is
-// computed. Lane (r, q) = (lane % 16, lane / 16) dequantises 32 weights of
-// row r per step (8 for each of the 4 MFMAs). The NK partial tiles are added
-// through LDS in wavefront order (deterministic), scaled by 2^-e_t, stored.
+// computed. Lane (r, q) = (lane % 16, lane / 16) decodes 32 weights of
+// row r per step (8 for each of the 4 MFMAs) and holds D for tokens 4q + 0..3
+// of row r. The NK partial tiles are added through LDS in wavefront order
+// (deterministic), scaled by 2^-e_t, stored.
 #include "gemv_formats.h"
 
 namespace rsllm_hip {
@@ -49,10 +51,32 @@ __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t vo
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0);
 }
 
+// The weights are the B operand of v_mfma_f32_16x16x32_f16 (K x 16 weight
+// rows) and the activations the A operand (16 tokens x K), so lane
+// (r16, q) = (lane % 16, lane / 16) supplies weights of row r16 and receives
+// D[4q + i][r16], i = 0..3: four tokens of its own row. Every B value is an
+// exact integer in f16 — Q4_K sc * q (at most 63 * 15), Q6_K sc * (q - 32)
+// (|.| <= 2048), Q8_0 q — and the per-row scales the reference multiplies
+// in f32 (d, dmin * m) are applied to each step's MFMA result in fp32 by the
+// lane that holds that row. Products of two f16 values are exact in fp32,
+// so the weights are exact; the one rounding left is f16(2^e x).
+//
+// Each format gives: W (a lane's bytes for one step), elem / piece (the K
+// order: element of MFMA j, lane group q, step s), load, and step<NT>: the
+// MFMAs of one step for one 16-row tile against NT token tiles, folded into
+// acc[NT] with the scales.
+
+__device__ __forceinline__ f32x4 mfma16x32(const uint4 &x, const f16x8 &w, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, x), w, c, 0, 0, 0);
+}
+
 // Q4_K (GGUF layout). Step s = half (s & 1) of super-block s >> 1. Lane group
 // q reads qs bytes 32q + 16 (s & 1) .. + 15 (sub-block pair q): low nibbles are
 // sub-block 2q, positions 16 (s & 1) + 0..15; high nibbles sub-block 2q + 1.
 // MFMA j: low (j even) / high (j odd) nibbles of bytes 0..7 (j < 2) or 8..15.
+// B = sc_j * q (exact); a second MFMA per j with B = m_j gives sum m_j x, and
+// the step adds d * P - dmin * M (dequant_q4_k, q4_k.rs:66-88: w = d sc q -
+// dmin m).
 struct MQ4K {
     struct W {
         uint4 hdr, qs;
@@ -73,10 +97,11 @@ struct MQ4K {
         w.hdr = bload16(r, off, 0);
         w.qs = bload16(r, off + 16u + 32u * (uint32_t)q + 16u * (uint32_t)(s & 1), 0);
     }
-    __device__ static void dequant(const W &w, int q, int, f16x8 (&a)[4]) {
+    template <int NT>
+    __device__ static void step(const W &w, int q, const uint4 (&x)[4][NT], const uint4 (&xl)[4][NT],
+                                f32x4 (&acc)[NT]) {
         const float d = f16_to_f32(w.hdr.x & 0xFFFFu), dmin = f16_to_f32(w.hdr.x >> 16);
-        // (sc, m) of sub-blocks 2q and 2q + 1 (q4_k_scale_min, dequant/mod.rs:48-58),
-        // both forms computed and selected per lane
+        // (sc, m) of sub-blocks 2q and 2q + 1 (q4_k_scale_min, dequant/mod.rs:48-58)
         const uint32_t s0 = w.hdr.y, s1 = w.hdr.z, s2 = w.hdr.w;
         uint32_t sc[2], m[2];
 #pragma unroll
@@ -90,32 +115,50 @@ struct MQ4K {
             sc[u] = jj < 4 ? lo_sc : hi_sc;
             m[u] = jj < 4 ? lo_m : hi_m;
         }
-        const _Float16 dl = (_Float16)(d * (float)sc[0]), ml = (_Float16)(dmin * (float)m[0]);
-        const _Float16 dh = (_Float16)(d * (float)sc[1]), mh = (_Float16)(dmin * (float)m[1]);
-        const f16x2 dsl = {dl, dl}, dml = {ml, ml}, dsh = {dh, dh}, dmh = {mh, mh};
-        a[0] = dequant_q4x8_f16(w.qs.x, w.qs.y, false, dsl, dml);
-        a[1] = dequant_q4x8_f16(w.qs.x, w.qs.y, true, dsh, dmh);
-        a[2] = dequant_q4x8_f16(w.qs.z, w.qs.w, false, dsl, dml);
-        a[3] = dequant_q4x8_f16(w.qs.z, w.qs.w, true, dsh, dmh);
+        const _Float16 sl = (_Float16)(float)sc[0], sh = (_Float16)(float)sc[1];
+        const f16x2 zero = {(_Float16)0.0f, (_Float16)0.0f};
+        const f16x2 ssl = {sl, sl}, ssh = {sh, sh};
+        f16x8 b[4];
+        b[0] = dequant_q4x8_f16(w.qs.x, w.qs.y, false, ssl, zero);
+        b[1] = dequant_q4x8_f16(w.qs.x, w.qs.y, true, ssh, zero);
+        b[2] = dequant_q4x8_f16(w.qs.z, w.qs.w, false, ssl, zero);
+        b[3] = dequant_q4x8_f16(w.qs.z, w.qs.w, true, ssh, zero);
+        const _Float16 ml = (_Float16)(float)m[0], mh = (_Float16)(float)m[1];
+        const f16x8 bml = {ml, ml, ml, ml, ml, ml, ml, ml}, bmh = {mh, mh, mh, mh, mh, mh, mh, mh};
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            f32x4 P = {0.f, 0.f, 0.f, 0.f}, M = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                P = mfma16x32(x[j][nt], b[j], P);
+                P = mfma16x32(xl[j][nt], b[j], P);
+                M = mfma16x32(x[j][nt], (j & 1) ? bmh : bml, M);
+                M = mfma16x32(xl[j][nt], (j & 1) ? bmh : bml, M);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[nt][i] = fmaf(-dmin, M[i], fmaf(d, P[i], acc[nt][i]));
+        }
     }
 };
 
-// Four 6-bit codes (bytes 0..63 of q6) -> f16 (q - 32) * dsc. v_perm_b32 pairs
+// Four 6-bit codes (bytes 0..63 of q6) -> f16 (q - 32) * sc. v_perm_b32 pairs
 // each byte with 0x64, the f16 pattern of 1024 + q (exact); subtracting 1056
-// gives q - 32 exactly, and the multiply rounds once.
-__device__ __forceinline__ void q6x4_f16(uint32_t q6, f16x2 dsc, f16x2 &w01, f16x2 &w23) {
+// gives q - 32 exactly, and the product with the integer scale sc
+// (|sc (q - 32)| <= 2048) is exact as well.
+__device__ __forceinline__ void q6x4_f16(uint32_t q6, f16x2 sc, f16x2 &w01, f16x2 &w23) {
     const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, q6, 0x04010400u);
     const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, q6, 0x04030402u);
     const f16x2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};
-    w01 = (__builtin_bit_cast(f16x2, p01) - bias) * dsc;
-    w23 = (__builtin_bit_cast(f16x2, p23) - bias) * dsc;
+    w01 = (__builtin_bit_cast(f16x2, p01) - bias) * sc;
+    w23 = (__builtin_bit_cast(f16x2, p23) - bias) * sc;
 }
 
 // Q6_K (super-tile device layout). Step s = half h = s & 1 of block s >> 1.
 // Lane group q reads ql bytes 64h + 16q .. + 15 and qh bytes 32h + 16 (q & 1)
 // .. + 15: low nibbles are elements 128h + 16q + b (high bits at 2 (q >> 1)),
 // high nibbles elements 128h + 64 + 16q + b (high bits at 4 + 2 (q >> 1));
-// their scales are sc[8h + q] and sc[8h + q + 4].
+// their scales are sc[8h + q] and sc[8h + q + 4]. B = sc * (q - 32), and the
+// step adds d * P (dequant_q6_k, q6_k.rs:86-92: w = d sc (q - 32)).
 struct MQ6K {
     struct W {
         uint4 ql, qh;
@@ -144,15 +187,17 @@ struct MQ6K {
         w.sh = bload4(r, base + rS * 192u + jb * 16u + 8u * h + 4u);
         w.d = bload2(r, base + rS * 208u + jb * 2u, 0);
     }
-    __device__ static void dequant(const W &w, int q, int, f16x8 (&a)[4]) {
+    template <int NT>
+    __device__ static void step(const W &w, int q, const uint4 (&x)[4][NT], const uint4 (&xl)[4][NT],
+                                f32x4 (&acc)[NT]) {
         const float d = f16_to_f32(w.d);
-        const float scl = (float)(int)(int8_t)(w.sl >> (8 * q));
-        const float sch = (float)(int)(int8_t)(w.sh >> (8 * q));
-        const _Float16 dl = (_Float16)(d * scl), dh = (_Float16)(d * sch);
-        const f16x2 dsl = {dl, dl}, dsh = {dh, dh};
+        const _Float16 scl = (_Float16)(float)(int)(int8_t)(w.sl >> (8 * q));
+        const _Float16 sch = (_Float16)(float)(int)(int8_t)(w.sh >> (8 * q));
+        const f16x2 dsl = {scl, scl}, dsh = {sch, sch};
         const uint32_t shl = 2u * (uint32_t)(q >> 1), shh = 4u + shl;
         const uint32_t l[4] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w};
         const uint32_t hb[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+        f16x8 b[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const bool hi = j & 1;
@@ -167,66 +212,108 @@ struct MQ6K {
             f16x8 r;
             r[0] = v[0][0]; r[1] = v[0][1]; r[2] = v[1][0]; r[3] = v[1][1];
             r[4] = v[2][0]; r[5] = v[2][1]; r[6] = v[3][0]; r[7] = v[3][1];
-            a[j] = r;
+            b[j] = r;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            f32x4 P = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                P = mfma16x32(x[j][nt], b[j], P);
+                P = mfma16x32(xl[j][nt], b[j], P);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[nt][i] = fmaf(d, P[i], acc[nt][i]);
         }
     }
 };
 
 // Q8_0 (super-tile device layout [qs 8x32 | d 8x2]). Step s = blocks 4s ..
-// 4s + 3 of the row; lane group q takes block 4s + q, MFMA j its elements
-// 8j .. 8j + 7. A code q (int8) becomes f16 exactly as the pattern 0x64 with
-// byte q ^ 0x80 (1024 + q + 128) minus 1152; the multiply by the f16 block
-// scale rounds once.
+// 4s + 3 of the row (in_dim is a multiple of 256, so they share one
+// super-tile); MFMA j is block 4s + j, lane group q its elements 8q .. 8q + 7.
+// A code q (int8) becomes f16 exactly as the pattern 0x64 with byte q ^ 0x80
+// (1024 + q + 128) minus 1152; each block's MFMA result is multiplied by its
+// scale d in fp32 (dequant_q8_0, q8_0.rs:25-63: w = d q).
 struct MQ8 {
     struct W {
-        uint4 q0, q1;
-        uint32_t d;
+        uint2 q[4];
+        uint2 d;  // the four blocks' f16 scales
     };
-    __device__ static int elem(int s, int j, int q) { return 128 * s + 32 * q + 8 * j; }
+    __device__ static int elem(int s, int j, int q) { return 128 * s + 32 * j + 8 * q; }
     __device__ static void piece(int e, int &s, int &j, int &q) {
         s = e >> 7;
-        q = (e >> 5) & 3;
-        j = (e >> 3) & 3;
+        j = (e >> 5) & 3;
+        q = (e >> 3) & 3;
     }
     __device__ static void load(W &w, __amdgpu_buffer_rsrc_t r, int row, int s, int q, int in_dim,
                                 int out_dim) {
         const uint32_t nb = (uint32_t)(in_dim >> 5);
         const uint32_t nblk = (uint32_t)out_dim * nb;
-        const uint32_t bi = (uint32_t)row * nb + 4u * (uint32_t)s + (uint32_t)q;
+        const uint32_t bi = (uint32_t)row * nb + 4u * (uint32_t)s;  // jb is 0 or 4
         const uint32_t S = bi >> 3, jb = bi & 7u;
         const uint32_t rS = (S < (nblk >> 3)) ? 8u : (nblk & 7u);
         const uint32_t base = S * 272u;
-        w.q0 = bload16(r, base + jb * 32u, 0);
-        w.q1 = bload16(r, base + jb * 32u + 16u, 0);
-        w.d = bload2(r, base + rS * 32u + jb * 2u, 0);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            w.q[j] = bload8(r, base + (jb + (uint32_t)j) * 32u + 8u * (uint32_t)q, 0);
+        w.d = bload8(r, base + rS * 32u + jb * 2u, 0);
     }
-    __device__ static void dequant(const W &w, int, int, f16x8 (&a)[4]) {
-        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(w.d & 0xFFFFu));
-        const f16x2 dd = {d, d};
+    template <int NT>
+    __device__ static void step(const W &w, int, const uint4 (&x)[4][NT], const uint4 (&xl)[4][NT],
+                                f32x4 (&acc)[NT]) {
         const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-        const uint32_t v[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        f16x8 b[4];
+        float d[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
+            d[j] = f16_to_f32(((j & 2) ? w.d.y : w.d.x) >> (16 * (j & 1)));
             f16x8 r;
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const uint32_t b = v[2 * j + u] ^ 0x80808080u;
-                const f16x2 w01 = (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u)) - bias) * dd;
-                const f16x2 w23 = (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)) - bias) * dd;
+                const uint32_t bb = (u ? w.q[j].y : w.q[j].x) ^ 0x80808080u;
+                const f16x2 w01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04010400u)) - bias;
+                const f16x2 w23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04030402u)) - bias;
                 r[4 * u] = w01[0];
                 r[4 * u + 1] = w01[1];
                 r[4 * u + 2] = w23[0];
                 r[4 * u + 3] = w23[1];
             }
-            a[j] = r;
+            b[j] = r;
         }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const f32x4 P =
+                    mfma16x32(xl[j][nt], b[j], mfma16x32(x[j][nt], b[j], f32x4{0.f, 0.f, 0.f, 0.f}));
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[nt][i] = fmaf(d[j], P[i], acc[nt][i]);
+            }
     }
 };
 
 // ---- activation pre-pass ---------------------------------------------------------
+// Every activation image has two planes of the same layout: hi = f16(v) and
+// lo = f16(v - hi) for v = 2^e x (v - hi is exact in fp32), so hi + lo holds
+// v to about 2^-22 relative, and each weight operand meets both planes.
+__device__ __forceinline__ void hilo8(const float4 &v0, const float4 &v1, float up, uint4 &hi,
+                                      uint4 &lo) {
+    const float v[8] = {v0.x * up, v0.y * up, v0.z * up, v0.w * up,
+                        v1.x * up, v1.y * up, v1.z * up, v1.w * up};
+    f16x8 h, l;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        h[i] = (_Float16)v[i];
+        l[i] = (_Float16)(v[i] - (float)h[i]);
+    }
+    hi = __builtin_bit_cast(uint4, h);
+    lo = __builtin_bit_cast(uint4, l);
+}
+
 // One workgroup per padded token: max |x| over the row, e with max * 2^e in
 // [2^14, 2^15) (e in [-126, 126]; a zero row gets e = 0), then each thread
-// writes 8-element pieces in operand order. Padding tokens write zeros.
+// writes 8-element pieces in operand order into both planes (the lo plane
+// ntp * in_dim values after the hi plane). Padding tokens write zeros.
 template <class F>
 __global__ __launch_bounds__(256) void k_mf_x(const float *__restrict__ x, _Float16 *__restrict__ xh,
                                               float *__restrict__ unscale, int n_tok, int in_dim,
@@ -255,30 +342,27 @@ __global__ __launch_bounds__(256) void k_mf_x(const float *__restrict__ x, _Floa
     }
     const float up = ldexpf(1.0f, e);
     if (tid == 0) unscale[t] = real ? ldexpf(1.0f, -e) : 0.f;
+    const size_t plane = (size_t)ntp * in_dim;
     for (int g = tid; g < nsteps * 16; g += 256) {
         const int s = g >> 4, j = (g >> 2) & 3, q = g & 3;
-        uint4 o = make_uint4(0, 0, 0, 0);
+        uint4 hi = make_uint4(0, 0, 0, 0), lo = hi;
         if (real) {
             const float *p = xt + F::elem(s, j, q);
-            const float4 v0 = *reinterpret_cast<const float4 *>(p);
-            const float4 v1 = *reinterpret_cast<const float4 *>(p + 4);
-            f16x8 h;
-            h[0] = (_Float16)(v0.x * up); h[1] = (_Float16)(v0.y * up);
-            h[2] = (_Float16)(v0.z * up); h[3] = (_Float16)(v0.w * up);
-            h[4] = (_Float16)(v1.x * up); h[5] = (_Float16)(v1.y * up);
-            h[6] = (_Float16)(v1.z * up); h[7] = (_Float16)(v1.w * up);
-            o = __builtin_bit_cast(uint4, h);
+            hilo8(*reinterpret_cast<const float4 *>(p), *reinterpret_cast<const float4 *>(p + 4), up,
+                  hi, lo);
         }
-        *reinterpret_cast<uint4 *>(xh + ((size_t)g * ntp + t) * 8) = o;
+        *reinterpret_cast<uint4 *>(xh + ((size_t)g * ntp + t) * 8) = hi;
+        *reinterpret_cast<uint4 *>(xh + plane + ((size_t)g * ntp + t) * 8) = lo;
     }
 }
 
 // ---- GEMV ----------------------------------------------------------------------------
 // One workgroup's 16 * RT rows from row0 against the n_tok (<= 16 * NT)
-// token columns of xh, y[t * y_stride + o]; red: NK * RT * NT * 64 f32x4 of LDS.
+// token columns of xh (two planes of plane_bytes each), y[t * y_stride + o];
+// red: NK * RT * NT * 64 f32x4 of LDS.
 template <class F, int NT, int NK, int RT>
 __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t w_bytes,
-                                        const _Float16 *__restrict__ xh, uint32_t xh_bytes,
+                                        const _Float16 *__restrict__ xh, uint32_t plane_bytes,
                                         const float *__restrict__ unscale, float *__restrict__ y,
                                         int n_tok, int in_dim, int out_dim, int y_stride, int row0,
                                         f32x4 *red) {
@@ -288,7 +372,7 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
     const int nsteps = in_dim / kMfStep;
     const int s0 = nsteps * wv / NK, s1 = nsteps * (wv + 1) / NK;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xh, xh_bytes);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xh, 2 * plane_bytes);
 
     f32x4 acc[RT][NT];
 #pragma unroll
@@ -297,38 +381,33 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
         for (int nt = 0; nt < NT; nt++) acc[rt][nt] = {0.f, 0.f, 0.f, 0.f};
 
     typename F::W wa[RT], wb[RT];
-    uint4 xa[4][NT], xb[4][NT];
-    auto load = [&](typename F::W (&wr)[RT], uint4 (&xr)[4][NT], int s) {
+    uint4 xa[4][NT], xb[4][NT], la[4][NT], lb[4][NT];
+    auto load = [&](typename F::W (&wr)[RT], uint4 (&xr)[4][NT], uint4 (&lr)[4][NT], int s) {
 #pragma unroll
         for (int rt = 0; rt < RT; rt++)
             F::load(wr[rt], rw, min(row0 + 16 * rt + r16, out_dim - 1), s, q, in_dim, out_dim);
 #pragma unroll
         for (int j = 0; j < 4; j++)
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++)
-                xr[j][nt] = bload16(rx, (uint32_t)((((s * 4 + j) * 4 + q) * ntp + nt * 16 + r16) * 16), 0);
+            for (int nt = 0; nt < NT; nt++) {
+                const uint32_t o = (uint32_t)((((s * 4 + j) * 4 + q) * ntp + nt * 16 + r16) * 16);
+                xr[j][nt] = bload16(rx, o, 0);
+                lr[j][nt] = bload16(rx, o + plane_bytes, 0);
+            }
     };
-    auto compute = [&](const typename F::W (&wr)[RT], const uint4 (&xr)[4][NT], int s) {
+    auto compute = [&](const typename F::W (&wr)[RT], const uint4 (&xr)[4][NT],
+                       const uint4 (&lr)[4][NT]) {
 #pragma unroll
-        for (int rt = 0; rt < RT; rt++) {
-            f16x8 a[4];
-            F::dequant(wr[rt], q, s, a);
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++)
-                    acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        a[j], __builtin_bit_cast(f16x8, xr[j][nt]), acc[rt][nt], 0, 0, 0);
-        }
+        for (int rt = 0; rt < RT; rt++) F::template step<NT>(wr[rt], q, xr, lr, acc[rt]);
     };
     if (s0 < s1) {
-        load(wa, xa, s0);
+        load(wa, xa, la, s0);
         for (int s = s0; s < s1; s += 2) {
-            if (s + 1 < s1) load(wb, xb, s + 1);
-            compute(wa, xa, s);
+            if (s + 1 < s1) load(wb, xb, lb, s + 1);
+            compute(wa, xa, la);
             if (s + 1 < s1) {
-                if (s + 2 < s1) load(wa, xa, s + 2);
-                compute(wb, xb, s + 1);
+                if (s + 2 < s1) load(wa, xa, la, s + 2);
+                compute(wb, xb, lb);
             }
         }
     }
@@ -341,14 +420,13 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
         const int rt = c / (NT * 64), nt = (c / 64) % NT, ln = c % 64;
         f32x4 v = red[(rt * NT + nt) * 64 + ln];
         for (int k = 1; k < NK; k++) v += red[((k * RT + rt) * NT + nt) * 64 + ln];
-        const int t = nt * 16 + (ln & 15);
-        const int o = row0 + 16 * rt + 4 * (ln >> 4);  // D rows 4 (lane / 16) + 0..3
-        if (t < n_tok) {
-            const float us = unscale[t];
-            float *yt = y + (size_t)t * y_stride;
+        // D: tokens 4 (lane / 16) + 0..3 of weight row lane % 16
+        const int o = row0 + 16 * rt + (ln & 15);
+        const int t0 = nt * 16 + 4 * (ln >> 4);
+        if (o < out_dim) {
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                if (o + i < out_dim) yt[o + i] = v[i] * us;
+                if (t0 + i < n_tok) y[(size_t)(t0 + i) * y_stride + o] = v[i] * unscale[t0 + i];
         }
     }
 }
@@ -356,27 +434,29 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
 template <class F, int NT, int NK, int RT>
 __global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__ w, uint32_t w_bytes,
                                                      const _Float16 *__restrict__ xh,
-                                                     uint32_t xh_bytes,
+                                                     uint32_t plane_bytes,
                                                      const float *__restrict__ unscale,
                                                      float *__restrict__ y, int n_tok, int in_dim,
                                                      int out_dim) {
     __shared__ f32x4 red[NK * RT * NT * 64];
-    mf_rows<F, NT, NK, RT>(w, w_bytes, xh, xh_bytes, unscale, y, n_tok, in_dim, out_dim, out_dim,
+    mf_rows<F, NT, NK, RT>(w, w_bytes, xh, plane_bytes, unscale, y, n_tok, in_dim, out_dim, out_dim,
                            blockIdx.x * 16 * RT, red);
 }
 
 // ---- routed experts grouped by expert (many tokens) --------------------------------
-// Slots sorted by expert (k_moe_route): expert e owns sorted slots [off[e],
-// off[e + 1]), cut into batches of up to kMfgBatch (k_moe_route lists them);
+// Slots sorted by expert (moe.hip routing): expert e owns sorted slots [off[e],
+// off[e + 1]), cut into batches of up to kMfgBatch (k_moe_scan lists them);
 // a batch is the token set (the N dimension) of one pass of mf_rows over
 // that expert's rows, so each expert's weights are streamed once per
-// kMfgBatch of its slots. Batch b's activation image sits at
-// xh + b * in_dim * kMfgBatch (the k_mf_x layout with ntp = kMfgBatch) and
-// its scales at unscale + b * kMfgBatch; its rows go to y + first * out_dim.
+// kMfgBatch of its slots. Batch b's activation image (two planes of
+// in_dim * kMfgBatch values, the k_mf_x layout with ntp = kMfgBatch) sits
+// at xh + 2 b in_dim kMfgBatch and its scales at unscale + b * kMfgBatch;
+// its rows go to y + first * out_dim.
 
 // One token column of a kMfgBatch-wide activation image (the k_mf_x
 // conversion, one workgroup of 256 threads): val4(i) gives elements
-// i .. i + 3 of the column's row; the column's pieces go to xb, 2^-e to *us.
+// i .. i + 3 of the column's row; the column's pieces go to both planes of
+// the image at xb, 2^-e to *us.
 template <class F, class V>
 __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 *__restrict__ xb,
                                             float *__restrict__ us) {
@@ -401,16 +481,14 @@ __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 
     }
     const float up = ldexpf(1.0f, e);
     if (tid == 0) *us = ldexpf(1.0f, -e);
+    const size_t plane = (size_t)in_dim * kMfgBatch;
     for (int g = tid; g < nsteps * 16; g += 256) {
         const int s = g >> 4, j = (g >> 2) & 3, q = g & 3;
         const int i = F::elem(s, j, q);
-        const float4 v0 = val4(i), v1 = val4(i + 4);
-        f16x8 h;
-        h[0] = (_Float16)(v0.x * up); h[1] = (_Float16)(v0.y * up);
-        h[2] = (_Float16)(v0.z * up); h[3] = (_Float16)(v0.w * up);
-        h[4] = (_Float16)(v1.x * up); h[5] = (_Float16)(v1.y * up);
-        h[6] = (_Float16)(v1.z * up); h[7] = (_Float16)(v1.w * up);
-        *reinterpret_cast<uint4 *>(xb + ((size_t)g * kMfgBatch + t) * 8) = __builtin_bit_cast(uint4, h);
+        uint4 hi, lo;
+        hilo8(val4(i), val4(i + 4), up, hi, lo);
+        *reinterpret_cast<uint4 *>(xb + ((size_t)g * kMfgBatch + t) * 8) = hi;
+        *reinterpret_cast<uint4 *>(xb + plane + ((size_t)g * kMfgBatch + t) * 8) = lo;
     }
 }
 
@@ -443,7 +521,7 @@ __global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
         }
         return v;
     };
-    mf_x_column<F>(val4, in_dim, t, xh + (size_t)b * in_dim * kMfgBatch,
+    mf_x_column<F>(val4, in_dim, t, xh + (size_t)b * 2 * in_dim * kMfgBatch,
                    unscale + (size_t)b * kMfgBatch + t);
 }
 
@@ -459,7 +537,7 @@ __global__ __launch_bounds__(256) void k_mfl_x(const float *__restrict__ x, int 
     if (tc >= n_tok) return;
     const float *xt = x + (size_t)tc * x_stride + (size_t)g * D;
     auto val4 = [&](int i) { return *reinterpret_cast<const float4 *>(xt + i); };
-    mf_x_column<F>(val4, D, blockIdx.x, xh + (size_t)b * D * kMfgBatch,
+    mf_x_column<F>(val4, D, blockIdx.x, xh + (size_t)b * 2 * D * kMfgBatch,
                    unscale + (size_t)b * kMfgBatch + blockIdx.x);
 }
 
@@ -476,8 +554,8 @@ __global__ __launch_bounds__(256) void k_gemv_mfl(const uint8_t *__restrict__ w,
     const int row0 = blockIdx.x * 16 * RT, c = blockIdx.y;
     const int b = (row0 / R) * nchunks + c;
     const int t0 = c * kMfgBatch;
-    const size_t img = (size_t)D * kMfgBatch;
-    mf_rows<F, kMfgBatch / 16, NK, RT>(w, w_bytes, xh + b * img, (uint32_t)(img * 2),
+    const size_t img = (size_t)D * kMfgBatch;  // values per plane
+    mf_rows<F, kMfgBatch / 16, NK, RT>(w, w_bytes, xh + b * 2 * img, (uint32_t)(img * 2),
                                        unscale + (size_t)b * kMfgBatch, y + (size_t)t0 * y_stride,
                                        min(kMfgBatch, n_tok - t0), D, out_dim, y_stride, row0,
                                        red);
@@ -503,19 +581,21 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mfg(const uint8_t *__restrict_
     const bool m1 = blockIdx.z != 0;
     const uint8_t *w = (m1 ? w1 : w0) + (size_t)bt.expert * w_stride;
     float *y = (m1 ? y1 : y0) + (size_t)bt.first * out_dim;
-    const size_t img = (size_t)in_dim * kMfgBatch;
-    mf_rows<F, kMfgBatch / 16, NK, RT>(w, (uint32_t)w_stride, xh + b * img, (uint32_t)(img * 2),
+    const size_t img = (size_t)in_dim * kMfgBatch;  // values per plane
+    mf_rows<F, kMfgBatch / 16, NK, RT>(w, (uint32_t)w_stride, xh + b * 2 * img, (uint32_t)(img * 2),
                                        unscale + (size_t)b * kMfgBatch, y, bt.count, in_dim,
                                        out_dim, out_dim, blockIdx.x * 16 * RT, red);
 }
 
 // ---- fused batched GEMV: activations converted into LDS ------------------------------
 // One launch of n_wg workgroups (one per CU) of NW wavefronts, for n_tok <=
-// 16 tokens whose f16 activations fit in LDS (n_tok * in_dim * 2 bytes).
+// 16 tokens whose two f16 activation planes fit in LDS (n_tok * in_dim * 4
+// bytes).
 //
 // Prologue: per-token max |x| (LDS atomic max on the float bits, all values
 // being non-negative), then every 8-element piece of x scaled by 2^e_t into
-// f16 at LDS slot ((s * 4 + j) * 4 + q) * n_tok + t (MFMA operand order);
+// f16 (hi and lo planes) at LDS slot ((s * 4 + j) * 4 + q) * n_tok + t of
+// each plane (MFMA operand order);
 // unscale[t] = 2^-e_t. Lanes of tokens >= n_tok read a zero slot.
 // Rows: blocks of 16 (the MFMA M); workgroup b owns blocks b + n_wg * l.
 // Every wavefront streams its share of K steps [w ns / NW, (w + 1) ns / NW)
@@ -540,8 +620,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfb(const uint8_t *__restrict_
     const int nrb = (n_rb - rb0 + n_wg - 1) / n_wg;  // this workgroup's row blocks
     const int s_beg = ns * wv / NW, s_end = ns * (wv + 1) / NW, my_ns = s_end - s_beg;
     const int T = nrb * my_ns;  // this wavefront's tiles (block-major)
-    uint4 *xs = lds;                                              // n_tok * in_dim / 8 slots
-    uint4 *zero = lds + (size_t)n_tok * in_dim / 8;               // one zero slot
+    const size_t n8s = (size_t)n_tok * in_dim / 8;
+    uint4 *xs = lds;                                              // hi plane: n8s slots
+    uint4 *xls = lds + n8s;                                       // lo plane: n8s slots
+    uint4 *zero = lds + 2 * n8s;                                  // one zero slot
     f32x4 *part = reinterpret_cast<f32x4 *>(zero + 1);            // [nrb][NW][64]
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
     const __amdgpu_buffer_rsrc_t rnull = make_rsrc(w, 0);
@@ -613,17 +695,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfb(const uint8_t *__restrict_
         if (i < n8) {
             const int t = (8 * i) / in_dim, e0 = 8 * i - t * in_dim;
             const float up = ldexpf(1.0f, (int)amax_bits[t]);
-            f16x8 h;
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                h[4 * u] = (_Float16)(__uint_as_float(xv[r][u].x) * up);
-                h[4 * u + 1] = (_Float16)(__uint_as_float(xv[r][u].y) * up);
-                h[4 * u + 2] = (_Float16)(__uint_as_float(xv[r][u].z) * up);
-                h[4 * u + 3] = (_Float16)(__uint_as_float(xv[r][u].w) * up);
-            }
+            uint4 hi, lo;
+            hilo8(__builtin_bit_cast(float4, xv[r][0]), __builtin_bit_cast(float4, xv[r][1]), up,
+                  hi, lo);
             int s, j, qq;
             F::piece(e0, s, j, qq);
-            xs[((s * 4 + j) * 4 + qq) * n_tok + t] = __builtin_bit_cast(uint4, h);
+            xs[((s * 4 + j) * 4 + qq) * n_tok + t] = hi;
+            xls[((s * 4 + j) * 4 + qq) * n_tok + t] = lo;
         }
     }
     __syncthreads();
@@ -639,14 +717,16 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfb(const uint8_t *__restrict_
             __builtin_amdgcn_sched_barrier(0);
             if (t < T) {
                 const int s = s_beg + sc;
-                f16x8 a[4];
-                F::dequant(buf[jj], q, s, a);
+                uint4 xr[4][1], lr[4][1];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const uint4 *px = tok_ok ? xs + ((s * 4 + j) * 4 + q) * n_tok + r16 : zero;
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        a[j], __builtin_bit_cast(f16x8, *px), acc, 0, 0, 0);
+                    const size_t o = ((size_t)(s * 4 + j) * 4 + q) * n_tok + r16;
+                    xr[j][0] = *(tok_ok ? xs + o : zero);
+                    lr[j][0] = *(tok_ok ? xls + o : zero);
                 }
+                f32x4 a1[1] = {acc};
+                F::template step<1>(buf[jj], q, xr, lr, a1);
+                acc = a1[0];
                 if (++sc == my_ns) {
                     part[((size_t)l * NW + wv) * 64 + lane] = acc;
                     acc = {0.f, 0.f, 0.f, 0.f};
@@ -660,19 +740,17 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfb(const uint8_t *__restrict_
     if (my_ns == 0)  // more wavefronts than K steps: this one contributes zeros
         for (int b = 0; b < nrb; b++) part[((size_t)b * NW + wv) * 64 + lane] = acc;
     __syncthreads();
-    // D lane layout: rows 4 (lane / 16) + 0..3, column (token) lane % 16
+    // D lane layout: tokens 4 (lane / 16) + 0..3 of weight row lane % 16
     for (int c = threadIdx.x; c < nrb * 64; c += kThreads) {
         const int b = c >> 6, ln = c & 63;
         f32x4 v = part[((size_t)b * NW) * 64 + ln];
         for (int k = 1; k < NW; k++) v += part[((size_t)b * NW + k) * 64 + ln];
-        const int tk = ln & 15;
-        const int o = 16 * (rb0 + n_wg * b) + 4 * (ln >> 4);
-        if (tk < n_tok) {
-            const float us = unscale[tk];
-            float *yt = y + (size_t)tk * out_dim;
+        const int o = 16 * (rb0 + n_wg * b) + (ln & 15);
+        const int t0 = 4 * (ln >> 4);
+        if (o < out_dim) {
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                if (o + i < out_dim) yt[o + i] = v[i] * us;
+                if (t0 + i < n_tok) y[(size_t)(t0 + i) * out_dim + o] = v[i] * unscale[t0 + i];
         }
     }
 }
@@ -681,7 +759,7 @@ template <class F>
 static size_t mfb_lds_bytes(int n_tok, int in_dim, int out_dim, int n_wg, int nw) {
     const int n_rb = (out_dim + 15) >> 4;
     const int nrb = (n_rb + n_wg - 1) / n_wg;
-    return ((size_t)n_tok * in_dim / 8 + 1) * 16 + (size_t)nrb * nw * 64 * 16;
+    return (2 * (size_t)n_tok * in_dim / 8 + 1) * 16 + (size_t)nrb * nw * 64 * 16;
 }
 constexpr size_t kMfbMaxLds = 152 * 1024;
 
@@ -723,36 +801,34 @@ static hipError_t mfb_xp_go(const uint8_t *w, size_t w_bytes, const float *x, fl
 // ---- launchers -----------------------------------------------------------------------
 // Taken from 5 tokens up: below that the int8-limb GEMV, whose VALU work
 // grows with the batch, is still faster (C1: 26 vs 29 us at 4 tokens, 55 vs
-// 29 us at 8). f16 weights and activations put the expected max|d|/max|y|
-// near 4e-4 for outputs of many rows (the maxima of both then track their
-// standard deviations); a matrix of a few dozen rows can exceed 1e-3 by
-// chance, so short matrices stay on the int8-limb GEMV.
+// 29 us at 8). The weights are exact, so any number of rows qualifies.
 bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
     // Q8_0 from 9 tokens: up to 8 the int8-limb kernel with x in LDS is as
     // fast on 4096 x 4096 and faster on 1024-row matrices
     const int min_tok = dtype == T_Q8_0 ? 9 : 5;
     return (dtype == T_Q4_K || dtype == T_Q6_K || dtype == T_Q8_0) && n_tok >= min_tok &&
-           n_tok <= 32 && in_dim % 256 == 0 && in_dim > 0 && out_dim >= 1024;
+           n_tok <= 32 && in_dim % 256 == 0 && in_dim > 0 && out_dim > 0;
 }
 
+// Two f16 planes of ntp x in_dim, then ntp unscale factors.
 size_t gemv_mfma_scratch_bytes(int n_tok, int in_dim) {
     const size_t ntp = n_tok <= 16 ? 16 : 32;
-    return (ntp * (size_t)in_dim * 2 + 255) / 256 * 256 + ntp * 4;
+    return (2 * ntp * (size_t)in_dim * 2 + 255) / 256 * 256 + ntp * 4;
 }
 
 template <class F, int NT, int NK, int RT>
 static hipError_t mf_go(const uint8_t *w, size_t w_bytes, const float *x, uint8_t *scratch, float *y,
                         int n_tok, int in_dim, int out_dim, hipStream_t s) {
     constexpr int ntp = NT * 16;
-    const size_t xh_bytes = ((size_t)ntp * in_dim * 2 + 255) / 256 * 256;
+    const size_t plane_bytes = (size_t)ntp * in_dim * 2;
     _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
-    float *unscale = reinterpret_cast<float *>(scratch + xh_bytes);
+    float *unscale = reinterpret_cast<float *>(scratch + (2 * plane_bytes + 255) / 256 * 256);
     k_mf_x<F><<<ntp, 256, 0, s>>>(x, xh, unscale, n_tok, in_dim, ntp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int rows_wg = 16 * RT;
     k_gemv_mf<F, NT, NK, RT><<<(unsigned)((out_dim + rows_wg - 1) / rows_wg), 64 * NK, 0, s>>>(
-        w, (uint32_t)w_bytes, xh, (uint32_t)xh_bytes, unscale, y, n_tok, in_dim, out_dim);
+        w, (uint32_t)w_bytes, xh, (uint32_t)plane_bytes, unscale, y, n_tok, in_dim, out_dim);
     return hipGetLastError();
 }
 
@@ -780,23 +856,21 @@ static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, 
     return mf_go<F, 2, 8, 1>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
 }
 
-// Q4_K gate/up and down only, both outputs at least 1024 rows. The f16
-// roundings of the gate/up pass reach the down pass through the SwiGLU and
-// add to its own. Measured max|d|/max|y| at n_embd 4096, n_ff 2048 (9..32
-// tokens): Q4_K 1.4e-4 to 4.9e-4 (C3: 6.0e-4 at 8 tokens); Q8_0 up to 9.3e-4
-// and Q6_K 1.1e-3 to 1.2e-3, over the 1e-3 bound. Q6_K's f16(d * sc) is one
-// rounding shared by a sub-block's 16 weights. Those formats take the
-// int8-limb routes.
+// Any pairing of Q4_K, Q6_K and Q8_0 experts with both dimensions multiples
+// of 256. The weights are exact; the activations of each of the two GEMVs
+// are rounded once to f16 (x, then the SwiGLU output), which keeps the
+// chained error near 2e-4 of max |y|.
+static bool mfma_format(uint32_t t) { return t == T_Q4_K || t == T_Q6_K || t == T_Q8_0; }
 bool moe_mfma_supported(uint32_t dt_gu, uint32_t dt_d, int n_embd, int n_ff) {
-    return dt_gu == T_Q4_K && dt_d == T_Q4_K && n_embd >= 1024 && n_ff >= 1024 &&
+    return mfma_format(dt_gu) && mfma_format(dt_d) && n_embd > 0 && n_ff > 0 &&
            n_embd % 256 == 0 && n_ff % 256 == 0;
 }
 
 size_t moe_mfma_scratch_bytes(int n_pairs, int n_expert, int n_embd, int n_ff) {
     const size_t nb = (size_t)mfg_max_batches(n_pairs, n_expert);
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
-    return mfg_batch_bytes(n_pairs, n_expert) + al(nb * kMfgBatch * (size_t)n_embd * 2) +
-           al(nb * kMfgBatch * 4) + al(nb * kMfgBatch * (size_t)n_ff * 2) + al(nb * kMfgBatch * 4);
+    return mfg_batch_bytes(n_pairs, n_expert) + al(nb * kMfgBatch * (size_t)n_embd * 4) +
+           al(nb * kMfgBatch * 4) + al(nb * kMfgBatch * (size_t)n_ff * 4) + al(nb * kMfgBatch * 4);
 }
 
 template <class F>
@@ -846,9 +920,9 @@ hipError_t launch_moe_mfma(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
         p += (n + 255) / 256 * 256;
         return r;
     };
-    _Float16 *xh1 = reinterpret_cast<_Float16 *>(take((size_t)max_b * kMfgBatch * n_embd * 2));
+    _Float16 *xh1 = reinterpret_cast<_Float16 *>(take((size_t)max_b * kMfgBatch * n_embd * 4));
     float *us1 = reinterpret_cast<float *>(take((size_t)max_b * kMfgBatch * 4));
-    _Float16 *xh2 = reinterpret_cast<_Float16 *>(take((size_t)max_b * kMfgBatch * n_ff * 2));
+    _Float16 *xh2 = reinterpret_cast<_Float16 *>(take((size_t)max_b * kMfgBatch * n_ff * 4));
     float *us2 = reinterpret_cast<float *>(take((size_t)max_b * kMfgBatch * 4));
     hipError_t e;
     if ((e = mfg_pass_dt(dt_gu, gate, up, gu_stride, x, nullptr, slot_tok, bat, n_bat, max_b, 0.f,
@@ -865,7 +939,7 @@ bool lora_mfma_supported(uint32_t dtype, int n_tok, int D, int G, int R) {
 
 size_t lora_mfma_scratch_bytes(int n_tok, int D, int G) {
     const size_t nb = (size_t)G * ((n_tok + kMfgBatch - 1) / kMfgBatch);
-    return (nb * kMfgBatch * (size_t)D * 2 + 255) / 256 * 256 + nb * kMfgBatch * 4;
+    return (nb * kMfgBatch * (size_t)D * 4 + 255) / 256 * 256 + nb * kMfgBatch * 4;
 }
 
 template <class F>
@@ -875,7 +949,7 @@ static hipError_t mfl_go(const uint8_t *w, size_t w_bytes, const float *x, int x
     const int nchunks = (n_tok + kMfgBatch - 1) / kMfgBatch;
     const size_t nb = (size_t)G * nchunks;
     _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
-    float *us = reinterpret_cast<float *>(scratch + (nb * kMfgBatch * (size_t)D * 2 + 255) / 256 * 256);
+    float *us = reinterpret_cast<float *>(scratch + (nb * kMfgBatch * (size_t)D * 4 + 255) / 256 * 256);
     k_mfl_x<F><<<dim3(kMfgBatch, (unsigned)nb), 256, 0, s>>>(x, x_stride, n_tok, D, nchunks, xh, us);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

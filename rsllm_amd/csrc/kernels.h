@@ -133,7 +133,7 @@ hipError_t launch_quantize_swiglu(uint32_t dtype, const float *hg, const float *
 // holds moe_mfma_scratch_bytes(n_pairs, n_expert, n_embd, n_ff) bytes.
 // The batches: each active expert's sorted slots cut into runs of up to
 // kMfgBatch (experts ascending, runs in slot order), *n_bat of them, as
-// k_moe_route lists them; at most mfg_max_batches(n_pairs, n_expert).
+// k_moe_scan lists them; at most mfg_max_batches(n_pairs, n_expert).
 // `scratch` holds moe_mfma_scratch_bytes(...) bytes: the batch list and its
 // count first (mfg_batch_bytes), then the activation images.
 constexpr int kMfgBatch = 16;

@@ -11,9 +11,11 @@
 // tokens (grouped GEMV, gemv.hip; for Q4_K experts from kMoeMfmaMinTok
 // tokens, batches of up to 16 on the matrix cores instead, launch_moe_mfma
 // in gemv_mfma.hip, steps 2-6 there):
-//   1. k_moe_route: slots sorted by expert (ties in (t, i) order), per-expert
+//   1. routing (k_moe_hist, k_moe_scan, k_moe_scatter, any number of
+//      pairs): slots sorted by expert (ties in (t, i) order), per-expert
 //      offsets, slot -> token, (t, i) -> slot, the list of active experts;
-//      slots with w == 0 are skipped (moe.rs:681-683).
+//      slots with w == 0 are skipped (moe.rs:681-683). Calls of more than
+//      kMoeMaxPairs pairs run in token chunks, one pass each.
 //   2. activation limbs of x for the gate/up format;
 //   3. grouped GEMV, gate and up in one launch -> hg, hu [slot x n_ff];
 //   4+5. clamp (only when c > 1e-6; NaN passes), silu(g) * u and the
@@ -25,60 +27,172 @@
 
 namespace rsllm_hip {
 
-// One workgroup. ids and weights are cached in LDS; a slot's rank inside its
-// expert is the number of earlier valid slots with the same expert
-// (deterministic order). Also lists the experts with at least one slot, in
-// ascending order (act, count in *n_act), for the grouped GEMV grids, and,
-// when bat is given, the matrix-core batches (MfgBatch, count in *n_bat).
-__global__ __launch_bounds__(256) void k_moe_route(const int *__restrict__ ids,
-                                                   const float *__restrict__ wts, int n_pairs,
-                                                   int k, int n_expert, int *__restrict__ off,
-                                                   int *__restrict__ slot_tok,
-                                                   int *__restrict__ slot_of,
-                                                   int *__restrict__ act, int *__restrict__ n_act,
-                                                   MfgBatch *__restrict__ bat,
-                                                   int *__restrict__ n_bat) {
-    extern __shared__ int lds[];
-    int *cnt = lds;                     // n_expert + 1
-    int *eid = lds + n_expert + 1;      // n_pairs: expert id, or -1 for a skipped slot
+// ---- routing: slots sorted by expert -----------------------------------------
+// The (t, i) pairs, p = t * k + i, are cut into blocks of 256. A valid pair
+// (w != 0, expert id in range) gets slot
+//     base[e][b] + (valid pairs of expert e before p in its block b),
+// base[e][b] = valid pairs of experts < e, plus those of expert e in blocks
+// before b: slots are sorted by expert, ties in pair order, for any number of
+// pairs. Three launches: per-block counts and in-block ranks; one workgroup
+// scans the counts (expert-major) into the bases and lists the active
+// experts and the matrix-core batches; per-pair scatter.
+constexpr int kRouteBlock = 256;
+
+inline int route_blocks(int n_pairs) { return (n_pairs + kRouteBlock - 1) / kRouteBlock; }
+
+// hist[e * nblk + b] = valid pairs of expert e in block b; rank[p] = valid
+// pairs of p's expert before p in its block.
+__global__ __launch_bounds__(kRouteBlock) void k_moe_hist(const int *__restrict__ ids,
+                                                          const float *__restrict__ wts,
+                                                          int n_pairs, int n_expert,
+                                                          int *__restrict__ hist,
+                                                          int *__restrict__ rank) {
+    extern __shared__ int cnt[];  // n_expert
+    __shared__ int eb[kRouteBlock];
+    const int tid = threadIdx.x, b = blockIdx.x, nblk = gridDim.x;
+    for (int e = tid; e < n_expert; e += kRouteBlock) cnt[e] = 0;
+    const int p = b * kRouteBlock + tid;
+    int e = -1;
+    if (p < n_pairs) {
+        const int id = ids[p];
+        if (wts[p] != 0.0f && id >= 0 && id < n_expert) e = id;
+    }
+    eb[tid] = e;
+    __syncthreads();
+    if (e >= 0) {
+        atomicAdd(&cnt[e], 1);
+        int r = 0;
+        for (int q = 0; q < tid; q++) r += eb[q] == e ? 1 : 0;
+        rank[p] = r;
+    }
+    __syncthreads();
+    for (int x = tid; x < n_expert; x += kRouteBlock) hist[(size_t)x * nblk + b] = cnt[x];
+}
+
+// Exclusive scan of v[0..n) in place by the whole workgroup (kScanThreads
+// threads), returning the total; `part` holds kScanThreads ints of LDS.
+constexpr int kScanThreads = 1024;
+__device__ int scan_inplace(int *__restrict__ v, size_t n, int *part) {
     const int tid = threadIdx.x;
-    for (int e = tid; e <= n_expert; e += 256) cnt[e] = 0;
+    const size_t seg = (n + kScanThreads - 1) / kScanThreads;
+    const size_t lo = min(n, (size_t)tid * seg), hi = min(n, lo + seg);
+    int sum = 0;
+    for (size_t i = lo; i < hi; i++) sum += v[i];
+    part[tid] = sum;
     __syncthreads();
-    for (int p = tid; p < n_pairs; p += 256) {
-        const int e = ids[p];
-        const bool valid = wts[p] != 0.0f && e >= 0 && e < n_expert;
-        eid[p] = valid ? e : -1;
-        if (valid) atomicAdd(&cnt[e], 1);
+    // Hillis-Steele over the per-thread sums
+    for (int d = 1; d < kScanThreads; d <<= 1) {
+        const int add = tid >= d ? part[tid - d] : 0;
+        __syncthreads();
+        part[tid] += add;
+        __syncthreads();
+    }
+    const int total = part[kScanThreads - 1];
+    int run = part[tid] - sum;  // exclusive prefix of this thread's segment
+    for (size_t i = lo; i < hi; i++) {
+        const int c = v[i];
+        v[i] = run;
+        run += c;
     }
     __syncthreads();
-    if (tid == 0) {
-        int run = 0, na = 0, nb = 0;
-        for (int e = 0; e < n_expert; e++) {
-            const int c = cnt[e];
-            cnt[e] = run;
-            off[e] = run;
-            if (c) act[na++] = e;
-            if (bat)
-                for (int f = 0; f < c; f += kMfgBatch)
-                    bat[nb++] = MfgBatch{run + f, c - f < kMfgBatch ? c - f : kMfgBatch, e, 0};
-            run += c;
-        }
-        off[n_expert] = run;
-        *n_act = na;
-        if (bat) *n_bat = nb;
+    return total;
+}
+
+// One workgroup: hist -> bases (in place); off[e] (n_expert + 1 entries);
+// the active experts in ascending order (act, *n_act); and, when bat is
+// given, each active expert's slots cut into batches of up to kMfgBatch
+// (experts ascending, batches in slot order; *n_bat of them). `flags` holds
+// n_expert + 1 ints of workspace.
+__global__ __launch_bounds__(kScanThreads) void k_moe_scan(int *__restrict__ hist, int nblk,
+                                                           int n_expert, int *__restrict__ off,
+                                                           int *__restrict__ act,
+                                                           int *__restrict__ n_act,
+                                                           MfgBatch *__restrict__ bat,
+                                                           int *__restrict__ n_bat,
+                                                           int *__restrict__ flags) {
+    __shared__ int part[kScanThreads];
+    const int tid = threadIdx.x;
+    const int total = scan_inplace(hist, (size_t)n_expert * nblk, part);
+    for (int e = tid; e < n_expert; e += kScanThreads) off[e] = hist[(size_t)e * nblk];
+    if (tid == 0) off[n_expert] = total;
+    __syncthreads();
+    // active experts: positions from a scan of the 0/1 flags
+    for (int e = tid; e < n_expert; e += kScanThreads) {
+        const int c = (e + 1 < n_expert ? hist[(size_t)(e + 1) * nblk] : total) -
+                      hist[(size_t)e * nblk];
+        flags[e] = c > 0 ? 1 : 0;
     }
     __syncthreads();
-    for (int p = tid; p < n_pairs; p += 256) {
-        const int e = eid[p];
-        int slot = -1;
-        if (e >= 0) {
-            int rank = 0;
-            for (int q = 0; q < p; q++) rank += eid[q] == e ? 1 : 0;
-            slot = cnt[e] + rank;
-            slot_tok[slot] = p / k;
-        }
-        slot_of[p] = slot;
+    const int na = scan_inplace(flags, (size_t)n_expert, part);
+    for (int e = tid; e < n_expert; e += kScanThreads) {
+        const int next = e + 1 < n_expert ? flags[e + 1] : na;
+        if (next != flags[e]) act[flags[e]] = e;
     }
+    if (tid == 0) *n_act = na;
+    if (!bat) return;
+    __syncthreads();
+    // batches: positions from a scan of ceil(count / kMfgBatch)
+    for (int e = tid; e < n_expert; e += kScanThreads) {
+        const int c = off[e + 1] - off[e];
+        flags[e] = (c + kMfgBatch - 1) / kMfgBatch;
+    }
+    __syncthreads();
+    const int nb = scan_inplace(flags, (size_t)n_expert, part);
+    for (int e = tid; e < n_expert; e += kScanThreads) {
+        const int c = off[e + 1] - off[e];
+        for (int f = 0, j = flags[e]; f < c; f += kMfgBatch, j++)
+            bat[j] = MfgBatch{off[e] + f, c - f < kMfgBatch ? c - f : kMfgBatch, e, 0};
+    }
+    if (tid == 0) *n_bat = nb;
+}
+
+// slot_of[p] = the pair's slot, or -1 when it is skipped; slot_tok[slot] = t.
+__global__ __launch_bounds__(kRouteBlock) void k_moe_scatter(const int *__restrict__ ids,
+                                                             const float *__restrict__ wts,
+                                                             int n_pairs, int k, int n_expert,
+                                                             const int *__restrict__ base,
+                                                             const int *__restrict__ rank,
+                                                             int *__restrict__ slot_tok,
+                                                             int *__restrict__ slot_of) {
+    const int b = blockIdx.x, p = b * kRouteBlock + threadIdx.x;
+    if (p >= n_pairs) return;
+    const int id = ids[p];
+    int slot = -1;
+    if (wts[p] != 0.0f && id >= 0 && id < n_expert) {
+        slot = base[(size_t)id * gridDim.x + b] + rank[p];
+        slot_tok[slot] = p / k;
+    }
+    slot_of[p] = slot;
+}
+
+// Workspace of launch_moe_route: hist (n_expert x blocks), rank (one per
+// pair), flags (n_expert + 1).
+static size_t moe_route_work_bytes(int n_pairs, int n_expert) {
+    auto al = [](size_t n) { return (n + 255) / 256 * 256; };
+    return al((size_t)n_expert * route_blocks(n_pairs) * 4) + al((size_t)n_pairs * 4) +
+           al(((size_t)n_expert + 1) * 4);
+}
+
+static hipError_t launch_moe_route(const int *ids, const float *wts, int n_pairs, int k,
+                                   int n_expert, uint8_t *work, int *off, int *slot_tok,
+                                   int *slot_of, int *act, int *n_act, MfgBatch *bat, int *n_bat,
+                                   hipStream_t s) {
+    auto al = [](size_t n) { return (n + 255) / 256 * 256; };
+    const int nblk = route_blocks(n_pairs);
+    int *hist = reinterpret_cast<int *>(work);
+    int *rank = reinterpret_cast<int *>(work + al((size_t)n_expert * nblk * 4));
+    int *flags = reinterpret_cast<int *>(work + al((size_t)n_expert * nblk * 4) +
+                                         al((size_t)n_pairs * 4));
+    k_moe_hist<<<(unsigned)nblk, kRouteBlock, (size_t)n_expert * 4, s>>>(ids, wts, n_pairs,
+                                                                          n_expert, hist, rank);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_moe_scan<<<1, kScanThreads, 0, s>>>(hist, nblk, n_expert, off, act, n_act, bat, n_bat,
+                                          flags);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    k_moe_scatter<<<(unsigned)nblk, kRouteBlock, 0, s>>>(ids, wts, n_pairs, k, n_expert, hist,
+                                                         rank, slot_tok, slot_of);
+    return hipGetLastError();
 }
 
 __global__ __launch_bounds__(256) void k_moe_accumulate(float *__restrict__ out,
@@ -128,7 +242,7 @@ struct MoeRoute {
 };
 
 // Threads p < P route pair p (P = n_tok * k <= kFusedPairs). Slots sorted by
-// expert, ties in pair order, as k_moe_route; skipped pairs (w == 0 or an
+// expert, ties in pair order, as the grid-wide routing; skipped pairs (w == 0 or an
 // expert id out of range) get no slot. Ends with a workgroup barrier.
 __device__ __forceinline__ void moe_route_lds(MoeRoute &r, int e_p, float w_p, int P, int k,
                                               int n_expert) {
@@ -547,8 +661,21 @@ static hipError_t moe_fused(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, 
     return e;
 }
 
-size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_expert,
-                         int n_embd, int n_ff) {
+// Pairs one pass of the layer takes: longer calls (prefill) run in token
+// chunks of at most this many (token, slot) pairs. Tokens are independent, so
+// the result is the same as one pass; the chunk bounds the workspace (about
+// 44 KB per pair at n_embd 4096, n_ff 2048) and each chunk re-reads the
+// experts it routes to.
+constexpr int kMoeMaxPairs = 8192;
+
+static int moe_chunk_tokens(int n_tok, int k) {
+    const int c = kMoeMaxPairs / k;
+    return c < 1 ? 1 : c < n_tok ? c : n_tok;
+}
+
+// Workspace of one pass over n_tok tokens.
+static size_t moe_pass_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_expert,
+                             int n_embd, int n_ff) {
     const size_t P = (size_t)n_tok * k;
     size_t b = 0;
     auto add = [&](size_t n) { b += (n + 255) / 256 * 256; };
@@ -556,6 +683,7 @@ size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_
     add((size_t)(n_expert + 1) * 4);                      // act, n_act
     add(P * 4);                                           // slot_tok
     add(P * 4);                                           // slot_of
+    add(moe_route_work_bytes((int)P, n_expert));          // routing
     add(gemv_scratch_bytes(dt_gu, n_tok, n_embd));        // x limbs
     add(P * n_ff * 4);                                    // hg
     add(P * n_ff * 4);                                    // hu
@@ -564,6 +692,12 @@ size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_
     if (moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff))
         add(moe_mfma_scratch_bytes((int)P, n_expert, n_embd, n_ff));
     return b;
+}
+
+size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_expert,
+                         int n_embd, int n_ff) {
+    if (n_tok <= 0 || k <= 0) return 0;
+    return moe_pass_bytes(dt_gu, dt_d, moe_chunk_tokens(n_tok, k), k, n_expert, n_embd, n_ff);
 }
 
 // Calls the fused pair does not take in one go run, from this many tokens,
@@ -575,11 +709,12 @@ size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_
 // chunks are faster (276 vs 226 us at 4).
 constexpr int kMoeMfmaMinTok = 8;
 
-hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
-                      const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
-                      const int *ids, const float *wts, float *out, uint8_t *scratch, int n_tok,
-                      int k, int n_expert, int n_embd, int n_ff, float clamp, hipStream_t s) {
-    if (n_tok <= 0 || k <= 0) return hipSuccess;
+// One pass over n_tok tokens (n_tok * k <= kMoeMaxPairs).
+static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
+                           const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
+                           const int *ids, const float *wts, float *out, uint8_t *scratch,
+                           int n_tok, int k, int n_expert, int n_embd, int n_ff, float clamp,
+                           hipStream_t s) {
     const size_t P = (size_t)n_tok * k;
     uint8_t *p = scratch;
     auto take = [&](size_t n) {
@@ -592,6 +727,7 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
     int *n_act = act + n_expert;
     int *slot_tok = reinterpret_cast<int *>(take(P * 4));
     int *slot_of = reinterpret_cast<int *>(take(P * 4));
+    uint8_t *route_work = take(moe_route_work_bytes((int)P, n_expert));
     const size_t xq1_bytes = gemv_scratch_bytes(dt_gu, n_tok, n_embd);
     uint8_t *xq1 = take(xq1_bytes);
     float *hg = reinterpret_cast<float *>(take(P * n_ff * 4));
@@ -602,14 +738,13 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
     const bool fused1 = moe_fused_fits(dt_gu, dt_d, n_tok, k, n_embd, n_ff, gu_stride, d_stride);
     const bool mfma = !fused1 && moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff) &&
                       n_tok >= kMoeMfmaMinTok && gu_stride <= 0xFFFFFFFFu &&
-                      d_stride <= 0xFFFFFFFFu && P <= (size_t)1 << 20;
+                      d_stride <= 0xFFFFFFFFu;
     if (mfma) {
         uint8_t *mscratch = take(moe_mfma_scratch_bytes((int)P, n_expert, n_embd, n_ff));
         MfgBatch *bat = reinterpret_cast<MfgBatch *>(mscratch);
         int *n_bat = reinterpret_cast<int *>(mscratch + mfg_batch_bytes((int)P, n_expert) - 256);
-        k_moe_route<<<1, 256, (size_t)(n_expert + 1 + P) * 4, s>>>(
-            ids, wts, (int)P, k, n_expert, off, slot_tok, slot_of, act, n_act, bat, n_bat);
-        hipError_t e = hipGetLastError();
+        hipError_t e = launch_moe_route(ids, wts, (int)P, k, n_expert, route_work, off, slot_tok,
+                                        slot_of, act, n_act, bat, n_bat, s);
         if (e != hipSuccess) return e;
         if ((e = launch_moe_mfma(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x, slot_tok,
                                  bat, n_bat, (int)P, n_expert, hg, hu, yd, mscratch, n_embd, n_ff,
@@ -641,10 +776,8 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
     }
     // at most min(n_expert, n_tok * k) experts are active
     const int grid_experts = (int)(P < (size_t)n_expert ? P : (size_t)n_expert);
-
-    k_moe_route<<<1, 256, (size_t)(n_expert + 1 + P) * 4, s>>>(
-        ids, wts, (int)P, k, n_expert, off, slot_tok, slot_of, act, n_act, nullptr, nullptr);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_moe_route(ids, wts, (int)P, k, n_expert, route_work, off, slot_tok,
+                                    slot_of, act, n_act, nullptr, nullptr, s);
     if (e != hipSuccess) return e;
     if ((e = launch_quantize_x(dt_gu, x, xq1, n_tok, n_embd, s)) != hipSuccess) return e;
     if ((e = launch_gemv_grouped(dt_gu, gate, up, gu_stride, xq1, xq1_bytes, off, slot_tok, act,
@@ -659,6 +792,23 @@ hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const 
     k_moe_accumulate<<<(unsigned)(((size_t)n_tok * n_embd + 255) / 256), 256, 0, s>>>(
         out, yd, wts, slot_of, n_tok, k, n_embd);
     return hipGetLastError();
+}
+
+hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
+                      const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
+                      const int *ids, const float *wts, float *out, uint8_t *scratch, int n_tok,
+                      int k, int n_expert, int n_embd, int n_ff, float clamp, hipStream_t s) {
+    if (n_tok <= 0 || k <= 0) return hipSuccess;
+    const int ct = moe_chunk_tokens(n_tok, k);
+    for (int t0 = 0; t0 < n_tok; t0 += ct) {
+        const int nt = n_tok - t0 < ct ? n_tok - t0 : ct;
+        const hipError_t e =
+            moe_pass(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x + (size_t)t0 * n_embd,
+                     ids + (size_t)t0 * k, wts + (size_t)t0 * k, out + (size_t)t0 * n_embd,
+                     scratch, nt, k, n_expert, n_embd, n_ff, clamp, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 // ---- shared expert (apply_shared_expert, moe.rs:422-455) ---------------------

@@ -30,7 +30,7 @@ def test_gemv_ragged_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
     assert rel_err(got, want) <= REL_TOL
 
 
-# The matrix-core path (5..32 tokens of Q4_K / Q6_K / Q8_0, out_dim >= 1024):
+# The matrix-core path (5..32 tokens of Q4_K / Q6_K, 9..32 of Q8_0):
 # one and two 16-token tiles, partial tiles, row counts off the 16-row tile,
 # few K steps per wavefront (in 256) and many (in 7168), token scales far
 # apart.
@@ -51,6 +51,25 @@ def test_gemv_mfma_batches(oracle, hip, dtype, out_dim, in_dim, n_tok):
     for t in range(n_tok):
         if np.abs(wv[t]).max() > 0:
             assert rel_err(g[t], wv[t]) <= REL_TOL, f"token {t}"
+
+
+# Exact weights and two-plane (hi + lo f16) activations on the matrix cores:
+# matrices of a few rows (where a maximum over few outputs is most
+# sensitive, and f16-rounded weights reached 1.2e-3 on 16 rows) within an
+# fp32-level bound (about 1e-6 measured; one f16 rounding gives 2e-4 and up).
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0])
+@pytest.mark.parametrize("out_dim", [1, 7, 16, 33, 100])
+@pytest.mark.parametrize("n_tok", [9, 16, 32])
+def test_gemv_mfma_exact_weights_few_rows(oracle, hip, dtype, out_dim, n_tok):
+    in_dim = 4096
+    w = synth.weight(dtype, out_dim, in_dim, 1700 + out_dim + n_tok)
+    x = synth.activations(n_tok, in_dim, 1800 + n_tok).reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, x, n_tok, in_dim, out_dim, int(dtype))
+    got = np.empty(n_tok * out_dim, np.float32)
+    hip.matmul_quant_f32(got, w, x, n_tok, in_dim, out_dim, dtype)
+    err = rel_err(got, want)
+    print(f"mfma exact {dtype.name} {out_dim}x{in_dim} T={n_tok}: rel err {err:.3e}")
+    assert err <= 2e-5
 
 
 # The fused matrix-core kernel (5..8 tokens, out_dim >= 8192, f16 x in LDS):

@@ -14,6 +14,13 @@ from rsllm_amd.ggml import GgmlType as G
 
 pytestmark = pytest.mark.gpu
 
+# Bound for the matrix-core routes: the weights reach the MFMA as exact
+# integers with their scales applied in fp32, and every activation as two
+# f16 planes (hi + lo, about 2^-22 relative), so the error is fp32-level
+# (about 1e-6 of max |y| measured); 2e-5 leaves a wide margin and still
+# fails a single f16 rounding of weights or activations (2e-4 and up).
+MFMA_TOL = 2e-5
+
 
 def make_case(n_tok, n_embd, n_ff, n_expert, k, dt_gu, dt_d, seed):
     gate = synth.weight(dt_gu, n_expert * n_ff, n_embd, seed)
@@ -201,10 +208,11 @@ def test_moe_grouped_many_tokens(oracle, hip, dt_gu, dt_d, n_tok, k):
 @pytest.mark.parametrize("n_tok", [9, 16, 32])
 def test_moe_grouped_dsv4_like_shapes(oracle, hip, dt, n_tok):
     """DS-V4-like expert shapes (n_embd 4096, n_ff 2048), all three matrices
-    in one format, checked on up to 6 tokens against the 1e-3 bound. Q4_K
-    takes the matrix-core route (two f16-rounded GEMVs in sequence); Q6_K
-    and Q8_0 exceeded or neared the bound there (1.2e-3, 9.3e-4) and take
-    the int8-limb routes."""
+    in one format, checked on up to 6 tokens. All three formats take the
+    matrix-core route from 8 tokens; its weights are exact and x and the
+    SwiGLU output reach it as hi + lo f16 planes, so the chained error is
+    held to MFMA_TOL (f16-rounded weights and activations reached 1.2e-3 for
+    Q6_K and 9.3e-4 for Q8_0 here)."""
     n_embd, n_ff, n_expert, k = 4096, 2048, 16, 6
     gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, dt, dt,
                                           700 + n_tok + int(dt))
@@ -216,4 +224,111 @@ def test_moe_grouped_dsv4_like_shapes(oracle, hip, dt, n_tok):
                       ids[toks], w[toks], len(toks), n_embd, n_ff, n_expert, k, dt, dt)
     err = rel_err(got.reshape(n_tok, n_embd)[toks], want.reshape(len(toks), n_embd))
     print(f"moe dsv4-like {dt.name} T={n_tok}: rel err {err:.3e}")
+    assert err <= MFMA_TOL
+
+
+# ---- prefill-sized calls: every token of a forward pass (moe.rs:281,346) ----
+
+def _subset_check(oracle, got, x, gate, up, down, ids, w, toks, n_embd, n_ff, n_expert, k, dt_gu,
+                  dt_d, base=None):
+    n_tok = x.shape[0]
+    b = np.zeros(len(toks) * n_embd, np.float32) if base is None else base[toks].reshape(-1).copy()
+    want = run_oracle(oracle, b, x[toks], gate, up, down, ids[toks], w[toks], len(toks), n_embd,
+                      n_ff, n_expert, k, dt_gu, dt_d)
+    g = got.reshape(n_tok, n_embd)[toks]
+    if base is not None:
+        g = g - base[toks]
+        want = want.reshape(len(toks), n_embd) - base[toks]
+    return rel_err(g, want.reshape(len(toks), n_embd))
+
+
+def test_moe_prefill_2048_tokens_top6_256_experts(oracle, hip):
+    """DS-V4 routing at prefill size: 2048 tokens, top-6 of 256 experts
+    (12288 pairs, past the 4096 the first build refused; two token chunks of
+    the 8192-pair pass), Q4_K experts on the matrix-core route, checked on
+    tokens from both chunks and at the chunk edge."""
+    n_tok, n_embd, n_ff, n_expert, k = 2048, 1024, 1024, 256, 6
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.Q4_K, G.Q4_K, 4100)
+    w[5, 2] = 0.0   # skipped slots
+    w[1700, 0] = 0.0
+    base = synth.activations(n_tok, n_embd, 4101)
+    got = base.reshape(-1).copy()
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   G.Q4_K, G.Q4_K, 10.0)
+    toks = np.array([0, 5, 700, 1364, 1365, 1700, 2047])
+    err = _subset_check(oracle, got, x, gate, up, down, ids, w, toks, n_embd, n_ff, n_expert, k,
+                        G.Q4_K, G.Q4_K, base=base)
+    print(f"moe prefill T={n_tok} k={k} E={n_expert}: rel err {err:.3e}")
     assert err <= REL_TOL
+
+
+def test_moe_prefill_iq2xxs_q2k_multilaunch_route(oracle, hip):
+    """The real DS-V4-Flash expert formats (IQ2_XXS gate/up, Q2_K down) at
+    1500 tokens x top-6 (9000 pairs: two chunks) through the int8-limb grouped
+    GEMVs."""
+    n_tok, n_embd, n_ff, n_expert, k = 1500, 512, 256, 64, 6
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.IQ2_XXS, G.Q2_K,
+                                          4200)
+    got = np.zeros(n_tok * n_embd, np.float32)
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   G.IQ2_XXS, G.Q2_K, 10.0)
+    toks = np.array([0, 1, 681, 1364, 1365, 1366, 1499])
+    err = _subset_check(oracle, got, x, gate, up, down, ids, w, toks, n_embd, n_ff, n_expert, k,
+                        G.IQ2_XXS, G.Q2_K)
+    print(f"moe prefill IQ2_XXS/Q2_K T={n_tok}: rel err {err:.3e}")
+    assert err <= REL_TOL
+
+
+def test_moe_many_pairs_one_expert_and_device_form(oracle, hip):
+    """Every pair on one expert (one long slot run across 40 routing blocks of
+    256 pairs) through the device-pointer form, against the host form."""
+    import torch
+    n_tok, n_embd, n_ff, n_expert, k = 2560, 256, 512, 4, 4
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.Q4_K, G.Q4_K, 4300)
+    ids[:] = 2
+    got = np.zeros(n_tok * n_embd, np.float32)
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   G.Q4_K, G.Q4_K, 10.0)
+    toks = np.array([0, 2047, 2048, 2559])
+    err = _subset_check(oracle, got, x, gate, up, down, ids, w, toks, n_embd, n_ff, n_expert, k,
+                        G.Q4_K, G.Q4_K)
+    assert err <= REL_TOL
+    s = torch.cuda.current_stream().cuda_stream
+    d = [torch.from_numpy(np.ascontiguousarray(a)).cuda()
+         for a in (gate, up, down, x.reshape(-1), ids.reshape(-1), w.reshape(-1))]
+    y = torch.zeros(n_tok * n_embd, dtype=torch.float32, device="cuda")
+    hip.moe_routed_dev(y.data_ptr(), y.numel(), d[3].data_ptr(), d[3].numel(), d[0].data_ptr(),
+                       d[1].data_ptr(), gate.nbytes, d[2].data_ptr(), down.nbytes,
+                       d[4].data_ptr(), d[5].data_ptr(), ids.size, n_tok, n_embd, n_ff, n_expert,
+                       k, G.Q4_K, G.Q4_K, 10.0, s)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), got.view(np.uint32))
+
+
+# ---- C3 at its real expert count (64 experts, BASELINE.json configs[3]) ------
+
+@pytest.fixture(scope="module")
+def c3_experts():
+    n_expert, n_embd, n_ff = 64, 7168, 2048
+    return (synth.weight(G.Q4_K, n_expert * n_ff, n_embd, 4400),
+            synth.weight(G.Q4_K, n_expert * n_ff, n_embd, 4401),
+            synth.weight(G.Q4_K, n_expert * n_embd, n_ff, 4402))
+
+
+@pytest.mark.parametrize("n_tok", [8, 32])
+def test_moe_c3_64_experts(oracle, hip, c3_experts, n_tok):
+    """C3 as configured: 64 experts, Q4_K gate/up (2048, 7168) and down
+    (7168, 2048), top-8 with softmax weights, T = 8 and 32, checked on up to
+    6 tokens against the oracle (accumulate_moe_outputs, moe.rs:648-707)."""
+    n_expert, n_embd, n_ff, k = 64, 7168, 2048, 8
+    gate, up, down = c3_experts
+    x = synth.activations(n_tok, n_embd, 4410 + n_tok)
+    ids, w = synth.moe_routing(n_tok, n_expert, k, 4420 + n_tok)
+    got = np.zeros(n_tok * n_embd, np.float32)
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   G.Q4_K, G.Q4_K, 10.0)
+    toks = np.unique(np.linspace(0, n_tok - 1, 6).astype(int))
+    err = _subset_check(oracle, got, x, gate, up, down, ids, w, toks, n_embd, n_ff, n_expert, k,
+                        G.Q4_K, G.Q4_K)
+    print(f"moe C3 64 experts T={n_tok}: rel err {err:.3e}")
+    assert err <= MFMA_TOL

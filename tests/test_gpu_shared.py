@@ -78,12 +78,22 @@ def test_reference_clamp_test_dsv4_shapes(hip):
     assert not out[1:].any()
 
 
-@pytest.mark.parametrize("n_tok", [2, 16])
-def test_shared_expert_dsv4_q8_0(oracle, hip, n_tok):
-    """DS-V4 shared expert shapes (n_embd 4096, n_ff 2048) in Q8_0: the
-    paired gate/up launch at 2 tokens, the matrix-core GEMVs at 16."""
-    err = run_case(oracle, hip, G.Q8_0, G.Q8_0, G.Q8_0, n_tok, 4096, 2048, 10.0, 123)
-    assert err <= REL_TOL
+# The matrix-core GEMVs carry exact weights and two-plane f16 activations
+# (hi + lo), so from 9 tokens, where gate, up and down all run on them, the
+# chained result is held to an fp32-level bound (about 2e-6 measured); a
+# single f16 rounding anywhere in the chain fails it.
+MFMA_TOL = 2e-5
+
+
+@pytest.mark.parametrize("dt", [G.Q8_0, G.Q6_K, G.Q4_K])
+@pytest.mark.parametrize("n_tok", [2, 16, 32])
+def test_shared_expert_dsv4(oracle, hip, dt, n_tok):
+    """DS-V4 shared expert shapes (n_embd 4096, n_ff 2048): the paired
+    gate/up launch at 2 tokens; at 16 and 32 gate, up and down on the matrix
+    cores, within MFMA_TOL."""
+    err = run_case(oracle, hip, dt, dt, dt, n_tok, 4096, 2048, 10.0, 123 + n_tok)
+    print(f"shared dsv4 {dt.name} T={n_tok}: rel err {err:.3e}")
+    assert err <= (MFMA_TOL if n_tok >= 9 else REL_TOL)
 
 
 @pytest.mark.parametrize("dg,du,dd", [(G.Q8_0, G.Q8_0, G.Q6_K), (G.F32, G.Q4_K, G.Q8_0)])
