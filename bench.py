@@ -125,6 +125,38 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
     res["roofline"] = {"bound": "mfma", "achieved": best["tflops"], "peak": MFMA_F16_PEAK_TFLOPS,
                        "unit": "TFLOP/s", "frac": best["frac_of_peak"],
                        "tokens": best["tokens"]}
+    # The reference's own prefill call: matmul_quant_f32 with f32 x and n_tok
+    # = T (engine_impl.rs:277 -> weight.rs:161-163 -> quant_matmul.rs:45),
+    # through the drop-in device entry point (f32 -> scaled f16 pre-pass +
+    # the same GEMM), beside the bf16 leg
+    res["f32_x"] = []
+    for T in (512, 2048):
+        x_host = synth.activations(T, in_dim, seed=406).reshape(-1)
+        d_x = torch.from_numpy(x_host).to(dev)
+        d_y = torch.empty(T * out_dim, dtype=torch.float32, device=dev)
+
+        def call_f32(i):
+            B.matmul_quant_f32_dev(d_y.data_ptr(), d_y.numel(), d_w.data_ptr(), d_w.numel(),
+                                   d_x.data_ptr(), d_x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
+        for i in range(3):
+            call_f32(i)
+        us = _time(call_f32, iters, stream)
+        tflops = 2.0 * T * in_dim * out_dim / (us * 1e-6) / 1e12
+        bf = next(e for e in res["by_tokens"] if e["tokens"] == T)
+        entry = {"tokens": T, "us_per_op": round(us, 2), "tflops": round(tflops, 1),
+                 "frac_of_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                 "vs_bf16_leg": round(bf["us_per_op"] / us, 3)}
+        if with_cpu and T == 512:
+            from oracle import oracle as O
+            toks = np.linspace(0, T - 1, 8).astype(int)
+            rc, want = O.matmul_quant_f32(w_host, x_host.reshape(T, in_dim)[toks].reshape(-1),
+                                          len(toks), in_dim, out_dim, int(G.Q4_K))
+            got = d_y.cpu().numpy().reshape(T, out_dim)[toks].reshape(-1)
+            entry["check"] = {"max_rel_err_vs_oracle": float(np.abs(got - want).max() /
+                                                             np.abs(want).max()),
+                              "tokens_checked": len(toks), "tolerance": 1e-3}
+        res["f32_x"].append(entry)
+        del d_x, d_y
     if with_cpu:
         # reference CPU path (oracle, all host threads = min(n_tok, cores) as
         # the rayon split gives) on a bounded token sample, scaled to TFLOP/s

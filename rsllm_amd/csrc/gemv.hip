@@ -570,7 +570,24 @@ size_t gemv_scratch_bytes(uint32_t dtype, int n_tok, int in_dim) {
     }
 }
 
+// Routes for more than 32 tokens (prefill, n_tok = T): Q4_K with in_dim a
+// multiple of 256 takes the prefill GEMM; Q6_K / Q8_0 with in_dim a multiple
+// of 256 the exact matrix-core GEMV over 32-token chunks (one weight pass per
+// 32 tokens instead of per 8 on the int8-limb GEMV).
+enum class Prefill { none, gemm_q4k, mfma_chunks };
+static Prefill prefill_route(uint32_t dtype, int n_tok, int in_dim) {
+    if (n_tok <= 32 || in_dim <= 0 || in_dim % 256 != 0) return Prefill::none;
+    if (dtype == T_Q4_K) return Prefill::gemm_q4k;
+    if (dtype == T_Q6_K || dtype == T_Q8_0) return Prefill::mfma_chunks;
+    return Prefill::none;
+}
+
 size_t gemv_work_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
+    switch (prefill_route(dtype, n_tok, in_dim)) {
+    case Prefill::gemm_q4k: return prefill_scratch_bytes(n_tok, in_dim);
+    case Prefill::mfma_chunks: return gemv_mfma_scratch_bytes(32, in_dim);
+    default: break;
+    }
     size_t b = gemv_scratch_bytes(dtype, n_tok, in_dim);
     if (gemv_mfma_supported(dtype, n_tok, in_dim, out_dim)) {
         const size_t m = gemv_mfma_scratch_bytes(n_tok, in_dim);
@@ -890,6 +907,25 @@ hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const f
                        uint8_t *xq_scratch, float *y, int n_tok, int in_dim, int out_dim,
                        hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
+    switch (prefill_route(dtype, n_tok, in_dim)) {
+    case Prefill::gemm_q4k:
+        // the GEMM's global->LDS copies move 16-byte pieces
+        if ((((uintptr_t)w | (uintptr_t)x) & 15) == 0)
+            return launch_prefill_q4k_f32(w, x, xq_scratch, y, n_tok, in_dim, out_dim, s);
+        break;
+    case Prefill::mfma_chunks:
+        // every chunk, a short tail included, on the matrix cores (which pad
+        // a partial token tile), so all tokens get the same exact weights
+        for (int t0 = 0; t0 < n_tok; t0 += 32) {
+            const int nt = n_tok - t0 < 32 ? n_tok - t0 : 32;
+            const hipError_t e =
+                launch_gemv_mfma(dtype, w, w_bytes, x + (size_t)t0 * in_dim, xq_scratch,
+                                 y + (size_t)t0 * out_dim, nt, in_dim, out_dim, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    default: break;
+    }
     if (gemv_mfma_supported(dtype, n_tok, in_dim, out_dim))
         return launch_gemv_mfma(dtype, w, w_bytes, x, xq_scratch, y, n_tok, in_dim, out_dim, s);
     const int bt = gemv1_tokens(dtype, n_tok, in_dim);

@@ -55,9 +55,10 @@ inline bool layout_converted(uint32_t t) {
 // gemv.hip: y[t, o] = sum_i W[o, i] x[t, i] for t < n_tok, W (w_bytes bytes)
 // in device layout. Batch 1 is one launch that quantises x in LDS; 5..32
 // tokens of Q4_K / Q6_K and 9..32 of Q8_0 run on the matrix cores
-// (gemv_mfma.hip); other
-// batches run the activation pre-pass, then the GEMV. `xq_scratch` must hold
-// gemv_work_bytes(dtype, n_tok, in_dim, out_dim) bytes.
+// (gemv_mfma.hip); more than 32 tokens (prefill) of Q4_K run the prefill GEMM
+// (prefill.hip), of Q6_K / Q8_0 the matrix-core GEMV in 32-token chunks;
+// other batches run the activation pre-pass, then the GEMV. `xq_scratch`
+// must hold gemv_work_bytes(dtype, n_tok, in_dim, out_dim) bytes.
 hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
                        uint8_t *xq_scratch, float *y, int n_tok, int in_dim, int out_dim,
                        hipStream_t s);
@@ -176,6 +177,11 @@ size_t prefill_scratch_bytes(int n_tok, int in_dim);
 hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *x_bf16,
                               uint8_t *scratch, float *out, int n_tok, int in_dim, int out_dim,
                               hipStream_t s);
+// The same GEMM on f32 activations x [n_tok x in_dim] (16-byte aligned; w
+// 16-byte aligned): each element rounded once to f16 after the per-token
+// 2^e scaling. Same scratch.
+hipError_t launch_prefill_q4k_f32(const uint8_t *w, const float *x, uint8_t *scratch, float *out,
+                                  int n_tok, int in_dim, int out_dim, hipStream_t s);
 
 // moe.hip: routed experts (accumulate_moe_outputs). Expert e of gate/up is
 // at gate/up + e * gu_stride, of down at down + e * d_stride (device

@@ -134,6 +134,73 @@ __global__ __launch_bounds__(256) void k_prefill_x(const uint16_t *__restrict__ 
     }
 }
 
+// f32 activations (the reference's own prefill input, engine_impl.rs:277 ->
+// weight.rs:161-163 -> quant_matmul.rs:45 with n_tok = T): the same scaled
+// f16 image. Each element is rounded once to f16 (at most 2^-11 relative);
+// pieces of 8 elements (two 16-byte loads), up to kPxCache per thread kept
+// in registers between the max pass and the conversion (in_dim <= 16384).
+__global__ __launch_bounds__(256) void k_prefill_x_f32(const float *__restrict__ x,
+                                                       _Float16 *__restrict__ xh,
+                                                       float *__restrict__ unscale, int in_dim) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float4 *xt = reinterpret_cast<const float4 *>(x + (size_t)t * in_dim);
+    uint4 *ht = reinterpret_cast<uint4 *>(xh + (size_t)t * in_dim);
+    const int n8 = in_dim >> 3;
+    const bool cached = n8 <= 256 * kPxCache;
+    float4 c[kPxCache][2];
+    auto amax8 = [](const float4 &a, const float4 &b) {
+        const float m0 = fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w)));
+        const float m1 = fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)));
+        return fmaxf(m0, m1);  // NaN lanes drop out of fmaxf
+    };
+    float m = 0.f;
+    if (cached) {
+#pragma unroll
+        for (int i = 0; i < kPxCache; i++) {
+            const int idx = i * 256 + tid;
+            if (idx < n8) {
+                c[i][0] = xt[2 * idx];
+                c[i][1] = xt[2 * idx + 1];
+                m = fmaxf(m, amax8(c[i][0], c[i][1]));
+            }
+        }
+    } else {
+        for (int idx = tid; idx < n8; idx += 256) m = fmaxf(m, amax8(xt[2 * idx], xt[2 * idx + 1]));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // e: amax * 2^e in [2^14, 2^15) for finite nonzero amax
+    int e = 0;
+    if (amax > 0.f && amax <= 3.4e38f) {
+        const int ex = (int)((__float_as_uint(amax) >> 23) & 0xFF) - 127;
+        e = 14 - (ex < -126 ? -126 : ex);
+        if (e > 120) e = 120;
+    }
+    const float up = __uint_as_float((uint32_t)(127 + e) << 23);
+    if (tid == 0) unscale[t] = __uint_as_float((uint32_t)(127 - e) << 23);
+    auto cvt = [&](const float4 &a, const float4 &b) {
+        h8 h;
+        h[0] = (_Float16)(a.x * up); h[1] = (_Float16)(a.y * up);
+        h[2] = (_Float16)(a.z * up); h[3] = (_Float16)(a.w * up);
+        h[4] = (_Float16)(b.x * up); h[5] = (_Float16)(b.y * up);
+        h[6] = (_Float16)(b.z * up); h[7] = (_Float16)(b.w * up);
+        return __builtin_bit_cast(uint4, h);
+    };
+    if (cached) {
+#pragma unroll
+        for (int i = 0; i < kPxCache; i++) {
+            const int idx = i * 256 + tid;
+            if (idx < n8) ht[idx] = cvt(c[i][0], c[i][1]);
+        }
+    } else {
+        for (int idx = tid; idx < n8; idx += 256) ht[idx] = cvt(xt[2 * idx], xt[2 * idx + 1]);
+    }
+}
+
 // ---- GEMM -------------------------------------------------------------------------
 // Eight f16 weights of one chunk: qs bytes b0..b7 are dwords d0 (b0..b3) and
 // d1 (b4..b7); `hi` selects the high nibbles. w = q * dsc - dm.
@@ -403,7 +470,8 @@ size_t prefill_scratch_bytes(int n_tok, int in_dim) {
     return ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16 + tiles * kPfTok * 4;
 }
 
-hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *x_bf16,
+// The GEMM on the pre-pass's image; x is bf16 (x_bf16) or f32 (x_f32).
+static hipError_t prefill_q4k(const uint8_t *w, const uint16_t *x_bf16, const float *x_f32,
                               uint8_t *scratch, float *out, int n_tok, int in_dim, int out_dim,
                               hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
@@ -414,17 +482,31 @@ hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    (void)w_bytes;
     const size_t tiles = ((size_t)n_tok + kPfTok - 1) / kPfTok;
     const size_t xb = ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16;
     _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
     float *unscale = reinterpret_cast<float *>(scratch + xb);
-    k_prefill_x<<<(unsigned)n_tok, 256, 0, s>>>(x_bf16, xh, unscale, in_dim);
+    if (x_f32)
+        k_prefill_x_f32<<<(unsigned)n_tok, 256, 0, s>>>(x_f32, xh, unscale, in_dim);
+    else
+        k_prefill_x<<<(unsigned)n_tok, 256, 0, s>>>(x_bf16, xh, unscale, in_dim);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 grid((unsigned)((out_dim + kPfRowsWg - 1) / kPfRowsWg), (unsigned)tiles);
     k_prefill_q4k<<<grid, 256, kPfLds, s>>>(w, xh, unscale, out, n_tok, in_dim, out_dim);
     return hipGetLastError();
+}
+
+hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *x_bf16,
+                              uint8_t *scratch, float *out, int n_tok, int in_dim, int out_dim,
+                              hipStream_t s) {
+    (void)w_bytes;
+    return prefill_q4k(w, x_bf16, nullptr, scratch, out, n_tok, in_dim, out_dim, s);
+}
+
+hipError_t launch_prefill_q4k_f32(const uint8_t *w, const float *x, uint8_t *scratch, float *out,
+                                  int n_tok, int in_dim, int out_dim, hipStream_t s) {
+    return prefill_q4k(w, nullptr, x, scratch, out, n_tok, in_dim, out_dim, s);
 }
 
 }  // namespace rsllm_hip

@@ -1,0 +1,121 @@
+"""The reference's own prefill call on the GPU: matmul_quant_f32 with f32
+activations and n_tok = T (rsllm-models/src/engine_impl.rs:277 ->
+dsv4/weight.rs:161-163 -> backend-cpu/src/ops/quant_matmul.rs:45-119),
+through the drop-in entry points, against the oracle.
+
+Routes above 32 tokens:
+* Q4_K: the prefill GEMM on the matrix cores (f32 x scaled per token by 2^e
+  and rounded once to f16; weights f16(d*sc)*q - f16(dmin*m)): within the
+  north star's 1e-3 (REL_TOL), overall and per token for tokens with at
+  least 1000 outputs, about 3e-4 measured on C4;
+* Q6_K, Q8_0: the exact matrix-core GEMV (integer weights, hi + lo f16
+  activations) over 32-token chunks, a short tail included: an fp32-level
+  bound (2e-5) on every token;
+* other formats: the int8-limb GEMV (REL_TOL).
+A device pointer that is not 16-byte aligned keeps the Q4_K call off the
+GEMM (its global->LDS copies move 16-byte pieces) and must still be right."""
+import numpy as np
+import pytest
+
+from conftest import REL_TOL, rel_err
+from rsllm_amd import synth
+from rsllm_amd.ggml import GgmlType as G
+
+pytestmark = pytest.mark.gpu
+
+EXACT_TOL = 2e-5
+
+
+def prepared(torch, hip, dtype, w, in_dim):
+    raw = torch.from_numpy(w).cuda()
+    if dtype == G.Q4_K:
+        return raw
+    d = torch.empty_like(raw)
+    hip.prepare_weights_dev(d.data_ptr(), raw.data_ptr(), raw.numel(), dtype, in_dim,
+                            torch.cuda.current_stream().cuda_stream)
+    return d
+
+
+def run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim, x_offset=0):
+    import torch
+    s = torch.cuda.current_stream().cuda_stream
+    d_w = prepared(torch, hip, dtype, w, in_dim)
+    # x_offset floats of padding in front: an x pointer off 16-byte alignment
+    d_x = torch.from_numpy(np.concatenate([np.zeros(x_offset, np.float32), x])).cuda()
+    d_y = torch.full((n_tok * out_dim,), float("nan"), device="cuda")
+    hip.matmul_quant_f32_dev(d_y.data_ptr(), d_y.numel(), d_w.data_ptr(), w.size,
+                             d_x.data_ptr() + 4 * x_offset, x.size, n_tok, in_dim, out_dim, dtype,
+                             s)
+    torch.cuda.synchronize()
+    return d_y.cpu().numpy()
+
+
+def check(oracle, got, w, x, tokens, dtype, n_tok, in_dim, out_dim, tol, per_token):
+    xs = x.reshape(n_tok, in_dim)[tokens].reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, xs, len(tokens), in_dim, out_dim, int(dtype))
+    assert rc == 0
+    g = got.reshape(n_tok, out_dim)[tokens]
+    want = want.reshape(len(tokens), out_dim)
+    assert not np.isnan(g).any()
+    err = rel_err(g, want)
+    print(f"prefill f32 {dtype.name} {out_dim}x{in_dim} T={n_tok}: rel err {err:.3e}")
+    assert err <= tol
+    if per_token:
+        for i in range(len(tokens)):
+            if np.abs(want[i]).max() > 0:
+                assert rel_err(g[i], want[i]) <= tol, f"token {tokens[i]}"
+    return err
+
+
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K])
+@pytest.mark.parametrize("out_dim,in_dim", [(300, 768), (1000, 2048), (4097, 256)])
+@pytest.mark.parametrize("n_tok", [33, 40, 100, 129])
+def test_prefill_f32_ragged(oracle, hip, dtype, out_dim, in_dim, n_tok):
+    w = synth.weight(dtype, out_dim, in_dim, seed=2000 + out_dim + n_tok)
+    x = synth.activations(n_tok, in_dim, seed=2100 + n_tok)
+    # token scales 1e-3 .. 1e3: each token is scaled on its own
+    x *= (np.float32(10.0) ** ((np.arange(n_tok) % 7) - 3)).astype(np.float32)[:, None]
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    got = run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim)
+    tol = EXACT_TOL if dtype in (G.Q6_K, G.Q8_0) else REL_TOL
+    per_token = dtype != G.Q4_K or out_dim >= 1000
+    check(oracle, got, w, x, np.arange(n_tok), dtype, n_tok, in_dim, out_dim, tol, per_token)
+
+
+@pytest.mark.parametrize("n_tok", [512, 2048])
+def test_prefill_f32_c4(oracle, hip, n_tok):
+    """C4's weights (Q4_K 14336 x 4096) at T = 512 and 2048 with f32 x, the
+    call the reference's prefill makes; oracle on a spread subset of tokens,
+    including both sides of the 128-token tile edges."""
+    out_dim, in_dim = 14336, 4096
+    w = synth.weight(G.Q4_K, out_dim, in_dim, seed=404)
+    x = synth.activations(n_tok, in_dim, seed=2205).reshape(-1)
+    got = run_dev(hip, G.Q4_K, w, x, n_tok, in_dim, out_dim)
+    tokens = np.unique(np.concatenate([np.arange(0, 4), np.arange(126, 130),
+                                       np.linspace(0, n_tok - 1, 12).astype(int)]))
+    check(oracle, got, w, x, tokens, G.Q4_K, n_tok, in_dim, out_dim, REL_TOL, True)
+
+
+@pytest.mark.parametrize("dtype", [G.Q6_K, G.Q8_0])
+def test_prefill_f32_exact_formats_c1_shape(oracle, hip, dtype):
+    """Q6_K / Q8_0 at a decode-FFN shape (14336 x 4096) with 200 tokens: six
+    32-token chunks and an 8-token tail, every token exact to fp32 level."""
+    out_dim, in_dim, n_tok = 14336, 4096, 200
+    w = synth.weight(dtype, out_dim, in_dim, seed=2300)
+    x = synth.activations(n_tok, in_dim, seed=2301).reshape(-1)
+    got = run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim)
+    tokens = np.array([0, 31, 32, 100, 191, 192, 199])
+    check(oracle, got, w, x, tokens, dtype, n_tok, in_dim, out_dim, EXACT_TOL, True)
+
+
+def test_prefill_f32_unaligned_x_and_host_form(oracle, hip):
+    """x off 16-byte alignment (the int8-limb route), and the synchronous
+    host-pointer form (the GEMM), on the same call."""
+    out_dim, in_dim, n_tok = 1000, 2048, 70
+    w = synth.weight(G.Q4_K, out_dim, in_dim, seed=2400)
+    x = synth.activations(n_tok, in_dim, seed=2401).reshape(-1)
+    got = run_dev(hip, G.Q4_K, w, x, n_tok, in_dim, out_dim, x_offset=1)
+    check(oracle, got, w, x, np.arange(n_tok), G.Q4_K, n_tok, in_dim, out_dim, REL_TOL, True)
+    host = np.empty(n_tok * out_dim, np.float32)
+    hip.matmul_quant_f32(host, w, x, n_tok, in_dim, out_dim, G.Q4_K)
+    check(oracle, host, w, x, np.arange(n_tok), G.Q4_K, n_tok, in_dim, out_dim, REL_TOL, True)
