@@ -56,10 +56,11 @@ __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t vo
 // (r16, q) = (lane % 16, lane / 16) supplies weights of row r16 and receives
 // D[4q + i][r16], i = 0..3: four tokens of its own row. Every B value is an
 // exact integer in f16 — Q4_K sc * q (at most 63 * 15), Q6_K sc * (q - 32)
-// (|.| <= 2048), Q8_0 q — and the per-row scales the reference multiplies
-// in f32 (d, dmin * m) are applied to each step's MFMA result in fp32 by the
-// lane that holds that row. Products of two f16 values are exact in fp32,
-// so the weights are exact; the one rounding left is f16(2^e x).
+// (an f16 part and a -1/0/1 remainder where |.| > 2048), Q8_0 q — and the
+// per-row scales the reference multiplies in f32 (d, dmin * m) are applied
+// to each step's MFMA result in fp32 by the lane that holds that row.
+// Products of two f16 values are exact in fp32, so the weights are exact;
+// the activations enter as hi + lo f16 planes (about 2^-22 relative).
 //
 // Each format gives: W (a lane's bytes for one step), elem / piece (the K
 // order: element of MFMA j, lane group q, step s), load, and step<NT>: the
@@ -141,16 +142,15 @@ struct MQ4K {
     }
 };
 
-// Four 6-bit codes (bytes 0..63 of q6) -> f16 (q - 32) * sc. v_perm_b32 pairs
-// each byte with 0x64, the f16 pattern of 1024 + q (exact); subtracting 1056
-// gives q - 32 exactly, and the product with the integer scale sc
-// (|sc (q - 32)| <= 2048) is exact as well.
-__device__ __forceinline__ void q6x4_f16(uint32_t q6, f16x2 sc, f16x2 &w01, f16x2 &w23) {
+// Four 6-bit codes (bytes 0..63 of q6) -> f16 q - 32 (exact): v_perm_b32
+// pairs each byte with 0x64, the f16 pattern of 1024 + q, and subtracting
+// 1056 leaves q - 32.
+__device__ __forceinline__ void q6x4_f16(uint32_t q6, f16x2 &w01, f16x2 &w23) {
     const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, q6, 0x04010400u);
     const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, q6, 0x04030402u);
     const f16x2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};
-    w01 = (__builtin_bit_cast(f16x2, p01) - bias) * sc;
-    w23 = (__builtin_bit_cast(f16x2, p23) - bias) * sc;
+    w01 = __builtin_bit_cast(f16x2, p01) - bias;
+    w23 = __builtin_bit_cast(f16x2, p23) - bias;
 }
 
 // Q6_K (super-tile device layout). Step s = half h = s & 1 of block s >> 1.
@@ -159,6 +159,12 @@ __device__ __forceinline__ void q6x4_f16(uint32_t q6, f16x2 sc, f16x2 &w01, f16x
 // high nibbles elements 128h + 64 + 16q + b (high bits at 4 + 2 (q >> 1));
 // their scales are sc[8h + q] and sc[8h + q + 4]. B = sc * (q - 32), and the
 // step adds d * P (dequant_q6_k, q6_k.rs:86-92: w = d sc (q - 32)).
+// |sc (q - 32)| <= 128 * 32 = 4096: exact in f16 up to 2048, and above that
+// (|sc| > 64, which GGUF's int8 scales allow) f16 keeps the even integers
+// only. So B = f16(sc (q - 32)) and B_lo = sc (q - 32) - B (one fused f16
+// multiply-add, exact, in {-1, 0, 1}); a step whose wavefront has any
+// |sc| > 64 adds x_hi * B_lo as a third MFMA per sub-step, which leaves out
+// only x_lo * B_lo (below 2^-22 of the term).
 struct MQ6K {
     struct W {
         uint4 ql, qh;
@@ -191,13 +197,13 @@ struct MQ6K {
     __device__ static void step(const W &w, int q, const uint4 (&x)[4][NT], const uint4 (&xl)[4][NT],
                                 f32x4 (&acc)[NT]) {
         const float d = f16_to_f32(w.d);
-        const _Float16 scl = (_Float16)(float)(int)(int8_t)(w.sl >> (8 * q));
-        const _Float16 sch = (_Float16)(float)(int)(int8_t)(w.sh >> (8 * q));
-        const f16x2 dsl = {scl, scl}, dsh = {sch, sch};
+        const int il = (int)(int8_t)(w.sl >> (8 * q)), ih = (int)(int8_t)(w.sh >> (8 * q));
+        const _Float16 scl = (_Float16)(float)il, sch = (_Float16)(float)ih;
+        const bool wide = __ballot(il > 64 || il < -64 || ih > 64 || ih < -64) != 0;
         const uint32_t shl = 2u * (uint32_t)(q >> 1), shh = 4u + shl;
         const uint32_t l[4] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w};
         const uint32_t hb[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
-        f16x8 b[4];
+        f16x8 a[4], b[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const bool hi = j & 1;
@@ -207,24 +213,40 @@ struct MQ6K {
             for (int u = 0; u < 2; u++) {
                 const uint32_t nib = hi ? (l[p + u] >> 4) & 0x0F0F0F0Fu : l[p + u] & 0x0F0F0F0Fu;
                 const uint32_t top = ((hb[p + u] >> (hi ? shh : shl)) & 0x03030303u) << 4;
-                q6x4_f16(nib | top, hi ? dsh : dsl, v[2 * u], v[2 * u + 1]);
+                q6x4_f16(nib | top, v[2 * u], v[2 * u + 1]);
             }
             f16x8 r;
             r[0] = v[0][0]; r[1] = v[0][1]; r[2] = v[1][0]; r[3] = v[1][1];
             r[4] = v[2][0]; r[5] = v[2][1]; r[6] = v[3][0]; r[7] = v[3][1];
-            b[j] = r;
+            const _Float16 sc = hi ? sch : scl;
+            const f16x8 sv = {sc, sc, sc, sc, sc, sc, sc, sc};
+            a[j] = r;
+            b[j] = r * sv;
         }
+        f32x4 P[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
-            f32x4 P = {0.f, 0.f, 0.f, 0.f};
+            P[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                P = mfma16x32(x[j][nt], b[j], P);
-                P = mfma16x32(xl[j][nt], b[j], P);
+                P[nt] = mfma16x32(x[j][nt], b[j], P[nt]);
+                P[nt] = mfma16x32(xl[j][nt], b[j], P[nt]);
             }
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[nt][i] = fmaf(d, P[i], acc[nt][i]);
         }
+        if (wide) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const _Float16 sc = (j & 1) ? sch : scl;
+                const f16x8 sv = {sc, sc, sc, sc, sc, sc, sc, sc};
+                const f16x8 bl = __builtin_elementwise_fma(a[j], sv, -b[j]);
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) P[nt] = mfma16x32(x[j][nt], bl, P[nt]);
+            }
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[nt][i] = fmaf(d, P[nt][i], acc[nt][i]);
     }
 };
 
@@ -310,49 +332,103 @@ __device__ __forceinline__ void hilo8(const float4 &v0, const float4 &v1, float 
     lo = __builtin_bit_cast(uint4, l);
 }
 
-// One workgroup per padded token: max |x| over the row, e with max * 2^e in
-// [2^14, 2^15) (e in [-126, 126]; a zero row gets e = 0), then each thread
-// writes 8-element pieces in operand order into both planes (the lo plane
-// ntp * in_dim values after the hi plane). Padding tokens write zeros.
-template <class F>
-__global__ __launch_bounds__(256) void k_mf_x(const float *__restrict__ x, _Float16 *__restrict__ xh,
-                                              float *__restrict__ unscale, int n_tok, int in_dim,
-                                              int ntp) {
-    __shared__ float red[4];
-    const int t = blockIdx.x, tid = threadIdx.x;
-    const int nsteps = in_dim / kMfStep;
-    const bool real = t < n_tok;
-    const float *xt = x + (size_t)(real ? t : 0) * in_dim;
-    float amax = 0.f;
-    if (real)
-        for (int i = tid * 4; i < in_dim; i += 1024) {
-            const float4 v = *reinterpret_cast<const float4 *>(xt + i);
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    if ((tid & 63) == 0) red[tid >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+// Scale exponent of a row whose largest magnitude is amax: amax * 2^e in
+// [2^14, 2^15) (e clamped to [-126, 126]; 0 for a zero or non-finite amax).
+__device__ __forceinline__ int mf_exponent(float amax) {
     int e = 0;
     if (amax > 0.f && amax <= 3.4e38f) {
         int ex;
         frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
         e = min(max(15 - ex, -126), 126);
     }
-    const float up = ldexpf(1.0f, e);
-    if (tid == 0) unscale[t] = real ? ldexpf(1.0f, -e) : 0.f;
+    return e;
+}
+
+__device__ __forceinline__ float max8(const float4 &a, const float4 &b) {
+    return fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                 fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+}
+
+// Max over a workgroup of kMfxThreads threads (every thread gets it); `red`
+// holds one float per wavefront.
+constexpr int kMfxThreads = 1024;
+__device__ __forceinline__ float block_max(float m, float *red) {
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < kMfxThreads / 64; i++) r = fmaxf(r, red[i]);
+    return r;
+}
+
+// One workgroup of kMfxThreads per padded token. Each thread holds up to
+// kMfxCache 8-element pieces of the row (piece i = thread + kMfxThreads r,
+// read once), the workgroup takes the row's max |x|, and the pieces are
+// scaled by 2^e, split into hi and lo and stored in operand order (the lo
+// plane ntp * in_dim values after the hi plane; F::piece gives a piece's
+// slot). Rows longer than kMfxThreads * kMfxCache pieces are read twice.
+// Padding tokens write zeros.
+constexpr int kMfxCache = 4;
+template <class F>
+__global__ __launch_bounds__(kMfxThreads) void k_mf_x(const float *__restrict__ x,
+                                                      _Float16 *__restrict__ xh,
+                                                      float *__restrict__ unscale, int n_tok,
+                                                      int in_dim, int ntp) {
+    __shared__ float red[kMfxThreads / 64];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const bool real = t < n_tok;
+    const int n8 = in_dim / 8;
+    const float4 *xt = reinterpret_cast<const float4 *>(x + (size_t)(real ? t : 0) * in_dim);
     const size_t plane = (size_t)ntp * in_dim;
-    for (int g = tid; g < nsteps * 16; g += 256) {
-        const int s = g >> 4, j = (g >> 2) & 3, q = g & 3;
-        uint4 hi = make_uint4(0, 0, 0, 0), lo = hi;
-        if (real) {
-            const float *p = xt + F::elem(s, j, q);
-            hilo8(*reinterpret_cast<const float4 *>(p), *reinterpret_cast<const float4 *>(p + 4), up,
-                  hi, lo);
+    auto store = [&](int i, const uint4 &hi, const uint4 &lo) {
+        int s, j, q;
+        F::piece(8 * i, s, j, q);
+        const size_t slot = ((size_t)(s * 4 + j) * 4 + q) * ntp + t;
+        *reinterpret_cast<uint4 *>(xh + slot * 8) = hi;
+        *reinterpret_cast<uint4 *>(xh + plane + slot * 8) = lo;
+    };
+    if (!real) {
+        if (tid == 0) unscale[t] = 0.f;
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        for (int i = tid; i < n8; i += kMfxThreads) store(i, z, z);
+        return;
+    }
+    const bool cached = n8 <= kMfxThreads * kMfxCache;
+    float4 c[kMfxCache][2];
+    float m = 0.f;
+    if (cached) {
+#pragma unroll
+        for (int r = 0; r < kMfxCache; r++) {
+            const int i = tid + r * kMfxThreads;
+            if (i < n8) {
+                c[r][0] = xt[2 * i];
+                c[r][1] = xt[2 * i + 1];
+                m = fmaxf(m, max8(c[r][0], c[r][1]));
+            }
         }
-        *reinterpret_cast<uint4 *>(xh + ((size_t)g * ntp + t) * 8) = hi;
-        *reinterpret_cast<uint4 *>(xh + plane + ((size_t)g * ntp + t) * 8) = lo;
+    } else {
+        for (int i = tid; i < n8; i += kMfxThreads) m = fmaxf(m, max8(xt[2 * i], xt[2 * i + 1]));
+    }
+    const int e = mf_exponent(block_max(m, red));
+    const float up = ldexpf(1.0f, e);
+    if (tid == 0) unscale[t] = ldexpf(1.0f, -e);
+    if (cached) {
+#pragma unroll
+        for (int r = 0; r < kMfxCache; r++) {
+            const int i = tid + r * kMfxThreads;
+            if (i < n8) {
+                uint4 hi, lo;
+                hilo8(c[r][0], c[r][1], up, hi, lo);
+                store(i, hi, lo);
+            }
+        }
+    } else {
+        for (int i = tid; i < n8; i += kMfxThreads) {
+            uint4 hi, lo;
+            hilo8(xt[2 * i], xt[2 * i + 1], up, hi, lo);
+            store(i, hi, lo);
+        }
     }
 }
 
@@ -454,41 +530,60 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__
 // its rows go to y + first * out_dim.
 
 // One token column of a kMfgBatch-wide activation image (the k_mf_x
-// conversion, one workgroup of 256 threads): val4(i) gives elements
-// i .. i + 3 of the column's row; the column's pieces go to both planes of
-// the image at xb, 2^-e to *us.
+// conversion, one workgroup of kMfxThreads threads, the row read once when
+// it fits in registers): val4(i) gives elements i .. i + 3 of the column's
+// row; the column's pieces go to both planes of the image at xb, 2^-e to
+// *us.
 template <class F, class V>
 __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 *__restrict__ xb,
                                             float *__restrict__ us) {
-    __shared__ float red[4];
+    __shared__ float red[kMfxThreads / 64];
     const int tid = threadIdx.x;
-    const int nsteps = in_dim / kMfStep;
-    float amax = 0.f;
-    for (int i = tid * 4; i < in_dim; i += 1024) {
-        const float4 v = val4(i);
-        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
+    const int n8 = in_dim / 8;
+    const size_t plane = (size_t)in_dim * kMfgBatch;
+    auto store = [&](int i, const uint4 &hi, const uint4 &lo) {
+        int s, j, q;
+        F::piece(8 * i, s, j, q);
+        const size_t slot = ((size_t)(s * 4 + j) * 4 + q) * kMfgBatch + t;
+        *reinterpret_cast<uint4 *>(xb + slot * 8) = hi;
+        *reinterpret_cast<uint4 *>(xb + plane + slot * 8) = lo;
+    };
+    // pieces read once (kept in registers) when the row fits
+    const bool cached = n8 <= kMfxThreads * kMfxCache;
+    float4 c[kMfxCache][2];
+    float m = 0.f;
+    if (cached) {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    if ((tid & 63) == 0) red[tid >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    int e = 0;
-    if (amax > 0.f && amax <= 3.4e38f) {
-        int ex;
-        frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
-        e = min(max(15 - ex, -126), 126);
+        for (int r = 0; r < kMfxCache; r++) {
+            const int i = tid + r * kMfxThreads;
+            if (i < n8) {
+                c[r][0] = val4(8 * i);
+                c[r][1] = val4(8 * i + 4);
+                m = fmaxf(m, max8(c[r][0], c[r][1]));
+            }
+        }
+    } else {
+        for (int i = tid; i < n8; i += kMfxThreads) m = fmaxf(m, max8(val4(8 * i), val4(8 * i + 4)));
     }
+    const int e = mf_exponent(block_max(m, red));
     const float up = ldexpf(1.0f, e);
     if (tid == 0) *us = ldexpf(1.0f, -e);
-    const size_t plane = (size_t)in_dim * kMfgBatch;
-    for (int g = tid; g < nsteps * 16; g += 256) {
-        const int s = g >> 4, j = (g >> 2) & 3, q = g & 3;
-        const int i = F::elem(s, j, q);
-        uint4 hi, lo;
-        hilo8(val4(i), val4(i + 4), up, hi, lo);
-        *reinterpret_cast<uint4 *>(xb + ((size_t)g * kMfgBatch + t) * 8) = hi;
-        *reinterpret_cast<uint4 *>(xb + plane + ((size_t)g * kMfgBatch + t) * 8) = lo;
+    if (cached) {
+#pragma unroll
+        for (int r = 0; r < kMfxCache; r++) {
+            const int i = tid + r * kMfxThreads;
+            if (i < n8) {
+                uint4 hi, lo;
+                hilo8(c[r][0], c[r][1], up, hi, lo);
+                store(i, hi, lo);
+            }
+        }
+    } else {
+        for (int i = tid; i < n8; i += kMfxThreads) {
+            uint4 hi, lo;
+            hilo8(val4(8 * i), val4(8 * i + 4), up, hi, lo);
+            store(i, hi, lo);
+        }
     }
 }
 
@@ -498,7 +593,7 @@ __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 
 // are: column t of an MFMA's B operand reaches only column t of its result,
 // and those outputs are not stored.
 template <class F, bool SWIGLU>
-__global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
+__global__ __launch_bounds__(kMfxThreads) void k_mfg_x(const float *__restrict__ x,
                                                const float *__restrict__ hu,
                                                const int *__restrict__ tok,
                                                const MfgBatch *__restrict__ bat,
@@ -530,7 +625,7 @@ __global__ __launch_bounds__(256) void k_mfg_x(const float *__restrict__ x,
 // group g = r / R's slice x[t * x_stride + g * D .. + D). Image (g, c) holds
 // tokens 16 c .. 16 c + 15 of group g's slice (kMfgBatch = 16 columns).
 template <class F>
-__global__ __launch_bounds__(256) void k_mfl_x(const float *__restrict__ x, int x_stride, int n_tok,
+__global__ __launch_bounds__(kMfxThreads) void k_mfl_x(const float *__restrict__ x, int x_stride, int n_tok,
                                                int D, int nchunks, _Float16 *__restrict__ xh,
                                                float *__restrict__ unscale) {
     const int b = blockIdx.y, g = b / nchunks, tc = (b - g * nchunks) * kMfgBatch + blockIdx.x;
@@ -823,7 +918,7 @@ static hipError_t mf_go(const uint8_t *w, size_t w_bytes, const float *x, uint8_
     const size_t plane_bytes = (size_t)ntp * in_dim * 2;
     _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
     float *unscale = reinterpret_cast<float *>(scratch + (2 * plane_bytes + 255) / 256 * 256);
-    k_mf_x<F><<<ntp, 256, 0, s>>>(x, xh, unscale, n_tok, in_dim, ntp);
+    k_mf_x<F><<<ntp, kMfxThreads, 0, s>>>(x, xh, unscale, n_tok, in_dim, ntp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int rows_wg = 16 * RT;
@@ -880,9 +975,9 @@ static hipError_t mfg_pass(const uint8_t *w0, const uint8_t *w1, size_t w_stride
                            int in_dim, int out_dim, hipStream_t s) {
     const dim3 gx(kMfgBatch, (unsigned)max_b);
     if (hu)
-        k_mfg_x<F, true><<<gx, 256, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim);
+        k_mfg_x<F, true><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim);
     else
-        k_mfg_x<F, false><<<gx, 256, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim);
+        k_mfg_x<F, false><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     constexpr int NK = 4, RT = 4;
@@ -950,7 +1045,7 @@ static hipError_t mfl_go(const uint8_t *w, size_t w_bytes, const float *x, int x
     const size_t nb = (size_t)G * nchunks;
     _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
     float *us = reinterpret_cast<float *>(scratch + (nb * kMfgBatch * (size_t)D * 4 + 255) / 256 * 256);
-    k_mfl_x<F><<<dim3(kMfgBatch, (unsigned)nb), 256, 0, s>>>(x, x_stride, n_tok, D, nchunks, xh, us);
+    k_mfl_x<F><<<dim3(kMfgBatch, (unsigned)nb), kMfxThreads, 0, s>>>(x, x_stride, n_tok, D, nchunks, xh, us);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int out_dim = G * R;

@@ -115,6 +115,17 @@ def weight(dtype: GgmlType, out_dim: int, in_dim: int, seed: int) -> np.ndarray:
     return _BLOCKS[dtype](rng(seed), n_blocks).reshape(-1)
 
 
+def q6k_full_scales(w: np.ndarray, seed: int) -> np.ndarray:
+    """A copy of a Q6_K weight with its 16 int8 scales per block redrawn from
+    the full int8 range -128..127 (what GGUF files hold; the benchmark's
+    statistics stop at -64..63), sc = -128 and 127 present in every block."""
+    b = np.array(w, dtype=np.uint8).reshape(-1, 210)
+    sc = rng(seed).integers(-128, 128, size=(b.shape[0], 16), dtype=np.int16).astype(np.int8)
+    sc[:, 0], sc[:, 15] = -128, 127
+    b[:, 192:208] = sc.view(np.uint8)
+    return b.reshape(-1)
+
+
 def activations(n_tok: int, dim: int, seed: int) -> np.ndarray:
     """fp32 N(0, 1) activations [n_tok x dim]."""
     return rng(seed).standard_normal((n_tok, dim), dtype=np.float32)

@@ -227,6 +227,23 @@ def test_moe_grouped_dsv4_like_shapes(oracle, hip, dt, n_tok):
     assert err <= MFMA_TOL
 
 
+def test_moe_grouped_q6k_full_range_scales(oracle, hip):
+    """Q6_K experts whose scales span the whole int8 range (sc (q - 32) up to
+    4096, past f16's exact integers) on the grouped matrix-core route: the
+    split f16 + remainder weights keep the chained error at MFMA_TOL."""
+    n_embd, n_ff, n_expert, k, n_tok = 2048, 1024, 8, 4, 16
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.Q6_K, G.Q6_K, 770)
+    gate, up, down = (synth.q6k_full_scales(m, 780 + i) for i, m in enumerate((gate, up, down)))
+    got = np.zeros(n_tok * n_embd, np.float32)
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   G.Q6_K, G.Q6_K, 10.0)
+    want = run_oracle(oracle, np.zeros(n_tok * n_embd, np.float32), x, gate, up, down, ids, w,
+                      n_tok, n_embd, n_ff, n_expert, k, G.Q6_K, G.Q6_K)
+    err = rel_err(got, want)
+    print(f"moe grouped q6k full-range scales T={n_tok}: rel err {err:.3e}")
+    assert err <= MFMA_TOL
+
+
 # ---- prefill-sized calls: every token of a forward pass (moe.rs:281,346) ----
 
 def _subset_check(oracle, got, x, gate, up, down, ids, w, toks, n_embd, n_ff, n_expert, k, dt_gu,
