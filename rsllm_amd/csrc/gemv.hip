@@ -585,12 +585,12 @@ static Prefill prefill_route(uint32_t dtype, int n_tok, int in_dim) {
 size_t gemv_work_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
     switch (prefill_route(dtype, n_tok, in_dim)) {
     case Prefill::gemm_q4k: return prefill_scratch_bytes(n_tok, in_dim);
-    case Prefill::mfma_chunks: return gemv_mfma_scratch_bytes(32, in_dim);
+    case Prefill::mfma_chunks: return gemv_mfma_scratch_bytes(dtype, 32, in_dim, out_dim);
     default: break;
     }
     size_t b = gemv_scratch_bytes(dtype, n_tok, in_dim);
     if (gemv_mfma_supported(dtype, n_tok, in_dim, out_dim)) {
-        const size_t m = gemv_mfma_scratch_bytes(n_tok, in_dim);
+        const size_t m = gemv_mfma_scratch_bytes(dtype, n_tok, in_dim, out_dim);
         if (m > b) b = m;
     }
     return b;

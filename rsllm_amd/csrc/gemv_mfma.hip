@@ -26,6 +26,8 @@
 // row r per step (8 for each of the 4 MFMAs) and holds D for tokens 4q + 0..3
 // of row r. The NK partial tiles are added through LDS in wavefront order
 // (deterministic), scaled by 2^-e_t, stored.
+#include <type_traits>
+
 #include "gemv_formats.h"
 
 namespace rsllm_hip {
@@ -519,6 +521,211 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__
                            blockIdx.x * 16 * RT, red);
 }
 
+// ---- GEMV with the weights staged through LDS -------------------------------------
+// The operand loads of mf_rows give each lane of a 16-row tile its own row,
+// so one load instruction touches 16 rows' cache lines for a few bytes each
+// (L1 requests about 4x those of a contiguous stream). Here a workgroup of 4
+// wavefronts owns kMfsRows = 32 rows and streams them in chunks of kMfsK =
+// 1024 elements: each row's chunk is one contiguous byte range (4 Q4_K
+// blocks; half a Q6_K super-tile's ql / qh / scale runs and its d run; 4
+// Q8_0 super-tiles), copied to LDS with 16-byte global_load_lds pieces in
+// row order (every line read whole, no registers held), two chunks in
+// flight (double buffer, one barrier per chunk). Wavefront w then takes
+// steps 2w, 2w + 1 of the chunk for both row tiles, reading the operand
+// fields from LDS (row strides pad to distinct LDS banks) against the
+// activation image as mf_rows does. The 4 wavefronts' tiles are summed in
+// LDS in wavefront order.
+//
+// Matrices with few rows split K: grid.y = sk workgroups per 32 rows, each
+// over an equal run of chunks, writing its partial tile to part[split]; a
+// second kernel adds the sk partials in split order (deterministic).
+typedef __attribute__((address_space(3))) void lds_void;
+
+// (a non-template wrapper: the builtin called directly inside a kernel
+// template keeps the host pass from emitting that kernel's stub)
+__device__ __forceinline__ void dma16(const void *g, lds_void *l) {
+    __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+}
+
+constexpr int kMfsRows = 32;
+constexpr int kMfsK = 1024;
+
+// Per format: PR 16-byte pieces per row chunk (one pad piece where needed for
+// the bank spread); piece k of chunk c of row r is at byte
+// off0(r, k) + c_off(c, k) of the weights; load() gives a step's operand
+// fields (as F::load) from a row's slice in LDS.
+template <class F> struct MfsStage;
+template <> struct MfsStage<MQ4K> {
+    static constexpr int PR = 37;  // 4 blocks x 144 B = 36 pieces + 1 pad
+    __device__ static uint32_t off0(uint32_t row, int k, int in_dim) {
+        return row * (uint32_t)(in_dim >> 8) * 144u + 16u * (uint32_t)(k < 36 ? k : 0);
+    }
+    __device__ static uint32_t c_off(int c, int) { return (uint32_t)c * 576u; }
+    __device__ static void load(MQ4K::W &v, const uint8_t *r, int st, int q, int) {
+        const int jb = st >> 1, h = st & 1;
+        v.hdr = *reinterpret_cast<const uint4 *>(r + 144 * jb);
+        v.qs = *reinterpret_cast<const uint4 *>(r + 144 * jb + 16 + 32 * q + 16 * h);
+    }
+};
+template <> struct MfsStage<MQ6K> {
+    // half super-tile (in_dim % 2048 == 0, so a row's blocks fill whole
+    // super-tiles): ql 512 B, qh 256 B, scales 64 B (32 + 16 + 4 pieces), and
+    // the super-tile's 16 bytes of d
+    static constexpr int PR = 53;
+    __device__ static uint32_t off0(uint32_t row, int k, int in_dim) {
+        const uint32_t base = row * (uint32_t)(in_dim >> 11) * 1680u;
+        if (k < 32) return base + 16u * k;
+        if (k < 48) return base + 1024u + 16u * (k - 32);
+        if (k < 52) return base + 1536u + 16u * (k - 48);
+        return base + 1664u;
+    }
+    __device__ static uint32_t c_off(int c, int k) {
+        const uint32_t half = k < 32 ? 512u : (k < 48 ? 256u : (k < 52 ? 64u : 0u));
+        return (uint32_t)(c >> 1) * 1680u + (uint32_t)(c & 1) * half;
+    }
+    __device__ static void load(MQ6K::W &v, const uint8_t *r, int st, int q, int c) {
+        const int jb = st >> 1, h = st & 1;
+        v.ql = *reinterpret_cast<const uint4 *>(r + 128 * jb + 64 * h + 16 * q);
+        v.qh = *reinterpret_cast<const uint4 *>(r + 512 + 64 * jb + 32 * h + 16 * (q & 1));
+        v.sl = *reinterpret_cast<const uint32_t *>(r + 768 + 16 * jb + 8 * h);
+        v.sh = *reinterpret_cast<const uint32_t *>(r + 768 + 16 * jb + 8 * h + 4);
+        v.d = *reinterpret_cast<const uint16_t *>(r + 832 + 2 * (4 * (c & 1) + jb));
+    }
+};
+template <> struct MfsStage<MQ8> {
+    static constexpr int PR = 69;  // 4 super-tiles x 272 B = 68 pieces + 1 pad
+    __device__ static uint32_t off0(uint32_t row, int k, int in_dim) {
+        return row * (uint32_t)(in_dim >> 8) * 272u + 16u * (uint32_t)(k < 68 ? k : 0);
+    }
+    __device__ static uint32_t c_off(int c, int) { return (uint32_t)c * 1088u; }
+    __device__ static void load(MQ8::W &v, const uint8_t *r, int st, int q, int) {
+        const uint8_t *t = r + 272 * (st >> 1);
+        const int jb = 4 * (st & 1);
+#pragma unroll
+        for (int j = 0; j < 4; j++) v.q[j] = *reinterpret_cast<const uint2 *>(t + (jb + j) * 32 + 8 * q);
+        v.d = *reinterpret_cast<const uint2 *>(t + 256 + 2 * jb);
+    }
+};
+
+template <class F> struct MfsGeo {
+    static constexpr int PIECES = kMfsRows * MfsStage<F>::PR;
+    static constexpr int P = (PIECES + 255) / 256;  // DMA instructions per thread per chunk
+    static constexpr int BUF = P * 4096;
+    static constexpr int LDS = 2 * BUF;
+};
+
+template <class F, int NT>
+__global__ __launch_bounds__(256) void k_gemv_mfs(const uint8_t *__restrict__ w,
+                                                  const _Float16 *__restrict__ xh,
+                                                  uint32_t plane_bytes,
+                                                  const float *__restrict__ unscale,
+                                                  float *__restrict__ y, int n_tok, int in_dim,
+                                                  int out_dim) {
+    using S = MfsStage<F>;
+    using G = MfsGeo<F>;
+    constexpr int ntp = NT * 16;
+    constexpr int RT = kMfsRows / 16;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int row0 = blockIdx.x * kMfsRows;
+    const int nall = in_dim / kMfsK;
+    const int c0 = nall * (int)blockIdx.y / (int)gridDim.y;
+    const int nch = nall * ((int)blockIdx.y + 1) / (int)gridDim.y - c0;
+    // this thread's DMA pieces: piece g = p * 256 + tid is piece g % PR of
+    // row g / PR (rows past out_dim repeat the last; the pieces past the
+    // tile fill the buffer's tail with copies of piece 0)
+    uint32_t o0[G::P];
+    int pk[G::P];
+#pragma unroll
+    for (int p = 0; p < G::P; p++) {
+        const int g = p * 256 + tid;
+        const int row = min(row0 + (g < G::PIECES ? g / S::PR : 0), out_dim - 1);
+        pk[p] = g < G::PIECES ? g % S::PR : 0;
+        o0[p] = S::off0((uint32_t)row, pk[p], in_dim);
+    }
+    auto dma = [&](int c) {
+        uint8_t *buf = smem + (c & 1) * G::BUF;
+#pragma unroll
+        for (int p = 0; p < G::P; p++)
+            dma16(w + (o0[p] + S::c_off(c0 + c, pk[p])),
+                  (lds_void *)(buf + 16 * (p * 256 + 64 * wv)));
+    };
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xh, 2 * plane_bytes);
+    uint4 xr[2][4][NT], lr[2][4][NT];
+    f32x4 acc[RT][NT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[rt][nt] = {0.f, 0.f, 0.f, 0.f};
+    dma(0);
+    for (int c = 0; c < nch; c++) {
+        // chunk c's pieces (every wavefront's) have landed, and chunk c - 1's
+        // buffer is no longer read
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        // this chunk's activations first, then the next chunk's DMA: the
+        // waits for the activations then leave the DMA in flight
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int st = (c0 + c) * (kMfsK / kMfStep) + 2 * wv + u;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const uint32_t o = (uint32_t)((((st * 4 + j) * 4 + q) * ntp + nt * 16 + r16) * 16);
+                    xr[u][j][nt] = bload16(rx, o, 0);
+                    lr[u][j][nt] = bload16(rx, o + plane_bytes, 0);
+                }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (c + 1 < nch) dma(c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t *buf = smem + (c & 1) * G::BUF;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                typename F::W wr;
+                S::load(wr, buf + (16 * rt + r16) * (S::PR * 16), 2 * wv + u, q, c0 + c);
+                F::template step<NT>(wr, q, xr[u], lr[u], acc[rt]);
+            }
+    }
+    __syncthreads();
+    f32x4 *red = reinterpret_cast<f32x4 *>(smem);
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) red[((wv * RT + rt) * NT + nt) * 64 + lane] = acc[rt][nt];
+    __syncthreads();
+    float *yo = y + (size_t)blockIdx.y * n_tok * out_dim;
+    for (int e = tid; e < RT * NT * 64; e += 256) {
+        const int rt = e / (NT * 64), nt = (e / 64) % NT, ln = e % 64;
+        f32x4 v = red[(rt * NT + nt) * 64 + ln];
+#pragma unroll
+        for (int k = 1; k < 4; k++) v += red[((k * RT + rt) * NT + nt) * 64 + ln];
+        // D: tokens 4 (lane / 16) + 0..3 of weight row lane % 16
+        const int o = row0 + 16 * rt + (ln & 15);
+        const int t0 = nt * 16 + 4 * (ln >> 4);
+        if (o < out_dim) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (t0 + i < n_tok) yo[(size_t)(t0 + i) * out_dim + o] = v[i] * unscale[t0 + i];
+        }
+    }
+}
+
+// y[i] = part[0][i] + part[1][i] + ... + part[sk - 1][i], in split order.
+__global__ __launch_bounds__(256) void k_mfs_sum(const float *__restrict__ part,
+                                                 float *__restrict__ y, int n, int sk) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float v = part[i];
+    for (int k = 1; k < sk; k++) v += part[(size_t)k * n + i];
+    y[i] = v;
+}
+
 // ---- routed experts grouped by expert (many tokens) --------------------------------
 // Slots sorted by expert (moe.hip routing): expert e owns sorted slots [off[e],
 // off[e + 1]), cut into batches of up to kMfgBatch (k_moe_scan lists them);
@@ -905,10 +1112,74 @@ bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
            n_tok <= 32 && in_dim % 256 == 0 && in_dim > 0 && out_dim > 0;
 }
 
-// Two f16 planes of ntp x in_dim, then ntp unscale factors.
-size_t gemv_mfma_scratch_bytes(int n_tok, int in_dim) {
+// K splits of the staged GEMV (k_gemv_mfs): the largest power of two up to
+// 8 (and up to the number of chunks) that keeps 32-row workgroups x splits
+// within 512, two per CU on 256 CUs (C1 4096 x 14336 Q6_K at 8 tokens: 4
+// splits, 26.8 vs 36.2 us for the mf_rows kernel); 0 where the staged
+// kernel does not apply (in_dim not a multiple of 1024, or of 2048 for Q6_K,
+// whose super-tiles must not straddle rows).
+template <class F> static int mfs_splits(int in_dim, int out_dim) {
+    if (in_dim <= 0 || out_dim <= 0 || in_dim % kMfsK != 0) return 0;
+    if (std::is_same<F, MQ6K>::value && in_dim % 2048 != 0) return 0;
+    const int nch = in_dim / kMfsK;
+    const long blocks = (out_dim + kMfsRows - 1) / kMfsRows;
+    int sk = 1;
+    while (sk < 8 && 2 * sk <= nch && blocks * 2 * sk <= 512) sk *= 2;
+    return sk;
+}
+static int mfs_splits_for(uint32_t dtype, int in_dim, int out_dim) {
+    switch (dtype) {
+    case T_Q4_K: return mfs_splits<MQ4K>(in_dim, out_dim);
+    case T_Q6_K: return mfs_splits<MQ6K>(in_dim, out_dim);
+    case T_Q8_0: return mfs_splits<MQ8>(in_dim, out_dim);
+    default: return 0;
+    }
+}
+
+// Two f16 planes of ntp x in_dim, ntp unscale factors, and the staged
+// kernel's partial outputs when it splits K.
+size_t gemv_mfma_scratch_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
+    auto al = [](size_t n) { return (n + 255) / 256 * 256; };
     const size_t ntp = n_tok <= 16 ? 16 : 32;
-    return (2 * ntp * (size_t)in_dim * 2 + 255) / 256 * 256 + ntp * 4;
+    const int sk = mfs_splits_for(dtype, in_dim, out_dim);
+    const size_t part = sk > 1 ? (size_t)sk * (size_t)n_tok * (size_t)out_dim * 4 : 0;
+    return al(2 * ntp * (size_t)in_dim * 2) + al(ntp * 4) + part;
+}
+
+template <class F>
+static hipError_t mfs_go(const uint8_t *w, const float *x, uint8_t *scratch, float *y, int n_tok,
+                         int in_dim, int out_dim, int sk, hipStream_t s) {
+    auto al = [](size_t n) { return (n + 255) / 256 * 256; };
+    const int ntp = n_tok <= 16 ? 16 : 32;
+    const size_t plane_bytes = (size_t)ntp * in_dim * 2;
+    _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
+    float *unscale = reinterpret_cast<float *>(scratch + al(2 * plane_bytes));
+    float *part = reinterpret_cast<float *>(scratch + al(2 * plane_bytes) + al((size_t)ntp * 4));
+    constexpr int lds = MfsGeo<F>::LDS;
+    // the attribute once per kernel (thread-safe static initialisation)
+    static const hipError_t attr1 = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&k_gemv_mfs<F, 1>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    static const hipError_t attr2 = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&k_gemv_mfs<F, 2>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr1 != hipSuccess) return attr1;
+    if (attr2 != hipSuccess) return attr2;
+    if (ntp == 16) k_mf_x<F><<<16, kMfxThreads, 0, s>>>(x, xh, unscale, n_tok, in_dim, 16);
+    else k_mf_x<F><<<32, kMfxThreads, 0, s>>>(x, xh, unscale, n_tok, in_dim, 32);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 grid((unsigned)((out_dim + kMfsRows - 1) / kMfsRows), (unsigned)sk);
+    float *dst = sk > 1 ? part : y;
+    if (ntp == 16)
+        k_gemv_mfs<F, 1><<<grid, 256, lds, s>>>(w, xh, (uint32_t)plane_bytes, unscale, dst, n_tok,
+                                                in_dim, out_dim);
+    else
+        k_gemv_mfs<F, 2><<<grid, 256, lds, s>>>(w, xh, (uint32_t)plane_bytes, unscale, dst, n_tok,
+                                                in_dim, out_dim);
+    e = hipGetLastError();
+    if (e != hipSuccess || sk == 1) return e;
+    const int n = n_tok * out_dim;
+    k_mfs_sum<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(part, y, n, sk);
+    return hipGetLastError();
 }
 
 template <class F, int NT, int NK, int RT>
@@ -934,6 +1205,12 @@ static hipError_t mf_go(const uint8_t *w, size_t w_bytes, const float *x, uint8_
 template <class F>
 static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, uint8_t *scratch,
                               float *y, int n_tok, int in_dim, int out_dim, hipStream_t s) {
+    // the staged kernel wherever it applies (16-byte aligned weights: its
+    // LDS copies move 16-byte pieces); it is the faster on every measured
+    // shape (C1 14336 x 4096 Q6_K at 8 tokens: 21.8 vs 30.1 us)
+    const int sk = mfs_splits<F>(in_dim, out_dim);
+    if (sk > 0 && ((uintptr_t)w & 15) == 0)
+        return mfs_go<F>(w, x, scratch, y, n_tok, in_dim, out_dim, sk, s);
     const int cus = device_cus();
     if (n_tok <= 8 && out_dim >= 8192 && mfb_xp(n_tok, in_dim, 16) != 0 &&
         mfb_lds_bytes<F>(n_tok, in_dim, out_dim, cus, 16) <= kMfbMaxLds)
@@ -952,9 +1229,9 @@ static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, 
 }
 
 // Any pairing of Q4_K, Q6_K and Q8_0 experts with both dimensions multiples
-// of 256. The weights are exact; the activations of each of the two GEMVs
-// are rounded once to f16 (x, then the SwiGLU output), which keeps the
-// chained error near 2e-4 of max |y|.
+// of 256. The weights are exact and the activations of each of the two
+// GEMVs (x, then the SwiGLU output) reach the matrix cores as hi + lo f16
+// planes, so the chained error stays at fp32 level.
 static bool mfma_format(uint32_t t) { return t == T_Q4_K || t == T_Q6_K || t == T_Q8_0; }
 bool moe_mfma_supported(uint32_t dt_gu, uint32_t dt_d, int n_embd, int n_ff) {
     return mfma_format(dt_gu) && mfma_format(dt_d) && n_embd > 0 && n_ff > 0 &&

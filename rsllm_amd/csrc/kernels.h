@@ -94,7 +94,7 @@ hipError_t launch_gemv_pair(uint32_t dtype, const uint8_t *w0, const uint8_t *w1
 // Q8_0) on the matrix cores (weights dequantised to f16 once, tokens as the
 // MFMA's N).
 bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim);
-size_t gemv_mfma_scratch_bytes(int n_tok, int in_dim);
+size_t gemv_mfma_scratch_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim);
 hipError_t launch_gemv_mfma(uint32_t dtype, const uint8_t *w, size_t w_bytes, const float *x,
                             uint8_t *scratch, float *y, int n_tok, int in_dim, int out_dim,
                             hipStream_t s);
