@@ -61,6 +61,8 @@ def parse():
                     help="skip the two rocprofv3 --pmc passes that measure roofline.traffic")
     ap.add_argument("--gemv-probe", action="store_true",
                     help="internal: the batch-1 GEMVs run under rocprofv3 --kernel-trace")
+    ap.add_argument("--batch-probe", action="store_true",
+                    help="run only the batched decode calls (for rocprofv3 traces and counters)")
     ap.add_argument("--no-trace", action="store_true",
                     help="skip the kernel-trace pass (roofline from HIP events only)")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -292,6 +294,43 @@ TRACE_LAUNCHES = 64
 # (tag, dtype name, out_dim, in_dim) of the batch-1 GEMVs --gemv-probe runs,
 # in launch order: C1 both orientations (the bench line), then C0
 PROBE_GEMVS = [("C1", "Q6_K", 14336, 4096), ("C1", "Q6_K", 4096, 14336), ("C0", "Q4_K", 4096, 4096)]
+
+
+# (tag, dtype name, out_dim, in_dim, tokens) of the batched decode calls
+# --batch-probe runs (C1 at 4 and 8 tokens, C2 Q8_0 at 8 and 32)
+PROBE_BATCHED = [("C1", "Q6_K", 14336, 4096, 4), ("C1", "Q6_K", 4096, 14336, 4),
+                 ("C1", "Q6_K", 14336, 4096, 8), ("C1", "Q6_K", 4096, 14336, 8),
+                 ("C2", "Q8_0", 4096, 4096, 8), ("C2", "Q8_0", 4096, 4096, 32),
+                 ("C2", "Q8_0", 1024, 4096, 32)]
+
+
+def batch_probe():
+    """Run under rocprofv3 (kernel trace, counters): the batched decode calls
+    of PROBE_BATCHED through matmul_quant_f32_dev, TRACE_LAUNCHES each, every
+    call reading a different weight copy so the weights stream from HBM."""
+    import torch
+    from rsllm_amd import backend as B
+    from rsllm_amd import synth
+    from rsllm_amd.ggml import GgmlType as G
+    dev = torch.device("cuda:0")
+    sptr = torch.cuda.current_stream().cuda_stream
+    for si, (_, dname, out_dim, in_dim, n_tok) in enumerate(PROBE_BATCHED):
+        dtype = G[dname]
+        w_host = synth.weight(dtype, out_dim, in_dim, seed=100 + si)
+        raw = torch.from_numpy(w_host).to(dev)
+        prep = torch.empty_like(raw)
+        B.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), dtype, in_dim, sptr)
+        del raw
+        reps = _rotating(prep)
+        x = torch.from_numpy(synth.activations(n_tok, in_dim, seed=200 + si)).to(dev).reshape(-1)
+        y = torch.empty(n_tok * out_dim, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        for i in range(TRACE_LAUNCHES):
+            w = reps[i % len(reps)]
+            B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
+                                   x.numel(), n_tok, in_dim, out_dim, dtype, sptr)
+        torch.cuda.synchronize()
+        del reps, prep
 
 
 def gemv_probe():
@@ -760,6 +799,9 @@ def main():
         return
     if args.gemv_probe:
         gemv_probe()
+        return
+    if args.batch_probe:
+        batch_probe()
         return
     if args.prefill_probe:
         prefill_probe(args.prefill_probe)

@@ -614,24 +614,22 @@ template <class F> struct MfsGeo {
     static constexpr int LDS = 2 * BUF;
 };
 
+// One workgroup's 32 rows from row0 of the matrix at w over chunks [c0, c0 +
+// nch) against the activation image xh (ntp token columns: 8, 16 or 32; with
+// 8, lanes of tokens 8..15 read past the resource, which returns zeros
+// without traffic); y[t * y_stride + o] = 2^-e_t * sum. smem: MfsGeo<F>::LDS
+// bytes.
 template <class F, int NT>
-__global__ __launch_bounds__(256) void k_gemv_mfs(const uint8_t *__restrict__ w,
-                                                  const _Float16 *__restrict__ xh,
-                                                  uint32_t plane_bytes,
-                                                  const float *__restrict__ unscale,
-                                                  float *__restrict__ y, int n_tok, int in_dim,
-                                                  int out_dim) {
+__device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
+                                         const _Float16 *__restrict__ xh, uint32_t plane_bytes,
+                                         const float *__restrict__ unscale, float *__restrict__ y,
+                                         int y_stride, int n_tok, int in_dim, int out_dim,
+                                         int row0, int c0, int nch, int ntp, uint8_t *smem) {
     using S = MfsStage<F>;
     using G = MfsGeo<F>;
-    constexpr int ntp = NT * 16;
     constexpr int RT = kMfsRows / 16;
-    extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, q = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int row0 = blockIdx.x * kMfsRows;
-    const int nall = in_dim / kMfsK;
-    const int c0 = nall * (int)blockIdx.y / (int)gridDim.y;
-    const int nch = nall * ((int)blockIdx.y + 1) / (int)gridDim.y - c0;
     // this thread's DMA pieces: piece g = p * 256 + tid is piece g % PR of
     // row g / PR (rows past out_dim repeat the last; the pieces past the
     // tile fill the buffer's tail with copies of piece 0)
@@ -674,9 +672,11 @@ __global__ __launch_bounds__(256) void k_gemv_mfs(const uint8_t *__restrict__ w,
             for (int j = 0; j < 4; j++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
-                    const uint32_t o = (uint32_t)((((st * 4 + j) * 4 + q) * ntp + nt * 16 + r16) * 16);
+                    const int col = nt * 16 + r16;
+                    const uint32_t o = col < ntp
+                        ? (uint32_t)((((st * 4 + j) * 4 + q) * ntp + col) * 16) : 0x7FFFFFF0u;
                     xr[u][j][nt] = bload16(rx, o, 0);
-                    lr[u][j][nt] = bload16(rx, o + plane_bytes, 0);
+                    lr[u][j][nt] = bload16(rx, col < ntp ? o + plane_bytes : 0x7FFFFFF0u, 0);
                 }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -699,7 +699,6 @@ __global__ __launch_bounds__(256) void k_gemv_mfs(const uint8_t *__restrict__ w,
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) red[((wv * RT + rt) * NT + nt) * 64 + lane] = acc[rt][nt];
     __syncthreads();
-    float *yo = y + (size_t)blockIdx.y * n_tok * out_dim;
     for (int e = tid; e < RT * NT * 64; e += 256) {
         const int rt = e / (NT * 64), nt = (e / 64) % NT, ln = e % 64;
         f32x4 v = red[(rt * NT + nt) * 64 + ln];
@@ -711,9 +710,26 @@ __global__ __launch_bounds__(256) void k_gemv_mfs(const uint8_t *__restrict__ w,
         if (o < out_dim) {
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                if (t0 + i < n_tok) yo[(size_t)(t0 + i) * out_dim + o] = v[i] * unscale[t0 + i];
+                if (t0 + i < n_tok) y[(size_t)(t0 + i) * y_stride + o] = v[i] * unscale[t0 + i];
         }
     }
+}
+
+// Grid (32-row blocks, K splits): split y of sk = gridDim.y takes an equal
+// run of chunks and writes y + split * n_tok * out_dim.
+template <class F, int NT>
+__global__ __launch_bounds__(256) void k_gemv_mfs(const uint8_t *__restrict__ w,
+                                                  const _Float16 *__restrict__ xh,
+                                                  uint32_t plane_bytes,
+                                                  const float *__restrict__ unscale,
+                                                  float *__restrict__ y, int n_tok, int in_dim,
+                                                  int out_dim, int ntp) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nall = in_dim / kMfsK;
+    const int c0 = nall * (int)blockIdx.y / (int)gridDim.y;
+    const int nch = nall * ((int)blockIdx.y + 1) / (int)gridDim.y - c0;
+    mfs_rows<F, NT>(w, xh, plane_bytes, unscale, y + (size_t)blockIdx.y * n_tok * out_dim, out_dim,
+                    n_tok, in_dim, out_dim, (int)blockIdx.x * kMfsRows, c0, nch, ntp, smem);
 }
 
 // y[i] = part[0][i] + part[1][i] + ... + part[sk - 1][i], in split order.
@@ -887,6 +903,34 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mfg(const uint8_t *__restrict_
     mf_rows<F, kMfgBatch / 16, NK, RT>(w, (uint32_t)w_stride, xh + b * 2 * img, (uint32_t)(img * 2),
                                        unscale + (size_t)b * kMfgBatch, y, bt.count, in_dim,
                                        out_dim, out_dim, blockIdx.x * 16 * RT, red);
+}
+
+// The grouped GEMV with its weights staged through LDS (mfs_rows): grid
+// (32-row blocks, batch slots, matrices); workgroup (x, b, m) computes rows
+// 32 x of W_m[expert(b)] for batch b's slots into y_m. Batch slots past
+// *n_bat exit at once.
+template <class F>
+__global__ __launch_bounds__(256) void k_gemv_mfgs(const uint8_t *__restrict__ w0,
+                                                   const uint8_t *__restrict__ w1,
+                                                   size_t w_stride,
+                                                   const _Float16 *__restrict__ xh,
+                                                   const float *__restrict__ unscale,
+                                                   const MfgBatch *__restrict__ bat,
+                                                   const int *__restrict__ n_bat,
+                                                   float *__restrict__ y0, float *__restrict__ y1,
+                                                   int in_dim, int out_dim) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int b = blockIdx.y;
+    if (b >= *n_bat) return;
+    const MfgBatch bt = bat[b];
+    const bool m1 = blockIdx.z != 0;
+    const uint8_t *w = (m1 ? w1 : w0) + (size_t)bt.expert * w_stride;
+    float *y = (m1 ? y1 : y0) + (size_t)bt.first * out_dim;
+    const size_t img = (size_t)in_dim * kMfgBatch;  // values per plane
+    mfs_rows<F, kMfgBatch / 16>(w, xh + b * 2 * img, (uint32_t)(img * 2),
+                                unscale + (size_t)b * kMfgBatch, y, out_dim, bt.count, in_dim,
+                                out_dim, (int)blockIdx.x * kMfsRows, 0, in_dim / kMfsK,
+                                kMfgBatch, smem);
 }
 
 // ---- fused batched GEMV: activations converted into LDS ------------------------------
@@ -1150,7 +1194,10 @@ template <class F>
 static hipError_t mfs_go(const uint8_t *w, const float *x, uint8_t *scratch, float *y, int n_tok,
                          int in_dim, int out_dim, int sk, hipStream_t s) {
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
-    const int ntp = n_tok <= 16 ? 16 : 32;
+    // 8 image columns up to 8 tokens: half the activation bytes every
+    // workgroup reads (C1 14336 x 4096 Q6_K at 8 tokens reads the image 448
+    // times)
+    const int ntp = n_tok <= 8 ? 8 : n_tok <= 16 ? 16 : 32;
     const size_t plane_bytes = (size_t)ntp * in_dim * 2;
     _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
     float *unscale = reinterpret_cast<float *>(scratch + al(2 * plane_bytes));
@@ -1163,18 +1210,17 @@ static hipError_t mfs_go(const uint8_t *w, const float *x, uint8_t *scratch, flo
         reinterpret_cast<const void *>(&k_gemv_mfs<F, 2>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr1 != hipSuccess) return attr1;
     if (attr2 != hipSuccess) return attr2;
-    if (ntp == 16) k_mf_x<F><<<16, kMfxThreads, 0, s>>>(x, xh, unscale, n_tok, in_dim, 16);
-    else k_mf_x<F><<<32, kMfxThreads, 0, s>>>(x, xh, unscale, n_tok, in_dim, 32);
+    k_mf_x<F><<<(unsigned)ntp, kMfxThreads, 0, s>>>(x, xh, unscale, n_tok, in_dim, ntp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 grid((unsigned)((out_dim + kMfsRows - 1) / kMfsRows), (unsigned)sk);
     float *dst = sk > 1 ? part : y;
-    if (ntp == 16)
+    if (ntp <= 16)
         k_gemv_mfs<F, 1><<<grid, 256, lds, s>>>(w, xh, (uint32_t)plane_bytes, unscale, dst, n_tok,
-                                                in_dim, out_dim);
+                                                in_dim, out_dim, ntp);
     else
         k_gemv_mfs<F, 2><<<grid, 256, lds, s>>>(w, xh, (uint32_t)plane_bytes, unscale, dst, n_tok,
-                                                in_dim, out_dim);
+                                                in_dim, out_dim, ntp);
     e = hipGetLastError();
     if (e != hipSuccess || sk == 1) return e;
     const int n = n_tok * out_dim;
@@ -1257,6 +1303,19 @@ static hipError_t mfg_pass(const uint8_t *w0, const uint8_t *w1, size_t w_stride
         k_mfg_x<F, false><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // weights staged through LDS where the layout allows (16-byte aligned
+    // expert matrices, in_dim a multiple of 1024, of 2048 for Q6_K)
+    if (mfs_splits<F>(in_dim, out_dim) > 0 &&
+        (((uintptr_t)w0 | (uintptr_t)(w1 ? w1 : w0) | (uintptr_t)w_stride) & 15) == 0) {
+        constexpr int lds = MfsGeo<F>::LDS;
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&k_gemv_mfgs<F>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (attr != hipSuccess) return attr;
+        const dim3 g((unsigned)((out_dim + kMfsRows - 1) / kMfsRows), (unsigned)max_b, w1 ? 2u : 1u);
+        k_gemv_mfgs<F><<<g, 256, lds, s>>>(w0, w1, w_stride, xh, us, bat, n_bat, y0, y1, in_dim,
+                                           out_dim);
+        return hipGetLastError();
+    }
     constexpr int NK = 4, RT = 4;
     const dim3 g((unsigned)((out_dim + 16 * RT - 1) / (16 * RT)), (unsigned)max_b, w1 ? 2u : 1u);
     k_gemv_mfg<F, NK, RT><<<g, 64 * NK, 0, s>>>(w0, w1, w_stride, xh, us, bat, n_bat, y0, y1,
