@@ -101,16 +101,19 @@ def test_prefill_special_blocks(oracle, hip):
     check(oracle, got, w, xb, np.arange(n_tok), n_tok, in_dim, out_dim, per_token=False)
 
 
-@pytest.mark.parametrize("n_tok", [512, 2048])
+@pytest.mark.parametrize("n_tok", [100, 512, 2048])
 def test_prefill_config_shape(oracle, hip, n_tok):
-    """Config C4: Q4_K (out, in) = (14336, 4096), T in {512, 2048}. The oracle
-    runs on a spread subset of tokens (every token's output is independent)."""
+    """Config C4: Q4_K (out, in) = (14336, 4096), T in {512, 2048}, and T = 100
+    (a grid that takes the 64-token workgroup tile). The oracle runs on a
+    spread subset of tokens (every token's output is independent), both
+    sides of the 64- and 128-token tile edges included."""
     out_dim, in_dim = 14336, 4096
     w = synth.weight(G.Q4_K, out_dim, in_dim, seed=404)
     xb = synth.bf16_activations(n_tok, in_dim, seed=405).reshape(-1)
     got = run_prefill(hip, w, xb, n_tok, in_dim, out_dim)
-    tokens = np.unique(np.concatenate([np.arange(0, 8), np.arange(125, 131),
+    tokens = np.unique(np.concatenate([np.arange(0, 8), np.arange(62, 67), np.arange(125, 131),
                                        np.linspace(0, n_tok - 1, 24).astype(int)]))
+    tokens = tokens[tokens < n_tok]
     err = check(oracle, got, w, xb, tokens, n_tok, in_dim, out_dim)
     print(f"C4 T={n_tok}: rel err {err:.3e} over {len(tokens)} tokens")
 
