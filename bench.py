@@ -159,6 +159,8 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
                               "tokens_checked": len(toks), "tolerance": 1e-3}
         res["f32_x"].append(entry)
         del d_x, d_y
+    res["mfma_ceiling"] = bench_mfma_ceiling(B, dev, stream)
+    res["dense_f16_library"] = bench_dense_f16(dev, stream, out_dim, in_dim, iters)
     if with_cpu:
         # reference CPU path (oracle, all host threads = min(n_tok, cores) as
         # the rayon split gives) on a bounded token sample, scaled to TFLOP/s
@@ -178,6 +180,56 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
             "cores": n_thr, "kind": "port",
             "sample": f"{n_done} tokens of C4 (Q4_K 14336x4096) in {t_cpu:.1f} s, oracle "
                       f"matmul_quant_f32 with one thread per token ({n_thr} threads)"}
+    return res
+
+
+def bench_mfma_ceiling(B, dev, stream, iters=200):
+    """prefill.mfma_ceiling: the matrix-core issue rate the prefill GEMM is
+    compared with (rsllm_hip_mfma_issue_dev): the GEMM's inner-loop shape,
+    32 groups of four independent 16x16x32 f16 MFMAs per round, with 0, 4 or
+    8 packed-f16 FMAs after each group, one or two 4-wavefront workgroups per
+    CU on all 256 CUs."""
+    import torch
+    out = {"unit": "TFLOP/s", "mfma_per_wave": 128 * iters, "by_case": []}
+    for valu in (0, 4, 8):
+        for two in (False, True):
+            n_wg = 512 if two else 256
+            sink = torch.empty(n_wg * 256, dtype=torch.int32, device=dev)
+
+            def call(i):
+                B.mfma_issue_dev(sink.data_ptr(), sink.numel(), n_wg, iters, valu, two,
+                                 stream.cuda_stream)
+            call(0)
+            us = _time(call, 5, stream)
+            flops = 16384.0 * 128 * iters * 4 * n_wg
+            tf = flops / (us * 1e-6) / 1e12
+            out["by_case"].append({"valu_per_mfma": valu / 4, "waves_per_simd": 2 if two else 1,
+                                   "us": round(us, 1), "tflops": round(tf, 1),
+                                   "frac_of_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+    return out
+
+
+def bench_dense_f16(dev, stream, out_dim, in_dim, iters):
+    """prefill.dense_f16_library: the platform GEMM library (torch ->
+    hipBLASLt) on the same shape with dense f16 weights and f16 output, no
+    dequantisation, as a reference point for the fused Q4_K GEMM. The weight
+    alternates between two copies."""
+    import torch
+    res = []
+    ws = [torch.randn(out_dim, in_dim, device=dev, dtype=torch.float16) for _ in range(2)]
+    for T in (512, 2048):
+        x = torch.randn(T, in_dim, device=dev, dtype=torch.float16)
+
+        def call(i):
+            torch.nn.functional.linear(x, ws[i & 1])
+        for i in range(3):
+            call(i)
+        us = _time(call, iters, stream)
+        tf = 2.0 * T * in_dim * out_dim / (us * 1e-6) / 1e12
+        res.append({"tokens": T, "us_per_op": round(us, 2), "tflops": round(tf, 1),
+                    "frac_of_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+        del x
+    del ws
     return res
 
 

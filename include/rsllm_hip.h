@@ -467,6 +467,17 @@ int rsllm_hip_stream_read_dev(const uint8_t *p, size_t bytes, uint32_t *sink, si
                               int n_wg, int threads, int unroll, int contiguous,
                               rsllm_hip_stream_t stream);
 
+/* No counterpart in the reference: the matrix-core issue ceiling the MFMA
+ * GEMMs are compared with. n_wg workgroups of 4 wavefronts (one per CU, or
+ * two with two_per_cu != 0), each wavefront running `iters` (1..100000)
+ * rounds of 32 groups of four independent v_mfma_f32_16x16x32_f16 with
+ * valu_per_group (0, 4, 8, 16) independent packed-f16 FMAs after each group:
+ * 128 * iters MFMAs of 16384 flops per wavefront. `sink` (device, n_wg * 256
+ * words) is written only when a lane's folded result equals a fixed
+ * constant. Enqueued on `stream`. */
+int rsllm_hip_mfma_issue_dev(uint32_t *sink, size_t sink_len, int n_wg, int iters,
+                             int valu_per_group, int two_per_cu, rsllm_hip_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

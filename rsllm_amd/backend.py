@@ -172,6 +172,7 @@ SIGNATURES = {
     "rsllm_hip_apply_shared_expert_dev": ([_P, _S, _P, _S, _P, _S, _U32, _P, _S, _U32, _P, _S,
                                            _U32, _S, _S, _S, ctypes.c_float, _P], _I),
     "rsllm_hip_stream_read_dev": ([_P, _S, _P, _S, _I, _I, _I, _I, _P], _I),
+    "rsllm_hip_mfma_issue_dev": ([_P, _S, _I, _I, _I, _I, _P], _I),
 }
 
 
@@ -536,6 +537,15 @@ def stream_read_dev(p: int, nbytes: int, sink_ptr: int, sink_len: int, n_wg: int
     nbytes at device pointer p."""
     _check(LIB.rsllm_hip_stream_read_dev(p or None, nbytes, sink_ptr or None, sink_len, n_wg,
                                          threads, unroll, int(bool(contiguous)), stream or None))
+
+
+def mfma_issue_dev(sink_ptr: int, sink_len: int, n_wg: int, iters: int, valu_per_group: int,
+                   two_per_cu: bool = False, stream: int = 0) -> None:
+    """Measurement aid (no reference counterpart): the matrix-core issue
+    ceiling, 128 * iters v_mfma_f32_16x16x32_f16 per wavefront with
+    valu_per_group packed-f16 FMAs after every four."""
+    _check(LIB.rsllm_hip_mfma_issue_dev(sink_ptr or None, sink_len, n_wg, iters, valu_per_group,
+                                        int(bool(two_per_cu)), stream or None))
 
 
 # ---------------------------------------------------------------------------

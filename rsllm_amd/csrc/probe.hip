@@ -1,6 +1,7 @@
-// Measurement aid: a pure streaming read of device memory, the ceiling any
-// HBM-bound kernel of this library is compared with (same bytes, no
-// arithmetic). Not part of the reference's interface.
+// Measurement aids, not part of the reference's interface: a pure streaming
+// read of device memory, the ceiling any HBM-bound kernel of this library is
+// compared with (same bytes, no arithmetic), and the matrix-core issue rate
+// the MFMA GEMMs are compared with.
 //
 // k_stream_read<U>: n_wg workgroups of `threads` threads. In the contiguous
 // mode workgroup b reads bytes [b * chunk, (b + 1) * chunk) (chunk = the
@@ -67,7 +68,100 @@ static hipError_t stream_read(const uint8_t *p, size_t bytes, uint32_t *sink, in
     return hipGetLastError();
 }
 
+// Matrix-core issue ceiling: every wavefront runs `iters` rounds of 32
+// groups of four independent v_mfma_f32_16x16x32_f16 (the prefill GEMM's
+// inner-loop shape, 32 accumulator tiles in VGPRs), each group followed by
+// NV independent packed-f16 FMAs (0: the bare matrix-core rate; 4, 8, 16:
+// one, two, four per MFMA, the dequantisation load of a fused GEMM). One
+// 4-wavefront workgroup per CU (the launch reserves 100 KiB of LDS), or two
+// with `two_per_cu`. The accumulators are folded into one word per lane,
+// written only when it equals a fixed constant.
+typedef _Float16 pr_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 pr_h2 __attribute__((ext_vector_type(2)));
+typedef float pr_f4 __attribute__((ext_vector_type(4)));
+
+template <int NV>
+__global__ __launch_bounds__(256) void k_mfma_issue(uint32_t *__restrict__ sink, int iters) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    pr_f4 acc[8][4];
+#pragma unroll
+    for (int a = 0; a < 8; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = pr_f4{0.f, 0.f, 0.f, 0.f};
+    pr_h8 bq[4], av[8];
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) bq[b][j] = (_Float16)(0.001f * (float)(lane + b + j));
+#pragma unroll
+    for (int b = 0; b < 8; b++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) av[b][j] = (_Float16)(0.001f * (float)(lane - b + j));
+    pr_h2 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = pr_h2{(_Float16)(0.001f * (float)lane), (_Float16)(0.002f * (float)j)};
+    const pr_h2 sc = pr_h2{(_Float16)0.999f, (_Float16)0.999f}, bi = pr_h2{(_Float16)0.001f, (_Float16)0.001f};
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int g = 0; g < 32; g++) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++)
+                acc[g & 7][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bq[nt], av[g & 7], acc[g & 7][nt], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < NV; j++) v[j & 7] = v[j & 7] * sc + bi;
+        }
+    }
+    float f = 0.f;
+#pragma unroll
+    for (int a = 0; a < 8; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) f += acc[a][b][0] + acc[a][b][1] + acc[a][b][2] + acc[a][b][3];
+#pragma unroll
+    for (int j = 0; j < 8; j++) f += (float)v[j][0] + (float)v[j][1];
+    const uint32_t word = __float_as_uint(f);
+    if (word == 0x9E3779B9u) sink[blockIdx.x * 256 + tid] = word;
+}
+
+static hipError_t mfma_issue(uint32_t *sink, int n_wg, int iters, int valu, int two_per_cu,
+                             hipStream_t s) {
+    const size_t lds = two_per_cu ? 64 * 1024 : 100 * 1024;
+    switch (valu) {
+#define V(N)                                                                                        \
+    case N: {                                                                                       \
+        static const hipError_t attr = hipFuncSetAttribute(                                          \
+            (const void *)k_mfma_issue<N>, hipFuncAttributeMaxDynamicSharedMemorySize, 100 * 1024);  \
+        if (attr != hipSuccess) return attr;                                                        \
+        k_mfma_issue<N><<<(unsigned)n_wg, 256, lds, s>>>(sink, iters);                              \
+        break;                                                                                      \
+    }
+        V(0) V(4) V(8) V(16)
+#undef V
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace rsllm_hip
+
+extern "C" int rsllm_hip_mfma_issue_dev(uint32_t *sink, size_t sink_len, int n_wg, int iters,
+                                        int valu_per_group, int two_per_cu,
+                                        rsllm_hip_stream_t stream) {
+    using namespace rsllm_hip;
+    if (n_wg <= 0 || n_wg > 65536 || iters <= 0 || iters > 100000)
+        return abi::set_error(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                              "mfma_issue: n_wg in 1..65536 and iters in 1..100000");
+    if (!sink || sink_len < (size_t)n_wg * 256)
+        return abi::set_error(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                              "mfma_issue: sink must hold n_wg * 256 words");
+    const hipError_t e = mfma_issue(sink, n_wg, iters, valu_per_group, two_per_cu,
+                                    (hipStream_t)stream);
+    if (e == hipErrorInvalidValue)
+        return abi::set_error(RSLLM_HIP_ERR_INVALID_ARGUMENT,
+                              "mfma_issue: valu_per_group must be 0, 4, 8 or 16");
+    if (e != hipSuccess) return abi::device_error(e, "mfma_issue");
+    return abi::ok_status();
+}
 
 extern "C" int rsllm_hip_stream_read_dev(const uint8_t *p, size_t bytes, uint32_t *sink,
                                          size_t sink_len, int n_wg, int threads, int unroll,
