@@ -197,11 +197,13 @@ int rsllm_hip_stream_release(rsllm_hip_stream_t stream);
  * host range, like rsllm_hip_register_weights, so the host-pointer entry
  * points use the resident copy. An upload whose fingerprint
  * (GgufFile::fingerprint, file.rs:175-177: names, types and shapes only),
- * tensor table and sampled payload digest (16 windows of 256 bytes per
- * tensor) match a live model on the same device returns that model, adds a
- * reference and registers the new host ranges, without copying: two files
- * of one layout that differ only outside the sampled windows would be taken
- * for the same. Errors, all before any device work: INVALID_ARGUMENT for
+ * tensor table and payload match a live model on the same device returns
+ * that model, adds a reference and registers the new host ranges, without
+ * copying. The payload comparison is a 64-bit hash of every byte (taken by
+ * the copy threads during an upload; for a candidate that also matches a
+ * 16-window sampled digest, over the new bytes by a host read pass), so
+ * files that differ anywhere get separate models. Errors, all before any
+ * device work: INVALID_ARGUMENT for
  * NULL arguments or duplicate names, SHAPE_MISMATCH for a matmul tensor
  * whose length is not whole rows of a block-aligned in_dim. Uploads are
  * serialised with each other and with the lookups below.

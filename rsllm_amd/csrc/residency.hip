@@ -17,9 +17,12 @@
 //   - every matmul-format tensor is added to the registry under its host
 //     range, so the host-pointer entry points use the resident copy;
 //   - a model is keyed by the GGUF fingerprint (file.rs:175-177, which
-//     hashes names, types and shapes only), the tensor table and a digest of
-//     sampled payload windows; an upload that matches a live model reuses
-//     it (reference count) and re-registers the new host ranges.
+//     hashes names, types and shapes only), the tensor table and a hash of
+//     every payload byte, taken by the copy threads as they stage the bytes.
+//     An upload whose fingerprint, table and sampled-window digest match a
+//     live model hashes its whole payload (a read pass, no device work) and
+//     reuses that model (reference count, new host ranges registered) only
+//     when the full hashes agree.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -53,7 +56,8 @@ struct Tensor {
 struct Model {
     uint64_t id;
     uint8_t fp[32];
-    uint64_t digest;
+    uint64_t digest;  // table + sampled windows: the cheap pre-filter
+    uint64_t full;    // table + every payload byte
     int device;
     std::vector<Tensor> t;
     // the arena; registry entries of the model share it, so it is freed when
@@ -133,24 +137,122 @@ int validate_tensor(const rsllm_hip_tensor_desc &d) {
     return RSLLM_HIP_OK;
 }
 
-// Parallel host copy (the source is usually a file mapping being paged in).
-// Pieces no thread could be started for are copied by the caller.
-void copy_parallel(uint8_t *dst, const uint8_t *src, size_t n) {
+// Payload hash: 64-bit words folded into four independent lanes (multiply,
+// rotate, multiply by odd constants), the lanes and the length mixed at the
+// end; the tail bytes go through FNV-1a. Not cryptographic: it tells apart
+// payloads that differ anywhere, which the sampled digest cannot.
+constexpr size_t kHashBlock = 1u << 20;  // bytes per block hash
+inline uint64_t rotl64(uint64_t v, int r) { return (v << r) | (v >> (64 - r)); }
+uint64_t hash_bytes(const uint8_t *p, size_t n) {
+    constexpr uint64_t K1 = 0x9E3779B97F4A7C15ull, K2 = 0xC2B2AE3D27D4EB4Full;
+    uint64_t a[4] = {K1, K2, K1 ^ K2, ~K1};
+    size_t i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int l = 0; l < 4; l++) {
+            uint64_t w;
+            memcpy(&w, p + i + 8 * l, 8);
+            a[l] = rotl64(a[l] + w * K2, 31) * K1;
+        }
+    Fnv f;
+    f.put((uint64_t)n);
+    for (int l = 0; l < 4; l++) f.put(a[l]);
+    f.add(p + i, n - i);
+    return f.h;
+}
+
+// hash_bytes of [src, src + n) while copying it to dst, in one pass over
+// the source.
+uint64_t copy_hash_bytes(uint8_t *dst, const uint8_t *src, size_t n) {
+    constexpr uint64_t K1 = 0x9E3779B97F4A7C15ull, K2 = 0xC2B2AE3D27D4EB4Full;
+    uint64_t a[4] = {K1, K2, K1 ^ K2, ~K1};
+    size_t i = 0;
+    for (; i + 32 <= n; i += 32) {
+        uint64_t w[4];
+        memcpy(w, src + i, 32);
+        memcpy(dst + i, w, 32);
+        for (int l = 0; l < 4; l++) a[l] = rotl64(a[l] + w[l] * K2, 31) * K1;
+    }
+    memcpy(dst + i, src + i, n - i);
+    Fnv f;
+    f.put((uint64_t)n);
+    for (int l = 0; l < 4; l++) f.put(a[l]);
+    f.add(src + i, n - i);
+    return f.h;
+}
+
+// Hashes of the kHashBlock blocks of [p, p + n) into h[0..] (copying them
+// to dst when dst is not NULL).
+void hash_blocks(uint8_t *dst, const uint8_t *p, size_t n, uint64_t *h) {
+    const size_t nblk = (n + kHashBlock - 1) / kHashBlock;
+    for (size_t k = 0; k < nblk; k++) {
+        const size_t o = k * kHashBlock, m = std::min(kHashBlock, n - o);
+        h[k] = dst ? copy_hash_bytes(dst + o, p + o, m) : hash_bytes(p + o, m);
+    }
+}
+
+// Block hashes of [src, src + n) into h, in parallel (the source is usually
+// a file mapping being paged in), copying the bytes to dst on the way when
+// dst is not NULL (the upload's staging copy). Threads take whole
+// kHashBlock blocks; pieces no thread could be started for are handled by
+// the caller.
+void copy_parallel(uint8_t *dst, const uint8_t *src, size_t n, uint64_t *h) {
     if (n < (8u << 20)) {
-        memcpy(dst, src, n);
+        hash_blocks(dst, src, n, h);
         return;
     }
-    const size_t per = (n / kCopyThreads + 4095) & ~(size_t)4095;
+    const size_t nblk = (n + kHashBlock - 1) / kHashBlock;
+    const size_t per = (nblk + kCopyThreads - 1) / kCopyThreads * kHashBlock;
     std::vector<std::thread> th;
     for (size_t o = 0; o < n; o += per) {
         const size_t m = std::min(per, n - o);
+        auto work = [=] { hash_blocks(dst ? dst + o : nullptr, src + o, m, h + o / kHashBlock); };
         try {
-            th.emplace_back([=] { memcpy(dst + o, src + o, m); });
+            th.emplace_back(work);
         } catch (...) {
-            memcpy(dst + o, src + o, m);
+            work();
         }
     }
     for (auto &t : th) t.join();
+}
+
+// Bytes per staging chunk of a tensor: converted formats move whole 8-block
+// super-tiles.
+size_t chunk_bytes(uint32_t dtype, size_t in_dim) {
+    const bool conv = layout_converted(dtype) && in_dim;
+    const size_t unit = conv ? 8 * block_bytes_of(dtype) : 1;
+    return kStage / unit * unit;
+}
+
+// Folds the tensor table, then every chunk's block hashes in upload order.
+struct FullHash {
+    Fnv f;
+    explicit FullHash(const rsllm_hip_tensor_desc *d, size_t n) {
+        f.put((uint64_t)n);
+        for (size_t i = 0; i < n; i++) {
+            f.add(d[i].name, strlen(d[i].name) + 1);
+            f.put(d[i].dtype);
+            f.put((uint64_t)d[i].len);
+            f.put((uint64_t)d[i].in_dim);
+        }
+    }
+    void add_chunk(const uint64_t *h, size_t nb) {
+        for (size_t k = 0; k < (nb + kHashBlock - 1) / kHashBlock; k++) f.put(h[k]);
+    }
+};
+
+// The full hash of a payload list, by a read pass (no device work).
+uint64_t payload_hash(const rsllm_hip_tensor_desc *d, size_t n) {
+    FullHash fh(d, n);
+    std::vector<uint64_t> h(kStage / kHashBlock + 1);
+    for (size_t i = 0; i < n; i++) {
+        const size_t chunk = chunk_bytes(d[i].dtype, d[i].in_dim);
+        for (size_t o = 0; o < d[i].len; o += chunk) {
+            const size_t nb = std::min(chunk, d[i].len - o);
+            copy_parallel(nullptr, d[i].data + o, nb, h.data());
+            fh.add_chunk(h.data(), nb);
+        }
+    }
+    return fh.f.h;
 }
 
 struct Staging {
@@ -181,18 +283,19 @@ int upload(Model &m, const rsllm_hip_tensor_desc *d, size_t n) {
         HIP_TRY(hipEventCreateWithFlags(&st.done[b], hipEventDisableTiming), "hipEventCreate");
         if (any_conv) HIP_TRY(hipMalloc((void **)&st.dev[b], kStage), "hipMalloc");
     }
+    FullHash fh(d, n);
+    std::vector<uint64_t> h(kStage / kHashBlock + 1);
     int k = 0;  // chunk counter (staging buffer k & 1)
     for (size_t i = 0; i < n; i++) {
         const Tensor &t = m.t[i];
         const bool conv = layout_converted(t.dtype) && t.in_dim;
-        // converted formats: chunks of whole 8-block super-tiles
-        const size_t unit = conv ? 8 * block_bytes_of(t.dtype) : 1;
-        const size_t chunk = kStage / unit * unit;
+        const size_t chunk = chunk_bytes(t.dtype, t.in_dim);
         for (size_t o = 0; o < t.len; o += chunk, k++) {
             const size_t nb = std::min(chunk, t.len - o);
             const int b = k & 1;
             if (k >= 2) HIP_TRY(hipEventSynchronize(st.done[b]), "hipEventSynchronize");
-            copy_parallel(st.host[b], d[i].data + o, nb);
+            copy_parallel(st.host[b], d[i].data + o, nb, h.data());
+            fh.add_chunk(h.data(), nb);
             uint8_t *dst = m.arena + t.off + o;
             if (conv) {
                 HIP_TRY(hipMemcpyAsync(st.dev[b], st.host[b], nb, hipMemcpyHostToDevice, st.s),
@@ -209,6 +312,7 @@ int upload(Model &m, const rsllm_hip_tensor_desc *d, size_t n) {
         }
     }
     HIP_TRY(hipStreamSynchronize(st.s), "hipStreamSynchronize");
+    m.full = fh.f.h;
     return RSLLM_HIP_OK;
 }
 
@@ -249,9 +353,18 @@ int rsllm_hip_model_upload(const uint8_t *fingerprint, const rsllm_hip_tensor_de
     HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
     const uint64_t digest = model_digest(tensors, n_tensors);
     std::lock_guard<std::mutex> lk(m_mu);
+    // a candidate passes the sampled digest; reuse needs the full hash too
+    // (taken once, over the new payload, for all candidates)
+    bool have_full = false;
+    uint64_t full = 0;
     for (auto &p : g_models) {
         if (p->device == dev && p->digest == digest && !memcmp(p->fp, fingerprint, 32) &&
             p->t.size() == n_tensors) {
+            if (!have_full) {
+                full = payload_hash(tensors, n_tensors);
+                have_full = true;
+            }
+            if (p->full != full) continue;
             p->refs++;
             register_host_ranges(*p, tensors);
             *model = p->id;

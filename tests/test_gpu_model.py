@@ -10,7 +10,8 @@ borrowed from the mapping (tensor_bytes :181-187).
 * Host-pointer matmuls on the mapped ranges use the resident copies and agree
   with the oracle (1e-3) and, bit for bit, with the same calls after release
   (weights uploaded per call).
-* Reuse by fingerprint + tensor table + sampled digest, and release."""
+* Reuse by fingerprint + tensor table + full payload hash (a byte changed
+  outside the sampled windows gives a new model), and release."""
 import ctypes
 import os
 
@@ -192,12 +193,25 @@ def test_reuse_by_fingerprint_and_release(hip, mapped, tmp_path):
         copies = [(n, np.array(v), dt, k) for n, v, dt, k in views[:4]]
         assert hip.model_upload(other_fp, copies) == c
         assert hip.model_info(c)["refs"] == 2
+        # one byte changed outside the 16 sampled windows (byte 300 of a
+        # 557 KB tensor: the windows start at 0, 37 KB, 74 KB, ...): the full
+        # payload hash tells it apart, a new model
+        assert copies[3][1].size > 16 * 4096
+        copies[3][1][300] ^= 0x01
+        e = hip.model_upload(other_fp, copies)
+        assert e not in (a, c)
+        assert hip.model_info(e)["uploaded_bytes"] == sum(v[1].size for v in copies)
+        ptr, n = hip.model_tensor(e, copies[3][0])
+        assert np.array_equal(device_bytes(ptr, n), prepared_reference(hip, copies[3][1], copies[3][2],
+                                                                       copies[3][3]))
+        # the same changed bytes again: that model is reused
+        assert hip.model_upload(other_fp, copies) == e
         # one sampled byte changed: a new model
         copies[2][1][0] ^= 0xFF
         d = hip.model_upload(other_fp, copies)
-        assert d not in (a, c)
+        assert d not in (a, c, e)
         assert hip.model_info(d)["uploaded_bytes"] == sum(v[1].size for v in copies)
-        for m in (d, c, c):
+        for m in (d, e, e, c, c):
             hip.model_release(m)
         with pytest.raises(hip.InvalidArgument):
             hip.model_info(c)
