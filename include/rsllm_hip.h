@@ -62,8 +62,9 @@ typedef enum rsllm_hip_status {
     RSLLM_HIP_ERR_INVALID_ARGUMENT = 8,      /* NULL pointer with nonzero length, or a shape the
                                                 reference would panic on (row_len == 0 in
                                                 parallel.rs:44) */
-    RSLLM_HIP_ERR_UNIMPLEMENTED = 10         /* dtype the reference accepts but this backend does
-                                                not implement (dequant of Q4_1, Q5_K, Q8_K) */
+    RSLLM_HIP_ERR_UNIMPLEMENTED = 10         /* a call the reference accepts but this backend
+                                                does not serve (e.g. the Q4_K-only prefill entry
+                                                given another dtype) */
 } rsllm_hip_status;
 
 /* GgmlType ids (rsllm-gguf/src/tensor.rs:26-85) used by this ABI. */
@@ -446,9 +447,10 @@ int rsllm_hip_matmul_q8_0_batch_dev(float *out, size_t out_len, const uint8_t *w
 /* ---- dequantisation ------------------------------------------------------ */
 
 /* dequant_to_f32 (rsllm-gguf/src/dequant/mod.rs:69-85): decode `src` (GGUF
- * bytes) into dst[dst_len]. Bit-exact with the reference for F32, F16, BF16,
- * Q4_0, Q4_K, Q6_K, Q8_0, Q2_K, IQ2_XXS. Size rule of q4_k.rs:36-49 (and
- * siblings). */
+ * bytes) into dst[dst_len]. Bit-exact with the reference on every arm of its
+ * dispatch: F32, F16, BF16, Q4_0, Q4_1, Q4_K, Q5_K, Q6_K, Q8_0, Q2_K, Q8_K,
+ * IQ2_XXS; any other dtype is UNSUPPORTED_DEQUANT. Size rule of
+ * q4_k.rs:36-49 (and siblings). */
 int rsllm_hip_dequant_to_f32(uint32_t dtype, const uint8_t *src, size_t src_len, float *dst,
                              size_t dst_len);
 int rsllm_hip_dequant_to_f32_dev(uint32_t dtype, const uint8_t *src, size_t src_len, float *dst,

@@ -7,7 +7,8 @@ Two independent restatements of the reference's dequantizers live here:
   citations in ``rsllm_oracle.c``). It is the parity oracle and the CPU
   baseline.
 * ``np_dequant_*``: vectorised numpy restatements written from the block
-  layouts alone (q4_k.rs:8-26, q6_k.rs:8-25, q8_0.rs:6-13). They share no
+  layouts alone (q4_k.rs:8-26, q6_k.rs:8-25, q8_0.rs:6-13, q2_k.rs:9-31,
+  iq2_xxs.rs:12-33, q4_0.rs:19-28, q5_k.rs:6-24, q8_k.rs:12-23). They share no
   code with the C file and are used to cross-check it over every block of
   seeded data.
 
@@ -29,8 +30,10 @@ OK, SHAPE_MISMATCH, NOT_BLOCK_ALIGNED, NON_FINITE_INPUT = 0, 1, 2, 3
 DEQUANT_SIZE_MISMATCH, UNSUPPORTED_DEQUANT, PANIC = 5, 6, 9
 
 F32, F16, Q4_0, Q8_0, Q2_K, Q4_K, Q6_K, IQ2_XXS, BF16 = 0, 1, 2, 8, 10, 12, 14, 16, 30
+Q4_1, Q5_K, Q8_K = 3, 13, 15
 BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q8_0: (32, 34),
-         Q4_K: (256, 144), Q6_K: (256, 210), Q2_K: (256, 84), IQ2_XXS: (256, 66)}
+         Q4_K: (256, 144), Q6_K: (256, 210), Q2_K: (256, 84), IQ2_XXS: (256, 66),
+         Q4_1: (32, 20), Q5_K: (256, 176), Q8_K: (256, 292)}
 
 _lib = None
 
@@ -317,6 +320,47 @@ def np_dequant_q2k(src: np.ndarray) -> np.ndarray:
     return ((dl * q).astype(np.float32) - ml).astype(np.float32).reshape(-1)
 
 
+def np_dequant_q4_1(src: np.ndarray) -> np.ndarray:
+    """Q4_1 from the block layout (q4_0.rs:19-28): [d f16 | m f16 | 16 code
+    bytes], element j < 16 the low nibble of byte j, j >= 16 the high nibble
+    of byte j - 16; code * d + m in float32."""
+    b = np.asarray(src, np.uint8).reshape(-1, 20)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)
+    m = b[:, 2:4].copy().view(np.float16).astype(np.float32)
+    qs = b[:, 4:20]
+    code = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.float32)
+    return ((code * d).astype(np.float32) + m).astype(np.float32).reshape(-1)
+
+
+def np_dequant_q5k(src: np.ndarray) -> np.ndarray:
+    """Q5_K from the block layout (q5_k.rs:6-24): [d | dmin | scales 12 |
+    qh 32 | qs 128]; element 32 j + l (sub-block j) has low bits from the
+    low (even j) or high (odd j) nibble of qs[32 (j // 2) + l] and bit 4
+    from bit j of qh[l]; (d * sc_j) * q - dmin * m_j in float32."""
+    b = np.asarray(src, np.uint8).reshape(-1, 176)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)
+    dmin = b[:, 2:4].copy().view(np.float16).astype(np.float32)
+    sc, m = np_scale_min(b[:, 4:16])
+    qh = b[:, 16:48].astype(np.uint32)
+    qs = b[:, 48:176].reshape(-1, 4, 32).astype(np.uint32)
+    j = np.arange(8)
+    nib = np.where((j % 2 == 0)[None, :, None], qs[:, j // 2, :] & 15, qs[:, j // 2, :] >> 4)
+    hb = (qh[:, None, :] >> j[None, :, None]) & 1
+    q = (nib | (hb << 4)).astype(np.float32)                     # [n, j, l]
+    ds = (d * sc.astype(np.float32)).astype(np.float32)
+    mm = (dmin * m.astype(np.float32)).astype(np.float32)
+    return ((ds[:, :, None] * q).astype(np.float32) - mm[:, :, None]).astype(np.float32).reshape(-1)
+
+
+def np_dequant_q8k(src: np.ndarray) -> np.ndarray:
+    """Q8_K from the block layout (q8_k.rs:12-23): [d f32 | qs 256 int8 |
+    bsums]; d * q in float32."""
+    b = np.asarray(src, np.uint8).reshape(-1, 292)
+    d = b[:, 0:4].copy().view(np.float32)
+    q = b[:, 4:260].view(np.int8).astype(np.float32)
+    return (d * q).astype(np.float32).reshape(-1)
+
+
 def iq2xxs_grid() -> np.ndarray:
     """The IQ2_XXS codebook as [256, 8] int8 (from the C restatement)."""
     g = np.array([lib().orc_iq2xxs_grid(i) for i in range(256)], np.uint64)
@@ -347,4 +391,5 @@ def np_dequant_iq2xxs(src: np.ndarray) -> np.ndarray:
 
 
 NP_DEQUANT = {Q4_K: np_dequant_q4k, Q6_K: np_dequant_q6k, Q8_0: np_dequant_q8_0,
-              Q2_K: np_dequant_q2k, IQ2_XXS: np_dequant_iq2xxs}
+              Q2_K: np_dequant_q2k, IQ2_XXS: np_dequant_iq2xxs, Q4_1: np_dequant_q4_1,
+              Q5_K: np_dequant_q5k, Q8_K: np_dequant_q8k}

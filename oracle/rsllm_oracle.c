@@ -18,9 +18,10 @@
  *   orc_f16_to_f32        all 65,536 bit patterns vs numpy float16 widening
  *   orc_q4k_scale_min     brute force over all 2^12 (sc, m) pairs through
  *                         the reference's inverse packer (q4_k.rs:100-124)
- *   orc_dequant_q4_k/q6_k/q8_0/q4_0
+ *   orc_dequant_q4_k/q6_k/q8_0/q4_0/q4_1/q5_k/q8_k
  *                         the reference's known-answer tests (q4_k.rs:167-250,
- *                         q6_k.rs:163-264, q8_0.rs:82-170, mod.rs:180-270),
+ *                         q6_k.rs:163-264, q8_0.rs:82-170, q4_0.rs:184-213,
+ *                         q5_k.rs:166-228, q8_k.rs:94-163, mod.rs:164-304),
  *                         closed forms d*sc*q - dmin*m, and an independent
  *                         numpy restatement over every block of seeded data
  *   orc_matmul_quant_f32  dequant-then-dot against float64 numpy (error
@@ -102,8 +103,9 @@ static inline float rd_f16(const uint8_t *p) {
 uint32_t orc_block_elements(uint32_t t) {
     switch (t) {
     case ORC_F32: case ORC_F16: case ORC_BF16: return 1;
-    case ORC_Q4_0: case ORC_Q8_0: return 32;
-    case ORC_Q2_K: case ORC_Q4_K: case ORC_Q6_K: case ORC_IQ2_XXS: return 256;
+    case ORC_Q4_0: case ORC_Q4_1: case ORC_Q8_0: return 32;
+    case ORC_Q2_K: case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_Q8_K:
+    case ORC_IQ2_XXS: return 256;
     default: return 0;
     }
 }
@@ -113,10 +115,13 @@ uint32_t orc_block_bytes(uint32_t t) {
     case ORC_F32: return 4;
     case ORC_F16: case ORC_BF16: return 2;
     case ORC_Q4_0: return 18;
+    case ORC_Q4_1: return 20;
     case ORC_Q8_0: return 34;
     case ORC_Q2_K: return 84;
     case ORC_Q4_K: return 144;
+    case ORC_Q5_K: return 176;
     case ORC_Q6_K: return 210;
+    case ORC_Q8_K: return 292;
     case ORC_IQ2_XXS: return 66;
     default: return 0;
     }
@@ -228,6 +233,90 @@ int orc_dequant_q4_0(const uint8_t *src, size_t src_len, float *dst, size_t n) {
             dst[b * 32 + j] = (float)x0 * d;
             dst[b * 32 + j + 16] = (float)x1 * d;
         }
+    }
+    return ORC_OK;
+}
+
+/* ---- dequant_q4_1: rsllm-gguf/src/dequant/q4_0.rs:66-87 ------------------ */
+/* 20-byte blocks [d f16 | m f16 | 16 code bytes]; x * d + m. */
+int orc_dequant_q4_1(const uint8_t *src, size_t src_len, float *dst, size_t n) {
+    int rc = check_blocks(src_len, n, 32, 20);
+    if (rc) return rc;
+    size_t nb = n / 32;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *blk = src + b * 20;
+        float d = rd_f16(blk);
+        float m = rd_f16(blk + 2);
+        for (int j = 0; j < 16; j++) {
+            float x0 = (float)(blk[4 + j] & 0x0F);
+            float x1 = (float)(blk[4 + j] >> 4);
+            dst[b * 32 + j] = x0 * d + m;
+            dst[b * 32 + j + 16] = x1 * d + m;
+        }
+    }
+    return ORC_OK;
+}
+
+/* ---- dequant_q5_k: rsllm-gguf/src/dequant/q5_k.rs:34-94 ------------------ */
+/* 176-byte blocks [d | dmin | scales 12 | qh 32 | qs 128]. Four rounds, each
+ * over a sub-block pair (is, is + 1): the low nibbles of qs[q_off + l] plus
+ * 16 where qh[l] & u1, then the high nibbles plus 16 where qh[l] & u2; u1,
+ * u2 start at 1, 2 and shift left by 2 per round. */
+int orc_dequant_q5_k(const uint8_t *src, size_t src_len, float *dst, size_t n) {
+    int rc = check_blocks(src_len, n, 256, 176);
+    if (rc) return rc;
+    size_t nb = n / 256;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *blk = src + b * 176;
+        float d = rd_f16(blk);
+        float dmin = rd_f16(blk + 2);
+        const uint8_t *scales = blk + 4;
+        const uint8_t *qh = blk + 16;
+        const uint8_t *qs = blk + 48;
+        float *o = dst + b * 256;
+        int is = 0, q_off = 0;
+        uint8_t u1 = 1, u2 = 2;
+        for (int it = 0; it < 4; it++) {
+            uint8_t sc1, m1, sc2, m2;
+            orc_q4k_scale_min(is, scales, &sc1, &m1);
+            orc_q4k_scale_min(is + 1, scales, &sc2, &m2);
+            float d1 = d * (float)sc1;
+            float m1f = dmin * (float)m1;
+            float d2 = d * (float)sc2;
+            float m2f = dmin * (float)m2;
+            for (int l = 0; l < 32; l++) {
+                uint8_t lo = qs[q_off + l] & 0x0F;
+                uint8_t hb = (qh[l] & u1) ? 16 : 0;
+                o[l] = d1 * (float)(uint8_t)(lo + hb) - m1f;
+            }
+            for (int l = 0; l < 32; l++) {
+                uint8_t lo = qs[q_off + l] >> 4;
+                uint8_t hb = (qh[l] & u2) ? 16 : 0;
+                o[32 + l] = d2 * (float)(uint8_t)(lo + hb) - m2f;
+            }
+            o += 64;
+            q_off += 32;
+            is += 2;
+            u1 = (uint8_t)(u1 << 2);
+            u2 = (uint8_t)(u2 << 2);
+        }
+    }
+    return ORC_OK;
+}
+
+/* ---- dequant_q8_k: rsllm-gguf/src/dequant/q8_k.rs:32-70 ------------------ */
+/* 292-byte blocks [d f32 | qs 256 int8 | bsums 32 (unused)]; d * q. */
+int orc_dequant_q8_k(const uint8_t *src, size_t src_len, float *dst, size_t n) {
+    int rc = check_blocks(src_len, n, 256, 292);
+    if (rc) return rc;
+    size_t nb = n / 256;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *blk = src + b * 292;
+        uint32_t bits = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8) | ((uint32_t)blk[2] << 16) |
+                        ((uint32_t)blk[3] << 24);
+        float d;
+        memcpy(&d, &bits, 4);
+        for (int i = 0; i < 256; i++) dst[b * 256 + i] = d * (float)(int8_t)blk[4 + i];
     }
     return ORC_OK;
 }
@@ -350,7 +439,10 @@ int orc_dequant_to_f32(uint32_t t, const uint8_t *src, size_t src_len, float *ds
     switch (t) {
     case ORC_F32: case ORC_F16: case ORC_BF16: return dequant_float(t, src, src_len, dst, n);
     case ORC_Q4_0: return orc_dequant_q4_0(src, src_len, dst, n);
+    case ORC_Q4_1: return orc_dequant_q4_1(src, src_len, dst, n);
     case ORC_Q4_K: return orc_dequant_q4_k(src, src_len, dst, n);
+    case ORC_Q5_K: return orc_dequant_q5_k(src, src_len, dst, n);
+    case ORC_Q8_K: return orc_dequant_q8_k(src, src_len, dst, n);
     case ORC_Q6_K: return orc_dequant_q6_k(src, src_len, dst, n);
     case ORC_Q8_0: return orc_dequant_q8_0(src, src_len, dst, n);
     case ORC_Q2_K: return orc_dequant_q2_k(src, src_len, dst, n);

@@ -33,8 +33,9 @@ enum {
 
 /* GgmlType ids, rsllm-gguf/src/tensor.rs:26-85 */
 enum {
-    ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 8,
-    ORC_Q2_K = 10, ORC_Q4_K = 12, ORC_Q6_K = 14, ORC_IQ2_XXS = 16, ORC_BF16 = 30
+    ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q8_0 = 8,
+    ORC_Q2_K = 10, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_Q8_K = 15,
+    ORC_IQ2_XXS = 16, ORC_BF16 = 30
 };
 
 /* Detail of the last error on this thread (sizes of NotBlockAligned /
@@ -66,10 +67,16 @@ int orc_dequant_q4_0(const uint8_t *src, size_t src_len, float *dst, size_t n);
 int orc_dequant_q2_k(const uint8_t *src, size_t src_len, float *dst, size_t n);
 int orc_dequant_iq2_xxs(const uint8_t *src, size_t src_len, float *dst, size_t n);
 uint64_t orc_iq2xxs_grid(int i);
+/* dequant_q4_1  rsllm-gguf/src/dequant/q4_0.rs:66-104
+ * dequant_q5_k  rsllm-gguf/src/dequant/q5_k.rs:34-94
+ * dequant_q8_k  rsllm-gguf/src/dequant/q8_k.rs:32-70 */
+int orc_dequant_q4_1(const uint8_t *src, size_t src_len, float *dst, size_t n);
+int orc_dequant_q5_k(const uint8_t *src, size_t src_len, float *dst, size_t n);
+int orc_dequant_q8_k(const uint8_t *src, size_t src_len, float *dst, size_t n);
 
-/* dequant_to_f32, rsllm-gguf/src/dequant/mod.rs:69-85 (the arms restated
- * here: F32, F16, BF16, Q4_0, Q4_K, Q6_K, Q8_0, Q2_K, IQ2_XXS; the rest
- * report ORC_UNSUPPORTED_DEQUANT). */
+/* dequant_to_f32, rsllm-gguf/src/dequant/mod.rs:69-85: every arm (F32,
+ * F16, BF16, Q4_0, Q4_1, Q4_K, Q5_K, Q6_K, Q8_0, Q2_K, Q8_K, IQ2_XXS); the
+ * rest report ORC_UNSUPPORTED_DEQUANT. */
 int orc_dequant_to_f32(uint32_t dtype, const uint8_t *src, size_t src_len, float *dst, size_t n);
 
 /* matmul_quant_f32, rsllm-backend-cpu/src/ops/quant_matmul.rs:45-119.

@@ -272,20 +272,15 @@ const char *ggml_name(uint32_t t) {
 // q4_k.rs:36-49, float.rs check_size).
 int validate_dequant(uint32_t dtype, const void *src, size_t src_len, const void *dst,
                      size_t dst_len) {
+    // every arm of the reference's dispatch (mod.rs:71-84)
     const bool impl = dtype == T_F32 || dtype == T_F16 || dtype == T_BF16 || dtype == T_Q4_0 ||
-                      dtype == T_Q4_K || dtype == T_Q6_K || dtype == T_Q8_0 || dtype == T_Q2_K ||
-                      dtype == T_IQ2_XXS;
-    const bool ref_decodable = impl || dtype == 3 /*Q4_1*/ || dtype == 13 /*Q5_K*/ ||
-                               dtype == 15 /*Q8_K*/;
-    if (!ref_decodable) {
+                      dtype == T_Q4_1 || dtype == T_Q4_K || dtype == T_Q5_K || dtype == T_Q6_K ||
+                      dtype == T_Q8_0 || dtype == T_Q2_K || dtype == T_Q8_K || dtype == T_IQ2_XXS;
+    if (!impl) {
         std::string m = std::string("dtype `") + ggml_name(dtype) +
                         "` is not yet supported for dequantization in this build";
         return set_err(RSLLM_HIP_ERR_UNSUPPORTED_DEQUANT, m.c_str(), ggml_name(dtype));
     }
-    if (!impl)
-        return set_err(RSLLM_HIP_ERR_UNIMPLEMENTED,
-                       "dequant_to_f32: dtype decodable by the reference is not implemented by "
-                       "the HIP backend");
     const size_t be = block_elems_of(dtype), bb = block_bytes_of(dtype);
     size_t expected;
     if (be > 1 && dst_len % be != 0) {

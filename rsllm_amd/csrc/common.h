@@ -9,8 +9,8 @@ namespace rsllm_hip {
 
 // GgmlType ids (rsllm-gguf/src/tensor.rs:26-85).
 enum : uint32_t {
-    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q2_K = 10,
-    T_Q4_K = 12, T_Q6_K = 14, T_IQ2_XXS = 16, T_BF16 = 30
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8, T_Q2_K = 10,
+    T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_Q8_K = 15, T_IQ2_XXS = 16, T_BF16 = 30
 };
 
 constexpr int kQ4kBytes = 144;

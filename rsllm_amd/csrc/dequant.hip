@@ -6,8 +6,10 @@
 // (Q4_K: d*sc <= 17 significant bits, times q <= 4 bits; Q6_K:
 // d*sc*(q-32) <= 23 bits; Q8_0/Q4_0: <= 18 bits; Q2_K: d*sc <= 15 bits,
 // times q <= 2; IQ2_XXS: d*(0.5+e)*0.25 <= 16 bits, times the grid byte
-// <= 6), so the only roundings are the final subtractions of Q4_K and Q2_K. Contraction is switched off anyway so each line
-// is evaluated exactly as written.
+// <= 6; Q5_K: d*sc <= 17 bits, times q <= 5 bits; Q4_1: d times q <= 4
+// bits), so the only roundings are the final subtractions / additions of
+// Q4_K, Q5_K, Q2_K and Q4_1 and Q8_K's product d*q (an f32 scale). Contraction
+// is switched off anyway so each line is evaluated exactly as written.
 #include "iq2xxs_grid.h"
 #include "kernels.h"
 
@@ -105,6 +107,80 @@ __global__ __launch_bounds__(256) void k_dequant_q4_0(const uint8_t *__restrict_
         o[j] = (float)x0 * d;
         o[j + 16] = (float)x1 * d;
     }
+}
+
+// One thread per Q4_1 block (20 bytes: d, m as f16, 16 code bytes):
+// q4_0.rs:66-87, code * d + m (the product exact: a 4-bit code times an f16
+// scale), one rounding in the addition.
+__global__ __launch_bounds__(256) void k_dequant_q4_1(const uint8_t *__restrict__ src,
+                                                      float *__restrict__ dst, size_t n_blocks) {
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_blocks) return;
+    const uint8_t *blk = src + b * 20;
+    const float d = f16_to_f32(blk[0] | (blk[1] << 8));
+    const float m = f16_to_f32(blk[2] | (blk[3] << 8));
+    float *o = dst + b * 32;
+    for (int j = 0; j < 16; j++) {
+        o[j] = (float)(blk[4 + j] & 15) * d + m;
+        o[j + 16] = (float)(blk[4 + j] >> 4) * d + m;
+    }
+}
+
+// One thread per (Q5_K block, 32-element sub-block j): q5_k.rs:53-91. Block
+// of 176 bytes: d, dmin (f16), the Q4_K scale packing (12 bytes), qh[32],
+// qs[128]. Element l of sub-block j: low 4 bits from qs[32 (j / 2) + l]
+// (low nibble for even j, high for odd), bit 4 from bit j of qh[l];
+// (d * sc_j) * q - dmin * m_j with both products exact (6-bit scale times
+// f16; 17-bit scale times a 5-bit code), one rounding in the subtraction.
+__global__ __launch_bounds__(256) void k_dequant_q5k(const uint8_t *__restrict__ src,
+                                                     float *__restrict__ dst, size_t n_blocks) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= n_blocks * 8) return;
+    const size_t b = gid >> 3;
+    const int j = (int)(gid & 7);
+    const uint8_t *blk = src + b * 176;
+    const float d = f16_to_f32(blk[0] | (blk[1] << 8));
+    const float dmin = f16_to_f32(blk[2] | (blk[3] << 8));
+    uint32_t s[3];
+    for (int i = 0; i < 3; i++)
+        s[i] = blk[4 + 4 * i] | (blk[5 + 4 * i] << 8) | (blk[6 + 4 * i] << 16) |
+               ((uint32_t)blk[7 + 4 * i] << 24);
+    uint32_t sc, m;
+    q4k_scale_min(j, s[0], s[1], s[2], sc, m);
+    const float d1 = d * (float)sc;
+    const float m1f = dmin * (float)m;
+    const uint8_t *qh = blk + 16;
+    const uint8_t *qs = blk + 48 + 32 * (j >> 1);
+    const int shift = (j & 1) ? 4 : 0;
+    float *o = dst + b * 256 + 32 * j;
+    for (int l = 0; l < 32; l += 4) {
+        float r[4];
+        for (int u = 0; u < 4; u++) {
+            const uint32_t q = ((qs[l + u] >> shift) & 15) | (((qh[l + u] >> j) & 1) << 4);
+            r[u] = d1 * (float)q - m1f;
+        }
+        *reinterpret_cast<float4 *>(o + l) = make_float4(r[0], r[1], r[2], r[3]);
+    }
+}
+
+// One thread per (Q8_K block, 32-element group g): q8_k.rs:50-66. Block of
+// 292 bytes: d (f32), qs[256] (int8), bsums (not used by the decode);
+// d * q, one rounding.
+__global__ __launch_bounds__(256) void k_dequant_q8k(const uint8_t *__restrict__ src,
+                                                     float *__restrict__ dst, size_t n_blocks) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= n_blocks * 8) return;
+    const size_t b = gid >> 3;
+    const int g = (int)(gid & 7);
+    const uint8_t *blk = src + b * 292;
+    const float d = __builtin_bit_cast(
+        float, (uint32_t)(blk[0] | (blk[1] << 8) | (blk[2] << 16) | ((uint32_t)blk[3] << 24)));
+    const uint8_t *q = blk + 4 + 32 * g;
+    float *o = dst + b * 256 + 32 * g;
+    for (int l = 0; l < 32; l += 4)
+        *reinterpret_cast<float4 *>(o + l) =
+            make_float4(d * (float)(int8_t)q[l], d * (float)(int8_t)q[l + 1],
+                        d * (float)(int8_t)q[l + 2], d * (float)(int8_t)q[l + 3]);
 }
 
 // F32 / F16 / BF16 arms (float.rs): element-wise widening.
@@ -282,6 +358,15 @@ hipError_t launch_dequant(uint32_t dtype, const uint8_t *src, float *dst, size_t
         break;
     case T_Q4_0:
         k_dequant_q4_0<<<grid_for(n_elems / 32, 256), 256, 0, s>>>(src, dst, n_elems / 32);
+        break;
+    case T_Q4_1:
+        k_dequant_q4_1<<<grid_for(n_elems / 32, 256), 256, 0, s>>>(src, dst, n_elems / 32);
+        break;
+    case T_Q5_K:
+        k_dequant_q5k<<<grid_for(n_elems / 256 * 8, 256), 256, 0, s>>>(src, dst, n_elems / 256);
+        break;
+    case T_Q8_K:
+        k_dequant_q8k<<<grid_for(n_elems / 256 * 8, 256), 256, 0, s>>>(src, dst, n_elems / 256);
         break;
     case T_Q2_K:
         k_dequant_q2k<<<grid_for(n_elems / 256 * 16, 256), 256, 0, s>>>(src, dst, n_elems / 256);

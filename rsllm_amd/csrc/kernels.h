@@ -10,8 +10,8 @@ namespace rsllm_hip {
 inline size_t block_elems_of(uint32_t t) {
     switch (t) {
     case T_F32: case T_F16: case T_BF16: return 1;
-    case T_Q4_0: case T_Q8_0: return 32;
-    case T_Q2_K: case T_Q4_K: case T_Q6_K: case T_IQ2_XXS: return 256;
+    case T_Q4_0: case T_Q4_1: case T_Q8_0: return 32;
+    case T_Q2_K: case T_Q4_K: case T_Q5_K: case T_Q6_K: case T_Q8_K: case T_IQ2_XXS: return 256;
     default: return 0;
     }
 }
@@ -21,10 +21,13 @@ inline size_t block_bytes_of(uint32_t t) {
     case T_F32: return 4;
     case T_F16: case T_BF16: return 2;
     case T_Q4_0: return 18;
+    case T_Q4_1: return 20;
     case T_Q8_0: return 34;
     case T_Q2_K: return 84;
     case T_Q4_K: return 144;
+    case T_Q5_K: return 176;
     case T_Q6_K: return 210;
+    case T_Q8_K: return 292;
     case T_IQ2_XXS: return 66;
     default: return 0;
     }

@@ -101,8 +101,35 @@ def iq2xxs_blocks(g: np.random.Generator, n_blocks: int) -> np.ndarray:
     return out
 
 
+def q4_1_blocks(g: np.random.Generator, n_blocks: int) -> np.ndarray:
+    """[n_blocks, 20] uint8 Q4_1 blocks: d = f16(|N(0, 1e-2)|), m = f16(N(0,
+    1e-2)), 16 random code bytes."""
+    out = g.integers(0, 256, size=(n_blocks, 20), dtype=np.uint8)
+    out[:, 0:2] = _f16_abs_normal(g, n_blocks, 1e-2).view(np.uint8).reshape(n_blocks, 2)
+    out[:, 2:4] = (g.standard_normal(n_blocks) * 1e-2).astype(np.float16).view(np.uint8).reshape(n_blocks, 2)
+    return out
+
+
+def q5k_blocks(g: np.random.Generator, n_blocks: int) -> np.ndarray:
+    """[n_blocks, 176] uint8 Q5_K blocks: d, dmin = f16(|N(0, 1e-3)|), scale
+    bytes, qh and qs uniform."""
+    out = g.integers(0, 256, size=(n_blocks, 176), dtype=np.uint8)
+    out[:, 0:2] = _f16_abs_normal(g, n_blocks, 1e-3).view(np.uint8).reshape(n_blocks, 2)
+    out[:, 2:4] = _f16_abs_normal(g, n_blocks, 1e-3).view(np.uint8).reshape(n_blocks, 2)
+    return out
+
+
+def q8k_blocks(g: np.random.Generator, n_blocks: int) -> np.ndarray:
+    """[n_blocks, 292] uint8 Q8_K blocks: d = f32(|N(0, 1e-2)|), qs and bsums
+    uniform."""
+    out = g.integers(0, 256, size=(n_blocks, 292), dtype=np.uint8)
+    out[:, 0:4] = np.abs(g.standard_normal(n_blocks) * 1e-2).astype(np.float32).view(np.uint8).reshape(n_blocks, 4)
+    return out
+
+
 _BLOCKS = {GgmlType.Q4_K: q4k_blocks, GgmlType.Q6_K: q6k_blocks, GgmlType.Q8_0: q8_0_blocks,
-           GgmlType.Q4_0: q4_0_blocks, GgmlType.Q2_K: q2k_blocks, GgmlType.IQ2_XXS: iq2xxs_blocks}
+           GgmlType.Q4_0: q4_0_blocks, GgmlType.Q2_K: q2k_blocks, GgmlType.IQ2_XXS: iq2xxs_blocks,
+           GgmlType.Q4_1: q4_1_blocks, GgmlType.Q5_K: q5k_blocks, GgmlType.Q8_K: q8k_blocks}
 
 
 def weight(dtype: GgmlType, out_dim: int, in_dim: int, seed: int) -> np.ndarray:

@@ -15,6 +15,7 @@ import numpy as np
 
 Q4_0, Q8_0, Q4_K, Q6_K, F32, F16, BF16, Q3_K = 2, 8, 12, 14, 0, 1, 30, 11
 Q2_K, IQ2_XXS = 10, 16
+Q4_1, Q5_K, Q8_K = 3, 13, 15
 DEQUANT_SIZE_MISMATCH, UNSUPPORTED_DEQUANT = 5, 6
 
 
@@ -118,6 +119,38 @@ def pack_iq2xxs(d, grids, signs, extras) -> np.ndarray:
 
 # --- dequant KATs: (name, dtype, src, n, check) -------------------------------
 # check(status, values) raises AssertionError on mismatch.
+
+def pack_q4_1(d, m, nibbles) -> np.ndarray:
+    """q4_0.rs:123-133 pack_q4_1: f16 d, f16 m, byte j = nibble j | nibble j + 16 << 4."""
+    nb = np.asarray(nibbles, np.uint8) & 15
+    qs = nb[:16] | (nb[16:] << 4)
+    return np.concatenate([np.frombuffer(f16_bytes(d) + f16_bytes(m), np.uint8), qs.astype(np.uint8)])
+
+
+def pack_q5k(d, dmin, sc, m, q5) -> np.ndarray:
+    """q5_k.rs:122-156 pack_block: f16 d, dmin, the Q4_K scale packing, qh bit
+    (2k) / (2k + 1) of byte l for elements 64k + l / 64k + 32 + l at or above
+    16, qs[32k + l] = low nibble of element 64k + l | that of 64k + 32 + l << 4."""
+    q5 = np.asarray(q5, np.uint8)
+    qh = np.zeros(32, np.uint8)
+    qs = np.zeros(128, np.uint8)
+    for k in range(4):
+        for l in range(32):
+            lo, hi = q5[64 * k + l], q5[64 * k + 32 + l]
+            if lo >= 16:
+                qh[l] |= 1 << (2 * k)
+            if hi >= 16:
+                qh[l] |= 1 << (2 * k + 1)
+            qs[32 * k + l] = (lo & 15) | ((hi & 15) << 4)
+    return np.concatenate([np.frombuffer(f16_bytes(d) + f16_bytes(dmin), np.uint8),
+                           pack_scales(sc, m), qh, qs])
+
+
+def pack_q8k(d, qs) -> np.ndarray:
+    """q8_k.rs:78-86 pack_block: f32 d, 256 int8 codes, 32 zero bsum bytes."""
+    return np.concatenate([np.frombuffer(np.float32(d).tobytes(), np.uint8),
+                           np.asarray(qs, np.int8).view(np.uint8), np.zeros(32, np.uint8)])
+
 
 def _close(want, tol):
     want = np.asarray(want, np.float32)
@@ -273,6 +306,56 @@ def dequant_kats():
     # iq2_xxs.rs:391-399 wrong_src_size_errors; dequant/mod.rs iq2_xxs dispatch arm
     k.append(("iq2xxs_wrong_src_size", IQ2_XXS, np.zeros(65, np.uint8), 256,
               _status(DEQUANT_SIZE_MISMATCH)))
+    # q4_0.rs:184-193 q4_1_min_only_offset
+    k.append(("q4_1_min_only_offset", Q4_1, pack_q4_1(0.0, 3.5, [7] * 32), 32,
+              _close(np.full(32, 3.5), 1e-3)))
+    # q4_0.rs:195-213 q4_1_linear_with_offset
+    nib = [i % 16 for i in range(32)]
+    k.append(("q4_1_linear_with_offset", Q4_1, pack_q4_1(0.5, 1.0, nib), 32,
+              _close(0.5 * np.array(nib, np.float32) + 1.0, 1e-3)))
+    # dequant/mod.rs:165-178 q4_1_dispatch_routes_to_q4_1_arm (d 0, m 7, zero codes)
+    k.append(("q4_1_arm", Q4_1, pack_q4_1(0.0, 7.0, [0] * 32), 32, _close(np.full(32, 7.0), 1e-3)))
+    # q5_k.rs:166-184 five_bit_range_zero_min
+    q5 = [i % 32 for i in range(256)]
+    k.append(("q5k_five_bit_range_zero_min", Q5_K, pack_q5k(1.0, 0.0, [1] * 8, [0] * 8, q5), 256,
+              _close(np.array(q5, np.float32), 1e-2)))
+    # q5_k.rs:185-195 full_range_with_offset
+    k.append(("q5k_full_range_with_offset", Q5_K, pack_q5k(0.5, 0.5, [2] * 8, [1] * 8, [31] * 256),
+              256, _close(np.full(256, 30.5), 1e-2)))
+    # q5_k.rs:197-218 distinct_per_sub_block_scales_and_mins
+    sc8 = list(range(1, 9))
+    k.append(("q5k_distinct_scales_and_mins", Q5_K, pack_q5k(1.0, 1.0, sc8, sc8, [0] * 256), 256,
+              _close(np.repeat(-np.array(sc8, np.float32), 32), 1e-2)))
+    # q5_k.rs:220-228 wrong_src_size_errors
+    k.append(("q5k_wrong_src_size", Q5_K, np.zeros(175, np.uint8), 256,
+              _status(DEQUANT_SIZE_MISMATCH)))
+    # dequant/mod.rs:236-255 q5_k_dispatch_routes_to_q5_k_arm (sc 2, qh 0, codes 1)
+    blk = np.concatenate([np.frombuffer(f16_bytes(1.0) + f16_bytes(0.0), np.uint8),
+                          pack_scales([2] * 8, [0] * 8), np.zeros(32, np.uint8),
+                          np.full(128, 0x11, np.uint8)])
+    k.append(("q5k_dispatch_arm", Q5_K, blk, 256, _close(np.full(256, 2.0), 1e-2)))
+    # q8_k.rs:94-109 unit_scale_passes_through_qs
+    qs = [i % 127 for i in range(256)]
+    k.append(("q8k_unit_scale", Q8_K, pack_q8k(1.0, qs), 256, _close(np.array(qs, np.float32), 1e-4)))
+    # q8_k.rs:110-120 negative_scale_inverts_sign
+    k.append(("q8k_negative_scale", Q8_K, pack_q8k(-0.5, [5] * 256), 256,
+              _close(np.full(256, -2.5), 1e-4)))
+    # q8_k.rs:121-136 boundary_quant_values
+    qs = [0] * 256
+    qs[0], qs[1], qs[2], qs[3] = -128, 127, 0, -1
+    want = np.float32(0.01) * np.array(qs, np.float32)
+    k.append(("q8k_boundary_values", Q8_K, pack_q8k(0.01, qs), 256, _close(want, 1e-4)))
+    # q8_k.rs:137-146 wrong_src_size_errors
+    k.append(("q8k_wrong_src_size", Q8_K, np.zeros(291, np.uint8), 256,
+              _status(DEQUANT_SIZE_MISMATCH)))
+    # q8_k.rs:147-163 multi_block_decode (wrapping int8 patterns)
+    qa = np.arange(256).astype(np.uint8).view(np.int8)
+    qb = (-qa.astype(np.int16)).astype(np.int8)
+    want = np.concatenate([2.0 * qa.astype(np.float32), -qb.astype(np.float32)])
+    k.append(("q8k_multi_block", Q8_K, np.concatenate([pack_q8k(2.0, qa), pack_q8k(-1.0, qb)]), 512,
+              _close(want, 1e-4)))
+    # dequant/mod.rs:291-303 q8_k_dispatch_routes_to_q8_k_arm (d 2, codes 3)
+    k.append(("q8k_dispatch_arm", Q8_K, pack_q8k(2.0, [3] * 256), 256, _close(np.full(256, 6.0), 1e-3)))
     return k
 
 

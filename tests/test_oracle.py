@@ -71,7 +71,8 @@ def test_np_scale_min_matches_oracle_all_12bit_pairs(oracle):
             assert oracle.q4k_scale_min(j, q[i]) == (sc[i, j], m[i, j])
 
 
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K, G.IQ2_XXS])
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K, G.IQ2_XXS, G.Q4_1, G.Q5_K,
+                                   G.Q8_K])
 def test_oracle_matches_independent_numpy_restatement(oracle, dtype):
     w = synth.weight(dtype, 512, 4096, seed=int(dtype))
     n = 512 * 4096
