@@ -195,7 +195,7 @@ struct Gemv1Shape {
     uint32_t w1_bytes;
 };
 
-template <class F, int NW, int PD, int GPT, int BT = 1>
+template <class F, int NW, int PD, int GPT, int BT = 1, bool UNI = false>
 __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w, uint32_t w_bytes,
                                                   const float *__restrict__ x,
                                                   float *__restrict__ y, Gemv1Shape sh,
@@ -240,11 +240,20 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
     };
     auto row_of = [&](int j) { return row_base + r0 + wpg * (wv + NW * j); };
     typename F::Slice buf[PD];
+    // UNI (rows of whole 8-unit groups, F::kUniform): per-lane offsets
+    // fixed, the tile's base a scalar offset
+    uint32_t loff[F::kNO];
+    if constexpr (UNI) F::lane_offs(loff, ks, k);
     auto load_tile = [&](typename F::Slice &sl, int t) {
         const int j = t / ncols, col = t - j * ncols;
-        const int unit = min(col * 8 + ks, nunits - 1);
         const __amdgpu_buffer_rsrc_t r = t < T ? rw : rnull;  // rows past T: no traffic
-        F::load(sl, r, min(row_of(j), out_dim - 1) - mbase, unit, k, in_dim, mrows);
+        const int row = min(row_of(j), out_dim - 1) - mbase;
+        if constexpr (UNI) {
+            F::load_u(sl, r, loff, F::tile_base((uint32_t)row, (uint32_t)col, in_dim));
+        } else {
+            const int unit = min(col * 8 + ks, nunits - 1);
+            F::load(sl, r, row, unit, k, in_dim, mrows);
+        }
     };
 
     // Prologue: x loads, the first tiles, then quantisation into LDS (token
@@ -350,26 +359,33 @@ static int gemv1_gpt(int in_dim, int nw, int bt = 1) {
     return gpt <= 1 ? 1 : gpt <= 2 ? 2 : gpt <= 4 ? 4 : 0;
 }
 
-template <class F, int NW, int PD, int GPT, int BT>
-static hipError_t gemv1_go(const uint8_t *w, size_t w_bytes, const float *x, float *y,
-                           const Gemv1Shape &sh, int n_tok, int n_wg, hipStream_t s) {
-    static bool attr_set = false;  // per instantiation; idempotent if raced
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemv1<F, NW, PD, GPT, BT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)kGemv1MaxLds);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+template <class F, int NW, int PD, int GPT, int BT, bool UNI>
+static hipError_t gemv1_launch(const uint8_t *w, size_t w_bytes, const float *x, float *y,
+                               const Gemv1Shape &sh, int n_tok, int n_wg, hipStream_t s) {
+    // the attribute once per kernel (thread-safe static initialisation)
+    static const hipError_t attr = hipFuncSetAttribute(
+        (const void *)k_gemv1<F, NW, PD, GPT, BT, UNI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)kGemv1MaxLds);
+    if (attr != hipSuccess) return attr;
     // n_wg workgroups dealt over the groups (at least one per group, at most
     // one per row)
     Gemv1Shape g = sh;
     const int n_grp = sh.out_dim / sh.rows_per_group;
     g.wpg = max(1, min(n_wg / n_grp, sh.rows_per_group));
-    k_gemv1<F, NW, PD, GPT, BT>
+    k_gemv1<F, NW, PD, GPT, BT, UNI>
         <<<(unsigned)(n_grp * g.wpg), 64 * NW, gemv1_lds_bytes<F>(sh.in_dim, BT), s>>>(
             w, (uint32_t)w_bytes, x, y, g, n_tok);
     return hipGetLastError();
+}
+
+template <class F, int NW, int PD, int GPT, int BT>
+static hipError_t gemv1_go(const uint8_t *w, size_t w_bytes, const float *x, float *y,
+                           const Gemv1Shape &sh, int n_tok, int n_wg, hipStream_t s) {
+    // rows of whole 8-unit groups take the scalar-offset tile loads
+    if constexpr (F::kUniform)
+        if ((sh.in_dim / F::kEPU) % 8 == 0)
+            return gemv1_launch<F, NW, PD, GPT, BT, true>(w, w_bytes, x, y, sh, n_tok, n_wg, s);
+    return gemv1_launch<F, NW, PD, GPT, BT, false>(w, w_bytes, x, y, sh, n_tok, n_wg, s);
 }
 
 template <class F, int NW, int PD, int BT = 1>

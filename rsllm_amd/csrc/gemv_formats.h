@@ -59,7 +59,12 @@ struct XSlice {
 // ---- formats ------------------------------------------------------------------
 // Each format gives: kEPU (elements per unit), kXF (activation fields per
 // lane: 5 = two groups, 3 = one group), units(in_dim), the element ranges of
-// a lane's groups, valid(), load() of a weight slice, dot().
+// a lane's groups, valid(), load() of a weight slice, dot(). Formats with
+// kUniform also give the split form of load() for matrices whose rows are
+// whole groups of 8 units (units(in_dim) % 8 == 0): the slice of lane
+// (ks, k) in column `col` of row `row` is at tile_base(row, col) (the same
+// for the whole wavefront, a scalar offset) plus lane_offs(ks, k) (fixed per
+// lane), so a tile costs no per-lane address arithmetic.
 
 // Q4_K, GGUF layout. Lane (ks, k) of column c reads block u = 8c + ks: the
 // header (d, dmin, 12 scale bytes) and qs bytes 16k..16k+15 = elements
@@ -67,9 +72,24 @@ struct XSlice {
 // (high nibbles, group "hi"), p = k/2.
 struct FQ4K {
     static constexpr int kEPU = 256, kXF = 5;
+    static constexpr bool kUniform = true;
+    static constexpr int kNO = 2;
     struct Slice {
         uint4 hdr, qs;
     };
+    // unit 8 col + ks of the row: block offset (row nb + 8 col) 144 + ks 144
+    __device__ static uint32_t tile_base(uint32_t row, uint32_t col, int in_dim) {
+        return (row * (uint32_t)(in_dim >> 8) + 8u * col) * 144u;
+    }
+    __device__ static void lane_offs(uint32_t (&o)[kNO], int ks, int k) {
+        o[0] = (uint32_t)ks * 144u;
+        o[1] = (uint32_t)ks * 144u + 16u + 16u * (uint32_t)k;
+    }
+    __device__ static void load_u(Slice &s, __amdgpu_buffer_rsrc_t r, const uint32_t (&o)[kNO],
+                                  uint32_t base) {
+        s.hdr = bload16(r, o[0], base);
+        s.qs = bload16(r, o[1], base);
+    }
     __device__ static int units(int in_dim) { return in_dim >> 8; }
     __device__ static int elem_lo(int unit, int k) { return unit * 256 + 64 * (k >> 1) + 16 * (k & 1); }
     __device__ static int elem_hi(int unit, int k) { return elem_lo(unit, k) + 32; }
@@ -108,10 +128,30 @@ struct FQ4K {
 // the block's 16 scales and d. Element e = 128h + 32kq + l uses scale e/16.
 struct FQ6K {
     static constexpr int kEPU = 256, kXF = 5;
+    static constexpr bool kUniform = true;
+    static constexpr int kNO = 4;
     struct Slice {
         uint4 ql, qh, sc;
         uint32_t d;
     };
+    // with units % 8 == 0, block row nb + 8 col + ks is block ks of super-tile
+    // row nb / 8 + col, and every super-tile holds 8 blocks
+    __device__ static uint32_t tile_base(uint32_t row, uint32_t col, int in_dim) {
+        return (row * (uint32_t)(in_dim >> 11) + col) * 1680u;
+    }
+    __device__ static void lane_offs(uint32_t (&o)[kNO], int ks, int k) {
+        o[0] = (uint32_t)ks * 128u + 16u * (uint32_t)k;
+        o[1] = 1024u + (uint32_t)ks * 64u + 32u * (uint32_t)(k >> 2) + 16u * (uint32_t)(k & 1);
+        o[2] = 1536u + (uint32_t)ks * 16u;
+        o[3] = 1664u + (uint32_t)ks * 2u;
+    }
+    __device__ static void load_u(Slice &s, __amdgpu_buffer_rsrc_t r, const uint32_t (&o)[kNO],
+                                  uint32_t base) {
+        s.ql = bload16(r, o[0], base);
+        s.qh = bload16(r, o[1], base);
+        s.sc = bload16(r, o[2], base);
+        s.d = bload2(r, o[3], base);
+    }
     __device__ static int units(int in_dim) { return in_dim >> 8; }
     __device__ static int elem_lo(int unit, int k) {
         return unit * 256 + 128 * (k >> 2) + 32 * ((k & 3) >> 1) + 16 * (k & 1);
@@ -164,6 +204,8 @@ struct FQ6K {
 template <bool Q4>
 struct FQ8 {
     static constexpr int kEPU = Q4 ? 256 : 128, kXF = Q4 ? 5 : 3;
+    static constexpr bool kUniform = false;
+    static constexpr int kNO = 1;
     static constexpr int kQB = Q4 ? 16 : 32, kSTB = Q4 ? 144 : 272;
     struct Slice {
         uint4 q;
@@ -211,6 +253,8 @@ struct FQ8 {
 // 8h + 4p + r) and the same + 32 (group "hi", sub-block + 2), as
 // dequant_q2_k's element order (q2_k.rs:62-94) gives.
 struct FQ2K {
+    static constexpr bool kUniform = false;
+    static constexpr int kNO = 1;
     static constexpr int kEPU = 256, kXF = 5;
     struct Slice {
         uint4 qs;
@@ -270,6 +314,8 @@ __device__ __forceinline__ uint32_t iq2_apply_signs(uint32_t mag, uint32_t bits4
 // +-{8, 25, 43} (iq2_xxs.rs:66-111); the sub-group scale
 // db = d * (0.5 + extra) * 0.25 multiplies the whole slice.
 struct FIQ2XXS {
+    static constexpr bool kUniform = false;
+    static constexpr int kNO = 1;
     static constexpr int kEPU = 256, kXF = 5;
     struct Slice {
         uint32_t a0, a1, d;
