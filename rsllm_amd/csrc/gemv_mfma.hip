@@ -65,9 +65,12 @@ __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t vo
 // the activations enter as hi + lo f16 planes (about 2^-22 relative).
 //
 // Each format gives: W (a lane's bytes for one step), elem / piece (the K
-// order: element of MFMA j, lane group q, step s), load, and step<NT>: the
-// MFMAs of one step for one 16-row tile against NT token tiles, folded into
-// acc[NT] with the scales.
+// order: element of MFMA j, lane group q, step s), load, and step<NT, PACK>:
+// the MFMAs of one step for one 16-row tile against NT token tiles, folded
+// into acc[NT] with the scales. With PACK (up to 8 tokens) the A operand x
+// holds the hi plane of tokens 0..7 in its rows 0..7 and the lo plane in
+// rows 8..15, and xl is not read: one MFMA per sub-step, and D rows t and
+// t + 8 add up to token t.
 
 __device__ __forceinline__ f32x4 mfma16x32(const uint4 &x, const f16x8 &w, const f32x4 &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, x), w, c, 0, 0, 0);
@@ -100,7 +103,7 @@ struct MQ4K {
         w.hdr = bload16(r, off, 0);
         w.qs = bload16(r, off + 16u + 32u * (uint32_t)q + 16u * (uint32_t)(s & 1), 0);
     }
-    template <int NT>
+    template <int NT, bool PACK = false>
     __device__ static void step(const W &w, int q, const uint4 (&x)[4][NT], const uint4 (&xl)[4][NT],
                                 f32x4 (&acc)[NT]) {
         const float d = f16_to_f32(w.hdr.x & 0xFFFFu), dmin = f16_to_f32(w.hdr.x >> 16);
@@ -134,9 +137,9 @@ struct MQ4K {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 P = mfma16x32(x[j][nt], b[j], P);
-                P = mfma16x32(xl[j][nt], b[j], P);
+                if (!PACK) P = mfma16x32(xl[j][nt], b[j], P);
                 M = mfma16x32(x[j][nt], (j & 1) ? bmh : bml, M);
-                M = mfma16x32(xl[j][nt], (j & 1) ? bmh : bml, M);
+                if (!PACK) M = mfma16x32(xl[j][nt], (j & 1) ? bmh : bml, M);
             }
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[nt][i] = fmaf(-dmin, M[i], fmaf(d, P[i], acc[nt][i]));
@@ -195,13 +198,25 @@ struct MQ6K {
         w.sh = bload4(r, base + rS * 192u + jb * 16u + 8u * h + 4u);
         w.d = bload2(r, base + rS * 208u + jb * 2u, 0);
     }
-    template <int NT>
+    // lane holds a scale with |sc| > 64
+    __device__ static bool wide_lane(const W &w, int q) {
+        const int il = (int)(int8_t)(w.sl >> (8 * q)), ih = (int)(int8_t)(w.sh >> (8 * q));
+        return il > 64 || il < -64 || ih > 64 || ih < -64;
+    }
+    template <int NT, bool PACK = false>
     __device__ static void step(const W &w, int q, const uint4 (&x)[4][NT], const uint4 (&xl)[4][NT],
                                 f32x4 (&acc)[NT]) {
+        step_m<NT, 2, PACK>(w, q, x, xl, acc);
+    }
+    // WIDE 0: no scale of the wavefront's step has |sc| > 64 (the caller
+    // checked); 1: add the B_lo MFMAs; 2: decide here, per step
+    template <int NT, int WIDE, bool PACK>
+    __device__ static void step_m(const W &w, int q, const uint4 (&x)[4][NT],
+                                  const uint4 (&xl)[4][NT], f32x4 (&acc)[NT]) {
         const float d = f16_to_f32(w.d);
         const int il = (int)(int8_t)(w.sl >> (8 * q)), ih = (int)(int8_t)(w.sh >> (8 * q));
         const _Float16 scl = (_Float16)(float)il, sch = (_Float16)(float)ih;
-        const bool wide = __ballot(il > 64 || il < -64 || ih > 64 || ih < -64) != 0;
+        const bool wide = WIDE == 1 || (WIDE == 2 && __ballot(wide_lane(w, q)) != 0);
         const uint32_t shl = 2u * (uint32_t)(q >> 1), shh = 4u + shl;
         const uint32_t l[4] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w};
         const uint32_t hb[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
@@ -232,7 +247,7 @@ struct MQ6K {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 P[nt] = mfma16x32(x[j][nt], b[j], P[nt]);
-                P[nt] = mfma16x32(xl[j][nt], b[j], P[nt]);
+                if (!PACK) P[nt] = mfma16x32(xl[j][nt], b[j], P[nt]);
             }
         }
         if (wide) {
@@ -282,7 +297,7 @@ struct MQ8 {
             w.q[j] = bload8(r, base + (jb + (uint32_t)j) * 32u + 8u * (uint32_t)q, 0);
         w.d = bload8(r, base + rS * 32u + jb * 2u, 0);
     }
-    template <int NT>
+    template <int NT, bool PACK = false>
     __device__ static void step(const W &w, int, const uint4 (&x)[4][NT], const uint4 (&xl)[4][NT],
                                 f32x4 (&acc)[NT]) {
         const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
@@ -308,8 +323,8 @@ struct MQ8 {
         for (int nt = 0; nt < NT; nt++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const f32x4 P =
-                    mfma16x32(xl[j][nt], b[j], mfma16x32(x[j][nt], b[j], f32x4{0.f, 0.f, 0.f, 0.f}));
+                const f32x4 P0 = mfma16x32(x[j][nt], b[j], f32x4{0.f, 0.f, 0.f, 0.f});
+                const f32x4 P = PACK ? P0 : mfma16x32(xl[j][nt], b[j], P0);
 #pragma unroll
                 for (int i = 0; i < 4; i++) acc[nt][i] = fmaf(d[j], P[i], acc[nt][i]);
             }
@@ -525,30 +540,39 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__
 // The operand loads of mf_rows give each lane of a 16-row tile its own row,
 // so one load instruction touches 16 rows' cache lines for a few bytes each
 // (L1 requests about 4x those of a contiguous stream). Here a workgroup of 4
-// wavefronts owns kMfsRows = 32 rows and streams them in chunks of kMfsK =
-// 1024 elements: each row's chunk is one contiguous byte range (4 Q4_K
-// blocks; half a Q6_K super-tile's ql / qh / scale runs and its d run; 4
-// Q8_0 super-tiles), copied to LDS with 16-byte global_load_lds pieces in
-// row order (every line read whole, no registers held), two chunks in
-// flight (double buffer, one barrier per chunk). Wavefront w then takes
-// steps 2w, 2w + 1 of the chunk for both row tiles, reading the operand
-// fields from LDS (row strides pad to distinct LDS banks) against the
-// activation image as mf_rows does. The 4 wavefronts' tiles are summed in
-// LDS in wavefront order.
+// wavefronts (8 up to 8 tokens) owns kMfsRows = 32 rows and streams them in
+// chunks of kMfsK = 1024 elements: each row's chunk is one contiguous byte
+// range (4 Q4_K blocks; half a Q6_K super-tile's ql / qh / scale runs and
+// its d run; 4 Q8_0 super-tiles), copied to LDS with 16-byte buffer-to-LDS
+// pieces in row order (every line read whole, no registers held), two
+// chunks in flight (double buffer, one barrier per chunk). The wavefronts
+// split the chunk's 8 steps (2 each, or 1 with 8 wavefronts) for both row
+// tiles, reading the operand fields from LDS (row strides pad to distinct
+// LDS banks) against the activation image as mf_rows does. The wavefronts'
+// tiles are summed in LDS in wavefront order.
+//
+// (A design with 512-element chunks in three buffers, two in flight, and
+// the activations loaded a chunk ahead measured slower: 19.4 against
+// 16.8 us at C1 14336 x 4096, 8 tokens; twice the barriers per byte.)
 //
 // Matrices with few rows split K: grid.y = sk workgroups per 32 rows, each
 // over an equal run of chunks, writing its partial tile to part[split]; a
 // second kernel adds the sk partials in split order (deterministic).
 typedef __attribute__((address_space(3))) void lds_void;
 
-// (a non-template wrapper: the builtin called directly inside a kernel
-// template keeps the host pass from emitting that kernel's stub)
-__device__ __forceinline__ void dma16(const void *g, lds_void *l) {
-    __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+// 16 bytes per lane from a buffer resource into LDS (lane i writes bytes
+// 16 i .. 16 i + 15 after the wavefront's base); a lane whose offset lies
+// past the resource's size moves zeros without a memory access. (A
+// non-template wrapper: the builtin called directly inside a kernel template
+// keeps the host pass from emitting that kernel's stub.)
+__device__ __forceinline__ void dma16b(__amdgpu_buffer_rsrc_t r, uint32_t voff, lds_void *l) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 16, voff, 0, 0, 0);
 }
 
 constexpr int kMfsRows = 32;
 constexpr int kMfsK = 1024;
+constexpr int kMfsPackWaves = 8;  // wavefronts per workgroup of the packed kernel
+constexpr uint32_t kMfsNoPiece = 0xFFFFFFF0u;  // past every resource: zeros, no access
 
 // Per format: PR 16-byte pieces per row chunk (one pad piece where needed for
 // the bank spread); piece k of chunk c of row r is at byte
@@ -557,8 +581,9 @@ constexpr int kMfsK = 1024;
 template <class F> struct MfsStage;
 template <> struct MfsStage<MQ4K> {
     static constexpr int PR = 37;  // 4 blocks x 144 B = 36 pieces + 1 pad
+    __device__ static uint32_t row_bytes(int in_dim) { return (uint32_t)(in_dim >> 8) * 144u; }
     __device__ static uint32_t off0(uint32_t row, int k, int in_dim) {
-        return row * (uint32_t)(in_dim >> 8) * 144u + 16u * (uint32_t)(k < 36 ? k : 0);
+        return k < 36 ? row * (uint32_t)(in_dim >> 8) * 144u + 16u * (uint32_t)k : kMfsNoPiece;
     }
     __device__ static uint32_t c_off(int c, int) { return (uint32_t)c * 576u; }
     __device__ static void load(MQ4K::W &v, const uint8_t *r, int st, int q, int) {
@@ -572,6 +597,7 @@ template <> struct MfsStage<MQ6K> {
     // super-tiles): ql 512 B, qh 256 B, scales 64 B (32 + 16 + 4 pieces), and
     // the super-tile's 16 bytes of d
     static constexpr int PR = 53;
+    __device__ static uint32_t row_bytes(int in_dim) { return (uint32_t)(in_dim >> 11) * 1680u; }
     __device__ static uint32_t off0(uint32_t row, int k, int in_dim) {
         const uint32_t base = row * (uint32_t)(in_dim >> 11) * 1680u;
         if (k < 32) return base + 16u * k;
@@ -594,8 +620,9 @@ template <> struct MfsStage<MQ6K> {
 };
 template <> struct MfsStage<MQ8> {
     static constexpr int PR = 69;  // 4 super-tiles x 272 B = 68 pieces + 1 pad
+    __device__ static uint32_t row_bytes(int in_dim) { return (uint32_t)(in_dim >> 8) * 272u; }
     __device__ static uint32_t off0(uint32_t row, int k, int in_dim) {
-        return row * (uint32_t)(in_dim >> 8) * 272u + 16u * (uint32_t)(k < 68 ? k : 0);
+        return k < 68 ? row * (uint32_t)(in_dim >> 8) * 272u + 16u * (uint32_t)k : kMfsNoPiece;
     }
     __device__ static uint32_t c_off(int c, int) { return (uint32_t)c * 1088u; }
     __device__ static void load(MQ8::W &v, const uint8_t *r, int st, int q, int) {
@@ -607,71 +634,91 @@ template <> struct MfsStage<MQ8> {
     }
 };
 
-template <class F> struct MfsGeo {
+template <class F, int NW = 4> struct MfsGeo {
+    static constexpr int THREADS = 64 * NW;
     static constexpr int PIECES = kMfsRows * MfsStage<F>::PR;
-    static constexpr int P = (PIECES + 255) / 256;  // DMA instructions per thread per chunk
-    static constexpr int BUF = P * 4096;
+    static constexpr int P = (PIECES + THREADS - 1) / THREADS;  // DMA instructions per thread per chunk
+    static constexpr int BUF = P * THREADS * 16;
     static constexpr int LDS = 2 * BUF;
 };
 
 // One workgroup's 32 rows from row0 of the matrix at w over chunks [c0, c0 +
-// nch) against the activation image xh (ntp token columns: 8, 16 or 32; with
-// 8, lanes of tokens 8..15 read past the resource, which returns zeros
-// without traffic); y[t * y_stride + o] = 2^-e_t * sum. smem: MfsGeo<F>::LDS
-// bytes.
-template <class F, int NT>
+// nch) against the activation image xh (ntp token columns: 8, 16 or 32);
+// y[t * y_stride + o] = 2^-e_t * sum. PACK (ntp = 8, NT = 1): lanes of A rows
+// 0..7 read the hi plane of tokens 0..7, lanes of rows 8..15 the lo plane.
+// NW wavefronts (64 NW threads) split each chunk's 8 steps, 8 / NW each.
+// smem: MfsGeo<F, NW>::LDS bytes.
+template <class F, int NT, bool PACK = false, int NW = 4>
 __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
                                          const _Float16 *__restrict__ xh, uint32_t plane_bytes,
                                          const float *__restrict__ unscale, float *__restrict__ y,
                                          int y_stride, int n_tok, int in_dim, int out_dim,
                                          int row0, int c0, int nch, int ntp, uint8_t *smem) {
     using S = MfsStage<F>;
-    using G = MfsGeo<F>;
+    using G = MfsGeo<F, NW>;
     constexpr int RT = kMfsRows / 16;
+    constexpr int SPW = (kMfsK / kMfStep) / NW;  // steps per wavefront per chunk
+    constexpr int TH = G::THREADS;
     const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, q = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // this thread's DMA pieces: piece g = p * 256 + tid is piece g % PR of
-    // row g / PR (rows past out_dim repeat the last; the pieces past the
-    // tile fill the buffer's tail with copies of piece 0)
+    // this thread's DMA pieces: piece g = p * TH + tid is piece g % PR of
+    // row g / PR (rows past out_dim repeat the last; slots past the tile
+    // read nothing)
     uint32_t o0[G::P];
     int pk[G::P];
 #pragma unroll
     for (int p = 0; p < G::P; p++) {
-        const int g = p * 256 + tid;
-        const int row = min(row0 + (g < G::PIECES ? g / S::PR : 0), out_dim - 1);
-        pk[p] = g < G::PIECES ? g % S::PR : 0;
-        o0[p] = S::off0((uint32_t)row, pk[p], in_dim);
+        const int g = p * TH + tid;
+        const int row = min(row0 + g / S::PR, out_dim - 1);
+        pk[p] = g % S::PR;
+        o0[p] = g < G::PIECES ? S::off0((uint32_t)row, pk[p], in_dim) : kMfsNoPiece;
     }
+    // The DMA of chunk c + 1 is issued on every pass, through a zero-size
+    // resource after the last chunk (no memory access; it fills the idle
+    // buffer with zeros): the compiler's vmcnt bookkeeping then sees the same
+    // count of loads in flight on every path, and the wait for this chunk's
+    // activations leaves the next chunk's weights in flight.
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)out_dim * S::row_bytes(in_dim));
     auto dma = [&](int c) {
         uint8_t *buf = smem + (c & 1) * G::BUF;
 #pragma unroll
         for (int p = 0; p < G::P; p++)
-            dma16(w + (o0[p] + S::c_off(c0 + c, pk[p])),
-                  (lds_void *)(buf + 16 * (p * 256 + 64 * wv)));
+            dma16b(rw, o0[p] == kMfsNoPiece ? kMfsNoPiece : o0[p] + S::c_off(c0 + c, pk[p]),
+                   (lds_void *)(buf + 16 * (p * TH + 64 * wv)));
     };
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(xh, 2 * plane_bytes);
-    uint4 xr[2][4][NT], lr[2][4][NT];
+    uint4 xr[SPW][4][NT], lr[SPW][4][NT];
     f32x4 acc[RT][NT];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) acc[rt][nt] = {0.f, 0.f, 0.f, 0.f};
-    dma(0);
-    for (int c = 0; c < nch; c++) {
+    // One pass per chunk; every pass but the last issues the next chunk's
+    // DMA. PACK: the last pass is a copy without it, so within each copy the
+    // count of loads in flight is fixed and the compiler's waits for this
+    // chunk's activations leave the next chunk's weights in flight (a
+    // conditional DMA in one loop body makes it wait for everything). The
+    // wider kernels keep the conditional: the copy costs them registers.
+    auto pass = [&](int c, auto has_next) {
         // chunk c's pieces (every wavefront's) have landed, and chunk c - 1's
         // buffer is no longer read
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
-        // this chunk's activations first, then the next chunk's DMA: the
-        // waits for the activations then leave the DMA in flight
+        // this chunk's activations first, then the next chunk's DMA
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int st = (c0 + c) * (kMfsK / kMfStep) + 2 * wv + u;
+        for (int u = 0; u < SPW; u++) {
+            const int st = (c0 + c) * (kMfsK / kMfStep) + SPW * wv + u;
 #pragma unroll
             for (int j = 0; j < 4; j++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
+                    if (PACK) {
+                        xr[u][j][nt] = bload16(
+                            rx, (uint32_t)((((st * 4 + j) * 4 + q) * 8 + (r16 & 7)) * 16) +
+                                    (r16 >= 8 ? plane_bytes : 0u), 0);
+                        continue;
+                    }
                     const int col = nt * 16 + r16;
                     const uint32_t o = col < ntp
                         ? (uint32_t)((((st * 4 + j) * 4 + q) * ntp + col) * 16) : 0x7FFFFFF0u;
@@ -680,17 +727,55 @@ __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
                 }
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (c + 1 < nch) dma(c + 1);
+        if constexpr (std::is_same<decltype(has_next), bool>::value) {
+            if (has_next) dma(c + 1);
+        } else if constexpr (decltype(has_next)::value) {
+            dma(c + 1);
+        }
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t *buf = smem + (c & 1) * G::BUF;
+        if constexpr (PACK && std::is_same<F, MQ6K>::value) {
+            // one test of the scales per chunk keeps the steps in one block,
+            // free to interleave
+            MQ6K::W wr[SPW][RT];
+            bool wl = false;
 #pragma unroll
-        for (int u = 0; u < 2; u++)
+            for (int u = 0; u < SPW; u++)
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) {
-                typename F::W wr;
-                S::load(wr, buf + (16 * rt + r16) * (S::PR * 16), 2 * wv + u, q, c0 + c);
-                F::template step<NT>(wr, q, xr[u], lr[u], acc[rt]);
+                for (int rt = 0; rt < RT; rt++) {
+                    S::load(wr[u][rt], buf + (16 * rt + r16) * (S::PR * 16), SPW * wv + u, q, c0 + c);
+                    wl = wl || MQ6K::wide_lane(wr[u][rt], q);
+                }
+            if (__ballot(wl) != 0) {
+#pragma unroll
+                for (int u = 0; u < SPW; u++)
+#pragma unroll
+                    for (int rt = 0; rt < RT; rt++)
+                        MQ6K::step_m<NT, 1, PACK>(wr[u][rt], q, xr[u], lr[u], acc[rt]);
+            } else {
+#pragma unroll
+                for (int u = 0; u < SPW; u++)
+#pragma unroll
+                    for (int rt = 0; rt < RT; rt++)
+                        MQ6K::step_m<NT, 0, PACK>(wr[u][rt], q, xr[u], lr[u], acc[rt]);
             }
+        } else {
+#pragma unroll
+            for (int u = 0; u < SPW; u++)
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++) {
+                    typename F::W wr;
+                    S::load(wr, buf + (16 * rt + r16) * (S::PR * 16), SPW * wv + u, q, c0 + c);
+                    F::template step<NT, PACK>(wr, q, xr[u], lr[u], acc[rt]);
+                }
+        }
+    };
+    dma(0);
+    if constexpr (PACK) {
+        for (int c = 0; c + 1 < nch; c++) pass(c, std::true_type{});
+        pass(nch - 1, std::false_type{});
+    } else {
+        for (int c = 0; c < nch; c++) pass(c, c + 1 < nch);
     }
     __syncthreads();
     f32x4 *red = reinterpret_cast<f32x4 *>(smem);
@@ -699,11 +784,17 @@ __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) red[((wv * RT + rt) * NT + nt) * 64 + lane] = acc[rt][nt];
     __syncthreads();
-    for (int e = tid; e < RT * NT * 64; e += 256) {
+    for (int e = tid; e < RT * NT * 64; e += TH) {
         const int rt = e / (NT * 64), nt = (e / 64) % NT, ln = e % 64;
+        if (PACK && ln >= 32) continue;
         f32x4 v = red[(rt * NT + nt) * 64 + ln];
 #pragma unroll
-        for (int k = 1; k < 4; k++) v += red[((k * RT + rt) * NT + nt) * 64 + ln];
+        for (int k = 1; k < NW; k++) v += red[((k * RT + rt) * NT + nt) * 64 + ln];
+        if (PACK) {
+            // D rows 8..15 (lanes 32..63): the lo plane of the same tokens
+#pragma unroll
+            for (int k = 0; k < NW; k++) v += red[((k * RT + rt) * NT + nt) * 64 + ln + 32];
+        }
         // D: tokens 4 (lane / 16) + 0..3 of weight row lane % 16
         const int o = row0 + 16 * rt + (ln & 15);
         const int t0 = nt * 16 + 4 * (ln >> 4);
@@ -717,8 +808,8 @@ __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
 
 // Grid (32-row blocks, K splits): split y of sk = gridDim.y takes an equal
 // run of chunks and writes y + split * n_tok * out_dim.
-template <class F, int NT>
-__global__ __launch_bounds__(256) void k_gemv_mfs(const uint8_t *__restrict__ w,
+template <class F, int NT, bool PACK = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void k_gemv_mfs(const uint8_t *__restrict__ w,
                                                   const _Float16 *__restrict__ xh,
                                                   uint32_t plane_bytes,
                                                   const float *__restrict__ unscale,
@@ -728,8 +819,9 @@ __global__ __launch_bounds__(256) void k_gemv_mfs(const uint8_t *__restrict__ w,
     const int nall = in_dim / kMfsK;
     const int c0 = nall * (int)blockIdx.y / (int)gridDim.y;
     const int nch = nall * ((int)blockIdx.y + 1) / (int)gridDim.y - c0;
-    mfs_rows<F, NT>(w, xh, plane_bytes, unscale, y + (size_t)blockIdx.y * n_tok * out_dim, out_dim,
-                    n_tok, in_dim, out_dim, (int)blockIdx.x * kMfsRows, c0, nch, ntp, smem);
+    mfs_rows<F, NT, PACK, NW>(w, xh, plane_bytes, unscale, y + (size_t)blockIdx.y * n_tok * out_dim,
+                          out_dim, n_tok, in_dim, out_dim, (int)blockIdx.x * kMfsRows, c0, nch, ntp,
+                          smem);
 }
 
 // y[i] = part[0][i] + part[1][i] + ... + part[sk - 1][i], in split order.
@@ -1203,19 +1295,27 @@ static hipError_t mfs_go(const uint8_t *w, const float *x, uint8_t *scratch, flo
     float *unscale = reinterpret_cast<float *>(scratch + al(2 * plane_bytes));
     float *part = reinterpret_cast<float *>(scratch + al(2 * plane_bytes) + al((size_t)ntp * 4));
     constexpr int lds = MfsGeo<F>::LDS;
+    constexpr int lds8 = MfsGeo<F, kMfsPackWaves>::LDS;
     // the attribute once per kernel (thread-safe static initialisation)
     static const hipError_t attr1 = hipFuncSetAttribute(
         reinterpret_cast<const void *>(&k_gemv_mfs<F, 1>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     static const hipError_t attr2 = hipFuncSetAttribute(
         reinterpret_cast<const void *>(&k_gemv_mfs<F, 2>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    static const hipError_t attr3 = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&k_gemv_mfs<F, 1, true, kMfsPackWaves>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, lds8);
     if (attr1 != hipSuccess) return attr1;
     if (attr2 != hipSuccess) return attr2;
+    if (attr3 != hipSuccess) return attr3;
     k_mf_x<F><<<(unsigned)ntp, kMfxThreads, 0, s>>>(x, xh, unscale, n_tok, in_dim, ntp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 grid((unsigned)((out_dim + kMfsRows - 1) / kMfsRows), (unsigned)sk);
     float *dst = sk > 1 ? part : y;
-    if (ntp <= 16)
+    if (ntp == 8)
+        k_gemv_mfs<F, 1, true, kMfsPackWaves><<<grid, 64 * kMfsPackWaves, lds8, s>>>(
+            w, xh, (uint32_t)plane_bytes, unscale, dst, n_tok, in_dim, out_dim, ntp);
+    else if (ntp == 16)
         k_gemv_mfs<F, 1><<<grid, 256, lds, s>>>(w, xh, (uint32_t)plane_bytes, unscale, dst, n_tok,
                                                 in_dim, out_dim, ntp);
     else
