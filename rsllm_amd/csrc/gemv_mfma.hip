@@ -458,8 +458,7 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
                                         const _Float16 *__restrict__ xh, uint32_t plane_bytes,
                                         const float *__restrict__ unscale, float *__restrict__ y,
                                         int n_tok, int in_dim, int out_dim, int y_stride, int row0,
-                                        f32x4 *red) {
-    constexpr int ntp = NT * 16;
+                                        f32x4 *red, int ntp) {
     const int lane = threadIdx.x & 63, r16 = lane & 15, q = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nsteps = in_dim / kMfStep;
@@ -483,9 +482,12 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
         for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                const uint32_t o = (uint32_t)((((s * 4 + j) * 4 + q) * ntp + nt * 16 + r16) * 16);
+                // image columns past ntp (ntp = 8): zeros, no access
+                const int col = nt * 16 + r16;
+                const uint32_t o = col < ntp
+                    ? (uint32_t)((((s * 4 + j) * 4 + q) * ntp + col) * 16) : 0x7FFFFFF0u;
                 xr[j][nt] = bload16(rx, o, 0);
-                lr[j][nt] = bload16(rx, o + plane_bytes, 0);
+                lr[j][nt] = bload16(rx, col < ntp ? o + plane_bytes : 0x7FFFFFF0u, 0);
             }
     };
     auto compute = [&](const typename F::W (&wr)[RT], const uint4 (&xr)[4][NT],
@@ -533,7 +535,7 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mf(const uint8_t *__restrict__
                                                      int out_dim) {
     __shared__ f32x4 red[NK * RT * NT * 64];
     mf_rows<F, NT, NK, RT>(w, w_bytes, xh, plane_bytes, unscale, y, n_tok, in_dim, out_dim, out_dim,
-                           blockIdx.x * 16 * RT, red);
+                           blockIdx.x * 16 * RT, red, NT * 16);
 }
 
 // ---- GEMV with the weights staged through LDS -------------------------------------
@@ -836,30 +838,28 @@ __global__ __launch_bounds__(256) void k_mfs_sum(const float *__restrict__ part,
 
 // ---- routed experts grouped by expert (many tokens) --------------------------------
 // Slots sorted by expert (moe.hip routing): expert e owns sorted slots [off[e],
-// off[e + 1]), cut into batches of up to kMfgBatch (k_moe_scan lists them);
-// a batch is the token set (the N dimension) of one pass of mf_rows over
-// that expert's rows, so each expert's weights are streamed once per
-// kMfgBatch of its slots. Batch b's activation image (two planes of
-// in_dim * kMfgBatch values, the k_mf_x layout with ntp = kMfgBatch) sits
-// at xh + 2 b in_dim kMfgBatch and its scales at unscale + b * kMfgBatch;
-// its rows go to y + first * out_dim.
+// off[e + 1]), cut into batches of up to bw = 8 or 16 (mfg_width; k_moe_scan
+// lists them); a batch is the token set (the N dimension) of one pass over
+// that expert's rows, so each expert's weights are streamed once per bw of
+// its slots. Batch b's activation image (two planes of in_dim * bw values,
+// the k_mf_x layout with ntp = bw) sits at xh + 2 b in_dim bw and its scales
+// at unscale + b * bw; its rows go to y + first * out_dim.
 
-// One token column of a kMfgBatch-wide activation image (the k_mf_x
-// conversion, one workgroup of kMfxThreads threads, the row read once when
-// it fits in registers): val4(i) gives elements i .. i + 3 of the column's
-// row; the column's pieces go to both planes of the image at xb, 2^-e to
-// *us.
+// One token column of an ntp-wide activation image (the k_mf_x conversion,
+// one workgroup of kMfxThreads threads, the row read once when it fits in
+// registers): val4(i) gives elements i .. i + 3 of the column's row; the
+// column's pieces go to both planes of the image at xb, 2^-e to *us.
 template <class F, class V>
 __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 *__restrict__ xb,
-                                            float *__restrict__ us) {
+                                            float *__restrict__ us, int ntp) {
     __shared__ float red[kMfxThreads / 64];
     const int tid = threadIdx.x;
     const int n8 = in_dim / 8;
-    const size_t plane = (size_t)in_dim * kMfgBatch;
+    const size_t plane = (size_t)in_dim * ntp;
     auto store = [&](int i, const uint4 &hi, const uint4 &lo) {
         int s, j, q;
         F::piece(8 * i, s, j, q);
-        const size_t slot = ((size_t)(s * 4 + j) * 4 + q) * kMfgBatch + t;
+        const size_t slot = ((size_t)(s * 4 + j) * 4 + q) * ntp + t;
         *reinterpret_cast<uint4 *>(xb + slot * 8) = hi;
         *reinterpret_cast<uint4 *>(xb + plane + slot * 8) = lo;
     };
@@ -914,7 +914,7 @@ __global__ __launch_bounds__(kMfxThreads) void k_mfg_x(const float *__restrict__
                                                const MfgBatch *__restrict__ bat,
                                                const int *__restrict__ n_bat, float clamp,
                                                _Float16 *__restrict__ xh,
-                                               float *__restrict__ unscale, int in_dim) {
+                                               float *__restrict__ unscale, int in_dim, int bw) {
     const int b = blockIdx.y, t = blockIdx.x;
     if (b >= *n_bat) return;
     const MfgBatch bt = bat[b];
@@ -931,8 +931,8 @@ __global__ __launch_bounds__(kMfxThreads) void k_mfg_x(const float *__restrict__
         }
         return v;
     };
-    mf_x_column<F>(val4, in_dim, t, xh + (size_t)b * 2 * in_dim * kMfgBatch,
-                   unscale + (size_t)b * kMfgBatch + t);
+    mf_x_column<F>(val4, in_dim, t, xh + (size_t)b * 2 * in_dim * bw, unscale + (size_t)b * bw + t,
+                   bw);
 }
 
 // ---- grouped LoRA-down on the matrix cores ----------------------------------------
@@ -948,7 +948,7 @@ __global__ __launch_bounds__(kMfxThreads) void k_mfl_x(const float *__restrict__
     const float *xt = x + (size_t)tc * x_stride + (size_t)g * D;
     auto val4 = [&](int i) { return *reinterpret_cast<const float4 *>(xt + i); };
     mf_x_column<F>(val4, D, blockIdx.x, xh + (size_t)b * 2 * D * kMfgBatch,
-                   unscale + (size_t)b * kMfgBatch + blockIdx.x);
+                   unscale + (size_t)b * kMfgBatch + blockIdx.x, kMfgBatch);
 }
 
 // Grid (G R / 64, chunks): workgroup (x, c) computes rows 64 x .. 64 x + 63
@@ -968,7 +968,7 @@ __global__ __launch_bounds__(256) void k_gemv_mfl(const uint8_t *__restrict__ w,
     mf_rows<F, kMfgBatch / 16, NK, RT>(w, w_bytes, xh + b * 2 * img, (uint32_t)(img * 2),
                                        unscale + (size_t)b * kMfgBatch, y + (size_t)t0 * y_stride,
                                        min(kMfgBatch, n_tok - t0), D, out_dim, y_stride, row0,
-                                       red);
+                                       red, kMfgBatch);
 }
 
 // Grid (row blocks, batch slots, matrices): workgroup (x, b, m) computes
@@ -983,26 +983,27 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mfg(const uint8_t *__restrict_
                                                       const MfgBatch *__restrict__ bat,
                                                       const int *__restrict__ n_bat,
                                                       float *__restrict__ y0, float *__restrict__ y1,
-                                                      int in_dim, int out_dim) {
-    __shared__ f32x4 red[NK * RT * (kMfgBatch / 16) * 64];
+                                                      int in_dim, int out_dim, int bw) {
+    __shared__ f32x4 red[NK * RT * 64];
     const int b = blockIdx.y;
     if (b >= *n_bat) return;
     const MfgBatch bt = bat[b];
     const bool m1 = blockIdx.z != 0;
     const uint8_t *w = (m1 ? w1 : w0) + (size_t)bt.expert * w_stride;
     float *y = (m1 ? y1 : y0) + (size_t)bt.first * out_dim;
-    const size_t img = (size_t)in_dim * kMfgBatch;  // values per plane
-    mf_rows<F, kMfgBatch / 16, NK, RT>(w, (uint32_t)w_stride, xh + b * 2 * img, (uint32_t)(img * 2),
-                                       unscale + (size_t)b * kMfgBatch, y, bt.count, in_dim,
-                                       out_dim, out_dim, blockIdx.x * 16 * RT, red);
+    const size_t img = (size_t)in_dim * bw;  // values per plane
+    mf_rows<F, 1, NK, RT>(w, (uint32_t)w_stride, xh + b * 2 * img, (uint32_t)(img * 2),
+                          unscale + (size_t)b * bw, y, bt.count, in_dim, out_dim, out_dim,
+                          blockIdx.x * 16 * RT, red, bw);
 }
 
 // The grouped GEMV with its weights staged through LDS (mfs_rows): grid
 // (32-row blocks, batch slots, matrices); workgroup (x, b, m) computes rows
 // 32 x of W_m[expert(b)] for batch b's slots into y_m. Batch slots past
-// *n_bat exit at once.
-template <class F>
-__global__ __launch_bounds__(256) void k_gemv_mfgs(const uint8_t *__restrict__ w0,
+// *n_bat exit at once. PACK: 8-slot batches on the packed kernel (8
+// wavefronts); else 16-slot batches (4 wavefronts).
+template <class F, bool PACK>
+__global__ __launch_bounds__(PACK ? 64 * kMfsPackWaves : 256) void k_gemv_mfgs(const uint8_t *__restrict__ w0,
                                                    const uint8_t *__restrict__ w1,
                                                    size_t w_stride,
                                                    const _Float16 *__restrict__ xh,
@@ -1018,11 +1019,11 @@ __global__ __launch_bounds__(256) void k_gemv_mfgs(const uint8_t *__restrict__ w
     const bool m1 = blockIdx.z != 0;
     const uint8_t *w = (m1 ? w1 : w0) + (size_t)bt.expert * w_stride;
     float *y = (m1 ? y1 : y0) + (size_t)bt.first * out_dim;
-    const size_t img = (size_t)in_dim * kMfgBatch;  // values per plane
-    mfs_rows<F, kMfgBatch / 16>(w, xh + b * 2 * img, (uint32_t)(img * 2),
-                                unscale + (size_t)b * kMfgBatch, y, out_dim, bt.count, in_dim,
-                                out_dim, (int)blockIdx.x * kMfsRows, 0, in_dim / kMfsK,
-                                kMfgBatch, smem);
+    constexpr int bw = PACK ? 8 : kMfgBatch;
+    const size_t img = (size_t)in_dim * bw;  // values per plane
+    mfs_rows<F, 1, PACK, PACK ? kMfsPackWaves : 4>(
+        w, xh + b * 2 * img, (uint32_t)(img * 2), unscale + (size_t)b * bw, y, out_dim, bt.count,
+        in_dim, out_dim, (int)blockIdx.x * kMfsRows, 0, in_dim / kMfsK, bw, smem);
 }
 
 // ---- fused batched GEMV: activations converted into LDS ------------------------------
@@ -1385,49 +1386,61 @@ bool moe_mfma_supported(uint32_t dt_gu, uint32_t dt_d, int n_embd, int n_ff) {
 }
 
 size_t moe_mfma_scratch_bytes(int n_pairs, int n_expert, int n_embd, int n_ff) {
-    const size_t nb = (size_t)mfg_max_batches(n_pairs, n_expert);
+    const int bw = mfg_width(n_pairs, n_expert);
+    const size_t nb = (size_t)mfg_max_batches(n_pairs, n_expert, bw);
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
-    return mfg_batch_bytes(n_pairs, n_expert) + al(nb * kMfgBatch * (size_t)n_embd * 4) +
-           al(nb * kMfgBatch * 4) + al(nb * kMfgBatch * (size_t)n_ff * 4) + al(nb * kMfgBatch * 4);
+    return mfg_batch_bytes(n_pairs, n_expert, bw) + al(nb * bw * (size_t)n_embd * 4) +
+           al(nb * bw * 4) + al(nb * bw * (size_t)n_ff * 4) + al(nb * bw * 4);
 }
 
 template <class F>
 static hipError_t mfg_pass(const uint8_t *w0, const uint8_t *w1, size_t w_stride, const float *x,
                            const float *hu, const int *tok, const MfgBatch *bat, const int *n_bat,
                            int max_b, float clamp, _Float16 *xh, float *us, float *y0, float *y1,
-                           int in_dim, int out_dim, hipStream_t s) {
-    const dim3 gx(kMfgBatch, (unsigned)max_b);
+                           int in_dim, int out_dim, int bw, hipStream_t s) {
+    const dim3 gx((unsigned)bw, (unsigned)max_b);
     if (hu)
-        k_mfg_x<F, true><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim);
+        k_mfg_x<F, true><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
     else
-        k_mfg_x<F, false><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim);
+        k_mfg_x<F, false><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // weights staged through LDS where the layout allows (16-byte aligned
     // expert matrices, in_dim a multiple of 1024, of 2048 for Q6_K)
     if (mfs_splits<F>(in_dim, out_dim) > 0 &&
         (((uintptr_t)w0 | (uintptr_t)(w1 ? w1 : w0) | (uintptr_t)w_stride) & 15) == 0) {
-        constexpr int lds = MfsGeo<F>::LDS;
-        static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&k_gemv_mfgs<F>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-        if (attr != hipSuccess) return attr;
         const dim3 g((unsigned)((out_dim + kMfsRows - 1) / kMfsRows), (unsigned)max_b, w1 ? 2u : 1u);
-        k_gemv_mfgs<F><<<g, 256, lds, s>>>(w0, w1, w_stride, xh, us, bat, n_bat, y0, y1, in_dim,
-                                           out_dim);
+        if (bw == 8) {
+            constexpr int lds = MfsGeo<F, kMfsPackWaves>::LDS;
+            static const hipError_t attr =
+                hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_mfgs<F, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+            if (attr != hipSuccess) return attr;
+            k_gemv_mfgs<F, true><<<g, 64 * kMfsPackWaves, lds, s>>>(w0, w1, w_stride, xh, us, bat,
+                                                                    n_bat, y0, y1, in_dim, out_dim);
+        } else {
+            constexpr int lds = MfsGeo<F>::LDS;
+            static const hipError_t attr =
+                hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_mfgs<F, false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+            if (attr != hipSuccess) return attr;
+            k_gemv_mfgs<F, false><<<g, 256, lds, s>>>(w0, w1, w_stride, xh, us, bat, n_bat, y0, y1,
+                                                      in_dim, out_dim);
+        }
         return hipGetLastError();
     }
     constexpr int NK = 4, RT = 4;
     const dim3 g((unsigned)((out_dim + 16 * RT - 1) / (16 * RT)), (unsigned)max_b, w1 ? 2u : 1u);
     k_gemv_mfg<F, NK, RT><<<g, 64 * NK, 0, s>>>(w0, w1, w_stride, xh, us, bat, n_bat, y0, y1,
-                                                in_dim, out_dim);
+                                                in_dim, out_dim, bw);
     return hipGetLastError();
 }
 
 static hipError_t mfg_pass_dt(uint32_t dt, const uint8_t *w0, const uint8_t *w1, size_t w_stride,
                               const float *x, const float *hu, const int *tok, const MfgBatch *bat,
                               const int *n_bat, int max_b, float clamp, _Float16 *xh, float *us,
-                              float *y0, float *y1, int in_dim, int out_dim, hipStream_t s) {
-#define MFG(F) mfg_pass<F>(w0, w1, w_stride, x, hu, tok, bat, n_bat, max_b, clamp, xh, us, y0, y1, in_dim, out_dim, s)
+                              float *y0, float *y1, int in_dim, int out_dim, int bw, hipStream_t s) {
+#define MFG(F) mfg_pass<F>(w0, w1, w_stride, x, hu, tok, bat, n_bat, max_b, clamp, xh, us, y0, y1, in_dim, out_dim, bw, s)
     switch (dt) {
     case T_Q4_K: return MFG(MQ4K);
     case T_Q6_K: return MFG(MQ6K);
@@ -1444,23 +1457,24 @@ hipError_t launch_moe_mfma(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
                            uint8_t *scratch, int n_embd, int n_ff, float clamp, hipStream_t s) {
     if (!moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff)) return hipErrorInvalidValue;
     if (gu_stride > 0xFFFFFFFFu || d_stride > 0xFFFFFFFFu) return hipErrorInvalidValue;
-    const int max_b = mfg_max_batches(n_pairs, n_expert);
-    uint8_t *p = scratch + mfg_batch_bytes(n_pairs, n_expert);
+    const int bw = mfg_width(n_pairs, n_expert);  // as the routing that listed the batches
+    const int max_b = mfg_max_batches(n_pairs, n_expert, bw);
+    uint8_t *p = scratch + mfg_batch_bytes(n_pairs, n_expert, bw);
     auto take = [&](size_t n) {
         uint8_t *r = p;
         p += (n + 255) / 256 * 256;
         return r;
     };
-    _Float16 *xh1 = reinterpret_cast<_Float16 *>(take((size_t)max_b * kMfgBatch * n_embd * 4));
-    float *us1 = reinterpret_cast<float *>(take((size_t)max_b * kMfgBatch * 4));
-    _Float16 *xh2 = reinterpret_cast<_Float16 *>(take((size_t)max_b * kMfgBatch * n_ff * 4));
-    float *us2 = reinterpret_cast<float *>(take((size_t)max_b * kMfgBatch * 4));
+    _Float16 *xh1 = reinterpret_cast<_Float16 *>(take((size_t)max_b * bw * n_embd * 4));
+    float *us1 = reinterpret_cast<float *>(take((size_t)max_b * bw * 4));
+    _Float16 *xh2 = reinterpret_cast<_Float16 *>(take((size_t)max_b * bw * n_ff * 4));
+    float *us2 = reinterpret_cast<float *>(take((size_t)max_b * bw * 4));
     hipError_t e;
     if ((e = mfg_pass_dt(dt_gu, gate, up, gu_stride, x, nullptr, slot_tok, bat, n_bat, max_b, 0.f,
-                         xh1, us1, hg, hu, n_embd, n_ff, s)) != hipSuccess)
+                         xh1, us1, hg, hu, n_embd, n_ff, bw, s)) != hipSuccess)
         return e;
     return mfg_pass_dt(dt_d, down, nullptr, d_stride, hg, hu, nullptr, bat, n_bat, max_b, clamp,
-                       xh2, us2, yd, nullptr, n_ff, n_embd, s);
+                       xh2, us2, yd, nullptr, n_ff, n_embd, bw, s);
 }
 
 bool lora_mfma_supported(uint32_t dtype, int n_tok, int D, int G, int R) {

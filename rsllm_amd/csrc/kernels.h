@@ -136,19 +136,26 @@ hipError_t launch_quantize_swiglu(uint32_t dtype, const float *hg, const float *
 // and yd [slot x n_embd] (down of the clamped SwiGLU of hg, hu). `scratch`
 // holds moe_mfma_scratch_bytes(n_pairs, n_expert, n_embd, n_ff) bytes.
 // The batches: each active expert's sorted slots cut into runs of up to
-// kMfgBatch (experts ascending, runs in slot order), *n_bat of them, as
-// k_moe_scan lists them; at most mfg_max_batches(n_pairs, n_expert).
-// `scratch` holds moe_mfma_scratch_bytes(...) bytes: the batch list and its
-// count first (mfg_batch_bytes), then the activation images.
+// mfg_width(n_pairs, n_expert) (experts ascending, runs in slot order),
+// *n_bat of them, as k_moe_scan lists them; at most mfg_max_batches(n_pairs,
+// n_expert, width). `scratch` holds moe_mfma_scratch_bytes(...) bytes: the
+// batch list and its count first (mfg_batch_bytes), then the activation
+// images.
 constexpr int kMfgBatch = 16;
 struct MfgBatch {
     int first, count, expert, pad;
 };
-inline int mfg_max_batches(int n_pairs, int n_expert) {
-    return (n_pairs + kMfgBatch - 1) / kMfgBatch + (n_pairs < n_expert ? n_pairs : n_expert);
+// Batch width of the grouped routed-expert route: 8 slots (the packed
+// 8-column kernel) when the experts average at most 8 slots, else 16.
+inline int mfg_width(int n_pairs, int n_expert) {
+    return (long long)n_pairs <= 8LL * n_expert ? 8 : kMfgBatch;
 }
-inline size_t mfg_batch_bytes(int n_pairs, int n_expert) {
-    return ((size_t)mfg_max_batches(n_pairs, n_expert) * sizeof(MfgBatch) + 255) / 256 * 256 + 256;
+inline int mfg_max_batches(int n_pairs, int n_expert, int width) {
+    return (n_pairs + width - 1) / width + (n_pairs < n_expert ? n_pairs : n_expert);
+}
+inline size_t mfg_batch_bytes(int n_pairs, int n_expert, int width) {
+    return ((size_t)mfg_max_batches(n_pairs, n_expert, width) * sizeof(MfgBatch) + 255) / 256 * 256 +
+           256;
 }
 bool moe_mfma_supported(uint32_t dt_gu, uint32_t dt_d, int n_embd, int n_ff);
 size_t moe_mfma_scratch_bytes(int n_pairs, int n_expert, int n_embd, int n_ff);

@@ -9,7 +9,7 @@
 // (token, slot) pairs are grouped by expert on the device, and each expert's
 // gate/up and down matrices are streamed once per batch of up to 4 of its
 // tokens (grouped GEMV, gemv.hip; for Q4_K experts from kMoeMfmaMinTok
-// tokens, batches of up to 16 on the matrix cores instead, launch_moe_mfma
+// tokens, batches of up to 8 or 16 on the matrix cores instead, launch_moe_mfma
 // in gemv_mfma.hip, steps 2-6 there):
 //   1. routing (k_moe_hist, k_moe_scan, k_moe_scatter, any number of
 //      pairs): slots sorted by expert (ties in (t, i) order), per-expert
@@ -100,15 +100,15 @@ __device__ int scan_inplace(int *__restrict__ v, size_t n, int *part) {
 
 // One workgroup: hist -> bases (in place); off[e] (n_expert + 1 entries);
 // the active experts in ascending order (act, *n_act); and, when bat is
-// given, each active expert's slots cut into batches of up to kMfgBatch
-// (experts ascending, batches in slot order; *n_bat of them). `flags` holds
-// n_expert + 1 ints of workspace.
+// given, each active expert's slots cut into batches of up to bw (experts
+// ascending, batches in slot order; *n_bat of them). `flags` holds n_expert
+// + 1 ints of workspace.
 __global__ __launch_bounds__(kScanThreads) void k_moe_scan(int *__restrict__ hist, int nblk,
                                                            int n_expert, int *__restrict__ off,
                                                            int *__restrict__ act,
                                                            int *__restrict__ n_act,
                                                            MfgBatch *__restrict__ bat,
-                                                           int *__restrict__ n_bat,
+                                                           int *__restrict__ n_bat, int bw,
                                                            int *__restrict__ flags) {
     __shared__ int part[kScanThreads];
     const int tid = threadIdx.x;
@@ -131,17 +131,17 @@ __global__ __launch_bounds__(kScanThreads) void k_moe_scan(int *__restrict__ his
     if (tid == 0) *n_act = na;
     if (!bat) return;
     __syncthreads();
-    // batches: positions from a scan of ceil(count / kMfgBatch)
+    // batches: positions from a scan of ceil(count / bw)
     for (int e = tid; e < n_expert; e += kScanThreads) {
         const int c = off[e + 1] - off[e];
-        flags[e] = (c + kMfgBatch - 1) / kMfgBatch;
+        flags[e] = (c + bw - 1) / bw;
     }
     __syncthreads();
     const int nb = scan_inplace(flags, (size_t)n_expert, part);
     for (int e = tid; e < n_expert; e += kScanThreads) {
         const int c = off[e + 1] - off[e];
-        for (int f = 0, j = flags[e]; f < c; f += kMfgBatch, j++)
-            bat[j] = MfgBatch{off[e] + f, c - f < kMfgBatch ? c - f : kMfgBatch, e, 0};
+        for (int f = 0, j = flags[e]; f < c; f += bw, j++)
+            bat[j] = MfgBatch{off[e] + f, c - f < bw ? c - f : bw, e, 0};
     }
     if (tid == 0) *n_bat = nb;
 }
@@ -176,7 +176,7 @@ static size_t moe_route_work_bytes(int n_pairs, int n_expert) {
 static hipError_t launch_moe_route(const int *ids, const float *wts, int n_pairs, int k,
                                    int n_expert, uint8_t *work, int *off, int *slot_tok,
                                    int *slot_of, int *act, int *n_act, MfgBatch *bat, int *n_bat,
-                                   hipStream_t s) {
+                                   int bw, hipStream_t s) {
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
     const int nblk = route_blocks(n_pairs);
     int *hist = reinterpret_cast<int *>(work);
@@ -187,7 +187,7 @@ static hipError_t launch_moe_route(const int *ids, const float *wts, int n_pairs
                                                                           n_expert, hist, rank);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_moe_scan<<<1, kScanThreads, 0, s>>>(hist, nblk, n_expert, off, act, n_act, bat, n_bat,
+    k_moe_scan<<<1, kScanThreads, 0, s>>>(hist, nblk, n_expert, off, act, n_act, bat, n_bat, bw,
                                           flags);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     k_moe_scatter<<<(unsigned)nblk, kRouteBlock, 0, s>>>(ids, wts, n_pairs, k, n_expert, hist,
@@ -742,9 +742,10 @@ static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
     if (mfma) {
         uint8_t *mscratch = take(moe_mfma_scratch_bytes((int)P, n_expert, n_embd, n_ff));
         MfgBatch *bat = reinterpret_cast<MfgBatch *>(mscratch);
-        int *n_bat = reinterpret_cast<int *>(mscratch + mfg_batch_bytes((int)P, n_expert) - 256);
+        const int bw = mfg_width((int)P, n_expert);
+        int *n_bat = reinterpret_cast<int *>(mscratch + mfg_batch_bytes((int)P, n_expert, bw) - 256);
         hipError_t e = launch_moe_route(ids, wts, (int)P, k, n_expert, route_work, off, slot_tok,
-                                        slot_of, act, n_act, bat, n_bat, s);
+                                        slot_of, act, n_act, bat, n_bat, bw, s);
         if (e != hipSuccess) return e;
         if ((e = launch_moe_mfma(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x, slot_tok,
                                  bat, n_bat, (int)P, n_expert, hg, hu, yd, mscratch, n_embd, n_ff,
@@ -777,7 +778,7 @@ static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
     // at most min(n_expert, n_tok * k) experts are active
     const int grid_experts = (int)(P < (size_t)n_expert ? P : (size_t)n_expert);
     hipError_t e = launch_moe_route(ids, wts, (int)P, k, n_expert, route_work, off, slot_tok,
-                                    slot_of, act, n_act, nullptr, nullptr, s);
+                                    slot_of, act, n_act, nullptr, nullptr, 0, s);
     if (e != hipSuccess) return e;
     if ((e = launch_quantize_x(dt_gu, x, xq1, n_tok, n_embd, s)) != hipSuccess) return e;
     if ((e = launch_gemv_grouped(dt_gu, gate, up, gu_stride, xq1, xq1_bytes, off, slot_tok, act,
