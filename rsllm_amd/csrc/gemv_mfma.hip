@@ -217,7 +217,9 @@ struct MQ6K {
         const int il = (int)(int8_t)(w.sl >> (8 * q)), ih = (int)(int8_t)(w.sh >> (8 * q));
         const _Float16 scl = (_Float16)(float)il, sch = (_Float16)(float)ih;
         const bool wide = WIDE == 1 || (WIDE == 2 && __ballot(wide_lane(w, q)) != 0);
-        const uint32_t shl = 2u * (uint32_t)(q >> 1), shh = 4u + shl;
+        // the high bit pairs sit at bits 2 (q >> 1) (low nibbles) and 4 + 2 (q >> 1)
+        // (high nibbles) of each qh byte; one shift puts either pair at bits 4, 5
+        const uint32_t shl = 2u * (uint32_t)(q >> 1), sup = 4u - shl;
         const uint32_t l[4] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w};
         const uint32_t hb[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
         f16x8 a[4], b[4];
@@ -229,7 +231,7 @@ struct MQ6K {
 #pragma unroll
             for (int u = 0; u < 2; u++) {
                 const uint32_t nib = hi ? (l[p + u] >> 4) & 0x0F0F0F0Fu : l[p + u] & 0x0F0F0F0Fu;
-                const uint32_t top = ((hb[p + u] >> (hi ? shh : shl)) & 0x03030303u) << 4;
+                const uint32_t top = (hi ? hb[p + u] >> shl : hb[p + u] << sup) & 0x30303030u;
                 q6x4_f16(nib | top, v[2 * u], v[2 * u + 1]);
             }
             f16x8 r;
