@@ -576,6 +576,10 @@ __device__ __forceinline__ void dma16b(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
 constexpr int kMfsRows = 32;
 constexpr int kMfsK = 1024;
 constexpr int kMfsPackWaves = 8;  // wavefronts per workgroup of the packed kernel
+// rows per workgroup of the grouped Q4_K kernel with 8-slot batches (64:
+// the batch's activation image is read once per 64 rows, and two 80 KB
+// workgroups still fit a CU; C3 T = 32: 468 -> 441 us per call)
+constexpr int kMfgPackRowsQ4K = 64;
 constexpr uint32_t kMfsNoPiece = 0xFFFFFFF0u;  // past every resource: zeros, no access
 
 // Per format: PR 16-byte pieces per row chunk (one pad piece where needed for
@@ -638,29 +642,29 @@ template <> struct MfsStage<MQ8> {
     }
 };
 
-template <class F, int NW = 4> struct MfsGeo {
+template <class F, int NW = 4, int ROWS = kMfsRows> struct MfsGeo {
     static constexpr int THREADS = 64 * NW;
-    static constexpr int PIECES = kMfsRows * MfsStage<F>::PR;
+    static constexpr int PIECES = ROWS * MfsStage<F>::PR;
     static constexpr int P = (PIECES + THREADS - 1) / THREADS;  // DMA instructions per thread per chunk
     static constexpr int BUF = P * THREADS * 16;
     static constexpr int LDS = 2 * BUF;
 };
 
-// One workgroup's 32 rows from row0 of the matrix at w over chunks [c0, c0 +
-// nch) against the activation image xh (ntp token columns: 8, 16 or 32);
-// y[t * y_stride + o] = 2^-e_t * sum. PACK (ntp = 8, NT = 1): lanes of A rows
-// 0..7 read the hi plane of tokens 0..7, lanes of rows 8..15 the lo plane.
-// NW wavefronts (64 NW threads) split each chunk's 8 steps, 8 / NW each.
-// smem: MfsGeo<F, NW>::LDS bytes.
-template <class F, int NT, bool PACK = false, int NW = 4>
+// One workgroup's ROWS rows (32 or 64) from row0 of the matrix at w over
+// chunks [c0, c0 + nch) against the activation image xh (ntp token columns:
+// 8, 16 or 32); y[t * y_stride + o] = 2^-e_t * sum. PACK (ntp = 8, NT = 1):
+// lanes of A rows 0..7 read the hi plane of tokens 0..7, lanes of rows 8..15
+// the lo plane. NW wavefronts (64 NW threads) split each chunk's 8 steps,
+// 8 / NW each, for every row tile. smem: MfsGeo<F, NW, ROWS>::LDS bytes.
+template <class F, int NT, bool PACK = false, int NW = 4, int ROWS = kMfsRows>
 __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
                                          const _Float16 *__restrict__ xh, uint32_t plane_bytes,
                                          const float *__restrict__ unscale, float *__restrict__ y,
                                          int y_stride, int n_tok, int in_dim, int out_dim,
                                          int row0, int c0, int nch, int ntp, uint8_t *smem) {
     using S = MfsStage<F>;
-    using G = MfsGeo<F, NW>;
-    constexpr int RT = kMfsRows / 16;
+    using G = MfsGeo<F, NW, ROWS>;
+    constexpr int RT = ROWS / 16;
     constexpr int SPW = (kMfsK / kMfStep) / NW;  // steps per wavefront per chunk
     constexpr int TH = G::THREADS;
     const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, q = lane >> 4;
@@ -677,11 +681,6 @@ __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
         pk[p] = g % S::PR;
         o0[p] = g < G::PIECES ? S::off0((uint32_t)row, pk[p], in_dim) : kMfsNoPiece;
     }
-    // The DMA of chunk c + 1 is issued on every pass, through a zero-size
-    // resource after the last chunk (no memory access; it fills the idle
-    // buffer with zeros): the compiler's vmcnt bookkeeping then sees the same
-    // count of loads in flight on every path, and the wait for this chunk's
-    // activations leaves the next chunk's weights in flight.
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)out_dim * S::row_bytes(in_dim));
     auto dma = [&](int c) {
         uint8_t *buf = smem + (c & 1) * G::BUF;
@@ -1000,11 +999,11 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mfg(const uint8_t *__restrict_
 }
 
 // The grouped GEMV with its weights staged through LDS (mfs_rows): grid
-// (32-row blocks, batch slots, matrices); workgroup (x, b, m) computes rows
-// 32 x of W_m[expert(b)] for batch b's slots into y_m. Batch slots past
-// *n_bat exit at once. PACK: 8-slot batches on the packed kernel (8
+// (ROWS-row blocks, batch slots, matrices); workgroup (x, b, m) computes
+// rows ROWS x of W_m[expert(b)] for batch b's slots into y_m. Batch slots
+// past *n_bat exit at once. PACK: 8-slot batches on the packed kernel (8
 // wavefronts); else 16-slot batches (4 wavefronts).
-template <class F, bool PACK>
+template <class F, bool PACK, int ROWS>
 __global__ __launch_bounds__(PACK ? 64 * kMfsPackWaves : 256) void k_gemv_mfgs(const uint8_t *__restrict__ w0,
                                                    const uint8_t *__restrict__ w1,
                                                    size_t w_stride,
@@ -1023,9 +1022,9 @@ __global__ __launch_bounds__(PACK ? 64 * kMfsPackWaves : 256) void k_gemv_mfgs(c
     float *y = (m1 ? y1 : y0) + (size_t)bt.first * out_dim;
     constexpr int bw = PACK ? 8 : kMfgBatch;
     const size_t img = (size_t)in_dim * bw;  // values per plane
-    mfs_rows<F, 1, PACK, PACK ? kMfsPackWaves : 4>(
+    mfs_rows<F, 1, PACK, PACK ? kMfsPackWaves : 4, ROWS>(
         w, xh + b * 2 * img, (uint32_t)(img * 2), unscale + (size_t)b * bw, y, out_dim, bt.count,
-        in_dim, out_dim, (int)blockIdx.x * kMfsRows, 0, in_dim / kMfsK, bw, smem);
+        in_dim, out_dim, (int)blockIdx.x * ROWS, 0, in_dim / kMfsK, bw, smem);
 }
 
 // ---- fused batched GEMV: activations converted into LDS ------------------------------
@@ -1411,23 +1410,28 @@ static hipError_t mfg_pass(const uint8_t *w0, const uint8_t *w1, size_t w_stride
     // expert matrices, in_dim a multiple of 1024, of 2048 for Q6_K)
     if (mfs_splits<F>(in_dim, out_dim) > 0 &&
         (((uintptr_t)w0 | (uintptr_t)(w1 ? w1 : w0) | (uintptr_t)w_stride) & 15) == 0) {
-        const dim3 g((unsigned)((out_dim + kMfsRows - 1) / kMfsRows), (unsigned)max_b, w1 ? 2u : 1u);
         if (bw == 8) {
-            constexpr int lds = MfsGeo<F, kMfsPackWaves>::LDS;
+            // Q4_K: 64-row blocks (each workgroup reads the batch's image once
+            // for twice the weight bytes); two still fit a CU
+            constexpr int rows = std::is_same<F, MQ4K>::value ? kMfgPackRowsQ4K : kMfsRows;
+            constexpr int lds = MfsGeo<F, kMfsPackWaves, rows>::LDS;
             static const hipError_t attr =
-                hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_mfgs<F, true>),
+                hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_mfgs<F, true, rows>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, lds);
             if (attr != hipSuccess) return attr;
-            k_gemv_mfgs<F, true><<<g, 64 * kMfsPackWaves, lds, s>>>(w0, w1, w_stride, xh, us, bat,
-                                                                    n_bat, y0, y1, in_dim, out_dim);
+            const dim3 g((unsigned)((out_dim + rows - 1) / rows), (unsigned)max_b, w1 ? 2u : 1u);
+            k_gemv_mfgs<F, true, rows><<<g, 64 * kMfsPackWaves, lds, s>>>(
+                w0, w1, w_stride, xh, us, bat, n_bat, y0, y1, in_dim, out_dim);
         } else {
             constexpr int lds = MfsGeo<F>::LDS;
             static const hipError_t attr =
-                hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_mfgs<F, false>),
+                hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_mfgs<F, false, kMfsRows>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, lds);
             if (attr != hipSuccess) return attr;
-            k_gemv_mfgs<F, false><<<g, 256, lds, s>>>(w0, w1, w_stride, xh, us, bat, n_bat, y0, y1,
-                                                      in_dim, out_dim);
+            const dim3 g((unsigned)((out_dim + kMfsRows - 1) / kMfsRows), (unsigned)max_b,
+                         w1 ? 2u : 1u);
+            k_gemv_mfgs<F, false, kMfsRows><<<g, 256, lds, s>>>(w0, w1, w_stride, xh, us, bat,
+                                                                n_bat, y0, y1, in_dim, out_dim);
         }
         return hipGetLastError();
     }
