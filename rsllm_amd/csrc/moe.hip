@@ -35,7 +35,8 @@ namespace rsllm_hip {
 // before b: slots are sorted by expert, ties in pair order, for any number of
 // pairs. Three launches: per-block counts and in-block ranks; one workgroup
 // scans the counts (expert-major) into the bases and lists the active
-// experts and the matrix-core batches; per-pair scatter.
+// experts and the matrix-core batches; per-pair scatter. Calls of up to
+// kRoute1Pairs pairs take the one-launch form k_moe_route1 (one block).
 constexpr int kRouteBlock = 256;
 
 inline int route_blocks(int n_pairs) { return (n_pairs + kRouteBlock - 1) / kRouteBlock; }
@@ -70,25 +71,36 @@ __global__ __launch_bounds__(kRouteBlock) void k_moe_hist(const int *__restrict_
 }
 
 // Exclusive scan of v[0..n) in place by the whole workgroup (kScanThreads
-// threads), returning the total; `part` holds kScanThreads ints of LDS.
+// threads), returning the total; `part` holds kScanThreads ints of LDS (the
+// first kScanThreads / 64 are used). Each thread sums a contiguous segment;
+// the per-thread sums are scanned within each wavefront (six shuffle-up
+// steps), the wavefront totals by every thread in turn (16 adds), so the
+// scan costs two barriers plus the final one. Integer sums: the order does
+// not change the result.
 constexpr int kScanThreads = 1024;
 __device__ int scan_inplace(int *__restrict__ v, size_t n, int *part) {
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const size_t seg = (n + kScanThreads - 1) / kScanThreads;
     const size_t lo = min(n, (size_t)tid * seg), hi = min(n, lo + seg);
     int sum = 0;
     for (size_t i = lo; i < hi; i++) sum += v[i];
-    part[tid] = sum;
-    __syncthreads();
-    // Hillis-Steele over the per-thread sums
-    for (int d = 1; d < kScanThreads; d <<= 1) {
-        const int add = tid >= d ? part[tid - d] : 0;
-        __syncthreads();
-        part[tid] += add;
-        __syncthreads();
+    // inclusive scan of the per-thread sums within the wavefront
+    int inc = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int add = __shfl_up(inc, (unsigned)d, 64);
+        if (lane >= d) inc += add;
     }
-    const int total = part[kScanThreads - 1];
-    int run = part[tid] - sum;  // exclusive prefix of this thread's segment
+    if (lane == 63) part[wv] = inc;
+    __syncthreads();
+    int base = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kScanThreads / 64; w++) {
+        const int t = part[w];
+        base += w < wv ? t : 0;
+        total += t;
+    }
+    int run = base + inc - sum;  // exclusive prefix of this thread's segment
     for (size_t i = lo; i < hi; i++) {
         const int c = v[i];
         v[i] = run;
@@ -165,6 +177,75 @@ __global__ __launch_bounds__(kRouteBlock) void k_moe_scatter(const int *__restri
     slot_of[p] = slot;
 }
 
+// The same routing in one workgroup and one launch, for calls of up to
+// kRoute1Pairs pairs and kRoute1Experts experts (decode batches): counts,
+// ranks and offsets in LDS, then the scatter, the active experts and the
+// batches, written as the three-launch path writes them. Each small launch
+// costs a few microseconds of dependent latency; this saves two.
+constexpr int kRoute1Pairs = 512;
+constexpr int kRoute1Experts = 4096;
+__global__ __launch_bounds__(kScanThreads) void k_moe_route1(const int *__restrict__ ids,
+                                                             const float *__restrict__ wts,
+                                                             int n_pairs, int k, int n_expert,
+                                                             int *__restrict__ off,
+                                                             int *__restrict__ slot_tok,
+                                                             int *__restrict__ slot_of,
+                                                             int *__restrict__ act,
+                                                             int *__restrict__ n_act,
+                                                             MfgBatch *__restrict__ bat,
+                                                             int *__restrict__ n_bat, int bw) {
+    extern __shared__ int sh[];  // base[n_expert], flags[n_expert]
+    __shared__ int ep[kRoute1Pairs];
+    __shared__ int part[kScanThreads];
+    int *base = sh, *flags = sh + n_expert;
+    const int tid = threadIdx.x;
+    for (int x = tid; x < n_expert; x += kScanThreads) base[x] = 0;
+    int e = -1;
+    if (tid < n_pairs) {
+        const int id = ids[tid];
+        if (wts[tid] != 0.0f && id >= 0 && id < n_expert) e = id;
+    }
+    if (tid < kRoute1Pairs) ep[tid] = e;
+    __syncthreads();
+    // rank: valid pairs of the same expert before this one (pair order)
+    int r = 0;
+    if (e >= 0) {
+        atomicAdd(&base[e], 1);
+        for (int q = 0; q < tid; q++) r += ep[q] == e ? 1 : 0;
+    }
+    __syncthreads();
+    const int total = scan_inplace(base, (size_t)n_expert, part);
+    for (int x = tid; x < n_expert; x += kScanThreads) off[x] = base[x];
+    if (tid == 0) off[n_expert] = total;
+    if (tid < n_pairs) {
+        const int slot = e >= 0 ? base[e] + r : -1;
+        if (e >= 0) slot_tok[slot] = tid / k;
+        slot_of[tid] = slot;
+    }
+    auto count = [&](int x) { return (x + 1 < n_expert ? base[x + 1] : total) - base[x]; };
+    // active experts: positions from a scan of the 0/1 flags
+    for (int x = tid; x < n_expert; x += kScanThreads) flags[x] = count(x) > 0 ? 1 : 0;
+    __syncthreads();
+    const int na = scan_inplace(flags, (size_t)n_expert, part);
+    for (int x = tid; x < n_expert; x += kScanThreads) {
+        const int next = x + 1 < n_expert ? flags[x + 1] : na;
+        if (next != flags[x]) act[flags[x]] = x;
+    }
+    if (tid == 0) *n_act = na;
+    if (!bat) return;
+    __syncthreads();
+    // batches: positions from a scan of ceil(count / bw)
+    for (int x = tid; x < n_expert; x += kScanThreads) flags[x] = (count(x) + bw - 1) / bw;
+    __syncthreads();
+    const int nb = scan_inplace(flags, (size_t)n_expert, part);
+    for (int x = tid; x < n_expert; x += kScanThreads) {
+        const int c = count(x);
+        for (int f = 0, j = flags[x]; f < c; f += bw, j++)
+            bat[j] = MfgBatch{base[x] + f, c - f < bw ? c - f : bw, x, 0};
+    }
+    if (tid == 0) *n_bat = nb;
+}
+
 // Workspace of launch_moe_route: hist (n_expert x blocks), rank (one per
 // pair), flags (n_expert + 1).
 static size_t moe_route_work_bytes(int n_pairs, int n_expert) {
@@ -177,6 +258,11 @@ static hipError_t launch_moe_route(const int *ids, const float *wts, int n_pairs
                                    int n_expert, uint8_t *work, int *off, int *slot_tok,
                                    int *slot_of, int *act, int *n_act, MfgBatch *bat, int *n_bat,
                                    int bw, hipStream_t s) {
+    if (n_pairs <= kRoute1Pairs && n_expert <= kRoute1Experts) {
+        k_moe_route1<<<1, kScanThreads, (size_t)n_expert * 8, s>>>(
+            ids, wts, n_pairs, k, n_expert, off, slot_tok, slot_of, act, n_act, bat, n_bat, bw);
+        return hipGetLastError();
+    }
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
     const int nblk = route_blocks(n_pairs);
     int *hist = reinterpret_cast<int *>(work);
