@@ -301,6 +301,62 @@ __global__ __launch_bounds__(256) void k_moe_accumulate(float *__restrict__ out,
     out[i] = v;
 }
 
+__global__ __launch_bounds__(256) void k_moe_accumulate4(float *__restrict__ out,
+                                                        const float *__restrict__ yd,
+                                                        const float *__restrict__ wts,
+                                                        const int *__restrict__ slot_of,
+                                                        int n_tok, int k, int n_embd) {
+#pragma clang fp contract(off)
+    // four consecutive outputs per thread (n_embd a multiple of 4, out
+    // 16-byte aligned); each
+    // group of 8 slots' ids and weights is loaded first and their rows' loads
+    // are issued together (a skipped slot reads row 0 and is not added), then
+    // the products are added in i order as before
+    const int n4 = n_embd >> 2;
+    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i4 >= (size_t)n_tok * n4) return;
+    const int t = (int)(i4 / n4), j = (int)(i4 % n4) * 4;
+    float4 v = reinterpret_cast<float4 *>(out)[i4];
+    for (int p0 = 0; p0 < k; p0 += 8) {
+        int sl[8];
+        float w[8];
+        float4 y[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int p = p0 + u;
+            sl[u] = p < k ? slot_of[t * k + p] : -1;
+            w[u] = p < k ? wts[t * k + p] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            y[u] = *reinterpret_cast<const float4 *>(yd + (size_t)(sl[u] >= 0 ? sl[u] : 0) * n_embd + j);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (sl[u] >= 0) {
+                v.x = v.x + w[u] * y[u].x;
+                v.y = v.y + w[u] * y[u].y;
+                v.z = v.z + w[u] * y[u].z;
+                v.w = v.w + w[u] * y[u].w;
+            }
+        }
+    }
+    reinterpret_cast<float4 *>(out)[i4] = v;
+}
+
+// out[t, j] += sum_i w[t, i] * yd[slot(t, i), j] in i order, without
+// contraction (skipped slots add nothing).
+static hipError_t launch_moe_accumulate(float *out, const float *yd, const float *wts,
+                                        const int *slot_of, int n_tok, int k, int n_embd,
+                                        hipStream_t s) {
+    if (n_embd % 4 == 0 && ((uintptr_t)out & 15) == 0)
+        k_moe_accumulate4<<<(unsigned)(((size_t)n_tok * (n_embd / 4) + 255) / 256), 256, 0, s>>>(
+            out, yd, wts, slot_of, n_tok, k, n_embd);
+    else
+        k_moe_accumulate<<<(unsigned)(((size_t)n_tok * n_embd + 255) / 256), 256, 0, s>>>(
+            out, yd, wts, slot_of, n_tok, k, n_embd);
+    return hipGetLastError();
+}
+
 
 // ---- fused path for a few tokens (decode) -----------------------------------
 // For n_tok * k <= kFusedPairs (and x, h fitting in LDS) the layer is two
@@ -837,9 +893,7 @@ static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
                                  bat, n_bat, (int)P, n_expert, hg, hu, yd, mscratch, n_embd, n_ff,
                                  clamp, s)) != hipSuccess)
             return e;
-        k_moe_accumulate<<<(unsigned)(((size_t)n_tok * n_embd + 255) / 256), 256, 0, s>>>(
-            out, yd, wts, slot_of, n_tok, k, n_embd);
-        return hipGetLastError();
+        return launch_moe_accumulate(out, yd, wts, slot_of, n_tok, k, n_embd, s);
     }
     if (fused1)
         return moe_fused(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x, ids, wts, out, hg,
@@ -876,9 +930,7 @@ static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
     if ((e = launch_gemv_grouped(dt_d, down, nullptr, d_stride, xq2, xq2_bytes, off, nullptr, act,
                                  n_act, grid_experts, yd, nullptr, n_ff, n_embd, s)) != hipSuccess)
         return e;
-    k_moe_accumulate<<<(unsigned)(((size_t)n_tok * n_embd + 255) / 256), 256, 0, s>>>(
-        out, yd, wts, slot_of, n_tok, k, n_embd);
-    return hipGetLastError();
+    return launch_moe_accumulate(out, yd, wts, slot_of, n_tok, k, n_embd, s);
 }
 
 hipError_t launch_moe(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
