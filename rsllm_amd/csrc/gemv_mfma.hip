@@ -368,16 +368,17 @@ __device__ __forceinline__ float max8(const float4 &a, const float4 &b) {
                  fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
 }
 
-// Max over a workgroup of kMfxThreads threads (every thread gets it); `red`
+// Max over a workgroup of TH threads (every thread gets it); `red`
 // holds one float per wavefront.
 constexpr int kMfxThreads = 1024;
+template <int TH = 1024>
 __device__ __forceinline__ float block_max(float m, float *red) {
     m = wave_max(m);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     float r = red[0];
 #pragma unroll
-    for (int i = 1; i < kMfxThreads / 64; i++) r = fmaxf(r, red[i]);
+    for (int i = 1; i < TH / 64; i++) r = fmaxf(r, red[i]);
     return r;
 }
 
@@ -847,13 +848,13 @@ __global__ __launch_bounds__(256) void k_mfs_sum(const float *__restrict__ part,
 // at unscale + b * bw; its rows go to y + first * out_dim.
 
 // One token column of an ntp-wide activation image (the k_mf_x conversion,
-// one workgroup of kMfxThreads threads, the row read once when it fits in
+// one workgroup of TH threads, the row read once when it fits in
 // registers): val4(i) gives elements i .. i + 3 of the column's row; the
 // column's pieces go to both planes of the image at xb, 2^-e to *us.
-template <class F, class V>
+template <class F, int TH = kMfxThreads, class V>
 __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 *__restrict__ xb,
                                             float *__restrict__ us, int ntp) {
-    __shared__ float red[kMfxThreads / 64];
+    __shared__ float red[TH / 64];
     const int tid = threadIdx.x;
     const int n8 = in_dim / 8;
     const size_t plane = (size_t)in_dim * ntp;
@@ -865,13 +866,13 @@ __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 
         *reinterpret_cast<uint4 *>(xb + plane + slot * 8) = lo;
     };
     // pieces read once (kept in registers) when the row fits
-    const bool cached = n8 <= kMfxThreads * kMfxCache;
+    const bool cached = n8 <= TH * kMfxCache;
     float4 c[kMfxCache][2];
     float m = 0.f;
     if (cached) {
 #pragma unroll
         for (int r = 0; r < kMfxCache; r++) {
-            const int i = tid + r * kMfxThreads;
+            const int i = tid + r * TH;
             if (i < n8) {
                 c[r][0] = val4(8 * i);
                 c[r][1] = val4(8 * i + 4);
@@ -879,15 +880,15 @@ __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 
             }
         }
     } else {
-        for (int i = tid; i < n8; i += kMfxThreads) m = fmaxf(m, max8(val4(8 * i), val4(8 * i + 4)));
+        for (int i = tid; i < n8; i += TH) m = fmaxf(m, max8(val4(8 * i), val4(8 * i + 4)));
     }
-    const int e = mf_exponent(block_max(m, red));
+    const int e = mf_exponent(block_max<TH>(m, red));
     const float up = ldexpf(1.0f, e);
     if (tid == 0) *us = ldexpf(1.0f, -e);
     if (cached) {
 #pragma unroll
         for (int r = 0; r < kMfxCache; r++) {
-            const int i = tid + r * kMfxThreads;
+            const int i = tid + r * TH;
             if (i < n8) {
                 uint4 hi, lo;
                 hilo8(c[r][0], c[r][1], up, hi, lo);
@@ -895,7 +896,7 @@ __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 
             }
         }
     } else {
-        for (int i = tid; i < n8; i += kMfxThreads) {
+        for (int i = tid; i < n8; i += TH) {
             uint4 hi, lo;
             hilo8(val4(8 * i), val4(8 * i + 4), up, hi, lo);
             store(i, hi, lo);
@@ -908,8 +909,8 @@ __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 
 // of hg, hu (SWIGLU true). Columns past the batch's count are left as they
 // are: column t of an MFMA's B operand reaches only column t of its result,
 // and those outputs are not stored.
-template <class F, bool SWIGLU>
-__global__ __launch_bounds__(kMfxThreads) void k_mfg_x(const float *__restrict__ x,
+template <class F, bool SWIGLU, int TH>
+__global__ __launch_bounds__(TH) void k_mfg_x(const float *__restrict__ x,
                                                const float *__restrict__ hu,
                                                const int *__restrict__ tok,
                                                const MfgBatch *__restrict__ bat,
@@ -932,8 +933,8 @@ __global__ __launch_bounds__(kMfxThreads) void k_mfg_x(const float *__restrict__
         }
         return v;
     };
-    mf_x_column<F>(val4, in_dim, t, xh + (size_t)b * 2 * in_dim * bw, unscale + (size_t)b * bw + t,
-                   bw);
+    mf_x_column<F, TH>(val4, in_dim, t, xh + (size_t)b * 2 * in_dim * bw,
+                       unscale + (size_t)b * bw + t, bw);
 }
 
 // ---- grouped LoRA-down on the matrix cores ----------------------------------------
@@ -1399,11 +1400,22 @@ static hipError_t mfg_pass(const uint8_t *w0, const uint8_t *w1, size_t w_stride
                            const float *hu, const int *tok, const MfgBatch *bat, const int *n_bat,
                            int max_b, float clamp, _Float16 *xh, float *us, float *y0, float *y1,
                            int in_dim, int out_dim, int bw, hipStream_t s) {
+    // one workgroup per column; 256 threads for rows of up to 2048 elements
+    // (one 8-element piece per thread), else kMfxThreads
     const dim3 gx((unsigned)bw, (unsigned)max_b);
-    if (hu)
-        k_mfg_x<F, true><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
-    else
-        k_mfg_x<F, false><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
+    if (in_dim <= 2048) {
+        if (hu)
+            k_mfg_x<F, true, 256><<<gx, 256, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
+        else
+            k_mfg_x<F, false, 256><<<gx, 256, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
+    } else {
+        if (hu)
+            k_mfg_x<F, true, kMfxThreads><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh,
+                                                                    us, in_dim, bw);
+        else
+            k_mfg_x<F, false, kMfxThreads><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh,
+                                                                     us, in_dim, bw);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // weights staged through LDS where the layout allows (16-byte aligned
