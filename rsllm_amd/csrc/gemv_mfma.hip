@@ -1408,6 +1408,11 @@ static hipError_t mfg_pass(const uint8_t *w0, const uint8_t *w1, size_t w_stride
             k_mfg_x<F, true, 256><<<gx, 256, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
         else
             k_mfg_x<F, false, 256><<<gx, 256, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
+    } else if (in_dim <= 8192) {
+        if (hu)
+            k_mfg_x<F, true, 512><<<gx, 512, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
+        else
+            k_mfg_x<F, false, 512><<<gx, 512, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
     } else {
         if (hu)
             k_mfg_x<F, true, kMfxThreads><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh,
