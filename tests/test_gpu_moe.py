@@ -322,6 +322,49 @@ def test_moe_many_pairs_one_expert_and_device_form(oracle, hip):
     assert np.array_equal(y.cpu().numpy().view(np.uint32), got.view(np.uint32))
 
 
+@pytest.mark.parametrize("n_tok", [40, 65])
+def test_moe_dev_skips_out_of_range_ids_and_unaligned_out(oracle, hip, n_tok):
+    """The device entry point skips slots whose expert id is out of range
+    (it cannot inspect ids), as it skips w = 0 slots: the result equals the
+    oracle's with those slots' weights zeroed. Q4_K experts from 8 tokens
+    take the matrix-core route; 40 x 8 pairs route in one launch, 65 x 8
+    (past 512) in three. A second call accumulates into an `out` 4 bytes off
+    16-byte alignment (the one-output-per-thread accumulate): the same bits."""
+    import torch
+    n_embd, n_ff, n_expert, k = 1024, 1024, 9, 8
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.Q4_K, G.Q4_K,
+                                          4500 + n_tok)
+    bad = [(0, 1, -1), (3, 0, n_expert), (n_tok - 1, 7, 1 << 20), (n_tok // 2, 4, -7)]
+    for t, i, e in bad:
+        ids[t, i] = e
+    w[2, 3] = 0.0
+    ids_ok, w_ok = ids.copy(), w.copy()
+    for t, i, _ in bad:
+        ids_ok[t, i], w_ok[t, i] = 0, 0.0
+    base = synth.activations(n_tok, n_embd, 4600 + n_tok).reshape(-1)
+    want = run_oracle(oracle, base, x, gate, up, down, ids_ok, w_ok, n_tok, n_embd, n_ff, n_expert,
+                      k, G.Q4_K, G.Q4_K)
+    s = torch.cuda.current_stream().cuda_stream
+    d = [torch.from_numpy(np.ascontiguousarray(a)).cuda()
+         for a in (gate, up, down, x.reshape(-1), ids.reshape(-1).astype(np.int32), w.reshape(-1))]
+    outs = []
+    for off in (0, 1):
+        y = torch.zeros(n_tok * n_embd + 4, dtype=torch.float32, device="cuda")
+        yv = y[off:off + n_tok * n_embd]
+        yv.copy_(torch.from_numpy(base).cuda())
+        assert (yv.data_ptr() % 16 == 0) == (off == 0)
+        hip.moe_routed_dev(yv.data_ptr(), yv.numel(), d[3].data_ptr(), d[3].numel(),
+                           d[0].data_ptr(), d[1].data_ptr(), gate.nbytes, d[2].data_ptr(),
+                           down.nbytes, d[4].data_ptr(), d[5].data_ptr(), ids.size, n_tok, n_embd,
+                           n_ff, n_expert, k, G.Q4_K, G.Q4_K, 10.0, s)
+        torch.cuda.synchronize()
+        outs.append(yv.cpu().numpy().copy())
+    err = rel_err(outs[0] - base, want - base)
+    print(f"moe dev out-of-range ids T={n_tok}: rel err {err:.3e}")
+    assert err <= MFMA_TOL
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 # ---- C3 at its real expert count (64 experts, BASELINE.json configs[3]) ------
 
 @pytest.fixture(scope="module")
