@@ -1,44 +1,30 @@
 // Prefill GEMM: out[t, o] = sum_i deq(W)[o, i] * x[t, i] for a Q4_K weight W
-// [out_dim x in_dim] and bf16 activations x [n_tok x in_dim], fp32 output.
+// [out_dim x in_dim] and bf16 or f32 activations x [n_tok x in_dim], fp32
+// output.
 //
-// The reference computes this as matmul_quant_f32 on f32(bf16 x)
-// (backend-cpu/src/ops/quant_matmul.rs:45-119): every weight row is
-// dequantised once per token and dotted in f32. Here it is one dense
-// contraction on the CDNA4 matrix cores:
+// The reference computes this as matmul_quant_f32 (backend-cpu/src/ops/
+// quant_matmul.rs:45-119): every weight row is dequantised once per token and
+// dotted in f32. Here it is one dense contraction on the CDNA4 matrix cores:
 //
-// 1. k_prefill_x: per token t, x is scaled by 2^e_t so that max|x_t| lands in
-//    [2^14, 2^15) and converted to f16. bf16 has an 8-bit significand, so the
-//    conversion is exact for every element within 2^-29 of the token's
-//    maximum; 2^-e_t is kept to undo the scaling in the epilogue.
-// 2. k_prefill_q4k: W is dequantised in registers to f16,
-//    w = f16(d*sc_j) * q - f16(dmin*m_j) (packed f16 FMA, q exact), straight
-//    into the operands of v_mfma_f32_16x16x32_f16 against the f16
-//    activations; products accumulate in fp32. The f16 weight rounding
-//    (about 2^-11 relative per weight) keeps the output within about 3e-4
-//    of the reference, inside the 1e-3 budget.
-//
-// Tiling: a workgroup is 4 wavefronts and covers 256 weight rows x TOK
-// tokens (TOK = 128, or 64 when the 128-token grid would leave most CUs
-// idle); a wavefront owns 64 rows (4 MFMA tiles) x TOK tokens (TOK / 16
-// tiles), accumulators held in VGPRs. Every weight is dequantised once per
-// workgroup and used for all TOK tokens: the larger tile halves the
-// dequantisation per MFMA, the smaller one fits two workgroups per CU (80
-// KiB of LDS instead of 112). The weights are the MFMA A operand and the
-// activations the B operand, so every lane ends with 4 consecutive outputs of
-// one token. The K loop runs in steps of
-// half a super-block (128 elements). Each step's activations (TOK tokens x
-// 128 f16), weight bytes (256 rows x the 64 qs bytes of that half,
-// 16 KB) and block headers (256 rows x 16 bytes) are copied global->LDS by
-// DMA into one of two stage buffers while the other is computed. Each
-// thread turns its own row's header into f16 (d*sc_j, dmin*m_j) once per
-// step and leaves them in LDS for the lanes that dequantise that row.
-//
-// K order: inside a super-block, MFMA chunk c (0..7) gives lane group q
-// (lanes 16q..16q+15) sub-block 2q + (c & 1), positions 8 * (c >> 1) .. + 7,
-// so a lane's weights for one half are 16 contiguous qs bytes (low nibbles
-// for even c, high for odd c); the activation stage is laid out in the same
-// order. Half h holds positions 16h .. 16h + 15 of every sub-block.
+// 1. k_prefill_x / k_prefill_x_f32: per token t, x is scaled by 2^e_t so that
+//    max|x_t| lands in [2^14, 2^15) and converted to f16. bf16 has an 8-bit
+//    significand, so that conversion is exact for every element within 2^-29
+//    of the token's maximum; f32 is rounded once (2^-11 relative). 2^-e_t is
+//    kept to undo the scaling in the epilogue.
+// 2. The GEMM dequantises W in registers to f16, w = f16(d*sc_j) * q -
+//    f16(dmin*m_j) (packed f16 FMA, q exact), straight into the operands of
+//    v_mfma_f32_16x16x32_f16 against the f16 activations; products
+//    accumulate in fp32. The f16 weight rounding (about 2^-11 relative per
+//    weight) keeps the output within about 4e-4 of the reference, inside the
+//    1e-3 budget. The weights are the MFMA A operand and the activations the
+//    B operand, so every lane ends with 4 consecutive outputs of one token.
+//    k_prefill_q4k_w8 runs it: a workgroup of 8 wavefronts covers 256 weight
+//    rows x 128 tokens, two wavefronts per SIMD that split K between them
+//    (described at the kernel).
 #include "kernels.h"
+
+#include <algorithm>
+#include <climits>
 
 namespace rsllm_hip {
 
@@ -46,27 +32,8 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kPfTok = 128;                      // largest token tile (tokens per workgroup)
-constexpr int kPfRowsWave = 64;                  // weight rows per wavefront
-constexpr int kPfRowsWg = 4 * kPfRowsWave;       // weight rows per workgroup
-constexpr int kPfQsBytes = kPfRowsWg * 64;      // weight qs stage: 256 rows x 64 bytes
-constexpr int kPfHdBytes = kPfRowsWg * 16;      // weight header stage: 256 rows x 16 bytes
-constexpr int kPfNStage = 2;                    // stage buffers
-// LDS of the TOK-token workgroup: two stages of (TOK rows x 128 f16
-// activations, qs, headers), then the f16 block scales (256 rows x 32 bytes):
-// 114688 bytes at TOK = 128, 81920 at TOK = 64
-constexpr int pf_lds(int tok) {
-    return kPfNStage * (tok * 256 + kPfQsBytes + kPfHdBytes) + kPfRowsWg * 32;
-}
-
-typedef __attribute__((address_space(3))) void lds_void;
-
-// 16-byte global->LDS DMA (a non-template wrapper: the builtin called
-// directly inside a kernel template keeps the host pass from emitting that
-// kernel's stub)
-__device__ __forceinline__ void pf_dma16(const void *g, uint8_t *l) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void *)l, 16, 0, 0);
-}
+constexpr int kPfTok = 128;    // tokens per workgroup
+constexpr int kPfRowsWg = 256;  // weight rows per workgroup
 
 // ---- activation pre-pass: bf16 -> scaled f16 ----------------------------------
 // One workgroup (256 threads) per token; each thread moves 16-byte pieces (8
@@ -225,254 +192,297 @@ __device__ __forceinline__ h8 pf_dequant8(uint32_t d0, uint32_t d1, bool hi, h2 
     return dequant_q4x8_f16(d0, d1, hi, dsc, dm);
 }
 
-struct pf_true { static constexpr bool value = true; };
-struct pf_false { static constexpr bool value = false; };
+// ---- 8-wavefront GEMM: two K groups per workgroup -----------------------------
+// The workgroup covers 256 weight rows x 128 tokens with 8 wavefronts: wave w
+// owns rows 64 (w & 3) .. + 63 for all 128 tokens (8 x 4 MFMA tiles in VGPRs)
+// and K group w >> 2, which takes every other quarter (64 elements) of each
+// super-block: group g computes quarters g and 2 + g. Each weight is
+// dequantised once per workgroup and used for 128 tokens, and every SIMD holds
+// two wavefronts,
+// one of each group, so one wavefront's dequantisation, LDS waits and barrier
+// drain run while the other issues MFMAs (a VALU instruction in an MFMA's own
+// wavefront stalls the matrix pipe on gfx950). The two groups' partial sums
+// are added once, through LDS, before the store.
+//
+// K order inside a quarter u (sub-blocks 2u, 2u + 1, elements 64u .. 64u + 63
+// of the super-block): MFMA chunk c is sub-block 2u + c, lane group q holds
+// its positions 8q .. 8q + 7. A lane's weights for both chunks are the 8 qs
+// bytes 32u + 8q .. + 7 (low nibbles chunk 0, high nibbles chunk 1); the
+// activations of chunk c are elements 64u + 32c + 8q .. + 7, 16 contiguous
+// bytes of the f16 image.
+//
+// LDS:
+// - weights: the 256 rows' whole blocks of one super-block (144 bytes each,
+//   row-major: the 144-byte row stride spreads 16 rows over distinct banks),
+//   shared by both groups, two super-blocks deep. A row's block is contiguous
+//   in HBM, so each 1 KB DMA instruction reads whole cache lines of about 7
+//   rows instead of 16 bytes from each of 64;
+// - activations: per group and step 128 tokens x 128 bytes (16-byte slot k of
+//   token row t holds piece k ^ ((t >> 1) & 7), so the operand reads of 16
+//   tokens hit 16 distinct bank groups), two steps deep;
+// - per group the f16 (d*sc_j, dmin*m_j) of its four sub-blocks, 16 bytes per
+//   row, each thread converting its own row's header once per super-block.
+constexpr int kP8Blk = kPfRowsWg * kQ4kBytes;        // 36 KB: one super-block of 256 rows
+constexpr int kP8Act = kPfTok * 128;                 // 16 KB: one group's activations of a step
+constexpr int kP8ActOff = 2 * kP8Blk;                // activation buffers (group, step parity)
+constexpr int kP8ScOff = kP8ActOff + 4 * kP8Act;     // scale records, 16 bytes per row per group
+constexpr int kP8Lds = kP8ScOff + 2 * kPfRowsWg * 16;  // 144 KB
+constexpr int kP8WPieces = kP8Blk / 1024;            // 36 weight DMA instructions per super-block
+static_assert(kP8WPieces <= 40, "at most five weight DMA instructions per wavefront");
+static_assert(2 * 4 * 16 * 64 * 16 <= kP8Lds, "the epilogue's exchange fits");
 
-// dword i (0..3) of a uint4 for a compile-time i
-__device__ __forceinline__ uint32_t pf_u4(const uint4 &v, int i) {
-    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+// LDS byte address of a pointer into a __shared__ array
+__device__ __forceinline__ uint32_t p8_lds(const void *p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)p;
+}
+// 16 bytes per lane from global to LDS: lane i copies base + voff_i to LDS
+// address lds + 16 i (base and lds uniform). Written out by hand, so the
+// compiler tracks no LDS write for it and inserts no wait for it: the
+// kernel's own waits (p8_barrier_*) order every copy against its readers.
+// The memory clobber keeps LDS accesses on their side of it; M0 is restored.
+// base and lds are wave-uniform by construction; readfirstlane makes them
+// scalar operands however the compiler placed them.
+__device__ __forceinline__ void p8_dma(const void *base, uint32_t voff, uint32_t lds) {
+    const uint64_t b = (uint64_t)(size_t)base;
+    const uint64_t bs = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b) |
+                        ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)) << 32);
+    const uint32_t ls = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(voff), "s"(bs), "s"(ls)
+                 : "memory");
+}
+// Wait for this wavefront's own copies except the newest n (n = 0 or 5) and
+// for its LDS accesses, then the workgroup barrier.
+__device__ __forceinline__ void p8_barrier_vm0() {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+__device__ __forceinline__ void p8_barrier_vm5() {
+    asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <int TOK>
-__global__ __launch_bounds__(256) void k_prefill_q4k(const uint8_t *__restrict__ w,
-                                                     const _Float16 *__restrict__ xh,
-                                                     const float *__restrict__ unscale,
-                                                     float *__restrict__ out, int n_tok, int in_dim,
-                                                     int out_dim) {
-    // token tiles per workgroup, activation DMA instructions per wavefront,
-    // DMA instructions per stage and wavefront, operand groups per step
-    constexpr int MT = TOK / 16, XP = TOK / 16, NP = XP + 5, NG = 4 * MT;
-    constexpr int kXBytes = TOK * 256, kStage = kXBytes + kPfQsBytes + kPfHdBytes;
-    constexpr int kScOff = kPfNStage * kStage;
-    extern __shared__ __align__(16) uint8_t smem[];
+template <int PAR, bool MORE> struct p8_step {
+    static constexpr int par = PAR;    // step parity within the super-block
+    static constexpr bool more = MORE;  // a next step exists
+};
+
+__global__ __launch_bounds__(512) void k_prefill_q4k_w8(const uint8_t *__restrict__ w,
+                                                        const _Float16 *__restrict__ xh,
+                                                        const float *__restrict__ unscale,
+                                                        float *__restrict__ out, int n_tok,
+                                                        int in_dim, int out_dim, int ld_out) {
+    __shared__ __align__(16) uint8_t smem[kP8Lds];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wv & 3, kg = wv >> 2;
     const int r16 = lane & 15, q = lane >> 4;
-    const int n0 = blockIdx.x * kPfRowsWg;  // first weight row of the workgroup
-    const int t0 = blockIdx.y * TOK;
+    const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
     const int nb = in_dim >> 8;
-    const int nsteps = 2 * nb;
+    const int ns = 2 * nb;  // steps of one K group
+    uint8_t *const act = smem + kP8ActOff + 2 * kg * kP8Act;  // this group's two step buffers
+    uint8_t *const scl = smem + kP8ScOff + kg * kPfRowsWg * 16;
+    const uint32_t row_bytes = (uint32_t)nb * (uint32_t)kQ4kBytes;
 
-    // DMA sources. Activations: instruction p of this wave moves token rows
-    // 4g .. 4g + 3 (g = 8 wv + p), lane i to row 4g + i / 16, slot i % 16;
-    // slot s of token row tl holds chunk k = s ^ (tl & 15), i.e. elements
-    // 32 (k >> 1) + 16h + 8 (k & 1) .. + 7 of the super-block. Rows past
-    // n_tok repeat the last token (their outputs are not stored).
-    uint32_t xoff[XP];
-#pragma unroll
-    for (int p = 0; p < XP; p++) {
-        const int tl = 4 * (XP * wv + p) + (lane >> 4);
-        const int k = (lane & 15) ^ (tl & 15);
-        const int t = min(t0 + tl, n_tok - 1);
-        xoff[p] = (uint32_t)t * (uint32_t)in_dim + 32u * (k >> 1) + 8u * (k & 1);
-    }
-    // Weight qs: instruction p (g = 4 wv + p) moves pieces j = 64 g + i, row
-    // j / 4, slot j % 4 holding qs piece k = slot ^ ((row >> 2) & 3) (bytes
-    // 32k + 16h .. + 15 of the block), so the operand reads below hit 16
-    // distinct bank groups. Headers: one instruction per wave, lane i moves
-    // the header of row 64 wv + i. Both cover exactly this wave's own rows.
-    uint32_t qoff[4];
+    // DMA sources (bytes from a uniform base). Activations: instruction p
+    // moves token rows 8 (4 wr + p) .. + 7 of this group's quarter, lane i to
+    // row 8 (4 wr + p) + i / 8, slot i % 8. Rows past n_tok repeat the last
+    // token (their outputs are not stored).
+    uint32_t xoff[4];
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-        const int j = 64 * (4 * wv + p) + lane;
-        const int row = j >> 2, k = (j & 3) ^ ((row >> 2) & 3);
-        const uint32_t rowg = (uint32_t)min(n0 + row, out_dim - 1);
-        qoff[p] = rowg * (uint32_t)nb * 144u + 16u + 32u * k;
+        const int tl = 8 * (4 * wr + p) + (lane >> 3);
+        const int pc = (lane & 7) ^ ((tl >> 1) & 7);
+        const int t = min(t0 + tl, n_tok - 1);
+        xoff[p] = 2u * ((uint32_t)t * (uint32_t)in_dim + 64 * kg + 32 * (pc >> 2) + 8 * (pc & 3));
     }
-    const uint32_t hoff = (uint32_t)min(n0 + 64 * wv + lane, out_dim - 1) * (uint32_t)nb * 144u;
-    // DMA instruction p (0..NP - 1) of stage st into buf: 0..XP - 1
-    // activations, XP..XP + 3 qs, XP + 4 headers.
-    auto dma_piece = [&](int st, uint8_t *buf, int p) {
-        const int s = st >> 1, h = st & 1;
-        if (p < XP)
-            pf_dma16(xh + xoff[p] + s * 256 + 16 * h, buf + 1024 * (XP * wv + p));
-        else if (p < XP + 4)
-            pf_dma16(w + qoff[p - XP] + s * 144 + 16 * h, buf + kXBytes + 1024 * (4 * wv + p - XP));
-        else
-            pf_dma16(w + hoff + s * 144, buf + kXBytes + kPfQsBytes + 1024 * wv);
-    };
-    // activation operand of group g (chunk g / MT of the step, token tile
-    // g % MT): elements of sub-block 2q + (c & 1) at positions 16h + 8 (c >> 1)
-    // .. + 7.
-    auto read_a = [&](const uint8_t *buf, int g) -> h8 {
-        const int c = g / MT, mt = g % MT;
-        const int k = 2 * (2 * q + (c & 1)) + (c >> 1);
-        return *reinterpret_cast<const h8 *>(buf + (mt * 16 + r16) * 256 + ((k ^ r16) << 4));
-    };
-    // this lane's weight rows in the stage: wave rows 16 nt + r16; qs piece
-    // q sits in slot q ^ ((row >> 2) & 3) = q ^ (r16 >> 2) (rows 16 nt + r16)
-    const int wrow = wv * kPfRowsWave + r16;
-    const int qslot = q ^ (r16 >> 2);
-
-    f4 acc[MT][4];
+    // Weights: instruction i = wv + 8k moves 16-byte pieces j = 64 i + lane of
+    // the stage, row j / 9, piece j % 9. Instructions past the last repeat it
+    // (same bytes to the same place), so every wavefront issues five.
+    uint32_t woff[5];
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
+    for (int k = 0; k < 5; k++) {
+        const int i = min(wv + 8 * k, kP8WPieces - 1);
+        const int j = 64 * i + lane, row = j / 9;
+        woff[k] = (uint32_t)min(n0 + row, out_dim - 1) * row_bytes + 16u * (uint32_t)(j % 9);
+    }
+    const uint32_t lds_act = p8_lds(act), lds_w = p8_lds(smem);
+    // piece p of group step s (clamped to the last) into the buffer of step parity s % 2
+    auto dma_act = [&](int s, int p) {
+        const uint32_t dst = lds_act + (uint32_t)((s & 1) * kP8Act + 1024 * (4 * wr + p));
+        s = min(s, ns - 1);
+        p8_dma(xh + (s >> 1) * 256 + 128 * (s & 1), xoff[p], dst);
+    };
+    // piece k of super-block sb (clamped to the last) into weight stage sb % 2
+    auto dma_w = [&](int sb, int k) {
+        const uint32_t dst = lds_w + (uint32_t)((sb & 1) * kP8Blk + 1024 * min(wv + 8 * k, kP8WPieces - 1));
+        sb = min(sb, nb - 1);
+        p8_dma(w + (size_t)sb * kQ4kBytes, woff[k], dst);
+    };
+    // header of this thread's row in a weight stage -> scale records of the
+    // group's four sub-blocks: 16 bytes, {d*sc, d*sc'} {dmin*m, dmin*m'} for
+    // the even step (sub-blocks 2 kg, 2 kg + 1), then for the odd step (4 +
+    // 2 kg, 5 + 2 kg) (q4_k_scale_min, dequant/mod.rs:48-58)
+    auto scales_from_header = [&](const uint8_t *wbuf) {
+        const int row = 64 * wr + lane;
+        const uint4 hd = *reinterpret_cast<const uint4 *>(wbuf + kQ4kBytes * row);
+        const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+        const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu, m_lo = hd.z & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+        const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+        const int b = 16 * kg;  // bit offset of byte 2 kg
+        uint32_t rec[4];
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+            const uint32_t sw = (hf ? sc_hi : sc_lo) >> b, mw = (hf ? m_hi : m_lo) >> b;
+            const _Float16 a0 = (_Float16)(d * (float)(sw & 0xFFu));
+            const _Float16 a1 = (_Float16)(d * (float)((sw >> 8) & 0xFFu));
+            const _Float16 m0 = (_Float16)(dmin * (float)(mw & 0xFFu));
+            const _Float16 m1 = (_Float16)(dmin * (float)((mw >> 8) & 0xFFu));
+            rec[2 * hf] = __builtin_bit_cast(uint32_t, h2{a0, a1});
+            rec[2 * hf + 1] = __builtin_bit_cast(uint32_t, h2{m0, m1});
+        }
+        *reinterpret_cast<uint4 *>(scl + 16 * row) = make_uint4(rec[0], rec[1], rec[2], rec[3]);
+    };
+    const int qbyte = 16 + 32 * kg + 8 * q;  // the lane's qs bytes in a block, step parity 0
+    const int aswz = (r16 >> 1) & 7;
+    // this lane's qs bytes and scale records of row tile nt at step parity hf
+    uint2 qs[4], sc[4];
+    auto load_weights = [&](const uint8_t *wbuf, int hf) {
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) {
+            const int row = 64 * wr + 16 * nt + r16;
+            qs[nt] = *reinterpret_cast<const uint2 *>(wbuf + kQ4kBytes * row + qbyte + 64 * hf);
+            sc[nt] = *reinterpret_cast<const uint2 *>(scl + 16 * row + 8 * hf);
+        }
+    };
+    auto dequant = [&](int c, int nt) -> h8 {
+        const h2 d2 = __builtin_bit_cast(h2, sc[nt].x), m2 = __builtin_bit_cast(h2, sc[nt].y);
+        return pf_dequant8(qs[nt].x, qs[nt].y, c != 0, c ? d2.yy : d2.xx, c ? m2.yy : m2.xx);
+    };
+    auto read_a = [&](const uint8_t *buf, int c, int mt) -> h8 {
+        return *reinterpret_cast<const h8 *>(buf + (16 * mt + r16) * 128 + 16 * ((4 * c + q) ^ aswz));
+    };
+
+    f4 acc[8][4];
+#pragma unroll
+    for (int mt = 0; mt < 8; mt++)
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
 
-    // f16 scales of this lane's sub-blocks 2q, 2q + 1: .x = (d*sc_2q,
-    // d*sc_2q+1), .y = (dmin*m_2q, dmin*m_2q+1)
-    uint2 sc[4];
-    uint4 qs[4];
+    // prologue: super-block 0 and step 0 in, step 1 in flight, step 0's
+    // chunk-0 operands ready
+#pragma unroll
+    for (int k = 0; k < 5; k++) dma_w(0, k);
+#pragma unroll
+    for (int p = 0; p < 4; p++) dma_act(0, p);
+    p8_barrier_vm0();
+#pragma unroll
+    for (int p = 0; p < 4; p++) dma_act(1, p);  // ns >= 2; super-block 1 in step 0
+    scales_from_header(smem);
+    load_weights(smem, 0);
     h8 bq[4];
-    uint8_t *const scl = smem + kScOff;
-    auto load_step_weights = [&](const uint8_t *buf) {
-        // this thread's row 64 wv + lane: header -> 16 f16 scales into LDS,
-        // record layout per q: {d*sc_2q, d*sc_2q+1, dmin*m_2q, dmin*m_2q+1}
-        // (q4_k_scale_min, dequant/mod.rs:48-58, on four bytes at a time)
-        {
-            const uint4 hd = *reinterpret_cast<const uint4 *>(buf + kXBytes + kPfQsBytes + 16 * (64 * wv + lane));
-            const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
-            const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu, m_lo = hd.z & 0x3F3F3F3Fu;
-            const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
-            const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-            uint32_t rec[8];
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                // sub-blocks 2qq, 2qq + 1: bytes of the low (j < 4) or high word
-                const uint32_t sw = qq < 2 ? sc_lo : sc_hi, mw = qq < 2 ? m_lo : m_hi;
-                const int b = 2 * (qq & 1);
-                const _Float16 a0 = (_Float16)(d * (float)((sw >> (8 * b)) & 0xFFu));
-                const _Float16 a1 = (_Float16)(d * (float)((sw >> (8 * b + 8)) & 0xFFu));
-                const _Float16 m0 = (_Float16)(dmin * (float)((mw >> (8 * b)) & 0xFFu));
-                const _Float16 m1 = (_Float16)(dmin * (float)((mw >> (8 * b + 8)) & 0xFFu));
-                rec[2 * qq] = __builtin_bit_cast(uint32_t, h2{a0, a1});
-                rec[2 * qq + 1] = __builtin_bit_cast(uint32_t, h2{m0, m1});
-            }
-            uint4 *dst = reinterpret_cast<uint4 *>(scl + 32 * (64 * wv + lane));
-            dst[0] = make_uint4(rec[0], rec[1], rec[2], rec[3]);
-            dst[1] = make_uint4(rec[4], rec[5], rec[6], rec[7]);
-        }
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++) {
-            const int row = wrow + 16 * nt;
-            qs[nt] = *reinterpret_cast<const uint4 *>(buf + kXBytes + row * 64 + qslot * 16);
-            sc[nt] = *reinterpret_cast<const uint2 *>(scl + row * 32 + q * 8);
-        }
-    };
-    // B operands of chunk c (0..3) of the current step
-    auto dequant = [&](int c, int nt) -> h8 {
-        const int run = c >> 1;  // bytes 8 run .. 8 run + 7 of the lane's 16
-        const h2 d2 = __builtin_bit_cast(h2, sc[nt].x), m2 = __builtin_bit_cast(h2, sc[nt].y);
-        const h2 ds = (c & 1) ? d2.yy : d2.xx;
-        const h2 dm = (c & 1) ? m2.yy : m2.xx;
-        return pf_dequant8(pf_u4(qs[nt], 2 * run), pf_u4(qs[nt], 2 * run + 1), (c & 1) != 0, ds,
-                           dm);
-    };
-
-    // Stage st + 1 is in flight while step st is computed: its DMA is issued
-    // right after the barrier in step st - 1, into the buffer step st - 1
-    // used. The last step's DMA repeats the last stage into a buffer nothing
-    // reads again.
-    auto sbuf = [&](int st) { return smem + (st & 1) * kStage; };
-#pragma unroll
-    for (int p = 0; p < NP; p++) dma_piece(0, sbuf(0), p);
-    __syncthreads();
-#pragma unroll
-    for (int p = 0; p < 4; p++) dma_piece(1, sbuf(1), p);  // nsteps >= 2 (in_dim >= 256)
-    load_step_weights(sbuf(0));
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) bq[nt] = dequant(0, nt);
-    h8 a0 = read_a(sbuf(0), 0), a1 = read_a(sbuf(0), 1);
+    h8 a0 = read_a(act, 0, 0), a1 = read_a(act, 0, 1);
 
-    // One K step: NG groups (4 chunks x MT token tiles) of 4 MFMAs. Operand
-    // reads run two groups ahead (across the step boundary), weight operands
-    // are dequantised one chunk ahead (chunk 3 prepares the next step's chunk
-    // 0 from the next stage's weight rows). The DMA of stage st + 2 is
-    // spread so the CU's return path is never flooded: instructions 0..3
-    // after the barrier in groups NG - 2, NG - 1 of step st, 4..NP - 1 one
-    // per group in groups 0..NP - 5 of step st + 1. MORE: a next step exists.
-    auto step = [&](int st, auto more_tag) {
-        constexpr bool more = decltype(more_tag)::value;
-        uint8_t *buf = sbuf(st);
-        const uint8_t *nbuf = sbuf(st + 1);
-        h8 bn[4];
+    // One step s (super-block sb = s / 2, step parity PAR = s % 2): 16 groups
+    // (2 chunks x 8 token tiles) of 4 MFMAs. Operand reads run two groups
+    // ahead, across the step boundary; chunk 1's weights are dequantised
+    // during chunk 0, the next step's chunk 0 in groups 14, 15. In group 14
+    // every wavefront has this step's operands in registers and waits for
+    // its own copies the next step needs (its activations; on the last step
+    // of a super-block also the next super-block's weights): after the
+    // barrier those are readable, this step's activation buffer takes step
+    // s + 2 (groups 14, 15), and after the last step of a super-block its
+    // weight stage takes super-block sb + 2 (groups 1, 3, .., 9 of the next
+    // step; super-block 1 in step 0). The weight copies are issued after the
+    // activation copies of the step after, so an even step waits only for the
+    // older activation pieces (vmcnt(5)).
+    auto step = [&](int s, auto tag) {
+        constexpr int PAR = decltype(tag)::par;
+        constexpr bool MORE = decltype(tag)::more;
+        const int sb = s >> 1;
+        const uint8_t *buf = act + PAR * kP8Act;
+        const uint8_t *nbuf = act + (1 - PAR) * kP8Act;
+        h8 b1[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
+        for (int g = 0; g < 16; g++) {
+            const int c = g >> 3, mt = g & 7;
             __builtin_amdgcn_sched_barrier(0);
-            if (more && c == 3) {
-                // stage st + 1: this wave's own weight rows are in once its
-                // own DMA has completed
-                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-                load_step_weights(nbuf);
+            if (MORE && PAR == 0 && (g & 1) && g < 10) dma_w(sb + 1, g >> 1);
+            if (MORE && g == 14) {
+                if (PAR) p8_barrier_vm0();
+                else p8_barrier_vm5();
+                if (PAR) scales_from_header(smem + ((sb + 1) & 1) * kP8Blk);
+                load_weights(smem + ((sb + PAR) & 1) * kP8Blk, 1 - PAR);
             }
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                const int g = MT * c + mt;
-                if (more && g <= NP - 5)  // rest of stage st + 1
-                    dma_piece(min(st + 1, nsteps - 1), buf + (nbuf - buf), 4 + g);
-                if (more && g == NG - 2) {
-                    // every wave has its operands up to group NG - 1 in
-                    // registers and its stage-(st+1) DMA complete: the next
-                    // stage's activation rows become readable and `buf` is
-                    // free for stage st + 2 (the last stage again when there
-                    // is none; nothing reads it then)
-                    __syncthreads();
-                }
-                if (more && g >= NG - 2) {
-                    dma_piece(min(st + 2, nsteps - 1), buf, 2 * (g - (NG - 2)));
-                    dma_piece(min(st + 2, nsteps - 1), buf, 2 * (g - (NG - 2)) + 1);
-                }
-                h8 a2 = a1;
-                if (g + 2 < NG) a2 = read_a(buf, g + 2);
-                else if (more) a2 = read_a(nbuf, g + 2 - NG);
-                const h8 acur = a0;
-#pragma unroll
-                for (int nt = 0; nt < 4; nt++)
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bq[nt], acur, acc[mt][nt], 0, 0, 0);
-                // the next chunk's 4 weight operands, spread over the groups
-                if (MT == 8 ? (mt & 1) : true) {
-                    const int nt = MT == 8 ? (mt >> 1) : mt;
-                    if (c < 3) bn[nt] = dequant(c + 1, nt);
-                    else if (more) bn[nt] = dequant(0, nt);
-                }
-                a0 = a1;
-                a1 = a2;
+            h8 a2 = a1;
+            if (g + 2 < 16) a2 = read_a(buf, (g + 2) >> 3, (g + 2) & 7);
+            else if (MORE) a2 = read_a(nbuf, 0, g - 14);
+            if (MORE && g >= 14) {
+                dma_act(s + 2, 2 * (g - 14));
+                dma_act(s + 2, 2 * (g - 14) + 1);
             }
-            // per group: 4 MFMAs, one operand read, the group's share of
-            // the dequantisation (VPS VALU instructions after each MFMA)
-            constexpr int VPS = MT == 8 ? 2 : 3;
+            const h8 acur = a0;
+            const h8 *bw = c ? b1 : bq;
 #pragma unroll
-            for (int i = 0; i < MT; i++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-                __builtin_amdgcn_sched_group_barrier(0x002, VPS, 0);  // VALU
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, VPS, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, VPS, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, VPS, 0);
+            for (int nt = 0; nt < 4; nt++)
+                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bw[nt], acur, acc[mt][nt], 0, 0, 0);
+            if (c == 0 && (mt & 1)) b1[mt >> 1] = dequant(1, mt >> 1);
+            if (MORE && g >= 14) {
+                bq[2 * (g - 14)] = dequant(0, 2 * (g - 14));
+                bq[2 * (g - 14) + 1] = dequant(0, 2 * (g - 14) + 1);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            if (c < 3 || more) {
-#pragma unroll
-                for (int nt = 0; nt < 4; nt++) bq[nt] = bn[nt];
-            }
+            a0 = a1;
+            a1 = a2;
         }
+        __builtin_amdgcn_sched_barrier(0);
     };
-    for (int st = 0; st + 1 < nsteps; st++) step(st, pf_true{});
-    step(nsteps - 1, pf_false{});
+    for (int sb = 0; sb + 1 < nb; sb++) {
+        step(2 * sb, p8_step<0, true>{});
+        step(2 * sb + 1, p8_step<1, true>{});
+    }
+    step(ns - 2, p8_step<0, true>{});
+    step(ns - 1, p8_step<1, false>{});
 
-    // The weights are the MFMA A operand, so tile (mt, nt) has weight rows
-    // as its rows: lane (r16, q) holds outputs o = 16 nt + 4q + i (i = 0..3)
-    // of token t = 16 mt + r16 — four consecutive outputs of one token, one
-    // 16-byte store. The unscale vector is padded to whole 128-token tiles,
-    // which cover whole 64-token tiles too.
-    float us[MT];
+    // Partial sums: group kg keeps token tiles 4 kg .. 4 kg + 3 and hands the
+    // other four to the partner wavefront (same rows, other group) through
+    // LDS; each lane then holds both groups' sums of its outputs.
+    p8_barrier_vm0();  // the reload copies of the last steps have landed; every stage read is done
+    f4 *xch = reinterpret_cast<f4 *>(smem);
+    auto xidx = [&](int g, int i) { return ((g * 4 + wr) * 16 + i) * 64 + lane; };
+    if (kg == 0) {
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) us[mt] = unscale[t0 + mt * 16 + r16];
-    const int ow = n0 + wv * kPfRowsWave + 4 * q;
-    const bool vec = (out_dim & 3) == 0;
+        for (int i = 0; i < 16; i++) xch[xidx(0, i)] = acc[4 + (i >> 2)][i & 3];
+    } else {
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        const int t = t0 + mt * 16 + r16;
+        for (int i = 0; i < 16; i++) xch[xidx(1, i)] = acc[i >> 2][i & 3];
+    }
+    __syncthreads();
+    f4 res[4][4];
+    if (kg == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) res[i >> 2][i & 3] = acc[i >> 2][i & 3] + xch[xidx(1, i)];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) res[i >> 2][i & 3] = acc[4 + (i >> 2)][i & 3] + xch[xidx(0, i)];
+    }
+    // lane (r16, q) holds outputs o = 16 nt + 4q + i of token 16 mt + r16
+    const int ow = n0 + 64 * wr + 4 * q;
+    const bool vec = ((out_dim | ld_out) & 3) == 0;
+#pragma unroll
+    for (int ml = 0; ml < 4; ml++) {
+        const int tl = 16 * (4 * kg + ml) + r16;
+        const int t = t0 + tl;
         if (t >= n_tok) continue;
-        float *orow = out + (size_t)t * out_dim;
+        const float us = unscale[t];
+        float *orow = out + (size_t)t * ld_out;
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) {
             const int o = ow + 16 * nt;
-            const f4 v = acc[mt][nt] * us[mt];
+            const f4 v = res[ml][nt] * us;
             if (vec && o + 3 < out_dim) {
                 *reinterpret_cast<f4 *>(orow + o) = v;
             } else {
@@ -491,24 +501,29 @@ size_t prefill_scratch_bytes(int n_tok, int in_dim) {
     return ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16 + tiles * kPfTok * 4;
 }
 
-// The GEMM on TOK-token workgroup tiles (the dynamic LDS size set once)
-template <int TOK>
+// One GEMM launch on the pre-pass's image
 static hipError_t prefill_gemm(const uint8_t *w, const _Float16 *xh, const float *unscale,
-                               float *out, int n_tok, int in_dim, int out_dim, hipStream_t s) {
-    static const hipError_t attr = hipFuncSetAttribute(
-        (const void *)k_prefill_q4k<TOK>, hipFuncAttributeMaxDynamicSharedMemorySize, pf_lds(TOK));
-    if (attr != hipSuccess) return attr;
+                               float *out, int n_tok, int in_dim, int out_dim, int ld_out,
+                               hipStream_t s) {
     const dim3 grid((unsigned)((out_dim + kPfRowsWg - 1) / kPfRowsWg),
-                    (unsigned)((n_tok + TOK - 1) / TOK));
-    k_prefill_q4k<TOK><<<grid, 256, pf_lds(TOK), s>>>(w, xh, unscale, out, n_tok, in_dim, out_dim);
+                    (unsigned)((n_tok + kPfTok - 1) / kPfTok));
+    k_prefill_q4k_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, n_tok, in_dim, out_dim, ld_out);
     return hipGetLastError();
 }
 
-// The GEMM on the pre-pass's image; x is bf16 (x_bf16) or f32 (x_f32).
+// The pre-pass, then the GEMM; x is bf16 (x_bf16) or f32 (x_f32). The
+// kernels address weights with 32-bit byte offsets and the activation image
+// with 32-bit byte offsets too, so a call whose weights pass 4 GiB or whose
+// image passes 2 GiB runs as several launches over row and token ranges
+// (whole 256-row and 128-token tiles).
 static hipError_t prefill_q4k(const uint8_t *w, const uint16_t *x_bf16, const float *x_f32,
                               uint8_t *scratch, float *out, int n_tok, int in_dim, int out_dim,
                               hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
+    const size_t row_bytes = (size_t)(in_dim / 256) * kQ4kBytes;
+    const size_t rows_max = (size_t)UINT32_MAX / row_bytes / kPfRowsWg * kPfRowsWg;
+    const size_t toks_max = (size_t)INT32_MAX / ((size_t)in_dim * 2) / kPfTok * kPfTok;
+    if (rows_max == 0 || toks_max == 0) return hipErrorInvalidValue;
     const size_t xb = ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16;
     _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
     float *unscale = reinterpret_cast<float *>(scratch + xb);
@@ -518,12 +533,16 @@ static hipError_t prefill_q4k(const uint8_t *w, const uint16_t *x_bf16, const fl
         k_prefill_x<<<(unsigned)n_tok, 256, 0, s>>>(x_bf16, xh, unscale, in_dim);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // 128-token tiles unless that grid fills under 160 of the 256 CUs: then
-    // 64-token tiles, two workgroups per CU (C4 at T = 100: 52 us instead of
-    // 68; at T = 512, 224 workgroups, the 128-token tile is 10% faster)
-    const size_t g128 = (size_t)((out_dim + kPfRowsWg - 1) / kPfRowsWg) * (size_t)((n_tok + 127) / 128);
-    if (g128 < 160) return prefill_gemm<64>(w, xh, unscale, out, n_tok, in_dim, out_dim, s);
-    return prefill_gemm<128>(w, xh, unscale, out, n_tok, in_dim, out_dim, s);
+    for (size_t t0 = 0; t0 < (size_t)n_tok; t0 += toks_max) {
+        const int nt = (int)std::min(toks_max, (size_t)n_tok - t0);
+        for (size_t r0 = 0; r0 < (size_t)out_dim; r0 += rows_max) {
+            const int nr = (int)std::min(rows_max, (size_t)out_dim - r0);
+            e = prefill_gemm(w + r0 * row_bytes, xh + t0 * in_dim, unscale + t0,
+                             out + t0 * out_dim + r0, nt, in_dim, nr, out_dim, s);
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *x_bf16,

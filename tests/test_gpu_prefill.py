@@ -101,12 +101,26 @@ def test_prefill_special_blocks(oracle, hip):
     check(oracle, got, w, xb, np.arange(n_tok), n_tok, in_dim, out_dim, per_token=False)
 
 
+def test_prefill_many_tiles_ragged(oracle, hip):
+    """16 row tiles (the last of 160 rows) x 11 token tiles (the last of one
+    token), an odd number of super-blocks per row (3: the K loop's tail of a
+    single super-block): tokens on both sides of every token-tile edge and the
+    last one are checked against the oracle."""
+    out_dim, in_dim, n_tok = 4000, 768, 1281
+    w = synth.weight(G.Q4_K, out_dim, in_dim, seed=4000)
+    xb = synth.bf16_activations(n_tok, in_dim, seed=4001).reshape(-1)
+    got = run_prefill(hip, w, xb, n_tok, in_dim, out_dim)
+    edges = np.arange(128, n_tok, 128)
+    tokens = np.unique(np.concatenate([[0, 1, n_tok - 1], edges - 1, edges]))
+    check(oracle, got, w, xb, tokens, n_tok, in_dim, out_dim)
+
+
 @pytest.mark.parametrize("n_tok", [100, 512, 2048])
 def test_prefill_config_shape(oracle, hip, n_tok):
     """Config C4: Q4_K (out, in) = (14336, 4096), T in {512, 2048}, and T = 100
-    (a grid that takes the 64-token workgroup tile). The oracle runs on a
-    spread subset of tokens (every token's output is independent), both
-    sides of the 64- and 128-token tile edges included."""
+    (one partial 128-token tile). The oracle runs on a spread subset of
+    tokens (every token's output is independent), both sides of the 64- and
+    128-token boundaries included."""
     out_dim, in_dim = 14336, 4096
     w = synth.weight(G.Q4_K, out_dim, in_dim, seed=404)
     xb = synth.bf16_activations(n_tok, in_dim, seed=405).reshape(-1)
