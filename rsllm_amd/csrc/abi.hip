@@ -838,7 +838,7 @@ int rsllm_hip_matmul_q4k_bf16_dev(float *out, size_t out_len, const uint8_t *wei
     }
     if ((rc = ensure_device())) return rc;
     ScratchLease sc = stream_scratch(s);
-    HIP_TRY(sc->xh.ensure(prefill_scratch_bytes((int)n_tok, (int)in_dim)), "hipMalloc");
+    HIP_TRY(sc->xh.ensure(prefill_scratch_bytes((int)n_tok, (int)in_dim, (int)out_dim)), "hipMalloc");
     HIP_TRY(launch_prefill_q4k(weights, weights_len, x_bf16, (uint8_t *)sc->xh.p, out,
                                (int)n_tok, (int)in_dim, (int)out_dim, s),
             "prefill_q4k");

@@ -600,7 +600,7 @@ static Prefill prefill_route(uint32_t dtype, int n_tok, int in_dim) {
 
 size_t gemv_work_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
     switch (prefill_route(dtype, n_tok, in_dim)) {
-    case Prefill::gemm_q4k: return prefill_scratch_bytes(n_tok, in_dim);
+    case Prefill::gemm_q4k: return prefill_scratch_bytes(n_tok, in_dim, out_dim);
     case Prefill::mfma_chunks: return gemv_mfma_scratch_bytes(dtype, 32, in_dim, out_dim);
     default: break;
     }

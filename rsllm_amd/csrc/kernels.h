@@ -181,9 +181,10 @@ hipError_t launch_lora_mfma(uint32_t dtype, const uint8_t *w, size_t w_bytes, co
 // prefill.hip: out[t, o] = sum_i deq(W)[o, i] * x[t, i] for a raw GGUF Q4_K
 // weight W [out_dim x in_dim] and bf16 activations x [n_tok x in_dim]
 // (n_tok x out_dim fp32 output, overwritten). `scratch` holds
-// prefill_scratch_bytes(n_tok, in_dim) bytes (scaled f16 activations and
-// per-token scales).
-size_t prefill_scratch_bytes(int n_tok, int in_dim);
+// prefill_scratch_bytes(n_tok, in_dim, out_dim) bytes (scaled f16
+// activations, per-token scales, and the partial sums of a call whose K is
+// split across workgroups).
+size_t prefill_scratch_bytes(int n_tok, int in_dim, int out_dim);
 hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *x_bf16,
                               uint8_t *scratch, float *out, int n_tok, int in_dim, int out_dim,
                               hipStream_t s);

@@ -26,6 +26,8 @@
 #include <algorithm>
 #include <climits>
 
+#include "../../include/rsllm_hip.h"
+
 namespace rsllm_hip {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -268,10 +270,16 @@ template <int PAR, bool MORE> struct p8_step {
     static constexpr bool more = MORE;  // a next step exists
 };
 
+//
+// K split (blockIdx.z of gridDim.z splits): split z covers super-blocks
+// [z nbt / S, (z + 1) nbt / S) of the nbt in a row and writes its sums to
+// `out` (z = 0) or to slice z - 1 of `part` (n_tok x ld_out each), which
+// k_prefill_sum then adds into `out` in split order.
 __global__ __launch_bounds__(512) void k_prefill_q4k_w8(const uint8_t *__restrict__ w,
                                                         const _Float16 *__restrict__ xh,
                                                         const float *__restrict__ unscale,
-                                                        float *__restrict__ out, int n_tok,
+                                                        float *__restrict__ out,
+                                                        float *__restrict__ part, int n_tok,
                                                         int in_dim, int out_dim, int ld_out) {
     __shared__ __align__(16) uint8_t smem[kP8Lds];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -279,11 +287,17 @@ __global__ __launch_bounds__(512) void k_prefill_q4k_w8(const uint8_t *__restric
     const int wr = wv & 3, kg = wv >> 2;
     const int r16 = lane & 15, q = lane >> 4;
     const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
-    const int nb = in_dim >> 8;
-    const int ns = 2 * nb;  // steps of one K group
+    const int nbt = in_dim >> 8;  // super-blocks in a row
+    const int z = blockIdx.z, nz = gridDim.z;
+    const int kb0 = (int)((long)z * nbt / nz);
+    const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;  // super-blocks of this split (>= 1)
+    const int ns = 2 * nb;                                 // steps of one K group
+    w += (size_t)kb0 * kQ4kBytes;
+    xh += (size_t)kb0 * 256;
+    if (z > 0) out = part + (size_t)(z - 1) * n_tok * ld_out;
     uint8_t *const act = smem + kP8ActOff + 2 * kg * kP8Act;  // this group's two step buffers
     uint8_t *const scl = smem + kP8ScOff + kg * kPfRowsWg * 16;
-    const uint32_t row_bytes = (uint32_t)nb * (uint32_t)kQ4kBytes;
+    const uint32_t row_bytes = (uint32_t)nbt * (uint32_t)kQ4kBytes;
 
     // DMA sources (bytes from a uniform base). Activations: instruction p
     // moves token rows 8 (4 wr + p) .. + 7 of this group's quarter, lane i to
@@ -471,7 +485,7 @@ __global__ __launch_bounds__(512) void k_prefill_q4k_w8(const uint8_t *__restric
     }
     // lane (r16, q) holds outputs o = 16 nt + 4q + i of token 16 mt + r16
     const int ow = n0 + 64 * wr + 4 * q;
-    const bool vec = ((out_dim | ld_out) & 3) == 0;
+    const bool vec = ((out_dim | ld_out) & 3) == 0 && ((uintptr_t)out & 15) == 0;
 #pragma unroll
     for (int ml = 0; ml < 4; ml++) {
         const int tl = 16 * (4 * kg + ml) + r16;
@@ -494,20 +508,65 @@ __global__ __launch_bounds__(512) void k_prefill_q4k_w8(const uint8_t *__restric
     }
 }
 
-size_t prefill_scratch_bytes(int n_tok, int in_dim) {
-    // f16 activations, then one f32 unscale per token padded to whole
-    // 128-token tiles (16-byte aligned)
-    const size_t tiles = ((size_t)n_tok + kPfTok - 1) / kPfTok;
-    return ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16 + tiles * kPfTok * 4;
+// out[i] += part[z][i] for z = 0 .. nz - 1 in order (n floats per slice)
+__global__ __launch_bounds__(256) void k_prefill_sum(float *__restrict__ out,
+                                                     const float *__restrict__ part, size_t n,
+                                                     int nz) {
+    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const bool vec = (n & 3) == 0 && ((uintptr_t)out & 15) == 0;  // part is 16-byte aligned
+    if (vec && i4 * 4 + 3 < n) {
+        f4 v = *reinterpret_cast<const f4 *>(out + i4 * 4);
+        for (int z = 0; z < nz; z++) v += *reinterpret_cast<const f4 *>(part + z * n + i4 * 4);
+        *reinterpret_cast<f4 *>(out + i4 * 4) = v;
+    } else {
+        for (size_t i = i4 * 4; i < n; i++) {
+            float v = out[i];
+            for (int z = 0; z < nz; z++) v += part[z * n + i];
+            out[i] = v;
+        }
+    }
 }
 
-// One GEMM launch on the pre-pass's image
+// K splits of a call: grids of fewer than 128 workgroups (one per CU, 256
+// CUs) split K into as many as keep the grid within one round of 256
+// workgroups (a partial second round costs more than the split gains), each
+// split keeping at least two super-blocks, at most 16 splits, and only where
+// the partial sums keep the whole workspace within the no-allocation entry
+// point's maximum (so a call that fits it without splitting still fits).
+// Calls that need more than one launch (32-bit offsets, below) are not split.
+static int prefill_splits(int n_tok, int in_dim, int out_dim) {
+    const size_t rt = (size_t)(out_dim + kPfRowsWg - 1) / kPfRowsWg;
+    const size_t tt = ((size_t)n_tok + kPfTok - 1) / kPfTok;
+    const size_t grid = rt * tt, nbt = (size_t)in_dim / 256;
+    if (grid >= 128 || nbt < 4) return 1;
+    const size_t row_bytes = nbt * kQ4kBytes;
+    if ((size_t)out_dim * row_bytes > UINT32_MAX || (size_t)n_tok * in_dim * 2 > INT32_MAX) return 1;
+    size_t nz = std::min<size_t>({256 / grid, nbt / 2, 16});
+    const size_t base = ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16 + tt * kPfTok * 4;
+    while (nz > 1 && base + (nz - 1) * (size_t)n_tok * out_dim * 4 > RSLLM_HIP_NOALLOC_SCRATCH_BYTES) nz--;
+    return (int)nz;
+}
+
+size_t prefill_scratch_bytes(int n_tok, int in_dim, int out_dim) {
+    // f16 activations, one f32 unscale per token padded to whole 128-token
+    // tiles (16-byte aligned), then the partial sums of splits 1 .. S - 1
+    const size_t tiles = ((size_t)n_tok + kPfTok - 1) / kPfTok;
+    const size_t nz = (size_t)prefill_splits(n_tok, in_dim, out_dim);
+    return ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16 + tiles * kPfTok * 4 +
+           (nz - 1) * (size_t)n_tok * out_dim * 4;
+}
+
+// One GEMM launch on the pre-pass's image (nz K splits: partial sums in part)
 static hipError_t prefill_gemm(const uint8_t *w, const _Float16 *xh, const float *unscale,
-                               float *out, int n_tok, int in_dim, int out_dim, int ld_out,
-                               hipStream_t s) {
+                               float *out, float *part, int nz, int n_tok, int in_dim, int out_dim,
+                               int ld_out, hipStream_t s) {
     const dim3 grid((unsigned)((out_dim + kPfRowsWg - 1) / kPfRowsWg),
-                    (unsigned)((n_tok + kPfTok - 1) / kPfTok));
-    k_prefill_q4k_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, n_tok, in_dim, out_dim, ld_out);
+                    (unsigned)((n_tok + kPfTok - 1) / kPfTok), (unsigned)nz);
+    k_prefill_q4k_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || nz == 1) return e;
+    const size_t n = (size_t)n_tok * out_dim;
+    k_prefill_sum<<<(unsigned)((n + 1023) / 1024), 256, 0, s>>>(out, part, n, nz - 1);
     return hipGetLastError();
 }
 
@@ -524,21 +583,24 @@ static hipError_t prefill_q4k(const uint8_t *w, const uint16_t *x_bf16, const fl
     const size_t rows_max = (size_t)UINT32_MAX / row_bytes / kPfRowsWg * kPfRowsWg;
     const size_t toks_max = (size_t)INT32_MAX / ((size_t)in_dim * 2) / kPfTok * kPfTok;
     if (rows_max == 0 || toks_max == 0) return hipErrorInvalidValue;
+    const size_t tiles = ((size_t)n_tok + kPfTok - 1) / kPfTok;
     const size_t xb = ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16;
     _Float16 *xh = reinterpret_cast<_Float16 *>(scratch);
     float *unscale = reinterpret_cast<float *>(scratch + xb);
+    float *part = unscale + tiles * kPfTok;
     if (x_f32)
         k_prefill_x_f32<<<(unsigned)n_tok, 256, 0, s>>>(x_f32, xh, unscale, in_dim);
     else
         k_prefill_x<<<(unsigned)n_tok, 256, 0, s>>>(x_bf16, xh, unscale, in_dim);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    const int nz = prefill_splits(n_tok, in_dim, out_dim);
     for (size_t t0 = 0; t0 < (size_t)n_tok; t0 += toks_max) {
         const int nt = (int)std::min(toks_max, (size_t)n_tok - t0);
         for (size_t r0 = 0; r0 < (size_t)out_dim; r0 += rows_max) {
             const int nr = (int)std::min(rows_max, (size_t)out_dim - r0);
             e = prefill_gemm(w + r0 * row_bytes, xh + t0 * in_dim, unscale + t0,
-                             out + t0 * out_dim + r0, nt, in_dim, nr, out_dim, s);
+                             out + t0 * out_dim + r0, part, nz, nt, in_dim, nr, out_dim, s);
             if (e != hipSuccess) return e;
         }
     }

@@ -115,6 +115,26 @@ def test_prefill_many_tiles_ragged(oracle, hip):
     check(oracle, got, w, xb, tokens, n_tok, in_dim, out_dim)
 
 
+@pytest.mark.parametrize("out_dim,in_dim,n_tok", [(4096, 14336, 300), (700, 2304, 40),
+                                                  (2048, 4096, 200)])
+def test_prefill_k_split(oracle, hip, out_dim, in_dim, n_tok):
+    """Grids of fewer than 128 workgroups split K across workgroups and add
+    the partial sums in split order: the FFN-down shape (4096 rows, K =
+    14336: 5 splits of 11 or 12 super-blocks), 9 super-blocks in 4 uneven
+    splits with a ragged last row tile, and 2048 x 4096 (8 splits of 2
+    super-blocks).
+    Results are deterministic: a second call gives the same bits."""
+    w = synth.weight(G.Q4_K, out_dim, in_dim, seed=out_dim + in_dim)
+    xb = synth.bf16_activations(n_tok, in_dim, seed=n_tok + 3).reshape(-1)
+    got = run_prefill(hip, w, xb, n_tok, in_dim, out_dim)
+    again = run_prefill(hip, w, xb, n_tok, in_dim, out_dim)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    tokens = np.unique(np.concatenate([np.arange(0, 4), np.linspace(0, n_tok - 1, 12).astype(int),
+                                       [127, 128, n_tok - 1]]))
+    tokens = tokens[tokens < n_tok]
+    check(oracle, got, w, xb, tokens, n_tok, in_dim, out_dim)
+
+
 @pytest.mark.parametrize("n_tok", [100, 512, 2048])
 def test_prefill_config_shape(oracle, hip, n_tok):
     """Config C4: Q4_K (out, in) = (14336, 4096), T in {512, 2048}, and T = 100
