@@ -159,6 +159,37 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
                               "tokens_checked": len(toks), "tolerance": 1e-3}
         res["f32_x"].append(entry)
         del d_x, d_y
+    # Grids under half the CUs (short prompts, few-row matrices): K split
+    # across workgroups, partial sums added in split order. The FFN-down
+    # shape (in 14336 -> out 4096) and C4 at T = 100, through the bf16 entry.
+    res["k_split"] = []
+    for (n_out, n_in, T, seed) in ((4096, 14336, 512, 407), (14336, 4096, 100, 408)):
+        w_s = synth.weight(G.Q4_K, n_out, n_in, seed=seed) if n_out != out_dim else w_host
+        d_ws = torch.from_numpy(w_s).to(dev) if n_out != out_dim else d_w
+        xb = synth.bf16_activations(T, n_in, seed=seed + 1).reshape(-1)
+        d_x = torch.from_numpy(xb.view(np.int16)).to(dev)
+        d_y = torch.empty(T * n_out, dtype=torch.float32, device=dev)
+
+        def call_s(i):
+            B.matmul_q4k_bf16_dev(d_y.data_ptr(), d_y.numel(), d_ws.data_ptr(), d_ws.numel(),
+                                  d_x.data_ptr(), d_x.numel(), T, n_in, n_out, G.Q4_K, sptr)
+        for i in range(3):
+            call_s(i)
+        us = _time(call_s, iters, stream)
+        tflops = 2.0 * T * n_in * n_out / (us * 1e-6) / 1e12
+        entry = {"shape": f"{n_out}x{n_in}", "tokens": T, "us_per_op": round(us, 2),
+                 "tflops": round(tflops, 1), "frac_of_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+        if with_cpu:
+            from oracle import oracle as O
+            toks = np.linspace(0, T - 1, 6).astype(int)
+            xf = synth.bf16_bits_to_f32(xb.reshape(T, n_in)[toks]).reshape(-1)
+            rc, want = O.matmul_quant_f32(w_s, xf, len(toks), n_in, n_out, int(G.Q4_K))
+            got = d_y.cpu().numpy().reshape(T, n_out)[toks].reshape(-1)
+            entry["check"] = {"max_rel_err_vs_oracle": float(np.abs(got - want).max() /
+                                                             np.abs(want).max()),
+                              "tokens_checked": len(toks), "tolerance": 1e-3}
+        res["k_split"].append(entry)
+        del d_x, d_y, d_ws
     res["mfma_ceiling"] = bench_mfma_ceiling(B, dev, stream)
     res["dense_f16_library"] = bench_dense_f16(dev, stream, out_dim, in_dim, iters)
     if with_cpu:
