@@ -14,6 +14,8 @@
 //   k_quant_swiglu  SwiGLU of the gate/up outputs fused with the pre-pass.
 #include "gemv_formats.h"
 
+#include <algorithm>
+
 namespace rsllm_hip {
 
 // One thread per 16-element group: thread (lane, half) of column `col` writes
@@ -586,21 +588,24 @@ size_t gemv_scratch_bytes(uint32_t dtype, int n_tok, int in_dim) {
     }
 }
 
-// Routes for more than 32 tokens (prefill, n_tok = T): Q4_K with in_dim a
-// multiple of 256 takes the prefill GEMM; Q6_K / Q8_0 with in_dim a multiple
-// of 256 the exact matrix-core GEMV over 32-token chunks (one weight pass per
-// 32 tokens instead of per 8 on the int8-limb GEMV).
-enum class Prefill { none, gemm_q4k, mfma_chunks };
+// Routes for more than 32 tokens (prefill, n_tok = T): Q4_K and Q8_0 with
+// in_dim a multiple of 256 take the prefill GEMM; Q6_K with in_dim a
+// multiple of 256 the exact matrix-core GEMV over 32-token chunks (one weight
+// pass per 32 tokens instead of per 8 on the int8-limb GEMV).
+enum class Prefill { none, gemm, mfma_chunks };
 static Prefill prefill_route(uint32_t dtype, int n_tok, int in_dim) {
     if (n_tok <= 32 || in_dim <= 0 || in_dim % 256 != 0) return Prefill::none;
-    if (dtype == T_Q4_K) return Prefill::gemm_q4k;
-    if (dtype == T_Q6_K || dtype == T_Q8_0) return Prefill::mfma_chunks;
+    if (dtype == T_Q4_K || dtype == T_Q8_0) return Prefill::gemm;
+    if (dtype == T_Q6_K) return Prefill::mfma_chunks;
     return Prefill::none;
 }
 
 size_t gemv_work_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
     switch (prefill_route(dtype, n_tok, in_dim)) {
-    case Prefill::gemm_q4k: return prefill_scratch_bytes(n_tok, in_dim, out_dim);
+    case Prefill::gemm:
+        // the GEMM, or the int8-limb GEMV where w or x is not 16-byte aligned
+        return std::max(prefill_scratch_bytes(n_tok, in_dim, out_dim),
+                        gemv_scratch_bytes(dtype, n_tok, in_dim));
     case Prefill::mfma_chunks: return gemv_mfma_scratch_bytes(dtype, 32, in_dim, out_dim);
     default: break;
     }
@@ -924,10 +929,10 @@ hipError_t launch_gemv(uint32_t dtype, const uint8_t *w, size_t w_bytes, const f
                        hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
     switch (prefill_route(dtype, n_tok, in_dim)) {
-    case Prefill::gemm_q4k:
+    case Prefill::gemm:
         // the GEMM's global->LDS copies move 16-byte pieces
         if ((((uintptr_t)w | (uintptr_t)x) & 15) == 0)
-            return launch_prefill_q4k_f32(w, x, xq_scratch, y, n_tok, in_dim, out_dim, s);
+            return launch_prefill_f32(dtype, w, x, xq_scratch, y, n_tok, in_dim, out_dim, s);
         break;
     case Prefill::mfma_chunks:
         // every chunk, a short tail included, on the matrix cores (which pad

@@ -189,10 +189,11 @@ hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *
                               uint8_t *scratch, float *out, int n_tok, int in_dim, int out_dim,
                               hipStream_t s);
 // The same GEMM on f32 activations x [n_tok x in_dim] (16-byte aligned; w
-// 16-byte aligned): each element rounded once to f16 after the per-token
-// 2^e scaling. Same scratch.
-hipError_t launch_prefill_q4k_f32(const uint8_t *w, const float *x, uint8_t *scratch, float *out,
-                                  int n_tok, int in_dim, int out_dim, hipStream_t s);
+// 16-byte aligned) for a Q4_K weight (GGUF bytes) or a Q8_0 weight (device
+// layout), in_dim a multiple of 256: each element of x rounded once to f16
+// after the per-token 2^e scaling. Same scratch.
+hipError_t launch_prefill_f32(uint32_t dtype, const uint8_t *w, const float *x, uint8_t *scratch,
+                              float *out, int n_tok, int in_dim, int out_dim, hipStream_t s);
 
 // moe.hip: routed experts (accumulate_moe_outputs). Expert e of gate/up is
 // at gate/up + e * gu_stride, of down at down + e * d_stride (device

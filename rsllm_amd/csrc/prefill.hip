@@ -265,6 +265,60 @@ __device__ __forceinline__ void p8_barrier_vm5() {
     asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// The end of an 8-wavefront workgroup (256 rows x 128 tokens, two K groups
+// holding partial sums of the same outputs): group kg keeps token tiles
+// 4 kg .. 4 kg + 3 and hands the other four to the partner wavefront (same
+// rows, other group) through LDS (128 KB of the kernel's LDS, free once every
+// copy has landed and every stage read is done); each lane then adds both
+// groups' sums of its outputs, scales them by the token's 2^-e and stores
+// them: lane (r16, q) holds outputs 16 nt + 4q .. + 3 of token 16 mt + r16.
+__device__ __forceinline__ void p8_epilogue(f4 (&acc)[8][4], uint8_t *smem, int kg, int wr,
+                                            int lane, int n0, int t0, float *out,
+                                            const float *unscale, int n_tok, int out_dim,
+                                            int ld_out) {
+    const int r16 = lane & 15, q = lane >> 4;
+    p8_barrier_vm0();
+    f4 *xch = reinterpret_cast<f4 *>(smem);
+    auto xidx = [=](int g, int i) { return ((g * 4 + wr) * 16 + i) * 64 + lane; };
+    if (kg == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) xch[xidx(0, i)] = acc[4 + (i >> 2)][i & 3];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) xch[xidx(1, i)] = acc[i >> 2][i & 3];
+    }
+    __syncthreads();
+    f4 res[4][4];
+    if (kg == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) res[i >> 2][i & 3] = acc[i >> 2][i & 3] + xch[xidx(1, i)];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) res[i >> 2][i & 3] = acc[4 + (i >> 2)][i & 3] + xch[xidx(0, i)];
+    }
+    const int ow = n0 + 64 * wr + 4 * q;
+    const bool vec = ((out_dim | ld_out) & 3) == 0 && ((uintptr_t)out & 15) == 0;
+#pragma unroll
+    for (int ml = 0; ml < 4; ml++) {
+        const int t = t0 + 16 * (4 * kg + ml) + r16;
+        if (t >= n_tok) continue;
+        const float us = unscale[t];
+        float *orow = out + (size_t)t * ld_out;
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) {
+            const int o = ow + 16 * nt;
+            const f4 v = res[ml][nt] * us;
+            if (vec && o + 3 < out_dim) {
+                *reinterpret_cast<f4 *>(orow + o) = v;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (o + i < out_dim) orow[o + i] = v[i];
+            }
+        }
+    }
+}
+
 template <int PAR, bool MORE> struct p8_step {
     static constexpr int par = PAR;    // step parity within the super-block
     static constexpr bool more = MORE;  // a next step exists
@@ -461,51 +515,190 @@ __global__ __launch_bounds__(512) void k_prefill_q4k_w8(const uint8_t *__restric
     step(ns - 2, p8_step<0, true>{});
     step(ns - 1, p8_step<1, false>{});
 
-    // Partial sums: group kg keeps token tiles 4 kg .. 4 kg + 3 and hands the
-    // other four to the partner wavefront (same rows, other group) through
-    // LDS; each lane then holds both groups' sums of its outputs.
-    p8_barrier_vm0();  // the reload copies of the last steps have landed; every stage read is done
-    f4 *xch = reinterpret_cast<f4 *>(smem);
-    auto xidx = [&](int g, int i) { return ((g * 4 + wr) * 16 + i) * 64 + lane; };
-    if (kg == 0) {
+    p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out);
+}
+
+// ---- Q8_0 weights ----------------------------------------------------------------
+// k_prefill_q8_w8: the workgroup of k_prefill_q4k_w8 (256 rows x 128 tokens,
+// 8 wavefronts, two K groups on alternate quarters of each 256 elements, the
+// same activation stages, epilogue and K split) on Q8_0 weights in this
+// backend's device layout: super-tiles of 8 blocks [qs 8 x 32 | d 8 x 2], 272
+// bytes per 256 elements of a row. A super-tile of 256 rows is 68 KB, too
+// large to keep two beside the activations, so the weights are staged per
+// K-group step with the activations: the quarter's two blocks' qs (64 bytes
+// per row; the four 16-byte pieces of row r in slot p ^ ((r >> 2) & 3), so
+// the operand reads of 16 rows hit distinct banks) and the row's 16-byte d
+// run. Chunk c of quarter u is block 2u + c; lane group q holds its bytes
+// 8q .. 8q + 7. w = f16(d * q): the byte ^ 0x80 paired with 0x64 is
+// 1152 + q exactly in f16, minus 1152 leaves q, and one multiply by the f16
+// d rounds once (about 2^-11 relative, as the Q4_K weights).
+constexpr int kQ8Qs = kPfRowsWg * 64;            // 16 KB
+constexpr int kQ8D = kPfRowsWg * 16;             // 4 KB
+constexpr int kQ8Stage = kP8Act + kQ8Qs + kQ8D;  // 36 KB per group step
+constexpr int kQ8Lds = 4 * kQ8Stage;             // 144 KB
+static_assert(2 * 4 * 16 * 64 * 16 <= kQ8Lds, "the epilogue's exchange fits");
+
+__global__ __launch_bounds__(512) void k_prefill_q8_w8(const uint8_t *__restrict__ w,
+                                                       const _Float16 *__restrict__ xh,
+                                                       const float *__restrict__ unscale,
+                                                       float *__restrict__ out,
+                                                       float *__restrict__ part, int n_tok,
+                                                       int in_dim, int out_dim, int ld_out) {
+    __shared__ __align__(16) uint8_t smem[kQ8Lds];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wv & 3, kg = wv >> 2;
+    const int r16 = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
+    const int nbt = in_dim >> 8;  // super-tiles in a row
+    const int z = blockIdx.z, nz = gridDim.z;
+    const int kb0 = (int)((long)z * nbt / nz);
+    const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;
+    const int ns = 2 * nb;
+    w += (size_t)kb0 * 272;
+    xh += (size_t)kb0 * 256;
+    if (z > 0) out = part + (size_t)(z - 1) * n_tok * ld_out;
+    uint8_t *const stg = smem + 2 * kg * kQ8Stage;  // this group's two step buffers
+    const uint32_t row_bytes = (uint32_t)nbt * 272u;
+
+    // DMA sources (bytes from a uniform base). Activations as in
+    // k_prefill_q4k_w8. qs: instruction p moves rows 16 (4 wr + p) .. + 15,
+    // lane i to row 16 (4 wr + p) + i / 4, slot i % 4 (holding piece
+    // (i % 4) ^ ((row >> 2) & 3) of the quarter's 64 bytes). d: lane i moves
+    // row 64 wr + i's 16-byte d run. Both cover exactly this wavefront's rows.
+    uint32_t xoff[4], qoff[4];
 #pragma unroll
-        for (int i = 0; i < 16; i++) xch[xidx(0, i)] = acc[4 + (i >> 2)][i & 3];
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; i++) xch[xidx(1, i)] = acc[i >> 2][i & 3];
+    for (int p = 0; p < 4; p++) {
+        const int tl = 8 * (4 * wr + p) + (lane >> 3);
+        const int pc = (lane & 7) ^ ((tl >> 1) & 7);
+        const int t = min(t0 + tl, n_tok - 1);
+        xoff[p] = 2u * ((uint32_t)t * (uint32_t)in_dim + 64 * kg + 32 * (pc >> 2) + 8 * (pc & 3));
+        const int row = 16 * (4 * wr + p) + (lane >> 2);
+        const int piece = (lane & 3) ^ ((row >> 2) & 3);
+        qoff[p] = (uint32_t)min(n0 + row, out_dim - 1) * row_bytes + 64u * kg + 16u * piece;
     }
-    __syncthreads();
-    f4 res[4][4];
-    if (kg == 0) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) res[i >> 2][i & 3] = acc[i >> 2][i & 3] + xch[xidx(1, i)];
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; i++) res[i >> 2][i & 3] = acc[4 + (i >> 2)][i & 3] + xch[xidx(0, i)];
-    }
-    // lane (r16, q) holds outputs o = 16 nt + 4q + i of token 16 mt + r16
-    const int ow = n0 + 64 * wr + 4 * q;
-    const bool vec = ((out_dim | ld_out) & 3) == 0 && ((uintptr_t)out & 15) == 0;
-#pragma unroll
-    for (int ml = 0; ml < 4; ml++) {
-        const int tl = 16 * (4 * kg + ml) + r16;
-        const int t = t0 + tl;
-        if (t >= n_tok) continue;
-        const float us = unscale[t];
-        float *orow = out + (size_t)t * ld_out;
+    const uint32_t doff = (uint32_t)min(n0 + 64 * wr + lane, out_dim - 1) * row_bytes + 256u;
+    const uint32_t lds_stg = p8_lds(stg);
+    // piece p (0..8) of group step s (clamped to the last) into the buffer of
+    // step parity s % 2: 0..3 activations, 4..7 qs, 8 the d run
+    auto dma = [=](int s, int p) {
+        const uint32_t buf = lds_stg + (uint32_t)((s & 1) * kQ8Stage);
+        s = min(s, ns - 1);
+        const int sb = s >> 1, hf = s & 1;
+        if (p < 4)
+            p8_dma(xh + sb * 256 + 128 * hf, xoff[p], buf + 1024 * (4 * wr + p));
+        else if (p < 8)
+            p8_dma(w + (size_t)sb * 272 + 128 * hf, qoff[p - 4], buf + kP8Act + 1024 * (4 * wr + p - 4));
+        else
+            p8_dma(w + (size_t)sb * 272, doff, buf + kP8Act + kQ8Qs + 1024 * wr);
+    };
+    const int sw = (r16 >> 2) & 3;
+    const int qb0 = 16 * ((q >> 1) ^ sw) + 8 * (q & 1);        // chunk 0: piece q / 2
+    const int qb1 = 16 * ((2 + (q >> 1)) ^ sw) + 8 * (q & 1);  // chunk 1: piece 2 + q / 2
+    const int aswz = (r16 >> 1) & 7;
+    uint2 qs0[4], qs1[4];
+    uint32_t dd[4];  // f16 d of blocks 2u, 2u + 1
+    auto load_weights = [&](const uint8_t *buf, int hf) {
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) {
-            const int o = ow + 16 * nt;
-            const f4 v = res[ml][nt] * us;
-            if (vec && o + 3 < out_dim) {
-                *reinterpret_cast<f4 *>(orow + o) = v;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (o + i < out_dim) orow[o + i] = v[i];
-            }
+            const int row = 64 * wr + 16 * nt + r16;
+            qs0[nt] = *reinterpret_cast<const uint2 *>(buf + kP8Act + 64 * row + qb0);
+            qs1[nt] = *reinterpret_cast<const uint2 *>(buf + kP8Act + 64 * row + qb1);
+            dd[nt] = *reinterpret_cast<const uint32_t *>(buf + kP8Act + kQ8Qs + 16 * row +
+                                                         4 * (2 * hf + kg));
         }
+    };
+    auto dequant = [&](int c, int nt) -> h8 {
+        const uint2 b = c ? qs1[nt] : qs0[nt];
+        const h2 d2 = __builtin_bit_cast(h2, dd[nt]);
+        const h2 ds = c ? d2.yy : d2.xx;
+        const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+        h8 r;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const uint32_t bb = (u ? b.y : b.x) ^ 0x80808080u;
+            const h2 w01 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04010400u)) - bias) * ds;
+            const h2 w23 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04030402u)) - bias) * ds;
+            r[4 * u] = w01[0];
+            r[4 * u + 1] = w01[1];
+            r[4 * u + 2] = w23[0];
+            r[4 * u + 3] = w23[1];
+        }
+        return r;
+    };
+    auto read_a = [&](const uint8_t *buf, int c, int mt) -> h8 {
+        return *reinterpret_cast<const h8 *>(buf + (16 * mt + r16) * 128 + 16 * ((4 * c + q) ^ aswz));
+    };
+
+    f4 acc[8][4];
+#pragma unroll
+    for (int mt = 0; mt < 8; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // prologue: step 0 in, step 1 in flight, step 0's chunk-0 operands ready
+#pragma unroll
+    for (int p = 0; p < 9; p++) dma(0, p);
+    p8_barrier_vm0();
+#pragma unroll
+    for (int p = 0; p < 9; p++) dma(1, p);  // ns >= 2
+    load_weights(stg, 0);
+    h8 bq[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) bq[nt] = dequant(0, nt);
+    h8 a0 = read_a(stg, 0, 0), a1 = read_a(stg, 0, 1);
+
+    // One step: as in k_prefill_q4k_w8, with the weights in the step's
+    // buffer: in group 14 every wavefront waits for its own copies of step
+    // s + 1, after the barrier reads that step's weights and first operands,
+    // and this step's buffer takes step s + 2 (pieces 0..5 in groups 14, 15,
+    // 6..8 in groups 0, 2, 4 of the next step).
+    auto step = [&](int s, auto tag) {
+        constexpr int PAR = decltype(tag)::par;
+        constexpr bool MORE = decltype(tag)::more;
+        const uint8_t *buf = stg + PAR * kQ8Stage;
+        const uint8_t *nbuf = stg + (1 - PAR) * kQ8Stage;
+        h8 b1[4];
+#pragma unroll
+        for (int g = 0; g < 16; g++) {
+            const int c = g >> 3, mt = g & 7;
+            __builtin_amdgcn_sched_barrier(0);
+            if (MORE && g < 6 && (g & 1) == 0 && s >= 1) dma(s + 1, 6 + (g >> 1));
+            if (MORE && g == 14) {
+                p8_barrier_vm0();
+                load_weights(nbuf, 1 - PAR);
+            }
+            h8 a2 = a1;
+            if (g + 2 < 16) a2 = read_a(buf, (g + 2) >> 3, (g + 2) & 7);
+            else if (MORE) a2 = read_a(nbuf, 0, g - 14);
+            if (MORE && g >= 14) {
+                dma(s + 2, 3 * (g - 14));
+                dma(s + 2, 3 * (g - 14) + 1);
+                dma(s + 2, 3 * (g - 14) + 2);
+            }
+            const h8 acur = a0;
+            const h8 *bw = c ? b1 : bq;
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++)
+                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bw[nt], acur, acc[mt][nt], 0, 0, 0);
+            if (c == 0 && (mt & 1)) b1[mt >> 1] = dequant(1, mt >> 1);
+            if (MORE && g >= 14) {
+                bq[2 * (g - 14)] = dequant(0, 2 * (g - 14));
+                bq[2 * (g - 14) + 1] = dequant(0, 2 * (g - 14) + 1);
+            }
+            a0 = a1;
+            a1 = a2;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int sb = 0; sb + 1 < nb; sb++) {
+        step(2 * sb, p8_step<0, true>{});
+        step(2 * sb + 1, p8_step<1, true>{});
     }
+    step(ns - 2, p8_step<0, true>{});
+    step(ns - 1, p8_step<1, false>{});
+
+    p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out);
 }
 
 // out[i] += part[z][i] for z = 0 .. nz - 1 in order (n floats per slice)
@@ -539,7 +732,7 @@ static int prefill_splits(int n_tok, int in_dim, int out_dim) {
     const size_t tt = ((size_t)n_tok + kPfTok - 1) / kPfTok;
     const size_t grid = rt * tt, nbt = (size_t)in_dim / 256;
     if (grid >= 128 || nbt < 4) return 1;
-    const size_t row_bytes = nbt * kQ4kBytes;
+    const size_t row_bytes = nbt * 272;  // the larger of Q8_0's and Q4_K's row bytes
     if ((size_t)out_dim * row_bytes > UINT32_MAX || (size_t)n_tok * in_dim * 2 > INT32_MAX) return 1;
     size_t nz = std::min<size_t>({256 / grid, nbt / 2, 16});
     const size_t base = ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16 + tt * kPfTok * 4;
@@ -557,12 +750,15 @@ size_t prefill_scratch_bytes(int n_tok, int in_dim, int out_dim) {
 }
 
 // One GEMM launch on the pre-pass's image (nz K splits: partial sums in part)
-static hipError_t prefill_gemm(const uint8_t *w, const _Float16 *xh, const float *unscale,
-                               float *out, float *part, int nz, int n_tok, int in_dim, int out_dim,
-                               int ld_out, hipStream_t s) {
+static hipError_t prefill_gemm(uint32_t dtype, const uint8_t *w, const _Float16 *xh,
+                               const float *unscale, float *out, float *part, int nz, int n_tok,
+                               int in_dim, int out_dim, int ld_out, hipStream_t s) {
     const dim3 grid((unsigned)((out_dim + kPfRowsWg - 1) / kPfRowsWg),
                     (unsigned)((n_tok + kPfTok - 1) / kPfTok), (unsigned)nz);
-    k_prefill_q4k_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out);
+    if (dtype == T_Q8_0)
+        k_prefill_q8_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out);
+    else
+        k_prefill_q4k_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || nz == 1) return e;
     const size_t n = (size_t)n_tok * out_dim;
@@ -575,11 +771,11 @@ static hipError_t prefill_gemm(const uint8_t *w, const _Float16 *xh, const float
 // with 32-bit byte offsets too, so a call whose weights pass 4 GiB or whose
 // image passes 2 GiB runs as several launches over row and token ranges
 // (whole 256-row and 128-token tiles).
-static hipError_t prefill_q4k(const uint8_t *w, const uint16_t *x_bf16, const float *x_f32,
-                              uint8_t *scratch, float *out, int n_tok, int in_dim, int out_dim,
-                              hipStream_t s) {
+static hipError_t prefill_run(uint32_t dtype, const uint8_t *w, const uint16_t *x_bf16,
+                              const float *x_f32, uint8_t *scratch, float *out, int n_tok,
+                              int in_dim, int out_dim, hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
-    const size_t row_bytes = (size_t)(in_dim / 256) * kQ4kBytes;
+    const size_t row_bytes = (size_t)(in_dim / 256) * (dtype == T_Q8_0 ? 272 : kQ4kBytes);
     const size_t rows_max = (size_t)UINT32_MAX / row_bytes / kPfRowsWg * kPfRowsWg;
     const size_t toks_max = (size_t)INT32_MAX / ((size_t)in_dim * 2) / kPfTok * kPfTok;
     if (rows_max == 0 || toks_max == 0) return hipErrorInvalidValue;
@@ -599,7 +795,7 @@ static hipError_t prefill_q4k(const uint8_t *w, const uint16_t *x_bf16, const fl
         const int nt = (int)std::min(toks_max, (size_t)n_tok - t0);
         for (size_t r0 = 0; r0 < (size_t)out_dim; r0 += rows_max) {
             const int nr = (int)std::min(rows_max, (size_t)out_dim - r0);
-            e = prefill_gemm(w + r0 * row_bytes, xh + t0 * in_dim, unscale + t0,
+            e = prefill_gemm(dtype, w + r0 * row_bytes, xh + t0 * in_dim, unscale + t0,
                              out + t0 * out_dim + r0, part, nz, nt, in_dim, nr, out_dim, s);
             if (e != hipSuccess) return e;
         }
@@ -611,12 +807,13 @@ hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *
                               uint8_t *scratch, float *out, int n_tok, int in_dim, int out_dim,
                               hipStream_t s) {
     (void)w_bytes;
-    return prefill_q4k(w, x_bf16, nullptr, scratch, out, n_tok, in_dim, out_dim, s);
+    return prefill_run(T_Q4_K, w, x_bf16, nullptr, scratch, out, n_tok, in_dim, out_dim, s);
 }
 
-hipError_t launch_prefill_q4k_f32(const uint8_t *w, const float *x, uint8_t *scratch, float *out,
-                                  int n_tok, int in_dim, int out_dim, hipStream_t s) {
-    return prefill_q4k(w, nullptr, x, scratch, out, n_tok, in_dim, out_dim, s);
+hipError_t launch_prefill_f32(uint32_t dtype, const uint8_t *w, const float *x, uint8_t *scratch,
+                              float *out, int n_tok, int in_dim, int out_dim, hipStream_t s) {
+    if (dtype != T_Q4_K && dtype != T_Q8_0) return hipErrorInvalidValue;
+    return prefill_run(dtype, w, nullptr, x, scratch, out, n_tok, in_dim, out_dim, s);
 }
 
 }  // namespace rsllm_hip

@@ -4,16 +4,16 @@ dsv4/weight.rs:161-163 -> backend-cpu/src/ops/quant_matmul.rs:45-119),
 through the drop-in entry points, against the oracle.
 
 Routes above 32 tokens:
-* Q4_K: the prefill GEMM on the matrix cores (f32 x scaled per token by 2^e
-  and rounded once to f16; weights f16(d*sc)*q - f16(dmin*m)): within the
-  north star's 1e-3 (REL_TOL), overall and per token for tokens with at
-  least 1000 outputs, about 3e-4 measured on C4;
-* Q6_K, Q8_0: the exact matrix-core GEMV (integer weights, hi + lo f16
+* Q4_K, Q8_0: the prefill GEMM on the matrix cores (f32 x scaled per token
+  by 2^e and rounded once to f16; weights f16(d*sc)*q - f16(dmin*m) for
+  Q4_K, f16(d*q) for Q8_0): within the north star's 1e-3 (REL_TOL), overall
+  and per token for tokens with at least 1000 outputs, about 3e-4 measured;
+* Q6_K: the exact matrix-core GEMV (integer weights, hi + lo f16
   activations) over 32-token chunks, a short tail included: an fp32-level
   bound (2e-5) on every token;
 * other formats: the int8-limb GEMV (REL_TOL).
-A device pointer that is not 16-byte aligned keeps the Q4_K call off the
-GEMM (its global->LDS copies move 16-byte pieces) and must still be right."""
+A device pointer that is not 16-byte aligned keeps the call off the GEMM
+(its global->LDS copies move 16-byte pieces) and must still be right."""
 import numpy as np
 import pytest
 
@@ -77,8 +77,8 @@ def test_prefill_f32_ragged(oracle, hip, dtype, out_dim, in_dim, n_tok):
     x *= (np.float32(10.0) ** ((np.arange(n_tok) % 7) - 3)).astype(np.float32)[:, None]
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
     got = run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim)
-    tol = EXACT_TOL if dtype in (G.Q6_K, G.Q8_0) else REL_TOL
-    per_token = dtype != G.Q4_K or out_dim >= 1000
+    tol = EXACT_TOL if dtype == G.Q6_K else REL_TOL
+    per_token = dtype not in (G.Q4_K, G.Q8_0) or out_dim >= 1000
     check(oracle, got, w, x, np.arange(n_tok), dtype, n_tok, in_dim, out_dim, tol, per_token)
 
 
@@ -97,15 +97,50 @@ def test_prefill_f32_c4(oracle, hip, n_tok):
 
 
 @pytest.mark.parametrize("dtype", [G.Q6_K, G.Q8_0])
-def test_prefill_f32_exact_formats_c1_shape(oracle, hip, dtype):
-    """Q6_K / Q8_0 at a decode-FFN shape (14336 x 4096) with 200 tokens: six
-    32-token chunks and an 8-token tail, every token exact to fp32 level."""
+def test_prefill_f32_c1_shape(oracle, hip, dtype):
+    """A decode-FFN shape (14336 x 4096) with 200 tokens. Q6_K: six 32-token
+    chunks and an 8-token tail, every token exact to fp32 level. Q8_0: the
+    GEMM (a partial second 128-token tile), every token within 1e-3."""
     out_dim, in_dim, n_tok = 14336, 4096, 200
     w = synth.weight(dtype, out_dim, in_dim, seed=2300)
     x = synth.activations(n_tok, in_dim, seed=2301).reshape(-1)
     got = run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim)
-    tokens = np.array([0, 31, 32, 100, 191, 192, 199])
-    check(oracle, got, w, x, tokens, dtype, n_tok, in_dim, out_dim, EXACT_TOL, True)
+    tokens = np.array([0, 31, 32, 100, 127, 128, 191, 192, 199])
+    tol = EXACT_TOL if dtype == G.Q6_K else REL_TOL
+    check(oracle, got, w, x, tokens, dtype, n_tok, in_dim, out_dim, tol, True)
+
+
+@pytest.mark.parametrize("out_dim,in_dim,n_tok", [(4096, 4096, 512), (1024, 4096, 512),
+                                                  (4000, 768, 1281), (700, 2304, 40)])
+def test_prefill_f32_q8_0_gemm(oracle, hip, out_dim, in_dim, n_tok):
+    """Q8_0 on the prefill GEMM: config C2's attention shapes at T = 512
+    (4096 x 4096 splits K 4 ways, 1024 x 4096 16 ways), 16 x 11 tiles with
+    ragged last row and token tiles and 3 super-tiles per row, and 9
+    super-tiles in 4 uneven splits with 40 tokens. Repeated calls are
+    bit-identical."""
+    w = synth.weight(G.Q8_0, out_dim, in_dim, seed=2500 + out_dim)
+    x = synth.activations(n_tok, in_dim, seed=2501 + n_tok).reshape(-1)
+    got = run_dev(hip, G.Q8_0, w, x, n_tok, in_dim, out_dim)
+    again = run_dev(hip, G.Q8_0, w, x, n_tok, in_dim, out_dim)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    edges = np.arange(128, n_tok, 128)
+    tokens = np.unique(np.concatenate([[0, 1, n_tok - 1], edges - 1, edges,
+                                       np.linspace(0, n_tok - 1, 8).astype(int)]))
+    check(oracle, got, w, x, tokens, G.Q8_0, n_tok, in_dim, out_dim, REL_TOL, out_dim >= 1000)
+
+
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q8_0])
+def test_prefill_f32_unaligned_large_grid(oracle, hip, dtype):
+    """x off 16-byte alignment on a grid that does not split K (56 x 3
+    workgroups): the int8-limb route then needs a larger workspace than the
+    GEMM would (2.5 or 3 bytes per element of x against 2), and the call
+    sizes it for either route."""
+    out_dim, in_dim, n_tok = 14336, 4096, 300
+    w = synth.weight(dtype, out_dim, in_dim, seed=2600)
+    x = synth.activations(n_tok, in_dim, seed=2601).reshape(-1)
+    got = run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim, x_offset=1)
+    tokens = np.array([0, 1, 150, 298, 299])
+    check(oracle, got, w, x, tokens, dtype, n_tok, in_dim, out_dim, REL_TOL, True)
 
 
 def test_prefill_f32_unaligned_x_and_host_form(oracle, hip):
