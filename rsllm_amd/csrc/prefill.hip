@@ -701,6 +701,261 @@ __global__ __launch_bounds__(512) void k_prefill_q8_w8(const uint8_t *__restrict
     p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out);
 }
 
+// ---- Q6_K weights -----------------------------------------------------------------
+// k_prefill_q6_w8: the same workgroup on Q6_K weights in the device layout
+// (super-tiles of 8 blocks [ql 8 x 128 | qh 8 x 64 | scales 8 x 16 | d 8 x 2],
+// 1680 bytes per 2048 elements of a row; rows of whole super-tiles, in_dim a
+// multiple of 2048). Element 128 h + 32 j + l of a block (q6_k.rs:65-92) is
+// the low (j < 2) or high nibble of ql[64 h + 32 (j & 1) + l] with bits 2j,
+// 2j + 1 of qh[32 h + l] above it, minus 32, times d * sc[8 h + 2 j + l / 16].
+// Group kg's step at half h takes j = 2 kg + c for its chunks c, so both
+// groups read the same half-block in a step: one weight stage per step,
+// shared by the 8 wavefronts, 128 bytes per row (the half's 64 ql and 32 qh
+// bytes, the block's 16 scales, the super-tile's 16-byte d run), its 16-byte
+// slot s of row r at slot s ^ ((r & 15) >> 1) so the 8-byte operand reads of
+// 16 rows hit distinct banks. Each thread turns its own row's scales into
+// f16 (d * sc) for its group once per step. Lane group q's 8 weights of a
+// chunk: the 6-bit codes (ql nibble | qh bits << 4), paired with 0x64 as
+// f16 1024 + code, minus 1056 (exact q - 32), times f16(d * sc) (one
+// rounding, as the Q4_K weights).
+constexpr int kQ6W = kPfRowsWg * 128;              // 32 KB: a step's weight stage
+constexpr int kQ6ActOff = 2 * kQ6W;                // activations: (group, step parity)
+constexpr int kQ6ScOff = kQ6ActOff + 4 * kP8Act;   // scale records: 8 bytes per row per group
+constexpr int kQ6Lds = kQ6ScOff + 2 * kPfRowsWg * 8;  // 132 KB
+static_assert(2 * 4 * 16 * 64 * 16 <= kQ6Lds, "the epilogue's exchange fits");
+
+__global__ __launch_bounds__(512) void k_prefill_q6_w8(const uint8_t *__restrict__ w,
+                                                       const _Float16 *__restrict__ xh,
+                                                       const float *__restrict__ unscale,
+                                                       float *__restrict__ out,
+                                                       float *__restrict__ part, int n_tok,
+                                                       int in_dim, int out_dim, int ld_out) {
+    __shared__ __align__(16) uint8_t smem[kQ6Lds];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wv & 3, kg = wv >> 2;
+    const int r16 = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
+    const int nbt = in_dim >> 8;  // blocks in a row (a multiple of 8)
+    const int z = blockIdx.z, nz = gridDim.z;
+    const int kb0 = (int)((long)z * nbt / nz);
+    const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;
+    const int ns = 2 * nb;
+    xh += (size_t)kb0 * 256;
+    if (z > 0) out = part + (size_t)(z - 1) * n_tok * ld_out;
+    uint8_t *const act = smem + kQ6ActOff + 2 * kg * kP8Act;  // this group's two step buffers
+    uint8_t *const scl = smem + kQ6ScOff + kg * kPfRowsWg * 8;
+    const uint32_t row_bytes = (uint32_t)(nbt >> 3) * 1680u;
+
+    // Copies, 16 bytes a lane, lane l to LDS row 8 R + l / 8 (a token of
+    // this group's activations, a weight row of the stage), 16-byte slot
+    // l % 8. Piece p of wavefront (wr or wv) covers R = 2 (4 (w >> 1) + p) +
+    // (w & 1), so a row's swizzle ((row & 15) >> 1 = 4 (w & 1) + l / 16), and
+    // with it what a lane copies, is the same for all four pieces: a column
+    // piece of the activations; for the weights field slot f = (l % 8) ^
+    // swizzle (0..3 ql, 4..5 qh, 6 the scales, 7 the d run) at byte
+    // base(f) + (b % 8) stride(f) + h half(f) of the super-tile of block b, h
+    // the half-block. Rows past the matrix repeat its last row: the row
+    // offset is min(l / 8, lim) rows from a clamped first row, lim passed
+    // through an empty asm at each copy so the compiler keeps no per-piece
+    // offsets in registers.
+    const int lr = lane >> 3;
+    const int aswz_dma = 4 * (wr & 1) + (lane >> 4), wswz_dma = 4 * (wv & 1) + (lane >> 4);
+    const int pc = (lane & 7) ^ aswz_dma;
+    const uint32_t xcol = 2u * (64 * kg + 32 * (pc >> 2) + 8 * (pc & 3));
+    const int f = (lane & 7) ^ wswz_dma;
+    const uint32_t wfld = f < 4 ? 16u * f : f < 6 ? 1024u + 16u * (f - 4) : f == 6 ? 1536u : 1664u;
+    const uint32_t wmul = (f < 4 ? 128u : f < 6 ? 64u : f == 6 ? 16u : 0u) |
+                          ((f < 4 ? 64u : f < 6 ? 32u : 0u) << 16);  // stride | half << 16
+    // this wavefront's first copy destinations, held in scalar registers
+    // (from an asm result) so no vector register keeps them
+    uint32_t lds_act, lds_w;
+    asm("s_mov_b32 %0, %1"
+        : "=s"(lds_act)
+        : "s"(__builtin_amdgcn_readfirstlane(p8_lds(act) + 8192 * (wr >> 1) + 1024 * (wr & 1))));
+    asm("s_mov_b32 %0, %1"
+        : "=s"(lds_w)
+        : "s"(__builtin_amdgcn_readfirstlane(p8_lds(smem) + 8192 * (wv >> 1) + 1024 * (wv & 1))));
+    // piece p (0..7) of group step s into the buffers of step parity par
+    // (s % 2, a constant at every call, so the half-block is one): 0..3 this
+    // group's activations, 4..7 the shared weight stage. A step past the end
+    // reloads the last block's half par, which no one reads.
+    auto dma = [=](int s, int p, auto par_c) {
+        constexpr int par = decltype(par_c)::value;
+        const int b = kb0 + (min(s, ns - 1) >> 1);  // block of the row
+        if (p < 4) {
+            const int R = 2 * (4 * (wr >> 1) + p) + (wr & 1);
+            const int t = min(t0 + 8 * R, n_tok - 1);
+            int lim = n_tok - 1 - t;
+            asm volatile("" : "+s"(lim));
+            const uint32_t o = (uint32_t)min(lr, lim) * (2u * (uint32_t)in_dim) + xcol;
+            p8_dma(xh + (size_t)t * in_dim + (b - kb0) * 256 + 128 * par, o,
+                   lds_act + (uint32_t)(par * kP8Act + 2048 * p));
+        } else {
+            const int R = 2 * (4 * (wv >> 1) + p - 4) + (wv & 1);
+            const int r = min(n0 + 8 * R, out_dim - 1);
+            int lim = out_dim - 1 - r;
+            asm volatile("" : "+s"(lim));
+            uint32_t o = (uint32_t)min(lr, lim) * row_bytes + (uint32_t)(b & 7) * (wmul & 0xFFFFu) + wfld;
+            if (par) o += wmul >> 16;
+            p8_dma(w + (size_t)r * row_bytes + (size_t)(b >> 3) * 1680, o,
+                   lds_w + (uint32_t)(par * kQ6W + 2048 * (p - 4)));
+        }
+    };
+    using par0 = std::integral_constant<int, 0>;
+    using par1 = std::integral_constant<int, 1>;
+    const int sw = r16 >> 1;
+    const int qlb0 = 16 * ((0 + (q >> 1)) ^ sw) + 8 * (q & 1);  // ql, chunk 0: field slot q / 2
+    const int aswz = (r16 >> 1) & 7;
+    // this thread's row's scales -> records for its group at half h:
+    // {f16(d sc[8h + 4kg]), f16(d sc[8h + 4kg + 2])} for lane groups q < 2,
+    // {f16(d sc[8h + 4kg + 1]), f16(d sc[8h + 4kg + 3])} for q >= 2
+    auto scales_of_step = [&](const uint8_t *wbuf, int b, int h) {
+        const int row = 64 * wr + lane;
+        const int rs = (row & 15) >> 1;
+        const uint32_t sc4 = *reinterpret_cast<const uint32_t *>(wbuf + 128 * row + 16 * (6 ^ rs) + 8 * h + 4 * kg);
+        const float d = f16_to_f32(*reinterpret_cast<const uint16_t *>(wbuf + 128 * row + 16 * (7 ^ rs) + 2 * (b & 7)));
+        auto f = [&](int i) { return (_Float16)(d * (float)(int8_t)(sc4 >> (8 * i))); };
+        const h2 lo = {f(0), f(2)}, hi = {f(1), f(3)};
+        *reinterpret_cast<uint2 *>(scl + 8 * row) =
+            make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+    };
+    // a lane's raw operands of chunk c, token tile nt: 8 ql bytes, the 8 qh
+    // bytes, (f16 scale of chunk 0, of chunk 1)
+    struct q6w {
+        uint2 ql, qh;
+        uint32_t sc;
+    };
+    // per-lane bases (row 64 wr + r16 of stage 0), so token tile nt and the
+    // stage are immediate offsets
+    // one per-lane base (row 64 wr + r16 of stage 0, the chunk-0 ql field):
+    // the chunk-1 ql and the qh fields are at base ^ 32 and base ^ 64 (slots
+    // q / 2 + 2 and + 4 under the swizzle), token tile nt and the stage are
+    // immediate offsets. The empty asm at each use keeps the compiler from
+    // holding the derived addresses in registers across the loop.
+    const uint32_t wq_base = 128u * (uint32_t)(64 * wr + r16) + (uint32_t)qlb0;  // from smem
+    const uint32_t ws_base = (uint32_t)(scl - smem) + 8u * (uint32_t)(64 * wr + r16) + 4u * (uint32_t)(q >> 1);
+    auto read_w = [&](int par, int c, int nt) -> q6w {
+        uint32_t a = wq_base, sa = ws_base;
+        asm volatile("" : "+v"(a), "+v"(sa));
+        const uint32_t o = (uint32_t)par * kQ6W + 2048u * nt;
+        return {*reinterpret_cast<const uint2 *>(smem + ((c ? a ^ 32u : a) + o)),
+                *reinterpret_cast<const uint2 *>(smem + ((a ^ 64u) + o)),
+                *reinterpret_cast<const uint32_t *>(smem + (sa + 128u * nt))};
+    };
+    const int nsh = 4 * kg;  // ql nibble shift; qh bits 2j = nsh + 2c
+    auto dequant = [&](const q6w &v, int c) -> h8 {
+        const int sh = nsh + 2 * c;  // qh bits of this chunk
+        const h2 d2 = __builtin_bit_cast(h2, v.sc);
+        const h2 ds = c ? d2.yy : d2.xx;
+        const h2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};
+        h8 r;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const uint32_t lw = ((u ? v.ql.y : v.ql.x) >> nsh) & 0x0F0F0F0Fu;
+            const uint32_t hw = ((u ? v.qh.y : v.qh.x) >> sh) & 0x03030303u;
+            const uint32_t code = lw | (hw << 4);
+            const h2 w01 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, code, 0x04010400u)) - bias) * ds;
+            const h2 w23 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, code, 0x04030402u)) - bias) * ds;
+            r[4 * u] = w01[0];
+            r[4 * u + 1] = w01[1];
+            r[4 * u + 2] = w23[0];
+            r[4 * u + 3] = w23[1];
+        }
+        return r;
+    };
+    auto read_a = [&](const uint8_t *buf, int c, int mt) -> h8 {
+        return *reinterpret_cast<const h8 *>(buf + (16 * mt + r16) * 128 + 16 * ((4 * c + q) ^ aswz));
+    };
+
+    f4 acc[8][4];
+#pragma unroll
+    for (int mt = 0; mt < 8; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // prologue: step 0 in, step 1 in flight, step 0's chunk-0 operands ready
+#pragma unroll
+    for (int p = 0; p < 8; p++) dma(0, p, par0{});
+    p8_barrier_vm0();
+#pragma unroll
+    for (int p = 0; p < 8; p++) dma(1, p, par1{});  // ns >= 2
+    scales_of_step(smem, kb0, 0);
+    h8 bq[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) bq[nt] = dequant(read_w(0, 0, nt), 0);
+    h8 a0 = read_a(act, 0, 0);
+
+    // One step: as in k_prefill_q8_w8, the weights in the shared stage of
+    // the step's parity: in group 14 every wavefront waits for its own
+    // copies of step s + 1, after the barrier decodes its row's scales of
+    // step s + 1 and reads that step's chunk-0 weights, and this step's
+    // buffers take step s + 2 (pieces 0..5 in groups 14, 15, 6..7 in groups
+    // 0, 2 of the next step). Chunk 1's raw weights of token tile i are read
+    // in group 2 i, dequantised in group 2 i + 1.
+    auto step = [&](int s, auto tag) {
+        constexpr int PAR = decltype(tag)::par;
+        constexpr bool MORE = decltype(tag)::more;
+        const uint8_t *buf = act + PAR * kP8Act;
+        const uint8_t *nbuf = act + (1 - PAR) * kP8Act;
+        const uint8_t *nwbuf = smem + (1 - PAR) * kQ6W;
+        h8 b1[4], a15;
+        q6w rw;
+#pragma unroll
+        for (int g = 0; g < 16; g++) {
+            const int c = g >> 3, mt = g & 7;
+            __builtin_amdgcn_sched_barrier(0);
+            if (MORE && g < 4 && (g & 1) == 0 && s >= 1)
+                dma(s + 1, 6 + (g >> 1), std::integral_constant<int, 1 - PAR>{});
+            if (c == 0 && (mt & 1) == 0) rw = read_w(PAR, 1, mt >> 1);
+            q6w rn0, rn1;
+            if (MORE && g == 14) p8_barrier_vm0();
+            if (MORE && g == 14) scales_of_step(nwbuf, kb0 + ((s + 1) >> 1), 1 - PAR);
+            if (MORE && g >= 14) {
+                rn0 = read_w(1 - PAR, 0, 2 * (g - 14));
+                rn1 = read_w(1 - PAR, 0, 2 * (g - 14) + 1);
+            }
+            // the activation operand one group ahead, except that group 13
+            // also reads group 15's, so every read of this step's buffer
+            // precedes the barrier of group 14 (after which it takes step
+            // s + 2), and group 15 reads the next step's first
+            h8 a1 = a0;
+            if (g < 13) a1 = read_a(buf, (g + 1) >> 3, (g + 1) & 7);
+            if (g == 13) {
+                a1 = read_a(buf, 1, 6);
+                a15 = read_a(buf, 1, 7);
+            }
+            if (g == 14) a1 = a15;
+            if (MORE && g == 15) a1 = read_a(nbuf, 0, 0);
+            if (MORE && g >= 14) {
+                dma(s + 2, 3 * (g - 14), std::integral_constant<int, PAR>{});
+                dma(s + 2, 3 * (g - 14) + 1, std::integral_constant<int, PAR>{});
+                dma(s + 2, 3 * (g - 14) + 2, std::integral_constant<int, PAR>{});
+            }
+            const h8 acur = a0;
+            const h8 *bw = c ? b1 : bq;
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++)
+                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bw[nt], acur, acc[mt][nt], 0, 0, 0);
+            if (c == 0 && (mt & 1)) b1[mt >> 1] = dequant(rw, 1);
+            if (MORE && g >= 14) {
+                bq[2 * (g - 14)] = dequant(rn0, 0);
+                bq[2 * (g - 14) + 1] = dequant(rn1, 0);
+            }
+            a0 = a1;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int sb = 0; sb + 1 < nb; sb++) {
+        step(2 * sb, p8_step<0, true>{});
+        step(2 * sb + 1, p8_step<1, true>{});
+    }
+    step(ns - 2, p8_step<0, true>{});
+    step(ns - 1, p8_step<1, false>{});
+
+    p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out);
+}
+
 // out[i] += part[z][i] for z = 0 .. nz - 1 in order (n floats per slice)
 __global__ __launch_bounds__(256) void k_prefill_sum(float *__restrict__ out,
                                                      const float *__restrict__ part, size_t n,
@@ -757,6 +1012,8 @@ static hipError_t prefill_gemm(uint32_t dtype, const uint8_t *w, const _Float16 
                     (unsigned)((n_tok + kPfTok - 1) / kPfTok), (unsigned)nz);
     if (dtype == T_Q8_0)
         k_prefill_q8_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out);
+    else if (dtype == T_Q6_K)
+        k_prefill_q6_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out);
     else
         k_prefill_q4k_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out);
     hipError_t e = hipGetLastError();
@@ -775,7 +1032,8 @@ static hipError_t prefill_run(uint32_t dtype, const uint8_t *w, const uint16_t *
                               const float *x_f32, uint8_t *scratch, float *out, int n_tok,
                               int in_dim, int out_dim, hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
-    const size_t row_bytes = (size_t)(in_dim / 256) * (dtype == T_Q8_0 ? 272 : kQ4kBytes);
+    const size_t row_bytes = dtype == T_Q6_K ? (size_t)(in_dim / 2048) * 1680
+                                             : (size_t)(in_dim / 256) * (dtype == T_Q8_0 ? 272 : kQ4kBytes);
     const size_t rows_max = (size_t)UINT32_MAX / row_bytes / kPfRowsWg * kPfRowsWg;
     const size_t toks_max = (size_t)INT32_MAX / ((size_t)in_dim * 2) / kPfTok * kPfTok;
     if (rows_max == 0 || toks_max == 0) return hipErrorInvalidValue;
@@ -812,7 +1070,8 @@ hipError_t launch_prefill_q4k(const uint8_t *w, size_t w_bytes, const uint16_t *
 
 hipError_t launch_prefill_f32(uint32_t dtype, const uint8_t *w, const float *x, uint8_t *scratch,
                               float *out, int n_tok, int in_dim, int out_dim, hipStream_t s) {
-    if (dtype != T_Q4_K && dtype != T_Q8_0) return hipErrorInvalidValue;
+    if (dtype != T_Q4_K && dtype != T_Q8_0 && !(dtype == T_Q6_K && in_dim % 2048 == 0))
+        return hipErrorInvalidValue;
     return prefill_run(dtype, w, nullptr, x, scratch, out, n_tok, in_dim, out_dim, s);
 }
 

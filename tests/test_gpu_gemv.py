@@ -77,10 +77,12 @@ def test_gemv_mfma_exact_weights_few_rows(oracle, hip, dtype, out_dim, n_tok):
 # the int8-limb GEMVs (1..4 tokens), the matrix-core GEMV (5..32), its fused
 # LDS kernel (5..8 tokens of tall matrices) and the 32-token chunks above 32
 # — stays at its bound with every block holding sc = -128 and 127 (an
-# f16-rounded sc (q - 32) gives 1e-4 and up).
+# f16-rounded sc (q - 32) gives 1e-4 and up). Above 32 tokens with in_dim a
+# multiple of 2048 the prefill GEMM (f16 weights and activations) takes the
+# call, within REL_TOL at these scales too.
 @pytest.mark.parametrize("out_dim,in_dim,n_tok", [
     (16, 4096, 1), (100, 2048, 3), (33, 4096, 5), (16, 4096, 9), (257, 2048, 12),
-    (1000, 1024, 16), (64, 4096, 32), (8200, 1024, 6), (300, 2048, 40)])
+    (1000, 1024, 16), (64, 4096, 32), (8200, 1024, 6), (300, 1280, 40), (300, 2048, 40)])
 def test_gemv_q6k_full_range_scales(oracle, hip, out_dim, in_dim, n_tok):
     w = synth.q6k_full_scales(synth.weight(G.Q6_K, out_dim, in_dim, 1900 + n_tok), 1950 + n_tok)
     x = synth.activations(n_tok, in_dim, 1960 + n_tok).reshape(-1)
@@ -90,7 +92,8 @@ def test_gemv_q6k_full_range_scales(oracle, hip, out_dim, in_dim, n_tok):
     hip.matmul_quant_f32(got, w, x, n_tok, in_dim, out_dim, G.Q6_K)
     err = rel_err(got, want)
     print(f"q6k full-range scales {out_dim}x{in_dim} T={n_tok}: rel err {err:.3e}")
-    assert err <= (2e-5 if n_tok >= 5 else REL_TOL)
+    exact = 5 <= n_tok <= 32 or (n_tok > 32 and in_dim % 2048 != 0)
+    assert err <= (2e-5 if exact else REL_TOL)
 
 
 # The fused matrix-core kernel (5..8 tokens, out_dim >= 8192, f16 x in LDS):

@@ -4,11 +4,13 @@ dsv4/weight.rs:161-163 -> backend-cpu/src/ops/quant_matmul.rs:45-119),
 through the drop-in entry points, against the oracle.
 
 Routes above 32 tokens:
-* Q4_K, Q8_0: the prefill GEMM on the matrix cores (f32 x scaled per token
-  by 2^e and rounded once to f16; weights f16(d*sc)*q - f16(dmin*m) for
-  Q4_K, f16(d*q) for Q8_0): within the north star's 1e-3 (REL_TOL), overall
-  and per token for tokens with at least 1000 outputs, about 3e-4 measured;
-* Q6_K: the exact matrix-core GEMV (integer weights, hi + lo f16
+* Q4_K, Q8_0, and Q6_K with in_dim a multiple of 2048 (rows of whole
+  8-block super-tiles): the prefill GEMM on the matrix cores (f32 x scaled
+  per token by 2^e and rounded once to f16; weights f16(d*sc)*q -
+  f16(dmin*m) for Q4_K, f16(d*q) for Q8_0, f16(d*sc)*(q-32) for Q6_K):
+  within the north star's 1e-3 (REL_TOL), overall and per token for tokens
+  with at least 1000 outputs, about 3e-4 measured;
+* other Q6_K rows: the exact matrix-core GEMV (integer weights, hi + lo f16
   activations) over 32-token chunks, a short tail included: an fp32-level
   bound (2e-5) on every token;
 * other formats: the int8-limb GEMV (REL_TOL).
@@ -77,8 +79,9 @@ def test_prefill_f32_ragged(oracle, hip, dtype, out_dim, in_dim, n_tok):
     x *= (np.float32(10.0) ** ((np.arange(n_tok) % 7) - 3)).astype(np.float32)[:, None]
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
     got = run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim)
-    tol = EXACT_TOL if dtype == G.Q6_K else REL_TOL
-    per_token = dtype not in (G.Q4_K, G.Q8_0) or out_dim >= 1000
+    gemm = dtype in (G.Q4_K, G.Q8_0) or (dtype == G.Q6_K and in_dim % 2048 == 0)
+    tol = EXACT_TOL if dtype == G.Q6_K and not gemm else REL_TOL
+    per_token = not gemm or out_dim >= 1000
     check(oracle, got, w, x, np.arange(n_tok), dtype, n_tok, in_dim, out_dim, tol, per_token)
 
 
@@ -98,16 +101,14 @@ def test_prefill_f32_c4(oracle, hip, n_tok):
 
 @pytest.mark.parametrize("dtype", [G.Q6_K, G.Q8_0])
 def test_prefill_f32_c1_shape(oracle, hip, dtype):
-    """A decode-FFN shape (14336 x 4096) with 200 tokens. Q6_K: six 32-token
-    chunks and an 8-token tail, every token exact to fp32 level. Q8_0: the
-    GEMM (a partial second 128-token tile), every token within 1e-3."""
+    """A decode-FFN shape (14336 x 4096) with 200 tokens on the GEMM (a
+    partial second 128-token tile), every token within 1e-3."""
     out_dim, in_dim, n_tok = 14336, 4096, 200
     w = synth.weight(dtype, out_dim, in_dim, seed=2300)
     x = synth.activations(n_tok, in_dim, seed=2301).reshape(-1)
     got = run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim)
     tokens = np.array([0, 31, 32, 100, 127, 128, 191, 192, 199])
-    tol = EXACT_TOL if dtype == G.Q6_K else REL_TOL
-    check(oracle, got, w, x, tokens, dtype, n_tok, in_dim, out_dim, tol, True)
+    check(oracle, got, w, x, tokens, dtype, n_tok, in_dim, out_dim, REL_TOL, True)
 
 
 @pytest.mark.parametrize("out_dim,in_dim,n_tok", [(4096, 4096, 512), (1024, 4096, 512),
@@ -129,7 +130,26 @@ def test_prefill_f32_q8_0_gemm(oracle, hip, out_dim, in_dim, n_tok):
     check(oracle, got, w, x, tokens, G.Q8_0, n_tok, in_dim, out_dim, REL_TOL, out_dim >= 1000)
 
 
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q8_0])
+@pytest.mark.parametrize("out_dim,in_dim,n_tok", [(14336, 4096, 512), (4096, 14336, 512),
+                                                  (4000, 2048, 1281), (700, 4096, 40)])
+def test_prefill_f32_q6_k_gemm(oracle, hip, out_dim, in_dim, n_tok):
+    """Q6_K on the prefill GEMM: the C1 FFN shapes at T = 512 (14336 x 4096
+    unsplit; 4096 x 14336 splits K 4 ways, 14 blocks each, so splits start
+    inside a super-tile), 16 x 11 tiles with a ragged last row tile (4000
+    rows) and a 1-token last token tile, and 16 blocks in 8 splits with 40
+    tokens. Repeated calls are bit-identical."""
+    w = synth.weight(G.Q6_K, out_dim, in_dim, seed=2700 + out_dim)
+    x = synth.activations(n_tok, in_dim, seed=2701 + n_tok).reshape(-1)
+    got = run_dev(hip, G.Q6_K, w, x, n_tok, in_dim, out_dim)
+    again = run_dev(hip, G.Q6_K, w, x, n_tok, in_dim, out_dim)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    edges = np.arange(128, n_tok, 128)
+    tokens = np.unique(np.concatenate([[0, 1, n_tok - 1], edges - 1, edges,
+                                       np.linspace(0, n_tok - 1, 8).astype(int)]))
+    check(oracle, got, w, x, tokens, G.Q6_K, n_tok, in_dim, out_dim, REL_TOL, True)
+
+
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q8_0, G.Q6_K])
 def test_prefill_f32_unaligned_large_grid(oracle, hip, dtype):
     """x off 16-byte alignment on a grid that does not split K (56 x 3
     workgroups): the int8-limb route then needs a larger workspace than the
