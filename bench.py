@@ -70,6 +70,8 @@ def parse():
     ap.add_argument("--prefill-probe", type=int, default=0, metavar="T",
                     help="internal: only run the C4 prefill call at T tokens 5 times (the "
                          "workload for rocprofv3 counter passes; prints no JSON)")
+    ap.add_argument("--prefill-format", default="Q4_K", choices=("Q4_K", "Q6_K", "Q8_0"),
+                    help="internal: weight format of --prefill-probe")
     ap.add_argument("--moe-probe", type=int, default=0, metavar="T",
                     help="internal: only run the C3 routed-expert call at T tokens 8 times "
                          "(for rocprofv3 kernel traces; prints no JSON)")
@@ -190,6 +192,42 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
                               "tokens_checked": len(toks), "tolerance": 1e-3}
         res["k_split"].append(entry)
         del d_x, d_y, d_ws
+    # The other formats on the same GEMM: Q6_K (C1's format) and Q8_0 (C2's)
+    # at C4's shape, T = 512, through the reference's f32-x call on
+    # weights in the device layout.
+    res["formats"] = []
+    T = 512
+    for (dt, seed) in ((G.Q6_K, 409), (G.Q8_0, 410)):
+        w_f = synth.weight(dt, out_dim, in_dim, seed=seed)
+        raw = torch.from_numpy(w_f).to(dev)
+        d_wf = torch.empty_like(raw)
+        B.prepare_weights_dev(d_wf.data_ptr(), raw.data_ptr(), raw.numel(), dt, in_dim, sptr)
+        del raw
+        xf_all = synth.activations(T, in_dim, seed=seed + 1).reshape(-1)
+        d_x = torch.from_numpy(xf_all).to(dev)
+        d_y = torch.empty(T * out_dim, dtype=torch.float32, device=dev)
+
+        def call_f(i):
+            B.matmul_quant_f32_dev(d_y.data_ptr(), d_y.numel(), d_wf.data_ptr(), d_wf.numel(),
+                                   d_x.data_ptr(), d_x.numel(), T, in_dim, out_dim, dt, sptr)
+        for i in range(3):
+            call_f(i)
+        us = _time(call_f, iters, stream)
+        tflops = 2.0 * T * in_dim * out_dim / (us * 1e-6) / 1e12
+        entry = {"format": dt.name, "shape": f"{out_dim}x{in_dim}", "tokens": T,
+                 "us_per_op": round(us, 2), "tflops": round(tflops, 1),
+                 "frac_of_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+        if with_cpu:
+            from oracle import oracle as O
+            toks = np.linspace(0, T - 1, 6).astype(int)
+            xs = xf_all.reshape(T, in_dim)[toks].reshape(-1)
+            rc, want = O.matmul_quant_f32(w_f, xs, len(toks), in_dim, out_dim, int(dt))
+            got = d_y.cpu().numpy().reshape(T, out_dim)[toks].reshape(-1)
+            entry["check"] = {"max_rel_err_vs_oracle": float(np.abs(got - want).max() /
+                                                             np.abs(want).max()),
+                              "tokens_checked": len(toks), "tolerance": 1e-3}
+        res["formats"].append(entry)
+        del d_x, d_y, d_wf
     res["mfma_ceiling"] = bench_mfma_ceiling(B, dev, stream)
     res["dense_f16_library"] = bench_dense_f16(dev, stream, out_dim, in_dim, iters)
     if with_cpu:
@@ -329,21 +367,32 @@ def pmc_probe():
         del reps, prep
 
 
-def prefill_probe(T):
+def prefill_probe(T, fmt="Q4_K"):
     """The C4 prefill call (Q4_K 14336x4096 weights, bf16 x [T x 4096]) five
-    times, for rocprofv3 runs that count MFMA and VALU work per dispatch."""
+    times, for rocprofv3 runs that count MFMA and VALU work per dispatch;
+    with fmt Q6_K or Q8_0, the same shape in that format through the f32-x
+    call (weights in the device layout)."""
     import torch
     from rsllm_amd import backend as B
     from rsllm_amd import synth
     from rsllm_amd.ggml import GgmlType as G
     out_dim, in_dim = 14336, 4096
     sptr = torch.cuda.current_stream().cuda_stream
-    w = torch.from_numpy(synth.weight(G.Q4_K, out_dim, in_dim, seed=300)).cuda()
-    x = torch.from_numpy(synth.bf16_activations(T, in_dim, seed=301).reshape(-1)).cuda()
+    dt = G[fmt]
+    w = torch.from_numpy(synth.weight(dt, out_dim, in_dim, seed=300)).cuda()
     y = torch.empty(T * out_dim, dtype=torch.float32, device="cuda")
-    for _ in range(5):
-        B.matmul_q4k_bf16_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
-                              x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
+    if dt == G.Q4_K:
+        x = torch.from_numpy(synth.bf16_activations(T, in_dim, seed=301).reshape(-1)).cuda()
+        for _ in range(5):
+            B.matmul_q4k_bf16_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
+                                  x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
+    else:
+        d = torch.empty_like(w)
+        B.prepare_weights_dev(d.data_ptr(), w.data_ptr(), w.numel(), dt, in_dim, sptr)
+        x = torch.from_numpy(synth.activations(T, in_dim, seed=301).reshape(-1)).cuda()
+        for _ in range(5):
+            B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), d.data_ptr(), d.numel(), x.data_ptr(),
+                                   x.numel(), T, in_dim, out_dim, dt, sptr)
     torch.cuda.synchronize()
 
 
@@ -887,7 +936,7 @@ def main():
         batch_probe()
         return
     if args.prefill_probe:
-        prefill_probe(args.prefill_probe)
+        prefill_probe(args.prefill_probe, args.prefill_format)
         return
     if args.moe_probe:
         moe_probe(args.moe_probe)
