@@ -12,11 +12,14 @@ from rsllm_amd.ggml import GgmlType as G
 
 # (dtype, out_dim, in_dim, n_tok): each takes a kernel path that uses the
 # workspace: the matrix-core batched GEMV (f16 activation image) for 5..32
-# tokens of >= 1024 rows, the activation pre-pass + GEMV otherwise
+# tokens of >= 1024 rows, the activation pre-pass + GEMV otherwise, and
+# above 32 tokens the prefill GEMM (f16 image, per-token scales and, on
+# small grids, the partial sums of its K splits: 8 and 4 splits here)
 CALLS = [
     [(G.Q4_K, 4096, 4096, 24), (G.Q6_K, 1024, 2048, 12)],   # matrix cores, then smaller
     [(G.Q8_0, 512, 4096, 20), (G.Q4_K, 256, 1024, 11)],     # pre-pass path, then smaller
     [(G.Q6_K, 2048, 4096, 32), (G.Q2_K, 300, 512, 13)],     # mixed paths, then smaller
+    [(G.Q6_K, 1024, 4096, 300), (G.Q8_0, 512, 2048, 40)],   # prefill GEMMs, then smaller
 ]
 
 
