@@ -967,7 +967,8 @@ __global__ __launch_bounds__(256) void k_prefill_sum(float *__restrict__ out,
         for (int z = 0; z < nz; z++) v += *reinterpret_cast<const f4 *>(part + z * n + i4 * 4);
         *reinterpret_cast<f4 *>(out + i4 * 4) = v;
     } else {
-        for (size_t i = i4 * 4; i < n; i++) {
+        // this thread's four elements (fewer at the end)
+        for (size_t i = i4 * 4; i < n && i < i4 * 4 + 4; i++) {
             float v = out[i];
             for (int z = 0; z < nz; z++) v += part[z * n + i];
             out[i] = v;

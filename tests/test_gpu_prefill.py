@@ -116,13 +116,15 @@ def test_prefill_many_tiles_ragged(oracle, hip):
 
 
 @pytest.mark.parametrize("out_dim,in_dim,n_tok", [(4096, 14336, 300), (700, 2304, 40),
-                                                  (2048, 4096, 200)])
+                                                  (2048, 4096, 200), (1023, 4096, 33),
+                                                  (1, 2048, 35)])
 def test_prefill_k_split(oracle, hip, out_dim, in_dim, n_tok):
     """Grids of fewer than 128 workgroups split K across workgroups and add
     the partial sums in split order: the FFN-down shape (4096 rows, K =
     14336: 5 splits of 11 or 12 super-blocks), 9 super-blocks in 4 uneven
-    splits with a ragged last row tile, and 2048 x 4096 (8 splits of 2
-    super-blocks).
+    splits with a ragged last row tile, 2048 x 4096 (8 splits of 2
+    super-blocks), and outputs whose count is not a multiple of 4 (33 x
+    1023, 35 x 1), which the split sum adds element by element.
     Results are deterministic: a second call gives the same bits."""
     w = synth.weight(G.Q4_K, out_dim, in_dim, seed=out_dim + in_dim)
     xb = synth.bf16_activations(n_tok, in_dim, seed=n_tok + 3).reshape(-1)

@@ -112,7 +112,8 @@ def test_prefill_f32_c1_shape(oracle, hip, dtype):
 
 
 @pytest.mark.parametrize("out_dim,in_dim,n_tok", [(4096, 4096, 512), (1024, 4096, 512),
-                                                  (4000, 768, 1281), (700, 2304, 40)])
+                                                  (4000, 768, 1281), (700, 2304, 40),
+                                                  (3, 2048, 35)])
 def test_prefill_f32_q8_0_gemm(oracle, hip, out_dim, in_dim, n_tok):
     """Q8_0 on the prefill GEMM: config C2's attention shapes at T = 512
     (4096 x 4096 splits K 4 ways, 1024 x 4096 16 ways), 16 x 11 tiles with
@@ -131,13 +132,16 @@ def test_prefill_f32_q8_0_gemm(oracle, hip, out_dim, in_dim, n_tok):
 
 
 @pytest.mark.parametrize("out_dim,in_dim,n_tok", [(14336, 4096, 512), (4096, 14336, 512),
-                                                  (4000, 2048, 1281), (700, 4096, 40)])
+                                                  (4000, 2048, 1281), (700, 4096, 40),
+                                                  (1, 2048, 33), (17, 6144, 200)])
 def test_prefill_f32_q6_k_gemm(oracle, hip, out_dim, in_dim, n_tok):
     """Q6_K on the prefill GEMM: the C1 FFN shapes at T = 512 (14336 x 4096
     unsplit; 4096 x 14336 splits K 4 ways, 14 blocks each, so splits start
     inside a super-tile), 16 x 11 tiles with a ragged last row tile (4000
-    rows) and a 1-token last token tile, and 16 blocks in 8 splits with 40
-    tokens. Repeated calls are bit-identical."""
+    rows) and a 1-token last token tile, 16 blocks in 8 splits with 40
+    tokens, a one-row matrix of one super-tile (every copy of the tile's
+    other rows repeats row 0), and 17 rows of three super-tiles. Repeated
+    calls are bit-identical."""
     w = synth.weight(G.Q6_K, out_dim, in_dim, seed=2700 + out_dim)
     x = synth.activations(n_tok, in_dim, seed=2701 + n_tok).reshape(-1)
     got = run_dev(hip, G.Q6_K, w, x, n_tok, in_dim, out_dim)
@@ -146,7 +150,7 @@ def test_prefill_f32_q6_k_gemm(oracle, hip, out_dim, in_dim, n_tok):
     edges = np.arange(128, n_tok, 128)
     tokens = np.unique(np.concatenate([[0, 1, n_tok - 1], edges - 1, edges,
                                        np.linspace(0, n_tok - 1, 8).astype(int)]))
-    check(oracle, got, w, x, tokens, G.Q6_K, n_tok, in_dim, out_dim, REL_TOL, True)
+    check(oracle, got, w, x, tokens, G.Q6_K, n_tok, in_dim, out_dim, REL_TOL, out_dim >= 1000)
 
 
 @pytest.mark.parametrize("dtype", [G.Q4_K, G.Q8_0, G.Q6_K])
