@@ -153,6 +153,28 @@ def test_prefill_f32_q6_k_gemm(oracle, hip, out_dim, in_dim, n_tok):
     check(oracle, got, w, x, tokens, G.Q6_K, n_tok, in_dim, out_dim, REL_TOL, out_dim >= 1000)
 
 
+@pytest.mark.parametrize("dtype", [G.Q6_K, G.Q8_0])
+def test_prefill_f32_special_blocks(oracle, hip, dtype):
+    """The Q6_K and Q8_0 GEMMs on blocks with zero, subnormal and small
+    normal d (a third of the blocks), and for Q6_K int8 scales of -128 and
+    127 in another third, 64 x 2048 with 33 tokens (K split 4 ways)."""
+    out_dim, in_dim, n_tok = 64, 2048, 33
+    bb, d_at = (210, 208) if dtype == G.Q6_K else (34, 0)
+    w = synth.weight(dtype, out_dim, in_dim, seed=2800).reshape(-1, bb).copy()
+    g = np.random.default_rng(2801)
+    idx = g.choice(w.shape[0], size=w.shape[0] // 3, replace=False)
+    choices = np.array([0x0000, 0x0001, 0x03FF, 0x0400, 0x1400, 0x2000], np.uint16)
+    w[idx, d_at:d_at + 2] = g.choice(choices, size=len(idx)).view(np.uint8).reshape(-1, 2)
+    if dtype == G.Q6_K:
+        rest = np.setdiff1d(np.arange(w.shape[0]), idx)[: w.shape[0] // 3]
+        sc = g.choice(np.array([-128, 127], np.int8), size=(len(rest), 16))
+        w[rest, 192:208] = sc.view(np.uint8)
+    w = w.reshape(-1)
+    x = synth.activations(n_tok, in_dim, seed=2802).reshape(-1)
+    got = run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim)
+    check(oracle, got, w, x, np.arange(n_tok), dtype, n_tok, in_dim, out_dim, REL_TOL, False)
+
+
 @pytest.mark.parametrize("dtype", [G.Q4_K, G.Q8_0, G.Q6_K])
 def test_prefill_f32_unaligned_large_grid(oracle, hip, dtype):
     """x off 16-byte alignment on a grid that does not split K (56 x 3
