@@ -1,6 +1,6 @@
-// Prefill GEMM: out[t, o] = sum_i deq(W)[o, i] * x[t, i] for a Q4_K weight W
-// [out_dim x in_dim] and bf16 or f32 activations x [n_tok x in_dim], fp32
-// output.
+// Prefill GEMM: out[t, o] = sum_i deq(W)[o, i] * x[t, i] for a Q4_K, Q8_0 or
+// Q6_K weight W [out_dim x in_dim] and bf16 or f32 activations x [n_tok x
+// in_dim], fp32 output.
 //
 // The reference computes this as matmul_quant_f32 (backend-cpu/src/ops/
 // quant_matmul.rs:45-119): every weight row is dequantised once per token and
@@ -20,7 +20,9 @@
 //    B operand, so every lane ends with 4 consecutive outputs of one token.
 //    k_prefill_q4k_w8 runs it: a workgroup of 8 wavefronts covers 256 weight
 //    rows x 128 tokens, two wavefronts per SIMD that split K between them
-//    (described at the kernel).
+//    (described at the kernel). k_prefill_q8_w8 (w = f16(d) * q) and
+//    k_prefill_q6_w8 (w = f16(d*sc) * (q - 32)) keep that workgroup and
+//    change only the weight stage and the dequantisation.
 #include "kernels.h"
 
 #include <algorithm>
@@ -826,8 +828,6 @@ __global__ __launch_bounds__(512) void k_prefill_q6_w8(const uint8_t *__restrict
         uint2 ql, qh;
         uint32_t sc;
     };
-    // per-lane bases (row 64 wr + r16 of stage 0), so token tile nt and the
-    // stage are immediate offsets
     // one per-lane base (row 64 wr + r16 of stage 0, the chunk-0 ql field):
     // the chunk-1 ql and the qh fields are at base ^ 32 and base ^ 64 (slots
     // q / 2 + 2 and + 4 under the swizzle), token tile nt and the stage are
