@@ -28,7 +28,14 @@ prefill      = BASELINE.json configs[4] (C4): Q4_K weight (out, in) =
                2048, fp32 output, on the MFMA path; TFLOP/s = 2 T in out / the
                event-timed mean of a run of back-to-back calls (activation
                pre-pass + GEMM), against the 2.5 PFLOP/s dense f16/bf16 MFMA
-               peak, with its own bounded CPU-oracle sample.
+               peak, with its own bounded CPU-oracle sample. The GEMM and
+               pre-pass durations come from the same kernel-trace pass as the
+               roofline, MFMA busy from one rocprofv3 --pmc pass.
+
+Output: ONE compact JSON line on stdout. Every prefill figure is a flat
+scalar member of "prefill"; the other configs are short rows in "extra".
+`--detail-out FILE` writes the full per-case tables, traces and counter
+details beside it.
 
 `--gpus N` with N > 1 exits: this build targets one GPU.
 """
@@ -75,7 +82,13 @@ def parse():
     ap.add_argument("--moe-probe", type=int, default=0, metavar="T",
                     help="internal: only run the C3 routed-expert call at T tokens 8 times "
                          "(for rocprofv3 kernel traces; prints no JSON)")
+    ap.add_argument("--prefill-pmc-probe", action="store_true",
+                    help="internal: the C4 prefill call at T = 512 and 2048, five times each, "
+                         "for the MFMA-busy counter pass (prints no JSON)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C4 prefill leg")
+    ap.add_argument("--detail-out", default="",
+                    help="also write the full per-case results (every leg's tables, traces and "
+                         "counter details) as JSON to this file; stdout keeps the compact line")
     ap.add_argument("--prefill-iters", type=int, default=20)
     return ap.parse_args()
 
@@ -465,12 +478,19 @@ def batch_probe():
         del reps, prep
 
 
+# C4 prefill calls the trace child runs after the batch-1 GEMVs: (T, calls);
+# the first PF_TRACE_SKIP of each T are dropped (warm-up)
+PF_TRACE = [(512, 12), (2048, 8)]
+PF_TRACE_SKIP = 2
+
+
 def gemv_probe():
     """Run under rocprofv3 --kernel-trace by kernel_trace(): the batch-1
     GEMVs of PROBE_GEMVS, TRACE_LAUNCHES launches each through
     matmul_quant_f32_dev (one kernel per call at batch 1), every launch
     reading a different weight copy (> 640 MB of copies per shape) so the
-    weights stream from HBM."""
+    weights stream from HBM; then the C4 prefill call (Q4_K 14336x4096,
+    bf16 x) at the token counts of PF_TRACE."""
     import torch
     from rsllm_amd import backend as B
     from rsllm_amd import synth
@@ -494,6 +514,25 @@ def gemv_probe():
                                    x.numel(), 1, in_dim, out_dim, dtype, sptr)
         torch.cuda.synchronize()
         del reps, prep
+    out_dim, in_dim = 14336, 4096
+    w = torch.from_numpy(synth.weight(G.Q4_K, out_dim, in_dim, seed=404)).to(dev)
+    for T, calls in PF_TRACE:
+        x = torch.from_numpy(synth.bf16_activations(T, in_dim, seed=405).reshape(-1)).to(dev)
+        y = torch.empty(T * out_dim, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(calls):
+            B.matmul_q4k_bf16_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
+                                  x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
+        torch.cuda.synchronize()
+        del x, y
+
+
+def _summary(us):
+    us = np.asarray(us, dtype=np.float64)
+    return {"n": int(us.size), "us_mean": round(float(us.mean()), 3),
+            "us_median": round(float(np.median(us)), 3),
+            "us_p10": round(float(np.percentile(us, 10)), 3),
+            "us_p90": round(float(np.percentile(us, 90)), 3)}
 
 
 def kernel_trace():
@@ -529,16 +568,88 @@ def kernel_trace():
     if len(durs) != TRACE_LAUNCHES * len(PROBE_GEMVS):
         return {"error": f"expected {TRACE_LAUNCHES * len(PROBE_GEMVS)} k_gemv1 dispatches, "
                          f"found {len(durs)}"}
-    out = []
+    gemv = []
     for si, (tag, dname, out_dim, in_dim) in enumerate(PROBE_GEMVS):
         part = durs[si * TRACE_LAUNCHES:(si + 1) * TRACE_LAUNCHES][8:]
-        us = np.array([v for _, v in part], dtype=np.float64) / 1e3
-        out.append({"config": tag, "dtype": dname, "shape": f"{out_dim}x{in_dim}",
-                    "kernel": part[0][0].split("(")[0], "n": int(us.size),
-                    "us_mean": round(float(us.mean()), 3),
-                    "us_median": round(float(np.median(us)), 3),
-                    "us_p10": round(float(np.percentile(us, 10)), 3),
-                    "us_p90": round(float(np.percentile(us, 90)), 3)})
+        gemv.append({"config": tag, "dtype": dname, "shape": f"{out_dim}x{in_dim}",
+                     "kernel": part[0][0].split("(")[0],
+                     **_summary([v / 1e3 for _, v in part])})
+    # prefill: per call one pre-pass (k_prefill_x) and one GEMM (k_prefill_q4k_w8)
+    pre = [v for n, v in rows if "k_prefill_x" in n]
+    gemm = [v for n, v in rows if "k_prefill_q4k_w8" in n]
+    n_calls = sum(c for _, c in PF_TRACE)
+    prefill = []
+    if len(pre) == n_calls and len(gemm) == n_calls:
+        o = 0
+        for T, calls in PF_TRACE:
+            sl = slice(o + PF_TRACE_SKIP, o + calls)
+            prefill.append({"tokens": T, "gemm": _summary([v / 1e3 for v in gemm[sl]]),
+                            "prepass": _summary([v / 1e3 for v in pre[sl]])})
+            o += calls
+    else:
+        prefill = {"error": f"expected {n_calls} prefill calls, found {len(pre)} pre-passes and "
+                            f"{len(gemm)} GEMMs"}
+    return {"gemv": gemv, "prefill": prefill}
+
+
+def prefill_pmc_probe():
+    """Run under rocprofv3 --pmc by prefill_mfma_busy(): the C4 prefill call
+    (Q4_K 14336x4096, bf16 x) five times at T = 512, then five times at
+    T = 2048."""
+    prefill_probe(512)
+    prefill_probe(2048)
+
+
+# MI355X: 256 CUs of 4 SIMDs in 8 XCDs (GRBM_GUI_ACTIVE is summed over the XCDs)
+N_SIMDS, N_XCDS = 1024, 8
+
+
+def prefill_mfma_busy():
+    """MFMA utilisation of the C4 prefill GEMM: one rocprofv3 --pmc pass
+    (SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_MFMA, SQ_INSTS_VALU, GRBM_GUI_ACTIVE)
+    over a child run of prefill_pmc_probe(). Busy fraction = matrix-pipe busy
+    cycles per SIMD / the kernel's GPU cycles (GRBM_GUI_ACTIVE per XCD), the
+    median over the five dispatches of each T."""
+    import shutil
+    import sqlite3
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(exe):
+        return {"error": "rocprofv3 not found"}
+    here = os.path.abspath(__file__)
+    env = dict(os.environ, TMPDIR="/tmp")
+    d = tempfile.mkdtemp(prefix="rsllm_pfpmc_", dir="/tmp")
+    ctrs = ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "GRBM_GUI_ACTIVE"]
+    cmd = ["timeout", "-s", "KILL", "120", exe, "--pmc", *ctrs, "-d", d, "-o", "p", "--",
+           sys.executable, here, "--prefill-pmc-probe"]
+    try:
+        r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True, timeout=150)
+    except subprocess.TimeoutExpired:
+        return {"error": "prefill counter pass timed out"}
+    dbs = [os.path.join(root, f) for root, _, fs in os.walk(d) for f in fs if f.endswith(".db")]
+    if r.returncode != 0 or not dbs:
+        return {"error": f"prefill counter pass failed (rc {r.returncode})",
+                "stderr_tail": r.stderr[-400:]}
+    rows = sqlite3.connect(dbs[0]).execute(
+        "select dispatch_id, name, counter_name, counter_value from pmc_events "
+        "order by dispatch_id").fetchall()
+    shutil.rmtree(d, ignore_errors=True)
+    per = {}
+    for did, name, cn, v in rows:
+        if "k_prefill_q4k_w8" in name:
+            per.setdefault(did, {})[cn] = per.get(did, {}).get(cn, 0.0) + float(v)
+    disp = [per[k] for k in sorted(per)]
+    if len(disp) != 10:
+        return {"error": f"expected 10 GEMM dispatches, found {len(disp)}"}
+    out = {"counters": ctrs, "simds": N_SIMDS, "xcds": N_XCDS}
+    for j, T in enumerate((512, 2048)):
+        busy = [c["SQ_VALU_MFMA_BUSY_CYCLES"] / N_SIMDS / (c["GRBM_GUI_ACTIVE"] / N_XCDS)
+                for c in disp[5 * j:5 * j + 5]]
+        valu = [(c["SQ_INSTS_VALU"] - c["SQ_INSTS_MFMA"]) / c["SQ_INSTS_MFMA"]
+                for c in disp[5 * j:5 * j + 5]]
+        out[f"t{T}"] = {"mfma_busy": round(float(np.median(busy)), 4),
+                        "valu_per_mfma": round(float(np.median(valu)), 3)}
     return out
 
 
@@ -686,7 +797,7 @@ def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
         rows.append(gemv_case("C1", G.Q6_K, 14336, 4096, n_tok, 510))
         rows.append(gemv_case("C1", G.Q6_K, 4096, 14336, n_tok, 520))
     for (o, i_) in ((4096, 4096), (1024, 4096)):
-        for n_tok in (1, 8, 32):
+        for n_tok in (1, 2, 4, 8, 16, 32):
             rows.append(gemv_case("C2", G.Q8_0, o, i_, n_tok, 530 + o // 1024))
     out["gemv"] = rows
     _progress("extra: gemv done")
@@ -868,7 +979,7 @@ def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
     per_expert = (gate.nbytes + up.nbytes + down.nbytes) // n_expert
     n_rout = 8
     moe = []
-    for T in (1, 8, 32):
+    for T in (1, 2, 4, 8, 16, 32):
         x_host = synth.activations(T, n_embd, 610 + T).reshape(-1)
         routs = [synth.moe_routing(T, n_expert, k, 620 + T + 1000 * r) for r in range(n_rout)]
         ids, wts = routs[0]
@@ -929,6 +1040,9 @@ def main():
     if args.pmc_probe:
         pmc_probe()
         return
+    if args.prefill_pmc_probe:
+        prefill_pmc_probe()
+        return
     if args.gemv_probe:
         gemv_probe()
         return
@@ -947,6 +1061,8 @@ def main():
     _progress("counter passes done")
     trace = {"skipped": True} if args.no_trace else kernel_trace()
     _progress("kernel-trace pass done")
+    pf_busy = {"skipped": True} if (args.no_trace or args.no_prefill) else prefill_mfma_busy()
+    _progress("prefill counter pass done")
 
     import torch
 
@@ -1045,9 +1161,9 @@ def main():
     # roofline from the kernel trace of the same launches when the trace pass
     # ran (its per-dispatch durations exclude launch gaps); the event mean
     # stays beside it
-    trace_ok = isinstance(trace, list)
+    trace_ok = isinstance(trace.get("gemv"), list)
     if trace_ok:
-        tr_us = [trace[si]["us_mean"] for si in range(len(mats))]
+        tr_us = [trace["gemv"][si]["us_mean"] for si in range(len(mats))]
         dom = max(range(len(mats)), key=lambda s: tr_us[s])
         dom_us = tr_us[dom]
     else:
@@ -1133,23 +1249,122 @@ def main():
             "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4),
             "traffic": traffic.get(per_kernel[dom]["shape"]) if traffic else None,
-            "traffic_by_shape": traffic,
-            "traffic_detail": traffic_detail,
             "kernel": "rsllm_hip::k_gemv1<FQ6K, NW, PD, GPT> (x quantised in LDS, one launch)",
             "kernel_shape": per_kernel[dom]["shape"],
             "kernel_us_mean": round(dom_us, 3),
             "kernel_us_from": "rocprofv3 kernel trace" if trace_ok else "HIP events",
             "kernel_us_events": round(kern_us[dom], 3),
             "achieved_events": round(ach_events, 2),
-            "trace": trace,
         },
-        "per_kernel": per_kernel,
         "cpu_baseline": cpu_baseline,
         "check": check,
-        "prefill": prefill,
-        "extra": extra,
     }
+    if trace_ok:
+        for e in trace["gemv"]:
+            key = f"trace_{e['dtype']}_{e['shape']}_us"
+            line["roofline"][key] = e["us_mean"]
+    if traffic:
+        for shape, nb in traffic.items():
+            line["roofline"][f"traffic_{shape}"] = nb
+    line["prefill"] = prefill_scalars(prefill, trace.get("prefill"), pf_busy)
+    line["extra"] = extra_compact(extra)
+    detail = {"per_kernel": per_kernel, "trace": trace, "traffic_by_shape": traffic,
+              "traffic_detail": traffic_detail, "prefill_mfma_busy": pf_busy,
+              "prefill": prefill, "extra": extra}
+    if args.detail_out:
+        with open(args.detail_out, "w") as f:
+            json.dump({"line": line, "detail": detail}, f, indent=1)
     print(json.dumps(line))
+
+
+def prefill_scalars(pf, pf_trace, pf_busy):
+    """The C4 prefill results as flat scalar members (whole call by HIP
+    events, GEMM and pre-pass by kernel trace, MFMA busy by counters, the CPU
+    baseline), so every figure survives a reader that keeps scalars only."""
+    if pf is None:
+        return None
+    peak = MFMA_F16_PEAK_TFLOPS
+    out = {"workload": pf["workload"], "peak_tflops": peak, "unit": "TFLOP/s"}
+    for e in pf["by_tokens"]:
+        t = e["tokens"]
+        out[f"t{t}_us"] = e["us_per_op"]
+        out[f"t{t}_tflops"] = e["tflops"]
+        out[f"t{t}_frac"] = e["frac_of_peak"]
+        if "check" in e:
+            out[f"t{t}_max_rel_err_vs_oracle"] = e["check"]["max_rel_err_vs_oracle"]
+    for e in pf.get("f32_x", []):
+        t = e["tokens"]
+        out[f"t{t}_f32x_us"] = e["us_per_op"]
+        out[f"t{t}_f32x_frac"] = e["frac_of_peak"]
+        if "check" in e:
+            out[f"t{t}_f32x_max_rel_err_vs_oracle"] = e["check"]["max_rel_err_vs_oracle"]
+    if isinstance(pf_trace, list):
+        out["kernel_us_from"] = "rocprofv3 kernel trace (k_prefill_q4k_w8, k_prefill_x)"
+        for e in pf_trace:
+            t = e["tokens"]
+            us = e["gemm"]["us_mean"]
+            out[f"t{t}_kernel_us"] = us
+            out[f"t{t}_kernel_frac"] = round(2.0 * t * 4096 * 14336 / (us * 1e-6) / 1e12 / peak, 4)
+            out[f"t{t}_prepass_us"] = e["prepass"]["us_mean"]
+    elif pf_trace is not None:
+        out["kernel_trace_error"] = str(pf_trace)[:120]
+    if isinstance(pf_busy, dict) and "t512" in pf_busy:
+        out["mfma_busy_from"] = ("rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs / "
+                                 "(GRBM_GUI_ACTIVE / 8 XCDs), this run")
+        for t in (512, 2048):
+            out[f"t{t}_mfma_busy"] = pf_busy[f"t{t}"]["mfma_busy"]
+            out[f"t{t}_valu_per_mfma"] = pf_busy[f"t{t}"]["valu_per_mfma"]
+    elif pf_busy is not None and not pf_busy.get("skipped"):
+        out["mfma_busy_error"] = str(pf_busy)[:120]
+    for e in pf.get("formats", []):
+        out[f"{e['format'].lower()}_t{e['tokens']}_us"] = e["us_per_op"]
+        out[f"{e['format'].lower()}_t{e['tokens']}_frac"] = e["frac_of_peak"]
+    for e in pf.get("k_split", []):
+        out[f"ksplit_{e['shape']}_t{e['tokens']}_us"] = e["us_per_op"]
+        out[f"ksplit_{e['shape']}_t{e['tokens']}_frac"] = e["frac_of_peak"]
+    for e in pf.get("dense_f16_library", []):
+        out[f"dense_f16_library_t{e['tokens']}_frac"] = e["frac_of_peak"]
+    cases = pf.get("mfma_ceiling", {}).get("by_case", [])
+    for e in cases:
+        if e["valu_per_mfma"] in (0.0, 2.0) and e["waves_per_simd"] == 2:
+            out[f"mfma_issue_ceiling_{int(e['valu_per_mfma'])}valu_frac"] = e["frac_of_peak"]
+    cb = pf.get("cpu_baseline")
+    if cb:
+        out["cpu_baseline_tflops"] = cb["value"]
+        out["cpu_baseline_cores"] = cb["cores"]
+        out["cpu_baseline_kind"] = cb["kind"]
+        out["cpu_baseline_sample"] = cb["sample"]
+    return out
+
+
+def extra_compact(ex):
+    """The other configs as short rows (the full tables go to --detail-out):
+    gemv [config dtype shape B, us, frac of 8 TB/s, max rel err vs oracle];
+    q8_int8 [shape B, quantize us, matmul us, frac, bit-exact];
+    moe [T, us, frac, active experts]; caller_chain [op shape B, us, frac];
+    stream_read [config, us, frac]."""
+    if ex is None:
+        return None
+
+    def r(v, n=4):
+        return None if v is None else round(v, n)
+    out = {"device_copy_GBps": ex["device_copy"]["GBps"]}
+    out["gemv"] = [[f"{e['config']} {e['dtype']} {e['shape']} B={e['batch']}", e["us"],
+                    e["frac_hbm"], r(e.get("max_rel_err_vs_oracle"), 7)] for e in ex["gemv"]]
+    out["stream_read"] = [[e["config"], e["us"], e["frac_hbm"]] for e in ex["stream_read"]]
+    out["q8_int8"] = [[f"{e['shape']} B={e['batch']}", e["quantize_us"], e["matmul_us"],
+                       e["frac_hbm"], e.get("bit_exact_vs_oracle")] for e in ex["q8_int8"]]
+    out["caller_chain"] = [[f"{e['op']} {e['dtype']} B={e['batch']}", e["us"], e["frac_hbm"]]
+                           for e in ex["caller_chain"]]
+    out["model_upload_GBps"] = ex["model_upload"]["GBps"]
+    out["moe_workload"] = ex["moe"]["workload"]
+    out["moe"] = [[e["tokens"], e["us"], e["frac_hbm"], e["active_experts"]]
+                  for e in ex["moe"]["by_tokens"]]
+    m1 = ex["moe"]["by_tokens"][0]
+    if "max_rel_err_vs_oracle" in m1:
+        out["moe_t1_max_rel_err_vs_oracle"] = r(m1["max_rel_err_vs_oracle"], 7)
+        out["moe_t1_cpu_baseline"] = m1["cpu_baseline"]
+    return out
 
 
 if __name__ == "__main__":
