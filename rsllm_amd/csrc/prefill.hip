@@ -23,6 +23,15 @@
 //    (described at the kernel). k_prefill_q8_w8 (w = f16(d) * q) and
 //    k_prefill_q6_w8 (w = f16(d*sc) * (q - 32)) keep that workgroup and
 //    change only the weight stage and the dequantisation.
+// 3. Range guard. d and dmin are f16 and sc, m, q integers, so every exact
+//    intermediate of a weight's dequantisation is a multiple of 2^-24 (f16's
+//    subnormal spacing): its f16 rounding is exact below 2^-13 and within
+//    2^-11 relative everywhere. The one failure is overflow past 65504 (d above
+//    about 69 for Q4_K, 16 for Q6_K, 511 for Q8_0), which turns the row's
+//    outputs into inf/NaN. The epilogue checks what it stores; a workgroup
+//    that stored a non-finite value runs its tile again with each row's
+//    weights scaled by a power of two 2^-E that keeps them in range, and
+//    stores again with the 2^E put back (see kPfNeedHi).
 #include "kernels.h"
 
 #include <algorithm>
@@ -196,6 +205,25 @@ __device__ __forceinline__ h8 pf_dequant8(uint32_t d0, uint32_t d1, bool hi, h2 
     return dequant_q4x8_f16(d0, d1, hi, dsc, dm);
 }
 
+// ---- weight range guard -------------------------------------------------------------
+// Every block has a bound N on its weights and on every f16 intermediate of
+// their dequantisation: 945 |d| + 63 |dmin| for Q4_K (sc, m <= 63, q <=
+// 15), 4096 |d| for Q6_K (|sc| <= 128, |q - 32| <= 32), 128 |d| for Q8_0.
+// A second pass scales row r's weights by 2^-E_r, E_r = max(0, k - 14) for
+// the row's largest N = m 2^k (m in [0.5, 1)) over the blocks of the
+// workgroup's K range, so N 2^-E < 2^15 and no f16 value passes 2^15 (1 +
+// 2^-11)^2 < 65504. With E_r > 0 a scaled scale is no longer a multiple of
+// 2^-24 and an f16 rounding may be off by 2^(E_r - 25) <= 2^-38 N absolute.
+constexpr float kPfNeedHi = 32768.0f;
+__device__ __forceinline__ int pf_row_exponent(float n) {
+    if (!(n > kPfNeedHi && n <= 3.4e38f)) return 0;
+    int k;
+    (void)frexpf(n, &k);  // n = m 2^k, m in [0.5, 1)
+    return k - 14;
+}
+// LDS words after a GEMM's stages: the workgroup's flag, then E of its 256 rows
+constexpr int kPfGuardBytes = 16 + 4 * kPfRowsWg;
+
 // ---- 8-wavefront GEMM: two K groups per workgroup -----------------------------
 // The workgroup covers 256 weight rows x 128 tokens with 8 wavefronts: wave w
 // owns rows 64 (w & 3) .. + 63 for all 128 tokens (8 x 4 MFMA tiles in VGPRs)
@@ -274,10 +302,13 @@ __device__ __forceinline__ void p8_barrier_vm5() {
 // copy has landed and every stage read is done); each lane then adds both
 // groups' sums of its outputs, scales them by the token's 2^-e and stores
 // them: lane (r16, q) holds outputs 16 nt + 4q .. + 3 of token 16 mt + r16.
+// First pass (erow null): a lane that stores a non-finite value raises
+// *flag. Second pass: output o of row r is scaled by 2^(erow[r] - e_t) in
+// one step (erow: the workgroup's 256 row exponents in LDS).
 __device__ __forceinline__ void p8_epilogue(f4 (&acc)[8][4], uint8_t *smem, int kg, int wr,
                                             int lane, int n0, int t0, float *out,
                                             const float *unscale, int n_tok, int out_dim,
-                                            int ld_out) {
+                                            int ld_out, const int *erow, int *flag) {
     const int r16 = lane & 15, q = lane >> 4;
     p8_barrier_vm0();
     f4 *xch = reinterpret_cast<f4 *>(smem);
@@ -300,6 +331,7 @@ __device__ __forceinline__ void p8_epilogue(f4 (&acc)[8][4], uint8_t *smem, int 
     }
     const int ow = n0 + 64 * wr + 4 * q;
     const bool vec = ((out_dim | ld_out) & 3) == 0 && ((uintptr_t)out & 15) == 0;
+    bool bad = false;  // a stored value is inf or NaN
 #pragma unroll
     for (int ml = 0; ml < 4; ml++) {
         const int t = t0 + 16 * (4 * kg + ml) + r16;
@@ -309,215 +341,285 @@ __device__ __forceinline__ void p8_epilogue(f4 (&acc)[8][4], uint8_t *smem, int 
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) {
             const int o = ow + 16 * nt;
-            const f4 v = res[ml][nt] * us;
+            f4 v = res[ml][nt] * us;
+            if (erow) {
+                // us = 2^-e_t exactly (a normal power of two)
+                const int eu = (int)((__float_as_uint(us) >> 23) & 0xFFu) - 127;
+                const int lr = 64 * wr + 16 * nt + 4 * q;
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = ldexpf(res[ml][nt][i], erow[lr + i] + eu);
+            }
             if (vec && o + 3 < out_dim) {
                 *reinterpret_cast<f4 *>(orow + o) = v;
+                if (!erow)
+                    bad |= !(__builtin_isfinite(v[0]) && __builtin_isfinite(v[1]) &&
+                             __builtin_isfinite(v[2]) && __builtin_isfinite(v[3]));
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    if (o + i < out_dim) orow[o + i] = v[i];
+                    if (o + i < out_dim) {
+                        orow[o + i] = v[i];
+                        if (!erow) bad |= !__builtin_isfinite(v[i]);
+                    }
             }
         }
     }
+    if (bad) *flag = 1;
 }
 
-template <int PAR, bool MORE> struct p8_step {
-    static constexpr int par = PAR;    // step parity within the super-block
-    static constexpr bool more = MORE;  // a next step exists
+template <int PAR, bool MORE, bool SCALED = false> struct p8_step {
+    static constexpr int par = PAR;         // step parity within the super-block
+    static constexpr bool more = MORE;      // a next step exists
+    static constexpr bool scaled = SCALED;  // a second pass: row exponents apply
 };
+
+// Between the passes of a GEMM workgroup: every stored value is checked and
+// every stage read; returns whether any was inf or NaN (uniform).
+__device__ __forceinline__ bool pf_again(const int *flag) {
+    __syncthreads();
+    return __builtin_amdgcn_readfirstlane(*flag) != 0;
+}
 
 //
 // K split (blockIdx.z of gridDim.z splits): split z covers super-blocks
 // [z nbt / S, (z + 1) nbt / S) of the nbt in a row and writes its sums to
 // `out` (z = 0) or to slice z - 1 of `part` (n_tok x ld_out each), which
 // k_prefill_sum then adds into `out` in split order.
-__global__ __launch_bounds__(512) void k_prefill_q4k_w8(const uint8_t *__restrict__ w,
-                                                        const _Float16 *__restrict__ xh,
+__global__ __launch_bounds__(512) void k_prefill_q4k_w8(const uint8_t *__restrict__ w_arg,
+                                                        const _Float16 *__restrict__ xh_arg,
                                                         const float *__restrict__ unscale,
-                                                        float *__restrict__ out,
+                                                        float *__restrict__ out_arg,
                                                         float *__restrict__ part, int n_tok,
                                                         int in_dim, int out_dim, int ld_out) {
-    __shared__ __align__(16) uint8_t smem[kP8Lds];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wr = wv & 3, kg = wv >> 2;
-    const int r16 = lane & 15, q = lane >> 4;
-    const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
-    const int nbt = in_dim >> 8;  // super-blocks in a row
-    const int z = blockIdx.z, nz = gridDim.z;
-    const int kb0 = (int)((long)z * nbt / nz);
-    const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;  // super-blocks of this split (>= 1)
-    const int ns = 2 * nb;                                 // steps of one K group
-    w += (size_t)kb0 * kQ4kBytes;
-    xh += (size_t)kb0 * 256;
-    if (z > 0) out = part + (size_t)(z - 1) * n_tok * ld_out;
-    uint8_t *const act = smem + kP8ActOff + 2 * kg * kP8Act;  // this group's two step buffers
-    uint8_t *const scl = smem + kP8ScOff + kg * kPfRowsWg * 16;
-    const uint32_t row_bytes = (uint32_t)nbt * (uint32_t)kQ4kBytes;
+    __shared__ __align__(16) uint8_t smem[kP8Lds + kPfGuardBytes];
+    // range guard: the workgroup's flag, its rows' exponents (after the
+    // stages)
+    int *const flag = reinterpret_cast<int *>(smem + kP8Lds);
+    int *const erow_lds = flag + 4;
+    if (threadIdx.x == 0) *flag = 0;  // before the prologue's barrier
+    // one pass of the workgroup: setup, the tile, the epilogue
+    auto body = [&](auto pass_c) __attribute__((always_inline)) {
+        int erow = 0;  // this thread's scale row's exponent (0 in the first pass)
+        // the second pass re-derives every per-lane value from an opaque copy
+        // of the thread index, so none of the first pass's stays live across
+        // its epilogue
+        int tid = threadIdx.x;
+        if constexpr (decltype(pass_c)::value) asm volatile("" : "+v"(tid));
+        const int lane = tid & 63;
+        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int wr = wv & 3, kg = wv >> 2;
+        const int r16 = lane & 15, q = lane >> 4;
+        const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
+        const int nbt = in_dim >> 8;  // super-blocks in a row
+        const int z = blockIdx.z, nz = gridDim.z;
+        const int kb0 = (int)((long)z * nbt / nz);
+        const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;  // super-blocks of this split (>= 1)
+        const int ns = 2 * nb;                                 // steps of one K group
+        // this K split's weights and activations, its output (split 0) or
+        // partial sums (the arguments stay unchanged for the second pass)
+        const uint8_t *const w = w_arg + (size_t)kb0 * kQ4kBytes;
+        const _Float16 *const xh = xh_arg + (size_t)kb0 * 256;
+        float *const out = z > 0 ? part + (size_t)(z - 1) * n_tok * ld_out : out_arg;
+        uint8_t *const act = smem + kP8ActOff + 2 * kg * kP8Act;  // this group's two step buffers
+        uint8_t *const scl = smem + kP8ScOff + kg * kPfRowsWg * 16;
+        const uint32_t row_bytes = (uint32_t)nbt * (uint32_t)kQ4kBytes;
 
-    // DMA sources (bytes from a uniform base). Activations: instruction p
-    // moves token rows 8 (4 wr + p) .. + 7 of this group's quarter, lane i to
-    // row 8 (4 wr + p) + i / 8, slot i % 8. Rows past n_tok repeat the last
-    // token (their outputs are not stored).
-    uint32_t xoff[4];
-#pragma unroll
-    for (int p = 0; p < 4; p++) {
-        const int tl = 8 * (4 * wr + p) + (lane >> 3);
-        const int pc = (lane & 7) ^ ((tl >> 1) & 7);
-        const int t = min(t0 + tl, n_tok - 1);
-        xoff[p] = 2u * ((uint32_t)t * (uint32_t)in_dim + 64 * kg + 32 * (pc >> 2) + 8 * (pc & 3));
-    }
-    // Weights: instruction i = wv + 8k moves 16-byte pieces j = 64 i + lane of
-    // the stage, row j / 9, piece j % 9. Instructions past the last repeat it
-    // (same bytes to the same place), so every wavefront issues five.
-    uint32_t woff[5];
-#pragma unroll
-    for (int k = 0; k < 5; k++) {
-        const int i = min(wv + 8 * k, kP8WPieces - 1);
-        const int j = 64 * i + lane, row = j / 9;
-        woff[k] = (uint32_t)min(n0 + row, out_dim - 1) * row_bytes + 16u * (uint32_t)(j % 9);
-    }
-    const uint32_t lds_act = p8_lds(act), lds_w = p8_lds(smem);
-    // piece p of group step s (clamped to the last) into the buffer of step parity s % 2
-    auto dma_act = [&](int s, int p) {
-        const uint32_t dst = lds_act + (uint32_t)((s & 1) * kP8Act + 1024 * (4 * wr + p));
-        s = min(s, ns - 1);
-        p8_dma(xh + (s >> 1) * 256 + 128 * (s & 1), xoff[p], dst);
-    };
-    // piece k of super-block sb (clamped to the last) into weight stage sb % 2
-    auto dma_w = [&](int sb, int k) {
-        const uint32_t dst = lds_w + (uint32_t)((sb & 1) * kP8Blk + 1024 * min(wv + 8 * k, kP8WPieces - 1));
-        sb = min(sb, nb - 1);
-        p8_dma(w + (size_t)sb * kQ4kBytes, woff[k], dst);
-    };
-    // header of this thread's row in a weight stage -> scale records of the
-    // group's four sub-blocks: 16 bytes, {d*sc, d*sc'} {dmin*m, dmin*m'} for
-    // the even step (sub-blocks 2 kg, 2 kg + 1), then for the odd step (4 +
-    // 2 kg, 5 + 2 kg) (q4_k_scale_min, dequant/mod.rs:48-58)
-    auto scales_from_header = [&](const uint8_t *wbuf) {
-        const int row = 64 * wr + lane;
-        const uint4 hd = *reinterpret_cast<const uint4 *>(wbuf + kQ4kBytes * row);
-        const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
-        const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu, m_lo = hd.z & 0x3F3F3F3Fu;
-        const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
-        const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-        const int b = 16 * kg;  // bit offset of byte 2 kg
-        uint32_t rec[4];
-#pragma unroll
-        for (int hf = 0; hf < 2; hf++) {
-            const uint32_t sw = (hf ? sc_hi : sc_lo) >> b, mw = (hf ? m_hi : m_lo) >> b;
-            const _Float16 a0 = (_Float16)(d * (float)(sw & 0xFFu));
-            const _Float16 a1 = (_Float16)(d * (float)((sw >> 8) & 0xFFu));
-            const _Float16 m0 = (_Float16)(dmin * (float)(mw & 0xFFu));
-            const _Float16 m1 = (_Float16)(dmin * (float)((mw >> 8) & 0xFFu));
-            rec[2 * hf] = __builtin_bit_cast(uint32_t, h2{a0, a1});
-            rec[2 * hf + 1] = __builtin_bit_cast(uint32_t, h2{m0, m1});
+        // DMA sources (bytes from a uniform base). Activations: instruction p
+        // moves token rows 8 (4 wr + p) .. + 7 of this group's quarter, lane i to
+        // row 8 (4 wr + p) + i / 8, slot i % 8. Rows past n_tok repeat the last
+        // token (their outputs are not stored).
+        uint32_t xoff[4];
+    #pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int tl = 8 * (4 * wr + p) + (lane >> 3);
+            const int pc = (lane & 7) ^ ((tl >> 1) & 7);
+            const int t = min(t0 + tl, n_tok - 1);
+            xoff[p] = 2u * ((uint32_t)t * (uint32_t)in_dim + 64 * kg + 32 * (pc >> 2) + 8 * (pc & 3));
         }
-        *reinterpret_cast<uint4 *>(scl + 16 * row) = make_uint4(rec[0], rec[1], rec[2], rec[3]);
-    };
-    const int qbyte = 16 + 32 * kg + 8 * q;  // the lane's qs bytes in a block, step parity 0
-    const int aswz = (r16 >> 1) & 7;
-    // this lane's qs bytes and scale records of row tile nt at step parity hf
-    uint2 qs[4], sc[4];
-    auto load_weights = [&](const uint8_t *wbuf, int hf) {
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++) {
-            const int row = 64 * wr + 16 * nt + r16;
-            qs[nt] = *reinterpret_cast<const uint2 *>(wbuf + kQ4kBytes * row + qbyte + 64 * hf);
-            sc[nt] = *reinterpret_cast<const uint2 *>(scl + 16 * row + 8 * hf);
+        // Weights: instruction i = wv + 8k moves 16-byte pieces j = 64 i + lane of
+        // the stage, row j / 9, piece j % 9. Instructions past the last repeat it
+        // (same bytes to the same place), so every wavefront issues five.
+        uint32_t woff[5];
+    #pragma unroll
+        for (int k = 0; k < 5; k++) {
+            const int i = min(wv + 8 * k, kP8WPieces - 1);
+            const int j = 64 * i + lane, row = j / 9;
+            woff[k] = (uint32_t)min(n0 + row, out_dim - 1) * row_bytes + 16u * (uint32_t)(j % 9);
         }
-    };
-    auto dequant = [&](int c, int nt) -> h8 {
-        const h2 d2 = __builtin_bit_cast(h2, sc[nt].x), m2 = __builtin_bit_cast(h2, sc[nt].y);
-        return pf_dequant8(qs[nt].x, qs[nt].y, c != 0, c ? d2.yy : d2.xx, c ? m2.yy : m2.xx);
-    };
-    auto read_a = [&](const uint8_t *buf, int c, int mt) -> h8 {
-        return *reinterpret_cast<const h8 *>(buf + (16 * mt + r16) * 128 + 16 * ((4 * c + q) ^ aswz));
-    };
+        const uint32_t lds_act = p8_lds(act), lds_w = p8_lds(smem);
+        // piece p of group step s (clamped to the last) into the buffer of step parity s % 2
+        auto dma_act = [&](int s, int p) {
+            const uint32_t dst = lds_act + (uint32_t)((s & 1) * kP8Act + 1024 * (4 * wr + p));
+            s = min(s, ns - 1);
+            p8_dma(xh + (s >> 1) * 256 + 128 * (s & 1), xoff[p], dst);
+        };
+        // piece k of super-block sb (clamped to the last) into weight stage sb % 2
+        auto dma_w = [&](int sb, int k) {
+            const uint32_t dst = lds_w + (uint32_t)((sb & 1) * kP8Blk + 1024 * min(wv + 8 * k, kP8WPieces - 1));
+            sb = min(sb, nb - 1);
+            p8_dma(w + (size_t)sb * kQ4kBytes, woff[k], dst);
+        };
+        // header of this thread's row in a weight stage -> scale records of the
+        // group's four sub-blocks: 16 bytes, {d*sc, d*sc'} {dmin*m, dmin*m'} for
+        // the even step (sub-blocks 2 kg, 2 kg + 1), then for the odd step (4 +
+        // 2 kg, 5 + 2 kg) (q4_k_scale_min, dequant/mod.rs:48-58)
+        auto scales_from_header = [&](const uint8_t *wbuf, auto scaled_c) {
+            const int row = 64 * wr + lane;
+            const uint4 hd = *reinterpret_cast<const uint4 *>(wbuf + kQ4kBytes * row);
+            float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+            if constexpr (decltype(scaled_c)::value) {
+                d = ldexpf(d, -erow);
+                dmin = ldexpf(dmin, -erow);
+            }
+            const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu, m_lo = hd.z & 0x3F3F3F3Fu;
+            const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+            const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+            const int b = 16 * kg;  // bit offset of byte 2 kg
+            uint32_t rec[4];
+    #pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                const uint32_t sw = (hf ? sc_hi : sc_lo) >> b, mw = (hf ? m_hi : m_lo) >> b;
+                const _Float16 a0 = (_Float16)(d * (float)(sw & 0xFFu));
+                const _Float16 a1 = (_Float16)(d * (float)((sw >> 8) & 0xFFu));
+                const _Float16 m0 = (_Float16)(dmin * (float)(mw & 0xFFu));
+                const _Float16 m1 = (_Float16)(dmin * (float)((mw >> 8) & 0xFFu));
+                rec[2 * hf] = __builtin_bit_cast(uint32_t, h2{a0, a1});
+                rec[2 * hf + 1] = __builtin_bit_cast(uint32_t, h2{m0, m1});
+            }
+            *reinterpret_cast<uint4 *>(scl + 16 * row) = make_uint4(rec[0], rec[1], rec[2], rec[3]);
+        };
+        const int qbyte = 16 + 32 * kg + 8 * q;  // the lane's qs bytes in a block, step parity 0
+        const int aswz = (r16 >> 1) & 7;
+        // this lane's qs bytes and scale records of row tile nt at step parity hf
+        uint2 qs[4], sc[4];
+        auto load_weights = [&](const uint8_t *wbuf, int hf) {
+    #pragma unroll
+            for (int nt = 0; nt < 4; nt++) {
+                const int row = 64 * wr + 16 * nt + r16;
+                qs[nt] = *reinterpret_cast<const uint2 *>(wbuf + kQ4kBytes * row + qbyte + 64 * hf);
+                sc[nt] = *reinterpret_cast<const uint2 *>(scl + 16 * row + 8 * hf);
+            }
+        };
+        auto dequant = [&](int c, int nt) -> h8 {
+            const h2 d2 = __builtin_bit_cast(h2, sc[nt].x), m2 = __builtin_bit_cast(h2, sc[nt].y);
+            return pf_dequant8(qs[nt].x, qs[nt].y, c != 0, c ? d2.yy : d2.xx, c ? m2.yy : m2.xx);
+        };
+        auto read_a = [&](const uint8_t *buf, int c, int mt) -> h8 {
+            return *reinterpret_cast<const h8 *>(buf + (16 * mt + r16) * 128 + 16 * ((4 * c + q) ^ aswz));
+        };
 
-    f4 acc[8][4];
-#pragma unroll
-    for (int mt = 0; mt < 8; mt++)
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+        f4 acc[8][4];
+        h8 bq[4], a0, a1;
 
-    // prologue: super-block 0 and step 0 in, step 1 in flight, step 0's
-    // chunk-0 operands ready
-#pragma unroll
-    for (int k = 0; k < 5; k++) dma_w(0, k);
-#pragma unroll
-    for (int p = 0; p < 4; p++) dma_act(0, p);
-    p8_barrier_vm0();
-#pragma unroll
-    for (int p = 0; p < 4; p++) dma_act(1, p);  // ns >= 2; super-block 1 in step 0
-    scales_from_header(smem);
-    load_weights(smem, 0);
-    h8 bq[4];
-#pragma unroll
-    for (int nt = 0; nt < 4; nt++) bq[nt] = dequant(0, nt);
-    h8 a0 = read_a(act, 0, 0), a1 = read_a(act, 0, 1);
-
-    // One step s (super-block sb = s / 2, step parity PAR = s % 2): 16 groups
-    // (2 chunks x 8 token tiles) of 4 MFMAs. Operand reads run two groups
-    // ahead, across the step boundary; chunk 1's weights are dequantised
-    // during chunk 0, the next step's chunk 0 in groups 14, 15. In group 14
-    // every wavefront has this step's operands in registers and waits for
-    // its own copies the next step needs (its activations; on the last step
-    // of a super-block also the next super-block's weights): after the
-    // barrier those are readable, this step's activation buffer takes step
-    // s + 2 (groups 14, 15), and after the last step of a super-block its
-    // weight stage takes super-block sb + 2 (groups 1, 3, .., 9 of the next
-    // step; super-block 1 in step 0). The weight copies are issued after the
-    // activation copies of the step after, so an even step waits only for the
-    // older activation pieces (vmcnt(5)).
-    auto step = [&](int s, auto tag) {
-        constexpr int PAR = decltype(tag)::par;
-        constexpr bool MORE = decltype(tag)::more;
-        const int sb = s >> 1;
-        const uint8_t *buf = act + PAR * kP8Act;
-        const uint8_t *nbuf = act + (1 - PAR) * kP8Act;
-        h8 b1[4];
-#pragma unroll
-        for (int g = 0; g < 16; g++) {
-            const int c = g >> 3, mt = g & 7;
+        // One step s (super-block sb = s / 2, step parity PAR = s % 2): 16 groups
+        // (2 chunks x 8 token tiles) of 4 MFMAs. Operand reads run two groups
+        // ahead, across the step boundary; chunk 1's weights are dequantised
+        // during chunk 0, the next step's chunk 0 in groups 14, 15. In group 14
+        // every wavefront has this step's operands in registers and waits for
+        // its own copies the next step needs (its activations; on the last step
+        // of a super-block also the next super-block's weights): after the
+        // barrier those are readable, this step's activation buffer takes step
+        // s + 2 (groups 14, 15), and after the last step of a super-block its
+        // weight stage takes super-block sb + 2 (groups 1, 3, .., 9 of the next
+        // step; super-block 1 in step 0). The weight copies are issued after the
+        // activation copies of the step after, so an even step waits only for the
+        // older activation pieces (vmcnt(5)).
+        auto step = [&](int s, auto tag) __attribute__((always_inline)) {
+            constexpr int PAR = decltype(tag)::par;
+            constexpr bool MORE = decltype(tag)::more;
+            const int sb = s >> 1;
+            const uint8_t *buf = act + PAR * kP8Act;
+            const uint8_t *nbuf = act + (1 - PAR) * kP8Act;
+            h8 b1[4];
+    #pragma unroll
+            for (int g = 0; g < 16; g++) {
+                const int c = g >> 3, mt = g & 7;
+                __builtin_amdgcn_sched_barrier(0);
+                if (MORE && PAR == 0 && (g & 1) && g < 10) dma_w(sb + 1, g >> 1);
+                if (MORE && g == 14) {
+                    if (PAR) p8_barrier_vm0();
+                    else p8_barrier_vm5();
+                    if (PAR)
+                        scales_from_header(smem + ((sb + 1) & 1) * kP8Blk,
+                                           std::integral_constant<bool, decltype(tag)::scaled>{});
+                    load_weights(smem + ((sb + PAR) & 1) * kP8Blk, 1 - PAR);
+                }
+                h8 a2 = a1;
+                if (g + 2 < 16) a2 = read_a(buf, (g + 2) >> 3, (g + 2) & 7);
+                else if (MORE) a2 = read_a(nbuf, 0, g - 14);
+                if (MORE && g >= 14) {
+                    dma_act(s + 2, 2 * (g - 14));
+                    dma_act(s + 2, 2 * (g - 14) + 1);
+                }
+                const h8 acur = a0;
+                const h8 *bw = c ? b1 : bq;
+    #pragma unroll
+                for (int nt = 0; nt < 4; nt++)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bw[nt], acur, acc[mt][nt], 0, 0, 0);
+                if (c == 0 && (mt & 1)) b1[mt >> 1] = dequant(1, mt >> 1);
+                if (MORE && g >= 14) {
+                    bq[2 * (g - 14)] = dequant(0, 2 * (g - 14));
+                    bq[2 * (g - 14) + 1] = dequant(0, 2 * (g - 14) + 1);
+                }
+                a0 = a1;
+                a1 = a2;
+            }
             __builtin_amdgcn_sched_barrier(0);
-            if (MORE && PAR == 0 && (g & 1) && g < 10) dma_w(sb + 1, g >> 1);
-            if (MORE && g == 14) {
-                if (PAR) p8_barrier_vm0();
-                else p8_barrier_vm5();
-                if (PAR) scales_from_header(smem + ((sb + 1) & 1) * kP8Blk);
-                load_weights(smem + ((sb + PAR) & 1) * kP8Blk, 1 - PAR);
+        };
+        if constexpr (decltype(pass_c)::value) {
+            // E of this thread's scale row from its blocks' bounds
+            // E of this thread's scale row from its blocks' bounds
+            const int r = min(n0 + 64 * wr + lane, out_dim - 1);
+            const uint8_t *hp = w + (size_t)r * row_bytes;
+            float m = 0.f;
+            for (int b = 0; b < nb; b++) {
+                const uint32_t h = *reinterpret_cast<const uint32_t *>(hp + (size_t)b * kQ4kBytes);
+                m = fmaxf(m, 945.f * fabsf(f16_to_f32(h & 0xFFFFu)) + 63.f * fabsf(f16_to_f32(h >> 16)));
             }
-            h8 a2 = a1;
-            if (g + 2 < 16) a2 = read_a(buf, (g + 2) >> 3, (g + 2) & 7);
-            else if (MORE) a2 = read_a(nbuf, 0, g - 14);
-            if (MORE && g >= 14) {
-                dma_act(s + 2, 2 * (g - 14));
-                dma_act(s + 2, 2 * (g - 14) + 1);
-            }
-            const h8 acur = a0;
-            const h8 *bw = c ? b1 : bq;
-#pragma unroll
-            for (int nt = 0; nt < 4; nt++)
-                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bw[nt], acur, acc[mt][nt], 0, 0, 0);
-            if (c == 0 && (mt & 1)) b1[mt >> 1] = dequant(1, mt >> 1);
-            if (MORE && g >= 14) {
-                bq[2 * (g - 14)] = dequant(0, 2 * (g - 14));
-                bq[2 * (g - 14) + 1] = dequant(0, 2 * (g - 14) + 1);
-            }
-            a0 = a1;
-            a1 = a2;
+            erow = pf_row_exponent(m);
+            if (kg == 0) erow_lds[64 * wr + lane] = erow;
         }
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    for (int sb = 0; sb + 1 < nb; sb++) {
-        step(2 * sb, p8_step<0, true>{});
-        step(2 * sb + 1, p8_step<1, true>{});
-    }
-    step(ns - 2, p8_step<0, true>{});
-    step(ns - 1, p8_step<1, false>{});
+        // one pass over the tile: the first with E = 0, a second (scaled) with
+        // this thread's row exponent erow
+        auto run = [&](auto scaled_c) __attribute__((always_inline)) {
+            constexpr bool SC = decltype(scaled_c)::value;
+    #pragma unroll
+            for (int mt = 0; mt < 8; mt++)
+    #pragma unroll
+                for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
 
-    p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out);
+            // prologue: super-block 0 and step 0 in, step 1 in flight, step 0's
+            // chunk-0 operands ready
+    #pragma unroll
+            for (int k = 0; k < 5; k++) dma_w(0, k);
+    #pragma unroll
+            for (int p = 0; p < 4; p++) dma_act(0, p);
+            p8_barrier_vm0();
+    #pragma unroll
+            for (int p = 0; p < 4; p++) dma_act(1, p);  // ns >= 2; super-block 1 in step 0
+            scales_from_header(smem, scaled_c);
+            load_weights(smem, 0);
+    #pragma unroll
+            for (int nt = 0; nt < 4; nt++) bq[nt] = dequant(0, nt);
+            a0 = read_a(act, 0, 0);
+            a1 = read_a(act, 0, 1);
+
+            for (int sb = 0; sb + 1 < nb; sb++) {
+                step(2 * sb, p8_step<0, true, SC>{});
+                step(2 * sb + 1, p8_step<1, true, SC>{});
+            }
+            step(ns - 2, p8_step<0, true, SC>{});
+            step(ns - 1, p8_step<1, false, SC>{});
+        };
+        run(pass_c);
+        if constexpr (!decltype(pass_c)::value)
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, nullptr, flag);
+        else
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, erow_lds,
+                        nullptr);
+    };
+    body(std::false_type{});
+    if (pf_again(flag)) body(std::true_type{});
 }
 
 // ---- Q8_0 weights ----------------------------------------------------------------
@@ -540,167 +642,225 @@ constexpr int kQ8Stage = kP8Act + kQ8Qs + kQ8D;  // 36 KB per group step
 constexpr int kQ8Lds = 4 * kQ8Stage;             // 144 KB
 static_assert(2 * 4 * 16 * 64 * 16 <= kQ8Lds, "the epilogue's exchange fits");
 
-__global__ __launch_bounds__(512) void k_prefill_q8_w8(const uint8_t *__restrict__ w,
-                                                       const _Float16 *__restrict__ xh,
+__global__ __launch_bounds__(512) void k_prefill_q8_w8(const uint8_t *__restrict__ w_arg,
+                                                       const _Float16 *__restrict__ xh_arg,
                                                        const float *__restrict__ unscale,
-                                                       float *__restrict__ out,
+                                                       float *__restrict__ out_arg,
                                                        float *__restrict__ part, int n_tok,
                                                        int in_dim, int out_dim, int ld_out) {
-    __shared__ __align__(16) uint8_t smem[kQ8Lds];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wr = wv & 3, kg = wv >> 2;
-    const int r16 = lane & 15, q = lane >> 4;
-    const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
-    const int nbt = in_dim >> 8;  // super-tiles in a row
-    const int z = blockIdx.z, nz = gridDim.z;
-    const int kb0 = (int)((long)z * nbt / nz);
-    const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;
-    const int ns = 2 * nb;
-    w += (size_t)kb0 * 272;
-    xh += (size_t)kb0 * 256;
-    if (z > 0) out = part + (size_t)(z - 1) * n_tok * ld_out;
-    uint8_t *const stg = smem + 2 * kg * kQ8Stage;  // this group's two step buffers
-    const uint32_t row_bytes = (uint32_t)nbt * 272u;
+    __shared__ __align__(16) uint8_t smem[kQ8Lds + kPfGuardBytes];
+    // range guard: the workgroup's flag, its rows' exponents (after the
+    // stages)
+    int *const flag = reinterpret_cast<int *>(smem + kQ8Lds);
+    int *const erow_lds = flag + 4;
+    if (threadIdx.x == 0) *flag = 0;  // before the prologue's barrier
+    // one pass of the workgroup: setup, the tile, the epilogue
+    auto body = [&](auto pass_c) __attribute__((always_inline)) {
+        int erow = 0;  // this thread's scale row's exponent (0 in the first pass)
+        // the second pass re-derives every per-lane value from an opaque copy
+        // of the thread index, so none of the first pass's stays live across
+        // its epilogue
+        int tid = threadIdx.x;
+        if constexpr (decltype(pass_c)::value) asm volatile("" : "+v"(tid));
+        const int lane = tid & 63;
+        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int wr = wv & 3, kg = wv >> 2;
+        const int r16 = lane & 15, q = lane >> 4;
+        const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
+        const int nbt = in_dim >> 8;  // super-tiles in a row
+        const int z = blockIdx.z, nz = gridDim.z;
+        const int kb0 = (int)((long)z * nbt / nz);
+        const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;
+        const int ns = 2 * nb;
+        // this K split's weights and activations, its output (split 0) or
+        // partial sums (the arguments stay unchanged for the second pass)
+        const uint8_t *const w = w_arg + (size_t)kb0 * 272;
+        const _Float16 *const xh = xh_arg + (size_t)kb0 * 256;
+        float *const out = z > 0 ? part + (size_t)(z - 1) * n_tok * ld_out : out_arg;
+        uint8_t *const stg = smem + 2 * kg * kQ8Stage;  // this group's two step buffers
+        const uint32_t row_bytes = (uint32_t)nbt * 272u;
 
-    // DMA sources (bytes from a uniform base). Activations as in
-    // k_prefill_q4k_w8. qs: instruction p moves rows 16 (4 wr + p) .. + 15,
-    // lane i to row 16 (4 wr + p) + i / 4, slot i % 4 (holding piece
-    // (i % 4) ^ ((row >> 2) & 3) of the quarter's 64 bytes). d: lane i moves
-    // row 64 wr + i's 16-byte d run. Both cover exactly this wavefront's rows.
-    uint32_t xoff[4], qoff[4];
-#pragma unroll
-    for (int p = 0; p < 4; p++) {
-        const int tl = 8 * (4 * wr + p) + (lane >> 3);
-        const int pc = (lane & 7) ^ ((tl >> 1) & 7);
-        const int t = min(t0 + tl, n_tok - 1);
-        xoff[p] = 2u * ((uint32_t)t * (uint32_t)in_dim + 64 * kg + 32 * (pc >> 2) + 8 * (pc & 3));
-        const int row = 16 * (4 * wr + p) + (lane >> 2);
-        const int piece = (lane & 3) ^ ((row >> 2) & 3);
-        qoff[p] = (uint32_t)min(n0 + row, out_dim - 1) * row_bytes + 64u * kg + 16u * piece;
-    }
-    const uint32_t doff = (uint32_t)min(n0 + 64 * wr + lane, out_dim - 1) * row_bytes + 256u;
-    const uint32_t lds_stg = p8_lds(stg);
-    // piece p (0..8) of group step s (clamped to the last) into the buffer of
-    // step parity s % 2: 0..3 activations, 4..7 qs, 8 the d run
-    auto dma = [=](int s, int p) {
-        const uint32_t buf = lds_stg + (uint32_t)((s & 1) * kQ8Stage);
-        s = min(s, ns - 1);
-        const int sb = s >> 1, hf = s & 1;
-        if (p < 4)
-            p8_dma(xh + sb * 256 + 128 * hf, xoff[p], buf + 1024 * (4 * wr + p));
-        else if (p < 8)
-            p8_dma(w + (size_t)sb * 272 + 128 * hf, qoff[p - 4], buf + kP8Act + 1024 * (4 * wr + p - 4));
-        else
-            p8_dma(w + (size_t)sb * 272, doff, buf + kP8Act + kQ8Qs + 1024 * wr);
-    };
-    const int sw = (r16 >> 2) & 3;
-    const int qb0 = 16 * ((q >> 1) ^ sw) + 8 * (q & 1);        // chunk 0: piece q / 2
-    const int qb1 = 16 * ((2 + (q >> 1)) ^ sw) + 8 * (q & 1);  // chunk 1: piece 2 + q / 2
-    const int aswz = (r16 >> 1) & 7;
-    uint2 qs0[4], qs1[4];
-    uint32_t dd[4];  // f16 d of blocks 2u, 2u + 1
-    auto load_weights = [&](const uint8_t *buf, int hf) {
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++) {
-            const int row = 64 * wr + 16 * nt + r16;
-            qs0[nt] = *reinterpret_cast<const uint2 *>(buf + kP8Act + 64 * row + qb0);
-            qs1[nt] = *reinterpret_cast<const uint2 *>(buf + kP8Act + 64 * row + qb1);
-            dd[nt] = *reinterpret_cast<const uint32_t *>(buf + kP8Act + kQ8Qs + 16 * row +
-                                                         4 * (2 * hf + kg));
+        // DMA sources (bytes from a uniform base). Activations as in
+        // k_prefill_q4k_w8. qs: instruction p moves rows 16 (4 wr + p) .. + 15,
+        // lane i to row 16 (4 wr + p) + i / 4, slot i % 4 (holding piece
+        // (i % 4) ^ ((row >> 2) & 3) of the quarter's 64 bytes). d: lane i moves
+        // row 64 wr + i's 16-byte d run. Both cover exactly this wavefront's rows.
+        uint32_t xoff[4], qoff[4];
+    #pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int tl = 8 * (4 * wr + p) + (lane >> 3);
+            const int pc = (lane & 7) ^ ((tl >> 1) & 7);
+            const int t = min(t0 + tl, n_tok - 1);
+            xoff[p] = 2u * ((uint32_t)t * (uint32_t)in_dim + 64 * kg + 32 * (pc >> 2) + 8 * (pc & 3));
+            const int row = 16 * (4 * wr + p) + (lane >> 2);
+            const int piece = (lane & 3) ^ ((row >> 2) & 3);
+            qoff[p] = (uint32_t)min(n0 + row, out_dim - 1) * row_bytes + 64u * kg + 16u * piece;
         }
-    };
-    auto dequant = [&](int c, int nt) -> h8 {
-        const uint2 b = c ? qs1[nt] : qs0[nt];
-        const h2 d2 = __builtin_bit_cast(h2, dd[nt]);
-        const h2 ds = c ? d2.yy : d2.xx;
-        const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-        h8 r;
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const uint32_t bb = (u ? b.y : b.x) ^ 0x80808080u;
-            const h2 w01 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04010400u)) - bias) * ds;
-            const h2 w23 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04030402u)) - bias) * ds;
-            r[4 * u] = w01[0];
-            r[4 * u + 1] = w01[1];
-            r[4 * u + 2] = w23[0];
-            r[4 * u + 3] = w23[1];
-        }
-        return r;
-    };
-    auto read_a = [&](const uint8_t *buf, int c, int mt) -> h8 {
-        return *reinterpret_cast<const h8 *>(buf + (16 * mt + r16) * 128 + 16 * ((4 * c + q) ^ aswz));
-    };
+        const uint32_t doff = (uint32_t)min(n0 + 64 * wr + lane, out_dim - 1) * row_bytes + 256u;
+        const uint32_t lds_stg = p8_lds(stg);
+        // piece p (0..8) of group step s (clamped to the last) into the buffer of
+        // step parity s % 2: 0..3 activations, 4..7 qs, 8 the d run
+        auto dma = [=](int s, int p) {
+            const uint32_t buf = lds_stg + (uint32_t)((s & 1) * kQ8Stage);
+            s = min(s, ns - 1);
+            const int sb = s >> 1, hf = s & 1;
+            if (p < 4)
+                p8_dma(xh + sb * 256 + 128 * hf, xoff[p], buf + 1024 * (4 * wr + p));
+            else if (p < 8)
+                p8_dma(w + (size_t)sb * 272 + 128 * hf, qoff[p - 4], buf + kP8Act + 1024 * (4 * wr + p - 4));
+            else
+                p8_dma(w + (size_t)sb * 272, doff, buf + kP8Act + kQ8Qs + 1024 * wr);
+        };
+        const int sw = (r16 >> 2) & 3;
+        const int qb0 = 16 * ((q >> 1) ^ sw) + 8 * (q & 1);        // chunk 0: piece q / 2
+        const int qb1 = 16 * ((2 + (q >> 1)) ^ sw) + 8 * (q & 1);  // chunk 1: piece 2 + q / 2
+        const int aswz = (r16 >> 1) & 7;
+        uint2 qs0[4], qs1[4];
+        uint32_t dd[4];  // f16 d of blocks 2u, 2u + 1
+        auto load_weights = [&](const uint8_t *buf, int hf) {
+    #pragma unroll
+            for (int nt = 0; nt < 4; nt++) {
+                const int row = 64 * wr + 16 * nt + r16;
+                qs0[nt] = *reinterpret_cast<const uint2 *>(buf + kP8Act + 64 * row + qb0);
+                qs1[nt] = *reinterpret_cast<const uint2 *>(buf + kP8Act + 64 * row + qb1);
+                dd[nt] = *reinterpret_cast<const uint32_t *>(buf + kP8Act + kQ8Qs + 16 * row +
+                                                             4 * (2 * hf + kg));
+            }
+        };
+        auto dequant = [&](int c, int nt) -> h8 {
+            const uint2 b = c ? qs1[nt] : qs0[nt];
+            const h2 d2 = __builtin_bit_cast(h2, dd[nt]);
+            const h2 ds = c ? d2.yy : d2.xx;
+            const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+            h8 r;
+    #pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t bb = (u ? b.y : b.x) ^ 0x80808080u;
+                const h2 w01 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04010400u)) - bias) * ds;
+                const h2 w23 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04030402u)) - bias) * ds;
+                r[4 * u] = w01[0];
+                r[4 * u + 1] = w01[1];
+                r[4 * u + 2] = w23[0];
+                r[4 * u + 3] = w23[1];
+            }
+            return r;
+        };
+        // second pass: the two d of this thread's row (64 wr + lane) that its
+        // group uses in the step held in buf (parity hf) are rewritten in place
+        // as f16(d 2^-E); the readers of that dword are lanes of this wavefront
+        auto scale_d = [&](uint8_t *buf, int hf) {
+            uint32_t *dp = reinterpret_cast<uint32_t *>(buf + kP8Act + kQ8Qs + 16 * (64 * wr + lane) +
+                                                        4 * (2 * hf + kg));
+            const uint32_t dv = *dp;
+            const h2 sd = {(_Float16)ldexpf(f16_to_f32(dv & 0xFFFFu), -erow),
+                           (_Float16)ldexpf(f16_to_f32(dv >> 16), -erow)};
+            *dp = __builtin_bit_cast(uint32_t, sd);
+        };
+        auto read_a = [&](const uint8_t *buf, int c, int mt) -> h8 {
+            return *reinterpret_cast<const h8 *>(buf + (16 * mt + r16) * 128 + 16 * ((4 * c + q) ^ aswz));
+        };
 
-    f4 acc[8][4];
-#pragma unroll
-    for (int mt = 0; mt < 8; mt++)
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+        f4 acc[8][4];
+        h8 bq[4], a0, a1;
 
-    // prologue: step 0 in, step 1 in flight, step 0's chunk-0 operands ready
-#pragma unroll
-    for (int p = 0; p < 9; p++) dma(0, p);
-    p8_barrier_vm0();
-#pragma unroll
-    for (int p = 0; p < 9; p++) dma(1, p);  // ns >= 2
-    load_weights(stg, 0);
-    h8 bq[4];
-#pragma unroll
-    for (int nt = 0; nt < 4; nt++) bq[nt] = dequant(0, nt);
-    h8 a0 = read_a(stg, 0, 0), a1 = read_a(stg, 0, 1);
-
-    // One step: as in k_prefill_q4k_w8, with the weights in the step's
-    // buffer: in group 14 every wavefront waits for its own copies of step
-    // s + 1, after the barrier reads that step's weights and first operands,
-    // and this step's buffer takes step s + 2 (pieces 0..5 in groups 14, 15,
-    // 6..8 in groups 0, 2, 4 of the next step).
-    auto step = [&](int s, auto tag) {
-        constexpr int PAR = decltype(tag)::par;
-        constexpr bool MORE = decltype(tag)::more;
-        const uint8_t *buf = stg + PAR * kQ8Stage;
-        const uint8_t *nbuf = stg + (1 - PAR) * kQ8Stage;
-        h8 b1[4];
-#pragma unroll
-        for (int g = 0; g < 16; g++) {
-            const int c = g >> 3, mt = g & 7;
+        // One step: as in k_prefill_q4k_w8, with the weights in the step's
+        // buffer: in group 14 every wavefront waits for its own copies of step
+        // s + 1, after the barrier reads that step's weights and first operands,
+        // and this step's buffer takes step s + 2 (pieces 0..5 in groups 14, 15,
+        // 6..8 in groups 0, 2, 4 of the next step).
+        auto step = [&](int s, auto tag) __attribute__((always_inline)) {
+            constexpr int PAR = decltype(tag)::par;
+            constexpr bool MORE = decltype(tag)::more;
+            const uint8_t *buf = stg + PAR * kQ8Stage;
+            const uint8_t *nbuf = stg + (1 - PAR) * kQ8Stage;
+            h8 b1[4];
+    #pragma unroll
+            for (int g = 0; g < 16; g++) {
+                const int c = g >> 3, mt = g & 7;
+                __builtin_amdgcn_sched_barrier(0);
+                if (MORE && g < 6 && (g & 1) == 0 && s >= 1) dma(s + 1, 6 + (g >> 1));
+                if (MORE && g == 14) {
+                    p8_barrier_vm0();
+                    if constexpr (decltype(tag)::scaled) scale_d(const_cast<uint8_t *>(nbuf), 1 - PAR);
+                    load_weights(nbuf, 1 - PAR);
+                }
+                h8 a2 = a1;
+                if (g + 2 < 16) a2 = read_a(buf, (g + 2) >> 3, (g + 2) & 7);
+                else if (MORE) a2 = read_a(nbuf, 0, g - 14);
+                if (MORE && g >= 14) {
+                    dma(s + 2, 3 * (g - 14));
+                    dma(s + 2, 3 * (g - 14) + 1);
+                    dma(s + 2, 3 * (g - 14) + 2);
+                }
+                const h8 acur = a0;
+                const h8 *bw = c ? b1 : bq;
+    #pragma unroll
+                for (int nt = 0; nt < 4; nt++)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bw[nt], acur, acc[mt][nt], 0, 0, 0);
+                if (c == 0 && (mt & 1)) b1[mt >> 1] = dequant(1, mt >> 1);
+                if (MORE && g >= 14) {
+                    bq[2 * (g - 14)] = dequant(0, 2 * (g - 14));
+                    bq[2 * (g - 14) + 1] = dequant(0, 2 * (g - 14) + 1);
+                }
+                a0 = a1;
+                a1 = a2;
+            }
             __builtin_amdgcn_sched_barrier(0);
-            if (MORE && g < 6 && (g & 1) == 0 && s >= 1) dma(s + 1, 6 + (g >> 1));
-            if (MORE && g == 14) {
-                p8_barrier_vm0();
-                load_weights(nbuf, 1 - PAR);
+        };
+        if constexpr (decltype(pass_c)::value) {
+            // E of this thread's scale row from its blocks' bounds
+            const int r = min(n0 + 64 * wr + lane, out_dim - 1);
+            const uint8_t *rp = w + (size_t)r * row_bytes + 256;  // the d run of super-tile 0
+            float m = 0.f;
+            for (int b = 0; b < nb; b++) {
+                const uint4 dr = *reinterpret_cast<const uint4 *>(rp + (size_t)b * 272);
+                const uint32_t dw[4] = {dr.x, dr.y, dr.z, dr.w};
+    #pragma unroll
+                for (int i = 0; i < 4; i++)
+                    m = fmaxf(m, 128.f * fmaxf(fabsf(f16_to_f32(dw[i] & 0xFFFFu)),
+                                               fabsf(f16_to_f32(dw[i] >> 16))));
             }
-            h8 a2 = a1;
-            if (g + 2 < 16) a2 = read_a(buf, (g + 2) >> 3, (g + 2) & 7);
-            else if (MORE) a2 = read_a(nbuf, 0, g - 14);
-            if (MORE && g >= 14) {
-                dma(s + 2, 3 * (g - 14));
-                dma(s + 2, 3 * (g - 14) + 1);
-                dma(s + 2, 3 * (g - 14) + 2);
-            }
-            const h8 acur = a0;
-            const h8 *bw = c ? b1 : bq;
-#pragma unroll
-            for (int nt = 0; nt < 4; nt++)
-                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bw[nt], acur, acc[mt][nt], 0, 0, 0);
-            if (c == 0 && (mt & 1)) b1[mt >> 1] = dequant(1, mt >> 1);
-            if (MORE && g >= 14) {
-                bq[2 * (g - 14)] = dequant(0, 2 * (g - 14));
-                bq[2 * (g - 14) + 1] = dequant(0, 2 * (g - 14) + 1);
-            }
-            a0 = a1;
-            a1 = a2;
+            erow = pf_row_exponent(m);
+            if (kg == 0) erow_lds[64 * wr + lane] = erow;
         }
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    for (int sb = 0; sb + 1 < nb; sb++) {
-        step(2 * sb, p8_step<0, true>{});
-        step(2 * sb + 1, p8_step<1, true>{});
-    }
-    step(ns - 2, p8_step<0, true>{});
-    step(ns - 1, p8_step<1, false>{});
+        // one pass over the tile: the first with E = 0, a second (scaled) with
+        // this thread's row exponent erow
+        auto run = [&](auto scaled_c) __attribute__((always_inline)) {
+            constexpr bool SC = decltype(scaled_c)::value;
+    #pragma unroll
+            for (int mt = 0; mt < 8; mt++)
+    #pragma unroll
+                for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
 
-    p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out);
+            // prologue: step 0 in, step 1 in flight, step 0's chunk-0 operands ready
+    #pragma unroll
+            for (int p = 0; p < 9; p++) dma(0, p);
+            p8_barrier_vm0();
+    #pragma unroll
+            for (int p = 0; p < 9; p++) dma(1, p);  // ns >= 2
+            if constexpr (SC) scale_d(stg, 0);
+            load_weights(stg, 0);
+    #pragma unroll
+            for (int nt = 0; nt < 4; nt++) bq[nt] = dequant(0, nt);
+            a0 = read_a(stg, 0, 0);
+            a1 = read_a(stg, 0, 1);
+
+            for (int sb = 0; sb + 1 < nb; sb++) {
+                step(2 * sb, p8_step<0, true, SC>{});
+                step(2 * sb + 1, p8_step<1, true, SC>{});
+            }
+            step(ns - 2, p8_step<0, true, SC>{});
+            step(ns - 1, p8_step<1, false, SC>{});
+        };
+        run(pass_c);
+        if constexpr (!decltype(pass_c)::value)
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, nullptr, flag);
+        else
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, erow_lds,
+                        nullptr);
+    };
+    body(std::false_type{});
+    if (pf_again(flag)) body(std::true_type{});
 }
 
 // ---- Q6_K weights -----------------------------------------------------------------
@@ -727,233 +887,276 @@ constexpr int kQ6Lds = kQ6ScOff + 2 * kPfRowsWg * 8;  // 132 KB
 static_assert(2 * 4 * 16 * 64 * 16 <= kQ6Lds, "the epilogue's exchange fits");
 
 __global__ __launch_bounds__(512) void k_prefill_q6_w8(const uint8_t *__restrict__ w,
-                                                       const _Float16 *__restrict__ xh,
+                                                       const _Float16 *__restrict__ xh_arg,
                                                        const float *__restrict__ unscale,
-                                                       float *__restrict__ out,
+                                                       float *__restrict__ out_arg,
                                                        float *__restrict__ part, int n_tok,
                                                        int in_dim, int out_dim, int ld_out) {
-    __shared__ __align__(16) uint8_t smem[kQ6Lds];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wr = wv & 3, kg = wv >> 2;
-    const int r16 = lane & 15, q = lane >> 4;
-    const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
-    const int nbt = in_dim >> 8;  // blocks in a row (a multiple of 8)
-    const int z = blockIdx.z, nz = gridDim.z;
-    const int kb0 = (int)((long)z * nbt / nz);
-    const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;
-    const int ns = 2 * nb;
-    xh += (size_t)kb0 * 256;
-    if (z > 0) out = part + (size_t)(z - 1) * n_tok * ld_out;
-    uint8_t *const act = smem + kQ6ActOff + 2 * kg * kP8Act;  // this group's two step buffers
-    uint8_t *const scl = smem + kQ6ScOff + kg * kPfRowsWg * 8;
-    const uint32_t row_bytes = (uint32_t)(nbt >> 3) * 1680u;
+    __shared__ __align__(16) uint8_t smem[kQ6Lds + kPfGuardBytes];
+    // range guard: the workgroup's flag, its rows' exponents (after the
+    // stages)
+    int *const flag = reinterpret_cast<int *>(smem + kQ6Lds);
+    int *const erow_lds = flag + 4;
+    if (threadIdx.x == 0) *flag = 0;  // before the prologue's barrier
+    // one pass of the workgroup: setup, the tile, the epilogue
+    auto body = [&](auto pass_c) __attribute__((always_inline)) {
+        int erow = 0;  // this thread's scale row's exponent (0 in the first pass)
+        // the second pass re-derives every per-lane value from an opaque copy
+        // of the thread index, so none of the first pass's stays live across
+        // its epilogue
+        int tid = threadIdx.x;
+        if constexpr (decltype(pass_c)::value) asm volatile("" : "+v"(tid));
+        const int lane = tid & 63;
+        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int wr = wv & 3, kg = wv >> 2;
+        const int r16 = lane & 15, q = lane >> 4;
+        const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
+        const int nbt = in_dim >> 8;  // blocks in a row (a multiple of 8)
+        const int z = blockIdx.z, nz = gridDim.z;
+        const int kb0 = (int)((long)z * nbt / nz);
+        const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;
+        const int ns = 2 * nb;
+        // this K split's activations, its output (split 0) or partial sums
+        // (the arguments stay unchanged for the second pass)
+        const _Float16 *const xh = xh_arg + (size_t)kb0 * 256;
+        float *const out = z > 0 ? part + (size_t)(z - 1) * n_tok * ld_out : out_arg;
+        uint8_t *const act = smem + kQ6ActOff + 2 * kg * kP8Act;  // this group's two step buffers
+        uint8_t *const scl = smem + kQ6ScOff + kg * kPfRowsWg * 8;
+        const uint32_t row_bytes = (uint32_t)(nbt >> 3) * 1680u;
 
-    // Copies, 16 bytes a lane, lane l to LDS row 8 R + l / 8 (a token of
-    // this group's activations, a weight row of the stage), 16-byte slot
-    // l % 8. Piece p of wavefront (wr or wv) covers R = 2 (4 (w >> 1) + p) +
-    // (w & 1), so a row's swizzle ((row & 15) >> 1 = 4 (w & 1) + l / 16), and
-    // with it what a lane copies, is the same for all four pieces: a column
-    // piece of the activations; for the weights field slot f = (l % 8) ^
-    // swizzle (0..3 ql, 4..5 qh, 6 the scales, 7 the d run) at byte
-    // base(f) + (b % 8) stride(f) + h half(f) of the super-tile of block b, h
-    // the half-block. Rows past the matrix repeat its last row: the row
-    // offset is min(l / 8, lim) rows from a clamped first row, lim passed
-    // through an empty asm at each copy so the compiler keeps no per-piece
-    // offsets in registers.
-    const int lr = lane >> 3;
-    const int aswz_dma = 4 * (wr & 1) + (lane >> 4), wswz_dma = 4 * (wv & 1) + (lane >> 4);
-    const int pc = (lane & 7) ^ aswz_dma;
-    const uint32_t xcol = 2u * (64 * kg + 32 * (pc >> 2) + 8 * (pc & 3));
-    const int f = (lane & 7) ^ wswz_dma;
-    const uint32_t wfld = f < 4 ? 16u * f : f < 6 ? 1024u + 16u * (f - 4) : f == 6 ? 1536u : 1664u;
-    const uint32_t wmul = (f < 4 ? 128u : f < 6 ? 64u : f == 6 ? 16u : 0u) |
-                          ((f < 4 ? 64u : f < 6 ? 32u : 0u) << 16);  // stride | half << 16
-    // this wavefront's first copy destinations, held in scalar registers
-    // (from an asm result) so no vector register keeps them
-    uint32_t lds_act, lds_w;
-    asm("s_mov_b32 %0, %1"
-        : "=s"(lds_act)
-        : "s"(__builtin_amdgcn_readfirstlane(p8_lds(act) + 8192 * (wr >> 1) + 1024 * (wr & 1))));
-    asm("s_mov_b32 %0, %1"
-        : "=s"(lds_w)
-        : "s"(__builtin_amdgcn_readfirstlane(p8_lds(smem) + 8192 * (wv >> 1) + 1024 * (wv & 1))));
-    // piece p (0..7) of group step s into the buffers of step parity par
-    // (s % 2, a constant at every call, so the half-block is one): 0..3 this
-    // group's activations, 4..7 the shared weight stage. A step past the end
-    // reloads the last block's half par, which no one reads.
-    auto dma = [=](int s, int p, auto par_c) {
-        constexpr int par = decltype(par_c)::value;
-        const int b = kb0 + (min(s, ns - 1) >> 1);  // block of the row
-        if (p < 4) {
-            const int R = 2 * (4 * (wr >> 1) + p) + (wr & 1);
-            const int t = min(t0 + 8 * R, n_tok - 1);
-            int lim = n_tok - 1 - t;
-            asm volatile("" : "+s"(lim));
-            const uint32_t o = (uint32_t)min(lr, lim) * (2u * (uint32_t)in_dim) + xcol;
-            p8_dma(xh + (size_t)t * in_dim + (b - kb0) * 256 + 128 * par, o,
-                   lds_act + (uint32_t)(par * kP8Act + 2048 * p));
-        } else {
-            const int R = 2 * (4 * (wv >> 1) + p - 4) + (wv & 1);
-            const int r = min(n0 + 8 * R, out_dim - 1);
-            int lim = out_dim - 1 - r;
-            asm volatile("" : "+s"(lim));
-            uint32_t o = (uint32_t)min(lr, lim) * row_bytes + (uint32_t)(b & 7) * (wmul & 0xFFFFu) + wfld;
-            if (par) o += wmul >> 16;
-            p8_dma(w + (size_t)r * row_bytes + (size_t)(b >> 3) * 1680, o,
-                   lds_w + (uint32_t)(par * kQ6W + 2048 * (p - 4)));
-        }
-    };
-    using par0 = std::integral_constant<int, 0>;
-    using par1 = std::integral_constant<int, 1>;
-    const int sw = r16 >> 1;
-    const int qlb0 = 16 * ((0 + (q >> 1)) ^ sw) + 8 * (q & 1);  // ql, chunk 0: field slot q / 2
-    const int aswz = (r16 >> 1) & 7;
-    // this thread's row's scales -> records for its group at half h:
-    // {f16(d sc[8h + 4kg]), f16(d sc[8h + 4kg + 2])} for lane groups q < 2,
-    // {f16(d sc[8h + 4kg + 1]), f16(d sc[8h + 4kg + 3])} for q >= 2
-    auto scales_of_step = [&](const uint8_t *wbuf, int b, int h) {
-        const int row = 64 * wr + lane;
-        const int rs = (row & 15) >> 1;
-        const uint32_t sc4 = *reinterpret_cast<const uint32_t *>(wbuf + 128 * row + 16 * (6 ^ rs) + 8 * h + 4 * kg);
-        const float d = f16_to_f32(*reinterpret_cast<const uint16_t *>(wbuf + 128 * row + 16 * (7 ^ rs) + 2 * (b & 7)));
-        auto f = [&](int i) { return (_Float16)(d * (float)(int8_t)(sc4 >> (8 * i))); };
-        const h2 lo = {f(0), f(2)}, hi = {f(1), f(3)};
-        *reinterpret_cast<uint2 *>(scl + 8 * row) =
-            make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
-    };
-    // a lane's raw operands of chunk c, token tile nt: 8 ql bytes, the 8 qh
-    // bytes, (f16 scale of chunk 0, of chunk 1)
-    struct q6w {
-        uint2 ql, qh;
-        uint32_t sc;
-    };
-    // one per-lane base (row 64 wr + r16 of stage 0, the chunk-0 ql field):
-    // the chunk-1 ql and the qh fields are at base ^ 32 and base ^ 64 (slots
-    // q / 2 + 2 and + 4 under the swizzle), token tile nt and the stage are
-    // immediate offsets. The empty asm at each use keeps the compiler from
-    // holding the derived addresses in registers across the loop.
-    const uint32_t wq_base = 128u * (uint32_t)(64 * wr + r16) + (uint32_t)qlb0;  // from smem
-    const uint32_t ws_base = (uint32_t)(scl - smem) + 8u * (uint32_t)(64 * wr + r16) + 4u * (uint32_t)(q >> 1);
-    auto read_w = [&](int par, int c, int nt) -> q6w {
-        uint32_t a = wq_base, sa = ws_base;
-        asm volatile("" : "+v"(a), "+v"(sa));
-        const uint32_t o = (uint32_t)par * kQ6W + 2048u * nt;
-        return {*reinterpret_cast<const uint2 *>(smem + ((c ? a ^ 32u : a) + o)),
-                *reinterpret_cast<const uint2 *>(smem + ((a ^ 64u) + o)),
-                *reinterpret_cast<const uint32_t *>(smem + (sa + 128u * nt))};
-    };
-    const int nsh = 4 * kg;  // ql nibble shift; qh bits 2j = nsh + 2c
-    auto dequant = [&](const q6w &v, int c) -> h8 {
-        const int sh = nsh + 2 * c;  // qh bits of this chunk
-        const h2 d2 = __builtin_bit_cast(h2, v.sc);
-        const h2 ds = c ? d2.yy : d2.xx;
-        const h2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};
-        h8 r;
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const uint32_t lw = ((u ? v.ql.y : v.ql.x) >> nsh) & 0x0F0F0F0Fu;
-            const uint32_t hw = ((u ? v.qh.y : v.qh.x) >> sh) & 0x03030303u;
-            const uint32_t code = lw | (hw << 4);
-            const h2 w01 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, code, 0x04010400u)) - bias) * ds;
-            const h2 w23 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, code, 0x04030402u)) - bias) * ds;
-            r[4 * u] = w01[0];
-            r[4 * u + 1] = w01[1];
-            r[4 * u + 2] = w23[0];
-            r[4 * u + 3] = w23[1];
-        }
-        return r;
-    };
-    auto read_a = [&](const uint8_t *buf, int c, int mt) -> h8 {
-        return *reinterpret_cast<const h8 *>(buf + (16 * mt + r16) * 128 + 16 * ((4 * c + q) ^ aswz));
-    };
+        // Copies, 16 bytes a lane, lane l to LDS row 8 R + l / 8 (a token of
+        // this group's activations, a weight row of the stage), 16-byte slot
+        // l % 8. Piece p of wavefront (wr or wv) covers R = 2 (4 (w >> 1) + p) +
+        // (w & 1), so a row's swizzle ((row & 15) >> 1 = 4 (w & 1) + l / 16), and
+        // with it what a lane copies, is the same for all four pieces: a column
+        // piece of the activations; for the weights field slot f = (l % 8) ^
+        // swizzle (0..3 ql, 4..5 qh, 6 the scales, 7 the d run) at byte
+        // base(f) + (b % 8) stride(f) + h half(f) of the super-tile of block b, h
+        // the half-block. Rows past the matrix repeat its last row: the row
+        // offset is min(l / 8, lim) rows from a clamped first row, lim passed
+        // through an empty asm at each copy so the compiler keeps no per-piece
+        // offsets in registers.
+        const int lr = lane >> 3;
+        const int aswz_dma = 4 * (wr & 1) + (lane >> 4), wswz_dma = 4 * (wv & 1) + (lane >> 4);
+        const int pc = (lane & 7) ^ aswz_dma;
+        const uint32_t xcol = 2u * (64 * kg + 32 * (pc >> 2) + 8 * (pc & 3));
+        const int f = (lane & 7) ^ wswz_dma;
+        const uint32_t wfld = f < 4 ? 16u * f : f < 6 ? 1024u + 16u * (f - 4) : f == 6 ? 1536u : 1664u;
+        const uint32_t wmul = (f < 4 ? 128u : f < 6 ? 64u : f == 6 ? 16u : 0u) |
+                              ((f < 4 ? 64u : f < 6 ? 32u : 0u) << 16);  // stride | half << 16
+        // this wavefront's first copy destinations, held in scalar registers
+        // (from an asm result) so no vector register keeps them
+        uint32_t lds_act, lds_w;
+        asm("s_mov_b32 %0, %1"
+            : "=s"(lds_act)
+            : "s"(__builtin_amdgcn_readfirstlane(p8_lds(act) + 8192 * (wr >> 1) + 1024 * (wr & 1))));
+        asm("s_mov_b32 %0, %1"
+            : "=s"(lds_w)
+            : "s"(__builtin_amdgcn_readfirstlane(p8_lds(smem) + 8192 * (wv >> 1) + 1024 * (wv & 1))));
+        // piece p (0..7) of group step s into the buffers of step parity par
+        // (s % 2, a constant at every call, so the half-block is one): 0..3 this
+        // group's activations, 4..7 the shared weight stage. A step past the end
+        // reloads the last block's half par, which no one reads.
+        auto dma = [=](int s, int p, auto par_c) {
+            constexpr int par = decltype(par_c)::value;
+            const int b = kb0 + (min(s, ns - 1) >> 1);  // block of the row
+            if (p < 4) {
+                const int R = 2 * (4 * (wr >> 1) + p) + (wr & 1);
+                const int t = min(t0 + 8 * R, n_tok - 1);
+                int lim = n_tok - 1 - t;
+                asm volatile("" : "+s"(lim));
+                const uint32_t o = (uint32_t)min(lr, lim) * (2u * (uint32_t)in_dim) + xcol;
+                p8_dma(xh + (size_t)t * in_dim + (b - kb0) * 256 + 128 * par, o,
+                       lds_act + (uint32_t)(par * kP8Act + 2048 * p));
+            } else {
+                const int R = 2 * (4 * (wv >> 1) + p - 4) + (wv & 1);
+                const int r = min(n0 + 8 * R, out_dim - 1);
+                int lim = out_dim - 1 - r;
+                asm volatile("" : "+s"(lim));
+                uint32_t o = (uint32_t)min(lr, lim) * row_bytes + (uint32_t)(b & 7) * (wmul & 0xFFFFu) + wfld;
+                if (par) o += wmul >> 16;
+                p8_dma(w + (size_t)r * row_bytes + (size_t)(b >> 3) * 1680, o,
+                       lds_w + (uint32_t)(par * kQ6W + 2048 * (p - 4)));
+            }
+        };
+        using par0 = std::integral_constant<int, 0>;
+        using par1 = std::integral_constant<int, 1>;
+        const int sw = r16 >> 1;
+        const int qlb0 = 16 * ((0 + (q >> 1)) ^ sw) + 8 * (q & 1);  // ql, chunk 0: field slot q / 2
+        const int aswz = (r16 >> 1) & 7;
+        // this thread's row's scales -> records for its group at half h:
+        // {f16(d sc[8h + 4kg]), f16(d sc[8h + 4kg + 2])} for lane groups q < 2,
+        // {f16(d sc[8h + 4kg + 1]), f16(d sc[8h + 4kg + 3])} for q >= 2
+        auto scales_of_step = [&](const uint8_t *wbuf, int b, int h, auto scaled_c) {
+            const int row = 64 * wr + lane;
+            const int rs = (row & 15) >> 1;
+            const uint32_t sc4 = *reinterpret_cast<const uint32_t *>(wbuf + 128 * row + 16 * (6 ^ rs) + 8 * h + 4 * kg);
+            float d = f16_to_f32(*reinterpret_cast<const uint16_t *>(wbuf + 128 * row + 16 * (7 ^ rs) + 2 * (b & 7)));
+            if constexpr (decltype(scaled_c)::value) d = ldexpf(d, -erow);
+            auto f = [&](int i) { return (_Float16)(d * (float)(int8_t)(sc4 >> (8 * i))); };
+            const h2 lo = {f(0), f(2)}, hi = {f(1), f(3)};
+            *reinterpret_cast<uint2 *>(scl + 8 * row) =
+                make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+        };
+        // a lane's raw operands of chunk c, token tile nt: 8 ql bytes, the 8 qh
+        // bytes, (f16 scale of chunk 0, of chunk 1)
+        struct q6w {
+            uint2 ql, qh;
+            uint32_t sc;
+        };
+        // one per-lane base (row 64 wr + r16 of stage 0, the chunk-0 ql field):
+        // the chunk-1 ql and the qh fields are at base ^ 32 and base ^ 64 (slots
+        // q / 2 + 2 and + 4 under the swizzle), token tile nt and the stage are
+        // immediate offsets. The empty asm at each use keeps the compiler from
+        // holding the derived addresses in registers across the loop.
+        const uint32_t wq_base = 128u * (uint32_t)(64 * wr + r16) + (uint32_t)qlb0;  // from smem
+        const uint32_t ws_base = (uint32_t)(scl - smem) + 8u * (uint32_t)(64 * wr + r16) + 4u * (uint32_t)(q >> 1);
+        auto read_w = [&](int par, int c, int nt) -> q6w {
+            uint32_t a = wq_base, sa = ws_base;
+            asm volatile("" : "+v"(a), "+v"(sa));
+            const uint32_t o = (uint32_t)par * kQ6W + 2048u * nt;
+            return {*reinterpret_cast<const uint2 *>(smem + ((c ? a ^ 32u : a) + o)),
+                    *reinterpret_cast<const uint2 *>(smem + ((a ^ 64u) + o)),
+                    *reinterpret_cast<const uint32_t *>(smem + (sa + 128u * nt))};
+        };
+        const int nsh = 4 * kg;  // ql nibble shift; qh bits 2j = nsh + 2c
+        auto dequant = [&](const q6w &v, int c) -> h8 {
+            const int sh = nsh + 2 * c;  // qh bits of this chunk
+            const h2 d2 = __builtin_bit_cast(h2, v.sc);
+            const h2 ds = c ? d2.yy : d2.xx;
+            const h2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};
+            h8 r;
+    #pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t lw = ((u ? v.ql.y : v.ql.x) >> nsh) & 0x0F0F0F0Fu;
+                const uint32_t hw = ((u ? v.qh.y : v.qh.x) >> sh) & 0x03030303u;
+                const uint32_t code = lw | (hw << 4);
+                const h2 w01 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, code, 0x04010400u)) - bias) * ds;
+                const h2 w23 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, code, 0x04030402u)) - bias) * ds;
+                r[4 * u] = w01[0];
+                r[4 * u + 1] = w01[1];
+                r[4 * u + 2] = w23[0];
+                r[4 * u + 3] = w23[1];
+            }
+            return r;
+        };
+        auto read_a = [&](const uint8_t *buf, int c, int mt) -> h8 {
+            return *reinterpret_cast<const h8 *>(buf + (16 * mt + r16) * 128 + 16 * ((4 * c + q) ^ aswz));
+        };
 
-    f4 acc[8][4];
-#pragma unroll
-    for (int mt = 0; mt < 8; mt++)
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+        f4 acc[8][4];
+        h8 bq[4], a0;
 
-    // prologue: step 0 in, step 1 in flight, step 0's chunk-0 operands ready
-#pragma unroll
-    for (int p = 0; p < 8; p++) dma(0, p, par0{});
-    p8_barrier_vm0();
-#pragma unroll
-    for (int p = 0; p < 8; p++) dma(1, p, par1{});  // ns >= 2
-    scales_of_step(smem, kb0, 0);
-    h8 bq[4];
-#pragma unroll
-    for (int nt = 0; nt < 4; nt++) bq[nt] = dequant(read_w(0, 0, nt), 0);
-    h8 a0 = read_a(act, 0, 0);
-
-    // One step: as in k_prefill_q8_w8, the weights in the shared stage of
-    // the step's parity: in group 14 every wavefront waits for its own
-    // copies of step s + 1, after the barrier decodes its row's scales of
-    // step s + 1 and reads that step's chunk-0 weights, and this step's
-    // buffers take step s + 2 (pieces 0..5 in groups 14, 15, 6..7 in groups
-    // 0, 2 of the next step). Chunk 1's raw weights of token tile i are read
-    // in group 2 i, dequantised in group 2 i + 1.
-    auto step = [&](int s, auto tag) {
-        constexpr int PAR = decltype(tag)::par;
-        constexpr bool MORE = decltype(tag)::more;
-        const uint8_t *buf = act + PAR * kP8Act;
-        const uint8_t *nbuf = act + (1 - PAR) * kP8Act;
-        const uint8_t *nwbuf = smem + (1 - PAR) * kQ6W;
-        h8 b1[4], a15;
-        q6w rw;
-#pragma unroll
-        for (int g = 0; g < 16; g++) {
-            const int c = g >> 3, mt = g & 7;
+        // One step: as in k_prefill_q8_w8, the weights in the shared stage of
+        // the step's parity: in group 14 every wavefront waits for its own
+        // copies of step s + 1, after the barrier decodes its row's scales of
+        // step s + 1 and reads that step's chunk-0 weights, and this step's
+        // buffers take step s + 2 (pieces 0..5 in groups 14, 15, 6..7 in groups
+        // 0, 2 of the next step). Chunk 1's raw weights of token tile i are read
+        // in group 2 i, dequantised in group 2 i + 1.
+        auto step = [&](int s, auto tag) __attribute__((always_inline)) {
+            constexpr int PAR = decltype(tag)::par;
+            constexpr bool MORE = decltype(tag)::more;
+            const uint8_t *buf = act + PAR * kP8Act;
+            const uint8_t *nbuf = act + (1 - PAR) * kP8Act;
+            const uint8_t *nwbuf = smem + (1 - PAR) * kQ6W;
+            h8 b1[4], a15;
+            q6w rw;
+    #pragma unroll
+            for (int g = 0; g < 16; g++) {
+                const int c = g >> 3, mt = g & 7;
+                __builtin_amdgcn_sched_barrier(0);
+                if (MORE && g < 4 && (g & 1) == 0 && s >= 1)
+                    dma(s + 1, 6 + (g >> 1), std::integral_constant<int, 1 - PAR>{});
+                if (c == 0 && (mt & 1) == 0) rw = read_w(PAR, 1, mt >> 1);
+                q6w rn0, rn1;
+                if (MORE && g == 14) p8_barrier_vm0();
+                if (MORE && g == 14)
+                    scales_of_step(nwbuf, kb0 + ((s + 1) >> 1), 1 - PAR,
+                                   std::integral_constant<bool, decltype(tag)::scaled>{});
+                if (MORE && g >= 14) {
+                    rn0 = read_w(1 - PAR, 0, 2 * (g - 14));
+                    rn1 = read_w(1 - PAR, 0, 2 * (g - 14) + 1);
+                }
+                // the activation operand one group ahead, except that group 13
+                // also reads group 15's, so every read of this step's buffer
+                // precedes the barrier of group 14 (after which it takes step
+                // s + 2), and group 15 reads the next step's first
+                h8 a1 = a0;
+                if (g < 13) a1 = read_a(buf, (g + 1) >> 3, (g + 1) & 7);
+                if (g == 13) {
+                    a1 = read_a(buf, 1, 6);
+                    a15 = read_a(buf, 1, 7);
+                }
+                if (g == 14) a1 = a15;
+                if (MORE && g == 15) a1 = read_a(nbuf, 0, 0);
+                if (MORE && g >= 14) {
+                    dma(s + 2, 3 * (g - 14), std::integral_constant<int, PAR>{});
+                    dma(s + 2, 3 * (g - 14) + 1, std::integral_constant<int, PAR>{});
+                    dma(s + 2, 3 * (g - 14) + 2, std::integral_constant<int, PAR>{});
+                }
+                const h8 acur = a0;
+                const h8 *bw = c ? b1 : bq;
+    #pragma unroll
+                for (int nt = 0; nt < 4; nt++)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bw[nt], acur, acc[mt][nt], 0, 0, 0);
+                if (c == 0 && (mt & 1)) b1[mt >> 1] = dequant(rw, 1);
+                if (MORE && g >= 14) {
+                    bq[2 * (g - 14)] = dequant(rn0, 0);
+                    bq[2 * (g - 14) + 1] = dequant(rn1, 0);
+                }
+                a0 = a1;
+            }
             __builtin_amdgcn_sched_barrier(0);
-            if (MORE && g < 4 && (g & 1) == 0 && s >= 1)
-                dma(s + 1, 6 + (g >> 1), std::integral_constant<int, 1 - PAR>{});
-            if (c == 0 && (mt & 1) == 0) rw = read_w(PAR, 1, mt >> 1);
-            q6w rn0, rn1;
-            if (MORE && g == 14) p8_barrier_vm0();
-            if (MORE && g == 14) scales_of_step(nwbuf, kb0 + ((s + 1) >> 1), 1 - PAR);
-            if (MORE && g >= 14) {
-                rn0 = read_w(1 - PAR, 0, 2 * (g - 14));
-                rn1 = read_w(1 - PAR, 0, 2 * (g - 14) + 1);
+        };
+        if constexpr (decltype(pass_c)::value) {
+            // E of this thread's scale row from its blocks' bounds
+            const int r = min(n0 + 64 * wr + lane, out_dim - 1);
+            const uint8_t *rp = w + (size_t)r * row_bytes + 1664;  // d runs
+            float m = 0.f;
+            for (int b = kb0; b < kb0 + nb; b++) {
+                const uint16_t h = *reinterpret_cast<const uint16_t *>(rp + (size_t)(b >> 3) * 1680 + 2 * (b & 7));
+                m = fmaxf(m, 4096.f * fabsf(f16_to_f32(h)));
             }
-            // the activation operand one group ahead, except that group 13
-            // also reads group 15's, so every read of this step's buffer
-            // precedes the barrier of group 14 (after which it takes step
-            // s + 2), and group 15 reads the next step's first
-            h8 a1 = a0;
-            if (g < 13) a1 = read_a(buf, (g + 1) >> 3, (g + 1) & 7);
-            if (g == 13) {
-                a1 = read_a(buf, 1, 6);
-                a15 = read_a(buf, 1, 7);
-            }
-            if (g == 14) a1 = a15;
-            if (MORE && g == 15) a1 = read_a(nbuf, 0, 0);
-            if (MORE && g >= 14) {
-                dma(s + 2, 3 * (g - 14), std::integral_constant<int, PAR>{});
-                dma(s + 2, 3 * (g - 14) + 1, std::integral_constant<int, PAR>{});
-                dma(s + 2, 3 * (g - 14) + 2, std::integral_constant<int, PAR>{});
-            }
-            const h8 acur = a0;
-            const h8 *bw = c ? b1 : bq;
-#pragma unroll
-            for (int nt = 0; nt < 4; nt++)
-                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bw[nt], acur, acc[mt][nt], 0, 0, 0);
-            if (c == 0 && (mt & 1)) b1[mt >> 1] = dequant(rw, 1);
-            if (MORE && g >= 14) {
-                bq[2 * (g - 14)] = dequant(rn0, 0);
-                bq[2 * (g - 14) + 1] = dequant(rn1, 0);
-            }
-            a0 = a1;
+            erow = pf_row_exponent(m);
+            if (kg == 0) erow_lds[64 * wr + lane] = erow;
         }
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    for (int sb = 0; sb + 1 < nb; sb++) {
-        step(2 * sb, p8_step<0, true>{});
-        step(2 * sb + 1, p8_step<1, true>{});
-    }
-    step(ns - 2, p8_step<0, true>{});
-    step(ns - 1, p8_step<1, false>{});
+        // one pass over the tile: the first with E = 0, a second (scaled) with
+        // this thread's row exponent erow
+        auto run = [&](auto scaled_c) __attribute__((always_inline)) {
+            constexpr bool SC = decltype(scaled_c)::value;
+    #pragma unroll
+            for (int mt = 0; mt < 8; mt++)
+    #pragma unroll
+                for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
 
-    p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out);
+            // prologue: step 0 in, step 1 in flight, step 0's chunk-0 operands ready
+    #pragma unroll
+            for (int p = 0; p < 8; p++) dma(0, p, par0{});
+            p8_barrier_vm0();
+    #pragma unroll
+            for (int p = 0; p < 8; p++) dma(1, p, par1{});  // ns >= 2
+            scales_of_step(smem, kb0, 0, scaled_c);
+    #pragma unroll
+            for (int nt = 0; nt < 4; nt++) bq[nt] = dequant(read_w(0, 0, nt), 0);
+            a0 = read_a(act, 0, 0);
+
+            for (int sb = 0; sb + 1 < nb; sb++) {
+                step(2 * sb, p8_step<0, true, SC>{});
+                step(2 * sb + 1, p8_step<1, true, SC>{});
+            }
+            step(ns - 2, p8_step<0, true, SC>{});
+            step(ns - 1, p8_step<1, false, SC>{});
+        };
+        run(pass_c);
+        if constexpr (!decltype(pass_c)::value)
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, nullptr, flag);
+        else
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, erow_lds,
+                        nullptr);
+    };
+    body(std::false_type{});
+    if (pf_again(flag)) body(std::true_type{});
 }
 
 // out[i] += part[z][i] for z = 0 .. nz - 1 in order (n floats per slice)

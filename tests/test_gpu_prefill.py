@@ -1,16 +1,19 @@
 """Prefill GEMM (Q4_K weights x bf16 activations, MFMA) against the oracle:
 the reference's matmul_quant_f32 (backend-cpu/src/ops/quant_matmul.rs:45-119)
-on f32(bf16 x). Bar: max|Δ|/max|y| <= 1e-3 (REL_TOL), checked over the whole
-output and also per token where a token has at least 1000 outputs (each
-token's activations are scaled separately on the device, so a token of small
-magnitude must not lose accuracy; with few outputs per token the per-token
-max|y| is dominated by chance cancellation, which the metric does not
-measure). Weights enter the matrix cores as f16 (d*sc, dmin*m rounded to f16,
-one f16 fma per weight), which puts the measured error at about 3e-4."""
+on f32(bf16 x). Two bars on every call:
+* every output of every checked token within the derived bound of
+  prefill_bound.py (the f16 weight and activation roundings and the fp32
+  sums, relative to sum_i |w_i x_i|), whatever the token's magnitude or
+  number of outputs;
+* max|d|/max|y| <= 1e-3 (REL_TOL) over the whole output, the north star's
+  metric.
+Weights enter the matrix cores as f16 (d*sc, dmin*m rounded to f16, one f16
+fma per weight), which puts the measured error at about 3e-4."""
 import numpy as np
 import pytest
 
 from conftest import REL_TOL, rel_err
+from prefill_bound import assert_within_bound
 from rsllm_amd import synth
 from rsllm_amd.ggml import GgmlType as G
 
@@ -29,8 +32,10 @@ def run_prefill(hip, w, xb, n_tok, in_dim, out_dim):
     return d_y.cpu().numpy()
 
 
-def check(oracle, got, w, xb, tokens, n_tok, in_dim, out_dim, per_token=True):
-    """Compare rows `tokens` of the GPU output with the oracle on those tokens."""
+def check(oracle, got, w, xb, tokens, n_tok, in_dim, out_dim):
+    """Compare rows `tokens` of the GPU output with the oracle on those
+    tokens: every output within the derived bound, and the whole within
+    REL_TOL."""
     xf = synth.bf16_bits_to_f32(xb.reshape(n_tok, in_dim)[tokens]).reshape(-1)
     rc, want = oracle.matmul_quant_f32(w, xf, len(tokens), in_dim, out_dim, int(G.Q4_K))
     assert rc == 0
@@ -38,11 +43,10 @@ def check(oracle, got, w, xb, tokens, n_tok, in_dim, out_dim, per_token=True):
     want = want.reshape(len(tokens), out_dim)
     assert not np.isnan(g).any()
     err = rel_err(g, want)
-    print(f"prefill {out_dim}x{in_dim} T={n_tok}: rel err {err:.3e}")
+    ratio = assert_within_bound(G.Q4_K, w, xf.reshape(len(tokens), in_dim), g, want, out_dim,
+                                in_dim, f"prefill {out_dim}x{in_dim} T={n_tok}")
+    print(f"prefill {out_dim}x{in_dim} T={n_tok}: rel err {err:.3e}, worst |d|/bound {ratio:.3f}")
     assert err <= REL_TOL, f"rel err {err:.3e}"
-    if per_token and out_dim >= 1000:
-        worst = max(rel_err(g[i], want[i]) for i in range(len(tokens)))
-        assert worst <= REL_TOL, f"worst per-token rel err {worst:.3e}"
     return err
 
 
@@ -69,8 +73,8 @@ def test_prefill_long_rows(oracle, hip, in_dim):
 
 def test_prefill_token_scales(oracle, hip):
     """Tokens spanning 60 binades (1e-18 .. 1e18), a zero token, and one
-    token with a single nonzero element: each token is exact to 1e-3 of its
-    own outputs."""
+    token with a single nonzero element: every output within the bound,
+    which scales with the token's own activations."""
     out_dim, in_dim, n_tok = 1024, 1024, 9
     w = synth.weight(G.Q4_K, out_dim, in_dim, seed=5)
     x = synth.activations(n_tok, in_dim, seed=6)
@@ -98,7 +102,7 @@ def test_prefill_special_blocks(oracle, hip):
     w = w.reshape(-1)
     xb = synth.bf16_activations(n_tok, in_dim, seed=10).reshape(-1)
     got = run_prefill(hip, w, xb, n_tok, in_dim, out_dim)
-    check(oracle, got, w, xb, np.arange(n_tok), n_tok, in_dim, out_dim, per_token=False)
+    check(oracle, got, w, xb, np.arange(n_tok), n_tok, in_dim, out_dim)
 
 
 def test_prefill_many_tiles_ragged(oracle, hip):
