@@ -87,6 +87,11 @@ typedef struct rsllm_hip_error_detail {
 
 void rsllm_hip_last_error(rsllm_hip_error_detail *out);
 
+/* No reference counterpart; a diagnostic: the number of device allocations
+ * (hipMalloc) the library has made in this process so far (workspace sets,
+ * staging, registered tensors, model arenas). It only grows. */
+uint64_t rsllm_hip_device_allocations(void);
+
 /* Backend handle analogue: CpuBackend::new (backend-cpu/src/lib.rs:50-53)
  * plus device choice. Optional; the first call of any entry point performs
  * it with device 0. */
@@ -175,7 +180,9 @@ int rsllm_hip_release_weights(void);
  * workspace the library keeps for `stream` on the current device, for a
  * caller about to destroy that stream. Work still enqueued there finishes
  * first (hipFree waits for the device); a later call on the stream makes a
- * new set. */
+ * new set. hipStreamPerThread names a different stream in each thread, so
+ * each thread that passes it gets a set of its own, and releasing it frees
+ * only the calling thread's set. */
 int rsllm_hip_stream_release(rsllm_hip_stream_t stream);
 
 /* ---- whole-model residency ---------------------------------------------------

@@ -140,6 +140,7 @@ SIGNATURES = {
     "rsllm_hip_matmul_quant_f32_dev_noalloc": ([_P, _S, _P, _S, _P, _S, _S, _S, _S, _U32, _P], _I),
     "rsllm_hip_register_weights": ([_P, _S, _U32, _S], _I),
     "rsllm_hip_release_weights": ([], _I),
+    "rsllm_hip_device_allocations": ([], ctypes.c_uint64),
     "rsllm_hip_stream_release": ([_P], _I),
     "rsllm_hip_model_upload": ([_P, ctypes.POINTER(TensorDesc), _S,
                                 ctypes.POINTER(ctypes.c_uint64)], _I),
@@ -307,6 +308,11 @@ def register_weights(weights: np.ndarray, dtype, in_dim: int) -> None:
 
 def release_weights() -> None:
     _check(LIB.rsllm_hip_release_weights())
+
+
+def device_allocations() -> int:
+    """Device allocations the library has made in this process so far."""
+    return int(LIB.rsllm_hip_device_allocations())
 
 
 def stream_release(stream: int = 0) -> None:

@@ -3,12 +3,14 @@
 // dispatch to the kernel launchers.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cstring>
 #include <map>
 #include <memory>
 #include <mutex>
 #include <string>
+#include <tuple>
 #include <unordered_map>
 #include <utility>
 #include <vector>
@@ -81,6 +83,9 @@ struct Lease {
     explicit operator bool() const { return dev != nullptr; }
 };
 
+// ---- device allocations ----------------------------------------------------
+std::atomic<uint64_t> g_dev_allocs{0};
+
 // ---- per-thread state -----------------------------------------------------
 struct DevBuf {
     void *p = nullptr;
@@ -91,7 +96,7 @@ struct DevBuf {
         p = nullptr;
         cap = 0;
         size_t want = n < 4096 ? 4096 : n;
-        hipError_t e = hipMalloc(&p, want);
+        hipError_t e = abi::dev_malloc(&p, want);
         if (e == hipSuccess) cap = want;
         return e;
     }
@@ -121,9 +126,18 @@ struct Scratch {
     }
 };
 std::mutex g_scratch_map_mu;
+// Key of a workspace set: (device, stream handle, thread tag). The special
+// handle hipStreamPerThread names a different stream in every thread, so
+// its sets also carry the calling thread's tag (0 for every other handle).
+using ScratchKey = std::tuple<int, hipStream_t, uint64_t>;
 // never destroyed: its buffers are freed only by rsllm_hip_stream_release,
 // not at process exit (when the HIP runtime may already be gone)
-auto *g_scratch_map = new std::map<std::pair<int, hipStream_t>, std::shared_ptr<Scratch>>();
+auto *g_scratch_map = new std::map<ScratchKey, std::shared_ptr<Scratch>>();
+std::atomic<uint64_t> g_thread_tags{0};
+ScratchKey scratch_key(int dev, hipStream_t st) {
+    thread_local const uint64_t tag = ++g_thread_tags;
+    return ScratchKey{dev, st, st == hipStreamPerThread ? tag : 0};
+}
 
 // The current device's set for stream `st`, locked for the caller.
 struct ScratchLease {
@@ -138,7 +152,7 @@ ScratchLease stream_scratch(hipStream_t st) {
     std::shared_ptr<Scratch> sc;
     {
         std::lock_guard<std::mutex> lk(g_scratch_map_mu);
-        auto &p = (*g_scratch_map)[{dev, st}];
+        auto &p = (*g_scratch_map)[scratch_key(dev, st)];
         if (!p) p = std::make_shared<Scratch>();
         sc = p;
     }
@@ -591,6 +605,11 @@ int shared_compute(float *out, const float *x, const uint8_t *gate, size_t gate_
 
 // ---- interface for the other host-side files (abi_internal.h) --------------
 namespace rsllm_hip::abi {
+hipError_t dev_malloc(void **p, size_t bytes) {
+    const hipError_t e = hipMalloc(p, bytes);
+    if (e == hipSuccess) g_dev_allocs.fetch_add(1, std::memory_order_relaxed);
+    return e;
+}
 int set_error(int status, const char *msg) { return set_err(status, msg); }
 int ok_status() { return ok(); }
 int device_error(hipError_t e, const char *where) { return dev_err(e, where); }
@@ -632,6 +651,8 @@ DevMem::~DevMem() {
 }  // namespace rsllm_hip::abi
 
 extern "C" {
+
+uint64_t rsllm_hip_device_allocations(void) { return g_dev_allocs.load(std::memory_order_relaxed); }
 
 void rsllm_hip_last_error(rsllm_hip_error_detail *out) {
     if (!out) return;
@@ -1165,13 +1186,13 @@ int rsllm_hip_register_weights(const uint8_t *weights, size_t weights_len, uint3
     if (rc) return rc;
     auto mem = std::make_shared<abi::DevMem>();
     HIP_TRY(hipGetDevice(&mem->device), "hipGetDevice");
-    HIP_TRY(hipMalloc(&mem->p, weights_len ? weights_len : 1), "hipMalloc");
+    HIP_TRY(abi::dev_malloc((void **)&mem->p, weights_len ? weights_len : 1), "hipMalloc");
     hipError_t e;
     if (!needs_prepare(dtype)) {
         e = hipMemcpy(mem->p, weights, weights_len, hipMemcpyHostToDevice);
     } else {
         uint8_t *raw = nullptr;
-        e = hipMalloc(&raw, weights_len ? weights_len : 1);
+        e = abi::dev_malloc((void **)&raw, weights_len ? weights_len : 1);
         if (e == hipSuccess) e = hipMemcpy(raw, weights, weights_len, hipMemcpyHostToDevice);
         if (e == hipSuccess)
             e = launch_prepare(dtype, raw, mem->p, weights_len / rb, in_dim, t_ctx.stream);
@@ -1203,7 +1224,7 @@ int rsllm_hip_stream_release(rsllm_hip_stream_t stream) {
     std::shared_ptr<Scratch> gone;
     {
         std::lock_guard<std::mutex> lk(g_scratch_map_mu);
-        auto it = g_scratch_map->find({dev, (hipStream_t)stream});
+        auto it = g_scratch_map->find(scratch_key(dev, (hipStream_t)stream));
         if (it != g_scratch_map->end()) {
             gone = std::move(it->second);
             g_scratch_map->erase(it);

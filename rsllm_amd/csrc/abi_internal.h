@@ -24,6 +24,10 @@ struct DevMem {
     ~DevMem();
 };
 
+// hipMalloc for every device allocation of the library, counted (see
+// rsllm_hip_device_allocations).
+hipError_t dev_malloc(void **p, size_t bytes);
+
 // Record the calling thread's error (rsllm_hip_last_error) and return status.
 int set_error(int status, const char *msg);
 // Record success and return RSLLM_HIP_OK.

@@ -387,7 +387,7 @@ int rsllm_hip_model_upload(const uint8_t *fingerprint, const rsllm_hip_tensor_de
     const auto t0 = std::chrono::steady_clock::now();
     m->mem = std::make_shared<abi::DevMem>();
     m->mem->device = dev;
-    if (off) HIP_TRY(hipMalloc((void **)&m->mem->p, off), "hipMalloc arena");
+    if (off) HIP_TRY(abi::dev_malloc((void **)&m->mem->p, off), "hipMalloc arena");
     m->arena = m->mem->p;
     rc = upload(*m, tensors, n_tensors);
     if (rc) return rc;  // m (and its arena) is dropped

@@ -12,7 +12,7 @@ HEADER = os.path.join(ROOT, "include", "rsllm_hip.h")
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)  # drop comments
-    names = re.findall(r"^\s*(?:int|size_t|void)\s+(rsllm_hip_\w+)\s*\(", text, flags=re.M)
+    names = re.findall(r"^\s*(?:int|size_t|void|uint64_t)\s+(rsllm_hip_\w+)\s*\(", text, flags=re.M)
     assert names, "no declarations parsed from the header"
     return sorted(set(names))
 

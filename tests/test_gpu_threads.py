@@ -12,7 +12,10 @@ its kernels on the rayon pool, parallel.rs:37-54):
   host-pointer matmuls on it: every result matches (registered copy or
   per-call upload, the same bytes through the same kernels);
 * rsllm_hip_stream_release frees a stream's workspace and a later call on
-  the stream still works.
+  the stream still works;
+* 2 threads enqueue the same workspace-using calls on hipStreamPerThread (one
+  handle value, a different stream in each thread): each thread gets a
+  workspace set of its own, and results are bit-identical to serial calls.
 ctypes releases the GIL around each library call, so the calls overlap."""
 import threading
 
@@ -206,3 +209,53 @@ def test_stream_release_then_reuse(hip):
         outs.append(y.cpu().numpy())
         hip.stream_release(s.cuda_stream)
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+HIP_STREAM_PER_THREAD = 2  # the value of hipStreamPerThread in hip_runtime_api.h
+
+
+def test_dev_calls_on_stream_per_thread_from_two_threads(hip):
+    """Batched GEMVs whose K is split across workgroups (activation image
+    and partial sums in the workspace: Q8_0 1024 x 4096 at 32 tokens, Q6_K
+    4096 x 8192 at 8), from two threads on hipStreamPerThread. Sharing one
+    workspace set between the two real streams would race on the activation
+    images and the partial sums."""
+    import torch
+    hip.init(0)
+    cases = [(G.Q8_0, 1024, 4096, 32), (G.Q6_K, 4096, 8192, 8)]
+    ws = []
+    for j, (dt, o, n, t) in enumerate(cases):
+        raw = torch.from_numpy(synth.weight(dt, o, n, 1700 + j)).cuda()
+        d = torch.empty_like(raw)
+        hip.prepare_weights_dev(d.data_ptr(), raw.data_ptr(), raw.numel(), dt, n, 0)
+        ws.append(d)
+    xs = [[torch.from_numpy(synth.activations(t, n, 1710 + 2 * j + i).reshape(-1)).cuda()
+           for i in range(2)] for j, (_, _, n, t) in enumerate(cases)]
+    torch.cuda.synchronize()
+
+    def calls(i, stream):
+        ys = []
+        for j, (dt, o, n, t) in enumerate(cases):
+            y = torch.empty(t * o, dtype=torch.float32, device="cuda")
+            hip.matmul_quant_f32_dev(y.data_ptr(), y.numel(), ws[j].data_ptr(), ws[j].numel(),
+                                     xs[j][i].data_ptr(), xs[j][i].numel(), t, n, o, dt, stream)
+            ys.append(y)
+        return ys
+
+    ref = []
+    for i in range(2):
+        ys = calls(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        ref.append([y.cpu().numpy() for y in ys])
+
+    def worker(i):
+        def run():
+            for _ in range(ITERS):
+                ys = calls(i, HIP_STREAM_PER_THREAD)
+                torch.cuda.synchronize()
+                for y, r in zip(ys, ref[i]):
+                    assert np.array_equal(y.cpu().numpy().view(np.uint32), r.view(np.uint32))
+            hip.stream_release(HIP_STREAM_PER_THREAD)
+        return run
+
+    _run_threads([worker(0), worker(1)])

@@ -1,8 +1,11 @@
 """rsllm_hip_matmul_quant_f32_dev_noalloc: the same results as
 rsllm_hip_matmul_quant_f32_dev (it runs the same kernels, with the static
 per-GPU workspace in place of the library-allocated one), on calls that use
-that workspace, twice in a row with the second call smaller; and the
-rejection of a call whose workspace would exceed the static maximum."""
+that workspace, twice in a row with the second call smaller; that those
+calls make no device allocation (the library's allocation counter does not
+move, on a stream no call has used before; the allocating entry point on
+another new stream does move it); and the rejection of a call whose
+workspace would exceed the static maximum."""
 import numpy as np
 import pytest
 
@@ -54,6 +57,41 @@ def test_noalloc_matches_dev_entry(hip, oracle, calls):
         rc, want = oracle.matmul_quant_f32(w, x, n_tok, in_dim, out_dim, int(dtype))
         assert rc == 0
         assert rel_err(got, want) <= REL_TOL
+
+
+@pytest.mark.gpu
+def test_noalloc_allocates_nothing(hip):
+    """Every path of CALLS on a fresh stream: rsllm_hip_device_allocations
+    is unchanged across the no-allocation calls (inputs and outputs are made
+    before the first count), and grows when the allocating _dev entry point
+    runs the same call on another fresh stream (a workspace set of its own)."""
+    import torch
+    hip.init(0)
+    s0 = torch.cuda.current_stream().cuda_stream
+    bufs = []
+    for i, (dtype, out_dim, in_dim, n_tok) in enumerate(c for calls in CALLS for c in calls):
+        raw = torch.from_numpy(synth.weight(dtype, out_dim, in_dim, seed=950 + i)).cuda()
+        prep = torch.empty_like(raw)
+        hip.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), dtype, in_dim, s0)
+        x = torch.from_numpy(synth.activations(n_tok, in_dim, seed=960 + i).reshape(-1)).cuda()
+        y = torch.empty(n_tok * out_dim, dtype=torch.float32, device="cuda")
+        bufs.append((dtype, out_dim, in_dim, n_tok, prep, x, y))
+    torch.cuda.synchronize()
+    fresh = torch.cuda.Stream()
+    before = hip.device_allocations()
+    for dtype, out_dim, in_dim, n_tok, prep, x, y in bufs:
+        hip.matmul_quant_f32_dev_noalloc(y.data_ptr(), y.numel(), prep.data_ptr(), prep.numel(),
+                                         x.data_ptr(), x.numel(), n_tok, in_dim, out_dim, dtype,
+                                         fresh.cuda_stream)
+    fresh.synchronize()
+    assert hip.device_allocations() == before
+    other = torch.cuda.Stream()
+    dtype, out_dim, in_dim, n_tok, prep, x, y = bufs[0]
+    hip.matmul_quant_f32_dev(y.data_ptr(), y.numel(), prep.data_ptr(), prep.numel(), x.data_ptr(),
+                             x.numel(), n_tok, in_dim, out_dim, dtype, other.cuda_stream)
+    other.synchronize()
+    assert hip.device_allocations() > before
+    hip.stream_release(other.cuda_stream)
 
 
 def test_noalloc_rejects_workspace_above_the_maximum(hip):
