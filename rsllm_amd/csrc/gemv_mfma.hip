@@ -13,11 +13,14 @@
 // MFMA result in fp32: the weights reach the products exactly.
 //
 // Activations: a pre-pass scales each token by 2^e (max |x| into
-// [2^14, 2^15)) and stores it as f16 in MFMA operand order,
-//   xh[((s * 4 + j) * 4 + q) * ntp + t][0..7] = f16(2^e_t x[t, F::elem(s, j, q) + 0..7]),
+// [2^14, 2^15)) and splits it into two f16 planes in MFMA operand order,
+//   hi[((s * 4 + j) * 4 + q) * ntp + t][0..7] = f16(v), lo[...] = f16(v - hi),
+//   v = 2^e_t x[t, F::elem(s, j, q) + 0..7],
 // s = K step of 128 elements, j = MFMA of the step, q = lane group, ntp =
-// padded token count (16 or 32, padding tokens zero); unscale[t] = 2^-e_t.
-// That f16 rounding (at most 2^-11 relative per element) is the only one.
+// padded token count (8, 16 or 32, padding tokens zero); unscale[t] =
+// 2^-e_t. v - hi is exact in fp32, so hi + lo holds x to about 2^-22
+// relative; every weight operand meets both planes (one packed operand up
+// to 8 tokens, two MFMAs above).
 //
 // Kernel: workgroup = NK wavefronts over the same 16*RT weight rows; wavefront
 // w takes K steps [w * nsteps / NK, (w + 1) * nsteps / NK) with the next

@@ -8,9 +8,9 @@
 // re-reading each selected expert's weights once per token. Here the
 // (token, slot) pairs are grouped by expert on the device, and each expert's
 // gate/up and down matrices are streamed once per batch of up to 4 of its
-// tokens (grouped GEMV, gemv.hip; for Q4_K experts from kMoeMfmaMinTok
-// tokens, batches of up to 8 or 16 on the matrix cores instead, launch_moe_mfma
-// in gemv_mfma.hip, steps 2-6 there):
+// tokens (grouped GEMV, gemv.hip; for Q4_K, Q6_K and Q8_0 experts from
+// kMoeMfmaMinTok tokens, batches of up to 8 or 16 on the matrix cores
+// instead, launch_moe_mfma in gemv_mfma.hip, steps 2-6 there):
 //   1. routing (k_moe_hist, k_moe_scan, k_moe_scatter, any number of
 //      pairs): slots sorted by expert (ties in (t, i) order), per-expert
 //      offsets, slot -> token, (t, i) -> slot, the list of active experts;

@@ -13,7 +13,7 @@
 // so the loads cannot be removed and nothing is stored in practice.
 #include <hip/hip_runtime.h>
 
-#include "../../include/rsllm_hip.h"
+#include "../../include/rsllm_hip_probe.h"
 #include "abi_internal.h"
 #include "kernels.h"
 

@@ -1,16 +1,18 @@
 """The C-ABI library loads (no GPU needed) and exports every entry point that
-include/rsllm_hip.h declares; the Python mirror declares a signature for
-each of them. No compute calls are made."""
+include/rsllm_hip.h (the drop-in boundary) and include/rsllm_hip_probe.h
+(the benchmark's measurement aids) declare; the Python mirror declares a
+signature for each of them. No compute calls are made."""
 import ctypes
 import os
 import re
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "rsllm_hip.h")
+PROBE_HEADER = os.path.join(ROOT, "include", "rsllm_hip_probe.h")
 
 
-def declared_functions():
-    text = open(HEADER).read()
+def declared_functions(headers=(HEADER, PROBE_HEADER)):
+    text = "".join(open(h).read() for h in headers)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)  # drop comments
     names = re.findall(r"^\s*(?:int|size_t|void|uint64_t)\s+(rsllm_hip_\w+)\s*\(", text, flags=re.M)
     assert names, "no declarations parsed from the header"
@@ -18,7 +20,8 @@ def declared_functions():
 
 
 def test_header_declares_the_boundary():
-    names = declared_functions()
+    names = declared_functions((HEADER,))
+    assert not any(n.endswith(("_stream_read_dev", "_mfma_issue_dev")) for n in names)
     for required in ("rsllm_hip_matmul_quant_f32", "rsllm_hip_matmul_quant_f32_dev",
                      "rsllm_hip_dequant_to_f32", "rsllm_hip_release_weights",
                      "rsllm_hip_matmul_q4k_bf16_dev"):

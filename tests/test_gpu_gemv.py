@@ -129,7 +129,8 @@ def test_gemv_mfma_fused_lds(oracle, hip, dtype, out_dim, in_dim, n_tok):
     (G.Q6_K, 14336, 4096, 32), (G.Q4_K, 4096, 4096, 16),
     (G.Q8_0, 4096, 4096, 1), (G.Q8_0, 4096, 4096, 2), (G.Q8_0, 4096, 4096, 4),
     (G.Q8_0, 4096, 4096, 8), (G.Q8_0, 4096, 4096, 16), (G.Q8_0, 4096, 4096, 32),
-    (G.Q8_0, 1024, 4096, 1), (G.Q8_0, 1024, 4096, 32),
+    (G.Q8_0, 1024, 4096, 1), (G.Q8_0, 1024, 4096, 2), (G.Q8_0, 1024, 4096, 4),
+    (G.Q8_0, 1024, 4096, 8), (G.Q8_0, 1024, 4096, 16), (G.Q8_0, 1024, 4096, 32),
     (G.Q2_K, 7168, 2048, 1), (G.Q2_K, 7168, 2048, 8),
     (G.IQ2_XXS, 2048, 7168, 1), (G.IQ2_XXS, 2048, 7168, 8),
 ])

@@ -375,11 +375,14 @@ def c3_experts():
             synth.weight(G.Q4_K, n_expert * n_embd, n_ff, 4402))
 
 
-@pytest.mark.parametrize("n_tok", [8, 32])
+@pytest.mark.parametrize("n_tok", [1, 2, 4, 8, 16, 32])
 def test_moe_c3_64_experts(oracle, hip, c3_experts, n_tok):
     """C3 as configured: 64 experts, Q4_K gate/up (2048, 7168) and down
-    (7168, 2048), top-8 with softmax weights, T = 8 and 32, checked on up to
-    6 tokens against the oracle (accumulate_moe_outputs, moe.rs:648-707)."""
+    (7168, 2048), top-8 with softmax weights, T = 1, 2, 4, 8, 16 and 32 (the
+    sweep of BASELINE.json configs[3]), checked on up to 6 tokens against
+    the oracle (accumulate_moe_outputs, moe.rs:648-707): the matrix-core
+    route from 8 tokens within MFMA_TOL, the fused int8-limb kernels below
+    it within REL_TOL."""
     n_expert, n_embd, n_ff, k = 64, 7168, 2048, 8
     gate, up, down = c3_experts
     x = synth.activations(n_tok, n_embd, 4410 + n_tok)
@@ -391,4 +394,4 @@ def test_moe_c3_64_experts(oracle, hip, c3_experts, n_tok):
     err = _subset_check(oracle, got, x, gate, up, down, ids, w, toks, n_embd, n_ff, n_expert, k,
                         G.Q4_K, G.Q4_K)
     print(f"moe C3 64 experts T={n_tok}: rel err {err:.3e}")
-    assert err <= MFMA_TOL
+    assert err <= (MFMA_TOL if n_tok >= 8 else REL_TOL)
