@@ -174,11 +174,11 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv(const uint8_t *__restri
 // skip it). Its x loads are issued first and the first PD - 1 tiles right
 // after, so the weight stream runs while x is quantised.
 //
-// Loads are branch-free: a tile past the wavefront's last one is read through
-// a zero-length buffer resource (the hardware returns zeros without memory
-// traffic), and compiler scheduling barriers keep each step's loads ahead of
-// its arithmetic, so the waits before each tile's arithmetic leave the later
-// tiles in flight.
+// Steps past a wavefront's last tile (its last round of PD) skip their
+// arithmetic: on MI355X a step costs about 0.2 us of issue, which showed at
+// the end of the kernel. Compiler scheduling barriers keep each
+// step's loads ahead of its arithmetic, so the waits before each tile's
+// arithmetic leave the later tiles in flight.
 //
 // Groups. The rows form groups of rows_per_group consecutive rows (one
 // group: rows_per_group = out_dim); row r of group g = r / rows_per_group
@@ -246,16 +246,27 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
     // fixed, the tile's base a scalar offset
     uint32_t loff[F::kNO];
     if constexpr (UNI) F::lane_offs(loff, ks, k);
-    auto load_tile = [&](typename F::Slice &sl, int t) {
-        const int j = t / ncols, col = t - j * ncols;
-        const __amdgpu_buffer_rsrc_t r = t < T ? rw : rnull;  // rows past T: no traffic
-        const int row = min(row_of(j), out_dim - 1) - mbase;
+    // Tiles are loaded in order through a cursor (row lj of this wavefront's
+    // list, column lc), advanced after each load.
+    // Loads are never branched over (the compiler would then wait for every
+    // load in flight where the paths join): a tile past the wavefront's last
+    // one is read through a zero-length buffer resource, which returns zeros
+    // without memory traffic.
+    int lj = 0, lc = 0;
+    auto load_next = [&](typename F::Slice &sl, bool real) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t r = real ? rw : rnull;
+        const int row = min(row_of(lj), out_dim - 1) - mbase;
         if constexpr (UNI) {
-            F::load_u(sl, r, loff, F::tile_base((uint32_t)row, (uint32_t)col, in_dim));
+            F::load_u(sl, r, loff, F::tile_base((uint32_t)row, (uint32_t)lc, in_dim));
         } else {
-            const int unit = min(col * 8 + ks, nunits - 1);
+            const int unit = min(lc * 8 + ks, nunits - 1);
             F::load(sl, r, row, unit, k, in_dim, mrows);
         }
+        // arithmetic updates (a conditional store to one of two captured
+        // variables is lowered through memory)
+        const bool wrap = lc + 1 == ncols;
+        lj += wrap ? 1 : 0;
+        lc = wrap ? 0 : lc + 1;
     };
 
     // Prologue: x loads, the first tiles, then quantisation into LDS (token
@@ -272,7 +283,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < PD - 1; j++) load_tile(buf[j], j);
+    for (int j = 0; j < PD - 1; j++) load_next(buf[j], j < T);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < GPT; i++) {
@@ -303,42 +314,46 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
     float acc[BT];
 #pragma unroll
     for (int tk = 0; tk < BT; tk++) acc[tk] = 0.f;
+    // One tile's arithmetic; the row's total is stored after its last column.
     int col = 0, j = 0;
+    auto step = [&](const typename F::Slice &sl) __attribute__((always_inline)) {
+        const int unit = col * 8 + ks;
+        const bool ok = unit < nunits && F::valid(unit, k, in_dim);
+#pragma unroll
+        for (int tk = 0; tk < BT; tk++) {
+            XSlice xs;
+            const uint4 *bx = xl + tk * tok_fields + col * F::kXF * 64 + lane;
+            xs.hlo = bx[0];
+            xs.llo = bx[64];
+            xs.meta = bx[128];
+            if (F::kXF == 5) {
+                xs.hhi = bx[192];
+                xs.lhi = bx[256];
+            }
+            const float d = F::dot(sl, k, xs);
+            acc[tk] += ok ? d : 0.f;
+        }
+        const bool last = col == ncols - 1;
+        if (last) {
+#pragma unroll
+            for (int tk = 0; tk < BT; tk++) {
+                const float tot = wave_sum_dpp(acc[tk]);
+                if (lane == 0 && tk < n_tok) y[(size_t)tk * sh.y_stride + row_of(j)] = tot;
+                acc[tk] = 0.f;
+            }
+        }
+        j += last ? 1 : 0;
+        col = last ? 0 : col + 1;
+    };
+    // Rounds of PD steps: step t uses slot t % PD and loads tile t + PD - 1
+    // into the slot step t - 1 used; steps past T (the last round's) load
+    // through the null resource and skip their arithmetic.
     for (int t0 = 0; t0 < T; t0 += PD) {
 #pragma unroll
         for (int jj = 0; jj < PD; jj++) {
-            const int t = t0 + jj;
-            load_tile(buf[(jj + PD - 1) % PD], t + PD - 1);
+            load_next(buf[(jj + PD - 1) % PD], t0 + jj + PD - 1 < T);
             __builtin_amdgcn_sched_barrier(0);
-            const int unit = col * 8 + ks;
-            const bool ok = t < T && unit < nunits && F::valid(unit, k, in_dim);
-#pragma unroll
-            for (int tk = 0; tk < BT; tk++) {
-                XSlice xs;
-                const uint4 *bx = xl + tk * tok_fields + col * F::kXF * 64 + lane;
-                xs.hlo = bx[0];
-                xs.llo = bx[64];
-                xs.meta = bx[128];
-                if (F::kXF == 5) {
-                    xs.hhi = bx[192];
-                    xs.lhi = bx[256];
-                }
-                const float d = F::dot(buf[jj], k, xs);
-                acc[tk] += ok ? d : 0.f;
-            }
-            if (col == ncols - 1) {
-#pragma unroll
-                for (int tk = 0; tk < BT; tk++) {
-                    const float tot = wave_sum_dpp(acc[tk]);
-                    if (lane == 0 && t < T && tk < n_tok)
-                        y[(size_t)tk * sh.y_stride + row_of(j)] = tot;
-                    acc[tk] = 0.f;
-                }
-                col = 0;
-                j++;
-            } else {
-                col++;
-            }
+            if (t0 + jj < T) step(buf[jj]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
