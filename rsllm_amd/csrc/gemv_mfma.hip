@@ -356,6 +356,27 @@ __device__ __forceinline__ void hilo8(const float4 &v0, const float4 &v1, float 
 
 // Scale exponent of a row whose largest magnitude is amax: amax * 2^e in
 // [2^14, 2^15) (e clamped to [-126, 126]; 0 for a zero or non-finite amax).
+// hilo8 with both roundings toward zero, two values per conversion
+// instruction: hi keeps a prefix of v's bits, so v - hi is exact in fp32,
+// and hi + lo is within 2^-21 |v| (the one-pass kernel converts its slice of
+// the activations in every workgroup, where the conversion's VALU time
+// shows).
+typedef __fp16 h2rtz __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void hilo8_rtz(const float4 &v0, const float4 &v1, float up, uint4 &hi,
+                                          uint4 &lo) {
+    const float v[8] = {v0.x * up, v0.y * up, v0.z * up, v0.w * up,
+                        v1.x * up, v1.y * up, v1.z * up, v1.w * up};
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const h2rtz p = __builtin_amdgcn_cvt_pkrtz(v[2 * k], v[2 * k + 1]);
+        h[k] = __builtin_bit_cast(uint32_t, p);
+        l[k] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(v[2 * k] - (float)p[0],
+                                                                       v[2 * k + 1] - (float)p[1]));
+    }
+    hi = make_uint4(h[0], h[1], h[2], h[3]);
+    lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
 __device__ __forceinline__ int mf_exponent(float amax) {
     int e = 0;
     if (amax > 0.f && amax <= 3.4e38f) {
@@ -840,13 +861,208 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfs(const uint8_t *__restrict_
 // reading the others' write-through partials after a system-scope counter,
 // was slower: 12.2 -> 14.6 us at C2 1024 x 4096, 32 tokens: its three
 // memory round trips cost more than this launch.)
+// The partials are loaded 8 at a time before any is added (a loop of
+// dependent load-add pairs waits a full memory round trip per split).
 __global__ __launch_bounds__(256) void k_mfs_sum(const float *__restrict__ part,
                                                  float *__restrict__ y, int n, int sk) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    float v = part[i];
-    for (int k = 1; k < sk; k++) v += part[(size_t)k * n + i];
+    float v = 0.f;
+    for (int k0 = 0; k0 < sk; k0 += 8) {
+        float p[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) p[k] = k0 + k < sk ? part[(size_t)(k0 + k) * n + i] : 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (k0 + k < sk) v = k0 + k == 0 ? p[k] : v + p[k];
+    }
     y[i] = v;
+}
+
+// ---- small matrices in one pass ----------------------------------------------------
+// Matrices whose weights, spread over about one workgroup per CU, fit in
+// LDS whole (C2-style 1024- and 4096-row Q8_0 / Q4_K matrices at 9..32
+// tokens). Grid (sk K slices, row blocks of R = 16 RTW NW rows), slice z
+// covering elements [z KS, (z + 1) KS). Each workgroup
+//   1. reads its activations' slice (ntp tokens x KS values, fp32) and
+//      issues the copy of its rows' weight slice (one contiguous byte run
+//      per row: KS / 256 Q8_0 super-tiles or Q4_K blocks) into LDS with
+//      16-byte buffer-to-LDS pieces, all in flight at once, in two phases
+//      of half the slice where KS = 512;
+//   2. scales each token's slice by 2^e (its max |x| into [2^14, 2^15),
+//      over this slice only) and stores the hi and lo f16 planes to LDS in
+//      the MFMA operand order of the activation image (k_mf_x);
+//   3. after a barrier, wavefront w runs row tiles RTW w .. RTW w + RTW - 1
+//      over the first phase's steps against every token tile (the
+//      activation operands read from LDS once per step for all of them),
+//      then, after a second barrier, over the second phase's, and
+//   4. stores its tile scaled by 2^-e: to y when there is one slice, else to
+//      the slice's partial, which k_mfs_sum adds in slice order.
+// No activation pre-pass launch and no activation image in memory, and
+// each workgroup reads only its slice of x (ntp * KS * 4 bytes, about its
+// weight bytes at R = 128, KS = 512). The weights reach the products
+// exactly, as in the other matrix-core kernels; the activations as hi + lo.
+// LDS slot of piece row p (the ((s * 4 + j) * 4 + q) of the image layout),
+// token column t: the column XOR-ed with p's low bits, so the prologue's
+// stores (a wavefront's lanes: one token, consecutive p) and the operand
+// reads (consecutive columns, four p) both spread over the LDS banks.
+template <int NTP>
+__device__ __forceinline__ int mfo_slot(int p, int t) {
+    return p * NTP + (t ^ (p & (NTP - 1)));
+}
+
+// Max over each half of a wavefront (lanes 0..31 and 32..63), returned to
+// every lane of that half: DPP within rows of 16, then the row maxima.
+__device__ __forceinline__ float half_wave_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 47));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    return (threadIdx.x & 32) ? fmaxf(c, d) : fmaxf(a, b);
+}
+
+template <class F> struct MfoRow;  // bytes per 256 elements of a row
+template <> struct MfoRow<MQ8> { static constexpr int kB256 = 272; };
+template <> struct MfoRow<MQ4K> { static constexpr int kB256 = 144; };
+
+template <class F, int NT, int NW, int KS, int RTW>
+struct MfoGeo {
+    static constexpr int NTP = 16 * NT;                     // token columns
+    static constexpr int TH = 64 * NW;
+    static constexpr int R = 16 * RTW * NW;                 // rows per workgroup
+    static constexpr int NPH = KS >= 512 ? 2 : 1;           // weight phases (256+ elements each)
+    static constexpr int KP = KS / NPH;                     // elements per phase
+    static constexpr int PR = KP / 256 * MfoRow<F>::kB256 / 16 + 1;  // pieces per row, + 1 pad
+    static constexpr int WP = (R * PR + TH - 1) / TH;       // weight pieces per thread per phase
+    static constexpr int NS = KS / kMfStep;                 // steps
+    static constexpr int NSP = NS / NPH;                    // steps per phase
+    static constexpr int PT = KS / 8;                       // 8-element pieces per token
+    static constexpr int XP = NTP * PT / TH;                // activation pieces per thread
+    static constexpr int W_BUF = WP * TH * 16;              // one phase's weights
+    static constexpr int W_LDS = NPH * W_BUF;
+    static constexpr int LDS = W_LDS + 2 * NTP * KS * 2;    // weights + two f16 planes
+};
+
+template <class F, int NT, int NW, int KS, int RTW>
+__global__ __launch_bounds__(64 * NW) void k_gemv_mfo(const uint8_t *__restrict__ w,
+                                                      const float *__restrict__ x,
+                                                      float *__restrict__ dst, int n_tok,
+                                                      int in_dim, int out_dim) {
+    using G = MfoGeo<F, NT, NW, KS, RTW>;
+    static_assert(G::PT == 32 || G::PT == 64, "a token's slice spans half or all of a wavefront");
+    static_assert(G::XP * G::TH == G::NTP * G::PT, "activation pieces divide evenly");
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float us[G::NTP];
+    uint8_t *wbuf = smem;
+    uint4 *xh = reinterpret_cast<uint4 *>(smem + G::W_LDS);  // hi plane, then lo
+    uint4 *xlo = xh + G::NS * 16 * G::NTP;
+    const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int z = blockIdx.x, k0 = z * KS, row0 = blockIdx.y * G::R;
+    // 1. activation loads, then the weight copy
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)n_tok * (uint32_t)in_dim * 4u);
+    uint4 xv[G::XP][2];
+#pragma unroll
+    for (int r = 0; r < G::XP; r++) {
+        const int g = r * G::TH + tid, t = g / G::PT, i = g - t * G::PT;
+        const uint32_t off =
+            t < n_tok ? ((uint32_t)t * (uint32_t)in_dim + (uint32_t)(k0 + 8 * i)) * 4u : 0x80000000u;
+        xv[r][0] = bload16(rx, off, 0);
+        xv[r][1] = bload16(rx, off + 16u, 0);
+    }
+    // the weight copy waits for the activations: issued together, the
+    // activation misses queue behind the whole slice's weight traffic
+    // (MI355X, 4096 x 4096 Q8_0 at 32 tokens: activations after 3.5 us
+    // instead of 0.8)
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t row_bytes = (uint32_t)(in_dim / 256) * (uint32_t)MfoRow<F>::kB256;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)out_dim * row_bytes);
+#pragma unroll
+    for (int ph = 0; ph < G::NPH; ph++) {
+        const uint32_t slice_off = (uint32_t)((k0 + ph * G::KP) / 256) * (uint32_t)MfoRow<F>::kB256;
+#pragma unroll
+        for (int p = 0; p < G::WP; p++) {
+            const int g = p * G::TH + tid, row = g / G::PR, k = g - row * G::PR;
+            const uint32_t off = g < G::R * G::PR && k < G::PR - 1 && row0 + row < out_dim
+                ? (uint32_t)(row0 + row) * row_bytes + slice_off + 16u * (uint32_t)k
+                : kMfsNoPiece;
+            dma16b(rw, off, (lds_void *)(wbuf + ph * G::W_BUF + 16 * (p * G::TH + 64 * wv)));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. per-token exponent over the slice (a wavefront holds one token's
+    // pieces, or two at PT = 32: its halves), then the two planes
+#pragma unroll
+    for (int r = 0; r < G::XP; r++) {
+        const int g = r * G::TH + tid, t = g / G::PT, i = g - t * G::PT;
+        const float4 a = __builtin_bit_cast(float4, xv[r][0]), b = __builtin_bit_cast(float4, xv[r][1]);
+        const float m = G::PT == 64 ? wave_max(max8(a, b)) : half_wave_max(max8(a, b));
+        const int e = mf_exponent(m);
+        if (i == 0) us[t] = ldexpf(1.0f, -e);
+        uint4 hi, lo;
+        hilo8_rtz(a, b, ldexpf(1.0f, e), hi, lo);
+        int s_, j_, q_;
+        F::piece(8 * i, s_, j_, q_);
+        const int slot = mfo_slot<G::NTP>((s_ * 4 + j_) * 4 + q_, t);
+        xh[slot] = hi;
+        xlo[slot] = lo;
+    }
+    // 3. row tiles wv * RTW .. + RTW - 1 over the slice (each step's
+    // activation operands read from LDS once for all of them), phase by
+    // phase: the first phase's steps run while the second's weights land
+    f32x4 acc[RTW][NT];
+#pragma unroll
+    for (int rt = 0; rt < RTW; rt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[rt][nt] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < G::NS; st++) {
+        if (st % G::NSP == 0) {
+            // this thread's pieces of phase st / NSP have landed (the later
+            // phase's, issued after, may still be in flight), then everyone's
+            if (st == 0 && G::NPH == 2)
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(G::WP) : "memory");
+            else
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+            __syncthreads();
+        }
+        const uint8_t *wph = wbuf + (st / G::NSP) * G::W_BUF;
+        uint4 xr[4][NT], lr[4][NT];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const int slot = mfo_slot<G::NTP>((st * 4 + j) * 4 + q, nt * 16 + r16);
+                xr[j][nt] = xh[slot];
+                lr[j][nt] = xlo[slot];
+            }
+#pragma unroll
+        for (int rt = 0; rt < RTW; rt++) {
+            typename F::W wr;
+            MfsStage<F>::load(wr, wph + (16 * (wv * RTW + rt) + r16) * G::PR * 16, st % G::NSP, q, 0);
+            F::template step<NT>(wr, q, xr, lr, acc[rt]);
+        }
+    }
+    // 4. D: tokens 16 nt + 4 q + 0..3 of weight row r16
+    float *out = dst + (gridDim.x > 1 ? (size_t)z * n_tok * out_dim : 0);
+#pragma unroll
+    for (int rt = 0; rt < RTW; rt++) {
+        const int o = row0 + 16 * (wv * RTW + rt) + r16;
+        if (o < out_dim) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int t = nt * 16 + 4 * q + i;
+                    if (t < n_tok) out[(size_t)t * out_dim + o] = acc[rt][nt][i] * us[t];
+                }
+        }
+    }
 }
 
 // ---- routed experts grouped by expert (many tokens) --------------------------------
@@ -1286,14 +1502,94 @@ static int mfs_splits_for(uint32_t dtype, int in_dim, int out_dim) {
     }
 }
 
+// The one-pass kernel's rows per workgroup and slice length for this shape,
+// or rows = 0: the first of (128, 512), (64, 512), (128, 256), (64, 256)
+// that divides K and gives 192..512 workgroups (one or two rounds of one per
+// CU). Q8_0 and Q4_K, whose rows' slices are contiguous byte runs; 9..32
+// tokens.
+template <class F>
+static void mfo_choose(int n_tok, int in_dim, int out_dim, int &rows, int &ks) {
+    rows = ks = 0;
+    if constexpr (std::is_same<F, MQ8>::value || std::is_same<F, MQ4K>::value) {
+        if (n_tok < 9 || n_tok > 32 || in_dim <= 0 || out_dim <= 0 || in_dim % 256 != 0) return;
+        const size_t row_bytes = (size_t)(in_dim / 256) * MfoRow<F>::kB256;
+        if ((size_t)out_dim * row_bytes > 0xFFFFFFF0u ||
+            (size_t)n_tok * (size_t)in_dim * 4 > 0x7FFFFFFFu)
+            return;
+        const int cand[4][2] = {{128, 512}, {64, 512}, {128, 256}, {64, 256}};
+        for (const auto &c : cand) {
+            if (in_dim % c[1] != 0) continue;
+            const long n_wg = (long)((out_dim + c[0] - 1) / c[0]) * (in_dim / c[1]);
+            if (n_wg >= 192 && n_wg <= 512) {
+                rows = c[0];
+                ks = c[1];
+                return;
+            }
+        }
+    }
+}
+static void mfo_choose_dt(uint32_t dtype, int n_tok, int in_dim, int out_dim, int &rows, int &ks) {
+    rows = ks = 0;
+    if (dtype == T_Q8_0) mfo_choose<MQ8>(n_tok, in_dim, out_dim, rows, ks);
+    if (dtype == T_Q4_K) mfo_choose<MQ4K>(n_tok, in_dim, out_dim, rows, ks);
+}
+
+template <class F, int NT, int NW, int KS, int RTW>
+static hipError_t mfo_launch(const uint8_t *w, const float *x, float *part, float *y, int n_tok,
+                             int in_dim, int out_dim, hipStream_t s) {
+    using G = MfoGeo<F, NT, NW, KS, RTW>;
+    static_assert(G::LDS + 16 * NT * 4 <= 160 * 1024, "one workgroup's LDS");
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_mfo<F, NT, NW, KS, RTW>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
+    if (attr != hipSuccess) return attr;
+    const int sk = in_dim / KS;
+    const dim3 grid((unsigned)sk, (unsigned)((out_dim + G::R - 1) / G::R));
+    k_gemv_mfo<F, NT, NW, KS, RTW><<<grid, G::TH, G::LDS, s>>>(w, x, sk > 1 ? part : y, n_tok,
+                                                               in_dim, out_dim);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || sk == 1) return e;
+    const int n = n_tok * out_dim;
+    k_mfs_sum<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(part, y, n, sk);
+    return hipGetLastError();
+}
+
+// Wavefronts x row tiles per wavefront of the one-pass kernel for R rows.
+constexpr int kMfoNW128 = 8, kMfoRTW128 = 1, kMfoNW64 = 4, kMfoRTW64 = 1;
+
+template <class F>
+static hipError_t mfo_go(const uint8_t *w, const float *x, uint8_t *scratch, float *y, int n_tok,
+                         int in_dim, int out_dim, int rows, int ks, hipStream_t s) {
+    if constexpr (std::is_same<F, MQ8>::value || std::is_same<F, MQ4K>::value) {
+        float *part = reinterpret_cast<float *>(scratch);
+        const int nt = n_tok > 16 ? 2 : 1;
+#define MFO(NT, R, KS, NW, RTW)                                                                  \
+    if (nt == NT && rows == R && ks == KS)                                                       \
+        return mfo_launch<F, NT, NW, KS, RTW>(w, x, part, y, n_tok, in_dim, out_dim, s);
+#define MFO_ALL(NT)                                                                              \
+    MFO(NT, 128, 512, kMfoNW128, kMfoRTW128) MFO(NT, 64, 512, kMfoNW64, kMfoRTW64)              \
+    MFO(NT, 128, 256, kMfoNW128, kMfoRTW128) MFO(NT, 64, 256, kMfoNW64, kMfoRTW64)
+        MFO_ALL(1) MFO_ALL(2)
+#undef MFO_ALL
+#undef MFO
+    }
+    return hipErrorInvalidValue;
+}
+
 // Two f16 planes of ntp x in_dim, ntp unscale factors, and the staged
-// kernel's partial outputs when it splits K.
+// kernel's partial outputs when it splits K; or the one-pass kernel's
+// partials, whichever is larger.
 size_t gemv_mfma_scratch_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
     const size_t ntp = n_tok <= 16 ? 16 : 32;
     const int sk = mfs_splits_for(dtype, in_dim, out_dim);
     const size_t part = sk > 1 ? (size_t)sk * (size_t)n_tok * (size_t)out_dim * 4 : 0;
-    return al(2 * ntp * (size_t)in_dim * 2) + al(ntp * 4) + part;
+    const size_t staged = al(2 * ntp * (size_t)in_dim * 2) + al(ntp * 4) + part;
+    // the one-pass kernel: only its slices' partial outputs
+    int rows, ks;
+    mfo_choose_dt(dtype, n_tok, in_dim, out_dim, rows, ks);
+    const size_t one = rows ? al((size_t)(in_dim / ks) * (size_t)n_tok * (size_t)out_dim * 4) : 0;
+    return one > staged ? one : staged;
 }
 
 template <class F>
@@ -1368,6 +1664,11 @@ static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, 
     // the staged kernel wherever it applies (16-byte aligned weights: its
     // LDS copies move 16-byte pieces); it is the faster on every measured
     // shape (C1 14336 x 4096 Q6_K at 8 tokens: 21.8 vs 30.1 us)
+    if (((uintptr_t)w & 15) == 0) {
+        int rows, ks;
+        mfo_choose<F>(n_tok, in_dim, out_dim, rows, ks);
+        if (rows) return mfo_go<F>(w, x, scratch, y, n_tok, in_dim, out_dim, rows, ks, s);
+    }
     const int sk = mfs_splits<F>(in_dim, out_dim);
     if (sk > 0 && ((uintptr_t)w & 15) == 0)
         return mfs_go<F>(w, x, scratch, y, n_tok, in_dim, out_dim, sk, s);

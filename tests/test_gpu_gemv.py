@@ -53,6 +53,28 @@ def test_gemv_mfma_batches(oracle, hip, dtype, out_dim, in_dim, n_tok):
             assert rel_err(g[t], wv[t]) <= REL_TOL, f"token {t}"
 
 
+# The one-pass kernel (k_gemv_mfo: Q8_0 / Q4_K, 9..32 tokens, 192..512
+# workgroups of 128 or 64 rows x a 512- or 256-element K slice): one slice
+# (y written directly), a partial last row block at both row counts, many
+# slices, token scales far apart.
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q8_0])
+@pytest.mark.parametrize("out_dim,in_dim", [(24576, 512), (3000, 4096), (1000, 4096)])
+@pytest.mark.parametrize("n_tok", [9, 17, 32])
+def test_gemv_one_pass_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
+    w = synth.weight(dtype, out_dim, in_dim, 70 + n_tok)
+    x = synth.activations(n_tok, in_dim, 71 + n_tok)
+    x *= (np.float32(10.0) ** ((np.arange(n_tok) % 9) - 4)).astype(np.float32)[:, None]
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, x, n_tok, in_dim, out_dim, int(dtype))
+    got = np.full(n_tok * out_dim, np.nan, np.float32)
+    hip.matmul_quant_f32(got, w, x, n_tok, in_dim, out_dim, dtype)
+    assert not np.isnan(got).any()
+    g = got.reshape(n_tok, out_dim)
+    wv = want.reshape(n_tok, out_dim)
+    for t in range(n_tok):
+        assert rel_err(g[t], wv[t]) <= 1e-5, f"token {t}"
+
+
 # Exact weights and two-plane (hi + lo f16) activations on the matrix cores:
 # matrices of a few rows (where a maximum over few outputs is most
 # sensitive, and f16-rounded weights reached 1.2e-3 on 16 rows) within an
