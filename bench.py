@@ -445,7 +445,8 @@ PROBE_GEMVS = [("C1", "Q6_K", 14336, 4096), ("C1", "Q6_K", 4096, 14336), ("C0", 
 # --batch-probe runs (C1 at 4 and 8 tokens, C2 Q8_0 at 8 and 32)
 PROBE_BATCHED = [("C1", "Q6_K", 14336, 4096, 4), ("C1", "Q6_K", 4096, 14336, 4),
                  ("C1", "Q6_K", 14336, 4096, 8), ("C1", "Q6_K", 4096, 14336, 8),
-                 ("C2", "Q8_0", 4096, 4096, 8), ("C2", "Q8_0", 4096, 4096, 32),
+                 ("C2", "Q8_0", 4096, 4096, 8), ("C2", "Q8_0", 4096, 4096, 16),
+                 ("C2", "Q8_0", 4096, 4096, 32), ("C2", "Q8_0", 1024, 4096, 16),
                  ("C2", "Q8_0", 1024, 4096, 32)]
 
 
