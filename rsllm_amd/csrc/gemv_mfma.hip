@@ -32,6 +32,7 @@
 #include <type_traits>
 
 #include "gemv_formats.h"
+#include "moe_route.h"
 
 namespace rsllm_hip {
 
@@ -479,13 +480,16 @@ __global__ __launch_bounds__(kMfxThreads) void k_mf_x(const float *__restrict__ 
 // ---- GEMV ----------------------------------------------------------------------------
 // One workgroup's 16 * RT rows from row0 against the n_tok (<= 16 * NT)
 // token columns of xh (two planes of plane_bytes each), y[t * y_stride + o];
-// red: NK * RT * NT * 64 f32x4 of LDS.
-template <class F, int NT, int NK, int RT>
+// red: NK * RT * NT * 64 f32x4 of LDS. ROWX (NT = 1): a per-row image, the
+// lane's column at byte xcol of each plane, and lanes 0..15 hold their
+// column's unscale in usc (unscale unused).
+template <class F, int NT, int NK, int RT, bool ROWX = false>
 __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t w_bytes,
                                         const _Float16 *__restrict__ xh, uint32_t plane_bytes,
                                         const float *__restrict__ unscale, float *__restrict__ y,
                                         int n_tok, int in_dim, int out_dim, int y_stride, int row0,
-                                        f32x4 *red, int ntp) {
+                                        f32x4 *red, int ntp, uint32_t xcol = 0, float usc = 0.f) {
+    static_assert(!ROWX || NT == 1, "per-row images take one token tile");
     const int lane = threadIdx.x & 63, r16 = lane & 15, q = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nsteps = in_dim / kMfStep;
@@ -509,6 +513,12 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
         for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
+                if (ROWX) {
+                    const uint32_t o = xcol + (uint32_t)(((s * 4 + j) * 4 + q) * 16);
+                    xr[j][nt] = bload16(rx, o, 0);
+                    lr[j][nt] = bload16(rx, o + plane_bytes, 0);
+                    continue;
+                }
                 // image columns past ntp (ntp = 8): zeros, no access
                 const int col = nt * 16 + r16;
                 const uint32_t o = col < ntp
@@ -537,6 +547,13 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) red[((wv * RT + rt) * NT + nt) * 64 + lane] = acc[rt][nt];
+    // ROWX: this lane's four tokens' unscales (lane % 64 is the same in
+    // every pass of the loop below), read while every lane is active
+    float uq[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (ROWX) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) uq[i] = __shfl(usc, 4 * q + i, 64);
+    }
     __syncthreads();
     for (int c = threadIdx.x; c < RT * NT * 64; c += 64 * NK) {
         const int rt = c / (NT * 64), nt = (c / 64) % NT, ln = c % 64;
@@ -548,7 +565,8 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
         if (o < out_dim) {
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                if (t0 + i < n_tok) y[(size_t)(t0 + i) * y_stride + o] = v[i] * unscale[t0 + i];
+                if (t0 + i < n_tok)
+                    y[(size_t)(t0 + i) * y_stride + o] = v[i] * (ROWX ? uq[i] : unscale[t0 + i]);
         }
     }
 }
@@ -681,12 +699,17 @@ template <class F, int NW = 4, int ROWS = kMfsRows> struct MfsGeo {
 // lanes of A rows 0..7 read the hi plane of tokens 0..7, lanes of rows 8..15
 // the lo plane. NW wavefronts (64 NW threads) split each chunk's 8 steps,
 // 8 / NW each, for every row tile. smem: MfsGeo<F, NW, ROWS>::LDS bytes.
-template <class F, int NT, bool PACK = false, int NW = 4, int ROWS = kMfsRows>
+// ROWX (NT = 1): a per-row image, the lane's column (r16 & 7 packed, else
+// r16) at byte xcol of each plane, and lanes 0..15 hold their column's
+// unscale in usc (unscale unused).
+template <class F, int NT, bool PACK = false, int NW = 4, int ROWS = kMfsRows, bool ROWX = false>
 __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
                                          const _Float16 *__restrict__ xh, uint32_t plane_bytes,
                                          const float *__restrict__ unscale, float *__restrict__ y,
                                          int y_stride, int n_tok, int in_dim, int out_dim,
-                                         int row0, int c0, int nch, int ntp, uint8_t *smem) {
+                                         int row0, int c0, int nch, int ntp, uint8_t *smem,
+                                         uint32_t xcol = 0, float usc = 0.f) {
+    static_assert(!ROWX || NT == 1, "per-row images take one token tile");
     using S = MfsStage<F>;
     using G = MfsGeo<F, NW, ROWS>;
     constexpr int RT = ROWS / 16;
@@ -741,6 +764,16 @@ __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
             for (int j = 0; j < 4; j++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
+                    if (ROWX) {
+                        const uint32_t o = xcol + (uint32_t)(((st * 4 + j) * 4 + q) * 16);
+                        if (PACK) {
+                            xr[u][j][nt] = bload16(rx, o + (r16 >= 8 ? plane_bytes : 0u), 0);
+                        } else {
+                            xr[u][j][nt] = bload16(rx, o, 0);
+                            lr[u][j][nt] = bload16(rx, o + plane_bytes, 0);
+                        }
+                        continue;
+                    }
                     if (PACK) {
                         xr[u][j][nt] = bload16(
                             rx, (uint32_t)((((st * 4 + j) * 4 + q) * 8 + (r16 & 7)) * 16) +
@@ -811,6 +844,13 @@ __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) red[((wv * RT + rt) * NT + nt) * 64 + lane] = acc[rt][nt];
+    // ROWX: this lane's four tokens' unscales (e % 64 below is the lane),
+    // read while every lane is active
+    float uq[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (ROWX) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) uq[i] = __shfl(usc, 4 * q + i, 64);
+    }
     __syncthreads();
     for (int e = tid; e < RT * NT * 64; e += TH) {
         const int rt = e / (NT * 64), nt = (e / 64) % NT, ln = e % 64;
@@ -829,7 +869,8 @@ __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
         if (o < out_dim) {
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                if (t0 + i < n_tok) y[(size_t)(t0 + i) * y_stride + o] = v[i] * unscale[t0 + i];
+                if (t0 + i < n_tok)
+                    y[(size_t)(t0 + i) * y_stride + o] = v[i] * (ROWX ? uq[i] : unscale[t0 + i]);
         }
     }
 }
@@ -1070,21 +1111,26 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfo(const uint8_t *__restrict_
 // off[e + 1]), cut into batches of up to bw = 8 or 16 (mfg_width; k_moe_scan
 // lists them); a batch is the token set (the N dimension) of one pass over
 // that expert's rows, so each expert's weights are streamed once per bw of
-// its slots. Batch b's activation image (two planes of in_dim * bw values,
-// the k_mf_x layout with ntp = bw) sits at xh + 2 b in_dim bw and its scales
-// at unscale + b * bw; its rows go to y + first * out_dim.
+// its slots. The activation images hold one row per x row (gate/up) or per
+// slot (down), not per batch column: row r's 8-element pieces in MFMA
+// operand order, piece ((s * 4 + j) * 4 + q) at halves r * in_dim + 8 *
+// piece of the hi plane, the lo plane n_rows * in_dim halves later, scaled
+// by 2^e_r; unscale[r] = 2^-e_r. Column c of batch b reads row
+// tok[first + c] (gate/up) or first + c (down). A row is written once
+// however many batches read it, by one workgroup, in whole cache lines.
 
 // One token column of an ntp-wide activation image (the k_mf_x conversion,
 // one workgroup of TH threads, the row read once when it fits in
 // registers): val4(i) gives elements i .. i + 3 of the column's row; the
-// column's pieces go to both planes of the image at xb, 2^-e to *us.
+// column's pieces go to both planes of the image at xb (the lo plane
+// `plane` halves after the hi plane; 0: in_dim * ntp), 2^-e to *us.
 template <class F, int TH = kMfxThreads, class V>
 __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 *__restrict__ xb,
-                                            float *__restrict__ us, int ntp) {
+                                            float *__restrict__ us, int ntp, size_t plane = 0) {
     __shared__ float red[TH / 64];
     const int tid = threadIdx.x;
     const int n8 = in_dim / 8;
-    const size_t plane = (size_t)in_dim * ntp;
+    if (plane == 0) plane = (size_t)in_dim * ntp;
     auto store = [&](int i, const uint4 &hi, const uint4 &lo) {
         int s, j, q;
         F::piece(8 * i, s, j, q);
@@ -1131,26 +1177,15 @@ __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 
     }
 }
 
-// Activation image of batch blockIdx.y, token column blockIdx.x: row =
-// x[tok[first + t]] (SWIGLU false) or the clamped SwiGLU of rows first + t
-// of hg, hu (SWIGLU true). Columns past the batch's count are left as they
-// are: column t of an MFMA's B operand reaches only column t of its result,
-// and those outputs are not stored.
+// Row blockIdx.x of a per-row image: x row r, or (SWIGLU) the clamped
+// SwiGLU of rows r of hg (x) and hu. Rows at or past *n_rows (when given)
+// exit: slots past the routed ones.
 template <class F, bool SWIGLU, int TH>
-__global__ __launch_bounds__(TH) void k_mfg_x(const float *__restrict__ x,
-                                               const float *__restrict__ hu,
-                                               const int *__restrict__ tok,
-                                               const MfgBatch *__restrict__ bat,
-                                               const int *__restrict__ n_bat, float clamp,
-                                               _Float16 *__restrict__ xh,
-                                               float *__restrict__ unscale, int in_dim, int bw) {
-    const int b = blockIdx.y, t = blockIdx.x;
-    if (b >= *n_bat) return;
-    const MfgBatch bt = bat[b];
-    if (t >= bt.count) return;
-    const size_t row = SWIGLU ? (size_t)(bt.first + t) : (size_t)tok[bt.first + t];
-    const float *xt = x + row * in_dim;
-    const float *ut = hu + (SWIGLU ? row * in_dim : 0);
+__device__ __forceinline__ void mfg_row(const float *__restrict__ x, const float *__restrict__ hu,
+                                        int r, float clamp, _Float16 *__restrict__ xh,
+                                        float *__restrict__ unscale, int in_dim, int n_alloc) {
+    const float *xt = x + (size_t)r * in_dim;
+    const float *ut = hu + (SWIGLU ? (size_t)r * in_dim : 0);
     auto val4 = [&](int i) {
         float4 v = *reinterpret_cast<const float4 *>(xt + i);
         if (SWIGLU) {
@@ -1160,8 +1195,44 @@ __global__ __launch_bounds__(TH) void k_mfg_x(const float *__restrict__ x,
         }
         return v;
     };
-    mf_x_column<F, TH>(val4, in_dim, t, xh + (size_t)b * 2 * in_dim * bw,
-                       unscale + (size_t)b * bw + t, bw);
+    mf_x_column<F, TH>(val4, in_dim, 0, xh + (size_t)r * in_dim, unscale + r, 1,
+                       (size_t)n_alloc * in_dim);
+}
+
+// The SwiGLU image of the down projection: one workgroup per slot.
+template <class F, int TH>
+__global__ __launch_bounds__(TH) void k_mfg_xs(const float *__restrict__ hg,
+                                               const float *__restrict__ hu,
+                                               const int *__restrict__ n_rows, float clamp,
+                                               _Float16 *__restrict__ xh,
+                                               float *__restrict__ unscale, int in_dim,
+                                               int n_alloc) {
+    const int r = blockIdx.x;
+    if (r >= *n_rows) return;
+    mfg_row<F, true, TH>(hg, hu, r, clamp, xh, unscale, in_dim, n_alloc);
+}
+
+// The first launch of the route: workgroup 0 runs the routing (when `route`;
+// moe_route1, batches into bat / *n_bat), the others write the per-token
+// image of x (x rows do not depend on the routing). Without `route` (calls
+// the three-launch routing serves) every workgroup writes an image row.
+template <class F>
+__global__ __launch_bounds__(kScanThreads) void k_mfg_route_x(MoeRoute1Args ra, MfgBatch *bat,
+                                                              int *n_bat, int bw, int route,
+                                                              const float *__restrict__ x,
+                                                              int n_tok, _Float16 *__restrict__ xh,
+                                                              float *__restrict__ unscale,
+                                                              int in_dim) {
+    extern __shared__ int sh[];  // routing: 2 n_expert ints
+    __shared__ int ep[kRoute1Pairs];
+    __shared__ int part[kScanThreads];
+    if (route && blockIdx.x == 0) {
+        moe_route1(ra.ids, ra.wts, ra.n_pairs, ra.k, ra.n_expert, ra.off, ra.slot_tok, ra.slot_of,
+                   ra.act, ra.n_act, bat, n_bat, bw, sh, ep, part);
+        return;
+    }
+    mfg_row<F, false, kScanThreads>(x, nullptr, (int)blockIdx.x - (route ? 1 : 0), 0.f, xh, unscale,
+                                    in_dim, n_tok);
 }
 
 // ---- grouped LoRA-down on the matrix cores ----------------------------------------
@@ -1200,19 +1271,35 @@ __global__ __launch_bounds__(256) void k_gemv_mfl(const uint8_t *__restrict__ w,
                                        red, kMfgBatch);
 }
 
+// Batch column of lane r16 (c = r16 & 7 in the packed 8-column operand,
+// else r16; columns past the batch's count read its first column, whose
+// results are not stored) and its image row: the slot's token (tok given,
+// gate/up) or the slot (down); its byte offset in a plane and its unscale.
+__device__ __forceinline__ void mfg_column(const MfgBatch &bt, const int *__restrict__ tok,
+                                           const float *__restrict__ unscale, int in_dim, int c,
+                                           uint32_t &xcol, float &usc) {
+    const int slot = bt.first + (c < bt.count ? c : 0);
+    const int row = tok ? tok[slot] : slot;
+    xcol = (uint32_t)row * (uint32_t)in_dim * 2u;
+    usc = unscale[row];
+}
+
 // Grid (row blocks, batch slots, matrices): workgroup (x, b, m) computes
 // rows 16 RT x of W_m[expert(b)] = w_m + expert * w_stride for batch b's
-// slots into y_m. Batch slots past *n_bat exit at once.
+// slots into y_m, against the per-row image xh (planes of plane_bytes).
+// Batch slots past *n_bat exit at once.
 template <class F, int NK, int RT>
 __global__ __launch_bounds__(64 * NK) void k_gemv_mfg(const uint8_t *__restrict__ w0,
                                                       const uint8_t *__restrict__ w1,
                                                       size_t w_stride,
                                                       const _Float16 *__restrict__ xh,
+                                                      uint32_t plane_bytes,
                                                       const float *__restrict__ unscale,
+                                                      const int *__restrict__ tok,
                                                       const MfgBatch *__restrict__ bat,
                                                       const int *__restrict__ n_bat,
                                                       float *__restrict__ y0, float *__restrict__ y1,
-                                                      int in_dim, int out_dim, int bw) {
+                                                      int in_dim, int out_dim) {
     __shared__ f32x4 red[NK * RT * 64];
     const int b = blockIdx.y;
     if (b >= *n_bat) return;
@@ -1220,23 +1307,27 @@ __global__ __launch_bounds__(64 * NK) void k_gemv_mfg(const uint8_t *__restrict_
     const bool m1 = blockIdx.z != 0;
     const uint8_t *w = (m1 ? w1 : w0) + (size_t)bt.expert * w_stride;
     float *y = (m1 ? y1 : y0) + (size_t)bt.first * out_dim;
-    const size_t img = (size_t)in_dim * bw;  // values per plane
-    mf_rows<F, 1, NK, RT>(w, (uint32_t)w_stride, xh + b * 2 * img, (uint32_t)(img * 2),
-                          unscale + (size_t)b * bw, y, bt.count, in_dim, out_dim, out_dim,
-                          blockIdx.x * 16 * RT, red, bw);
+    uint32_t xcol;
+    float usc;
+    mfg_column(bt, tok, unscale, in_dim, threadIdx.x & 15, xcol, usc);
+    mf_rows<F, 1, NK, RT, true>(w, (uint32_t)w_stride, xh, plane_bytes, nullptr, y, bt.count,
+                                in_dim, out_dim, out_dim, blockIdx.x * 16 * RT, red, 16, xcol, usc);
 }
 
 // The grouped GEMV with its weights staged through LDS (mfs_rows): grid
 // (ROWS-row blocks, batch slots, matrices); workgroup (x, b, m) computes
-// rows ROWS x of W_m[expert(b)] for batch b's slots into y_m. Batch slots
-// past *n_bat exit at once. PACK: 8-slot batches on the packed kernel (8
-// wavefronts); else 16-slot batches (4 wavefronts).
+// rows ROWS x of W_m[expert(b)] for batch b's slots into y_m, against the
+// per-row image xh (planes of plane_bytes). Batch slots past *n_bat exit at
+// once. PACK: 8-slot batches on the packed kernel (8 wavefronts); else
+// 16-slot batches (4 wavefronts).
 template <class F, bool PACK, int ROWS>
 __global__ __launch_bounds__(PACK ? 64 * kMfsPackWaves : 256) void k_gemv_mfgs(const uint8_t *__restrict__ w0,
                                                    const uint8_t *__restrict__ w1,
                                                    size_t w_stride,
                                                    const _Float16 *__restrict__ xh,
+                                                   uint32_t plane_bytes,
                                                    const float *__restrict__ unscale,
+                                                   const int *__restrict__ tok,
                                                    const MfgBatch *__restrict__ bat,
                                                    const int *__restrict__ n_bat,
                                                    float *__restrict__ y0, float *__restrict__ y1,
@@ -1249,10 +1340,12 @@ __global__ __launch_bounds__(PACK ? 64 * kMfsPackWaves : 256) void k_gemv_mfgs(c
     const uint8_t *w = (m1 ? w1 : w0) + (size_t)bt.expert * w_stride;
     float *y = (m1 ? y1 : y0) + (size_t)bt.first * out_dim;
     constexpr int bw = PACK ? 8 : kMfgBatch;
-    const size_t img = (size_t)in_dim * bw;  // values per plane
-    mfs_rows<F, 1, PACK, PACK ? kMfsPackWaves : 4, ROWS>(
-        w, xh + b * 2 * img, (uint32_t)(img * 2), unscale + (size_t)b * bw, y, out_dim, bt.count,
-        in_dim, out_dim, (int)blockIdx.x * ROWS, 0, in_dim / kMfsK, bw, smem);
+    uint32_t xcol;
+    float usc;
+    mfg_column(bt, tok, unscale, in_dim, threadIdx.x & (bw - 1), xcol, usc);
+    mfs_rows<F, 1, PACK, PACK ? kMfsPackWaves : 4, ROWS, true>(
+        w, xh, plane_bytes, nullptr, y, out_dim, bt.count, in_dim, out_dim,
+        (int)blockIdx.x * ROWS, 0, in_dim / kMfsK, bw, smem, xcol, usc);
 }
 
 // ---- fused batched GEMV: activations converted into LDS ------------------------------
@@ -1701,40 +1794,26 @@ bool moe_mfma_supported(uint32_t dt_gu, uint32_t dt_d, int n_embd, int n_ff) {
 
 size_t moe_mfma_scratch_bytes(int n_pairs, int n_expert, int n_embd, int n_ff) {
     const int bw = mfg_width(n_pairs, n_expert);
-    const size_t nb = (size_t)mfg_max_batches(n_pairs, n_expert, bw);
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
-    return mfg_batch_bytes(n_pairs, n_expert, bw) + al(nb * bw * (size_t)n_embd * 4) +
-           al(nb * bw * 4) + al(nb * bw * (size_t)n_ff * 4) + al(nb * bw * 4);
+    // the batch list, then the x image (at most n_pairs tokens) and the
+    // SwiGLU image (one row per slot), two f16 planes and a scale per row
+    return mfg_batch_bytes(n_pairs, n_expert, bw) + al((size_t)n_pairs * n_embd * 4) +
+           al((size_t)n_pairs * 4) + al((size_t)n_pairs * n_ff * 4) + al((size_t)n_pairs * 4);
 }
 
+bool moe_mfma_fits(int n_pairs, int n_embd, int n_ff) {
+    // image offsets are 32-bit: two planes of n_pairs rows
+    return (size_t)n_pairs * (size_t)(n_embd > n_ff ? n_embd : n_ff) * 4 <= 0xFFFFFFFFu;
+}
+
+// The grouped GEMV of one matrix pair (w1 given: gate and up) or matrix over
+// the batches, against the per-row image xh of n_rows rows.
 template <class F>
-static hipError_t mfg_pass(const uint8_t *w0, const uint8_t *w1, size_t w_stride, const float *x,
-                           const float *hu, const int *tok, const MfgBatch *bat, const int *n_bat,
-                           int max_b, float clamp, _Float16 *xh, float *us, float *y0, float *y1,
+static hipError_t mfg_gemv(const uint8_t *w0, const uint8_t *w1, size_t w_stride,
+                           const _Float16 *xh, const float *us, int n_rows, const int *tok,
+                           const MfgBatch *bat, const int *n_bat, int max_b, float *y0, float *y1,
                            int in_dim, int out_dim, int bw, hipStream_t s) {
-    // one workgroup per column; 256 threads for rows of up to 2048 elements
-    // (one 8-element piece per thread), else kMfxThreads
-    const dim3 gx((unsigned)bw, (unsigned)max_b);
-    if (in_dim <= 2048) {
-        if (hu)
-            k_mfg_x<F, true, 256><<<gx, 256, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
-        else
-            k_mfg_x<F, false, 256><<<gx, 256, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
-    } else if (in_dim <= 8192) {
-        if (hu)
-            k_mfg_x<F, true, 512><<<gx, 512, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
-        else
-            k_mfg_x<F, false, 512><<<gx, 512, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh, us, in_dim, bw);
-    } else {
-        if (hu)
-            k_mfg_x<F, true, kMfxThreads><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh,
-                                                                    us, in_dim, bw);
-        else
-            k_mfg_x<F, false, kMfxThreads><<<gx, kMfxThreads, 0, s>>>(x, hu, tok, bat, n_bat, clamp, xh,
-                                                                     us, in_dim, bw);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    const uint32_t plane = (uint32_t)((size_t)n_rows * in_dim * 2);
     // weights staged through LDS where the layout allows (16-byte aligned
     // expert matrices, in_dim a multiple of 1024, of 2048 for Q6_K)
     if (mfs_splits<F>(in_dim, out_dim) > 0 &&
@@ -1750,7 +1829,7 @@ static hipError_t mfg_pass(const uint8_t *w0, const uint8_t *w1, size_t w_stride
             if (attr != hipSuccess) return attr;
             const dim3 g((unsigned)((out_dim + rows - 1) / rows), (unsigned)max_b, w1 ? 2u : 1u);
             k_gemv_mfgs<F, true, rows><<<g, 64 * kMfsPackWaves, lds, s>>>(
-                w0, w1, w_stride, xh, us, bat, n_bat, y0, y1, in_dim, out_dim);
+                w0, w1, w_stride, xh, plane, us, tok, bat, n_bat, y0, y1, in_dim, out_dim);
         } else {
             constexpr int lds = MfsGeo<F>::LDS;
             static const hipError_t attr =
@@ -1759,39 +1838,84 @@ static hipError_t mfg_pass(const uint8_t *w0, const uint8_t *w1, size_t w_stride
             if (attr != hipSuccess) return attr;
             const dim3 g((unsigned)((out_dim + kMfsRows - 1) / kMfsRows), (unsigned)max_b,
                          w1 ? 2u : 1u);
-            k_gemv_mfgs<F, false, kMfsRows><<<g, 256, lds, s>>>(w0, w1, w_stride, xh, us, bat,
-                                                                n_bat, y0, y1, in_dim, out_dim);
+            k_gemv_mfgs<F, false, kMfsRows><<<g, 256, lds, s>>>(
+                w0, w1, w_stride, xh, plane, us, tok, bat, n_bat, y0, y1, in_dim, out_dim);
         }
         return hipGetLastError();
     }
     constexpr int NK = 4, RT = 4;
     const dim3 g((unsigned)((out_dim + 16 * RT - 1) / (16 * RT)), (unsigned)max_b, w1 ? 2u : 1u);
-    k_gemv_mfg<F, NK, RT><<<g, 64 * NK, 0, s>>>(w0, w1, w_stride, xh, us, bat, n_bat, y0, y1,
-                                                in_dim, out_dim, bw);
+    k_gemv_mfg<F, NK, RT><<<g, 64 * NK, 0, s>>>(w0, w1, w_stride, xh, plane, us, tok, bat, n_bat,
+                                                y0, y1, in_dim, out_dim);
     return hipGetLastError();
 }
 
-static hipError_t mfg_pass_dt(uint32_t dt, const uint8_t *w0, const uint8_t *w1, size_t w_stride,
-                              const float *x, const float *hu, const int *tok, const MfgBatch *bat,
-                              const int *n_bat, int max_b, float clamp, _Float16 *xh, float *us,
-                              float *y0, float *y1, int in_dim, int out_dim, int bw, hipStream_t s) {
-#define MFG(F) mfg_pass<F>(w0, w1, w_stride, x, hu, tok, bat, n_bat, max_b, clamp, xh, us, y0, y1, in_dim, out_dim, bw, s)
-    switch (dt) {
-    case T_Q4_K: return MFG(MQ4K);
-    case T_Q6_K: return MFG(MQ6K);
-    case T_Q8_0: return MFG(MQ8);
-    default: return hipErrorInvalidValue;
-    }
-#undef MFG
+// The SwiGLU image of the down projection, one workgroup per slot (n_alloc
+// rows allocated, *n_rows routed).
+template <class F>
+static hipError_t mfg_swiglu_image(const float *hg, const float *hu, const int *n_rows,
+                                   int n_alloc, float clamp, _Float16 *xh, float *us, int in_dim,
+                                   hipStream_t s) {
+    // 256 threads for rows of up to 2048 elements (one 8-element piece per
+    // thread), 512 up to 8192, else kMfxThreads
+    const dim3 g((unsigned)n_alloc);
+    if (in_dim <= 2048)
+        k_mfg_xs<F, 256><<<g, 256, 0, s>>>(hg, hu, n_rows, clamp, xh, us, in_dim, n_alloc);
+    else if (in_dim <= 8192)
+        k_mfg_xs<F, 512><<<g, 512, 0, s>>>(hg, hu, n_rows, clamp, xh, us, in_dim, n_alloc);
+    else
+        k_mfg_xs<F, kMfxThreads><<<g, kMfxThreads, 0, s>>>(hg, hu, n_rows, clamp, xh, us, in_dim,
+                                                         n_alloc);
+    return hipGetLastError();
 }
+
+#define MFG_DT(dt, call)                            \
+    switch (dt) {                                   \
+    case T_Q4_K: { using F = MQ4K; return call; }   \
+    case T_Q6_K: { using F = MQ6K; return call; }   \
+    case T_Q8_0: { using F = MQ8; return call; }    \
+    default: return hipErrorInvalidValue;           \
+    }
+
+static hipError_t mfg_gemv_dt(uint32_t dt, const uint8_t *w0, const uint8_t *w1, size_t w_stride,
+                              const _Float16 *xh, const float *us, int n_rows, const int *tok,
+                              const MfgBatch *bat, const int *n_bat, int max_b, float *y0,
+                              float *y1, int in_dim, int out_dim, int bw, hipStream_t s) {
+    MFG_DT(dt, mfg_gemv<F>(w0, w1, w_stride, xh, us, n_rows, tok, bat, n_bat, max_b, y0, y1,
+                           in_dim, out_dim, bw, s))
+}
+
+static hipError_t mfg_swiglu_image_dt(uint32_t dt, const float *hg, const float *hu,
+                                      const int *n_rows, int n_alloc, float clamp, _Float16 *xh,
+                                      float *us, int in_dim, hipStream_t s) {
+    MFG_DT(dt, mfg_swiglu_image<F>(hg, hu, n_rows, n_alloc, clamp, xh, us, in_dim, s))
+}
+
+static hipError_t mfg_route_x_dt(uint32_t dt, const MoeRoute1Args *ra, MfgBatch *bat, int *n_bat,
+                                 int bw, const float *x, int n_tok, _Float16 *xh, float *us,
+                                 int in_dim, hipStream_t s) {
+    const MoeRoute1Args none{};
+    const unsigned grid = (unsigned)n_tok + (ra ? 1u : 0u);
+    const size_t lds = ra ? (size_t)ra->n_expert * 8 : 0;
+    MFG_DT(dt, (k_mfg_route_x<F><<<grid, kScanThreads, lds, s>>>(ra ? *ra : none, bat, n_bat, bw,
+                                                                 ra ? 1 : 0, x, n_tok, xh, us,
+                                                                 in_dim),
+                hipGetLastError()))
+}
+#undef MFG_DT
 
 hipError_t launch_moe_mfma(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
                            const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
-                           const int *slot_tok, const MfgBatch *bat, const int *n_bat,
-                           int n_pairs, int n_expert, float *hg, float *hu, float *yd,
-                           uint8_t *scratch, int n_embd, int n_ff, float clamp, hipStream_t s) {
-    if (!moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff)) return hipErrorInvalidValue;
-    if (gu_stride > 0xFFFFFFFFu || d_stride > 0xFFFFFFFFu) return hipErrorInvalidValue;
+                           int n_tok, const MoeRoute1Args *route, const int *off,
+                           const int *slot_tok, MfgBatch *bat, int *n_bat, int n_pairs,
+                           int n_expert, float *hg, float *hu, float *yd, uint8_t *scratch,
+                           int n_embd, int n_ff, float clamp, hipStream_t s) {
+    if (!moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff) || !moe_mfma_fits(n_pairs, n_embd, n_ff))
+        return hipErrorInvalidValue;
+    if (gu_stride > 0xFFFFFFFFu || d_stride > 0xFFFFFFFFu || n_tok > n_pairs)
+        return hipErrorInvalidValue;
+    if (route && (route->n_pairs > kRoute1Pairs || route->n_expert > kRoute1Experts))
+        return hipErrorInvalidValue;
     const int bw = mfg_width(n_pairs, n_expert);  // as the routing that listed the batches
     const int max_b = mfg_max_batches(n_pairs, n_expert, bw);
     uint8_t *p = scratch + mfg_batch_bytes(n_pairs, n_expert, bw);
@@ -1800,16 +1924,24 @@ hipError_t launch_moe_mfma(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
         p += (n + 255) / 256 * 256;
         return r;
     };
-    _Float16 *xh1 = reinterpret_cast<_Float16 *>(take((size_t)max_b * bw * n_embd * 4));
-    float *us1 = reinterpret_cast<float *>(take((size_t)max_b * bw * 4));
-    _Float16 *xh2 = reinterpret_cast<_Float16 *>(take((size_t)max_b * bw * n_ff * 4));
-    float *us2 = reinterpret_cast<float *>(take((size_t)max_b * bw * 4));
+    _Float16 *xh1 = reinterpret_cast<_Float16 *>(take((size_t)n_pairs * n_embd * 4));
+    float *us1 = reinterpret_cast<float *>(take((size_t)n_pairs * 4));
+    _Float16 *xh2 = reinterpret_cast<_Float16 *>(take((size_t)n_pairs * n_ff * 4));
+    float *us2 = reinterpret_cast<float *>(take((size_t)n_pairs * 4));
     hipError_t e;
-    if ((e = mfg_pass_dt(dt_gu, gate, up, gu_stride, x, nullptr, slot_tok, bat, n_bat, max_b, 0.f,
-                         xh1, us1, hg, hu, n_embd, n_ff, bw, s)) != hipSuccess)
+    // routing (when given) and the x image in one launch
+    if ((e = mfg_route_x_dt(dt_gu, route, bat, n_bat, bw, x, n_tok, xh1, us1, n_embd, s)) !=
+        hipSuccess)
         return e;
-    return mfg_pass_dt(dt_d, down, nullptr, d_stride, hg, hu, nullptr, bat, n_bat, max_b, clamp,
-                       xh2, us2, yd, nullptr, n_ff, n_embd, bw, s);
+    if ((e = mfg_gemv_dt(dt_gu, gate, up, gu_stride, xh1, us1, n_tok, slot_tok, bat, n_bat, max_b,
+                         hg, hu, n_embd, n_ff, bw, s)) != hipSuccess)
+        return e;
+    // off[n_expert]: the routed slot count
+    if ((e = mfg_swiglu_image_dt(dt_d, hg, hu, off + n_expert, n_pairs, clamp, xh2, us2, n_ff,
+                                 s)) != hipSuccess)
+        return e;
+    return mfg_gemv_dt(dt_d, down, nullptr, d_stride, xh2, us2, n_pairs, nullptr, bat, n_bat,
+                       max_b, yd, nullptr, n_ff, n_embd, bw, s);
 }
 
 bool lora_mfma_supported(uint32_t dtype, int n_tok, int D, int G, int R) {

@@ -128,23 +128,27 @@ hipError_t launch_quantize_swiglu(uint32_t dtype, const float *hg, const float *
                                   uint8_t *xq, int n_rows, int n, const int *off, int n_expert,
                                   hipStream_t s);
 
-// gemv_mfma.hip, routed experts on the matrix cores (Q4_K gate/up and down;
-// n_embd and n_ff multiples of 256, at least 1024). Slots sorted by expert as
-// launch_gemv_grouped's (off: n_expert + 1 entries on the device, slot_tok:
-// the token of each sorted slot, n_pairs = n_tok * k bounding the slot
-// count). Writes hg, hu [slot x n_ff] (gate and up of x[slot_tok[slot]])
-// and yd [slot x n_embd] (down of the clamped SwiGLU of hg, hu). `scratch`
-// holds moe_mfma_scratch_bytes(n_pairs, n_expert, n_embd, n_ff) bytes.
-// The batches: each active expert's sorted slots cut into runs of up to
-// mfg_width(n_pairs, n_expert) (experts ascending, runs in slot order),
-// *n_bat of them, as k_moe_scan lists them; at most mfg_max_batches(n_pairs,
-// n_expert, width). `scratch` holds moe_mfma_scratch_bytes(...) bytes: the
-// batch list and its count first (mfg_batch_bytes), then the activation
-// images.
+// gemv_mfma.hip, routed experts on the matrix cores (Q4_K, Q6_K or Q8_0
+// gate/up and down; n_embd and n_ff multiples of 256). Slots sorted by
+// expert as launch_gemv_grouped's (off: n_expert + 1 entries on the device,
+// slot_tok: the token of each sorted slot, n_pairs = n_tok * k bounding the
+// slot count). Writes hg, hu [slot x n_ff] (gate and up of
+// x[slot_tok[slot]]) and yd [slot x n_embd] (down of the clamped SwiGLU of
+// hg, hu). The batches: each active expert's sorted slots cut into runs of
+// up to mfg_width(n_pairs, n_expert) (experts ascending, runs in slot
+// order), *n_bat of them, as k_moe_scan lists them; at most
+// mfg_max_batches(n_pairs, n_expert, width). With `route` (calls of up to
+// kRoute1Pairs pairs) the first launch also runs the one-workgroup routing
+// that writes off, slot_tok, slot_of, the active experts and the batches;
+// without it the caller has routed. `scratch` holds
+// moe_mfma_scratch_bytes(n_pairs, n_expert, n_embd, n_ff) bytes: the batch
+// list and its count first (mfg_batch_bytes; bat, n_bat point there), then
+// the activation images.
 constexpr int kMfgBatch = 16;
 struct MfgBatch {
     int first, count, expert, pad;
 };
+struct MoeRoute1Args;
 // Batch width of the grouped routed-expert route: 8 slots (the packed
 // 8-column kernel) when the experts average at most 8 slots, else 16.
 inline int mfg_width(int n_pairs, int n_expert) {
@@ -158,12 +162,15 @@ inline size_t mfg_batch_bytes(int n_pairs, int n_expert, int width) {
            256;
 }
 bool moe_mfma_supported(uint32_t dt_gu, uint32_t dt_d, int n_embd, int n_ff);
+// the images' byte offsets fit 32 bits
+bool moe_mfma_fits(int n_pairs, int n_embd, int n_ff);
 size_t moe_mfma_scratch_bytes(int n_pairs, int n_expert, int n_embd, int n_ff);
 hipError_t launch_moe_mfma(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
                            const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
-                           const int *slot_tok, const MfgBatch *bat, const int *n_bat,
-                           int n_pairs, int n_expert, float *hg, float *hu, float *yd,
-                           uint8_t *scratch, int n_embd, int n_ff, float clamp, hipStream_t s);
+                           int n_tok, const MoeRoute1Args *route, const int *off,
+                           const int *slot_tok, MfgBatch *bat, int *n_bat, int n_pairs,
+                           int n_expert, float *hg, float *hu, float *yd, uint8_t *scratch,
+                           int n_embd, int n_ff, float clamp, hipStream_t s);
 
 // gemv_mfma.hip, matmul_grouped_lora_down on the matrix cores: y[t *
 // y_stride + g * R + r] = sum_i W[g R + r, i] x[t * x_stride + g * D + i]

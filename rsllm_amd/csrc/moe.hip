@@ -24,6 +24,7 @@
 //   7. k_moe_accumulate: out[t, j] += w[t, i] * yd[slot(t, i), j] in i order,
 //      as the reference's `out_t[j] += we * expert_out[j]` (no contraction).
 #include "gemv_formats.h"
+#include "moe_route.h"
 
 namespace rsllm_hip {
 
@@ -68,46 +69,6 @@ __global__ __launch_bounds__(kRouteBlock) void k_moe_hist(const int *__restrict_
     }
     __syncthreads();
     for (int x = tid; x < n_expert; x += kRouteBlock) hist[(size_t)x * nblk + b] = cnt[x];
-}
-
-// Exclusive scan of v[0..n) in place by the whole workgroup (kScanThreads
-// threads), returning the total; `part` holds kScanThreads ints of LDS (the
-// first kScanThreads / 64 are used). Each thread sums a contiguous segment;
-// the per-thread sums are scanned within each wavefront (six shuffle-up
-// steps), the wavefront totals by every thread in turn (16 adds), so the
-// scan costs two barriers plus the final one. Integer sums: the order does
-// not change the result.
-constexpr int kScanThreads = 1024;
-__device__ int scan_inplace(int *__restrict__ v, size_t n, int *part) {
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const size_t seg = (n + kScanThreads - 1) / kScanThreads;
-    const size_t lo = min(n, (size_t)tid * seg), hi = min(n, lo + seg);
-    int sum = 0;
-    for (size_t i = lo; i < hi; i++) sum += v[i];
-    // inclusive scan of the per-thread sums within the wavefront
-    int inc = sum;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int add = __shfl_up(inc, (unsigned)d, 64);
-        if (lane >= d) inc += add;
-    }
-    if (lane == 63) part[wv] = inc;
-    __syncthreads();
-    int base = 0, total = 0;
-#pragma unroll
-    for (int w = 0; w < kScanThreads / 64; w++) {
-        const int t = part[w];
-        base += w < wv ? t : 0;
-        total += t;
-    }
-    int run = base + inc - sum;  // exclusive prefix of this thread's segment
-    for (size_t i = lo; i < hi; i++) {
-        const int c = v[i];
-        v[i] = run;
-        run += c;
-    }
-    __syncthreads();
-    return total;
 }
 
 // One workgroup: hist -> bases (in place); off[e] (n_expert + 1 entries);
@@ -177,13 +138,10 @@ __global__ __launch_bounds__(kRouteBlock) void k_moe_scatter(const int *__restri
     slot_of[p] = slot;
 }
 
-// The same routing in one workgroup and one launch, for calls of up to
-// kRoute1Pairs pairs and kRoute1Experts experts (decode batches): counts,
-// ranks and offsets in LDS, then the scatter, the active experts and the
-// batches, written as the three-launch path writes them. Each small launch
-// costs a few microseconds of dependent latency; this saves two.
-constexpr int kRoute1Pairs = 512;
-constexpr int kRoute1Experts = 4096;
+// The same routing in one workgroup and one launch (moe_route1), for calls
+// of up to kRoute1Pairs pairs and kRoute1Experts experts (decode batches).
+// Each small launch costs a few microseconds of dependent latency; this
+// saves two.
 __global__ __launch_bounds__(kScanThreads) void k_moe_route1(const int *__restrict__ ids,
                                                              const float *__restrict__ wts,
                                                              int n_pairs, int k, int n_expert,
@@ -194,56 +152,11 @@ __global__ __launch_bounds__(kScanThreads) void k_moe_route1(const int *__restri
                                                              int *__restrict__ n_act,
                                                              MfgBatch *__restrict__ bat,
                                                              int *__restrict__ n_bat, int bw) {
-    extern __shared__ int sh[];  // base[n_expert], flags[n_expert]
+    extern __shared__ int sh[];  // 2 n_expert
     __shared__ int ep[kRoute1Pairs];
     __shared__ int part[kScanThreads];
-    int *base = sh, *flags = sh + n_expert;
-    const int tid = threadIdx.x;
-    for (int x = tid; x < n_expert; x += kScanThreads) base[x] = 0;
-    int e = -1;
-    if (tid < n_pairs) {
-        const int id = ids[tid];
-        if (wts[tid] != 0.0f && id >= 0 && id < n_expert) e = id;
-    }
-    if (tid < kRoute1Pairs) ep[tid] = e;
-    __syncthreads();
-    // rank: valid pairs of the same expert before this one (pair order)
-    int r = 0;
-    if (e >= 0) {
-        atomicAdd(&base[e], 1);
-        for (int q = 0; q < tid; q++) r += ep[q] == e ? 1 : 0;
-    }
-    __syncthreads();
-    const int total = scan_inplace(base, (size_t)n_expert, part);
-    for (int x = tid; x < n_expert; x += kScanThreads) off[x] = base[x];
-    if (tid == 0) off[n_expert] = total;
-    if (tid < n_pairs) {
-        const int slot = e >= 0 ? base[e] + r : -1;
-        if (e >= 0) slot_tok[slot] = tid / k;
-        slot_of[tid] = slot;
-    }
-    auto count = [&](int x) { return (x + 1 < n_expert ? base[x + 1] : total) - base[x]; };
-    // active experts: positions from a scan of the 0/1 flags
-    for (int x = tid; x < n_expert; x += kScanThreads) flags[x] = count(x) > 0 ? 1 : 0;
-    __syncthreads();
-    const int na = scan_inplace(flags, (size_t)n_expert, part);
-    for (int x = tid; x < n_expert; x += kScanThreads) {
-        const int next = x + 1 < n_expert ? flags[x + 1] : na;
-        if (next != flags[x]) act[flags[x]] = x;
-    }
-    if (tid == 0) *n_act = na;
-    if (!bat) return;
-    __syncthreads();
-    // batches: positions from a scan of ceil(count / bw)
-    for (int x = tid; x < n_expert; x += kScanThreads) flags[x] = (count(x) + bw - 1) / bw;
-    __syncthreads();
-    const int nb = scan_inplace(flags, (size_t)n_expert, part);
-    for (int x = tid; x < n_expert; x += kScanThreads) {
-        const int c = count(x);
-        for (int f = 0, j = flags[x]; f < c; f += bw, j++)
-            bat[j] = MfgBatch{base[x] + f, c - f < bw ? c - f : bw, x, 0};
-    }
-    if (tid == 0) *n_bat = nb;
+    moe_route1(ids, wts, n_pairs, k, n_expert, off, slot_tok, slot_of, act, n_act, bat, n_bat, bw,
+               sh, ep, part);
 }
 
 // Workspace of launch_moe_route: hist (n_expert x blocks), rank (one per
@@ -879,19 +792,26 @@ static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
     float *yd = reinterpret_cast<float *>(take(P * n_embd * 4));
     const bool fused1 = moe_fused_fits(dt_gu, dt_d, n_tok, k, n_embd, n_ff, gu_stride, d_stride);
     const bool mfma = !fused1 && moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff) &&
-                      n_tok >= kMoeMfmaMinTok && gu_stride <= 0xFFFFFFFFu &&
-                      d_stride <= 0xFFFFFFFFu;
+                      moe_mfma_fits((int)P, n_embd, n_ff) && n_tok >= kMoeMfmaMinTok &&
+                      gu_stride <= 0xFFFFFFFFu && d_stride <= 0xFFFFFFFFu;
     if (mfma) {
         uint8_t *mscratch = take(moe_mfma_scratch_bytes((int)P, n_expert, n_embd, n_ff));
         MfgBatch *bat = reinterpret_cast<MfgBatch *>(mscratch);
         const int bw = mfg_width((int)P, n_expert);
         int *n_bat = reinterpret_cast<int *>(mscratch + mfg_batch_bytes((int)P, n_expert, bw) - 256);
-        hipError_t e = launch_moe_route(ids, wts, (int)P, k, n_expert, route_work, off, slot_tok,
-                                        slot_of, act, n_act, bat, n_bat, bw, s);
-        if (e != hipSuccess) return e;
-        if ((e = launch_moe_mfma(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x, slot_tok,
-                                 bat, n_bat, (int)P, n_expert, hg, hu, yd, mscratch, n_embd, n_ff,
-                                 clamp, s)) != hipSuccess)
+        hipError_t e;
+        // up to kRoute1Pairs pairs the routing runs inside the route's first
+        // launch, beside the x image
+        const bool route1 = P <= (size_t)kRoute1Pairs && n_expert <= kRoute1Experts;
+        const MoeRoute1Args ra{ids, wts, (int)P, k, n_expert, off, slot_tok, slot_of, act, n_act};
+        if (!route1 && (e = launch_moe_route(ids, wts, (int)P, k, n_expert, route_work, off,
+                                             slot_tok, slot_of, act, n_act, bat, n_bat, bw, s)) !=
+                           hipSuccess)
+            return e;
+        if ((e = launch_moe_mfma(dt_gu, dt_d, gate, up, down, gu_stride, d_stride, x, n_tok,
+                                 route1 ? &ra : nullptr, off, slot_tok, bat, n_bat, (int)P,
+                                 n_expert, hg, hu, yd, mscratch, n_embd, n_ff, clamp, s)) !=
+            hipSuccess)
             return e;
         return launch_moe_accumulate(out, yd, wts, slot_of, n_tok, k, n_embd, s);
     }
