@@ -111,21 +111,26 @@ struct MQ4K {
     __device__ static void step(const W &w, int q, const uint4 (&x)[4][NT], const uint4 (&xl)[4][NT],
                                 f32x4 (&acc)[NT]) {
         const float d = f16_to_f32(w.hdr.x & 0xFFFFu), dmin = f16_to_f32(w.hdr.x >> 16);
-        // (sc, m) of sub-blocks 2q and 2q + 1 (q4_k_scale_min, dequant/mod.rs:48-58)
+        // (sc, m) of sub-blocks 2q and 2q + 1 (q4_k_scale_min,
+        // dequant/mod.rs:48-58), all four bytes of a word at once: sub-block
+        // j < 4 has sc = s0[j] & 63, m = s1[j] & 63; j >= 4 has sc =
+        // s2[j - 4] & 15 | (s0[j - 4] >> 6) << 4, m = s2[j - 4] >> 4 |
+        // (s1[j - 4] >> 6) << 4. Lane group q takes bytes 2 (q & 1) and
+        // 2 (q & 1) + 1 of the low (q < 2) or high words, each paired with
+        // 0x64 by v_perm_b32 (the f16 1024 + v, exact) less 1024.
+        // (masks and selectors as arithmetic: a conditional here became a
+        // branch per tile)
         const uint32_t s0 = w.hdr.y, s1 = w.hdr.z, s2 = w.hdr.w;
-        uint32_t sc[2], m[2];
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int jj = 2 * q + u;
-            const uint32_t sh = 8u * (uint32_t)(jj & 3);
-            const uint32_t lo_sc = (s0 >> sh) & 63u, lo_m = (s1 >> sh) & 63u;
-            const uint32_t b2 = (s2 >> sh) & 0xFFu;
-            const uint32_t hi_sc = (b2 & 15u) | (((s0 >> sh) >> 6) & 3u) << 4;
-            const uint32_t hi_m = (b2 >> 4) | (((s1 >> sh) >> 6) & 3u) << 4;
-            sc[u] = jj < 4 ? lo_sc : hi_sc;
-            m[u] = jj < 4 ? lo_m : hi_m;
-        }
-        const _Float16 sl = (_Float16)(float)sc[0], sh = (_Float16)(float)sc[1];
+        const uint32_t hm = 0u - (uint32_t)(q >> 1);  // all ones for q >= 2
+        const uint32_t sc4 = (((s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)) & hm) |
+                             (s0 & 0x3F3F3F3Fu & ~hm);
+        const uint32_t m4 = ((((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)) & hm) |
+                            (s1 & 0x3F3F3F3Fu & ~hm);
+        const uint32_t sel = 0x04010400u + (uint32_t)(q & 1) * 0x00020002u;
+        const f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const f16x2 scp = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, sc4, sel)) - k1024;
+        const f16x2 mp = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, m4, sel)) - k1024;
+        const _Float16 sl = scp[0], sh = scp[1];
         const f16x2 zero = {(_Float16)0.0f, (_Float16)0.0f};
         const f16x2 ssl = {sl, sl}, ssh = {sh, sh};
         f16x8 b[4];
@@ -133,7 +138,7 @@ struct MQ4K {
         b[1] = dequant_q4x8_f16(w.qs.x, w.qs.y, true, ssh, zero);
         b[2] = dequant_q4x8_f16(w.qs.z, w.qs.w, false, ssl, zero);
         b[3] = dequant_q4x8_f16(w.qs.z, w.qs.w, true, ssh, zero);
-        const _Float16 ml = (_Float16)(float)m[0], mh = (_Float16)(float)m[1];
+        const _Float16 ml = mp[0], mh = mp[1];
         const f16x8 bml = {ml, ml, ml, ml, ml, ml, ml, ml}, bmh = {mh, mh, mh, mh, mh, mh, mh, mh};
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
