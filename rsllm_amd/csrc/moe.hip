@@ -8,9 +8,10 @@
 // re-reading each selected expert's weights once per token. Here the
 // (token, slot) pairs are grouped by expert on the device, and each expert's
 // gate/up and down matrices are streamed once per batch of up to 4 of its
-// tokens (grouped GEMV, gemv.hip; for Q4_K, Q6_K and Q8_0 experts from
-// kMoeMfmaMinTok tokens, batches of up to 8 or 16 on the matrix cores
-// instead, launch_moe_mfma in gemv_mfma.hip, steps 2-6 there):
+// tokens (grouped GEMV, gemv.hip; for Q4_K, Q6_K and Q8_0 experts whenever
+// the fused pair does not take the call in one go, batches of up to 8 or 16
+// on the matrix cores instead, launch_moe_mfma in gemv_mfma.hip, steps 2-6
+// there):
 //   1. routing (k_moe_hist, k_moe_scan, k_moe_scatter, any number of
 //      pairs): slots sorted by expert (ties in (t, i) order), per-expert
 //      offsets, slot -> token, (t, i) -> slot, the list of active experts;
@@ -755,14 +756,14 @@ size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_
     return moe_pass_bytes(dt_gu, dt_d, moe_chunk_tokens(n_tok, k), k, n_expert, n_embd, n_ff);
 }
 
-// Calls the fused pair does not take in one go run, from this many tokens,
-// grouped by expert on the matrix cores (formats moe_mfma_supported takes):
-// each expert's weights are streamed once per batch of up to 16 of its
-// slots, where the fused pair over token chunks streams them once per chunk
-// that routes to the expert. C3 (64 experts, top-8) on MI355X: 411 vs 401 us
-// at 8 tokens, 537 vs 741 us at 16, 596 vs 1492 us at 32; below 8 tokens the
-// chunks are faster (276 vs 226 us at 4).
-constexpr int kMoeMfmaMinTok = 8;
+// Calls the fused pair does not take in one go run grouped by expert on the
+// matrix cores (formats moe_mfma_supported takes): each expert's weights are
+// streamed once per batch of up to 8 or 16 of its slots, where the fused
+// pair over token chunks streams them once per chunk that routes to the
+// expert. C3 (64 experts, top-8) on MI355X, grouped against chunks: 158 vs
+// 187 us at 4 tokens, 204 vs 272 us at 6, 225 vs 335 us at 7 (one process,
+// one box); 8 tokens and more were already grouped.
+constexpr int kMoeMfmaMinTok = 1;
 
 // One pass over n_tok tokens (n_tok * k <= kMoeMaxPairs).
 static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,

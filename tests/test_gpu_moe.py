@@ -182,9 +182,9 @@ def test_moe_fused_rows_spanning_columns(oracle, hip, dt_gu, dt_d, n_embd, n_ff,
 @pytest.mark.parametrize("n_tok,k", [(40, 2), (5, 8), (9, 8)])
 def test_moe_grouped_many_tokens(oracle, hip, dt_gu, dt_d, n_tok, k):
     """Calls the fused pair does not take in one go run grouped by expert:
-    on the matrix cores for Q4_K experts from 8 tokens (each expert's slots
-    in batches of up to 16), through the fused pair over token chunks or the
-    int8-limb grouped GEMV otherwise. Every token's first pick is expert
+    on the matrix cores for Q4_K, Q6_K and Q8_0 experts (each expert's slots
+    in batches of up to 8 or 16), through the fused pair over token chunks or
+    the int8-limb grouped GEMV otherwise. Every token's first pick is expert
     0 (40 slots: three batches, the last partial), token 1 picks one expert
     twice and one slot has weight 0."""
     n_embd, n_ff, n_expert = 1024, 1024, 9
