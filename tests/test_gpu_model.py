@@ -97,7 +97,7 @@ def mapped(tmp_path_factory):
 
 def prepared_reference(hip, arr, dtype, in_dim):
     import torch
-    raw = torch.from_numpy(np.ascontiguousarray(arr)).cuda()
+    raw = torch.from_numpy(np.array(arr, copy=True)).cuda()  # a writable copy (arr may be a read-only view)
     out = torch.empty_like(raw)
     hip.prepare_weights_dev(out.data_ptr(), raw.data_ptr(), raw.numel(), dtype, in_dim,
                             torch.cuda.current_stream().cuda_stream)
