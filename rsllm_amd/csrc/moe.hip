@@ -756,14 +756,17 @@ size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_
     return moe_pass_bytes(dt_gu, dt_d, moe_chunk_tokens(n_tok, k), k, n_expert, n_embd, n_ff);
 }
 
-// Calls the fused pair does not take in one go run grouped by expert on the
-// matrix cores (formats moe_mfma_supported takes): each expert's weights are
-// streamed once per batch of up to 8 or 16 of its slots, where the fused
-// pair over token chunks streams them once per chunk that routes to the
-// expert. C3 (64 experts, top-8) on MI355X, grouped against chunks: 158 vs
-// 187 us at 4 tokens, 204 vs 272 us at 6, 225 vs 335 us at 7 (one process,
-// one box); 8 tokens and more were already grouped.
+// Calls of more than kMoeFusedMfmaPairs pairs, and those the fused pair does
+// not take in one go, run grouped by expert on the matrix cores (formats
+// moe_mfma_supported takes): each expert's weights are streamed once per
+// batch of up to 8 or 16 of its slots, where the fused pair over token
+// chunks streams them once per chunk that routes to the expert. C3 (64
+// experts, top-8) on MI355X, grouped against the fused pair: 66 vs 54 us at
+// 1 token, 104 vs 96 us at 2, 136 vs 143 us at 3; against the fused pair's
+// token chunks 158 vs 187 us at 4, 204 vs 272 us at 6, 225 vs 335 us at 7
+// (one process, one box each).
 constexpr int kMoeMfmaMinTok = 1;
+constexpr size_t kMoeFusedMfmaPairs = 16;
 
 // One pass over n_tok tokens (n_tok * k <= kMoeMaxPairs).
 static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
@@ -791,10 +794,12 @@ static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
     const size_t xq2_bytes = gemv_scratch_bytes(dt_d, (int)P, n_ff);
     uint8_t *xq2 = take(xq2_bytes);
     float *yd = reinterpret_cast<float *>(take(P * n_embd * 4));
-    const bool fused1 = moe_fused_fits(dt_gu, dt_d, n_tok, k, n_embd, n_ff, gu_stride, d_stride);
-    const bool mfma = !fused1 && moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff) &&
-                      moe_mfma_fits((int)P, n_embd, n_ff) && n_tok >= kMoeMfmaMinTok &&
-                      gu_stride <= 0xFFFFFFFFu && d_stride <= 0xFFFFFFFFu;
+    const bool mfma_ok = moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff) &&
+                         moe_mfma_fits((int)P, n_embd, n_ff) && n_tok >= kMoeMfmaMinTok &&
+                         gu_stride <= 0xFFFFFFFFu && d_stride <= 0xFFFFFFFFu;
+    const bool fused1 = (!mfma_ok || P <= kMoeFusedMfmaPairs) &&
+                        moe_fused_fits(dt_gu, dt_d, n_tok, k, n_embd, n_ff, gu_stride, d_stride);
+    const bool mfma = !fused1 && mfma_ok;
     if (mfma) {
         uint8_t *mscratch = take(moe_mfma_scratch_bytes((int)P, n_expert, n_embd, n_ff));
         MfgBatch *bat = reinterpret_cast<MfgBatch *>(mscratch);
