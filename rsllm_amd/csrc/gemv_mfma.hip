@@ -485,9 +485,9 @@ __global__ __launch_bounds__(kMfxThreads) void k_mf_x(const float *__restrict__ 
 // ---- GEMV ----------------------------------------------------------------------------
 // One workgroup's 16 * RT rows from row0 against the n_tok (<= 16 * NT)
 // token columns of xh (two planes of plane_bytes each), y[t * y_stride + o];
-// red: NK * RT * NT * 64 f32x4 of LDS. ROWX (NT = 1): a per-row image, the
-// lane's column at byte xcol of each plane, and lanes 0..15 hold their
-// column's unscale in usc (unscale unused).
+// red: NK * RT * NT * 64 f32x4 of LDS. ROWX (NT = 1): a per-row image (a
+// piece's hi and lo 16 bytes side by side), the lane's row at byte xcol,
+// and lanes 0..15 hold their column's unscale in usc (unscale unused).
 template <class F, int NT, int NK, int RT, bool ROWX = false>
 __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t w_bytes,
                                         const _Float16 *__restrict__ xh, uint32_t plane_bytes,
@@ -519,9 +519,9 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 if (ROWX) {
-                    const uint32_t o = xcol + (uint32_t)(((s * 4 + j) * 4 + q) * 16);
+                    const uint32_t o = xcol + (uint32_t)(((s * 4 + j) * 4 + q) * 32);
                     xr[j][nt] = bload16(rx, o, 0);
-                    lr[j][nt] = bload16(rx, o + plane_bytes, 0);
+                    lr[j][nt] = bload16(rx, o + 16u, 0);
                     continue;
                 }
                 // image columns past ntp (ntp = 8): zeros, no access
@@ -704,9 +704,10 @@ template <class F, int NW = 4, int ROWS = kMfsRows> struct MfsGeo {
 // lanes of A rows 0..7 read the hi plane of tokens 0..7, lanes of rows 8..15
 // the lo plane. NW wavefronts (64 NW threads) split each chunk's 8 steps,
 // 8 / NW each, for every row tile. smem: MfsGeo<F, NW, ROWS>::LDS bytes.
-// ROWX (NT = 1): a per-row image, the lane's column (r16 & 7 packed, else
-// r16) at byte xcol of each plane, and lanes 0..15 hold their column's
-// unscale in usc (unscale unused).
+// ROWX (NT = 1): a per-row image (a piece's hi and lo 16 bytes side by
+// side), the row of the lane's column (r16 & 7 packed, else r16) at byte
+// xcol, and lanes 0..15 hold their column's unscale in usc (unscale
+// unused).
 template <class F, int NT, bool PACK = false, int NW = 4, int ROWS = kMfsRows, bool ROWX = false>
 __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
                                          const _Float16 *__restrict__ xh, uint32_t plane_bytes,
@@ -770,12 +771,12 @@ __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
                     if (ROWX) {
-                        const uint32_t o = xcol + (uint32_t)(((st * 4 + j) * 4 + q) * 16);
+                        const uint32_t o = xcol + (uint32_t)(((st * 4 + j) * 4 + q) * 32);
                         if (PACK) {
-                            xr[u][j][nt] = bload16(rx, o + (r16 >= 8 ? plane_bytes : 0u), 0);
+                            xr[u][j][nt] = bload16(rx, o + (r16 >= 8 ? 16u : 0u), 0);
                         } else {
                             xr[u][j][nt] = bload16(rx, o, 0);
-                            lr[u][j][nt] = bload16(rx, o + plane_bytes, 0);
+                            lr[u][j][nt] = bload16(rx, o + 16u, 0);
                         }
                         continue;
                     }
@@ -1118,11 +1119,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfo(const uint8_t *__restrict_
 // that expert's rows, so each expert's weights are streamed once per bw of
 // its slots. The activation images hold one row per x row (gate/up) or per
 // slot (down), not per batch column: row r's 8-element pieces in MFMA
-// operand order, piece ((s * 4 + j) * 4 + q) at halves r * in_dim + 8 *
-// piece of the hi plane, the lo plane n_rows * in_dim halves later, scaled
-// by 2^e_r; unscale[r] = 2^-e_r. Column c of batch b reads row
-// tok[first + c] (gate/up) or first + c (down). A row is written once
-// however many batches read it, by one workgroup, in whole cache lines.
+// operand order, scaled by 2^e_r, piece p = ((s * 4 + j) * 4 + q) as its hi
+// 16 bytes at byte 4 r in_dim + 32 p and its lo 16 bytes right after (a
+// lane group's hi and lo pieces of one MFMA share a 128-byte line);
+// unscale[r] = 2^-e_r. Column c of batch b reads row tok[first + c]
+// (gate/up) or first + c (down). A row is written once however many
+// batches read it, by one workgroup, in whole cache lines.
 
 // One token column of an ntp-wide activation image (the k_mf_x conversion,
 // one workgroup of TH threads, the row read once when it fits in
@@ -1188,7 +1190,7 @@ __device__ __forceinline__ void mf_x_column(V val4, int in_dim, int t, _Float16 
 template <class F, bool SWIGLU, int TH>
 __device__ __forceinline__ void mfg_row(const float *__restrict__ x, const float *__restrict__ hu,
                                         int r, float clamp, _Float16 *__restrict__ xh,
-                                        float *__restrict__ unscale, int in_dim, int n_alloc) {
+                                        float *__restrict__ unscale, int in_dim) {
     const float *xt = x + (size_t)r * in_dim;
     const float *ut = hu + (SWIGLU ? (size_t)r * in_dim : 0);
     auto val4 = [&](int i) {
@@ -1200,8 +1202,9 @@ __device__ __forceinline__ void mfg_row(const float *__restrict__ x, const float
         }
         return v;
     };
-    mf_x_column<F, TH>(val4, in_dim, 0, xh + (size_t)r * in_dim, unscale + r, 1,
-                       (size_t)n_alloc * in_dim);
+    // hi of piece p at halves 16 p, lo 8 halves later: two "columns" per
+    // piece with the lo plane 8 halves after the hi one
+    mf_x_column<F, TH>(val4, in_dim, 0, xh + (size_t)r * 2 * in_dim, unscale + r, 2, 8);
 }
 
 // The SwiGLU image of the down projection: one workgroup per slot.
@@ -1210,11 +1213,10 @@ __global__ __launch_bounds__(TH) void k_mfg_xs(const float *__restrict__ hg,
                                                const float *__restrict__ hu,
                                                const int *__restrict__ n_rows, float clamp,
                                                _Float16 *__restrict__ xh,
-                                               float *__restrict__ unscale, int in_dim,
-                                               int n_alloc) {
+                                               float *__restrict__ unscale, int in_dim) {
     const int r = blockIdx.x;
     if (r >= *n_rows) return;
-    mfg_row<F, true, TH>(hg, hu, r, clamp, xh, unscale, in_dim, n_alloc);
+    mfg_row<F, true, TH>(hg, hu, r, clamp, xh, unscale, in_dim);
 }
 
 // The first launch of the route: workgroup 0 runs the routing (when `route`;
@@ -1225,7 +1227,7 @@ template <class F>
 __global__ __launch_bounds__(kScanThreads) void k_mfg_route_x(MoeRoute1Args ra, MfgBatch *bat,
                                                               int *n_bat, int bw, int route,
                                                               const float *__restrict__ x,
-                                                              int n_tok, _Float16 *__restrict__ xh,
+                                                              _Float16 *__restrict__ xh,
                                                               float *__restrict__ unscale,
                                                               int in_dim) {
     extern __shared__ int sh[];  // routing: 2 n_expert ints
@@ -1237,7 +1239,7 @@ __global__ __launch_bounds__(kScanThreads) void k_mfg_route_x(MoeRoute1Args ra, 
         return;
     }
     mfg_row<F, false, kScanThreads>(x, nullptr, (int)blockIdx.x - (route ? 1 : 0), 0.f, xh, unscale,
-                                    in_dim, n_tok);
+                                    in_dim);
 }
 
 // ---- grouped LoRA-down on the matrix cores ----------------------------------------
@@ -1285,7 +1287,7 @@ __device__ __forceinline__ void mfg_column(const MfgBatch &bt, const int *__rest
                                            uint32_t &xcol, float &usc) {
     const int slot = bt.first + (c < bt.count ? c : 0);
     const int row = tok ? tok[slot] : slot;
-    xcol = (uint32_t)row * (uint32_t)in_dim * 2u;
+    xcol = (uint32_t)row * (uint32_t)in_dim * 4u;
     usc = unscale[row];
 }
 
@@ -1865,12 +1867,11 @@ static hipError_t mfg_swiglu_image(const float *hg, const float *hu, const int *
     // thread), 512 up to 8192, else kMfxThreads
     const dim3 g((unsigned)n_alloc);
     if (in_dim <= 2048)
-        k_mfg_xs<F, 256><<<g, 256, 0, s>>>(hg, hu, n_rows, clamp, xh, us, in_dim, n_alloc);
+        k_mfg_xs<F, 256><<<g, 256, 0, s>>>(hg, hu, n_rows, clamp, xh, us, in_dim);
     else if (in_dim <= 8192)
-        k_mfg_xs<F, 512><<<g, 512, 0, s>>>(hg, hu, n_rows, clamp, xh, us, in_dim, n_alloc);
+        k_mfg_xs<F, 512><<<g, 512, 0, s>>>(hg, hu, n_rows, clamp, xh, us, in_dim);
     else
-        k_mfg_xs<F, kMfxThreads><<<g, kMfxThreads, 0, s>>>(hg, hu, n_rows, clamp, xh, us, in_dim,
-                                                         n_alloc);
+        k_mfg_xs<F, kMfxThreads><<<g, kMfxThreads, 0, s>>>(hg, hu, n_rows, clamp, xh, us, in_dim);
     return hipGetLastError();
 }
 
@@ -1903,8 +1904,7 @@ static hipError_t mfg_route_x_dt(uint32_t dt, const MoeRoute1Args *ra, MfgBatch 
     const unsigned grid = (unsigned)n_tok + (ra ? 1u : 0u);
     const size_t lds = ra ? (size_t)ra->n_expert * 8 : 0;
     MFG_DT(dt, (k_mfg_route_x<F><<<grid, kScanThreads, lds, s>>>(ra ? *ra : none, bat, n_bat, bw,
-                                                                 ra ? 1 : 0, x, n_tok, xh, us,
-                                                                 in_dim),
+                                                                 ra ? 1 : 0, x, xh, us, in_dim),
                 hipGetLastError()))
 }
 #undef MFG_DT
