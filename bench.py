@@ -10,7 +10,12 @@ copies (> 512 MB) that every launch streams its weights from HBM rather than
 the 256 MB Infinity Cache; steps rotate through the copies.
 
 value        = whole-job algorithmic bytes / wall time of the K timed steps
-               (bytes = packed weight bytes + x + y, per launch)
+               (bytes = packed weight bytes + x + y, per launch); before the W
+               warmup steps the GPU runs --spinup-ms (50) of 256 MB device
+               copies, and every other timed region gets 20 ms of them, so
+               timed regions of well under a millisecond measure the GPU's
+               steady state rather than its wake-up after host-side idle
+               time (on MI355X that ramp costs about 5% of a 20-step run)
 roofline     = the same bytes per launch / mean duration of the dominant kernel
                (at batch 1 the whole drop-in call is one kernel, k_gemv1, which
                quantises x in LDS), measured with one HIP-event pair around a
@@ -58,6 +63,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--spinup-ms", type=float, default=50.0,
+                    help="device copies before the warmup steps, so the timed steps see the "
+                         "GPU's steady state rather than its wake-up from idle")
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0 = auto)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
@@ -114,7 +122,7 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
                                   d_x.data_ptr(), d_x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
         for _ in range(3):
             call()
-        torch.cuda.synchronize()
+        _spinup(20)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
         for _ in range(iters):
@@ -321,10 +329,38 @@ def _progress(msg):
     print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
-def _time(fn, iters, stream):
-    """Mean microseconds per call over `iters` back-to-back calls, one HIP
-    event pair on the launch stream around the whole run."""
+SPINUP_COPY_BYTES = 256 << 20
+_spin_bufs = []
+
+
+def _spinup(ms):
+    """Keep the GPU busy for `ms` milliseconds of 256 MB device copies (HBM
+    traffic, outside any timed region), then wait for them. After the host
+    has left the GPU idle (weight synthesis, oracle checks) its first
+    milliseconds of work run slower than its steady state (measured on
+    MI355X: the first 40 C1 GEMVs after 1 s idle took 254 us each, the next
+    few hundred 11.9-12.3 us, against 11.4 us after a 20 ms copy spin); a
+    timed region of well under a millisecond would measure that ramp."""
     import torch
+    if ms <= 0:
+        return
+    if not _spin_bufs:
+        a = torch.empty(SPINUP_COPY_BYTES, dtype=torch.uint8, device="cuda")
+        _spin_bufs.extend([a, torch.empty_like(a)])
+    a, b = _spin_bufs
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(4):
+            b.copy_(a)
+        torch.cuda.synchronize()
+
+
+def _time(fn, iters, stream, spin_ms=20):
+    """Mean microseconds per call over `iters` back-to-back calls, one HIP
+    event pair on the launch stream around the whole run, after a spin-up
+    of `spin_ms` (_spinup)."""
+    import torch
+    _spinup(spin_ms)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     a.record(stream)
@@ -470,7 +506,7 @@ def batch_probe():
         reps = _rotating(prep)
         x = torch.from_numpy(synth.activations(n_tok, in_dim, seed=200 + si)).to(dev).reshape(-1)
         y = torch.empty(n_tok * out_dim, dtype=torch.float32, device=dev)
-        torch.cuda.synchronize()
+        _spinup(20)
         for i in range(TRACE_LAUNCHES):
             w = reps[i % len(reps)]
             B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
@@ -508,7 +544,7 @@ def gemv_probe():
         reps = _rotating(prep)
         x = torch.from_numpy(synth.activations(1, in_dim, seed=200 + si)).to(dev).reshape(-1)
         y = torch.empty(out_dim, dtype=torch.float32, device=dev)
-        torch.cuda.synchronize()
+        _spinup(20)
         for i in range(TRACE_LAUNCHES):
             w = reps[i % len(reps)]
             B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
@@ -520,7 +556,7 @@ def gemv_probe():
     for T, calls in PF_TRACE:
         x = torch.from_numpy(synth.bf16_activations(T, in_dim, seed=405).reshape(-1)).to(dev)
         y = torch.empty(T * out_dim, dtype=torch.float32, device=dev)
-        torch.cuda.synchronize()
+        _spinup(20)
         for _ in range(calls):
             B.matmul_q4k_bf16_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
                                   x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
@@ -1114,7 +1150,8 @@ def main():
     bytes_per_launch = [m[3].numel() + n_tok * (m[1] + m[0]) * 4 for m in mats]
     bytes_per_step = sum(bytes_per_launch)
 
-    # ---- warmup ----
+    # ---- spin-up (device copies, not steps), then warmup ----
+    _spinup(args.spinup_ms)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -1227,6 +1264,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "spinup_ms": args.spinup_ms,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
