@@ -178,7 +178,9 @@ __device__ __forceinline__ void q6x4_f16(uint32_t q6, f16x2 &w01, f16x2 &w23) {
 // only. So B = f16(sc (q - 32)) and B_lo = sc (q - 32) - B (one fused f16
 // multiply-add, exact, in {-1, 0, 1}); a step whose wavefront has any
 // |sc| > 64 adds x_hi * B_lo as a third MFMA per sub-step, which leaves out
-// only x_lo * B_lo (below 2^-22 of the term).
+// only x_lo * B_lo (below 2^-22 of the term). A step without such scales
+// builds 2^-15 B instead, with one FMA per two weights on subnormal codes
+// (the same products scaled by a power of two, so the same sums).
 struct MQ6K {
     struct W {
         uint4 ql, qh;
@@ -224,44 +226,77 @@ struct MQ6K {
                                   const uint4 (&xl)[4][NT], f32x4 (&acc)[NT]) {
         const float d = f16_to_f32(w.d);
         const int il = (int)(int8_t)(w.sl >> (8 * q)), ih = (int)(int8_t)(w.sh >> (8 * q));
-        const _Float16 scl = (_Float16)(float)il, sch = (_Float16)(float)ih;
         const bool wide = WIDE == 1 || (WIDE == 2 && __ballot(wide_lane(w, q)) != 0);
         // the high bit pairs sit at bits 2 (q >> 1) (low nibbles) and 4 + 2 (q >> 1)
         // (high nibbles) of each qh byte; one shift puts either pair at bits 4, 5
         const uint32_t shl = 2u * (uint32_t)(q >> 1), sup = 4u - shl;
         const uint32_t l[4] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w};
         const uint32_t hb[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
-        f16x8 a[4], b[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
+        // four 6-bit codes of MFMA j, word u (bytes in K order)
+        auto codes = [&](int j, int u) {
             const bool hi = j & 1;
-            const int p = 2 * (j >> 1);
-            f16x2 v[4];
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const uint32_t nib = hi ? (l[p + u] >> 4) & 0x0F0F0F0Fu : l[p + u] & 0x0F0F0F0Fu;
-                const uint32_t top = (hi ? hb[p + u] >> shl : hb[p + u] << sup) & 0x30303030u;
-                q6x4_f16(nib | top, v[2 * u], v[2 * u + 1]);
-            }
-            f16x8 r;
-            r[0] = v[0][0]; r[1] = v[0][1]; r[2] = v[1][0]; r[3] = v[1][1];
-            r[4] = v[2][0]; r[5] = v[2][1]; r[6] = v[3][0]; r[7] = v[3][1];
-            const _Float16 sc = hi ? sch : scl;
-            const f16x8 sv = {sc, sc, sc, sc, sc, sc, sc, sc};
-            a[j] = r;
-            b[j] = r * sv;
-        }
+            const int p = 2 * (j >> 1) + u;
+            const uint32_t nib = hi ? (l[p] >> 4) & 0x0F0F0F0Fu : l[p] & 0x0F0F0F0Fu;
+            const uint32_t top = (hi ? hb[p] >> shl : hb[p] << sup) & 0x30303030u;
+            return nib | top;
+        };
         f32x4 P[NT];
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            P[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < NT; nt++) P[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto mma = [&](const f16x8 (&b)[4]) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    P[nt] = mfma16x32(x[j][nt], b[j], P[nt]);
+                    if (!PACK) P[nt] = mfma16x32(xl[j][nt], b[j], P[nt]);
+                }
+        };
+        float dd = d;
+        if (!wide) {
+            // |sc| <= 64: B = 2^-15 sc (q - 32), exact, in one FMA per pair:
+            // v_perm_b32 zero-extends two codes to f16 bit patterns (the
+            // subnormals code * 2^-24), times sc * 2^9, plus -sc * 2^-10; the
+            // step's sum is scaled back by 2^15 with d
+            const _Float16 ml = (_Float16)((float)il * 512.0f), mh = (_Float16)((float)ih * 512.0f);
+            const _Float16 cl = (_Float16)((float)il * -0x1p-10f), ch = (_Float16)((float)ih * -0x1p-10f);
+            f16x8 b[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                P[nt] = mfma16x32(x[j][nt], b[j], P[nt]);
-                if (!PACK) P[nt] = mfma16x32(xl[j][nt], b[j], P[nt]);
+                const f16x2 m2 = (j & 1) ? f16x2{mh, mh} : f16x2{ml, ml};
+                const f16x2 c2 = (j & 1) ? f16x2{ch, ch} : f16x2{cl, cl};
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const uint32_t c = codes(j, u);
+                    const f16x2 t01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0u, c, 0x0c010c00u));
+                    const f16x2 t23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0u, c, 0x0c030c02u));
+                    const f16x2 w01 = __builtin_elementwise_fma(t01, m2, c2);
+                    const f16x2 w23 = __builtin_elementwise_fma(t23, m2, c2);
+                    b[j][4 * u] = w01[0];
+                    b[j][4 * u + 1] = w01[1];
+                    b[j][4 * u + 2] = w23[0];
+                    b[j][4 * u + 3] = w23[1];
+                }
             }
-        }
-        if (wide) {
+            mma(b);
+            dd = d * 32768.0f;
+        } else {
+            const _Float16 scl = (_Float16)(float)il, sch = (_Float16)(float)ih;
+            f16x8 a[4], b[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                f16x2 v[4];
+#pragma unroll
+                for (int u = 0; u < 2; u++) q6x4_f16(codes(j, u), v[2 * u], v[2 * u + 1]);
+                f16x8 r;
+                r[0] = v[0][0]; r[1] = v[0][1]; r[2] = v[1][0]; r[3] = v[1][1];
+                r[4] = v[2][0]; r[5] = v[2][1]; r[6] = v[3][0]; r[7] = v[3][1];
+                const _Float16 sc = (j & 1) ? sch : scl;
+                const f16x8 sv = {sc, sc, sc, sc, sc, sc, sc, sc};
+                a[j] = r;
+                b[j] = r * sv;
+            }
+            mma(b);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const _Float16 sc = (j & 1) ? sch : scl;
@@ -274,7 +309,7 @@ struct MQ6K {
 #pragma unroll
         for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[nt][i] = fmaf(d, P[nt][i], acc[nt][i]);
+            for (int i = 0; i < 4; i++) acc[nt][i] = fmaf(dd, P[nt][i], acc[nt][i]);
     }
 };
 
