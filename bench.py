@@ -460,6 +460,7 @@ def moe_probe(T):
     d_g, d_u, d_d = (torch.from_numpy(a).cuda() for a in (gate, up, down))
     x = torch.from_numpy(synth.activations(T, n_embd, 610 + T).reshape(-1)).cuda()
     y = torch.zeros(T * n_embd, dtype=torch.float32, device="cuda")
+    _spinup(20)
     for r in range(8):
         ids, wts = synth.moe_routing(T, n_expert, k, 620 + T + 1000 * r)
         d_i = torch.from_numpy(ids.reshape(-1)).cuda()
