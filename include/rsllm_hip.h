@@ -139,7 +139,7 @@ int rsllm_hip_matmul_quant_f32_dev(float *out, size_t out_len, const uint8_t *we
  * GPU shares its array and leaves its contents behind: calls that overlap in
  * time on one GPU (two streams, or two threads) race on it, so enqueue them
  * on one stream. */
-#define RSLLM_HIP_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+#define RSLLM_HIP_NOALLOC_SCRATCH_BYTES ((size_t)48 << 20)
 int rsllm_hip_matmul_quant_f32_dev_noalloc(float *out, size_t out_len, const uint8_t *weights,
                                            size_t weights_len, const float *x, size_t x_len,
                                            size_t n_tok, size_t in_dim, size_t out_dim,

@@ -376,7 +376,7 @@ def matmul_quant_f32_dev(out_ptr: int, out_len: int, w_ptr: int, w_len: int, x_p
                                               int(dtype), stream or None))
 
 
-NOALLOC_SCRATCH_BYTES = 32 << 20
+NOALLOC_SCRATCH_BYTES = 48 << 20
 
 
 def matmul_quant_f32_dev_noalloc(out_ptr: int, out_len: int, w_ptr: int, w_len: int, x_ptr: int,

@@ -295,6 +295,61 @@ __device__ __forceinline__ void p8_barrier_vm5() {
     asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// A GEMM workgroup's tile, K split and destination. A 3D grid (row tiles,
+// token tiles, S) gives every tile S K splits: split z >= 1 stores its sums
+// to slice z - 1 of `part` (n_tok x ld_out each), which k_prefill_sum adds
+// into `out` in split order. A 1D grid (tail_s > 0; used when the tiles
+// leave a last partial round of at most half the CUs) gives tiles 0 ..
+// n_full - 1 (row tile fastest) one workgroup each and each later tile
+// tail_s splits, split z of tail tile j at block n_full + j tail_s + z:
+// split 0 stores to `out`, split z >= 1 to compact slice (z - 1) n_tail + j
+// of `part` (kPfTok token rows of kPfRowsWg floats), which
+// k_prefill_sum_tail adds in split order. The sums of token t, row o go to
+// out[(t - t_org) ld + o - n_org].
+struct PfTile {
+    int n0, t0;  // first row, first token
+    int z, nz;   // K split, splits of this tile
+    float *out;
+    int ld, t_org, n_org;
+};
+__device__ __forceinline__ PfTile pf_tile(float *out, float *part, int n_tok, int ld_out, int rt,
+                                          int n_full, int tail_s) {
+    PfTile p;
+    if (tail_s == 0) {
+        p.n0 = blockIdx.x * kPfRowsWg;
+        p.t0 = blockIdx.y * kPfTok;
+        p.z = blockIdx.z;
+        p.nz = gridDim.z;
+        p.out = p.z > 0 ? part + (size_t)(p.z - 1) * n_tok * ld_out : out;
+        p.ld = ld_out;
+        p.t_org = p.n_org = 0;
+        return p;
+    }
+    const int b = blockIdx.x;
+    int tile = b;
+    p.z = 0;
+    p.nz = 1;
+    if (b >= n_full) {
+        const int j = (b - n_full) / tail_s;
+        tile = n_full + j;
+        p.z = b - n_full - j * tail_s;
+        p.nz = tail_s;
+    }
+    p.n0 = tile % rt * kPfRowsWg;
+    p.t0 = tile / rt * kPfTok;
+    p.out = out;
+    p.ld = ld_out;
+    p.t_org = p.n_org = 0;
+    if (p.z > 0) {
+        const int n_tail = ((int)gridDim.x - n_full) / tail_s;
+        p.out = part + ((size_t)(p.z - 1) * n_tail + (tile - n_full)) * (kPfTok * kPfRowsWg);
+        p.ld = kPfRowsWg;
+        p.t_org = p.t0;
+        p.n_org = p.n0;
+    }
+    return p;
+}
+
 // The end of an 8-wavefront workgroup (256 rows x 128 tokens, two K groups
 // holding partial sums of the same outputs): group kg keeps token tiles
 // 4 kg .. 4 kg + 3 and hands the other four to the partner wavefront (same
@@ -306,9 +361,9 @@ __device__ __forceinline__ void p8_barrier_vm5() {
 // *flag. Second pass: output o of row r is scaled by 2^(erow[r] - e_t) in
 // one step (erow: the workgroup's 256 row exponents in LDS).
 __device__ __forceinline__ void p8_epilogue(f4 (&acc)[8][4], uint8_t *smem, int kg, int wr,
-                                            int lane, int n0, int t0, float *out,
+                                            int lane, int n0, int t0, const PfTile &tile,
                                             const float *unscale, int n_tok, int out_dim,
-                                            int ld_out, const int *erow, int *flag) {
+                                            const int *erow, int *flag) {
     const int r16 = lane & 15, q = lane >> 4;
     p8_barrier_vm0();
     f4 *xch = reinterpret_cast<f4 *>(smem);
@@ -330,6 +385,8 @@ __device__ __forceinline__ void p8_epilogue(f4 (&acc)[8][4], uint8_t *smem, int 
         for (int i = 0; i < 16; i++) res[i >> 2][i & 3] = acc[4 + (i >> 2)][i & 3] + xch[xidx(0, i)];
     }
     const int ow = n0 + 64 * wr + 4 * q;
+    float *const out = tile.out;
+    const int ld_out = tile.ld;
     const bool vec = ((out_dim | ld_out) & 3) == 0 && ((uintptr_t)out & 15) == 0;
     bool bad = false;  // a stored value is inf or NaN
 #pragma unroll
@@ -337,7 +394,7 @@ __device__ __forceinline__ void p8_epilogue(f4 (&acc)[8][4], uint8_t *smem, int 
         const int t = t0 + 16 * (4 * kg + ml) + r16;
         if (t >= n_tok) continue;
         const float us = unscale[t];
-        float *orow = out + (size_t)t * ld_out;
+        float *orow = out + (size_t)(t - tile.t_org) * ld_out;
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) {
             const int o = ow + 16 * nt;
@@ -349,8 +406,9 @@ __device__ __forceinline__ void p8_epilogue(f4 (&acc)[8][4], uint8_t *smem, int 
 #pragma unroll
                 for (int i = 0; i < 4; i++) v[i] = ldexpf(res[ml][nt][i], erow[lr + i] + eu);
             }
+            const int oc = o - tile.n_org;  // column in the destination
             if (vec && o + 3 < out_dim) {
-                *reinterpret_cast<f4 *>(orow + o) = v;
+                *reinterpret_cast<f4 *>(orow + oc) = v;
                 if (!erow)
                     bad |= !(__builtin_isfinite(v[0]) && __builtin_isfinite(v[1]) &&
                              __builtin_isfinite(v[2]) && __builtin_isfinite(v[3]));
@@ -358,7 +416,7 @@ __device__ __forceinline__ void p8_epilogue(f4 (&acc)[8][4], uint8_t *smem, int 
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     if (o + i < out_dim) {
-                        orow[o + i] = v[i];
+                        orow[oc + i] = v[i];
                         if (!erow) bad |= !__builtin_isfinite(v[i]);
                     }
             }
@@ -381,16 +439,15 @@ __device__ __forceinline__ bool pf_again(const int *flag) {
 }
 
 //
-// K split (blockIdx.z of gridDim.z splits): split z covers super-blocks
-// [z nbt / S, (z + 1) nbt / S) of the nbt in a row and writes its sums to
-// `out` (z = 0) or to slice z - 1 of `part` (n_tok x ld_out each), which
-// k_prefill_sum then adds into `out` in split order.
+// K split: split z of a tile's S covers super-blocks [z nbt / S, (z + 1)
+// nbt / S) of the nbt in a row and stores its sums where pf_tile says.
 __global__ __launch_bounds__(512) void k_prefill_q4k_w8(const uint8_t *__restrict__ w_arg,
                                                         const _Float16 *__restrict__ xh_arg,
                                                         const float *__restrict__ unscale,
                                                         float *__restrict__ out_arg,
                                                         float *__restrict__ part, int n_tok,
-                                                        int in_dim, int out_dim, int ld_out) {
+                                                        int in_dim, int out_dim, int ld_out,
+                                                        int rt, int n_full, int tail_s) {
     __shared__ __align__(16) uint8_t smem[kP8Lds + kPfGuardBytes];
     // range guard: the workgroup's flag, its rows' exponents (after the
     // stages)
@@ -409,17 +466,17 @@ __global__ __launch_bounds__(512) void k_prefill_q4k_w8(const uint8_t *__restric
         const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int wr = wv & 3, kg = wv >> 2;
         const int r16 = lane & 15, q = lane >> 4;
-        const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
+        const PfTile tile = pf_tile(out_arg, part, n_tok, ld_out, rt, n_full, tail_s);
+        const int n0 = tile.n0, t0 = tile.t0;
         const int nbt = in_dim >> 8;  // super-blocks in a row
-        const int z = blockIdx.z, nz = gridDim.z;
+        const int z = tile.z, nz = tile.nz;
         const int kb0 = (int)((long)z * nbt / nz);
         const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;  // super-blocks of this split (>= 1)
         const int ns = 2 * nb;                                 // steps of one K group
-        // this K split's weights and activations, its output (split 0) or
-        // partial sums (the arguments stay unchanged for the second pass)
+        // this K split's weights and activations (the arguments stay
+        // unchanged for the second pass)
         const uint8_t *const w = w_arg + (size_t)kb0 * kQ4kBytes;
         const _Float16 *const xh = xh_arg + (size_t)kb0 * 256;
-        float *const out = z > 0 ? part + (size_t)(z - 1) * n_tok * ld_out : out_arg;
         uint8_t *const act = smem + kP8ActOff + 2 * kg * kP8Act;  // this group's two step buffers
         uint8_t *const scl = smem + kP8ScOff + kg * kPfRowsWg * 16;
         const uint32_t row_bytes = (uint32_t)nbt * (uint32_t)kQ4kBytes;
@@ -613,9 +670,9 @@ __global__ __launch_bounds__(512) void k_prefill_q4k_w8(const uint8_t *__restric
         };
         run(pass_c);
         if constexpr (!decltype(pass_c)::value)
-            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, nullptr, flag);
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, tile, unscale, n_tok, out_dim, nullptr, flag);
         else
-            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, erow_lds,
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, tile, unscale, n_tok, out_dim, erow_lds,
                         nullptr);
     };
     body(std::false_type{});
@@ -647,7 +704,8 @@ __global__ __launch_bounds__(512) void k_prefill_q8_w8(const uint8_t *__restrict
                                                        const float *__restrict__ unscale,
                                                        float *__restrict__ out_arg,
                                                        float *__restrict__ part, int n_tok,
-                                                       int in_dim, int out_dim, int ld_out) {
+                                                       int in_dim, int out_dim, int ld_out,
+                                                       int rt, int n_full, int tail_s) {
     __shared__ __align__(16) uint8_t smem[kQ8Lds + kPfGuardBytes];
     // range guard: the workgroup's flag, its rows' exponents (after the
     // stages)
@@ -666,17 +724,17 @@ __global__ __launch_bounds__(512) void k_prefill_q8_w8(const uint8_t *__restrict
         const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int wr = wv & 3, kg = wv >> 2;
         const int r16 = lane & 15, q = lane >> 4;
-        const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
+        const PfTile tile = pf_tile(out_arg, part, n_tok, ld_out, rt, n_full, tail_s);
+        const int n0 = tile.n0, t0 = tile.t0;
         const int nbt = in_dim >> 8;  // super-tiles in a row
-        const int z = blockIdx.z, nz = gridDim.z;
+        const int z = tile.z, nz = tile.nz;
         const int kb0 = (int)((long)z * nbt / nz);
         const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;
         const int ns = 2 * nb;
-        // this K split's weights and activations, its output (split 0) or
-        // partial sums (the arguments stay unchanged for the second pass)
+        // this K split's weights and activations (the arguments stay
+        // unchanged for the second pass)
         const uint8_t *const w = w_arg + (size_t)kb0 * 272;
         const _Float16 *const xh = xh_arg + (size_t)kb0 * 256;
-        float *const out = z > 0 ? part + (size_t)(z - 1) * n_tok * ld_out : out_arg;
         uint8_t *const stg = smem + 2 * kg * kQ8Stage;  // this group's two step buffers
         const uint32_t row_bytes = (uint32_t)nbt * 272u;
 
@@ -854,9 +912,9 @@ __global__ __launch_bounds__(512) void k_prefill_q8_w8(const uint8_t *__restrict
         };
         run(pass_c);
         if constexpr (!decltype(pass_c)::value)
-            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, nullptr, flag);
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, tile, unscale, n_tok, out_dim, nullptr, flag);
         else
-            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, erow_lds,
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, tile, unscale, n_tok, out_dim, erow_lds,
                         nullptr);
     };
     body(std::false_type{});
@@ -891,7 +949,8 @@ __global__ __launch_bounds__(512) void k_prefill_q6_w8(const uint8_t *__restrict
                                                        const float *__restrict__ unscale,
                                                        float *__restrict__ out_arg,
                                                        float *__restrict__ part, int n_tok,
-                                                       int in_dim, int out_dim, int ld_out) {
+                                                       int in_dim, int out_dim, int ld_out,
+                                                       int rt, int n_full, int tail_s) {
     __shared__ __align__(16) uint8_t smem[kQ6Lds + kPfGuardBytes];
     // range guard: the workgroup's flag, its rows' exponents (after the
     // stages)
@@ -910,16 +969,16 @@ __global__ __launch_bounds__(512) void k_prefill_q6_w8(const uint8_t *__restrict
         const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int wr = wv & 3, kg = wv >> 2;
         const int r16 = lane & 15, q = lane >> 4;
-        const int n0 = blockIdx.x * kPfRowsWg, t0 = blockIdx.y * kPfTok;
+        const PfTile tile = pf_tile(out_arg, part, n_tok, ld_out, rt, n_full, tail_s);
+        const int n0 = tile.n0, t0 = tile.t0;
         const int nbt = in_dim >> 8;  // blocks in a row (a multiple of 8)
-        const int z = blockIdx.z, nz = gridDim.z;
+        const int z = tile.z, nz = tile.nz;
         const int kb0 = (int)((long)z * nbt / nz);
         const int nb = (int)((long)(z + 1) * nbt / nz) - kb0;
         const int ns = 2 * nb;
-        // this K split's activations, its output (split 0) or partial sums
-        // (the arguments stay unchanged for the second pass)
+        // this K split's activations (the arguments stay unchanged for the
+        // second pass)
         const _Float16 *const xh = xh_arg + (size_t)kb0 * 256;
-        float *const out = z > 0 ? part + (size_t)(z - 1) * n_tok * ld_out : out_arg;
         uint8_t *const act = smem + kQ6ActOff + 2 * kg * kP8Act;  // this group's two step buffers
         uint8_t *const scl = smem + kQ6ScOff + kg * kPfRowsWg * 8;
         const uint32_t row_bytes = (uint32_t)(nbt >> 3) * 1680u;
@@ -1150,9 +1209,9 @@ __global__ __launch_bounds__(512) void k_prefill_q6_w8(const uint8_t *__restrict
         };
         run(pass_c);
         if constexpr (!decltype(pass_c)::value)
-            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, nullptr, flag);
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, tile, unscale, n_tok, out_dim, nullptr, flag);
         else
-            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, out, unscale, n_tok, out_dim, ld_out, erow_lds,
+            p8_epilogue(acc, smem, kg, wr, lane, n0, t0, tile, unscale, n_tok, out_dim, erow_lds,
                         nullptr);
     };
     body(std::false_type{});
@@ -1179,51 +1238,120 @@ __global__ __launch_bounds__(256) void k_prefill_sum(float *__restrict__ out,
     }
 }
 
-// K splits of a call: grids of fewer than 128 workgroups (one per CU, 256
-// CUs) split K into as many as keep the grid within one round of 256
-// workgroups (a partial second round costs more than the split gains), each
-// split keeping at least two super-blocks, at most 16 splits, and only where
-// the partial sums keep the whole workspace within the no-allocation entry
-// point's maximum (so a call that fits it without splitting still fits).
-// Calls that need more than one launch (32-bit offsets, below) are not split.
-static int prefill_splits(int n_tok, int in_dim, int out_dim) {
+// out[t][o] += the compact slices 1 .. nz - 1 of the tail tiles in split
+// order (block (i, j): float4s 256 i .. 256 i + 255 of tail tile j, a tile
+// being kPfTok token rows of kPfRowsWg floats; slice z - 1 of tile j at
+// part + ((z - 1) n_tail + j) kPfTok kPfRowsWg)
+__global__ __launch_bounds__(256) void k_prefill_sum_tail(float *__restrict__ out,
+                                                          const float *__restrict__ part,
+                                                          int n_tok, int out_dim, int ld_out,
+                                                          int rt, int n_full, int n_tail, int nz) {
+    constexpr int kTile = kPfTok * kPfRowsWg;
+    const int j = blockIdx.y, tile = n_full + j;
+    const int i4 = blockIdx.x * 256 + threadIdx.x;
+    const int tl = i4 / (kPfRowsWg / 4), oc = i4 % (kPfRowsWg / 4) * 4;
+    const int t = tile / rt * kPfTok + tl, o = tile % rt * kPfRowsWg + oc;
+    if (t >= n_tok || o >= out_dim) return;
+    const size_t slice = (size_t)n_tail * kTile;
+    const float *p = part + (size_t)j * kTile + tl * kPfRowsWg + oc;
+    float *y = out + (size_t)t * ld_out + o;
+    if (o + 3 < out_dim && (ld_out & 3) == 0 && ((uintptr_t)out & 15) == 0) {
+        f4 v = *reinterpret_cast<const f4 *>(y);
+        for (int z = 1; z < nz; z++) v += *reinterpret_cast<const f4 *>(p + (z - 1) * slice);
+        *reinterpret_cast<f4 *>(y) = v;
+    } else {
+        for (int i = 0; i < 4 && o + i < out_dim; i++) {
+            float v = y[i];
+            for (int z = 1; z < nz; z++) v += p[(z - 1) * slice + i];
+            y[i] = v;
+        }
+    }
+}
+
+// How a call's GEMM covers its tiles (256 rows x 128 tokens each, one
+// workgroup per CU, 256 CUs):
+// * grids of fewer than 128 workgroups split K into nz splits, as many as
+//   keep the grid within one round of 256 workgroups (a partial second round
+//   costs more than the split gains), each split keeping at least two
+//   super-blocks, at most 16;
+// * grids of more than one round whose last round holds R <= 128 tiles
+//   split those R tiles into tail_s splits each (tail_s R <= 256, the same
+//   limits), so the last round runs tail_s R shorter workgroups;
+// either only where the partial sums keep the whole workspace within the
+// no-allocation entry point's maximum (so a call that fits it without
+// splitting still fits). Calls that need more than one launch (32-bit
+// offsets, below) are not split.
+struct PfPlan {
+    int nz = 1;                  // K splits of every tile (3D grid)
+    int tail_s = 0;              // K splits of each tail tile (1D grid), or 0
+    int n_full = 0, n_tail = 0;  // whole tiles, tail tiles (tail_s > 0)
+};
+constexpr size_t kPfCUs = 256;
+static PfPlan prefill_plan(int n_tok, int in_dim, int out_dim) {
+    PfPlan p;
     const size_t rt = (size_t)(out_dim + kPfRowsWg - 1) / kPfRowsWg;
     const size_t tt = ((size_t)n_tok + kPfTok - 1) / kPfTok;
     const size_t grid = rt * tt, nbt = (size_t)in_dim / 256;
-    if (grid >= 128 || nbt < 4) return 1;
+    if (nbt < 4) return p;
     const size_t row_bytes = nbt * 272;  // the larger of Q8_0's and Q4_K's row bytes
-    if ((size_t)out_dim * row_bytes > UINT32_MAX || (size_t)n_tok * in_dim * 2 > INT32_MAX) return 1;
-    size_t nz = std::min<size_t>({256 / grid, nbt / 2, 16});
+    if ((size_t)out_dim * row_bytes > UINT32_MAX || (size_t)n_tok * in_dim * 2 > INT32_MAX) return p;
     const size_t base = ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16 + tt * kPfTok * 4;
-    while (nz > 1 && base + (nz - 1) * (size_t)n_tok * out_dim * 4 > RSLLM_HIP_NOALLOC_SCRATCH_BYTES) nz--;
-    return (int)nz;
+    if (grid < kPfCUs / 2) {
+        size_t nz = std::min<size_t>({kPfCUs / grid, nbt / 2, 16});
+        while (nz > 1 && base + (nz - 1) * (size_t)n_tok * out_dim * 4 > RSLLM_HIP_NOALLOC_SCRATCH_BYTES)
+            nz--;
+        p.nz = (int)nz;
+        return p;
+    }
+    const size_t r = grid % kPfCUs;
+    if (grid < kPfCUs || r == 0 || r > kPfCUs / 2) return p;
+    size_t s = std::min<size_t>({kPfCUs / r, nbt / 2, 16});
+    while (s > 1 && base + (s - 1) * r * kPfTok * kPfRowsWg * 4 > RSLLM_HIP_NOALLOC_SCRATCH_BYTES) s--;
+    if (s > 1) {
+        p.tail_s = (int)s;
+        p.n_tail = (int)r;
+        p.n_full = (int)(grid - r);
+    }
+    return p;
 }
 
 size_t prefill_scratch_bytes(int n_tok, int in_dim, int out_dim) {
     // f16 activations, one f32 unscale per token padded to whole 128-token
     // tiles (16-byte aligned), then the partial sums of splits 1 .. S - 1
     const size_t tiles = ((size_t)n_tok + kPfTok - 1) / kPfTok;
-    const size_t nz = (size_t)prefill_splits(n_tok, in_dim, out_dim);
-    return ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16 + tiles * kPfTok * 4 +
-           (nz - 1) * (size_t)n_tok * out_dim * 4;
+    const PfPlan p = prefill_plan(n_tok, in_dim, out_dim);
+    const size_t part = p.tail_s ? (size_t)(p.tail_s - 1) * p.n_tail * kPfTok * kPfRowsWg
+                                 : (size_t)(p.nz - 1) * n_tok * out_dim;
+    return ((size_t)n_tok * in_dim * 2 + 15) / 16 * 16 + tiles * kPfTok * 4 + part * 4;
 }
 
-// One GEMM launch on the pre-pass's image (nz K splits: partial sums in part)
+// One GEMM launch on the pre-pass's image (partial sums in part)
 static hipError_t prefill_gemm(uint32_t dtype, const uint8_t *w, const _Float16 *xh,
-                               const float *unscale, float *out, float *part, int nz, int n_tok,
-                               int in_dim, int out_dim, int ld_out, hipStream_t s) {
-    const dim3 grid((unsigned)((out_dim + kPfRowsWg - 1) / kPfRowsWg),
-                    (unsigned)((n_tok + kPfTok - 1) / kPfTok), (unsigned)nz);
+                               const float *unscale, float *out, float *part, const PfPlan &p,
+                               int n_tok, int in_dim, int out_dim, int ld_out, hipStream_t s) {
+    const dim3 grid = p.tail_s ? dim3((unsigned)(p.n_full + p.n_tail * p.tail_s))
+                               : dim3((unsigned)((out_dim + kPfRowsWg - 1) / kPfRowsWg),
+                                      (unsigned)((n_tok + kPfTok - 1) / kPfTok), (unsigned)p.nz);
+    const int rt = (out_dim + kPfRowsWg - 1) / kPfRowsWg;
     if (dtype == T_Q8_0)
-        k_prefill_q8_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out);
+        k_prefill_q8_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out,
+                                             rt, p.n_full, p.tail_s);
     else if (dtype == T_Q6_K)
-        k_prefill_q6_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out);
+        k_prefill_q6_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out,
+                                             rt, p.n_full, p.tail_s);
     else
-        k_prefill_q4k_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim, ld_out);
+        k_prefill_q4k_w8<<<grid, 512, 0, s>>>(w, xh, unscale, out, part, n_tok, in_dim, out_dim,
+                                              ld_out, rt, p.n_full, p.tail_s);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || nz == 1) return e;
+    if (e != hipSuccess) return e;
+    if (p.tail_s) {
+        k_prefill_sum_tail<<<dim3(kPfTok * kPfRowsWg / 4 / 256, (unsigned)p.n_tail), 256, 0, s>>>(
+            out, part, n_tok, out_dim, ld_out, rt, p.n_full, p.n_tail, p.tail_s);
+        return hipGetLastError();
+    }
+    if (p.nz == 1) return hipSuccess;
     const size_t n = (size_t)n_tok * out_dim;
-    k_prefill_sum<<<(unsigned)((n + 1023) / 1024), 256, 0, s>>>(out, part, n, nz - 1);
+    k_prefill_sum<<<(unsigned)((n + 1023) / 1024), 256, 0, s>>>(out, part, n, p.nz - 1);
     return hipGetLastError();
 }
 
@@ -1252,13 +1380,13 @@ static hipError_t prefill_run(uint32_t dtype, const uint8_t *w, const uint16_t *
         k_prefill_x<<<(unsigned)n_tok, 256, 0, s>>>(x_bf16, xh, unscale, in_dim);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int nz = prefill_splits(n_tok, in_dim, out_dim);
+    const PfPlan plan = prefill_plan(n_tok, in_dim, out_dim);
     for (size_t t0 = 0; t0 < (size_t)n_tok; t0 += toks_max) {
         const int nt = (int)std::min(toks_max, (size_t)n_tok - t0);
         for (size_t r0 = 0; r0 < (size_t)out_dim; r0 += rows_max) {
             const int nr = (int)std::min(rows_max, (size_t)out_dim - r0);
             e = prefill_gemm(dtype, w + r0 * row_bytes, xh + t0 * in_dim, unscale + t0,
-                             out + t0 * out_dim + r0, part, nz, nt, in_dim, nr, out_dim, s);
+                             out + t0 * out_dim + r0, part, plan, nt, in_dim, nr, out_dim, s);
             if (e != hipSuccess) return e;
         }
     }

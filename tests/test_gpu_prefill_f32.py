@@ -162,6 +162,28 @@ def test_prefill_f32_q6_k_gemm(oracle, hip, out_dim, in_dim, n_tok):
     check(oracle, got, w, x, tokens, G.Q6_K, n_tok, in_dim, out_dim, REL_TOL, "gemm")
 
 
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q8_0, G.Q6_K])
+@pytest.mark.parametrize("out_dim,in_dim,n_tok", [(4000, 2048, 2100), (2500, 2048, 4400)])
+def test_prefill_f32_tail_split(oracle, hip, dtype, out_dim, in_dim, n_tok):
+    """Grids of more than one round of 256 tiles whose last round holds at
+    most 128 tiles split those tiles' K (the others one workgroup each) and
+    add the compact partial sums in split order: 16 x 17 tiles (the last 16,
+    token tile 16 of 52 tokens on every row tile, the last row tile of 160
+    rows: 4 splits of 2 blocks), and 10 x 35 tiles (the last 94, from row
+    tile 6 of token tile 25 on, a 196-row last row tile, a 48-token last
+    token tile: 2 splits of 4 blocks). Repeated calls are bit-identical; the
+    checked tokens take both sides of every token-tile edge."""
+    w = synth.weight(dtype, out_dim, in_dim, seed=2900 + out_dim + int(dtype))
+    x = synth.activations(n_tok, in_dim, seed=2901 + n_tok).reshape(-1)
+    got = run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim)
+    again = run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    edges = np.arange(128, n_tok, 128)
+    tokens = np.unique(np.concatenate([[0, 1, n_tok - 1], edges - 1, edges,
+                                       np.linspace(0, n_tok - 1, 8).astype(int)]))
+    check(oracle, got, w, x, tokens, dtype, n_tok, in_dim, out_dim, REL_TOL, "gemm")
+
+
 @pytest.mark.parametrize("dtype", [G.Q6_K, G.Q8_0])
 def test_prefill_f32_special_blocks(oracle, hip, dtype):
     """The Q6_K and Q8_0 GEMMs on blocks with zero, subnormal and small

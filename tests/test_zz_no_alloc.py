@@ -17,12 +17,14 @@ from rsllm_amd.ggml import GgmlType as G
 # workspace: the matrix-core batched GEMV (f16 activation image) for 5..32
 # tokens of >= 1024 rows, the activation pre-pass + GEMV otherwise, and
 # above 32 tokens the prefill GEMM (f16 image, per-token scales and, on
-# small grids, the partial sums of its K splits: 8 and 4 splits here)
+# small grids, the partial sums of its K splits: 8 and 4 splits here; on a
+# grid of 272 tiles, the compact partial sums of its last 16 tiles' 2 splits)
 CALLS = [
     [(G.Q4_K, 4096, 4096, 24), (G.Q6_K, 1024, 2048, 12)],   # matrix cores, then smaller
     [(G.Q8_0, 512, 4096, 20), (G.Q4_K, 256, 1024, 11)],     # pre-pass path, then smaller
     [(G.Q6_K, 2048, 4096, 32), (G.Q2_K, 300, 512, 13)],     # mixed paths, then smaller
     [(G.Q6_K, 1024, 4096, 300), (G.Q8_0, 512, 2048, 40)],   # prefill GEMMs, then smaller
+    [(G.Q4_K, 4000, 1024, 2049), (G.Q8_0, 3000, 2048, 1100)],  # tail split, then K split
 ]
 
 
@@ -95,10 +97,10 @@ def test_noalloc_allocates_nothing(hip):
 
 
 def test_noalloc_rejects_workspace_above_the_maximum(hip):
-    # 32 tokens of a 600k-element Q8_0 row need a 38 MB f16 activation image;
+    # 32 tokens of a 1M-element Q8_0 row need a 64 MB f16 activation image;
     # validation and the size check run before any device work (placeholder
     # addresses, never dereferenced)
-    in_dim, out_dim, n_tok = 600_064, 1024, 32
+    in_dim, out_dim, n_tok = 1_000_192, 1024, 32
     w_len = out_dim * (in_dim // 32) * 34
     fake = 1 << 40
     with pytest.raises(hip.InvalidArgument, match="workspace"):
