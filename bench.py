@@ -32,10 +32,13 @@ prefill      = BASELINE.json configs[4] (C4): Q4_K weight (out, in) =
                (14336, 4096) times bf16 activations [T x 4096], T = 512 and
                2048, fp32 output, on the MFMA path; TFLOP/s = 2 T in out / the
                event-timed mean of a run of back-to-back calls (activation
-               pre-pass + GEMM), against the 2.5 PFLOP/s dense f16/bf16 MFMA
-               peak, with its own bounded CPU-oracle sample. The GEMM and
-               pre-pass durations come from the same kernel-trace pass as the
-               roofline, MFMA busy from one rocprofv3 --pmc pass.
+               pre-pass + GEMM), taken after 50 ms of the same call back to
+               back (the clocks' warm-up under sustained matrix-core load,
+               as a forward pass's back-to-back calls run), against the
+               2.5 PFLOP/s dense f16/bf16 MFMA peak, with its own bounded
+               CPU-oracle sample. The GEMM and pre-pass durations come from
+               the same kernel-trace pass as the roofline (after 25 ms of
+               warm-up calls), MFMA busy from one rocprofv3 --pmc pass.
 
 Output: ONE compact JSON line on stdout. Every prefill figure is a flat
 scalar member of "prefill"; the other configs are short rows in "extra".
@@ -120,9 +123,7 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
         def call():
             B.matmul_q4k_bf16_dev(d_y.data_ptr(), d_y.numel(), d_w.data_ptr(), d_w.numel(),
                                   d_x.data_ptr(), d_x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
-        for _ in range(3):
-            call()
-        _spinup(20)
+        _sustain(lambda i: call(), PF_SUSTAIN_MS)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
         for _ in range(iters):
@@ -165,7 +166,7 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
                                    d_x.data_ptr(), d_x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
         for i in range(3):
             call_f32(i)
-        us = _time(call_f32, iters, stream)
+        us = _time(call_f32, iters, stream, sustain_ms=PF_SUSTAIN_MS)
         tflops = 2.0 * T * in_dim * out_dim / (us * 1e-6) / 1e12
         bf = next(e for e in res["by_tokens"] if e["tokens"] == T)
         entry = {"tokens": T, "us_per_op": round(us, 2), "tflops": round(tflops, 1),
@@ -198,7 +199,7 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
                                   d_x.data_ptr(), d_x.numel(), T, n_in, n_out, G.Q4_K, sptr)
         for i in range(3):
             call_s(i)
-        us = _time(call_s, iters, stream)
+        us = _time(call_s, iters, stream, sustain_ms=PF_SUSTAIN_MS)
         tflops = 2.0 * T * n_in * n_out / (us * 1e-6) / 1e12
         entry = {"shape": f"{n_out}x{n_in}", "tokens": T, "us_per_op": round(us, 2),
                  "tflops": round(tflops, 1), "frac_of_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
@@ -233,7 +234,7 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
                                    d_x.data_ptr(), d_x.numel(), T, in_dim, out_dim, dt, sptr)
         for i in range(3):
             call_f(i)
-        us = _time(call_f, iters, stream)
+        us = _time(call_f, iters, stream, sustain_ms=PF_SUSTAIN_MS)
         tflops = 2.0 * T * in_dim * out_dim / (us * 1e-6) / 1e12
         entry = {"format": dt.name, "shape": f"{out_dim}x{in_dim}", "tokens": T,
                  "us_per_op": round(us, 2), "tflops": round(tflops, 1),
@@ -312,9 +313,7 @@ def bench_dense_f16(dev, stream, out_dim, in_dim, iters):
 
         def call(i):
             torch.nn.functional.linear(x, ws[i & 1])
-        for i in range(3):
-            call(i)
-        us = _time(call, iters, stream)
+        us = _time(call, iters, stream, sustain_ms=PF_SUSTAIN_MS)
         tf = 2.0 * T * in_dim * out_dim / (us * 1e-6) / 1e12
         res.append({"tokens": T, "us_per_op": round(us, 2), "tflops": round(tf, 1),
                     "frac_of_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
@@ -355,12 +354,36 @@ def _spinup(ms):
         torch.cuda.synchronize()
 
 
-def _time(fn, iters, stream, spin_ms=20):
+def _sustain(fn, ms):
+    """Run `fn` back to back for `ms` milliseconds of wall time (outside any
+    timed region), then wait for it. Under sustained matrix-core load the
+    GPU's clocks settle some 10-20 ms after a spell of other work (measured
+    on MI355X: the C4 prefill call at T = 2048 took 230-250 us over its first
+    50 calls after a 20 ms copy spin-up, then 222-224 us); prefill calls come
+    back to back in a forward pass, so the prefill figures are taken after
+    this warm-up on the timed call itself."""
+    import torch
+    t0, i = time.perf_counter(), 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(4):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
+PF_SUSTAIN_MS = 50
+
+
+def _time(fn, iters, stream, spin_ms=20, sustain_ms=0):
     """Mean microseconds per call over `iters` back-to-back calls, one HIP
     event pair on the launch stream around the whole run, after a spin-up
-    of `spin_ms` (_spinup)."""
+    of `spin_ms` (_spinup) or, with sustain_ms, `sustain_ms` of the call
+    itself (_sustain)."""
     import torch
-    _spinup(spin_ms)
+    if sustain_ms > 0:
+        _sustain(fn, sustain_ms)
+    else:
+        _spinup(spin_ms)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     a.record(stream)
@@ -416,11 +439,13 @@ def pmc_probe():
         del reps, prep
 
 
-def prefill_probe(T, fmt="Q4_K"):
+def prefill_probe(T, fmt="Q4_K", warm=True):
     """The C4 prefill call (Q4_K 14336x4096 weights, bf16 x [T x 4096]) five
     times, for rocprofv3 runs that count MFMA and VALU work per dispatch;
     with fmt Q6_K or Q8_0, the same shape in that format through the f32-x
-    call (weights in the device layout)."""
+    call (weights in the device layout). With `warm`, PF_PROBE_WARM[T] calls
+    (about 25 ms back to back, the clock warm-up of _sustain) come first:
+    a kernel trace's last five calls of each kernel are the measured ones."""
     import torch
     from rsllm_amd import backend as B
     from rsllm_amd import synth
@@ -428,18 +453,19 @@ def prefill_probe(T, fmt="Q4_K"):
     out_dim, in_dim = 14336, 4096
     sptr = torch.cuda.current_stream().cuda_stream
     dt = G[fmt]
+    n_warm = PF_PROBE_WARM.get(T, 0) if warm else 0
     w = torch.from_numpy(synth.weight(dt, out_dim, in_dim, seed=300)).cuda()
     y = torch.empty(T * out_dim, dtype=torch.float32, device="cuda")
     if dt == G.Q4_K:
         x = torch.from_numpy(synth.bf16_activations(T, in_dim, seed=301).reshape(-1)).cuda()
-        for _ in range(5):
+        for _ in range(5 + n_warm):
             B.matmul_q4k_bf16_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
                                   x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
     else:
         d = torch.empty_like(w)
         B.prepare_weights_dev(d.data_ptr(), w.data_ptr(), w.numel(), dt, in_dim, sptr)
         x = torch.from_numpy(synth.activations(T, in_dim, seed=301).reshape(-1)).cuda()
-        for _ in range(5):
+        for _ in range(5 + n_warm):
             B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), d.data_ptr(), d.numel(), x.data_ptr(),
                                    x.numel(), T, in_dim, out_dim, dt, sptr)
     torch.cuda.synchronize()
@@ -516,10 +542,11 @@ def batch_probe():
         del reps, prep
 
 
-# C4 prefill calls the trace child runs after the batch-1 GEMVs: (T, calls);
-# the first PF_TRACE_SKIP of each T are dropped (warm-up)
-PF_TRACE = [(512, 12), (2048, 8)]
-PF_TRACE_SKIP = 2
+# C4 prefill calls the trace child runs after the batch-1 GEMVs: (T, calls,
+# skipped): the first `skipped` calls of each T (about 25 ms of back-to-back
+# calls, the clock warm-up of _sustain) are dropped
+PF_TRACE = [(512, 480, 380), (2048, 150, 110)]
+PF_PROBE_WARM = {512: 380, 2048: 110}
 
 
 def gemv_probe():
@@ -554,7 +581,7 @@ def gemv_probe():
         del reps, prep
     out_dim, in_dim = 14336, 4096
     w = torch.from_numpy(synth.weight(G.Q4_K, out_dim, in_dim, seed=404)).to(dev)
-    for T, calls in PF_TRACE:
+    for T, calls, _ in PF_TRACE:
         x = torch.from_numpy(synth.bf16_activations(T, in_dim, seed=405).reshape(-1)).to(dev)
         y = torch.empty(T * out_dim, dtype=torch.float32, device=dev)
         _spinup(20)
@@ -612,21 +639,29 @@ def kernel_trace():
         gemv.append({"config": tag, "dtype": dname, "shape": f"{out_dim}x{in_dim}",
                      "kernel": part[0][0].split("(")[0],
                      **_summary([v / 1e3 for _, v in part])})
-    # prefill: per call one pre-pass (k_prefill_x) and one GEMM (k_prefill_q4k_w8)
-    pre = [v for n, v in rows if "k_prefill_x" in n]
-    gemm = [v for n, v in rows if "k_prefill_q4k_w8" in n]
-    n_calls = sum(c for _, c in PF_TRACE)
+    # prefill: per call one pre-pass (k_prefill_x), one GEMM (k_prefill_q4k_w8)
+    # and, where the GEMM splits K, the partial-sum kernel (k_prefill_sum*),
+    # counted with the GEMM
+    calls_seen = []  # [pre-pass, GEMM, partial sums] in ns per call
+    for n, v in rows:
+        if "k_prefill_x" in n:
+            calls_seen.append([v, 0, 0])
+        elif calls_seen and "k_prefill_q4k_w8" in n:
+            calls_seen[-1][1] += v
+        elif calls_seen and "k_prefill_sum" in n:
+            calls_seen[-1][2] += v
+    n_calls = sum(c for _, c, _ in PF_TRACE)
     prefill = []
-    if len(pre) == n_calls and len(gemm) == n_calls:
+    if len(calls_seen) == n_calls and all(c[1] > 0 for c in calls_seen):
         o = 0
-        for T, calls in PF_TRACE:
-            sl = slice(o + PF_TRACE_SKIP, o + calls)
-            prefill.append({"tokens": T, "gemm": _summary([v / 1e3 for v in gemm[sl]]),
-                            "prepass": _summary([v / 1e3 for v in pre[sl]])})
+        for T, calls, skip in PF_TRACE:
+            sl = calls_seen[o + skip:o + calls]
+            prefill.append({"tokens": T, "gemm": _summary([(c[1] + c[2]) / 1e3 for c in sl]),
+                            "partial_sums": _summary([c[2] / 1e3 for c in sl]),
+                            "prepass": _summary([c[0] / 1e3 for c in sl])})
             o += calls
     else:
-        prefill = {"error": f"expected {n_calls} prefill calls, found {len(pre)} pre-passes and "
-                            f"{len(gemm)} GEMMs"}
+        prefill = {"error": f"expected {n_calls} prefill calls, found {len(calls_seen)}"}
     return {"gemv": gemv, "prefill": prefill}
 
 
@@ -634,8 +669,8 @@ def prefill_pmc_probe():
     """Run under rocprofv3 --pmc by prefill_mfma_busy(): the C4 prefill call
     (Q4_K 14336x4096, bf16 x) five times at T = 512, then five times at
     T = 2048."""
-    prefill_probe(512)
-    prefill_probe(2048)
+    prefill_probe(512, warm=False)
+    prefill_probe(2048, warm=False)
 
 
 # MI355X: 256 CUs of 4 SIMDs in 8 XCDs (GRBM_GUI_ACTIVE is summed over the XCDs)
@@ -1339,12 +1374,14 @@ def prefill_scalars(pf, pf_trace, pf_busy):
         if "check" in e:
             out[f"t{t}_f32x_max_rel_err_vs_oracle"] = e["check"]["max_rel_err_vs_oracle"]
     if isinstance(pf_trace, list):
-        out["kernel_us_from"] = "rocprofv3 kernel trace (k_prefill_q4k_w8, k_prefill_x)"
+        out["kernel_us_from"] = ("rocprofv3 kernel trace (k_prefill_q4k_w8 plus its partial-sum "
+                                 "kernel where K is split, k_prefill_x)")
         for e in pf_trace:
             t = e["tokens"]
             us = e["gemm"]["us_mean"]
             out[f"t{t}_kernel_us"] = us
             out[f"t{t}_kernel_frac"] = round(2.0 * t * 4096 * 14336 / (us * 1e-6) / 1e12 / peak, 4)
+            out[f"t{t}_partial_sums_us"] = e["partial_sums"]["us_mean"]
             out[f"t{t}_prepass_us"] = e["prepass"]["us_mean"]
     elif pf_trace is not None:
         out["kernel_trace_error"] = str(pf_trace)[:120]
