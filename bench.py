@@ -123,7 +123,7 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
         def call():
             B.matmul_q4k_bf16_dev(d_y.data_ptr(), d_y.numel(), d_w.data_ptr(), d_w.numel(),
                                   d_x.data_ptr(), d_x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
-        _sustain(lambda i: call(), PF_SUSTAIN_MS)
+        _sustain(lambda i: call(), SUSTAIN_MS)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
         for _ in range(iters):
@@ -166,7 +166,7 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
                                    d_x.data_ptr(), d_x.numel(), T, in_dim, out_dim, G.Q4_K, sptr)
         for i in range(3):
             call_f32(i)
-        us = _time(call_f32, iters, stream, sustain_ms=PF_SUSTAIN_MS)
+        us = _time(call_f32, iters, stream, sustain_ms=SUSTAIN_MS)
         tflops = 2.0 * T * in_dim * out_dim / (us * 1e-6) / 1e12
         bf = next(e for e in res["by_tokens"] if e["tokens"] == T)
         entry = {"tokens": T, "us_per_op": round(us, 2), "tflops": round(tflops, 1),
@@ -199,7 +199,7 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
                                   d_x.data_ptr(), d_x.numel(), T, n_in, n_out, G.Q4_K, sptr)
         for i in range(3):
             call_s(i)
-        us = _time(call_s, iters, stream, sustain_ms=PF_SUSTAIN_MS)
+        us = _time(call_s, iters, stream, sustain_ms=SUSTAIN_MS)
         tflops = 2.0 * T * n_in * n_out / (us * 1e-6) / 1e12
         entry = {"shape": f"{n_out}x{n_in}", "tokens": T, "us_per_op": round(us, 2),
                  "tflops": round(tflops, 1), "frac_of_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
@@ -234,7 +234,7 @@ def bench_prefill(B, synth, G, dev, stream, iters, with_cpu, cpu_seconds):
                                    d_x.data_ptr(), d_x.numel(), T, in_dim, out_dim, dt, sptr)
         for i in range(3):
             call_f(i)
-        us = _time(call_f, iters, stream, sustain_ms=PF_SUSTAIN_MS)
+        us = _time(call_f, iters, stream, sustain_ms=SUSTAIN_MS)
         tflops = 2.0 * T * in_dim * out_dim / (us * 1e-6) / 1e12
         entry = {"format": dt.name, "shape": f"{out_dim}x{in_dim}", "tokens": T,
                  "us_per_op": round(us, 2), "tflops": round(tflops, 1),
@@ -313,7 +313,7 @@ def bench_dense_f16(dev, stream, out_dim, in_dim, iters):
 
         def call(i):
             torch.nn.functional.linear(x, ws[i & 1])
-        us = _time(call, iters, stream, sustain_ms=PF_SUSTAIN_MS)
+        us = _time(call, iters, stream, sustain_ms=SUSTAIN_MS)
         tf = 2.0 * T * in_dim * out_dim / (us * 1e-6) / 1e12
         res.append({"tokens": T, "us_per_op": round(us, 2), "tflops": round(tf, 1),
                     "frac_of_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
@@ -359,9 +359,11 @@ def _sustain(fn, ms):
     timed region), then wait for it. Under sustained matrix-core load the
     GPU's clocks settle some 10-20 ms after a spell of other work (measured
     on MI355X: the C4 prefill call at T = 2048 took 230-250 us over its first
-    50 calls after a 20 ms copy spin-up, then 222-224 us); prefill calls come
-    back to back in a forward pass, so the prefill figures are taken after
-    this warm-up on the timed call itself."""
+    50 calls after a 20 ms copy spin-up, then 222-224 us; the C3 routed
+    experts at T = 8 took 277 us per call over its first 16 calls, 241 us
+    after 200); prefill and routed-expert calls come back to back in a
+    forward pass, so those figures are taken after this warm-up on the timed
+    call itself. The batched decode calls measured the same either way."""
     import torch
     t0, i = time.perf_counter(), 0
     while (time.perf_counter() - t0) * 1e3 < ms:
@@ -371,7 +373,7 @@ def _sustain(fn, ms):
         torch.cuda.synchronize()
 
 
-PF_SUSTAIN_MS = 50
+SUSTAIN_MS = 50
 
 
 def _time(fn, iters, stream, spin_ms=20, sustain_ms=0):
@@ -473,7 +475,9 @@ def prefill_probe(T, fmt="Q4_K", warm=True):
 
 def moe_probe(T):
     """The C3 routed-expert call (64 experts, Q4_K gate/up 2048x7168, down
-    7168x2048, top-8) at T tokens, 8 calls over 8 routings."""
+    7168x2048, top-8) at T tokens over 8 routings: 25 ms of calls back to
+    back (the clock warm-up of _sustain), then 8 calls, one per routing; a
+    kernel trace's last 8 calls are the measured ones."""
     import torch
     from rsllm_amd import backend as B
     from rsllm_amd import synth
@@ -486,15 +490,20 @@ def moe_probe(T):
     d_g, d_u, d_d = (torch.from_numpy(a).cuda() for a in (gate, up, down))
     x = torch.from_numpy(synth.activations(T, n_embd, 610 + T).reshape(-1)).cuda()
     y = torch.zeros(T * n_embd, dtype=torch.float32, device="cuda")
-    _spinup(20)
+    routs = []
     for r in range(8):
-        ids, wts = synth.moe_routing(T, n_expert, k, 620 + T + 1000 * r)
-        d_i = torch.from_numpy(ids.reshape(-1)).cuda()
-        d_w = torch.from_numpy(wts.reshape(-1)).cuda()
+        routs.append(tuple(torch.from_numpy(a.reshape(-1)).cuda()
+                           for a in synth.moe_routing(T, n_expert, k, 620 + T + 1000 * r)))
+
+    def call(i):
+        d_i, d_w = routs[i % 8]
         B.moe_routed_dev(y.data_ptr(), y.numel(), x.data_ptr(), x.numel(), d_g.data_ptr(),
                          d_u.data_ptr(), gate.nbytes, d_d.data_ptr(), down.nbytes, d_i.data_ptr(),
-                         d_w.data_ptr(), ids.size, T, n_embd, n_ff, n_expert, k, G.Q4_K, G.Q4_K,
-                         10.0, sptr)
+                         d_w.data_ptr(), d_i.numel(), T, n_embd, n_ff, n_expert, k, G.Q4_K,
+                         G.Q4_K, 10.0, sptr)
+    _sustain(call, 25)
+    for r in range(8):
+        call(r)
     torch.cuda.synchronize()
 
 
@@ -1071,7 +1080,7 @@ def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
         for i in range(4):
             call(i)
         n_it = 2 * n_rout * max(1, iters // 64)
-        us = _time(call, n_it, stream)
+        us = _time(call, n_it, stream, sustain_ms=SUSTAIN_MS)
         n_act = float(np.mean([len(np.unique(i_)) for i_, _ in routs]))
         nbytes = int(n_act * per_expert + 2 * T * n_embd * 4)
         e = {"tokens": T, "active_experts": n_act, "bytes": nbytes, "us": round(us, 2),
