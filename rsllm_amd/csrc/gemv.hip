@@ -606,13 +606,16 @@ size_t gemv_scratch_bytes(uint32_t dtype, int n_tok, int in_dim) {
 // Routes for more than 32 tokens (prefill, n_tok = T): Q4_K and Q8_0 with
 // in_dim a multiple of 256, and Q6_K with rows of whole 8-block super-tiles
 // (in_dim a multiple of 2048), take the prefill GEMM; other Q6_K rows with
-// in_dim a multiple of 256 the exact matrix-core GEMV over 32-token chunks
-// (one weight pass per 32 tokens instead of per 8 on the int8-limb GEMV).
+// in_dim a multiple of 256, and Q2_K and IQ2_XXS (the DS-V4 expert formats)
+// with in_dim a multiple of 256, the exact matrix-core GEMV over 32-token
+// chunks (one weight pass per 32 tokens instead of per 8 on the int8-limb
+// GEMV).
 enum class Prefill { none, gemm, mfma_chunks };
 static Prefill prefill_route(uint32_t dtype, int n_tok, int in_dim) {
     if (n_tok <= 32 || in_dim <= 0 || in_dim % 256 != 0) return Prefill::none;
     if (dtype == T_Q4_K || dtype == T_Q8_0) return Prefill::gemm;
     if (dtype == T_Q6_K) return in_dim % 2048 == 0 ? Prefill::gemm : Prefill::mfma_chunks;
+    if (dtype == T_Q2_K || dtype == T_IQ2_XXS) return Prefill::mfma_chunks;
     return Prefill::none;
 }
 

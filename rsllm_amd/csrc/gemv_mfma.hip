@@ -377,6 +377,162 @@ struct MQ8 {
     }
 };
 
+// Q2_K (super-tile device layout [qs 8x64 | scales 8x16 | (d, dmin) 8x4],
+// 672 bytes per 8 blocks; the matrix's last super-tile holds the blocks
+// left). Step s = half n = s & 1 of block s >> 1, its elements in order:
+// element 128 n + 32 j + l (l < 32) is bits 2j, 2j + 1 of qs byte 32 n + l
+// under scale byte 8 n + 2 j + l / 16 (low nibble sc, high nibble m)
+// (dequant_q2_k, q2_k.rs:73-95: w = d sc q - dmin m). MFMA j takes the codes at
+// shift 2j; lane group q reads qs bytes 32 n + 8 q .. + 7, all of sub-block
+// 8 n + 2 j + q / 2. B = sc * q (exact, at most 45); a second MFMA per j
+// with B = m gives sum m x; the step adds d * P - dmin * M.
+struct MQ2K {
+    struct W {
+        uint2 qs, sc;  // the lane's 8 qs bytes; the half's 8 scale bytes
+        uint32_t dd;   // f16 d, dmin
+    };
+    __device__ static int elem(int s, int j, int q) { return 128 * s + 32 * j + 8 * q; }
+    __device__ static void piece(int e, int &s, int &j, int &q) {
+        s = e >> 7;
+        j = (e >> 5) & 3;
+        q = (e >> 3) & 3;
+    }
+    __device__ static void load(W &w, __amdgpu_buffer_rsrc_t r, int row, int s, int q, int in_dim,
+                                int out_dim) {
+        const uint32_t nb = (uint32_t)(in_dim >> 8);
+        const uint32_t nblk = (uint32_t)out_dim * nb;
+        const uint32_t bi = (uint32_t)row * nb + (uint32_t)(s >> 1);
+        const uint32_t S = bi >> 3, jb = bi & 7u;
+        const uint32_t rS = (S < (nblk >> 3)) ? 8u : (nblk & 7u);
+        const uint32_t base = S * 672u, n = (uint32_t)(s & 1);
+        w.qs = bload8(r, base + jb * 64u + 32u * n + 8u * (uint32_t)q, 0);
+        w.sc = bload8(r, base + rS * 64u + jb * 16u + 8u * n, 0);
+        w.dd = bload4(r, base + rS * 80u + jb * 4u);
+    }
+    template <int NT, bool PACK = false>
+    __device__ static void step(const W &w, int q, const uint4 (&x)[4][NT], const uint4 (&xl)[4][NT],
+                                f32x4 (&acc)[NT]) {
+        const float d = f16_to_f32(w.dd & 0xFFFFu), dmin = f16_to_f32(w.dd >> 16);
+        // the scale bytes 2 j + q / 2 (j = 0..3) of the half, then sc and m
+        // as f16 integers (v_perm_b32 against 0x64: the f16 1024 + v, exact,
+        // less 1024)
+        const uint32_t b4 = __builtin_amdgcn_perm(w.sc.y, w.sc.x,
+                                                  0x06040200u + (uint32_t)(q >> 1) * 0x01010101u);
+        const uint32_t sc4 = b4 & 0x0F0F0F0Fu, m4 = (b4 >> 4) & 0x0F0F0F0Fu;
+        const f16x2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const f16x2 s01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, sc4, 0x04010400u)) - k1024;
+        const f16x2 s23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, sc4, 0x04030402u)) - k1024;
+        const f16x2 m01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, m4, 0x04010400u)) - k1024;
+        const f16x2 m23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, m4, 0x04030402u)) - k1024;
+        const _Float16 scj[4] = {s01[0], s01[1], s23[0], s23[1]};
+        const _Float16 mj[4] = {m01[0], m01[1], m23[0], m23[1]};
+        const f16x2 zero = {(_Float16)0.0f, (_Float16)0.0f};
+        f16x8 b[4], bm[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t c0 = (w.qs.x >> (2 * j)) & 0x03030303u;
+            const uint32_t c1 = (w.qs.y >> (2 * j)) & 0x03030303u;
+            const f16x2 sc2 = {scj[j], scj[j]};
+            b[j] = dequant_q4x8_f16(c0, c1, false, sc2, zero);
+            const _Float16 m = mj[j];
+            bm[j] = f16x8{m, m, m, m, m, m, m, m};
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            f32x4 P = {0.f, 0.f, 0.f, 0.f}, M = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                P = mfma16x32(x[j][nt], b[j], P);
+                if (!PACK) P = mfma16x32(xl[j][nt], b[j], P);
+                M = mfma16x32(x[j][nt], bm[j], M);
+                if (!PACK) M = mfma16x32(xl[j][nt], bm[j], M);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[nt][i] = fmaf(-dmin, M[i], fmaf(d, P[i], acc[nt][i]));
+        }
+    }
+};
+
+// IQ2_XXS (super-tile device layout [qs 8x64 | d 8x2], 528 bytes per 8
+// blocks). Step s = sub-groups 4 (s & 1) .. + 3 of block s >> 1, its
+// elements in order: MFMA j is sub-group 4 (s & 1) + j (32 elements: 8
+// bytes aux0, aux1), lane group q its grid slot q, 8 values from the
+// codebook entry aux0 byte q with the sign bits of aux1 bits 7q .. 7q + 6
+// (and their parity), each an exact int8 +-{8, 25, 43}; the sub-group's
+// scale db = d (0.5 + (aux1 >> 28)) / 4 is exact in fp32 (iq2_xxs.rs:66-111).
+// B = the value; the step adds db_j * P_j.
+struct MIQ2 {
+    struct W {
+        uint4 a[2];  // the step's 4 sub-groups: (aux0, aux1) of 2 per uint4
+        uint32_t d;  // f16 d in the low half
+    };
+    __device__ static int elem(int s, int j, int q) { return 128 * s + 32 * j + 8 * q; }
+    __device__ static void piece(int e, int &s, int &j, int &q) {
+        s = e >> 7;
+        j = (e >> 5) & 3;
+        q = (e >> 3) & 3;
+    }
+    __device__ static void load(W &w, __amdgpu_buffer_rsrc_t r, int row, int s, int, int in_dim,
+                                int out_dim) {
+        const uint32_t nb = (uint32_t)(in_dim >> 8);
+        const uint32_t nblk = (uint32_t)out_dim * nb;
+        const uint32_t bi = (uint32_t)row * nb + (uint32_t)(s >> 1);
+        const uint32_t S = bi >> 3, jb = bi & 7u;
+        const uint32_t rS = (S < (nblk >> 3)) ? 8u : (nblk & 7u);
+        const uint32_t base = S * 528u, off = base + jb * 64u + 32u * (uint32_t)(s & 1);
+        w.a[0] = bload16(r, off, 0);
+        w.a[1] = bload16(r, off + 16u, 0);
+        w.d = bload2(r, base + rS * 64u + jb * 2u, 0);
+    }
+    template <int NT, bool PACK = false>
+    __device__ static void step(const W &w, int q, const uint4 (&x)[4][NT], const uint4 (&xl)[4][NT],
+                                f32x4 (&acc)[NT]) {
+        const float d = f16_to_f32(w.d & 0xFFFFu);
+        const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+        f16x8 b[4];
+        float db[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint4 &a = w.a[j >> 1];
+            const uint32_t aux0 = (j & 1) ? a.z : a.x, aux1 = (j & 1) ? a.w : a.y;
+            db[j] = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
+            const uint64_t g = kIq2Grid.v[(aux0 >> (8 * q)) & 0xFFu];
+            const uint32_t sg = iq2_signs((aux1 >> (7 * q)) & 0x7Fu);
+            const uint32_t v[2] = {iq2_apply_signs((uint32_t)g, sg & 15u),
+                                   iq2_apply_signs((uint32_t)(g >> 32), sg >> 4)};
+            // int8 -> f16: the byte with its sign bit flipped (q + 128) paired
+            // with 0x64 is the f16 1152 + q exactly; less 1152 leaves q
+            f16x8 r;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t bb = v[u] ^ 0x80808080u;
+                const f16x2 w01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04010400u)) - bias;
+                const f16x2 w23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04030402u)) - bias;
+                r[4 * u] = w01[0];
+                r[4 * u + 1] = w01[1];
+                r[4 * u + 2] = w23[0];
+                r[4 * u + 3] = w23[1];
+            }
+            b[j] = r;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const f32x4 P0 = mfma16x32(x[j][nt], b[j], f32x4{0.f, 0.f, 0.f, 0.f});
+                const f32x4 P = PACK ? P0 : mfma16x32(xl[j][nt], b[j], P0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[nt][i] = fmaf(db[j], P[i], acc[nt][i]);
+            }
+    }
+};
+
+// Formats whose rows the staged kernels (k_gemv_mfs, k_gemv_mfgs) copy
+// through LDS (MfsStage): the others take mf_rows.
+template <class F>
+constexpr bool kMfsStaged =
+    std::is_same<F, MQ4K>::value || std::is_same<F, MQ6K>::value || std::is_same<F, MQ8>::value;
+
 // ---- activation pre-pass ---------------------------------------------------------
 // Every activation image has two planes of the same layout: hi = f16(v) and
 // lo = f16(v - hi) for v = 2^e x (v - hi is exact in fp32), so hi + lo holds
@@ -1609,8 +1765,9 @@ bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
     // Q8_0 from 9 tokens: up to 8 the int8-limb kernel with x in LDS is as
     // fast on 4096 x 4096 and faster on 1024-row matrices
     const int min_tok = dtype == T_Q8_0 ? 9 : 5;
-    return (dtype == T_Q4_K || dtype == T_Q6_K || dtype == T_Q8_0) && n_tok >= min_tok &&
-           n_tok <= 32 && in_dim % 256 == 0 && in_dim > 0 && out_dim > 0;
+    return (dtype == T_Q4_K || dtype == T_Q6_K || dtype == T_Q8_0 || dtype == T_Q2_K ||
+            dtype == T_IQ2_XXS) &&
+           n_tok >= min_tok && n_tok <= 32 && in_dim % 256 == 0 && in_dim > 0 && out_dim > 0;
 }
 
 // K splits of the staged GEMV (k_gemv_mfs): the largest power of two up to
@@ -1620,7 +1777,7 @@ bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
 // kernel does not apply (in_dim not a multiple of 1024, or of 2048 for Q6_K,
 // whose super-tiles must not straddle rows).
 template <class F> static int mfs_splits(int in_dim, int out_dim) {
-    if (in_dim <= 0 || out_dim <= 0 || in_dim % kMfsK != 0) return 0;
+    if (!kMfsStaged<F> || in_dim <= 0 || out_dim <= 0 || in_dim % kMfsK != 0) return 0;
     if (std::is_same<F, MQ6K>::value && in_dim % 2048 != 0) return 0;
     const int nch = in_dim / kMfsK;
     const long blocks = (out_dim + kMfsRows - 1) / kMfsRows;
@@ -1804,9 +1961,11 @@ static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, 
         mfo_choose<F>(n_tok, in_dim, out_dim, rows, ks);
         if (rows) return mfo_go<F>(w, x, scratch, y, n_tok, in_dim, out_dim, rows, ks, s);
     }
-    const int sk = mfs_splits<F>(in_dim, out_dim);
-    if (sk > 0 && ((uintptr_t)w & 15) == 0)
-        return mfs_go<F>(w, x, scratch, y, n_tok, in_dim, out_dim, sk, s);
+    if constexpr (kMfsStaged<F>) {
+        const int sk = mfs_splits<F>(in_dim, out_dim);
+        if (sk > 0 && ((uintptr_t)w & 15) == 0)
+            return mfs_go<F>(w, x, scratch, y, n_tok, in_dim, out_dim, sk, s);
+    }
     const int cus = device_cus();
     if (n_tok <= 8 && out_dim >= 8192 && mfb_xp(n_tok, in_dim, 16) != 0 &&
         mfb_lds_bytes<F>(n_tok, in_dim, out_dim, cus, 16) <= kMfbMaxLds)
@@ -1824,11 +1983,14 @@ static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, 
     return mf_go<F, 2, 8, 1>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
 }
 
-// Any pairing of Q4_K, Q6_K and Q8_0 experts with both dimensions multiples
-// of 256. The weights are exact and the activations of each of the two
+// Any pairing of Q4_K, Q6_K, Q8_0, Q2_K and IQ2_XXS experts with both
+// dimensions multiples of 256 (Q2_K and IQ2_XXS, the DS-V4 expert formats,
+// on mf_rows: no staged layout). The weights are exact and the activations of each of the two
 // GEMVs (x, then the SwiGLU output) reach the matrix cores as hi + lo f16
 // planes, so the chained error stays at fp32 level.
-static bool mfma_format(uint32_t t) { return t == T_Q4_K || t == T_Q6_K || t == T_Q8_0; }
+static bool mfma_format(uint32_t t) {
+    return t == T_Q4_K || t == T_Q6_K || t == T_Q8_0 || t == T_Q2_K || t == T_IQ2_XXS;
+}
 bool moe_mfma_supported(uint32_t dt_gu, uint32_t dt_d, int n_embd, int n_ff) {
     return mfma_format(dt_gu) && mfma_format(dt_d) && n_embd > 0 && n_ff > 0 &&
            n_embd % 256 == 0 && n_ff % 256 == 0;
@@ -1858,6 +2020,7 @@ static hipError_t mfg_gemv(const uint8_t *w0, const uint8_t *w1, size_t w_stride
     const uint32_t plane = (uint32_t)((size_t)n_rows * in_dim * 2);
     // weights staged through LDS where the layout allows (16-byte aligned
     // expert matrices, in_dim a multiple of 1024, of 2048 for Q6_K)
+    if constexpr (kMfsStaged<F>) {
     if (mfs_splits<F>(in_dim, out_dim) > 0 &&
         (((uintptr_t)w0 | (uintptr_t)(w1 ? w1 : w0) | (uintptr_t)w_stride) & 15) == 0) {
         if (bw == 8) {
@@ -1884,6 +2047,7 @@ static hipError_t mfg_gemv(const uint8_t *w0, const uint8_t *w1, size_t w_stride
                 w0, w1, w_stride, xh, plane, us, tok, bat, n_bat, y0, y1, in_dim, out_dim);
         }
         return hipGetLastError();
+    }
     }
     constexpr int NK = 4, RT = 4;
     const dim3 g((unsigned)((out_dim + 16 * RT - 1) / (16 * RT)), (unsigned)max_b, w1 ? 2u : 1u);
@@ -1915,6 +2079,8 @@ static hipError_t mfg_swiglu_image(const float *hg, const float *hu, const int *
     case T_Q4_K: { using F = MQ4K; return call; }   \
     case T_Q6_K: { using F = MQ6K; return call; }   \
     case T_Q8_0: { using F = MQ8; return call; }    \
+    case T_Q2_K: { using F = MQ2K; return call; }   \
+    case T_IQ2_XXS: { using F = MIQ2; return call; } \
     default: return hipErrorInvalidValue;           \
     }
 
@@ -2032,6 +2198,8 @@ hipError_t launch_gemv_mfma(uint32_t dtype, const uint8_t *w, size_t w_bytes, co
     case T_Q4_K: return mf_dispatch<MQ4K>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
     case T_Q6_K: return mf_dispatch<MQ6K>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
     case T_Q8_0: return mf_dispatch<MQ8>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
+    case T_Q2_K: return mf_dispatch<MQ2K>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
+    case T_IQ2_XXS: return mf_dispatch<MIQ2>(w, w_bytes, x, scratch, y, n_tok, in_dim, out_dim, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -8,10 +8,10 @@
 // re-reading each selected expert's weights once per token. Here the
 // (token, slot) pairs are grouped by expert on the device, and each expert's
 // gate/up and down matrices are streamed once per batch of up to 4 of its
-// tokens (grouped GEMV, gemv.hip; for Q4_K, Q6_K and Q8_0 experts whenever
-// the fused pair does not take the call in one go, batches of up to 8 or 16
-// on the matrix cores instead, launch_moe_mfma in gemv_mfma.hip, steps 2-6
-// there):
+// tokens (grouped GEMV, gemv.hip; for Q4_K, Q6_K, Q8_0, Q2_K and IQ2_XXS
+// experts whenever the fused pair does not take the call in one go, batches
+// of up to 8 or 16 on the matrix cores instead, launch_moe_mfma in
+// gemv_mfma.hip, steps 2-6 there):
 //   1. routing (k_moe_hist, k_moe_scan, k_moe_scatter, any number of
 //      pairs): slots sorted by expert (ties in (t, i) order), per-expert
 //      offsets, slot -> token, (t, i) -> slot, the list of active experts;
@@ -768,6 +768,18 @@ size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_
 constexpr int kMoeMfmaMinTok = 1;
 constexpr size_t kMoeFusedMfmaPairs = 16;
 
+// Q2_K and IQ2_XXS experts reach the matrix cores without staged weights
+// (mf_rows), which loses to the int8-limb routes while most active experts
+// hold a single slot. DS-V4 shapes (IQ2_XXS gate/up, Q2_K down, 4096 / 2048,
+// 256 experts, top-6), int8-limb against matrix cores: 229 vs 292 us at 8
+// tokens, 465 vs 494 us at 16, 693 vs 674 us at 24, 923 vs 810 us at 32,
+// 5290 vs 1930 us at 512 (one process, one box). So with either format the
+// grouped matrix-core route takes calls of at least n_expert / 2 pairs.
+static bool moe_mfma_dense_enough(uint32_t dt_gu, uint32_t dt_d, size_t n_pairs, int n_expert) {
+    auto unstaged = [](uint32_t t) { return t == T_Q2_K || t == T_IQ2_XXS; };
+    return !(unstaged(dt_gu) || unstaged(dt_d)) || n_pairs >= (size_t)n_expert / 2;
+}
+
 // One pass over n_tok tokens (n_tok * k <= kMoeMaxPairs).
 static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, const uint8_t *up,
                            const uint8_t *down, size_t gu_stride, size_t d_stride, const float *x,
@@ -796,6 +808,7 @@ static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
     float *yd = reinterpret_cast<float *>(take(P * n_embd * 4));
     const bool mfma_ok = moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff) &&
                          moe_mfma_fits((int)P, n_embd, n_ff) && n_tok >= kMoeMfmaMinTok &&
+                         moe_mfma_dense_enough(dt_gu, dt_d, P, n_expert) &&
                          gu_stride <= 0xFFFFFFFFu && d_stride <= 0xFFFFFFFFu;
     const bool fused1 = (!mfma_ok || P <= kMoeFusedMfmaPairs) &&
                         moe_fused_fits(dt_gu, dt_d, n_tok, k, n_embd, n_ff, gu_stride, d_stride);

@@ -30,11 +30,12 @@ def test_gemv_ragged_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
     assert rel_err(got, want) <= REL_TOL
 
 
-# The matrix-core path (5..32 tokens of Q4_K / Q6_K, 9..32 of Q8_0):
-# one and two 16-token tiles, partial tiles, row counts off the 16-row tile,
-# few K steps per wavefront (in 256) and many (in 7168), token scales far
-# apart.
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0])
+# The matrix-core path (5..32 tokens of Q4_K / Q6_K / Q2_K / IQ2_XXS, 9..32
+# of Q8_0): one and two 16-token tiles, partial tiles, row counts off the
+# 16-row tile, few K steps per wavefront (in 256) and many (in 7168), token
+# scales far apart. Q2_K and IQ2_XXS (the DS-V4 expert formats) have no
+# staged layout and run mf_rows (or the fused LDS kernel) at every shape.
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K, G.IQ2_XXS])
 @pytest.mark.parametrize("out_dim,in_dim", [(1024, 256), (1030, 1024), (2000, 7168), (4097, 512)])
 @pytest.mark.parametrize("n_tok", [5, 9, 15, 16, 17, 31, 32])
 def test_gemv_mfma_batches(oracle, hip, dtype, out_dim, in_dim, n_tok):
@@ -79,7 +80,7 @@ def test_gemv_one_pass_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
 # matrices of a few rows (where a maximum over few outputs is most
 # sensitive, and f16-rounded weights reached 1.2e-3 on 16 rows) within an
 # fp32-level bound (about 1e-6 measured; one f16 rounding gives 2e-4 and up).
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0])
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K, G.IQ2_XXS])
 @pytest.mark.parametrize("out_dim", [1, 7, 16, 33, 100])
 @pytest.mark.parametrize("n_tok", [9, 16, 32])
 def test_gemv_mfma_exact_weights_few_rows(oracle, hip, dtype, out_dim, n_tok):
@@ -122,7 +123,7 @@ def test_gemv_q6k_full_range_scales(oracle, hip, out_dim, in_dim, n_tok):
 # row counts off the 16-row block, K steps fewer than wavefronts (256 -> 2
 # steps over 16 wavefronts) and many, token scales far apart, one token
 # zero. (Q8_0 takes the matrix cores from 9 tokens only.)
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K])
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q2_K, G.IQ2_XXS])
 @pytest.mark.parametrize("out_dim,in_dim", [(8192, 256), (8200, 1024), (9001, 3072)])
 @pytest.mark.parametrize("n_tok", [5, 6, 8])
 def test_gemv_mfma_fused_lds(oracle, hip, dtype, out_dim, in_dim, n_tok):
@@ -153,8 +154,8 @@ def test_gemv_mfma_fused_lds(oracle, hip, dtype, out_dim, in_dim, n_tok):
     (G.Q8_0, 4096, 4096, 8), (G.Q8_0, 4096, 4096, 16), (G.Q8_0, 4096, 4096, 32),
     (G.Q8_0, 1024, 4096, 1), (G.Q8_0, 1024, 4096, 2), (G.Q8_0, 1024, 4096, 4),
     (G.Q8_0, 1024, 4096, 8), (G.Q8_0, 1024, 4096, 16), (G.Q8_0, 1024, 4096, 32),
-    (G.Q2_K, 7168, 2048, 1), (G.Q2_K, 7168, 2048, 8),
-    (G.IQ2_XXS, 2048, 7168, 1), (G.IQ2_XXS, 2048, 7168, 8),
+    (G.Q2_K, 7168, 2048, 1), (G.Q2_K, 7168, 2048, 8), (G.Q2_K, 7168, 2048, 32),
+    (G.IQ2_XXS, 2048, 7168, 1), (G.IQ2_XXS, 2048, 7168, 8), (G.IQ2_XXS, 2048, 7168, 32),
 ])
 def test_gemv_config_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
     got, want = run_both(oracle, hip, dtype, out_dim, in_dim, n_tok, seed=11)

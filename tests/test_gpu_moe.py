@@ -229,6 +229,28 @@ def test_moe_grouped_dsv4_like_shapes(oracle, hip, dt, n_tok):
     assert err <= MFMA_TOL
 
 
+@pytest.mark.parametrize("n_tok", [3, 9, 32])
+def test_moe_grouped_dsv4_formats(oracle, hip, n_tok):
+    """The DS-V4-Flash expert formats (IQ2_XXS gate/up, Q2_K down) at DS-V4
+    expert shapes (n_embd 4096, n_ff 2048, top-6 of 16) on the grouped
+    matrix-core route (calls past the fused pair's 16 pairs): exact codebook
+    and 2-bit weights with their scales in fp32, hi + lo activations, so the
+    chained error is held to MFMA_TOL. Checked on up to 6 tokens."""
+    n_embd, n_ff, n_expert, k = 4096, 2048, 16, 6
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.IQ2_XXS, G.Q2_K,
+                                          740 + n_tok)
+    w[0, 1] = 0.0  # a skipped slot
+    got = np.zeros(n_tok * n_embd, np.float32)
+    hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
+                   G.IQ2_XXS, G.Q2_K, 10.0)
+    toks = np.unique(np.linspace(0, n_tok - 1, min(n_tok, 6)).astype(int))
+    want = run_oracle(oracle, np.zeros(len(toks) * n_embd, np.float32), x[toks], gate, up, down,
+                      ids[toks], w[toks], len(toks), n_embd, n_ff, n_expert, k, G.IQ2_XXS, G.Q2_K)
+    err = rel_err(got.reshape(n_tok, n_embd)[toks], want.reshape(len(toks), n_embd))
+    print(f"moe dsv4 formats T={n_tok}: rel err {err:.3e}")
+    assert err <= MFMA_TOL
+
+
 def test_moe_grouped_q6k_full_range_scales(oracle, hip):
     """Q6_K experts whose scales span the whole int8 range (sc (q - 32) up to
     4096, past f16's exact integers) on the grouped matrix-core route: the
@@ -281,21 +303,23 @@ def test_moe_prefill_2048_tokens_top6_256_experts(oracle, hip):
     assert err <= REL_TOL
 
 
-def test_moe_prefill_iq2xxs_q2k_multilaunch_route(oracle, hip):
-    """The real DS-V4-Flash expert formats (IQ2_XXS gate/up, Q2_K down) at
-    1500 tokens x top-6 (9000 pairs: two chunks) through the int8-limb grouped
-    GEMVs."""
+@pytest.mark.parametrize("dt_d,tol", [(G.Q2_K, MFMA_TOL), (G.Q4_0, REL_TOL)])
+def test_moe_prefill_iq2xxs_1500_tokens(oracle, hip, dt_d, tol):
+    """IQ2_XXS gate/up at 1500 tokens x top-6 (9000 pairs: two chunks): with
+    Q2_K down (the real DS-V4-Flash pairing) on the grouped matrix-core
+    route, within MFMA_TOL; with Q4_0 down (no matrix-core form) through the
+    int8-limb grouped GEMVs of the multi-launch route."""
     n_tok, n_embd, n_ff, n_expert, k = 1500, 512, 256, 64, 6
-    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.IQ2_XXS, G.Q2_K,
+    gate, up, down, x, ids, w = make_case(n_tok, n_embd, n_ff, n_expert, k, G.IQ2_XXS, dt_d,
                                           4200)
     got = np.zeros(n_tok * n_embd, np.float32)
     hip.moe_routed(got, x.reshape(-1), gate, up, down, ids, w, n_tok, n_embd, n_ff, n_expert, k,
-                   G.IQ2_XXS, G.Q2_K, 10.0)
+                   G.IQ2_XXS, dt_d, 10.0)
     toks = np.array([0, 1, 681, 1364, 1365, 1366, 1499])
     err = _subset_check(oracle, got, x, gate, up, down, ids, w, toks, n_embd, n_ff, n_expert, k,
-                        G.IQ2_XXS, G.Q2_K)
-    print(f"moe prefill IQ2_XXS/Q2_K T={n_tok}: rel err {err:.3e}")
-    assert err <= REL_TOL
+                        G.IQ2_XXS, dt_d)
+    print(f"moe prefill IQ2_XXS/{dt_d.name} T={n_tok}: rel err {err:.3e}")
+    assert err <= tol
 
 
 def test_moe_many_pairs_one_expert_and_device_form(oracle, hip):

@@ -11,9 +11,10 @@ Routes above 32 tokens:
   every output of every checked token within the derived bound of
   prefill_bound.py, and the whole within the north star's 1e-3 (REL_TOL),
   about 3e-4 measured;
-* other Q6_K rows: the exact matrix-core GEMV (integer weights, hi + lo f16
-  activations) over 32-token chunks, a short tail included: an fp32-level
-  bound (2e-5) on every token;
+* other Q6_K rows, and Q2_K and IQ2_XXS (the DS-V4 expert formats): the
+  exact matrix-core GEMV (integer weights, hi + lo f16 activations) over
+  32-token chunks, a short tail included: an fp32-level bound (2e-5) on
+  every token;
 * other formats: the int8-limb GEMV (REL_TOL).
 A device pointer that is not 16-byte aligned keeps the call off the GEMM
 (its global->LDS copies move 16-byte pieces) and must still be right."""
@@ -78,7 +79,7 @@ def check(oracle, got, w, x, tokens, dtype, n_tok, in_dim, out_dim, tol, route):
     return err
 
 
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K])
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K, G.IQ2_XXS])
 @pytest.mark.parametrize("out_dim,in_dim", [(300, 768), (1000, 2048), (4097, 256)])
 @pytest.mark.parametrize("n_tok", [33, 40, 100, 129])
 def test_prefill_f32_ragged(oracle, hip, dtype, out_dim, in_dim, n_tok):
@@ -89,7 +90,7 @@ def test_prefill_f32_ragged(oracle, hip, dtype, out_dim, in_dim, n_tok):
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
     got = run_dev(hip, dtype, w, x, n_tok, in_dim, out_dim)
     gemm = dtype in (G.Q4_K, G.Q8_0) or (dtype == G.Q6_K and in_dim % 2048 == 0)
-    route = "gemm" if gemm else "chunks" if dtype == G.Q6_K else "limb"
+    route = "gemm" if gemm else "chunks"
     tol = EXACT_TOL if route == "chunks" else REL_TOL
     check(oracle, got, w, x, np.arange(n_tok), dtype, n_tok, in_dim, out_dim, tol, route)
 
