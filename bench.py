@@ -1109,7 +1109,107 @@ def bench_extra(B, synth, G, dev, stream, iters, with_cpu):
                   "timing": "back-to-back calls alternating two weight copies and cycling 8 "
                             "routings (active_experts and bytes are their means)"}
     del wcopies
+    _progress("extra: moe done")
+    out["dsv4"] = bench_dsv4(B, synth, G, dev, stream, iters, with_cpu)
     return out
+
+
+def bench_dsv4(B, synth, G, dev, stream, iters, with_cpu):
+    """extra.dsv4: the DS-V4-Flash expert formats (IQ2_XXS gate/up, Q2_K
+    down) at the reference's expert shapes (n_embd 4096, n_ff 2048): one
+    expert matrix of each format through matmul_quant_f32_dev at 8 and 32
+    tokens (decode batches) and at 512 (a prefill call), and the routed
+    experts (256 experts, top-6, moe_routed_dev) from 1 to 2048 tokens. Every
+    figure is taken after 50 ms of the same call back to back; the oracle
+    checks 4 tokens of each dense case and of the 32-token MoE call."""
+    import torch
+    sptr = stream.cuda_stream
+    if with_cpu:
+        sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+        from oracle import oracle as O
+    res = {"dense": [], "moe": []}
+    for (dt, o, i_, seed) in ((G.Q2_K, 4096, 2048, 640), (G.IQ2_XXS, 2048, 4096, 641)):
+        w_host = synth.weight(dt, o, i_, seed)
+        raw = torch.from_numpy(w_host).to(dev)
+        prep = torch.empty_like(raw)
+        B.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), dt, i_, sptr)
+        del raw
+        reps = _rotating(prep)
+        for T in (8, 32, 512):
+            x_host = synth.activations(T, i_, seed + T).reshape(-1)
+            x = torch.from_numpy(x_host).to(dev)
+            y = torch.empty(T * o, dtype=torch.float32, device=dev)
+
+            def call(i):
+                w = reps[i % len(reps)]
+                B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(),
+                                       x.data_ptr(), x.numel(), T, i_, o, dt, sptr)
+            us = _time(call, iters, stream, sustain_ms=SUSTAIN_MS)
+            nbytes = prep.numel() + T * (i_ + o) * 4
+            e = {"dtype": dt.name, "shape": f"{o}x{i_}", "tokens": T, "us": round(us, 3),
+                 "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                 "tflops": round(2.0 * T * o * i_ / (us * 1e-6) / 1e12, 2)}
+            if with_cpu:
+                toks = np.unique(np.linspace(0, T - 1, 4).astype(int))
+                xs = x_host.reshape(T, i_)[toks].reshape(-1)
+                rc, want = O.matmul_quant_f32(w_host, xs, len(toks), i_, o, int(dt))
+                got = y.cpu().numpy().reshape(T, o)[toks].reshape(-1)
+                e["max_rel_err_vs_oracle"] = float(np.abs(got - want).max() / np.abs(want).max())
+            res["dense"].append(e)
+            del x, y
+        del reps, prep
+    n_expert, n_embd, n_ff, k = 256, 4096, 2048, 6
+    gate = synth.weight(G.IQ2_XXS, n_expert * n_ff, n_embd, 650)
+    up = synth.weight(G.IQ2_XXS, n_expert * n_ff, n_embd, 651)
+    down = synth.weight(G.Q2_K, n_expert * n_embd, n_ff, 652)
+    # the device layout of both formats (8-block super-tiles; each expert's
+    # matrix holds a whole number of them)
+    dev_w = []
+    for a, dt, ind in ((gate, G.IQ2_XXS, n_embd), (up, G.IQ2_XXS, n_embd), (down, G.Q2_K, n_ff)):
+        raw = torch.from_numpy(a).to(dev)
+        d = torch.empty_like(raw)
+        B.prepare_weights_dev(d.data_ptr(), raw.data_ptr(), raw.numel(), dt, ind, sptr)
+        dev_w.append(d)
+        del raw
+    d_g, d_u, d_d = dev_w
+    per_expert = (gate.nbytes + up.nbytes + down.nbytes) // n_expert
+    for T in (1, 8, 32, 512, 2048):
+        x_host = synth.activations(T, n_embd, 660 + T).reshape(-1)
+        routs = [synth.moe_routing(T, n_expert, k, 670 + T + 1000 * r) for r in range(4)]
+        x = torch.from_numpy(x_host).to(dev)
+        d_rout = [tuple(torch.from_numpy(a.reshape(-1)).to(dev) for a in rw) for rw in routs]
+        y = torch.zeros(T * n_embd, dtype=torch.float32, device=dev)
+
+        def call(i):
+            d_ids, d_w = d_rout[i % 4]
+            B.moe_routed_dev(y.data_ptr(), y.numel(), x.data_ptr(), x.numel(), d_g.data_ptr(),
+                             d_u.data_ptr(), gate.nbytes, d_d.data_ptr(), down.nbytes,
+                             d_ids.data_ptr(), d_w.data_ptr(), T * k, T, n_embd, n_ff, n_expert,
+                             k, G.IQ2_XXS, G.Q2_K, 10.0, sptr)
+        us = _time(call, 8 if T >= 512 else 16, stream, sustain_ms=SUSTAIN_MS)
+        n_act = float(np.mean([len(np.unique(i_)) for i_, _ in routs]))
+        nbytes = n_act * per_expert + 2 * T * n_embd * 4
+        e = {"tokens": T, "active_experts": n_act, "us": round(us, 2),
+             "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+             "tflops": round(2.0 * T * k * 3 * n_embd * n_ff / (us * 1e-6) / 1e12, 2)}
+        if with_cpu and T == 32:
+            ids, wts = routs[0]
+            y.zero_()
+            call(0)
+            torch.cuda.synchronize()
+            toks = np.array([0, 11, 22, 31])
+            want = np.zeros(len(toks) * n_embd, np.float32)
+            rc = O.moe_routed(want, x_host.reshape(T, n_embd)[toks].reshape(-1), len(toks),
+                              n_embd, n_ff, gate, up, down, int(G.IQ2_XXS), int(G.Q2_K), n_expert,
+                              ids[toks], wts[toks], k, 10.0)
+            got = y.cpu().numpy().reshape(T, n_embd)[toks].reshape(-1)
+            e["max_rel_err_vs_oracle"] = float(np.abs(got - want).max() / np.abs(want).max())
+        res["moe"].append(e)
+        del x, y, d_rout
+    del d_g, d_u, d_d, dev_w
+    res["workload"] = ("DS-V4 expert formats: IQ2_XXS gate/up (2048, 4096), Q2_K down (4096, "
+                       "2048); routed experts 256 x (gate, up, down), top-6")
+    return res
 
 
 def main():
@@ -1428,7 +1528,9 @@ def extra_compact(ex):
     gemv [config dtype shape B, us, frac of 8 TB/s, max rel err vs oracle];
     q8_int8 [shape B, quantize us, matmul us, frac, bit-exact];
     moe [T, us, frac, active experts]; caller_chain [op shape B, us, frac];
-    stream_read [config, us, frac]."""
+    stream_read [config, us, frac]; dsv4_dense [format shape T, us, frac,
+    TFLOP/s, max rel err]; dsv4_moe [T, us, frac, TFLOP/s, active experts,
+    max rel err]."""
     if ex is None:
         return None
 
@@ -1450,6 +1552,14 @@ def extra_compact(ex):
     if "max_rel_err_vs_oracle" in m1:
         out["moe_t1_max_rel_err_vs_oracle"] = r(m1["max_rel_err_vs_oracle"], 7)
         out["moe_t1_cpu_baseline"] = m1["cpu_baseline"]
+    ds = ex.get("dsv4")
+    if ds:
+        out["dsv4_workload"] = ds["workload"]
+        out["dsv4_dense"] = [[f"{e['dtype']} {e['shape']} T={e['tokens']}", e["us"],
+                              e["frac_hbm"], e["tflops"], r(e.get("max_rel_err_vs_oracle"), 7)]
+                             for e in ds["dense"]]
+        out["dsv4_moe"] = [[e["tokens"], e["us"], e["frac_hbm"], e["tflops"], e["active_experts"],
+                            r(e.get("max_rel_err_vs_oracle"), 7)] for e in ds["moe"]]
     return out
 
 
