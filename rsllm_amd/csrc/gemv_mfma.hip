@@ -453,14 +453,47 @@ struct MQ2K {
     }
 };
 
+// IQ2_XXS operands as f16: codebook entry i as 8 f16 magnitudes (8, 25, 43,
+// exact), and for each 7-bit sign index the 8 f16 sign bits (its parity as
+// the 8th), so a lane's 8 weights are one XOR of two 16-byte table reads.
+struct Iq2F16Tables {
+    uint32_t grid[256][4];
+    uint32_t sign[128][4];
+    constexpr Iq2F16Tables() : grid(), sign() {
+        constexpr uint32_t f16v[3] = {0x4800u, 0x4E40u, 0x5160u};  // 8, 25, 43
+        for (int i = 0; i < 256; i++) {
+            uint32_t code = kIq2Codes[i];
+            uint32_t h[8] = {};
+            for (int j = 0; j < 8; j++) {
+                h[j] = f16v[code % 3];
+                code /= 3;
+            }
+            for (int k = 0; k < 4; k++) grid[i][k] = h[2 * k] | h[2 * k + 1] << 16;
+        }
+        for (uint32_t si = 0; si < 128; si++) {
+            uint32_t par = 0;
+            for (int b = 0; b < 7; b++) par ^= (si >> b) & 1u;
+            const uint32_t s8 = si | par << 7;
+            for (int k = 0; k < 4; k++)
+                sign[si][k] = ((s8 >> (2 * k)) & 1u) << 15 | ((s8 >> (2 * k + 1)) & 1u) << 31;
+        }
+    }
+};
+static __constant__ Iq2F16Tables kIq2F16 = Iq2F16Tables();
+// The workgroup's LDS copy (6 KB), staged by MIQ2::stage_tables before the
+// first step of a kernel that runs MIQ2::step.
+static __shared__ uint4 s_iq2_grid[256];
+static __shared__ uint4 s_iq2_sign[128];
+
 // IQ2_XXS (super-tile device layout [qs 8x64 | d 8x2], 528 bytes per 8
 // blocks). Step s = sub-groups 4 (s & 1) .. + 3 of block s >> 1, its
 // elements in order: MFMA j is sub-group 4 (s & 1) + j (32 elements: 8
 // bytes aux0, aux1), lane group q its grid slot q, 8 values from the
 // codebook entry aux0 byte q with the sign bits of aux1 bits 7q .. 7q + 6
-// (and their parity), each an exact int8 +-{8, 25, 43}; the sub-group's
-// scale db = d (0.5 + (aux1 >> 28)) / 4 is exact in fp32 (iq2_xxs.rs:66-111).
-// B = the value; the step adds db_j * P_j.
+// (and their parity), each +-{8, 25, 43} (iq2_xxs.rs:66-111), read as f16
+// from the tables in LDS; the sub-group's scale db = d (0.5 + (aux1 >> 28)) / 4 is
+// exact in fp32 (one FMA: ls d/4 + d/8). B = the value; the step adds
+// db_j * P_j.
 struct MIQ2 {
     struct W {
         uint4 a[2];  // the step's 4 sub-groups: (aux0, aux1) of 2 per uint4
@@ -471,6 +504,16 @@ struct MIQ2 {
         s = e >> 7;
         j = (e >> 5) & 3;
         q = (e >> 3) & 3;
+    }
+    // every thread of the workgroup, before its first step
+    __device__ static void stage_tables() {
+        for (int i = threadIdx.x; i < 384; i += blockDim.x) {
+            if (i < 256)
+                s_iq2_grid[i] = *reinterpret_cast<const uint4 *>(kIq2F16.grid[i]);
+            else
+                s_iq2_sign[i - 256] = *reinterpret_cast<const uint4 *>(kIq2F16.sign[i - 256]);
+        }
+        __syncthreads();
     }
     __device__ static void load(W &w, __amdgpu_buffer_rsrc_t r, int row, int s, int, int in_dim,
                                 int out_dim) {
@@ -487,33 +530,18 @@ struct MIQ2 {
     template <int NT, bool PACK = false>
     __device__ static void step(const W &w, int q, const uint4 (&x)[4][NT], const uint4 (&xl)[4][NT],
                                 f32x4 (&acc)[NT]) {
-        const float d = f16_to_f32(w.d & 0xFFFFu);
-        const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+        const float d = f16_to_f32(w.d & 0xFFFFu), d4 = d * 0.25f, d8 = d * 0.125f;
         f16x8 b[4];
         float db[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint4 &a = w.a[j >> 1];
             const uint32_t aux0 = (j & 1) ? a.z : a.x, aux1 = (j & 1) ? a.w : a.y;
-            db[j] = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
-            const uint64_t g = kIq2Grid.v[(aux0 >> (8 * q)) & 0xFFu];
-            const uint32_t sg = iq2_signs((aux1 >> (7 * q)) & 0x7Fu);
-            const uint32_t v[2] = {iq2_apply_signs((uint32_t)g, sg & 15u),
-                                   iq2_apply_signs((uint32_t)(g >> 32), sg >> 4)};
-            // int8 -> f16: the byte with its sign bit flipped (q + 128) paired
-            // with 0x64 is the f16 1152 + q exactly; less 1152 leaves q
-            f16x8 r;
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const uint32_t bb = v[u] ^ 0x80808080u;
-                const f16x2 w01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04010400u)) - bias;
-                const f16x2 w23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, bb, 0x04030402u)) - bias;
-                r[4 * u] = w01[0];
-                r[4 * u + 1] = w01[1];
-                r[4 * u + 2] = w23[0];
-                r[4 * u + 3] = w23[1];
-            }
-            b[j] = r;
+            db[j] = fmaf((float)(aux1 >> 28), d4, d8);
+            const uint4 gv = s_iq2_grid[(aux0 >> (8 * q)) & 0xFFu];
+            const uint4 sv = s_iq2_sign[(aux1 >> (7 * q)) & 0x7Fu];
+            b[j] = __builtin_bit_cast(f16x8, make_uint4(gv.x ^ sv.x, gv.y ^ sv.y, gv.z ^ sv.z,
+                                                        gv.w ^ sv.w));
         }
 #pragma unroll
         for (int nt = 0; nt < NT; nt++)
@@ -686,6 +714,7 @@ __device__ __forceinline__ void mf_rows(const uint8_t *__restrict__ w, uint32_t 
                                         int n_tok, int in_dim, int out_dim, int y_stride, int row0,
                                         f32x4 *red, int ntp, uint32_t xcol = 0, float usc = 0.f) {
     static_assert(!ROWX || NT == 1, "per-row images take one token tile");
+    if constexpr (std::is_same<F, MIQ2>::value) MIQ2::stage_tables();
     const int lane = threadIdx.x & 63, r16 = lane & 15, q = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nsteps = in_dim / kMfStep;
@@ -1967,9 +1996,12 @@ static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, 
             return mfs_go<F>(w, x, scratch, y, n_tok, in_dim, out_dim, sk, s);
     }
     const int cus = device_cus();
-    if (n_tok <= 8 && out_dim >= 8192 && mfb_xp(n_tok, in_dim, 16) != 0 &&
-        mfb_lds_bytes<F>(n_tok, in_dim, out_dim, cus, 16) <= kMfbMaxLds)
-        return mfb_xp_go<F, 16, 2>(w, w_bytes, x, y, n_tok, in_dim, out_dim, cus, s);
+    // (not IQ2_XXS: its operand tables are staged in LDS by mf_rows)
+    if constexpr (!std::is_same<F, MIQ2>::value) {
+        if (n_tok <= 8 && out_dim >= 8192 && mfb_xp(n_tok, in_dim, 16) != 0 &&
+            mfb_lds_bytes<F>(n_tok, in_dim, out_dim, cus, 16) <= kMfbMaxLds)
+            return mfb_xp_go<F, 16, 2>(w, w_bytes, x, y, n_tok, in_dim, out_dim, cus, s);
+    }
     // Every workgroup reads the whole activation image, so more rows per
     // workgroup read it fewer times; 4 row tiles (4 wavefronts over K) where
     // that still leaves 224 or more workgroups (C1 14336 x 4096 Q4_K: 20.6 vs
