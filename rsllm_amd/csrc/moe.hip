@@ -769,15 +769,16 @@ constexpr int kMoeMfmaMinTok = 1;
 constexpr size_t kMoeFusedMfmaPairs = 16;
 
 // Q2_K and IQ2_XXS experts reach the matrix cores without staged weights
-// (mf_rows), which loses to the int8-limb routes while most active experts
-// hold a single slot. DS-V4 shapes (IQ2_XXS gate/up, Q2_K down, 4096 / 2048,
-// 256 experts, top-6), int8-limb against matrix cores: 229 vs 292 us at 8
-// tokens, 465 vs 494 us at 16, 693 vs 674 us at 24, 923 vs 810 us at 32,
-// 5290 vs 1930 us at 512 (one process, one box). So with either format the
-// grouped matrix-core route takes calls of at least n_expert / 2 pairs.
+// (mf_rows), which loses to the int8-limb routes while few active experts
+// hold more than one slot. DS-V4 shapes (IQ2_XXS gate/up, Q2_K down, 4096 /
+// 2048, 256 experts, top-6), int8-limb against matrix cores: 113 vs 126 us
+// at 4 tokens (24 pairs), 229 vs 228 us at 8 (48), 343 vs 305 us at 12
+// (72), 465 vs 381 us at 16, 571 vs 447 us at 20 (one process, one box). So
+// with either format the grouped matrix-core route takes calls of at least
+// n_expert / 5 pairs.
 static bool moe_mfma_dense_enough(uint32_t dt_gu, uint32_t dt_d, size_t n_pairs, int n_expert) {
     auto unstaged = [](uint32_t t) { return t == T_Q2_K || t == T_IQ2_XXS; };
-    return !(unstaged(dt_gu) || unstaged(dt_d)) || n_pairs >= (size_t)n_expert / 2;
+    return !(unstaged(dt_gu) || unstaged(dt_d)) || n_pairs >= (size_t)n_expert / 5;
 }
 
 // One pass over n_tok tokens (n_tok * k <= kMoeMaxPairs).
