@@ -556,10 +556,12 @@ struct MIQ2 {
 };
 
 // Formats whose rows the staged kernels (k_gemv_mfs, k_gemv_mfgs) copy
-// through LDS (MfsStage): the others take mf_rows.
+// through LDS (MfsStage); Q6_K, Q2_K and IQ2_XXS only where in_dim is a
+// multiple of 2048 (whole super-tiles per row).
 template <class F>
 constexpr bool kMfsStaged =
-    std::is_same<F, MQ4K>::value || std::is_same<F, MQ6K>::value || std::is_same<F, MQ8>::value;
+    std::is_same<F, MQ4K>::value || std::is_same<F, MQ6K>::value || std::is_same<F, MQ8>::value ||
+    std::is_same<F, MQ2K>::value || std::is_same<F, MIQ2>::value;
 
 // ---- activation pre-pass ---------------------------------------------------------
 // Every activation image has two planes of the same layout: hi = f16(v) and
@@ -910,6 +912,52 @@ template <> struct MfsStage<MQ8> {
     }
 };
 
+template <> struct MfsStage<MQ2K> {
+    // half super-tile (in_dim % 2048 == 0: a row's blocks fill whole
+    // super-tiles): qs 256 B, scales 64 B, (d, dmin) 16 B (16 + 4 + 1
+    // pieces), in that order in LDS
+    static constexpr int PR = 22;
+    __device__ static uint32_t row_bytes(int in_dim) { return (uint32_t)(in_dim >> 11) * 672u; }
+    __device__ static uint32_t off0(uint32_t row, int k, int in_dim) {
+        const uint32_t base = row * (uint32_t)(in_dim >> 11) * 672u;
+        if (k < 16) return base + 16u * k;
+        if (k < 20) return base + 512u + 16u * (k - 16);
+        if (k == 20) return base + 640u;
+        return kMfsNoPiece;
+    }
+    __device__ static uint32_t c_off(int c, int k) {
+        const uint32_t half = k < 16 ? 256u : (k < 20 ? 64u : 16u);
+        return (uint32_t)(c >> 1) * 672u + (uint32_t)(c & 1) * half;
+    }
+    __device__ static void load(MQ2K::W &v, const uint8_t *r, int st, int q, int) {
+        const int jb = st >> 1, n = st & 1;
+        v.qs = *reinterpret_cast<const uint2 *>(r + 64 * jb + 32 * n + 8 * q);
+        v.sc = *reinterpret_cast<const uint2 *>(r + 256 + 16 * jb + 8 * n);
+        v.dd = *reinterpret_cast<const uint32_t *>(r + 320 + 4 * jb);
+    }
+};
+template <> struct MfsStage<MIQ2> {
+    // half super-tile (in_dim % 2048 == 0): qs 256 B (16 pieces) and the
+    // super-tile's 16-byte d run
+    static constexpr int PR = 18;
+    __device__ static uint32_t row_bytes(int in_dim) { return (uint32_t)(in_dim >> 11) * 528u; }
+    __device__ static uint32_t off0(uint32_t row, int k, int in_dim) {
+        const uint32_t base = row * (uint32_t)(in_dim >> 11) * 528u;
+        if (k < 16) return base + 16u * k;
+        if (k == 16) return base + 512u;
+        return kMfsNoPiece;
+    }
+    __device__ static uint32_t c_off(int c, int k) {
+        return (uint32_t)(c >> 1) * 528u + (k < 16 ? (uint32_t)(c & 1) * 256u : 0u);
+    }
+    __device__ static void load(MIQ2::W &v, const uint8_t *r, int st, int, int c) {
+        const int jb = st >> 1;
+        v.a[0] = *reinterpret_cast<const uint4 *>(r + 64 * jb + 32 * (st & 1));
+        v.a[1] = *reinterpret_cast<const uint4 *>(r + 64 * jb + 32 * (st & 1) + 16);
+        v.d = *reinterpret_cast<const uint16_t *>(r + 256 + 2 * (4 * (c & 1) + jb));
+    }
+};
+
 template <class F, int NW = 4, int ROWS = kMfsRows> struct MfsGeo {
     static constexpr int THREADS = 64 * NW;
     static constexpr int PIECES = ROWS * MfsStage<F>::PR;
@@ -936,6 +984,7 @@ __device__ __forceinline__ void mfs_rows(const uint8_t *__restrict__ w,
                                          int row0, int c0, int nch, int ntp, uint8_t *smem,
                                          uint32_t xcol = 0, float usc = 0.f) {
     static_assert(!ROWX || NT == 1, "per-row images take one token tile");
+    if constexpr (std::is_same<F, MIQ2>::value) MIQ2::stage_tables();
     using S = MfsStage<F>;
     using G = MfsGeo<F, NW, ROWS>;
     constexpr int RT = ROWS / 16;
@@ -1807,18 +1856,33 @@ bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
 // whose super-tiles must not straddle rows).
 template <class F> static int mfs_splits(int in_dim, int out_dim) {
     if (!kMfsStaged<F> || in_dim <= 0 || out_dim <= 0 || in_dim % kMfsK != 0) return 0;
-    if (std::is_same<F, MQ6K>::value && in_dim % 2048 != 0) return 0;
+    if ((std::is_same<F, MQ6K>::value || std::is_same<F, MQ2K>::value ||
+         std::is_same<F, MIQ2>::value) &&
+        in_dim % 2048 != 0)
+        return 0;
     const int nch = in_dim / kMfsK;
     const long blocks = (out_dim + kMfsRows - 1) / kMfsRows;
     int sk = 1;
     while (sk < 8 && 2 * sk <= nch && blocks * 2 * sk <= 512) sk *= 2;
     return sk;
 }
-static int mfs_splits_for(uint32_t dtype, int in_dim, int out_dim) {
+// The staged kernel's K splits for a dense call of n_tok tokens, or 0 where
+// the call takes another kernel: Q2_K and IQ2_XXS take it above 16 tokens
+// only (below, the unstaged kernel was the faster: Q2_K 7168 x 2048 at 8
+// tokens 9.9 vs 11.8 us, 4096 x 4096 at 16 11.2 vs 12.8 us, IQ2_XXS 2048 x
+// 4096 at 8 10.5 vs 12.0 us; at 32 tokens 14.5 vs 13.9 and 13.4 vs 13.4 us).
+template <class F> static int mfs_dense_splits(int n_tok, int in_dim, int out_dim) {
+    if ((std::is_same<F, MQ2K>::value || std::is_same<F, MIQ2>::value) && n_tok <= 16) return 0;
+    return mfs_splits<F>(in_dim, out_dim);
+}
+// (the workspace sizing: every format the staged kernel takes must be here)
+static int mfs_splits_for(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
     switch (dtype) {
-    case T_Q4_K: return mfs_splits<MQ4K>(in_dim, out_dim);
-    case T_Q6_K: return mfs_splits<MQ6K>(in_dim, out_dim);
-    case T_Q8_0: return mfs_splits<MQ8>(in_dim, out_dim);
+    case T_Q4_K: return mfs_dense_splits<MQ4K>(n_tok, in_dim, out_dim);
+    case T_Q6_K: return mfs_dense_splits<MQ6K>(n_tok, in_dim, out_dim);
+    case T_Q8_0: return mfs_dense_splits<MQ8>(n_tok, in_dim, out_dim);
+    case T_Q2_K: return mfs_dense_splits<MQ2K>(n_tok, in_dim, out_dim);
+    case T_IQ2_XXS: return mfs_dense_splits<MIQ2>(n_tok, in_dim, out_dim);
     default: return 0;
     }
 }
@@ -1903,7 +1967,7 @@ static hipError_t mfo_go(const uint8_t *w, const float *x, uint8_t *scratch, flo
 size_t gemv_mfma_scratch_bytes(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
     const size_t ntp = n_tok <= 16 ? 16 : 32;
-    const int sk = mfs_splits_for(dtype, in_dim, out_dim);
+    const int sk = mfs_splits_for(dtype, n_tok, in_dim, out_dim);
     const size_t part = sk > 1 ? (size_t)sk * (size_t)n_tok * (size_t)out_dim * 4 : 0;
     const size_t staged = al(2 * ntp * (size_t)in_dim * 2) + al(ntp * 4) + part;
     // the one-pass kernel: only its slices' partial outputs
@@ -1991,7 +2055,7 @@ static hipError_t mf_dispatch(const uint8_t *w, size_t w_bytes, const float *x, 
         if (rows) return mfo_go<F>(w, x, scratch, y, n_tok, in_dim, out_dim, rows, ks, s);
     }
     if constexpr (kMfsStaged<F>) {
-        const int sk = mfs_splits<F>(in_dim, out_dim);
+        const int sk = mfs_dense_splits<F>(n_tok, in_dim, out_dim);
         if (sk > 0 && ((uintptr_t)w & 15) == 0)
             return mfs_go<F>(w, x, scratch, y, n_tok, in_dim, out_dim, sk, s);
     }

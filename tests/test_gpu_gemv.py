@@ -33,8 +33,9 @@ def test_gemv_ragged_shapes(oracle, hip, dtype, out_dim, in_dim, n_tok):
 # The matrix-core path (5..32 tokens of Q4_K / Q6_K / Q2_K / IQ2_XXS, 9..32
 # of Q8_0): one and two 16-token tiles, partial tiles, row counts off the
 # 16-row tile, few K steps per wavefront (in 256) and many (in 7168), token
-# scales far apart. Q2_K and IQ2_XXS (the DS-V4 expert formats) have no
-# staged layout and run mf_rows (or the fused LDS kernel) at every shape.
+# scales far apart. Q2_K and IQ2_XXS (the DS-V4 expert formats) run
+# mf_rows (or, Q2_K, the fused LDS kernel) at these in_dim, which are not
+# multiples of 2048.
 @pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K, G.IQ2_XXS])
 @pytest.mark.parametrize("out_dim,in_dim", [(1024, 256), (1030, 1024), (2000, 7168), (4097, 512)])
 @pytest.mark.parametrize("n_tok", [5, 9, 15, 16, 17, 31, 32])
@@ -93,6 +94,32 @@ def test_gemv_mfma_exact_weights_few_rows(oracle, hip, dtype, out_dim, n_tok):
     err = rel_err(got, want)
     print(f"mfma exact {dtype.name} {out_dim}x{in_dim} T={n_tok}: rel err {err:.3e}")
     assert err <= 2e-5
+
+
+# Q2_K and IQ2_XXS rows of whole 8-block super-tiles (in_dim a multiple of
+# 2048) take the staged kernel above 16 tokens (weights copied through LDS
+# in half super-tiles: Q2_K qs, scales and (d, dmin) runs, IQ2_XXS qs and the
+# d run; K split over workgroups for matrices of few rows, 64 x 8192) and
+# the unstaged kernel up to 16 (the grouped MoE route takes the staged
+# kernel at every batch: test_gpu_moe). Ragged last row blocks, 1 to 4
+# super-tiles per row, within the exact-route bound.
+@pytest.mark.parametrize("dtype", [G.Q2_K, G.IQ2_XXS])
+@pytest.mark.parametrize("out_dim,in_dim", [(1030, 4096), (4097, 2048), (64, 8192), (300, 6144)])
+@pytest.mark.parametrize("n_tok", [5, 8, 16, 32])
+def test_gemv_mfma_staged_dsv4_formats(oracle, hip, dtype, out_dim, in_dim, n_tok):
+    w = synth.weight(dtype, out_dim, in_dim, 2100 + out_dim + n_tok)
+    x = synth.activations(n_tok, in_dim, 2200 + n_tok)
+    x *= (np.float32(10.0) ** ((np.arange(n_tok) % 5) - 2)).astype(np.float32)[:, None]
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, x, n_tok, in_dim, out_dim, int(dtype))
+    assert rc == 0
+    got = np.full(n_tok * out_dim, np.nan, np.float32)
+    hip.matmul_quant_f32(got, w, x, n_tok, in_dim, out_dim, dtype)
+    g = got.reshape(n_tok, out_dim)
+    wv = want.reshape(n_tok, out_dim)
+    assert not np.isnan(g).any()
+    for t in range(n_tok):
+        assert rel_err(g[t], wv[t]) <= 2e-5, f"token {t}"
 
 
 # GGUF Q6_K scales use the whole int8 range (-128..127); |sc (q - 32)| then
