@@ -1867,12 +1867,13 @@ template <class F> static int mfs_splits(int in_dim, int out_dim) {
     return sk;
 }
 // The staged kernel's K splits for a dense call of n_tok tokens, or 0 where
-// the call takes another kernel: Q2_K and IQ2_XXS take it above 16 tokens
-// only (below, the unstaged kernel was the faster: Q2_K 7168 x 2048 at 8
-// tokens 9.9 vs 11.8 us, 4096 x 4096 at 16 11.2 vs 12.8 us, IQ2_XXS 2048 x
-// 4096 at 8 10.5 vs 12.0 us; at 32 tokens 14.5 vs 13.9 and 13.4 vs 13.4 us).
+// the call takes another kernel: IQ2_XXS takes it above 16 tokens only,
+// Q2_K never (unstaged against staged: IQ2_XXS 2048 x 4096 at 8 tokens 10.5
+// vs 12.0 us, at 32 13.2 vs 11.9 us, 14336 x 4096 at T = 512 in 32-token
+// chunks 398 vs 342 us; Q2_K 7168 x 2048 at 8 tokens 9.9 vs 11.8 us,
+// 4096 x 2048 at 32 9.4 vs 11.3 us, at T = 512 143 vs 176 us).
 template <class F> static int mfs_dense_splits(int n_tok, int in_dim, int out_dim) {
-    if ((std::is_same<F, MQ2K>::value || std::is_same<F, MIQ2>::value) && n_tok <= 16) return 0;
+    if (std::is_same<F, MQ2K>::value || (std::is_same<F, MIQ2>::value && n_tok <= 16)) return 0;
     return mfs_splits<F>(in_dim, out_dim);
 }
 // (the workspace sizing: every format the staged kernel takes must be here)
@@ -2116,8 +2117,12 @@ static hipError_t mfg_gemv(const uint8_t *w0, const uint8_t *w1, size_t w_stride
     const uint32_t plane = (uint32_t)((size_t)n_rows * in_dim * 2);
     // weights staged through LDS where the layout allows (16-byte aligned
     // expert matrices, in_dim a multiple of 1024, of 2048 for Q6_K)
+    // (Q2_K and IQ2_XXS: 8-slot batches only; with 16-slot batches the
+    // unstaged kernel measured faster, 5075 vs 5443 us for DS-V4 routed
+    // experts at 2048 tokens)
+    constexpr bool dsv4 = std::is_same<F, MQ2K>::value || std::is_same<F, MIQ2>::value;
     if constexpr (kMfsStaged<F>) {
-    if (mfs_splits<F>(in_dim, out_dim) > 0 &&
+    if (mfs_splits<F>(in_dim, out_dim) > 0 && (!dsv4 || bw == 8) &&
         (((uintptr_t)w0 | (uintptr_t)(w1 ? w1 : w0) | (uintptr_t)w_stride) & 15) == 0) {
         if (bw == 8) {
             // Q4_K: 64-row blocks (each workgroup reads the batch's image once

@@ -768,17 +768,22 @@ size_t moe_scratch_bytes(uint32_t dt_gu, uint32_t dt_d, int n_tok, int k, int n_
 constexpr int kMoeMfmaMinTok = 1;
 constexpr size_t kMoeFusedMfmaPairs = 16;
 
-// Q2_K and IQ2_XXS experts reach the matrix cores without staged weights
+// Q2_K and IQ2_XXS experts whose rows are not whole super-tiles (in_dim not
+// a multiple of 2048) reach the matrix cores without staged weights
 // (mf_rows), which loses to the int8-limb routes while few active experts
 // hold more than one slot. DS-V4 shapes (IQ2_XXS gate/up, Q2_K down, 4096 /
-// 2048, 256 experts, top-6), int8-limb against matrix cores: 113 vs 126 us
-// at 4 tokens (24 pairs), 229 vs 228 us at 8 (48), 343 vs 305 us at 12
-// (72), 465 vs 381 us at 16, 571 vs 447 us at 20 (one process, one box). So
-// with either format the grouped matrix-core route takes calls of at least
-// n_expert / 5 pairs.
-static bool moe_mfma_dense_enough(uint32_t dt_gu, uint32_t dt_d, size_t n_pairs, int n_expert) {
-    auto unstaged = [](uint32_t t) { return t == T_Q2_K || t == T_IQ2_XXS; };
-    return !(unstaged(dt_gu) || unstaged(dt_d)) || n_pairs >= (size_t)n_expert / 5;
+// 2048, 256 experts, top-6) on mf_rows, int8-limb against matrix cores: 113
+// vs 126 us at 4 tokens (24 pairs), 229 vs 228 us at 8 (48), 343 vs 305 us
+// at 12 (72), 465 vs 381 us at 16 (one process, one box). So such calls take
+// the grouped matrix-core route from n_expert / 5 pairs. Staged, the same
+// shapes take it from the fused pair's limit: 92 vs 74 us at 3 tokens, 114
+// vs 89 at 4, 229 vs 156 at 8.
+static bool moe_mfma_dense_enough(uint32_t dt_gu, uint32_t dt_d, size_t n_pairs, int n_expert,
+                                  int n_embd, int n_ff) {
+    auto unstaged = [](uint32_t t, int in_dim) {
+        return (t == T_Q2_K || t == T_IQ2_XXS) && in_dim % 2048 != 0;
+    };
+    return !(unstaged(dt_gu, n_embd) || unstaged(dt_d, n_ff)) || n_pairs >= (size_t)n_expert / 5;
 }
 
 // One pass over n_tok tokens (n_tok * k <= kMoeMaxPairs).
@@ -809,7 +814,7 @@ static hipError_t moe_pass(uint32_t dt_gu, uint32_t dt_d, const uint8_t *gate, c
     float *yd = reinterpret_cast<float *>(take(P * n_embd * 4));
     const bool mfma_ok = moe_mfma_supported(dt_gu, dt_d, n_embd, n_ff) &&
                          moe_mfma_fits((int)P, n_embd, n_ff) && n_tok >= kMoeMfmaMinTok &&
-                         moe_mfma_dense_enough(dt_gu, dt_d, P, n_expert) &&
+                         moe_mfma_dense_enough(dt_gu, dt_d, P, n_expert, n_embd, n_ff) &&
                          gu_stride <= 0xFFFFFFFFu && d_stride <= 0xFFFFFFFFu;
     const bool fused1 = (!mfma_ok || P <= kMoeFusedMfmaPairs) &&
                         moe_fused_fits(dt_gu, dt_d, n_tok, k, n_embd, n_ff, gu_stride, d_stride);

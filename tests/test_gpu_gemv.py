@@ -96,13 +96,13 @@ def test_gemv_mfma_exact_weights_few_rows(oracle, hip, dtype, out_dim, n_tok):
     assert err <= 2e-5
 
 
-# Q2_K and IQ2_XXS rows of whole 8-block super-tiles (in_dim a multiple of
-# 2048) take the staged kernel above 16 tokens (weights copied through LDS
-# in half super-tiles: Q2_K qs, scales and (d, dmin) runs, IQ2_XXS qs and the
-# d run; K split over workgroups for matrices of few rows, 64 x 8192) and
-# the unstaged kernel up to 16 (the grouped MoE route takes the staged
-# kernel at every batch: test_gpu_moe). Ragged last row blocks, 1 to 4
-# super-tiles per row, within the exact-route bound.
+# IQ2_XXS rows of whole 8-block super-tiles (in_dim a multiple of 2048) take
+# the staged kernel above 16 tokens (weights copied through LDS in half
+# super-tiles, qs and the d run; K split over workgroups for matrices of few
+# rows, 64 x 8192) and the unstaged kernel up to 16; dense Q2_K calls keep
+# the unstaged kernel (the grouped MoE route stages both formats in its
+# 8-slot batches: test_gpu_moe). Ragged last row blocks, 1 to 4 super-tiles
+# per row, within the exact-route bound.
 @pytest.mark.parametrize("dtype", [G.Q2_K, G.IQ2_XXS])
 @pytest.mark.parametrize("out_dim,in_dim", [(1030, 4096), (4097, 2048), (64, 8192), (300, 6144)])
 @pytest.mark.parametrize("n_tok", [5, 8, 16, 32])
