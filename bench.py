@@ -93,6 +93,10 @@ def parse():
     ap.add_argument("--moe-probe", type=int, default=0, metavar="T",
                     help="internal: only run the C3 routed-expert call at T tokens 8 times "
                          "(for rocprofv3 kernel traces; prints no JSON)")
+    ap.add_argument("--dsv4-probe", type=int, default=0, metavar="T",
+                    help="internal: only run the DS-V4 routed-expert call (IQ2_XXS / Q2_K, 256 "
+                         "experts, top-6) at T tokens 8 times after 25 ms of it (for rocprofv3 "
+                         "kernel traces; prints no JSON)")
     ap.add_argument("--prefill-pmc-probe", action="store_true",
                     help="internal: the C4 prefill call at T = 512 and 2048, five times each, "
                          "for the MFMA-busy counter pass (prints no JSON)")
@@ -501,6 +505,44 @@ def moe_probe(T):
                          d_u.data_ptr(), gate.nbytes, d_d.data_ptr(), down.nbytes, d_i.data_ptr(),
                          d_w.data_ptr(), d_i.numel(), T, n_embd, n_ff, n_expert, k, G.Q4_K,
                          G.Q4_K, 10.0, sptr)
+    _sustain(call, 25)
+    for r in range(8):
+        call(r)
+    torch.cuda.synchronize()
+
+
+def dsv4_probe(T):
+    """The DS-V4 routed-expert call (IQ2_XXS gate/up 2048x4096, Q2_K down
+    4096x2048, 256 experts, top-6, weights in the device layout) at T tokens
+    over 4 routings: 25 ms of calls back to back, then 8 calls; a kernel
+    trace's last 8 calls are the measured ones."""
+    import torch
+    from rsllm_amd import backend as B
+    from rsllm_amd import synth
+    from rsllm_amd.ggml import GgmlType as G
+    n_expert, n_embd, n_ff, k = 256, 4096, 2048, 6
+    sptr = torch.cuda.current_stream().cuda_stream
+    mats = []
+    for seed, dt, rows, ind in ((650, G.IQ2_XXS, n_expert * n_ff, n_embd),
+                                (651, G.IQ2_XXS, n_expert * n_ff, n_embd),
+                                (652, G.Q2_K, n_expert * n_embd, n_ff)):
+        raw = torch.from_numpy(synth.weight(dt, rows, ind, seed)).cuda()
+        d = torch.empty_like(raw)
+        B.prepare_weights_dev(d.data_ptr(), raw.data_ptr(), raw.numel(), dt, ind, sptr)
+        mats.append(d)
+        del raw
+    d_g, d_u, d_d = mats
+    x = torch.from_numpy(synth.activations(T, n_embd, 660 + T).reshape(-1)).cuda()
+    y = torch.zeros(T * n_embd, dtype=torch.float32, device="cuda")
+    routs = [tuple(torch.from_numpy(a.reshape(-1)).cuda()
+                   for a in synth.moe_routing(T, n_expert, k, 670 + T + 1000 * r)) for r in range(4)]
+
+    def call(i):
+        d_i, d_w = routs[i % 4]
+        B.moe_routed_dev(y.data_ptr(), y.numel(), x.data_ptr(), x.numel(), d_g.data_ptr(),
+                         d_u.data_ptr(), d_g.numel(), d_d.data_ptr(), d_d.numel(), d_i.data_ptr(),
+                         d_w.data_ptr(), d_i.numel(), T, n_embd, n_ff, n_expert, k, G.IQ2_XXS,
+                         G.Q2_K, 10.0, sptr)
     _sustain(call, 25)
     for r in range(8):
         call(r)
@@ -1236,6 +1278,9 @@ def main():
         return
     if args.moe_probe:
         moe_probe(args.moe_probe)
+        return
+    if args.dsv4_probe:
+        dsv4_probe(args.dsv4_probe)
         return
     # the counter passes run first, in child processes, before this process
     # touches the GPU
