@@ -94,6 +94,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv(const uint8_t *__restri
                                                float *__restrict__ y, int n_tok, int in_dim,
                                                int out_dim) {
     __shared__ float red[kMaxWaves * RT * BT];
+    stage_format_tables<F>();
     const int nw = blockDim.x >> 6;
     // wavefront index, made explicitly uniform so per-column offsets stay scalar
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -204,6 +205,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv1(const uint8_t *__restrict__ w
                                                   int n_tok) {
     const int in_dim = sh.in_dim, out_dim = sh.out_dim;
     extern __shared__ uint4 xl[];
+    stage_format_tables<F, false>();  // before the barrier that ends the x prologue
     constexpr int kHalves = F::kXF == 5 ? 2 : 1;
     constexpr int kThreads = 64 * NW;
     const int lane = threadIdx.x & 63, k = lane & 7, ks = lane >> 3;
@@ -382,7 +384,7 @@ static hipError_t gemv1_launch(const uint8_t *w, size_t w_bytes, const float *x,
     // the attribute once per kernel (thread-safe static initialisation)
     static const hipError_t attr = hipFuncSetAttribute(
         (const void *)k_gemv1<F, NW, PD, GPT, BT, UNI>, hipFuncAttributeMaxDynamicSharedMemorySize,
-        (int)kGemv1MaxLds);
+        (int)(kGemv1MaxLds - kFormatTableLds<F>));
     if (attr != hipSuccess) return attr;
     // n_wg workgroups dealt over the groups (at least one per group, at most
     // one per row)
@@ -512,6 +514,7 @@ __device__ __forceinline__ void grouped_batch(const GroupedArgs &a, __amdgpu_buf
 template <class F, int RT>
 __global__ __launch_bounds__(64 * kMaxWaves) void k_gemv_grouped(GroupedArgs a) {
     __shared__ float red[kMaxWaves * RT * 4];
+    stage_format_tables<F>();
     if ((int)blockIdx.y >= *a.n_act) return;
     const int e = a.act[blockIdx.y], m = blockIdx.z;
     const int s0 = a.off[e], cnt = a.off[e + 1] - s0;
@@ -746,7 +749,7 @@ constexpr int gemv1_batch_nw(int bt) {
 
 template <class F>
 static bool gemv1_fits_f(int in_dim, int bt) {
-    return gemv1_lds_bytes<F>(in_dim, bt) <= kGemv1MaxLds &&
+    return gemv1_lds_bytes<F>(in_dim, bt) <= kGemv1MaxLds - kFormatTableLds<F> &&
            gemv1_gpt<F>(in_dim, bt == 1 ? 8 : gemv1_batch_nw<F>(bt), bt) != 0;
 }
 
@@ -776,7 +779,7 @@ static hipError_t gemv1_batch(const uint8_t *w, size_t w_bytes, const float *x, 
 
 #define GEMV_FORMATS(X)                                                                            \
     X(T_Q4_K, FQ4K) X(T_Q6_K, FQ6K) X(T_Q8_0, FQ8<false>) X(T_Q4_0, FQ8<true>) X(T_Q2_K, FQ2K)     \
-    X(T_IQ2_XXS, FIQ2XXS)
+    X(T_IQ2_XXS, FIQ2XXSK)
 
 static int gemv1_tokens(uint32_t dtype, int n_tok, int in_dim) {
 #define X(T, F) if (dtype == T) return gemv1_bt<F>(n_tok, in_dim);

@@ -430,6 +430,7 @@ __global__ __launch_bounds__(64 * NW) void k_moe_fused(
 #pragma clang fp contract(off)
     extern __shared__ uint4 xlds[];
     __shared__ MoeRoute rt;
+    stage_format_tables<F>();
     const int lane = threadIdx.x & 63, kk = lane & 7, ks = lane >> 3;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int P = n_tok * k;
