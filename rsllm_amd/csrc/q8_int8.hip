@@ -143,6 +143,130 @@ __global__ __launch_bounds__(256) void k_q8_int8_gemv(const uint8_t *__restrict_
     }
 }
 
+// Row-tiled form for 5 or more tokens. Thread (h, j), j = tid % CB, h = tid
+// / CB, holds weight block c0 + j of each of the workgroup's ROWS rows in
+// registers and multiplies it with tokens h, h + 256/CB, ... of the tile, so
+// an activation block is read once per workgroup rather than once per row.
+// The products go to LDS and thread (t, r) adds them in block order as in
+// k_q8_int8_gemv. Workgroup order: ids go round robin over the 8 XCDs, and
+// the token tiles of one row tile take ids L, L + 8, ..., so they run on one
+// XCD and share its L2 copy of the rows.
+template <int ROWS, int BT, int CB>
+__global__ __launch_bounds__(256) void k_q8_int8_rows(const uint8_t *__restrict__ w,
+                                                      uint32_t w_bytes,
+                                                      const int8_t *__restrict__ xq,
+                                                      const float *__restrict__ xscale,
+                                                      float *__restrict__ out, int n_tok,
+                                                      int in_dim, int out_dim, int blocks,
+                                                      int n_rt, int n_tt) {
+#pragma clang fp contract(off)
+    constexpr int TG = 256 / CB, Pad = CB + 1;
+    static_assert(BT * ROWS <= 256 && BT % TG == 0, "tile");
+    __shared__ float prod[BT * ROWS * Pad];
+    const int L = blockIdx.x;
+    const int rt = (L / (8 * n_tt)) * 8 + L % 8, tt = (L / 8) % n_tt;
+    if (rt >= n_rt) return;  // the whole workgroup, before any barrier
+    const int tid = threadIdx.x, j = tid % CB, h = tid / CB;
+    const int row0 = rt * ROWS, t0 = tt * BT;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
+    const uint32_t nblk = (uint32_t)out_dim * (uint32_t)blocks;
+    const uint32_t full_tiles = nblk >> 3, last_r = nblk & 7u;
+    const int last_bn = in_dim - (blocks - 1) * 32;
+    float acc = 0.0f;  // thread (t, r) = (tid / ROWS, tid % ROWS)
+    for (int c0 = 0; c0 < blocks; c0 += CB) {
+        const int b = c0 + j;
+        const bool live = b < blocks;
+        const int bb = min(b, blocks - 1);
+        uint4 qa[ROWS], qb[ROWS];
+        float ws[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) {
+            const int row = min(row0 + r, out_dim - 1);
+            const uint32_t g = (uint32_t)row * (uint32_t)blocks + (uint32_t)bb;
+            const uint32_t S = g >> 3, sl = g & 7u;
+            const uint32_t rS = S < full_tiles ? 8u : last_r;
+            const uint32_t base = S * (uint32_t)kQ8Tile;
+            qa[r] = bload16(rw, base + sl * 32u, 0);
+            qb[r] = bload16(rw, base + sl * 32u + 16u, 0);
+            const float sc = f16_to_f32(bload2(rw, base + rS * 32u + sl * 2u, 0));
+            ws[r] = __builtin_isfinite(sc) ? sc : 0.0f;
+        }
+        // only the first last_bn lanes of a partial last block take part (:184-187)
+        const bool part = last_bn < 32 && b == blocks - 1;
+        uint32_t m[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int keep = part ? min(max(last_bn - 4 * i, 0), 4) : 4;
+            m[i] = keep == 4 ? 0xFFFFFFFFu : ((1u << (8 * keep)) - 1u);
+        }
+#pragma unroll
+        for (int t = h; t < BT; t += TG) {
+            const int tok = min(t0 + t, n_tok - 1);
+            float p[ROWS];
+#pragma unroll
+            for (int r = 0; r < ROWS; r++) p[r] = 0.0f;
+            if (live) {
+                const uint4 *xp =
+                    reinterpret_cast<const uint4 *>(xq + ((size_t)tok * blocks + b) * 32);
+                uint4 u0 = xp[0], u1 = xp[1];
+                if (part) {
+                    u0.x &= m[0]; u0.y &= m[1]; u0.z &= m[2]; u0.w &= m[3];
+                    u1.x &= m[4]; u1.y &= m[5]; u1.z &= m[6]; u1.w &= m[7];
+                }
+                const float xs = xscale[(size_t)tok * blocks + b];
+#pragma unroll
+                for (int r = 0; r < ROWS; r++) {
+                    int dot = 0;
+                    dot = __builtin_amdgcn_sdot4((int)qa[r].x, (int)u0.x, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)qa[r].y, (int)u0.y, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)qa[r].z, (int)u0.z, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)qa[r].w, (int)u0.w, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)qb[r].x, (int)u1.x, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)qb[r].y, (int)u1.y, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)qb[r].z, (int)u1.z, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)qb[r].w, (int)u1.w, dot, false);
+                    p[r] = (ws[r] * xs) * (float)dot;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < ROWS; r++) prod[(t * ROWS + r) * Pad + j] = p[r];
+        }
+        __syncthreads();
+        if (tid < BT * ROWS) {
+            const float *pr = prod + tid * Pad;
+            const int n = min(CB, blocks - c0);
+            for (int i = 0; i < n; i++) acc = acc + pr[i];
+        }
+        __syncthreads();
+    }
+    if (tid < BT * ROWS) {
+        const int t = t0 + tid / ROWS, o = row0 + tid % ROWS;
+        if (t < n_tok && o < out_dim) out[(size_t)t * out_dim + o] = acc;
+    }
+}
+
+template <int ROWS, int BT, int CB>
+static hipError_t q8_rows_go(const uint8_t *w, size_t w_bytes, const int8_t *xq,
+                             const float *xscale, float *out, int n_tok, int in_dim, int out_dim,
+                             hipStream_t s) {
+    const int blocks = (in_dim + 31) / 32;
+    const int n_rt = (out_dim + ROWS - 1) / ROWS, n_tt = (n_tok + BT - 1) / BT;
+    const long long n_wg = (long long)((n_rt + 7) / 8) * 8 * n_tt;
+    k_q8_int8_rows<ROWS, BT, CB><<<(unsigned)n_wg, 256, 0, s>>>(
+        w, (uint32_t)w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, blocks, n_rt, n_tt);
+    return hipGetLastError();
+}
+
+template <int ROWS, int BT>
+static hipError_t q8_rows_cb(const uint8_t *w, size_t w_bytes, const int8_t *xq,
+                             const float *xscale, float *out, int n_tok, int in_dim, int out_dim,
+                             hipStream_t s) {
+    const int blocks = (in_dim + 31) / 32;
+    if (blocks >= 128) return q8_rows_go<ROWS, BT, 128>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+    if (blocks >= 64) return q8_rows_go<ROWS, BT, 64>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+    return q8_rows_go<ROWS, BT, 32>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+}
+
 hipError_t launch_q8_quantize(const float *x, int8_t *xq, float *scale, int n_tok, int in_dim,
                               int *status, hipStream_t s) {
     const int blocks = (in_dim + 31) / 32;
@@ -178,6 +302,11 @@ hipError_t launch_q8_int8_matmul(const uint8_t *w, size_t w_bytes, const int8_t 
                                  const float *xscale, float *out, int n_tok, int in_dim,
                                  int out_dim, hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0 || in_dim <= 0) return hipSuccess;
+    // 5 or more tokens: the row-tiled kernel (8 rows x 8 tokens up to 8
+    // tokens, 4 x 16 above)
+    if (n_tok >= 5 && n_tok <= 8)
+        return q8_rows_cb<8, 8>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+    if (n_tok > 8) return q8_rows_cb<4, 16>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
     // fewer rows per workgroup for short matrices, so the grid still fills
     // the 256 CUs
     if (out_dim >= 4096) return q8_gemv_bt<8>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
