@@ -1840,9 +1840,13 @@ static hipError_t mfb_xp_go(const uint8_t *w, size_t w_bytes, const float *x, fl
 // grows with the batch, is still faster (C1: 26 vs 29 us at 4 tokens, 55 vs
 // 29 us at 8). The weights are exact, so any number of rows qualifies.
 bool gemv_mfma_supported(uint32_t dtype, int n_tok, int in_dim, int out_dim) {
-    // Q8_0 from 9 tokens: up to 8 the int8-limb kernel with x in LDS is as
-    // fast on 4096 x 4096 and faster on 1024-row matrices
-    const int min_tok = dtype == T_Q8_0 ? 9 : 5;
+    // Q8_0 below 8192 rows and 8192 columns from 9 tokens: up to 8 the
+    // int8-limb kernel with x in LDS is as fast on 4096 x 4096 and faster on
+    // 1024-row matrices. Taller ones gain from 5 (14336 x 4096: 28 -> 19 us
+    // at 5 and 8 tokens), wider ones from 3 (4096 x 14336: 30 -> 23 us at 3
+    // and 4 tokens, 76 -> 24 us at 8)
+    const int min_tok =
+        dtype != T_Q8_0 ? 5 : in_dim >= 8192 ? 3 : out_dim >= 8192 ? 5 : 9;
     return (dtype == T_Q4_K || dtype == T_Q6_K || dtype == T_Q8_0 || dtype == T_Q2_K ||
             dtype == T_IQ2_XXS) &&
            n_tok >= min_tok && n_tok <= 32 && in_dim % 256 == 0 && in_dim > 0 && out_dim > 0;

@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void k_q8_int8_gemv(const uint8_t *__restrict_
     }
 }
 
-// Row-tiled form for 5 or more tokens. Thread (h, j), j = tid % CB, h = tid
+// Row-tiled form for 2 or more tokens. Thread (h, j), j = tid % CB, h = tid
 // / CB, holds weight block c0 + j of each of the workgroup's ROWS rows in
 // registers and multiplies it with tokens h, h + 256/CB, ... of the tile, so
 // an activation block is read once per workgroup rather than once per row.
@@ -161,7 +161,7 @@ __global__ __launch_bounds__(256) void k_q8_int8_rows(const uint8_t *__restrict_
                                                       int n_rt, int n_tt) {
 #pragma clang fp contract(off)
     constexpr int TG = 256 / CB, Pad = CB + 1;
-    static_assert(BT * ROWS <= 256 && BT % TG == 0, "tile");
+    static_assert(BT * ROWS <= 256, "tile");
     __shared__ float prod[BT * ROWS * Pad];
     const int L = blockIdx.x;
     const int rt = (L / (8 * n_tt)) * 8 + L % 8, tt = (L / 8) % n_tt;
@@ -288,29 +288,23 @@ static hipError_t q8_gemv_go(const uint8_t *w, size_t w_bytes, const int8_t *xq,
     return hipGetLastError();
 }
 
-template <int ROWS>
-static hipError_t q8_gemv_bt(const uint8_t *w, size_t w_bytes, const int8_t *xq,
-                             const float *xscale, float *out, int n_tok, int in_dim, int out_dim,
-                             hipStream_t s) {
-    if (n_tok == 1) return q8_gemv_go<ROWS, 1>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
-    if (n_tok == 2) return q8_gemv_go<ROWS, 2>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
-    if (n_tok <= 4) return q8_gemv_go<ROWS, 4>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
-    return q8_gemv_go<ROWS, 8>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
-}
-
 hipError_t launch_q8_int8_matmul(const uint8_t *w, size_t w_bytes, const int8_t *xq,
                                  const float *xscale, float *out, int n_tok, int in_dim,
                                  int out_dim, hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0 || in_dim <= 0) return hipSuccess;
-    // 5 or more tokens: the row-tiled kernel (8 rows x 8 tokens up to 8
-    // tokens, 4 x 16 above)
-    if (n_tok >= 5 && n_tok <= 8)
-        return q8_rows_cb<8, 8>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
-    if (n_tok > 8) return q8_rows_cb<4, 16>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
-    // fewer rows per workgroup for short matrices, so the grid still fills
-    // the 256 CUs
-    if (out_dim >= 4096) return q8_gemv_bt<8>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
-    return q8_gemv_bt<4>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+    // one token: k_q8_int8_gemv, fewer rows per workgroup for short matrices
+    // so the grid still fills the 256 CUs
+    if (n_tok == 1) {
+        if (out_dim >= 4096)
+            return q8_gemv_go<8, 1>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+        return q8_gemv_go<4, 1>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+    }
+    // more: the row-tiled kernel, 8 rows x 2, 4 or 8 tokens up to 8 tokens,
+    // 4 x 16 above
+    if (n_tok == 2) return q8_rows_cb<8, 2>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+    if (n_tok <= 4) return q8_rows_cb<8, 4>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+    if (n_tok <= 8) return q8_rows_cb<8, 8>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+    return q8_rows_cb<4, 16>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
 }
 
 }  // namespace rsllm_hip

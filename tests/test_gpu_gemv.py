@@ -122,6 +122,26 @@ def test_gemv_mfma_staged_dsv4_formats(oracle, hip, dtype, out_dim, in_dim, n_to
         assert rel_err(g[t], wv[t]) <= 2e-5, f"token {t}"
 
 
+# Q8_0 takes the matrix cores from 3 tokens on matrices of 8192 or more
+# columns, from 5 on 8192 or more rows, from 9 otherwise; each side of each
+# threshold against the oracle, per token: within 2e-5 on the matrix cores
+# (exact weights, hi + lo activations), REL_TOL on the int8-limb route
+@pytest.mark.parametrize("out_dim,in_dim,n_tok,mfma", [
+    (96, 8192, 2, False), (96, 8192, 3, True), (40, 14336, 4, True), (8200, 512, 4, False),
+    (8200, 512, 5, True), (8192, 1024, 8, True), (300, 4096, 8, False), (300, 4096, 9, True)])
+def test_gemv_q8_0_matrix_core_thresholds(oracle, hip, out_dim, in_dim, n_tok, mfma):
+    w = synth.weight(G.Q8_0, out_dim, in_dim, 2300 + out_dim + n_tok)
+    x = synth.activations(n_tok, in_dim, 2400 + n_tok).reshape(-1)
+    rc, want = oracle.matmul_quant_f32(w, x, n_tok, in_dim, out_dim, int(G.Q8_0))
+    assert rc == 0
+    got = np.full(n_tok * out_dim, np.nan, np.float32)
+    hip.matmul_quant_f32(got, w, x, n_tok, in_dim, out_dim, G.Q8_0)
+    g, wv = got.reshape(n_tok, out_dim), want.reshape(n_tok, out_dim)
+    tol = 2e-5 if mfma else REL_TOL
+    for t in range(n_tok):
+        assert rel_err(g[t], wv[t]) <= tol, f"token {t}"
+
+
 # GGUF Q6_K scales use the whole int8 range (-128..127); |sc (q - 32)| then
 # reaches 4096, past the integers f16 holds exactly (2048). Every route —
 # the int8-limb GEMVs (1..4 tokens), the matrix-core GEMV (5..32), its fused
