@@ -81,6 +81,8 @@ def parse():
                     help="internal: the batch-1 GEMVs run under rocprofv3 --kernel-trace")
     ap.add_argument("--batch-probe", action="store_true",
                     help="run only the batched decode calls (for rocprofv3 traces and counters)")
+    ap.add_argument("--q8-probe", action="store_true",
+                    help="run only the C2 int8-activation calls (quantize + matmul) for traces")
     ap.add_argument("--no-trace", action="store_true",
                     help="skip the kernel-trace pass (roofline from HIP events only)")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -590,6 +592,41 @@ def batch_probe():
             B.matmul_quant_f32_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(), x.data_ptr(),
                                    x.numel(), n_tok, in_dim, out_dim, dtype, sptr)
         torch.cuda.synchronize()
+        del reps, prep
+
+
+def q8_probe():
+    """Run under rocprofv3 --kernel-trace: C2 (4096x4096, 1024x4096) through
+    the int8-activation path at 1..32 tokens, TRACE_LAUNCHES calls of
+    quantize_q8_0_batch_dev + matmul_q8_0_batch_dev each after 20 ms of
+    copies, every matmul reading a different weight copy."""
+    import torch
+    from rsllm_amd import backend as B
+    from rsllm_amd import synth
+    from rsllm_amd.ggml import GgmlType as G
+    dev = torch.device("cuda:0")
+    sptr = torch.cuda.current_stream().cuda_stream
+    for (o, i_) in ((4096, 4096), (1024, 4096)):
+        raw = torch.from_numpy(synth.weight(G.Q8_0, o, i_, 540 + o // 1024)).to(dev)
+        prep = torch.empty_like(raw)
+        B.prepare_weights_dev(prep.data_ptr(), raw.data_ptr(), raw.numel(), G.Q8_0, i_, sptr)
+        del raw
+        reps = _rotating(prep)
+        blocks = i_ // 32
+        for n_tok in (1, 2, 4, 8, 16, 32):
+            x = torch.from_numpy(synth.activations(n_tok, i_, 550 + n_tok).reshape(-1)).to(dev)
+            xq = torch.empty(n_tok * blocks * 32, dtype=torch.int8, device=dev)
+            xs = torch.empty(n_tok * blocks, dtype=torch.float32, device=dev)
+            y = torch.empty(n_tok * o, dtype=torch.float32, device=dev)
+            _spinup(20)
+            for i in range(TRACE_LAUNCHES):
+                w = reps[i % len(reps)]
+                B.quantize_q8_0_batch_dev(x.data_ptr(), x.numel(), xq.data_ptr(), xq.numel(),
+                                          xs.data_ptr(), xs.numel(), n_tok, i_, 0, sptr)
+                B.matmul_q8_0_batch_dev(y.data_ptr(), y.numel(), w.data_ptr(), w.numel(),
+                                        xq.data_ptr(), xq.numel(), xs.data_ptr(), xs.numel(),
+                                        n_tok, i_, o, sptr)
+            torch.cuda.synchronize()
         del reps, prep
 
 
@@ -1269,6 +1306,9 @@ def main():
         return
     if args.gemv_probe:
         gemv_probe()
+        return
+    if args.q8_probe:
+        q8_probe()
         return
     if args.batch_probe:
         batch_probe()

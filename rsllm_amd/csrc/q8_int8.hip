@@ -299,8 +299,13 @@ hipError_t launch_q8_int8_matmul(const uint8_t *w, size_t w_bytes, const int8_t 
             return q8_gemv_go<8, 1>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
         return q8_gemv_go<4, 1>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
     }
-    // more: the row-tiled kernel, 8 rows x 2, 4 or 8 tokens up to 8 tokens,
-    // 4 x 16 above
+    // more: the row-tiled kernel, 8 rows (4 below 4096 rows, for a fuller
+    // grid) x 2, 4 or 8 tokens up to 8 tokens, 4 x 16 above
+    if (out_dim < 4096 && n_tok <= 8) {
+        if (n_tok == 2) return q8_rows_cb<4, 2>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+        if (n_tok <= 4) return q8_rows_cb<4, 4>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+        return q8_rows_cb<4, 8>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
+    }
     if (n_tok == 2) return q8_rows_cb<8, 2>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
     if (n_tok <= 4) return q8_rows_cb<8, 4>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
     if (n_tok <= 8) return q8_rows_cb<8, 8>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
