@@ -205,7 +205,8 @@ __global__ __launch_bounds__(256) void k_q8_int8_rows(const uint8_t *__restrict_
             float p[ROWS];
 #pragma unroll
             for (int r = 0; r < ROWS; r++) p[r] = 0.0f;
-            if (live) {
+            // tokens past n_tok (a partial last tile) give 0: their sums are not stored
+            if (live && t0 + t < n_tok) {
                 const uint4 *xp =
                     reinterpret_cast<const uint4 *>(xq + ((size_t)tok * blocks + b) * 32);
                 uint4 u0 = xp[0], u1 = xp[1];
