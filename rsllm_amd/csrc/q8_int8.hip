@@ -293,9 +293,14 @@ hipError_t launch_q8_int8_matmul(const uint8_t *w, size_t w_bytes, const int8_t 
                                  const float *xscale, float *out, int n_tok, int in_dim,
                                  int out_dim, hipStream_t s) {
     if (n_tok <= 0 || out_dim <= 0 || in_dim <= 0) return hipSuccess;
-    // one token: k_q8_int8_gemv, fewer rows per workgroup for short matrices
-    // so the grid still fills the 256 CUs
+    // one token: the row-tiled kernel's 2-token tile (4096 x 4096: 6.7 ->
+    // 6.3 us, 4096 x 14336: 18.8 -> 14.8 us) except on tall, narrow
+    // matrices (14336 x 4096: 13.4 against 14.0 us) and below 4096 rows,
+    // where k_q8_int8_gemv is kept, with fewer rows per workgroup for short
+    // matrices so the grid still fills the 256 CUs
     if (n_tok == 1) {
+        if (out_dim >= 4096 && (out_dim < 8192 || in_dim >= 8192))
+            return q8_rows_cb<8, 2>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
         if (out_dim >= 4096)
             return q8_gemv_go<8, 1>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);
         return q8_gemv_go<4, 1>(w, w_bytes, xq, xscale, out, n_tok, in_dim, out_dim, s);

@@ -115,7 +115,8 @@ def q8_weights(out_dim, in_dim, seed, specials=False):
 @pytest.mark.parametrize("n_tok,in_dim,out_dim", [
     (1, 32, 1), (1, 64, 17), (2, 100, 3), (3, 4096, 33), (4, 1000, 16), (5, 7168, 48),
     (8, 256, 100), (9, 2048, 31), (16, 4096, 64), (32, 520, 129), (33, 4096, 20),
-    (12, 14336, 40), (20, 100, 9), (64, 4096, 130), (17, 2080, 257), (7, 1500, 1025)])
+    (12, 14336, 40), (20, 100, 9), (64, 4096, 130), (17, 2080, 257), (7, 1500, 1025),
+    (1, 14336, 4100), (1, 4000, 8200), (1, 1000, 4097)])
 def test_matmul_bit_exact(oracle, hip, n_tok, in_dim, out_dim):
     w = q8_weights(out_dim, in_dim, 7 * in_dim + out_dim, specials=True)
     x = ragged_activations(n_tok, in_dim, in_dim + n_tok)
