@@ -1,4 +1,5 @@
-// Batched GEMV (5..32 tokens; Q8_0 from 9) on the matrix cores:
+// Batched GEMV (5..32 tokens; Q8_0 from 9, or from 3 / 5 on matrices of 8192
+// or more columns / rows) on the matrix cores:
 // y[t, o] = sum_i W[o, i] x[t, i].
 //
 // Restates matmul_quant_f32 (rsllm-backend-cpu/src/ops/quant_matmul.rs:45-119)

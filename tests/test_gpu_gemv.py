@@ -169,8 +169,9 @@ def test_gemv_q6k_full_range_scales(oracle, hip, out_dim, in_dim, n_tok):
 # The fused matrix-core kernel (5..8 tokens, out_dim >= 8192, f16 x in LDS):
 # row counts off the 16-row block, K steps fewer than wavefronts (256 -> 2
 # steps over 16 wavefronts) and many, token scales far apart, one token
-# zero. (Q8_0 takes the matrix cores from 9 tokens only.)
-@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q2_K, G.IQ2_XXS])
+# zero. (Q8_0 takes the matrix cores below 9 tokens from 8192 rows, where
+# these shapes are.)
+@pytest.mark.parametrize("dtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K, G.IQ2_XXS])
 @pytest.mark.parametrize("out_dim,in_dim", [(8192, 256), (8200, 1024), (9001, 3072)])
 @pytest.mark.parametrize("n_tok", [5, 6, 8])
 def test_gemv_mfma_fused_lds(oracle, hip, dtype, out_dim, in_dim, n_tok):
